@@ -1,0 +1,228 @@
+"""Benchmark of the HIP tree-growing path on one MI355X.
+
+Workload: one best-first tree over a dense binned matrix of 10 000 000 rows x
+100 features of uint8 bins uniform on 0..255, gradients N(0,1), hessians
+U(0.1,1) (fp32), 255 leaves, min_samples_leaf 20, min_child_weight 1e-3,
+lambda 1, gamma 0, lr 0.1, identity binner (nbins 256).  Inputs are generated
+on the device and resident in HBM before timing.
+
+A step is one full tree (root histogram, 254 splits of partition + smaller
+child histogram + sibling subtraction + split scans).  ``value`` is the tree's
+histogram work, sum over built nodes of rows x features (row.feature updates),
+divided by the measured time per tree, in G updates/s.
+
+Also reported:
+  * root_hist: the streaming root-histogram kernel timed alone with HIP events
+    (10M x 100 = 1.0e9 updates per launch); ``roofline`` is computed from it:
+    algorithmic bytes per launch = n*F (bins) + 8n (fp32 g, h) = 1.08 GB;
+  * cpu_baseline: the reference grow.c (compiled from the reference sources
+    into oracle/_ref/, kind "reference") or, if that library is absent, the
+    oracle's restatement of it (kind "port"), on a bounded row sample of the
+    same workload, timed on this host's cores.
+
+Usage: python bench.py [--gpus 1] [--steps 5] [--warmup 1] [--no-cpu]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "histogram G row·feature updates/s + ms/tree at 10M×100, % of HBM peak"
+HBM_PEAK_GBS = 8000.0
+N_ROWS, N_FEAT, MAX_LEAVES = 10_000_000, 100, 255
+PARAMS = dict(lam=1.0, gamma=0.0, mcw=1e-3, msl=20, lr=0.1, max_leaves=MAX_LEAVES, max_depth=64)
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def node_sizes(feature, left, right, leaf_of_row) -> np.ndarray:
+    """Rows per node from per-row leaf ids (children have larger ids)."""
+    size = np.bincount(leaf_of_row, minlength=len(feature)).astype(np.int64)
+    for nid in range(len(feature) - 1, -1, -1):
+        if feature[nid] >= 0:
+            size[nid] = size[left[nid]] + size[right[nid]]
+    return size
+
+
+def tree_updates(feature, left, right, sizes, F) -> int:
+    """Histogram work of one tree: the root plus the smaller child of every
+    split (ties to the left, grow.c:355), times F."""
+    rows = int(sizes[0])
+    for nid in np.nonzero(feature >= 0)[0]:
+        rows += int(min(sizes[left[nid]], sizes[right[nid]]))
+    return rows * F
+
+
+def gpu_inputs(torch, n, F, seed=0):
+    from yabt_amd import grow_hip as G
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    ld_fm = (n + 15) // 16 * 16
+    fm = torch.randint(0, 256, (F, ld_fm), generator=gen, dtype=torch.uint8, device=dev)
+    ld_rm = (F + 15) // 16 * 16
+    rm = torch.zeros((n, ld_rm), dtype=torch.uint8, device=dev)
+    lib = G._lib.load()
+    G._lib.check(lib.yabt_transpose_bins(G._ptr(fm), ld_fm, n, F, G._ptr(rm), ld_rm, G._stream(dev)),
+                 "yabt_transpose_bins")
+    g = torch.randn(n, generator=gen, device=dev, dtype=torch.float32)
+    h = torch.rand(n, generator=gen, device=dev, dtype=torch.float32) * 0.9 + 0.1
+    torch.cuda.synchronize()
+    return G.BinLayouts(fm, rm, n, F), g, h
+
+
+def time_root_hist(torch, lay, g, h, reps=20):
+    """Average duration of the streaming root-histogram kernel (one launch per
+    call of yabt_hist_accumulate), HIP events on the launch stream."""
+    from yabt_amd import grow_hip as G
+    from yabt_amd import _lib
+    dev = lay.fm.device
+    lib = _lib.load()
+    out = torch.zeros((3, lay.F, 256), dtype=torch.int64, device=dev)
+    _, (sg, sh) = G.hist(lay, g, h)
+    stream = torch.cuda.current_stream(dev)
+
+    def launch():
+        _lib.check(lib.yabt_hist_accumulate(G._ptr(lay.fm), lay.ld_fm, G._ptr(lay.rm), lay.ld_rm,
+                                            G._ptr(g), G._ptr(h), lay.n, lay.F, None, 0, sg, sh,
+                                            None, G._ptr(out), G._stream(dev)),
+                   "yabt_hist_accumulate")
+
+    for _ in range(3):
+        launch()
+    torch.cuda.synchronize()
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
+    for i in range(reps):
+        starts[i].record(stream)
+        launch()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+    return float(np.mean(ms)), float(np.median(ms))
+
+
+def cpu_baseline(budget_s: float = 20.0) -> dict:
+    """Reference grow.c (or its restatement) on a row sample of the workload."""
+    from oracle import oracle as O
+    reference = O.ref_available()
+    threads = min(os.cpu_count() or 1, 8)   # the reference default (grow_c.py:283-302)
+    F = N_FEAT
+    n = 1_000_000
+    rng = np.random.default_rng(0)
+    bins_fm = rng.integers(0, 256, size=(F, n), dtype=np.uint8)
+    g = rng.normal(size=n).astype(np.float32)
+    h = rng.uniform(0.1, 1.0, size=n).astype(np.float32)
+    kw = dict(PARAMS, nbins=np.full(F, 256, np.int32), n_threads=threads)
+    times = []
+    res = None
+    t_start = time.perf_counter()
+    for _ in range(4):  # warm-up + up to 3 timed runs within the budget
+        t0 = time.perf_counter()
+        res = O.grow(bins_fm, g, h, reference=reference, **kw)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start > budget_s:
+            break
+    timed = times[1:] if len(times) > 1 else times
+    sec = float(np.median(timed))
+    leaf = O.apply(bins_fm.T.astype(np.float32), res["feature"],
+                   np.where(res["feature"] >= 0, res["thr_bin"], 0).astype(np.float32),
+                   res["left"], res["right"], n_threads=threads)
+    sizes = node_sizes(res["feature"], res["left"], res["right"], leaf)
+    upd = tree_updates(res["feature"], res["left"], res["right"], sizes, F)
+    return {"value": round(upd / sec / 1e9, 4), "unit": "G row·feature updates/s",
+            "cores": threads, "kind": "reference" if reference else "port",
+            "ms_per_tree": round(sec * 1e3, 1),
+            "sample": f"one 255-leaf tree on 1,000,000 x 100 uniform u8 bins (1/10 of the rows), "
+                      f"{len(timed)} timed run(s) after 1 warm-up, median; {threads} OpenMP threads; "
+                      f"host has {os.cpu_count()} logical CPUs"}
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--rows", type=int, default=N_ROWS)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the tree-growing path "
+              "runs on a single device", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from yabt_amd import grow_hip as G
+
+    n, F = args.rows, N_FEAT
+    log(f"[bench] generating {n} x {F} inputs on cuda:0")
+    lay, g, h = gpu_inputs(torch, n, F)
+    nbins = np.full(F, 256, np.int32)
+
+    log("[bench] root histogram kernel")
+    root_mean_ms, root_med_ms = time_root_hist(torch, lay, g, h)
+
+    log(f"[bench] warm-up trees: {args.warmup}")
+    for _ in range(args.warmup):
+        res = G.grow_device(lay, g, h, nbins, **PARAMS)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    log(f"[bench] timed trees: {args.steps}")
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(args.steps):
+        res = G.grow_device(lay, g, h, nbins, sync=False, **PARAMS)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_per_tree = e0.elapsed_time(e1) / args.steps
+
+    nn = int(res._status.item())
+    feat = res.feature[:nn].cpu().numpy()
+    left = res.left[:nn].cpu().numpy()
+    right = res.right[:nn].cpu().numpy()
+    leaf = G.leaf_ids(res, n, F, MAX_LEAVES).cpu().numpy()
+    sizes = node_sizes(feat, left, right, leaf)
+    upd = tree_updates(feat, left, right, sizes, F)
+    value = upd / (ms_per_tree * 1e-3) / 1e9
+
+    root_bytes = n * F + 8 * n
+    achieved = root_bytes / (root_mean_ms * 1e-3) / 1e9
+    line = {
+        "metric": METRIC, "value": round(value, 3), "unit": "G row·feature updates/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_per_tree, 3), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int64",
+        "data": "synthetic (device RNG, seed 0)",
+        "config": {"workload": "best-first tree, 10M rows x 100 features x 256 uint8 bins, 255 leaves",
+                   "rows": n, "features": F, "bins": 256, "max_leaves": MAX_LEAVES,
+                   "min_samples_leaf": 20, "leaves_grown": int((feat == -1).sum()),
+                   "tree_updates": upd},
+        "ms_per_tree": round(ms_per_tree, 3),
+        "root_hist": {"ms": round(root_mean_ms, 4), "ms_median": round(root_med_ms, 4),
+                      "updates_per_s": round(n * F / (root_mean_ms * 1e-3) / 1e9, 3),
+                      "unit": "G updates/s", "GBps": round(achieved, 1),
+                      "frac_hbm": round(achieved / HBM_PEAK_GBS, 4)},
+        "roofline": {"kernel": "k_hist_root<16> (streaming root histogram)", "bound": "hbm",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+    }
+    if not args.no_cpu:
+        log("[bench] CPU baseline")
+        line["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

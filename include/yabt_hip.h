@@ -1,0 +1,132 @@
+/*
+ * yabt_hip.h -- C ABI of the gfx950 tree-growing library (libyabt_hip.so).
+ *
+ * Drop-in for the native boundary of YABT's C grower: the reference loads
+ * yabt/_cgrow/grow.c through ctypes (yabt/grow_c.py:154-200, 412-426) and calls
+ * `cgrow` / `capply`.  This library exports the same operations on device
+ * memory (HIP), plus the per-stage kernels so each can be tested alone.
+ *
+ * Conventions
+ *   - every pointer is device memory unless stated; sizes are plain integers;
+ *   - calls are asynchronous on `stream` (hipStream_t, 0 = null stream);
+ *   - return 0 on success, < 0 on a rejected argument or launch failure; the
+ *     message is available from yabt_last_error() (per calling thread);
+ *   - histograms are exact int64 fixed point: the caller's grad/hess are
+ *     quantised as q = rint(x * 2^s) with one shift per call,
+ *     s = 61 - ceil(log2(n)) - e where max|x| < 2^e (s = 0 if max|x| = 0), so
+ *     every sum over <= n rows is exact and below 2^62 in magnitude;
+ *   - bins: feature-major (F, ld_fm) uint8 with ld_fm >= n, ld_fm % 16 == 0,
+ *     and a row-major copy (n, ld_rm) uint8 with ld_rm >= F, ld_rm % 16 == 0
+ *     (yabt_transpose_bins builds it); bins, grad, hess 16-byte aligned.
+ */
+#ifndef YABT_HIP_H
+#define YABT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *yabt_stream_t; /* == hipStream_t */
+
+/* Last error message of the calling thread ("" if none).
+ * Replaces: the RuntimeError text of yabt/grow_c.py:236-238. */
+const char *yabt_last_error(void);
+
+/* Bytes of device workspace yabt_grow needs for (n, F, max_leaves). */
+size_t yabt_grow_workspace_bytes(int64_t n, int F, int max_leaves);
+
+/* Grow one best-first tree.  Replaces `int cgrow(...)` (yabt/_cgrow/grow.c:243-250,
+ * ctypes signature yabt/grow_c.py:168-200; caller yabt/grow_c.py:412-426).
+ * Same parameters and the same node-array outputs (each of length
+ * 2*max_leaves+1, device memory); differences:
+ *   - bins come in both layouts (bins_fm, bins_rm) instead of `binned` (F,n);
+ *   - the sparse CSR arguments of cgrow are dropped: with exact integer sums
+ *     the sparse builder (grow.c:68-107) and the dense one give identical
+ *     histograms, so the dense kernels serve both;
+ *   - B (always 256) and n_threads are dropped;
+ *   - `workspace` (>= yabt_grow_workspace_bytes) replaces cgrow's mallocs;
+ *   - the node count is written to out_status[0] on the device (cgrow's return
+ *     value); out_status[0] = -1 if grad or hess holds a non-finite value.
+ * Requires 0 <= n < 2^32, F >= 1, 1 <= max_leaves <= 32767. */
+int yabt_grow(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
+              const float *grad, const float *hess, const uint8_t *fmask, const float *imat,
+              float ib, int use_imat, const int32_t *nbins, int64_t n, int F, float lam,
+              float gamma, float mcw, int msl, float lr, int max_leaves, int max_depth,
+              void *workspace, size_t workspace_bytes, int64_t *out_feature,
+              int64_t *out_thr_bin, int64_t *out_left, int64_t *out_right, float *out_value,
+              int64_t *out_depth, int32_t *out_status, yabt_stream_t stream);
+
+/* Per-row leaf node id (int64, n) of the tree the previous yabt_grow call on
+ * `workspace` grew, read from the final partition (the membership cgrow's
+ * rows[] holds at grow.c:410; what yabt/boosting.py:492 recomputes with
+ * Tree.apply).  feature/depth/status are that call's outputs. */
+int yabt_grow_leaf_ids(void *workspace, int64_t n, int F, int max_leaves, const int64_t *feature,
+                       const int64_t *depth, const int32_t *status, int64_t *out,
+                       yabt_stream_t stream);
+
+/* Row-major copy of the feature-major bins; padding columns are zero.
+ * Replaces the host-side transpose of yabt/grow_c.py:364-367 (its inverse). */
+int yabt_transpose_bins(const uint8_t *bins_fm, int64_t ld_fm, int64_t n, int F,
+                        uint8_t *bins_rm, int64_t ld_rm, yabt_stream_t stream);
+
+/* Route raw X (n, ldx) row-major to leaves: x[f] <= threshold goes left.
+ * Replaces `void capply(...)` (yabt/_cgrow/grow.c:223-225, caller
+ * yabt/grow_c.py:305-333); n_threads is dropped, n_nodes bounds the walk. */
+int yabt_apply(const float *X, int64_t ldx, int64_t n, int F, const int64_t *feature,
+               const float *threshold, const int64_t *left, const int64_t *right, int n_nodes,
+               int64_t *out_node, yabt_stream_t stream);
+
+/* Workspace bytes of yabt_hist. */
+size_t yabt_hist_workspace_bytes(void);
+
+/* Exact node histogram out[3][F][256] int64 = (sum q(g), sum q(h), count) over
+ * the rows rows[0:m] (row-major gather), or over all n rows when rows == NULL
+ * (feature-major stream).  out_shifts[0..1] (device int32) receive the shifts.
+ * Replaces `build_hist` (yabt/_cgrow/grow.c:37-62) and the CUDA `hist_build`
+ * K==1 path (yabt/_cuda/hist.cu:101-125, yabt/cuda_hist.py:79-89). */
+int yabt_hist(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
+              const float *grad, const float *hess, int64_t n, int F, const uint32_t *rows,
+              int64_t m, void *workspace, int64_t *out, int32_t *out_shifts,
+              yabt_stream_t stream);
+
+/* yabt_hist with caller-given shifts (sg, sh), adding into `out` without
+ * clearing it; with rows == NULL it is exactly one kernel launch (the
+ * streaming root histogram), which is what a timing harness brackets.
+ * workspace: >= yabt_hist_workspace_bytes() when rows != NULL, else unused.
+ * Replaces `build_hist` (yabt/_cgrow/grow.c:37-62) for callers that manage
+ * the quantisation themselves. */
+int yabt_hist_accumulate(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm,
+                         int64_t ld_rm, const float *grad, const float *hess, int64_t n, int F,
+                         const uint32_t *rows, int64_t m, int sg, int sh, void *workspace,
+                         int64_t *out, yabt_stream_t stream);
+
+/* Workspace bytes of yabt_best_split for F features. */
+size_t yabt_best_split_workspace_bytes(int F);
+
+/* Best split of one exact histogram; out_gain[0] (device double) = true gain
+ * or -inf, out_fb[0..1] (device int32) = (feature, bin), -1 if none.
+ * boost may be NULL (all 1).  Replaces `best_split` (yabt/_cgrow/grow.c:129-197). */
+int yabt_best_split(const int64_t *hist, int F, const int32_t *nbins, const uint8_t *fmask,
+                    const float *boost, int sg, int sh, double lam, double gamma, double mcw,
+                    int msl, void *workspace, double *out_gain, int32_t *out_fb,
+                    yabt_stream_t stream);
+
+/* Workspace bytes of yabt_partition. */
+size_t yabt_partition_workspace_bytes(void);
+
+/* Stable partition of rows_in[0:m] (NULL: the positions 0..m-1) by
+ * bins_fm[f*ld_fm + row] <= b into rows_out (lefts first, each side in input
+ * order); out_mid[0] (device int64) = number of left rows.  Same membership as
+ * `partition_rows` (yabt/_cgrow/grow.c:201-217), whose order is unstable. */
+int yabt_partition(const uint8_t *bins_fm, int64_t ld_fm, int64_t n, int f, int b,
+                   const uint32_t *rows_in, int64_t m, uint32_t *rows_out, void *workspace,
+                   int64_t *out_mid, yabt_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* YABT_HIP_H */

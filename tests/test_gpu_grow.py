@@ -1,0 +1,117 @@
+"""Whole-tree parity of yabt_grow.
+
+* against the oracle's fixed-point mode: bit-identical node arrays (feature,
+  thr_bin, left, right, depth, value bits) and identical per-row leaf ids;
+* against the reference arithmetic (oracle fp32 mode, itself pinned to the
+  compiled reference grow.c by tests/golden): identical feature sequence and
+  leaf membership; thr_bin equal or differing only across bins that are empty
+  in that node; leaf values within 1e-5.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import empty_between, grad_hess, skewed_bins, tree_arrays_equal, uniform_bins
+from yabt_amd import IdentityBinner, TreeParams, grow_tree_hip
+from yabt_amd import grow_hip as G
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0) if torch.cuda.is_available() else None
+
+
+def _grow_gpu(bins, g, h, nbins, **kw):
+    lay = G.make_layouts(torch.from_numpy(bins), DEV)
+    res = G.grow_device(lay, torch.from_numpy(g).to(DEV), torch.from_numpy(h).to(DEV), nbins, **kw)
+    out = {k: getattr(res, k).cpu().numpy() for k in
+           ("feature", "thr_bin", "left", "right", "value", "depth")}
+    leaf = G.leaf_ids(res, bins.shape[0], bins.shape[1], kw.get("max_leaves", 31)).cpu().numpy()
+    return out, leaf
+
+
+def _oracle_kw(kw):
+    m = dict(kw)
+    for a, b in (("max_leaves", "max_leaves"),):
+        pass
+    return m
+
+
+CASES = [
+    dict(n=3000, F=12, nb=256, kind="normal", max_leaves=31),
+    dict(n=20_000, F=20, nb=255, kind="normal", max_leaves=31, imat=True),
+    dict(n=5000, F=9, nb=28, kind="logistic", max_leaves=256, max_depth=8, msl=1),
+    dict(n=8000, F=40, nb=256, kind="laplace", max_leaves=64, max_depth=6, skew=True),
+    dict(n=4000, F=17, nb=64, kind="normal", max_leaves=63, fmask=True, lam=0.0, gamma=0.05),
+    dict(n=1, F=1, nb=256, kind="normal", max_leaves=31, msl=0),
+    dict(n=100, F=3, nb=256, kind="normal", max_leaves=1),
+    dict(n=50_000, F=30, nb=256, kind="normal", max_leaves=255, msl=20),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"n{c['n']}F{c['F']}L{c['max_leaves']}")
+def test_grow_matches_oracle(case):
+    c = dict(case)
+    n, F, nb = c.pop("n"), c.pop("F"), c.pop("nb")
+    rng = np.random.default_rng(n * 31 + F)
+    bins = skewed_bins(rng, n, F) if c.pop("skew", False) else uniform_bins(rng, n, F, nb)
+    g, h = grad_hess(rng, n, c.pop("kind"))
+    kw = dict(max_leaves=c.pop("max_leaves"), max_depth=c.pop("max_depth", 64),
+              msl=c.pop("msl", 20), lam=c.pop("lam", 1.0), gamma=c.pop("gamma", 0.0),
+              mcw=1e-3, lr=0.1)
+    if c.pop("imat", False):
+        kw["imat"] = rng.random((F, F)).astype(np.float32)
+        kw["ib"] = 0.5
+    if c.pop("fmask", False):
+        kw["fmask"] = rng.random(F) < 0.7
+    assert not c
+    nbins = np.full(F, nb, np.int32)
+    got, leaf = _grow_gpu(bins, g, h, nbins, **kw)
+    ref = O.grow(bins.T, g, h, mode=O.MODE_FIXED, nbins=nbins, **kw)
+    bad = tree_arrays_equal(got, ref)
+    assert bad is None, f"{bad} differs from the fixed-point oracle"
+    assert np.array_equal(leaf, O.leaf_of_rows(ref, n))
+
+    # against the reference arithmetic
+    r32 = O.grow(bins.T, g, h, mode=O.MODE_FP32, nbins=nbins, **kw)
+    assert np.array_equal(got["feature"], r32["feature"])
+    assert np.array_equal(leaf, O.leaf_of_rows(r32, n))
+    assert np.abs(got["value"] - r32["value"]).max(initial=0) <= 1e-5
+    for nid in np.nonzero(got["feature"] >= 0)[0]:
+        if got["thr_bin"][nid] != r32["thr_bin"][nid]:
+            rows = ref["rows"][ref["seg_lo"][nid]:ref["seg_hi"][nid]]
+            f = got["feature"][nid]
+            counts = np.bincount(bins[rows, f], minlength=256)
+            assert empty_between(counts, got["thr_bin"][nid], r32["thr_bin"][nid])
+
+
+def test_grow_tree_hip_dropin():
+    """grow_tree_c's signature and Tree output (grow_c.py:336-452)."""
+    rng = np.random.default_rng(5)
+    n, F = 6000, 10
+    bins = uniform_bins(rng, n, F, 100)
+    g, h = grad_hess(rng, n)
+    binner = IdentityBinner(F, 100)
+    tp = TreeParams(max_leaves=24, min_samples_leaf=10)
+    tree = grow_tree_hip(torch.from_numpy(bins), torch.from_numpy(g), torch.from_numpy(h),
+                         binner, tp)
+    assert tree.feature.device.type == "cpu"
+    ref = O.grow(bins.T, g, h, mode=O.MODE_FIXED, nbins=np.full(F, 100, np.int32),
+                 max_leaves=24, msl=10)
+    assert np.array_equal(tree.feature.numpy(), ref["feature"])
+    internal = ref["feature"] >= 0
+    assert np.array_equal(tree.threshold.numpy()[internal], ref["thr_bin"][internal].astype(np.float32))
+    assert tree.depth == int(ref["depth"].max()) + 1
+    assert np.array_equal(tree.apply(torch.from_numpy(bins.astype(np.float32))).numpy(),
+                          O.leaf_of_rows(ref, n))
+
+
+def test_grow_rejects_nonfinite():
+    rng = np.random.default_rng(1)
+    n, F = 100, 3
+    bins = uniform_bins(rng, n, F)
+    g, h = grad_hess(rng, n)
+    g[7] = np.nan
+    with pytest.raises(ValueError):
+        _grow_gpu(bins, g, h, np.full(F, 256, np.int32), max_leaves=4)

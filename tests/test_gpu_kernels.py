@@ -1,0 +1,145 @@
+"""Per-stage parity of the HIP kernels against the CPU oracle, through the C ABI.
+
+Histograms: bit-exact against the oracle's fixed-point histogram (same shifts),
+counts bit-exact against the reference-order fp32 histogram, g/h sums within
+1e-5 normwise of it.  Split scan: identical (gain bits, feature, bin) to the
+oracle's fixed-point scan.  Partition: identical row order to the oracle's
+stable partition and the same membership as the reference two-pointer one.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import grad_hess, normwise_rel, skewed_bins, uniform_bins
+from yabt_amd import grow_hip as G
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0) if torch.cuda.is_available() else None
+
+
+def _layouts(bins):
+    return G.make_layouts(torch.from_numpy(bins), DEV)
+
+
+@pytest.mark.parametrize("n,F,kind,skew", [
+    (1, 1, "normal", False), (17, 3, "normal", False), (1000, 16, "normal", False),
+    (4099, 17, "laplace", False), (50_000, 33, "normal", False), (20_000, 24, "normal", True),
+    (65_536, 100, "logistic", False),
+])
+def test_root_hist_exact(n, F, kind, skew):
+    rng = np.random.default_rng(n + F)
+    bins = skewed_bins(rng, n, F) if skew else uniform_bins(rng, n, F)
+    g, h = grad_hess(rng, n, kind)
+    lay = _layouts(bins)
+    got, (sg, sh) = G.hist(lay, torch.from_numpy(g), torch.from_numpy(h))
+    got = got.cpu().numpy()
+    assert (sg, sh) == O.quant_shifts(g, h)
+    ref = O.hist_fixed(bins.T, g, h, sg, sh)
+    assert np.array_equal(got, ref)
+    f32 = O.hist_f32(bins.T, g, h)
+    assert np.array_equal(got[2], f32[2].astype(np.int64))
+    assert normwise_rel(got[0] * 2.0 ** -sg, f32[0]) < 1e-5
+    assert normwise_rel(got[1] * 2.0 ** -sh, f32[1]) < 1e-5
+
+
+@pytest.mark.parametrize("n,F,m", [(5000, 16, 1), (5000, 16, 777), (40_000, 21, 19_999),
+                                   (40_000, 100, 40_000), (10, 3, 0)])
+def test_gather_hist_exact(n, F, m):
+    rng = np.random.default_rng(m + 7)
+    bins = uniform_bins(rng, n, F)
+    g, h = grad_hess(rng, n)
+    rows = np.sort(rng.choice(n, size=m, replace=False)).astype(np.int64)
+    lay = _layouts(bins)
+    got, (sg, sh) = G.hist(lay, torch.from_numpy(g), torch.from_numpy(h),
+                           torch.from_numpy(rows.astype(np.int32)))
+    ref = O.hist_fixed(bins.T, g, h, sg, sh, rows=rows)
+    assert np.array_equal(got.cpu().numpy(), ref)
+
+
+def test_hist_large_count_exact():
+    """Counts and sums exact with 100 000 rows in one bin (test_fixes.py:22-32)."""
+    n = 100_000
+    bins = np.zeros((n, 2), np.uint8)
+    g = np.ones(n, np.float32)
+    h = np.full(n, 0.5, np.float32)
+    got, (sg, sh) = G.hist(_layouts(bins), torch.from_numpy(g), torch.from_numpy(h))
+    got = got.cpu().numpy()
+    assert got[2, 0, 0] == n
+    assert got[0, 0, 0] * 2.0 ** -sg == n
+    assert got[1, 0, 0] * 2.0 ** -sh == 0.5 * n
+
+
+def _random_qhist(rng, F, n=3000, nb=256):
+    bins = uniform_bins(rng, n, F, nb)
+    g, h = grad_hess(rng, n)
+    sg, sh = O.quant_shifts(g, h)
+    return O.hist_fixed(bins.T, g, h, sg, sh), sg, sh
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_best_split_identical(seed):
+    rng = np.random.default_rng(seed)
+    F = int(rng.integers(1, 70))
+    q, sg, sh = _random_qhist(rng, F, nb=int(rng.choice([4, 30, 256])))
+    kw = dict(nbins=rng.integers(1, 257, size=F).astype(np.int32),
+              lam=float(rng.choice([0.0, 1.0, 2.5])), gamma=float(rng.choice([0.0, 0.3])),
+              mcw=1e-3, msl=int(rng.choice([0, 1, 20])),
+              fmask=(rng.random(F) < 0.8).astype(np.uint8),
+              boost=(1 + 0.5 * rng.random(F)).astype(np.float32))
+    ref = O.best_split_fixed(q, sg, sh, **kw)
+    got = G.best_split(torch.from_numpy(q).to(DEV), sg, sh, **kw)
+    assert got[1:] == ref[1:]
+    assert np.float64(got[0]).tobytes() == np.float64(ref[0]).tobytes()
+
+
+def test_best_split_ties_and_no_split():
+    # duplicated features tie exactly: the lowest feature wins (grow.c:181-192)
+    rng = np.random.default_rng(3)
+    q, sg, sh = _random_qhist(rng, 1)
+    q3 = np.concatenate([q, q, q], axis=1)
+    got = G.best_split(torch.from_numpy(q3).to(DEV), sg, sh, msl=1)
+    ref = O.best_split_fixed(q3, sg, sh, msl=1)
+    assert got[1:] == ref[1:] and got[1] == 0
+    # msl above the node size: no valid split anywhere
+    got = G.best_split(torch.from_numpy(q3).to(DEV), sg, sh, msl=10**6)
+    assert got[1] == -1 and got[0] == float("-inf")
+
+
+@pytest.mark.parametrize("n,m,b", [(1, 1, 0), (5000, 5000, 127), (70_000, 33_333, 3),
+                                   (70_000, 70_000, 255), (300_000, 250_001, 100)])
+def test_partition_identical(n, m, b):
+    rng = np.random.default_rng(m)
+    F = 5
+    bins = uniform_bins(rng, n, F)
+    lay = _layouts(bins)
+    f = int(rng.integers(F))
+    if m == n:
+        rows = np.arange(n, dtype=np.int64)
+        got, mid = G.partition(lay, f, b)
+    else:
+        rows = rng.permutation(n)[:m].astype(np.int64)
+        got, mid = G.partition(lay, f, b, torch.from_numpy(rows.astype(np.int32)))
+    ref, rmid = O.partition(bins[:, f], rows, b, stable=True)
+    assert mid == rmid
+    assert np.array_equal(got.cpu().numpy().astype(np.int64), ref)
+    two, tmid = O.partition(bins[:, f], rows, b, stable=False)
+    assert tmid == mid
+    assert set(two[:tmid].tolist()) == set(ref[:mid].tolist())
+
+
+def test_apply_matches_oracle():
+    rng = np.random.default_rng(11)
+    n, F = 20_000, 7
+    bins = uniform_bins(rng, n, F, 50)
+    g, h = grad_hess(rng, n)
+    tree = O.grow(bins.T, g, h, mode=O.MODE_FIXED, max_leaves=40, msl=5)
+    X = rng.normal(size=(n, F)).astype(np.float32) * 20
+    thr = np.where(tree["feature"] >= 0, tree["thr_bin"], 0).astype(np.float32)
+    ref = O.apply(X, tree["feature"], thr, tree["left"], tree["right"])
+    got = G.apply_hip(torch.from_numpy(X).to(DEV), torch.from_numpy(tree["feature"]),
+                      torch.from_numpy(thr), torch.from_numpy(tree["left"]),
+                      torch.from_numpy(tree["right"]))
+    assert np.array_equal(got.cpu().numpy(), ref)

@@ -1,0 +1,342 @@
+"""HIP grower: a drop-in for ``grow_tree_c`` (yabt/grow_c.py:336-452).
+
+``grow_tree_hip`` takes exactly ``grow_tree_c``'s arguments and returns the
+same ``Tree``; it grows the tree on the GPU through ``yabt_grow``
+(include/yabt_hip.h).  Differences from the reference, all deliberate:
+
+* arithmetic: histograms are exact int64 fixed point (see include/yabt_hip.h),
+  so results are deterministic and sibling subtraction is exact; the split
+  (feature, bin) sequence and leaf membership match the reference grower
+  except where the reference's fp32 rounding decides a tie;
+* ``sparse_layout`` is accepted and ignored: with exact sums the sparse
+  builder (grow.c:68-107) and the dense one give identical histograms;
+* ``n_threads`` is accepted and ignored (no host threads);
+* inputs on the CPU are copied to the current HIP device once per binned
+  matrix (cached); the returned Tree lives on ``binned.device`` as in the
+  reference.
+
+The module never falls back to a CPU path: if the library or a HIP device is
+missing, ``grow_tree_hip`` raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+import weakref
+
+import numpy as np
+import torch
+
+from . import _lib
+from .tree import LEAF, Tree, TreeParams
+
+MAX_BINS = 256
+
+_CACHE_LOCK = threading.Lock()
+_LAYOUTS: "weakref.WeakKeyDictionary[torch.Tensor, tuple]" = weakref.WeakKeyDictionary()
+_WORKSPACES: dict = {}
+
+
+def _round16(x: int) -> int:
+    return (x + 15) // 16 * 16
+
+
+def _ptr(t: torch.Tensor | None):
+    return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
+
+
+def _stream(dev: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _dev_f32(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
+    """Contiguous float32 copy on ``dev`` whose data is 16-byte aligned (the
+    kernels use 16-byte vector loads)."""
+    t = t.detach().to(dev, torch.float32).contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _device() -> torch.device:
+    if not torch.cuda.is_available():
+        raise RuntimeError("yabt_amd: no HIP device available")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+class BinLayouts:
+    """Both device layouts of one binned matrix: feature-major (F, ld_fm) for
+    streaming and partitions, row-major (n, ld_rm) for gathered child nodes."""
+
+    def __init__(self, fm: torch.Tensor, rm: torch.Tensor, n: int, F: int):
+        self.fm, self.rm, self.n, self.F = fm, rm, n, F
+        self.ld_fm = fm.shape[1]
+        self.ld_rm = rm.shape[1]
+
+
+def make_layouts(binned: torch.Tensor, dev: torch.device,
+                 binned_fmajor: np.ndarray | None = None) -> BinLayouts:
+    """Device copies of binned (n, F) uint8 in both padded layouts."""
+    n, F = binned.shape
+    ld_fm, ld_rm = max(16, _round16(n)), _round16(F)
+    fm = torch.zeros((F, ld_fm), dtype=torch.uint8, device=dev)
+    if binned_fmajor is not None:
+        fm[:, :n].copy_(torch.from_numpy(np.ascontiguousarray(binned_fmajor, dtype=np.uint8)))
+    else:
+        fm[:, :n].copy_(binned.to(dev, torch.uint8).t())
+    rm = torch.zeros((max(n, 1), ld_rm), dtype=torch.uint8, device=dev)
+    lib = _lib.load()
+    _lib.check(lib.yabt_transpose_bins(_ptr(fm), ld_fm, n, F, _ptr(rm), ld_rm, _stream(dev)),
+               "yabt_transpose_bins")
+    return BinLayouts(fm, rm, n, F)
+
+
+def layouts_for(binned: torch.Tensor, dev: torch.device,
+                binned_fmajor: np.ndarray | None = None) -> BinLayouts:
+    """Cached per binned tensor (keyed by object, checked against its version),
+    mirroring the reference's cached feature-major copy (boosting.py:454-459)."""
+    key_state = (binned._version, binned.data_ptr(), tuple(binned.shape), dev)
+    with _CACHE_LOCK:
+        hit = _LAYOUTS.get(binned)
+        if hit is not None and hit[0] == key_state:
+            return hit[1]
+    lay = make_layouts(binned, dev, binned_fmajor)
+    with _CACHE_LOCK:
+        _LAYOUTS[binned] = (key_state, lay)
+    return lay
+
+
+def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
+    key = (dev, "grow")
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def nbins_of(binner, F: int) -> np.ndarray:
+    """Used bins per feature, min(len(edges)+1, 256) (grow_c.py:395-401)."""
+    nb = getattr(binner, "_c_nbins", None)
+    if nb is None or nb.shape[0] != F:
+        nb = np.fromiter((min(len(e) + 1, MAX_BINS) for e in binner.edges_), dtype=np.int32, count=F)
+        binner._c_nbins = nb
+    return nb
+
+
+class GrowResult:
+    """Device outputs of one yabt_grow call (node arrays trimmed to n_nodes)."""
+
+    def __init__(self, feature, thr_bin, left, right, value, depth, n_nodes, workspace, status):
+        self.feature, self.thr_bin, self.left, self.right = feature, thr_bin, left, right
+        self.value, self.depth, self.n_nodes = value, depth, n_nodes
+        self._ws, self._status = workspace, status
+
+
+def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: np.ndarray, *,
+                fmask=None, imat=None, ib: float = 0.5, lam=1.0, gamma=0.0, mcw=1e-3, msl=20,
+                lr=0.1, max_leaves=31, max_depth=64, sync: bool = True) -> GrowResult:
+    """One yabt_grow call on device-resident layouts.  grad/hess must be on
+    the layouts' device; parameters are rounded to float32 as ctypes.c_float
+    rounds them in the reference (grow_c.py:418-421)."""
+    lib = _lib.load()
+    dev = lay.fm.device
+    n, F = lay.n, lay.F
+    g = _dev_f32(grad, dev)
+    h = _dev_f32(hess, dev)
+    if g.shape[0] != n or h.shape[0] != n:
+        raise ValueError("grad/hess length must equal the number of rows")
+    fm = (torch.ones(F, dtype=torch.uint8, device=dev) if fmask is None
+          else torch.as_tensor(fmask).to(dev).bool().to(torch.uint8).contiguous())
+    use_imat = imat is not None
+    im = (torch.as_tensor(imat).to(dev, torch.float32).contiguous() if use_imat
+          else torch.zeros(1, dtype=torch.float32, device=dev))
+    if use_imat and tuple(im.shape) != (F, F):
+        raise ValueError("interaction_matrix must be (F, F)")
+    nb = torch.from_numpy(np.ascontiguousarray(nbins, dtype=np.int32)).to(dev)
+    L = int(max_leaves)
+    N = 2 * L + 1
+    nbytes = int(lib.yabt_grow_workspace_bytes(n, F, L))
+    if nbytes == 0:
+        raise ValueError("yabt_grow: invalid sizes")
+    ws = _workspace(dev, nbytes)
+    out_i = torch.empty((5, N), dtype=torch.int64, device=dev)
+    value = torch.empty(N, dtype=torch.float32, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    rc = lib.yabt_grow(
+        _ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h), _ptr(fm), _ptr(im),
+        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), n, F,
+        ctypes.c_float(float(lam)), ctypes.c_float(float(gamma)), ctypes.c_float(float(mcw)),
+        int(msl), ctypes.c_float(float(lr)), L, int(max_depth), _ptr(ws), ws.numel(),
+        _ptr(out_i[0]), _ptr(out_i[1]), _ptr(out_i[2]), _ptr(out_i[3]), _ptr(value),
+        _ptr(out_i[4]), _ptr(status), _stream(dev))
+    _lib.check(rc, "yabt_grow")
+    # keep the argument tensors alive until the stream has consumed them
+    res = GrowResult(out_i[0], out_i[1], out_i[2], out_i[3], value, out_i[4], None, ws, status)
+    res._keep = (g, h, fm, im, nb)
+    if sync:
+        nn = int(status.item())
+        if nn < 0:
+            raise ValueError("yabt_grow: gradients or hessians contain non-finite values")
+        res.n_nodes = nn
+        for k in ("feature", "thr_bin", "left", "right", "value", "depth"):
+            setattr(res, k, getattr(res, k)[:nn])
+    return res
+
+
+def leaf_ids(res: GrowResult, n: int, F: int, max_leaves: int) -> torch.Tensor:
+    """Per-row leaf node ids of a grown tree, from its final partition."""
+    lib = _lib.load()
+    dev = res.value.device
+    out = torch.empty(n, dtype=torch.int64, device=dev)
+    _lib.check(lib.yabt_grow_leaf_ids(_ptr(res._ws), n, F, int(max_leaves), _ptr(res.feature),
+                                      _ptr(res.depth), _ptr(res._status), _ptr(out), _stream(dev)),
+               "yabt_grow_leaf_ids")
+    return out
+
+
+def _edge_table(binner, F: int, dev: torch.device):
+    """(F, 256) float32 table with edge_value(f, b) = edges_f[min(b, len-1)]
+    (binning.py:126-129), cached on the binner per device."""
+    cache = getattr(binner, "_hip_edge_table", None)
+    if cache is not None and cache[0] == dev and cache[1].shape[0] == F:
+        return cache[1], cache[2]
+    tab = np.zeros((F, MAX_BINS), dtype=np.float32)
+    for f, e in enumerate(binner.edges_):
+        e = np.asarray(e.cpu() if isinstance(e, torch.Tensor) else e, dtype=np.float32)
+        if e.size == 0:
+            continue  # no edges: no split on f can be chosen (nbins == 1)
+        idx = np.minimum(np.arange(MAX_BINS), e.size - 1)
+        tab[f] = e[idx]
+    scales = torch.as_tensor(binner.scales_, dtype=torch.float32).clamp_min(1e-12)
+    out = (torch.from_numpy(tab).to(dev), scales.to(dev))
+    binner._hip_edge_table = (dev, out[0], out[1])
+    return out
+
+
+def grow_tree_hip(
+    binned: torch.Tensor,
+    grad: torch.Tensor,
+    hess: torch.Tensor,
+    binner,
+    params: TreeParams,
+    feature_mask: torch.Tensor | None = None,
+    interaction_matrix: torch.Tensor | None = None,
+    interaction_boost: float = 0.5,
+    sparse_layout=None,
+    n_threads: int = 0,
+    binned_fmajor: np.ndarray | None = None,
+) -> Tree:
+    """Drop-in for ``grow_tree_c`` (yabt/grow_c.py:336-452) on a HIP device."""
+    del sparse_layout, n_threads  # see module docstring
+    out_dev = binned.device
+    dev = binned.device if binned.device.type == "cuda" else _device()
+    n, F = binned.shape
+    lay = layouts_for(binned, dev, binned_fmajor)
+    res = grow_device(lay, grad, hess, nbins_of(binner, F), fmask=feature_mask,
+                      imat=interaction_matrix, ib=interaction_boost, lam=params.reg_lambda,
+                      gamma=params.gamma, mcw=params.min_child_weight,
+                      msl=params.min_samples_leaf, lr=params.learning_rate,
+                      max_leaves=params.max_leaves, max_depth=params.max_depth)
+    return tree_from_result(res, binner, F, out_dev)
+
+
+def tree_from_result(res: GrowResult, binner, F: int, out_dev: torch.device) -> Tree:
+    """Thresholds and gate scales from the binner (grow_c.py:435-452)."""
+    dev = res.feature.device
+    tab, scales = _edge_table(binner, F, dev)
+    feat = res.feature
+    internal = feat != LEAF
+    fc = feat.clamp(min=0)
+    threshold = torch.where(internal, tab[fc, res.thr_bin.clamp(0, MAX_BINS - 1)],
+                            torch.zeros((), device=dev))
+    gate = torch.where(internal, scales[fc], torch.ones((), device=dev))
+    depth = int(res.depth.max()) + 1
+    return Tree(feature=feat.to(out_dev), threshold=threshold.to(out_dev), left=res.left.to(out_dev),
+                right=res.right.to(out_dev), value=res.value.to(out_dev), depth=depth,
+                gate_scale=gate.to(out_dev))
+
+
+def apply_hip(X: torch.Tensor, feature: torch.Tensor, threshold: torch.Tensor,
+              left: torch.Tensor, right: torch.Tensor) -> torch.Tensor:
+    """Leaf index per row of raw X on the GPU; drop-in for ``apply_c``
+    (yabt/grow_c.py:305-333)."""
+    lib = _lib.load()
+    dev = X.device if X.device.type == "cuda" else _device()
+    Xd = X.detach().to(dev, torch.float32).contiguous()
+    n, F = Xd.shape
+    fe = feature.to(dev, torch.int64).contiguous()
+    th = threshold.to(dev, torch.float32).contiguous()
+    le = left.to(dev, torch.int64).contiguous()
+    ri = right.to(dev, torch.int64).contiguous()
+    out = torch.empty(n, dtype=torch.int64, device=dev)
+    if n > 0:
+        _lib.check(lib.yabt_apply(_ptr(Xd), F, n, F, _ptr(fe), _ptr(th), _ptr(le), _ptr(ri),
+                                  int(fe.shape[0]), _ptr(out), _stream(dev)), "yabt_apply")
+    return out.to(X.device)
+
+
+def is_available() -> bool:
+    return _lib.is_available()
+
+
+# ---------------------------------------------------------------------------
+# per-stage entry points (exposed for tests and benchmarks)
+# ---------------------------------------------------------------------------
+
+def hist(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor,
+         rows: torch.Tensor | None = None) -> tuple[torch.Tensor, tuple[int, int]]:
+    """Exact (3, F, 256) int64 histogram over ``rows`` (uint32/int) or all rows."""
+    lib = _lib.load()
+    dev = lay.fm.device
+    g = _dev_f32(grad, dev)
+    h = _dev_f32(hess, dev)
+    r = None if rows is None else rows.to(dev, torch.int32).contiguous()
+    m = 0 if r is None else r.shape[0]
+    if r is not None and m == 0:
+        r = torch.zeros(1, dtype=torch.int32, device=dev)  # non-NULL: "no rows", not "all rows"
+    out = torch.empty((3, lay.F, MAX_BINS), dtype=torch.int64, device=dev)
+    shifts = torch.zeros(2, dtype=torch.int32, device=dev)
+    ws = torch.empty(int(lib.yabt_hist_workspace_bytes()), dtype=torch.uint8, device=dev)
+    _lib.check(lib.yabt_hist(_ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h),
+                             lay.n, lay.F, _ptr(r), m, _ptr(ws), _ptr(out), _ptr(shifts),
+                             _stream(dev)), "yabt_hist")
+    s = shifts.cpu().tolist()
+    return out, (int(s[0]), int(s[1]))
+
+
+def best_split(qhist: torch.Tensor, sg: int, sh: int, nbins=None, lam=1.0, gamma=0.0, mcw=1e-3,
+               msl=20, fmask=None, boost=None) -> tuple[float, int, int]:
+    lib = _lib.load()
+    dev = qhist.device
+    F = qhist.shape[1]
+    nb = (torch.full((F,), MAX_BINS, dtype=torch.int32, device=dev) if nbins is None
+          else torch.as_tensor(np.asarray(nbins, np.int32)).to(dev))
+    fm = (torch.ones(F, dtype=torch.uint8, device=dev) if fmask is None
+          else torch.as_tensor(np.asarray(fmask).astype(np.uint8)).to(dev))
+    bo = None if boost is None else torch.as_tensor(np.asarray(boost, np.float32)).to(dev)
+    ws = torch.empty(int(lib.yabt_best_split_workspace_bytes(F)), dtype=torch.uint8, device=dev)
+    og = torch.empty(1, dtype=torch.float64, device=dev)
+    ofb = torch.empty(2, dtype=torch.int32, device=dev)
+    q = qhist.contiguous()
+    _lib.check(lib.yabt_best_split(_ptr(q), F, _ptr(nb), _ptr(fm), _ptr(bo), int(sg), int(sh),
+                                   float(np.float32(lam)), float(np.float32(gamma)),
+                                   float(np.float32(mcw)), int(msl), _ptr(ws), _ptr(og), _ptr(ofb),
+                                   _stream(dev)), "yabt_best_split")
+    fb = ofb.cpu().tolist()
+    return float(og.item()), int(fb[0]), int(fb[1])
+
+
+def partition(lay: BinLayouts, f: int, b: int,
+              rows: torch.Tensor | None = None, m: int | None = None) -> tuple[torch.Tensor, int]:
+    lib = _lib.load()
+    dev = lay.fm.device
+    r = None if rows is None else rows.to(dev, torch.int32).contiguous()
+    mm = (lay.n if m is None else int(m)) if r is None else r.shape[0]
+    if r is not None and mm == 0:
+        r = torch.zeros(1, dtype=torch.int32, device=dev)  # non-NULL: "no rows", not "positions"
+    out = torch.empty(max(mm, 1), dtype=torch.int32, device=dev)
+    ws = torch.empty(int(lib.yabt_partition_workspace_bytes()), dtype=torch.uint8, device=dev)
+    mid = torch.zeros(1, dtype=torch.int64, device=dev)
+    _lib.check(lib.yabt_partition(_ptr(lay.fm), lay.ld_fm, lay.n, int(f), int(b), _ptr(r), mm,
+                                  _ptr(out), _ptr(ws), _ptr(mid), _stream(dev)), "yabt_partition")
+    return out[:mm], int(mid.item())
