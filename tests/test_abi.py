@@ -1,0 +1,56 @@
+"""The C-ABI library loads without a GPU and exports every symbol of
+include/yabt_hip.h; the ctypes table covers exactly those symbols; host-only
+size queries answer without touching a device."""
+
+import ctypes
+import os
+import re
+
+from yabt_amd import _build, _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "yabt_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(yabt_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_is_built():
+    assert os.path.exists(_build.LIB), "run __graft_entry__.build() first"
+
+
+def test_exports_every_declared_symbol():
+    lib = ctypes.CDLL(_build.LIB)
+    names = _declared()
+    assert len(names) >= 12
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_ctypes_table_matches_header():
+    assert sorted(_lib.SIGNATURES) == _declared()
+
+
+def test_host_size_queries():
+    lib = _lib.load()
+    a = lib.yabt_grow_workspace_bytes(10_000_000, 100, 255)
+    # two u32 row lists + one int64 (3,F,256) slot per leaf dominate
+    assert a >= 2 * 4 * 10_000_000 + 255 * 3 * 100 * 256 * 8
+    assert a < 2 * (2 * 4 * 10_000_000 + 255 * 3 * 100 * 256 * 8)
+    assert lib.yabt_grow_workspace_bytes(0, 0, 31) == 0
+    assert lib.yabt_grow_workspace_bytes(100, 4, 0) == 0
+    assert lib.yabt_hist_workspace_bytes() > 0
+    assert lib.yabt_partition_workspace_bytes() > 0
+    assert lib.yabt_best_split_workspace_bytes(100) >= 100 * 24
+
+
+def test_argument_errors_are_reported_without_a_device():
+    lib = _lib.load()
+    rc = lib.yabt_grow(None, 0, None, 0, None, None, None, None, ctypes.c_float(0.5), 0, None, 10, 0,
+                       ctypes.c_float(1), ctypes.c_float(0), ctypes.c_float(1e-3), 20,
+                       ctypes.c_float(0.1), 31, 64, None, 0, None, None, None, None, None, None,
+                       None, None)
+    assert rc < 0
+    assert "bad sizes" in _lib.last_error()

@@ -1,0 +1,74 @@
+"""Host-side mirrors of the reference interface: Binner semantics, the Tree
+type's CPU routing and path pairs, the identity binner."""
+
+import numpy as np
+import torch
+
+from oracle import oracle as O
+from tests.helpers import grad_hess, uniform_bins
+from yabt_amd import Binner, IdentityBinner, Tree
+
+
+def test_binner_split_equivalence():
+    """bin(x) <= b  <=>  x <= edge_value(f, b) (test_splits.py:58-68)."""
+    rng = np.random.default_rng(1)
+    X = rng.normal(size=(1000, 3)).astype(np.float32)
+    binner = Binner(max_bins=16).fit(X)
+    binned = binner.transform(X).numpy()
+    for f in range(3):
+        for b in range(len(binner.edges_[f])):
+            assert ((binned[:, f] <= b) == (X[:, f] <= binner.edge_value(f, b))).all()
+
+
+def test_binner_edges_closed_form():
+    X = np.arange(1, 101, dtype=np.float32).reshape(100, 1)
+    b = Binner(max_bins=4).fit(X)
+    assert np.allclose(b.edges_[0].numpy(), np.quantile(X[:, 0], [0.25, 0.5, 0.75]))
+    assert float(b.scales_[0]) == np.float32(np.quantile(X[:, 0], 0.75) - np.quantile(X[:, 0], 0.25))
+    codes = b.transform(X).numpy()[:, 0]
+    assert codes.min() == 0 and codes.max() == 3
+    # constant column: one edge, zero IQR -> std -> 1.0
+    c = Binner().fit(np.ones((50, 1), np.float32))
+    assert len(c.edges_[0]) == 1 and float(c.scales_[0]) == 1.0
+
+
+def test_binner_imputes_nan_with_median():
+    X = np.array([[1.0], [np.nan], [3.0], [5.0]], np.float32)
+    b = Binner(max_bins=4).fit(X)
+    assert b.medians_[0] == 3.0
+    assert b.impute(X)[1, 0] == 3.0
+
+
+def test_tree_cpu_apply_matches_oracle_routing():
+    rng = np.random.default_rng(2)
+    n, F = 4000, 6
+    bins = uniform_bins(rng, n, F, 32)
+    g, h = grad_hess(rng, n)
+    t = O.grow(bins.T, g, h, mode=O.MODE_FIXED, max_leaves=25, msl=10)
+    thr = np.where(t["feature"] >= 0, t["thr_bin"], 0).astype(np.float32)
+    tree = Tree(feature=torch.from_numpy(t["feature"]), threshold=torch.from_numpy(thr),
+                left=torch.from_numpy(t["left"]), right=torch.from_numpy(t["right"]),
+                value=torch.from_numpy(t["value"]), depth=int(t["depth"].max()) + 1)
+    X = rng.normal(size=(n, F)).astype(np.float32) * 15
+    assert np.array_equal(tree.apply(torch.from_numpy(X)).numpy(),
+                          O.apply(X, t["feature"], thr, t["left"], t["right"]))
+
+
+def test_path_feature_pairs():
+    # root(f0) -> [leaf, node(f2) -> [leaf, leaf]]  (test_interaction_aware.py:44-56)
+    tree = Tree(feature=torch.tensor([0, -1, 2, -1, -1]), threshold=torch.zeros(5),
+                left=torch.tensor([1, -1, 3, -1, -1]), right=torch.tensor([2, -1, 4, -1, -1]),
+                value=torch.zeros(5), depth=3)
+    assert tree.path_feature_pairs() == [(0, 2)]
+    # deeper: 0 -> (1 -> (3, 4), 2:f5 -> (5:f0 -> ...)): every ancestor pairs with each split below
+    tree = Tree(feature=torch.tensor([0, 1, 5, -1, -1, 0, -1, -1, -1]), threshold=torch.zeros(9),
+                left=torch.tensor([1, 3, 5, -1, -1, 7, -1, -1, -1]),
+                right=torch.tensor([2, 4, 6, -1, -1, 8, -1, -1, -1]), value=torch.zeros(9), depth=4)
+    assert sorted(tree.path_feature_pairs()) == sorted([(0, 1), (0, 5), (0, 0), (5, 0)])
+
+
+def test_identity_binner():
+    b = IdentityBinner(3, 256)
+    assert b.edge_value(1, 17) == 17.0
+    assert b.edge_value(1, 300) == 254.0
+    assert len(b.edges_[0]) == 255
