@@ -43,9 +43,12 @@ size_t yabt_grow_workspace_bytes(int64_t n, int F, int max_leaves);
  * Same parameters and the same node-array outputs (each of length
  * 2*max_leaves+1, device memory); differences:
  *   - bins come in both layouts (bins_fm, bins_rm) instead of `binned` (F,n);
- *   - the sparse CSR arguments of cgrow are dropped: with exact integer sums
- *     the sparse builder (grow.c:68-107) and the dense one give identical
- *     histograms, so the dense kernels serve both;
+ *   - the sparse CSR arguments of cgrow are replaced by `default_bin` (F int32,
+ *     may be NULL): rows in a feature's default bin are not accumulated and
+ *     that bin is restored as node total minus the other bins, which with
+ *     exact integer sums gives the dense histogram bit for bit (the sparse
+ *     builder's default-bin fill, grow.c:68-107, made exact).  Any bin is a
+ *     correct choice; the most frequent one saves the most work;
  *   - B (always 256) and n_threads are dropped;
  *   - `workspace` (>= yabt_grow_workspace_bytes) replaces cgrow's mallocs;
  *   - the node count is written to out_status[0] on the device (cgrow's return
@@ -53,9 +56,9 @@ size_t yabt_grow_workspace_bytes(int64_t n, int F, int max_leaves);
  * Requires 0 <= n < 2^32, F >= 1, 1 <= max_leaves <= 32767. */
 int yabt_grow(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
               const float *grad, const float *hess, const uint8_t *fmask, const float *imat,
-              float ib, int use_imat, const int32_t *nbins, int64_t n, int F, float lam,
-              float gamma, float mcw, int msl, float lr, int max_leaves, int max_depth,
-              void *workspace, size_t workspace_bytes, int64_t *out_feature,
+              float ib, int use_imat, const int32_t *nbins, const int32_t *default_bin, int64_t n,
+              int F, float lam, float gamma, float mcw, int msl, float lr, int max_leaves,
+              int max_depth, void *workspace, size_t workspace_bytes, int64_t *out_feature,
               int64_t *out_thr_bin, int64_t *out_left, int64_t *out_right, float *out_value,
               int64_t *out_depth, int32_t *out_status, yabt_stream_t stream);
 
@@ -83,8 +86,8 @@ int yabt_apply(const float *X, int64_t ldx, int64_t n, int F, const int64_t *fea
 size_t yabt_hist_workspace_bytes(void);
 
 /* Exact node histogram out[3][F][256] int64 = (sum q(g), sum q(h), count) over
- * the rows rows[0:m] (row-major gather), or over all n rows when rows == NULL
- * (feature-major stream).  out_shifts[0..1] (device int32) receive the shifts.
+ * the rows rows[0:m] (row-major gather; every id < n), or over all n rows when
+ * rows == NULL (feature-major stream).  out_shifts[0..1] (device int32) receive the shifts.
  * Replaces `build_hist` (yabt/_cgrow/grow.c:37-62) and the CUDA `hist_build`
  * K==1 path (yabt/_cuda/hist.cu:101-125, yabt/cuda_hist.py:79-89). */
 int yabt_hist(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
@@ -120,7 +123,8 @@ size_t yabt_partition_workspace_bytes(void);
 /* Stable partition of rows_in[0:m] (NULL: the positions 0..m-1) by
  * bins_fm[f*ld_fm + row] <= b into rows_out (lefts first, each side in input
  * order); out_mid[0] (device int64) = number of left rows.  Same membership as
- * `partition_rows` (yabt/_cgrow/grow.c:201-217), whose order is unstable. */
+ * `partition_rows` (yabt/_cgrow/grow.c:201-217), whose order is unstable.
+ * The caller guarantees f < F and every row id < n. */
 int yabt_partition(const uint8_t *bins_fm, int64_t ld_fm, int64_t n, int f, int b,
                    const uint32_t *rows_in, int64_t m, uint32_t *rows_out, void *workspace,
                    int64_t *out_mid, yabt_stream_t stream);

@@ -28,14 +28,8 @@ def _grow_gpu(bins, g, h, nbins, **kw):
     out = {k: getattr(res, k).cpu().numpy() for k in
            ("feature", "thr_bin", "left", "right", "value", "depth")}
     leaf = G.leaf_ids(res, bins.shape[0], bins.shape[1], kw.get("max_leaves", 31)).cpu().numpy()
+    res._keep = None
     return out, leaf
-
-
-def _oracle_kw(kw):
-    m = dict(kw)
-    for a, b in (("max_leaves", "max_leaves"),):
-        pass
-    return m
 
 
 CASES = [
@@ -50,8 +44,9 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("dflt", ["auto", None], ids=["skip-default-bin", "no-skip"])
 @pytest.mark.parametrize("case", CASES, ids=lambda c: f"n{c['n']}F{c['F']}L{c['max_leaves']}")
-def test_grow_matches_oracle(case):
+def test_grow_matches_oracle(case, dflt):
     c = dict(case)
     n, F, nb = c.pop("n"), c.pop("F"), c.pop("nb")
     rng = np.random.default_rng(n * 31 + F)
@@ -67,7 +62,7 @@ def test_grow_matches_oracle(case):
         kw["fmask"] = rng.random(F) < 0.7
     assert not c
     nbins = np.full(F, nb, np.int32)
-    got, leaf = _grow_gpu(bins, g, h, nbins, **kw)
+    got, leaf = _grow_gpu(bins, g, h, nbins, default_bin=dflt, **kw)
     ref = O.grow(bins.T, g, h, mode=O.MODE_FIXED, nbins=nbins, **kw)
     bad = tree_arrays_equal(got, ref)
     assert bad is None, f"{bad} differs from the fixed-point oracle"

@@ -30,7 +30,7 @@ _sz = ctypes.c_size_t
 SIGNATURES = {
     "yabt_last_error": (ctypes.c_char_p, []),
     "yabt_grow_workspace_bytes": (_sz, [_i64, _int, _int]),
-    "yabt_grow": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _i64, _int,
+    "yabt_grow": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _vp, _i64, _int,
                          _flt, _flt, _flt, _int, _flt, _int, _int, _vp, _sz,
                          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "yabt_grow_leaf_ids": (_int, [_vp, _i64, _int, _int, _vp, _vp, _vp, _vp, _vp]),

@@ -4,15 +4,20 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <climits>
+
 namespace yabt {
 
-constexpr int NB = 256;          // histogram width: bins are uint8 (grow_c.py:417)
-constexpr int WAVE = 64;         // CDNA wavefront
-constexpr int LEAF = -1;         // grow.c:28
+constexpr int NB = 256;   // histogram width: bins are uint8 (grow_c.py:417)
+constexpr int WAVE = 64;  // CDNA wavefront
+constexpr int LEAF = -1;  // grow.c:28
 
-// Fixed-point contract shared with oracle/grow_oracle.c (or_quant_shift):
-// q = rint(x * 2^s), s = 61 - k - e with max|x| < 2^e, n <= 2^k, so every
+// ---------------------------------------------------------------------------
+// fixed-point quantisation, shared with oracle/grow_oracle.c (or_quant_shift):
+// q = rint(x * 2^s), s = 61 - k - e with max|x| < 2^e and n <= 2^k, so every
 // partial sum of <= n quantised values stays below 2^62 in magnitude.
+// ---------------------------------------------------------------------------
+
 __host__ __device__ inline int quant_shift(float maxabs, int64_t n) {
     if (!(maxabs > 0.0f)) return 0;
     int e = 0;
@@ -26,25 +31,234 @@ __device__ __forceinline__ int64_t quantise(float x, double scale) {
     return (int64_t)rint((double)x * scale);
 }
 
-// Wave-wide exclusive prefix sum of a 64-bit value.
-__device__ __forceinline__ int64_t wave_excl_scan(int64_t v, int lane) {
-    int64_t incl = v;
+// Per-call quantisation record, filled on the device.
+struct Quant {
+    int32_t sg, sh;            // shifts
+    double scg, sch;           // 2^sg, 2^sh
+    double ig, ih;             // 2^-sg, 2^-sh
+    uint32_t maxg_bits;        // max |g| (float bits; non-negative floats order like uints)
+    uint32_t maxh_bits;        // max |h|
+    uint32_t hmin_key;         // order-preserving key of min h
+    uint32_t hmax_key;         // order-preserving key of max h
+    int32_t nonfinite;         // any g or h is inf/nan
+    int32_t const_h;           // every h equal and nonzero: counts = sum q(h) / hq_const
+    int64_t hq_const;
+    int64_t tot_g, tot_h;      // sum of q(g), q(h) over all rows (root totals)
+    uint32_t ticket;
+    uint32_t pad;
+};
+
+__device__ __forceinline__ uint32_t float_key(float x) {
+    const uint32_t b = __float_as_uint(x);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// ---------------------------------------------------------------------------
+// cross-lane helpers
+// ---------------------------------------------------------------------------
+
+// Broadcast lane J of every 16-lane row to the whole row (DPP row_newbcast).
+template <int J>
+__device__ __forceinline__ uint32_t row_bcast32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x150 + J, 0xf, 0xf, false);
+}
+
+template <int J>
+__device__ __forceinline__ uint64_t row_bcast64(uint64_t v) {
+    const uint32_t lo = row_bcast32<J>((uint32_t)v);
+    const uint32_t hi = row_bcast32<J>((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Wave-wide exclusive prefix sum.
+template <typename T>
+__device__ __forceinline__ T wave_excl_scan(T v, int lane) {
+    T incl = v;
 #pragma unroll
     for (int d = 1; d < WAVE; d <<= 1) {
-        int64_t o = __shfl_up(incl, d, WAVE);
+        T o = __shfl_up(incl, d, WAVE);
         if (lane >= d) incl += o;
     }
     return incl - v;
 }
 
-__device__ __forceinline__ uint32_t wave_excl_scan_u32(uint32_t v, int lane) {
-    uint32_t incl = v;
+template <typename T>
+__device__ __forceinline__ T wave_sum(T v) {
 #pragma unroll
-    for (int d = 1; d < WAVE; d <<= 1) {
-        uint32_t o = __shfl_up(incl, d, WAVE);
-        if (lane >= d) incl += o;
+    for (int d = WAVE / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, WAVE);
+    return v;
+}
+
+// Block-wide exclusive scan of one value per thread (NT threads).
+template <int NT, typename T>
+__device__ __forceinline__ T block_excl_scan(T v, T* s_wave, T* total) {
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+    const T ex = wave_excl_scan<T>(v, lane);
+    if (lane == WAVE - 1) s_wave[w] = ex + v;
+    __syncthreads();
+    T off = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < NT / WAVE; ++i) {
+        if (i < w) off += s_wave[i];
+        tot += s_wave[i];
     }
-    return incl - v;
+    __syncthreads();
+    *total = tot;
+    return off + ex;
+}
+
+template <int NT, typename T>
+__device__ __forceinline__ T block_sum(T v, T* s_red) {
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+    v = wave_sum<T>(v);
+    if (lane == 0) s_red[w] = v;
+    __syncthreads();
+    T t = 0;
+#pragma unroll
+    for (int i = 0; i < NT / WAVE; ++i) t += s_red[i];
+    __syncthreads();
+    return t;
+}
+
+// (key, idx) beats (k2, i2) iff key > k2, or equal keys and idx < i2.
+__device__ __forceinline__ bool better(double k1, int i1, double k2, int i2) {
+    return k1 > k2 || (k1 == k2 && i1 < i2);
+}
+
+// Block argmax (NT threads); invalid candidates carry idx = INT_MAX.
+template <int NT>
+__device__ void block_argmax(double& key, int& idx, double* s_key, int* s_idx) {
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) {
+        const double ok = __shfl_xor(key, d, WAVE);
+        const int oi = __shfl_xor(idx, d, WAVE);
+        if (better(ok, oi, key, idx)) {
+            key = ok;
+            idx = oi;
+        }
+    }
+    if (lane == 0) {
+        s_key[w] = key;
+        s_idx[w] = idx;
+    }
+    __syncthreads();
+    key = s_key[0];
+    idx = s_idx[0];
+#pragma unroll
+    for (int i = 1; i < NT / WAVE; ++i)
+        if (better(s_key[i], s_idx[i], key, idx)) {
+            key = s_key[i];
+            idx = s_idx[i];
+        }
+    __syncthreads();
+}
+
+// Last-block-done: true in exactly one block, after every block of the grid
+// has reached this point; that block then sees all their global writes.
+__device__ inline bool last_block(uint32_t* ticket) {
+    __shared__ int s_last;
+    __threadfence();
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const uint32_t t = atomicAdd(ticket, 1u);
+        s_last = (t == gridDim.x * gridDim.y - 1);
+    }
+    __syncthreads();
+    if (s_last) {
+        __threadfence();
+        if (threadIdx.x == 0) *ticket = 0;
+    }
+    return s_last != 0;
+}
+
+// ---------------------------------------------------------------------------
+// quantisation passes
+// ---------------------------------------------------------------------------
+
+// Grid-stride max|g|, max|h|, min/max h and finiteness into q (NT threads).
+template <int NT>
+__device__ void quant_reduce(const float* grad, const float* hess, int64_t n, Quant* q) {
+    __shared__ float s_m[2][NT / WAVE];
+    __shared__ uint32_t s_k[2][NT / WAVE];
+    __shared__ int s_nf;
+    if (threadIdx.x == 0) s_nf = 0;
+    __syncthreads();
+    float mg = 0.0f, mh = 0.0f;
+    uint32_t kmin = 0xffffffffu, kmax = 0u;
+    int nf = 0;
+    for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * NT) {
+        const float a = grad[i], c = hess[i];
+        if (!isfinite(a) || !isfinite(c)) nf = 1;
+        mg = fmaxf(mg, fabsf(a));
+        mh = fmaxf(mh, fabsf(c));
+        const uint32_t kc = float_key(c);
+        kmin = min(kmin, kc);
+        kmax = max(kmax, kc);
+    }
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) {
+        mg = fmaxf(mg, __shfl_xor(mg, d, WAVE));
+        mh = fmaxf(mh, __shfl_xor(mh, d, WAVE));
+        kmin = min(kmin, (uint32_t)__shfl_xor(kmin, d, WAVE));
+        kmax = max(kmax, (uint32_t)__shfl_xor(kmax, d, WAVE));
+    }
+    if (nf) atomicOr(&s_nf, 1);
+    if (lane == 0) {
+        s_m[0][w] = mg;
+        s_m[1][w] = mh;
+        s_k[0][w] = kmin;
+        s_k[1][w] = kmax;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < NT / WAVE; ++i) {
+            mg = fmaxf(mg, s_m[0][i]);
+            mh = fmaxf(mh, s_m[1][i]);
+            kmin = min(kmin, s_k[0][i]);
+            kmax = max(kmax, s_k[1][i]);
+        }
+        atomicMax(&q->maxg_bits, __float_as_uint(mg));
+        atomicMax(&q->maxh_bits, __float_as_uint(mh));
+        atomicMin(&q->hmin_key, kmin);
+        atomicMax(&q->hmax_key, kmax);
+        if (s_nf) atomicOr(&q->nonfinite, 1);
+    }
+}
+
+__device__ inline void quant_finish(Quant* q, int64_t n) {
+    const float mg = __uint_as_float(q->maxg_bits), mh = __uint_as_float(q->maxh_bits);
+    q->sg = quant_shift(mg, n);
+    q->sh = quant_shift(mh, n);
+    q->scg = ldexp(1.0, q->sg);
+    q->sch = ldexp(1.0, q->sh);
+    q->ig = ldexp(1.0, -q->sg);
+    q->ih = ldexp(1.0, -q->sh);
+    q->const_h = 0;
+    q->hq_const = 0;
+    if (n > 0 && q->hmin_key == q->hmax_key) {
+        const uint32_t k = q->hmin_key;
+        const float h = __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+        const int64_t hq = quantise(h, q->sch);
+        if (hq != 0) {
+            q->const_h = 1;
+            q->hq_const = hq;
+        }
+    }
+}
+
+static __global__ void k_quant_clear(Quant* q) {
+    q->maxg_bits = 0;
+    q->maxh_bits = 0;
+    q->hmin_key = 0xffffffffu;
+    q->hmax_key = 0u;
+    q->nonfinite = 0;
+    q->const_h = 0;
+    q->hq_const = 0;
+    q->tot_g = 0;
+    q->tot_h = 0;
+    q->ticket = 0;
 }
 
 }  // namespace yabt

@@ -71,6 +71,23 @@ class BinLayouts:
         self.fm, self.rm, self.n, self.F = fm, rm, n, F
         self.ld_fm = fm.shape[1]
         self.ld_rm = rm.shape[1]
+        self._default = None
+
+    def default_bin(self, sample: int = 65536) -> torch.Tensor:
+        """Most frequent bin per feature over an evenly spaced row sample (the
+        sparse layout's default bin, grow_numba.py:341-367, estimated); any
+        choice gives identical histograms, this one skips the most rows."""
+        if self._default is None:
+            F, n = self.F, self.n
+            if n == 0:
+                self._default = torch.zeros(F, dtype=torch.int32, device=self.fm.device)
+            else:
+                idx = torch.linspace(0, n - 1, min(n, sample), device=self.fm.device).long()
+                cols = self.fm[:, idx].long()                       # (F, s)
+                counts = torch.zeros((F, MAX_BINS), dtype=torch.int64, device=self.fm.device)
+                counts.scatter_add_(1, cols, torch.ones_like(cols))
+                self._default = counts.argmax(dim=1).to(torch.int32).contiguous()
+        return self._default
 
 
 def make_layouts(binned: torch.Tensor, dev: torch.device,
@@ -134,10 +151,14 @@ class GrowResult:
 
 def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: np.ndarray, *,
                 fmask=None, imat=None, ib: float = 0.5, lam=1.0, gamma=0.0, mcw=1e-3, msl=20,
-                lr=0.1, max_leaves=31, max_depth=64, sync: bool = True) -> GrowResult:
+                lr=0.1, max_leaves=31, max_depth=64, default_bin="auto",
+                sync: bool = True) -> GrowResult:
     """One yabt_grow call on device-resident layouts.  grad/hess must be on
     the layouts' device; parameters are rounded to float32 as ctypes.c_float
-    rounds them in the reference (grow_c.py:418-421)."""
+    rounds them in the reference (grow_c.py:418-421).
+
+    ``default_bin``: "auto" uses the layouts' most frequent bin per feature,
+    None disables the skip, or an (F,) int array."""
     lib = _lib.load()
     dev = lay.fm.device
     n, F = lay.n, lay.F
@@ -153,6 +174,12 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
     if use_imat and tuple(im.shape) != (F, F):
         raise ValueError("interaction_matrix must be (F, F)")
     nb = torch.from_numpy(np.ascontiguousarray(nbins, dtype=np.int32)).to(dev)
+    if isinstance(default_bin, str):
+        db = lay.default_bin()
+    elif default_bin is None:
+        db = None
+    else:
+        db = torch.as_tensor(np.asarray(default_bin, np.int32)).to(dev)
     L = int(max_leaves)
     N = 2 * L + 1
     nbytes = int(lib.yabt_grow_workspace_bytes(n, F, L))
@@ -164,7 +191,7 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
     status = torch.zeros(1, dtype=torch.int32, device=dev)
     rc = lib.yabt_grow(
         _ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h), _ptr(fm), _ptr(im),
-        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), n, F,
+        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), _ptr(db), n, F,
         ctypes.c_float(float(lam)), ctypes.c_float(float(gamma)), ctypes.c_float(float(mcw)),
         int(msl), ctypes.c_float(float(lr)), L, int(max_depth), _ptr(ws), ws.numel(),
         _ptr(out_i[0]), _ptr(out_i[1]), _ptr(out_i[2]), _ptr(out_i[3]), _ptr(value),
@@ -172,7 +199,7 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
     _lib.check(rc, "yabt_grow")
     # keep the argument tensors alive until the stream has consumed them
     res = GrowResult(out_i[0], out_i[1], out_i[2], out_i[3], value, out_i[4], None, ws, status)
-    res._keep = (g, h, fm, im, nb)
+    res._keep = (g, h, fm, im, nb, db)
     if sync:
         nn = int(status.item())
         if nn < 0:
