@@ -70,6 +70,60 @@ __device__ __forceinline__ uint64_t row_bcast64(uint64_t v) {
     return ((uint64_t)hi << 32) | lo;
 }
 
+// DPP move within 16-lane rows; lanes whose source is outside the row read 0.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, true);
+}
+
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
+    return ((uint64_t)dpp32<CTRL>((uint32_t)(v >> 32)) << 32) | dpp32<CTRL>((uint32_t)v);
+}
+
+template <int CTRL>
+__device__ __forceinline__ double dpp_f64(double v) {
+    return __longlong_as_double((long long)dpp64<CTRL>((uint64_t)__double_as_longlong(v)));
+}
+
+constexpr int DPP_ROW_SHR = 0x110;    // row_shr:n   = 0x110 + n
+constexpr int DPP_ROW_ROR = 0x120;    // row_ror:n   = 0x120 + n (rotate inside the row)
+
+__device__ __forceinline__ int64_t readlane64(int64_t v, int lane) {
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)v, lane);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)((uint64_t)v >> 32), lane);
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+__device__ __forceinline__ double readlane_f64(double v, int lane) {
+    return __longlong_as_double(readlane64(__double_as_longlong(v), lane));
+}
+
+// Inclusive prefix sum over the 64 lanes: DPP shifts inside each 16-lane row,
+// then the three lower row totals (read into scalars) are added per row.
+__device__ __forceinline__ int64_t wave_incl_scan_i64(int64_t v, int lane) {
+    uint64_t u = (uint64_t)v;
+    u += dpp64<DPP_ROW_SHR + 1>(u);
+    u += dpp64<DPP_ROW_SHR + 2>(u);
+    u += dpp64<DPP_ROW_SHR + 4>(u);
+    u += dpp64<DPP_ROW_SHR + 8>(u);
+    const int64_t t0 = readlane64((int64_t)u, 15), t1 = readlane64((int64_t)u, 31), t2 = readlane64((int64_t)u, 47);
+    const int64_t off = (lane >= 16 ? t0 : 0) + (lane >= 32 ? t1 : 0) + (lane >= 48 ? t2 : 0);
+    return (int64_t)u + off;
+}
+
+// Sum over the 64 lanes, returned in every lane (row rotations 8, 4, 2, 1
+// leave each row's total in all of its lanes).
+__device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
+    uint64_t u = (uint64_t)v;
+    u += dpp64<DPP_ROW_ROR + 8>(u);
+    u += dpp64<DPP_ROW_ROR + 4>(u);
+    u += dpp64<DPP_ROW_ROR + 2>(u);
+    u += dpp64<DPP_ROW_ROR + 1>(u);
+    return readlane64((int64_t)u, 0) + readlane64((int64_t)u, 16) + readlane64((int64_t)u, 32) +
+           readlane64((int64_t)u, 48);
+}
+
 // Wave-wide exclusive prefix sum.
 template <typename T>
 __device__ __forceinline__ T wave_excl_scan(T v, int lane) {

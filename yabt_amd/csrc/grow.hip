@@ -60,6 +60,8 @@ constexpr int PART_MAX_BLOCKS = 1024;
 struct LeafRec {
     float gain;                // (float) true gain, -inf if none (grow.c:316,394,404)
     int32_t node, f, b;
+    int32_t depth, slot;       // node depth, histogram slot
+    int64_t s, e;              // node segment in its row list
     int64_t tot[3];            // node totals: sum q(g), sum q(h), rows
     int64_t left[3];           // totals of bins <= b of feature f
 };
@@ -69,14 +71,13 @@ struct SplitJob {
     int32_t f, b;
     int32_t build_left;        // 1: the left child is built, the right is subtracted
     int32_t parent_slot, new_slot;
-    int32_t pad;
+    int32_t depth;             // children's depth
     const uint32_t* src;       // parent's rows (nullptr: identity)
     uint32_t* dst;             // children's rows
     int64_t s, e, mid;
     int64_t tot[3];            // parent totals
     int64_t left[3];           // left-child totals
-    int64_t* zero_ptr;         // new slot, cleared by the partition launch
-    int64_t zero_count;
+    int64_t* new_hist;         // the built child's slot (cleared by the previous scan launch)
     unsigned long long cursor[2];   // next write position, left / right
 };
 
@@ -114,7 +115,6 @@ struct GrowArgs {
     uint32_t* rows0;
     uint32_t* rows1;
     int64_t* hist;
-    int32_t* slot_of;
     uint8_t* path;
     LeafRec* leaf;
     int64_t* seg_lo;
@@ -151,31 +151,31 @@ __global__ void __launch_bounds__(SB) k_setup(GrowArgs A) {
         A.depth[i] = 0;
         A.seg_lo[i] = 0;
         A.seg_hi[i] = 0;
-        A.slot_of[i] = -1;
     }
     for (int64_t i = tid; i < (int64_t)N * A.F; i += stride) A.path[i] = 0;
     const int64_t ne = (int64_t)slot_elems(A.F);
     for (int64_t i = tid; i < ne; i += stride) A.hist[i] = 0;
-    if (last_block(&A.q->ticket) && threadIdx.x == 0) {
-        GrowState* st = A.st;
-        quant_finish(A.q, A.n);
-        st->status = 0;
-        st->done = 0;
-        st->active = 0;
-        st->hist.active = 0;
-        st->scan_ticket = 0;
-        st->n_nodes = 1;
-        st->n_leaves = 1;
-        st->n_active = 1;
-        if (A.q->nonfinite) {
-            st->status = -1;
-            st->done = 1;
-            A.out_status[0] = -1;
-        }
-        A.seg_lo[0] = 0;
-        A.seg_hi[0] = A.n;
-        A.slot_of[0] = 0;
+}
+
+// One thread, after k_setup: shifts and tree state.
+__global__ void k_setup_finish(GrowArgs A) {
+    GrowState* st = A.st;
+    quant_finish(A.q, A.n);
+    st->status = 0;
+    st->done = 0;
+    st->active = 0;
+    st->hist.active = 0;
+    st->scan_ticket = 0;
+    st->n_nodes = 1;
+    st->n_leaves = 1;
+    st->n_active = 1;
+    if (A.q->nonfinite) {
+        st->status = -1;
+        st->done = 1;
+        A.out_status[0] = -1;
     }
+    A.seg_lo[0] = 0;
+    A.seg_hi[0] = A.n;
 }
 
 // ---------------------------------------------------------------------------
@@ -194,9 +194,6 @@ __global__ void __launch_bounds__(SB) k_split_partition(const uint8_t* __restric
     const int fcol = J.f, b = J.b;
     const uint32_t* src = J.src;
     uint32_t* dst = J.dst;
-    int64_t* zp = J.zero_ptr;
-    const int64_t zc = J.zero_count;
-    for (int64_t i = (int64_t)blockIdx.x * SB + threadIdx.x; i < zc; i += (int64_t)gridDim.x * SB) zp[i] = 0;
     const int64_t m = e - s;
     const int64_t tiles = (m + PART_TILE - 1) / PART_TILE;
     const int nblk = (int)min((int64_t)gridDim.x, max(tiles, (int64_t)1));
@@ -306,8 +303,7 @@ __device__ void select_next(const GrowArgs& A) {
         A.path[(size_t)nr * A.F + j] = v;
     }
     if (threadIdx.x != 0) return;
-    const int64_t d = A.depth[nid], s = A.seg_lo[nid], e = A.seg_hi[nid];
-    const int32_t pslot = A.slot_of[nid];
+    const int64_t d = L.depth, s = L.s, e = L.e;
     const int64_t cl = L.left[2], c = L.tot[2];
     const int bl = cl <= c - cl;
     const int new_slot = n_leaves;           // slots 0..n_leaves-1 are live
@@ -328,8 +324,9 @@ __device__ void select_next(const GrowArgs& A) {
     J.f = L.f;
     J.b = L.b;
     J.build_left = bl;
-    J.parent_slot = pslot;
+    J.parent_slot = L.slot;
     J.new_slot = new_slot;
+    J.depth = (int32_t)(d + 1);
     J.src = (d == 0) ? nullptr : ((d & 1) ? A.rows1 : A.rows0);
     J.dst = ((d + 1) & 1) ? A.rows1 : A.rows0;
     J.s = s;
@@ -339,15 +336,14 @@ __device__ void select_next(const GrowArgs& A) {
         J.tot[i] = L.tot[i];
         J.left[i] = L.left[i];
     }
-    J.zero_ptr = A.hist + (size_t)new_slot * slot_elems(A.F);
-    J.zero_count = (int64_t)slot_elems(A.F);
+    J.new_hist = A.hist + (size_t)new_slot * slot_elems(A.F);
     J.cursor[0] = (unsigned long long)s;
     J.cursor[1] = (unsigned long long)(s + cl);
     HistJob& H = st->hist;
     H.rows = J.dst;
     H.lo = bl ? s : s + cl;
     H.hi = bl ? s + cl : e;
-    H.out = J.zero_ptr;
+    H.out = J.new_hist;
     H.active = 1;
     st->active = 1;
 }
@@ -362,6 +358,15 @@ __global__ void __launch_bounds__(SB) k_scan(GrowArgs A) {
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
     const int f = blockIdx.x * (SB / WAVE) + w;
     const ScanParams sp = {(double)A.lam, (double)A.gamma, (double)A.mcw, A.msl};
+    {
+        // the next split builds its child into slot n_leaves (select_next): clear it now
+        const int next_slot = st->n_leaves;
+        if (next_slot < A.max_leaves) {
+            int64_t* z = A.hist + (size_t)next_slot * slot_elems(A.F);
+            const int64_t ne = (int64_t)slot_elems(A.F);
+            for (int64_t i = (int64_t)blockIdx.x * SB + threadIdx.x; i < ne; i += (int64_t)gridDim.x * SB) z[i] = 0;
+        }
+    }
     if (f < A.F) {
         const int nb = max(0, min(NB, A.nbins[f]));
         const bool use = A.fmask[f] != 0;
@@ -431,6 +436,10 @@ __global__ void __launch_bounds__(SB) k_scan(GrowArgs A) {
         if (ROOT) {
             LeafRec L;
             L.node = 0;
+            L.depth = 0;
+            L.slot = 0;
+            L.s = 0;
+            L.e = A.n;
             L.tot[0] = q->tot_g;
             L.tot[1] = q->tot_h;
             L.tot[2] = A.n;
@@ -442,10 +451,17 @@ __global__ void __launch_bounds__(SB) k_scan(GrowArgs A) {
             st->n_active = 1;
         } else {
             const SplitJob& J = st->job;
-            const bool capped = A.depth[J.nl] >= A.max_depth;
+            const bool capped = J.depth >= A.max_depth;
             LeafRec Ll, Lr;
             Ll.node = J.nl;
             Lr.node = J.nr;
+            Ll.depth = Lr.depth = J.depth;
+            Ll.s = J.s;
+            Ll.e = J.mid;
+            Lr.s = J.mid;
+            Lr.e = J.e;
+            Ll.slot = J.build_left ? J.new_slot : J.parent_slot;
+            Lr.slot = J.build_left ? J.parent_slot : J.new_slot;
             for (int i = 0; i < 3; ++i) {
                 Ll.tot[i] = J.left[i];
                 Lr.tot[i] = J.tot[i] - J.left[i];
@@ -456,8 +472,6 @@ __global__ void __launch_bounds__(SB) k_scan(GrowArgs A) {
             A.seg_hi[J.nl] = J.mid;
             A.seg_lo[J.nr] = J.mid;
             A.seg_hi[J.nr] = J.e;
-            A.slot_of[J.build_left ? J.nl : J.nr] = J.new_slot;
-            A.slot_of[J.build_left ? J.nr : J.nl] = J.parent_slot;
             A.value[J.nl] = node_value(Ll.tot, q, A.lr, A.lam);
             A.value[J.nr] = node_value(Lr.tot, q, A.lr, A.lam);
             const int na = st->n_active;
@@ -495,7 +509,6 @@ size_t carve_grow(char* base, int64_t n, int F, int max_leaves, GrowArgs* A) {
     a.rows0 = c.take<uint32_t>((size_t)(n > 0 ? n : 1));
     a.rows1 = c.take<uint32_t>((size_t)(n > 0 ? n : 1));
     a.hist = c.take<int64_t>((size_t)max_leaves * 3 * (size_t)F * NB);
-    a.slot_of = c.take<int32_t>(N);
     a.path = c.take<uint8_t>(N * (size_t)F);
     a.leaf = c.take<LeafRec>(N);
     a.seg_lo = c.take<int64_t>(N);
@@ -566,6 +579,7 @@ int yabt_grow(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int
     const int tiles = (F + HFL - 1) / HFL;
     k_quant_clear<<<1, 1, 0, stream>>>(A.q);
     k_setup<<<launch_grid(n, SB * 16, 1024), SB, 0, stream>>>(A);
+    k_setup_finish<<<1, 1, 0, stream>>>(A);
     const int rc = root_chunks(n, tiles);
     k_hist_root<<<tiles * rc, HBLOCK, 0, stream>>>(bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, A.dflt, A.q,
                                                    A.hist, rc, 1, &A.st->done);

@@ -47,13 +47,11 @@ __device__ __forceinline__ void store_bins(int64_t* slot, int F, int f, int lane
 // the sum over all 256 bins (exact; a no-op when nothing was skipped).
 __device__ __forceinline__ void fill_default(int64_t g4[4], int64_t h4[4], int64_t c4[4], int d, const int64_t tot[3],
                                              bool counts, int lane) {
-    int64_t sg = g4[0] + g4[1] + g4[2] + g4[3];
-    int64_t sh = h4[0] + h4[1] + h4[2] + h4[3];
-    int64_t sc = c4[0] + c4[1] + c4[2] + c4[3];
-    sg = wave_sum<int64_t>(sg);
-    sh = wave_sum<int64_t>(sh);
-    sc = wave_sum<int64_t>(sc);
-    if (d >= 0 && (d >> 2) == lane) {
+    if (d < 0) return;
+    const int64_t sg = wave_sum_i64(g4[0] + g4[1] + g4[2] + g4[3]);
+    const int64_t sh = wave_sum_i64(h4[0] + h4[1] + h4[2] + h4[3]);
+    const int64_t sc = counts ? wave_sum_i64(c4[0] + c4[1] + c4[2] + c4[3]) : 0;
+    if ((d >> 2) == lane) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             if ((d & 3) == j) {
@@ -64,9 +62,16 @@ __device__ __forceinline__ void fill_default(int64_t g4[4], int64_t h4[4], int64
     }
 }
 
+// (sel, b) of `other` beats mine: larger sel, then lower bin; b < 0 never wins.
+__device__ __forceinline__ bool split_beats(double os, int ob, double s, int b) {
+    return ob >= 0 && (b < 0 || os > s || (os == s && ob < b));
+}
+
 // One wave scans one feature; lane l holds bins 4l..4l+3 (g, h, count).
 // Every lane returns the feature's record; t256 receives the totals over all
-// 256 bins (the node totals, used for node values).
+// 256 bins (the node totals).  Prefix sums use DPP row shifts plus scalar row
+// totals, the argmax DPP row rotations (every lane of a row ends with the
+// row's winner) plus the four row winners.
 __device__ inline ScanRec scan_feature(const int64_t g4[4], const int64_t h4[4], const int64_t c4[4], int nb,
                                        double ig, double ih, const ScanParams& sp, double bo, int lane,
                                        int64_t t256[3]) {
@@ -80,18 +85,18 @@ __device__ inline ScanRec scan_feature(const int64_t g4[4], const int64_t h4[4],
         ph[j] = ph[j - 1] + h4[j];
         pc[j] = pc[j - 1] + c4[j];
     }
-    const int64_t og = wave_excl_scan<int64_t>(pg[3], lane);
-    const int64_t oh = wave_excl_scan<int64_t>(ph[3], lane);
-    const int64_t oc = wave_excl_scan<int64_t>(pc[3], lane);
+    const int64_t og = wave_incl_scan_i64(pg[3], lane) - pg[3];
+    const int64_t oh = wave_incl_scan_i64(ph[3], lane) - ph[3];
+    const int64_t oc = wave_incl_scan_i64(pc[3], lane) - pc[3];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         pg[j] += og;
         ph[j] += oh;
         pc[j] += oc;
     }
-    t256[0] = __shfl(pg[3], WAVE - 1, WAVE);
-    t256[1] = __shfl(ph[3], WAVE - 1, WAVE);
-    t256[2] = __shfl(pc[3], WAVE - 1, WAVE);
+    t256[0] = readlane64(pg[3], WAVE - 1);
+    t256[1] = readlane64(ph[3], WAVE - 1);
+    t256[2] = readlane64(pc[3], WAVE - 1);
     // totals over the feature's used bins b < nb (grow.c:151-156)
     int64_t Gt = 0, Ht = 0, Ct = 0;
     if (nb > 0) {
@@ -104,9 +109,9 @@ __device__ inline ScanRec scan_feature(const int64_t g4[4], const int64_t h4[4],
                 vh = ph[j];
                 vc = pc[j];
             }
-        Gt = __shfl(vg, src, WAVE);
-        Ht = __shfl(vh, src, WAVE);
-        Ct = __shfl(vc, src, WAVE);
+        Gt = readlane64(vg, src);
+        Ht = readlane64(vh, src);
+        Ct = readlane64(vc, src);
     }
     const double G = (double)Gt * ig, H = (double)Ht * ih;
     const double parent = G * G / (H + sp.lam);
@@ -130,38 +135,56 @@ __device__ inline ScanRec scan_feature(const int64_t g4[4], const int64_t h4[4],
             }
         }
     }
-    ScanRec r;
-    r.sel = best_sel;
-    r.gain = best_gain;
-    r.b = best_j < 0 ? -1 : 4 * lane + best_j;
-    r.pad = 0;
-    r.left[0] = r.left[1] = r.left[2] = 0;
+    // lane-best record kept in place; the wave argmax moves only (sel, b)
+    int64_t lg = 0, lh = 0, lc = 0;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
         if (best_j == j) {
-            r.left[0] = pg[j];
-            r.left[1] = ph[j];
-            r.left[2] = pc[j];
+            lg = pg[j];
+            lh = ph[j];
+            lc = pc[j];
         }
-    // wave argmax: larger sel, then lower bin; lanes without a valid bin lose
+    double s = best_sel;
+    int b = best_j < 0 ? -1 : 4 * lane + best_j;
+#define YABT_ARGMAX_STEP(M)                                                    \
+    {                                                                          \
+        const double os = dpp_f64<DPP_ROW_ROR + (M)>(s);                     \
+        const int ob = (int)dpp32<DPP_ROW_ROR + (M)>((uint32_t)b);           \
+        if (split_beats(os, ob, s, b)) {                                       \
+            s = os;                                                            \
+            b = ob;                                                            \
+        }                                                                      \
+    }
+    YABT_ARGMAX_STEP(8) YABT_ARGMAX_STEP(4) YABT_ARGMAX_STEP(2) YABT_ARGMAX_STEP(1)
+#undef YABT_ARGMAX_STEP
+    // rows 0..3: each row now holds its winner in every lane
+    double ws = readlane_f64(s, 0);
+    int wb = __builtin_amdgcn_readlane(b, 0);
 #pragma unroll
-    for (int dd = WAVE / 2; dd > 0; dd >>= 1) {
-        const double os = __shfl_xor(r.sel, dd, WAVE);
-        const double ogn = __shfl_xor(r.gain, dd, WAVE);
-        const int ob = __shfl_xor(r.b, dd, WAVE);
-        const int64_t l0 = __shfl_xor(r.left[0], dd, WAVE);
-        const int64_t l1 = __shfl_xor(r.left[1], dd, WAVE);
-        const int64_t l2 = __shfl_xor(r.left[2], dd, WAVE);
-        const bool take = ob >= 0 && (r.b < 0 || os > r.sel || (os == r.sel && ob < r.b));
-        if (take) {
-            r.sel = os;
-            r.gain = ogn;
-            r.b = ob;
-            r.left[0] = l0;
-            r.left[1] = l1;
-            r.left[2] = l2;
+    for (int row = 1; row < 4; ++row) {
+        const double os = readlane_f64(s, 16 * row);
+        const int ob = __builtin_amdgcn_readlane(b, 16 * row);
+        if (split_beats(os, ob, ws, wb)) {
+            ws = os;
+            wb = ob;
         }
     }
+    ScanRec r;
+    r.pad = 0;
+    if (wb < 0) {
+        r.sel = -INFINITY;
+        r.gain = -INFINITY;
+        r.b = -1;
+        r.left[0] = r.left[1] = r.left[2] = 0;
+        return r;
+    }
+    const int src = wb >> 2;     // the lane whose lane-best is the winner
+    r.sel = ws;
+    r.b = wb;
+    r.gain = readlane_f64(best_gain, src);
+    r.left[0] = readlane64(lg, src);
+    r.left[1] = readlane64(lh, src);
+    r.left[2] = readlane64(lc, src);
     return r;
 }
 
@@ -180,12 +203,20 @@ __device__ inline float path_boost(const uint8_t* path, const float* imat, float
             const float v = imat[(size_t)p * F + f];
             if (v > m) m = v;
         }
-#pragma unroll
-    for (int dd = WAVE / 2; dd > 0; dd >>= 1) {
-        const float o = __shfl_xor(m, dd, WAVE);
-        if (o > m) m = o;
+#define YABT_MAX_STEP(M)                                                       \
+    {                                                                          \
+        const float o = __uint_as_float(dpp32<DPP_ROW_ROR + (M)>(__float_as_uint(m))); \
+        if (o > m) m = o;                                                      \
     }
-    return 1.0f + ib * m;
+    YABT_MAX_STEP(8) YABT_MAX_STEP(4) YABT_MAX_STEP(2) YABT_MAX_STEP(1)
+#undef YABT_MAX_STEP
+    float r = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(m), 0));
+#pragma unroll
+    for (int row = 1; row < 4; ++row) {
+        const float o = __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(m), 16 * row));
+        if (o > r) r = o;
+    }
+    return 1.0f + ib * r;
 }
 
 // Feature-major reduction of one node's records (grow.c:181-192), NT threads;
