@@ -41,7 +41,7 @@ struct Quant {
     uint32_t hmin_key;         // order-preserving key of min h
     uint32_t hmax_key;         // order-preserving key of max h
     int32_t nonfinite;         // any g or h is inf/nan
-    int32_t const_h;           // every h equal and nonzero: counts = sum q(h) / hq_const
+    int32_t const_h;           // every h equal and nonzero: sum q(h) = count * hq_const
     int64_t hq_const;
     int64_t tot_g, tot_h;      // sum of q(g), q(h) over all rows (root totals)
     uint32_t ticket;
@@ -84,6 +84,11 @@ __device__ __forceinline__ uint64_t dpp64(uint64_t v) {
 template <int CTRL>
 __device__ __forceinline__ double dpp_f64(double v) {
     return __longlong_as_double((long long)dpp64<CTRL>((uint64_t)__double_as_longlong(v)));
+}
+
+// Number of set bits of mask in the lanes below this one.
+__device__ __forceinline__ uint32_t lane_prefix(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));
 }
 
 constexpr int DPP_ROW_SHR = 0x110;    // row_shr:n   = 0x110 + n

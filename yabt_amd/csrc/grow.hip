@@ -18,14 +18,17 @@
 //
 // Launch sequence of one tree (caller's stream):
 //   k_quant_clear, k_setup   max|g|,|h| -> shifts; table init; clear slot 0
+//   k_setup_finish           shifts, constant-hessian detection, tree state
 //   k_hist_root              streaming histogram of all rows (+ root totals)
 //   k_scan<ROOT>             default-bin fill, scan, controller: first split
 //   max_leaves - 1 times (each kernel returns at once once the tree is done):
-//     k_split_partition      one pass: children's rows to the other row list,
-//                            written through two atomic cursors (left, right)
+//     k_split_partition      clear the built child's slot; one pass: the
+//                            children's rows to the other row list, written
+//                            through two atomic cursors (left, right)
 //     k_hist_gather          histogram of the smaller child
-//     k_scan<SPLIT>          fill, sibling = parent - child in place, scan
-//                            both children, controller picks the next split
+//     k_scan<SPLIT>          fill, sibling = parent - child, scan both
+//                            children (one wave each), the last block picks
+//                            the next split
 //
 // The left child's size is known exactly before partitioning (the count prefix
 // at the chosen bin), so the partition needs no counting pass and the smaller
@@ -54,6 +57,7 @@ constexpr int SB = 256;                        // threads per scan / partition /
 constexpr int PART_IPT = 16;                   // rows per thread per partition tile
 constexpr int PART_TILE = SB * PART_IPT;
 constexpr int PART_MAX_BLOCKS = 1024;
+constexpr int SCAN_FEATS = 4;                  // features per scan block
 
 // Best split of one live leaf (grow.c's leaf_node/leaf_gain/leaf_f/leaf_b
 // table, grow.c:284-287, plus the node's exact totals).
@@ -77,7 +81,7 @@ struct SplitJob {
     int64_t s, e, mid;
     int64_t tot[3];            // parent totals
     int64_t left[3];           // left-child totals
-    int64_t* new_hist;         // the built child's slot (cleared by the previous scan launch)
+    int64_t* new_hist;         // the built child's slot, cleared by the partition launch
     unsigned long long cursor[2];   // next write position, left / right
 };
 
@@ -131,7 +135,6 @@ struct GrowArgs {
 
 __device__ __forceinline__ size_t slot_elems(int F) { return (size_t)3 * (size_t)F * NB; }
 
-__device__ __forceinline__ bool tree_done(const GrowState* st) { return *(volatile const int32_t*)&st->done != 0; }
 
 // ---------------------------------------------------------------------------
 // setup
@@ -183,17 +186,25 @@ __global__ void k_setup_finish(GrowArgs A) {
 // ---------------------------------------------------------------------------
 
 // Rows of [s, e) with bin <= b go to [s, mid), the others to [mid, e) of the
-// children's row list.  Each block compacts a tile in order and reserves its
-// output ranges with one atomic add per side, so rows stay grouped by tile;
-// the order inside a child does not affect any result (sums are exact).
+// children's row list.  A block takes tiles of PART_TILE rows; a thread holds
+// rows t0 + j * SB + tid (j < PART_IPT), so each of its loads is coalesced
+// across the block and all row-id loads, then all bin loads, are in flight
+// together.  Waves compact with ballots and lane prefixes; the block reserves
+// its output ranges with one atomic add per side, so the order inside a child
+// depends on the schedule, which no result does (sums are exact).
+// Every block first clears its share of the slot the gather adds into next.
 __global__ void __launch_bounds__(SB) k_split_partition(const uint8_t* __restrict__ bins_fm, int64_t ld,
-                                                        GrowState* st) {
-    if (tree_done(st) || !st->active) return;
+                                                        GrowState* st, int64_t slot_n) {
+    // independent loads first
+    const int32_t done = st->done, active = st->active;
     SplitJob& J = st->job;
     const int64_t s = J.s, e = J.e;
     const int fcol = J.f, b = J.b;
     const uint32_t* src = J.src;
     uint32_t* dst = J.dst;
+    int64_t* z = J.new_hist;
+    if (done || !active) return;
+    for (int64_t i = (int64_t)blockIdx.x * SB + threadIdx.x; i < slot_n; i += (int64_t)gridDim.x * SB) z[i] = 0;
     const int64_t m = e - s;
     const int64_t tiles = (m + PART_TILE - 1) / PART_TILE;
     const int nblk = (int)min((int64_t)gridDim.x, max(tiles, (int64_t)1));
@@ -202,37 +213,59 @@ __global__ void __launch_bounds__(SB) k_split_partition(const uint8_t* __restric
     const int64_t lo = s + (int64_t)blockIdx.x * tpb * PART_TILE;
     const int64_t hi = min(e, lo + tpb * PART_TILE);
     const uint8_t* col = bins_fm + (size_t)fcol * ld;
-    __shared__ uint32_t s_wave[SB / WAVE];
-    __shared__ unsigned long long s_base[2];
+    const int w = threadIdx.x / WAVE;
+    __shared__ uint32_t s_cnt[SB / WAVE][2];
+    __shared__ unsigned long long s_base[SB / WAVE][2];
     for (int64_t t0 = lo; t0 < hi; t0 += PART_TILE) {
-        const int64_t a = t0 + (int64_t)threadIdx.x * PART_IPT;
         uint32_t rid[PART_IPT];
-        uint32_t flags = 0, nv = 0;
 #pragma unroll
         for (int j = 0; j < PART_IPT; ++j) {
-            const int64_t i = a + j;
-            if (i < hi) {
-                rid[j] = src ? src[i] : (uint32_t)i;
-                flags |= ((int)col[rid[j]] <= b ? 1u : 0u) << j;
-                ++nv;
-            }
+            const int64_t i = min(t0 + (int64_t)j * SB + threadIdx.x, hi - 1);
+            rid[j] = src ? src[i] : (uint32_t)i;
         }
-        const uint32_t nl = __popc(flags), nr = nv - nl;
-        uint32_t tl, tr;
-        const uint32_t ol = block_excl_scan<SB, uint32_t>(nl, s_wave, &tl);
-        const uint32_t orr = block_excl_scan<SB, uint32_t>(nr, s_wave, &tr);
-        if (threadIdx.x == 0) {
-            s_base[0] = atomicAdd(&J.cursor[0], (unsigned long long)tl);
-            s_base[1] = atomicAdd(&J.cursor[1], (unsigned long long)tr);
+        uint32_t bv[PART_IPT];
+#pragma unroll
+        for (int j = 0; j < PART_IPT; ++j) bv[j] = col[rid[j]];
+        uint32_t left = 0, valid = 0, nl = 0, nv = 0;
+#pragma unroll
+        for (int j = 0; j < PART_IPT; ++j) {
+            const bool v = t0 + (int64_t)j * SB + threadIdx.x < hi;
+            const bool l = v && (int)bv[j] <= b;
+            valid |= (v ? 1u : 0u) << j;
+            left |= (l ? 1u : 0u) << j;
+            nl += (uint32_t)__popcll(__ballot(l));
+            nv += (uint32_t)__popcll(__ballot(v));
+        }
+        if ((threadIdx.x & (WAVE - 1)) == 0) {
+            s_cnt[w][0] = nl;
+            s_cnt[w][1] = nv - nl;
         }
         __syncthreads();
-        uint64_t pl = s_base[0] + ol, pr = s_base[1] + orr;
+        if (threadIdx.x == 0) {
+            uint32_t tl = 0, tr = 0;
+            for (int i = 0; i < SB / WAVE; ++i) {
+                tl += s_cnt[i][0];
+                tr += s_cnt[i][1];
+            }
+            unsigned long long bl = atomicAdd(&J.cursor[0], (unsigned long long)tl);
+            unsigned long long br = atomicAdd(&J.cursor[1], (unsigned long long)tr);
+            for (int i = 0; i < SB / WAVE; ++i) {
+                s_base[i][0] = bl;
+                s_base[i][1] = br;
+                bl += s_cnt[i][0];
+                br += s_cnt[i][1];
+            }
+        }
+        __syncthreads();
+        uint64_t pl = s_base[w][0], pr = s_base[w][1];
 #pragma unroll
         for (int j = 0; j < PART_IPT; ++j) {
-            if ((uint32_t)j < nv) {
-                if ((flags >> j) & 1u) dst[pl++] = rid[j];
-                else dst[pr++] = rid[j];
-            }
+            const bool v = (valid >> j) & 1u, l = (left >> j) & 1u;
+            const uint64_t ml = __ballot(l), mr = __ballot(v && !l);
+            if (l) dst[pl + lane_prefix(ml)] = rid[j];
+            else if (v) dst[pr + lane_prefix(mr)] = rid[j];
+            pl += (uint64_t)__popcll(ml);
+            pr += (uint64_t)__popcll(mr);
         }
         __syncthreads();
     }
@@ -247,15 +280,15 @@ __device__ __forceinline__ float node_value(const int64_t tot[3], const Quant* q
     return (float)(-lr * G / (H + lam));
 }
 
-__device__ __forceinline__ void leaf_from_record(LeafRec& L, const ScanRec* rec, int bf, bool capped) {
-    if (bf >= 0) {
-        const ScanRec& r = rec[bf];
-        L.gain = (float)(capped ? -INFINITY : r.gain);
-        L.f = bf;
-        L.b = r.b;
-        L.left[0] = r.left[0];
-        L.left[1] = r.left[1];
-        L.left[2] = r.left[2];
+// r: the node's best record, or nullptr when no feature has a valid split.
+__device__ __forceinline__ void leaf_from_record(LeafRec& L, const ScanRec* r, bool capped) {
+    if (r) {
+        L.gain = (float)(capped ? -INFINITY : r->gain);
+        L.f = r->f;
+        L.b = r->b;
+        L.left[0] = r->left[0];
+        L.left[1] = r->left[1];
+        L.left[2] = r->left[2];
     } else {
         L.gain = -INFINITY;
         L.f = -1;
@@ -265,23 +298,24 @@ __device__ __forceinline__ void leaf_from_record(LeafRec& L, const ScanRec* rec,
 }
 
 // Pick the next split (grow.c:321-350) and write its job, or finish the tree.
+template <int NT>
 __device__ void select_next(const GrowArgs& A) {
     GrowState* st = A.st;
-    __shared__ double s_key[SB / WAVE];
-    __shared__ int s_idx[SB / WAVE];
+    __shared__ double s_key[NT / WAVE];
+    __shared__ int s_idx[NT / WAVE];
     const int n_active = st->n_active, n_leaves = st->n_leaves;
     int k = -1;
     if (n_leaves < A.max_leaves) {
         double key = -INFINITY;
         int idx = INT_MAX;
-        for (int a = threadIdx.x; a < n_active; a += SB) {
+        for (int a = threadIdx.x; a < n_active; a += NT) {
             const float g = A.leaf[a].gain;
             if (g > 0.0f && better((double)g, a, key, idx)) {
                 key = (double)g;
                 idx = a;
             }
         }
-        block_argmax<SB>(key, idx, s_key, s_idx);
+        block_argmax<NT>(key, idx, s_key, s_idx);
         k = idx == INT_MAX ? -1 : idx;
     }
     if (k < 0) {
@@ -297,7 +331,7 @@ __device__ void select_next(const GrowArgs& A) {
     const int nid = L.node, nl = st->n_nodes, nr = nl + 1;
     // children inherit the parent's path plus f (grow.c:347-350)
     const uint8_t* pp = A.path + (size_t)nid * A.F;
-    for (int j = threadIdx.x; j < A.F; j += SB) {
+    for (int j = threadIdx.x; j < A.F; j += NT) {
         const uint8_t v = (j == L.f) ? (uint8_t)1 : pp[j];
         A.path[(size_t)nl * A.F + j] = v;
         A.path[(size_t)nr * A.F + j] = v;
@@ -327,8 +361,11 @@ __device__ void select_next(const GrowArgs& A) {
     J.parent_slot = L.slot;
     J.new_slot = new_slot;
     J.depth = (int32_t)(d + 1);
-    J.src = (d == 0) ? nullptr : ((d & 1) ? A.rows1 : A.rows0);
-    J.dst = ((d + 1) & 1) ? A.rows1 : A.rows0;
+    // rows1 = rows0 + (rows1 - rows0): pointer arithmetic instead of a select,
+    // which the compiler would turn into a two-entry table in scratch memory
+    const ptrdiff_t r1 = A.rows1 - A.rows0;
+    J.src = (d == 0) ? nullptr : A.rows0 + (d & 1) * r1;
+    J.dst = A.rows0 + ((d + 1) & 1) * r1;
     J.s = s;
     J.e = e;
     J.mid = s + cl;
@@ -348,88 +385,113 @@ __device__ void select_next(const GrowArgs& A) {
     st->active = 1;
 }
 
+// Scan launch: SCAN_FEATS features per block; the split form gives each
+// feature two waves, one per child (wave w: feature w % SCAN_FEATS, child
+// w / SCAN_FEATS).  Each block publishes its best record per child (thread 0
+// stores them and alone issues the release fence, so the fence covers only
+// those stores); the histogram stores follow the ticket.  The last block to
+// take a ticket is the controller.
 template <bool ROOT>
-__global__ void __launch_bounds__(SB) k_scan(GrowArgs A) {
+__global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : 2 * SCAN_FEATS * WAVE) k_scan(GrowArgs A) {
+    constexpr int NT = ROOT ? SCAN_FEATS * WAVE : 2 * SCAN_FEATS * WAVE;
+    constexpr int NC = ROOT ? 1 : 2;
     GrowState* st = A.st;
-    if (tree_done(st)) return;
     const Quant* q = A.q;
-    const bool derive = q->const_h != 0;     // no count channel: counts = h / hq_const
+    const SplitJob& J = st->job;
+    // independent loads first
+    const int32_t done = st->done;
+    const bool derive = q->const_h != 0;     // no h channel: sum q(h) = count * hq_const
     const int64_t hqc = q->hq_const;
+    const int bl = ROOT ? 1 : J.build_left;
+    const int parent_slot = ROOT ? 0 : J.parent_slot, new_slot = ROOT ? 0 : J.new_slot;
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-    const int f = blockIdx.x * (SB / WAVE) + w;
+    const int f = blockIdx.x * SCAN_FEATS + (w % SCAN_FEATS);
+    const int c = w / SCAN_FEATS;
+    const bool fok = f < A.F;
+    const int fc = min(f, A.F - 1);          // unconditional loads: issued together
+    const int nb_f = A.nbins[fc];
+    const uint8_t use_f = A.fmask[fc];
+    const int d_f = A.dflt ? A.dflt[fc] : -1;
+    if (done) return;
+    const int nb = fok ? max(0, min(NB, nb_f)) : 0;
+    const bool use = fok && use_f != 0;
+    const int d = fok ? d_f : -1;
     const ScanParams sp = {(double)A.lam, (double)A.gamma, (double)A.mcw, A.msl};
-    {
-        // the next split builds its child into slot n_leaves (select_next): clear it now
-        const int next_slot = st->n_leaves;
-        if (next_slot < A.max_leaves) {
-            int64_t* z = A.hist + (size_t)next_slot * slot_elems(A.F);
-            const int64_t ne = (int64_t)slot_elems(A.F);
-            for (int64_t i = (int64_t)blockIdx.x * SB + threadIdx.x; i < ne; i += (int64_t)gridDim.x * SB) z[i] = 0;
-        }
-    }
-    if (f < A.F) {
-        const int nb = max(0, min(NB, A.nbins[f]));
-        const bool use = A.fmask[f] != 0;
-        const int d = A.dflt ? A.dflt[f] : -1;
-        const size_t plane = (size_t)A.F * NB, at = (size_t)f * NB + 4 * lane;
-        int64_t t256[3];
+    const bool has_h = !derive;
+    const bool built = ROOT || (c == 0) == (bl != 0);     // this wave scans the built child (the root: slot 0)
+    int64_t* hp = A.hist + (size_t)parent_slot * slot_elems(A.F);
+    int64_t* hn = A.hist + (size_t)new_slot * slot_elems(A.F);
+    __shared__ ScanRec s_rec[NT / WAVE];
+    __shared__ int s_last;
+    int64_t g4[4], h4[4], c4[4];
+    if (fok) {
+        int64_t tot[3];
         if (ROOT) {
-            const int64_t tot[3] = {q->tot_g, q->tot_h, A.n};
-            int64_t g4[4], h4[4], c4[4];
-            load_bins(A.hist, A.F, f, lane, g4, h4, c4);
-            fill_default(g4, h4, c4, d, tot, !derive, lane);
-            if (d >= 0 && (d >> 2) == lane) store_bins(A.hist, A.F, f, lane, g4, h4, c4);
-            if (derive)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) c4[j] = h4[j] / hqc;
-            ScanRec r = scan_feature(g4, h4, c4, nb, q->ig, q->ih, sp, 1.0, lane, t256);
-            if (!use) no_split(r);
-            if (lane == 0) A.rec[f] = r;
+            tot[0] = q->tot_g;
+            tot[1] = derive ? A.n * hqc : q->tot_h;
+            tot[2] = A.n;
         } else {
-            const SplitJob& J = st->job;
-            const int bl = J.build_left;
-            int64_t* hp = A.hist + (size_t)J.parent_slot * slot_elems(A.F);
-            int64_t* hn = A.hist + (size_t)J.new_slot * slot_elems(A.F);
-            int64_t btot[3];
-            for (int i = 0; i < 3; ++i) btot[i] = bl ? J.left[i] : J.tot[i] - J.left[i];
-            int64_t bg[4], bh[4], bc[4], sg4[4], sh4[4], sc4[4];
-            load_bins(hn, A.F, f, lane, bg, bh, bc);
-            load_bins(hp, A.F, f, lane, sg4, sh4, sc4);
-            fill_default(bg, bh, bc, d, btot, !derive, lane);
-            if (d >= 0 && (d >> 2) == lane) store_bins(hn, A.F, f, lane, bg, bh, bc);
+            for (int i = 0; i < 3; ++i) tot[i] = bl ? J.left[i] : J.tot[i] - J.left[i];
+        }
+        load_bins(hn, A.F, f, lane, g4, h4, c4, has_h);
+        fill_default(g4, h4, c4, d, tot, has_h, lane);
+        if (!built) {
+            int64_t pg[4], ph[4], pc[4];
+            load_bins(hp, A.F, f, lane, pg, ph, pc, has_h);
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                sg4[j] -= bg[j];
-                sh4[j] -= bh[j];
-                sc4[j] -= bc[j];
-                hp[at + j] = sg4[j];
-                hp[plane + at + j] = sh4[j];
-                hp[2 * plane + at + j] = sc4[j];
-            }
-            if (derive)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    bc[j] = bh[j] / hqc;
-                    sc4[j] = sh4[j] / hqc;
-                }
-            const float bo = (A.use_imat && use) ? path_boost(A.path + (size_t)J.nl * A.F, A.imat, A.ib, A.F, f, lane)
-                                                 : 1.0f;
-            for (int c = 0; c < 2; ++c) {
-                const bool built = (c == 0) == (bl != 0);
-                ScanRec r = built ? scan_feature(bg, bh, bc, nb, q->ig, q->ih, sp, (double)bo, lane, t256)
-                                  : scan_feature(sg4, sh4, sc4, nb, q->ig, q->ih, sp, (double)bo, lane, t256);
-                if (!use) no_split(r);
-                if (lane == 0) A.rec[(size_t)c * A.F + f] = r;
+                g4[j] = pg[j] - g4[j];
+                h4[j] = ph[j] - h4[j];
+                c4[j] = pc[j] - c4[j];
             }
         }
+        int64_t hs[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) hs[j] = derive ? c4[j] * hqc : h4[j];
+        const float bo = (!ROOT && A.use_imat && use)
+                             ? path_boost(A.path + (size_t)J.nl * A.F, A.imat, A.ib, A.F, f, lane)
+                             : 1.0f;
+        int64_t t256[3];
+        ScanRec r = scan_feature(g4, hs, c4, nb, q->ig, q->ih, sp, (double)bo, lane, t256);
+        if (!use) no_split(r);
+        r.f = f;
+        if (lane == 0) s_rec[w] = r;
+    } else if (lane == 0) {
+        no_split(s_rec[w]);
+        s_rec[w].f = -1;
     }
-    if (!last_block(&st->scan_ticket)) return;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int cc = 0; cc < NC; ++cc) {
+            int bi = cc * SCAN_FEATS;
+            for (int i = 1; i < SCAN_FEATS; ++i) {
+                const ScanRec& o = s_rec[cc * SCAN_FEATS + i];
+                if (rec_beats(o.sel, o.f, o.b, s_rec[bi].sel, s_rec[bi].f, s_rec[bi].b)) bi = cc * SCAN_FEATS + i;
+            }
+            A.rec[(size_t)cc * gridDim.x + blockIdx.x] = s_rec[bi];
+        }
+        __threadfence();
+        const uint32_t t = atomicAdd(&st->scan_ticket, 1u);
+        s_last = (t == gridDim.x - 1);
+    }
+    __syncthreads();
+    // every wave of the block has loaded its bins (barriers above): store
+    if (fok) {
+        if (built) {
+            if (d >= 0 && (d >> 2) == lane) store_bins(hn, A.F, f, lane, g4, h4, c4, has_h);
+        } else {
+            store_bins(hp, A.F, f, lane, g4, h4, c4, has_h);
+        }
+    }
+    if (!s_last) return;
+    __threadfence();
+    if (threadIdx.x == 0) st->scan_ticket = 0;
 
     // ---- controller (one block) ----
-    __shared__ int s_bf[2];
-    for (int c = 0; c < (ROOT ? 1 : 2); ++c) {
-        const int bf = reduce_records<SB>(A.rec + (size_t)c * A.F, A.F);
-        if (threadIdx.x == 0) s_bf[c] = bf;
+    __shared__ int s_bi[NC];
+    if (w < NC) {
+        const int bi = wave_best_record(A.rec + (size_t)w * gridDim.x, gridDim.x, lane);
+        if (lane == 0) s_bi[w] = bi < 0 ? -1 : w * (int)gridDim.x + bi;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -441,9 +503,9 @@ __global__ void __launch_bounds__(SB) k_scan(GrowArgs A) {
             L.s = 0;
             L.e = A.n;
             L.tot[0] = q->tot_g;
-            L.tot[1] = q->tot_h;
+            L.tot[1] = derive ? A.n * hqc : q->tot_h;
             L.tot[2] = A.n;
-            leaf_from_record(L, A.rec, s_bf[0], 0 >= A.max_depth);
+            leaf_from_record(L, s_bi[0] >= 0 ? A.rec + s_bi[0] : nullptr, 0 >= A.max_depth);
             A.leaf[0] = L;
             A.value[0] = node_value(L.tot, q, A.lr, A.lam);
             st->n_nodes = 1;
@@ -466,8 +528,8 @@ __global__ void __launch_bounds__(SB) k_scan(GrowArgs A) {
                 Ll.tot[i] = J.left[i];
                 Lr.tot[i] = J.tot[i] - J.left[i];
             }
-            leaf_from_record(Ll, A.rec, s_bf[0], capped);
-            leaf_from_record(Lr, A.rec + A.F, s_bf[1], capped);
+            leaf_from_record(Ll, s_bi[0] >= 0 ? A.rec + s_bi[0] : nullptr, capped);
+            leaf_from_record(Lr, s_bi[1] >= 0 ? A.rec + s_bi[1] : nullptr, capped);
             A.seg_lo[J.nl] = J.s;
             A.seg_hi[J.nl] = J.mid;
             A.seg_lo[J.nr] = J.mid;
@@ -483,7 +545,7 @@ __global__ void __launch_bounds__(SB) k_scan(GrowArgs A) {
         }
     }
     __syncthreads();
-    select_next(A);
+    select_next<NT>(A);
 }
 
 // out[row] = leaf node id, from each leaf's segment of the final row lists.
@@ -583,14 +645,15 @@ int yabt_grow(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int
     const int rc = root_chunks(n, tiles);
     k_hist_root<<<tiles * rc, HBLOCK, 0, stream>>>(bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, A.dflt, A.q,
                                                    A.hist, rc, 1, &A.st->done);
-    const int scan_grid = (F + SB / WAVE - 1) / (SB / WAVE);
-    k_scan<true><<<scan_grid, SB, 0, stream>>>(A);
+    const int scan_grid = (F + SCAN_FEATS - 1) / SCAN_FEATS;
+    k_scan<true><<<scan_grid, SCAN_FEATS * WAVE, 0, stream>>>(A);
     const int pgrid = launch_grid(n, PART_TILE, PART_MAX_BLOCKS);
+    const int64_t slot_n = (int64_t)3 * F * NB;
     for (int it = 1; it < max_leaves; ++it) {
-        k_split_partition<<<pgrid, SB, 0, stream>>>(bins_fm, ld_fm, A.st);
+        k_split_partition<<<pgrid, SB, 0, stream>>>(bins_fm, ld_fm, A.st, slot_n);
         k_hist_gather<<<tiles * GATHER_MAX_CHUNKS, HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, A.q, 0.0,
                                                                         0.0, A.dflt, &A.st->hist, 1, &A.st->done);
-        k_scan<false><<<scan_grid, SB, 0, stream>>>(A);
+        k_scan<false><<<scan_grid, 2 * SCAN_FEATS * WAVE, 0, stream>>>(A);
     }
     return launch_status("yabt_grow launch");
 }

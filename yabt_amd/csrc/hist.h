@@ -16,7 +16,8 @@
 //   * dflt[f] (may be NULL): rows whose bin equals dflt[f] are not added; the
 //     caller restores that bin as node total minus the other bins (the
 //     default-bin fill of grow.c:101-106, here exact);
-//   * CNT = false: no count channel (every h equal): counts = sum q(h) / q(h).
+//   * HCH = false: no h channel (every h equal): sum q(h) = count * q(h), and
+//     the h plane of the output is left untouched.
 #pragma once
 
 #include "common.h"
@@ -36,39 +37,37 @@ struct HistLds {
     uint32_t c[NB * HFL];
 };
 
-template <bool CNT>
+template <bool HCH>
 __device__ __forceinline__ void hist_clear(HistLds& L) {
     for (int i = threadIdx.x; i < NB * HFL; i += HBLOCK) {
         L.g[i] = 0;
-        L.h[i] = 0;
-        if (CNT) L.c[i] = 0;
+        if (HCH) L.h[i] = 0;
+        L.c[i] = 0;
     }
 }
 
 // Add the block's histogram into out[3][F][256] (entries that received no row
 // are skipped).
-template <bool CNT>
+template <bool HCH>
 __device__ __forceinline__ void hist_flush(HistLds& L, int64_t* out, int F, int f0) {
     const size_t plane = (size_t)F * NB;
     for (int i = threadIdx.x; i < NB * HFL; i += HBLOCK) {
         const int f = f0 + (i % HFL);
-        if (f >= F) continue;
-        const unsigned long long g = L.g[i], h = L.h[i];
-        const uint32_t c = CNT ? L.c[i] : 0u;
-        if (CNT ? c == 0 : (g == 0 && h == 0)) continue;
+        const uint32_t c = L.c[i];
+        if (f >= F || c == 0) continue;
         const size_t at = (size_t)f * NB + (size_t)(i / HFL);
-        atomicAdd((unsigned long long*)(out + at), g);
-        atomicAdd((unsigned long long*)(out + plane + at), h);
-        if (CNT) atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)c);
+        atomicAdd((unsigned long long*)(out + at), L.g[i]);
+        if (HCH) atomicAdd((unsigned long long*)(out + plane + at), L.h[i]);
+        atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)c);
     }
 }
 
-template <bool CNT>
+template <bool HCH>
 __device__ __forceinline__ void hist_add(HistLds& L, int b, int fl, uint64_t g, uint64_t h) {
     const int at = b * HFL + fl;
     atomicAdd(&L.g[at], (unsigned long long)g);
-    atomicAdd(&L.h[at], (unsigned long long)h);
-    if (CNT) atomicAdd(&L.c[at], 1u);
+    if (HCH) atomicAdd(&L.h[at], (unsigned long long)h);
+    atomicAdd(&L.c[at], 1u);
 }
 
 // Rows per block chunk for the streaming kernel: about two resident blocks
@@ -84,8 +83,9 @@ inline int root_chunks(int64_t n, int tiles) {
 
 // Streaming histogram of rows [0, n) from the feature-major bins.
 // Grid: tiles * chunks blocks, block -> (tile = bid / chunks, chunk = bid % chunks).
-// q_tot (may be NULL): the tile-0 blocks add sum q(g), sum q(h) of all rows.
-template <bool CNT>
+// q_tot (may be NULL): the tile-0 blocks add sum q(g), sum q(h) of all rows
+// (sum q(h) only with the h channel; without it the caller uses n * q(h)).
+template <bool HCH>
 __device__ __forceinline__ void hist_root_body(HistLds& L, const uint8_t* __restrict__ bins_fm, int64_t ld,
                                                const float* __restrict__ grad, const float* __restrict__ hess,
                                                int64_t n, int F, double scg, double sch,
@@ -102,7 +102,7 @@ __device__ __forceinline__ void hist_root_body(HistLds& L, const uint8_t* __rest
     if (f0 >= F || lo >= hi) return;
     const int d = (fok && dflt) ? dflt[f] : -1;
     const bool totals = q_tot != nullptr && tile == 0;
-    hist_clear<CNT>(L);
+    hist_clear<HCH>(L);
     __syncthreads();
     const uint8_t* col = bins_fm + (size_t)(fok ? f : f0) * ld;
     int64_t sum_g = 0, sum_h = 0;
@@ -111,7 +111,7 @@ __device__ __forceinline__ void hist_root_body(HistLds& L, const uint8_t* __rest
         uint64_t gq = 0, hq = 0;
         if (rl < hi) {
             gq = (uint64_t)quantise(grad[rl], scg);
-            hq = (uint64_t)quantise(hess[rl], sch);
+            if (HCH) hq = (uint64_t)quantise(hess[rl], sch);
         }
         sum_g += (int64_t)gq;
         sum_h += (int64_t)hq;
@@ -123,9 +123,9 @@ __device__ __forceinline__ void hist_root_body(HistLds& L, const uint8_t* __rest
         const int nv = (int)min((int64_t)HFL, max((int64_t)0, hi - base));
 #define YABT_ROOT_STEP(J)                                                        \
         {                                                                        \
-            const uint64_t gj = row_bcast64<J>(gq), hj = row_bcast64<J>(hq);     \
+            const uint64_t gj = row_bcast64<J>(gq), hj = HCH ? row_bcast64<J>(hq) : 0; \
             const int b = (int)((w[(J) >> 2] >> (8 * ((J) & 3))) & 0xffu);       \
-            if (fok && (J) < nv && b != d) hist_add<CNT>(L, b, fl, gj, hj);       \
+            if (fok && (J) < nv && b != d) hist_add<HCH>(L, b, fl, gj, hj);       \
         }
         YABT_ROOT_STEP(0) YABT_ROOT_STEP(1) YABT_ROOT_STEP(2) YABT_ROOT_STEP(3)
         YABT_ROOT_STEP(4) YABT_ROOT_STEP(5) YABT_ROOT_STEP(6) YABT_ROOT_STEP(7)
@@ -142,10 +142,10 @@ __device__ __forceinline__ void hist_root_body(HistLds& L, const uint8_t* __rest
         }
     }
     __syncthreads();
-    hist_flush<CNT>(L, out, F, f0);
+    hist_flush<HCH>(L, out, F, f0);
 }
 
-// count_mode 0: always count rows; 1: no count channel when q->const_h.
+// count_mode 0: all three channels; 1: no h channel when q->const_h.
 static __global__ void __launch_bounds__(HBLOCK) k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld,
                                                       const float* __restrict__ grad,
                                                       const float* __restrict__ hess, int64_t n, int F,
@@ -153,10 +153,12 @@ static __global__ void __launch_bounds__(HBLOCK) k_hist_root(const uint8_t* __re
                                                       const int32_t* __restrict__ dflt, Quant* q_tot,
                                                       int64_t* out, int chunks, int count_mode,
                                                       const int32_t* done) {
-    if (done && *(volatile const int32_t*)done) return;
-    __shared__ HistLds L;
+    const int32_t dn = done ? *done : 0;
     const double scg = q ? q->scg : scg_v, sch = q ? q->sch : sch_v;
-    if (count_mode && q && q->const_h)
+    const bool no_h = count_mode && q && q->const_h;
+    if (dn) return;
+    __shared__ HistLds L;
+    if (no_h)
         hist_root_body<false>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks);
     else
         hist_root_body<true>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks);
@@ -171,19 +173,28 @@ struct HistJob {
     int64_t* out;              // [3][F][256], cleared beforehand, added into
 };
 
-// Histogram of the rows listed at job->rows[lo:hi], bins gathered from the
+// Chunks of a gather launch over m rows.
+__host__ __device__ inline int gather_chunks(int64_t m) {
+    const int64_t c = (m + GATHER_MIN_ROWS - 1) / GATHER_MIN_ROWS;
+    return (int)(c < GATHER_MAX_CHUNKS ? c : GATHER_MAX_CHUNKS);
+}
+
+// Histogram of the rows listed at rows[lo:hi], bins gathered from the
 // row-major copy.  Grid: tiles * GATHER_MAX_CHUNKS blocks (chunk-minor); a
 // node uses ceil(m / GATHER_MIN_ROWS) chunks, the other blocks exit at once.
-template <bool CNT>
+// Each wave loads the row ids, g and h of its next 64 rows one step ahead, so
+// the dependent row-id -> g/h loads overlap the LDS clear and the adds.
+template <bool HCH>
 __device__ __forceinline__ void hist_gather_body(HistLds& L, const uint8_t* __restrict__ bins_rm, int64_t ld,
                                                  const float* __restrict__ grad, const float* __restrict__ hess,
                                                  int F, double scg, double sch, const int32_t* __restrict__ dflt,
-                                                 const HistJob* job) {
+                                                 const uint32_t* __restrict__ rows, int64_t jlo, int64_t jhi,
+                                                 int64_t* out) {
     const int tile = blockIdx.x / GATHER_MAX_CHUNKS, chunk = blockIdx.x % GATHER_MAX_CHUNKS;
     const int f0 = tile * HFL;
-    const int64_t jlo = job->lo, jhi = job->hi, m = jhi - jlo;
+    const int64_t m = jhi - jlo;
     if (f0 >= F || m <= 0) return;
-    const int nch = (int)min((int64_t)GATHER_MAX_CHUNKS, (m + GATHER_MIN_ROWS - 1) / GATHER_MIN_ROWS);
+    const int nch = gather_chunks(m);
     if (chunk >= nch) return;
     const int64_t per = ((m + nch - 1) / nch + WAVE - 1) / WAVE * WAVE;
     const int64_t lo = jlo + (int64_t)chunk * per, hi = min(jhi, lo + per);
@@ -193,20 +204,19 @@ __device__ __forceinline__ void hist_gather_body(HistLds& L, const uint8_t* __re
     const int f = f0 + fl;
     const bool fok = f < F;
     const int d = (fok && dflt) ? dflt[f] : -1;
-    const uint32_t* rows = job->rows;
-    int64_t* out = job->out;
-    hist_clear<CNT>(L);
+    int64_t i0 = lo + (int64_t)wave * WAVE;
+    uint32_t r = 0;
+    float gx = 0.0f, hx = 0.0f;
+    if (i0 + lane < hi) {
+        r = rows[i0 + lane];
+        gx = grad[r];
+        if (HCH) hx = hess[r];
+    }
+    hist_clear<HCH>(L);
     __syncthreads();
     const uint8_t* fbase = bins_rm + f0 + (fok ? fl : 0);
-    for (int64_t i0 = lo + (int64_t)wave * WAVE; i0 < hi; i0 += HSTEP) {
-        const int64_t il = i0 + lane;
-        uint32_t r = 0;
-        uint64_t gq = 0, hq = 0;
-        if (il < hi) {
-            r = rows[il];
-            gq = (uint64_t)quantise(grad[r], scg);
-            hq = (uint64_t)quantise(hess[r], sch);
-        }
+    for (; i0 < hi; i0 += HSTEP) {
+        const uint64_t gq = (uint64_t)quantise(gx, scg), hq = HCH ? (uint64_t)quantise(hx, sch) : 0;
         const int nv = (int)min((int64_t)HFL, max((int64_t)0, hi - (i0 + HFL * rg)));
         int bj[HFL];
 #define YABT_GATHER_LOAD(J)                                                       \
@@ -219,35 +229,51 @@ __device__ __forceinline__ void hist_gather_body(HistLds& L, const uint8_t* __re
         YABT_GATHER_LOAD(8) YABT_GATHER_LOAD(9) YABT_GATHER_LOAD(10) YABT_GATHER_LOAD(11)
         YABT_GATHER_LOAD(12) YABT_GATHER_LOAD(13) YABT_GATHER_LOAD(14) YABT_GATHER_LOAD(15)
 #undef YABT_GATHER_LOAD
+        // next step's rows
+        const int64_t in = i0 + HSTEP + lane;
+        uint32_t rn = 0;
+        float gn = 0.0f, hn = 0.0f;
+        if (in < hi) {
+            rn = rows[in];
+            gn = grad[rn];
+            if (HCH) hn = hess[rn];
+        }
 #define YABT_GATHER_ADD(J)                                                        \
         {                                                                         \
-            const uint64_t gj = row_bcast64<J>(gq), hj = row_bcast64<J>(hq);      \
-            if (bj[J] >= 0 && bj[J] != d) hist_add<CNT>(L, bj[J], fl, gj, hj);    \
+            const uint64_t gj = row_bcast64<J>(gq), hj = HCH ? row_bcast64<J>(hq) : 0; \
+            if (bj[J] >= 0 && bj[J] != d) hist_add<HCH>(L, bj[J], fl, gj, hj);    \
         }
         YABT_GATHER_ADD(0) YABT_GATHER_ADD(1) YABT_GATHER_ADD(2) YABT_GATHER_ADD(3)
         YABT_GATHER_ADD(4) YABT_GATHER_ADD(5) YABT_GATHER_ADD(6) YABT_GATHER_ADD(7)
         YABT_GATHER_ADD(8) YABT_GATHER_ADD(9) YABT_GATHER_ADD(10) YABT_GATHER_ADD(11)
         YABT_GATHER_ADD(12) YABT_GATHER_ADD(13) YABT_GATHER_ADD(14) YABT_GATHER_ADD(15)
 #undef YABT_GATHER_ADD
+        r = rn;
+        gx = gn;
+        hx = hn;
     }
     __syncthreads();
-    hist_flush<CNT>(L, out, F, f0);
+    hist_flush<HCH>(L, out, F, f0);
 }
 
+// job->active == 0 or *done != 0 (done may be NULL): nothing to do.
 static __global__ void __launch_bounds__(HBLOCK) k_hist_gather(const uint8_t* __restrict__ bins_rm, int64_t ld,
                                                         const float* __restrict__ grad,
                                                         const float* __restrict__ hess, int F, const Quant* q,
                                                         double scg_v, double sch_v,
                                                         const int32_t* __restrict__ dflt, const HistJob* job,
                                                         int count_mode, const int32_t* done) {
-    if (done && *(volatile const int32_t*)done) return;
-    if (!job->active) return;
-    __shared__ HistLds L;
+    // independent loads first: the job record, the done flag, the shifts
+    const HistJob jb = *job;
+    const int32_t dn = done ? *done : 0;
     const double scg = q ? q->scg : scg_v, sch = q ? q->sch : sch_v;
-    if (count_mode && q && q->const_h)
-        hist_gather_body<false>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, job);
+    const bool no_h = count_mode && q && q->const_h;
+    if (dn || !jb.active) return;
+    __shared__ HistLds L;
+    if (no_h)
+        hist_gather_body<false>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi, jb.out);
     else
-        hist_gather_body<true>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, job);
+        hist_gather_body<true>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi, jb.out);
 }
 
 }  // namespace yabt

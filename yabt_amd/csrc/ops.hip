@@ -34,6 +34,7 @@ __global__ void k_fill_i64(int64_t* p, int64_t v, int64_t count) {
 
 __global__ void k_set_hist_job(HistJob* j, const uint32_t* rows, int64_t lo, int64_t hi, int64_t* out) {
     j->active = 1;
+    j->pad = 0;
     j->rows = rows;
     j->lo = lo;
     j->hi = hi;
@@ -131,7 +132,7 @@ __global__ void __launch_bounds__(OB) k_scan_one(const int64_t* hist, int F, con
     const int f = blockIdx.x * (OB / WAVE) + w;
     if (f < F) {
         int64_t g4[4], h4[4], c4[4], t256[3];
-        load_bins(hist, F, f, lane, g4, h4, c4);
+        load_bins(hist, F, f, lane, g4, h4, c4, true);
         const int nb = max(0, min(NB, nbins[f]));
         ScanRec r = scan_feature(g4, h4, c4, nb, ldexp(1.0, -sg), ldexp(1.0, -sh), sp,
                                  (double)(boost ? boost[f] : 1.0f), lane, t256);

@@ -16,48 +16,50 @@ struct ScanRec {
     double sel;               // gain * boost[f]; what the argmax ranks
     double gain;              // true gain at the chosen bin
     int32_t b;                // chosen bin, -1: no valid split on this feature
-    int32_t pad;
+    int32_t f;                // feature (set by the caller)
     int64_t left[3];          // (sum q(g), sum q(h), count) of bins <= b
 };
 
-// Bins 4*lane .. 4*lane+3 of one feature of a histogram slot [3][F][256].
+// Bins 4*lane .. 4*lane+3 of one feature of a histogram slot [3][F][256];
+// has_h false: the h plane is not read (h4 is set to zero).
 __device__ __forceinline__ void load_bins(const int64_t* slot, int F, int f, int lane, int64_t g4[4], int64_t h4[4],
-                                          int64_t c4[4]) {
+                                          int64_t c4[4], bool has_h) {
     const size_t plane = (size_t)F * NB, at = (size_t)f * NB + 4 * lane;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         g4[j] = slot[at + j];
-        h4[j] = slot[plane + at + j];
+        h4[j] = has_h ? slot[plane + at + j] : 0;
         c4[j] = slot[2 * plane + at + j];
     }
 }
 
 __device__ __forceinline__ void store_bins(int64_t* slot, int F, int f, int lane, const int64_t g4[4],
-                                           const int64_t h4[4], const int64_t c4[4]) {
+                                           const int64_t h4[4], const int64_t c4[4], bool has_h) {
     const size_t plane = (size_t)F * NB, at = (size_t)f * NB + 4 * lane;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         slot[at + j] = g4[j];
-        slot[plane + at + j] = h4[j];
+        if (has_h) slot[plane + at + j] = h4[j];
         slot[2 * plane + at + j] = c4[j];
     }
 }
 
 // Restore the skipped default bin d of one feature: bin d += node total minus
-// the sum over all 256 bins (exact; a no-op when nothing was skipped).
+// the sum over all 256 bins (exact; a no-op when nothing was skipped).  has_h
+// false: the h channel is not kept (derived from the counts afterwards).
 __device__ __forceinline__ void fill_default(int64_t g4[4], int64_t h4[4], int64_t c4[4], int d, const int64_t tot[3],
-                                             bool counts, int lane) {
+                                             bool has_h, int lane) {
     if (d < 0) return;
     const int64_t sg = wave_sum_i64(g4[0] + g4[1] + g4[2] + g4[3]);
-    const int64_t sh = wave_sum_i64(h4[0] + h4[1] + h4[2] + h4[3]);
-    const int64_t sc = counts ? wave_sum_i64(c4[0] + c4[1] + c4[2] + c4[3]) : 0;
+    const int64_t sh = has_h ? wave_sum_i64(h4[0] + h4[1] + h4[2] + h4[3]) : 0;
+    const int64_t sc = wave_sum_i64(c4[0] + c4[1] + c4[2] + c4[3]);
     if ((d >> 2) == lane) {
 #pragma unroll
         for (int j = 0; j < 4; ++j)
             if ((d & 3) == j) {
                 g4[j] += tot[0] - sg;
-                h4[j] += tot[1] - sh;
-                if (counts) c4[j] += tot[2] - sc;
+                if (has_h) h4[j] += tot[1] - sh;
+                c4[j] += tot[2] - sc;
             }
     }
 }
@@ -72,7 +74,7 @@ __device__ __forceinline__ bool split_beats(double os, int ob, double s, int b) 
 // 256 bins (the node totals).  Prefix sums use DPP row shifts plus scalar row
 // totals, the argmax DPP row rotations (every lane of a row ends with the
 // row's winner) plus the four row winners.
-__device__ inline ScanRec scan_feature(const int64_t g4[4], const int64_t h4[4], const int64_t c4[4], int nb,
+__device__ __forceinline__ ScanRec scan_feature(const int64_t g4[4], const int64_t h4[4], const int64_t c4[4], int nb,
                                        double ig, double ih, const ScanParams& sp, double bo, int lane,
                                        int64_t t256[3]) {
     int64_t pg[4], ph[4], pc[4];
@@ -170,7 +172,7 @@ __device__ inline ScanRec scan_feature(const int64_t g4[4], const int64_t h4[4],
         }
     }
     ScanRec r;
-    r.pad = 0;
+    r.f = -1;
     if (wb < 0) {
         r.sel = -INFINITY;
         r.gain = -INFINITY;
@@ -217,6 +219,39 @@ __device__ inline float path_boost(const uint8_t* path, const float* imat, float
         if (o > r) r = o;
     }
     return 1.0f + ib * r;
+}
+
+// Record a beats record b in grow.c's feature order (grow.c:181-192): a valid
+// split beats none, then larger sel, then the lower feature.
+__device__ __forceinline__ bool rec_beats(double sa, int fa, int ba, double sb, int fb, int bb) {
+    return ba >= 0 && (bb < 0 || sa > sb || (sa == sb && fa < fb));
+}
+
+// One wave: index in rec[0, n) of the best record (-1: none valid).
+__device__ inline int wave_best_record(const ScanRec* rec, int n, int lane) {
+    double s = -INFINITY;
+    int f = INT_MAX, b = -1, idx = -1;
+    for (int i = lane; i < n; i += WAVE) {
+        const ScanRec& r = rec[i];
+        if (rec_beats(r.sel, r.f, r.b, s, f, b)) {
+            s = r.sel;
+            f = r.f;
+            b = r.b;
+            idx = i;
+        }
+    }
+#pragma unroll
+    for (int m = WAVE / 2; m > 0; m >>= 1) {
+        const double os = __shfl_xor(s, m, WAVE);
+        const int of = __shfl_xor(f, m, WAVE), ob = __shfl_xor(b, m, WAVE), oi = __shfl_xor(idx, m, WAVE);
+        if (rec_beats(os, of, ob, s, f, b)) {
+            s = os;
+            f = of;
+            b = ob;
+            idx = oi;
+        }
+    }
+    return idx;
 }
 
 // Feature-major reduction of one node's records (grow.c:181-192), NT threads;
