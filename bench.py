@@ -20,7 +20,14 @@ Also reported:
     oracle's restatement of it (kind "port"), on a bounded row sample of the
     same workload, timed on this host's cores.
 
+``roofline.traffic`` (HBM bytes per root-histogram launch) is read from the
+committed counter summary profiles/k_hist_root_10Mx100_traffic.md, made by two
+rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over ``bench.py --counters``,
+which launches a plain copy kernel of known size (for the counter scale) and
+the root-histogram kernel, three times each.
+
 Usage: python bench.py [--gpus 1] [--steps 5] [--warmup 1] [--no-cpu]
+       python bench.py --counters
 """
 
 from __future__ import annotations
@@ -28,6 +35,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import re
 import sys
 import time
 
@@ -113,6 +121,45 @@ def time_root_hist(torch, lay, g, h, reps=20):
     return float(np.mean(ms)), float(np.median(ms))
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_hist_root_10Mx100_traffic.md")
+COPY_ELEMS = 1 << 28          # fp32 elements of the copy kernel: 1 GiB read + 1 GiB written
+
+
+def counter_launches(torch, lay, g, h) -> None:
+    """Kernels for the rocprofv3 --pmc passes: a plain elementwise copy of
+    known size (torch.neg over 2^28 fp32: 1 GiB read, 1 GiB written) and the
+    root-histogram kernel, three launches each."""
+    from yabt_amd import grow_hip as G
+    from yabt_amd import _lib
+    dev = lay.fm.device
+    x = torch.ones(COPY_ELEMS, dtype=torch.float32, device=dev)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        torch.neg(x, out=y)
+    torch.cuda.synchronize()
+    del x, y
+    lib = _lib.load()
+    out = torch.zeros((3, lay.F, 256), dtype=torch.int64, device=dev)
+    _, (sg, sh) = G.hist(lay, g, h)
+    for _ in range(3):
+        _lib.check(lib.yabt_hist_accumulate(G._ptr(lay.fm), lay.ld_fm, G._ptr(lay.rm), lay.ld_rm,
+                                            G._ptr(g), G._ptr(h), lay.n, lay.F, None, 0, sg, sh,
+                                            None, G._ptr(out), G._stream(dev)),
+                   "yabt_hist_accumulate")
+    torch.cuda.synchronize()
+
+
+def committed_traffic():
+    """HBM bytes per root-histogram launch from the committed counter summary
+    (a line `traffic_bytes_per_launch: N`), or None."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            m = re.search(r"traffic_bytes_per_launch:\s*([0-9]+)", fh.read())
+        return int(m.group(1)) if m else None
+    except OSError:
+        return None
+
+
 def cpu_baseline(budget_s: float = 20.0) -> dict:
     """Reference grow.c (or its restatement) on a row sample of the workload."""
     from oracle import oracle as O
@@ -156,6 +203,8 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--rows", type=int, default=N_ROWS)
+    ap.add_argument("--counters", action="store_true",
+                    help="only launch the copy and root-histogram kernels for rocprofv3 --pmc")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the tree-growing path "
@@ -169,6 +218,11 @@ def main() -> None:
     log(f"[bench] generating {n} x {F} inputs on cuda:0")
     lay, g, h = gpu_inputs(torch, n, F)
     nbins = np.full(F, 256, np.int32)
+    if args.counters:
+        log("[bench] copy and root-histogram kernels for counter passes")
+        counter_launches(torch, lay, g, h)
+        log("[bench] done")
+        return
 
     log("[bench] root histogram kernel")
     root_mean_ms, root_med_ms = time_root_hist(torch, lay, g, h)
@@ -216,7 +270,7 @@ def main() -> None:
                       "frac_hbm": round(achieved / HBM_PEAK_GBS, 4)},
         "roofline": {"kernel": "k_hist_root<16> (streaming root histogram)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic()},
     }
     if not args.no_cpu:
         log("[bench] CPU baseline")
