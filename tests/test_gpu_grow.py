@@ -41,10 +41,13 @@ CASES = [
     dict(n=1, F=1, nb=256, kind="normal", max_leaves=31, msl=0),
     dict(n=100, F=3, nb=256, kind="normal", max_leaves=1),
     dict(n=50_000, F=30, nb=256, kind="normal", max_leaves=255, msl=20),
+    # n > 2^18: packed root histogram, three channels and constant hessian
+    dict(n=400_000, F=9, nb=256, kind="normal", max_leaves=63, msl=20),
+    dict(n=400_000, F=9, nb=64, kind="laplace", max_leaves=63, msl=20),
 ]
 
 
-@pytest.mark.parametrize("dflt", ["auto", None], ids=["skip-default-bin", "no-skip"])
+@pytest.mark.parametrize("dflt", ["auto", None, "modal"], ids=["skip-auto", "no-skip", "skip-every-feature"])
 @pytest.mark.parametrize("case", CASES, ids=lambda c: f"n{c['n']}F{c['F']}L{c['max_leaves']}")
 def test_grow_matches_oracle(case, dflt):
     c = dict(case)
@@ -62,6 +65,8 @@ def test_grow_matches_oracle(case, dflt):
         kw["fmask"] = rng.random(F) < 0.7
     assert not c
     nbins = np.full(F, nb, np.int32)
+    if dflt == "modal":   # skip each feature's most frequent bin, however rare
+        dflt = np.array([np.bincount(bins[:, f], minlength=256).argmax() for f in range(F)], np.int32)
     got, leaf = _grow_gpu(bins, g, h, nbins, default_bin=dflt, **kw)
     ref = O.grow(bins.T, g, h, mode=O.MODE_FIXED, nbins=nbins, **kw)
     bad = tree_arrays_equal(got, ref)

@@ -24,10 +24,21 @@ def _layouts(bins):
     return G.make_layouts(torch.from_numpy(bins), DEV)
 
 
+def _hist_f64(bins, g, h):
+    n, F = bins.shape
+    out = np.zeros((2, F, 256))
+    for f in range(F):
+        np.add.at(out[0, f], bins[:, f], g.astype(np.float64))
+        np.add.at(out[1, f], bins[:, f], h.astype(np.float64))
+    return out
+
+
 @pytest.mark.parametrize("n,F,kind,skew", [
     (1, 1, "normal", False), (17, 3, "normal", False), (1000, 16, "normal", False),
     (4099, 17, "laplace", False), (50_000, 33, "normal", False), (20_000, 24, "normal", True),
     (65_536, 100, "logistic", False),
+    # n > 2^18: the packed (count | q) LDS word with windowed unpack
+    (300_001, 20, "normal", False), (600_000, 7, "laplace", True), (1_048_577, 3, "logistic", False),
 ])
 def test_root_hist_exact(n, F, kind, skew):
     rng = np.random.default_rng(n + F)
@@ -41,12 +52,19 @@ def test_root_hist_exact(n, F, kind, skew):
     assert np.array_equal(got, ref)
     f32 = O.hist_f32(bins.T, g, h)
     assert np.array_equal(got[2], f32[2].astype(np.int64))
-    assert normwise_rel(got[0] * 2.0 ** -sg, f32[0]) < 1e-5
-    assert normwise_rel(got[1] * 2.0 ** -sh, f32[1]) < 1e-5
+    # exact sums of the quantised values against fp64 sums of the inputs
+    f64 = _hist_f64(bins, g, h)
+    assert normwise_rel(got[0] * 2.0 ** -sg, f64[0]) < 1e-9
+    assert normwise_rel(got[1] * 2.0 ** -sh, f64[1]) < 1e-9
+    if n <= 100_000:  # beyond that the reference's row-order fp32 sums drift past 1e-5 themselves
+        assert normwise_rel(got[0] * 2.0 ** -sg, f32[0]) < 1e-5
+        assert normwise_rel(got[1] * 2.0 ** -sh, f32[1]) < 1e-5
 
 
 @pytest.mark.parametrize("n,F,m", [(5000, 16, 1), (5000, 16, 777), (40_000, 21, 19_999),
-                                   (40_000, 100, 40_000), (10, 3, 0)])
+                                   (40_000, 100, 40_000), (10, 3, 0),
+                                   # n > 2^18: packed words, pipelined gather
+                                   (300_000, 20, 5), (300_000, 17, 150_001), (600_000, 9, 600_000)])
 def test_gather_hist_exact(n, F, m):
     rng = np.random.default_rng(m + 7)
     bins = uniform_bins(rng, n, F)
@@ -70,6 +88,23 @@ def test_hist_large_count_exact():
     assert got[2, 0, 0] == n
     assert got[0, 0, 0] * 2.0 ** -sg == n
     assert got[1, 0, 0] * 2.0 ** -sh == 0.5 * n
+
+
+@pytest.mark.parametrize("n", [(1 << 19) + 3, 1 << 22])
+def test_hist_packed_window_extreme(n):
+    """Every row in one bin with the largest |g| and h the shift allows: the
+    packed word's window sums reach their bound and must stay exact."""
+    bins = np.zeros((n, 1), np.uint8)
+    g = np.full(n, -1.9999999, np.float32)
+    h = np.full(n, 1.9999999, np.float32)
+    got, (sg, sh) = G.hist(_layouts(bins), torch.from_numpy(g), torch.from_numpy(h))
+    got = got.cpu().numpy()
+    qg = int(np.rint(np.float64(g[0]) * 2.0 ** sg))
+    qh = int(np.rint(np.float64(h[0]) * 2.0 ** sh))
+    assert got[2, 0, 0] == n
+    assert int(got[0, 0, 0]) == n * qg
+    assert int(got[1, 0, 0]) == n * qh
+    assert (got[:, 0, 1:] == 0).all()
 
 
 def _random_qhist(rng, F, n=3000, nb=256):

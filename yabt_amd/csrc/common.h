@@ -57,10 +57,11 @@ __device__ __forceinline__ uint32_t float_key(float x) {
 // cross-lane helpers
 // ---------------------------------------------------------------------------
 
-// Broadcast lane J of every 16-lane row to the whole row (DPP row_newbcast).
+// Broadcast lane J of every 16-lane row to the whole row (DPP row_newbcast;
+// every lane has a source, so no old value is needed).
 template <int J>
 __device__ __forceinline__ uint32_t row_bcast32(uint32_t v) {
-    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x150 + J, 0xf, 0xf, false);
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x150 + J, 0xf, 0xf, false);
 }
 
 template <int J>

@@ -652,7 +652,8 @@ int yabt_grow(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int
     for (int it = 1; it < max_leaves; ++it) {
         k_split_partition<<<pgrid, SB, 0, stream>>>(bins_fm, ld_fm, A.st, slot_n);
         k_hist_gather<<<tiles * GATHER_MAX_CHUNKS, HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, A.q, 0.0,
-                                                                        0.0, A.dflt, &A.st->hist, 1, &A.st->done);
+                                                                        0.0, A.dflt, &A.st->hist, 1, &A.st->done,
+                                                                        pack_window_log2(n));
         k_scan<false><<<scan_grid, 2 * SCAN_FEATS * WAVE, 0, stream>>>(A);
     }
     return launch_status("yabt_grow launch");

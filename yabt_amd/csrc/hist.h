@@ -145,6 +145,175 @@ __device__ __forceinline__ void hist_root_body(HistLds& L, const uint8_t* __rest
     hist_flush<HCH>(L, out, F, f0);
 }
 
+// ---------------------------------------------------------------------------
+// Packed count channel.  The count rides in the low bits of one 64-bit LDS
+// word next to q (q(h), or q(g) without the h channel): every row adds
+// (q << cb) + 1, so a sum over R rows is (sum q) << cb + R, exact while
+// R < 2^cb and |sum q| < 2^(63 - cb).  With |q| <= 2^(61 - k) (n <= 2^k, the
+// standard shift) both hold for windows of R <= 2^w rows, w = (k + 1) / 2,
+// cb = w + 1; after each window every thread moves its 4 entries into
+// registers (exact integer unpack) and clears them.  Two LDS atomics per
+// update instead of three (one without the h channel).
+// ---------------------------------------------------------------------------
+
+constexpr int HENT = NB * HFL / HBLOCK;       // entries per thread in an unpack
+
+struct HistLdsP {
+    unsigned long long g[NB * HFL];           // sum q(g) (with the h channel)
+    unsigned long long p[NB * HFL];           // packed (q << cb) + 1
+};
+
+// log2 of the packing window for n rows, or -1 when a window would be
+// shorter than one block step (then the three-word layout is used).
+__host__ __device__ inline int pack_window_log2(int64_t n) {
+    int k = 0;
+    while (k < 62 && ((int64_t)1 << k) < n) ++k;
+    const int w = (k + 1) / 2;
+    return w >= 10 ? (w > 16 ? 16 : w) : -1;   // 2^10 rows = one block step
+}
+
+// SKIP: dflt is given (rows in a feature's default bin are not added).
+// Lanes of features >= F read feature f0's column and add into their own LDS
+// columns, which the flush ignores, so the adds need no feature test.  Each
+// wave loads the next step's g, h and bins before adding the current step.
+template <bool HCH, bool SKIP>
+__device__ __forceinline__ void hist_root_packed(HistLdsP& L, const uint8_t* __restrict__ bins_fm, int64_t ld,
+                                                 const float* __restrict__ grad, const float* __restrict__ hess,
+                                                 int64_t n, int F, double scg, double sch,
+                                                 const int32_t* __restrict__ dflt, Quant* q_tot, int64_t* out,
+                                                 int chunks, int wlog) {
+    const int tile = blockIdx.x / chunks, chunk = blockIdx.x % chunks;
+    const int f0 = tile * HFL;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int fl = lane & (HFL - 1), rg = lane / HFL;
+    const int f = f0 + fl;
+    const bool fok = f < F;
+    const int64_t per = ((n + chunks - 1) / chunks + HSTEP - 1) / HSTEP * HSTEP;
+    const int64_t lo = (int64_t)chunk * per, hi = min(n, lo + per);
+    if (f0 >= F || lo >= hi) return;
+    const int d = (SKIP && fok) ? dflt[f] : -1;
+    const bool totals = q_tot != nullptr && tile == 0;
+    const int cb = wlog + 1;
+    const uint64_t cmask = ((uint64_t)1 << cb) - 1;
+    const int64_t win_steps = (int64_t)1 << (wlog - 10);
+    for (int i = threadIdx.x; i < NB * HFL; i += HBLOCK) {
+        if (HCH) L.g[i] = 0;
+        L.p[i] = 0;
+    }
+    int64_t qa[HENT];
+    uint32_t ca[HENT];
+#pragma unroll
+    for (int k = 0; k < HENT; ++k) {
+        qa[k] = 0;
+        ca[k] = 0;
+    }
+    const uint8_t* col = bins_fm + (size_t)(fok ? f : f0) * ld;
+    // r0 % 64 == 0, so base % 16 == 0; base < hi <= n <= ld, ld % 16 == 0:
+    // the 16-byte load stays inside the row
+    float gx = 0.0f, hx = 0.0f;
+    uint4 bv = make_uint4(0, 0, 0, 0);
+    {
+        const int64_t r0 = lo + (int64_t)wave * WAVE;
+        if (r0 + lane < hi) {
+            gx = grad[r0 + lane];
+            if (HCH) hx = hess[r0 + lane];
+        }
+        if (r0 + HFL * rg < hi) bv = *reinterpret_cast<const uint4*>(col + r0 + HFL * rg);
+    }
+    __syncthreads();
+    int64_t sum_g = 0, sum_h = 0;
+    const int64_t steps = (hi - lo + HSTEP - 1) / HSTEP;   // the same in every wave: barriers below
+    for (int64_t s = 0; s < steps; ++s) {
+        const int64_t r0 = lo + s * HSTEP + (int64_t)wave * WAVE;
+        // next step's inputs
+        float gn = 0.0f, hn = 0.0f;
+        uint4 bn = make_uint4(0, 0, 0, 0);
+        {
+            const int64_t r1 = r0 + HSTEP;
+            if (r1 + lane < hi) {
+                gn = grad[r1 + lane];
+                if (HCH) hn = hess[r1 + lane];
+            }
+            if (r1 + HFL * rg < hi) bn = *reinterpret_cast<const uint4*>(col + r1 + HFL * rg);
+        }
+        const bool rok = r0 + lane < hi;
+        const int64_t gq = rok ? quantise(gx, scg) : 0;
+        const int64_t hq = (HCH && rok) ? quantise(hx, sch) : 0;
+        sum_g += gq;
+        sum_h += hq;
+        const uint64_t gw = HCH ? (uint64_t)gq : ((uint64_t)gq << cb) + 1;
+        const uint64_t pw = HCH ? ((uint64_t)hq << cb) + 1 : 0;
+        const uint32_t wv[4] = {bv.x, bv.y, bv.z, bv.w};
+#define YABT_PACK_ADD(J)                                                         \
+        {                                                                        \
+            const int at = b * HFL + fl;                                         \
+            if (HCH) {                                                           \
+                atomicAdd(&L.g[at], (unsigned long long)gj);                     \
+                atomicAdd(&L.p[at], (unsigned long long)pj);                     \
+            } else {                                                             \
+                atomicAdd(&L.p[at], (unsigned long long)gj);                     \
+            }                                                                    \
+        }
+#define YABT_PACK_STEP(J, TAIL)                                                  \
+        {                                                                        \
+            const uint64_t gj = row_bcast64<J>(gw);                              \
+            const uint64_t pj = HCH ? row_bcast64<J>(pw) : 0;                     \
+            const int b = (int)((wv[(J) >> 2] >> (8 * ((J) & 3))) & 0xffu);      \
+            if ((!(TAIL) || (J) < nv) && (!SKIP || b != d)) YABT_PACK_ADD(J)     \
+        }
+        if (r0 + WAVE <= hi) {   // wave-uniform: all 64 rows valid
+            constexpr int nv = HFL;
+            YABT_PACK_STEP(0, 0) YABT_PACK_STEP(1, 0) YABT_PACK_STEP(2, 0) YABT_PACK_STEP(3, 0)
+            YABT_PACK_STEP(4, 0) YABT_PACK_STEP(5, 0) YABT_PACK_STEP(6, 0) YABT_PACK_STEP(7, 0)
+            YABT_PACK_STEP(8, 0) YABT_PACK_STEP(9, 0) YABT_PACK_STEP(10, 0) YABT_PACK_STEP(11, 0)
+            YABT_PACK_STEP(12, 0) YABT_PACK_STEP(13, 0) YABT_PACK_STEP(14, 0) YABT_PACK_STEP(15, 0)
+        } else if (r0 < hi) {
+            const int nv = (int)min((int64_t)HFL, max((int64_t)0, hi - (r0 + HFL * rg)));
+            YABT_PACK_STEP(0, 1) YABT_PACK_STEP(1, 1) YABT_PACK_STEP(2, 1) YABT_PACK_STEP(3, 1)
+            YABT_PACK_STEP(4, 1) YABT_PACK_STEP(5, 1) YABT_PACK_STEP(6, 1) YABT_PACK_STEP(7, 1)
+            YABT_PACK_STEP(8, 1) YABT_PACK_STEP(9, 1) YABT_PACK_STEP(10, 1) YABT_PACK_STEP(11, 1)
+            YABT_PACK_STEP(12, 1) YABT_PACK_STEP(13, 1) YABT_PACK_STEP(14, 1) YABT_PACK_STEP(15, 1)
+        }
+#undef YABT_PACK_STEP
+#undef YABT_PACK_ADD
+        if ((s + 1) % win_steps == 0 || s + 1 == steps) {
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < HENT; ++k) {
+                const int i = threadIdx.x + k * HBLOCK;
+                const uint64_t v = L.p[i];
+                L.p[i] = 0;
+                const uint64_t c = v & cmask;
+                qa[k] += (int64_t)(v - c) >> cb;
+                ca[k] += (uint32_t)c;
+            }
+            __syncthreads();
+        }
+        gx = gn;
+        hx = hn;
+        bv = bn;
+    }
+    if (totals) {
+        sum_g = wave_sum<int64_t>(sum_g);
+        sum_h = wave_sum<int64_t>(sum_h);
+        if (lane == 0) {
+            atomicAdd((unsigned long long*)&q_tot->tot_g, (unsigned long long)sum_g);
+            atomicAdd((unsigned long long*)&q_tot->tot_h, (unsigned long long)sum_h);
+        }
+    }
+    const size_t plane = (size_t)F * NB;
+#pragma unroll
+    for (int k = 0; k < HENT; ++k) {
+        const int i = threadIdx.x + k * HBLOCK;
+        const int fi = f0 + (i % HFL);
+        if (fi >= F || ca[k] == 0) continue;
+        const size_t at = (size_t)fi * NB + (size_t)(i / HFL);
+        atomicAdd((unsigned long long*)(out + at), HCH ? L.g[i] : (unsigned long long)qa[k]);
+        if (HCH) atomicAdd((unsigned long long*)(out + plane + at), (unsigned long long)qa[k]);
+        atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)ca[k]);
+    }
+}
+
 // count_mode 0: all three channels; 1: no h channel when q->const_h.
 static __global__ void __launch_bounds__(HBLOCK) k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld,
                                                       const float* __restrict__ grad,
@@ -157,11 +326,32 @@ static __global__ void __launch_bounds__(HBLOCK) k_hist_root(const uint8_t* __re
     const double scg = q ? q->scg : scg_v, sch = q ? q->sch : sch_v;
     const bool no_h = count_mode && q && q->const_h;
     if (dn) return;
-    __shared__ HistLds L;
-    if (no_h)
-        hist_root_body<false>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks);
-    else
-        hist_root_body<true>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks);
+    __shared__ union {
+        HistLds u;
+        HistLdsP p;
+    } L;
+    const int wlog = pack_window_log2(n);
+    if (wlog >= 0) {
+        if (no_h) {
+            if (dflt)
+                hist_root_packed<false, true>(L.p, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out,
+                                              chunks, wlog);
+            else
+                hist_root_packed<false, false>(L.p, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out,
+                                               chunks, wlog);
+        } else {
+            if (dflt)
+                hist_root_packed<true, true>(L.p, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out,
+                                             chunks, wlog);
+            else
+                hist_root_packed<true, false>(L.p, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out,
+                                              chunks, wlog);
+        }
+    } else if (no_h) {
+        hist_root_body<false>(L.u, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks);
+    } else {
+        hist_root_body<true>(L.u, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks);
+    }
 }
 
 // Rows of one node for a gather launch.
@@ -256,24 +446,200 @@ __device__ __forceinline__ void hist_gather_body(HistLds& L, const uint8_t* __re
     hist_flush<HCH>(L, out, F, f0);
 }
 
-// job->active == 0 or *done != 0 (done may be NULL): nothing to do.
+// Packed-word form of hist_gather_body (see hist_root_packed), with a
+// three-stage software pipeline per wave: at step s the wave adds step s,
+// loads g, h and the bins of step s + 1 (its row ids are already in
+// registers) and the row ids of step s + 2.
+template <bool HCH, bool SKIP>
+__device__ __forceinline__ void hist_gather_packed(HistLdsP& L, const uint8_t* __restrict__ bins_rm, int64_t ld,
+                                                   const float* __restrict__ grad, const float* __restrict__ hess,
+                                                   int F, double scg, double sch, const int32_t* __restrict__ dflt,
+                                                   const uint32_t* __restrict__ rows, int64_t jlo, int64_t jhi,
+                                                   int64_t* out, int wlog) {
+    const int tile = blockIdx.x / GATHER_MAX_CHUNKS, chunk = blockIdx.x % GATHER_MAX_CHUNKS;
+    const int f0 = tile * HFL;
+    const int64_t m = jhi - jlo;
+    if (f0 >= F || m <= 0) return;
+    const int nch = gather_chunks(m);
+    if (chunk >= nch) return;
+    const int64_t per = ((m + nch - 1) / nch + WAVE - 1) / WAVE * WAVE;
+    const int64_t lo = jlo + (int64_t)chunk * per, hi = min(jhi, lo + per);
+    if (lo >= hi) return;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int fl = lane & (HFL - 1), rg = lane / HFL;
+    const int f = f0 + fl;
+    const bool fok = f < F;
+    const int d = (SKIP && fok) ? dflt[f] : -1;
+    const int cb = wlog + 1;
+    const uint64_t cmask = ((uint64_t)1 << cb) - 1;
+    const int64_t win_steps = (int64_t)1 << (wlog - 10);
+    // lanes of features >= F gather feature f0's byte and add into their own
+    // LDS columns, which the flush ignores
+    const uint8_t* fbase = bins_rm + f0 + (fok ? fl : 0);
+    const int64_t w0 = lo + (int64_t)wave * WAVE;   // this wave's rows at step s: w0 + s * HSTEP + [0, 64)
+    // stage inputs: row ids of steps 0 and 1, g/h/bins of step 0
+    uint32_t r0 = 0, r1 = 0;
+    if (w0 + lane < hi) r0 = rows[w0 + lane];
+    if (w0 + HSTEP + lane < hi) r1 = rows[w0 + HSTEP + lane];
+    for (int i = threadIdx.x; i < NB * HFL; i += HBLOCK) {
+        if (HCH) L.g[i] = 0;
+        L.p[i] = 0;
+    }
+    int64_t qa[HENT];
+    uint32_t ca[HENT];
+#pragma unroll
+    for (int k = 0; k < HENT; ++k) {
+        qa[k] = 0;
+        ca[k] = 0;
+    }
+    float gx = 0.0f, hx = 0.0f;
+    uint32_t bj[HFL];
+#define YABT_GATHER_BINS(J, R, BASE)                                             \
+    {                                                                            \
+        const uint32_t rj = row_bcast32<J>(R);                                   \
+        bj[J] = ((BASE) + HFL * rg + (J) < hi) ? (uint32_t)fbase[(size_t)rj * ld] : 0u; \
+    }
+    if (w0 + lane < hi) {
+        gx = grad[r0];
+        if (HCH) hx = hess[r0];
+    }
+    YABT_GATHER_BINS(0, r0, w0) YABT_GATHER_BINS(1, r0, w0) YABT_GATHER_BINS(2, r0, w0)
+    YABT_GATHER_BINS(3, r0, w0) YABT_GATHER_BINS(4, r0, w0) YABT_GATHER_BINS(5, r0, w0)
+    YABT_GATHER_BINS(6, r0, w0) YABT_GATHER_BINS(7, r0, w0) YABT_GATHER_BINS(8, r0, w0)
+    YABT_GATHER_BINS(9, r0, w0) YABT_GATHER_BINS(10, r0, w0) YABT_GATHER_BINS(11, r0, w0)
+    YABT_GATHER_BINS(12, r0, w0) YABT_GATHER_BINS(13, r0, w0) YABT_GATHER_BINS(14, r0, w0)
+    YABT_GATHER_BINS(15, r0, w0)
+    __syncthreads();
+    const int64_t steps = (hi - lo + HSTEP - 1) / HSTEP;   // the same in every wave: barriers below
+    for (int64_t s = 0; s < steps; ++s) {
+        const int64_t i0 = w0 + s * HSTEP, i1 = i0 + HSTEP, i2 = i1 + HSTEP;
+        // stage: row ids of step s + 2
+        uint32_t r2 = 0;
+        if (i2 + lane < hi) r2 = rows[i2 + lane];
+        // stage: g, h and bins of step s + 1
+        float gn = 0.0f, hn = 0.0f;
+        if (i1 + lane < hi) {
+            gn = grad[r1];
+            if (HCH) hn = hess[r1];
+        }
+        uint32_t bn[HFL];
+#define YABT_GATHER_NEXT(J)                                                      \
+        {                                                                        \
+            const uint32_t rj = row_bcast32<J>(r1);                              \
+            bn[J] = (i1 + HFL * rg + (J) < hi) ? (uint32_t)fbase[(size_t)rj * ld] : 0u; \
+        }
+        YABT_GATHER_NEXT(0) YABT_GATHER_NEXT(1) YABT_GATHER_NEXT(2) YABT_GATHER_NEXT(3)
+        YABT_GATHER_NEXT(4) YABT_GATHER_NEXT(5) YABT_GATHER_NEXT(6) YABT_GATHER_NEXT(7)
+        YABT_GATHER_NEXT(8) YABT_GATHER_NEXT(9) YABT_GATHER_NEXT(10) YABT_GATHER_NEXT(11)
+        YABT_GATHER_NEXT(12) YABT_GATHER_NEXT(13) YABT_GATHER_NEXT(14) YABT_GATHER_NEXT(15)
+#undef YABT_GATHER_NEXT
+        // step s
+        const bool rok = i0 + lane < hi;
+        const int64_t gq = rok ? quantise(gx, scg) : 0;
+        const int64_t hq = (HCH && rok) ? quantise(hx, sch) : 0;
+        const uint64_t gw = HCH ? (uint64_t)gq : ((uint64_t)gq << cb) + 1;
+        const uint64_t pw = HCH ? ((uint64_t)hq << cb) + 1 : 0;
+#define YABT_GATHER_STEP(J, TAIL)                                                \
+        {                                                                        \
+            const uint64_t gj = row_bcast64<J>(gw);                              \
+            const uint64_t pj = HCH ? row_bcast64<J>(pw) : 0;                     \
+            const int b = (int)bj[J];                                            \
+            if ((!(TAIL) || (J) < nv) && (!SKIP || b != d)) {                    \
+                const int at = b * HFL + fl;                                     \
+                if (HCH) {                                                       \
+                    atomicAdd(&L.g[at], (unsigned long long)gj);                 \
+                    atomicAdd(&L.p[at], (unsigned long long)pj);                 \
+                } else {                                                         \
+                    atomicAdd(&L.p[at], (unsigned long long)gj);                 \
+                }                                                                \
+            }                                                                    \
+        }
+        if (i0 + WAVE <= hi) {   // wave-uniform: all 64 rows valid
+            constexpr int nv = HFL;
+            YABT_GATHER_STEP(0, 0) YABT_GATHER_STEP(1, 0) YABT_GATHER_STEP(2, 0) YABT_GATHER_STEP(3, 0)
+            YABT_GATHER_STEP(4, 0) YABT_GATHER_STEP(5, 0) YABT_GATHER_STEP(6, 0) YABT_GATHER_STEP(7, 0)
+            YABT_GATHER_STEP(8, 0) YABT_GATHER_STEP(9, 0) YABT_GATHER_STEP(10, 0) YABT_GATHER_STEP(11, 0)
+            YABT_GATHER_STEP(12, 0) YABT_GATHER_STEP(13, 0) YABT_GATHER_STEP(14, 0) YABT_GATHER_STEP(15, 0)
+        } else if (i0 < hi) {
+            const int nv = (int)min((int64_t)HFL, max((int64_t)0, hi - (i0 + HFL * rg)));
+            YABT_GATHER_STEP(0, 1) YABT_GATHER_STEP(1, 1) YABT_GATHER_STEP(2, 1) YABT_GATHER_STEP(3, 1)
+            YABT_GATHER_STEP(4, 1) YABT_GATHER_STEP(5, 1) YABT_GATHER_STEP(6, 1) YABT_GATHER_STEP(7, 1)
+            YABT_GATHER_STEP(8, 1) YABT_GATHER_STEP(9, 1) YABT_GATHER_STEP(10, 1) YABT_GATHER_STEP(11, 1)
+            YABT_GATHER_STEP(12, 1) YABT_GATHER_STEP(13, 1) YABT_GATHER_STEP(14, 1) YABT_GATHER_STEP(15, 1)
+        }
+#undef YABT_GATHER_STEP
+        if ((s + 1) % win_steps == 0 || s + 1 == steps) {
+            __syncthreads();
+#pragma unroll
+            for (int k = 0; k < HENT; ++k) {
+                const int i = threadIdx.x + k * HBLOCK;
+                const uint64_t v = L.p[i];
+                L.p[i] = 0;
+                const uint64_t c = v & cmask;
+                qa[k] += (int64_t)(v - c) >> cb;
+                ca[k] += (uint32_t)c;
+            }
+            __syncthreads();
+        }
+        r1 = r2;
+        gx = gn;
+        hx = hn;
+#pragma unroll
+        for (int J = 0; J < HFL; ++J) bj[J] = bn[J];
+    }
+#undef YABT_GATHER_BINS
+    const size_t plane = (size_t)F * NB;
+#pragma unroll
+    for (int k = 0; k < HENT; ++k) {
+        const int i = threadIdx.x + k * HBLOCK;
+        const int fi = f0 + (i % HFL);
+        if (fi >= F || ca[k] == 0) continue;
+        const size_t at = (size_t)fi * NB + (size_t)(i / HFL);
+        atomicAdd((unsigned long long*)(out + at), HCH ? L.g[i] : (unsigned long long)qa[k]);
+        if (HCH) atomicAdd((unsigned long long*)(out + plane + at), (unsigned long long)qa[k]);
+        atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)ca[k]);
+    }
+}
+
+// job->active == 0 or *done != 0 (done may be NULL): nothing to do.  wlog:
+// pack_window_log2(n) for the n rows the shifts were chosen for.
 static __global__ void __launch_bounds__(HBLOCK) k_hist_gather(const uint8_t* __restrict__ bins_rm, int64_t ld,
                                                         const float* __restrict__ grad,
                                                         const float* __restrict__ hess, int F, const Quant* q,
                                                         double scg_v, double sch_v,
                                                         const int32_t* __restrict__ dflt, const HistJob* job,
-                                                        int count_mode, const int32_t* done) {
+                                                        int count_mode, const int32_t* done, int wlog) {
     // independent loads first: the job record, the done flag, the shifts
     const HistJob jb = *job;
     const int32_t dn = done ? *done : 0;
     const double scg = q ? q->scg : scg_v, sch = q ? q->sch : sch_v;
     const bool no_h = count_mode && q && q->const_h;
     if (dn || !jb.active) return;
-    __shared__ HistLds L;
-    if (no_h)
-        hist_gather_body<false>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi, jb.out);
-    else
-        hist_gather_body<true>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi, jb.out);
+    __shared__ union {
+        HistLds u;
+        HistLdsP p;
+    } L;
+    if (wlog >= 0) {
+        if (no_h) {
+            if (dflt)
+                hist_gather_packed<false, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo,
+                                                jb.hi, jb.out, wlog);
+            else
+                hist_gather_packed<false, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo,
+                                                 jb.hi, jb.out, wlog);
+        } else {
+            if (dflt)
+                hist_gather_packed<true, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo,
+                                               jb.hi, jb.out, wlog);
+            else
+                hist_gather_packed<true, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo,
+                                                jb.hi, jb.out, wlog);
+        }
+    } else if (no_h) {
+        hist_gather_body<false>(L.u, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi, jb.out);
+    } else {
+        hist_gather_body<true>(L.u, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi, jb.out);
+    }
 }
 
 }  // namespace yabt

@@ -267,7 +267,7 @@ int yabt_hist(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int
     } else if (m > 0) {
         k_set_hist_job<<<1, 1, 0, stream>>>(job, rows, 0, m, out);
         k_hist_gather<<<tiles * GATHER_MAX_CHUNKS, HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, q, 0.0, 0.0,
-                                                                        nullptr, job, 0, nullptr);
+                                                                        nullptr, job, 0, nullptr, pack_window_log2(n));
     }
     k_copy_shifts<<<1, 1, 0, stream>>>(q, out_shifts);
     return launch_status("yabt_hist launch");
@@ -294,7 +294,7 @@ int yabt_hist_accumulate(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* b
         HistJob* job = c.take<HistJob>(1);
         k_set_hist_job<<<1, 1, 0, stream>>>(job, rows, 0, m, out);
         k_hist_gather<<<tiles * GATHER_MAX_CHUNKS, HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, nullptr, scg,
-                                                                        sch, nullptr, job, 0, nullptr);
+                                                                        sch, nullptr, job, 0, nullptr, pack_window_log2(n));
     }
     return launch_status("yabt_hist_accumulate launch");
 }

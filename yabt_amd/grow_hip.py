@@ -73,21 +73,32 @@ class BinLayouts:
         self.ld_rm = rm.shape[1]
         self._default = None
 
-    def default_bin(self, sample: int = 65536) -> torch.Tensor:
+    # a default bin is skipped only where it holds at least this share of the
+    # sampled rows; below it the per-update test costs more than it saves
+    SKIP_MIN_SHARE = 0.125
+
+    def default_bin(self, sample: int = 65536) -> torch.Tensor | None:
         """Most frequent bin per feature over an evenly spaced row sample (the
-        sparse layout's default bin, grow_numba.py:341-367, estimated); any
-        choice gives identical histograms, this one skips the most rows."""
+        sparse layout's default bin, grow_numba.py:341-367, estimated), -1 for
+        features whose modal bin holds under SKIP_MIN_SHARE of the sample, or
+        None when no feature qualifies.  Any choice gives identical
+        histograms; this one skips the most rows where skipping pays."""
         if self._default is None:
             F, n = self.F, self.n
             if n == 0:
-                self._default = torch.zeros(F, dtype=torch.int32, device=self.fm.device)
+                self._default = False
             else:
                 idx = torch.linspace(0, n - 1, min(n, sample), device=self.fm.device).long()
                 cols = self.fm[:, idx].long()                       # (F, s)
                 counts = torch.zeros((F, MAX_BINS), dtype=torch.int64, device=self.fm.device)
                 counts.scatter_add_(1, cols, torch.ones_like(cols))
-                self._default = counts.argmax(dim=1).to(torch.int32).contiguous()
-        return self._default
+                top, arg = counts.max(dim=1)
+                frequent = top.double() >= self.SKIP_MIN_SHARE * idx.numel()
+                if bool(frequent.any()):
+                    self._default = torch.where(frequent, arg, torch.full_like(arg, -1)).to(torch.int32).contiguous()
+                else:
+                    self._default = False
+        return self._default if self._default is not False else None
 
 
 def make_layouts(binned: torch.Tensor, dev: torch.device,
