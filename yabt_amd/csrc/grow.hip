@@ -121,6 +121,7 @@ struct GrowArgs {
     int64_t* hist;
     uint8_t* path;
     LeafRec* leaf;
+    float* gains;              // leaf[a].gain, contiguous (read by every scan block at launch)
     int64_t* seg_lo;
     int64_t* seg_hi;
     ScanRec* rec;
@@ -297,25 +298,49 @@ __device__ __forceinline__ void leaf_from_record(LeafRec& L, const ScanRec* r, b
     }
 }
 
+constexpr int GAIN_REGS = 4;                   // leaf gains a scan thread preloads
+
 // Pick the next split (grow.c:321-350) and write its job, or finish the tree.
+// gpre[i] holds gains[threadIdx.x + i * NT] as read at launch for the n_pre
+// leaves that existed then, -inf for skip_idx (the split leaf); leaves past
+// the preload are read here.  The leaves written since, s_new_idx[0..n_new),
+// compete with their records s_new.
 template <int NT>
-__device__ void select_next(const GrowArgs& A) {
+__device__ void select_next(const GrowArgs& A, const float* gpre, int n_pre, int skip_idx, const LeafRec* s_new,
+                            const int* s_new_idx, int n_new) {
     GrowState* st = A.st;
     __shared__ double s_key[NT / WAVE];
     __shared__ int s_idx[NT / WAVE];
-    const int n_active = st->n_active, n_leaves = st->n_leaves;
+    __shared__ LeafRec s_L;
+    const int n_leaves = st->n_leaves;
     int k = -1;
     if (n_leaves < A.max_leaves) {
         double key = -INFINITY;
         int idx = INT_MAX;
-        for (int a = threadIdx.x; a < n_active; a += NT) {
-            const float g = A.leaf[a].gain;
-            if (g > 0.0f && better((double)g, a, key, idx)) {
+#pragma unroll
+        for (int i = 0; i < GAIN_REGS; ++i) {
+            const int a = threadIdx.x + i * NT;
+            const float g = gpre[i];
+            if (a < n_pre && g > 0.0f && better((double)g, a, key, idx)) {
+                key = (double)g;
+                idx = a;
+            }
+        }
+        for (int a = GAIN_REGS * NT + threadIdx.x; a < n_pre; a += NT) {
+            const float g = A.gains[a];
+            if (a != skip_idx && g > 0.0f && better((double)g, a, key, idx)) {
                 key = (double)g;
                 idx = a;
             }
         }
         block_argmax<NT>(key, idx, s_key, s_idx);
+        for (int j = 0; j < n_new; ++j) {
+            const float g = s_new[j].gain;
+            if (g > 0.0f && better((double)g, s_new_idx[j], key, idx)) {
+                key = (double)g;
+                idx = s_new_idx[j];
+            }
+        }
         k = idx == INT_MAX ? -1 : idx;
     }
     if (k < 0) {
@@ -327,14 +352,24 @@ __device__ void select_next(const GrowArgs& A) {
         }
         return;
     }
-    const LeafRec L = A.leaf[k];
+    // the chosen leaf's record: one of the new ones, or a load
+    if (threadIdx.x == 0) {
+        if (k == s_new_idx[0]) s_L = s_new[0];
+        else if (n_new > 1 && k == s_new_idx[1]) s_L = s_new[1];
+        else s_L = A.leaf[k];
+    }
+    __syncthreads();
+    const LeafRec& L = s_L;
     const int nid = L.node, nl = st->n_nodes, nr = nl + 1;
-    // children inherit the parent's path plus f (grow.c:347-350)
-    const uint8_t* pp = A.path + (size_t)nid * A.F;
-    for (int j = threadIdx.x; j < A.F; j += NT) {
-        const uint8_t v = (j == L.f) ? (uint8_t)1 : pp[j];
-        A.path[(size_t)nl * A.F + j] = v;
-        A.path[(size_t)nr * A.F + j] = v;
+    if (A.use_imat) {
+        // children inherit the parent's path plus f (grow.c:347-350); only the
+        // interaction boost reads the paths
+        const uint8_t* pp = A.path + (size_t)nid * A.F;
+        for (int j = threadIdx.x; j < A.F; j += NT) {
+            const uint8_t v = (j == L.f) ? (uint8_t)1 : pp[j];
+            A.path[(size_t)nl * A.F + j] = v;
+            A.path[(size_t)nr * A.F + j] = v;
+        }
     }
     if (threadIdx.x != 0) return;
     const int64_t d = L.depth, s = L.s, e = L.e;
@@ -403,6 +438,17 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : 2 * SCAN_FEATS * WA
     const bool derive = q->const_h != 0;     // no h channel: sum q(h) = count * hq_const
     const int64_t hqc = q->hq_const;
     const int bl = ROOT ? 1 : J.build_left;
+    // leaf gains for the controller's next-split choice (every block loads
+    // them; only the last block uses them)
+    const int n_pre = ROOT ? 0 : st->n_active;
+    const int skip_idx = ROOT ? -1 : J.k;
+    float gpre[GAIN_REGS];
+#pragma unroll
+    for (int i = 0; i < GAIN_REGS; ++i) {
+        const int a = threadIdx.x + i * NT;
+        const float g = A.gains[min(a, 2 * A.max_leaves)];
+        gpre[i] = (a < n_pre && a != skip_idx) ? g : -INFINITY;
+    }
     const int parent_slot = ROOT ? 0 : J.parent_slot, new_slot = ROOT ? 0 : J.new_slot;
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
     const int f = blockIdx.x * SCAN_FEATS + (w % SCAN_FEATS);
@@ -470,11 +516,13 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : 2 * SCAN_FEATS * WA
             }
             A.rec[(size_t)cc * gridDim.x + blockIdx.x] = s_rec[bi];
         }
-        __threadfence();
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         const uint32_t t = atomicAdd(&st->scan_ticket, 1u);
         s_last = (t == gridDim.x - 1);
     }
     __syncthreads();
+    const bool last = s_last != 0;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     // every wave of the block has loaded its bins (barriers above): store
     if (fok) {
         if (built) {
@@ -483,16 +531,17 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : 2 * SCAN_FEATS * WA
             store_bins(hp, A.F, f, lane, g4, h4, c4, has_h);
         }
     }
-    if (!s_last) return;
-    __threadfence();
+    if (!last) return;
     if (threadIdx.x == 0) st->scan_ticket = 0;
 
     // ---- controller (one block) ----
-    __shared__ int s_bi[NC];
+    __shared__ ScanRec s_best[NC];
     if (w < NC) {
-        const int bi = wave_best_record(A.rec + (size_t)w * gridDim.x, gridDim.x, lane);
-        if (lane == 0) s_bi[w] = bi < 0 ? -1 : w * (int)gridDim.x + bi;
+        const ScanRec r = wave_best_record(A.rec + (size_t)w * gridDim.x, gridDim.x, lane);
+        if (lane == 0) s_best[w] = r;
     }
+    __shared__ LeafRec s_new[2];
+    __shared__ int s_new_idx[2];
     __syncthreads();
     if (threadIdx.x == 0) {
         if (ROOT) {
@@ -505,12 +554,16 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : 2 * SCAN_FEATS * WA
             L.tot[0] = q->tot_g;
             L.tot[1] = derive ? A.n * hqc : q->tot_h;
             L.tot[2] = A.n;
-            leaf_from_record(L, s_bi[0] >= 0 ? A.rec + s_bi[0] : nullptr, 0 >= A.max_depth);
+            leaf_from_record(L, s_best[0].b >= 0 ? &s_best[0] : nullptr, 0 >= A.max_depth);
             A.leaf[0] = L;
+            A.gains[0] = L.gain;
             A.value[0] = node_value(L.tot, q, A.lr, A.lam);
             st->n_nodes = 1;
             st->n_leaves = 1;
             st->n_active = 1;
+            s_new[0] = L;
+            s_new_idx[0] = 0;
+            s_new_idx[1] = -1;
         } else {
             const SplitJob& J = st->job;
             const bool capped = J.depth >= A.max_depth;
@@ -528,8 +581,8 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : 2 * SCAN_FEATS * WA
                 Ll.tot[i] = J.left[i];
                 Lr.tot[i] = J.tot[i] - J.left[i];
             }
-            leaf_from_record(Ll, s_bi[0] >= 0 ? A.rec + s_bi[0] : nullptr, capped);
-            leaf_from_record(Lr, s_bi[1] >= 0 ? A.rec + s_bi[1] : nullptr, capped);
+            leaf_from_record(Ll, s_best[0].b >= 0 ? &s_best[0] : nullptr, capped);
+            leaf_from_record(Lr, s_best[1].b >= 0 ? &s_best[1] : nullptr, capped);
             A.seg_lo[J.nl] = J.s;
             A.seg_hi[J.nl] = J.mid;
             A.seg_lo[J.nr] = J.mid;
@@ -539,13 +592,19 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : 2 * SCAN_FEATS * WA
             const int na = st->n_active;
             A.leaf[J.k] = Ll;            // left child replaces the split leaf
             A.leaf[na] = Lr;             // right child is appended (grow.c:393-407)
+            A.gains[J.k] = Ll.gain;
+            A.gains[na] = Lr.gain;
             st->n_active = na + 1;
             st->active = 0;
             st->hist.active = 0;
+            s_new[0] = Ll;
+            s_new[1] = Lr;
+            s_new_idx[0] = J.k;
+            s_new_idx[1] = na;
         }
     }
     __syncthreads();
-    select_next<NT>(A);
+    select_next<NT>(A, gpre, n_pre, skip_idx, s_new, s_new_idx, ROOT ? 1 : 2);
 }
 
 // out[row] = leaf node id, from each leaf's segment of the final row lists.
@@ -573,6 +632,7 @@ size_t carve_grow(char* base, int64_t n, int F, int max_leaves, GrowArgs* A) {
     a.hist = c.take<int64_t>((size_t)max_leaves * 3 * (size_t)F * NB);
     a.path = c.take<uint8_t>(N * (size_t)F);
     a.leaf = c.take<LeafRec>(N);
+    a.gains = c.take<float>(N);
     a.seg_lo = c.take<int64_t>(N);
     a.seg_hi = c.take<int64_t>(N);
     a.rec = c.take<ScanRec>((size_t)2 * F);

@@ -227,19 +227,24 @@ __device__ __forceinline__ bool rec_beats(double sa, int fa, int ba, double sb, 
     return ba >= 0 && (bb < 0 || sa > sb || (sa == sb && fa < fb));
 }
 
-// One wave: index in rec[0, n) of the best record (-1: none valid).
-__device__ inline int wave_best_record(const ScanRec* rec, int n, int lane) {
-    double s = -INFINITY;
-    int f = INT_MAX, b = -1, idx = -1;
+// One wave: the best of rec[0, n) in every lane (b = -1: none valid).
+__device__ inline ScanRec wave_best_record(const ScanRec* rec, int n, int lane) {
+    ScanRec mine;
+    mine.sel = -INFINITY;
+    mine.gain = -INFINITY;
+    mine.b = -1;
+    mine.f = INT_MAX;
+    mine.left[0] = mine.left[1] = mine.left[2] = 0;
+    int my_idx = -1;
     for (int i = lane; i < n; i += WAVE) {
-        const ScanRec& r = rec[i];
-        if (rec_beats(r.sel, r.f, r.b, s, f, b)) {
-            s = r.sel;
-            f = r.f;
-            b = r.b;
-            idx = i;
+        const ScanRec r = rec[i];
+        if (rec_beats(r.sel, r.f, r.b, mine.sel, mine.f, mine.b)) {
+            mine = r;
+            my_idx = i;
         }
     }
+    double s = mine.sel;
+    int f = mine.f, b = mine.b, idx = my_idx;
 #pragma unroll
     for (int m = WAVE / 2; m > 0; m >>= 1) {
         const double os = __shfl_xor(s, m, WAVE);
@@ -251,7 +256,23 @@ __device__ inline int wave_best_record(const ScanRec* rec, int n, int lane) {
             idx = oi;
         }
     }
-    return idx;
+    ScanRec r;
+    const uint64_t owner = __ballot(idx >= 0 && my_idx == idx);
+    if (owner == 0) {
+        r = mine;          // no valid record anywhere: every lane's is empty
+        r.b = -1;
+        r.f = -1;
+        return r;
+    }
+    const int src = __ffsll((unsigned long long)owner) - 1;
+    r.sel = readlane_f64(mine.sel, src);
+    r.gain = readlane_f64(mine.gain, src);
+    r.b = __builtin_amdgcn_readlane(mine.b, src);
+    r.f = __builtin_amdgcn_readlane(mine.f, src);
+    r.left[0] = readlane64(mine.left[0], src);
+    r.left[1] = readlane64(mine.left[1], src);
+    r.left[2] = readlane64(mine.left[2], src);
+    return r;
 }
 
 // Feature-major reduction of one node's records (grow.c:181-192), NT threads;
