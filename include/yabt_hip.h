@@ -129,6 +129,30 @@ int yabt_partition(const uint8_t *bins_fm, int64_t ld_fm, int64_t n, int f, int 
                    const uint32_t *rows_in, int64_t m, uint32_t *rows_out, void *workspace,
                    int64_t *out_mid, yabt_stream_t stream);
 
+/* Workspace bytes of yabt_leaf_fit for n rows, n_nodes nodes, K inputs. */
+size_t yabt_leaf_fit_workspace_bytes(int64_t n, int n_nodes, int K);
+
+/* Linear leaf models of one tree: for every leaf (feature[node] == -1) with at
+ * least min_samples rows, theta = solve(M + diag(lam,..,lam,1e-8), b) with
+ * x1 = [(x - mu) / sd (fp32), 1], M = sum h x1 x1^T, b = -sum g x1 over the
+ * leaf's rows (fp64 products, summed exactly in int64 fixed point).
+ * Replaces `_fit_linear` (yabt/neural_leaves.py:42-90) and the counts and
+ * envelopes of `fit_leaf_networks` (yabt/neural_leaves.py:157-176).
+ *   x_kind 0: X is fp32 row-major (n, ldx), input j of row i = X[i*ldx + feats[j]];
+ *   x_kind 1: X is uint8 feature-major (F, ldx >= n), input = (float)X[feats[j]*ldx + i];
+ *   leaf_of_row (n) node ids in [0, n_nodes); mu, sd (K) fp32; 1 <= K <= 8.
+ * Outputs (device): out_W (n_nodes, K) and out_b (n_nodes) in the standardised
+ * inputs (zero where not fitted); out_lo/out_hi (n_nodes, K) per-node min/max of
+ * the raw inputs (+inf/-inf for empty nodes); out_count (n_nodes) rows per node;
+ * out_status[0] = 0, -1 (a leaf id out of range or a non-finite input) or -2
+ * (a singular system, where the reference's torch.linalg.solve raises). */
+int yabt_leaf_fit(int x_kind, const void *X, int64_t ldx, int64_t n, const int32_t *feats, int K,
+                  const float *mu, const float *sd, const float *grad, const float *hess,
+                  const int64_t *leaf_of_row, const int64_t *feature, int n_nodes, int min_samples,
+                  double lam, void *workspace, size_t workspace_bytes, float *out_W, float *out_b,
+                  float *out_lo, float *out_hi, int64_t *out_count, int32_t *out_status,
+                  yabt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

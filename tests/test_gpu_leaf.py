@@ -1,0 +1,145 @@
+"""Linear leaf models (yabt_leaf_fit) against the oracle, through the C ABI.
+
+Counts and envelopes must be identical; weights and biases, solved in fp64 on
+exact fixed-point sums of the reference's fp64 products, within 1e-5 relative
+of the oracle's fp64 normal equations (the fp32 outputs of two fp64 solves).
+Two calls give identical bits, and the uint8 input path equals the fp32 path
+on the same values.
+"""
+
+from dataclasses import dataclass
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import neural_oracle as NO
+from tests.helpers import grad_hess, uniform_bins
+from yabt_amd import IdentityBinner, TreeParams, grow_tree_hip
+from yabt_amd import grow_hip as G
+from yabt_amd.losses import MSELoss
+from yabt_amd.neural_leaves import fit_leaf_networks, leaf_fit
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0) if torch.cuda.is_available() else None
+
+
+def _problem(seed, n, K, n_nodes, bins=False):
+    rng = np.random.default_rng(seed)
+    F = K + 3
+    if bins:
+        X = uniform_bins(rng, n, F)                      # (n, F) u8
+        Xf = X.astype(np.float32)
+    else:
+        Xf = (rng.normal(size=(n, F)) * 2 + 0.5).astype(np.float32)
+        X = Xf
+    feats = rng.permutation(F)[:K].astype(np.int32)
+    g, h = grad_hess(rng, n)
+    feature = np.full(n_nodes, -1, np.int64)
+    feature[: n_nodes // 2] = rng.integers(0, F, n_nodes // 2)   # the first half are internal
+    leaves = np.nonzero(feature == -1)[0]
+    leaf = rng.choice(leaves, size=n).astype(np.int64)
+    Xs = Xf[:, feats]
+    mu = Xs.mean(axis=0).astype(np.float32)
+    sd = np.maximum(Xs.std(axis=0, ddof=1), 1e-6).astype(np.float32)
+    return X, Xf, feats, g, h, feature, leaf, mu, sd
+
+
+def _oracle(Xf, feats, g, h, feature, leaf, mu, sd, min_samples, lam):
+    n_nodes = feature.size
+    Xs = Xf[:, feats]
+    cnt = NO.counts(leaf, n_nodes)
+    lo, hi = NO.envelopes(Xs, leaf, n_nodes)
+    W, db = NO.fit_linear(NO.standardise(Xs, mu, sd), g, h, leaf, NO.eligible_nodes(feature, cnt, min_samples),
+                          n_nodes, lam)
+    return W, db, lo, hi, cnt
+
+
+def _gpu(X, x_kind, feats, g, h, feature, leaf, mu, sd, min_samples, lam):
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    Xd = t(X) if x_kind == 0 else t(np.ascontiguousarray(X.T))
+    out = leaf_fit(Xd, x_kind, t(feats), t(mu), t(sd), t(g), t(h), t(leaf), t(feature), min_samples, lam)
+    return [o.cpu().numpy() for o in out]
+
+
+@pytest.mark.parametrize("n,K,n_nodes,x_kind,lam", [
+    (5000, 8, 61, 0, 1.0), (20_000, 5, 31, 1, 1e-3), (777, 1, 7, 0, 1.0), (300_000, 8, 511, 1, 1.0),
+    (40_000, 3, 1501, 0, 0.5),   # more nodes than the LDS tables hold
+])
+def test_leaf_fit_matches_oracle(n, K, n_nodes, x_kind, lam):
+    X, Xf, feats, g, h, feature, leaf, mu, sd = _problem(n + K, n, K, n_nodes, bins=x_kind == 1)
+    W, b, lo, hi, cnt = _gpu(X, x_kind, feats, g, h, feature, leaf, mu, sd, 50, lam)
+    rW, rb, rlo, rhi, rcnt = _oracle(Xf, feats, g, h, feature, leaf, mu, sd, 50, lam)
+    assert np.array_equal(cnt, rcnt)
+    assert np.array_equal(lo, rlo) and np.array_equal(hi, rhi)
+    np.testing.assert_allclose(W, rW, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(b, rb, rtol=1e-5, atol=1e-6)
+
+
+def test_leaf_fit_deterministic_and_u8_equals_f32():
+    X, Xf, feats, g, h, feature, leaf, mu, sd = _problem(9, 50_000, 6, 63, bins=True)
+    a = _gpu(X, 1, feats, g, h, feature, leaf, mu, sd, 50, 1.0)
+    b = _gpu(X, 1, feats, g, h, feature, leaf, mu, sd, 50, 1.0)
+    c = _gpu(Xf, 0, feats, g, h, feature, leaf, mu, sd, 50, 1.0)
+    for u, v, w in zip(a, b, c):
+        assert np.array_equal(u, v)
+        assert np.array_equal(u, w)
+
+
+def test_leaf_fit_rejects_bad_leaf_ids():
+    X, Xf, feats, g, h, feature, leaf, mu, sd = _problem(3, 1000, 2, 9)
+    leaf[17] = 9
+    with pytest.raises(ValueError):
+        _gpu(X, 0, feats, g, h, feature, leaf, mu, sd, 50, 1.0)
+
+
+@dataclass
+class _P:
+    learning_rate: float = 0.1
+    leaf_net_features: int = 8
+    leaf_net_min_samples: int = 50
+    leaf_net_l2: float = 1.0
+    leaf_net_hidden: int = 0
+
+
+def test_fit_leaf_networks_end_to_end():
+    """grow_tree_hip + fit_leaf_networks against the oracle on the same
+    selected features and standardisation (neural_leaves.py:131-184)."""
+    rng = np.random.default_rng(11)
+    n, F = 30_000, 12
+    Xf = rng.normal(size=(n, F)).astype(np.float32)
+    y = (np.sin(Xf[:, 0]) + 0.5 * Xf[:, 1] * Xf[:, 2] + Xf[:, 3] ** 2).astype(np.float32)
+    binner = IdentityBinner(F, 256)
+    bins = np.clip(np.floor((Xf + 4) * 32), 0, 255).astype(np.uint8)
+    Xraw = bins.astype(np.float32)
+    margin = np.zeros(n, np.float32)
+    g, h = MSELoss.grad_hess(torch.from_numpy(margin), torch.from_numpy(y))
+    tree = grow_tree_hip(torch.from_numpy(bins).to(DEV), g.to(DEV), h.to(DEV), binner, TreeParams(max_leaves=31))
+    Xd, yd, md = (torch.from_numpy(a).to(DEV) for a in (Xraw, y, margin))
+    out = fit_leaf_networks(tree, Xd, yd, md, MSELoss, _P())
+    feats = out.leaf_net_feats.cpu().numpy()
+    used = tree.feature.cpu().numpy()
+    used = used[used >= 0]
+    # the most used split features come first
+    counts = np.bincount(used, minlength=F)
+    m = min(8, len(set(used.tolist())))
+    assert (np.diff(counts[feats[:m]]) <= 0).all() and (counts[feats[:m]] > 0).all()
+    Xs = Xd[:, out.leaf_net_feats]
+    mu, sd = Xs.mean(dim=0), Xs.std(dim=0).clamp_min(1e-6)
+    leaf = tree.apply(Xd).cpu().numpy()
+    value = tree.value.cpu().numpy()
+    g2 = (margin + value[leaf] - y).astype(np.float32)
+    h2 = np.ones(n, np.float32)
+    feature = tree.feature.cpu().numpy()
+    W, db, lo, hi, cnt = _oracle(Xraw, feats.astype(np.int32), g2, h2, feature, leaf, mu.cpu().numpy(),
+                                 sd.cpu().numpy(), 50, 1.0)
+    v2, lin = NO.fold(value, W, db, mu.cpu().numpy(), sd.cpu().numpy(), 0.1)
+    np.testing.assert_allclose(out.value.cpu().numpy(), v2, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(out.leaf_net_linear.cpu().numpy(), lin, rtol=1e-5, atol=1e-7)
+    assert np.array_equal(out.leaf_net_lo.cpu().numpy(), lo)
+    assert np.array_equal(out.leaf_net_hi.cpu().numpy(), hi)
+    # the fitted model lowers the squared loss of the constant tree on its rows
+    pred0 = value[leaf]
+    pred1 = out.predict(Xd).cpu().numpy()
+    assert ((pred1 - (y - margin)) ** 2).mean() < ((pred0 - (y - margin)) ** 2).mean()

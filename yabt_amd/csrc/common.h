@@ -308,7 +308,7 @@ __device__ inline void quant_finish(Quant* q, int64_t n) {
     }
 }
 
-static __global__ void k_quant_clear(Quant* q) {
+static __global__ __attribute__((unused)) void k_quant_clear(Quant* q) {
     q->maxg_bits = 0;
     q->maxh_bits = 0;
     q->hmin_key = 0xffffffffu;

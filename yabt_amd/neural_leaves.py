@@ -1,0 +1,167 @@
+"""Linear leaf models on the GPU (mirror of yabt/neural_leaves.py:21-184).
+
+``fit_leaf_networks`` keeps the reference's signature and result: after a tree
+is grown, every leaf with at least ``leaf_net_min_samples`` rows gets a ridge
+model over up to ``leaf_net_features`` inputs, fitted to the Newton objective
+at ``margin + value[leaf]``, folded into raw space and shrunk by the learning
+rate, with per-leaf input envelopes.  The per-leaf Gram matrices, envelopes,
+counts and solves run in the HIP kernels of ``csrc/leaf.hip``
+(``yabt_leaf_fit``); feature selection, standardisation and the fold are the
+reference's own torch expressions on the device.  Only the linear form
+(``leaf_net_hidden == 0``) is provided.
+"""
+
+from __future__ import annotations
+
+from dataclasses import replace
+
+import torch
+
+from . import _lib
+from .tree import LEAF, Tree
+
+_WS: dict = {}
+
+
+def _stream(dev: torch.device):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _select_features(tree: Tree, Xraw: torch.Tensor, grad: torch.Tensor, k: int) -> torch.Tensor:
+    """The tree's split features, most used first, padded by |corr(x, g)|
+    (neural_leaves.py:21-39)."""
+    k = min(k, Xraw.shape[1])
+    f = tree.feature[tree.feature >= 0]
+    if f.numel() > 0:
+        vals, counts = f.unique(return_counts=True)
+        used = vals[counts.argsort(descending=True)][:k]
+    else:
+        used = torch.empty(0, dtype=torch.long, device=Xraw.device)
+    if used.numel() >= k:
+        return used
+    score = (Xraw.T @ grad - Xraw.mean(dim=0) * grad.sum()).abs()
+    score = score / Xraw.std(dim=0).clamp_min(1e-6)
+    score[used] = float("-inf")
+    extra = score.argsort(descending=True)[: k - used.numel()]
+    return torch.cat([used, extra])
+
+
+def leaf_fit(X: torch.Tensor, x_kind: int, feats: torch.Tensor, mu: torch.Tensor, sd: torch.Tensor,
+             grad: torch.Tensor, hess: torch.Tensor, leaf_idx: torch.Tensor, feature: torch.Tensor,
+             min_samples: int, lam: float):
+    """One ``yabt_leaf_fit`` call.  X: fp32 (n, F) row-major (x_kind 0) or
+    uint8 feature-major (F, ld >= n) (x_kind 1).  Returns (W (N, K), b (N),
+    lo (N, K), hi (N, K), count (N)) on X's device; W, b act on the
+    standardised inputs."""
+    lib = _lib.load()
+    dev = X.device
+    if dev.type != "cuda":
+        raise RuntimeError("yabt_leaf_fit needs device tensors")
+    n = int(grad.shape[0])
+    K = int(feats.numel())
+    N = int(feature.shape[0])
+    if x_kind == 0:
+        if X.dtype != torch.float32 or X.dim() != 2 or X.shape[0] != n or X.stride(1) != 1:
+            raise ValueError("X must be fp32 (n, F) with unit column stride")
+        ldx = X.stride(0)
+    else:
+        if X.dtype != torch.uint8 or X.dim() != 2 or X.shape[1] < n or X.stride(1) != 1:
+            raise ValueError("X must be uint8 (F, ld >= n)")
+        ldx = X.stride(0)
+    fi = feats.to(dev, torch.int32).contiguous()
+    m = mu.to(dev, torch.float32).contiguous()
+    s = sd.to(dev, torch.float32).contiguous()
+    g = grad.to(dev, torch.float32).contiguous()
+    h = hess.to(dev, torch.float32).contiguous()
+    li = leaf_idx.to(dev, torch.int64).contiguous()
+    ft = feature.to(dev, torch.int64).contiguous()
+    nbytes = int(lib.yabt_leaf_fit_workspace_bytes(n, N, K))
+    if nbytes == 0:
+        raise ValueError("yabt_leaf_fit: invalid sizes (1 <= K <= 8 inputs)")
+    ws = _WS.get(dev)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _WS[dev] = ws
+    W = torch.empty((N, K), dtype=torch.float32, device=dev)
+    b = torch.empty(N, dtype=torch.float32, device=dev)
+    lo = torch.empty((N, K), dtype=torch.float32, device=dev)
+    hi = torch.empty((N, K), dtype=torch.float32, device=dev)
+    cnt = torch.empty(N, dtype=torch.int64, device=dev)
+    status = torch.empty(1, dtype=torch.int32, device=dev)
+    _lib.check(lib.yabt_leaf_fit(x_kind, X.data_ptr(), ldx, n, fi.data_ptr(), K, m.data_ptr(), s.data_ptr(),
+                                 g.data_ptr(), h.data_ptr(), li.data_ptr(), ft.data_ptr(), N, int(min_samples),
+                                 float(lam), ws.data_ptr(), nbytes, W.data_ptr(), b.data_ptr(), lo.data_ptr(),
+                                 hi.data_ptr(), cnt.data_ptr(), status.data_ptr(), _stream(dev)),
+               "yabt_leaf_fit")
+    st = int(status.item())
+    if st == -1:
+        raise ValueError("yabt_leaf_fit: a leaf id is out of range or an input is not finite")
+    if st == -2:
+        raise RuntimeError("yabt_leaf_fit: singular leaf system (torch.linalg.solve would raise)")
+    return W, b, lo, hi, cnt
+
+
+def fold(tree: Tree, W, db, mu, sd, lr, feats, lo, hi) -> Tree:
+    """Normalisation and shrinkage folded into raw space (neural_leaves.py:178-184)."""
+    value = tree.value.to(W.device) + lr * (db - (W * (mu / sd)).sum(dim=1))
+    return replace(tree, value=value, leaf_net_feats=feats, leaf_net_linear=lr * W / sd,
+                   leaf_net_lo=lo, leaf_net_hi=hi)
+
+
+def fit_leaf_networks(tree: Tree, Xraw: torch.Tensor, y: torch.Tensor, margin: torch.Tensor, loss_fn,
+                      params, gen: torch.Generator | None = None, leaf_idx: torch.Tensor | None = None) -> Tree:
+    """Drop-in for yabt.neural_leaves.fit_leaf_networks (neural_leaves.py:131-184),
+    linear leaves; Xraw (n, F) fp32 on a HIP device."""
+    if getattr(params, "leaf_net_hidden", 0) != 0:
+        raise NotImplementedError("MLP leaves (leaf_net_hidden > 0) are not provided by this backend")
+    dev = Xraw.device
+    tree_d = replace(tree, feature=tree.feature.to(dev), threshold=tree.threshold.to(dev),
+                     left=tree.left.to(dev), right=tree.right.to(dev), value=tree.value.to(dev))
+    if leaf_idx is None:
+        leaf_idx = tree_d.apply(Xraw)
+    grad, hess = loss_fn.grad_hess(margin + tree_d.value[leaf_idx], y)
+    feats = _select_features(tree_d, Xraw, grad, getattr(params, "leaf_net_features", 8))
+    if feats.numel() == 0:
+        return tree
+    Xs = Xraw[:, feats]
+    mu = Xs.mean(dim=0)
+    sd = Xs.std(dim=0).clamp_min(1e-6)
+    X = Xraw if Xraw.dtype == torch.float32 and Xraw.stride(1) == 1 else Xraw.float().contiguous()
+    W, db, lo, hi, cnt = leaf_fit(X, 0, feats, mu, sd, grad, hess, leaf_idx, tree_d.feature,
+                                  getattr(params, "leaf_net_min_samples", 50),
+                                  getattr(params, "leaf_net_l2", 1.0))
+    eligible = (tree_d.feature == LEAF) & (cnt >= getattr(params, "leaf_net_min_samples", 50))
+    if not bool(eligible.any()):
+        return tree
+    return fold(tree_d, W, db, mu, sd, params.learning_rate, feats, lo, hi)
+
+
+def fit_leaf_networks_binned(tree: Tree, bins_fm: torch.Tensor, grad: torch.Tensor, hess: torch.Tensor,
+                             leaf_idx: torch.Tensor, params, n: int | None = None) -> Tree:
+    """The same fit with raw inputs x = float(bin) read straight from the
+    feature-major bins (F, ld) (the identity-binner case), and g, h already
+    evaluated at margin + value[leaf]."""
+    if getattr(params, "leaf_net_hidden", 0) != 0:
+        raise NotImplementedError("MLP leaves (leaf_net_hidden > 0) are not provided by this backend")
+    dev = bins_fm.device
+    n = int(grad.shape[0]) if n is None else n
+    feature = tree.feature.to(dev)
+    k = min(getattr(params, "leaf_net_features", 8), bins_fm.shape[0])
+    f = feature[feature >= 0]
+    if f.numel() == 0:
+        return tree
+    vals, counts = f.unique(return_counts=True)
+    feats = vals[counts.argsort(descending=True)][:k]
+    if feats.numel() < k:
+        # padding by gradient correlation needs the raw columns: take them as floats
+        Xraw = bins_fm[:, :n].t().float()
+        feats = _select_features(replace(tree, feature=feature), Xraw, grad, k)
+    Xs = bins_fm[feats, :n].float()              # (K, n)
+    mu = Xs.mean(dim=1)
+    sd = Xs.std(dim=1).clamp_min(1e-6)
+    del Xs
+    W, db, lo, hi, cnt = leaf_fit(bins_fm, 1, feats, mu, sd, grad, hess, leaf_idx, feature,
+                                  getattr(params, "leaf_net_min_samples", 50),
+                                  getattr(params, "leaf_net_l2", 1.0))
+    tree_d = replace(tree, feature=feature, value=tree.value.to(dev))
+    return fold(tree_d, W, db, mu, sd, params.learning_rate, feats, lo, hi)
