@@ -6,10 +6,14 @@ U(0.1,1) (fp32), 255 leaves, min_samples_leaf 20, min_child_weight 1e-3,
 lambda 1, gamma 0, lr 0.1, identity binner (nbins 256).  Inputs are generated
 on the device and resident in HBM before timing.
 
-A step is one full tree (root histogram, 254 splits of partition + smaller
-child histogram + sibling subtraction + split scans).  ``value`` is the tree's
-histogram work, sum over built nodes of rows x features (row.feature updates),
-divided by the measured time per tree, in G updates/s.
+A step is one full tree: root histogram, 254 splits (partition + smaller
+child histogram + sibling subtraction + split scans), then the linear leaf
+models (K = 8 most used split features, raw input x = float(bin), g and h at
+margin + value[leaf] for a quadratic objective: g + h * value[leaf], h;
+min 50 rows, l2 1).  ``value`` is the tree's histogram work, sum over built
+nodes of rows x features (row.feature updates), divided by the measured time
+per step, in G updates/s; ``ms_grow`` is the same loop without the leaf
+models.
 
 Also reported:
   * root_hist: the streaming root-histogram kernel timed alone with HIP events
@@ -48,6 +52,14 @@ METRIC = "histogram G row·feature updates/s + ms/tree at 10M×100, % of HBM pea
 HBM_PEAK_GBS = 8000.0
 N_ROWS, N_FEAT, MAX_LEAVES = 10_000_000, 100, 255
 PARAMS = dict(lam=1.0, gamma=0.0, mcw=1e-3, msl=20, lr=0.1, max_leaves=MAX_LEAVES, max_depth=64)
+
+
+class LeafNetParams:
+    learning_rate = 0.1
+    leaf_net_features = 8
+    leaf_net_min_samples = 50
+    leaf_net_l2 = 1.0
+    leaf_net_hidden = 0
 
 
 def log(msg: str) -> None:
@@ -203,6 +215,7 @@ def main() -> None:
     ap.add_argument("--warmup", type=int, default=1)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--rows", type=int, default=N_ROWS)
+    ap.add_argument("--no-neural", action="store_true", help="time the grower only")
     ap.add_argument("--counters", action="store_true",
                     help="only launch the copy and root-histogram kernels for rocprofv3 --pmc")
     args = ap.parse_args()
@@ -227,22 +240,46 @@ def main() -> None:
     log("[bench] root histogram kernel")
     root_mean_ms, root_med_ms = time_root_hist(torch, lay, g, h)
 
+    from yabt_amd.neural_leaves import fit_leaf_networks_binned
+    from yabt_amd.tree import Tree
+
+    def step(neural: bool):
+        res = G.grow_device(lay, g, h, nbins, sync=False, **PARAMS)
+        if not neural:
+            return res, None
+        # node arrays are full length (2L + 1); unused slots are empty leaves
+        leaf = G.leaf_ids(res, n, F, MAX_LEAVES)
+        tree = Tree(res.feature, res.thr_bin.float(), res.left, res.right, res.value, 0)
+        g2 = g + h * res.value[leaf]
+        return res, fit_leaf_networks_binned(tree, lay.fm, g2, h, leaf, LeafNetParams, n=n)
+
+    def timed(neural: bool, steps: int) -> float:
+        stream = torch.cuda.current_stream()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        for _ in range(steps):
+            step(neural)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    neural = not args.no_neural
     log(f"[bench] warm-up trees: {args.warmup}")
     for _ in range(args.warmup):
-        res = G.grow_device(lay, g, h, nbins, **PARAMS)
+        step(neural)
     torch.cuda.synchronize()
-    stream = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    log(f"[bench] timed trees: {args.steps}")
+    log(f"[bench] timed trees: {args.steps} (grower only)")
+    ms_grow = timed(False, args.steps)
+    ms_per_tree = ms_grow
+    if neural:
+        log(f"[bench] timed trees: {args.steps} (grower + leaf models)")
+        ms_per_tree = timed(True, args.steps)
+    res, net = step(neural)
     torch.cuda.synchronize()
-    e0.record(stream)
-    for _ in range(args.steps):
-        res = G.grow_device(lay, g, h, nbins, sync=False, **PARAMS)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    ms_per_tree = e0.elapsed_time(e1) / args.steps
+    res.n_nodes = int(res._status.item())
 
-    nn = int(res._status.item())
+    nn = res.n_nodes
     feat = res.feature[:nn].cpu().numpy()
     left = res.left[:nn].cpu().numpy()
     right = res.right[:nn].cpu().numpy()
@@ -259,11 +296,13 @@ def main() -> None:
         "ms_per_step": round(ms_per_tree, 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "int64",
         "data": "synthetic (device RNG, seed 0)",
-        "config": {"workload": "best-first tree, 10M rows x 100 features x 256 uint8 bins, 255 leaves",
+        "config": {"workload": "best-first tree, 10M rows x 100 features x 256 uint8 bins, 255 leaves"
+                               + (", linear leaf models (K=8)" if neural else ""),
                    "rows": n, "features": F, "bins": 256, "max_leaves": MAX_LEAVES,
                    "min_samples_leaf": 20, "leaves_grown": int((feat == -1).sum()),
                    "tree_updates": upd},
-        "ms_per_tree": round(ms_per_tree, 3),
+        "ms_per_tree": round(ms_per_tree, 3), "ms_grow": round(ms_grow, 3),
+        "leaf_models_fitted": (int((net.leaf_net_linear.abs().sum(dim=1) > 0).sum()) if neural else 0),
         "root_hist": {"ms": round(root_mean_ms, 4), "ms_median": round(root_med_ms, 4),
                       "updates_per_s": round(n * F / (root_mean_ms * 1e-3) / 1e9, 3),
                       "unit": "G updates/s", "GBps": round(achieved, 1),

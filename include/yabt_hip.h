@@ -153,6 +153,17 @@ int yabt_leaf_fit(int x_kind, const void *X, int64_t ldx, int64_t n, const int32
                   float *out_lo, float *out_hi, int64_t *out_count, int32_t *out_status,
                   yabt_stream_t stream);
 
+/* Workspace bytes of yabt_leaf_moments for n rows. */
+size_t yabt_leaf_moments_workspace_bytes(int64_t n);
+
+/* Standardisation of the leaf-model inputs: out_mu[j] = mean, out_sd[j] =
+ * max(unbiased std, 1e-6) of input j over the n rows (fp32 results of fp64
+ * sums reduced in a fixed order).  Same inputs as yabt_leaf_fit.  Replaces
+ * `Xs.mean(dim=0)`, `Xs.std(dim=0).clamp_min(1e-6)` (yabt/neural_leaves.py:152-154). */
+int yabt_leaf_moments(int x_kind, const void *X, int64_t ldx, int64_t n, const int32_t *feats, int K,
+                      void *workspace, size_t workspace_bytes, float *out_mu, float *out_sd,
+                      yabt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

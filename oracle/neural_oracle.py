@@ -31,6 +31,15 @@ def envelopes(Xs: np.ndarray, leaf: np.ndarray, n_nodes: int):
     return lo, hi
 
 
+def moments(Xs: np.ndarray):
+    """Mean and unbiased std clamped at 1e-6 (neural_leaves.py:152-154), in
+    float64, rounded to float32."""
+    X = Xs.astype(np.float64)
+    mu = X.mean(axis=0)
+    sd = X.std(axis=0, ddof=1)
+    return mu.astype(np.float32), np.maximum(sd.astype(np.float32), np.float32(1e-6))
+
+
 def standardise(Xs: np.ndarray, mu: np.ndarray, sd: np.ndarray) -> np.ndarray:
     """(Xs - mu) / sd in float32 (neural_leaves.py:152-155)."""
     return ((Xs.astype(np.float32) - mu.astype(np.float32)) / sd.astype(np.float32)).astype(np.float32)

@@ -18,7 +18,7 @@ from tests.helpers import grad_hess, uniform_bins
 from yabt_amd import IdentityBinner, TreeParams, grow_tree_hip
 from yabt_amd import grow_hip as G
 from yabt_amd.losses import MSELoss
-from yabt_amd.neural_leaves import fit_leaf_networks, leaf_fit
+from yabt_amd.neural_leaves import fit_leaf_networks, leaf_fit, leaf_moments
 
 pytestmark = pytest.mark.gpu
 
@@ -77,6 +77,20 @@ def test_leaf_fit_matches_oracle(n, K, n_nodes, x_kind, lam):
     np.testing.assert_allclose(b, rb, rtol=1e-5, atol=1e-6)
 
 
+@pytest.mark.parametrize("n,K,x_kind", [(1, 1, 0), (1000, 3, 0), (100_003, 8, 1), (2_000_000, 5, 1)])
+def test_leaf_moments(n, K, x_kind):
+    X, Xf, feats, g, h, feature, leaf, mu, sd = _problem(n, n, K, 5, bins=x_kind == 1)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    Xd = t(X) if x_kind == 0 else t(np.ascontiguousarray(X.T))
+    m, s = (v.cpu().numpy() for v in leaf_moments(Xd, x_kind, t(feats), n))
+    rm, rs = NO.moments(Xf[:, feats])
+    np.testing.assert_allclose(m, rm, rtol=2e-7, atol=0)
+    if n > 1:
+        np.testing.assert_allclose(s, rs, rtol=2e-7, atol=0)
+    a = [v.cpu().numpy() for v in leaf_moments(Xd, x_kind, t(feats), n)]
+    assert np.array_equal(a[0], m) and np.array_equal(a[1], s)
+
+
 def test_leaf_fit_deterministic_and_u8_equals_f32():
     X, Xf, feats, g, h, feature, leaf, mu, sd = _problem(9, 50_000, 6, 63, bins=True)
     a = _gpu(X, 1, feats, g, h, feature, leaf, mu, sd, 50, 1.0)
@@ -125,8 +139,7 @@ def test_fit_leaf_networks_end_to_end():
     counts = np.bincount(used, minlength=F)
     m = min(8, len(set(used.tolist())))
     assert (np.diff(counts[feats[:m]]) <= 0).all() and (counts[feats[:m]] > 0).all()
-    Xs = Xd[:, out.leaf_net_feats]
-    mu, sd = Xs.mean(dim=0), Xs.std(dim=0).clamp_min(1e-6)
+    mu, sd = (torch.from_numpy(v) for v in NO.moments(Xraw[:, feats]))
     leaf = tree.apply(Xd).cpu().numpy()
     value = tree.value.cpu().numpy()
     g2 = (margin + value[leaf] - y).astype(np.float32)

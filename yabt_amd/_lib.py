@@ -46,6 +46,8 @@ SIGNATURES = {
     "yabt_partition_workspace_bytes": (_sz, []),
     "yabt_partition": (_int, [_vp, _i64, _i64, _int, _int, _vp, _i64, _vp, _vp, _vp, _vp]),
     "yabt_leaf_fit_workspace_bytes": (_sz, [_i64, _int, _int]),
+    "yabt_leaf_moments_workspace_bytes": (_sz, [_i64]),
+    "yabt_leaf_moments": (_int, [_int, _vp, _i64, _i64, _vp, _int, _vp, _sz, _vp, _vp, _vp]),
     "yabt_leaf_fit": (_int, [_int, _vp, _i64, _i64, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _int, _int,
                              _dbl, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
 }

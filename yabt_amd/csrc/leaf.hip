@@ -155,14 +155,12 @@ __global__ void __launch_bounds__(LB) k_leaf_stats(LeafArgs A) {
             const float xn = (x[j] - s_mu[j]) / s_sd[j];
             if (!isfinite(xn)) bad = 1;
             mx = fmaxf(mx, fabsf(xn));
+            // the extremes settle quickly: read first, update only when improving
             const uint32_t kx = float_key(x[j]);
-            if (LDS) {
-                atomicMin(&s_lo[node * K + j], kx);
-                atomicMax(&s_hi[node * K + j], kx);
-            } else {
-                atomicMin(&A.lo_key[node * K + j], kx);
-                atomicMax(&A.hi_key[node * K + j], kx);
-            }
+            uint32_t* plo = LDS ? &s_lo[node * K + j] : &A.lo_key[node * K + j];
+            uint32_t* phi = LDS ? &s_hi[node * K + j] : &A.hi_key[node * K + j];
+            if (kx < *(volatile uint32_t*)plo) atomicMin(plo, kx);
+            if (kx > *(volatile uint32_t*)phi) atomicMax(phi, kx);
         }
         if (LDS) atomicAdd(&s_cnt[node], 1u);
         else atomicAdd(&A.count[node], 1u);
@@ -422,6 +420,75 @@ __global__ void __launch_bounds__(LB) k_leaf_solve(LeafArgs A, float* out_W, flo
 
 __global__ void k_leaf_status(const LeafStats* st, int32_t* out) { out[0] = st->status; }
 
+// ---------------------------------------------------------------------------
+// input moments: mu = mean, sd = max(unbiased std, 1e-6) per input
+// (neural_leaves.py:152-155), from fp64 sums of x and x^2 reduced in a fixed
+// order (per-block partials, then one block), so the result is deterministic
+// ---------------------------------------------------------------------------
+
+constexpr int MROWS = 16384;                   // rows per moments block
+
+template <int K>
+__global__ void __launch_bounds__(LB) k_leaf_moments(int x_kind, const void* X, int64_t ldx, int64_t n,
+                                                     const int32_t* feats, double* part) {
+    __shared__ int32_t s_fs[LKMAX];
+    __shared__ double s_red[LB / WAVE][2 * LKMAX];
+    if (threadIdx.x < K) s_fs[threadIdx.x] = feats[threadIdx.x];
+    __syncthreads();
+    LeafArgs A;
+    A.x_kind = x_kind;
+    A.X = X;
+    A.ldx = ldx;
+    const int64_t lo = (int64_t)blockIdx.x * MROWS, hi = min(n, lo + MROWS);
+    double s1[K], s2[K];
+#pragma unroll
+    for (int j = 0; j < K; ++j) s1[j] = s2[j] = 0.0;
+    for (int64_t i = lo + threadIdx.x; i < hi; i += LB) {
+        float x[K];
+        load_x<K>(A, i, s_fs, x);
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            const double v = (double)x[j];
+            s1[j] += v;
+            s2[j] += v * v;
+        }
+    }
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+#pragma unroll
+    for (int j = 0; j < K; ++j) {
+#pragma unroll
+        for (int d = WAVE / 2; d > 0; d >>= 1) {
+            s1[j] += __shfl_xor(s1[j], d, WAVE);
+            s2[j] += __shfl_xor(s2[j], d, WAVE);
+        }
+        if (lane == 0) {
+            s_red[w][j] = s1[j];
+            s_red[w][LKMAX + j] = s2[j];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < 2 * K) {
+        const int j = threadIdx.x % K, which = threadIdx.x / K;
+        double t = 0.0;
+        for (int i = 0; i < LB / WAVE; ++i) t += s_red[i][which * LKMAX + j];
+        part[((size_t)blockIdx.x * 2 + which) * LKMAX + j] = t;
+    }
+}
+
+__global__ void k_leaf_moments_final(const double* part, int nblocks, int64_t n, int K, float* mu, float* sd) {
+    const int j = threadIdx.x;
+    if (j >= K) return;
+    double s1 = 0.0, s2 = 0.0;
+    for (int b = 0; b < nblocks; ++b) {
+        s1 += part[((size_t)b * 2 + 0) * LKMAX + j];
+        s2 += part[((size_t)b * 2 + 1) * LKMAX + j];
+    }
+    const double m = n > 0 ? s1 / (double)n : NAN;
+    const double var = n > 1 ? fmax(s2 - s1 * m, 0.0) / (double)(n - 1) : NAN;
+    mu[j] = (float)m;
+    sd[j] = fmaxf((float)sqrt(var), 1e-6f);
+}
+
 size_t carve_leaf(char* base, int64_t n, int n_nodes, int K, LeafArgs* A) {
     Carve c{base, 0};
     LeafArgs tmp;
@@ -508,6 +575,35 @@ int yabt_leaf_fit(int x_kind, const void* X, int64_t ldx, int64_t n, const int32
     }
     k_leaf_status<<<1, 1, 0, stream>>>(A.st, out_status);
     return launch_status("yabt_leaf_fit launch");
+}
+
+size_t yabt_leaf_moments_workspace_bytes(int64_t n) {
+    if (n < 0) return 0;
+    const int64_t nb = n > 0 ? (n + MROWS - 1) / MROWS : 1;
+    return align_up((size_t)nb * 2 * LKMAX * sizeof(double), 256);
+}
+
+int yabt_leaf_moments(int x_kind, const void* X, int64_t ldx, int64_t n, const int32_t* feats, int K,
+                      void* workspace, size_t workspace_bytes, float* out_mu, float* out_sd, hipStream_t stream) {
+    if (n < 1 || K < 1 || K > LKMAX || (x_kind != 0 && x_kind != 1))
+        return fail(-2, "yabt_leaf_moments: bad sizes (need n >= 1, 1 <= K <= 8, x_kind 0 or 1)");
+    if (!X || !feats || !workspace || !out_mu || !out_sd) return fail(-2, "yabt_leaf_moments: null pointer argument");
+    if (x_kind == 1 ? ldx < n : ldx < 1) return fail(-2, "yabt_leaf_moments: leading dimension too small");
+    if (workspace_bytes < yabt_leaf_moments_workspace_bytes(n)) return fail(-2, "yabt_leaf_moments: workspace too small");
+    const int nb = (int)((n + MROWS - 1) / MROWS);
+    double* part = (double*)workspace;
+    switch (K) {
+        case 1: k_leaf_moments<1><<<nb, LB, 0, stream>>>(x_kind, X, ldx, n, feats, part); break;
+        case 2: k_leaf_moments<2><<<nb, LB, 0, stream>>>(x_kind, X, ldx, n, feats, part); break;
+        case 3: k_leaf_moments<3><<<nb, LB, 0, stream>>>(x_kind, X, ldx, n, feats, part); break;
+        case 4: k_leaf_moments<4><<<nb, LB, 0, stream>>>(x_kind, X, ldx, n, feats, part); break;
+        case 5: k_leaf_moments<5><<<nb, LB, 0, stream>>>(x_kind, X, ldx, n, feats, part); break;
+        case 6: k_leaf_moments<6><<<nb, LB, 0, stream>>>(x_kind, X, ldx, n, feats, part); break;
+        case 7: k_leaf_moments<7><<<nb, LB, 0, stream>>>(x_kind, X, ldx, n, feats, part); break;
+        default: k_leaf_moments<8><<<nb, LB, 0, stream>>>(x_kind, X, ldx, n, feats, part); break;
+    }
+    k_leaf_moments_final<<<1, WAVE, 0, stream>>>(part, nb, n, K, out_mu, out_sd);
+    return launch_status("yabt_leaf_moments launch");
 }
 
 }  // extern "C"

@@ -5,9 +5,10 @@ is grown, every leaf with at least ``leaf_net_min_samples`` rows gets a ridge
 model over up to ``leaf_net_features`` inputs, fitted to the Newton objective
 at ``margin + value[leaf]``, folded into raw space and shrunk by the learning
 rate, with per-leaf input envelopes.  The per-leaf Gram matrices, envelopes,
-counts and solves run in the HIP kernels of ``csrc/leaf.hip``
-(``yabt_leaf_fit``); feature selection, standardisation and the fold are the
-reference's own torch expressions on the device.  Only the linear form
+counts, solves and the input moments run in the HIP kernels of
+``csrc/leaf.hip`` (``yabt_leaf_moments``, ``yabt_leaf_fit``); feature
+selection and the fold are the reference's own torch expressions on the
+device.  Only the linear form
 (``leaf_net_hidden == 0``) is provided.
 """
 
@@ -101,6 +102,27 @@ def leaf_fit(X: torch.Tensor, x_kind: int, feats: torch.Tensor, mu: torch.Tensor
     return W, b, lo, hi, cnt
 
 
+def leaf_moments(X: torch.Tensor, x_kind: int, feats: torch.Tensor, n: int):
+    """(mu, sd) of the selected inputs over n rows: mean and unbiased std
+    clamped at 1e-6 (neural_leaves.py:152-154), from ``yabt_leaf_moments``."""
+    lib = _lib.load()
+    dev = X.device
+    K = int(feats.numel())
+    if x_kind == 0 and (X.dtype != torch.float32 or X.shape[0] != n or X.stride(1) != 1):
+        raise ValueError("X must be fp32 (n, F) with unit column stride")
+    if x_kind == 1 and (X.dtype != torch.uint8 or X.shape[1] < n or X.stride(1) != 1):
+        raise ValueError("X must be uint8 (F, ld >= n)")
+    fi = feats.to(dev, torch.int32).contiguous()
+    nbytes = int(lib.yabt_leaf_moments_workspace_bytes(n))
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    mu = torch.empty(K, dtype=torch.float32, device=dev)
+    sd = torch.empty(K, dtype=torch.float32, device=dev)
+    _lib.check(lib.yabt_leaf_moments(x_kind, X.data_ptr(), X.stride(0), n, fi.data_ptr(), K, ws.data_ptr(),
+                                     nbytes, mu.data_ptr(), sd.data_ptr(), _stream(dev)),
+               "yabt_leaf_moments")
+    return mu, sd
+
+
 def fold(tree: Tree, W, db, mu, sd, lr, feats, lo, hi) -> Tree:
     """Normalisation and shrinkage folded into raw space (neural_leaves.py:178-184)."""
     value = tree.value.to(W.device) + lr * (db - (W * (mu / sd)).sum(dim=1))
@@ -123,10 +145,8 @@ def fit_leaf_networks(tree: Tree, Xraw: torch.Tensor, y: torch.Tensor, margin: t
     feats = _select_features(tree_d, Xraw, grad, getattr(params, "leaf_net_features", 8))
     if feats.numel() == 0:
         return tree
-    Xs = Xraw[:, feats]
-    mu = Xs.mean(dim=0)
-    sd = Xs.std(dim=0).clamp_min(1e-6)
     X = Xraw if Xraw.dtype == torch.float32 and Xraw.stride(1) == 1 else Xraw.float().contiguous()
+    mu, sd = leaf_moments(X, 0, feats, X.shape[0])
     W, db, lo, hi, cnt = leaf_fit(X, 0, feats, mu, sd, grad, hess, leaf_idx, tree_d.feature,
                                   getattr(params, "leaf_net_min_samples", 50),
                                   getattr(params, "leaf_net_l2", 1.0))
@@ -156,10 +176,7 @@ def fit_leaf_networks_binned(tree: Tree, bins_fm: torch.Tensor, grad: torch.Tens
         # padding by gradient correlation needs the raw columns: take them as floats
         Xraw = bins_fm[:, :n].t().float()
         feats = _select_features(replace(tree, feature=feature), Xraw, grad, k)
-    Xs = bins_fm[feats, :n].float()              # (K, n)
-    mu = Xs.mean(dim=1)
-    sd = Xs.std(dim=1).clamp_min(1e-6)
-    del Xs
+    mu, sd = leaf_moments(bins_fm, 1, feats, n)
     W, db, lo, hi, cnt = leaf_fit(bins_fm, 1, feats, mu, sd, grad, hess, leaf_idx, feature,
                                   getattr(params, "leaf_net_min_samples", 50),
                                   getattr(params, "leaf_net_l2", 1.0))
