@@ -164,6 +164,21 @@ int yabt_leaf_moments(int x_kind, const void *X, int64_t ldx, int64_t n, const i
                       void *workspace, size_t workspace_bytes, float *out_mu, float *out_sd,
                       yabt_stream_t stream);
 
+/* Workspace bytes of yabt_hist_slots. */
+size_t yabt_hist_slots_workspace_bytes(int64_t n, int F, int K);
+
+/* K-slot histogram of the level-wise grower: out (3, K, F, 256) fp32,
+ * out[0][s][f][b] = sum g, out[1] = sum h, out[2] = sum w over the rows i with
+ * slot[i] == s and binned[i*ldb + f] == b; rows with slot outside [0, K) are
+ * skipped.  g, h, w are each quantised to int64 fixed point (one shift per
+ * channel from max|.| and n), summed exactly and rounded to fp32.
+ * out_status (device int32 x 4): status (0, or -1 for a non-finite input) and
+ * the three shifts.  Replaces `hist_build` (yabt/_cuda/hist.cu:101-133) behind
+ * `cuda_hist.build_hist` (yabt/cuda_hist.py:79-89), B fixed at 256. */
+int yabt_hist_slots(const uint8_t *binned, int64_t ldb, const int64_t *slot, const float *g,
+                    const float *h, const float *w, int64_t n, int F, int K, void *workspace,
+                    size_t workspace_bytes, float *out, int32_t *out_status, yabt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

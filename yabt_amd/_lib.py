@@ -45,6 +45,8 @@ SIGNATURES = {
                                _vp, _vp, _vp]),
     "yabt_partition_workspace_bytes": (_sz, []),
     "yabt_partition": (_int, [_vp, _i64, _i64, _int, _int, _vp, _i64, _vp, _vp, _vp, _vp]),
+    "yabt_hist_slots_workspace_bytes": (_sz, [_i64, _int, _int]),
+    "yabt_hist_slots": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _int, _int, _vp, _sz, _vp, _vp, _vp]),
     "yabt_leaf_fit_workspace_bytes": (_sz, [_i64, _int, _int]),
     "yabt_leaf_moments_workspace_bytes": (_sz, [_i64]),
     "yabt_leaf_moments": (_int, [_int, _vp, _i64, _i64, _vp, _int, _vp, _sz, _vp, _vp, _vp]),

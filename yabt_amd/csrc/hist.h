@@ -315,7 +315,7 @@ __device__ __forceinline__ void hist_root_packed(HistLdsP& L, const uint8_t* __r
 }
 
 // count_mode 0: all three channels; 1: no h channel when q->const_h.
-static __global__ void __launch_bounds__(HBLOCK) k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld,
+static __global__ __attribute__((unused)) void __launch_bounds__(HBLOCK) k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld,
                                                       const float* __restrict__ grad,
                                                       const float* __restrict__ hess, int64_t n, int F,
                                                       const Quant* q, double scg_v, double sch_v,
@@ -603,7 +603,7 @@ __device__ __forceinline__ void hist_gather_packed(HistLdsP& L, const uint8_t* _
 
 // job->active == 0 or *done != 0 (done may be NULL): nothing to do.  wlog:
 // pack_window_log2(n) for the n rows the shifts were chosen for.
-static __global__ void __launch_bounds__(HBLOCK) k_hist_gather(const uint8_t* __restrict__ bins_rm, int64_t ld,
+static __global__ __attribute__((unused)) void __launch_bounds__(HBLOCK) k_hist_gather(const uint8_t* __restrict__ bins_rm, int64_t ld,
                                                         const float* __restrict__ grad,
                                                         const float* __restrict__ hess, int F, const Quant* q,
                                                         double scg_v, double sch_v,
