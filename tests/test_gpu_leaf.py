@@ -108,6 +108,14 @@ def test_leaf_fit_rejects_bad_leaf_ids():
         _gpu(X, 0, feats, g, h, feature, leaf, mu, sd, 50, 1.0)
 
 
+def test_leaf_fit_rejects_nonfinite_inputs():
+    X, Xf, feats, g, h, feature, leaf, mu, sd = _problem(4, 1000, 3, 9)
+    X = X.copy()
+    X[5, feats[1]] = np.nan
+    with pytest.raises(ValueError):
+        _gpu(X, 0, feats, g, h, feature, leaf, mu, sd, 50, 1.0)
+
+
 @dataclass
 class _P:
     learning_rate: float = 0.1

@@ -21,7 +21,8 @@
 //   k_leaf_stats<K>    rows per node, envelopes min/max of raw x, max |x1|, |g|, |h|
 //   k_leaf_offsets     node offsets of the sorted rows, fixed-point shifts
 //   k_leaf_scatter     rows -> sorted by node
-//   k_leaf_gram<K>     per-leaf fixed-point sums of M and b
+//   k_leaf_gram<K>     fixed-point sums of M and b per (chunk, leaf) segment
+//   k_leaf_reduce<K>   per-leaf sums of the segments
 //   k_leaf_solve<K>    fp64 LU with partial pivoting per eligible leaf
 
 #include "common.h"
@@ -68,8 +69,10 @@ struct LeafArgs {
     uint32_t* count;           // (n_nodes)
     int64_t* off;              // (n_nodes + 1)
     unsigned long long* cursor;   // (n_nodes)
-    uint32_t* sorted;          // (n)
+    uint8_t* sorted_x;         // rows' inputs in sorted order: 8 bytes (uint8) or K floats per row
+    float2* sorted_gh;         // (n) g, h in sorted order
     int64_t* sums;             // (n_nodes, gram_entries(LKMAX))
+    int64_t* parts;            // (chunks + n_nodes, gram_entries(LKMAX)) per-segment partial sums
     uint32_t* lo_key;          // (n_nodes, K) order-preserving float keys
     uint32_t* hi_key;
 };
@@ -120,12 +123,7 @@ __global__ void __launch_bounds__(LB) k_leaf_stats(LeafArgs A) {
     __shared__ float s_red[3][LB / WAVE];
     __shared__ int s_bad;
     __shared__ int32_t s_fs[LKMAX];
-    __shared__ float s_mu[LKMAX], s_sd[LKMAX];
-    if (threadIdx.x < K) {
-        s_fs[threadIdx.x] = A.feats[threadIdx.x];
-        s_mu[threadIdx.x] = A.mu[threadIdx.x];
-        s_sd[threadIdx.x] = A.sd[threadIdx.x];
-    }
+    if (threadIdx.x < K) s_fs[threadIdx.x] = A.feats[threadIdx.x];
     if (threadIdx.x == 0) s_bad = 0;
     if (LDS) {
         for (int i = threadIdx.x; i < A.n_nodes; i += LB) s_cnt[i] = 0;
@@ -136,7 +134,7 @@ __global__ void __launch_bounds__(LB) k_leaf_stats(LeafArgs A) {
     }
     __syncthreads();
     const int64_t lo = (int64_t)blockIdx.x * LROWS, hi = min(A.n, lo + LROWS);
-    float mx = 1.0f, mg = 0.0f, mh = 0.0f;
+    float mg = 0.0f, mh = 0.0f;
     int bad = 0;
     for (int64_t i = lo + threadIdx.x; i < hi; i += LB) {
         const int64_t node = A.leaf[i];
@@ -150,11 +148,10 @@ __global__ void __launch_bounds__(LB) k_leaf_stats(LeafArgs A) {
         if (!isfinite(gi) || !isfinite(hi_)) bad = 1;
         mg = fmaxf(mg, fabsf(gi));
         mh = fmaxf(mh, fabsf(hi_));
+        // per-node envelopes; their extremes also bound |x1| (k_leaf_offsets) and
+        // expose non-finite inputs (keys beyond those of -inf / +inf)
 #pragma unroll
         for (int j = 0; j < K; ++j) {
-            const float xn = (x[j] - s_mu[j]) / s_sd[j];
-            if (!isfinite(xn)) bad = 1;
-            mx = fmaxf(mx, fabsf(xn));
             // the extremes settle quickly: read first, update only when improving
             const uint32_t kx = float_key(x[j]);
             uint32_t* plo = LDS ? &s_lo[node * K + j] : &A.lo_key[node * K + j];
@@ -169,24 +166,20 @@ __global__ void __launch_bounds__(LB) k_leaf_stats(LeafArgs A) {
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
 #pragma unroll
     for (int d = WAVE / 2; d > 0; d >>= 1) {
-        mx = fmaxf(mx, __shfl_xor(mx, d, WAVE));
         mg = fmaxf(mg, __shfl_xor(mg, d, WAVE));
         mh = fmaxf(mh, __shfl_xor(mh, d, WAVE));
     }
     if (lane == 0) {
-        s_red[0][w] = mx;
         s_red[1][w] = mg;
         s_red[2][w] = mh;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int i = 1; i < LB / WAVE; ++i) {
-            mx = fmaxf(mx, s_red[0][i]);
             mg = fmaxf(mg, s_red[1][i]);
             mh = fmaxf(mh, s_red[2][i]);
         }
         // |x| <= inf as float bits: non-negative floats order like their bits
-        atomicMax(&A.st->max_x1_bits, __float_as_uint(mx));
         atomicMax(&A.st->max_g_bits, __float_as_uint(mg));
         atomicMax(&A.st->max_h_bits, __float_as_uint(mh));
         if (s_bad) atomicMin(&A.st->status, -1);
@@ -203,8 +196,19 @@ __global__ void __launch_bounds__(LB) k_leaf_stats(LeafArgs A) {
 
 // One block: node offsets of the sorted rows (exclusive scan of the counts),
 // write cursors, and the fixed-point shifts.
-__global__ void __launch_bounds__(1024) k_leaf_offsets(LeafArgs A) {
+__global__ void __launch_bounds__(1024) k_leaf_offsets(LeafArgs A, int K) {
     __shared__ int64_t s_wave[1024 / WAVE];
+    __shared__ uint32_t s_xlo[LKMAX], s_xhi[LKMAX];
+    if (threadIdx.x < K) {
+        s_xlo[threadIdx.x] = float_key(INFINITY);
+        s_xhi[threadIdx.x] = float_key(-INFINITY);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < A.n_nodes * K; i += 1024) {
+        atomicMin(&s_xlo[i % K], A.lo_key[i]);
+        atomicMax(&s_xhi[i % K], A.hi_key[i]);
+    }
+    __syncthreads();
     int64_t carry = 0;
     for (int base = 0; base < A.n_nodes; base += 1024) {
         const int i = base + threadIdx.x;
@@ -219,9 +223,24 @@ __global__ void __launch_bounds__(1024) k_leaf_offsets(LeafArgs A) {
     }
     if (threadIdx.x == 0) {
         A.off[A.n_nodes] = carry;
+        // max |x1| <= max(1, max_j max(|xmax_j - mu_j|, |xmin_j - mu_j|) / sd_j),
+        // taken 2^-20 above for the fp32 rounding of (x - mu) / sd
+        double mx = 1.0;
+        for (int j = 0; j < K; ++j) {
+            if (s_xlo[j] == float_key(INFINITY)) continue;                 // no rows at all
+            if (s_xlo[j] < float_key(-INFINITY) || s_xhi[j] > float_key(INFINITY) ||
+                !isfinite(key_float(s_xlo[j])) || !isfinite(key_float(s_xhi[j]))) {
+                atomicMin(&A.st->status, -1);                               // a non-finite input
+                continue;
+            }
+            const double m = (double)A.mu[j], d = (double)A.sd[j];
+            const double b = fmax(fabs((double)key_float(s_xhi[j]) - m), fabs((double)key_float(s_xlo[j]) - m)) / d;
+            mx = fmax(mx, b * (1.0 + 0x1p-20));
+        }
+        if (!isfinite(mx)) atomicMin(&A.st->status, -1);
+        A.st->max_x1_bits = __float_as_uint((float)mx);
         // |p| <= max|x1|^2 max|h| for M and max|x1| max|g| for b; the bounds
         // are taken 2^-20 above to cover the rounding of the fp64 products
-        const double mx = (double)__uint_as_float(A.st->max_x1_bits);
         const double bm = mx * mx * (double)__uint_as_float(A.st->max_h_bits) * (1.0 + 0x1p-20);
         const double bb = mx * (double)__uint_as_float(A.st->max_g_bits) * (1.0 + 0x1p-20);
         const float fm = (float)bm, fb = (float)bb;
@@ -232,8 +251,32 @@ __global__ void __launch_bounds__(1024) k_leaf_offsets(LeafArgs A) {
 
 // Rows [blockIdx.x * LROWS, +LROWS) to their node's range of `sorted`; the
 // block reserves one range per node with one atomic add.
-template <bool LDS>
+// The inputs, g and h of row i go to position pos of the sorted arrays.
+template <int K>
+__device__ __forceinline__ void put_sorted(const LeafArgs& A, const int32_t* fs, int64_t i, uint64_t pos) {
+    A.sorted_gh[pos] = make_float2(A.grad[i], A.hess[i]);
+    if (A.x_kind == 1) {
+        const uint8_t* B = reinterpret_cast<const uint8_t*>(A.X);
+        uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            const uint32_t b = B[(size_t)fs[j] * (size_t)A.ldx + (size_t)i];
+            if (j < 4) w0 |= b << (8 * j);
+            else w1 |= b << (8 * (j - 4));
+        }
+        reinterpret_cast<uint2*>(A.sorted_x)[pos] = make_uint2(w0, w1);
+    } else {
+        const float* row = reinterpret_cast<const float*>(A.X) + (size_t)i * (size_t)A.ldx;
+        float* dst = reinterpret_cast<float*>(A.sorted_x) + pos * K;
+#pragma unroll
+        for (int j = 0; j < K; ++j) dst[j] = row[fs[j]];
+    }
+}
+
+template <int K, bool LDS>
 __global__ void __launch_bounds__(LB) k_leaf_scatter(LeafArgs A) {
+    __shared__ int32_t s_fs[LKMAX];
+    if (threadIdx.x < K) s_fs[threadIdx.x] = A.feats[threadIdx.x];
     __shared__ uint32_t s_cnt[LDS ? LDS_NODES : 1];
     __shared__ unsigned long long s_base[LDS ? LDS_NODES : 1];
     if (LDS)
@@ -255,13 +298,13 @@ __global__ void __launch_bounds__(LB) k_leaf_scatter(LeafArgs A) {
             const int64_t node = A.leaf[i];
             if (node < 0 || node >= A.n_nodes) continue;
             const uint32_t r = atomicAdd(&s_cnt[node], 1u);
-            A.sorted[s_base[node] + r] = (uint32_t)i;
+            put_sorted<K>(A, s_fs, i, s_base[node] + r);
         }
     } else {
         for (int64_t i = lo + threadIdx.x; i < hi; i += LB) {
             const int64_t node = A.leaf[i];
             if (node < 0 || node >= A.n_nodes) continue;
-            A.sorted[atomicAdd(&A.cursor[node], 1ull)] = (uint32_t)i;
+            put_sorted<K>(A, s_fs, i, atomicAdd(&A.cursor[node], 1ull));
         }
     }
 }
@@ -273,11 +316,16 @@ __device__ __forceinline__ bool leaf_eligible(const LeafArgs& A, int node) {
 // Sorted positions [blockIdx.x * LCHUNK, +LCHUNK): for each node run inside
 // the chunk, every thread sums the fixed-point products of its rows in
 // registers; waves reduce with DPP and add into the node's sums.
-template <int K>
+// FAST (n > 1024, so every scaled product is below 2^51 in magnitude): the
+// product is rounded to an integer by adding 1.5 * 2^52 (round to nearest
+// even, like rint) and its bits are summed as they are; the constant's bits
+// are taken off once per row at the end.  Otherwise rint and a conversion.
+template <int K, bool FAST>
 __global__ void __launch_bounds__(LB) k_leaf_gram(LeafArgs A) {
     constexpr int NE = gram_entries(K);
     __shared__ int32_t s_fs[LKMAX];
     __shared__ float s_mu[LKMAX], s_sd[LKMAX];
+    __shared__ int64_t s_part[LB / WAVE][NE];
     if (threadIdx.x < K) {
         s_fs[threadIdx.x] = A.feats[threadIdx.x];
         s_mu[threadIdx.x] = A.mu[threadIdx.x];
@@ -295,40 +343,99 @@ __global__ void __launch_bounds__(LB) k_leaf_gram(LeafArgs A) {
         if (A.off[mid] <= c0) lo = mid;
         else hi = mid - 1;
     }
-    const int lane = threadIdx.x & (WAVE - 1);
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
     for (int node = lo; node < A.n_nodes && A.off[node] < c1; ++node) {
         const int64_t s = max(c0, A.off[node]), e = min(c1, A.off[node + 1]);
         if (s >= e || !leaf_eligible(A, node)) continue;   // uniform across the block
-        int64_t acc[NE];
+        constexpr double MAGIC = 6755399441055744.0;   // 1.5 * 2^52
+        uint64_t acc[NE];
 #pragma unroll
         for (int t = 0; t < NE; ++t) acc[t] = 0;
+        uint64_t nrow = 0;
         for (int64_t p = s + threadIdx.x; p < e; p += LB) {
-            const int64_t i = A.sorted[p];
+            const float2 gh = A.sorted_gh[p];
             float x[K];
-            load_x<K>(A, i, s_fs, x);
-            const double g = (double)A.grad[i], h = (double)A.hess[i];
-            double x1[K + 1];
+            if (A.x_kind == 1) {
+                const uint2 v = reinterpret_cast<const uint2*>(A.sorted_x)[p];
+#pragma unroll
+                for (int j = 0; j < K; ++j) x[j] = (float)(((j < 4 ? v.x : v.y) >> (8 * (j & 3))) & 0xffu);
+            } else {
+                const float* src = reinterpret_cast<const float*>(A.sorted_x) + (size_t)p * K;
+#pragma unroll
+                for (int j = 0; j < K; ++j) x[j] = src[j];
+            }
+            const double h = (double)gh.y;
+            const double gs = (double)gh.x * scb;           // exact power-of-two scaling
+            double x1[K + 1], xhs[K + 1];
 #pragma unroll
             for (int j = 0; j < K; ++j) x1[j] = (double)((x[j] - s_mu[j]) / s_sd[j]);
             x1[K] = 1.0;
+#pragma unroll
+            for (int b = 0; b <= K; ++b) xhs[b] = (x1[b] * h) * scM;   // Xh = X1 * h (neural_leaves.py:72), scaled
+            ++nrow;
             int t = 0;
 #pragma unroll
             for (int a = 0; a <= K; ++a) {
 #pragma unroll
                 for (int b = a; b <= K; ++b) {
-                    const double xh = x1[b] * h;             // Xh = X1 * h    (neural_leaves.py:72)
-                    acc[t++] += (int64_t)rint(x1[a] * xh * scM);
+                    const double v = x1[a] * xhs[b];      // the reference's product, times 2^sM exactly
+                    if (FAST) acc[t++] += (uint64_t)__double_as_longlong(v + MAGIC);
+                    else acc[t++] += (uint64_t)(int64_t)rint(v);
                 }
             }
 #pragma unroll
-            for (int a = 0; a <= K; ++a) acc[t++] += (int64_t)rint(-(x1[a] * g) * scb);   // rhs = -(X1 * g)
+            for (int a = 0; a <= K; ++a) {                // rhs = -(X1 * g)
+                const double v = -(x1[a] * gs);
+                if (FAST) acc[t++] += (uint64_t)__double_as_longlong(v + MAGIC);
+                else acc[t++] += (uint64_t)(int64_t)rint(v);
+            }
         }
-        int64_t* out = A.sums + (size_t)node * gram_entries(LKMAX);
+        if (FAST) {
+            const uint64_t off = nrow * (uint64_t)__double_as_longlong(MAGIC);
+#pragma unroll
+            for (int t = 0; t < NE; ++t) acc[t] -= off;
+        }
+        // block sum of this (chunk, node) segment into its own partial slot,
+        // chunk + node: distinct for every segment (nodes and chunks both
+        // advance along the sorted rows), so no atomics and no contention
 #pragma unroll
         for (int t = 0; t < NE; ++t) {
-            const int64_t v = wave_sum_i64(acc[t]);
-            if (lane == 0 && v != 0) atomicAdd((unsigned long long*)&out[t], (unsigned long long)v);
+            const int64_t v = wave_sum_i64((int64_t)acc[t]);
+            if (lane == 0) s_part[w][t] = v;
         }
+        __syncthreads();
+        int64_t* out = A.parts + ((size_t)blockIdx.x + (size_t)node) * gram_entries(LKMAX);
+        for (int t = threadIdx.x; t < NE; t += LB) {
+            int64_t v = 0;
+#pragma unroll
+            for (int i = 0; i < LB / WAVE; ++i) v += s_part[i][t];
+            out[t] = v;
+        }
+        __syncthreads();
+    }
+}
+
+// One wave per eligible node: the sum of its segments' partials (chunks
+// first_chunk .. last_chunk of the sorted rows), in a fixed order.
+template <int K>
+__global__ void __launch_bounds__(WAVE) k_leaf_reduce(LeafArgs A) {
+    constexpr int NE = gram_entries(K);
+    const int node = blockIdx.x, lane = threadIdx.x;
+    if (!leaf_eligible(A, node)) return;
+    const int64_t c0 = A.off[node] / LCHUNK, c1 = (A.off[node + 1] - 1) / LCHUNK;
+    int64_t acc[NE];
+#pragma unroll
+    for (int t = 0; t < NE; ++t) acc[t] = 0;
+    for (int64_t c = c0 + lane; c <= c1; c += WAVE) {
+        const int64_t* q = A.parts + ((size_t)c + (size_t)node) * gram_entries(LKMAX);
+#pragma unroll
+        for (int t = 0; t < NE; ++t) acc[t] += q[t];
+    }
+    int64_t* out = A.sums + (size_t)node * gram_entries(LKMAX);
+#pragma unroll
+    for (int t = 0; t < NE; ++t) {
+        const int64_t v = wave_sum_i64(acc[t]);
+        if (lane == 0) out[t] = v;
     }
 }
 
@@ -420,6 +527,8 @@ __global__ void __launch_bounds__(LB) k_leaf_solve(LeafArgs A, float* out_W, flo
 
 __global__ void k_leaf_status(const LeafStats* st, int32_t* out) { out[0] = st->status; }
 
+
+
 // ---------------------------------------------------------------------------
 // input moments: mu = mean, sd = max(unbiased std, 1e-6) per input
 // (neural_leaves.py:152-155), from fp64 sums of x and x^2 reduced in a fixed
@@ -428,6 +537,7 @@ __global__ void k_leaf_status(const LeafStats* st, int32_t* out) { out[0] = st->
 
 constexpr int MROWS = 16384;                   // rows per moments block
 
+// fp32 inputs: per-block fp64 partials of x and x^2.
 template <int K>
 __global__ void __launch_bounds__(LB) k_leaf_moments(int x_kind, const void* X, int64_t ldx, int64_t n,
                                                      const int32_t* feats, double* part) {
@@ -475,16 +585,93 @@ __global__ void __launch_bounds__(LB) k_leaf_moments(int x_kind, const void* X, 
     }
 }
 
+// One wave per input: lane l sums partials l, l + 64, ..., then a fixed
+// butterfly; the same order on every run.
 __global__ void k_leaf_moments_final(const double* part, int nblocks, int64_t n, int K, float* mu, float* sd) {
-    const int j = threadIdx.x;
+    const int j = blockIdx.x, lane = threadIdx.x;
     if (j >= K) return;
     double s1 = 0.0, s2 = 0.0;
-    for (int b = 0; b < nblocks; ++b) {
+    for (int b = lane; b < nblocks; b += WAVE) {
         s1 += part[((size_t)b * 2 + 0) * LKMAX + j];
         s2 += part[((size_t)b * 2 + 1) * LKMAX + j];
     }
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) {
+        s1 += __shfl_xor(s1, d, WAVE);
+        s2 += __shfl_xor(s2, d, WAVE);
+    }
+    if (lane != 0) return;
     const double m = n > 0 ? s1 / (double)n : NAN;
     const double var = n > 1 ? fmax(s2 - s1 * m, 0.0) / (double)(n - 1) : NAN;
+    mu[j] = (float)m;
+    sd[j] = fmaxf((float)sqrt(var), 1e-6f);
+}
+
+// uint8 inputs: exact integer sums of x and x^2, 16 rows per 16-byte load;
+// grid (MU8_BLOCKS, K), one partial pair per block (no atomics).
+constexpr int MU8_BLOCKS = 256;
+
+__global__ void __launch_bounds__(LB) k_leaf_moments_u8(const uint8_t* X, int64_t ldx, int64_t n,
+                                                        const int32_t* feats, uint64_t* part) {
+    __shared__ uint64_t s_red[2][LB / WAVE];
+    const int j = blockIdx.y;
+    const uint8_t* col = X + (size_t)feats[j] * (size_t)ldx;
+    uint64_t s1 = 0, s2 = 0;
+    const int64_t n16 = n / 16 * 16;
+    const bool vec = ((uintptr_t)col & 15u) == 0;
+    const int64_t stride = (int64_t)gridDim.x * LB;
+    if (vec) {
+        for (int64_t i = ((int64_t)blockIdx.x * LB + threadIdx.x) * 16; i < n16; i += stride * 16) {
+            const uint4 v = *reinterpret_cast<const uint4*>(col + i);
+            const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+            uint32_t a1 = 0, a2 = 0;                  // 16 bytes: sums fit 32 bits
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t b = (w[k] >> (8 * t)) & 0xffu;
+                    a1 += b;
+                    a2 += b * b;
+                }
+            s1 += a1;
+            s2 += a2;
+        }
+    }
+    for (int64_t i = (vec ? n16 : 0) + (int64_t)blockIdx.x * LB + threadIdx.x; i < n; i += stride) {
+        const uint32_t b = col[i];
+        s1 += b;
+        s2 += b * b;
+    }
+    s1 = (uint64_t)wave_sum_i64((int64_t)s1);
+    s2 = (uint64_t)wave_sum_i64((int64_t)s2);
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+    if (lane == 0) {
+        s_red[0][w] = s1;
+        s_red[1][w] = s2;
+    }
+    __syncthreads();
+    if (threadIdx.x < 2) {
+        uint64_t t = 0;
+        for (int i = 0; i < LB / WAVE; ++i) t += s_red[threadIdx.x][i];
+        part[((size_t)j * gridDim.x + blockIdx.x) * 2 + threadIdx.x] = t;
+    }
+}
+
+// One wave per input: exact sums, then mean and unbiased variance from the
+// exact n (n - 1) var = n sum x^2 - (sum x)^2.
+__global__ void k_leaf_moments_u8_final(const uint64_t* part, int nblocks, int64_t n, float* mu, float* sd) {
+    const int j = blockIdx.x, lane = threadIdx.x;
+    uint64_t s1 = 0, s2 = 0;
+    for (int b = lane; b < nblocks; b += WAVE) {
+        s1 += part[((size_t)j * nblocks + b) * 2];
+        s2 += part[((size_t)j * nblocks + b) * 2 + 1];
+    }
+    s1 = (uint64_t)wave_sum_i64((int64_t)s1);
+    s2 = (uint64_t)wave_sum_i64((int64_t)s2);
+    if (lane != 0) return;
+    const double m = (double)s1 / (double)n;
+    const __int128 num = (__int128)n * (__int128)s2 - (__int128)s1 * (__int128)s1;
+    const double var = n > 1 ? (double)num / ((double)n * (double)(n - 1)) : NAN;
     mu[j] = (float)m;
     sd[j] = fmaxf((float)sqrt(var), 1e-6f);
 }
@@ -497,8 +684,10 @@ size_t carve_leaf(char* base, int64_t n, int n_nodes, int K, LeafArgs* A) {
     a.count = c.take<uint32_t>((size_t)n_nodes);
     a.off = c.take<int64_t>((size_t)n_nodes + 1);
     a.cursor = c.take<unsigned long long>((size_t)n_nodes);
-    a.sorted = c.take<uint32_t>((size_t)(n > 0 ? n : 1));
+    a.sorted_x = c.take<uint8_t>((size_t)(n > 0 ? n : 1) * 4 * LKMAX);
+    a.sorted_gh = c.take<float2>((size_t)(n > 0 ? n : 1));
     a.sums = c.take<int64_t>((size_t)n_nodes * gram_entries(LKMAX));
+    a.parts = c.take<int64_t>(((size_t)((n + LCHUNK - 1) / LCHUNK) + (size_t)n_nodes) * gram_entries(LKMAX));
     a.lo_key = c.take<uint32_t>((size_t)n_nodes * K);
     a.hi_key = c.take<uint32_t>((size_t)n_nodes * K);
     return align_up(c.off, 256);
@@ -514,11 +703,13 @@ void launch_leaf_fit(LeafArgs& A, float* out_W, float* out_b, float* out_lo, flo
         if (lds) k_leaf_stats<K, true><<<row_blocks, LB, 0, stream>>>(A);
         else k_leaf_stats<K, false><<<row_blocks, LB, 0, stream>>>(A);
     }
-    k_leaf_offsets<<<1, 1024, 0, stream>>>(A);
+    k_leaf_offsets<<<1, 1024, 0, stream>>>(A, K);
     if (row_blocks > 0) {
-        if (lds) k_leaf_scatter<true><<<row_blocks, LB, 0, stream>>>(A);
-        else k_leaf_scatter<false><<<row_blocks, LB, 0, stream>>>(A);
-        k_leaf_gram<K><<<(int)((A.n + LCHUNK - 1) / LCHUNK), LB, 0, stream>>>(A);
+        if (lds) k_leaf_scatter<K, true><<<row_blocks, LB, 0, stream>>>(A);
+        else k_leaf_scatter<K, false><<<row_blocks, LB, 0, stream>>>(A);
+        if (A.n > 1024) k_leaf_gram<K, true><<<(int)((A.n + LCHUNK - 1) / LCHUNK), LB, 0, stream>>>(A);
+        else k_leaf_gram<K, false><<<(int)((A.n + LCHUNK - 1) / LCHUNK), LB, 0, stream>>>(A);
+        k_leaf_reduce<K><<<A.n_nodes, WAVE, 0, stream>>>(A);
     }
     k_leaf_solve<K><<<(A.n_nodes + LB - 1) / LB, LB, 0, stream>>>(A, out_W, out_b, out_lo, out_hi, out_count);
 }
@@ -580,7 +771,8 @@ int yabt_leaf_fit(int x_kind, const void* X, int64_t ldx, int64_t n, const int32
 size_t yabt_leaf_moments_workspace_bytes(int64_t n) {
     if (n < 0) return 0;
     const int64_t nb = n > 0 ? (n + MROWS - 1) / MROWS : 1;
-    return align_up((size_t)nb * 2 * LKMAX * sizeof(double), 256);
+    const size_t f = (size_t)nb * 2 * LKMAX * sizeof(double), u = (size_t)MU8_BLOCKS * LKMAX * 2 * sizeof(uint64_t);
+    return align_up(f > u ? f : u, 256);
 }
 
 int yabt_leaf_moments(int x_kind, const void* X, int64_t ldx, int64_t n, const int32_t* feats, int K,
@@ -592,6 +784,12 @@ int yabt_leaf_moments(int x_kind, const void* X, int64_t ldx, int64_t n, const i
     if (workspace_bytes < yabt_leaf_moments_workspace_bytes(n)) return fail(-2, "yabt_leaf_moments: workspace too small");
     const int nb = (int)((n + MROWS - 1) / MROWS);
     double* part = (double*)workspace;
+    if (x_kind == 1) {
+        const int gb = launch_grid((n + 15) / 16, LB, MU8_BLOCKS);
+        k_leaf_moments_u8<<<dim3(gb, K), LB, 0, stream>>>((const uint8_t*)X, ldx, n, feats, (uint64_t*)workspace);
+        k_leaf_moments_u8_final<<<K, WAVE, 0, stream>>>((const uint64_t*)workspace, gb, n, out_mu, out_sd);
+        return launch_status("yabt_leaf_moments launch");
+    }
     switch (K) {
         case 1: k_leaf_moments<1><<<nb, LB, 0, stream>>>(x_kind, X, ldx, n, feats, part); break;
         case 2: k_leaf_moments<2><<<nb, LB, 0, stream>>>(x_kind, X, ldx, n, feats, part); break;
@@ -602,7 +800,7 @@ int yabt_leaf_moments(int x_kind, const void* X, int64_t ldx, int64_t n, const i
         case 7: k_leaf_moments<7><<<nb, LB, 0, stream>>>(x_kind, X, ldx, n, feats, part); break;
         default: k_leaf_moments<8><<<nb, LB, 0, stream>>>(x_kind, X, ldx, n, feats, part); break;
     }
-    k_leaf_moments_final<<<1, WAVE, 0, stream>>>(part, nb, n, K, out_mu, out_sd);
+    k_leaf_moments_final<<<K, WAVE, 0, stream>>>(part, nb, n, K, out_mu, out_sd);
     return launch_status("yabt_leaf_moments launch");
 }
 
