@@ -179,6 +179,50 @@ int yabt_hist_slots(const uint8_t *binned, int64_t ldb, const int64_t *slot, con
                     const float *h, const float *w, int64_t n, int F, int K, void *workspace,
                     size_t workspace_bytes, float *out, int32_t *out_status, yabt_stream_t stream);
 
+/* Gradients and hessians of the boosting losses, fp32 (n rows):
+ *   loss 0, MSELoss:  g = m - y, h = 1            (yabt/boosting.py:52-54)
+ *   loss 1, LogLoss:  p = 1 / (1 + exp(-m)), g = p - y, h = max(p (1 - p), 1e-6)
+ *                                                 (yabt/boosting.py:35-38)
+ * with m = margin[i], or m = margin[i] + value[leaf_of_row[i]] when both
+ * leaf_of_row and value (n_nodes entries) are given (the leaf-model targets of
+ * yabt/neural_leaves.py:147); a leaf id outside [0, n_nodes) reads nothing
+ * and leaves m = margin[i].  Replaces `self.loss.grad_hess(margin, yt)`
+ * (yabt/boosting.py:362). */
+int yabt_grad_hess(int loss, const float *margin, const int64_t *leaf_of_row, const float *value,
+                   int64_t n_nodes, const float *y, int64_t n, float *out_g, float *out_h,
+                   yabt_stream_t stream);
+
+/* Margin update of one boosting round, in place (n rows):
+ *   margin[i] += value[l] + sum_{j<K} linear[l*K+j] * clamp(x_ij, lo[l*K+j], hi[l*K+j]),
+ *   l = leaf_of_row[i] in [0, n_nodes) (rows with other ids are left unchanged);
+ *   K = 0 adds value[l] only (no leaf models);
+ * inputs x_ij as in yabt_leaf_fit (x_kind 0: fp32 row-major X[i*ldx + feats[j]];
+ * x_kind 1: uint8 feature-major X[feats[j]*ldx + i]); 0 <= K <= 8.
+ * Replaces `contrib = tree.value[leaf_idx] + tree.net_contribution(Xraw,
+ * leaf_idx); margin = margin + contrib` (yabt/boosting.py:508-511,
+ * yabt/tree.py:118-128). */
+int yabt_margin_update(float *margin, int64_t n, const int64_t *leaf_of_row, const float *value,
+                       int64_t n_nodes, int K, const int32_t *feats, const float *linear,
+                       const float *lo, const float *hi, int x_kind, const void *X, int64_t ldx,
+                       yabt_stream_t stream);
+
+/* Forest prediction: out[i] = (accumulate ? out[i] : base) + sum over trees
+ * t = 0..T-1, in order, of value[node] + the node's linear-leaf contribution,
+ * where node is the leaf that row i of X (fp32 row-major, ldx >= F) reaches in
+ * tree t.  The trees are concatenated: tree t owns global nodes
+ * [node_off[t], node_off[t+1]) (node_off (T+1) int64 on the device,
+ * node_off[T] <= n_total) and its left/right ids are local to the tree.
+ * Linear leaves (optional, net_k == NULL for none): tree t has net_k[t] <= K
+ * inputs net_feats[t*K + j]; linear, lo, hi are (n_total, K) (lo/hi NULL:
+ * unclamped).  Replaces `Booster._margin` / `Tree.predict`
+ * (yabt/boosting.py:536-545, yabt/tree.py:82-135) and `capply`
+ * (yabt/_cgrow/grow.c:223-239) for whole forests. */
+int yabt_predict(const float *X, int64_t ldx, int64_t n, int F, int T, const int64_t *node_off,
+                 int64_t n_total, const int64_t *feature, const float *threshold, const int64_t *left,
+                 const int64_t *right, const float *value, int K, const int32_t *net_k,
+                 const int32_t *net_feats, const float *linear, const float *lo, const float *hi,
+                 float base, int accumulate, float *out, yabt_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

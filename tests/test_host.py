@@ -1,11 +1,10 @@
 """Host-side mirrors of the reference interface: Binner semantics, the Tree
-type's CPU routing and path pairs, the identity binner."""
+type's path pairs (and that its routing has no CPU path), the identity binner."""
 
 import numpy as np
+import pytest
 import torch
 
-from oracle import oracle as O
-from tests.helpers import grad_hess, uniform_bins
 from yabt_amd import Binner, IdentityBinner, Tree
 
 
@@ -39,19 +38,19 @@ def test_binner_imputes_nan_with_median():
     assert b.impute(X)[1, 0] == 3.0
 
 
-def test_tree_cpu_apply_matches_oracle_routing():
-    rng = np.random.default_rng(2)
-    n, F = 4000, 6
-    bins = uniform_bins(rng, n, F, 32)
-    g, h = grad_hess(rng, n)
-    t = O.grow(bins.T, g, h, mode=O.MODE_FIXED, max_leaves=25, msl=10)
-    thr = np.where(t["feature"] >= 0, t["thr_bin"], 0).astype(np.float32)
-    tree = Tree(feature=torch.from_numpy(t["feature"]), threshold=torch.from_numpy(thr),
-                left=torch.from_numpy(t["left"]), right=torch.from_numpy(t["right"]),
-                value=torch.from_numpy(t["value"]), depth=int(t["depth"].max()) + 1)
-    X = rng.normal(size=(n, F)).astype(np.float32) * 15
-    assert np.array_equal(tree.apply(torch.from_numpy(X)).numpy(),
-                          O.apply(X, t["feature"], thr, t["left"], t["right"]))
+def test_tree_routing_has_no_cpu_path():
+    """Tree.apply / Tree.predict run the HIP kernels only: without a device
+    they raise instead of routing on the CPU."""
+    if torch.cuda.is_available():
+        pytest.skip("a HIP device is present; routing is covered by the GPU tests")
+    tree = Tree(feature=torch.tensor([0, -1, -1]), threshold=torch.tensor([0.5, 0.0, 0.0]),
+                left=torch.tensor([1, -1, -1]), right=torch.tensor([2, -1, -1]),
+                value=torch.tensor([0.0, 1.0, 2.0]), depth=2)
+    X = torch.zeros(4, 2)
+    with pytest.raises(RuntimeError):
+        tree.apply(X)
+    with pytest.raises(RuntimeError):
+        tree.predict(X)
 
 
 def test_path_feature_pairs():

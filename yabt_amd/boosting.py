@@ -1,0 +1,369 @@
+"""Newton boosting on the GPU (mirror of yabt/boosting.py:60-561 and
+yabt/multiclass.py:9-48).
+
+``BoostParams`` carries every field of the reference with the same defaults,
+so parameter sets written for the reference construct unchanged.  ``Booster``
+runs the reference's training loop (boosting.py:271-534) with the data kept
+on the HIP device from binning to the last margin update:
+
+* g, h by ``yabt_grad_hess``; trees by the HIP grower (``yabt_grow``), whose
+  final partition gives every training row's leaf, so the routing pass
+  ``tree.apply(Xraw)`` of boosting.py:492 is not needed (rows are the same:
+  ``bin <= b  <=>  x <= edge_value(f, b)``); with row subsampling the grower
+  sees a subset and the full set is routed by ``yabt_apply``;
+* linear leaf models by ``fit_leaf_networks`` (``yabt_leaf_moments``,
+  ``yabt_leaf_fit``);
+* the margin update by ``yabt_margin_update``; evaluation-set and
+  ``predict_margin`` outputs by ``yabt_predict`` over packed forests.
+
+Interaction steering (``FeatureInteractionDetector``, adaptive_features.py:
+113-180) keeps its (F, F) count matrix on the host: the counts are integers,
+so its normalisation is the reference's own fp32 expression.
+
+The reference's grower switches (``levelwise`` "auto"/False, ``numba_grower``,
+``c_grower``, ``c_grower_threads``, ``sparse_hist``) all select the leaf-wise
+grower here.  Features outside the tree-growing path raise
+``NotImplementedError`` when switched on: differentiable refinement and
+refits, adaptive features, GOSS, product features, kernel splits, auto-tuning,
+stochastic routing, MLP leaves and the level-wise grower (``levelwise=True``).
+There is no CPU execution: ``device="cpu"`` is rejected.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, fields, replace
+
+import numpy as np
+import torch
+
+from . import boost_ops
+from .binning import Binner
+from .grow_hip import grow_device, grow_tree_hip, layouts_for, leaf_ids, nbins_of, tree_from_result
+from .losses import LogLoss, MSELoss
+from .neural_leaves import fit_leaf_networks
+from .tree import Tree, TreeParams
+
+# interaction steering is switched off below this row count (boosting.py:21-24)
+_INTERACTION_MIN_ROWS = 2000
+
+
+@dataclass
+class BoostParams:
+    """The reference's parameter set (boosting.py:60-200), same names and defaults."""
+    n_estimators: int = 500
+    learning_rate: float = 0.1
+    max_leaves: int = 31
+    max_depth: int = 64
+    reg_lambda: float = 1.0
+    gamma: float = 0.0
+    min_split_gain_rel: float = 0.0
+    min_child_weight: float = 1e-3
+    min_samples_leaf: int = 20
+    subsample: float = 1.0
+    colsample: float = 1.0
+    max_bins: int = 256
+    refine_steps: int = 0
+    refine_lr: float = 0.02
+    refine_min_gain: float = 1e-4
+    refit_every: int = 0
+    refit_steps: int = 30
+    refit_lr: float = 0.05
+    adaptive_features: bool = False
+    feature_importance_alpha: float = 0.1
+    goss_enabled: bool = False
+    goss_ratio: float = 0.9
+    detect_interactions: bool = False
+    interaction_aware: bool = True
+    interaction_boost: float = 0.5
+    product_features: bool = False
+    product_max_features: int = 5
+    product_max_order: int = 3
+    product_min_corr: float = 0.03
+    product_corr_gain: float = 1.3
+    kernel_splits: bool = False
+    kernel_candidates: int = 8
+    kernel_gamma: float = 0.0
+    kernel_min_samples: int = 64
+    kernel_importance_weighting: bool | str = False
+    neural_leaves: bool = True
+    leaf_net_hidden: int = 0
+    leaf_net_features: int = 8
+    leaf_net_l2: float = 1.0
+    leaf_net_steps: int = 40
+    leaf_net_lr: float = 0.05
+    leaf_net_min_samples: int = 50
+    auto_tune: bool = False
+    stochastic_routing: bool = False
+    routing_tau: float = 0.05
+    levelwise: bool | str = "auto"
+    numba_grower: bool | str = "auto"
+    c_grower: bool | str = "auto"
+    c_grower_threads: int = 0
+    sparse_hist: bool | str = "auto"
+    sparse_hist_max_density: float = 0.5
+    early_stopping_rounds: int = 0
+    seed: int = 0
+    device: str = "auto"
+    verbose: bool = False
+
+    def resolve_device(self) -> str:
+        """"auto" -> "cuda" (boosting.py:196-199); this backend runs on a HIP device only."""
+        if self.device == "auto":
+            return "cuda"
+        return self.device
+
+
+PARAM_NAMES = [f.name for f in fields(BoostParams)]
+
+# (field, value that keeps it off, what it is) for the features outside the grower path
+_OFF = [
+    ("refine_steps", 0, "differentiable refinement"),
+    ("refit_every", 0, "global leaf refits"),
+    ("adaptive_features", False, "adaptive feature selection"),
+    ("goss_enabled", False, "GOSS sampling"),
+    ("product_features", False, "product features"),
+    ("kernel_splits", False, "kernel splits"),
+    ("auto_tune", False, "auto-tuning"),
+    ("stochastic_routing", False, "stochastic routing"),
+    ("leaf_net_hidden", 0, "MLP leaves"),
+]
+
+
+def check_supported(p: BoostParams) -> None:
+    for name, off, what in _OFF:
+        if getattr(p, name) != off:
+            raise NotImplementedError(f"{what} ({name}={getattr(p, name)!r}) is not provided by this backend")
+    if p.levelwise is True:
+        raise NotImplementedError("the level-wise grower (levelwise=True) is not provided by this backend")
+    if p.resolve_device() not in ("cuda",) and not str(p.resolve_device()).startswith("cuda:"):
+        raise NotImplementedError(f"device={p.device!r}: this backend runs on a HIP device only")
+    if not torch.cuda.is_available():
+        raise RuntimeError("yabt_amd: no HIP device available")
+
+
+class FeatureInteractionDetector:
+    """Ancestor/descendant split-pair counts (adaptive_features.py:113-180),
+    held on the host in fp32."""
+
+    def __init__(self, n_features: int, device: str = "cpu"):
+        self.n_features = n_features
+        self.device = device
+        self.interaction_scores = torch.zeros((n_features, n_features), device=device)
+        self.update_count = 0
+
+    def update_from_path_pairs(self, pairs: list[tuple[int, int]]) -> None:
+        """Symmetric +1 per (a, b) pair with a != b (adaptive_features.py:129-145)."""
+        if not pairs:
+            return
+        idx = torch.tensor(pairs, dtype=torch.long, device=self.device)
+        a, b = idx[:, 0], idx[:, 1]
+        keep = a != b
+        a, b = a[keep], b[keep]
+        ones = torch.ones(a.shape[0], device=self.device)
+        self.interaction_scores.index_put_((a, b), ones, accumulate=True)
+        self.interaction_scores.index_put_((b, a), ones, accumulate=True)
+        self.update_count += 1
+
+    def normalized_matrix(self) -> torch.Tensor:
+        """((m - bg) / (max - bg + 1e-8)).clamp_min(0), bg = mean of the nonzero
+        counts; m itself while it is all zero (adaptive_features.py:147-160)."""
+        m = self.interaction_scores
+        mx = m.max()
+        if mx <= 0:
+            return m
+        bg = m[m > 0].mean()
+        return ((m - bg) / (mx - bg + 1e-8)).clamp_min(0)
+
+    def get_top_interactions(self, k: int = 5) -> list[tuple[int, int, float]]:
+        """Top-k pairs of the upper triangle by count per update (adaptive_features.py:162-180)."""
+        if self.update_count == 0:
+            return []
+        scores = self.interaction_scores / (self.update_count + 1e-8)
+        s = scores.tolist()
+        pairs = [(i, j, s[i][j]) for i in range(self.n_features) for j in range(i + 1, self.n_features)]
+        pairs.sort(key=lambda x: x[2], reverse=True)
+        return pairs[:k]
+
+
+class Booster:
+    """Newton boosting with the HIP grower (boosting.py:202-561)."""
+
+    def __init__(self, params: BoostParams, loss):
+        self.p = params
+        self.loss = loss
+        self.trees: list[Tree] = []
+        self.binner: Binner | None = None
+        self.base_score: float = 0.0
+        self.best_iter: int | None = None
+        self.interaction_detector: FeatureInteractionDetector | None = None
+        self.tuning_report_: dict | None = None
+        self.product_spec_: list[tuple[int, ...]] = []
+        self._forest: boost_ops.Forest | None = None
+
+    def _tree_params(self) -> TreeParams:
+        p = self.p
+        return TreeParams(max_leaves=p.max_leaves, max_depth=p.max_depth, reg_lambda=p.reg_lambda,
+                          gamma=p.gamma, min_child_weight=p.min_child_weight,
+                          min_samples_leaf=p.min_samples_leaf, learning_rate=p.learning_rate)
+
+    def _device(self) -> torch.device:
+        d = self.p.resolve_device()
+        return torch.device("cuda", torch.cuda.current_device()) if d == "cuda" else torch.device(d)
+
+    def fit(self, X: np.ndarray, y: np.ndarray,
+            eval_set: tuple[np.ndarray, np.ndarray] | None = None) -> "Booster":
+        """The reference's training loop (boosting.py:271-534) on the device."""
+        p = self.p
+        check_supported(p)
+        dev = self._device()
+        self.device_ = dev
+        gen = torch.Generator(device="cpu").manual_seed(p.seed)
+        self.trees = []
+        self.best_iter = None
+        self._forest = None
+
+        self.binner = Binner(max_bins=p.max_bins).fit(X)
+        binned = self.binner.transform(X, device=dev)
+        Xraw = torch.from_numpy(self.binner.impute(X)).to(dev)
+        yt = torch.as_tensor(np.asarray(y, dtype=np.float32), device=dev)
+        n, F = Xraw.shape
+
+        use_interaction_aware = p.interaction_aware and n >= _INTERACTION_MIN_ROWS
+        self.interaction_detector = (FeatureInteractionDetector(F)
+                                     if p.detect_interactions or use_interaction_aware else None)
+
+        self.base_score = self.loss.base_score(yt)
+        margin = torch.full((n,), self.base_score, device=dev)
+
+        if eval_set is not None:
+            Xv = torch.from_numpy(self.binner.impute(eval_set[0])).to(dev)
+            yv = torch.as_tensor(np.asarray(eval_set[1], dtype=np.float32), device=dev)
+            margin_v = torch.full((Xv.shape[0],), self.base_score, device=dev)
+            best_val, rounds_since_best = float("inf"), 0
+
+        tp = self._tree_params()
+        nbins = nbins_of(self.binner, F)
+        lay = layouts_for(binned, dev) if n > 0 else None
+
+        for t in range(p.n_estimators):
+            grad, hess = boost_ops.grad_hess(self.loss, margin, yt)
+
+            tp_t = tp
+            if p.min_split_gain_rel > 0.0:
+                tp_t = replace(tp, gamma=p.gamma + p.min_split_gain_rel * float(grad.var()))
+
+            rows = None
+            if p.subsample < 1.0:
+                m = int(n * p.subsample)
+                rows = torch.randperm(n, generator=gen)[:m].to(dev)
+
+            fmask = None
+            if p.colsample < 1.0:
+                k = max(1, int(F * p.colsample))
+                fmask = torch.zeros(F, dtype=torch.bool, device=dev)
+                fmask[torch.randperm(F, generator=gen)[:k].to(dev)] = True
+
+            imat = None
+            if use_interaction_aware and self.interaction_detector is not None:
+                imat = self.interaction_detector.normalized_matrix()
+
+            if rows is None:
+                res = grow_device(lay, grad, hess, nbins, fmask=fmask, imat=imat, ib=p.interaction_boost,
+                                  lam=tp_t.reg_lambda, gamma=tp_t.gamma, mcw=tp_t.min_child_weight,
+                                  msl=tp_t.min_samples_leaf, lr=tp_t.learning_rate,
+                                  max_leaves=tp_t.max_leaves, max_depth=tp_t.max_depth)
+                tree = tree_from_result(res, self.binner, F, dev)
+                leaf_idx = leaf_ids(res, n, F, tp_t.max_leaves)
+            else:
+                tree = grow_tree_hip(binned[rows], grad[rows], hess[rows], self.binner, tp_t, fmask,
+                                     interaction_matrix=imat, interaction_boost=p.interaction_boost)
+                leaf_idx = tree.apply(Xraw)
+
+            if p.neural_leaves:
+                tree = fit_leaf_networks(tree, Xraw, yt, margin, self.loss, p, gen, leaf_idx=leaf_idx)
+
+            if self.interaction_detector is not None:
+                self.interaction_detector.update_from_path_pairs(tree.path_feature_pairs())
+
+            boost_ops.margin_update(margin, leaf_idx, tree, Xraw)
+            self.trees.append(tree)
+
+            if eval_set is not None:
+                boost_ops.predict(boost_ops.Forest([tree], dev), Xv, out=margin_v, accumulate=True)
+                vl = float(self.loss.loss(margin_v, yv))
+                if vl < best_val - 1e-7:
+                    best_val, self.best_iter, rounds_since_best = vl, t, 0
+                else:
+                    rounds_since_best += 1
+                if p.verbose and t % 50 == 0:
+                    print(f"[{t}] train={float(self.loss.loss(margin, yt)):.5f} val={vl:.5f}")
+                if p.early_stopping_rounds and rounds_since_best >= p.early_stopping_rounds:
+                    break
+        self.margin_ = margin
+        return self
+
+    def top_interactions(self, k: int = 5) -> list[tuple[int, int, float]]:
+        if self.interaction_detector is None:
+            return []
+        return self.interaction_detector.get_top_interactions(k)
+
+    def forest(self, n_trees: int | None = None) -> boost_ops.Forest:
+        """The first n_trees trees packed for yabt_predict (cached for all trees)."""
+        dev = getattr(self, "device_", None) or self._device()
+        if n_trees is None or n_trees >= len(self.trees):
+            if self._forest is None or self._forest.T != len(self.trees):
+                self._forest = boost_ops.Forest(self.trees, dev)
+            return self._forest
+        return boost_ops.Forest(self.trees[:n_trees], dev)
+
+    def _margin(self, Xt: torch.Tensor, n_trees: int | None = None, soft: bool | None = None) -> torch.Tensor:
+        """base_score + the first n_trees trees' outputs (boosting.py:536-545)."""
+        if soft:
+            raise NotImplementedError("stochastic routing is not provided by this backend")
+        return boost_ops.predict(self.forest(n_trees), Xt, self.base_score)
+
+    def predict_margin(self, X: np.ndarray, use_best_iter: bool = True) -> np.ndarray:
+        """Raw margins of X (boosting.py:547-561)."""
+        dev = getattr(self, "device_", None) or self._device()
+        Xt = torch.from_numpy(self.binner.impute(X)).to(dev)
+        n_trees = None
+        if use_best_iter and self.best_iter is not None and self.p.refit_every == 0:
+            n_trees = self.best_iter + 1
+        return self._margin(Xt, n_trees).cpu().numpy()
+
+
+class MulticlassBooster:
+    """One-vs-rest: one LogLoss booster per class, softmax over the per-class
+    margins (multiclass.py:9-48)."""
+
+    def __init__(self, params: BoostParams):
+        self.params = params
+        self.boosters_: list[Booster] = []
+        self.classes_: np.ndarray | None = None
+
+    def fit(self, X: np.ndarray, y: np.ndarray,
+            eval_set: tuple[np.ndarray, np.ndarray] | None = None) -> "MulticlassBooster":
+        self.classes_ = np.unique(y)
+        self.boosters_ = []
+        for label in self.classes_:
+            yb = (y == label).astype(np.float32)
+            evb = None
+            if eval_set is not None:
+                evb = (eval_set[0], (eval_set[1] == label).astype(np.float32))
+            self.boosters_.append(Booster(self.params, LogLoss()).fit(X, yb, eval_set=evb))
+        return self
+
+    def predict_margin(self, X: np.ndarray) -> np.ndarray:
+        return np.stack([b.predict_margin(X) for b in self.boosters_], axis=1)
+
+    def predict_proba(self, X: np.ndarray) -> np.ndarray:
+        m = self.predict_margin(X)
+        e = np.exp(m - m.max(axis=1, keepdims=True))
+        return e / e.sum(axis=1, keepdims=True)
+
+    def predict(self, X: np.ndarray) -> np.ndarray:
+        return self.classes_[np.argmax(self.predict_proba(X), axis=1)]
+
+
+__all__ = ["BoostParams", "Booster", "MulticlassBooster", "FeatureInteractionDetector", "LogLoss", "MSELoss",
+           "PARAM_NAMES", "check_supported"]

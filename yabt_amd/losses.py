@@ -1,7 +1,9 @@
 """Losses producing the grower's g and h (mirror of yabt/boosting.py:27-58).
 
 Same classes, static methods and formulas as the reference, evaluated with
-torch on the margin's device.
+torch on the margin's device.  ``loss_id`` names the loss to the device
+kernel of the boosting step (``yabt_grad_hess``: 0 squared error, 1 logistic),
+which computes the same formulas in fp32.
 """
 
 from __future__ import annotations
@@ -13,6 +15,7 @@ import torch
 class LogLoss:
     """Binary log loss on logits (boosting.py:27-42)."""
     is_classification = True
+    loss_id = 1
 
     @staticmethod
     def base_score(y: torch.Tensor) -> float:
@@ -32,6 +35,7 @@ class LogLoss:
 class MSELoss:
     """Squared error (boosting.py:45-58); h = 1."""
     is_classification = False
+    loss_id = 0
 
     @staticmethod
     def base_score(y: torch.Tensor) -> float:

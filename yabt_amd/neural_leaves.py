@@ -6,7 +6,8 @@ model over up to ``leaf_net_features`` inputs, fitted to the Newton objective
 at ``margin + value[leaf]``, folded into raw space and shrunk by the learning
 rate, with per-leaf input envelopes.  The per-leaf Gram matrices, envelopes,
 counts, solves and the input moments run in the HIP kernels of
-``csrc/leaf.hip`` (``yabt_leaf_moments``, ``yabt_leaf_fit``); feature
+``csrc/leaf.hip`` (``yabt_leaf_moments``, ``yabt_leaf_fit``), the targets g, h
+at margin + value[leaf] in ``yabt_grad_hess`` (``csrc/boost.hip``); feature
 selection and the fold are the reference's own torch expressions on the
 device.  Only the linear form
 (``leaf_net_hidden == 0``) is provided.
@@ -18,7 +19,7 @@ from dataclasses import replace
 
 import torch
 
-from . import _lib
+from . import _lib, boost_ops
 from .tree import LEAF, Tree
 
 _WS: dict = {}
@@ -28,16 +29,24 @@ def _stream(dev: torch.device):
     return torch.cuda.current_stream(dev).cuda_stream
 
 
+def _used_features(feature: torch.Tensor, k: int) -> torch.Tensor:
+    """The tree's split features, most used first (neural_leaves.py:27-31).
+    Evaluated on the host with the reference's own torch calls: the node
+    array is tiny, and torch's CPU argsort fixes the order of equal counts
+    (insertion order up to 16 distinct features, introsort order above)."""
+    f = feature.cpu()
+    f = f[f >= 0]
+    if f.numel() == 0:
+        return torch.empty(0, dtype=torch.long)
+    vals, counts = f.unique(return_counts=True)
+    return vals[counts.argsort(descending=True)][:k]
+
+
 def _select_features(tree: Tree, Xraw: torch.Tensor, grad: torch.Tensor, k: int) -> torch.Tensor:
     """The tree's split features, most used first, padded by |corr(x, g)|
     (neural_leaves.py:21-39)."""
     k = min(k, Xraw.shape[1])
-    f = tree.feature[tree.feature >= 0]
-    if f.numel() > 0:
-        vals, counts = f.unique(return_counts=True)
-        used = vals[counts.argsort(descending=True)][:k]
-    else:
-        used = torch.empty(0, dtype=torch.long, device=Xraw.device)
+    used = _used_features(tree.feature, k).to(Xraw.device)
     if used.numel() >= k:
         return used
     score = (Xraw.T @ grad - Xraw.mean(dim=0) * grad.sum()).abs()
@@ -141,7 +150,7 @@ def fit_leaf_networks(tree: Tree, Xraw: torch.Tensor, y: torch.Tensor, margin: t
                      left=tree.left.to(dev), right=tree.right.to(dev), value=tree.value.to(dev))
     if leaf_idx is None:
         leaf_idx = tree_d.apply(Xraw)
-    grad, hess = loss_fn.grad_hess(margin + tree_d.value[leaf_idx], y)
+    grad, hess = boost_ops.grad_hess(loss_fn, margin, y, leaf_idx, tree_d.value)
     feats = _select_features(tree_d, Xraw, grad, getattr(params, "leaf_net_features", 8))
     if feats.numel() == 0:
         return tree
@@ -167,11 +176,9 @@ def fit_leaf_networks_binned(tree: Tree, bins_fm: torch.Tensor, grad: torch.Tens
     n = int(grad.shape[0]) if n is None else n
     feature = tree.feature.to(dev)
     k = min(getattr(params, "leaf_net_features", 8), bins_fm.shape[0])
-    f = feature[feature >= 0]
-    if f.numel() == 0:
+    feats = _used_features(feature, k).to(dev)
+    if feats.numel() == 0:
         return tree
-    vals, counts = f.unique(return_counts=True)
-    feats = vals[counts.argsort(descending=True)][:k]
     if feats.numel() < k:
         # padding by gradient correlation needs the raw columns: take them as floats
         Xraw = bins_fm[:, :n].t().float()

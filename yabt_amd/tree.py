@@ -60,23 +60,13 @@ class Tree:
         return self.feature == LEAF
 
     def apply(self, X: torch.Tensor) -> torch.Tensor:
-        """Leaf (node) index per row of raw X (n, F) (yabt/tree.py:82-116).
-
-        On a HIP device the routing kernel (yabt_apply) walks each row; on the
-        CPU the reference's depth-bounded torch loop is used."""
+        """Leaf (node) index per row of raw X (n, F) (yabt/tree.py:82-116), by
+        the routing kernel (yabt_apply); CPU inputs are routed on the current
+        HIP device and the result is returned on X's device."""
         if self.kernel_id is not None:
             raise NotImplementedError("kernel splits are not supported by this backend")
-        if X.device.type == "cuda":
-            from .grow_hip import apply_hip
-            return apply_hip(X, self.feature, self.threshold, self.left, self.right)
-        node = torch.zeros(X.shape[0], dtype=torch.long, device=X.device)
-        for _ in range(self.depth):
-            f = self.feature[node]
-            internal = f >= 0
-            x = X.gather(1, f.clamp(min=0).unsqueeze(1)).squeeze(1)
-            nxt = torch.where(x <= self.threshold[node], self.left[node], self.right[node])
-            node = torch.where(internal, nxt, node)
-        return node
+        from .grow_hip import apply_hip
+        return apply_hip(X, self.feature, self.threshold, self.left, self.right)
 
     def net_contribution(self, X: torch.Tensor, node: torch.Tensor) -> torch.Tensor:
         """Per-row linear-leaf output, inputs clamped to the leaf's envelope
@@ -91,11 +81,13 @@ class Tree:
         return (self.leaf_net_linear[node] * Xs).sum(dim=1)
 
     def predict(self, X: torch.Tensor) -> torch.Tensor:
-        node = self.apply(X)
-        out = self.value[node]
-        if self.leaf_net_feats is not None:
-            out = out + self.net_contribution(X, node)
-        return out
+        """value[leaf] + linear-leaf term per row (yabt/tree.py:130-135): one
+        ``yabt_predict`` launch; CPU inputs are evaluated on the current HIP
+        device and the result is returned on X's device."""
+        from .boost_ops import Forest, predict
+        from .grow_hip import _device
+        dev = X.device if X.device.type == "cuda" else _device()
+        return predict(Forest([self], dev), X.to(dev)).to(X.device)
 
     def num_leaves(self) -> int:
         return int((self.feature == LEAF).sum())
