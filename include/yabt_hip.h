@@ -179,6 +179,30 @@ int yabt_hist_slots(const uint8_t *binned, int64_t ldb, const int64_t *slot, con
                     const float *h, const float *w, int64_t n, int F, int K, void *workspace,
                     size_t workspace_bytes, float *out, int32_t *out_status, yabt_stream_t stream);
 
+/* Bytes of device workspace yabt_grow_ref needs for (n, F, max_leaves). */
+size_t yabt_grow_ref_workspace_bytes(int64_t n, int F, int max_leaves);
+
+/* Grow one best-first tree with the reference's own arithmetic: the same
+ * trees as `cgrow` (yabt/_cgrow/grow.c:243-427, dense path) bit for bit --
+ * fp32 histograms summed per (feature, bin) in cgrow's row order, cgrow's
+ * in-place two-pointer partition order (grow.c:201-217), fp32 sibling
+ * subtraction, the double-precision scan and node values, fp32 leaf gains.
+ * Arguments as yabt_grow (no default_bin); out_status is replaced by
+ * out_n_nodes (device int32, cgrow's return value).  Optional outputs (NULL
+ * to skip): out_leaf_of_row (n int64) per-row leaf node ids; out_rows (n
+ * int64) cgrow's final rows[] array.  The control loop runs on the host, one
+ * device round trip per split, and the call returns after the stream has
+ * finished (it synchronises `stream`).  Requires n < 2^32, F >= 1,
+ * 1 <= max_leaves <= 32767. */
+int yabt_grow_ref(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
+                  const float *grad, const float *hess, const uint8_t *fmask, const float *imat,
+                  float ib, int use_imat, const int32_t *nbins, int64_t n, int F, float lam,
+                  float gamma, float mcw, int msl, float lr, int max_leaves, int max_depth,
+                  void *workspace, size_t workspace_bytes, int64_t *out_feature,
+                  int64_t *out_thr_bin, int64_t *out_left, int64_t *out_right, float *out_value,
+                  int64_t *out_depth, int64_t *out_leaf_of_row, int64_t *out_rows,
+                  int32_t *out_n_nodes, yabt_stream_t stream);
+
 /* Gradients and hessians of the boosting losses, fp32 (n rows):
  *   loss 0, MSELoss:  g = m - y, h = 1            (yabt/boosting.py:52-54)
  *   loss 1, LogLoss:  p = 1 / (1 + exp(-m)), g = p - y, h = max(p (1 - p), 1e-6)

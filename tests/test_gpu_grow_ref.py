@@ -1,0 +1,153 @@
+"""yabt_grow_ref (cgrow's own arithmetic on the GPU) against the reference.
+
+* the golden fixtures written by the compiled reference grow.c
+  (tests/golden/grow_*.npz, dense ones): node arrays and value bits equal;
+* the oracle's fp32 mode (oracle/grow_oracle.c, pinned to the same fixtures)
+  on seeded cases: node arrays and value bits equal, cgrow's final rows[]
+  order equal, per-row leaf ids equal to the partition membership;
+* the boosting golden vectors of the reference (tests/golden/booster_*.npz):
+  with grower_arithmetic="reference" every tree's split sequence is the
+  reference's and predictions agree to 1e-6 (leaf models by two fp64 solvers).
+"""
+
+import glob
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+from tests.helpers import grad_hess, skewed_bins, tree_arrays_equal, uniform_bins
+from yabt_amd import YABTClassifier, YABTRegressor
+from yabt_amd import grow_hip as G
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0) if torch.cuda.is_available() else None
+HERE = os.path.dirname(os.path.abspath(__file__))
+FIXTURES = sorted(p for p in glob.glob(os.path.join(HERE, "golden", "grow_*.npz")) if "sparse" not in p)
+
+
+def _grow_ref(bins_nf, g, h, nbins, **kw):
+    lay = G.make_layouts(torch.from_numpy(np.ascontiguousarray(bins_nf)), DEV)
+    res = G.grow_device(lay, torch.from_numpy(g).to(DEV), torch.from_numpy(h).to(DEV), nbins,
+                        arithmetic="reference", **kw)
+    out = {k: getattr(res, k).cpu().numpy() for k in ("feature", "thr_bin", "left", "right", "value", "depth")}
+    return out, res.leaf_of_row.cpu().numpy(), res.rows.cpu().numpy()
+
+
+@pytest.mark.parametrize("path", FIXTURES, ids=os.path.basename)
+def test_matches_reference_fixtures(path):
+    print(f"fixture {os.path.basename(path)}", flush=True)
+    with np.load(path, allow_pickle=False) as z:
+        d = {k: z[k] for k in z.files}
+    lam, gamma, mcw, msl, lr, L, depth = d["params"]
+    kw = dict(lam=float(lam), gamma=float(gamma), mcw=float(mcw), msl=int(msl), lr=float(lr),
+              max_leaves=int(L), max_depth=int(depth))
+    if "imat" in d:
+        kw.update(imat=d["imat"], ib=float(d["ib"]))
+    if "fmask" in d:
+        kw["fmask"] = d["fmask"]
+    got, leaf, rows = _grow_ref(d["bins_fm"].T, d["grad"], d["hess"], d["nbins"], **kw)
+    want = {k[4:]: d[k] for k in d if k.startswith("out_")}
+    assert tree_arrays_equal(got, want) is None
+
+
+CASES = [
+    dict(n=3000, F=12, nb=256, kind="normal", max_leaves=31),
+    dict(n=20_000, F=20, nb=255, kind="normal", max_leaves=31, imat=True),
+    dict(n=5000, F=9, nb=28, kind="logistic", max_leaves=256, max_depth=8, msl=1),
+    dict(n=8000, F=40, nb=256, kind="laplace", max_leaves=64, max_depth=6, skew=True),
+    dict(n=4000, F=17, nb=64, kind="normal", max_leaves=63, fmask=True, lam=0.0, gamma=0.05),
+    dict(n=1, F=1, nb=256, kind="normal", max_leaves=31, msl=0),
+    dict(n=100, F=3, nb=256, kind="normal", max_leaves=1),
+    dict(n=50_000, F=30, nb=256, kind="normal", max_leaves=255, msl=20),
+    dict(n=300_000, F=24, nb=256, kind="normal", max_leaves=63, msl=20, imat=True),
+    dict(n=200_000, F=33, nb=256, kind="laplace", max_leaves=40, max_depth=6, skew=True),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=lambda c: f"n{c['n']}_F{c['F']}_L{c['max_leaves']}")
+def test_matches_fp32_oracle(case):
+    print(f"case {case}", flush=True)
+    c = dict(case)
+    rng = np.random.default_rng(c["n"] + c["F"])
+    n, F, nb = c.pop("n"), c.pop("F"), c.pop("nb")
+    bins = (skewed_bins(rng, n, F) if c.pop("skew", False) else uniform_bins(rng, n, F, nb))
+    g, h = grad_hess(rng, n, c.pop("kind"))
+    kw = dict(max_leaves=c.pop("max_leaves"), max_depth=c.pop("max_depth", 64), msl=c.pop("msl", 20),
+              lam=c.pop("lam", 1.0), gamma=c.pop("gamma", 0.0))
+    if c.pop("imat", False):
+        im = rng.random((F, F)).astype(np.float32)
+        kw.update(imat=(im + im.T) / 2, ib=0.5)
+    if c.pop("fmask", False):
+        kw["fmask"] = rng.random(F) < 0.7
+    nbins = np.full(F, nb, np.int32)
+    got, leaf, rows = _grow_ref(bins, g, h, nbins, **kw)
+    okw = dict(kw)
+    if "fmask" in okw:
+        okw["fmask"] = okw["fmask"]
+    want = O.grow(np.ascontiguousarray(bins.T), g, h, mode=O.MODE_FP32, nbins=nbins, **okw)
+    assert tree_arrays_equal(got, want) is None
+    assert np.array_equal(rows, want["rows"]), "cgrow's rows[] order"
+    assert np.array_equal(leaf, O.leaf_of_rows(want, n))
+
+
+def _golden(name):
+    with np.load(os.path.join(HERE, "golden", name), allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def _cfg1(n, seed):
+    rng = np.random.default_rng(seed)
+    X = rng.normal(size=(n, 20)).astype(np.float32)
+    y = (np.sin(X[:, 0]) + 0.5 * X[:, 1] * X[:, 2] + X[:, 3] ** 2 + 0.3 * X[:, 4:10].sum(axis=1)
+         + rng.normal(scale=0.1, size=n)).astype(np.float32)
+    return X, y
+
+
+def _logistic(n, F, seed):
+    rng = np.random.default_rng(seed)
+    X = rng.normal(size=(n, F)).astype(np.float32)
+    w = rng.normal(size=F)
+    y = (rng.random(n) < 1 / (1 + np.exp(-(X @ w)))).astype(np.float32)
+    return X, y
+
+
+def _same_as_golden(trees, d):
+    off = d["node_off"]
+    assert len(trees) == off.size - 1
+    for t, tr in enumerate(trees):
+        a, b = off[t], off[t + 1]
+        f = tr.feature.cpu().numpy()
+        assert np.array_equal(f, d["feature"][a:b]), f"tree {t}: split features"
+        assert np.array_equal(tr.threshold.cpu().numpy()[f >= 0], d["threshold"][a:b][f >= 0]), f"tree {t}"
+        assert np.array_equal(tr.left.cpu().numpy(), d["left"][a:b]), f"tree {t}: children"
+
+
+@pytest.mark.parametrize("arith", ["reference", "exact"])
+def test_regressor_matches_reference_golden(arith):
+    """20 000 x 20, 25 trees, 31 leaves, linear leaves, 255 bins."""
+    print(f"regressor golden {arith}", flush=True)
+    d = _golden("booster_regression_20kx20.npz")
+    X, y = _cfg1(20_000, 0)
+    Xt, _ = _cfg1(4_000, 11)
+    est = YABTRegressor(n_estimators=25, max_leaves=31, learning_rate=0.1, max_bins=255, neural_leaves=True,
+                        grower_arithmetic=arith).fit(X, y)
+    _same_as_golden(est.booster_.trees, d)
+    assert np.abs(est.predict(Xt) - d["pred"]).max() <= 1e-5
+
+
+def test_classifier_matches_reference_golden():
+    """50 000 x 28, 28 bins, depth 8, 10 trees: the fp32 arithmetic decides
+    splits that exact sums decide differently, so only the reference
+    arithmetic reproduces the reference's trees."""
+    print("classifier golden", flush=True)
+    d = _golden("booster_logistic_50kx28.npz")
+    X, y = _logistic(50_000, 28, 1)
+    Xt, _ = _logistic(4_000, 28, 2)
+    clf = YABTClassifier(n_estimators=10, max_leaves=256, max_depth=8, max_bins=28, neural_leaves=False,
+                         grower_arithmetic="reference").fit(X, y)
+    _same_as_golden(clf.booster_.trees, d)
+    assert np.abs(clf.predict_proba(Xt)[:, 1] - d["proba"]).max() <= 1e-6

@@ -6,7 +6,8 @@ so parameter sets written for the reference construct unchanged.  ``Booster``
 runs the reference's training loop (boosting.py:271-534) with the data kept
 on the HIP device from binning to the last margin update:
 
-* g, h by ``yabt_grad_hess``; trees by the HIP grower (``yabt_grow``), whose
+* g, h by ``yabt_grad_hess``; trees by the HIP grower (``yabt_grow``, or
+  ``yabt_grow_ref`` with ``grower_arithmetic="reference"``), whose
   final partition gives every training row's leaf, so the routing pass
   ``tree.apply(Xraw)`` of boosting.py:492 is not needed (rows are the same:
   ``bin <= b  <=>  x <= edge_value(f, b)``); with row subsampling the grower
@@ -105,6 +106,11 @@ class BoostParams:
     seed: int = 0
     device: str = "auto"
     verbose: bool = False
+    # This backend's own switch (not a reference field): "exact" grows with
+    # exact fixed-point histograms on the device; "reference" reproduces the
+    # reference C grower's fp32 arithmetic and row order, giving its trees
+    # bit for bit at a higher cost per split.
+    grower_arithmetic: str = "exact"
 
     def resolve_device(self) -> str:
         """"auto" -> "cuda" (boosting.py:196-199); this backend runs on a HIP device only."""
@@ -133,6 +139,8 @@ def check_supported(p: BoostParams) -> None:
     for name, off, what in _OFF:
         if getattr(p, name) != off:
             raise NotImplementedError(f"{what} ({name}={getattr(p, name)!r}) is not provided by this backend")
+    if p.grower_arithmetic not in ("exact", "reference"):
+        raise ValueError("grower_arithmetic must be 'exact' or 'reference'")
     if p.levelwise is True:
         raise NotImplementedError("the level-wise grower (levelwise=True) is not provided by this backend")
     if p.resolve_device() not in ("cuda",) and not str(p.resolve_device()).startswith("cuda:"):
@@ -271,12 +279,14 @@ class Booster:
                 res = grow_device(lay, grad, hess, nbins, fmask=fmask, imat=imat, ib=p.interaction_boost,
                                   lam=tp_t.reg_lambda, gamma=tp_t.gamma, mcw=tp_t.min_child_weight,
                                   msl=tp_t.min_samples_leaf, lr=tp_t.learning_rate,
-                                  max_leaves=tp_t.max_leaves, max_depth=tp_t.max_depth)
+                                  max_leaves=tp_t.max_leaves, max_depth=tp_t.max_depth,
+                                  arithmetic=p.grower_arithmetic)
                 tree = tree_from_result(res, self.binner, F, dev)
                 leaf_idx = leaf_ids(res, n, F, tp_t.max_leaves)
             else:
                 tree = grow_tree_hip(binned[rows], grad[rows], hess[rows], self.binner, tp_t, fmask,
-                                     interaction_matrix=imat, interaction_boost=p.interaction_boost)
+                                     interaction_matrix=imat, interaction_boost=p.interaction_boost,
+                                     arithmetic=p.grower_arithmetic)
                 leaf_idx = tree.apply(Xraw)
 
             if p.neural_leaves:

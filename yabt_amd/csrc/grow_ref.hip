@@ -1,0 +1,821 @@
+// Reference-arithmetic best-first growth on gfx950: the trees of
+// yabt/_cgrow/grow.c `cgrow` (grow.c:243-427), bit for bit.
+//
+// yabt_grow (grow.hip) sums exact fixed-point values; its trees equal cgrow's
+// except where cgrow's own fp32 rounding decides a split.  This grower
+// reproduces cgrow's arithmetic instead:
+//   * a node histogram is the fp32 sum, per (feature, bin), of the node's rows
+//     in the order cgrow's rows[] array holds them (grow.c:37-62): the node's
+//     rows are bucketed by bin with a stable counting sort, and one thread adds
+//     each (feature, bin) chain in order;
+//   * rows[] follows cgrow's in-place two-pointer partition (grow.c:201-217),
+//     which is a fixed permutation of the node's rows, computed in parallel
+//     (see "partition" below);
+//   * the larger child is parent - smaller child in fp32 (grow.c:355-369);
+//   * the split scan sums the bins in double in bin order and evaluates
+//     grow.c's gain expression and tie-breaks (grow.c:129-197); node values
+//     come from feature 0's 256 bins summed in double (grow.c:302-308,
+//     371-379); interaction boosts are grow.c's fp32 compute_boost
+//     (grow.c:111-122);
+//   * the leaf table, its fp32 gains and the first-maximum selection
+//     (grow.c:284-407) run on the host between splits: one device round trip
+//     per split.
+//
+// Partition.  With positions relative to the node start, m rows, and
+//   p_k = position of the k-th row going right, counted from the left,
+//   q_k = position of the k-th row going left, counted from the right, q_0 = m,
+//   K   = #{k : p_k < q_k},
+// the two-pointer loop sends
+//   * the right row of rank r to q_{r-1} - 1 if r <= K, or if r = K + 1 and
+//     its position is below q_K; every other right row moves one place left;
+//   * the left row of rank t to p_t if t <= K; every other left row stays.
+//
+// Workspace (yabt_grow_ref_workspace_bytes): rows and a copy (n u32), the
+// partition's flags / ranks / p / q arrays, the built child's g and h in row
+// order, per-chunk bin counts (F, n/CH, 256), the bucketed (g, h) pairs of up
+// to SORT_FEATS features, and one (3, F, 256) fp32 histogram per node.
+
+#include "common.h"
+#include "host.h"
+#include "yabt_hip.h"
+
+#include <math.h>
+#include <string.h>
+
+#include <vector>
+
+namespace yabt {
+namespace ref {
+
+constexpr int RB = 256;            // threads per block
+constexpr int PT = 2048;           // partition rows per block
+constexpr int CH = 4096;           // rows per counting-sort chunk
+constexpr int FT = 16;             // features per counting block (one 16-byte row load)
+constexpr int SF = 4;              // features per scatter block (one wave each)
+constexpr int SORT_FEATS = 16;     // bucketed features per pass at the root
+
+struct Job {
+    int64_t s, e;                  // parent segment
+    int64_t nl;                    // rows going left
+    uint32_t K;                    // pairs moved by the two-pointer loop
+    int32_t build_left;
+    int64_t cs, ce;                // built child's segment
+};
+
+struct ChildRes {
+    double gain;                   // best true gain (-inf if none)
+    int32_t f, b;
+    float value;
+    int32_t pad;
+};
+
+struct Res {
+    ChildRes c[2];
+    int64_t mid;
+    int32_t build_left;
+    int32_t pad;
+};
+
+struct Ws {
+    uint32_t* rows;
+    uint32_t* rows_tmp;
+    uint8_t* flag;
+    uint32_t* rank;
+    uint32_t* p;
+    uint32_t* q;
+    uint32_t* blk;                 // per-block left counts, then their exclusive prefix
+    float* G;
+    float* H;
+    uint32_t* counts;              // (F, chunks, 256)
+    uint32_t* bstart;              // (F, 257)
+    float2* sorted;                // (SORT_FEATS, n)
+    float* hist;                   // (N, 3, F, 256)
+    double* fsel;                  // (2, F)
+    double* fgain;                 // (2, F)
+    int32_t* fb;                   // (2, F)
+    uint8_t* path;                 // (N, F)
+    int64_t* segs;                 // (N, 3): leaf node, start, end
+    Job* job;
+    Res* res;
+    size_t bytes;
+};
+
+inline int64_t chunks_of(int64_t n) { return (n + CH - 1) / CH; }
+
+Ws carve(char* base, int64_t n, int F, int max_leaves) {
+    Carve c{base, 0};
+    Ws w;
+    const int64_t N = 2 * (int64_t)max_leaves + 1;
+    const int64_t nn = n > 0 ? n : 1;
+    w.rows = c.take<uint32_t>(nn);
+    w.rows_tmp = c.take<uint32_t>(nn);
+    w.flag = c.take<uint8_t>(nn);
+    w.rank = c.take<uint32_t>(nn);
+    w.p = c.take<uint32_t>(nn);
+    w.q = c.take<uint32_t>(nn);
+    w.blk = c.take<uint32_t>((nn + PT - 1) / PT + 1);
+    w.G = c.take<float>(nn);
+    w.H = c.take<float>(nn);
+    w.counts = c.take<uint32_t>((size_t)F * chunks_of(nn) * NB);
+    w.bstart = c.take<uint32_t>((size_t)F * (NB + 1));
+    w.sorted = c.take<float2>((size_t)min(F, SORT_FEATS) * nn);
+    w.hist = c.take<float>((size_t)N * 3 * F * NB);
+    w.fsel = c.take<double>(2 * (size_t)F);
+    w.fgain = c.take<double>(2 * (size_t)F);
+    w.fb = c.take<int32_t>(2 * (size_t)F);
+    w.path = c.take<uint8_t>((size_t)N * F);
+    w.segs = c.take<int64_t>((size_t)N * 3);
+    w.job = c.take<Job>(1);
+    w.res = c.take<Res>(1);
+    w.bytes = c.off;
+    return w;
+}
+
+// ---------------------------------------------------------------------------
+// setup
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(RB) k_init(uint32_t* rows, int64_t n, uint8_t* path, int64_t path_n,
+                                             int64_t* feature, int64_t* thr_bin, int64_t* left, int64_t* right,
+                                             float* value, int64_t* depth, int N) {
+    const int64_t tid = (int64_t)blockIdx.x * RB + threadIdx.x, stride = (int64_t)gridDim.x * RB;
+    for (int64_t i = tid; i < n; i += stride) rows[i] = (uint32_t)i;
+    for (int64_t i = tid; i < path_n; i += stride) path[i] = 0;
+    for (int64_t i = tid; i < N; i += stride) {
+        feature[i] = LEAF;
+        thr_bin[i] = 0;
+        left[i] = -1;
+        right[i] = -1;
+        value[i] = 0.0f;
+        depth[i] = 0;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// partition in cgrow's order
+// ---------------------------------------------------------------------------
+
+// Flags (row goes left) and the left count of each PT-row block.
+__global__ void __launch_bounds__(RB) k_part_flags(const uint8_t* __restrict__ bins_fm, int64_t ld, int f, int b,
+                                                   const uint32_t* __restrict__ rows, int64_t s, int64_t m,
+                                                   uint8_t* __restrict__ flag, uint32_t* __restrict__ blk) {
+    __shared__ uint32_t s_red[RB / WAVE];
+    const uint8_t* col = bins_fm + (size_t)f * ld;
+    const int64_t x0 = (int64_t)blockIdx.x * PT;
+    uint32_t cnt = 0;
+    for (int j = threadIdx.x; j < PT; j += RB) {
+        const int64_t x = x0 + j;
+        if (x < m) {
+            const uint8_t l = (int)col[rows[s + x]] <= b ? 1 : 0;
+            flag[x] = l;
+            cnt += l;
+        }
+    }
+    cnt = block_sum<RB, uint32_t>(cnt, s_red);
+    if (threadIdx.x == 0) blk[blockIdx.x] = cnt;
+}
+
+// One block: exclusive prefix of the block counts; the job record.
+__global__ void __launch_bounds__(RB) k_part_offsets(uint32_t* blk, int nblk, Job* job, int64_t s, int64_t e) {
+    __shared__ uint32_t s_w[RB / WAVE];
+    uint32_t carry = 0;
+    for (int i0 = 0; i0 < nblk; i0 += RB) {
+        const int i = i0 + threadIdx.x;
+        const uint32_t v = i < nblk ? blk[i] : 0u;
+        uint32_t tot;
+        const uint32_t ex = block_excl_scan<RB, uint32_t>(v, s_w, &tot);
+        if (i < nblk) blk[i] = carry + ex;
+        carry += tot;
+    }
+    if (threadIdx.x == 0) {
+        const int64_t m = e - s;
+        job->s = s;
+        job->e = e;
+        job->nl = carry;
+        job->K = 0;
+        job->build_left = (int64_t)carry <= m - (int64_t)carry ? 1 : 0;
+        job->cs = job->build_left ? s : s + (int64_t)carry;
+        job->ce = job->build_left ? s + (int64_t)carry : e;
+    }
+}
+
+// Ranks: rank[x] = left rows before x; p (right rows, from the left) and q
+// (left rows, from the right) hold positions.
+__global__ void __launch_bounds__(RB) k_part_rank(const uint8_t* __restrict__ flag, const uint32_t* __restrict__ blk,
+                                                  const Job* __restrict__ job, int64_t m, uint32_t* __restrict__ rank,
+                                                  uint32_t* __restrict__ p, uint32_t* __restrict__ q) {
+    __shared__ uint32_t s_w[RB / WAVE];
+    const uint32_t nl = (uint32_t)job->nl;
+    const int64_t x0 = (int64_t)blockIdx.x * PT;
+    uint32_t carry = blk[blockIdx.x];
+    for (int j0 = 0; j0 < PT; j0 += RB) {
+        const int64_t x = x0 + j0 + threadIdx.x;
+        const uint32_t l = x < m ? flag[x] : 0u;
+        uint32_t tot;
+        const uint32_t ex = carry + block_excl_scan<RB, uint32_t>(l, s_w, &tot);
+        if (x < m) {
+            rank[x] = ex;
+            if (l) q[nl - ex - 1] = (uint32_t)x;
+            else p[(uint32_t)x - ex] = (uint32_t)x;
+        }
+        carry += tot;
+    }
+}
+
+// K = #{k : p_k < q_k} over k < min(#right, #left).
+__global__ void __launch_bounds__(RB) k_part_pairs(const uint32_t* __restrict__ p, const uint32_t* __restrict__ q,
+                                                   Job* job, int64_t m) {
+    __shared__ uint32_t s_red[RB / WAVE];
+    const int64_t nl = job->nl;
+    const int64_t kmax = min(nl, m - nl);
+    uint32_t c = 0;
+    for (int64_t k = (int64_t)blockIdx.x * RB + threadIdx.x; k < kmax; k += (int64_t)gridDim.x * RB)
+        c += p[k] < q[k] ? 1u : 0u;
+    c = block_sum<RB, uint32_t>(c, s_red);
+    if (threadIdx.x == 0 && c) atomicAdd(&job->K, c);
+}
+
+// Destinations of the two-pointer loop; rows_tmp[s + dest] = rows[s + x].
+// Block 0 also records the children's path masks and node bookkeeping.
+__global__ void __launch_bounds__(RB) k_part_permute(const uint8_t* __restrict__ flag,
+                                                     const uint32_t* __restrict__ rank, const uint32_t* __restrict__ p,
+                                                     const uint32_t* __restrict__ q, const Job* __restrict__ job,
+                                                     const uint32_t* __restrict__ rows, uint32_t* __restrict__ rows_tmp,
+                                                     int64_t s, int64_t m, uint8_t* path, int F, int nid, int f,
+                                                     int nl_id, int nr_id) {
+    const int64_t nl = job->nl;
+    const int64_t K = job->K;
+    const int64_t qK = K == 0 ? m : (int64_t)q[K - 1];
+    for (int64_t x = (int64_t)blockIdx.x * RB + threadIdx.x; x < m; x += (int64_t)gridDim.x * RB) {
+        const int64_t lb = rank[x];
+        int64_t dest;
+        if (flag[x]) {
+            const int64_t t = nl - lb;                 // rank from the right, 1-based
+            dest = t <= K ? (int64_t)p[t - 1] : x;
+        } else {
+            const int64_t r = x - lb + 1;              // rank from the left, 1-based
+            if (r <= K) dest = (r == 1 ? m : (int64_t)q[r - 2]) - 1;
+            else if (r == K + 1 && x < qK) dest = qK - 1;
+            else dest = x - 1;
+        }
+        rows_tmp[s + dest] = rows[s + x];
+    }
+    if (blockIdx.x == 0) {
+        for (int j = threadIdx.x; j < F; j += RB) {
+            const uint8_t v = (uint8_t)(path[(size_t)nid * F + j] | (j == f ? 1 : 0));
+            path[(size_t)nl_id * F + j] = v;
+            path[(size_t)nr_id * F + j] = v;
+        }
+    }
+}
+
+// rows[s:e) = rows_tmp[s:e); the built child's g, h in its row order.
+__global__ void __launch_bounds__(RB) k_part_commit(uint32_t* __restrict__ rows, const uint32_t* __restrict__ rows_tmp,
+                                                    const Job* __restrict__ job, int64_t s, int64_t m,
+                                                    const float* __restrict__ grad, const float* __restrict__ hess,
+                                                    float* __restrict__ G, float* __restrict__ H) {
+    const int64_t cs = job->cs, ce = job->ce;
+    for (int64_t x = (int64_t)blockIdx.x * RB + threadIdx.x; x < m; x += (int64_t)gridDim.x * RB) {
+        const int64_t i = s + x;
+        const uint32_t r = rows_tmp[i];
+        rows[i] = r;
+        if (i >= cs && i < ce) {
+            G[i - cs] = grad[r];
+            H[i - cs] = hess[r];
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// histogram: stable bucketing by bin, then one sequential chain per (f, b)
+// ---------------------------------------------------------------------------
+
+// Segment [cs, ce): the job's built child, or [0, n) for the root (job null).
+struct Seg {
+    int64_t cs, m;
+};
+
+__device__ __forceinline__ Seg seg_of(const Job* job, int64_t n) {
+    if (!job) return Seg{0, n};
+    return Seg{job->cs, job->ce - job->cs};
+}
+
+// counts[f][chunk][b] = rows of the chunk in bin b of feature f.
+__global__ void __launch_bounds__(RB) k_hist_count(const uint8_t* __restrict__ bins_rm, int64_t ld_rm,
+                                                   const uint32_t* __restrict__ rows, const Job* __restrict__ job,
+                                                   int64_t n, int F, int64_t nchunks, uint32_t* __restrict__ counts) {
+    __shared__ uint32_t s_c[FT][NB];
+    const Seg sg = seg_of(job, n);
+    const int64_t chunk = blockIdx.x;
+    const int f0 = blockIdx.y * FT;
+    const int64_t c0 = chunk * CH;
+    if (c0 >= sg.m) return;
+    for (int i = threadIdx.x; i < FT * NB; i += RB) (&s_c[0][0])[i] = 0;
+    __syncthreads();
+    const int64_t c1 = min(sg.m, c0 + CH);
+    for (int64_t x = c0 + threadIdx.x; x < c1; x += RB) {
+        const uint32_t r = rows[sg.cs + x];
+        const uint4 v = *reinterpret_cast<const uint4*>(bins_rm + (size_t)r * (size_t)ld_rm + f0);
+        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int j = 0; j < FT; ++j)
+            if (f0 + j < F) atomicAdd(&s_c[j][(w4[j >> 2] >> (8 * (j & 3))) & 0xff], 1u);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < FT * NB; i += RB) {
+        const int j = i / NB, bb = i % NB;
+        if (f0 + j < F) counts[((size_t)(f0 + j) * nchunks + chunk) * NB + bb] = s_c[j][bb];
+    }
+}
+
+// Per feature: counts -> global bucket positions (bin start + earlier chunks),
+// bstart[f][b] = first position of bin b, bstart[f][256] = m.
+__global__ void __launch_bounds__(NB) k_hist_offsets(uint32_t* __restrict__ counts, uint32_t* __restrict__ bstart,
+                                                     const Job* __restrict__ job, int64_t n, int64_t nchunks) {
+    __shared__ uint32_t s_w[NB / WAVE];
+    const Seg sg = seg_of(job, n);
+    const int f = blockIdx.x, b = threadIdx.x;
+    const int64_t used = (sg.m + CH - 1) / CH;
+    uint32_t* c = counts + (size_t)f * nchunks * NB + b;
+    uint32_t run = 0;
+    for (int64_t k = 0; k < used; ++k) {
+        const uint32_t v = c[(size_t)k * NB];
+        c[(size_t)k * NB] = run;
+        run += v;
+    }
+    uint32_t tot;
+    const uint32_t start = block_excl_scan<NB, uint32_t>(run, s_w, &tot);
+    for (int64_t k = 0; k < used; ++k) c[(size_t)k * NB] += start;
+    bstart[(size_t)f * (NB + 1) + b] = start;
+    if (b == NB - 1) bstart[(size_t)f * (NB + 1) + NB] = start + run;
+}
+
+// Bucket the (g, h) pairs of features [fb0, fb0 + nf) by bin, stably: one wave
+// per feature walks the chunk's rows in order, 64 at a time; lanes with equal
+// bins are ranked by lane (eight ballots find the lanes sharing a bin).
+__global__ void __launch_bounds__(SF * WAVE) k_hist_scatter(const uint8_t* __restrict__ bins_rm, int64_t ld_rm,
+                                                            const uint32_t* __restrict__ rows,
+                                                            const Job* __restrict__ job, int64_t n, int fb0, int nf,
+                                                            int64_t nchunks, const uint32_t* __restrict__ counts,
+                                                            const float* __restrict__ G, const float* __restrict__ H,
+                                                            float2* __restrict__ sorted, int64_t sort_ld) {
+    __shared__ uint32_t s_pos[SF][NB];
+    const Seg sg = seg_of(job, n);
+    const int64_t chunk = blockIdx.x;
+    const int w = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
+    const int fi = blockIdx.y * SF + w;           // feature index inside the batch
+    const int64_t c0 = chunk * CH;
+    if (c0 >= sg.m || fi >= nf) return;
+    const int f = fb0 + fi;
+    const uint32_t* cnt = counts + ((size_t)f * nchunks + chunk) * NB;
+    for (int bb = lane; bb < NB; bb += WAVE) s_pos[w][bb] = cnt[bb];
+    // s_pos is private to this wave: the wave's own LDS writes are visible to
+    // its later reads without a block barrier
+    __builtin_amdgcn_wave_barrier();
+    const int64_t c1 = min(sg.m, c0 + CH);
+    float2* out = sorted + (size_t)fi * sort_ld;
+    for (int64_t g0 = c0; g0 < c1; g0 += WAVE) {
+        const int64_t x = g0 + lane;
+        const bool v = x < c1;
+        uint32_t bin = 0;
+        float gv = 0.0f, hv = 0.0f;
+        if (v) {
+            const uint32_t r = rows[sg.cs + x];
+            bin = bins_rm[(size_t)r * (size_t)ld_rm + f];
+            gv = G ? G[x] : 0.0f;
+            hv = H ? H[x] : 0.0f;
+        }
+        uint64_t peers = __ballot(v);
+#pragma unroll
+        for (int bit = 0; bit < 8; ++bit) {
+            const bool on = (bin >> bit) & 1u;
+            const uint64_t bal = __ballot(on);
+            peers &= on ? bal : ~bal;
+        }
+        if (v) {
+            const uint32_t rk = lane_prefix(peers);
+            const uint32_t base = s_pos[w][bin];
+            out[base + rk] = make_float2(gv, hv);
+            __builtin_amdgcn_wave_barrier();
+            if (rk == 0) s_pos[w][bin] = base + (uint32_t)__popcll(peers);
+        }
+        __builtin_amdgcn_wave_barrier();
+    }
+}
+
+// One thread per (feature, bin): the bin's pairs added in row order in fp32;
+// the count chain adds 1.0f per row (grow.c:55-60).
+__global__ void __launch_bounds__(RB) k_hist_chain(const float2* __restrict__ sorted, int64_t sort_ld,
+                                                   const uint32_t* __restrict__ bstart, int fb0, int nf, int F,
+                                                   float* __restrict__ hist_base, size_t hsz,
+                                                   const Job* __restrict__ job, int slot_l, int slot_r) {
+    const int t = blockIdx.x * RB + threadIdx.x;
+    if (t >= nf * NB) return;
+    const int slot = (!job || job->build_left) ? slot_l : slot_r;
+    float* hist = hist_base + (size_t)slot * hsz;
+    const int fi = t / NB, b = t % NB, f = fb0 + fi;
+    const uint32_t lo = bstart[(size_t)f * (NB + 1) + b], hi = bstart[(size_t)f * (NB + 1) + b + 1];
+    const float2* src = sorted + (size_t)fi * sort_ld;
+    float ag = 0.0f, ah = 0.0f, ac = 0.0f;
+    uint32_t k = lo;
+    for (; k + 4 <= hi; k += 4) {
+        const float2 a0 = src[k], a1 = src[k + 1], a2 = src[k + 2], a3 = src[k + 3];
+        ag += a0.x; ah += a0.y; ac += 1.0f;
+        ag += a1.x; ah += a1.y; ac += 1.0f;
+        ag += a2.x; ah += a2.y; ac += 1.0f;
+        ag += a3.x; ah += a3.y; ac += 1.0f;
+    }
+    for (; k < hi; ++k) {
+        const float2 a = src[k];
+        ag += a.x; ah += a.y; ac += 1.0f;
+    }
+    hist[(size_t)0 * F * NB + (size_t)f * NB + b] = ag;
+    hist[(size_t)1 * F * NB + (size_t)f * NB + b] = ah;
+    hist[(size_t)2 * F * NB + (size_t)f * NB + b] = ac;
+}
+
+// The sibling: hist[other] = hist[parent] - hist[built] (grow.c:361,368).
+__global__ void __launch_bounds__(RB) k_hist_sub(float* __restrict__ hist, size_t hsz, int parent, int nl_id,
+                                                 int nr_id, const Job* __restrict__ job) {
+    const int built = job->build_left ? nl_id : nr_id, other = job->build_left ? nr_id : nl_id;
+    const float* hp = hist + (size_t)parent * hsz;
+    const float* hb = hist + (size_t)built * hsz;
+    float* ho = hist + (size_t)other * hsz;
+    for (size_t i = (size_t)blockIdx.x * RB + threadIdx.x; i < hsz; i += (size_t)gridDim.x * RB) ho[i] = hp[i] - hb[i];
+}
+
+// ---------------------------------------------------------------------------
+// split scan (grow.c:129-197), one wave per (feature, child)
+// ---------------------------------------------------------------------------
+
+struct ScanParams {
+    const int32_t* nbins;
+    const uint8_t* fmask;
+    const float* imat;
+    float ib;
+    int use_imat;
+    double lam, gamma, mcw;
+    int msl;
+    int F;
+};
+
+__global__ void __launch_bounds__(WAVE) k_scan_feature(const float* __restrict__ hist, size_t hsz, int node0, int node1,
+                                                       const uint8_t* __restrict__ path, ScanParams P,
+                                                       double* __restrict__ fsel, double* __restrict__ fgain,
+                                                       int32_t* __restrict__ fb) {
+    __shared__ double s_gl[NB], s_hl[NB], s_cl[NB];
+    const int f = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
+    const int node = c == 0 ? node0 : node1;
+    const int F = P.F;
+    double best_sel = -INFINITY, best_true = -INFINITY;
+    int best_b = -1;
+    if (P.fmask[f]) {
+        const int nb = min(max(P.nbins[f], 1), NB);
+        const float* hg = hist + (size_t)node * hsz + (size_t)f * NB;
+        const float* hh = hg + (size_t)F * NB;
+        const float* hc = hh + (size_t)F * NB;
+        if (lane == 0) {
+            double G = 0.0, H = 0.0, C = 0.0;
+            for (int b = 0; b < nb; ++b) {
+                G += hg[b];
+                H += hh[b];
+                C += hc[b];
+                s_gl[b] = G;
+                s_hl[b] = H;
+                s_cl[b] = C;
+            }
+        }
+        __syncthreads();
+        // compute_boost (grow.c:111-122): 1 + ib * max(0, max over the path of imat[p][f])
+        float mx = 0.0f;
+        if (P.use_imat) {
+            for (int p = 0; p < F; ++p)
+                if (path[(size_t)node * F + p]) {
+                    const float v = P.imat[(size_t)p * F + f];
+                    if (v > mx) mx = v;
+                }
+        }
+        const double bo = P.use_imat ? (double)(1.0f + P.ib * mx) : 1.0;
+        const double Gt = s_gl[nb - 1], Ht = s_hl[nb - 1], Ct = s_cl[nb - 1];
+        const double parent = Gt * Gt / (Ht + P.lam);
+        for (int b = lane; b < nb - 1; b += WAVE) {
+            const double GL = s_gl[b], HL = s_hl[b], CL = s_cl[b];
+            const double GR = Gt - GL, HR = Ht - HL, CR = Ct - CL;
+            if (CL >= P.msl && CR >= P.msl && HL >= P.mcw && HR >= P.mcw) {
+                const double gain = 0.5 * (GL * GL / (HL + P.lam) + GR * GR / (HR + P.lam) - parent) - P.gamma;
+                const double sel = gain * bo;
+                if (sel > best_sel) {           // lanes visit b in increasing order
+                    best_sel = sel;
+                    best_true = gain;
+                    best_b = b;
+                }
+            }
+        }
+        // the first maximum over b: largest sel, then smallest b
+#pragma unroll
+        for (int d = WAVE / 2; d > 0; d >>= 1) {
+            const double os = __shfl_xor(best_sel, d, WAVE);
+            const double ot = __shfl_xor(best_true, d, WAVE);
+            const int ob = __shfl_xor(best_b, d, WAVE);
+            const bool take = ob >= 0 && (best_b < 0 || os > best_sel || (os == best_sel && ob < best_b));
+            if (take) {
+                best_sel = os;
+                best_true = ot;
+                best_b = ob;
+            }
+        }
+    }
+    if (lane == 0) {
+        fsel[(size_t)c * F + f] = best_sel;
+        fgain[(size_t)c * F + f] = best_true;
+        fb[(size_t)c * F + f] = best_b;
+    }
+}
+
+// One wave per child: the feature-major first maximum (grow.c:183-192) and
+// the node value from feature 0's 256 bins (grow.c:371-379).
+__global__ void __launch_bounds__(WAVE) k_scan_pick(const float* __restrict__ hist, size_t hsz, int node0, int node1,
+                                                    int F, const double* __restrict__ fsel,
+                                                    const double* __restrict__ fgain, const int32_t* __restrict__ fb,
+                                                    float lr, double lam, float* __restrict__ out_value,
+                                                    Res* __restrict__ res, const Job* __restrict__ job, int nid,
+                                                    int split_f, int split_b, int64_t child_depth,
+                                                    int64_t* __restrict__ out_feature, int64_t* __restrict__ out_thr_bin,
+                                                    int64_t* __restrict__ out_left, int64_t* __restrict__ out_right,
+                                                    int64_t* __restrict__ out_depth) {
+    const int c = blockIdx.x;
+    if (threadIdx.x != 0) return;
+    if (nid >= 0 && c == 0) {                   // the split's record (grow.c:340-350, 381-386)
+        out_feature[nid] = split_f;
+        out_thr_bin[nid] = split_b;
+        out_left[nid] = node0;
+        out_right[nid] = node1;
+        out_value[nid] = 0.0f;
+        out_depth[node0] = child_depth;
+        out_depth[node1] = child_depth;
+    }
+    const int node = c == 0 ? node0 : node1;
+    double best_sel = -INFINITY, best_true = -INFINITY;
+    int bf = -1, bb = -1;
+    for (int f = 0; f < F; ++f) {
+        const int b = fb[(size_t)c * F + f];
+        const double s = fsel[(size_t)c * F + f];
+        if (b >= 0 && s > best_sel) {
+            best_sel = s;
+            best_true = fgain[(size_t)c * F + f];
+            bf = f;
+            bb = b;
+        }
+    }
+    const float* hg = hist + (size_t)node * hsz;
+    const float* hh = hg + (size_t)F * NB;
+    double G = 0.0, H = 0.0;
+    for (int b = 0; b < NB; ++b) {
+        G += hg[b];
+        H += hh[b];
+    }
+    const float v = (float)(-lr * G / (H + lam));
+    out_value[node] = v;
+    ChildRes& r = res->c[c];
+    r.gain = bf < 0 ? -INFINITY : best_true;
+    r.f = bf;
+    r.b = bb;
+    r.value = v;
+    if (c == 0) {
+        res->mid = job ? job->s + job->nl : 0;
+        res->build_left = job ? job->build_left : 0;
+    }
+}
+
+// Per-row leaf ids from the final rows[] and the leaves' segments.
+__global__ void __launch_bounds__(RB) k_leaf_rows(const uint32_t* __restrict__ rows, const int64_t* __restrict__ seg,
+                                                  int n_leaf, int64_t* __restrict__ out) {
+    const int k = blockIdx.y;
+    if (k >= n_leaf) return;
+    const int64_t node = seg[3 * k], s = seg[3 * k + 1], e = seg[3 * k + 2];
+    for (int64_t i = s + (int64_t)blockIdx.x * RB + threadIdx.x; i < e; i += (int64_t)gridDim.x * RB)
+        out[rows[i]] = node;
+}
+
+__global__ void k_set_status(int32_t* out, int v) { out[0] = v; }
+
+__global__ void __launch_bounds__(RB) k_rows_out(const uint32_t* __restrict__ rows, int64_t n, int64_t* __restrict__ out) {
+    for (int64_t i = (int64_t)blockIdx.x * RB + threadIdx.x; i < n; i += (int64_t)gridDim.x * RB) out[i] = rows[i];
+}
+
+// ---------------------------------------------------------------------------
+// host driver
+// ---------------------------------------------------------------------------
+
+struct Grower {
+    const uint8_t* bins_fm;
+    int64_t ld_fm;
+    const uint8_t* bins_rm;
+    int64_t ld_rm;
+    const float* grad;
+    const float* hess;
+    int64_t n;
+    int F;
+    Ws w;
+    size_t hsz;
+    int64_t nchunks;
+    hipStream_t st;
+
+    // Histogram of the job's built child (at most m_max rows) into node slot_l
+    // (left child built) or slot_r; job null: all rows into slot_l.
+    void hist(const Job* job, int64_t m_max, int slot_l, int slot_r, const float* G, const float* H) {
+        const int64_t ch = chunks_of(m_max > 0 ? m_max : 1);
+        k_hist_count<<<dim3((unsigned)ch, (unsigned)((F + FT - 1) / FT)), RB, 0, st>>>(bins_rm, ld_rm, w.rows, job, n, F,
+                                                                                      nchunks, w.counts);
+        k_hist_offsets<<<F, NB, 0, st>>>(w.counts, w.bstart, job, n, nchunks);
+        const int64_t cap = (int64_t)min(F, SORT_FEATS) * (n > 0 ? n : 1);
+        const int per = (int)max((int64_t)1, min((int64_t)F, cap / max(m_max, (int64_t)1)));
+        for (int fb0 = 0; fb0 < F; fb0 += per) {
+            const int nf = min(per, F - fb0);
+            k_hist_scatter<<<dim3((unsigned)ch, (unsigned)((nf + SF - 1) / SF)), SF * WAVE, 0, st>>>(
+                bins_rm, ld_rm, w.rows, job, n, fb0, nf, nchunks, w.counts, G, H, w.sorted, m_max);
+            k_hist_chain<<<(nf * NB + RB - 1) / RB, RB, 0, st>>>(w.sorted, m_max, w.bstart, fb0, nf, F, w.hist, hsz,
+                                                                job, slot_l, slot_r);
+        }
+    }
+};
+
+}  // namespace ref
+}  // namespace yabt
+
+using namespace yabt;
+using namespace yabt::ref;
+
+extern "C" {
+
+size_t yabt_grow_ref_workspace_bytes(int64_t n, int F, int max_leaves) {
+    if (n < 0 || n > 0xFFFFFFFFll || F < 1 || max_leaves < 1 || max_leaves > 32767) return 0;
+    return carve(nullptr, n, F, max_leaves).bytes;
+}
+
+int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm, const float* grad,
+                  const float* hess, const uint8_t* fmask, const float* imat, float ib, int use_imat,
+                  const int32_t* nbins, int64_t n, int F, float lam, float gamma, float mcw, int msl, float lr,
+                  int max_leaves, int max_depth, void* workspace, size_t workspace_bytes, int64_t* out_feature,
+                  int64_t* out_thr_bin, int64_t* out_left, int64_t* out_right, float* out_value, int64_t* out_depth,
+                  int64_t* out_leaf_of_row, int64_t* out_rows, int32_t* out_n_nodes, hipStream_t stream) {
+    if (n < 0 || n > 0xFFFFFFFFll || F < 1 || max_leaves < 1 || max_leaves > 32767)
+        return fail(-2, "yabt_grow_ref: bad sizes");
+    if (!grad || !hess || !fmask || !nbins || !workspace || !out_feature || !out_thr_bin || !out_left || !out_right ||
+        !out_value || !out_depth || !out_n_nodes || (use_imat && !imat))
+        return fail(-2, "yabt_grow_ref: null pointer argument");
+    if (n > 0 && (!bins_fm || !bins_rm || ld_fm < n || ld_rm < F || ld_rm % 16 || !aligned16(bins_rm)))
+        return fail(-2, "yabt_grow_ref: bins layout (pointer, alignment or leading dimension) invalid");
+    const size_t need = carve(nullptr, n, F, max_leaves).bytes;
+    if (workspace_bytes < need) return fail(-2, "yabt_grow_ref: workspace too small");
+
+    Grower g;
+    g.bins_fm = bins_fm;
+    g.ld_fm = ld_fm;
+    g.bins_rm = bins_rm;
+    g.ld_rm = ld_rm;
+    g.grad = grad;
+    g.hess = hess;
+    g.n = n;
+    g.F = F;
+    g.w = carve((char*)workspace, n, F, max_leaves);
+    g.hsz = (size_t)3 * F * NB;
+    g.nchunks = chunks_of(n > 0 ? n : 1);
+    g.st = stream;
+    const Ws& w = g.w;
+    const int N = 2 * max_leaves + 1;
+
+    Res* h_res = nullptr;
+    hipError_t he = hipHostMalloc((void**)&h_res, sizeof(Res), hipHostMallocDefault);
+    if (he != hipSuccess) return hip_fail(he, "yabt_grow_ref: pinned result buffer");
+    struct Free {
+        Res* p;
+        ~Free() { (void)hipHostFree(p); }
+    } free_res{h_res};
+
+    k_init<<<launch_grid(max((int64_t)N * F, n), RB, 1024), RB, 0, stream>>>(
+        w.rows, n, w.path, (int64_t)N * F, out_feature, out_thr_bin, out_left, out_right, out_value, out_depth, N);
+
+    ScanParams P;
+    P.nbins = nbins;
+    P.fmask = fmask;
+    P.imat = imat;
+    P.ib = ib;
+    P.use_imat = use_imat;
+    P.lam = (double)lam;
+    P.gamma = (double)gamma;
+    P.mcw = (double)mcw;
+    P.msl = msl;
+    P.F = F;
+
+    // host copy of cgrow's leaf table (grow.c:284-287) and node segments
+    std::vector<int64_t> node_start(N, 0), node_end(N, 0), node_depth(N, 0);
+    std::vector<int64_t> leaf_node(N), leaf_f(N), leaf_b(N);
+    std::vector<float> leaf_gain(N);
+    auto sync_res = [&]() -> int {
+        hipError_t e = hipMemcpyAsync(h_res, w.res, sizeof(Res), hipMemcpyDeviceToHost, stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(stream);
+        return e == hipSuccess ? 0 : hip_fail(e, "yabt_grow_ref: result copy");
+    };
+
+    // root
+    node_end[0] = n;
+    g.hist(nullptr, n, 0, 0, grad, hess);
+    k_scan_feature<<<dim3(F, 1), WAVE, 0, stream>>>(w.hist, g.hsz, 0, 0, w.path, P, w.fsel, w.fgain, w.fb);
+    k_scan_pick<<<1, WAVE, 0, stream>>>(w.hist, g.hsz, 0, 0, F, w.fsel, w.fgain, w.fb, lr, (double)lam, out_value,
+                                        w.res, nullptr, -1, 0, 0, 0, out_feature, out_thr_bin, out_left, out_right,
+                                        out_depth);
+    int rc = launch_status("yabt_grow_ref launch");
+    if (rc) return rc;
+    if ((rc = sync_res())) return rc;
+    double g0 = h_res->c[0].gain;
+    if (0 >= max_depth) g0 = -INFINITY;
+    leaf_node[0] = 0;
+    leaf_gain[0] = (float)g0;
+    leaf_f[0] = h_res->c[0].f;
+    leaf_b[0] = h_res->c[0].b;
+    int n_active = 1, n_leaves = 1, n_nodes = 1;
+    std::vector<char> split(N, 0);
+
+    while (n_leaves < max_leaves) {             // grow.c:321-408
+        int best_k = -1;
+        float best_g = 0.0f;
+        for (int k = 0; k < n_active; ++k)
+            if (leaf_gain[k] > best_g) {
+                best_g = leaf_gain[k];
+                best_k = k;
+            }
+        if (best_k < 0) break;
+        const int nid = (int)leaf_node[best_k];
+        const int f = (int)leaf_f[best_k], b = (int)leaf_b[best_k];
+        const int64_t s = node_start[nid], e = node_end[nid], m = e - s;
+        const int nl = n_nodes, nr = n_nodes + 1;
+        n_nodes += 2;
+        const int64_t d = node_depth[nid] + 1;
+        split[nid] = 1;
+
+        // partition rows[s:e) in cgrow's order; the smaller child's g, h
+        const int pblk = (int)max((int64_t)1, (m + PT - 1) / PT);
+        k_part_flags<<<pblk, RB, 0, stream>>>(bins_fm, ld_fm, f, b, w.rows, s, m, w.flag, w.blk);
+        k_part_offsets<<<1, RB, 0, stream>>>(w.blk, pblk, w.job, s, e);
+        k_part_rank<<<pblk, RB, 0, stream>>>(w.flag, w.blk, w.job, m, w.rank, w.p, w.q);
+        k_part_pairs<<<launch_grid(m / 2 + 1, RB * 4, 1024), RB, 0, stream>>>(w.p, w.q, w.job, m);
+        k_part_permute<<<launch_grid(m, RB * 4, 4096), RB, 0, stream>>>(w.flag, w.rank, w.p, w.q, w.job, w.rows,
+                                                                      w.rows_tmp, s, m, w.path, F, nid, f, nl, nr);
+        k_part_commit<<<launch_grid(m, RB * 4, 4096), RB, 0, stream>>>(w.rows, w.rows_tmp, w.job, s, m, grad, hess, w.G,
+                                                                     w.H);
+        // the smaller child (ties left, grow.c:355) has at most m / 2 rows;
+        // the other is parent - built (grow.c:361,368)
+        g.hist(w.job, m / 2, nl, nr, w.G, w.H);
+        k_hist_sub<<<launch_grid((int64_t)g.hsz, RB * 4, 1024), RB, 0, stream>>>(w.hist, g.hsz, nid, nl, nr, w.job);
+        k_scan_feature<<<dim3(F, 2), WAVE, 0, stream>>>(w.hist, g.hsz, nl, nr, w.path, P, w.fsel, w.fgain, w.fb);
+        k_scan_pick<<<2, WAVE, 0, stream>>>(w.hist, g.hsz, nl, nr, F, w.fsel, w.fgain, w.fb, lr, (double)lam,
+                                            out_value, w.res, w.job, nid, f, b, d, out_feature, out_thr_bin, out_left,
+                                            out_right, out_depth);
+        if ((rc = launch_status("yabt_grow_ref launch"))) return rc;
+        if ((rc = sync_res())) return rc;
+        const int64_t mid = h_res->mid;
+        node_start[nl] = s;
+        node_end[nl] = mid;
+        node_start[nr] = mid;
+        node_end[nr] = e;
+        node_depth[nl] = d;
+        node_depth[nr] = d;
+        n_leaves += 1;
+        double glg = h_res->c[0].gain, grg = h_res->c[1].gain;
+        if (d >= max_depth) glg = grg = -INFINITY;
+        leaf_node[best_k] = nl;
+        leaf_gain[best_k] = (float)glg;
+        leaf_f[best_k] = h_res->c[0].f;
+        leaf_b[best_k] = h_res->c[0].b;
+        leaf_node[n_active] = nr;
+        leaf_gain[n_active] = (float)grg;
+        leaf_f[n_active] = h_res->c[1].f;
+        leaf_b[n_active] = h_res->c[1].b;
+        n_active += 1;
+    }
+
+    // outputs: node count, per-row leaf ids, cgrow's final rows[]
+    k_set_status<<<1, 1, 0, stream>>>(out_n_nodes, n_nodes);
+    std::vector<int64_t> segs;   // read by the copy below until the final synchronisation
+    if (out_leaf_of_row && n > 0) {
+        for (int i = 0; i < n_nodes; ++i)
+            if (!split[i]) {
+                segs.push_back(i);
+                segs.push_back(node_start[i]);
+                segs.push_back(node_end[i]);
+            }
+        const int n_leaf = (int)(segs.size() / 3);
+        hipError_t e = hipMemcpyAsync(w.segs, segs.data(), segs.size() * sizeof(int64_t), hipMemcpyHostToDevice, stream);
+        if (e != hipSuccess) return hip_fail(e, "yabt_grow_ref: leaf segments");
+        k_leaf_rows<<<dim3((unsigned)launch_grid(n, RB * 4, 256), (unsigned)n_leaf), RB, 0, stream>>>(w.rows, w.segs,
+                                                                                                   n_leaf,
+                                                                                                   out_leaf_of_row);
+    }
+    if (out_rows && n > 0) k_rows_out<<<launch_grid(n, RB * 4, 4096), RB, 0, stream>>>(w.rows, n, out_rows);
+    if ((rc = launch_status("yabt_grow_ref launch"))) return rc;
+    const hipError_t e = hipStreamSynchronize(stream);
+    return e == hipSuccess ? 0 : hip_fail(e, "yabt_grow_ref: final synchronisation");
+}
+
+}  // extern "C"

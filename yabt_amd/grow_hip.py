@@ -160,16 +160,29 @@ class GrowResult:
         self._ws, self._status = workspace, status
 
 
+ARITHMETICS = ("exact", "reference")
+
+
 def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: np.ndarray, *,
                 fmask=None, imat=None, ib: float = 0.5, lam=1.0, gamma=0.0, mcw=1e-3, msl=20,
                 lr=0.1, max_leaves=31, max_depth=64, default_bin="auto",
-                sync: bool = True) -> GrowResult:
-    """One yabt_grow call on device-resident layouts.  grad/hess must be on
-    the layouts' device; parameters are rounded to float32 as ctypes.c_float
+                sync: bool = True, arithmetic: str = "exact") -> GrowResult:
+    """One grow call on device-resident layouts.  grad/hess must be on the
+    layouts' device; parameters are rounded to float32 as ctypes.c_float
     rounds them in the reference (grow_c.py:418-421).
 
-    ``default_bin``: "auto" uses the layouts' most frequent bin per feature,
-    None disables the skip, or an (F,) int array."""
+    ``arithmetic``: "exact" (yabt_grow: exact fixed-point sums, the whole
+    tree on the device) or "reference" (yabt_grow_ref: cgrow's own fp32
+    arithmetic and row order, the same trees as the reference bit for bit,
+    one host round trip per split).
+
+    ``default_bin`` ("exact" only): "auto" uses the layouts' most frequent bin
+    per feature, None disables the skip, or an (F,) int array."""
+    if arithmetic not in ARITHMETICS:
+        raise ValueError(f"arithmetic must be one of {ARITHMETICS}")
+    if arithmetic == "reference":
+        return _grow_device_ref(lay, grad, hess, nbins, fmask=fmask, imat=imat, ib=ib, lam=lam, gamma=gamma,
+                                mcw=mcw, msl=msl, lr=lr, max_leaves=max_leaves, max_depth=max_depth)
     lib = _lib.load()
     dev = lay.fm.device
     n, F = lay.n, lay.F
@@ -221,8 +234,58 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
     return res
 
 
+def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam, gamma, mcw, msl, lr,
+                     max_leaves, max_depth) -> GrowResult:
+    """yabt_grow_ref: cgrow's arithmetic on the device (synchronous)."""
+    lib = _lib.load()
+    dev = lay.fm.device
+    n, F = lay.n, lay.F
+    g = _dev_f32(grad, dev)
+    h = _dev_f32(hess, dev)
+    if g.shape[0] != n or h.shape[0] != n:
+        raise ValueError("grad/hess length must equal the number of rows")
+    fm = (torch.ones(F, dtype=torch.uint8, device=dev) if fmask is None
+          else torch.as_tensor(fmask).to(dev).bool().to(torch.uint8).contiguous())
+    use_imat = imat is not None
+    im = (torch.as_tensor(imat).to(dev, torch.float32).contiguous() if use_imat
+          else torch.zeros(1, dtype=torch.float32, device=dev))
+    if use_imat and tuple(im.shape) != (F, F):
+        raise ValueError("interaction_matrix must be (F, F)")
+    nb = torch.from_numpy(np.ascontiguousarray(nbins, dtype=np.int32)).to(dev)
+    L = int(max_leaves)
+    N = 2 * L + 1
+    nbytes = int(lib.yabt_grow_ref_workspace_bytes(n, F, L))
+    if nbytes == 0:
+        raise ValueError("yabt_grow_ref: invalid sizes")
+    key = (dev, "grow_ref")
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = ws
+    out_i = torch.empty((5, N), dtype=torch.int64, device=dev)
+    value = torch.empty(N, dtype=torch.float32, device=dev)
+    leaf = torch.empty(max(n, 1), dtype=torch.int64, device=dev)
+    rows = torch.empty(max(n, 1), dtype=torch.int64, device=dev)
+    nn = torch.zeros(1, dtype=torch.int32, device=dev)
+    rc = lib.yabt_grow_ref(
+        _ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h), _ptr(fm), _ptr(im),
+        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), n, F,
+        ctypes.c_float(float(lam)), ctypes.c_float(float(gamma)), ctypes.c_float(float(mcw)),
+        int(msl), ctypes.c_float(float(lr)), L, int(max_depth), _ptr(ws), ws.numel(),
+        _ptr(out_i[0]), _ptr(out_i[1]), _ptr(out_i[2]), _ptr(out_i[3]), _ptr(value), _ptr(out_i[4]),
+        _ptr(leaf), _ptr(rows), _ptr(nn), _stream(dev))
+    _lib.check(rc, "yabt_grow_ref")
+    k = int(nn.item())
+    res = GrowResult(out_i[0][:k], out_i[1][:k], out_i[2][:k], out_i[3][:k], value[:k], out_i[4][:k], k, ws, nn)
+    res.leaf_of_row = leaf[:n]
+    res.rows = rows[:n]
+    return res
+
+
 def leaf_ids(res: GrowResult, n: int, F: int, max_leaves: int) -> torch.Tensor:
     """Per-row leaf node ids of a grown tree, from its final partition."""
+    if getattr(res, "leaf_of_row", None) is not None:
+        return res.leaf_of_row
     lib = _lib.load()
     dev = res.value.device
     out = torch.empty(n, dtype=torch.int64, device=dev)
@@ -263,8 +326,10 @@ def grow_tree_hip(
     sparse_layout=None,
     n_threads: int = 0,
     binned_fmajor: np.ndarray | None = None,
+    arithmetic: str = "exact",
 ) -> Tree:
-    """Drop-in for ``grow_tree_c`` (yabt/grow_c.py:336-452) on a HIP device."""
+    """Drop-in for ``grow_tree_c`` (yabt/grow_c.py:336-452) on a HIP device;
+    ``arithmetic`` as in ``grow_device`` ("reference": cgrow's trees bit for bit)."""
     del sparse_layout, n_threads  # see module docstring
     out_dev = binned.device
     dev = binned.device if binned.device.type == "cuda" else _device()
@@ -274,7 +339,7 @@ def grow_tree_hip(
                       imat=interaction_matrix, ib=interaction_boost, lam=params.reg_lambda,
                       gamma=params.gamma, mcw=params.min_child_weight,
                       msl=params.min_samples_leaf, lr=params.learning_rate,
-                      max_leaves=params.max_leaves, max_depth=params.max_depth)
+                      max_leaves=params.max_leaves, max_depth=params.max_depth, arithmetic=arithmetic)
     return tree_from_result(res, binner, F, out_dev)
 
 

@@ -133,8 +133,14 @@ def leaf_moments(X: torch.Tensor, x_kind: int, feats: torch.Tensor, n: int):
 
 
 def fold(tree: Tree, W, db, mu, sd, lr, feats, lo, hi) -> Tree:
-    """Normalisation and shrinkage folded into raw space (neural_leaves.py:178-184)."""
-    value = tree.value.to(W.device) + lr * (db - (W * (mu / sd)).sum(dim=1))
+    """Normalisation and shrinkage folded into raw space (neural_leaves.py:178-184).
+    The K products are added left to right, the order torch's CPU reduction
+    takes for the reference's K = 8 inputs."""
+    prod = W * (mu / sd)
+    acc = prod[:, 0].clone()
+    for j in range(1, prod.shape[1]):
+        acc = acc + prod[:, j]
+    value = tree.value.to(W.device) + lr * (db - acc)
     return replace(tree, value=value, leaf_net_feats=feats, leaf_net_linear=lr * W / sd,
                    leaf_net_lo=lo, leaf_net_hi=hi)
 
