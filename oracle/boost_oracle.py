@@ -21,10 +21,11 @@ Only tests/ use it, as the reference the GPU booster is compared against.
 Pinned by tests/test_boost_oracle.py: loss closed forms and base scores, the
 detector against hand-counted pairs, the margin update and prediction against
 direct per-row evaluation, the leaf ids against raw-space routing of the
-training rows, and a fitted model that reduces training loss monotonically
-in the MSE case.  The trajectory as a whole (many trees composed) is
-"parity unpinned" against the reference beyond those parts: the reference's
-Booster cannot be run in this container (its CPU path imports numba).
+training rows, monotone training loss, and whole fits against the
+reference's own boosting fits (tests/golden/booster_*.npz, written by
+tests/golden/make_booster_golden.py): in the fp32 mode every tree of the
+regression (linear leaves, interaction steering, 25 trees) and logistic (10
+depth-8 trees) fits is the reference's, predictions within 1e-6.
 """
 
 from __future__ import annotations
@@ -92,19 +93,25 @@ class Binner:
 # --------------------------------------------------------------------------
 
 def base_score(loss: str, y: np.ndarray) -> float:
+    """The mean, or the logit of the clamped mean (boosting.py:31-33, 49-50);
+    the float32 mean is torch's CPU reduction, the call the reference makes."""
+    import torch
+    mu = torch.from_numpy(np.ascontiguousarray(y, dtype=np.float32)).mean()
     if loss == "mse":
-        return float(np.float32(y.astype(np.float32).mean()))
-    p = float(np.clip(np.float32(y.astype(np.float32).mean()), 1e-6, 1 - 1e-6))
+        return float(mu)
+    p = float(mu.clamp(1e-6, 1 - 1e-6))
     return float(np.log(p / (1 - p)))
 
 
 def grad_hess(loss: str, m: np.ndarray, y: np.ndarray):
+    """g, h in float32; the logistic p is torch's CPU sigmoid, the call the
+    reference makes (boosting.py:36)."""
     m = m.astype(np.float32)
     y = y.astype(np.float32)
     if loss == "mse":
         return (m - y).astype(np.float32), np.ones_like(y)
-    with np.errstate(over="ignore"):  # exp(-m) -> inf gives p = 0, as in fp32 on the device
-        p = (np.float32(1) / (np.float32(1) + np.exp(-m))).astype(np.float32)
+    import torch
+    p = torch.sigmoid(torch.from_numpy(np.ascontiguousarray(m))).numpy()
     return (p - y).astype(np.float32), np.maximum(p * (np.float32(1) - p), np.float32(1e-6)).astype(np.float32)
 
 

@@ -134,3 +134,57 @@ def test_select_features_pads_by_gradient_correlation():
     # split features by use count first, then the two most gradient-correlated
     assert f.tolist() == [2, 5, 4, 1]
     assert BO.select_features(feature, X, g, 1).tolist() == [2]
+
+
+def _golden(name):
+    import os
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", name)
+    with np.load(path, allow_pickle=False) as z:
+        return {k: z[k] for k in z.files}
+
+
+def _logistic(n, F, seed):
+    rng = np.random.default_rng(seed)
+    X = rng.normal(size=(n, F)).astype(np.float32)
+    w = rng.normal(size=F)
+    y = (rng.random(n) < 1 / (1 + np.exp(-(X @ w)))).astype(np.float32)
+    return X, y
+
+
+def _same_trees(model, d):
+    off = d["node_off"]
+    assert len(model["trees"]) == off.size - 1
+    for t, tr in enumerate(model["trees"]):
+        a, b = off[t], off[t + 1]
+        assert np.array_equal(tr["feature"], d["feature"][a:b]), f"tree {t}"
+        assert np.array_equal(tr["threshold"], d["threshold"][a:b]), f"tree {t}"
+        assert np.array_equal(tr["left"], d["left"][a:b]) and np.array_equal(tr["right"], d["right"][a:b])
+        assert np.abs(tr["value"] - d["value"][a:b]).max() <= 1e-6
+
+
+def test_fp32_oracle_reproduces_reference_regression_fit():
+    """The reference's estimator fit on 20 000 x 20 (25 trees, 31 leaves,
+    linear leaves, interaction steering, 255 bins, y standardised)."""
+    d = _golden("booster_regression_20kx20.npz")
+    X, y = _cfg1(20_000, 0)
+    Xt, _ = _cfg1(4_000, 11)
+    mean, std = float(y.mean()), float(y.std()) or 1.0
+    assert float(d["y_mean"]) == mean and float(d["y_std"]) == std
+    model = BO.fit(X, (y - mean) / std, loss="mse", n_estimators=25, max_leaves=31, max_bins=255,
+                   mode=O.MODE_FP32)
+    assert model["base"] == pytest.approx(float(d["base"]), abs=1e-12)
+    _same_trees(model, d)
+    assert np.abs(BO.predict_margin(model, Xt) * std + mean - d["pred"]).max() <= 1e-5
+
+
+def test_fp32_oracle_reproduces_reference_logistic_fit():
+    """The reference's binary fit on 50 000 x 28 (10 depth-8 trees, 28 bins)."""
+    d = _golden("booster_logistic_50kx28.npz")
+    X, y = _logistic(50_000, 28, 1)
+    Xt, _ = _logistic(4_000, 28, 2)
+    model = BO.fit(X, y, loss="log", n_estimators=10, max_leaves=256, max_depth=8, max_bins=28,
+                   neural_leaves=False, mode=O.MODE_FP32)
+    assert model["base"] == pytest.approx(float(d["base"]), abs=1e-12)
+    _same_trees(model, d)
+    p = 1 / (1 + np.exp(-BO.predict_margin(model, Xt).astype(np.float64)))
+    assert np.abs(p - d["proba"]).max() <= 1e-6
