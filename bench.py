@@ -30,7 +30,12 @@ rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over ``bench.py --counters``,
 which launches a plain copy kernel of known size (for the counter scale) and
 the root-histogram kernel, three times each.
 
+Also reported, outside the timed region: ``ms_grow_reference`` (one tree of
+the same workload grown with the reference's own fp32 arithmetic,
+yabt_grow_ref) and ``boosting`` (whole estimator fits, see boosting_fits).
+
 Usage: python bench.py [--gpus 1] [--steps 5] [--warmup 1] [--no-cpu]
+                       [--ref-steps 1] [--no-boosting]
        python bench.py --counters
 """
 
@@ -208,6 +213,45 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
                       f"host has {os.cpu_count()} logical CPUs"}
 
 
+def boosting_fits(torch) -> dict:
+    """Wall time of whole estimator fits (binning included, after one warm-up
+    fit) in both grower arithmetics:
+      * regression: X ~ N(0,1) 20 000 x 20, y = sin x0 + 0.5 x1 x2 + x3^2 +
+        0.3 sum x4..x9 + N(0, 0.1^2); 25 trees, 31 leaves, lr 0.1, linear
+        leaves, 255 bins;
+      * binary: X ~ N(0,1) 1 000 000 x 28, y ~ Bernoulli(sigmoid(X w)),
+        w ~ N(0,1); 100 trees of depth 8 (256 leaves), 28 bins, no leaf models."""
+    from yabt_amd import YABTClassifier, YABTRegressor
+    out = {}
+    rng = np.random.default_rng(0)
+    X = rng.normal(size=(20_000, 20)).astype(np.float32)
+    y = (np.sin(X[:, 0]) + 0.5 * X[:, 1] * X[:, 2] + X[:, 3] ** 2 + 0.3 * X[:, 4:10].sum(axis=1)
+         + rng.normal(scale=0.1, size=20_000)).astype(np.float32)
+    for arith in ("exact", "reference"):
+        mk = lambda: YABTRegressor(n_estimators=25, max_leaves=31, learning_rate=0.1, max_bins=255,
+                                   grower_arithmetic=arith)
+        mk().fit(X, y)
+        t0 = time.perf_counter()
+        mk().fit(X, y)
+        torch.cuda.synchronize()
+        out[f"regression_20kx20_25trees_s_{arith}"] = round(time.perf_counter() - t0, 3)
+    log("[bench] binary classifier fits")
+    rng = np.random.default_rng(0)
+    X = rng.normal(size=(1_000_000, 28)).astype(np.float32)
+    w = rng.normal(size=28)
+    y = (rng.random(1_000_000) < 1 / (1 + np.exp(-(X @ w)))).astype(np.float32)
+    for arith in ("exact", "reference"):
+        mk = lambda: YABTClassifier(n_estimators=100, max_leaves=256, max_depth=8, max_bins=28,
+                                    neural_leaves=False, grower_arithmetic=arith)
+        if arith == "exact":
+            mk().fit(X[:50_000], y[:50_000])
+        t0 = time.perf_counter()
+        mk().fit(X, y)
+        torch.cuda.synchronize()
+        out[f"binary_1Mx28_100trees_s_{arith}"] = round(time.perf_counter() - t0, 2)
+    return out
+
+
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -216,6 +260,9 @@ def main() -> None:
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--rows", type=int, default=N_ROWS)
     ap.add_argument("--no-neural", action="store_true", help="time the grower only")
+    ap.add_argument("--ref-steps", type=int, default=1,
+                    help="trees grown with the reference arithmetic (0: skip)")
+    ap.add_argument("--no-boosting", action="store_true", help="skip the estimator fits")
     ap.add_argument("--counters", action="store_true",
                     help="only launch the copy and root-histogram kernels for rocprofv3 --pmc")
     args = ap.parse_args()
@@ -311,6 +358,19 @@ def main() -> None:
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic()},
     }
+    if args.ref_steps > 0:
+        log(f"[bench] reference-arithmetic trees: {args.ref_steps}")
+        G.grow_device(lay, g, h, nbins, arithmetic="reference", **PARAMS)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.ref_steps):
+            G.grow_device(lay, g, h, nbins, arithmetic="reference", **PARAMS)
+        torch.cuda.synchronize()
+        line["ms_grow_reference"] = round((time.perf_counter() - t0) * 1e3 / args.ref_steps, 1)
+    if not args.no_boosting:
+        del lay, g, h
+        torch.cuda.empty_cache()
+        line["boosting"] = boosting_fits(torch)
     if not args.no_cpu:
         log("[bench] CPU baseline")
         line["cpu_baseline"] = cpu_baseline()
