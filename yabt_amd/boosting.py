@@ -240,7 +240,9 @@ class Booster:
         self.interaction_detector = (FeatureInteractionDetector(F)
                                      if p.detect_interactions or use_interaction_aware else None)
 
-        self.base_score = self.loss.base_score(yt)
+        # one scalar of set-up, taken from the host copy of y with the loss's
+        # own torch expression, as the reference's CPU fit computes it
+        self.base_score = self.loss.base_score(torch.as_tensor(np.asarray(y, dtype=np.float32)))
         margin = torch.full((n,), self.base_score, device=dev)
 
         if eval_set is not None:
