@@ -203,6 +203,35 @@ int yabt_grow_ref(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm,
                   int64_t *out_depth, int64_t *out_leaf_of_row, int64_t *out_rows,
                   int32_t *out_n_nodes, yabt_stream_t stream);
 
+/* Bytes of device workspace yabt_bin_fit needs for an m-row sample of F features. */
+size_t yabt_bin_fit_workspace_bytes(int64_t m, int F);
+
+/* Fit the quantile binner (yabt/binning.py:29-69, the numpy path) on X
+ * (fp32 row-major (n, ldx)).  The sample is rows sample_rows[0:m] in that
+ * order (NULL: all rows, m == n; the reference draws 200 000 rows with
+ * default_rng(0).choice when n > 200 000).  Per feature f, over the sample's
+ * non-NaN values (or [0.0] if none):
+ *   out_edges[f*ld_edges + 0 : out_nedges[f]] = np.unique of the fp32-rounded
+ *     numpy linear quantiles at linspace(0, 1, max_bins + 1)[1:-1];
+ *   out_scales[f] = q75 - q25 (double, numpy linear quantiles), or numpy's
+ *     float32 std of the sample column when that is 0, or 1;
+ * and over all n rows: out_medians[f] = np.nanmedian (0 where all NaN).
+ * 2 <= max_bins <= 256, ld_edges >= max_bins - 1. */
+int yabt_bin_fit(const float *X, int64_t ldx, int64_t n, int F, const int64_t *sample_rows, int64_t m,
+                 int max_bins, void *workspace, size_t workspace_bytes, float *out_edges,
+                 int64_t ld_edges, int32_t *out_nedges, float *out_scales, float *out_medians,
+                 yabt_stream_t stream);
+
+/* Transform with a fitted binner (yabt/binning.py:71-112): x := medians[f] where
+ * NaN, bin = #{edges_f < x} (torch.searchsorted, left).  Any of the outputs may
+ * be NULL: out_fm (F, ld_fm >= n) feature-major bins (the grower's layout),
+ * out_rm (n, ld_rm >= F) row-major bins, out_imputed (n, ld_imputed >= F) fp32
+ * imputed X (binning.py:114-118). */
+int yabt_bin_transform(const float *X, int64_t ldx, int64_t n, int F, const float *edges,
+                       int64_t ld_edges, const int32_t *nedges, const float *medians,
+                       uint8_t *out_fm, int64_t ld_fm, uint8_t *out_rm, int64_t ld_rm,
+                       float *out_imputed, int64_t ld_imputed, yabt_stream_t stream);
+
 /* Gradients and hessians of the boosting losses, fp32 (n rows):
  *   loss 0, MSELoss:  g = m - y, h = 1            (yabt/boosting.py:52-54)
  *   loss 1, LogLoss:  p = 1 / (1 + exp(-m)), g = p - y, h = max(p (1 - p), 1e-6)

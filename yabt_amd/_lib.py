@@ -56,6 +56,10 @@ SIGNATURES = {
     "yabt_grow_ref": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _i64, _int,
                              _flt, _flt, _flt, _int, _flt, _int, _int, _vp, _sz,
                              _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "yabt_bin_fit_workspace_bytes": (_sz, [_i64, _int]),
+    "yabt_bin_fit": (_int, [_vp, _i64, _i64, _int, _vp, _i64, _int, _vp, _sz, _vp, _i64, _vp, _vp, _vp, _vp]),
+    "yabt_bin_transform": (_int, [_vp, _i64, _i64, _int, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _i64,
+                                  _vp]),
     "yabt_grad_hess": (_int, [_int, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _vp, _vp]),
     "yabt_margin_update": (_int, [_vp, _i64, _vp, _vp, _i64, _int, _vp, _vp, _vp, _vp, _int, _vp, _i64, _vp]),
     "yabt_predict": (_int, [_vp, _i64, _i64, _int, _int, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _int, _vp, _vp,

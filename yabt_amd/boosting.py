@@ -39,7 +39,7 @@ import torch
 
 from . import boost_ops
 from .binning import Binner
-from .grow_hip import grow_device, grow_tree_hip, layouts_for, leaf_ids, nbins_of, tree_from_result
+from .grow_hip import grow_device, grow_tree_hip, leaf_ids, nbins_of, tree_from_result
 from .losses import LogLoss, MSELoss
 from .neural_leaves import fit_leaf_networks
 from .tree import Tree, TreeParams
@@ -230,11 +230,15 @@ class Booster:
         self.best_iter = None
         self._forest = None
 
-        self.binner = Binner(max_bins=p.max_bins).fit(X)
-        binned = self.binner.transform(X, device=dev)
-        Xraw = torch.from_numpy(self.binner.impute(X)).to(dev)
-        yt = torch.as_tensor(np.asarray(y, dtype=np.float32), device=dev)
+        # binning on the device: fit, then both bin layouts and the imputed
+        # matrix from one pass over the raw X
+        Xd = torch.from_numpy(np.ascontiguousarray(np.asarray(X, dtype=np.float32))).to(dev)
+        self.binner = Binner(max_bins=p.max_bins).fit(Xd)
+        lay, Xraw = self.binner.layouts(Xd)
+        del Xd
         n, F = Xraw.shape
+        binned = lay.rm[:n, :F]          # (n, F) view, used for row subsamples
+        yt = torch.as_tensor(np.asarray(y, dtype=np.float32), device=dev)
 
         use_interaction_aware = p.interaction_aware and n >= _INTERACTION_MIN_ROWS
         self.interaction_detector = (FeatureInteractionDetector(F)
@@ -246,14 +250,13 @@ class Booster:
         margin = torch.full((n,), self.base_score, device=dev)
 
         if eval_set is not None:
-            Xv = torch.from_numpy(self.binner.impute(eval_set[0])).to(dev)
+            Xv = self.binner.impute_device(eval_set[0])
             yv = torch.as_tensor(np.asarray(eval_set[1], dtype=np.float32), device=dev)
             margin_v = torch.full((Xv.shape[0],), self.base_score, device=dev)
             best_val, rounds_since_best = float("inf"), 0
 
         tp = self._tree_params()
         nbins = nbins_of(self.binner, F)
-        lay = layouts_for(binned, dev) if n > 0 else None
 
         for t in range(p.n_estimators):
             grad, hess = boost_ops.grad_hess(self.loss, margin, yt)
@@ -337,7 +340,7 @@ class Booster:
     def predict_margin(self, X: np.ndarray, use_best_iter: bool = True) -> np.ndarray:
         """Raw margins of X (boosting.py:547-561)."""
         dev = getattr(self, "device_", None) or self._device()
-        Xt = torch.from_numpy(self.binner.impute(X)).to(dev)
+        Xt = self.binner.impute_device(np.asarray(X, dtype=np.float32))
         n_trees = None
         if use_best_iter and self.best_iter is not None and self.p.refit_every == 0:
             n_trees = self.best_iter + 1
