@@ -179,6 +179,28 @@ int yabt_hist_slots(const uint8_t *binned, int64_t ldb, const int64_t *slot, con
                     const float *h, const float *w, int64_t n, int F, int K, void *workspace,
                     size_t workspace_bytes, float *out, int32_t *out_status, yabt_stream_t stream);
 
+/* Bytes of device workspace yabt_grow_levelwise needs; 0 when the sizes are
+ * out of range or max_leaves < 2^max_depth. */
+size_t yabt_grow_levelwise_workspace_bytes(int64_t n, int F, int max_leaves, int max_depth);
+
+/* yabt_grow for trees whose leaf budget cannot bind (max_leaves >= 2^max_depth,
+ * max_depth <= 16): every node of one depth is grown in one batch (routing
+ * pass, histograms of all built children, sibling subtraction, one scan
+ * launch), and the nodes are then numbered by replaying cgrow's best-first
+ * leaf table (yabt/_cgrow/grow.c:321-408) over the computed gains.  Same
+ * arguments and outputs as yabt_grow (no default_bin) -- bit-identical node
+ * arrays -- plus out_leaf_of_row (n int64, may be NULL): each row's leaf.
+ * Returns -3 if the budget could bind.  One device round trip per depth;
+ * the call synchronises `stream`. */
+int yabt_grow_levelwise(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
+                        const float *grad, const float *hess, const uint8_t *fmask, const float *imat,
+                        float ib, int use_imat, const int32_t *nbins, int64_t n, int F, float lam,
+                        float gamma, float mcw, int msl, float lr, int max_leaves, int max_depth,
+                        void *workspace, size_t workspace_bytes, int64_t *out_feature,
+                        int64_t *out_thr_bin, int64_t *out_left, int64_t *out_right, float *out_value,
+                        int64_t *out_depth, int64_t *out_leaf_of_row, int32_t *out_status,
+                        yabt_stream_t stream);
+
 /* Bytes of device workspace yabt_grow_ref needs for (n, F, max_leaves). */
 size_t yabt_grow_ref_workspace_bytes(int64_t n, int F, int max_leaves);
 

@@ -166,7 +166,7 @@ ARITHMETICS = ("exact", "reference")
 def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: np.ndarray, *,
                 fmask=None, imat=None, ib: float = 0.5, lam=1.0, gamma=0.0, mcw=1e-3, msl=20,
                 lr=0.1, max_leaves=31, max_depth=64, default_bin="auto",
-                sync: bool = True, arithmetic: str = "exact") -> GrowResult:
+                sync: bool = True, arithmetic: str = "exact", batched: bool | None = None) -> GrowResult:
     """One grow call on device-resident layouts.  grad/hess must be on the
     layouts' device; parameters are rounded to float32 as ctypes.c_float
     rounds them in the reference (grow_c.py:418-421).
@@ -176,13 +176,26 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
     arithmetic and row order, the same trees as the reference bit for bit,
     one host round trip per split).
 
-    ``default_bin`` ("exact" only): "auto" uses the layouts' most frequent bin
-    per feature, None disables the skip, or an (F,) int array."""
+    ``batched`` ("exact" only): grow depth by depth (yabt_grow_levelwise) --
+    the same tree, numbered by replaying the best-first order -- which needs
+    max_leaves >= 2^max_depth (the leaf budget cannot bind); None uses it
+    whenever that holds.
+
+    ``default_bin`` ("exact", not batched): "auto" uses the layouts' most
+    frequent bin per feature, None disables the skip, or an (F,) int array."""
     if arithmetic not in ARITHMETICS:
         raise ValueError(f"arithmetic must be one of {ARITHMETICS}")
     if arithmetic == "reference":
         return _grow_device_ref(lay, grad, hess, nbins, fmask=fmask, imat=imat, ib=ib, lam=lam, gamma=gamma,
                                 mcw=mcw, msl=msl, lr=lr, max_leaves=max_leaves, max_depth=max_depth)
+    can_batch = 0 <= int(max_depth) <= 16 and int(max_leaves) >= (1 << int(max_depth)) and int(max_leaves) <= 65535
+    if batched is None:
+        batched = can_batch and lay.n < 2 ** 31
+    if batched:
+        if not can_batch:
+            raise ValueError("batched growth needs max_leaves >= 2^max_depth and max_depth <= 16")
+        return _grow_device_level(lay, grad, hess, nbins, fmask=fmask, imat=imat, ib=ib, lam=lam, gamma=gamma,
+                                  mcw=mcw, msl=msl, lr=lr, max_leaves=max_leaves, max_depth=max_depth)
     lib = _lib.load()
     dev = lay.fm.device
     n, F = lay.n, lay.F
@@ -231,6 +244,55 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
         res.n_nodes = nn
         for k in ("feature", "thr_bin", "left", "right", "value", "depth"):
             setattr(res, k, getattr(res, k)[:nn])
+    return res
+
+
+def _grow_device_level(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam, gamma, mcw, msl, lr,
+                       max_leaves, max_depth) -> GrowResult:
+    """yabt_grow_levelwise: depth-batched growth, yabt_grow's tree (synchronous)."""
+    lib = _lib.load()
+    dev = lay.fm.device
+    n, F = lay.n, lay.F
+    g = _dev_f32(grad, dev)
+    h = _dev_f32(hess, dev)
+    if g.shape[0] != n or h.shape[0] != n:
+        raise ValueError("grad/hess length must equal the number of rows")
+    fm = (torch.ones(F, dtype=torch.uint8, device=dev) if fmask is None
+          else torch.as_tensor(fmask).to(dev).bool().to(torch.uint8).contiguous())
+    use_imat = imat is not None
+    im = (torch.as_tensor(imat).to(dev, torch.float32).contiguous() if use_imat
+          else torch.zeros(1, dtype=torch.float32, device=dev))
+    if use_imat and tuple(im.shape) != (F, F):
+        raise ValueError("interaction_matrix must be (F, F)")
+    nb = torch.from_numpy(np.ascontiguousarray(nbins, dtype=np.int32)).to(dev)
+    L = int(max_leaves)
+    N = 2 * L + 1
+    nbytes = int(lib.yabt_grow_levelwise_workspace_bytes(n, F, L, int(max_depth)))
+    if nbytes == 0:
+        raise ValueError("yabt_grow_levelwise: invalid sizes")
+    key = (dev, "grow_level")
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+        _WORKSPACES[key] = ws
+    out_i = torch.empty((5, N), dtype=torch.int64, device=dev)
+    value = torch.empty(N, dtype=torch.float32, device=dev)
+    leaf = torch.empty(max(n, 1), dtype=torch.int64, device=dev)
+    status = torch.zeros(1, dtype=torch.int32, device=dev)
+    rc = lib.yabt_grow_levelwise(
+        _ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h), _ptr(fm), _ptr(im),
+        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), n, F,
+        ctypes.c_float(float(lam)), ctypes.c_float(float(gamma)), ctypes.c_float(float(mcw)),
+        int(msl), ctypes.c_float(float(lr)), L, int(max_depth), _ptr(ws), ws.numel(),
+        _ptr(out_i[0]), _ptr(out_i[1]), _ptr(out_i[2]), _ptr(out_i[3]), _ptr(value), _ptr(out_i[4]),
+        _ptr(leaf), _ptr(status), _stream(dev))
+    _lib.check(rc, "yabt_grow_levelwise")
+    k = int(status.item())
+    if k < 0:
+        raise ValueError("yabt_grow: gradients or hessians contain non-finite values")
+    res = GrowResult(out_i[0][:k], out_i[1][:k], out_i[2][:k], out_i[3][:k], value[:k], out_i[4][:k], k, ws,
+                     status)
+    res.leaf_of_row = leaf[:n]
     return res
 
 
