@@ -213,6 +213,50 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
                       f"host has {os.cpu_count()} logical CPUs"}
 
 
+def depthwise_trees(torch, trees: int = 10) -> dict:
+    """ms per tree of the 4 000 000 x 500 skewed workload: each column bin 0
+    with probability 0.9 else uniform on 1..255, g ~ Laplace(0, 1), h = 1,
+    max_depth 6, 64 leaves, min_samples_leaf 20, with the margin update of a
+    squared loss (y = -g0, margin0 = 0) between trees; grown depth by depth
+    (the leaf budget cannot bind) and, for comparison, split by split."""
+    from yabt_amd import grow_hip as G
+    from yabt_amd import boost_ops
+    from yabt_amd.losses import MSELoss
+    from yabt_amd.tree import Tree
+    dev = torch.device("cuda", 0)
+    n, F = 4_000_000, 500
+    gen = torch.Generator(device=dev).manual_seed(0)
+    b = torch.randint(1, 256, (n, F), dtype=torch.uint8, device=dev, generator=gen)
+    b[torch.rand((n, F), device=dev, generator=gen) < 0.9] = 0
+    lay = G.make_layouts(b, dev)
+    del b
+    u = torch.rand(n, device=dev, generator=gen) - 0.5
+    g0 = -torch.sign(u) * torch.log1p(-2 * u.abs())            # Laplace(0, 1)
+    y = -g0
+    nbins = np.full(F, 256, np.int32)
+    P = dict(lam=1.0, gamma=0.0, mcw=1e-3, msl=20, lr=0.1, max_leaves=64, max_depth=6)
+    out = {}
+    for batched in (True, False):
+        margin = torch.zeros(n, device=dev)
+        def tree_step():
+            g, h = boost_ops.grad_hess(MSELoss(), margin, y)
+            res = G.grow_device(lay, g, h, nbins, batched=batched, **P)
+            leaf = G.leaf_ids(res, n, F, P["max_leaves"])
+            boost_ops.margin_update(margin, leaf, Tree(res.feature, res.thr_bin.float(), res.left, res.right,
+                                                       res.value, 0), None)
+        tree_step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(trees):
+            tree_step()
+        torch.cuda.synchronize()
+        key = "depth6_4Mx500_skewed_ms_per_tree_" + ("batched" if batched else "sequential")
+        out[key] = round((time.perf_counter() - t0) * 1e3 / trees, 2)
+    del lay
+    torch.cuda.empty_cache()
+    return out
+
+
 def boosting_fits(torch) -> dict:
     """Wall time of whole estimator fits (binning included, after one warm-up
     fit) in both grower arithmetics:
@@ -235,6 +279,8 @@ def boosting_fits(torch) -> dict:
         mk().fit(X, y)
         torch.cuda.synchronize()
         out[f"regression_20kx20_25trees_s_{arith}"] = round(time.perf_counter() - t0, 3)
+    log("[bench] depth-6 trees on 4M x 500 mostly-zero bins")
+    out.update(depthwise_trees(torch))
     log("[bench] binary classifier fits")
     rng = np.random.default_rng(0)
     X = rng.normal(size=(1_000_000, 28)).astype(np.float32)
