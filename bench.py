@@ -37,6 +37,7 @@ yabt_grow_ref) and ``boosting`` (whole estimator fits, see boosting_fits).
 Usage: python bench.py [--gpus 1] [--steps 5] [--warmup 1] [--no-cpu]
                        [--ref-steps 1] [--no-boosting]
        python bench.py --counters
+       python bench.py --boosting-only
 """
 
 from __future__ import annotations
@@ -257,6 +258,29 @@ def depthwise_trees(torch, trees: int = 10) -> dict:
     return out
 
 
+def multiclass_fit(torch) -> dict:
+    """Wall time of the 10-class estimator on X ~ N(0,1) 2 000 000 x 50 fp32,
+    y = argmax(X W + Gumbel noise), W ~ N(0,1) (50, 10): one-vs-rest boosters
+    of 20 trees each, 63 leaves, linear leaf models over 8 inputs with
+    leaf_net_l2 1e-3, 256 bins (binning of every class's booster included),
+    after one warm-up fit on 50 000 rows."""
+    from yabt_amd import YABTClassifier
+    rng = np.random.default_rng(0)
+    n, F, C = 2_000_000, 50, 10
+    X = rng.normal(size=(n, F)).astype(np.float32)
+    W = rng.normal(size=(F, C)).astype(np.float32)
+    y = np.argmax(X @ W + rng.gumbel(size=(n, C)).astype(np.float32), axis=1).astype(np.float32)
+    mk = lambda t: YABTClassifier(n_estimators=t, max_leaves=63, leaf_net_l2=1e-3, max_bins=256)
+    mk(2).fit(X[:50_000], y[:50_000])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    mk(20).fit(X, y)
+    torch.cuda.synchronize()
+    sec = time.perf_counter() - t0
+    return {"multiclass_2Mx50_10cls_20trees_s": round(sec, 2),
+            "multiclass_2Mx50_ms_per_tree": round(sec * 1e3 / (20 * C), 2)}
+
+
 def boosting_fits(torch) -> dict:
     """Wall time of whole estimator fits (binning included, after one warm-up
     fit) in both grower arithmetics:
@@ -281,6 +305,8 @@ def boosting_fits(torch) -> dict:
         out[f"regression_20kx20_25trees_s_{arith}"] = round(time.perf_counter() - t0, 3)
     log("[bench] depth-6 trees on 4M x 500 mostly-zero bins")
     out.update(depthwise_trees(torch))
+    log("[bench] 10-class fits with linear leaves")
+    out.update(multiclass_fit(torch))
     log("[bench] binary classifier fits")
     rng = np.random.default_rng(0)
     X = rng.normal(size=(1_000_000, 28)).astype(np.float32)
@@ -309,6 +335,8 @@ def main() -> None:
     ap.add_argument("--ref-steps", type=int, default=1,
                     help="trees grown with the reference arithmetic (0: skip)")
     ap.add_argument("--no-boosting", action="store_true", help="skip the estimator fits")
+    ap.add_argument("--boosting-only", action="store_true",
+                    help="only the estimator fits and depth-6 trees (one JSON line of their timings)")
     ap.add_argument("--counters", action="store_true",
                     help="only launch the copy and root-histogram kernels for rocprofv3 --pmc")
     args = ap.parse_args()
@@ -319,6 +347,10 @@ def main() -> None:
 
     import torch
     from yabt_amd import grow_hip as G
+
+    if args.boosting_only:
+        print(json.dumps({"boosting": boosting_fits(torch)}), flush=True)
+        return
 
     n, F = args.rows, N_FEAT
     log(f"[bench] generating {n} x {F} inputs on cuda:0")

@@ -418,12 +418,33 @@ __global__ void __launch_bounds__(RB) k_hist_chain(const float2* __restrict__ so
     const float2* src = sorted + (size_t)fi * sort_ld;
     float ag = 0.0f, ah = 0.0f, ac = 0.0f;
     uint32_t k = lo;
-    for (; k + 4 <= hi; k += 4) {
-        const float2 a0 = src[k], a1 = src[k + 1], a2 = src[k + 2], a3 = src[k + 3];
-        ag += a0.x; ah += a0.y; ac += 1.0f;
-        ag += a1.x; ah += a1.y; ac += 1.0f;
-        ag += a2.x; ah += a2.y; ac += 1.0f;
-        ag += a3.x; ah += a3.y; ac += 1.0f;
+    // the chain is latency-bound: batches of CB pairs are loaded one batch
+    // ahead of the (in-order, dependent) adds
+    constexpr uint32_t CB = 16;
+    if (k + CB <= hi) {
+        float2 cur[CB];
+#pragma unroll
+        for (uint32_t j = 0; j < CB; ++j) cur[j] = src[k + j];
+        k += CB;
+        for (; k + CB <= hi; k += CB) {
+            float2 nxt[CB];
+#pragma unroll
+            for (uint32_t j = 0; j < CB; ++j) nxt[j] = src[k + j];
+#pragma unroll
+            for (uint32_t j = 0; j < CB; ++j) {
+                ag += cur[j].x;
+                ah += cur[j].y;
+                ac += 1.0f;
+            }
+#pragma unroll
+            for (uint32_t j = 0; j < CB; ++j) cur[j] = nxt[j];
+        }
+#pragma unroll
+        for (uint32_t j = 0; j < CB; ++j) {
+            ag += cur[j].x;
+            ah += cur[j].y;
+            ac += 1.0f;
+        }
     }
     for (; k < hi; ++k) {
         const float2 a = src[k];
@@ -544,6 +565,18 @@ __global__ void __launch_bounds__(WAVE) k_scan_pick(const float* __restrict__ hi
                                                     int64_t* __restrict__ out_left, int64_t* __restrict__ out_right,
                                                     int64_t* __restrict__ out_depth) {
     const int c = blockIdx.x;
+    const int node = c == 0 ? node0 : node1;
+    // the wave stages feature 0's g and h bins in LDS; one lane adds them in order
+    __shared__ float s_g[NB], s_h[NB];
+    {
+        const float* hg = hist + (size_t)node * hsz;
+        const float* hh = hg + (size_t)F * NB;
+        for (int b = threadIdx.x; b < NB; b += WAVE) {
+            s_g[b] = hg[b];
+            s_h[b] = hh[b];
+        }
+    }
+    __syncthreads();
     if (threadIdx.x != 0) return;
     if (nid >= 0 && c == 0) {                   // the split's record (grow.c:340-350, 381-386)
         out_feature[nid] = split_f;
@@ -554,7 +587,6 @@ __global__ void __launch_bounds__(WAVE) k_scan_pick(const float* __restrict__ hi
         out_depth[node0] = child_depth;
         out_depth[node1] = child_depth;
     }
-    const int node = c == 0 ? node0 : node1;
     double best_sel = -INFINITY, best_true = -INFINITY;
     int bf = -1, bb = -1;
     for (int f = 0; f < F; ++f) {
@@ -567,12 +599,10 @@ __global__ void __launch_bounds__(WAVE) k_scan_pick(const float* __restrict__ hi
             bb = b;
         }
     }
-    const float* hg = hist + (size_t)node * hsz;
-    const float* hh = hg + (size_t)F * NB;
     double G = 0.0, H = 0.0;
     for (int b = 0; b < NB; ++b) {
-        G += hg[b];
-        H += hh[b];
+        G += s_g[b];
+        H += s_h[b];
     }
     const float v = (float)(-lr * G / (H + lam));
     out_value[node] = v;
