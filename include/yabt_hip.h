@@ -205,11 +205,19 @@ int yabt_grow_levelwise(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bi
 size_t yabt_grow_ref_workspace_bytes(int64_t n, int F, int max_leaves);
 
 /* Grow one best-first tree with the reference's own arithmetic: the same
- * trees as `cgrow` (yabt/_cgrow/grow.c:243-427, dense path) bit for bit --
- * fp32 histograms summed per (feature, bin) in cgrow's row order, cgrow's
+ * trees as `cgrow` (yabt/_cgrow/grow.c:243-427) bit for bit -- fp32
+ * histograms summed per (feature, bin) in cgrow's row order, cgrow's
  * in-place two-pointer partition order (grow.c:201-217), fp32 sibling
  * subtraction, the double-precision scan and node values, fp32 leaf gains.
- * Arguments as yabt_grow (no default_bin); out_status is replaced by
+ * Arguments as yabt_grow, except that default_bin selects the histogram
+ * builder rather than a shortcut: NULL is cgrow's dense builder
+ * (use_sparse = 0, grow.c:37-62); a device (F,) int32 array, entries in
+ * [0, 255], is cgrow's sparse builder (use_sparse = 1, grow.c:68-107) for a
+ * CSR layout of the same bins whose implicit bins are these (the layout of
+ * yabt/grow_numba.py:341-367; only its default bins are read, the entries
+ * are the bins outside them): each node's default-bin cell is
+ * (float)(double row-order sum over the node - double row-order sum over the
+ * node's rows outside the default bin).  out_status is replaced by
  * out_n_nodes (device int32, cgrow's return value).  Optional outputs (NULL
  * to skip): out_leaf_of_row (n int64) per-row leaf node ids; out_rows (n
  * int64) cgrow's final rows[] array.  The control loop runs on the host, one
@@ -218,11 +226,11 @@ size_t yabt_grow_ref_workspace_bytes(int64_t n, int F, int max_leaves);
  * 1 <= max_leaves <= 32767. */
 int yabt_grow_ref(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
                   const float *grad, const float *hess, const uint8_t *fmask, const float *imat,
-                  float ib, int use_imat, const int32_t *nbins, int64_t n, int F, float lam,
-                  float gamma, float mcw, int msl, float lr, int max_leaves, int max_depth,
-                  void *workspace, size_t workspace_bytes, int64_t *out_feature,
-                  int64_t *out_thr_bin, int64_t *out_left, int64_t *out_right, float *out_value,
-                  int64_t *out_depth, int64_t *out_leaf_of_row, int64_t *out_rows,
+                  float ib, int use_imat, const int32_t *nbins, const int32_t *default_bin,
+                  int64_t n, int F, float lam, float gamma, float mcw, int msl, float lr,
+                  int max_leaves, int max_depth, void *workspace, size_t workspace_bytes,
+                  int64_t *out_feature, int64_t *out_thr_bin, int64_t *out_left, int64_t *out_right,
+                  float *out_value, int64_t *out_depth, int64_t *out_leaf_of_row, int64_t *out_rows,
                   int32_t *out_n_nodes, yabt_stream_t stream);
 
 /* Bytes of device workspace yabt_bin_fit needs for an m-row sample of F features. */

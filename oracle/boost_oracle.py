@@ -8,7 +8,8 @@ prediction:
 * the losses' base scores and g, h in float32 (yabt/boosting.py:27-58);
 * the loop of Booster.fit without sampling (yabt/boosting.py:271-534):
   g, h -> interaction matrix -> grow -> leaf ids -> linear leaves -> path
-  pairs -> margin update;
+  pairs -> margin update, with the sparse-histogram choice and layout
+  (yabt/boosting.py:240-258, yabt/grow_numba.py:341-395);
 * the interaction detector (yabt/adaptive_features.py:121-160);
 * leaf-model feature selection (yabt/neural_leaves.py:21-39): the order of
   equal split-use counts is the one torch's CPU argsort gives, as in the
@@ -166,6 +167,31 @@ class Interactions:
 # trees
 # --------------------------------------------------------------------------
 
+def sparse_layout(bins: np.ndarray):
+    """The sparse histogram layout (yabt/grow_numba.py:341-367): each
+    feature's most frequent bin over all rows (lowest on ties) is its
+    default; (indptr, indices, data) is the row-major CSR of the other
+    cells.  bins: (n, F) uint8."""
+    n, F = bins.shape
+    default = np.array([np.bincount(bins[:, f], minlength=256).argmax() for f in range(F)], np.int64)
+    nondef = bins != default[None, :].astype(bins.dtype)
+    indptr = np.zeros(n + 1, np.int64)
+    np.cumsum(nondef.sum(axis=1), out=indptr[1:])
+    r, c = np.nonzero(nondef)
+    return indptr, c.astype(np.int64), bins[r, c].astype(np.int64), default
+
+
+def estimate_density(bins: np.ndarray, sample_rows: int = 4096) -> float:
+    """Share of non-modal cells over np.linspace(0, n - 1, sample_rows) rows
+    (yabt/grow_numba.py:375-395), which gates the sparse layout."""
+    n, F = bins.shape
+    if n > sample_rows:
+        bins = bins[np.linspace(0, n - 1, sample_rows).astype(np.int64)]
+    m = bins.shape[0]
+    modal = sum(int(np.bincount(bins[:, f], minlength=256).max()) for f in range(F))
+    return float(1.0 - modal / max(1, m * F))
+
+
 def thresholds(binner: Binner, feature, thr_bin) -> np.ndarray:
     return np.array([binner.edge_value(int(f), int(b)) if f >= 0 else np.float32(0)
                      for f, b in zip(feature, thr_bin)], np.float32)
@@ -255,10 +281,13 @@ def fit(X: np.ndarray, y: np.ndarray, *, loss: str = "mse", n_estimators: int = 
         subsample: float = 1.0, colsample: float = 1.0, seed: int = 0,
         interaction_aware: bool = True, interaction_boost: float = 0.5, neural_leaves: bool = True,
         leaf_net_features: int = 8, leaf_net_l2: float = 1.0, leaf_net_min_samples: int = 50,
-        mode: int = O.MODE_FIXED) -> dict:
+        sparse_hist="auto", sparse_hist_max_density: float = 0.5, mode: int = O.MODE_FIXED) -> dict:
     """Booster.fit (boosting.py:271-534).  Row and column samples are drawn
     from a CPU torch generator seeded with ``seed``, rows first, by the same
-    calls as the reference (boosting.py:369-383)."""
+    calls as the reference (boosting.py:369-383).  Trees grown on all rows
+    use the sparse histogram builder when ``sparse_hist`` is True, or "auto"
+    and the estimated density is at most ``sparse_hist_max_density``
+    (boosting.py:240-258, 438-439); it changes only the fp32 mode's sums."""
     import torch
     gen = torch.Generator(device="cpu").manual_seed(seed)
     binner = Binner(max_bins).fit(X)
@@ -272,6 +301,9 @@ def fit(X: np.ndarray, y: np.ndarray, *, loss: str = "mse", n_estimators: int = 
     det = Interactions(F) if use_ia else None
     base = base_score(loss, yt)
     margin = np.full(n, base, np.float32)
+    sl = None
+    if sparse_hist is True or (sparse_hist == "auto" and estimate_density(bins) <= sparse_hist_max_density):
+        sl = sparse_layout(bins)
     trees, train_loss = [], []
     for _ in range(n_estimators):
         g, h = grad_hess(loss, margin, yt)
@@ -286,6 +318,7 @@ def fit(X: np.ndarray, y: np.ndarray, *, loss: str = "mse", n_estimators: int = 
         bfm, gg, hh = ((bins_fm, g, h) if rows is None
                        else (np.ascontiguousarray(bins_fm[:, rows]), g[rows], h[rows]))
         t = O.grow(bfm, gg, hh, mode=mode, fmask=fmask, imat=imat, ib=interaction_boost, nbins=nb,
+                   sparse=sl if rows is None else None,
                    lam=reg_lambda, gamma=gamma, mcw=min_child_weight, msl=min_samples_leaf,
                    lr=learning_rate, max_leaves=max_leaves, max_depth=max_depth)
         tree = {k: t[k] for k in ("feature", "thr_bin", "left", "right", "value")}

@@ -60,6 +60,43 @@ def logistic(n, F, seed):
     return X, y
 
 
+def sparse_regression(n, F, seed):
+    """X: 90% zeros, the rest N(0,1); y = x0 + 2 x5 - x7 x9 + N(0, 0.1^2)."""
+    rng = np.random.default_rng(seed)
+    X = np.where(rng.random((n, F)) < 0.1, rng.normal(size=(n, F)), 0.0).astype(np.float32)
+    y = (X[:, 0] + 2 * X[:, 5] - X[:, 7] * X[:, 9] + rng.normal(scale=0.1, size=n)).astype(np.float32)
+    return X, y
+
+
+# The reference's sparse-layout helpers live in yabt/grow_numba.py, whose
+# import needs numba (absent here); these two follow them step for step.
+def build_sparse_layout(binned):
+    """yabt/grow_numba.py:341-367: per-feature most common bin (np.argmax of
+    the counts: lowest on ties) and the row-major CSR of the other cells."""
+    bn = np.ascontiguousarray(binned.detach().cpu().numpy())
+    n, F = bn.shape
+    counts = np.zeros((F, 256), dtype=np.int64)
+    np.add.at(counts, (np.arange(F)[None, :].repeat(n, 0).ravel(), bn.ravel()), 1)
+    default_bin = counts.argmax(axis=1).astype(np.int64)
+    nondef = bn != default_bin[None, :].astype(bn.dtype)
+    indptr = np.zeros(n + 1, dtype=np.int64)
+    np.cumsum(nondef.sum(axis=1), out=indptr[1:])
+    rows_idx, cols_idx = np.nonzero(nondef)
+    return indptr, cols_idx.astype(np.int64), bn[rows_idx, cols_idx].astype(np.int64), default_bin
+
+
+def estimate_density(binned, sample_rows=4096):
+    """yabt/grow_numba.py:375-395: non-modal share over linspace-sampled rows."""
+    bn = binned.detach().cpu().numpy()
+    n, F = bn.shape
+    if n > sample_rows:
+        bn = bn[np.linspace(0, n - 1, sample_rows).astype(np.int64)]
+    m = bn.shape[0]
+    counts = np.zeros((F, 256), dtype=np.int64)
+    np.add.at(counts, (np.arange(F)[None, :].repeat(m, 0).ravel(), bn.ravel()), 1)
+    return float(1.0 - counts.max(axis=1).sum() / max(1, m * F))
+
+
 def digest(*arrays) -> str:
     h = hashlib.sha256()
     for a in arrays:
@@ -122,13 +159,18 @@ def booster_fit(yabt, booster, X, y):
     margin = torch.full((n,), booster.base_score, device=dev)
     tp = booster._tree_params()
     bfm = np.ascontiguousarray(binned.detach().cpu().numpy().T, dtype=np.uint8)
+    sl = None                      # Booster._get_sparse_layout (boosting.py:240-258, 438-439)
+    if p.sparse_hist is True or (p.sparse_hist == "auto"
+                                 and estimate_density(binned) <= p.sparse_hist_max_density):
+        sl = build_sparse_layout(binned)
+    booster.sparse_used_ = sl is not None
     for _ in range(p.n_estimators):
         grad, hess = loss.grad_hess(margin, yt)
         imat = None
         if use_interaction_aware and booster.interaction_detector is not None:
             imat = booster.interaction_detector.normalized_matrix()
         tree = grow_tree_c(binned, grad, hess, booster.binner, tp, None, interaction_matrix=imat,
-                           interaction_boost=p.interaction_boost, sparse_layout=None,
+                           interaction_boost=p.interaction_boost, sparse_layout=sl,
                            n_threads=p.c_grower_threads, binned_fmajor=bfm)
         leaf_idx = tree.apply(Xraw)
         if p.neural_leaves:
@@ -187,6 +229,23 @@ def main() -> None:
                         x_digest=np.array(digest(X, y, Xt)), base=np.float64(clf.booster_.base_score),
                         proba=clf.predict_proba(Xt)[:, 1].astype(np.float32),
                         torch_threads=np.int64(torch.get_num_threads()), **arr)
+
+    # sparse regression: 30 000 x 60, 90% zeros, depth 6, 10 trees; sparse_hist
+    # "auto" picks cgrow's sparse histogram builder
+    X, y = sparse_regression(30_000, 60, 3)
+    Xt, _ = sparse_regression(4_000, 60, 4)
+    est = yabt.YABTRegressor(n_estimators=10, max_leaves=64, max_depth=6, max_bins=255, neural_leaves=False,
+                             **dict(common, sparse_hist="auto"))
+    est._cat_idx = []
+    yt = est._transform_y(np.asarray(y, dtype=np.float32), fit=True)
+    est.booster_ = booster_fit(yabt, Booster(est._boost_params(), MSELoss()), est._encode(X, yt, True), yt)
+    assert est.booster_.sparse_used_, "the sparse builder was expected"
+    arr = tree_arrays(est.booster_.trees)
+    np.savez_compressed(os.path.join(HERE, "booster_sparse_30kx60.npz"),
+                        x_digest=np.array(digest(X, y, Xt)), base=np.float64(est.booster_.base_score),
+                        y_mean=np.float64(est._y_mean), y_std=np.float64(est._y_std),
+                        pred=est.predict(Xt).astype(np.float32), torch_threads=np.int64(torch.get_num_threads()),
+                        **arr)
     print("wrote", sorted(f for f in os.listdir(HERE) if f.startswith("booster_")))
 
 

@@ -188,3 +188,61 @@ def test_fp32_oracle_reproduces_reference_logistic_fit():
     _same_trees(model, d)
     p = 1 / (1 + np.exp(-BO.predict_margin(model, Xt).astype(np.float64)))
     assert np.abs(p - d["proba"]).max() <= 1e-6
+
+
+def _sparse_regression(n, F, seed):
+    rng = np.random.default_rng(seed)
+    X = np.where(rng.random((n, F)) < 0.1, rng.normal(size=(n, F)), 0.0).astype(np.float32)
+    y = (X[:, 0] + 2 * X[:, 5] - X[:, 7] * X[:, 9] + rng.normal(scale=0.1, size=n)).astype(np.float32)
+    return X, y
+
+
+def test_fp32_oracle_reproduces_reference_sparse_fit():
+    """The reference's fit on 30 000 x 60 with 90% zeros (10 depth-6 trees):
+    sparse_hist "auto" estimates the density at about 0.1 and grows every tree
+    with cgrow's sparse builder, whose default-bin cells are fp32 roundings of
+    double sums (grow.c:68-107)."""
+    d = _golden("booster_sparse_30kx60.npz")
+    X, y = _sparse_regression(30_000, 60, 3)
+    Xt, _ = _sparse_regression(4_000, 60, 4)
+    mean, std = float(y.mean()), float(y.std()) or 1.0
+    assert float(d["y_mean"]) == mean and float(d["y_std"]) == std
+    kw = dict(loss="mse", n_estimators=10, max_leaves=64, max_depth=6, max_bins=255, neural_leaves=False,
+              mode=O.MODE_FP32)
+    model = BO.fit(X, (y - mean) / std, **kw)
+    assert model["base"] == pytest.approx(float(d["base"]), abs=1e-12)
+    _same_trees(model, d)
+    # without leaf models the node values are cgrow's own: equal bit for bit,
+    # which the dense builder's sums miss by up to ~2e-6 on this data
+    v = np.concatenate([t["value"] for t in model["trees"]])
+    assert np.array_equal(v.view(np.uint32), d["value"].view(np.uint32))
+    dense = np.concatenate([t["value"] for t in BO.fit(X, (y - mean) / std, sparse_hist=False, **kw)["trees"]])
+    assert not np.array_equal(dense.view(np.uint32), d["value"].view(np.uint32))
+    assert np.abs(BO.predict_margin(model, Xt) * std + mean - d["pred"]).max() <= 1e-5
+
+
+def test_sparse_layout_and_density():
+    """The layout's default bin is the most frequent (lowest on ties), its CSR
+    lists exactly the other cells row by row, and the density estimate counts
+    the non-modal cells of the linspace-sampled rows (brute force with
+    collections.Counter)."""
+    import collections
+    rng = np.random.default_rng(5)
+    n, F = 9000, 7
+    bins = np.where(rng.random((n, F)) < 0.8, 3, rng.integers(0, 256, (n, F))).astype(np.uint8)
+    bins[:, 1] = np.arange(n) % 4                   # ties: 0..3 equally often
+    bins[:, 2] = 200
+    indptr, indices, data, default = BO.sparse_layout(bins)
+    assert default.tolist() == [3, 0, 200, 3, 3, 3, 3]
+    rebuilt = np.repeat(default[None, :], n, 0)
+    for r in range(n):
+        for k in range(indptr[r], indptr[r + 1]):
+            assert data[k] != default[indices[k]]
+            rebuilt[r, indices[k]] = data[k]
+        assert np.all(np.diff(indices[indptr[r]:indptr[r + 1]]) > 0)
+    assert np.array_equal(rebuilt, bins)
+    idx = [int(i) for i in np.linspace(0, n - 1, 4096)]
+    modal = sum(collections.Counter(bins[i, f] for i in idx).most_common(1)[0][1] for f in range(F))
+    assert BO.estimate_density(bins) == pytest.approx(1 - modal / (4096 * F), abs=1e-15)
+    assert BO.estimate_density(bins[:100]) == pytest.approx(
+        1 - sum(collections.Counter(bins[:100, f]).most_common(1)[0][1] for f in range(F)) / (100 * F), abs=1e-15)

@@ -7,7 +7,10 @@
   order equal, per-row leaf ids equal to the partition membership;
 * the boosting golden vectors of the reference (tests/golden/booster_*.npz):
   with grower_arithmetic="reference" every tree's split sequence is the
-  reference's and predictions agree to 1e-6 (leaf models by two fp64 solvers).
+  reference's and predictions agree to 1e-6 (leaf models by two fp64 solvers);
+* cgrow's sparse builder (grow.c:68-107): the reference's sparse fixture, the
+  oracle's fp32 sparse mode on seeded cases (modal and arbitrary default
+  bins), and the reference's fit on 90%-zero data, where "auto" picks it.
 """
 
 import glob
@@ -17,6 +20,7 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import boost_oracle as BO
 from oracle import oracle as O
 from tests.helpers import grad_hess, skewed_bins, tree_arrays_equal, uniform_bins
 from yabt_amd import YABTClassifier, YABTRegressor
@@ -26,7 +30,7 @@ pytestmark = pytest.mark.gpu
 
 DEV = torch.device("cuda", 0) if torch.cuda.is_available() else None
 HERE = os.path.dirname(os.path.abspath(__file__))
-FIXTURES = sorted(p for p in glob.glob(os.path.join(HERE, "golden", "grow_*.npz")) if "sparse" not in p)
+FIXTURES = sorted(glob.glob(os.path.join(HERE, "golden", "grow_*.npz")))
 
 
 def _grow_ref(bins_nf, g, h, nbins, **kw):
@@ -49,6 +53,8 @@ def test_matches_reference_fixtures(path):
         kw.update(imat=d["imat"], ib=float(d["ib"]))
     if "fmask" in d:
         kw["fmask"] = d["fmask"]
+    if "sp_default" in d:         # the fixture grown with cgrow's sparse builder
+        kw["default_bin"] = d["sp_default"]
     got, leaf, rows = _grow_ref(d["bins_fm"].T, d["grad"], d["hess"], d["nbins"], **kw)
     want = {k[4:]: d[k] for k in d if k.startswith("out_")}
     assert tree_arrays_equal(got, want) is None
@@ -151,3 +157,115 @@ def test_classifier_matches_reference_golden():
                          grower_arithmetic="reference").fit(X, y)
     _same_as_golden(clf.booster_.trees, d)
     assert np.abs(clf.predict_proba(Xt)[:, 1] - d["proba"]).max() <= 1e-6
+
+
+def _modal_bins(rng, n, F, share=0.7):
+    """Each column: a random bin with probability ``share``, else uniform."""
+    b = rng.integers(0, 256, size=(n, F))
+    dflt = rng.integers(0, 256, size=F)
+    return np.where(rng.random((n, F)) < share, dflt[None, :], b).astype(np.uint8)
+
+
+def _layout_for(bins, default):
+    """CSR of the cells outside the given default bins (any default bins:
+    cgrow reads whatever layout it is handed)."""
+    nondef = bins != default[None, :].astype(bins.dtype)
+    indptr = np.concatenate([[0], np.cumsum(nondef.sum(axis=1))]).astype(np.int64)
+    r, c = np.nonzero(nondef)
+    return indptr, c.astype(np.int64), bins[r, c].astype(np.int64), default.astype(np.int64)
+
+
+SPARSE_CASES = [
+    dict(n=3000, F=40, bins="skew", kind="normal", max_leaves=31),
+    dict(n=8000, F=40, bins="skew", kind="laplace", max_leaves=64, max_depth=6),
+    dict(n=50_000, F=20, bins="modal", kind="normal", max_leaves=255),
+    dict(n=20_000, F=12, bins="modal", kind="laplace", max_leaves=63, imat=True, fmask=True),
+    dict(n=5000, F=1, bins="skew", kind="normal", max_leaves=15),
+    dict(n=1, F=1, bins="skew", kind="normal", max_leaves=31, msl=0),
+    dict(n=300_000, F=5, bins="skew", kind="laplace", max_leaves=63),
+    dict(n=200_000, F=33, bins="skew", kind="laplace", max_leaves=40, max_depth=6),
+    dict(n=10_000, F=9, bins="uniform", kind="normal", max_leaves=31, arbitrary=True),
+]
+
+
+@pytest.mark.parametrize("case", SPARSE_CASES,
+                         ids=lambda c: f"{c['bins']}_n{c['n']}_F{c['F']}_L{c['max_leaves']}")
+def test_sparse_builder_matches_fp32_oracle(case):
+    print(f"sparse case {case}", flush=True)
+    c = dict(case)
+    rng = np.random.default_rng(c["n"] * 3 + c["F"])
+    n, F, kind = c.pop("n"), c.pop("F"), c.pop("bins")
+    bins = {"skew": lambda: skewed_bins(rng, n, F), "modal": lambda: _modal_bins(rng, n, F),
+            "uniform": lambda: uniform_bins(rng, n, F)}[kind]()
+    g, h = grad_hess(rng, n, c.pop("kind"))
+    kw = dict(max_leaves=c.pop("max_leaves"), max_depth=c.pop("max_depth", 64), msl=c.pop("msl", 20))
+    if c.pop("imat", False):
+        im = rng.random((F, F)).astype(np.float32)
+        kw.update(imat=(im + im.T) / 2, ib=0.5)
+    if c.pop("fmask", False):
+        kw["fmask"] = rng.random(F) < 0.7
+    layout = (_layout_for(bins, rng.integers(0, 256, size=F)) if c.pop("arbitrary", False)
+              else BO.sparse_layout(bins))
+    nbins = np.full(F, 256, np.int32)
+    got, leaf, rows = _grow_ref(bins, g, h, nbins, default_bin=layout[3], **kw)
+    want = O.grow(np.ascontiguousarray(bins.T), g, h, mode=O.MODE_FP32, nbins=nbins, sparse=layout, **kw)
+    assert tree_arrays_equal(got, want) is None
+    assert np.array_equal(rows, want["rows"]), "cgrow's rows[] order"
+    assert np.array_equal(leaf, O.leaf_of_rows(want, n))
+
+
+def test_grow_tree_hip_follows_the_sparse_layout():
+    """grow_tree_hip(..., sparse_layout=...) in the reference arithmetic is
+    cgrow's sparse tree; the exact arithmetic ignores the layout."""
+    from yabt_amd.binning import IdentityBinner
+    from yabt_amd.grow_hip import grow_tree_hip
+    from yabt_amd.tree import TreeParams
+    rng = np.random.default_rng(17)
+    n, F = 40_000, 24
+    bins = skewed_bins(rng, n, F)
+    g, h = grad_hess(rng, n, "laplace")
+    layout = BO.sparse_layout(bins)
+    tp = TreeParams(max_leaves=48, max_depth=6)
+    bt = torch.from_numpy(bins)
+    tree = grow_tree_hip(bt, torch.from_numpy(g), torch.from_numpy(h), IdentityBinner(F), tp,
+                         sparse_layout=layout, arithmetic="reference")
+    want = O.grow(np.ascontiguousarray(bins.T), g, h, mode=O.MODE_FP32, sparse=layout, max_leaves=48, max_depth=6)
+    assert np.array_equal(tree.feature.numpy(), want["feature"])
+    assert np.array_equal(tree.value.numpy().view(np.uint32), want["value"].view(np.uint32))
+    ex = grow_tree_hip(bt, torch.from_numpy(g), torch.from_numpy(h), IdentityBinner(F), tp, sparse_layout=layout)
+    ex0 = grow_tree_hip(bt, torch.from_numpy(g), torch.from_numpy(h), IdentityBinner(F), tp)
+    assert torch.equal(ex.feature, ex0.feature) and torch.equal(ex.value, ex0.value)
+
+
+def test_sparse_default_bins_are_checked():
+    rng = np.random.default_rng(2)
+    bins = skewed_bins(rng, 500, 4)
+    g, h = grad_hess(rng, 500)
+    for bad in ([0, 0, 256, 0], [0, -1, 0, 0]):
+        with pytest.raises(RuntimeError, match="default_bin"):
+            _grow_ref(bins, g, h, np.full(4, 256, np.int32), default_bin=np.array(bad, np.int32), max_leaves=8)
+    with pytest.raises(ValueError):
+        _grow_ref(bins, g, h, np.full(4, 256, np.int32), default_bin=np.zeros(3, np.int32), max_leaves=8)
+
+
+def _sparse_regression(n, F, seed):
+    rng = np.random.default_rng(seed)
+    X = np.where(rng.random((n, F)) < 0.1, rng.normal(size=(n, F)), 0.0).astype(np.float32)
+    y = (X[:, 0] + 2 * X[:, 5] - X[:, 7] * X[:, 9] + rng.normal(scale=0.1, size=n)).astype(np.float32)
+    return X, y
+
+
+def test_sparse_regressor_matches_reference_golden():
+    """30 000 x 60 with 90% zeros, 10 depth-6 trees: the reference's fit
+    takes cgrow's sparse builder (sparse_hist "auto"); in the reference
+    arithmetic every node value is the reference's bit for bit."""
+    print("sparse regressor golden", flush=True)
+    d = _golden("booster_sparse_30kx60.npz")
+    X, y = _sparse_regression(30_000, 60, 3)
+    Xt, _ = _sparse_regression(4_000, 60, 4)
+    est = YABTRegressor(n_estimators=10, max_leaves=64, max_depth=6, max_bins=255, neural_leaves=False,
+                        grower_arithmetic="reference").fit(X, y)
+    _same_as_golden(est.booster_.trees, d)
+    v = np.concatenate([t.value.cpu().numpy() for t in est.booster_.trees])
+    assert np.array_equal(v.view(np.uint32), d["value"].view(np.uint32))
+    assert np.abs(est.predict(Xt) - d["pred"]).max() <= 1e-5

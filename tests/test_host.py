@@ -74,3 +74,26 @@ def test_identity_binner():
     assert b.edge_value(1, 17) == 17.0
     assert b.edge_value(1, 300) == 254.0
     assert len(b.edges_[0]) == 255
+
+
+def test_layout_cache_reuses_per_tensor_and_forgets_dead_tensors(monkeypatch):
+    """layouts_for caches one layout pair per binned tensor: the same tensor
+    again hits (a second call once failed on tensor key comparison), an
+    in-place change rebuilds, and the entry goes when the tensor dies."""
+    import gc
+
+    from yabt_amd import grow_hip as G
+    built = []
+    monkeypatch.setattr(G, "make_layouts", lambda b, d, f=None: built.append(object()) or built[-1])
+    monkeypatch.setattr(G, "_LAYOUTS", {})
+    t = torch.zeros(5, 3, dtype=torch.uint8)
+    a = G.layouts_for(t, "dev")
+    assert G.layouts_for(t, "dev") is a and len(built) == 1
+    t.add_(1)
+    assert G.layouts_for(t, "dev") is not a and len(built) == 2
+    u = torch.zeros(5, 3, dtype=torch.uint8)
+    G.layouts_for(u, "dev")
+    assert len(G._LAYOUTS) == 2
+    del t
+    gc.collect()
+    assert list(G._LAYOUTS) == [id(u)]

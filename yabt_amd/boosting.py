@@ -22,8 +22,10 @@ Interaction steering (``FeatureInteractionDetector``, adaptive_features.py:
 so its normalisation is the reference's own fp32 expression.
 
 The reference's grower switches (``levelwise`` "auto"/False, ``numba_grower``,
-``c_grower``, ``c_grower_threads``, ``sparse_hist``) all select the leaf-wise
-grower here.  Features outside the tree-growing path raise
+``c_grower``, ``c_grower_threads``) all select the leaf-wise grower here;
+``sparse_hist`` / ``sparse_hist_max_density`` pick cgrow's sparse or dense
+histogram builder as the reference does, which matters only to
+``grower_arithmetic="reference"`` (exact sums are the same either way).  Features outside the tree-growing path raise
 ``NotImplementedError`` when switched on: differentiable refinement and
 refits, adaptive features, GOSS, product features, kernel splits, auto-tuning,
 stochastic routing, MLP leaves and the level-wise grower (``levelwise=True``).
@@ -218,6 +220,36 @@ class Booster:
         d = self.p.resolve_device()
         return torch.device("cuda", torch.cuda.current_device()) if d == "cuda" else torch.device(d)
 
+    # rows the reference's density estimate samples (grow_numba.py:375)
+    _DENSITY_SAMPLE_ROWS = 4096
+
+    def _sparse_default_bins(self, lay, n: int, F: int) -> torch.Tensor | None:
+        """The reference's sparse-histogram choice for unsubsampled trees
+        (boosting.py:240-258, 438-439): ``sparse_hist`` True always, "auto" when
+        the estimated share of non-modal cells is at most
+        ``sparse_hist_max_density``.  The estimate takes the modal count per
+        feature over np.linspace(0, n - 1, 4096) rows (grow_numba.py:375-395);
+        the layout's default bin is each feature's most frequent bin over all
+        rows, lowest bin on ties (grow_numba.py:356-359).  Only the default
+        bins are needed: the explicit entries are the bins outside them.
+        Returns the (F,) device default bins, or None for the dense builder."""
+        p = self.p
+        if p.sparse_hist is False or n == 0:
+            return None
+        fm = lay.fm[:, :n]
+        if p.sparse_hist is not True:
+            idx = np.arange(n) if n <= self._DENSITY_SAMPLE_ROWS else \
+                np.linspace(0, n - 1, self._DENSITY_SAMPLE_ROWS).astype(np.int64)
+            cols = fm[:, torch.from_numpy(idx).to(fm.device)].long()
+            counts = torch.zeros((F, 256), dtype=torch.int64, device=fm.device)
+            counts.scatter_add_(1, cols, torch.ones_like(cols))
+            modal = int(counts.max(dim=1).values.sum())
+            dens = 1.0 - modal / max(1, idx.size * F)
+            if not dens <= p.sparse_hist_max_density:
+                return None
+        full = torch.stack([torch.bincount(fm[f], minlength=256) for f in range(F)])
+        return full.argmax(dim=1).to(torch.int32).contiguous()
+
     def fit(self, X: np.ndarray, y: np.ndarray,
             eval_set: tuple[np.ndarray, np.ndarray] | None = None) -> "Booster":
         """The reference's training loop (boosting.py:271-534) on the device."""
@@ -257,6 +289,9 @@ class Booster:
 
         tp = self._tree_params()
         nbins = nbins_of(self.binner, F)
+        # cgrow's histogram builder for unsubsampled trees: only the reference
+        # arithmetic depends on it (exact sums are the same either way)
+        sparse_db = (self._sparse_default_bins(lay, n, F) if p.grower_arithmetic == "reference" else None)
 
         for t in range(p.n_estimators):
             grad, hess = boost_ops.grad_hess(self.loss, margin, yt)
@@ -285,6 +320,7 @@ class Booster:
                                   lam=tp_t.reg_lambda, gamma=tp_t.gamma, mcw=tp_t.min_child_weight,
                                   msl=tp_t.min_samples_leaf, lr=tp_t.learning_rate,
                                   max_leaves=tp_t.max_leaves, max_depth=tp_t.max_depth,
+                                  default_bin=sparse_db if sparse_db is not None else "auto",
                                   arithmetic=p.grower_arithmetic)
                 tree = tree_from_result(res, self.binner, F, dev)
                 leaf_idx = leaf_ids(res, n, F, tp_t.max_leaves)

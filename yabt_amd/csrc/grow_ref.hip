@@ -88,7 +88,9 @@ struct Ws {
     float* H;
     uint32_t* counts;              // (F, chunks, 256)
     uint32_t* bstart;              // (F, 257)
-    float2* sorted;                // (SORT_FEATS, n)
+    float2* sorted;                // (max(min(F, SORT_FEATS), 2), n)
+    double* expl;                  // (F, 2): sparse builder's explicit g, h sums
+    double* tot;                   // (2): sparse builder's node g, h sums
     float* hist;                   // (N, 3, F, 256)
     double* fsel;                  // (2, F)
     double* fgain;                 // (2, F)
@@ -118,7 +120,9 @@ Ws carve(char* base, int64_t n, int F, int max_leaves) {
     w.H = c.take<float>(nn);
     w.counts = c.take<uint32_t>((size_t)F * chunks_of(nn) * NB);
     w.bstart = c.take<uint32_t>((size_t)F * (NB + 1));
-    w.sorted = c.take<float2>((size_t)min(F, SORT_FEATS) * nn);
+    w.sorted = c.take<float2>((size_t)max(min(F, SORT_FEATS), 2) * nn);
+    w.expl = c.take<double>(2 * (size_t)F);
+    w.tot = c.take<double>(2);
     w.hist = c.take<float>((size_t)N * 3 * F * NB);
     w.fsel = c.take<double>(2 * (size_t)F);
     w.fgain = c.take<double>(2 * (size_t)F);
@@ -353,12 +357,18 @@ __global__ void __launch_bounds__(NB) k_hist_offsets(uint32_t* __restrict__ coun
 // Bucket the (g, h) pairs of features [fb0, fb0 + nf) by bin, stably: one wave
 // per feature walks the chunk's rows in order, 64 at a time; lanes with equal
 // bins are ranked by lane (eight ballots find the lanes sharing a bin).
+// Sparse builder (dbin non-null): the pairs outside the feature's default bin
+// are also written, in row order, to expl[fi * sort_ld + ...]; the default
+// bin's own pairs are not bucketed (no chain reads them).
 __global__ void __launch_bounds__(SF * WAVE) k_hist_scatter(const uint8_t* __restrict__ bins_rm, int64_t ld_rm,
                                                             const uint32_t* __restrict__ rows,
                                                             const Job* __restrict__ job, int64_t n, int fb0, int nf,
                                                             int64_t nchunks, const uint32_t* __restrict__ counts,
+                                                            const uint32_t* __restrict__ bstart,
                                                             const float* __restrict__ G, const float* __restrict__ H,
-                                                            float2* __restrict__ sorted, int64_t sort_ld) {
+                                                            float2* __restrict__ sorted, int64_t sort_ld,
+                                                            const int32_t* __restrict__ dbin,
+                                                            float2* __restrict__ expl) {
     __shared__ uint32_t s_pos[SF][NB];
     const Seg sg = seg_of(job, n);
     const int64_t chunk = blockIdx.x;
@@ -374,6 +384,15 @@ __global__ void __launch_bounds__(SF * WAVE) k_hist_scatter(const uint8_t* __res
     __builtin_amdgcn_wave_barrier();
     const int64_t c1 = min(sg.m, c0 + CH);
     float2* out = sorted + (size_t)fi * sort_ld;
+    // sparse: rows of earlier chunks outside the default bin = c0 minus the
+    // default-bin rows of earlier chunks (cnt[df] - bstart[df])
+    const uint32_t df = dbin ? (uint32_t)dbin[f] : (uint32_t)NB;
+    uint32_t nd = 0;
+    float2* xout = nullptr;
+    if (dbin) {
+        nd = (uint32_t)c0 - (cnt[df] - bstart[(size_t)f * (NB + 1) + df]);
+        xout = expl + (size_t)fi * sort_ld;
+    }
     for (int64_t g0 = c0; g0 < c1; g0 += WAVE) {
         const int64_t x = g0 + lane;
         const bool v = x < c1;
@@ -395,26 +414,94 @@ __global__ void __launch_bounds__(SF * WAVE) k_hist_scatter(const uint8_t* __res
         if (v) {
             const uint32_t rk = lane_prefix(peers);
             const uint32_t base = s_pos[w][bin];
-            out[base + rk] = make_float2(gv, hv);
+            if (bin != df) out[base + rk] = make_float2(gv, hv);
             __builtin_amdgcn_wave_barrier();
             if (rk == 0) s_pos[w][bin] = base + (uint32_t)__popcll(peers);
+        }
+        if (xout) {
+            const bool x_on = v && bin != df;
+            const uint64_t xb = __ballot(x_on);
+            if (x_on) xout[nd + lane_prefix(xb)] = make_float2(gv, hv);
+            nd += (uint32_t)__popcll(xb);
         }
         __builtin_amdgcn_wave_barrier();
     }
 }
 
+// Sequential double sums, in order, of the pairs at(k), k in [lo, hi): the
+// sparse builder's `+=` of fp32 values into double accumulators
+// (grow.c:85-97).  Loads run one batch of CB ahead of the dependent adds.
+template <class At>
+__device__ __forceinline__ void chain_f64(const At& at, int64_t lo, int64_t hi, double& ag, double& ah) {
+    constexpr int64_t CB = 16;
+    int64_t k = lo;
+    if (k + CB <= hi) {
+        float2 cur[CB];
+#pragma unroll
+        for (int64_t j = 0; j < CB; ++j) cur[j] = at(k + j);
+        k += CB;
+        for (; k + CB <= hi; k += CB) {
+            float2 nxt[CB];
+#pragma unroll
+            for (int64_t j = 0; j < CB; ++j) nxt[j] = at(k + j);
+#pragma unroll
+            for (int64_t j = 0; j < CB; ++j) {
+                ag += (double)cur[j].x;
+                ah += (double)cur[j].y;
+            }
+#pragma unroll
+            for (int64_t j = 0; j < CB; ++j) cur[j] = nxt[j];
+        }
+#pragma unroll
+        for (int64_t j = 0; j < CB; ++j) {
+            ag += (double)cur[j].x;
+            ah += (double)cur[j].y;
+        }
+    }
+    for (; k < hi; ++k) {
+        const float2 a = at(k);
+        ag += (double)a.x;
+        ah += (double)a.y;
+    }
+}
+
 // One thread per (feature, bin): the bin's pairs added in row order in fp32;
 // the count chain adds 1.0f per row (grow.c:55-60).
+// Sparse builder (dbin non-null, grow.c:68-107): the thread of a feature's
+// default bin instead sums the feature's explicit pairs (expl, row order) in
+// double into eout[f]; with tot non-null one more thread sums the node's
+// g and h (Gt, Ht, row order) in double into tot.  k_hist_default then fills
+// the default bin's cell.
 __global__ void __launch_bounds__(RB) k_hist_chain(const float2* __restrict__ sorted, int64_t sort_ld,
                                                    const uint32_t* __restrict__ bstart, int fb0, int nf, int F,
                                                    float* __restrict__ hist_base, size_t hsz,
-                                                   const Job* __restrict__ job, int slot_l, int slot_r) {
+                                                   const Job* __restrict__ job, int slot_l, int slot_r,
+                                                   const int32_t* __restrict__ dbin, const float2* __restrict__ expl,
+                                                   double* __restrict__ eout, const float* __restrict__ Gt,
+                                                   const float* __restrict__ Ht, double* __restrict__ tot, int64_t n) {
     const int t = blockIdx.x * RB + threadIdx.x;
+    if (tot && t == nf * NB) {
+        const Seg sg = seg_of(job, n);
+        double ag = 0.0, ah = 0.0;
+        chain_f64([&](int64_t k) { return make_float2(Gt[k], Ht[k]); }, 0, sg.m, ag, ah);
+        tot[0] = ag;
+        tot[1] = ah;
+        return;
+    }
     if (t >= nf * NB) return;
     const int slot = (!job || job->build_left) ? slot_l : slot_r;
     float* hist = hist_base + (size_t)slot * hsz;
     const int fi = t / NB, b = t % NB, f = fb0 + fi;
     const uint32_t lo = bstart[(size_t)f * (NB + 1) + b], hi = bstart[(size_t)f * (NB + 1) + b + 1];
+    if (dbin && b == dbin[f]) {
+        const uint32_t n_expl = bstart[(size_t)f * (NB + 1) + NB] - (hi - lo);
+        const float2* src = expl + (size_t)fi * sort_ld;
+        double ag = 0.0, ah = 0.0;
+        chain_f64([&](int64_t k) { return src[k]; }, 0, n_expl, ag, ah);
+        eout[2 * (size_t)f] = ag;
+        eout[2 * (size_t)f + 1] = ah;
+        return;
+    }
     const float2* src = sorted + (size_t)fi * sort_ld;
     float ag = 0.0f, ah = 0.0f, ac = 0.0f;
     uint32_t k = lo;
@@ -453,6 +540,25 @@ __global__ void __launch_bounds__(RB) k_hist_chain(const float2* __restrict__ so
     hist[(size_t)0 * F * NB + (size_t)f * NB + b] = ag;
     hist[(size_t)1 * F * NB + (size_t)f * NB + b] = ah;
     hist[(size_t)2 * F * NB + (size_t)f * NB + b] = ac;
+}
+
+// Sparse builder's default-bin cells (grow.c:101-106): 0 + (float)(node sum -
+// explicit sum) for g and h, 0 + (float)(rows in the default bin) for the count.
+__global__ void __launch_bounds__(RB) k_hist_default(const int32_t* __restrict__ dbin,
+                                                     const uint32_t* __restrict__ bstart,
+                                                     const double* __restrict__ eout, const double* __restrict__ tot,
+                                                     int F, float* __restrict__ hist_base, size_t hsz,
+                                                     const Job* __restrict__ job, int slot_l, int slot_r) {
+    const int f = blockIdx.x * RB + threadIdx.x;
+    if (f >= F) return;
+    const int slot = (!job || job->build_left) ? slot_l : slot_r;
+    float* hist = hist_base + (size_t)slot * hsz;
+    const int df = dbin[f];
+    const uint32_t cnt = bstart[(size_t)f * (NB + 1) + df + 1] - bstart[(size_t)f * (NB + 1) + df];
+    const size_t at = (size_t)f * NB + df;
+    hist[(size_t)0 * F * NB + at] = 0.0f + (float)(tot[0] - eout[2 * (size_t)f]);
+    hist[(size_t)1 * F * NB + at] = 0.0f + (float)(tot[1] - eout[2 * (size_t)f + 1]);
+    hist[(size_t)2 * F * NB + at] = 0.0f + (float)(double)cnt;
 }
 
 // The sibling: hist[other] = hist[parent] - hist[built] (grow.c:361,368).
@@ -649,24 +755,35 @@ struct Grower {
     Ws w;
     size_t hsz;
     int64_t nchunks;
+    const int32_t* dbin;           // sparse builder's default bins, or null
     hipStream_t st;
 
     // Histogram of the job's built child (at most m_max rows) into node slot_l
-    // (left child built) or slot_r; job null: all rows into slot_l.
+    // (left child built) or slot_r; job null: all rows into slot_l.  With
+    // default bins, the sparse builder's arithmetic (grow.c:68-107).
     void hist(const Job* job, int64_t m_max, int slot_l, int slot_r, const float* G, const float* H) {
         const int64_t ch = chunks_of(m_max > 0 ? m_max : 1);
         k_hist_count<<<dim3((unsigned)ch, (unsigned)((F + FT - 1) / FT)), RB, 0, st>>>(bins_rm, ld_rm, w.rows, job, n, F,
                                                                                       nchunks, w.counts);
         k_hist_offsets<<<F, NB, 0, st>>>(w.counts, w.bstart, job, n, nchunks);
-        const int64_t cap = (int64_t)min(F, SORT_FEATS) * (n > 0 ? n : 1);
-        const int per = (int)max((int64_t)1, min((int64_t)F, cap / max(m_max, (int64_t)1)));
+        // sorted holds max(min(F, SORT_FEATS), 2) * n pairs: per features'
+        // buckets, and in sparse mode as many explicit-pair runs after them
+        const int64_t mm = max(m_max, (int64_t)1);
+        const int64_t cap = (int64_t)max(min(F, SORT_FEATS), 2) * (n > 0 ? n : 1);
+        const int per = (int)max((int64_t)1, min((int64_t)F, cap / (dbin ? 2 * mm : mm)));
+        float2* expl = dbin ? w.sorted + (size_t)per * mm : nullptr;
         for (int fb0 = 0; fb0 < F; fb0 += per) {
             const int nf = min(per, F - fb0);
+            const bool tot = dbin && fb0 == 0;
             k_hist_scatter<<<dim3((unsigned)ch, (unsigned)((nf + SF - 1) / SF)), SF * WAVE, 0, st>>>(
-                bins_rm, ld_rm, w.rows, job, n, fb0, nf, nchunks, w.counts, G, H, w.sorted, m_max);
-            k_hist_chain<<<(nf * NB + RB - 1) / RB, RB, 0, st>>>(w.sorted, m_max, w.bstart, fb0, nf, F, w.hist, hsz,
-                                                                job, slot_l, slot_r);
+                bins_rm, ld_rm, w.rows, job, n, fb0, nf, nchunks, w.counts, w.bstart, G, H, w.sorted, mm, dbin, expl);
+            k_hist_chain<<<(nf * NB + (tot ? 1 : 0) + RB - 1) / RB, RB, 0, st>>>(
+                w.sorted, mm, w.bstart, fb0, nf, F, w.hist, hsz, job, slot_l, slot_r, dbin, expl, w.expl, G, H,
+                tot ? w.tot : nullptr, n);
         }
+        if (dbin)
+            k_hist_default<<<(F + RB - 1) / RB, RB, 0, st>>>(dbin, w.bstart, w.expl, w.tot, F, w.hist, hsz, job,
+                                                             slot_l, slot_r);
     }
 };
 
@@ -685,8 +802,9 @@ size_t yabt_grow_ref_workspace_bytes(int64_t n, int F, int max_leaves) {
 
 int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm, const float* grad,
                   const float* hess, const uint8_t* fmask, const float* imat, float ib, int use_imat,
-                  const int32_t* nbins, int64_t n, int F, float lam, float gamma, float mcw, int msl, float lr,
-                  int max_leaves, int max_depth, void* workspace, size_t workspace_bytes, int64_t* out_feature,
+                  const int32_t* nbins, const int32_t* default_bin, int64_t n, int F, float lam, float gamma,
+                  float mcw, int msl, float lr, int max_leaves, int max_depth, void* workspace,
+                  size_t workspace_bytes, int64_t* out_feature,
                   int64_t* out_thr_bin, int64_t* out_left, int64_t* out_right, float* out_value, int64_t* out_depth,
                   int64_t* out_leaf_of_row, int64_t* out_rows, int32_t* out_n_nodes, hipStream_t stream) {
     if (n < 0 || n > 0xFFFFFFFFll || F < 1 || max_leaves < 1 || max_leaves > 32767)
@@ -698,6 +816,14 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
         return fail(-2, "yabt_grow_ref: bins layout (pointer, alignment or leading dimension) invalid");
     const size_t need = carve(nullptr, n, F, max_leaves).bytes;
     if (workspace_bytes < need) return fail(-2, "yabt_grow_ref: workspace too small");
+    if (default_bin) {   // the kernels index bin tables with it: check it first
+        std::vector<int32_t> db(F);
+        hipError_t e = hipMemcpyAsync(db.data(), default_bin, (size_t)F * sizeof(int32_t), hipMemcpyDeviceToHost, stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(stream);
+        if (e != hipSuccess) return hip_fail(e, "yabt_grow_ref: default_bin copy");
+        for (int f = 0; f < F; ++f)
+            if (db[f] < 0 || db[f] >= NB) return fail(-2, "yabt_grow_ref: default_bin entries must be in [0, 255]");
+    }
 
     Grower g;
     g.bins_fm = bins_fm;
@@ -711,6 +837,7 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
     g.w = carve((char*)workspace, n, F, max_leaves);
     g.hsz = (size_t)3 * F * NB;
     g.nchunks = chunks_of(n > 0 ? n : 1);
+    g.dbin = default_bin;
     g.st = stream;
     const Ws& w = g.w;
     const int N = 2 * max_leaves + 1;

@@ -8,8 +8,10 @@ same ``Tree``; it grows the tree on the GPU through ``yabt_grow``
   so results are deterministic and sibling subtraction is exact; the split
   (feature, bin) sequence and leaf membership match the reference grower
   except where the reference's fp32 rounding decides a tie;
-* ``sparse_layout`` is accepted and ignored: with exact sums the sparse
-  builder (grow.c:68-107) and the dense one give identical histograms;
+* ``sparse_layout``: with exact sums the sparse builder (grow.c:68-107) and
+  the dense one give identical histograms, so "exact" ignores it;
+  "reference" follows it (cgrow's sparse arithmetic on the layout's default
+  bins, which must describe ``binned`` as ``build_sparse_layout`` makes it);
 * ``n_threads`` is accepted and ignored (no host threads);
 * inputs on the CPU are copied to the current HIP device once per binned
   matrix (cached); the returned Tree lives on ``binned.device`` as in the
@@ -34,7 +36,9 @@ from .tree import LEAF, Tree, TreeParams
 MAX_BINS = 256
 
 _CACHE_LOCK = threading.Lock()
-_LAYOUTS: "weakref.WeakKeyDictionary[torch.Tensor, tuple]" = weakref.WeakKeyDictionary()
+# id(binned) -> (state, layouts); an entry is dropped when its tensor dies (a
+# WeakKeyDictionary would compare tensor keys with ==, which is elementwise)
+_LAYOUTS: dict[int, tuple] = {}
 _WORKSPACES: dict = {}
 
 
@@ -123,13 +127,17 @@ def layouts_for(binned: torch.Tensor, dev: torch.device,
     """Cached per binned tensor (keyed by object, checked against its version),
     mirroring the reference's cached feature-major copy (boosting.py:454-459)."""
     key_state = (binned._version, binned.data_ptr(), tuple(binned.shape), dev)
+    key = id(binned)
     with _CACHE_LOCK:
-        hit = _LAYOUTS.get(binned)
+        hit = _LAYOUTS.get(key)
         if hit is not None and hit[0] == key_state:
             return hit[1]
     lay = make_layouts(binned, dev, binned_fmajor)
     with _CACHE_LOCK:
-        _LAYOUTS[binned] = (key_state, lay)
+        if key not in _LAYOUTS:
+            # runs when binned dies, before its id can be reused
+            weakref.finalize(binned, _LAYOUTS.pop, key, None)
+        _LAYOUTS[key] = (key_state, lay)
     return lay
 
 
@@ -181,13 +189,19 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
     max_leaves >= 2^max_depth (the leaf budget cannot bind); None uses it
     whenever that holds.
 
-    ``default_bin`` ("exact", not batched): "auto" uses the layouts' most
-    frequent bin per feature, None disables the skip, or an (F,) int array."""
+    ``default_bin``: with "exact" (not batched) a shortcut that leaves the
+    sums unchanged -- "auto" uses the layouts' most frequent bin per feature,
+    None disables the skip, or an (F,) int array.  With "reference" it picks
+    cgrow's histogram builder: an (F,) array of default bins in [0, 255] is
+    the sparse builder (grow.c:68-107) over those bins; "auto" or None is the
+    dense builder."""
     if arithmetic not in ARITHMETICS:
         raise ValueError(f"arithmetic must be one of {ARITHMETICS}")
     if arithmetic == "reference":
+        db = None if default_bin is None or isinstance(default_bin, str) else default_bin
         return _grow_device_ref(lay, grad, hess, nbins, fmask=fmask, imat=imat, ib=ib, lam=lam, gamma=gamma,
-                                mcw=mcw, msl=msl, lr=lr, max_leaves=max_leaves, max_depth=max_depth)
+                                mcw=mcw, msl=msl, lr=lr, max_leaves=max_leaves, max_depth=max_depth,
+                                default_bin=db)
     can_batch = 0 <= int(max_depth) <= 16 and int(max_leaves) >= (1 << int(max_depth)) and int(max_leaves) <= 65535
     if batched is None:
         batched = can_batch and lay.n < 2 ** 31
@@ -297,8 +311,9 @@ def _grow_device_level(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, l
 
 
 def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam, gamma, mcw, msl, lr,
-                     max_leaves, max_depth) -> GrowResult:
-    """yabt_grow_ref: cgrow's arithmetic on the device (synchronous)."""
+                     max_leaves, max_depth, default_bin=None) -> GrowResult:
+    """yabt_grow_ref: cgrow's arithmetic on the device (synchronous);
+    default_bin selects cgrow's sparse builder."""
     lib = _lib.load()
     dev = lay.fm.device
     n, F = lay.n, lay.F
@@ -314,6 +329,11 @@ def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam
     if use_imat and tuple(im.shape) != (F, F):
         raise ValueError("interaction_matrix must be (F, F)")
     nb = torch.from_numpy(np.ascontiguousarray(nbins, dtype=np.int32)).to(dev)
+    db = None
+    if default_bin is not None:
+        db = torch.as_tensor(default_bin).to(dev, torch.int32).contiguous()
+        if tuple(db.shape) != (F,):
+            raise ValueError("default_bin must have one entry per feature")
     L = int(max_leaves)
     N = 2 * L + 1
     nbytes = int(lib.yabt_grow_ref_workspace_bytes(n, F, L))
@@ -331,7 +351,7 @@ def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam
     nn = torch.zeros(1, dtype=torch.int32, device=dev)
     rc = lib.yabt_grow_ref(
         _ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h), _ptr(fm), _ptr(im),
-        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), n, F,
+        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), _ptr(db), n, F,
         ctypes.c_float(float(lam)), ctypes.c_float(float(gamma)), ctypes.c_float(float(mcw)),
         int(msl), ctypes.c_float(float(lr)), L, int(max_depth), _ptr(ws), ws.numel(),
         _ptr(out_i[0]), _ptr(out_i[1]), _ptr(out_i[2]), _ptr(out_i[3]), _ptr(value), _ptr(out_i[4]),
@@ -391,17 +411,25 @@ def grow_tree_hip(
     arithmetic: str = "exact",
 ) -> Tree:
     """Drop-in for ``grow_tree_c`` (yabt/grow_c.py:336-452) on a HIP device;
-    ``arithmetic`` as in ``grow_device`` ("reference": cgrow's trees bit for bit)."""
-    del sparse_layout, n_threads  # see module docstring
+    ``arithmetic`` as in ``grow_device`` ("reference": cgrow's trees bit for
+    bit, with cgrow's sparse builder when ``sparse_layout`` is given,
+    grow_c.py:382-393)."""
+    del n_threads  # see module docstring
     out_dev = binned.device
     dev = binned.device if binned.device.type == "cuda" else _device()
     n, F = binned.shape
     lay = layouts_for(binned, dev, binned_fmajor)
+    db = "auto"
+    if sparse_layout is not None and arithmetic == "reference":
+        db = np.ascontiguousarray(sparse_layout[3], dtype=np.int64)
+        if db.shape != (F,) or db.min(initial=0) < 0 or db.max(initial=0) >= MAX_BINS:
+            raise ValueError("sparse_layout's default bins must be (F,) in [0, 255]")
     res = grow_device(lay, grad, hess, nbins_of(binner, F), fmask=feature_mask,
                       imat=interaction_matrix, ib=interaction_boost, lam=params.reg_lambda,
                       gamma=params.gamma, mcw=params.min_child_weight,
                       msl=params.min_samples_leaf, lr=params.learning_rate,
-                      max_leaves=params.max_leaves, max_depth=params.max_depth, arithmetic=arithmetic)
+                      max_leaves=params.max_leaves, max_depth=params.max_depth, default_bin=db,
+                      arithmetic=arithmetic)
     return tree_from_result(res, binner, F, out_dev)
 
 
