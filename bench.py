@@ -219,7 +219,9 @@ def depthwise_trees(torch, trees: int = 10) -> dict:
     with probability 0.9 else uniform on 1..255, g ~ Laplace(0, 1), h = 1,
     max_depth 6, 64 leaves, min_samples_leaf 20, with the margin update of a
     squared loss (y = -g0, margin0 = 0) between trees; grown depth by depth
-    (the leaf budget cannot bind) and, for comparison, split by split."""
+    (the leaf budget cannot bind) and, for comparison, split by split; and
+    in the reference arithmetic with cgrow's sparse builder (default bin 0),
+    the builder the reference picks for data this sparse."""
     from yabt_amd import grow_hip as G
     from yabt_amd import boost_ops
     from yabt_amd.losses import MSELoss
@@ -237,22 +239,23 @@ def depthwise_trees(torch, trees: int = 10) -> dict:
     nbins = np.full(F, 256, np.int32)
     P = dict(lam=1.0, gamma=0.0, mcw=1e-3, msl=20, lr=0.1, max_leaves=64, max_depth=6)
     out = {}
-    for batched in (True, False):
+    modes = [("batched", dict(batched=True), trees), ("sequential", dict(batched=False), trees),
+             ("reference_sparse", dict(arithmetic="reference", default_bin=np.zeros(F, np.int32)), min(trees, 3))]
+    for name, kw, k_trees in modes:
         margin = torch.zeros(n, device=dev)
         def tree_step():
             g, h = boost_ops.grad_hess(MSELoss(), margin, y)
-            res = G.grow_device(lay, g, h, nbins, batched=batched, **P)
+            res = G.grow_device(lay, g, h, nbins, **kw, **P)
             leaf = G.leaf_ids(res, n, F, P["max_leaves"])
             boost_ops.margin_update(margin, leaf, Tree(res.feature, res.thr_bin.float(), res.left, res.right,
                                                        res.value, 0), None)
         tree_step()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(trees):
+        for _ in range(k_trees):
             tree_step()
         torch.cuda.synchronize()
-        key = "depth6_4Mx500_skewed_ms_per_tree_" + ("batched" if batched else "sequential")
-        out[key] = round((time.perf_counter() - t0) * 1e3 / trees, 2)
+        out["depth6_4Mx500_skewed_ms_per_tree_" + name] = round((time.perf_counter() - t0) * 1e3 / k_trees, 2)
     del lay
     torch.cuda.empty_cache()
     return out

@@ -56,7 +56,7 @@ SIGNATURES = {
     "yabt_grow_levelwise": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _i64, _int,
                                    _flt, _flt, _flt, _int, _flt, _int, _int, _vp, _sz,
                                    _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
-    "yabt_grow_ref_workspace_bytes": (_sz, [_i64, _int, _int]),
+    "yabt_grow_ref_workspace_bytes": (_sz, [_i64, _int, _int, _int]),
     "yabt_grow_ref": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _vp, _i64, _int,
                              _flt, _flt, _flt, _int, _flt, _int, _int, _vp, _sz,
                              _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),

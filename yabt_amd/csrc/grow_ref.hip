@@ -5,9 +5,10 @@
 // except where cgrow's own fp32 rounding decides a split.  This grower
 // reproduces cgrow's arithmetic instead:
 //   * a node histogram is the fp32 sum, per (feature, bin), of the node's rows
-//     in the order cgrow's rows[] array holds them (grow.c:37-62): the node's
-//     rows are bucketed by bin with a stable counting sort, and one thread adds
-//     each (feature, bin) chain in order;
+//     in the order cgrow's rows[] array holds them (grow.c:37-62): one block
+//     per feature streams the node's rows in that order, buckets each tile by
+//     bin with a stable counting sort in LDS, and one thread per bin keeps the
+//     bin's running sums (the sparse builder, grow.c:68-107, likewise);
 //   * rows[] follows cgrow's in-place two-pointer partition (grow.c:201-217),
 //     which is a fixed permutation of the node's rows, computed in parallel
 //     (see "partition" below);
@@ -32,8 +33,7 @@
 //
 // Workspace (yabt_grow_ref_workspace_bytes): rows and a copy (n u32), the
 // partition's flags / ranks / p / q arrays, the built child's g and h in row
-// order, per-chunk bin counts (F, n/CH, 256), the bucketed (g, h) pairs of up
-// to SORT_FEATS features, and one (3, F, 256) fp32 histogram per node.
+// order, and one (3, F, 256) fp32 histogram per node.
 
 #include "common.h"
 #include "host.h"
@@ -49,10 +49,8 @@ namespace ref {
 
 constexpr int RB = 256;            // threads per block
 constexpr int PT = 2048;           // partition rows per block
-constexpr int CH = 4096;           // rows per counting-sort chunk
-constexpr int FT = 16;             // features per counting block (one 16-byte row load)
-constexpr int SF = 4;              // features per scatter block (one wave each)
-constexpr int SORT_FEATS = 16;     // bucketed features per pass at the root
+constexpr int WT = 4096;           // histogram rows per tile
+constexpr int ST = NB + 1;         // bucket starts per (feature, tile)
 
 struct Job {
     int64_t s, e;                  // parent segment
@@ -86,10 +84,11 @@ struct Ws {
     uint32_t* blk;                 // per-block left counts, then their exclusive prefix
     float* G;
     float* H;
-    uint32_t* counts;              // (F, chunks, 256)
-    uint32_t* bstart;              // (F, 257)
-    float2* sorted;                // (max(min(F, SORT_FEATS), 2), n)
-    double* expl;                  // (F, 2): sparse builder's explicit g, h sums
+    uint16_t* perm;                // (F, ld_perm): per tile, positions bucketed by bin
+    uint16_t* xperm;               // (F, ld_perm): sparse builder, per tile, rows outside the default bin
+    uint16_t* starts;              // (F, n_tiles, 257): per tile, bucket starts
+    int64_t n_tiles, ld_perm;
+    double* expl;                  // (F, 3): sparse builder's explicit g, h sums, default-bin rows
     double* tot;                   // (2): sparse builder's node g, h sums
     float* hist;                   // (N, 3, F, 256)
     double* fsel;                  // (2, F)
@@ -102,13 +101,13 @@ struct Ws {
     size_t bytes;
 };
 
-inline int64_t chunks_of(int64_t n) { return (n + CH - 1) / CH; }
-
-Ws carve(char* base, int64_t n, int F, int max_leaves) {
+Ws carve(char* base, int64_t n, int F, int max_leaves, bool sparse) {
     Carve c{base, 0};
     Ws w;
     const int64_t N = 2 * (int64_t)max_leaves + 1;
     const int64_t nn = n > 0 ? n : 1;
+    w.n_tiles = (nn + WT - 1) / WT;
+    w.ld_perm = w.n_tiles * WT;
     w.rows = c.take<uint32_t>(nn);
     w.rows_tmp = c.take<uint32_t>(nn);
     w.flag = c.take<uint8_t>(nn);
@@ -118,10 +117,10 @@ Ws carve(char* base, int64_t n, int F, int max_leaves) {
     w.blk = c.take<uint32_t>((nn + PT - 1) / PT + 1);
     w.G = c.take<float>(nn);
     w.H = c.take<float>(nn);
-    w.counts = c.take<uint32_t>((size_t)F * chunks_of(nn) * NB);
-    w.bstart = c.take<uint32_t>((size_t)F * (NB + 1));
-    w.sorted = c.take<float2>((size_t)max(min(F, SORT_FEATS), 2) * nn);
-    w.expl = c.take<double>(2 * (size_t)F);
+    w.perm = c.take<uint16_t>((size_t)F * (size_t)w.ld_perm);
+    w.xperm = sparse ? c.take<uint16_t>((size_t)F * (size_t)w.ld_perm) : nullptr;
+    w.starts = c.take<uint16_t>((size_t)F * (size_t)w.n_tiles * ST);
+    w.expl = c.take<double>(3 * (size_t)F);
     w.tot = c.take<double>(2);
     w.hist = c.take<float>((size_t)N * 3 * F * NB);
     w.fsel = c.take<double>(2 * (size_t)F);
@@ -291,10 +290,22 @@ __global__ void __launch_bounds__(RB) k_part_commit(uint32_t* __restrict__ rows,
 }
 
 // ---------------------------------------------------------------------------
-// histogram: stable bucketing by bin, then one sequential chain per (f, b)
+// histogram: cgrow's row-order fp32 chains, bucketed per tile
 // ---------------------------------------------------------------------------
+//
+// cgrow adds each row into its (feature, bin) cell in fp32, in rows[] order
+// (grow.c:37-62).  The node's rows are cut into tiles of WT rows in that
+// order.  k_walk_sort buckets every (feature, tile) by bin, stably, in
+// parallel over the whole device; k_walk_chain then runs one block per
+// feature over the tiles in order, thread b adding bin b's run of each tile
+// to its fp32 accumulators, so every cell is cgrow's sequential sum.
+//
+// Sparse builder (grow.c:68-107, default bins dbin): the default bin gets no
+// run; its thread instead adds, in double and in row order, the tile's rows
+// outside the default bin; block F adds the node's g and h in double in row
+// order; k_hist_default combines them.
 
-// Segment [cs, ce): the job's built child, or [0, n) for the root (job null).
+// Segment [cs, cs + m): the job's built child, or [0, n) for the root (job null).
 struct Seg {
     int64_t cs, m;
 };
@@ -304,248 +315,307 @@ __device__ __forceinline__ Seg seg_of(const Job* job, int64_t n) {
     return Seg{job->cs, job->ce - job->cs};
 }
 
-// counts[f][chunk][b] = rows of the chunk in bin b of feature f.
-__global__ void __launch_bounds__(RB) k_hist_count(const uint8_t* __restrict__ bins_rm, int64_t ld_rm,
-                                                   const uint32_t* __restrict__ rows, const Job* __restrict__ job,
-                                                   int64_t n, int F, int64_t nchunks, uint32_t* __restrict__ counts) {
-    __shared__ uint32_t s_c[FT][NB];
-    const Seg sg = seg_of(job, n);
-    const int64_t chunk = blockIdx.x;
-    const int f0 = blockIdx.y * FT;
-    const int64_t c0 = chunk * CH;
-    if (c0 >= sg.m) return;
-    for (int i = threadIdx.x; i < FT * NB; i += RB) (&s_c[0][0])[i] = 0;
-    __syncthreads();
-    const int64_t c1 = min(sg.m, c0 + CH);
-    for (int64_t x = c0 + threadIdx.x; x < c1; x += RB) {
-        const uint32_t r = rows[sg.cs + x];
-        const uint4 v = *reinterpret_cast<const uint4*>(bins_rm + (size_t)r * (size_t)ld_rm + f0);
-        const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int j = 0; j < FT; ++j)
-            if (f0 + j < F) atomicAdd(&s_c[j][(w4[j >> 2] >> (8 * (j & 3))) & 0xff], 1u);
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < FT * NB; i += RB) {
-        const int j = i / NB, bb = i % NB;
-        if (f0 + j < F) counts[((size_t)(f0 + j) * nchunks + chunk) * NB + bb] = s_c[j][bb];
-    }
+constexpr int SW = RB / WAVE;             // waves per sort / chain block
+constexpr int SSUB = WT / SW;             // rows per wave per tile (sort)
+constexpr int SGR = SSUB / WAVE;          // 64-row groups per wave per tile (sort)
+constexpr int TPT = WT / RB;              // rows per thread per tile
+
+// Bin of the node's row at position x: row x for the root (rows[] is the
+// identity there, grow.c:289), rows[cs + x] for a built child.
+template <bool ROOT>
+__device__ __forceinline__ uint32_t node_bin(const uint8_t* __restrict__ bins_fm, int64_t ld_fm,
+                                            const uint8_t* __restrict__ bins_rm, int64_t ld_rm,
+                                            const uint32_t* __restrict__ rows, int64_t cs, int f, int64_t x) {
+    if (ROOT) return bins_fm[(size_t)f * (size_t)ld_fm + (size_t)x];
+    return bins_rm[(size_t)rows[cs + x] * (size_t)ld_rm + f];
 }
 
-// Per feature: counts -> global bucket positions (bin start + earlier chunks),
-// bstart[f][b] = first position of bin b, bstart[f][256] = m.
-__global__ void __launch_bounds__(NB) k_hist_offsets(uint32_t* __restrict__ counts, uint32_t* __restrict__ bstart,
-                                                     const Job* __restrict__ job, int64_t n, int64_t nchunks) {
-    __shared__ uint32_t s_w[NB / WAVE];
+// Stable bucketing of one tile of one feature (block (f, t)): perm[f][t*WT +
+// k] lists the tile's positions bin by bin, each bin in row order, and
+// starts[f][t][b] is where bin b's run begins (starts[...][256] = the run
+// total).  The lanes of a wave sharing a bin are found by an LDS atomic OR of
+// each lane's bit into s_peer[w][bin] (order-free), read back and cleared; a
+// row's rank is the number of those lanes below it plus the wave's running
+// count s_cnt[w][bin].  Sparse builder (dbin): the default bin gets no run,
+// and xperm lists the tile's other positions in row order.
+template <bool ROOT, bool SPARSE>
+__global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bins_fm, int64_t ld_fm,
+                                                  const uint8_t* __restrict__ bins_rm, int64_t ld_rm,
+                                                  const uint32_t* __restrict__ rows, const Job* __restrict__ job,
+                                                  int64_t n, const int32_t* __restrict__ dbin,
+                                                  uint16_t* __restrict__ perm, uint16_t* __restrict__ xperm,
+                                                  int64_t ld_perm, uint16_t* __restrict__ starts, int64_t n_tiles) {
+    __shared__ uint8_t s_bin[WT];
+    __shared__ uint64_t s_peer[SW][NB];
+    __shared__ uint32_t s_cnt[SW][NB];
+    __shared__ uint16_t s_perm[WT];
+    __shared__ uint16_t s_xperm[SPARSE ? WT : 1];
+    __shared__ uint32_t s_scan[SW];
+    __shared__ uint32_t s_xoff[SW + 1];
     const Seg sg = seg_of(job, n);
-    const int f = blockIdx.x, b = threadIdx.x;
-    const int64_t used = (sg.m + CH - 1) / CH;
-    uint32_t* c = counts + (size_t)f * nchunks * NB + b;
-    uint32_t run = 0;
-    for (int64_t k = 0; k < used; ++k) {
-        const uint32_t v = c[(size_t)k * NB];
-        c[(size_t)k * NB] = run;
-        run += v;
+    const int f = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
+    const int df = SPARSE ? dbin[f] : -1;
+    for (int64_t t = blockIdx.y; t * WT < sg.m; t += gridDim.y) {
+    const int64_t t0 = t * WT;
+    const int tn = (int)min((int64_t)WT, sg.m - t0);
+    for (int i = tid; i < SW * NB; i += RB) {
+        (&s_cnt[0][0])[i] = 0;
+        (&s_peer[0][0])[i] = 0;
     }
-    uint32_t tot;
-    const uint32_t start = block_excl_scan<NB, uint32_t>(run, s_w, &tot);
-    for (int64_t k = 0; k < used; ++k) c[(size_t)k * NB] += start;
-    bstart[(size_t)f * (NB + 1) + b] = start;
-    if (b == NB - 1) bstart[(size_t)f * (NB + 1) + NB] = start + run;
-}
-
-// Bucket the (g, h) pairs of features [fb0, fb0 + nf) by bin, stably: one wave
-// per feature walks the chunk's rows in order, 64 at a time; lanes with equal
-// bins are ranked by lane (eight ballots find the lanes sharing a bin).
-// Sparse builder (dbin non-null): the pairs outside the feature's default bin
-// are also written, in row order, to expl[fi * sort_ld + ...]; the default
-// bin's own pairs are not bucketed (no chain reads them).
-__global__ void __launch_bounds__(SF * WAVE) k_hist_scatter(const uint8_t* __restrict__ bins_rm, int64_t ld_rm,
-                                                            const uint32_t* __restrict__ rows,
-                                                            const Job* __restrict__ job, int64_t n, int fb0, int nf,
-                                                            int64_t nchunks, const uint32_t* __restrict__ counts,
-                                                            const uint32_t* __restrict__ bstart,
-                                                            const float* __restrict__ G, const float* __restrict__ H,
-                                                            float2* __restrict__ sorted, int64_t sort_ld,
-                                                            const int32_t* __restrict__ dbin,
-                                                            float2* __restrict__ expl) {
-    __shared__ uint32_t s_pos[SF][NB];
-    const Seg sg = seg_of(job, n);
-    const int64_t chunk = blockIdx.x;
-    const int w = threadIdx.x / WAVE, lane = threadIdx.x & (WAVE - 1);
-    const int fi = blockIdx.y * SF + w;           // feature index inside the batch
-    const int64_t c0 = chunk * CH;
-    if (c0 >= sg.m || fi >= nf) return;
-    const int f = fb0 + fi;
-    const uint32_t* cnt = counts + ((size_t)f * nchunks + chunk) * NB;
-    for (int bb = lane; bb < NB; bb += WAVE) s_pos[w][bb] = cnt[bb];
-    // s_pos is private to this wave: the wave's own LDS writes are visible to
-    // its later reads without a block barrier
-    __builtin_amdgcn_wave_barrier();
-    const int64_t c1 = min(sg.m, c0 + CH);
-    float2* out = sorted + (size_t)fi * sort_ld;
-    // sparse: rows of earlier chunks outside the default bin = c0 minus the
-    // default-bin rows of earlier chunks (cnt[df] - bstart[df])
-    const uint32_t df = dbin ? (uint32_t)dbin[f] : (uint32_t)NB;
-    uint32_t nd = 0;
-    float2* xout = nullptr;
-    if (dbin) {
-        nd = (uint32_t)c0 - (cnt[df] - bstart[(size_t)f * (NB + 1) + df]);
-        xout = expl + (size_t)fi * sort_ld;
-    }
-    for (int64_t g0 = c0; g0 < c1; g0 += WAVE) {
-        const int64_t x = g0 + lane;
-        const bool v = x < c1;
-        uint32_t bin = 0;
-        float gv = 0.0f, hv = 0.0f;
-        if (v) {
-            const uint32_t r = rows[sg.cs + x];
-            bin = bins_rm[(size_t)r * (size_t)ld_rm + f];
-            gv = G ? G[x] : 0.0f;
-            hv = H ? H[x] : 0.0f;
-        }
-        uint64_t peers = __ballot(v);
 #pragma unroll
-        for (int bit = 0; bit < 8; ++bit) {
-            const bool on = (bin >> bit) & 1u;
-            const uint64_t bal = __ballot(on);
-            peers &= on ? bal : ~bal;
-        }
-        if (v) {
-            const uint32_t rk = lane_prefix(peers);
-            const uint32_t base = s_pos[w][bin];
-            if (bin != df) out[base + rk] = make_float2(gv, hv);
-            __builtin_amdgcn_wave_barrier();
-            if (rk == 0) s_pos[w][bin] = base + (uint32_t)__popcll(peers);
-        }
-        if (xout) {
-            const bool x_on = v && bin != df;
-            const uint64_t xb = __ballot(x_on);
-            if (x_on) xout[nd + lane_prefix(xb)] = make_float2(gv, hv);
-            nd += (uint32_t)__popcll(xb);
-        }
+    for (int j = 0; j < TPT; ++j) {
+        const int x = j * RB + tid;
+        if (x < tn) s_bin[x] = (uint8_t)node_bin<ROOT>(bins_fm, ld_fm, bins_rm, ld_rm, rows, sg.cs, f, t0 + x);
+    }
+    __syncthreads();
+    uint32_t rk[SGR], xr[SGR];
+    uint8_t qb[SGR];
+    uint32_t xrun = 0;
+#pragma unroll
+    for (int q = 0; q < SGR; ++q) {
+        const int x = w * SSUB + q * WAVE + lane;
+        const bool v = x < tn;
+        const uint32_t bin = v ? (uint32_t)s_bin[x] : 0u;
+        qb[q] = (uint8_t)bin;
+        if (v) atomicOr(&s_peer[w][bin], 1ull << lane);
         __builtin_amdgcn_wave_barrier();
+        const uint64_t peers = v ? s_peer[w][bin] : 0ull;
+        const uint32_t base = v ? s_cnt[w][bin] : 0u;
+        __builtin_amdgcn_wave_barrier();
+        const uint32_t r = lane_prefix(peers);
+        if (v) s_peer[w][bin] = 0ull;
+        if (v && r == 0) s_cnt[w][bin] = base + (uint32_t)__popcll(peers);
+        __builtin_amdgcn_wave_barrier();
+        rk[q] = base + r;
+        if (SPARSE) {
+            const uint64_t xb = __ballot(v && (int)bin != df);
+            xr[q] = xrun + lane_prefix(xb);
+            xrun += (uint32_t)__popcll(xb);
+        }
+    }
+    if (SPARSE && lane == 0) s_xoff[w] = xrun;
+    __syncthreads();
+    // bucket starts (sparse: no room for the default bin) and wave bases
+    uint16_t* st_out = starts + ((size_t)f * (size_t)n_tiles + (size_t)t) * ST;
+    {
+        const int b = tid;
+        uint32_t c[SW];
+        uint32_t tb = 0;
+#pragma unroll
+        for (int u = 0; u < SW; ++u) {
+            c[u] = s_cnt[u][b];
+            tb += c[u];
+        }
+        if (SPARSE && b == df) tb = 0;
+        uint32_t total;
+        const uint32_t st = block_excl_scan<RB, uint32_t>(tb, s_scan, &total);
+        st_out[b] = (uint16_t)st;
+        if (b == NB - 1) st_out[NB] = (uint16_t)(st + tb);
+        uint32_t run = st;
+#pragma unroll
+        for (int u = 0; u < SW; ++u) {
+            s_cnt[u][b] = run;
+            run += c[u];
+        }
+        if (SPARSE && tid == 0) {
+            uint32_t o = 0;
+#pragma unroll
+            for (int u = 0; u < SW; ++u) {
+                const uint32_t v = s_xoff[u];
+                s_xoff[u] = o;
+                o += v;
+            }
+            s_xoff[SW] = o;
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < SGR; ++q) {
+        const int x = w * SSUB + q * WAVE + lane;
+        if (x < tn && (!SPARSE || (int)qb[q] != df)) {
+            s_perm[s_cnt[w][qb[q]] + rk[q]] = (uint16_t)x;
+            if (SPARSE) s_xperm[s_xoff[w] + xr[q]] = (uint16_t)x;
+        }
+    }
+    __syncthreads();
+    const int total = SPARSE ? (int)s_xoff[SW] : tn;
+    uint16_t* po = perm + (size_t)f * (size_t)ld_perm + (size_t)t0;
+    for (int k = tid; k < total; k += RB) po[k] = s_perm[k];
+    if (SPARSE) {
+        uint16_t* xo = xperm + (size_t)f * (size_t)ld_perm + (size_t)t0;
+        for (int k = tid; k < total; k += RB) xo[k] = s_xperm[k];
+    }
+    __syncthreads();
     }
 }
 
-// Sequential double sums, in order, of the pairs at(k), k in [lo, hi): the
-// sparse builder's `+=` of fp32 values into double accumulators
-// (grow.c:85-97).  Loads run one batch of CB ahead of the dependent adds.
-template <class At>
-__device__ __forceinline__ void chain_f64(const At& at, int64_t lo, int64_t hi, double& ag, double& ah) {
-    constexpr int64_t CB = 16;
-    int64_t k = lo;
-    if (k + CB <= hi) {
-        float2 cur[CB];
+// Sequential fp32 sums of the pairs s_gh[idx[k]], k in [lo, hi).
+__device__ __forceinline__ void run_f32(const float2* s_gh, const uint16_t* idx, uint32_t lo, uint32_t hi,
+                                        float& ag, float& ah) {
+    uint32_t k = lo;
+    for (; k + 8 <= hi; k += 8) {
+        uint32_t i[8];
 #pragma unroll
-        for (int64_t j = 0; j < CB; ++j) cur[j] = at(k + j);
-        k += CB;
-        for (; k + CB <= hi; k += CB) {
-            float2 nxt[CB];
+        for (int j = 0; j < 8; ++j) i[j] = idx[k + j];
+        float2 p[8];
 #pragma unroll
-            for (int64_t j = 0; j < CB; ++j) nxt[j] = at(k + j);
+        for (int j = 0; j < 8; ++j) p[j] = s_gh[i[j]];
 #pragma unroll
-            for (int64_t j = 0; j < CB; ++j) {
-                ag += (double)cur[j].x;
-                ah += (double)cur[j].y;
-            }
-#pragma unroll
-            for (int64_t j = 0; j < CB; ++j) cur[j] = nxt[j];
-        }
-#pragma unroll
-        for (int64_t j = 0; j < CB; ++j) {
-            ag += (double)cur[j].x;
-            ah += (double)cur[j].y;
+        for (int j = 0; j < 8; ++j) {
+            ag += p[j].x;
+            ah += p[j].y;
         }
     }
     for (; k < hi; ++k) {
-        const float2 a = at(k);
-        ag += (double)a.x;
-        ah += (double)a.y;
+        const float2 p = s_gh[idx[k]];
+        ag += p.x;
+        ah += p.y;
     }
 }
 
-// One thread per (feature, bin): the bin's pairs added in row order in fp32;
-// the count chain adds 1.0f per row (grow.c:55-60).
-// Sparse builder (dbin non-null, grow.c:68-107): the thread of a feature's
-// default bin instead sums the feature's explicit pairs (expl, row order) in
-// double into eout[f]; with tot non-null one more thread sums the node's
-// g and h (Gt, Ht, row order) in double into tot.  k_hist_default then fills
-// the default bin's cell.
-__global__ void __launch_bounds__(RB) k_hist_chain(const float2* __restrict__ sorted, int64_t sort_ld,
-                                                   const uint32_t* __restrict__ bstart, int fb0, int nf, int F,
-                                                   float* __restrict__ hist_base, size_t hsz,
-                                                   const Job* __restrict__ job, int slot_l, int slot_r,
-                                                   const int32_t* __restrict__ dbin, const float2* __restrict__ expl,
-                                                   double* __restrict__ eout, const float* __restrict__ Gt,
-                                                   const float* __restrict__ Ht, double* __restrict__ tot, int64_t n) {
-    const int t = blockIdx.x * RB + threadIdx.x;
-    if (tot && t == nf * NB) {
-        const Seg sg = seg_of(job, n);
-        double ag = 0.0, ah = 0.0;
-        chain_f64([&](int64_t k) { return make_float2(Gt[k], Ht[k]); }, 0, sg.m, ag, ah);
-        tot[0] = ag;
-        tot[1] = ah;
+// Sequential double sums of the fp32 pairs s_gh[idx[k]] (idx null: s_gh[k]),
+// k in [0, hi).
+__device__ __forceinline__ void run_f64(const float2* s_gh, const uint16_t* idx, uint32_t hi, double& ag,
+                                        double& ah) {
+    uint32_t k = 0;
+    for (; k + 8 <= hi; k += 8) {
+        float2 p[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p[j] = s_gh[idx ? (uint32_t)idx[k + j] : k + j];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            ag += (double)p[j].x;
+            ah += (double)p[j].y;
+        }
+    }
+    for (; k < hi; ++k) {
+        const float2 p = s_gh[idx ? (uint32_t)idx[k] : k];
+        ag += (double)p.x;
+        ah += (double)p.y;
+    }
+}
+
+// One tile of a chain block, TPT entries per thread, loaded a tile ahead.
+struct ChainTile {
+    float g[TPT], h[TPT];
+    uint32_t idx[TPT], xidx[TPT];
+    uint32_t st, st_end;
+};
+
+template <bool SPARSE>
+__device__ __forceinline__ void chain_load(ChainTile& c, const float* __restrict__ G, const float* __restrict__ H,
+                                           const uint16_t* __restrict__ pf, const uint16_t* __restrict__ xf,
+                                           const uint16_t* __restrict__ sf, bool totals, int64_t t, int64_t m) {
+    const int64_t t0 = t * WT;
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+        const int64_t x = t0 + j * RB + threadIdx.x;
+        if (x < m) {
+            c.g[j] = G[x];
+            c.h[j] = H[x];
+            if (!totals) {
+                c.idx[j] = pf[x];
+                if (SPARSE) c.xidx[j] = xf[x];
+            }
+        }
+    }
+    if (!totals) {
+        c.st = sf[(size_t)t * ST + threadIdx.x];
+        if (threadIdx.x == 0) c.st_end = sf[(size_t)t * ST + NB];
+    }
+}
+
+// The chains (block f, thread b = bin): the node's tiles in order, each
+// tile's g, h and bucketed positions staged in LDS, bin b's run added in fp32
+// in row order (grow.c:55-59); the count cell is cgrow's chain of 1.0f adds,
+// which is min(count, 2^24) exactly.  Sparse builder: the default bin's
+// thread adds the tile's other rows in double in row order (xperm), and
+// block F adds the node's g and h in double in row order (grow.c:85-97);
+// k_hist_default combines them.  G, H hold the node's g, h by position.
+template <bool SPARSE>
+__global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ G, const float* __restrict__ H,
+                                                   const Job* __restrict__ job, int64_t n, int F,
+                                                   const int32_t* __restrict__ dbin,
+                                                   const uint16_t* __restrict__ perm,
+                                                   const uint16_t* __restrict__ xperm, int64_t ld_perm,
+                                                   const uint16_t* __restrict__ starts, int64_t n_tiles,
+                                                   float* __restrict__ hist_base, size_t hsz, int slot_l, int slot_r,
+                                                   double* __restrict__ eout, double* __restrict__ tot) {
+    __shared__ float2 s_gh[WT];
+    __shared__ uint16_t s_idx[WT];
+    __shared__ uint16_t s_xidx[SPARSE ? WT : 1];
+    __shared__ uint16_t s_st[ST];
+    const Seg sg = seg_of(job, n);
+    const int64_t m = sg.m;
+    const int tid = threadIdx.x;
+    const int f = blockIdx.x;
+    const bool totals = SPARSE && f == F;
+    const int df = (SPARSE && !totals) ? dbin[f] : -1;
+    const size_t fo = (size_t)(totals ? 0 : f);
+    const uint16_t* pf = perm + fo * (size_t)ld_perm;
+    const uint16_t* xf = SPARSE ? xperm + fo * (size_t)ld_perm : nullptr;
+    const uint16_t* sf = starts + fo * (size_t)n_tiles * ST;
+    float ag = 0.0f, ah = 0.0f;
+    double eg = 0.0, eh = 0.0;
+    int64_t cnt = 0;
+    ChainTile nxt;
+    if (m > 0) chain_load<SPARSE>(nxt, G, H, pf, xf, sf, totals, 0, m);
+    for (int64_t t = 0, t0 = 0; t0 < m; ++t, t0 += WT) {
+        const int tn = (int)min((int64_t)WT, m - t0);
+#pragma unroll
+        for (int j = 0; j < TPT; ++j) {
+            const int x = j * RB + tid;
+            if (x < tn) {
+                s_gh[x] = make_float2(nxt.g[j], nxt.h[j]);
+                if (!totals) {
+                    s_idx[x] = (uint16_t)nxt.idx[j];
+                    if (SPARSE) s_xidx[x] = (uint16_t)nxt.xidx[j];
+                }
+            }
+        }
+        if (!totals) {
+            s_st[tid] = (uint16_t)nxt.st;
+            if (tid == 0) s_st[NB] = (uint16_t)nxt.st_end;
+        }
+        __syncthreads();
+        if (t0 + WT < m) chain_load<SPARSE>(nxt, G, H, pf, xf, sf, totals, t + 1, m);
+        if (totals) {
+            if (tid == 0) run_f64(s_gh, nullptr, (uint32_t)tn, eg, eh);
+        } else if (SPARSE && tid == df) {
+            const uint32_t nx = s_st[NB];      // the tile's rows outside the default bin
+            run_f64(s_gh, s_xidx, nx, eg, eh);
+            cnt += (int64_t)tn - nx;
+        } else {
+            const uint32_t lo = s_st[tid], hi = s_st[tid + 1];
+            run_f32(s_gh, s_idx, lo, hi, ag, ah);
+            cnt += hi - lo;
+        }
+        __syncthreads();
+    }
+    if (totals) {
+        if (tid == 0) {
+            tot[0] = eg;
+            tot[1] = eh;
+        }
         return;
     }
-    if (t >= nf * NB) return;
     const int slot = (!job || job->build_left) ? slot_l : slot_r;
     float* hist = hist_base + (size_t)slot * hsz;
-    const int fi = t / NB, b = t % NB, f = fb0 + fi;
-    const uint32_t lo = bstart[(size_t)f * (NB + 1) + b], hi = bstart[(size_t)f * (NB + 1) + b + 1];
-    if (dbin && b == dbin[f]) {
-        const uint32_t n_expl = bstart[(size_t)f * (NB + 1) + NB] - (hi - lo);
-        const float2* src = expl + (size_t)fi * sort_ld;
-        double ag = 0.0, ah = 0.0;
-        chain_f64([&](int64_t k) { return src[k]; }, 0, n_expl, ag, ah);
-        eout[2 * (size_t)f] = ag;
-        eout[2 * (size_t)f + 1] = ah;
-        return;
+    if (SPARSE && tid == df) {
+        eout[3 * (size_t)f] = eg;
+        eout[3 * (size_t)f + 1] = eh;
+        eout[3 * (size_t)f + 2] = (double)cnt;
+    } else {
+        hist[(size_t)0 * F * NB + (size_t)f * NB + tid] = ag;
+        hist[(size_t)1 * F * NB + (size_t)f * NB + tid] = ah;
+        hist[(size_t)2 * F * NB + (size_t)f * NB + tid] = (float)min(cnt, (int64_t)1 << 24);
     }
-    const float2* src = sorted + (size_t)fi * sort_ld;
-    float ag = 0.0f, ah = 0.0f, ac = 0.0f;
-    uint32_t k = lo;
-    // the chain is latency-bound: batches of CB pairs are loaded one batch
-    // ahead of the (in-order, dependent) adds
-    constexpr uint32_t CB = 16;
-    if (k + CB <= hi) {
-        float2 cur[CB];
-#pragma unroll
-        for (uint32_t j = 0; j < CB; ++j) cur[j] = src[k + j];
-        k += CB;
-        for (; k + CB <= hi; k += CB) {
-            float2 nxt[CB];
-#pragma unroll
-            for (uint32_t j = 0; j < CB; ++j) nxt[j] = src[k + j];
-#pragma unroll
-            for (uint32_t j = 0; j < CB; ++j) {
-                ag += cur[j].x;
-                ah += cur[j].y;
-                ac += 1.0f;
-            }
-#pragma unroll
-            for (uint32_t j = 0; j < CB; ++j) cur[j] = nxt[j];
-        }
-#pragma unroll
-        for (uint32_t j = 0; j < CB; ++j) {
-            ag += cur[j].x;
-            ah += cur[j].y;
-            ac += 1.0f;
-        }
-    }
-    for (; k < hi; ++k) {
-        const float2 a = src[k];
-        ag += a.x; ah += a.y; ac += 1.0f;
-    }
-    hist[(size_t)0 * F * NB + (size_t)f * NB + b] = ag;
-    hist[(size_t)1 * F * NB + (size_t)f * NB + b] = ah;
-    hist[(size_t)2 * F * NB + (size_t)f * NB + b] = ac;
 }
 
 // Sparse builder's default-bin cells (grow.c:101-106): 0 + (float)(node sum -
 // explicit sum) for g and h, 0 + (float)(rows in the default bin) for the count.
 __global__ void __launch_bounds__(RB) k_hist_default(const int32_t* __restrict__ dbin,
-                                                     const uint32_t* __restrict__ bstart,
                                                      const double* __restrict__ eout, const double* __restrict__ tot,
                                                      int F, float* __restrict__ hist_base, size_t hsz,
                                                      const Job* __restrict__ job, int slot_l, int slot_r) {
@@ -553,12 +623,10 @@ __global__ void __launch_bounds__(RB) k_hist_default(const int32_t* __restrict__
     if (f >= F) return;
     const int slot = (!job || job->build_left) ? slot_l : slot_r;
     float* hist = hist_base + (size_t)slot * hsz;
-    const int df = dbin[f];
-    const uint32_t cnt = bstart[(size_t)f * (NB + 1) + df + 1] - bstart[(size_t)f * (NB + 1) + df];
-    const size_t at = (size_t)f * NB + df;
-    hist[(size_t)0 * F * NB + at] = 0.0f + (float)(tot[0] - eout[2 * (size_t)f]);
-    hist[(size_t)1 * F * NB + at] = 0.0f + (float)(tot[1] - eout[2 * (size_t)f + 1]);
-    hist[(size_t)2 * F * NB + at] = 0.0f + (float)(double)cnt;
+    const size_t at = (size_t)f * NB + dbin[f];
+    hist[(size_t)0 * F * NB + at] = 0.0f + (float)(tot[0] - eout[3 * (size_t)f]);
+    hist[(size_t)1 * F * NB + at] = 0.0f + (float)(tot[1] - eout[3 * (size_t)f + 1]);
+    hist[(size_t)2 * F * NB + at] = 0.0f + (float)eout[3 * (size_t)f + 2];
 }
 
 // The sibling: hist[other] = hist[parent] - hist[built] (grow.c:361,368).
@@ -754,36 +822,34 @@ struct Grower {
     int F;
     Ws w;
     size_t hsz;
-    int64_t nchunks;
     const int32_t* dbin;           // sparse builder's default bins, or null
     hipStream_t st;
 
-    // Histogram of the job's built child (at most m_max rows) into node slot_l
-    // (left child built) or slot_r; job null: all rows into slot_l.  With
-    // default bins, the sparse builder's arithmetic (grow.c:68-107).
+    // Histogram of the job's built child (at most m_max rows) into node
+    // slot_l (left child built) or slot_r; job null: all rows into slot_l.
+    // With default bins, the sparse builder's arithmetic (grow.c:68-107).
     void hist(const Job* job, int64_t m_max, int slot_l, int slot_r, const float* G, const float* H) {
-        const int64_t ch = chunks_of(m_max > 0 ? m_max : 1);
-        k_hist_count<<<dim3((unsigned)ch, (unsigned)((F + FT - 1) / FT)), RB, 0, st>>>(bins_rm, ld_rm, w.rows, job, n, F,
-                                                                                      nchunks, w.counts);
-        k_hist_offsets<<<F, NB, 0, st>>>(w.counts, w.bstart, job, n, nchunks);
-        // sorted holds max(min(F, SORT_FEATS), 2) * n pairs: per features'
-        // buckets, and in sparse mode as many explicit-pair runs after them
-        const int64_t mm = max(m_max, (int64_t)1);
-        const int64_t cap = (int64_t)max(min(F, SORT_FEATS), 2) * (n > 0 ? n : 1);
-        const int per = (int)max((int64_t)1, min((int64_t)F, cap / (dbin ? 2 * mm : mm)));
-        float2* expl = dbin ? w.sorted + (size_t)per * mm : nullptr;
-        for (int fb0 = 0; fb0 < F; fb0 += per) {
-            const int nf = min(per, F - fb0);
-            const bool tot = dbin && fb0 == 0;
-            k_hist_scatter<<<dim3((unsigned)ch, (unsigned)((nf + SF - 1) / SF)), SF * WAVE, 0, st>>>(
-                bins_rm, ld_rm, w.rows, job, n, fb0, nf, nchunks, w.counts, w.bstart, G, H, w.sorted, mm, dbin, expl);
-            k_hist_chain<<<(nf * NB + (tot ? 1 : 0) + RB - 1) / RB, RB, 0, st>>>(
-                w.sorted, mm, w.bstart, fb0, nf, F, w.hist, hsz, job, slot_l, slot_r, dbin, expl, w.expl, G, H,
-                tot ? w.tot : nullptr, n);
+        const int64_t tiles = min((int64_t)65535, max((int64_t)1, (m_max + WT - 1) / WT));
+        const dim3 sgrid((unsigned)F, (unsigned)tiles);
+        const uint32_t* rows = w.rows;
+#define YABT_SORT(ROOT, SPARSE)                                                                                     \
+    k_walk_sort<ROOT, SPARSE><<<sgrid, RB, 0, st>>>(bins_fm, ld_fm, bins_rm, ld_rm, rows, job, n, dbin, w.perm, w.xperm, \
+                                                    w.ld_perm, w.starts, w.n_tiles)
+        if (!job) {
+            if (dbin) YABT_SORT(true, true); else YABT_SORT(true, false);
+        } else {
+            if (dbin) YABT_SORT(false, true); else YABT_SORT(false, false);
         }
+#undef YABT_SORT
+        const unsigned cgrid = (unsigned)F + (dbin ? 1u : 0u);
         if (dbin)
-            k_hist_default<<<(F + RB - 1) / RB, RB, 0, st>>>(dbin, w.bstart, w.expl, w.tot, F, w.hist, hsz, job,
-                                                             slot_l, slot_r);
+            k_walk_chain<true><<<cgrid, RB, 0, st>>>(G, H, job, n, F, dbin, w.perm, w.xperm, w.ld_perm, w.starts,
+                                                     w.n_tiles, w.hist, hsz, slot_l, slot_r, w.expl, w.tot);
+        else
+            k_walk_chain<false><<<cgrid, RB, 0, st>>>(G, H, job, n, F, dbin, w.perm, w.xperm, w.ld_perm, w.starts,
+                                                      w.n_tiles, w.hist, hsz, slot_l, slot_r, w.expl, w.tot);
+        if (dbin)
+            k_hist_default<<<(F + RB - 1) / RB, RB, 0, st>>>(dbin, w.expl, w.tot, F, w.hist, hsz, job, slot_l, slot_r);
     }
 };
 
@@ -795,9 +861,9 @@ using namespace yabt::ref;
 
 extern "C" {
 
-size_t yabt_grow_ref_workspace_bytes(int64_t n, int F, int max_leaves) {
+size_t yabt_grow_ref_workspace_bytes(int64_t n, int F, int max_leaves, int sparse) {
     if (n < 0 || n > 0xFFFFFFFFll || F < 1 || max_leaves < 1 || max_leaves > 32767) return 0;
-    return carve(nullptr, n, F, max_leaves).bytes;
+    return carve(nullptr, n, F, max_leaves, sparse != 0).bytes;
 }
 
 int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm, const float* grad,
@@ -814,7 +880,7 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
         return fail(-2, "yabt_grow_ref: null pointer argument");
     if (n > 0 && (!bins_fm || !bins_rm || ld_fm < n || ld_rm < F || ld_rm % 16 || !aligned16(bins_rm)))
         return fail(-2, "yabt_grow_ref: bins layout (pointer, alignment or leading dimension) invalid");
-    const size_t need = carve(nullptr, n, F, max_leaves).bytes;
+    const size_t need = carve(nullptr, n, F, max_leaves, default_bin != nullptr).bytes;
     if (workspace_bytes < need) return fail(-2, "yabt_grow_ref: workspace too small");
     if (default_bin) {   // the kernels index bin tables with it: check it first
         std::vector<int32_t> db(F);
@@ -834,9 +900,8 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
     g.hess = hess;
     g.n = n;
     g.F = F;
-    g.w = carve((char*)workspace, n, F, max_leaves);
+    g.w = carve((char*)workspace, n, F, max_leaves, default_bin != nullptr);
     g.hsz = (size_t)3 * F * NB;
-    g.nchunks = chunks_of(n > 0 ? n : 1);
     g.dbin = default_bin;
     g.st = stream;
     const Ws& w = g.w;

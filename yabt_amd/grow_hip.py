@@ -336,7 +336,7 @@ def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam
             raise ValueError("default_bin must have one entry per feature")
     L = int(max_leaves)
     N = 2 * L + 1
-    nbytes = int(lib.yabt_grow_ref_workspace_bytes(n, F, L))
+    nbytes = int(lib.yabt_grow_ref_workspace_bytes(n, F, L, int(db is not None)))
     if nbytes == 0:
         raise ValueError("yabt_grow_ref: invalid sizes")
     key = (dev, "grow_ref")
