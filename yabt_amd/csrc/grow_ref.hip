@@ -658,6 +658,7 @@ __global__ void __launch_bounds__(WAVE) k_scan_feature(const float* __restrict__
                                                        const uint8_t* __restrict__ path, ScanParams P,
                                                        double* __restrict__ fsel, double* __restrict__ fgain,
                                                        int32_t* __restrict__ fb) {
+    __shared__ float s_in[3][NB];
     __shared__ double s_gl[NB], s_hl[NB], s_cl[NB];
     const int f = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
     const int node = c == 0 ? node0 : node1;
@@ -669,26 +670,50 @@ __global__ void __launch_bounds__(WAVE) k_scan_feature(const float* __restrict__
         const float* hg = hist + (size_t)node * hsz + (size_t)f * NB;
         const float* hh = hg + (size_t)F * NB;
         const float* hc = hh + (size_t)F * NB;
-        if (lane == 0) {
+        for (int b = lane; b < NB; b += WAVE) {
+            s_in[0][b] = hg[b];
+            s_in[1][b] = hh[b];
+            s_in[2][b] = hc[b];
+        }
+        __syncthreads();
+        if (lane == 0) {   // the prefix sums in double, in bin order (grow.c:146-160)
             double G = 0.0, H = 0.0, C = 0.0;
-            for (int b = 0; b < nb; ++b) {
-                G += hg[b];
-                H += hh[b];
-                C += hc[b];
-                s_gl[b] = G;
-                s_hl[b] = H;
-                s_cl[b] = C;
+            for (int b0 = 0; b0 < nb; b0 += 8) {
+                float vg[8], vh[8], vc[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int b = min(b0 + j, nb - 1);
+                    vg[j] = s_in[0][b];
+                    vh[j] = s_in[1][b];
+                    vc[j] = s_in[2][b];
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (b0 + j < nb) {
+                        G += vg[j];
+                        H += vh[j];
+                        C += vc[j];
+                        s_gl[b0 + j] = G;
+                        s_hl[b0 + j] = H;
+                        s_cl[b0 + j] = C;
+                    }
             }
         }
         __syncthreads();
-        // compute_boost (grow.c:111-122): 1 + ib * max(0, max over the path of imat[p][f])
+        // compute_boost (grow.c:111-122): 1 + ib * max(0, max over the path
+        // of imat[p][f]); the maximum is taken lane-parallel (max is exact)
         float mx = 0.0f;
         if (P.use_imat) {
-            for (int p = 0; p < F; ++p)
+            for (int p = lane; p < F; p += WAVE)
                 if (path[(size_t)node * F + p]) {
                     const float v = P.imat[(size_t)p * F + f];
                     if (v > mx) mx = v;
                 }
+#pragma unroll
+            for (int d = WAVE / 2; d > 0; d >>= 1) {
+                const float o = __shfl_xor(mx, d, WAVE);
+                if (o > mx) mx = o;
+            }
         }
         const double bo = P.use_imat ? (double)(1.0f + P.ib * mx) : 1.0;
         const double Gt = s_gl[nb - 1], Ht = s_hl[nb - 1], Ct = s_cl[nb - 1];
@@ -751,8 +776,8 @@ __global__ void __launch_bounds__(WAVE) k_scan_pick(const float* __restrict__ hi
         }
     }
     __syncthreads();
-    if (threadIdx.x != 0) return;
-    if (nid >= 0 && c == 0) {                   // the split's record (grow.c:340-350, 381-386)
+    const int lane = threadIdx.x;
+    if (lane == 0 && nid >= 0 && c == 0) {      // the split's record (grow.c:340-350, 381-386)
         out_feature[nid] = split_f;
         out_thr_bin[nid] = split_b;
         out_left[nid] = node0;
@@ -761,9 +786,11 @@ __global__ void __launch_bounds__(WAVE) k_scan_pick(const float* __restrict__ hi
         out_depth[node0] = child_depth;
         out_depth[node1] = child_depth;
     }
+    // the feature-major first maximum: lanes take features in increasing
+    // order with grow.c's strict >, then the largest sel, lowest f wins
     double best_sel = -INFINITY, best_true = -INFINITY;
     int bf = -1, bb = -1;
-    for (int f = 0; f < F; ++f) {
+    for (int f = lane; f < F; f += WAVE) {
         const int b = fb[(size_t)c * F + f];
         const double s = fsel[(size_t)c * F + f];
         if (b >= 0 && s > best_sel) {
@@ -773,10 +800,33 @@ __global__ void __launch_bounds__(WAVE) k_scan_pick(const float* __restrict__ hi
             bb = b;
         }
     }
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) {
+        const double os = __shfl_xor(best_sel, d, WAVE);
+        const double ot = __shfl_xor(best_true, d, WAVE);
+        const int of = __shfl_xor(bf, d, WAVE);
+        const int ob = __shfl_xor(bb, d, WAVE);
+        if (of >= 0 && (bf < 0 || os > best_sel || (os == best_sel && of < bf))) {
+            best_sel = os;
+            best_true = ot;
+            bf = of;
+            bb = ob;
+        }
+    }
+    if (lane != 0) return;
     double G = 0.0, H = 0.0;
-    for (int b = 0; b < NB; ++b) {
-        G += s_g[b];
-        H += s_h[b];
+    for (int b0 = 0; b0 < NB; b0 += 8) {
+        float vg[8], vh[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            vg[j] = s_g[b0 + j];
+            vh[j] = s_h[b0 + j];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            G += vg[j];
+            H += vh[j];
+        }
     }
     const float v = (float)(-lr * G / (H + lam));
     out_value[node] = v;
