@@ -206,12 +206,59 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
                    res["left"], res["right"], n_threads=threads)
     sizes = node_sizes(res["feature"], res["left"], res["right"], leaf)
     upd = tree_updates(res["feature"], res["left"], res["right"], sizes, F)
-    return {"value": round(upd / sec / 1e9, 4), "unit": "G row·feature updates/s",
-            "cores": threads, "kind": "reference" if reference else "port",
-            "ms_per_tree": round(sec * 1e3, 1),
-            "sample": f"one 255-leaf tree on 1,000,000 x 100 uniform u8 bins (1/10 of the rows), "
-                      f"{len(timed)} timed run(s) after 1 warm-up, median; {threads} OpenMP threads; "
-                      f"host has {os.cpu_count()} logical CPUs"}
+    out = {"value": round(upd / sec / 1e9, 4), "unit": "G row·feature updates/s",
+           "cores": threads, "kind": "reference" if reference else "port",
+           "ms_per_tree": round(sec * 1e3, 1),
+           "sample": f"one 255-leaf tree on 1,000,000 x 100 uniform u8 bins (1/10 of the rows), "
+                     f"{len(timed)} timed run(s) after 1 warm-up, median; {threads} OpenMP threads; "
+                     f"host has {os.cpu_count()} logical CPUs"}
+    # the same tree on every logical CPU of the host (one run after the warm-ups above)
+    all_threads = os.cpu_count() or 1
+    t0 = time.perf_counter()
+    O.grow(bins_fm, g, h, reference=reference, **dict(kw, n_threads=all_threads))
+    sec_all = time.perf_counter() - t0
+    out["all_cores"] = {"threads": all_threads, "ms_per_tree": round(sec_all * 1e3, 1),
+                        "value": round(upd / sec_all / 1e9, 4)}
+    out["other_workloads"] = cpu_other_workloads(O, reference, threads)
+    return out
+
+
+def cpu_other_workloads(O, reference: bool, threads: int) -> dict:
+    """The same C grower, one tree each, on the other tree workloads (context
+    for the estimator timings): the binary 1M x 28 workload (28 bins, depth 8,
+    g = 0.5 - y, h = 0.25 from p = 0.5), and a 400 000-row sample (1/10) of the
+    4M x 500 depth-6 mostly-zero workload through the sparse builder the
+    reference picks for it (grow.c:68-107, which is serial)."""
+    out = {}
+    rng = np.random.default_rng(1)
+    n, F = 1_000_000, 28
+    bins = rng.integers(0, 28, size=(F, n), dtype=np.uint8)
+    y = (rng.random(n) < 0.5).astype(np.float32)
+    g = (np.float32(0.5) - y).astype(np.float32)
+    h = np.full(n, 0.25, np.float32)
+    kw = dict(lam=1.0, gamma=0.0, mcw=1e-3, msl=20, lr=0.1, max_leaves=256, max_depth=8,
+              nbins=np.full(F, 28, np.int32), n_threads=threads)
+    O.grow(bins, g, h, reference=reference, **kw)
+    t0 = time.perf_counter()
+    O.grow(bins, g, h, reference=reference, **kw)
+    out["binary_1Mx28_depth8_ms_per_tree"] = round((time.perf_counter() - t0) * 1e3, 1)
+    n, F = 400_000, 500
+    bins = rng.integers(1, 256, size=(n, F), dtype=np.uint8)
+    bins[rng.random((n, F), dtype=np.float32) < 0.9] = 0
+    g = rng.laplace(size=n).astype(np.float32)
+    h = np.ones(n, np.float32)
+    nondef = bins != 0
+    indptr = np.concatenate([[0], np.cumsum(nondef.sum(axis=1))]).astype(np.int64)
+    r, c = np.nonzero(nondef)
+    layout = (indptr, c.astype(np.int32), bins[r, c].astype(np.int32), np.zeros(F, np.int32))
+    bins_fm = np.ascontiguousarray(bins.T)
+    del bins, nondef, r, c
+    kw = dict(lam=1.0, gamma=0.0, mcw=1e-3, msl=20, lr=0.1, max_leaves=64, max_depth=6,
+              nbins=np.full(F, 256, np.int32), n_threads=threads)
+    t0 = time.perf_counter()
+    O.grow(bins_fm, g, h, reference=reference, sparse=layout, **kw)
+    out["depth6_400kx500_sparse_ms_per_tree"] = round((time.perf_counter() - t0) * 1e3, 1)
+    return out
 
 
 def depthwise_trees(torch, trees: int = 10) -> dict:
