@@ -71,7 +71,18 @@ CASES = [
     dict(n=50_000, F=30, nb=256, kind="normal", max_leaves=255, msl=20),
     dict(n=300_000, F=24, nb=256, kind="normal", max_leaves=63, msl=20, imat=True),
     dict(n=200_000, F=33, nb=256, kind="laplace", max_leaves=40, max_depth=6, skew=True),
+    dict(n=30_000, F=10, nb=256, kind="normal", max_leaves=63, msl=5, wide=True),
+    dict(n=5000, F=6, nb=32, kind="laplace", max_leaves=31, msl=1, lam=0.0, wide=True),
 ]
+
+
+def wide_gradients(rng, bins, g, h):
+    """g, h scaled by 10^(-20 + 23 x/255) and 10^(-6 + 7 x/255), x = the row's
+    bin of feature 0: that feature's bin sums span ~76 binary orders, so
+    their double prefix sums round and the scan must add them in bin order;
+    the other features' bins mix all magnitudes and sum exactly."""
+    x = bins[:, 0].astype(np.float64) / 255.0
+    return ((g * 10.0 ** (-20 + 23 * x)).astype(np.float32), (h * 10.0 ** (-6 + 7 * x)).astype(np.float32))
 
 
 @pytest.mark.parametrize("case", CASES, ids=lambda c: f"n{c['n']}_F{c['F']}_L{c['max_leaves']}")
@@ -82,6 +93,8 @@ def test_matches_fp32_oracle(case):
     n, F, nb = c.pop("n"), c.pop("F"), c.pop("nb")
     bins = (skewed_bins(rng, n, F) if c.pop("skew", False) else uniform_bins(rng, n, F, nb))
     g, h = grad_hess(rng, n, c.pop("kind"))
+    if c.pop("wide", False):
+        g, h = wide_gradients(rng, bins, g, h)
     kw = dict(max_leaves=c.pop("max_leaves"), max_depth=c.pop("max_depth", 64), msl=c.pop("msl", 20),
               lam=c.pop("lam", 1.0), gamma=c.pop("gamma", 0.0))
     if c.pop("imat", False):

@@ -643,6 +643,45 @@ __global__ void __launch_bounds__(RB) k_hist_sub(float* __restrict__ hist, size_
 // split scan (grow.c:129-197), one wave per (feature, child)
 // ---------------------------------------------------------------------------
 
+// Exponent bounds of a set of fp32 values, for deciding when double sums of
+// them are exact in any order: every value is a multiple of 2^lsb and below
+// 2^(top + 1) in magnitude.  Non-finite values make the set inexact.
+struct ExpRange {
+    int lsb, top;
+    bool finite;
+};
+
+__device__ __forceinline__ void exp_range_add(ExpRange& r, float x) {
+    const uint32_t u = __float_as_uint(x);
+    const int ex = (int)((u >> 23) & 0xffu);
+    const uint32_t mant = u & 0x7fffffu;
+    if (ex == 0xff) {
+        r.finite = false;
+        return;
+    }
+    if (ex == 0 && mant == 0) return;                  // +-0 adds nothing
+    const uint32_t m24 = ex == 0 ? mant : (mant | 0x800000u);
+    const int e0 = ex == 0 ? -149 : ex - 150;          // weight of the mantissa's bit 0
+    const int lsb = e0 + __builtin_ctz(m24);
+    const int top = e0 + 31 - __builtin_clz(m24);
+    r.lsb = min(r.lsb, lsb);
+    r.top = max(r.top, top);
+}
+
+// Wave-wide: true when every partial sum of up to 256 of the wave's values
+// (any subset, so any order of addition) is exactly representable in double:
+// all are multiples of 2^lsb and |sum| < 256 * 2^(top + 1) = 2^(top + 9), so
+// top + 9 - lsb <= 53 suffices.
+__device__ __forceinline__ bool wave_sums_exact(ExpRange r) {
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) {
+        r.lsb = min(r.lsb, __shfl_xor(r.lsb, d, WAVE));
+        r.top = max(r.top, __shfl_xor(r.top, d, WAVE));
+        r.finite = r.finite && __shfl_xor((int)r.finite, d, WAVE);
+    }
+    return r.finite && (r.top < r.lsb || r.top + 9 - r.lsb <= 53);
+}
+
 struct ScanParams {
     const int32_t* nbins;
     const uint8_t* fmask;
@@ -676,23 +715,65 @@ __global__ void __launch_bounds__(WAVE) k_scan_feature(const float* __restrict__
             s_in[2][b] = hc[b];
         }
         __syncthreads();
-        if (lane == 0) {   // the prefix sums in double, in bin order (grow.c:146-160)
+        // the prefix sums in double, in bin order (grow.c:146-160).  When
+        // every partial sum of the node's bins is exact in double, the prefix
+        // is the exact one whatever the order of the additions, so the wave
+        // scans it in parallel (4 bins per lane); otherwise lane 0 adds the
+        // bins in order as cgrow does.
+        ExpRange rg{1 << 20, -(1 << 20), true}, rh = rg;
+        float vg[4], vh[4], vc[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int b = 4 * lane + j;
+            vg[j] = b < nb ? s_in[0][b] : 0.0f;
+            vh[j] = b < nb ? s_in[1][b] : 0.0f;
+            vc[j] = b < nb ? s_in[2][b] : 0.0f;
+            exp_range_add(rg, vg[j]);
+            exp_range_add(rh, vh[j]);
+        }
+        // counts are integers below 2^24: their sums are always exact
+        const bool exact = wave_sums_exact(rg) && wave_sums_exact(rh);
+        if (exact) {
+            double pg[4], ph[4], pc[4];
+            double ag = 0.0, ah = 0.0, ac = 0.0;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                ag += (double)vg[j];
+                ah += (double)vh[j];
+                ac += (double)vc[j];
+                pg[j] = ag;
+                ph[j] = ah;
+                pc[j] = ac;
+            }
+            const double og = wave_excl_scan<double>(ag, lane);
+            const double oh = wave_excl_scan<double>(ah, lane);
+            const double oc = wave_excl_scan<double>(ac, lane);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int b = 4 * lane + j;
+                if (b < nb) {
+                    s_gl[b] = og + pg[j];
+                    s_hl[b] = oh + ph[j];
+                    s_cl[b] = oc + pc[j];
+                }
+            }
+        } else if (lane == 0) {
             double G = 0.0, H = 0.0, C = 0.0;
             for (int b0 = 0; b0 < nb; b0 += 8) {
-                float vg[8], vh[8], vc[8];
+                float wg[8], wh[8], wc[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const int b = min(b0 + j, nb - 1);
-                    vg[j] = s_in[0][b];
-                    vh[j] = s_in[1][b];
-                    vc[j] = s_in[2][b];
+                    wg[j] = s_in[0][b];
+                    wh[j] = s_in[1][b];
+                    wc[j] = s_in[2][b];
                 }
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
                     if (b0 + j < nb) {
-                        G += vg[j];
-                        H += vh[j];
-                        C += vc[j];
+                        G += wg[j];
+                        H += wh[j];
+                        C += wc[j];
                         s_gl[b0 + j] = G;
                         s_hl[b0 + j] = H;
                         s_cl[b0 + j] = C;
