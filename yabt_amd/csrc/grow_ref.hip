@@ -55,7 +55,6 @@ constexpr int ST = NB + 1;         // bucket starts per (feature, tile)
 struct Job {
     int64_t s, e;                  // parent segment
     int64_t nl;                    // rows going left
-    uint32_t K;                    // pairs moved by the two-pointer loop
     int32_t build_left;
     int64_t cs, ce;                // built child's segment
 };
@@ -195,7 +194,6 @@ __global__ void __launch_bounds__(RB) k_part_offsets(uint32_t* blk, int nblk, Jo
         job->s = s;
         job->e = e;
         job->nl = carry;
-        job->K = 0;
         job->build_left = (int64_t)carry <= m - (int64_t)carry ? 1 : 0;
         job->cs = job->build_left ? s : s + (int64_t)carry;
         job->ce = job->build_left ? s + (int64_t)carry : e;
@@ -225,19 +223,6 @@ __global__ void __launch_bounds__(RB) k_part_rank(const uint8_t* __restrict__ fl
     }
 }
 
-// K = #{k : p_k < q_k} over k < min(#right, #left).
-__global__ void __launch_bounds__(RB) k_part_pairs(const uint32_t* __restrict__ p, const uint32_t* __restrict__ q,
-                                                   Job* job, int64_t m) {
-    __shared__ uint32_t s_red[RB / WAVE];
-    const int64_t nl = job->nl;
-    const int64_t kmax = min(nl, m - nl);
-    uint32_t c = 0;
-    for (int64_t k = (int64_t)blockIdx.x * RB + threadIdx.x; k < kmax; k += (int64_t)gridDim.x * RB)
-        c += p[k] < q[k] ? 1u : 0u;
-    c = block_sum<RB, uint32_t>(c, s_red);
-    if (threadIdx.x == 0 && c) atomicAdd(&job->K, c);
-}
-
 // Destinations of the two-pointer loop; rows_tmp[s + dest] = rows[s + x].
 // Block 0 also records the children's path masks and node bookkeeping.
 __global__ void __launch_bounds__(RB) k_part_permute(const uint8_t* __restrict__ flag,
@@ -247,7 +232,10 @@ __global__ void __launch_bounds__(RB) k_part_permute(const uint8_t* __restrict__
                                                      int64_t s, int64_t m, uint8_t* path, int F, int nid, int f,
                                                      int nl_id, int nr_id) {
     const int64_t nl = job->nl;
-    const int64_t K = job->K;
+    // K = #{k : p_k < q_k}: p rises and q falls, and p_k < q_k exactly when
+    // the k-th left row from the right lies at or after nl, so K is the
+    // number of left rows in [nl, m): nl minus the left rows before nl
+    const int64_t K = nl < m ? nl - (int64_t)rank[nl] : 0;
     const int64_t qK = K == 0 ? m : (int64_t)q[K - 1];
     for (int64_t x = (int64_t)blockIdx.x * RB + threadIdx.x; x < m; x += (int64_t)gridDim.x * RB) {
         const int64_t lb = rank[x];
@@ -629,16 +617,6 @@ __global__ void __launch_bounds__(RB) k_hist_default(const int32_t* __restrict__
     hist[(size_t)2 * F * NB + at] = 0.0f + (float)eout[3 * (size_t)f + 2];
 }
 
-// The sibling: hist[other] = hist[parent] - hist[built] (grow.c:361,368).
-__global__ void __launch_bounds__(RB) k_hist_sub(float* __restrict__ hist, size_t hsz, int parent, int nl_id,
-                                                 int nr_id, const Job* __restrict__ job) {
-    const int built = job->build_left ? nl_id : nr_id, other = job->build_left ? nr_id : nl_id;
-    const float* hp = hist + (size_t)parent * hsz;
-    const float* hb = hist + (size_t)built * hsz;
-    float* ho = hist + (size_t)other * hsz;
-    for (size_t i = (size_t)blockIdx.x * RB + threadIdx.x; i < hsz; i += (size_t)gridDim.x * RB) ho[i] = hp[i] - hb[i];
-}
-
 // ---------------------------------------------------------------------------
 // split scan (grow.c:129-197), one wave per (feature, child)
 // ---------------------------------------------------------------------------
@@ -693,10 +671,109 @@ struct ScanParams {
     int F;
 };
 
-__global__ void __launch_bounds__(WAVE) k_scan_feature(const float* __restrict__ hist, size_t hsz, int node0, int node1,
-                                                       const uint8_t* __restrict__ path, ScanParams P,
+// The pick's inputs and the split record it writes.
+struct PickArgs {
+    float lr;
+    double lam;
+    float* out_value;
+    Res* res;
+    const Job* job;                // null at the root
+    int nid, split_f, split_b;     // the split (nid < 0 at the root)
+    int64_t child_depth;
+    int64_t *out_feature, *out_thr_bin, *out_left, *out_right, *out_depth;
+};
+
+// One child's feature-major first maximum (grow.c:183-192), node value from
+// feature 0's 256 bins summed in double (grow.c:302-308, 371-379), and (for
+// the left child of a split) the split's node record (grow.c:340-350,
+// 381-386).  One wave.
+__device__ void ref_pick(const float* __restrict__ hist, size_t hsz, int node0, int node1, int c, int F,
+                         const double* __restrict__ fsel, const double* __restrict__ fgain,
+                         const int32_t* __restrict__ fb, const PickArgs& A, float* s_g, float* s_h) {
+    const int node = c == 0 ? node0 : node1;
+    const int lane = threadIdx.x;
+    {
+        const float* hg = hist + (size_t)node * hsz;
+        const float* hh = hg + (size_t)F * NB;
+        for (int b = lane; b < NB; b += WAVE) {
+            s_g[b] = hg[b];
+            s_h[b] = hh[b];
+        }
+    }
+    __syncthreads();
+    if (lane == 0 && A.nid >= 0 && c == 0) {
+        A.out_feature[A.nid] = A.split_f;
+        A.out_thr_bin[A.nid] = A.split_b;
+        A.out_left[A.nid] = node0;
+        A.out_right[A.nid] = node1;
+        A.out_value[A.nid] = 0.0f;
+        A.out_depth[node0] = A.child_depth;
+        A.out_depth[node1] = A.child_depth;
+    }
+    // lanes take features in increasing order with grow.c's strict >, then
+    // the largest sel, lowest f wins
+    double best_sel = -INFINITY, best_true = -INFINITY;
+    int bf = -1, bb = -1;
+    for (int f = lane; f < F; f += WAVE) {
+        const int b = fb[(size_t)c * F + f];
+        const double s = fsel[(size_t)c * F + f];
+        if (b >= 0 && s > best_sel) {
+            best_sel = s;
+            best_true = fgain[(size_t)c * F + f];
+            bf = f;
+            bb = b;
+        }
+    }
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) {
+        const double os = __shfl_xor(best_sel, d, WAVE);
+        const double ot = __shfl_xor(best_true, d, WAVE);
+        const int of = __shfl_xor(bf, d, WAVE);
+        const int ob = __shfl_xor(bb, d, WAVE);
+        if (of >= 0 && (bf < 0 || os > best_sel || (os == best_sel && of < bf))) {
+            best_sel = os;
+            best_true = ot;
+            bf = of;
+            bb = ob;
+        }
+    }
+    if (lane == 0) {
+        double G = 0.0, H = 0.0;
+        for (int b0 = 0; b0 < NB; b0 += 8) {
+            float vg[8], vh[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                vg[j] = s_g[b0 + j];
+                vh[j] = s_h[b0 + j];
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                G += vg[j];
+                H += vh[j];
+            }
+        }
+        const float v = (float)(-A.lr * G / (H + A.lam));
+        A.out_value[node] = v;
+        ChildRes& r = A.res->c[c];
+        r.gain = bf < 0 ? -INFINITY : best_true;
+        r.f = bf;
+        r.b = bb;
+        r.value = v;
+        if (c == 0) {
+            A.res->mid = A.job ? A.job->s + A.job->nl : 0;
+            A.res->build_left = A.job ? A.job->build_left : 0;
+        }
+    }
+    __syncthreads();
+}
+
+// One wave per (feature, child): the split scan (grow.c:129-197).  At a split
+// (parent >= 0) the subtracted child's block first forms its feature's bins
+// as parent - built child in fp32 (grow.c:361,368) and stores them.
+__global__ void __launch_bounds__(WAVE) k_scan_feature(float* __restrict__ hist, size_t hsz, int node0, int node1,
+                                                       int parent, const uint8_t* __restrict__ path, ScanParams P,
                                                        double* __restrict__ fsel, double* __restrict__ fgain,
-                                                       int32_t* __restrict__ fb) {
+                                                       int32_t* __restrict__ fb, PickArgs A) {
     __shared__ float s_in[3][NB];
     __shared__ double s_gl[NB], s_hl[NB], s_cl[NB];
     const int f = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
@@ -704,15 +781,33 @@ __global__ void __launch_bounds__(WAVE) k_scan_feature(const float* __restrict__
     const int F = P.F;
     double best_sel = -INFINITY, best_true = -INFINITY;
     int best_b = -1;
+    const bool sub = parent >= 0 && node == (A.job->build_left ? node1 : node0);
+    if (sub) {
+        const int built = A.job->build_left ? node0 : node1;
+        const size_t plane = (size_t)F * NB;
+        const float* hp = hist + (size_t)parent * hsz + (size_t)f * NB;
+        const float* hb = hist + (size_t)built * hsz + (size_t)f * NB;
+        float* ho = hist + (size_t)node * hsz + (size_t)f * NB;
+        for (int b = lane; b < NB; b += WAVE) {
+#pragma unroll
+            for (int ch = 0; ch < 3; ++ch) {
+                const float v = hp[ch * plane + b] - hb[ch * plane + b];
+                ho[ch * plane + b] = v;
+                s_in[ch][b] = v;
+            }
+        }
+    }
     if (P.fmask[f]) {
         const int nb = min(max(P.nbins[f], 1), NB);
-        const float* hg = hist + (size_t)node * hsz + (size_t)f * NB;
-        const float* hh = hg + (size_t)F * NB;
-        const float* hc = hh + (size_t)F * NB;
-        for (int b = lane; b < NB; b += WAVE) {
-            s_in[0][b] = hg[b];
-            s_in[1][b] = hh[b];
-            s_in[2][b] = hc[b];
+        if (!sub) {
+            const float* hg = hist + (size_t)node * hsz + (size_t)f * NB;
+            const float* hh = hg + (size_t)F * NB;
+            const float* hc = hh + (size_t)F * NB;
+            for (int b = lane; b < NB; b += WAVE) {
+                s_in[0][b] = hg[b];
+                s_in[1][b] = hh[b];
+                s_in[2][b] = hc[b];
+            }
         }
         __syncthreads();
         // the prefix sums in double, in bin order (grow.c:146-160).  When
@@ -833,93 +928,13 @@ __global__ void __launch_bounds__(WAVE) k_scan_feature(const float* __restrict__
     }
 }
 
-// One wave per child: the feature-major first maximum (grow.c:183-192) and
-// the node value from feature 0's 256 bins (grow.c:371-379).
+// One wave per child: ref_pick after every scan block is done.
 __global__ void __launch_bounds__(WAVE) k_scan_pick(const float* __restrict__ hist, size_t hsz, int node0, int node1,
                                                     int F, const double* __restrict__ fsel,
                                                     const double* __restrict__ fgain, const int32_t* __restrict__ fb,
-                                                    float lr, double lam, float* __restrict__ out_value,
-                                                    Res* __restrict__ res, const Job* __restrict__ job, int nid,
-                                                    int split_f, int split_b, int64_t child_depth,
-                                                    int64_t* __restrict__ out_feature, int64_t* __restrict__ out_thr_bin,
-                                                    int64_t* __restrict__ out_left, int64_t* __restrict__ out_right,
-                                                    int64_t* __restrict__ out_depth) {
-    const int c = blockIdx.x;
-    const int node = c == 0 ? node0 : node1;
-    // the wave stages feature 0's g and h bins in LDS; one lane adds them in order
+                                                    PickArgs A) {
     __shared__ float s_g[NB], s_h[NB];
-    {
-        const float* hg = hist + (size_t)node * hsz;
-        const float* hh = hg + (size_t)F * NB;
-        for (int b = threadIdx.x; b < NB; b += WAVE) {
-            s_g[b] = hg[b];
-            s_h[b] = hh[b];
-        }
-    }
-    __syncthreads();
-    const int lane = threadIdx.x;
-    if (lane == 0 && nid >= 0 && c == 0) {      // the split's record (grow.c:340-350, 381-386)
-        out_feature[nid] = split_f;
-        out_thr_bin[nid] = split_b;
-        out_left[nid] = node0;
-        out_right[nid] = node1;
-        out_value[nid] = 0.0f;
-        out_depth[node0] = child_depth;
-        out_depth[node1] = child_depth;
-    }
-    // the feature-major first maximum: lanes take features in increasing
-    // order with grow.c's strict >, then the largest sel, lowest f wins
-    double best_sel = -INFINITY, best_true = -INFINITY;
-    int bf = -1, bb = -1;
-    for (int f = lane; f < F; f += WAVE) {
-        const int b = fb[(size_t)c * F + f];
-        const double s = fsel[(size_t)c * F + f];
-        if (b >= 0 && s > best_sel) {
-            best_sel = s;
-            best_true = fgain[(size_t)c * F + f];
-            bf = f;
-            bb = b;
-        }
-    }
-#pragma unroll
-    for (int d = WAVE / 2; d > 0; d >>= 1) {
-        const double os = __shfl_xor(best_sel, d, WAVE);
-        const double ot = __shfl_xor(best_true, d, WAVE);
-        const int of = __shfl_xor(bf, d, WAVE);
-        const int ob = __shfl_xor(bb, d, WAVE);
-        if (of >= 0 && (bf < 0 || os > best_sel || (os == best_sel && of < bf))) {
-            best_sel = os;
-            best_true = ot;
-            bf = of;
-            bb = ob;
-        }
-    }
-    if (lane != 0) return;
-    double G = 0.0, H = 0.0;
-    for (int b0 = 0; b0 < NB; b0 += 8) {
-        float vg[8], vh[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            vg[j] = s_g[b0 + j];
-            vh[j] = s_h[b0 + j];
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            G += vg[j];
-            H += vh[j];
-        }
-    }
-    const float v = (float)(-lr * G / (H + lam));
-    out_value[node] = v;
-    ChildRes& r = res->c[c];
-    r.gain = bf < 0 ? -INFINITY : best_true;
-    r.f = bf;
-    r.b = bb;
-    r.value = v;
-    if (c == 0) {
-        res->mid = job ? job->s + job->nl : 0;
-        res->build_left = job ? job->build_left : 0;
-    }
+    ref_pick(hist, hsz, node0, node1, blockIdx.x, F, fsel, fgain, fb, A, s_g, s_h);
 }
 
 // Per-row leaf ids from the final rows[] and the leaves' segments.
@@ -1074,10 +1089,22 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
     // root
     node_end[0] = n;
     g.hist(nullptr, n, 0, 0, grad, hess);
-    k_scan_feature<<<dim3(F, 1), WAVE, 0, stream>>>(w.hist, g.hsz, 0, 0, w.path, P, w.fsel, w.fgain, w.fb);
-    k_scan_pick<<<1, WAVE, 0, stream>>>(w.hist, g.hsz, 0, 0, F, w.fsel, w.fgain, w.fb, lr, (double)lam, out_value,
-                                        w.res, nullptr, -1, 0, 0, 0, out_feature, out_thr_bin, out_left, out_right,
-                                        out_depth);
+    PickArgs A;
+    A.lr = lr;
+    A.lam = (double)lam;
+    A.out_value = out_value;
+    A.res = w.res;
+    A.job = nullptr;
+    A.nid = -1;
+    A.split_f = A.split_b = 0;
+    A.child_depth = 0;
+    A.out_feature = out_feature;
+    A.out_thr_bin = out_thr_bin;
+    A.out_left = out_left;
+    A.out_right = out_right;
+    A.out_depth = out_depth;
+    k_scan_feature<<<dim3(F, 1), WAVE, 0, stream>>>(w.hist, g.hsz, 0, 0, -1, w.path, P, w.fsel, w.fgain, w.fb, A);
+    k_scan_pick<<<1, WAVE, 0, stream>>>(w.hist, g.hsz, 0, 0, F, w.fsel, w.fgain, w.fb, A);
     int rc = launch_status("yabt_grow_ref launch");
     if (rc) return rc;
     if ((rc = sync_res())) return rc;
@@ -1112,7 +1139,6 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
         k_part_flags<<<pblk, RB, 0, stream>>>(bins_fm, ld_fm, f, b, w.rows, s, m, w.flag, w.blk);
         k_part_offsets<<<1, RB, 0, stream>>>(w.blk, pblk, w.job, s, e);
         k_part_rank<<<pblk, RB, 0, stream>>>(w.flag, w.blk, w.job, m, w.rank, w.p, w.q);
-        k_part_pairs<<<launch_grid(m / 2 + 1, RB * 4, 1024), RB, 0, stream>>>(w.p, w.q, w.job, m);
         k_part_permute<<<launch_grid(m, RB * 4, 4096), RB, 0, stream>>>(w.flag, w.rank, w.p, w.q, w.job, w.rows,
                                                                       w.rows_tmp, s, m, w.path, F, nid, f, nl, nr);
         k_part_commit<<<launch_grid(m, RB * 4, 4096), RB, 0, stream>>>(w.rows, w.rows_tmp, w.job, s, m, grad, hess, w.G,
@@ -1120,11 +1146,14 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
         // the smaller child (ties left, grow.c:355) has at most m / 2 rows;
         // the other is parent - built (grow.c:361,368)
         g.hist(w.job, m / 2, nl, nr, w.G, w.H);
-        k_hist_sub<<<launch_grid((int64_t)g.hsz, RB * 4, 1024), RB, 0, stream>>>(w.hist, g.hsz, nid, nl, nr, w.job);
-        k_scan_feature<<<dim3(F, 2), WAVE, 0, stream>>>(w.hist, g.hsz, nl, nr, w.path, P, w.fsel, w.fgain, w.fb);
-        k_scan_pick<<<2, WAVE, 0, stream>>>(w.hist, g.hsz, nl, nr, F, w.fsel, w.fgain, w.fb, lr, (double)lam,
-                                            out_value, w.res, w.job, nid, f, b, d, out_feature, out_thr_bin, out_left,
-                                            out_right, out_depth);
+        A.job = w.job;
+        A.nid = nid;
+        A.split_f = f;
+        A.split_b = b;
+        A.child_depth = d;
+        k_scan_feature<<<dim3(F, 2), WAVE, 0, stream>>>(w.hist, g.hsz, nl, nr, nid, w.path, P, w.fsel, w.fgain,
+                                                        w.fb, A);
+        k_scan_pick<<<2, WAVE, 0, stream>>>(w.hist, g.hsz, nl, nr, F, w.fsel, w.fgain, w.fb, A);
         if ((rc = launch_status("yabt_grow_ref launch"))) return rc;
         if ((rc = sync_res())) return rc;
         const int64_t mid = h_res->mid;
