@@ -42,6 +42,7 @@
 #include <math.h>
 #include <string.h>
 
+#include <atomic>
 #include <vector>
 
 namespace yabt {
@@ -63,7 +64,7 @@ struct ChildRes {
     double gain;                   // best true gain (-inf if none)
     int32_t f, b;
     float value;
-    int32_t pad;
+    int32_t seq;                   // the round that wrote this record (written last)
 };
 
 struct Res {
@@ -96,7 +97,6 @@ struct Ws {
     uint8_t* path;                 // (N, F)
     int64_t* segs;                 // (N, 3): leaf node, start, end
     Job* job;
-    Res* res;
     size_t bytes;
 };
 
@@ -128,7 +128,6 @@ Ws carve(char* base, int64_t n, int F, int max_leaves, bool sparse) {
     w.path = c.take<uint8_t>((size_t)N * F);
     w.segs = c.take<int64_t>((size_t)N * 3);
     w.job = c.take<Job>(1);
-    w.res = c.take<Res>(1);
     w.bytes = c.off;
     return w;
 }
@@ -679,6 +678,7 @@ struct PickArgs {
     Res* res;
     const Job* job;                // null at the root
     int nid, split_f, split_b;     // the split (nid < 0 at the root)
+    int32_t seq;                   // round number stamped on the records
     int64_t child_depth;
     int64_t *out_feature, *out_thr_bin, *out_left, *out_right, *out_depth;
 };
@@ -754,15 +754,20 @@ __device__ void ref_pick(const float* __restrict__ hist, size_t hsz, int node0, 
         }
         const float v = (float)(-A.lr * G / (H + A.lam));
         A.out_value[node] = v;
-        ChildRes& r = A.res->c[c];
+        // A.res is host memory mapped for the device: the record's fields,
+        // a system-scope fence, then the round number the host waits for
+        volatile ChildRes& r = A.res->c[c];
         r.gain = bf < 0 ? -INFINITY : best_true;
         r.f = bf;
         r.b = bb;
         r.value = v;
         if (c == 0) {
-            A.res->mid = A.job ? A.job->s + A.job->nl : 0;
-            A.res->build_left = A.job ? A.job->build_left : 0;
+            volatile Res* R = A.res;
+            R->mid = A.job ? A.job->s + A.job->nl : 0;
+            R->build_left = A.job ? A.job->build_left : 0;
         }
+        __threadfence_system();
+        r.seq = A.seq;
     }
     __syncthreads();
 }
@@ -1054,7 +1059,7 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
     const int N = 2 * max_leaves + 1;
 
     Res* h_res = nullptr;
-    hipError_t he = hipHostMalloc((void**)&h_res, sizeof(Res), hipHostMallocDefault);
+    hipError_t he = hipHostMalloc((void**)&h_res, sizeof(Res), hipHostMallocMapped | hipHostMallocCoherent);
     if (he != hipSuccess) return hip_fail(he, "yabt_grow_ref: pinned result buffer");
     struct Free {
         Res* p;
@@ -1080,10 +1085,34 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
     std::vector<int64_t> node_start(N, 0), node_end(N, 0), node_depth(N, 0);
     std::vector<int64_t> leaf_node(N), leaf_f(N), leaf_b(N);
     std::vector<float> leaf_gain(N);
-    auto sync_res = [&]() -> int {
-        hipError_t e = hipMemcpyAsync(h_res, w.res, sizeof(Res), hipMemcpyDeviceToHost, stream);
-        if (e == hipSuccess) e = hipStreamSynchronize(stream);
-        return e == hipSuccess ? 0 : hip_fail(e, "yabt_grow_ref: result copy");
+    Res* d_res = nullptr;   // the device's address of h_res
+    he = hipHostGetDevicePointer((void**)&d_res, h_res, 0);
+    if (he != hipSuccess) return hip_fail(he, "yabt_grow_ref: mapped result buffer");
+    h_res->c[0].seq = h_res->c[1].seq = -1;
+    // The pick writes each child's record into h_res and stamps it with the
+    // round number last; the host spins on the stamps (checking the stream
+    // for errors, and for completion without a stamp) instead of a copy and
+    // a stream synchronisation.
+    auto sync_res = [&](int32_t seq, int children) -> int {
+        volatile Res* R = h_res;
+        for (uint64_t spin = 0;; ++spin) {
+            bool ok = true;
+            for (int c = 0; c < children; ++c) ok = ok && R->c[c].seq == seq;
+            if (ok) {
+                std::atomic_thread_fence(std::memory_order_acquire);
+                return 0;
+            }
+            if ((spin & 1023) == 1023) {
+                const hipError_t e = hipStreamQuery(stream);
+                if (e == hipSuccess) {
+                    ok = true;
+                    for (int c = 0; c < children; ++c) ok = ok && R->c[c].seq == seq;
+                    if (ok) return 0;
+                    return fail(-4, "yabt_grow_ref: stream finished without the split result");
+                }
+                if (e != hipErrorNotReady) return hip_fail(e, "yabt_grow_ref: split");
+            }
+        }
     };
 
     // root
@@ -1093,7 +1122,8 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
     A.lr = lr;
     A.lam = (double)lam;
     A.out_value = out_value;
-    A.res = w.res;
+    A.res = d_res;
+    A.seq = 0;
     A.job = nullptr;
     A.nid = -1;
     A.split_f = A.split_b = 0;
@@ -1107,7 +1137,7 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
     k_scan_pick<<<1, WAVE, 0, stream>>>(w.hist, g.hsz, 0, 0, F, w.fsel, w.fgain, w.fb, A);
     int rc = launch_status("yabt_grow_ref launch");
     if (rc) return rc;
-    if ((rc = sync_res())) return rc;
+    if ((rc = sync_res(0, 1))) return rc;
     double g0 = h_res->c[0].gain;
     if (0 >= max_depth) g0 = -INFINITY;
     leaf_node[0] = 0;
@@ -1147,6 +1177,7 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
         // the other is parent - built (grow.c:361,368)
         g.hist(w.job, m / 2, nl, nr, w.G, w.H);
         A.job = w.job;
+        A.seq = n_leaves;               // 1, 2, ... one per split
         A.nid = nid;
         A.split_f = f;
         A.split_b = b;
@@ -1155,7 +1186,7 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
                                                         w.fb, A);
         k_scan_pick<<<2, WAVE, 0, stream>>>(w.hist, g.hsz, nl, nr, F, w.fsel, w.fgain, w.fb, A);
         if ((rc = launch_status("yabt_grow_ref launch"))) return rc;
-        if ((rc = sync_res())) return rc;
+        if ((rc = sync_res(A.seq, 2))) return rc;
         const int64_t mid = h_res->mid;
         node_start[nl] = s;
         node_end[nl] = mid;
