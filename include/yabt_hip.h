@@ -201,11 +201,18 @@ int yabt_grow_levelwise(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bi
                         int64_t *out_depth, int64_t *out_leaf_of_row, int32_t *out_status,
                         yabt_stream_t stream);
 
-/* Bytes of device workspace yabt_grow_ref needs for (n, F, max_leaves), with
- * sparse != 0 when it is called with default bins (the sparse builder);
- * about n * F * (2 + 2 * sparse) bytes plus the (2L+1, 3, F, 256) fp32
- * histograms. */
+/* Bytes of device workspace yabt_grow_ref is meant to get for (n, F,
+ * max_leaves), with sparse != 0 when it is called with default bins (the
+ * sparse builder): the per-tile bucket lists of every feature at once, about
+ * n * F * (2 + 2 * sparse) bytes, while those stay within 8 GiB (else of as
+ * many features as fit), plus the (2L+1, 3, F, 256) fp32 histograms. */
 size_t yabt_grow_ref_workspace_bytes(int64_t n, int F, int max_leaves, int sparse);
+
+/* The smallest workspace yabt_grow_ref accepts: bucket lists of one feature
+ * at a time.  Any size from this one up works; yabt_grow_ref buckets as many
+ * features per pass as the workspace it is given holds (the result does not
+ * depend on it). */
+size_t yabt_grow_ref_workspace_min_bytes(int64_t n, int F, int max_leaves, int sparse);
 
 /* Grow one best-first tree with the reference's own arithmetic: the same
  * trees as `cgrow` (yabt/_cgrow/grow.c:243-427) bit for bit -- fp32

@@ -282,3 +282,37 @@ def test_sparse_regressor_matches_reference_golden():
     v = np.concatenate([t.value.cpu().numpy() for t in est.booster_.trees])
     assert np.array_equal(v.view(np.uint32), d["value"].view(np.uint32))
     assert np.abs(est.predict(Xt) - d["pred"]).max() <= 1e-5
+
+
+@pytest.mark.parametrize("sparse", [False, True])
+def test_feature_groups_give_the_same_tree(sparse):
+    """A workspace of the minimum size (one feature bucketed per pass) or of a
+    few features' lists gives the tree of the full workspace, bit for bit."""
+    from yabt_amd import _lib
+    rng = np.random.default_rng(21)
+    n, F = 30_000, 7
+    bins = skewed_bins(rng, n, F) if sparse else uniform_bins(rng, n, F)
+    g, h = grad_hess(rng, n, "laplace")
+    lay = G.make_layouts(torch.from_numpy(bins), DEV)
+    db = np.zeros(F, np.int32) if sparse else None
+    kw = dict(lam=1.0, gamma=0.0, mcw=1e-3, msl=20, lr=0.1, max_leaves=40, max_depth=64, fmask=None, imat=None,
+              ib=0.5, default_bin=db)
+    lib = _lib.load()
+    lo = int(lib.yabt_grow_ref_workspace_min_bytes(n, F, 40, int(sparse)))
+    full = int(lib.yabt_grow_ref_workspace_bytes(n, F, 40, int(sparse)))
+    assert 0 < lo < full
+    trees = []
+    for size in (None, lo, lo + (full - lo) // 3):
+        res = G._grow_device_ref(lay, torch.from_numpy(g).to(DEV), torch.from_numpy(h).to(DEV),
+                                 np.full(F, 256, np.int32), workspace_bytes=size, **kw)
+        trees.append((_arrays(res), res.leaf_of_row.cpu().numpy()))
+    for t, leaf in trees[1:]:
+        assert tree_arrays_equal(t, trees[0][0]) is None
+        assert np.array_equal(leaf, trees[0][1])
+    with pytest.raises(RuntimeError, match="workspace too small"):
+        G._grow_device_ref(lay, torch.from_numpy(g).to(DEV), torch.from_numpy(h).to(DEV),
+                           np.full(F, 256, np.int32), workspace_bytes=lo - 1, **kw)
+
+
+def _arrays(res):
+    return {k: getattr(res, k).cpu().numpy() for k in ("feature", "thr_bin", "left", "right", "value", "depth")}

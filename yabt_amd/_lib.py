@@ -57,6 +57,7 @@ SIGNATURES = {
                                    _flt, _flt, _flt, _int, _flt, _int, _int, _vp, _sz,
                                    _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "yabt_grow_ref_workspace_bytes": (_sz, [_i64, _int, _int, _int]),
+    "yabt_grow_ref_workspace_min_bytes": (_sz, [_i64, _int, _int, _int]),
     "yabt_grow_ref": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _vp, _i64, _int,
                              _flt, _flt, _flt, _int, _flt, _int, _int, _vp, _sz,
                              _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),

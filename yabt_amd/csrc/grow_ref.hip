@@ -84,10 +84,11 @@ struct Ws {
     uint32_t* blk;                 // per-block left counts, then their exclusive prefix
     float* G;
     float* H;
-    uint16_t* perm;                // (F, ld_perm): per tile, positions bucketed by bin
-    uint16_t* xperm;               // (F, ld_perm): sparse builder, per tile, rows outside the default bin
-    uint16_t* starts;              // (F, n_tiles, 257): per tile, bucket starts
+    uint16_t* perm;                // (fgroup, ld_perm): per tile, positions bucketed by bin
+    uint16_t* xperm;               // (fgroup, ld_perm): sparse builder, per tile, rows outside the default bin
+    uint16_t* starts;              // (fgroup, n_tiles, 257): per tile, bucket starts
     int64_t n_tiles, ld_perm;
+    int fgroup;                    // features bucketed per pass
     double* expl;                  // (F, 3): sparse builder's explicit g, h sums, default-bin rows
     double* tot;                   // (2): sparse builder's node g, h sums
     float* hist;                   // (N, 3, F, 256)
@@ -100,13 +101,15 @@ struct Ws {
     size_t bytes;
 };
 
-Ws carve(char* base, int64_t n, int F, int max_leaves, bool sparse) {
+// The workspace for feature groups of fgroup features.
+Ws carve(char* base, int64_t n, int F, int max_leaves, bool sparse, int fgroup) {
     Carve c{base, 0};
     Ws w;
     const int64_t N = 2 * (int64_t)max_leaves + 1;
     const int64_t nn = n > 0 ? n : 1;
     w.n_tiles = (nn + WT - 1) / WT;
     w.ld_perm = w.n_tiles * WT;
+    w.fgroup = fgroup;
     w.rows = c.take<uint32_t>(nn);
     w.rows_tmp = c.take<uint32_t>(nn);
     w.flag = c.take<uint8_t>(nn);
@@ -116,9 +119,9 @@ Ws carve(char* base, int64_t n, int F, int max_leaves, bool sparse) {
     w.blk = c.take<uint32_t>((nn + PT - 1) / PT + 1);
     w.G = c.take<float>(nn);
     w.H = c.take<float>(nn);
-    w.perm = c.take<uint16_t>((size_t)F * (size_t)w.ld_perm);
-    w.xperm = sparse ? c.take<uint16_t>((size_t)F * (size_t)w.ld_perm) : nullptr;
-    w.starts = c.take<uint16_t>((size_t)F * (size_t)w.n_tiles * ST);
+    w.perm = c.take<uint16_t>((size_t)fgroup * (size_t)w.ld_perm);
+    w.xperm = sparse ? c.take<uint16_t>((size_t)fgroup * (size_t)w.ld_perm) : nullptr;
+    w.starts = c.take<uint16_t>((size_t)fgroup * (size_t)w.n_tiles * ST);
     w.expl = c.take<double>(3 * (size_t)F);
     w.tot = c.take<double>(2);
     w.hist = c.take<float>((size_t)N * 3 * F * NB);
@@ -130,6 +133,28 @@ Ws carve(char* base, int64_t n, int F, int max_leaves, bool sparse) {
     w.job = c.take<Job>(1);
     w.bytes = c.off;
     return w;
+}
+
+// The recommended feature group: every feature at once while the bucket
+// buffers stay within GROUP_BUDGET bytes, else as many as fit.
+constexpr size_t GROUP_BUDGET = (size_t)8 << 30;
+
+int recommended_group(int64_t n, int F, int max_leaves, bool sparse) {
+    const size_t one = carve(nullptr, n, F, max_leaves, sparse, 1).bytes;
+    const size_t two = carve(nullptr, n, F, max_leaves, sparse, 2).bytes;
+    const size_t per = two - one;                  // bucket buffers of one more feature (+ alignment)
+    return (int)max((size_t)1, min((size_t)F, GROUP_BUDGET / max(per, (size_t)1)));
+}
+
+// The largest feature group whose workspace fits in `bytes` (0: none does).
+int group_for(size_t bytes, int64_t n, int F, int max_leaves, bool sparse) {
+    int lo = 0, hi = F;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) / 2;
+        if (carve(nullptr, n, F, max_leaves, sparse, mid).bytes <= bytes) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
 }
 
 // ---------------------------------------------------------------------------
@@ -329,7 +354,7 @@ template <bool ROOT, bool SPARSE>
 __global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bins_fm, int64_t ld_fm,
                                                   const uint8_t* __restrict__ bins_rm, int64_t ld_rm,
                                                   const uint32_t* __restrict__ rows, const Job* __restrict__ job,
-                                                  int64_t n, const int32_t* __restrict__ dbin,
+                                                  int64_t n, int fg0, const int32_t* __restrict__ dbin,
                                                   uint16_t* __restrict__ perm, uint16_t* __restrict__ xperm,
                                                   int64_t ld_perm, uint16_t* __restrict__ starts, int64_t n_tiles) {
     __shared__ uint8_t s_bin[WT];
@@ -340,7 +365,7 @@ __global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bi
     __shared__ uint32_t s_scan[SW];
     __shared__ uint32_t s_xoff[SW + 1];
     const Seg sg = seg_of(job, n);
-    const int f = blockIdx.x;
+    const int fl = blockIdx.x, f = fg0 + fl;       // buffers by group position, bins by feature
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
     const int df = SPARSE ? dbin[f] : -1;
     for (int64_t t = blockIdx.y; t * WT < sg.m; t += gridDim.y) {
@@ -384,7 +409,7 @@ __global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bi
     if (SPARSE && lane == 0) s_xoff[w] = xrun;
     __syncthreads();
     // bucket starts (sparse: no room for the default bin) and wave bases
-    uint16_t* st_out = starts + ((size_t)f * (size_t)n_tiles + (size_t)t) * ST;
+    uint16_t* st_out = starts + ((size_t)fl * (size_t)n_tiles + (size_t)t) * ST;
     {
         const int b = tid;
         uint32_t c[SW];
@@ -427,10 +452,10 @@ __global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bi
     }
     __syncthreads();
     const int total = SPARSE ? (int)s_xoff[SW] : tn;
-    uint16_t* po = perm + (size_t)f * (size_t)ld_perm + (size_t)t0;
+    uint16_t* po = perm + (size_t)fl * (size_t)ld_perm + (size_t)t0;
     for (int k = tid; k < total; k += RB) po[k] = s_perm[k];
     if (SPARSE) {
-        uint16_t* xo = xperm + (size_t)f * (size_t)ld_perm + (size_t)t0;
+        uint16_t* xo = xperm + (size_t)fl * (size_t)ld_perm + (size_t)t0;
         for (int k = tid; k < total; k += RB) xo[k] = s_xperm[k];
     }
     __syncthreads();
@@ -522,7 +547,7 @@ __device__ __forceinline__ void chain_load(ChainTile& c, const float* __restrict
 // k_hist_default combines them.  G, H hold the node's g, h by position.
 template <bool SPARSE>
 __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ G, const float* __restrict__ H,
-                                                   const Job* __restrict__ job, int64_t n, int F,
+                                                   const Job* __restrict__ job, int64_t n, int F, int fg0, int nf,
                                                    const int32_t* __restrict__ dbin,
                                                    const uint16_t* __restrict__ perm,
                                                    const uint16_t* __restrict__ xperm, int64_t ld_perm,
@@ -536,10 +561,10 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ G, 
     const Seg sg = seg_of(job, n);
     const int64_t m = sg.m;
     const int tid = threadIdx.x;
-    const int f = blockIdx.x;
-    const bool totals = SPARSE && f == F;
+    const int fl = blockIdx.x, f = fg0 + fl;       // buffers by group position, cells by feature
+    const bool totals = SPARSE && fl == nf;        // the extra block of the first group
     const int df = (SPARSE && !totals) ? dbin[f] : -1;
-    const size_t fo = (size_t)(totals ? 0 : f);
+    const size_t fo = (size_t)(totals ? 0 : fl);
     const uint16_t* pf = perm + fo * (size_t)ld_perm;
     const uint16_t* xf = SPARSE ? xperm + fo * (size_t)ld_perm : nullptr;
     const uint16_t* sf = starts + fo * (size_t)n_tiles * ST;
@@ -981,24 +1006,30 @@ struct Grower {
     // With default bins, the sparse builder's arithmetic (grow.c:68-107).
     void hist(const Job* job, int64_t m_max, int slot_l, int slot_r, const float* G, const float* H) {
         const int64_t tiles = min((int64_t)65535, max((int64_t)1, (m_max + WT - 1) / WT));
-        const dim3 sgrid((unsigned)F, (unsigned)tiles);
         const uint32_t* rows = w.rows;
-#define YABT_SORT(ROOT, SPARSE)                                                                                     \
-    k_walk_sort<ROOT, SPARSE><<<sgrid, RB, 0, st>>>(bins_fm, ld_fm, bins_rm, ld_rm, rows, job, n, dbin, w.perm, w.xperm, \
-                                                    w.ld_perm, w.starts, w.n_tiles)
-        if (!job) {
-            if (dbin) YABT_SORT(true, true); else YABT_SORT(true, false);
-        } else {
-            if (dbin) YABT_SORT(false, true); else YABT_SORT(false, false);
-        }
+        for (int fg0 = 0; fg0 < F; fg0 += w.fgroup) {
+            const int nf = min(w.fgroup, F - fg0);
+            const dim3 sgrid((unsigned)nf, (unsigned)tiles);
+#define YABT_SORT(ROOT, SPARSE)                                                                                      \
+    k_walk_sort<ROOT, SPARSE><<<sgrid, RB, 0, st>>>(bins_fm, ld_fm, bins_rm, ld_rm, rows, job, n, fg0, dbin, w.perm, \
+                                                    w.xperm, w.ld_perm, w.starts, w.n_tiles)
+            if (!job) {
+                if (dbin) YABT_SORT(true, true); else YABT_SORT(true, false);
+            } else {
+                if (dbin) YABT_SORT(false, true); else YABT_SORT(false, false);
+            }
 #undef YABT_SORT
-        const unsigned cgrid = (unsigned)F + (dbin ? 1u : 0u);
-        if (dbin)
-            k_walk_chain<true><<<cgrid, RB, 0, st>>>(G, H, job, n, F, dbin, w.perm, w.xperm, w.ld_perm, w.starts,
-                                                     w.n_tiles, w.hist, hsz, slot_l, slot_r, w.expl, w.tot);
-        else
-            k_walk_chain<false><<<cgrid, RB, 0, st>>>(G, H, job, n, F, dbin, w.perm, w.xperm, w.ld_perm, w.starts,
-                                                      w.n_tiles, w.hist, hsz, slot_l, slot_r, w.expl, w.tot);
+            // the sparse builder's node totals: one more block with the first group
+            const unsigned cgrid = (unsigned)nf + (dbin && fg0 == 0 ? 1u : 0u);
+            if (dbin)
+                k_walk_chain<true><<<cgrid, RB, 0, st>>>(G, H, job, n, F, fg0, nf, dbin, w.perm, w.xperm, w.ld_perm,
+                                                         w.starts, w.n_tiles, w.hist, hsz, slot_l, slot_r, w.expl,
+                                                         w.tot);
+            else
+                k_walk_chain<false><<<cgrid, RB, 0, st>>>(G, H, job, n, F, fg0, nf, dbin, w.perm, w.xperm,
+                                                          w.ld_perm, w.starts, w.n_tiles, w.hist, hsz, slot_l, slot_r,
+                                                          w.expl, w.tot);
+        }
         if (dbin)
             k_hist_default<<<(F + RB - 1) / RB, RB, 0, st>>>(dbin, w.expl, w.tot, F, w.hist, hsz, job, slot_l, slot_r);
     }
@@ -1014,7 +1045,12 @@ extern "C" {
 
 size_t yabt_grow_ref_workspace_bytes(int64_t n, int F, int max_leaves, int sparse) {
     if (n < 0 || n > 0xFFFFFFFFll || F < 1 || max_leaves < 1 || max_leaves > 32767) return 0;
-    return carve(nullptr, n, F, max_leaves, sparse != 0).bytes;
+    return carve(nullptr, n, F, max_leaves, sparse != 0, recommended_group(n, F, max_leaves, sparse != 0)).bytes;
+}
+
+size_t yabt_grow_ref_workspace_min_bytes(int64_t n, int F, int max_leaves, int sparse) {
+    if (n < 0 || n > 0xFFFFFFFFll || F < 1 || max_leaves < 1 || max_leaves > 32767) return 0;
+    return carve(nullptr, n, F, max_leaves, sparse != 0, 1).bytes;
 }
 
 int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm, const float* grad,
@@ -1031,8 +1067,9 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
         return fail(-2, "yabt_grow_ref: null pointer argument");
     if (n > 0 && (!bins_fm || !bins_rm || ld_fm < n || ld_rm < F || ld_rm % 16 || !aligned16(bins_rm)))
         return fail(-2, "yabt_grow_ref: bins layout (pointer, alignment or leading dimension) invalid");
-    const size_t need = carve(nullptr, n, F, max_leaves, default_bin != nullptr).bytes;
-    if (workspace_bytes < need) return fail(-2, "yabt_grow_ref: workspace too small");
+    const bool sparse = default_bin != nullptr;
+    const int fgroup = group_for(workspace_bytes, n, F, max_leaves, sparse);
+    if (fgroup < 1) return fail(-2, "yabt_grow_ref: workspace too small");
     if (default_bin) {   // the kernels index bin tables with it: check it first
         std::vector<int32_t> db(F);
         hipError_t e = hipMemcpyAsync(db.data(), default_bin, (size_t)F * sizeof(int32_t), hipMemcpyDeviceToHost, stream);
@@ -1051,7 +1088,7 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
     g.hess = hess;
     g.n = n;
     g.F = F;
-    g.w = carve((char*)workspace, n, F, max_leaves, default_bin != nullptr);
+    g.w = carve((char*)workspace, n, F, max_leaves, sparse, fgroup);
     g.hsz = (size_t)3 * F * NB;
     g.dbin = default_bin;
     g.st = stream;

@@ -311,9 +311,12 @@ def _grow_device_level(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, l
 
 
 def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam, gamma, mcw, msl, lr,
-                     max_leaves, max_depth, default_bin=None) -> GrowResult:
+                     max_leaves, max_depth, default_bin=None, workspace_bytes=None) -> GrowResult:
     """yabt_grow_ref: cgrow's arithmetic on the device (synchronous);
-    default_bin selects cgrow's sparse builder."""
+    default_bin selects cgrow's sparse builder.  workspace_bytes (None: the
+    library's recommended size) may be anything from
+    yabt_grow_ref_workspace_min_bytes up: features are bucketed in groups
+    that fit."""
     lib = _lib.load()
     dev = lay.fm.device
     n, F = lay.n, lay.F
@@ -339,6 +342,8 @@ def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam
     nbytes = int(lib.yabt_grow_ref_workspace_bytes(n, F, L, int(db is not None)))
     if nbytes == 0:
         raise ValueError("yabt_grow_ref: invalid sizes")
+    if workspace_bytes is not None:
+        nbytes = int(workspace_bytes)
     key = (dev, "grow_ref")
     ws = _WORKSPACES.get(key)
     if ws is None or ws.numel() < nbytes:
@@ -353,7 +358,7 @@ def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam
         _ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h), _ptr(fm), _ptr(im),
         ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), _ptr(db), n, F,
         ctypes.c_float(float(lam)), ctypes.c_float(float(gamma)), ctypes.c_float(float(mcw)),
-        int(msl), ctypes.c_float(float(lr)), L, int(max_depth), _ptr(ws), ws.numel(),
+        int(msl), ctypes.c_float(float(lr)), L, int(max_depth), _ptr(ws), nbytes,
         _ptr(out_i[0]), _ptr(out_i[1]), _ptr(out_i[2]), _ptr(out_i[3]), _ptr(value), _ptr(out_i[4]),
         _ptr(leaf), _ptr(rows), _ptr(nn), _stream(dev))
     _lib.check(rc, "yabt_grow_ref")
