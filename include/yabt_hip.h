@@ -179,6 +179,35 @@ int yabt_hist_slots(const uint8_t *binned, int64_t ldb, const int64_t *slot, con
                     const float *h, const float *w, int64_t n, int F, int K, void *workspace,
                     size_t workspace_bytes, float *out, int32_t *out_status, yabt_stream_t stream);
 
+/* Bytes of device workspace yabt_grow_batched needs for (n, F, max_leaves);
+ * 0 when the sizes are out of range (max_leaves above 4096). */
+size_t yabt_grow_batched_workspace_bytes(int64_t n, int F, int max_leaves);
+
+/* yabt_grow in rounds: several splits are computed per round (one
+ * partition, one histogram and one scan launch for all of them), and cgrow's
+ * best-first leaf table (yabt/_cgrow/grow.c:321-408) is replayed over the
+ * computed splits to commit them in cgrow's order and numbering.  The next
+ * round is planned by running the table further ahead -- a leaf with a
+ * computed split gives way to its children -- and taking up to 16 leaves
+ * without one, at most 2 uncomputed levels below a committed leaf, while the
+ * leaves committed and taken fit in the leaf budget.  A leaf's split depends
+ * only on its rows, so the node arrays, values and per-row leaf ids are
+ * yabt_grow's bit for bit.  Same arguments and outputs as yabt_grow, plus
+ * out_leaf_of_row (n int64, may be NULL): each row's leaf; out_status holds
+ * 3 int32: the node count (or -1 for a non-finite input), the rounds run and
+ * the splits computed (committed or not).  Requires max_leaves <= 4096.  The
+ * host keeps three rounds in flight (it watches a round counter in mapped
+ * host memory), so the call returns when the tree is grown; it synchronises
+ * `stream`. */
+int yabt_grow_batched(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
+                      const float *grad, const float *hess, const uint8_t *fmask, const float *imat,
+                      float ib, int use_imat, const int32_t *nbins, const int32_t *default_bin,
+                      int64_t n, int F, float lam, float gamma, float mcw, int msl, float lr,
+                      int max_leaves, int max_depth, void *workspace, size_t workspace_bytes,
+                      int64_t *out_feature, int64_t *out_thr_bin, int64_t *out_left,
+                      int64_t *out_right, float *out_value, int64_t *out_depth,
+                      int64_t *out_leaf_of_row, int32_t *out_status, yabt_stream_t stream);
+
 /* Bytes of device workspace yabt_grow_levelwise needs; 0 when the sizes are
  * out of range or max_leaves < 2^max_depth. */
 size_t yabt_grow_levelwise_workspace_bytes(int64_t n, int F, int max_leaves, int max_depth);

@@ -124,6 +124,17 @@ def test_exact_arithmetic_properties(inputs, reference_tree):
         assert not ((b > lo) & (b <= hi)).any()
 
 
+def test_rounds_equal_split_by_split(inputs):
+    """The exact grower with up to 16 splits per round: yabt_grow's tree bit
+    for bit, and the same per-row leaf ids."""
+    lay, gd, hd = inputs[3:]
+    print("yabt_grow_batched and yabt_grow, 10M x 100", flush=True)
+    rr = G.grow_device(lay, gd, hd, NBINS, growth="rounds", **PARAMS)
+    rs = G.grow_device(lay, gd, hd, NBINS, growth="sequential", **PARAMS)
+    assert tree_arrays_equal(_arrays(rr), _arrays(rs)) is None
+    assert torch.equal(G.leaf_ids(rr, N, F, PARAMS["max_leaves"]), G.leaf_ids(rs, N, F, PARAMS["max_leaves"]))
+
+
 # ---------------------------------------------------------------------------
 # depth 6 over 4M rows x 500 features, each bin 0 with probability 0.9 else
 # uniform on 1..255, g ~ Laplace(0, 1), h = 1, 64 leaves

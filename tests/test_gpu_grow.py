@@ -1,4 +1,4 @@
-"""Whole-tree parity of yabt_grow.
+"""Whole-tree parity of yabt_grow and yabt_grow_batched (growth "rounds").
 
 * against the oracle's fixed-point mode: bit-identical node arrays (feature,
   thr_bin, left, right, depth, value bits) and identical per-row leaf ids;
@@ -47,9 +47,11 @@ CASES = [
 ]
 
 
+@pytest.mark.parametrize("growth", ["sequential", "rounds"])
 @pytest.mark.parametrize("dflt", ["auto", None, "modal"], ids=["skip-auto", "no-skip", "skip-every-feature"])
 @pytest.mark.parametrize("case", CASES, ids=lambda c: f"n{c['n']}F{c['F']}L{c['max_leaves']}")
-def test_grow_matches_oracle(case, dflt):
+def test_grow_matches_oracle(case, dflt, growth):
+    print(f"case {case} default_bin {dflt} growth {growth}", flush=True)
     c = dict(case)
     n, F, nb = c.pop("n"), c.pop("F"), c.pop("nb")
     rng = np.random.default_rng(n * 31 + F)
@@ -67,7 +69,7 @@ def test_grow_matches_oracle(case, dflt):
     nbins = np.full(F, nb, np.int32)
     if dflt == "modal":   # skip each feature's most frequent bin, however rare
         dflt = np.array([np.bincount(bins[:, f], minlength=256).argmax() for f in range(F)], np.int32)
-    got, leaf = _grow_gpu(bins, g, h, nbins, default_bin=dflt, **kw)
+    got, leaf = _grow_gpu(bins, g, h, nbins, default_bin=dflt, growth=growth, **kw)
     ref = O.grow(bins.T, g, h, mode=O.MODE_FIXED, nbins=nbins, **kw)
     bad = tree_arrays_equal(got, ref)
     assert bad is None, f"{bad} differs from the fixed-point oracle"
@@ -107,11 +109,12 @@ def test_grow_tree_hip_dropin():
                           O.leaf_of_rows(ref, n))
 
 
-def test_grow_rejects_nonfinite():
+@pytest.mark.parametrize("growth", ["sequential", "rounds"])
+def test_grow_rejects_nonfinite(growth):
     rng = np.random.default_rng(1)
     n, F = 100, 3
     bins = uniform_bins(rng, n, F)
     g, h = grad_hess(rng, n)
     g[7] = np.nan
     with pytest.raises(ValueError):
-        _grow_gpu(bins, g, h, np.full(F, 256, np.int32), max_leaves=4)
+        _grow_gpu(bins, g, h, np.full(F, 256, np.int32), max_leaves=4, growth=growth)

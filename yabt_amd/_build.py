@@ -13,7 +13,7 @@ CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(os.path.dirname(HERE), "include")
 OUT_DIR = os.path.join(HERE, "_lib")
 LIB = os.path.join(OUT_DIR, "libyabt_hip.so")
-SOURCES = ["grow.hip", "grow_level.hip", "grow_ref.hip", "ops.hip", "leaf.hip", "slots.hip", "boost.hip", "binner.hip"]
+SOURCES = ["grow.hip", "grow_batch.hip", "grow_level.hip", "grow_ref.hip", "ops.hip", "leaf.hip", "slots.hip", "boost.hip", "binner.hip"]
 ARCH = "gfx950"
 
 # -ffp-contract=off: no fused multiply-add may change a rounding that the

@@ -1,0 +1,1007 @@
+// Best-first growth in rounds on gfx950: yabt_grow's trees (exact fixed-point
+// sums, cgrow's best-first order, grow.c:243-427) with several splits
+// computed per round.
+//
+// A leaf's best split and the histograms of its children depend only on the
+// leaf's rows, not on when the leaf is split.  So a round computes several
+// splits at once -- one partition launch, one histogram launch over every
+// built child, one scan launch over every child -- and the scan's last block
+// (the controller, one wave, working in LDS) then replays cgrow's leaf table
+// (grow.c:321-408: first maximum of the fp32 gains above 0, left child
+// replaces the split slot, right child appended, node ids in that order)
+// over the computed splits, committing them until the leaf it would split
+// next has no computed split.  It then plans the next round by running the
+// same table further ahead: a leaf whose split is computed (committed or
+// not) gives way to its children, whose best splits are known, and a leaf
+// without one is taken for the round, until KMAX are taken or the leaves
+// committed and taken fill the leaf budget.  Splits are taken at any depth
+// below the committed tree, so in trees grown deep-first (fresh children
+// often beat the older leaves) a round follows every branch one level down.
+//
+// Rows: a node at depth d >= 1 keeps its rows at [s, e) of row list d & 1
+// (the root: the identity), written by its parent's split and intact until
+// the node itself is split (only its ancestors, split before it, and its
+// descendants, split after it, write inside [s, e)).  The rows of a final
+// leaf whose computed split was never committed are the rows of the
+// uncomputed nodes below it; the per-row leaf ids are written from those.
+// Committed splits get exactly yabt_grow's node arrays, values and per-row
+// leaf ids (same sums, same scan, same order); the others are never read.
+//
+// Launches: k_setup, k_setup_finish, k_hist_root, k_scan<true> (root, plans
+// round 1), then per round k_part, k_gather, k_scan<false>, and k_leaf_ids.
+// The controller writes the round count and the done flag to mapped host
+// memory; the host keeps at most LOOKAHEAD rounds in flight and stops when
+// the tree is done.
+//
+// HBM layout: bins feature-major (partitions) and row-major (gathers); two
+// lists of n uint32 row ids; hist: (PEND_PER_LEAF L + KMAX + 1, 3, F, 256)
+// int64 slots, one per computed split plus the root's.
+
+#include "common.h"
+#include "hist.h"
+#include "host.h"
+#include "scan.h"
+#include "yabt_hip.h"
+
+#include <limits.h>
+#include <string.h>
+
+#include <atomic>
+
+namespace yabt {
+namespace rnd {
+
+constexpr int SB = 256;                          // threads of the partition / setup blocks
+constexpr int PART_IPT = 16;                     // rows per thread per partition tile
+constexpr int PART_TILE = SB * PART_IPT;
+constexpr int PART_BLOCKS = 1024;
+constexpr int SCAN_FEATS = 4;                    // features per scan block
+constexpr int KMAX = 16;                         // splits computed per round, at most
+constexpr int GCHUNKS = 64;                      // gather blocks per 16-feature tile
+constexpr int CT = 2 * SCAN_FEATS * WAVE;        // threads of a split-scan block (the controller)
+constexpr int LOOKAHEAD = 3;                     // rounds the host keeps in flight
+constexpr int MAX_LEAVES = 1024;                 // leaf table held in the controller's LDS
+constexpr int PEND_PER_LEAF = 3;                 // computed splits per leaf of the budget, at most
+constexpr int MAX_PEND = PEND_PER_LEAF * MAX_LEAVES + KMAX;
+constexpr int LEAF_BLOCKS = 32;                  // leaf-id blocks per segment
+
+// A computed split.  Leaves of the table name their origin as 2 p + c (child
+// c of split p) or -1 (the root).
+struct Pend {
+    int32_t f, b, build_left, depth;     // depth of the children
+    int32_t parent_slot, new_slot;
+    int32_t child_pend[2];               // the children's computed splits, -1: none
+    int32_t child_node[2];               // the children's node ids once committed, -1: not committed
+    int32_t origin, pad;                 // the split leaf's origin
+    const uint32_t* src;                 // the leaf's rows (null: the identity)
+    uint32_t* dst;                       // the children's rows
+    int64_t s, e, mid;
+    int64_t tot[3], left[3];
+    int64_t* new_hist;                   // the built child's slot
+    unsigned long long cursor[2];        // next write position, left / right
+    ScanRec child[2];                    // the children's best records (b = -1: none)
+};
+
+// What the controller needs of a computed split, packed.
+struct PendSum {
+    float gain[2];                       // the children's table gains (depth cap applied)
+    int32_t child_pend[2];
+};
+
+struct State {
+    int32_t n_nodes, n_leaves, done;
+    int32_t n_round;                     // splits computed this round
+    int32_t n_pend;                      // Pend entries used
+    int32_t round;                       // controllers run
+    uint32_t scan_ticket;
+    int32_t pad;
+    int32_t round_pend[KMAX];            // this round's Pend entries
+    int64_t tile_off[KMAX + 1];          // partition tiles of this round's splits, prefix sums
+    int32_t chunk_off[KMAX + 1];         // gather chunks of this round's built children, prefix sums
+};
+
+// The host's view, in mapped host memory.
+struct Flags {
+    int32_t round;
+    int32_t done;
+    int32_t n_nodes;
+    int32_t status;
+};
+
+struct Args {
+    const uint8_t* bins_fm;
+    int64_t ld_fm;
+    const uint8_t* bins_rm;
+    int64_t ld_rm;
+    const float* grad;
+    const float* hess;
+    const uint8_t* fmask;
+    const float* imat;
+    float ib;
+    int use_imat;
+    const int32_t* nbins;
+    const int32_t* dflt;
+    int64_t n;
+    int F;
+    float lam, gamma, mcw, lr;
+    int msl;
+    int max_leaves, max_depth;
+    int pend_cap;                        // Pend entries (and new slots) available
+    State* st;
+    Quant* q;
+    uint32_t* rows;                      // two lists of rows_ld row ids
+    int64_t rows_ld;
+    int64_t* hist;
+    uint8_t* pend_path;                  // (pend_cap, F) features on the path to each split's children
+    float* gains;                        // the leaf table: fp32 gain, computed split, origin, node id
+    int32_t* leaf_pend;
+    int32_t* leaf_src;
+    int32_t* leaf_node;
+    Pend* pend;
+    PendSum* psum;
+    ScanRec* rec;                        // (KMAX, 2, scan blocks)
+    int64_t* feature;
+    int64_t* thr_bin;
+    int64_t* left;
+    int64_t* right;
+    float* value;
+    int64_t* depth;
+    int32_t* out_status;
+    Flags* flags;                        // device address of the mapped host flags
+};
+
+__device__ __forceinline__ size_t slot_elems(int F) { return (size_t)3 * (size_t)F * NB; }
+
+// ---------------------------------------------------------------------------
+// setup
+// ---------------------------------------------------------------------------
+
+__global__ void __launch_bounds__(SB) k_setup(Args A) {
+    quant_reduce<SB>(A.grad, A.hess, A.n, A.q);
+    const int N = 2 * A.max_leaves + 1;
+    const int64_t tid = (int64_t)blockIdx.x * SB + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * SB;
+    for (int64_t i = tid; i < N; i += stride) {
+        A.feature[i] = LEAF;
+        A.thr_bin[i] = 0;
+        A.left[i] = -1;
+        A.right[i] = -1;
+        A.value[i] = 0.0f;
+        A.depth[i] = 0;
+    }
+    const int64_t ne = (int64_t)slot_elems(A.F);
+    for (int64_t i = tid; i < ne; i += stride) A.hist[i] = 0;
+}
+
+__global__ void k_setup_finish(Args A) {
+    State* st = A.st;
+    quant_finish(A.q, A.n);
+    st->done = 0;
+    st->n_round = 0;
+    st->n_pend = 0;
+    st->round = 0;
+    st->scan_ticket = 0;
+    st->n_nodes = 1;
+    st->n_leaves = 1;
+    if (A.q->nonfinite) {
+        st->done = 1;
+        A.out_status[0] = -1;
+        A.out_status[1] = 0;
+        A.out_status[2] = 0;
+        A.flags->status = -1;
+        A.flags->done = 1;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// partition: every split of the round, tiles grid-strided
+// ---------------------------------------------------------------------------
+
+// Rows of [s, e) with bin <= b go to [s, mid), the others to [mid, e) of the
+// children's row list, through two atomic cursors per split (the order inside
+// a child depends on the schedule, which no exact sum does).  The blocks also
+// clear the round's new histogram slots, which the gather adds into.
+__global__ void __launch_bounds__(SB) k_part(const uint8_t* __restrict__ bins_fm, int64_t ld, int64_t n, State* st,
+                                             Pend* pend, int64_t slot_n) {
+    const int32_t done = st->done, nr = st->n_round;
+    if (done || nr == 0) return;
+    for (int64_t i = (int64_t)blockIdx.x * SB + threadIdx.x; i < (int64_t)nr * slot_n;
+         i += (int64_t)gridDim.x * SB) {
+        const int j = (int)(i / slot_n);
+        pend[st->round_pend[j]].new_hist[i - (int64_t)j * slot_n] = 0;
+    }
+    const int64_t T = st->tile_off[nr];
+    const int w = threadIdx.x / WAVE;
+    __shared__ uint32_t s_cnt[SB / WAVE][2];
+    __shared__ unsigned long long s_base[SB / WAVE][2];
+    for (int64_t t = blockIdx.x; t < T; t += gridDim.x) {
+        int j = 0;
+        while (j + 1 < nr && st->tile_off[j + 1] <= t) ++j;
+        Pend& P = pend[st->round_pend[j]];
+        const int64_t t0 = P.s + (t - st->tile_off[j]) * PART_TILE;
+        const int64_t hi = min(P.e, t0 + PART_TILE);
+        const uint8_t* col = bins_fm + (size_t)P.f * ld;
+        const int b = P.b;
+        const uint32_t* src = P.src;
+        uint32_t* dst = P.dst;
+        uint32_t rid[PART_IPT];
+#pragma unroll
+        for (int k = 0; k < PART_IPT; ++k) {
+            const int64_t i = min(t0 + (int64_t)k * SB + threadIdx.x, hi - 1);
+            rid[k] = src ? min(src[i], (uint32_t)(n - 1)) : (uint32_t)i;   // a row id stays a row id
+        }
+        uint32_t bv[PART_IPT];
+#pragma unroll
+        for (int k = 0; k < PART_IPT; ++k) bv[k] = col[rid[k]];
+        uint32_t left = 0, valid = 0, nl = 0, nv = 0;
+#pragma unroll
+        for (int k = 0; k < PART_IPT; ++k) {
+            const bool v = t0 + (int64_t)k * SB + threadIdx.x < hi;
+            const bool l = v && (int)bv[k] <= b;
+            valid |= (v ? 1u : 0u) << k;
+            left |= (l ? 1u : 0u) << k;
+            nl += (uint32_t)__popcll(__ballot(l));
+            nv += (uint32_t)__popcll(__ballot(v));
+        }
+        if ((threadIdx.x & (WAVE - 1)) == 0) {
+            s_cnt[w][0] = nl;
+            s_cnt[w][1] = nv - nl;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            uint32_t tl = 0, tr = 0;
+            for (int i = 0; i < SB / WAVE; ++i) {
+                tl += s_cnt[i][0];
+                tr += s_cnt[i][1];
+            }
+            unsigned long long bl = atomicAdd(&P.cursor[0], (unsigned long long)tl);
+            unsigned long long br = atomicAdd(&P.cursor[1], (unsigned long long)tr);
+            for (int i = 0; i < SB / WAVE; ++i) {
+                s_base[i][0] = bl;
+                s_base[i][1] = br;
+                bl += s_cnt[i][0];
+                br += s_cnt[i][1];
+            }
+        }
+        __syncthreads();
+        uint64_t pl = s_base[w][0], pr = s_base[w][1];
+#pragma unroll
+        for (int k = 0; k < PART_IPT; ++k) {
+            const bool v = (valid >> k) & 1u, l = (left >> k) & 1u;
+            const uint64_t ml = __ballot(l), mr = __ballot(v && !l);
+            if (l) dst[pl + lane_prefix(ml)] = rid[k];
+            else if (v) dst[pr + lane_prefix(mr)] = rid[k];
+            pl += (uint64_t)__popcll(ml);
+            pr += (uint64_t)__popcll(mr);
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// gather: the built child of every split of the round, (split, chunk) units
+// ---------------------------------------------------------------------------
+
+// Block (tile, u0) takes units u0, u0 + GCHUNKS, ... of the round's flattened
+// chunk list; each unit is one chunk of one built child (hist.h's gather
+// bodies), added into that split's new slot.
+__global__ void __launch_bounds__(HBLOCK) k_gather(const uint8_t* __restrict__ bins_rm, int64_t ld,
+                                                   const float* __restrict__ grad, const float* __restrict__ hess,
+                                                   int F, const Quant* q, const int32_t* __restrict__ dflt,
+                                                   const State* st, const Pend* pend, int wlog) {
+    const int32_t done = st->done, nr = st->n_round;
+    const double scg = q->scg, sch = q->sch;
+    const bool no_h = q->const_h != 0;
+    if (done || nr == 0) return;
+    __shared__ union {
+        HistLds u;
+        HistLdsP p;
+    } L;
+    const int tile = blockIdx.x / GCHUNKS;
+    const int C = st->chunk_off[nr];
+    for (int u = blockIdx.x % GCHUNKS; u < C; u += GCHUNKS) {
+        int j = 0;
+        while (j + 1 < nr && st->chunk_off[j + 1] <= u) ++j;
+        const Pend& P = pend[st->round_pend[j]];
+        const int chunk = u - st->chunk_off[j];
+        const int64_t lo = P.build_left ? P.s : P.mid, hi = P.build_left ? P.mid : P.e;
+        const uint32_t* rows = P.dst;
+        int64_t* out = P.new_hist;
+        if (wlog >= 0) {
+            if (no_h) {
+                if (dflt)
+                    hist_gather_packed<false, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi,
+                                                    out, wlog, tile, chunk);
+                else
+                    hist_gather_packed<false, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi,
+                                                     out, wlog, tile, chunk);
+            } else {
+                if (dflt)
+                    hist_gather_packed<true, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi,
+                                                   out, wlog, tile, chunk);
+                else
+                    hist_gather_packed<true, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi,
+                                                    out, wlog, tile, chunk);
+            }
+        } else if (no_h) {
+            hist_gather_body<false>(L.u, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out, tile, chunk);
+        } else {
+            hist_gather_body<true>(L.u, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out, tile, chunk);
+        }
+        __syncthreads();   // the next unit clears the LDS histogram
+    }
+}
+
+// ---------------------------------------------------------------------------
+// scan + controller
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float node_value(const int64_t tot[3], const Quant* q, float lr, float lam) {
+    const double G = (double)tot[0] * q->ig, H = (double)tot[1] * q->ih;
+    return (float)(-lr * G / (H + lam));
+}
+
+// A child's table gain from its best record: the fp32 gain, -inf if it has
+// no split or sits at the depth cap (grow.c:296-305).
+__device__ __forceinline__ float rec_gain(const ScanRec& r, bool capped) {
+    return (r.b >= 0 && !capped) ? (float)r.gain : -INFINITY;
+}
+
+// LDS written by one lane, then read by the others of the wave.
+__device__ __forceinline__ void wave_sync() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+// First maximum of s_gain[0..na) above 0 (cgrow's strict > from 0.0f, the
+// lowest index on ties), over one wave; -1: none.
+__device__ __forceinline__ int wave_table_argmax(const float* s_gain, int na, int lane) {
+    float key = 0.0f;
+    int idx = INT_MAX;
+    for (int a = lane; a < na; a += WAVE) {
+        const float g = s_gain[a];
+        if (g > key) {
+            key = g;
+            idx = a;
+        }
+    }
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) {
+        const float ok = __shfl_xor(key, d, WAVE);
+        const int oi = __shfl_xor(idx, d, WAVE);
+        if (ok > key || (ok == key && oi < idx)) {
+            key = ok;
+            idx = oi;
+        }
+    }
+    return idx == INT_MAX ? -1 : idx;
+}
+
+// Inclusive prefix sum over the wave.
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T v, int lane) {
+#pragma unroll
+    for (int d = 1; d < WAVE; d <<= 1) {
+        const T o = __shfl_up(v, d, WAVE);
+        if (lane >= d) v += o;
+    }
+    return v;
+}
+
+// A leaf as a split candidate, from its origin (2 p + c, or -1: the root
+// with record *root).
+struct LeafV {
+    int32_t f, b, depth, slot;
+    int64_t s, e, tot[3], left[3];
+};
+
+__device__ __forceinline__ LeafV leaf_view(const Args& A, int src, const ScanRec* root) {
+    LeafV v;
+    const ScanRec* r;
+    if (src < 0) {
+        const Quant* q = A.q;
+        v.depth = 0;
+        v.slot = 0;
+        v.s = 0;
+        v.e = A.n;
+        v.tot[0] = q->tot_g;
+        v.tot[1] = q->const_h ? A.n * q->hq_const : q->tot_h;
+        v.tot[2] = A.n;
+        r = root;
+    } else {
+        const Pend& P = A.pend[src >> 1];
+        const int c = src & 1;
+        v.depth = P.depth;
+        v.slot = ((c == 0) == (P.build_left != 0)) ? P.new_slot : P.parent_slot;
+        v.s = c ? P.mid : P.s;
+        v.e = c ? P.e : P.mid;
+        for (int i = 0; i < 3; ++i) v.tot[i] = c ? P.tot[i] - P.left[i] : P.left[i];
+        r = &P.child[c];
+    }
+    v.f = r->f;
+    v.b = r->b;
+    for (int i = 0; i < 3; ++i) v.left[i] = r->left[i];
+    return v;
+}
+
+// The controller's LDS: cgrow's leaf table (entry a: leaf a), the computed
+// splits' children, and the lists this controller fills.
+struct Table {
+    float gain[MAX_LEAVES];
+    int16_t pend[MAX_LEAVES];            // computed split, -1: none
+    int16_t src[MAX_LEAVES];             // origin
+    int16_t node[MAX_LEAVES];            // node id; while planning: the entry's split after the round
+    uint8_t moved[MAX_LEAVES];           // while planning: the entry no longer holds the committed leaf
+    float cgain[MAX_PEND][2];            // PendSum, per computed split
+    int16_t cpend[MAX_PEND][2];
+    int16_t commit_p[MAX_LEAVES];        // this controller's commits: split, parent node
+    int16_t commit_nid[MAX_LEAVES];
+    int16_t plan_src[KMAX];              // this round's splits: origin
+};
+
+// Node arrays of commit i (split p of node nid, children nl, nl + 1); the
+// parent's value is cleared afterwards (it may be a child of this batch).
+__device__ __forceinline__ void write_commit(const Args& A, int p, int nid, int nl) {
+    Pend& P = A.pend[p];
+    const int nr = nl + 1;
+    int64_t tl[3], tr[3];
+    for (int i = 0; i < 3; ++i) {
+        tl[i] = P.left[i];
+        tr[i] = P.tot[i] - P.left[i];
+    }
+    A.feature[nid] = P.f;
+    A.thr_bin[nid] = P.b;
+    A.left[nid] = nl;
+    A.right[nid] = nr;
+    A.depth[nl] = P.depth;
+    A.depth[nr] = P.depth;
+    A.value[nl] = node_value(tl, A.q, A.lr, A.lam);
+    A.value[nr] = node_value(tr, A.q, A.lr, A.lam);
+    P.child_node[0] = nl;
+    P.child_node[1] = nr;
+}
+
+// The controller, one wave: T holds the table (nn nodes, na leaves) and the
+// np computed splits' children.  Replay cgrow's leaf table over the computed
+// splits, store it, plan the next round (or finish the tree), publish.
+// root: the root's record while the root is an uncomputed leaf (the first
+// controller), else null.
+__device__ void control(const Args& A, Table& T, int nn, int na, int np, const ScanRec* root, int lane) {
+    State* st = A.st;
+    const int L = A.max_leaves;
+    const int nn0 = nn;
+    // replay (grow.c:321-330): commit the best leaf while its split is computed
+    int best = -1, ncm = 0;
+    while (na < L) {
+        best = wave_table_argmax(T.gain, na, lane);
+        if (best < 0 || T.pend[best] < 0) break;
+        const int p = T.pend[best];
+        if (lane == 0) {
+            T.commit_p[ncm] = (int16_t)p;
+            T.commit_nid[ncm] = T.node[best];
+            // left child replaces the split leaf, right child is appended
+            // (grow.c:393-407)
+            T.gain[best] = T.cgain[p][0];
+            T.pend[best] = T.cpend[p][0];
+            T.src[best] = (int16_t)(2 * p);
+            T.node[best] = (int16_t)nn;
+            T.gain[na] = T.cgain[p][1];
+            T.pend[na] = T.cpend[p][1];
+            T.src[na] = (int16_t)(2 * p + 1);
+            T.node[na] = (int16_t)(nn + 1);
+        }
+        nn += 2;
+        ++na;
+        ++ncm;
+        best = -1;
+        wave_sync();
+    }
+    // the commits' node arrays, then the cleared parent values
+    for (int i = lane; i < ncm; i += WAVE) write_commit(A, T.commit_p[i], T.commit_nid[i], nn0 + 2 * i);
+    __threadfence();
+    for (int i = lane; i < ncm; i += WAVE) A.value[T.commit_nid[i]] = 0.0f;
+    // store the table; T.node then holds each entry's split after planning
+    for (int a = lane; a < na; a += WAVE) {
+        A.gains[a] = T.gain[a];
+        A.leaf_src[a] = T.src[a];
+        A.leaf_node[a] = T.node[a];
+        T.node[a] = T.pend[a];
+        T.moved[a] = 0;
+    }
+    wave_sync();
+    int status = 0, j = 0;
+    const int np0 = np;
+    if (best >= 0) {
+        // plan: the table run ahead; entry `best` comes first
+        int nas = na, nls = na;
+        while (nls + j < L && j < KMAX) {
+            const int a = wave_table_argmax(T.gain, nas, lane);
+            if (a < 0) break;
+            const int p = T.pend[a];
+            if (p >= 0) {
+                // a computed split: its children take its place
+                if (lane == 0) {
+                    T.gain[a] = T.cgain[p][0];
+                    T.pend[a] = T.cpend[p][0];
+                    T.src[a] = (int16_t)(2 * p);
+                    T.moved[a] = 1;
+                    T.gain[nas] = T.cgain[p][1];
+                    T.pend[nas] = T.cpend[p][1];
+                    T.src[nas] = (int16_t)(2 * p + 1);
+                    T.moved[nas] = 1;
+                }
+                ++nas;
+                ++nls;
+            } else {
+                // Pend capacity: every controller may need one for the leaf
+                // it is blocked on, at most L - na more; extras keep
+                // np + L - na <= pend_cap - 1 (so the first, j == 0, fits)
+                if (np >= A.pend_cap) {
+                    status = -5;
+                    break;
+                }
+                if (j > 0 && np + L - na > A.pend_cap - 1) break;
+                if (lane == 0) {
+                    T.plan_src[j] = T.src[a];
+                    if (!T.moved[a]) T.node[a] = (int16_t)np;
+                    T.gain[a] = -INFINITY;
+                }
+                ++np;
+                ++j;
+            }
+            wave_sync();
+        }
+    }
+    // this round's splits, one per lane
+    int64_t tiles = 0;
+    int chunks = 0, f = -1, src = -1;
+    if (lane < j) {
+        src = T.plan_src[lane];
+        const int p = np0 + lane;
+        const LeafV Lv = leaf_view(A, src, root);
+        const int64_t cl = Lv.left[2], c = Lv.tot[2], m = Lv.e - Lv.s;
+        const bool build_left = cl <= c - cl;        // the smaller child, ties left (grow.c:355)
+        const int64_t built = build_left ? cl : c - cl;
+        tiles = (m + PART_TILE - 1) / PART_TILE;
+        chunks = built > 0 ? gather_chunks(built) : 0;
+        f = Lv.f;
+        Pend P;
+        P.f = Lv.f;
+        P.b = Lv.b;
+        P.build_left = build_left ? 1 : 0;
+        P.depth = Lv.depth + 1;
+        P.parent_slot = Lv.slot;
+        P.new_slot = p + 1;
+        P.child_pend[0] = P.child_pend[1] = -1;
+        P.child_node[0] = P.child_node[1] = -1;
+        P.origin = src;
+        P.pad = 0;
+        P.src = (Lv.depth == 0) ? nullptr : A.rows + (size_t)(Lv.depth & 1) * A.rows_ld;
+        P.dst = A.rows + (size_t)((Lv.depth + 1) & 1) * A.rows_ld;
+        P.s = Lv.s;
+        P.e = Lv.e;
+        P.mid = Lv.s + cl;
+        for (int i = 0; i < 3; ++i) {
+            P.tot[i] = Lv.tot[i];
+            P.left[i] = Lv.left[i];
+        }
+        P.new_hist = A.hist + (size_t)(p + 1) * slot_elems(A.F);
+        P.cursor[0] = (unsigned long long)P.s;
+        P.cursor[1] = (unsigned long long)P.mid;
+        P.child[0].b = P.child[1].b = -1;
+        A.pend[p] = P;
+        PendSum S;
+        S.gain[0] = S.gain[1] = -INFINITY;
+        S.child_pend[0] = S.child_pend[1] = -1;
+        A.psum[p] = S;
+        st->round_pend[lane] = p;
+        // the split's parent split names it (a committed leaf's entry too,
+        // through the leaf table, below)
+        if (src >= 0) {
+            A.pend[src >> 1].child_pend[src & 1] = p;
+            A.psum[src >> 1].child_pend[src & 1] = p;
+        }
+    }
+    tiles = wave_incl_scan<int64_t>(tiles, lane);
+    chunks = wave_incl_scan<int>(chunks, lane);
+    if (lane < j) {
+        st->tile_off[lane + 1] = tiles;
+        st->chunk_off[lane + 1] = chunks;
+    }
+    if (A.use_imat) {
+        // the children's path: the leaf's path plus its split feature
+        for (int i = 0; i < j; ++i) {
+            const int si = __shfl(src, i, WAVE), fi = __shfl(f, i, WAVE);
+            const uint8_t* pp = si < 0 ? nullptr : A.pend_path + (size_t)(si >> 1) * A.F;
+            uint8_t* out = A.pend_path + (size_t)(np0 + i) * A.F;
+            for (int c = lane; c < A.F; c += WAVE) out[c] = (c == fi) ? (uint8_t)1 : (pp ? pp[c] : (uint8_t)0);
+        }
+    }
+    for (int a = lane; a < na; a += WAVE) A.leaf_pend[a] = T.node[a];
+    const int done = (status < 0 || j == 0) ? 1 : 0;
+    if (lane == 0) {
+        st->n_nodes = nn;
+        st->n_leaves = na;
+        st->n_pend = np;
+        st->tile_off[0] = 0;
+        st->chunk_off[0] = 0;
+        if (status < 0) {
+            A.out_status[0] = status;
+        } else if (done) {
+            A.out_status[0] = nn;
+        }
+        if (done) {
+            A.out_status[1] = st->round + 1;
+            A.out_status[2] = np;
+        }
+        st->done = done;
+        st->n_round = done ? 0 : j;
+        const int r = st->round + 1;
+        st->round = r;
+        // the host's view: fields, then the round number, each after a
+        // system-scope fence
+        volatile Flags* fl = A.flags;
+        fl->n_nodes = nn;
+        fl->done = done;
+        __threadfence_system();
+        fl->round = r;
+    }
+}
+
+// Scan launch: SCAN_FEATS features per block and, for a split round, block y
+// scans both children of the round's split y (wave w: feature w % SCAN_FEATS,
+// child w / SCAN_FEATS).  Each block publishes its best record per child;
+// the last block to take a ticket is the controller.
+template <bool ROOT>
+__global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) {
+    constexpr int NT = ROOT ? SCAN_FEATS * WAVE : CT;
+    constexpr int NC = ROOT ? 1 : 2;
+    State* st = A.st;
+    const Quant* q = A.q;
+    const int32_t done = st->done, nr = ROOT ? 1 : st->n_round;
+    const int y = ROOT ? 0 : blockIdx.y;
+    if (done || y >= nr) return;
+    const bool derive = q->const_h != 0;
+    const int64_t hqc = q->hq_const;
+    const int pidx = ROOT ? 0 : st->round_pend[y];
+    const Pend* P = ROOT ? nullptr : A.pend + pidx;
+    const int bl = ROOT ? 1 : P->build_left;
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+    const int f = blockIdx.x * SCAN_FEATS + (w % SCAN_FEATS);
+    const int c = w / SCAN_FEATS;
+    const bool fok = f < A.F;
+    const int fc = min(f, A.F - 1);
+    const int nb_f = A.nbins[fc];
+    const uint8_t use_f = A.fmask[fc];
+    const int d_f = A.dflt ? A.dflt[fc] : -1;
+    const int nb = fok ? max(0, min(NB, nb_f)) : 0;
+    const bool use = fok && use_f != 0;
+    const int d = fok ? d_f : -1;
+    const ScanParams sp = {(double)A.lam, (double)A.gamma, (double)A.mcw, A.msl};
+    const bool has_h = !derive;
+    const bool built = ROOT || (c == 0) == (bl != 0);
+    int64_t* hp = A.hist + (size_t)(ROOT ? 0 : P->parent_slot) * slot_elems(A.F);
+    int64_t* hn = A.hist + (size_t)(ROOT ? 0 : P->new_slot) * slot_elems(A.F);
+    __shared__ ScanRec s_rec[NT / WAVE];
+    __shared__ int s_last;
+    int64_t g4[4], h4[4], c4[4];
+    if (fok) {
+        int64_t tot[3];
+        if (ROOT) {
+            tot[0] = q->tot_g;
+            tot[1] = derive ? A.n * hqc : q->tot_h;
+            tot[2] = A.n;
+        } else {
+            for (int i = 0; i < 3; ++i) tot[i] = bl ? P->left[i] : P->tot[i] - P->left[i];
+        }
+        load_bins(hn, A.F, f, lane, g4, h4, c4, has_h);
+        fill_default(g4, h4, c4, d, tot, has_h, lane);
+        if (!built) {
+            int64_t pg[4], ph[4], pc[4];
+            load_bins(hp, A.F, f, lane, pg, ph, pc, has_h);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                g4[i] = pg[i] - g4[i];
+                h4[i] = ph[i] - h4[i];
+                c4[i] = pc[i] - c4[i];
+            }
+        }
+        int64_t hs[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) hs[i] = derive ? c4[i] * hqc : h4[i];
+        const float bo = (!ROOT && A.use_imat && use)
+                             ? path_boost(A.pend_path + (size_t)pidx * A.F, A.imat, A.ib, A.F, f, lane)
+                             : 1.0f;
+        int64_t t256[3];
+        ScanRec r = scan_feature(g4, hs, c4, nb, q->ig, q->ih, sp, (double)bo, lane, t256);
+        if (!use) no_split(r);
+        r.f = f;
+        if (lane == 0) s_rec[w] = r;
+    } else if (lane == 0) {
+        no_split(s_rec[w]);
+        s_rec[w].f = -1;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int cc = 0; cc < NC; ++cc) {
+            int bi = cc * SCAN_FEATS;
+            for (int i = 1; i < SCAN_FEATS; ++i) {
+                const ScanRec& o = s_rec[cc * SCAN_FEATS + i];
+                if (rec_beats(o.sel, o.f, o.b, s_rec[bi].sel, s_rec[bi].f, s_rec[bi].b)) bi = cc * SCAN_FEATS + i;
+            }
+            A.rec[((size_t)y * 2 + cc) * gridDim.x + blockIdx.x] = s_rec[bi];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        const uint32_t t = atomicAdd(&st->scan_ticket, 1u);
+        s_last = (t == gridDim.x * (uint32_t)nr - 1);
+    }
+    __syncthreads();
+    const bool last = s_last != 0;
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    // every wave of the block has loaded its bins (barriers above): store
+    if (fok) {
+        if (built) {
+            if (d >= 0 && (d >> 2) == lane) store_bins(hn, A.F, f, lane, g4, h4, c4, has_h);
+        } else {
+            store_bins(hp, A.F, f, lane, g4, h4, c4, has_h);
+        }
+    }
+    if (!last) return;
+    if (threadIdx.x == 0) st->scan_ticket = 0;
+
+    // ---- controller ----
+    __shared__ Table T;
+    if (ROOT) {
+        __shared__ ScanRec s_root;
+        if (w != 0) return;
+        const ScanRec r = wave_best_record(A.rec, gridDim.x, lane);
+        if (lane == 0) {
+            s_root = r;
+            int64_t tot[3] = {q->tot_g, derive ? A.n * hqc : q->tot_h, A.n};
+            A.value[0] = node_value(tot, q, A.lr, A.lam);
+            T.gain[0] = rec_gain(r, 0 >= A.max_depth);
+            T.pend[0] = -1;
+            T.src[0] = -1;
+            T.node[0] = 0;
+        }
+        wave_sync();
+        control(A, T, 1, 1, 0, &s_root, lane);
+    } else {
+        // the round's children: best record over the scan blocks, per child
+        for (int i = w; i < 2 * nr; i += NT / WAVE) {
+            const ScanRec r = wave_best_record(A.rec + (size_t)i * gridDim.x, gridDim.x, lane);
+            if (lane == 0) {
+                const int p = st->round_pend[i / 2];
+                Pend& Pp = A.pend[p];
+                Pp.child[i % 2] = r;
+                T.cgain[p][i % 2] = rec_gain(r, Pp.depth >= A.max_depth);
+            }
+        }
+        const int nn = st->n_nodes, na = st->n_leaves, np = st->n_pend;
+        const int p0 = np - nr;                   // this round's splits: p0 .. np - 1
+        for (int a = threadIdx.x; a < na; a += NT) {
+            T.gain[a] = A.gains[a];
+            T.pend[a] = (int16_t)A.leaf_pend[a];
+            T.src[a] = (int16_t)A.leaf_src[a];
+            T.node[a] = (int16_t)A.leaf_node[a];
+        }
+        for (int p = threadIdx.x; p < np; p += NT) {
+            const PendSum S = A.psum[p];
+            if (p < p0) {
+                T.cgain[p][0] = S.gain[0];
+                T.cgain[p][1] = S.gain[1];
+            }
+            T.cpend[p][0] = (int16_t)S.child_pend[0];
+            T.cpend[p][1] = (int16_t)S.child_pend[1];
+        }
+        __syncthreads();
+        // this round's children's gains, kept for later controllers
+        if (threadIdx.x < 2 * nr) {
+            const int p = p0 + threadIdx.x / 2;
+            A.psum[p].gain[threadIdx.x % 2] = T.cgain[p][threadIdx.x % 2];
+        }
+        if (w != 0) return;
+        control(A, T, nn, na, np, nullptr, lane);
+    }
+}
+
+// out[row] = leaf node id.  Block y < n_pend labels the uncomputed children
+// of computed split y: with the split committed, the child's own node id;
+// otherwise the node id of the final leaf above the split (walking up the
+// uncommitted splits to the committed node they hang from).  Block y ==
+// n_pend labels the root's rows when the root is the only node.
+__global__ void __launch_bounds__(SB) k_leaf_ids(const State* st, const Pend* pend, int64_t n,
+                                                 const int32_t* out_status, int64_t* out) {
+    const int y = blockIdx.y, np = st->n_pend;
+    if (out_status[0] < 1 || y > np) return;
+    if (y == np) {
+        if (out_status[0] != 1) return;
+        for (int64_t i = (int64_t)blockIdx.x * SB + threadIdx.x; i < n; i += (int64_t)gridDim.x * SB) out[i] = 0;
+        return;
+    }
+    const Pend& P = pend[y];
+    const bool committed = P.child_node[0] >= 0;
+    int owner = -1;
+    if (!committed) {
+        int src = P.origin;
+        for (;;) {
+            if (src < 0) {
+                owner = 0;
+                break;
+            }
+            const Pend& Q = pend[src >> 1];
+            if (Q.child_node[0] >= 0) {
+                owner = Q.child_node[src & 1];
+                break;
+            }
+            src = Q.origin;
+        }
+    }
+    for (int c = 0; c < 2; ++c) {
+        if (P.child_pend[c] >= 0) continue;
+        const int64_t label = committed ? P.child_node[c] : owner;
+        const int64_t lo = c ? P.mid : P.s, hi = c ? P.e : P.mid;
+        const uint32_t* rows = P.dst;
+        for (int64_t i = lo + (int64_t)blockIdx.x * SB + threadIdx.x; i < hi; i += (int64_t)gridDim.x * SB)
+            out[rows[i]] = label;
+    }
+}
+
+size_t carve(char* base, int64_t n, int F, int max_leaves, Args* A) {
+    Carve c{base, 0};
+    const size_t N = (size_t)(2 * max_leaves + 1);
+    const int pend_cap = PEND_PER_LEAF * max_leaves + KMAX;
+    Args tmp;
+    Args& a = A ? *A : tmp;
+    a.pend_cap = pend_cap;
+    a.rows_ld = ((n > 0 ? n : 1) + 63) / 64 * 64;
+    a.st = c.take<State>(1);
+    a.q = c.take<Quant>(1);
+    a.rows = c.take<uint32_t>((size_t)2 * (size_t)a.rows_ld);
+    a.hist = c.take<int64_t>((size_t)(pend_cap + 1) * 3 * (size_t)F * NB);
+    a.pend_path = c.take<uint8_t>((size_t)pend_cap * (size_t)F);
+    a.gains = c.take<float>(N);
+    a.leaf_pend = c.take<int32_t>(N);
+    a.leaf_src = c.take<int32_t>(N);
+    a.leaf_node = c.take<int32_t>(N);
+    a.pend = c.take<Pend>((size_t)pend_cap);
+    a.psum = c.take<PendSum>((size_t)pend_cap);
+    a.rec = c.take<ScanRec>((size_t)KMAX * 2 * ((F + SCAN_FEATS - 1) / SCAN_FEATS));
+    return align_up(c.off, 256);
+}
+
+}  // namespace rnd
+}  // namespace yabt
+
+using namespace yabt;
+using namespace yabt::rnd;
+
+extern "C" {
+
+size_t yabt_grow_batched_workspace_bytes(int64_t n, int F, int max_leaves) {
+    if (n < 0 || n > 0xFFFFFFFFll || F < 1 || max_leaves < 1 || max_leaves > MAX_LEAVES) return 0;
+    return carve(nullptr, n, F, max_leaves, nullptr);
+}
+
+int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm,
+                      const float* grad, const float* hess, const uint8_t* fmask, const float* imat, float ib,
+                      int use_imat, const int32_t* nbins, const int32_t* default_bin, int64_t n, int F, float lam,
+                      float gamma, float mcw, int msl, float lr, int max_leaves, int max_depth, void* workspace,
+                      size_t workspace_bytes, int64_t* out_feature, int64_t* out_thr_bin, int64_t* out_left,
+                      int64_t* out_right, float* out_value, int64_t* out_depth, int64_t* out_leaf_of_row,
+                      int32_t* out_status, hipStream_t stream) {
+    if (F < 1 || n < 0 || n > 0xFFFFFFFFll || max_leaves < 1 || max_leaves > MAX_LEAVES)
+        return fail(-2, "yabt_grow_batched: bad sizes (need F >= 1, 0 <= n < 2^32, 1 <= max_leaves <= 1024)");
+    if (ld_fm < n || ld_fm % 16 || ld_rm < F || ld_rm % 16)
+        return fail(-2, "yabt_grow_batched: leading dimensions must be multiples of 16 covering n (bins_fm) and F "
+                        "(bins_rm)");
+    if (!bins_fm || !bins_rm || !grad || !hess || !fmask || !nbins || (use_imat && !imat) || !workspace ||
+        !out_feature || !out_thr_bin || !out_left || !out_right || !out_value || !out_depth || !out_status)
+        return fail(-2, "yabt_grow_batched: null pointer argument");
+    if (!aligned16(bins_fm) || !aligned16(bins_rm) || !aligned16(grad) || !aligned16(hess))
+        return fail(-2, "yabt_grow_batched: bins, grad and hess must be 16-byte aligned");
+    Args A;
+    memset(&A, 0, sizeof A);
+    const size_t need = carve((char*)workspace, n, F, max_leaves, &A);
+    if (workspace_bytes < need) return fail(-2, "yabt_grow_batched: workspace too small");
+    A.bins_fm = bins_fm;
+    A.ld_fm = ld_fm;
+    A.bins_rm = bins_rm;
+    A.ld_rm = ld_rm;
+    A.grad = grad;
+    A.hess = hess;
+    A.fmask = fmask;
+    A.imat = imat;
+    A.ib = ib;
+    A.use_imat = use_imat ? 1 : 0;
+    A.nbins = nbins;
+    A.dflt = default_bin;
+    A.n = n;
+    A.F = F;
+    A.lam = lam;
+    A.gamma = gamma;
+    A.mcw = mcw;
+    A.lr = lr;
+    A.msl = msl;
+    A.max_leaves = max_leaves;
+    A.max_depth = max_depth;
+    A.feature = out_feature;
+    A.thr_bin = out_thr_bin;
+    A.left = out_left;
+    A.right = out_right;
+    A.value = out_value;
+    A.depth = out_depth;
+    A.out_status = out_status;
+
+    Flags* h_flags = nullptr;
+    hipError_t he = hipHostMalloc((void**)&h_flags, sizeof(Flags), hipHostMallocMapped | hipHostMallocCoherent);
+    if (he != hipSuccess) return hip_fail(he, "yabt_grow_batched: mapped flags");
+    // every return waits for the stream first: enqueued controllers write
+    // the flags until the last of them has run
+    struct Free {
+        Flags* p;
+        hipStream_t s;
+        ~Free() {
+            (void)hipStreamSynchronize(s);
+            (void)hipHostFree(p);
+        }
+    } free_flags{h_flags, stream};
+    h_flags->round = -1;
+    h_flags->done = 0;
+    h_flags->n_nodes = 0;
+    h_flags->status = 0;
+    he = hipHostGetDevicePointer((void**)&A.flags, h_flags, 0);
+    if (he != hipSuccess) return hip_fail(he, "yabt_grow_batched: mapped flags");
+
+    const int tiles = (F + HFL - 1) / HFL;
+    k_quant_clear<<<1, 1, 0, stream>>>(A.q);
+    k_setup<<<launch_grid(n, SB * 16, 1024), SB, 0, stream>>>(A);
+    k_setup_finish<<<1, 1, 0, stream>>>(A);
+    const int rc = root_chunks(n, tiles);
+    k_hist_root<<<tiles * rc, HBLOCK, 0, stream>>>(bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, A.dflt, A.q,
+                                                   A.hist, rc, 1, &A.st->done);
+    const int scan_grid = (F + SCAN_FEATS - 1) / SCAN_FEATS;
+    k_scan<true><<<scan_grid, SCAN_FEATS * WAVE, 0, stream>>>(A);
+    int lrc = launch_status("yabt_grow_batched launch");
+    if (lrc) return lrc;
+    const int64_t slot_n = (int64_t)3 * F * NB;
+    const int wlog = pack_window_log2(n);
+    // rounds: at most max_leaves - 1 (one split each); the controller of round
+    // r stamps r + 1 into h_flags->round, so round r may be enqueued once
+    // round r - LOOKAHEAD has finished
+    volatile Flags* fl = h_flags;
+    for (int r = 1; r < max_leaves; ++r) {
+        for (uint64_t spin = 0;; ++spin) {
+            if (fl->done) break;
+            if (fl->round >= r - LOOKAHEAD) break;
+            if ((spin & 1023) == 1023) {
+                const hipError_t e = hipStreamQuery(stream);
+                if (e == hipSuccess) {
+                    if (fl->done || fl->round >= r - LOOKAHEAD) break;
+                    return fail(-4, "yabt_grow_batched: stream finished without the round's result");
+                }
+                if (e != hipErrorNotReady) return hip_fail(e, "yabt_grow_batched: round");
+            }
+        }
+        if (fl->done) break;
+        k_part<<<PART_BLOCKS, SB, 0, stream>>>(bins_fm, ld_fm, n, A.st, A.pend, slot_n);
+        k_gather<<<tiles * GCHUNKS, HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, A.q, A.dflt, A.st, A.pend,
+                                                        wlog);
+        k_scan<false><<<dim3(scan_grid, KMAX), CT, 0, stream>>>(A);
+        if ((lrc = launch_status("yabt_grow_batched launch"))) return lrc;
+    }
+    if (out_leaf_of_row && n > 0) {
+        dim3 grid(LEAF_BLOCKS, A.pend_cap + 1);
+        k_leaf_ids<<<grid, SB, 0, stream>>>(A.st, A.pend, n, out_status, out_leaf_of_row);
+    }
+    if ((lrc = launch_status("yabt_grow_batched launch"))) return lrc;
+    const hipError_t e = hipStreamSynchronize(stream);
+    if (e != hipSuccess) return hip_fail(e, "yabt_grow_batched: synchronisation");
+    // every round commits at least one split, so max_leaves - 1 rounds finish
+    // any tree
+    if (!fl->done) return fail(-4, "yabt_grow_batched: tree not finished after max_leaves - 1 rounds");
+    return 0;
+}
+
+}  // extern "C"

@@ -370,8 +370,9 @@ __host__ __device__ inline int gather_chunks(int64_t m) {
 }
 
 // Histogram of the rows listed at rows[lo:hi], bins gathered from the
-// row-major copy.  Grid: tiles * GATHER_MAX_CHUNKS blocks (chunk-minor); a
-// node uses ceil(m / GATHER_MIN_ROWS) chunks, the other blocks exit at once.
+// row-major copy: chunk `chunk` of the node's rows for features
+// [16 tile, 16 tile + 16).  A node uses gather_chunks(m) chunks; other chunk
+// numbers return at once.
 // Each wave loads the row ids, g and h of its next 64 rows one step ahead, so
 // the dependent row-id -> g/h loads overlap the LDS clear and the adds.
 template <bool HCH>
@@ -379,8 +380,7 @@ __device__ __forceinline__ void hist_gather_body(HistLds& L, const uint8_t* __re
                                                  const float* __restrict__ grad, const float* __restrict__ hess,
                                                  int F, double scg, double sch, const int32_t* __restrict__ dflt,
                                                  const uint32_t* __restrict__ rows, int64_t jlo, int64_t jhi,
-                                                 int64_t* out) {
-    const int tile = blockIdx.x / GATHER_MAX_CHUNKS, chunk = blockIdx.x % GATHER_MAX_CHUNKS;
+                                                 int64_t* out, int tile, int chunk) {
     const int f0 = tile * HFL;
     const int64_t m = jhi - jlo;
     if (f0 >= F || m <= 0) return;
@@ -455,8 +455,7 @@ __device__ __forceinline__ void hist_gather_packed(HistLdsP& L, const uint8_t* _
                                                    const float* __restrict__ grad, const float* __restrict__ hess,
                                                    int F, double scg, double sch, const int32_t* __restrict__ dflt,
                                                    const uint32_t* __restrict__ rows, int64_t jlo, int64_t jhi,
-                                                   int64_t* out, int wlog) {
-    const int tile = blockIdx.x / GATHER_MAX_CHUNKS, chunk = blockIdx.x % GATHER_MAX_CHUNKS;
+                                                   int64_t* out, int wlog, int tile, int chunk) {
     const int f0 = tile * HFL;
     const int64_t m = jhi - jlo;
     if (f0 >= F || m <= 0) return;
@@ -615,6 +614,7 @@ static __global__ __attribute__((unused)) void __launch_bounds__(HBLOCK) k_hist_
     const double scg = q ? q->scg : scg_v, sch = q ? q->sch : sch_v;
     const bool no_h = count_mode && q && q->const_h;
     if (dn || !jb.active) return;
+    const int tile = blockIdx.x / GATHER_MAX_CHUNKS, chunk = blockIdx.x % GATHER_MAX_CHUNKS;
     __shared__ union {
         HistLds u;
         HistLdsP p;
@@ -623,22 +623,22 @@ static __global__ __attribute__((unused)) void __launch_bounds__(HBLOCK) k_hist_
         if (no_h) {
             if (dflt)
                 hist_gather_packed<false, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo,
-                                                jb.hi, jb.out, wlog);
+                                                jb.hi, jb.out, wlog, tile, chunk);
             else
                 hist_gather_packed<false, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo,
-                                                 jb.hi, jb.out, wlog);
+                                                 jb.hi, jb.out, wlog, tile, chunk);
         } else {
             if (dflt)
                 hist_gather_packed<true, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo,
-                                               jb.hi, jb.out, wlog);
+                                               jb.hi, jb.out, wlog, tile, chunk);
             else
                 hist_gather_packed<true, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo,
-                                                jb.hi, jb.out, wlog);
+                                                jb.hi, jb.out, wlog, tile, chunk);
         }
     } else if (no_h) {
-        hist_gather_body<false>(L.u, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi, jb.out);
+        hist_gather_body<false>(L.u, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi, jb.out, tile, chunk);
     } else {
-        hist_gather_body<true>(L.u, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi, jb.out);
+        hist_gather_body<true>(L.u, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi, jb.out, tile, chunk);
     }
 }
 

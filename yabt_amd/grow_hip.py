@@ -169,12 +169,15 @@ class GrowResult:
 
 
 ARITHMETICS = ("exact", "reference")
+GROWTHS = ("auto", "sequential", "levelwise", "rounds")
+ROUNDS_MAX_LEAVES = 1024
 
 
 def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: np.ndarray, *,
                 fmask=None, imat=None, ib: float = 0.5, lam=1.0, gamma=0.0, mcw=1e-3, msl=20,
                 lr=0.1, max_leaves=31, max_depth=64, default_bin="auto",
-                sync: bool = True, arithmetic: str = "exact", batched: bool | None = None) -> GrowResult:
+                sync: bool = True, arithmetic: str = "exact", batched: bool | None = None,
+                growth: str = "auto") -> GrowResult:
     """One grow call on device-resident layouts.  grad/hess must be on the
     layouts' device; parameters are rounded to float32 as ctypes.c_float
     rounds them in the reference (grow_c.py:418-421).
@@ -184,12 +187,16 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
     arithmetic and row order, the same trees as the reference bit for bit,
     one host round trip per split).
 
-    ``batched`` ("exact" only): grow depth by depth (yabt_grow_levelwise) --
-    the same tree, numbered by replaying the best-first order -- which needs
-    max_leaves >= 2^max_depth (the leaf budget cannot bind); None uses it
-    whenever that holds.
+    ``growth`` ("exact" only; every choice gives the same tree bit for bit):
+    "sequential" (yabt_grow, one split per launch triple, all on the
+    device), "levelwise" (yabt_grow_levelwise: depth by depth, needs
+    max_leaves >= 2^max_depth so that the leaf budget cannot bind), "rounds"
+    (yabt_grow_batched: up to 16 splits per round, max_leaves <= 1024), or
+    "auto": levelwise where the budget cannot bind, else rounds, else
+    sequential.  ``batched`` True / False is the older spelling of
+    "levelwise" / "sequential".
 
-    ``default_bin``: with "exact" (not batched) a shortcut that leaves the
+    ``default_bin``: with "exact" (not levelwise) a shortcut that leaves the
     sums unchanged -- "auto" uses the layouts' most frequent bin per feature,
     None disables the skip, or an (F,) int array.  With "reference" it picks
     cgrow's histogram builder: an (F,) array of default bins in [0, 255] is
@@ -203,13 +210,20 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
                                 mcw=mcw, msl=msl, lr=lr, max_leaves=max_leaves, max_depth=max_depth,
                                 default_bin=db)
     can_batch = 0 <= int(max_depth) <= 16 and int(max_leaves) >= (1 << int(max_depth)) and int(max_leaves) <= 65535
-    if batched is None:
-        batched = can_batch and lay.n < 2 ** 31
-    if batched:
+    if batched is not None:
+        growth = "levelwise" if batched else "sequential"
+    if growth not in GROWTHS:
+        raise ValueError(f"growth must be one of {GROWTHS}")
+    if growth == "auto":
+        growth = "levelwise" if can_batch and lay.n < 2 ** 31 else "sequential"
+    if growth == "levelwise":
         if not can_batch:
             raise ValueError("batched growth needs max_leaves >= 2^max_depth and max_depth <= 16")
         return _grow_device_level(lay, grad, hess, nbins, fmask=fmask, imat=imat, ib=ib, lam=lam, gamma=gamma,
                                   mcw=mcw, msl=msl, lr=lr, max_leaves=max_leaves, max_depth=max_depth)
+    rounds = growth == "rounds"
+    if rounds and int(max_leaves) > ROUNDS_MAX_LEAVES:
+        raise ValueError(f"growth in rounds needs max_leaves <= {ROUNDS_MAX_LEAVES}")
     lib = _lib.load()
     dev = lay.fm.device
     n, F = lay.n, lay.F
@@ -233,6 +247,9 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
         db = torch.as_tensor(np.asarray(default_bin, np.int32)).to(dev)
     L = int(max_leaves)
     N = 2 * L + 1
+    if rounds:
+        return _grow_device_rounds(lib, lay, g, h, fm, im, use_imat, nb, db, ib=ib, lam=lam, gamma=gamma,
+                                   mcw=mcw, msl=msl, lr=lr, max_leaves=L, max_depth=max_depth)
     nbytes = int(lib.yabt_grow_workspace_bytes(n, F, L))
     if nbytes == 0:
         raise ValueError("yabt_grow: invalid sizes")
@@ -258,6 +275,42 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
         res.n_nodes = nn
         for k in ("feature", "thr_bin", "left", "right", "value", "depth"):
             setattr(res, k, getattr(res, k)[:nn])
+    return res
+
+
+def _grow_device_rounds(lib, lay: BinLayouts, g, h, fm, im, use_imat, nb, db, *, ib, lam, gamma, mcw, msl, lr,
+                        max_leaves, max_depth) -> GrowResult:
+    """yabt_grow_batched: yabt_grow's tree with up to 16 splits per round
+    (synchronous); per-row leaf ids come with it."""
+    dev = lay.fm.device
+    n, F = lay.n, lay.F
+    L = int(max_leaves)
+    N = 2 * L + 1
+    nbytes = int(lib.yabt_grow_batched_workspace_bytes(n, F, L))
+    if nbytes == 0:
+        raise ValueError("yabt_grow_batched: invalid sizes")
+    ws = _workspace(dev, nbytes)
+    out_i = torch.empty((5, N), dtype=torch.int64, device=dev)
+    value = torch.empty(N, dtype=torch.float32, device=dev)
+    leaf = torch.empty(max(n, 1), dtype=torch.int64, device=dev)
+    status = torch.zeros(3, dtype=torch.int32, device=dev)
+    rc = lib.yabt_grow_batched(
+        _ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h), _ptr(fm), _ptr(im),
+        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), _ptr(db), n, F,
+        ctypes.c_float(float(lam)), ctypes.c_float(float(gamma)), ctypes.c_float(float(mcw)),
+        int(msl), ctypes.c_float(float(lr)), L, int(max_depth), _ptr(ws), ws.numel(),
+        _ptr(out_i[0]), _ptr(out_i[1]), _ptr(out_i[2]), _ptr(out_i[3]), _ptr(value), _ptr(out_i[4]),
+        _ptr(leaf), _ptr(status), _stream(dev))
+    _lib.check(rc, "yabt_grow_batched")
+    k, rounds, computed = (int(v) for v in status.cpu())
+    if k == -1:
+        raise ValueError("yabt_grow: gradients or hessians contain non-finite values")
+    if k < 0:
+        raise RuntimeError(f"yabt_grow_batched failed ({k})")
+    res = GrowResult(out_i[0][:k], out_i[1][:k], out_i[2][:k], out_i[3][:k], value[:k], out_i[4][:k], k, ws,
+                     status)
+    res.leaf_of_row = leaf[:n]
+    res.rounds, res.splits_computed = rounds, computed
     return res
 
 
