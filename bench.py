@@ -72,6 +72,15 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+def growth_of(res) -> str:
+    """Which grower produced ``res``: best-first split by split, or in rounds
+    of several computed splits (with the round count)."""
+    rounds = getattr(res, "rounds", None)
+    if rounds is None:
+        return "sequential"
+    return f"rounds ({rounds} rounds, {res.splits_computed} splits computed)"
+
+
 def node_sizes(feature, left, right, leaf_of_row) -> np.ndarray:
     """Rows per node from per-row leaf ids (children have larger ids)."""
     size = np.bincount(leaf_of_row, minlength=len(feature)).astype(np.int64)
@@ -452,7 +461,8 @@ def main() -> None:
         ms_per_tree = timed(True, args.steps)
     res, net = step(neural)
     torch.cuda.synchronize()
-    res.n_nodes = int(res._status.item())
+    if res.n_nodes is None:
+        res.n_nodes = int(res._status[0].item())
 
     nn = res.n_nodes
     feat = res.feature[:nn].cpu().numpy()
@@ -475,7 +485,7 @@ def main() -> None:
                                + (", linear leaf models (K=8)" if neural else ""),
                    "rows": n, "features": F, "bins": 256, "max_leaves": MAX_LEAVES,
                    "min_samples_leaf": 20, "leaves_grown": int((feat == -1).sum()),
-                   "tree_updates": upd},
+                   "tree_updates": upd, "growth": growth_of(res)},
         "ms_per_tree": round(ms_per_tree, 3), "ms_grow": round(ms_grow, 3),
         "leaf_models_fitted": (int((net.leaf_net_linear.abs().sum(dim=1) > 0).sum()) if neural else 0),
         "root_hist": {"ms": round(root_mean_ms, 4), "ms_median": round(root_med_ms, 4),

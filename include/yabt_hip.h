@@ -180,7 +180,7 @@ int yabt_hist_slots(const uint8_t *binned, int64_t ldb, const int64_t *slot, con
                     size_t workspace_bytes, float *out, int32_t *out_status, yabt_stream_t stream);
 
 /* Bytes of device workspace yabt_grow_batched needs for (n, F, max_leaves);
- * 0 when the sizes are out of range (max_leaves above 4096). */
+ * 0 when the sizes are out of range (max_leaves above 1024). */
 size_t yabt_grow_batched_workspace_bytes(int64_t n, int F, int max_leaves);
 
 /* yabt_grow in rounds: several splits are computed per round (one
@@ -195,7 +195,7 @@ size_t yabt_grow_batched_workspace_bytes(int64_t n, int F, int max_leaves);
  * yabt_grow's bit for bit.  Same arguments and outputs as yabt_grow, plus
  * out_leaf_of_row (n int64, may be NULL): each row's leaf; out_status holds
  * 3 int32: the node count (or -1 for a non-finite input), the rounds run and
- * the splits computed (committed or not).  Requires max_leaves <= 4096.  The
+ * the splits computed (committed or not).  Requires max_leaves <= 1024.  The
  * host keeps three rounds in flight (it watches a round counter in mapped
  * host memory), so the call returns when the tree is grown; it synchronises
  * `stream`. */

@@ -64,11 +64,11 @@ __device__ __forceinline__ uint32_t row_bcast32(uint32_t v) {
     return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, 0x150 + J, 0xf, 0xf, false);
 }
 
+// 64-bit form: one v_mov_b64_dpp (row_newbcast is a 64-bit DPP control on
+// this target).
 template <int J>
 __device__ __forceinline__ uint64_t row_bcast64(uint64_t v) {
-    const uint32_t lo = row_bcast32<J>((uint32_t)v);
-    const uint32_t hi = row_bcast32<J>((uint32_t)(v >> 32));
-    return ((uint64_t)hi << 32) | lo;
+    return (uint64_t)__builtin_amdgcn_mov_dpp((long)v, 0x150 + J, 0xf, 0xf, false);
 }
 
 // DPP move within 16-lane rows; lanes whose source is outside the row read 0.
@@ -128,6 +128,27 @@ __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
     u += dpp64<DPP_ROW_ROR + 1>(u);
     return readlane64((int64_t)u, 0) + readlane64((int64_t)u, 16) + readlane64((int64_t)u, 32) +
            readlane64((int64_t)u, 48);
+}
+
+// Maximum / minimum over the 64 lanes, returned in every lane (row rotations
+// leave each row's result in all of its lanes, then the four rows combine).
+__device__ __forceinline__ float wave_max_f32(float v) {
+    v = fmaxf(v, __uint_as_float(dpp32<DPP_ROW_ROR + 8>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp32<DPP_ROW_ROR + 4>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp32<DPP_ROW_ROR + 2>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp32<DPP_ROW_ROR + 1>(__float_as_uint(v))));
+    const int b = __float_as_int(v);
+    return fmaxf(fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 0)), __int_as_float(__builtin_amdgcn_readlane(b, 16))),
+                 fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 32)), __int_as_float(__builtin_amdgcn_readlane(b, 48))));
+}
+
+__device__ __forceinline__ int wave_min_i32(int v) {
+    v = min(v, (int)dpp32<DPP_ROW_ROR + 8>((uint32_t)v));
+    v = min(v, (int)dpp32<DPP_ROW_ROR + 4>((uint32_t)v));
+    v = min(v, (int)dpp32<DPP_ROW_ROR + 2>((uint32_t)v));
+    v = min(v, (int)dpp32<DPP_ROW_ROR + 1>((uint32_t)v));
+    return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+               min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 
 // Wave-wide exclusive prefix sum.

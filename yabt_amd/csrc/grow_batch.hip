@@ -356,6 +356,9 @@ __device__ __forceinline__ void wave_sync() {
 
 // First maximum of s_gain[0..na) above 0 (cgrow's strict > from 0.0f, the
 // lowest index on ties), over one wave; -1: none.
+// Each lane keeps the first maximum above 0 of its entries (lane, lane + 64,
+// ...); the table's is the lowest index among the lanes holding the wave's
+// maximum.
 __device__ __forceinline__ int wave_table_argmax(const float* s_gain, int na, int lane) {
     float key = 0.0f;
     int idx = INT_MAX;
@@ -366,16 +369,9 @@ __device__ __forceinline__ int wave_table_argmax(const float* s_gain, int na, in
             idx = a;
         }
     }
-#pragma unroll
-    for (int d = WAVE / 2; d > 0; d >>= 1) {
-        const float ok = __shfl_xor(key, d, WAVE);
-        const int oi = __shfl_xor(idx, d, WAVE);
-        if (ok > key || (ok == key && oi < idx)) {
-            key = ok;
-            idx = oi;
-        }
-    }
-    return idx == INT_MAX ? -1 : idx;
+    const float m = wave_max_f32(key);
+    if (!(m > 0.0f)) return -1;
+    return wave_min_i32(key == m ? idx : INT_MAX);
 }
 
 // Inclusive prefix sum over the wave.
@@ -959,8 +955,8 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
     k_setup<<<launch_grid(n, SB * 16, 1024), SB, 0, stream>>>(A);
     k_setup_finish<<<1, 1, 0, stream>>>(A);
     const int rc = root_chunks(n, tiles);
-    k_hist_root<<<tiles * rc, HBLOCK, 0, stream>>>(bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, A.dflt, A.q,
-                                                   A.hist, rc, 1, &A.st->done);
+    launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, A.dflt, A.q, A.hist, 1,
+                     &A.st->done);
     const int scan_grid = (F + SCAN_FEATS - 1) / SCAN_FEATS;
     k_scan<true><<<scan_grid, SCAN_FEATS * WAVE, 0, stream>>>(A);
     int lrc = launch_status("yabt_grow_batched launch");

@@ -172,12 +172,31 @@ __host__ __device__ inline int pack_window_log2(int64_t n) {
     return w >= 10 ? (w > 16 ? 16 : w) : -1;   // 2^10 rows = one block step
 }
 
+// LDS of the streaming root histogram: 256 bins x 32 words of 8 bytes.  Word
+// fl of a bin is sum q(g) of feature f0 + fl (with the h channel), word
+// 16 + fl the packed (q << cb) + 1 of feature f0 + fl.  A bin's words span
+// 256 bytes, so the byte address of an entry is (bin << 8) | (fl << 3)
+// (+ 128 for the packed word): one byte permute of the loaded bin word
+// builds it.  Within the 16 lanes of a row group the 16 features hit 16
+// distinct bank pairs whatever the bins are.
+struct HistLdsR {
+    unsigned long long w[NB * 2 * HFL];
+};
+
+constexpr int ROOT_PW = HFL;                  // word offset of the packed words in a bin row
+
+// Byte J of `word` placed in bits 8..15 over `lo` (bits 0..7).
+template <int J>
+__device__ __forceinline__ uint32_t bin_addr(uint32_t word, uint32_t lo) {
+    return __builtin_amdgcn_perm(word, lo, 0x0c0c0000u | ((4u + J) << 8));
+}
+
 // SKIP: dflt is given (rows in a feature's default bin are not added).
 // Lanes of features >= F read feature f0's column and add into their own LDS
 // columns, which the flush ignores, so the adds need no feature test.  Each
 // wave loads the next step's g, h and bins before adding the current step.
 template <bool HCH, bool SKIP>
-__device__ __forceinline__ void hist_root_packed(HistLdsP& L, const uint8_t* __restrict__ bins_fm, int64_t ld,
+__device__ __forceinline__ void hist_root_packed(HistLdsR& L, const uint8_t* __restrict__ bins_fm, int64_t ld,
                                                  const float* __restrict__ grad, const float* __restrict__ hess,
                                                  int64_t n, int F, double scg, double sch,
                                                  const int32_t* __restrict__ dflt, Quant* q_tot, int64_t* out,
@@ -196,10 +215,9 @@ __device__ __forceinline__ void hist_root_packed(HistLdsP& L, const uint8_t* __r
     const int cb = wlog + 1;
     const uint64_t cmask = ((uint64_t)1 << cb) - 1;
     const int64_t win_steps = (int64_t)1 << (wlog - 10);
-    for (int i = threadIdx.x; i < NB * HFL; i += HBLOCK) {
-        if (HCH) L.g[i] = 0;
-        L.p[i] = 0;
-    }
+    for (int i = threadIdx.x; i < NB * 2 * HFL; i += HBLOCK) L.w[i] = 0;
+    const uint32_t lbase = (uint32_t)fl << 3;
+    char* const lds = reinterpret_cast<char*>(L.w);
     int64_t qa[HENT];
     uint32_t ca[HENT];
 #pragma unroll
@@ -246,20 +264,27 @@ __device__ __forceinline__ void hist_root_packed(HistLdsP& L, const uint8_t* __r
         const uint32_t wv[4] = {bv.x, bv.y, bv.z, bv.w};
 #define YABT_PACK_ADD(J)                                                         \
         {                                                                        \
-            const int at = b * HFL + fl;                                         \
+            char* const at = lds + bin_addr<(J) & 3>(wv[(J) >> 2], lbase);       \
+            unsigned long long* const pw_at = reinterpret_cast<unsigned long long*>(at + 8 * ROOT_PW); \
             if (HCH) {                                                           \
-                atomicAdd(&L.g[at], (unsigned long long)gj);                     \
-                atomicAdd(&L.p[at], (unsigned long long)pj);                     \
+                atomicAdd(reinterpret_cast<unsigned long long*>(at), (unsigned long long)gj); \
+                atomicAdd(pw_at, (unsigned long long)pj);                        \
             } else {                                                             \
-                atomicAdd(&L.p[at], (unsigned long long)gj);                     \
+                atomicAdd(pw_at, (unsigned long long)gj);                        \
             }                                                                    \
         }
 #define YABT_PACK_STEP(J, TAIL)                                                  \
         {                                                                        \
             const uint64_t gj = row_bcast64<J>(gw);                              \
             const uint64_t pj = HCH ? row_bcast64<J>(pw) : 0;                     \
-            const int b = (int)((wv[(J) >> 2] >> (8 * ((J) & 3))) & 0xffu);      \
-            if ((!(TAIL) || (J) < nv) && (!SKIP || b != d)) YABT_PACK_ADD(J)     \
+            if (!(TAIL) || (J) < nv) {                                           \
+                if (SKIP) {                                                      \
+                    const int b = (int)((wv[(J) >> 2] >> (8 * ((J) & 3))) & 0xffu); \
+                    if (b != d) YABT_PACK_ADD(J)                                 \
+                } else {                                                         \
+                    YABT_PACK_ADD(J)                                             \
+                }                                                                \
+            }                                                                    \
         }
         if (r0 + WAVE <= hi) {   // wave-uniform: all 64 rows valid
             constexpr int nv = HFL;
@@ -281,8 +306,9 @@ __device__ __forceinline__ void hist_root_packed(HistLdsP& L, const uint8_t* __r
 #pragma unroll
             for (int k = 0; k < HENT; ++k) {
                 const int i = threadIdx.x + k * HBLOCK;
-                const uint64_t v = L.p[i];
-                L.p[i] = 0;
+                const int pi = (i / HFL) * (2 * HFL) + ROOT_PW + (i % HFL);
+                const uint64_t v = L.w[pi];
+                L.w[pi] = 0;
                 const uint64_t c = v & cmask;
                 qa[k] += (int64_t)(v - c) >> cb;
                 ca[k] += (uint32_t)c;
@@ -308,13 +334,17 @@ __device__ __forceinline__ void hist_root_packed(HistLdsP& L, const uint8_t* __r
         const int fi = f0 + (i % HFL);
         if (fi >= F || ca[k] == 0) continue;
         const size_t at = (size_t)fi * NB + (size_t)(i / HFL);
-        atomicAdd((unsigned long long*)(out + at), HCH ? L.g[i] : (unsigned long long)qa[k]);
+        atomicAdd((unsigned long long*)(out + at),
+                  HCH ? L.w[(i / HFL) * (2 * HFL) + (i % HFL)] : (unsigned long long)qa[k]);
         if (HCH) atomicAdd((unsigned long long*)(out + plane + at), (unsigned long long)qa[k]);
         atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)ca[k]);
     }
 }
 
 // count_mode 0: all three channels; 1: no h channel when q->const_h.
+// SKIP: dflt is given (a separate kernel, so that the loops without the
+// default-bin test are compiled on their own).
+template <bool SKIP>
 static __global__ __attribute__((unused)) void __launch_bounds__(HBLOCK) k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld,
                                                       const float* __restrict__ grad,
                                                       const float* __restrict__ hess, int64_t n, int F,
@@ -328,30 +358,36 @@ static __global__ __attribute__((unused)) void __launch_bounds__(HBLOCK) k_hist_
     if (dn) return;
     __shared__ union {
         HistLds u;
-        HistLdsP p;
+        HistLdsR p;
     } L;
     const int wlog = pack_window_log2(n);
     if (wlog >= 0) {
-        if (no_h) {
-            if (dflt)
-                hist_root_packed<false, true>(L.p, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out,
-                                              chunks, wlog);
-            else
-                hist_root_packed<false, false>(L.p, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out,
-                                               chunks, wlog);
-        } else {
-            if (dflt)
-                hist_root_packed<true, true>(L.p, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out,
-                                             chunks, wlog);
-            else
-                hist_root_packed<true, false>(L.p, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out,
-                                              chunks, wlog);
-        }
+        if (no_h)
+            hist_root_packed<false, SKIP>(L.p, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks,
+                                          wlog);
+        else
+            hist_root_packed<true, SKIP>(L.p, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks,
+                                         wlog);
     } else if (no_h) {
         hist_root_body<false>(L.u, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks);
     } else {
         hist_root_body<true>(L.u, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks);
     }
+}
+
+// Launch k_hist_root over `tiles * chunks` blocks (the instantiation with
+// the default-bin test only when dflt is given).
+static __attribute__((unused)) void launch_hist_root(int tiles, int chunks, hipStream_t stream,
+                                                     const uint8_t* bins_fm, int64_t ld, const float* grad,
+                                                     const float* hess, int64_t n, int F, const Quant* q,
+                                                     double scg, double sch, const int32_t* dflt, Quant* q_tot,
+                                                     int64_t* out, int count_mode, const int32_t* done) {
+    if (dflt)
+        k_hist_root<true><<<tiles * chunks, HBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, dflt,
+                                                                 q_tot, out, chunks, count_mode, done);
+    else
+        k_hist_root<false><<<tiles * chunks, HBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch,
+                                                                  nullptr, q_tot, out, chunks, count_mode, done);
 }
 
 // Rows of one node for a gather launch.

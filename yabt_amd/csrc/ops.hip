@@ -261,8 +261,8 @@ int yabt_hist(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int
     if (!rows) {
         if (n > 0) {
             const int rc = root_chunks(n, tiles);
-            k_hist_root<<<tiles * rc, HBLOCK, 0, stream>>>(bins_fm, ld_fm, grad, hess, n, F, q, 0.0, 0.0, nullptr,
-                                                           nullptr, out, rc, 0, nullptr);
+            launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, q, 0.0, 0.0, nullptr, nullptr, out,
+                             0, nullptr);
         }
     } else if (m > 0) {
         k_set_hist_job<<<1, 1, 0, stream>>>(job, rows, 0, m, out);
@@ -285,8 +285,8 @@ int yabt_hist_accumulate(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* b
     if (!rows) {
         if (n > 0) {
             const int rc = root_chunks(n, tiles);
-            k_hist_root<<<tiles * rc, HBLOCK, 0, stream>>>(bins_fm, ld_fm, grad, hess, n, F, nullptr, scg, sch,
-                                                           nullptr, nullptr, out, rc, 0, nullptr);
+            launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, nullptr, scg, sch, nullptr, nullptr,
+                             out, 0, nullptr);
         }
     } else if (m > 0) {
         Carve c{(char*)workspace, 0};

@@ -215,7 +215,12 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
     if growth not in GROWTHS:
         raise ValueError(f"growth must be one of {GROWTHS}")
     if growth == "auto":
-        growth = "levelwise" if can_batch and lay.n < 2 ** 31 else "sequential"
+        if can_batch and lay.n < 2 ** 31:
+            growth = "levelwise"
+        elif int(max_leaves) <= ROUNDS_MAX_LEAVES and lay.n <= 0xFFFFFFFF:
+            growth = "rounds"
+        else:
+            growth = "sequential"
     if growth == "levelwise":
         if not can_batch:
             raise ValueError("batched growth needs max_leaves >= 2^max_depth and max_depth <= 16")
