@@ -106,7 +106,7 @@ def gpu_inputs(torch, n, F, seed=0):
     gen.manual_seed(seed)
     ld_fm = (n + 15) // 16 * 16
     fm = torch.randint(0, 256, (F, ld_fm), generator=gen, dtype=torch.uint8, device=dev)
-    ld_rm = (F + 15) // 16 * 16
+    ld_rm = G._lib.row_stride(F)
     rm = torch.zeros((n, ld_rm), dtype=torch.uint8, device=dev)
     lib = G._lib.load()
     G._lib.check(lib.yabt_transpose_bins(G._ptr(fm), ld_fm, n, F, G._ptr(rm), ld_rm, G._stream(dev)),

@@ -16,6 +16,16 @@ import threading
 
 from ._build import LIB as LIB_PATH
 
+def row_stride(F: int) -> int:
+    """Bytes per row of the row-major bin layout for F features: 16, 32 or
+    64 for up to 64 features, else a multiple of 128, so that no row straddles
+    a 128-byte cache line and a gathered row costs one line per 128 bytes."""
+    for w in (16, 32, 64):
+        if F <= w:
+            return w
+    return (F + 127) // 128 * 128
+
+
 _LOCK = threading.Lock()
 _LIB = None  # ctypes handle, or False once loading failed
 

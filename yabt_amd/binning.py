@@ -147,7 +147,7 @@ class Binner:
         dev = Xd.device
         n, F = Xd.shape
         fm = torch.zeros((F, max(16, _round16(n))), dtype=torch.uint8, device=dev)
-        rm = torch.zeros((max(n, 1), _round16(F)), dtype=torch.uint8, device=dev)
+        rm = torch.zeros((max(n, 1), _lib.row_stride(F)), dtype=torch.uint8, device=dev)
         imp = torch.empty((n, F), dtype=torch.float32, device=dev)
         if n:
             self._run(Xd, fm=fm, rm=rm, imp=imp)

@@ -63,7 +63,8 @@ constexpr int LOOKAHEAD = 3;                     // rounds the host keeps in fli
 constexpr int MAX_LEAVES = 1024;                 // leaf table held in the controller's LDS
 constexpr int PEND_PER_LEAF = 3;                 // computed splits per leaf of the budget, at most
 constexpr int MAX_PEND = PEND_PER_LEAF * MAX_LEAVES + KMAX;
-constexpr int LEAF_BLOCKS = 32;                  // leaf-id blocks per segment
+constexpr int LEAF_CHUNK = 8192;                 // rows per leaf-id block
+constexpr int LEAF_PLAN = 1024;                  // threads of the leaf-id planning block
 
 // A computed split.  Leaves of the table name their origin as 2 p + c (child
 // c of split p) or -1 (the root).
@@ -98,6 +99,15 @@ struct State {
     int32_t round_pend[KMAX];            // this round's Pend entries
     int64_t tile_off[KMAX + 1];          // partition tiles of this round's splits, prefix sums
     int32_t chunk_off[KMAX + 1];         // gather chunks of this round's built children, prefix sums
+};
+
+// A run of final-leaf rows for the leaf-id pass: positions [lo, hi) of a row
+// list (rows null: the identity) all belong to node `label`; its chunks of
+// LEAF_CHUNK rows are numbered from chunk0.
+struct LeafRun {
+    const uint32_t* rows;
+    int64_t lo, hi;
+    int64_t label;
 };
 
 // The host's view, in mapped host memory.
@@ -140,6 +150,9 @@ struct Args {
     Pend* pend;
     PendSum* psum;
     ScanRec* rec;                        // (KMAX, 2, scan blocks)
+    LeafRun* leaf_runs;                  // 2 pend_cap + 1 runs
+    int32_t* leaf_chunk0;                // their first chunks, then the run count and the chunk count
+    int leaf_chunk_cap;                  // chunks, at most
     int64_t* feature;
     int64_t* thr_bin;
     int64_t* left;
@@ -802,45 +815,134 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
     }
 }
 
-// out[row] = leaf node id.  Block y < n_pend labels the uncomputed children
-// of computed split y: with the split committed, the child's own node id;
-// otherwise the node id of the final leaf above the split (walking up the
-// uncommitted splits to the committed node they hang from).  Block y ==
-// n_pend labels the root's rows when the root is the only node.
-__global__ void __launch_bounds__(SB) k_leaf_ids(const State* st, const Pend* pend, int64_t n,
-                                                 const int32_t* out_status, int64_t* out) {
-    const int y = blockIdx.y, np = st->n_pend;
-    if (out_status[0] < 1 || y > np) return;
-    if (y == np) {
-        if (out_status[0] != 1) return;
-        for (int64_t i = (int64_t)blockIdx.x * SB + threadIdx.x; i < n; i += (int64_t)gridDim.x * SB) out[i] = 0;
+// Leaf-id planning, one block: run 2 p + c is child c of computed split p --
+// empty when that child has a computed split of its own, else labelled with
+// the child's node id when the split is committed, or with the node id of
+// the final leaf above the split (found by walking up the uncommitted splits
+// to the committed node they hang from); with the root alone, one run of the
+// identity.  Each run is numbered with its first chunk of LEAF_CHUNK rows.
+// The run and chunk counts follow the max_runs = 2 pend_cap + 1 entries of
+// leaf_chunk0.
+__global__ void __launch_bounds__(LEAF_PLAN) k_leaf_plan(Args A, int64_t n) {
+    __shared__ int32_t s_cnt[LEAF_PLAN / WAVE + 1];
+    LeafRun* runs = A.leaf_runs;
+    int32_t* chunk0 = A.leaf_chunk0;
+    int32_t* counts = chunk0 + 2 * A.pend_cap + 1;
+    const int np = A.st->n_pend;
+    const int st0 = A.out_status[0];
+    if (st0 < 1 || st0 == 1 || np == 0) {
+        if (threadIdx.x == 0) {
+            const bool root = st0 >= 1;
+            LeafRun r;
+            r.rows = nullptr;
+            r.lo = 0;
+            r.hi = root ? n : 0;
+            r.label = 0;
+            runs[0] = r;
+            chunk0[0] = 0;
+            counts[0] = root ? 1 : 0;
+            counts[1] = root ? (int32_t)((n + LEAF_CHUNK - 1) / LEAF_CHUNK) : 0;
+        }
         return;
     }
-    const Pend& P = pend[y];
-    const bool committed = P.child_node[0] >= 0;
-    int owner = -1;
-    if (!committed) {
-        int src = P.origin;
-        for (;;) {
-            if (src < 0) {
-                owner = 0;
-                break;
+    // thread t owns the runs of splits [t per, (t + 1) per): chunk offsets in
+    // thread order are then in run order
+    const int per = (np + LEAF_PLAN - 1) / LEAF_PLAN;
+    const int p_lo = (int)threadIdx.x * per, p_hi = min(np, p_lo + per);
+    int mine = 0;
+    for (int p = p_lo; p < p_hi; ++p) {
+        const Pend& P = A.pend[p];
+        const int32_t cp0 = P.child_pend[0], cp1 = P.child_pend[1];
+        const int64_t ps = P.s, pm = P.mid, pe = P.e;
+        if (cp0 < 0) mine += (int)((pm - ps + LEAF_CHUNK - 1) / LEAF_CHUNK);
+        if (cp1 < 0) mine += (int)((pe - pm + LEAF_CHUNK - 1) / LEAF_CHUNK);
+    }
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+    const int incl = wave_incl_scan<int>(mine, lane);
+    if (lane == WAVE - 1) s_cnt[w] = incl;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int acc = 0;
+        for (int t = 0; t < LEAF_PLAN / WAVE; ++t) {
+            const int v = s_cnt[t];
+            s_cnt[t] = acc;
+            acc += v;
+        }
+        s_cnt[LEAF_PLAN / WAVE] = acc;
+    }
+    __syncthreads();
+    int at = s_cnt[w] + incl - mine;
+    for (int p = p_lo; p < p_hi; ++p) {
+        const Pend& P = A.pend[p];
+        const int32_t cn0 = P.child_node[0], cn1 = P.child_node[1];
+        const int32_t cp0 = P.child_pend[0], cp1 = P.child_pend[1];
+        const int64_t ps = P.s, pm = P.mid, pe = P.e;
+        const uint32_t* const dst = P.dst;
+        const bool committed = cn0 >= 0;
+        int64_t owner = -1;
+        if (!committed && (cp0 < 0 || cp1 < 0)) {
+            int src = P.origin;
+            for (;;) {
+                if (src < 0) {
+                    owner = 0;
+                    break;
+                }
+                const Pend& Q = A.pend[src >> 1];
+                if (Q.child_node[0] >= 0) {
+                    owner = Q.child_node[src & 1];
+                    break;
+                }
+                src = Q.origin;
             }
-            const Pend& Q = pend[src >> 1];
-            if (Q.child_node[0] >= 0) {
-                owner = Q.child_node[src & 1];
-                break;
-            }
-            src = Q.origin;
+        }
+        for (int c = 0; c < 2; ++c) {
+            const bool run = (c ? cp1 : cp0) < 0;
+            LeafRun r;
+            r.rows = dst;
+            r.lo = c ? pm : ps;
+            r.hi = run ? (c ? pe : pm) : r.lo;
+            r.label = committed ? (c ? cn1 : cn0) : owner;
+            runs[2 * p + c] = r;
+            chunk0[2 * p + c] = at;
+            at += (int)((r.hi - r.lo + LEAF_CHUNK - 1) / LEAF_CHUNK);
         }
     }
-    for (int c = 0; c < 2; ++c) {
-        if (P.child_pend[c] >= 0) continue;
-        const int64_t label = committed ? P.child_node[c] : owner;
-        const int64_t lo = c ? P.mid : P.s, hi = c ? P.e : P.mid;
-        const uint32_t* rows = P.dst;
-        for (int64_t i = lo + (int64_t)blockIdx.x * SB + threadIdx.x; i < hi; i += (int64_t)gridDim.x * SB)
-            out[rows[i]] = label;
+    if (threadIdx.x == 0) {
+        counts[0] = 2 * np;
+        counts[1] = min(s_cnt[LEAF_PLAN / WAVE], A.leaf_chunk_cap);
+    }
+}
+
+// out[row] = leaf node id, one chunk per block (blocks past the chunk count
+// exit): the block's run is the last with chunk0 <= its chunk (binary
+// search); each thread loads its rows' ids eight at a time before storing.
+__global__ void __launch_bounds__(SB) k_leaf_ids(const LeafRun* runs, const int32_t* chunk0, int max_runs,
+                                                 int64_t* out) {
+    const int nruns = chunk0[max_runs], total = chunk0[max_runs + 1];
+    const int b = (int)blockIdx.x;
+    if (b >= total || nruns < 1 || nruns > max_runs) return;
+    int lo = 0, hi = nruns - 1;   // last run with chunk0 <= b
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (chunk0[mid] <= b) lo = mid;
+        else hi = mid - 1;
+    }
+    const LeafRun r = runs[lo];
+    const int64_t c_lo = r.lo + (int64_t)(b - chunk0[lo]) * LEAF_CHUNK;
+    const int64_t c_hi = min(r.hi, c_lo + LEAF_CHUNK);
+    constexpr int U = 8;
+    for (int64_t i0 = c_lo + threadIdx.x; i0 < c_hi; i0 += (int64_t)SB * U) {
+        uint32_t rw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + (int64_t)u * SB;
+            rw[u] = i < c_hi ? (r.rows ? r.rows[i] : (uint32_t)i) : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t i = i0 + (int64_t)u * SB;
+            if (i < c_hi) out[rw[u]] = r.label;
+        }
     }
 }
 
@@ -864,6 +966,10 @@ size_t carve(char* base, int64_t n, int F, int max_leaves, Args* A) {
     a.pend = c.take<Pend>((size_t)pend_cap);
     a.psum = c.take<PendSum>((size_t)pend_cap);
     a.rec = c.take<ScanRec>((size_t)KMAX * 2 * ((F + SCAN_FEATS - 1) / SCAN_FEATS));
+    // chunks: every run is at most one chunk longer than its rows need
+    a.leaf_chunk_cap = (int)((n + LEAF_CHUNK - 1) / LEAF_CHUNK + 2 * (int64_t)pend_cap + 2);
+    a.leaf_runs = c.take<LeafRun>((size_t)2 * pend_cap + 1);
+    a.leaf_chunk0 = c.take<int32_t>((size_t)2 * pend_cap + 3);
     return align_up(c.off, 256);
 }
 
@@ -988,8 +1094,9 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
         if ((lrc = launch_status("yabt_grow_batched launch"))) return lrc;
     }
     if (out_leaf_of_row && n > 0) {
-        dim3 grid(LEAF_BLOCKS, A.pend_cap + 1);
-        k_leaf_ids<<<grid, SB, 0, stream>>>(A.st, A.pend, n, out_status, out_leaf_of_row);
+        k_leaf_plan<<<1, LEAF_PLAN, 0, stream>>>(A, n);
+        k_leaf_ids<<<A.leaf_chunk_cap, SB, 0, stream>>>(A.leaf_runs, A.leaf_chunk0, 2 * A.pend_cap + 1,
+                                                        out_leaf_of_row);
     }
     if ((lrc = launch_status("yabt_grow_batched launch"))) return lrc;
     const hipError_t e = hipStreamSynchronize(stream);

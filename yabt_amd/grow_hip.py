@@ -109,7 +109,7 @@ def make_layouts(binned: torch.Tensor, dev: torch.device,
                  binned_fmajor: np.ndarray | None = None) -> BinLayouts:
     """Device copies of binned (n, F) uint8 in both padded layouts."""
     n, F = binned.shape
-    ld_fm, ld_rm = max(16, _round16(n)), _round16(F)
+    ld_fm, ld_rm = max(16, _round16(n)), _lib.row_stride(F)
     fm = torch.zeros((F, ld_fm), dtype=torch.uint8, device=dev)
     if binned_fmajor is not None:
         fm[:, :n].copy_(torch.from_numpy(np.ascontiguousarray(binned_fmajor, dtype=np.uint8)))
