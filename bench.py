@@ -7,7 +7,8 @@ lambda 1, gamma 0, lr 0.1, identity binner (nbins 256).  Inputs are generated
 on the device and resident in HBM before timing.
 
 A step is one full tree: root histogram, 254 splits (partition + smaller
-child histogram + sibling subtraction + split scans), then the linear leaf
+child histogram + sibling subtraction + split scans; grown in rounds of up
+to 16 computed splits, committed in best-first order), then the linear leaf
 models (K = 8 most used split features, raw input x = float(bin), g and h at
 margin + value[leaf] for a quadratic objective: g + h * value[leaf], h;
 min 50 rows, l2 1).  ``value`` is the tree's histogram work, sum over built
