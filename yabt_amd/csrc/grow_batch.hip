@@ -375,11 +375,22 @@ __device__ __forceinline__ void wave_sync() {
 __device__ __forceinline__ int wave_table_argmax(const float* s_gain, int na, int lane) {
     float key = 0.0f;
     int idx = INT_MAX;
-    for (int a = lane; a < na; a += WAVE) {
-        const float g = s_gain[a];
-        if (g > key) {
-            key = g;
-            idx = a;
+    // four loads in flight before the compares (one LDS round trip per 256
+    // entries, not one per 64)
+    constexpr int U = 4;
+    for (int a0 = lane; a0 < na; a0 += U * WAVE) {
+        float g[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int a = a0 + u * WAVE;
+            g[u] = a < na ? s_gain[a] : -INFINITY;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (g[u] > key) {
+                key = g[u];
+                idx = a0 + u * WAVE;
+            }
         }
     }
     const float m = wave_max_f32(key);
