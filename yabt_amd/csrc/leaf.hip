@@ -35,7 +35,10 @@ namespace yabt {
 
 constexpr int LKMAX = 8;                       // model inputs per leaf, at most
 constexpr int LB = 256;                        // threads per block
-constexpr int LROWS = 4096;                    // rows per stats/scatter block
+constexpr int LSB = 1024;                      // threads per stats/scatter block
+constexpr int LROWS = 4096;                    // rows per stats/scatter block, at least
+constexpr int LROW_BLOCKS = 512;               // stats/scatter blocks, at most: each flushes its
+                                               // node tables once, so fewer blocks flush less
 constexpr int LCHUNK = 4096;                   // sorted positions per gram block
 constexpr int LDS_NODES = 640;                 // node tables kept in LDS up to this many nodes
 
@@ -64,6 +67,7 @@ struct LeafArgs {
     int n_nodes;
     int min_samples;
     double lam;
+    int64_t rows_per_block;    // stats/scatter rows per block
     // workspace
     LeafStats* st;
     uint32_t* count;           // (n_nodes)
@@ -115,28 +119,29 @@ __global__ void __launch_bounds__(LB) k_leaf_init(LeafArgs A, int K) {
     }
 }
 
-// Rows [blockIdx.x * LROWS, +LROWS): counts, envelopes and magnitudes.
+// Rows [blockIdx.x * rows_per_block, +rows_per_block): counts, envelopes and
+// magnitudes.
 template <int K, bool LDS>
-__global__ void __launch_bounds__(LB) k_leaf_stats(LeafArgs A) {
+__global__ void __launch_bounds__(LSB) k_leaf_stats(LeafArgs A) {
     __shared__ uint32_t s_cnt[LDS ? LDS_NODES : 1];
     __shared__ uint32_t s_lo[LDS ? LDS_NODES * K : 1], s_hi[LDS ? LDS_NODES * K : 1];
-    __shared__ float s_red[3][LB / WAVE];
+    __shared__ float s_red[3][LSB / WAVE];
     __shared__ int s_bad;
     __shared__ int32_t s_fs[LKMAX];
     if (threadIdx.x < K) s_fs[threadIdx.x] = A.feats[threadIdx.x];
     if (threadIdx.x == 0) s_bad = 0;
     if (LDS) {
-        for (int i = threadIdx.x; i < A.n_nodes; i += LB) s_cnt[i] = 0;
-        for (int i = threadIdx.x; i < A.n_nodes * K; i += LB) {
+        for (int i = threadIdx.x; i < A.n_nodes; i += LSB) s_cnt[i] = 0;
+        for (int i = threadIdx.x; i < A.n_nodes * K; i += LSB) {
             s_lo[i] = float_key(INFINITY);
             s_hi[i] = float_key(-INFINITY);
         }
     }
     __syncthreads();
-    const int64_t lo = (int64_t)blockIdx.x * LROWS, hi = min(A.n, lo + LROWS);
+    const int64_t lo = (int64_t)blockIdx.x * A.rows_per_block, hi = min(A.n, lo + A.rows_per_block);
     float mg = 0.0f, mh = 0.0f;
     int bad = 0;
-    for (int64_t i = lo + threadIdx.x; i < hi; i += LB) {
+    for (int64_t i = lo + threadIdx.x; i < hi; i += LSB) {
         const int64_t node = A.leaf[i];
         if (node < 0 || node >= A.n_nodes) {
             bad = 1;
@@ -175,7 +180,7 @@ __global__ void __launch_bounds__(LB) k_leaf_stats(LeafArgs A) {
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int i = 1; i < LB / WAVE; ++i) {
+        for (int i = 1; i < LSB / WAVE; ++i) {
             mg = fmaxf(mg, s_red[1][i]);
             mh = fmaxf(mh, s_red[2][i]);
         }
@@ -185,9 +190,9 @@ __global__ void __launch_bounds__(LB) k_leaf_stats(LeafArgs A) {
         if (s_bad) atomicMin(&A.st->status, -1);
     }
     if (LDS) {
-        for (int i = threadIdx.x; i < A.n_nodes; i += LB)
+        for (int i = threadIdx.x; i < A.n_nodes; i += LSB)
             if (s_cnt[i]) atomicAdd(&A.count[i], s_cnt[i]);
-        for (int i = threadIdx.x; i < A.n_nodes * K; i += LB) {
+        for (int i = threadIdx.x; i < A.n_nodes * K; i += LSB) {
             if (s_lo[i] != float_key(INFINITY)) atomicMin(&A.lo_key[i], s_lo[i]);
             if (s_hi[i] != float_key(-INFINITY)) atomicMax(&A.hi_key[i], s_hi[i]);
         }
@@ -249,8 +254,8 @@ __global__ void __launch_bounds__(1024) k_leaf_offsets(LeafArgs A, int K) {
     }
 }
 
-// Rows [blockIdx.x * LROWS, +LROWS) to their node's range of `sorted`; the
-// block reserves one range per node with one atomic add.
+// Rows [blockIdx.x * rows_per_block, +rows_per_block) to their node's range
+// of `sorted`; the block reserves one range per node with one atomic add.
 // The inputs, g and h of row i go to position pos of the sorted arrays.
 template <int K>
 __device__ __forceinline__ void put_sorted(const LeafArgs& A, const int32_t* fs, int64_t i, uint64_t pos) {
@@ -274,34 +279,34 @@ __device__ __forceinline__ void put_sorted(const LeafArgs& A, const int32_t* fs,
 }
 
 template <int K, bool LDS>
-__global__ void __launch_bounds__(LB) k_leaf_scatter(LeafArgs A) {
+__global__ void __launch_bounds__(LSB) k_leaf_scatter(LeafArgs A) {
     __shared__ int32_t s_fs[LKMAX];
     if (threadIdx.x < K) s_fs[threadIdx.x] = A.feats[threadIdx.x];
     __shared__ uint32_t s_cnt[LDS ? LDS_NODES : 1];
     __shared__ unsigned long long s_base[LDS ? LDS_NODES : 1];
     if (LDS)
-        for (int i = threadIdx.x; i < A.n_nodes; i += LB) s_cnt[i] = 0;
+        for (int i = threadIdx.x; i < A.n_nodes; i += LSB) s_cnt[i] = 0;
     __syncthreads();
-    const int64_t lo = (int64_t)blockIdx.x * LROWS, hi = min(A.n, lo + LROWS);
+    const int64_t lo = (int64_t)blockIdx.x * A.rows_per_block, hi = min(A.n, lo + A.rows_per_block);
     if (LDS) {
-        for (int64_t i = lo + threadIdx.x; i < hi; i += LB) {
+        for (int64_t i = lo + threadIdx.x; i < hi; i += LSB) {
             const int64_t node = A.leaf[i];
             if (node >= 0 && node < A.n_nodes) atomicAdd(&s_cnt[node], 1u);
         }
         __syncthreads();
-        for (int i = threadIdx.x; i < A.n_nodes; i += LB) {
+        for (int i = threadIdx.x; i < A.n_nodes; i += LSB) {
             s_base[i] = s_cnt[i] ? atomicAdd(&A.cursor[i], (unsigned long long)s_cnt[i]) : 0ull;
             s_cnt[i] = 0;
         }
         __syncthreads();
-        for (int64_t i = lo + threadIdx.x; i < hi; i += LB) {
+        for (int64_t i = lo + threadIdx.x; i < hi; i += LSB) {
             const int64_t node = A.leaf[i];
             if (node < 0 || node >= A.n_nodes) continue;
             const uint32_t r = atomicAdd(&s_cnt[node], 1u);
             put_sorted<K>(A, s_fs, i, s_base[node] + r);
         }
     } else {
-        for (int64_t i = lo + threadIdx.x; i < hi; i += LB) {
+        for (int64_t i = lo + threadIdx.x; i < hi; i += LSB) {
             const int64_t node = A.leaf[i];
             if (node < 0 || node >= A.n_nodes) continue;
             put_sorted<K>(A, s_fs, i, atomicAdd(&A.cursor[node], 1ull));
@@ -697,16 +702,19 @@ template <int K>
 void launch_leaf_fit(LeafArgs& A, float* out_W, float* out_b, float* out_lo, float* out_hi, int64_t* out_count,
                      hipStream_t stream) {
     const bool lds = A.n_nodes <= LDS_NODES;
-    const int row_blocks = (int)((A.n + LROWS - 1) / LROWS);
+    int64_t per = (A.n + LROW_BLOCKS - 1) / LROW_BLOCKS;
+    per = per < LROWS ? LROWS : (per + LSB - 1) / LSB * LSB;
+    A.rows_per_block = per;
+    const int row_blocks = (int)((A.n + per - 1) / per);
     k_leaf_init<<<launch_grid((int64_t)A.n_nodes * gram_entries(LKMAX), LB, 1024), LB, 0, stream>>>(A, K);
     if (row_blocks > 0) {
-        if (lds) k_leaf_stats<K, true><<<row_blocks, LB, 0, stream>>>(A);
-        else k_leaf_stats<K, false><<<row_blocks, LB, 0, stream>>>(A);
+        if (lds) k_leaf_stats<K, true><<<row_blocks, LSB, 0, stream>>>(A);
+        else k_leaf_stats<K, false><<<row_blocks, LSB, 0, stream>>>(A);
     }
     k_leaf_offsets<<<1, 1024, 0, stream>>>(A, K);
     if (row_blocks > 0) {
-        if (lds) k_leaf_scatter<K, true><<<row_blocks, LB, 0, stream>>>(A);
-        else k_leaf_scatter<K, false><<<row_blocks, LB, 0, stream>>>(A);
+        if (lds) k_leaf_scatter<K, true><<<row_blocks, LSB, 0, stream>>>(A);
+        else k_leaf_scatter<K, false><<<row_blocks, LSB, 0, stream>>>(A);
         if (A.n > 1024) k_leaf_gram<K, true><<<(int)((A.n + LCHUNK - 1) / LCHUNK), LB, 0, stream>>>(A);
         else k_leaf_gram<K, false><<<(int)((A.n + LCHUNK - 1) / LCHUNK), LB, 0, stream>>>(A);
         k_leaf_reduce<K><<<A.n_nodes, WAVE, 0, stream>>>(A);
