@@ -19,8 +19,15 @@
 //     371-379); interaction boosts are grow.c's fp32 compute_boost
 //     (grow.c:111-122);
 //   * the leaf table, its fp32 gains and the first-maximum selection
-//     (grow.c:284-407) run on the host between splits: one device round trip
-//     per split.
+//     (grow.c:284-407) run on the host.  A leaf's split, its children's rows
+//     (in cgrow's order) and histograms depend only on the leaf's own rows,
+//     so the host computes up to KR splits per round -- planned by running
+//     the leaf table ahead through the splits already computed -- and
+//     commits them in cgrow's best-first order: one device round trip per
+//     round.  A node at depth d keeps its rows at [s, e) of row array d % 3,
+//     so a computed split never moves its leaf's rows (the lookahead goes at
+//     most two levels below a committed leaf) and cgrow's final rows[] is the
+//     final leaves' segments of their arrays.
 //
 // Partition.  With positions relative to the node start, m rows, and
 //   p_k = position of the k-th row going right, counted from the left,
@@ -31,9 +38,10 @@
 //     its position is below q_K; every other right row moves one place left;
 //   * the left row of rank t to p_t if t <= K; every other left row stays.
 //
-// Workspace (yabt_grow_ref_workspace_bytes): rows and a copy (n u32), the
-// partition's flags / ranks / p / q arrays, the built child's g and h in row
-// order, and one (3, F, 256) fp32 histogram per node.
+// Workspace (yabt_grow_ref_workspace_bytes): three row arrays (n u32), the
+// partition's flags / ranks / p / q arrays and the built children's g and h
+// by position, the bucket lists, and one (3, F, 256) fp32 histogram per
+// slot: the root's and the two children of every computed split.
 
 #include "common.h"
 #include "host.h"
@@ -52,12 +60,30 @@ constexpr int RB = 256;            // threads per block
 constexpr int PT = 2048;           // partition rows per block
 constexpr int WT = 4096;           // histogram rows per tile
 constexpr int ST = NB + 1;         // bucket starts per (feature, tile)
+constexpr int KR = 16;             // splits computed per round, at most
+constexpr int PEND_PER_LEAF = 3;   // computed splits per leaf of the budget, at most
 
+// One split of a round (the root's histogram: a pseudo-job with the whole
+// row range as its built child).  The host fills the split; k_part_offsets
+// fills the partition's outcome.
 struct Job {
-    int64_t s, e;                  // parent segment
+    int32_t f, b;                  // the split
+    int32_t src, dst;              // row arrays of the leaf (depth % 3) and of its children
+    int32_t slot_p, slot_l, slot_r;    // histogram / path slots: the leaf (-1: none), its children
+    int32_t build_left;            // the smaller child, ties left (grow.c:355)
+    int64_t s, e;                  // the leaf's segment
     int64_t nl;                    // rows going left
-    int32_t build_left;
     int64_t cs, ce;                // built child's segment
+};
+
+// A round as the kernels see it: its splits, their partition blocks and the
+// sort tiles of their built children (prefix sums), the round number.
+struct Round {
+    int32_t K;
+    int32_t seq;
+    int32_t boff[KR + 1];
+    int32_t toff[KR + 1];
+    Job job[KR];
 };
 
 struct ChildRes {
@@ -74,30 +100,39 @@ struct Res {
     int32_t pad;
 };
 
+// Job k of `R` for flattened block or tile index x of prefix sums off[0..K].
+__device__ __forceinline__ int job_of(const int32_t* off, int K, int64_t x) {
+    int k = 0;
+    while (k + 1 < K && off[k + 1] <= x) ++k;
+    return k;
+}
+
 struct Ws {
-    uint32_t* rows;
-    uint32_t* rows_tmp;
+    uint32_t* rows;                // three arrays of rows_ld ids: depth % 3
+    int64_t rows_ld;
     uint8_t* flag;
     uint32_t* rank;
     uint32_t* p;
     uint32_t* q;
     uint32_t* blk;                 // per-block left counts, then their exclusive prefix
-    float* G;
+    float* G;                      // built children's g, h by position
     float* H;
     uint16_t* perm;                // (fgroup, ld_perm): per tile, positions bucketed by bin
     uint16_t* xperm;               // (fgroup, ld_perm): sparse builder, per tile, rows outside the default bin
     uint16_t* starts;              // (fgroup, n_tiles, 257): per tile, bucket starts
     int64_t n_tiles, ld_perm;
     int fgroup;                    // features bucketed per pass
-    double* expl;                  // (F, 3): sparse builder's explicit g, h sums, default-bin rows
-    double* tot;                   // (2): sparse builder's node g, h sums
-    float* hist;                   // (N, 3, F, 256)
-    double* fsel;                  // (2, F)
-    double* fgain;                 // (2, F)
-    int32_t* fb;                   // (2, F)
-    uint8_t* path;                 // (N, F)
-    int64_t* segs;                 // (N, 3): leaf node, start, end
-    Job* job;
+    double* expl;                  // (KR, F, 3): sparse builder's explicit g, h sums, default-bin rows
+    double* tot;                   // (KR, 2): sparse builder's node g, h sums
+    float* hist;                   // (slots, 3, F, 256)
+    int slots;                     // the root's and 2 per computed split
+    int pend_cap;                  // computed splits, at most
+    double* fsel;                  // (2 KR, F)
+    double* fgain;                 // (2 KR, F)
+    int32_t* fb;                   // (2 KR, F)
+    uint8_t* path;                 // (slots, F)
+    int64_t* segs;                 // (N, 4): leaf node, start, end, row array
+    Round* round;
     size_t bytes;
 };
 
@@ -107,30 +142,35 @@ Ws carve(char* base, int64_t n, int F, int max_leaves, bool sparse, int fgroup) 
     Ws w;
     const int64_t N = 2 * (int64_t)max_leaves + 1;
     const int64_t nn = n > 0 ? n : 1;
-    w.n_tiles = (nn + WT - 1) / WT;
+    // a round's built children hold at most half of each leaf's rows: at
+    // most n / 2 rows in at most n / (2 WT) + KR tiles; the root's n rows in
+    // n / WT tiles
+    w.n_tiles = (nn + WT - 1) / WT + KR;
     w.ld_perm = w.n_tiles * WT;
     w.fgroup = fgroup;
-    w.rows = c.take<uint32_t>(nn);
-    w.rows_tmp = c.take<uint32_t>(nn);
+    w.pend_cap = PEND_PER_LEAF * max_leaves + KR;
+    w.slots = 1 + 2 * w.pend_cap;
+    w.rows_ld = (nn + 63) / 64 * 64;
+    w.rows = c.take<uint32_t>(3 * (size_t)w.rows_ld);
     w.flag = c.take<uint8_t>(nn);
     w.rank = c.take<uint32_t>(nn);
     w.p = c.take<uint32_t>(nn);
     w.q = c.take<uint32_t>(nn);
-    w.blk = c.take<uint32_t>((nn + PT - 1) / PT + 1);
+    w.blk = c.take<uint32_t>((nn + PT - 1) / PT + KR + 1);
     w.G = c.take<float>(nn);
     w.H = c.take<float>(nn);
     w.perm = c.take<uint16_t>((size_t)fgroup * (size_t)w.ld_perm);
     w.xperm = sparse ? c.take<uint16_t>((size_t)fgroup * (size_t)w.ld_perm) : nullptr;
     w.starts = c.take<uint16_t>((size_t)fgroup * (size_t)w.n_tiles * ST);
-    w.expl = c.take<double>(3 * (size_t)F);
-    w.tot = c.take<double>(2);
-    w.hist = c.take<float>((size_t)N * 3 * F * NB);
-    w.fsel = c.take<double>(2 * (size_t)F);
-    w.fgain = c.take<double>(2 * (size_t)F);
-    w.fb = c.take<int32_t>(2 * (size_t)F);
-    w.path = c.take<uint8_t>((size_t)N * F);
-    w.segs = c.take<int64_t>((size_t)N * 3);
-    w.job = c.take<Job>(1);
+    w.expl = c.take<double>((size_t)KR * 3 * (size_t)F);
+    w.tot = c.take<double>((size_t)KR * 2);
+    w.hist = c.take<float>((size_t)w.slots * 3 * F * NB);
+    w.fsel = c.take<double>((size_t)2 * KR * F);
+    w.fgain = c.take<double>((size_t)2 * KR * F);
+    w.fb = c.take<int32_t>((size_t)2 * KR * F);
+    w.path = c.take<uint8_t>((size_t)w.slots * F);
+    w.segs = c.take<int64_t>((size_t)N * 4);
+    w.round = c.take<Round>(1);
     w.bytes = c.off;
     return w;
 }
@@ -161,39 +201,40 @@ int group_for(size_t bytes, int64_t n, int F, int max_leaves, bool sparse) {
 // setup
 // ---------------------------------------------------------------------------
 
-__global__ void __launch_bounds__(RB) k_init(uint32_t* rows, int64_t n, uint8_t* path, int64_t path_n,
-                                             int64_t* feature, int64_t* thr_bin, int64_t* left, int64_t* right,
-                                             float* value, int64_t* depth, int N) {
+__global__ void __launch_bounds__(RB) k_init(uint32_t* rows, int64_t n, uint8_t* path, int F) {
     const int64_t tid = (int64_t)blockIdx.x * RB + threadIdx.x, stride = (int64_t)gridDim.x * RB;
-    for (int64_t i = tid; i < n; i += stride) rows[i] = (uint32_t)i;
-    for (int64_t i = tid; i < path_n; i += stride) path[i] = 0;
-    for (int64_t i = tid; i < N; i += stride) {
-        feature[i] = LEAF;
-        thr_bin[i] = 0;
-        left[i] = -1;
-        right[i] = -1;
-        value[i] = 0.0f;
-        depth[i] = 0;
-    }
+    for (int64_t i = tid; i < n; i += stride) rows[i] = (uint32_t)i;     // grow.c:289
+    for (int64_t i = tid; i < F; i += stride) path[i] = 0;               // the root's path
 }
 
 // ---------------------------------------------------------------------------
-// partition in cgrow's order
+// partition in cgrow's order, every split of a round
 // ---------------------------------------------------------------------------
+//
+// Job k's partition blocks are R->boff[k] .. R->boff[k + 1] - 1, PT rows each
+// of its leaf's segment; flags, ranks, p and q are indexed by position (the
+// leaves of a round have disjoint segments), p and q hold positions relative
+// to the leaf's start.
 
 // Flags (row goes left) and the left count of each PT-row block.
-__global__ void __launch_bounds__(RB) k_part_flags(const uint8_t* __restrict__ bins_fm, int64_t ld, int f, int b,
-                                                   const uint32_t* __restrict__ rows, int64_t s, int64_t m,
-                                                   uint8_t* __restrict__ flag, uint32_t* __restrict__ blk) {
+__global__ void __launch_bounds__(RB) k_part_flags(const uint8_t* __restrict__ bins_fm, int64_t ld,
+                                                   const Round* __restrict__ R, const uint32_t* __restrict__ rows,
+                                                   int64_t rows_ld, uint8_t* __restrict__ flag,
+                                                   uint32_t* __restrict__ blk) {
     __shared__ uint32_t s_red[RB / WAVE];
-    const uint8_t* col = bins_fm + (size_t)f * ld;
-    const int64_t x0 = (int64_t)blockIdx.x * PT;
+    const int k = job_of(R->boff, R->K, blockIdx.x);
+    const Job& J = R->job[k];
+    const int64_t s = J.s, m = J.e - J.s;
+    const uint32_t* src = rows + (size_t)J.src * (size_t)rows_ld;
+    const uint8_t* col = bins_fm + (size_t)J.f * ld;
+    const int b = J.b;
+    const int64_t x0 = (int64_t)(blockIdx.x - R->boff[k]) * PT;
     uint32_t cnt = 0;
     for (int j = threadIdx.x; j < PT; j += RB) {
         const int64_t x = x0 + j;
         if (x < m) {
-            const uint8_t l = (int)col[rows[s + x]] <= b ? 1 : 0;
-            flag[x] = l;
+            const uint8_t l = (int)col[src[s + x]] <= b ? 1 : 0;
+            flag[s + x] = l;
             cnt += l;
         }
     }
@@ -201,102 +242,104 @@ __global__ void __launch_bounds__(RB) k_part_flags(const uint8_t* __restrict__ b
     if (threadIdx.x == 0) blk[blockIdx.x] = cnt;
 }
 
-// One block: exclusive prefix of the block counts; the job record.
-__global__ void __launch_bounds__(RB) k_part_offsets(uint32_t* blk, int nblk, Job* job, int64_t s, int64_t e) {
+// Block k: exclusive prefix of job k's block counts; the partition's outcome.
+__global__ void __launch_bounds__(RB) k_part_offsets(uint32_t* blk, Round* R) {
     __shared__ uint32_t s_w[RB / WAVE];
+    const int k = blockIdx.x;
+    Job& J = R->job[k];
+    const int b0 = R->boff[k], nblk = R->boff[k + 1] - b0;
     uint32_t carry = 0;
     for (int i0 = 0; i0 < nblk; i0 += RB) {
         const int i = i0 + threadIdx.x;
-        const uint32_t v = i < nblk ? blk[i] : 0u;
+        const uint32_t v = i < nblk ? blk[b0 + i] : 0u;
         uint32_t tot;
         const uint32_t ex = block_excl_scan<RB, uint32_t>(v, s_w, &tot);
-        if (i < nblk) blk[i] = carry + ex;
+        if (i < nblk) blk[b0 + i] = carry + ex;
         carry += tot;
     }
     if (threadIdx.x == 0) {
-        const int64_t m = e - s;
-        job->s = s;
-        job->e = e;
-        job->nl = carry;
-        job->build_left = (int64_t)carry <= m - (int64_t)carry ? 1 : 0;
-        job->cs = job->build_left ? s : s + (int64_t)carry;
-        job->ce = job->build_left ? s + (int64_t)carry : e;
+        const int64_t m = J.e - J.s;
+        J.nl = carry;
+        J.build_left = (int64_t)carry <= m - (int64_t)carry ? 1 : 0;
+        J.cs = J.build_left ? J.s : J.s + (int64_t)carry;
+        J.ce = J.build_left ? J.s + (int64_t)carry : J.e;
     }
 }
 
 // Ranks: rank[x] = left rows before x; p (right rows, from the left) and q
 // (left rows, from the right) hold positions.
 __global__ void __launch_bounds__(RB) k_part_rank(const uint8_t* __restrict__ flag, const uint32_t* __restrict__ blk,
-                                                  const Job* __restrict__ job, int64_t m, uint32_t* __restrict__ rank,
+                                                  const Round* __restrict__ R, uint32_t* __restrict__ rank,
                                                   uint32_t* __restrict__ p, uint32_t* __restrict__ q) {
     __shared__ uint32_t s_w[RB / WAVE];
-    const uint32_t nl = (uint32_t)job->nl;
-    const int64_t x0 = (int64_t)blockIdx.x * PT;
+    const int k = job_of(R->boff, R->K, blockIdx.x);
+    const Job& J = R->job[k];
+    const int64_t s = J.s, m = J.e - J.s;
+    const uint32_t nl = (uint32_t)J.nl;
+    const int64_t x0 = (int64_t)(blockIdx.x - R->boff[k]) * PT;
     uint32_t carry = blk[blockIdx.x];
     for (int j0 = 0; j0 < PT; j0 += RB) {
         const int64_t x = x0 + j0 + threadIdx.x;
-        const uint32_t l = x < m ? flag[x] : 0u;
+        const uint32_t l = x < m ? flag[s + x] : 0u;
         uint32_t tot;
         const uint32_t ex = carry + block_excl_scan<RB, uint32_t>(l, s_w, &tot);
         if (x < m) {
-            rank[x] = ex;
-            if (l) q[nl - ex - 1] = (uint32_t)x;
-            else p[(uint32_t)x - ex] = (uint32_t)x;
+            rank[s + x] = ex;
+            if (l) q[s + nl - ex - 1] = (uint32_t)x;
+            else p[s + (uint32_t)x - ex] = (uint32_t)x;
         }
         carry += tot;
     }
 }
 
-// Destinations of the two-pointer loop; rows_tmp[s + dest] = rows[s + x].
-// Block 0 also records the children's path masks and node bookkeeping.
+// Destinations of the two-pointer loop: the children's array at s + dest gets
+// the leaf's row at s + x, and the built child's g, h go to the same
+// position.  Block 0 of a job records the children's path masks.
 __global__ void __launch_bounds__(RB) k_part_permute(const uint8_t* __restrict__ flag,
                                                      const uint32_t* __restrict__ rank, const uint32_t* __restrict__ p,
-                                                     const uint32_t* __restrict__ q, const Job* __restrict__ job,
-                                                     const uint32_t* __restrict__ rows, uint32_t* __restrict__ rows_tmp,
-                                                     int64_t s, int64_t m, uint8_t* path, int F, int nid, int f,
-                                                     int nl_id, int nr_id) {
-    const int64_t nl = job->nl;
+                                                     const uint32_t* __restrict__ q, const Round* __restrict__ R,
+                                                     uint32_t* __restrict__ rows, int64_t rows_ld,
+                                                     const float* __restrict__ grad, const float* __restrict__ hess,
+                                                     float* __restrict__ G, float* __restrict__ H, uint8_t* path,
+                                                     int F) {
+    const int k = job_of(R->boff, R->K, blockIdx.x);
+    const Job& J = R->job[k];
+    const int64_t s = J.s, m = J.e - J.s, nl = J.nl, cs = J.cs, ce = J.ce;
+    const uint32_t* src = rows + (size_t)J.src * (size_t)rows_ld;
+    uint32_t* dst = rows + (size_t)J.dst * (size_t)rows_ld;
     // K = #{k : p_k < q_k}: p rises and q falls, and p_k < q_k exactly when
     // the k-th left row from the right lies at or after nl, so K is the
     // number of left rows in [nl, m): nl minus the left rows before nl
-    const int64_t K = nl < m ? nl - (int64_t)rank[nl] : 0;
-    const int64_t qK = K == 0 ? m : (int64_t)q[K - 1];
-    for (int64_t x = (int64_t)blockIdx.x * RB + threadIdx.x; x < m; x += (int64_t)gridDim.x * RB) {
-        const int64_t lb = rank[x];
+    const int64_t K = nl < m ? nl - (int64_t)rank[s + nl] : 0;
+    const int64_t qK = K == 0 ? m : (int64_t)q[s + K - 1];
+    const int64_t x0 = (int64_t)(blockIdx.x - R->boff[k]) * PT;
+    for (int j = threadIdx.x; j < PT; j += RB) {
+        const int64_t x = x0 + j;
+        if (x >= m) break;
+        const int64_t lb = rank[s + x];
         int64_t dest;
-        if (flag[x]) {
+        if (flag[s + x]) {
             const int64_t t = nl - lb;                 // rank from the right, 1-based
-            dest = t <= K ? (int64_t)p[t - 1] : x;
+            dest = t <= K ? (int64_t)p[s + t - 1] : x;
         } else {
             const int64_t r = x - lb + 1;              // rank from the left, 1-based
-            if (r <= K) dest = (r == 1 ? m : (int64_t)q[r - 2]) - 1;
+            if (r <= K) dest = (r == 1 ? m : (int64_t)q[s + r - 2]) - 1;
             else if (r == K + 1 && x < qK) dest = qK - 1;
             else dest = x - 1;
         }
-        rows_tmp[s + dest] = rows[s + x];
-    }
-    if (blockIdx.x == 0) {
-        for (int j = threadIdx.x; j < F; j += RB) {
-            const uint8_t v = (uint8_t)(path[(size_t)nid * F + j] | (j == f ? 1 : 0));
-            path[(size_t)nl_id * F + j] = v;
-            path[(size_t)nr_id * F + j] = v;
+        const uint32_t row = src[s + x];
+        const int64_t at = s + dest;
+        dst[at] = row;
+        if (at >= cs && at < ce) {
+            G[at] = grad[row];
+            H[at] = hess[row];
         }
     }
-}
-
-// rows[s:e) = rows_tmp[s:e); the built child's g, h in its row order.
-__global__ void __launch_bounds__(RB) k_part_commit(uint32_t* __restrict__ rows, const uint32_t* __restrict__ rows_tmp,
-                                                    const Job* __restrict__ job, int64_t s, int64_t m,
-                                                    const float* __restrict__ grad, const float* __restrict__ hess,
-                                                    float* __restrict__ G, float* __restrict__ H) {
-    const int64_t cs = job->cs, ce = job->ce;
-    for (int64_t x = (int64_t)blockIdx.x * RB + threadIdx.x; x < m; x += (int64_t)gridDim.x * RB) {
-        const int64_t i = s + x;
-        const uint32_t r = rows_tmp[i];
-        rows[i] = r;
-        if (i >= cs && i < ce) {
-            G[i - cs] = grad[r];
-            H[i - cs] = hess[r];
+    if (blockIdx.x == R->boff[k]) {
+        for (int jf = threadIdx.x; jf < F; jf += RB) {
+            const uint8_t v = (uint8_t)(path[(size_t)J.slot_p * F + jf] | (jf == J.f ? 1 : 0));
+            path[(size_t)J.slot_l * F + jf] = v;
+            path[(size_t)J.slot_r * F + jf] = v;
         }
     }
 }
@@ -317,23 +360,14 @@ __global__ void __launch_bounds__(RB) k_part_commit(uint32_t* __restrict__ rows,
 // outside the default bin; block F adds the node's g and h in double in row
 // order; k_hist_default combines them.
 
-// Segment [cs, cs + m): the job's built child, or [0, n) for the root (job null).
-struct Seg {
-    int64_t cs, m;
-};
-
-__device__ __forceinline__ Seg seg_of(const Job* job, int64_t n) {
-    if (!job) return Seg{0, n};
-    return Seg{job->cs, job->ce - job->cs};
-}
-
 constexpr int SW = RB / WAVE;             // waves per sort / chain block
 constexpr int SSUB = WT / SW;             // rows per wave per tile (sort)
 constexpr int SGR = SSUB / WAVE;          // 64-row groups per wave per tile (sort)
 constexpr int TPT = WT / RB;              // rows per thread per tile
 
 // Bin of the node's row at position x: row x for the root (rows[] is the
-// identity there, grow.c:289), rows[cs + x] for a built child.
+// identity there, grow.c:289), rows[cs + x] of the children's array for a
+// built child.
 template <bool ROOT>
 __device__ __forceinline__ uint32_t node_bin(const uint8_t* __restrict__ bins_fm, int64_t ld_fm,
                                             const uint8_t* __restrict__ bins_rm, int64_t ld_rm,
@@ -342,8 +376,10 @@ __device__ __forceinline__ uint32_t node_bin(const uint8_t* __restrict__ bins_fm
     return bins_rm[(size_t)rows[cs + x] * (size_t)ld_rm + f];
 }
 
-// Stable bucketing of one tile of one feature (block (f, t)): perm[f][t*WT +
-// k] lists the tile's positions bin by bin, each bin in row order, and
+// Stable bucketing of one tile of one feature (block (f, t), t a tile of
+// the round's built children: job k's tiles are R->toff[k] ..
+// R->toff[k + 1] - 1, the ones past its child's rows idle): perm[f][t*WT + k]
+// lists the tile's positions bin by bin, each bin in row order, and
 // starts[f][t][b] is where bin b's run begins (starts[...][256] = the run
 // total).  The lanes of a wave sharing a bin are found by an LDS atomic OR of
 // each lane's bit into s_peer[w][bin] (order-free), read back and cleared; a
@@ -353,10 +389,11 @@ __device__ __forceinline__ uint32_t node_bin(const uint8_t* __restrict__ bins_fm
 template <bool ROOT, bool SPARSE>
 __global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bins_fm, int64_t ld_fm,
                                                   const uint8_t* __restrict__ bins_rm, int64_t ld_rm,
-                                                  const uint32_t* __restrict__ rows, const Job* __restrict__ job,
-                                                  int64_t n, int fg0, const int32_t* __restrict__ dbin,
-                                                  uint16_t* __restrict__ perm, uint16_t* __restrict__ xperm,
-                                                  int64_t ld_perm, uint16_t* __restrict__ starts, int64_t n_tiles) {
+                                                  const uint32_t* __restrict__ rows, int64_t rows_ld,
+                                                  const Round* __restrict__ R, int fg0,
+                                                  const int32_t* __restrict__ dbin, uint16_t* __restrict__ perm,
+                                                  uint16_t* __restrict__ xperm, int64_t ld_perm,
+                                                  uint16_t* __restrict__ starts, int64_t n_tiles) {
     __shared__ uint8_t s_bin[WT];
     __shared__ uint64_t s_peer[SW][NB];
     __shared__ uint32_t s_cnt[SW][NB];
@@ -364,13 +401,18 @@ __global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bi
     __shared__ uint16_t s_xperm[SPARSE ? WT : 1];
     __shared__ uint32_t s_scan[SW];
     __shared__ uint32_t s_xoff[SW + 1];
-    const Seg sg = seg_of(job, n);
     const int fl = blockIdx.x, f = fg0 + fl;       // buffers by group position, bins by feature
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
     const int df = SPARSE ? dbin[f] : -1;
-    for (int64_t t = blockIdx.y; t * WT < sg.m; t += gridDim.y) {
-    const int64_t t0 = t * WT;
-    const int tn = (int)min((int64_t)WT, sg.m - t0);
+    const int K = R->K;
+    for (int64_t t = blockIdx.y; t < R->toff[K]; t += gridDim.y) {
+    const int kj = job_of(R->toff, K, t);
+    const Job& J = R->job[kj];
+    const int64_t cs = J.cs, m = J.ce - J.cs;
+    const int64_t t0 = (t - R->toff[kj]) * WT;      // the tile's first row in the child
+    if (t0 >= m) continue;                          // uniform across the block
+    const uint32_t* crow = rows + (size_t)J.dst * (size_t)rows_ld;
+    const int tn = (int)min((int64_t)WT, m - t0);
     for (int i = tid; i < SW * NB; i += RB) {
         (&s_cnt[0][0])[i] = 0;
         (&s_peer[0][0])[i] = 0;
@@ -378,7 +420,7 @@ __global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bi
 #pragma unroll
     for (int j = 0; j < TPT; ++j) {
         const int x = j * RB + tid;
-        if (x < tn) s_bin[x] = (uint8_t)node_bin<ROOT>(bins_fm, ld_fm, bins_rm, ld_rm, rows, sg.cs, f, t0 + x);
+        if (x < tn) s_bin[x] = (uint8_t)node_bin<ROOT>(bins_fm, ld_fm, bins_rm, ld_rm, crow, cs, f, t0 + x);
     }
     __syncthreads();
     uint32_t rk[SGR], xr[SGR];
@@ -452,10 +494,10 @@ __global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bi
     }
     __syncthreads();
     const int total = SPARSE ? (int)s_xoff[SW] : tn;
-    uint16_t* po = perm + (size_t)fl * (size_t)ld_perm + (size_t)t0;
+    uint16_t* po = perm + (size_t)fl * (size_t)ld_perm + (size_t)t * WT;
     for (int k = tid; k < total; k += RB) po[k] = s_perm[k];
     if (SPARSE) {
-        uint16_t* xo = xperm + (size_t)fl * (size_t)ld_perm + (size_t)t0;
+        uint16_t* xo = xperm + (size_t)fl * (size_t)ld_perm + (size_t)t * WT;
         for (int k = tid; k < total; k += RB) xo[k] = s_xperm[k];
     }
     __syncthreads();
@@ -545,29 +587,37 @@ __device__ __forceinline__ void chain_load(ChainTile& c, const float* __restrict
 // thread adds the tile's other rows in double in row order (xperm), and
 // block F adds the node's g and h in double in row order (grow.c:85-97);
 // k_hist_default combines them.  G, H hold the node's g, h by position.
+// Block (f, k): job k's built child (its tiles R->toff[k] ..); G, H hold the
+// g, h of the child's rows at their positions.
 template <bool SPARSE>
-__global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ G, const float* __restrict__ H,
-                                                   const Job* __restrict__ job, int64_t n, int F, int fg0, int nf,
+__global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb, const float* __restrict__ Hb,
+                                                   const Round* __restrict__ R, int F, int fg0, int nf,
                                                    const int32_t* __restrict__ dbin,
                                                    const uint16_t* __restrict__ perm,
                                                    const uint16_t* __restrict__ xperm, int64_t ld_perm,
                                                    const uint16_t* __restrict__ starts, int64_t n_tiles,
-                                                   float* __restrict__ hist_base, size_t hsz, int slot_l, int slot_r,
-                                                   double* __restrict__ eout, double* __restrict__ tot) {
+                                                   float* __restrict__ hist_base, size_t hsz,
+                                                   double* __restrict__ eout_b, double* __restrict__ tot_b) {
     __shared__ float2 s_gh[WT];
     __shared__ uint16_t s_idx[WT];
     __shared__ uint16_t s_xidx[SPARSE ? WT : 1];
     __shared__ uint16_t s_st[ST];
-    const Seg sg = seg_of(job, n);
-    const int64_t m = sg.m;
+    const int kj = blockIdx.y;
+    const Job& J = R->job[kj];
+    const int64_t m = J.ce - J.cs;
+    const int64_t tile0 = R->toff[kj];
+    const float* G = Gb + J.cs;
+    const float* H = Hb + J.cs;
+    double* eout = eout_b + (size_t)kj * 3 * F;
+    double* tot = tot_b + (size_t)kj * 2;
     const int tid = threadIdx.x;
     const int fl = blockIdx.x, f = fg0 + fl;       // buffers by group position, cells by feature
     const bool totals = SPARSE && fl == nf;        // the extra block of the first group
     const int df = (SPARSE && !totals) ? dbin[f] : -1;
     const size_t fo = (size_t)(totals ? 0 : fl);
-    const uint16_t* pf = perm + fo * (size_t)ld_perm;
-    const uint16_t* xf = SPARSE ? xperm + fo * (size_t)ld_perm : nullptr;
-    const uint16_t* sf = starts + fo * (size_t)n_tiles * ST;
+    const uint16_t* pf = perm + fo * (size_t)ld_perm + (size_t)tile0 * WT;
+    const uint16_t* xf = SPARSE ? xperm + fo * (size_t)ld_perm + (size_t)tile0 * WT : nullptr;
+    const uint16_t* sf = starts + (fo * (size_t)n_tiles + (size_t)tile0) * ST;
     float ag = 0.0f, ah = 0.0f;
     double eg = 0.0, eh = 0.0;
     int64_t cnt = 0;
@@ -612,7 +662,7 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ G, 
         }
         return;
     }
-    const int slot = (!job || job->build_left) ? slot_l : slot_r;
+    const int slot = J.build_left ? J.slot_l : J.slot_r;
     float* hist = hist_base + (size_t)slot * hsz;
     if (SPARSE && tid == df) {
         eout[3 * (size_t)f] = eg;
@@ -627,13 +677,18 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ G, 
 
 // Sparse builder's default-bin cells (grow.c:101-106): 0 + (float)(node sum -
 // explicit sum) for g and h, 0 + (float)(rows in the default bin) for the count.
+// Block (., k): job k's built child.
 __global__ void __launch_bounds__(RB) k_hist_default(const int32_t* __restrict__ dbin,
-                                                     const double* __restrict__ eout, const double* __restrict__ tot,
-                                                     int F, float* __restrict__ hist_base, size_t hsz,
-                                                     const Job* __restrict__ job, int slot_l, int slot_r) {
+                                                     const double* __restrict__ eout_b,
+                                                     const double* __restrict__ tot_b, int F,
+                                                     float* __restrict__ hist_base, size_t hsz,
+                                                     const Round* __restrict__ R) {
     const int f = blockIdx.x * RB + threadIdx.x;
     if (f >= F) return;
-    const int slot = (!job || job->build_left) ? slot_l : slot_r;
+    const Job& J = R->job[blockIdx.y];
+    const double* eout = eout_b + (size_t)blockIdx.y * 3 * F;
+    const double* tot = tot_b + (size_t)blockIdx.y * 2;
+    const int slot = J.build_left ? J.slot_l : J.slot_r;
     float* hist = hist_base + (size_t)slot * hsz;
     const size_t at = (size_t)f * NB + dbin[f];
     hist[(size_t)0 * F * NB + at] = 0.0f + (float)(tot[0] - eout[3 * (size_t)f]);
@@ -695,27 +750,16 @@ struct ScanParams {
     int F;
 };
 
-// The pick's inputs and the split record it writes.
-struct PickArgs {
-    float lr;
-    double lam;
-    float* out_value;
-    Res* res;
-    const Job* job;                // null at the root
-    int nid, split_f, split_b;     // the split (nid < 0 at the root)
-    int32_t seq;                   // round number stamped on the records
-    int64_t child_depth;
-    int64_t *out_feature, *out_thr_bin, *out_left, *out_right, *out_depth;
-};
-
-// One child's feature-major first maximum (grow.c:183-192), node value from
-// feature 0's 256 bins summed in double (grow.c:302-308, 371-379), and (for
-// the left child of a split) the split's node record (grow.c:340-350,
-// 381-386).  One wave.
-__device__ void ref_pick(const float* __restrict__ hist, size_t hsz, int node0, int node1, int c, int F,
-                         const double* __restrict__ fsel, const double* __restrict__ fgain,
-                         const int32_t* __restrict__ fb, const PickArgs& A, float* s_g, float* s_h) {
-    const int node = c == 0 ? node0 : node1;
+// One child's feature-major first maximum (grow.c:183-192) and node value
+// from feature 0's 256 bins summed in double (grow.c:302-308, 371-379),
+// written to the round's record for the host.  One wave; child y of the
+// round is child y % nc of job y / nc (nc = 1 at the root, else 2).
+__device__ void ref_pick(const float* __restrict__ hist, size_t hsz, const Round* __restrict__ R, int y, int nc,
+                         int F, const double* __restrict__ fsel, const double* __restrict__ fgain,
+                         const int32_t* __restrict__ fb, float lr, double lam, Res* res, float* s_g, float* s_h) {
+    const int kj = y / nc, c = y % nc;
+    const Job& J = R->job[kj];
+    const int node = c == 0 ? J.slot_l : J.slot_r;
     const int lane = threadIdx.x;
     {
         const float* hg = hist + (size_t)node * hsz;
@@ -726,25 +770,16 @@ __device__ void ref_pick(const float* __restrict__ hist, size_t hsz, int node0, 
         }
     }
     __syncthreads();
-    if (lane == 0 && A.nid >= 0 && c == 0) {
-        A.out_feature[A.nid] = A.split_f;
-        A.out_thr_bin[A.nid] = A.split_b;
-        A.out_left[A.nid] = node0;
-        A.out_right[A.nid] = node1;
-        A.out_value[A.nid] = 0.0f;
-        A.out_depth[node0] = A.child_depth;
-        A.out_depth[node1] = A.child_depth;
-    }
     // lanes take features in increasing order with grow.c's strict >, then
     // the largest sel, lowest f wins
     double best_sel = -INFINITY, best_true = -INFINITY;
     int bf = -1, bb = -1;
     for (int f = lane; f < F; f += WAVE) {
-        const int b = fb[(size_t)c * F + f];
-        const double s = fsel[(size_t)c * F + f];
+        const int b = fb[(size_t)y * F + f];
+        const double s = fsel[(size_t)y * F + f];
         if (b >= 0 && s > best_sel) {
             best_sel = s;
-            best_true = fgain[(size_t)c * F + f];
+            best_true = fgain[(size_t)y * F + f];
             bf = f;
             bb = b;
         }
@@ -777,43 +812,47 @@ __device__ void ref_pick(const float* __restrict__ hist, size_t hsz, int node0, 
                 H += vh[j];
             }
         }
-        const float v = (float)(-A.lr * G / (H + A.lam));
-        A.out_value[node] = v;
-        // A.res is host memory mapped for the device: the record's fields,
-        // a system-scope fence, then the round number the host waits for
-        volatile ChildRes& r = A.res->c[c];
+        const float v = (float)(-lr * G / (H + lam));
+        // res is host memory mapped for the device: the record's fields, a
+        // system-scope fence, then the round number the host waits for
+        volatile ChildRes& r = res[kj].c[c];
         r.gain = bf < 0 ? -INFINITY : best_true;
         r.f = bf;
         r.b = bb;
         r.value = v;
         if (c == 0) {
-            volatile Res* R = A.res;
-            R->mid = A.job ? A.job->s + A.job->nl : 0;
-            R->build_left = A.job ? A.job->build_left : 0;
+            volatile Res* rk = res + kj;
+            rk->mid = J.s + J.nl;
+            rk->build_left = J.build_left;
         }
         __threadfence_system();
-        r.seq = A.seq;
+        r.seq = R->seq;
     }
     __syncthreads();
 }
 
-// One wave per (feature, child): the split scan (grow.c:129-197).  At a split
-// (parent >= 0) the subtracted child's block first forms its feature's bins
-// as parent - built child in fp32 (grow.c:361,368) and stores them.
-__global__ void __launch_bounds__(WAVE) k_scan_feature(float* __restrict__ hist, size_t hsz, int node0, int node1,
-                                                       int parent, const uint8_t* __restrict__ path, ScanParams P,
+// One wave per (feature, child): the split scan (grow.c:129-197); child y of
+// the round is child y % nc of job y / nc (nc = 1 at the root, else 2).  At
+// a split the subtracted child's block first forms its feature's bins as
+// parent - built child in fp32 (grow.c:361,368) and stores them.
+__global__ void __launch_bounds__(WAVE) k_scan_feature(float* __restrict__ hist, size_t hsz,
+                                                       const Round* __restrict__ R, int nc,
+                                                       const uint8_t* __restrict__ path, ScanParams P,
                                                        double* __restrict__ fsel, double* __restrict__ fgain,
-                                                       int32_t* __restrict__ fb, PickArgs A) {
+                                                       int32_t* __restrict__ fb) {
     __shared__ float s_in[3][NB];
     __shared__ double s_gl[NB], s_hl[NB], s_cl[NB];
-    const int f = blockIdx.x, c = blockIdx.y, lane = threadIdx.x;
-    const int node = c == 0 ? node0 : node1;
+    const int f = blockIdx.x, y = blockIdx.y, lane = threadIdx.x;
+    const Job& J = R->job[y / nc];
+    const int c = y % nc;
+    const int node = c == 0 ? J.slot_l : J.slot_r;
+    const int parent = J.slot_p;
     const int F = P.F;
     double best_sel = -INFINITY, best_true = -INFINITY;
     int best_b = -1;
-    const bool sub = parent >= 0 && node == (A.job->build_left ? node1 : node0);
+    const bool sub = parent >= 0 && c == (J.build_left ? 1 : 0);
     if (sub) {
-        const int built = A.job->build_left ? node0 : node1;
+        const int built = J.build_left ? J.slot_l : J.slot_r;
         const size_t plane = (size_t)F * NB;
         const float* hp = hist + (size_t)parent * hsz + (size_t)f * NB;
         const float* hb = hist + (size_t)built * hsz + (size_t)f * NB;
@@ -952,35 +991,37 @@ __global__ void __launch_bounds__(WAVE) k_scan_feature(float* __restrict__ hist,
         }
     }
     if (lane == 0) {
-        fsel[(size_t)c * F + f] = best_sel;
-        fgain[(size_t)c * F + f] = best_true;
-        fb[(size_t)c * F + f] = best_b;
+        fsel[(size_t)y * F + f] = best_sel;
+        fgain[(size_t)y * F + f] = best_true;
+        fb[(size_t)y * F + f] = best_b;
     }
 }
 
-// One wave per child: ref_pick after every scan block is done.
-__global__ void __launch_bounds__(WAVE) k_scan_pick(const float* __restrict__ hist, size_t hsz, int node0, int node1,
-                                                    int F, const double* __restrict__ fsel,
+// One wave per child of the round: ref_pick after every scan block is done.
+__global__ void __launch_bounds__(WAVE) k_scan_pick(const float* __restrict__ hist, size_t hsz,
+                                                    const Round* __restrict__ R, int nc, int F,
+                                                    const double* __restrict__ fsel,
                                                     const double* __restrict__ fgain, const int32_t* __restrict__ fb,
-                                                    PickArgs A) {
+                                                    float lr, double lam, Res* res) {
     __shared__ float s_g[NB], s_h[NB];
-    ref_pick(hist, hsz, node0, node1, blockIdx.x, F, fsel, fgain, fb, A, s_g, s_h);
+    ref_pick(hist, hsz, R, blockIdx.x, nc, F, fsel, fgain, fb, lr, lam, res, s_g, s_h);
 }
 
-// Per-row leaf ids from the final rows[] and the leaves' segments.
-__global__ void __launch_bounds__(RB) k_leaf_rows(const uint32_t* __restrict__ rows, const int64_t* __restrict__ seg,
-                                                  int n_leaf, int64_t* __restrict__ out) {
+// Per-row leaf ids and cgrow's final rows[] from the final leaves' segments:
+// leaf k is node seg[4k] with rows [seg[4k+1], seg[4k+2]) of row array
+// seg[4k+3].  Either output may be null.
+__global__ void __launch_bounds__(RB) k_leaf_rows(const uint32_t* __restrict__ rows, int64_t rows_ld,
+                                                  const int64_t* __restrict__ seg, int n_leaf,
+                                                  int64_t* __restrict__ out_leaf, int64_t* __restrict__ out_rows) {
     const int k = blockIdx.y;
     if (k >= n_leaf) return;
-    const int64_t node = seg[3 * k], s = seg[3 * k + 1], e = seg[3 * k + 2];
-    for (int64_t i = s + (int64_t)blockIdx.x * RB + threadIdx.x; i < e; i += (int64_t)gridDim.x * RB)
-        out[rows[i]] = node;
-}
-
-__global__ void k_set_status(int32_t* out, int v) { out[0] = v; }
-
-__global__ void __launch_bounds__(RB) k_rows_out(const uint32_t* __restrict__ rows, int64_t n, int64_t* __restrict__ out) {
-    for (int64_t i = (int64_t)blockIdx.x * RB + threadIdx.x; i < n; i += (int64_t)gridDim.x * RB) out[i] = rows[i];
+    const int64_t node = seg[4 * k], s = seg[4 * k + 1], e = seg[4 * k + 2];
+    const uint32_t* r = rows + (size_t)seg[4 * k + 3] * (size_t)rows_ld;
+    for (int64_t i = s + (int64_t)blockIdx.x * RB + threadIdx.x; i < e; i += (int64_t)gridDim.x * RB) {
+        const uint32_t row = r[i];
+        if (out_leaf) out_leaf[row] = node;
+        if (out_rows) out_rows[i] = row;
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1001,38 +1042,56 @@ struct Grower {
     const int32_t* dbin;           // sparse builder's default bins, or null
     hipStream_t st;
 
-    // Histogram of the job's built child (at most m_max rows) into node
-    // slot_l (left child built) or slot_r; job null: all rows into slot_l.
-    // With default bins, the sparse builder's arithmetic (grow.c:68-107).
-    void hist(const Job* job, int64_t m_max, int slot_l, int slot_r, const float* G, const float* H) {
-        const int64_t tiles = min((int64_t)65535, max((int64_t)1, (m_max + WT - 1) / WT));
-        const uint32_t* rows = w.rows;
+    // Histograms of the round's K built children (the root: every row), in
+    // `tiles` sort tiles; G, H: their g, h by position.  With default bins,
+    // the sparse builder's arithmetic (grow.c:68-107).
+    void hist(bool root, int K, int64_t tiles, const float* G, const float* H) {
+        const unsigned ty = (unsigned)min((int64_t)65535, max((int64_t)1, tiles));
         for (int fg0 = 0; fg0 < F; fg0 += w.fgroup) {
             const int nf = min(w.fgroup, F - fg0);
-            const dim3 sgrid((unsigned)nf, (unsigned)tiles);
-#define YABT_SORT(ROOT, SPARSE)                                                                                      \
-    k_walk_sort<ROOT, SPARSE><<<sgrid, RB, 0, st>>>(bins_fm, ld_fm, bins_rm, ld_rm, rows, job, n, fg0, dbin, w.perm, \
-                                                    w.xperm, w.ld_perm, w.starts, w.n_tiles)
-            if (!job) {
+            const dim3 sgrid((unsigned)nf, ty);
+#define YABT_SORT(ROOT, SPARSE)                                                                             \
+    k_walk_sort<ROOT, SPARSE><<<sgrid, RB, 0, st>>>(bins_fm, ld_fm, bins_rm, ld_rm, w.rows, w.rows_ld, w.round, \
+                                                    fg0, dbin, w.perm, w.xperm, w.ld_perm, w.starts, w.n_tiles)
+            if (root) {
                 if (dbin) YABT_SORT(true, true); else YABT_SORT(true, false);
             } else {
                 if (dbin) YABT_SORT(false, true); else YABT_SORT(false, false);
             }
 #undef YABT_SORT
             // the sparse builder's node totals: one more block with the first group
-            const unsigned cgrid = (unsigned)nf + (dbin && fg0 == 0 ? 1u : 0u);
+            const dim3 cgrid((unsigned)nf + (dbin && fg0 == 0 ? 1u : 0u), (unsigned)K);
             if (dbin)
-                k_walk_chain<true><<<cgrid, RB, 0, st>>>(G, H, job, n, F, fg0, nf, dbin, w.perm, w.xperm, w.ld_perm,
-                                                         w.starts, w.n_tiles, w.hist, hsz, slot_l, slot_r, w.expl,
-                                                         w.tot);
+                k_walk_chain<true><<<cgrid, RB, 0, st>>>(G, H, w.round, F, fg0, nf, dbin, w.perm, w.xperm, w.ld_perm,
+                                                         w.starts, w.n_tiles, w.hist, hsz, w.expl, w.tot);
             else
-                k_walk_chain<false><<<cgrid, RB, 0, st>>>(G, H, job, n, F, fg0, nf, dbin, w.perm, w.xperm,
-                                                          w.ld_perm, w.starts, w.n_tiles, w.hist, hsz, slot_l, slot_r,
-                                                          w.expl, w.tot);
+                k_walk_chain<false><<<cgrid, RB, 0, st>>>(G, H, w.round, F, fg0, nf, dbin, w.perm, w.xperm,
+                                                          w.ld_perm, w.starts, w.n_tiles, w.hist, hsz, w.expl, w.tot);
         }
         if (dbin)
-            k_hist_default<<<(F + RB - 1) / RB, RB, 0, st>>>(dbin, w.expl, w.tot, F, w.hist, hsz, job, slot_l, slot_r);
+            k_hist_default<<<dim3((F + RB - 1) / RB, (unsigned)K), RB, 0, st>>>(dbin, w.expl, w.tot, F, w.hist, hsz,
+                                                                              w.round);
     }
+};
+
+// A computed split, on the host.  Leaves name their origin as 2 p + c (child
+// c of split p) or -1 (the root).
+struct HSplit {
+    int origin;
+    int f, b, depth;               // the split; depth of its children
+    int slot_p;
+    int64_t s, e, mid;
+    int child_pend[2];             // the children's computed splits (-1: none)
+    int child_node[2];             // the children's node ids once committed (-1: not committed)
+    float cgain[2];                // the children's table gains (depth cap applied)
+    int cf[2], cb[2];              // the children's best splits
+    float cval[2];                 // the children's values
+};
+
+// A leaf as a split candidate.
+struct LeafView {
+    int f, b, depth, slot, arr;
+    int64_t s, e;
 };
 
 }  // namespace ref
@@ -1094,17 +1153,36 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
     g.st = stream;
     const Ws& w = g.w;
     const int N = 2 * max_leaves + 1;
+    const int L = max_leaves;
 
+    // host staging of a round, and the round's records in mapped host memory
+    Round* h_round = nullptr;
     Res* h_res = nullptr;
-    hipError_t he = hipHostMalloc((void**)&h_res, sizeof(Res), hipHostMallocMapped | hipHostMallocCoherent);
-    if (he != hipSuccess) return hip_fail(he, "yabt_grow_ref: pinned result buffer");
+    hipError_t he = hipHostMalloc((void**)&h_round, sizeof(Round), hipHostMallocDefault);
+    if (he != hipSuccess) return hip_fail(he, "yabt_grow_ref: pinned round buffer");
+    he = hipHostMalloc((void**)&h_res, KR * sizeof(Res), hipHostMallocMapped | hipHostMallocCoherent);
+    if (he != hipSuccess) {
+        (void)hipHostFree(h_round);
+        return hip_fail(he, "yabt_grow_ref: pinned result buffer");
+    }
+    // every return waits for the stream first: enqueued picks write h_res and
+    // enqueued copies read h_round until they have run
     struct Free {
+        Round* r;
         Res* p;
-        ~Free() { (void)hipHostFree(p); }
-    } free_res{h_res};
+        hipStream_t s;
+        ~Free() {
+            (void)hipStreamSynchronize(s);
+            (void)hipHostFree(r);
+            (void)hipHostFree(p);
+        }
+    } free_bufs{h_round, h_res, stream};
+    Res* d_res = nullptr;   // the device's address of h_res
+    he = hipHostGetDevicePointer((void**)&d_res, h_res, 0);
+    if (he != hipSuccess) return hip_fail(he, "yabt_grow_ref: mapped result buffer");
+    for (int k = 0; k < KR; ++k) h_res[k].c[0].seq = h_res[k].c[1].seq = -1;
 
-    k_init<<<launch_grid(max((int64_t)N * F, n), RB, 1024), RB, 0, stream>>>(
-        w.rows, n, w.path, (int64_t)N * F, out_feature, out_thr_bin, out_left, out_right, out_value, out_depth, N);
+    k_init<<<launch_grid(n > F ? n : F, RB, 1024), RB, 0, stream>>>(w.rows, n, w.path, F);
 
     ScanParams P;
     P.nbins = nbins;
@@ -1118,153 +1196,295 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
     P.msl = msl;
     P.F = F;
 
-    // host copy of cgrow's leaf table (grow.c:284-287) and node segments
-    std::vector<int64_t> node_start(N, 0), node_end(N, 0), node_depth(N, 0);
-    std::vector<int64_t> leaf_node(N), leaf_f(N), leaf_b(N);
-    std::vector<float> leaf_gain(N);
-    Res* d_res = nullptr;   // the device's address of h_res
-    he = hipHostGetDevicePointer((void**)&d_res, h_res, 0);
-    if (he != hipSuccess) return hip_fail(he, "yabt_grow_ref: mapped result buffer");
-    h_res->c[0].seq = h_res->c[1].seq = -1;
-    // The pick writes each child's record into h_res and stamps it with the
+    // The picks write each child's record into h_res and stamp it with the
     // round number last; the host spins on the stamps (checking the stream
     // for errors, and for completion without a stamp) instead of a copy and
     // a stream synchronisation.
-    auto sync_res = [&](int32_t seq, int children) -> int {
+    auto sync_res = [&](int32_t seq, int jobs, int children) -> int {
         volatile Res* R = h_res;
+        auto all = [&]() {
+            for (int k = 0; k < jobs; ++k)
+                for (int c = 0; c < children; ++c)
+                    if (R[k].c[c].seq != seq) return false;
+            return true;
+        };
         for (uint64_t spin = 0;; ++spin) {
-            bool ok = true;
-            for (int c = 0; c < children; ++c) ok = ok && R->c[c].seq == seq;
-            if (ok) {
+            if (all()) {
                 std::atomic_thread_fence(std::memory_order_acquire);
                 return 0;
             }
             if ((spin & 1023) == 1023) {
                 const hipError_t e = hipStreamQuery(stream);
                 if (e == hipSuccess) {
-                    ok = true;
-                    for (int c = 0; c < children; ++c) ok = ok && R->c[c].seq == seq;
-                    if (ok) return 0;
-                    return fail(-4, "yabt_grow_ref: stream finished without the split result");
+                    if (all()) return 0;
+                    return fail(-4, "yabt_grow_ref: stream finished without the round's results");
                 }
-                if (e != hipErrorNotReady) return hip_fail(e, "yabt_grow_ref: split");
+                if (e != hipErrorNotReady) return hip_fail(e, "yabt_grow_ref: round");
             }
         }
     };
+    auto launch_round = [&]() -> int {
+        const hipError_t e = hipMemcpyAsync(w.round, h_round, sizeof(Round), hipMemcpyHostToDevice, stream);
+        return e == hipSuccess ? 0 : hip_fail(e, "yabt_grow_ref: round copy");
+    };
 
-    // root
-    node_end[0] = n;
-    g.hist(nullptr, n, 0, 0, grad, hess);
-    PickArgs A;
-    A.lr = lr;
-    A.lam = (double)lam;
-    A.out_value = out_value;
-    A.res = d_res;
-    A.seq = 0;
-    A.job = nullptr;
-    A.nid = -1;
-    A.split_f = A.split_b = 0;
-    A.child_depth = 0;
-    A.out_feature = out_feature;
-    A.out_thr_bin = out_thr_bin;
-    A.out_left = out_left;
-    A.out_right = out_right;
-    A.out_depth = out_depth;
-    k_scan_feature<<<dim3(F, 1), WAVE, 0, stream>>>(w.hist, g.hsz, 0, 0, -1, w.path, P, w.fsel, w.fgain, w.fb, A);
-    k_scan_pick<<<1, WAVE, 0, stream>>>(w.hist, g.hsz, 0, 0, F, w.fsel, w.fgain, w.fb, A);
-    int rc = launch_status("yabt_grow_ref launch");
-    if (rc) return rc;
-    if ((rc = sync_res(0, 1))) return rc;
-    double g0 = h_res->c[0].gain;
-    if (0 >= max_depth) g0 = -INFINITY;
-    leaf_node[0] = 0;
-    leaf_gain[0] = (float)g0;
-    leaf_f[0] = h_res->c[0].f;
-    leaf_b[0] = h_res->c[0].b;
-    int n_active = 1, n_leaves = 1, n_nodes = 1;
-    std::vector<char> split(N, 0);
-
-    while (n_leaves < max_leaves) {             // grow.c:321-408
-        int best_k = -1;
-        float best_g = 0.0f;
-        for (int k = 0; k < n_active; ++k)
-            if (leaf_gain[k] > best_g) {
-                best_g = leaf_gain[k];
-                best_k = k;
-            }
-        if (best_k < 0) break;
-        const int nid = (int)leaf_node[best_k];
-        const int f = (int)leaf_f[best_k], b = (int)leaf_b[best_k];
-        const int64_t s = node_start[nid], e = node_end[nid], m = e - s;
-        const int nl = n_nodes, nr = n_nodes + 1;
-        n_nodes += 2;
-        const int64_t d = node_depth[nid] + 1;
-        split[nid] = 1;
-
-        // partition rows[s:e) in cgrow's order; the smaller child's g, h
-        const int pblk = (int)max((int64_t)1, (m + PT - 1) / PT);
-        k_part_flags<<<pblk, RB, 0, stream>>>(bins_fm, ld_fm, f, b, w.rows, s, m, w.flag, w.blk);
-        k_part_offsets<<<1, RB, 0, stream>>>(w.blk, pblk, w.job, s, e);
-        k_part_rank<<<pblk, RB, 0, stream>>>(w.flag, w.blk, w.job, m, w.rank, w.p, w.q);
-        k_part_permute<<<launch_grid(m, RB * 4, 4096), RB, 0, stream>>>(w.flag, w.rank, w.p, w.q, w.job, w.rows,
-                                                                      w.rows_tmp, s, m, w.path, F, nid, f, nl, nr);
-        k_part_commit<<<launch_grid(m, RB * 4, 4096), RB, 0, stream>>>(w.rows, w.rows_tmp, w.job, s, m, grad, hess, w.G,
-                                                                     w.H);
-        // the smaller child (ties left, grow.c:355) has at most m / 2 rows;
-        // the other is parent - built (grow.c:361,368)
-        g.hist(w.job, m / 2, nl, nr, w.G, w.H);
-        A.job = w.job;
-        A.seq = n_leaves;               // 1, 2, ... one per split
-        A.nid = nid;
-        A.split_f = f;
-        A.split_b = b;
-        A.child_depth = d;
-        k_scan_feature<<<dim3(F, 2), WAVE, 0, stream>>>(w.hist, g.hsz, nl, nr, nid, w.path, P, w.fsel, w.fgain,
-                                                        w.fb, A);
-        k_scan_pick<<<2, WAVE, 0, stream>>>(w.hist, g.hsz, nl, nr, F, w.fsel, w.fgain, w.fb, A);
+    // the root: one pseudo-job whose built child is every row
+    int rc = 0;
+    {
+        Round& R = *h_round;
+        memset(&R, 0, sizeof R);
+        R.K = 1;
+        R.seq = 0;
+        R.toff[1] = (int32_t)max((int64_t)1, (n + WT - 1) / WT);
+        Job& J = R.job[0];
+        J.f = -1;
+        J.slot_p = -1;
+        J.slot_l = 0;
+        J.slot_r = 0;
+        J.build_left = 1;
+        J.s = 0;
+        J.e = n;
+        J.nl = n;
+        J.cs = 0;
+        J.ce = n;
+        if ((rc = launch_round())) return rc;
+        g.hist(true, 1, R.toff[1], grad, hess);
+        k_scan_feature<<<dim3(F, 1), WAVE, 0, stream>>>(w.hist, g.hsz, w.round, 1, w.path, P, w.fsel, w.fgain, w.fb);
+        k_scan_pick<<<1, WAVE, 0, stream>>>(w.hist, g.hsz, w.round, 1, F, w.fsel, w.fgain, w.fb, lr, (double)lam,
+                                             d_res);
         if ((rc = launch_status("yabt_grow_ref launch"))) return rc;
-        if ((rc = sync_res(A.seq, 2))) return rc;
-        const int64_t mid = h_res->mid;
-        node_start[nl] = s;
-        node_end[nl] = mid;
-        node_start[nr] = mid;
-        node_end[nr] = e;
-        node_depth[nl] = d;
-        node_depth[nr] = d;
-        n_leaves += 1;
-        double glg = h_res->c[0].gain, grg = h_res->c[1].gain;
-        if (d >= max_depth) glg = grg = -INFINITY;
-        leaf_node[best_k] = nl;
-        leaf_gain[best_k] = (float)glg;
-        leaf_f[best_k] = h_res->c[0].f;
-        leaf_b[best_k] = h_res->c[0].b;
-        leaf_node[n_active] = nr;
-        leaf_gain[n_active] = (float)grg;
-        leaf_f[n_active] = h_res->c[1].f;
-        leaf_b[n_active] = h_res->c[1].b;
-        n_active += 1;
+        if ((rc = sync_res(0, 1, 1))) return rc;
+    }
+    const double root_gain = h_res[0].c[0].gain;
+    const int root_f = h_res[0].c[0].f, root_b = h_res[0].c[0].b;
+
+    // node arrays (cgrow's outputs), written on the host as splits commit
+    std::vector<int64_t> o_feature(N, LEAF), o_thr(N, 0), o_left(N, -1), o_right(N, -1), o_depth(N, 0);
+    std::vector<float> o_value(N, 0.0f);
+    o_value[0] = h_res[0].c[0].value;
+
+    std::vector<HSplit> sp;
+    sp.reserve((size_t)w.pend_cap);
+    auto view = [&](int src) -> LeafView {
+        LeafView v;
+        if (src < 0) {
+            v.f = root_f;
+            v.b = root_b;
+            v.depth = 0;
+            v.slot = 0;
+            v.s = 0;
+            v.e = n;
+        } else {
+            const HSplit& q = sp[(size_t)(src >> 1)];
+            const int c = src & 1;
+            v.f = q.cf[c];
+            v.b = q.cb[c];
+            v.depth = q.depth;
+            v.slot = 1 + 2 * (src >> 1) + c;
+            v.s = c ? q.mid : q.s;
+            v.e = c ? q.e : q.mid;
+        }
+        v.arr = v.depth % 3;
+        return v;
+    };
+    // cgrow's leaf table (grow.c:284-287): gain, computed split, origin, node id
+    std::vector<float> t_gain(N, 0.0f);
+    std::vector<int> t_pend(N, -1), t_src(N, -1), t_node(N, -1);
+    t_gain[0] = (float)(0 >= max_depth ? -INFINITY : root_gain);
+    t_src[0] = -1;
+    t_node[0] = 0;
+    int na = 1, nn = 1;
+    // the first maximum of the fp32 gains above 0.0f (grow.c:322-330)
+    auto argmax = [](const std::vector<float>& gain, int cnt) {
+        int best = -1;
+        float bg = 0.0f;
+        for (int a = 0; a < cnt; ++a)
+            if (gain[a] > bg) {
+                bg = gain[a];
+                best = a;
+            }
+        return best;
+    };
+    std::vector<float> p_gain(N);
+    std::vector<int> p_pend(N), p_src(N), p_level(N);
+    std::vector<char> p_moved(N);
+
+    for (int32_t seq = 1;; ++seq) {
+        // replay: commit the best leaf while its split is computed
+        int best = -1;
+        while (na < L) {
+            best = argmax(t_gain, na);
+            if (best < 0 || t_pend[best] < 0) break;
+            const int p = t_pend[best];
+            HSplit& q = sp[(size_t)p];
+            const int nid = t_node[best], nl = nn, nr = nn + 1;
+            // the split's node record (grow.c:338-350, 371-386)
+            o_feature[nid] = q.f;
+            o_thr[nid] = q.b;
+            o_left[nid] = nl;
+            o_right[nid] = nr;
+            o_value[nid] = 0.0f;
+            o_depth[nl] = o_depth[nr] = q.depth;
+            o_value[nl] = q.cval[0];
+            o_value[nr] = q.cval[1];
+            q.child_node[0] = nl;
+            q.child_node[1] = nr;
+            // left child replaces the split leaf, right child is appended
+            // (grow.c:393-407)
+            t_gain[best] = q.cgain[0];
+            t_pend[best] = q.child_pend[0];
+            t_src[best] = 2 * p;
+            t_node[best] = nl;
+            t_gain[na] = q.cgain[1];
+            t_pend[na] = q.child_pend[1];
+            t_src[na] = 2 * p + 1;
+            t_node[na] = nr;
+            nn += 2;
+            ++na;
+            best = -1;
+        }
+        if (best < 0) break;   // no leaf with a positive gain, or the budget is spent
+        // plan: the table run ahead -- a leaf whose split is computed gives
+        // way to its children, a leaf without one is taken for the round.
+        // Only leaves at most one computed split below a committed leaf are
+        // taken (level <= 1): a split at depth d writes row array (d + 1) % 3,
+        // so a third level would overwrite the rows of a committed leaf that
+        // may stay a leaf.
+        for (int a = 0; a < na; ++a) {
+            p_gain[a] = t_gain[a];
+            p_pend[a] = t_pend[a];
+            p_src[a] = t_src[a];
+            p_level[a] = 0;
+            p_moved[a] = 0;
+        }
+        Round& R = *h_round;
+        memset(&R, 0, sizeof R);
+        R.seq = seq;
+        int j = 0, nas = na, nls = na;
+        const int np0 = (int)sp.size();
+        while (nls + j < L && j < KR) {
+            const int a = argmax(p_gain, nas);
+            if (a < 0) break;
+            const int p = p_pend[a];
+            if (p >= 0) {
+                const HSplit& q = sp[(size_t)p];
+                const int lv = p_level[a] + 1;
+                p_gain[a] = q.cgain[0];
+                p_pend[a] = q.child_pend[0];
+                p_src[a] = 2 * p;
+                p_level[a] = lv;
+                p_moved[a] = 1;
+                p_gain[nas] = q.cgain[1];
+                p_pend[nas] = q.child_pend[1];
+                p_src[nas] = 2 * p + 1;
+                p_level[nas] = lv;
+                p_moved[nas] = 1;
+                ++nas;
+                ++nls;
+                continue;
+            }
+            if (p_level[a] > 1) {
+                p_gain[a] = -INFINITY;   // not taken; the simulation goes on below it
+                continue;
+            }
+            // computed splits: every round may need one for the leaf it is
+            // blocked on, at most L - na more; extras keep np + L - na <=
+            // pend_cap - 1 (so the first of a round always fits)
+            const int np = (int)sp.size();
+            if (np >= w.pend_cap) return fail(-5, "yabt_grow_ref: computed splits exceed the workspace");
+            if (j > 0 && np + L - na > w.pend_cap - 1) break;
+            const LeafView v = view(p_src[a]);
+            HSplit q;
+            q.origin = p_src[a];
+            q.f = v.f;
+            q.b = v.b;
+            q.depth = v.depth + 1;
+            q.slot_p = v.slot;
+            q.s = v.s;
+            q.e = v.e;
+            q.mid = v.s;
+            q.child_pend[0] = q.child_pend[1] = -1;
+            q.child_node[0] = q.child_node[1] = -1;
+            sp.push_back(q);
+            if (q.origin >= 0) sp[(size_t)(q.origin >> 1)].child_pend[q.origin & 1] = np;
+            if (!p_moved[a]) t_pend[a] = np;    // a committed leaf's entry
+            p_gain[a] = -INFINITY;
+            Job& J = R.job[j];
+            J.f = v.f;
+            J.b = v.b;
+            J.src = v.arr;
+            J.dst = (v.depth + 1) % 3;
+            J.slot_p = v.slot;
+            J.slot_l = 1 + 2 * np;
+            J.slot_r = 2 + 2 * np;
+            J.s = v.s;
+            J.e = v.e;
+            const int64_t m = v.e - v.s;
+            R.boff[j + 1] = R.boff[j] + (int32_t)max((int64_t)1, (m + PT - 1) / PT);
+            R.toff[j + 1] = R.toff[j] + (int32_t)max((int64_t)1, (m / 2 + WT - 1) / WT);
+            ++j;
+        }
+        if (j == 0) break;
+        R.K = j;
+        // partition, histograms of the built children, both children's scans
+        if ((rc = launch_round())) return rc;
+        const int nblk = R.boff[j];
+        k_part_flags<<<nblk, RB, 0, stream>>>(bins_fm, ld_fm, w.round, w.rows, w.rows_ld, w.flag, w.blk);
+        k_part_offsets<<<j, RB, 0, stream>>>(w.blk, w.round);
+        k_part_rank<<<nblk, RB, 0, stream>>>(w.flag, w.blk, w.round, w.rank, w.p, w.q);
+        k_part_permute<<<nblk, RB, 0, stream>>>(w.flag, w.rank, w.p, w.q, w.round, w.rows, w.rows_ld, grad, hess,
+                                                 w.G, w.H, w.path, F);
+        g.hist(false, j, R.toff[j], w.G, w.H);
+        k_scan_feature<<<dim3(F, 2 * j), WAVE, 0, stream>>>(w.hist, g.hsz, w.round, 2, w.path, P, w.fsel, w.fgain,
+                                                             w.fb);
+        k_scan_pick<<<2 * j, WAVE, 0, stream>>>(w.hist, g.hsz, w.round, 2, F, w.fsel, w.fgain, w.fb, lr,
+                                                 (double)lam, d_res);
+        if ((rc = launch_status("yabt_grow_ref launch"))) return rc;
+        if ((rc = sync_res(seq, j, 2))) return rc;
+        for (int k = 0; k < j; ++k) {
+            HSplit& q = sp[(size_t)(np0 + k)];
+            q.mid = h_res[k].mid;
+            for (int c = 0; c < 2; ++c) {
+                const ChildRes& r = h_res[k].c[c];
+                q.cgain[c] = (float)(q.depth >= max_depth ? -INFINITY : r.gain);
+                q.cf[c] = r.f;
+                q.cb[c] = r.b;
+                q.cval[c] = r.value;
+            }
+        }
     }
 
-    // outputs: node count, per-row leaf ids, cgrow's final rows[]
-    k_set_status<<<1, 1, 0, stream>>>(out_n_nodes, n_nodes);
+    // outputs: the node arrays, per-row leaf ids, cgrow's final rows[]
+    const int32_t n_nodes = nn;
+    hipError_t e = hipSuccess;
+    auto put = [&](void* dst, const void* src, size_t bytes) {
+        if (e == hipSuccess) e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream);
+    };
+    put(out_feature, o_feature.data(), (size_t)N * sizeof(int64_t));
+    put(out_thr_bin, o_thr.data(), (size_t)N * sizeof(int64_t));
+    put(out_left, o_left.data(), (size_t)N * sizeof(int64_t));
+    put(out_right, o_right.data(), (size_t)N * sizeof(int64_t));
+    put(out_value, o_value.data(), (size_t)N * sizeof(float));
+    put(out_depth, o_depth.data(), (size_t)N * sizeof(int64_t));
+    put(out_n_nodes, &n_nodes, sizeof(int32_t));
     std::vector<int64_t> segs;   // read by the copy below until the final synchronisation
-    if (out_leaf_of_row && n > 0) {
-        for (int i = 0; i < n_nodes; ++i)
-            if (!split[i]) {
-                segs.push_back(i);
-                segs.push_back(node_start[i]);
-                segs.push_back(node_end[i]);
-            }
-        const int n_leaf = (int)(segs.size() / 3);
-        hipError_t e = hipMemcpyAsync(w.segs, segs.data(), segs.size() * sizeof(int64_t), hipMemcpyHostToDevice, stream);
-        if (e != hipSuccess) return hip_fail(e, "yabt_grow_ref: leaf segments");
-        k_leaf_rows<<<dim3((unsigned)launch_grid(n, RB * 4, 256), (unsigned)n_leaf), RB, 0, stream>>>(w.rows, w.segs,
-                                                                                                   n_leaf,
-                                                                                                   out_leaf_of_row);
+    if ((out_leaf_of_row || out_rows) && n > 0) {
+        for (int a = 0; a < na; ++a) {
+            const LeafView v = view(t_src[a]);
+            segs.push_back(t_node[a]);
+            segs.push_back(v.s);
+            segs.push_back(v.e);
+            segs.push_back(v.arr);
+        }
+        const int n_leaf = (int)(segs.size() / 4);
+        put(w.segs, segs.data(), segs.size() * sizeof(int64_t));
+        if (e == hipSuccess)
+            k_leaf_rows<<<dim3((unsigned)launch_grid(n, RB * 4, 256), (unsigned)n_leaf), RB, 0, stream>>>(
+                w.rows, w.rows_ld, w.segs, n_leaf, out_leaf_of_row, out_rows);
     }
-    if (out_rows && n > 0) k_rows_out<<<launch_grid(n, RB * 4, 4096), RB, 0, stream>>>(w.rows, n, out_rows);
+    if (e != hipSuccess) return hip_fail(e, "yabt_grow_ref: outputs");
     if ((rc = launch_status("yabt_grow_ref launch"))) return rc;
-    const hipError_t e = hipStreamSynchronize(stream);
+    e = hipStreamSynchronize(stream);
     return e == hipSuccess ? 0 : hip_fail(e, "yabt_grow_ref: final synchronisation");
 }
 
