@@ -46,21 +46,31 @@ def test_host_size_queries():
     assert lib.yabt_best_split_workspace_bytes(100) >= 100 * 24
 
 
+def _ref_hist_bytes(F, L):
+    """fp32 (3, F, 256) histograms of the root and both children of every
+    split the grower may compute: 3 L + 16 of them (16 per round)."""
+    return (1 + 2 * (3 * L + 16)) * 3 * F * 256 * 4
+
+
 def test_reference_grower_workspace_sizes():
     """The reference grower's bucket lists: 2 bytes per (row, feature), 4 with
     the sparse builder, all features at once up to 8 GiB, one feature at the
-    minimum."""
+    minimum; plus the histogram slots and ~33 bytes per row of row arrays,
+    partition arrays and g, h."""
     lib = _lib.load()
     n, F, L = 10_000_000, 100, 255
-    hist = (2 * L + 1) * 3 * F * 256 * 4
+    hist = _ref_hist_bytes(F, L)
     full = lib.yabt_grow_ref_workspace_bytes(n, F, L, 0)
-    assert 2 * n * F + hist < full < 2 * n * F + hist + 28 * n + 300 << 20
+    assert 2 * n * F + hist < full < 2 * n * F + hist + 40 * n + (300 << 20)
     assert lib.yabt_grow_ref_workspace_bytes(n, F, L, 1) - full >= 2 * n * F
     low = lib.yabt_grow_ref_workspace_min_bytes(n, F, L, 0)
     assert full - low >= 2 * n * (F - 1)
     # 4M x 5000 would need 40 GB of lists: capped near 8 GiB
-    big = lib.yabt_grow_ref_workspace_bytes(4_000_000, 5000, 64, 0)
-    assert (8 << 30) < big < (8 << 30) + 5000 * 64 * 3 * 256 * 4 * 2 + (1 << 30)
+    nb, Fb, Lb = 4_000_000, 5000, 64
+    hist = _ref_hist_bytes(Fb, Lb)
+    big = lib.yabt_grow_ref_workspace_bytes(nb, Fb, Lb, 0)
+    lists_of_one = 2 * (nb + 16 * 4096)
+    assert (8 << 30) - lists_of_one + hist < big < (8 << 30) + hist + 40 * nb + (1 << 30)
     assert lib.yabt_grow_ref_workspace_bytes(100, 0, 31, 0) == 0
     assert lib.yabt_grow_ref_workspace_min_bytes(100, 4, 0, 0) == 0
 
