@@ -24,10 +24,10 @@
 //     so the host computes up to KR splits per round -- planned by running
 //     the leaf table ahead through the splits already computed -- and
 //     commits them in cgrow's best-first order: one device round trip per
-//     round.  A node at depth d keeps its rows at [s, e) of row array d % 3,
-//     so a computed split never moves its leaf's rows (the lookahead goes at
-//     most two levels below a committed leaf) and cgrow's final rows[] is the
-//     final leaves' segments of their arrays.
+//     round.  A node at depth d keeps its rows at [s, e) of row array
+//     d % RA, so a computed split never moves its leaf's rows (the lookahead
+//     goes at most RA - 1 levels below a committed leaf) and cgrow's final
+//     rows[] is the final leaves' segments of their arrays.
 //
 // Partition.  With positions relative to the node start, m rows, and
 //   p_k = position of the k-th row going right, counted from the left,
@@ -38,7 +38,7 @@
 //     its position is below q_K; every other right row moves one place left;
 //   * the left row of rank t to p_t if t <= K; every other left row stays.
 //
-// Workspace (yabt_grow_ref_workspace_bytes): three row arrays (n u32), the
+// Workspace (yabt_grow_ref_workspace_bytes): RA row arrays (n u32), the
 // partition's flags / ranks / p / q arrays and the built children's g and h
 // by position, the bucket lists, and one (3, F, 256) fp32 histogram per
 // slot: the root's and the two children of every computed split.
@@ -61,6 +61,7 @@ constexpr int PT = 2048;           // partition rows per block
 constexpr int WT = 4096;           // histogram rows per tile
 constexpr int ST = NB + 1;         // bucket starts per (feature, tile)
 constexpr int KR = 16;             // splits computed per round, at most
+constexpr int RA = 6;              // row arrays: a node at depth d uses array d % RA
 constexpr int PEND_PER_LEAF = 3;   // computed splits per leaf of the budget, at most
 
 // One split of a round (the root's histogram: a pseudo-job with the whole
@@ -68,7 +69,7 @@ constexpr int PEND_PER_LEAF = 3;   // computed splits per leaf of the budget, at
 // fills the partition's outcome.
 struct Job {
     int32_t f, b;                  // the split
-    int32_t src, dst;              // row arrays of the leaf (depth % 3) and of its children
+    int32_t src, dst;              // row arrays of the leaf (depth % RA) and of its children
     int32_t slot_p, slot_l, slot_r;    // histogram / path slots: the leaf (-1: none), its children
     int32_t build_left;            // the smaller child, ties left (grow.c:355)
     int64_t s, e;                  // the leaf's segment
@@ -108,7 +109,7 @@ __device__ __forceinline__ int job_of(const int32_t* off, int K, int64_t x) {
 }
 
 struct Ws {
-    uint32_t* rows;                // three arrays of rows_ld ids: depth % 3
+    uint32_t* rows;                // RA arrays of rows_ld ids: depth % RA
     int64_t rows_ld;
     uint8_t* flag;
     uint32_t* rank;
@@ -151,7 +152,7 @@ Ws carve(char* base, int64_t n, int F, int max_leaves, bool sparse, int fgroup) 
     w.pend_cap = PEND_PER_LEAF * max_leaves + KR;
     w.slots = 1 + 2 * w.pend_cap;
     w.rows_ld = (nn + 63) / 64 * 64;
-    w.rows = c.take<uint32_t>(3 * (size_t)w.rows_ld);
+    w.rows = c.take<uint32_t>((size_t)RA * (size_t)w.rows_ld);
     w.flag = c.take<uint8_t>(nn);
     w.rank = c.take<uint32_t>(nn);
     w.p = c.take<uint32_t>(nn);
@@ -1284,7 +1285,7 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
             v.s = c ? q.mid : q.s;
             v.e = c ? q.e : q.mid;
         }
-        v.arr = v.depth % 3;
+        v.arr = v.depth % RA;
         return v;
     };
     // cgrow's leaf table (grow.c:284-287): gain, computed split, origin, node id
@@ -1347,9 +1348,9 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
         // plan: the table run ahead -- a leaf whose split is computed gives
         // way to its children, a leaf without one is taken for the round.
         // Only leaves at most one computed split below a committed leaf are
-        // taken (level <= 1): a split at depth d writes row array (d + 1) % 3,
-        // so a third level would overwrite the rows of a committed leaf that
-        // may stay a leaf.
+        // taken (level <= RA - 2): a split at depth d writes row array
+        // (d + 1) % RA, so one level more would overwrite the rows of a
+        // committed leaf that may stay a leaf.
         for (int a = 0; a < na; ++a) {
             p_gain[a] = t_gain[a];
             p_pend[a] = t_pend[a];
@@ -1383,7 +1384,7 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
                 ++nls;
                 continue;
             }
-            if (p_level[a] > 1) {
+            if (p_level[a] > RA - 2) {
                 p_gain[a] = -INFINITY;   // not taken; the simulation goes on below it
                 continue;
             }
@@ -1413,7 +1414,7 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
             J.f = v.f;
             J.b = v.b;
             J.src = v.arr;
-            J.dst = (v.depth + 1) % 3;
+            J.dst = (v.depth + 1) % RA;
             J.slot_p = v.slot;
             J.slot_l = 1 + 2 * np;
             J.slot_r = 2 + 2 * np;
