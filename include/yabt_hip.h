@@ -259,9 +259,11 @@ size_t yabt_grow_ref_workspace_min_bytes(int64_t n, int F, int max_leaves, int s
  * node's rows outside the default bin).  out_status is replaced by
  * out_n_nodes (device int32, cgrow's return value).  Optional outputs (NULL
  * to skip): out_leaf_of_row (n int64) per-row leaf node ids; out_rows (n
- * int64) cgrow's final rows[] array.  The control loop runs on the host, one
- * device round trip per split, and the call returns after the stream has
- * finished (it synchronises `stream`).  Requires n < 2^32, F >= 1,
+ * int64) cgrow's final rows[] array.  cgrow's leaf table runs on the host,
+ * which computes up to 16 splits per round (planned by running the table
+ * ahead through the splits already computed) and commits them in cgrow's
+ * order: one device round trip per round.  The call returns after the
+ * stream has finished (it synchronises `stream`).  Requires n < 2^32, F >= 1,
  * 1 <= max_leaves <= 32767. */
 int yabt_grow_ref(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
                   const float *grad, const float *hess, const uint8_t *fmask, const float *imat,

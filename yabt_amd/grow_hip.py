@@ -185,7 +185,7 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
     ``arithmetic``: "exact" (yabt_grow: exact fixed-point sums, the whole
     tree on the device) or "reference" (yabt_grow_ref: cgrow's own fp32
     arithmetic and row order, the same trees as the reference bit for bit,
-    one host round trip per split).
+    one host round trip per round of up to 16 splits).
 
     ``growth`` ("exact" only; every choice gives the same tree bit for bit):
     "sequential" (yabt_grow, one split per launch triple, all on the
