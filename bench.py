@@ -493,7 +493,7 @@ def main() -> None:
                       "updates_per_s": round(n * F / (root_mean_ms * 1e-3) / 1e9, 3),
                       "unit": "G updates/s", "GBps": round(achieved, 1),
                       "frac_hbm": round(achieved / HBM_PEAK_GBS, 4)},
-        "roofline": {"kernel": "k_hist_root<16> (streaming root histogram)", "bound": "hbm",
+        "roofline": {"kernel": "k_hist_root<false> (streaming root histogram)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic()},
     }
