@@ -28,7 +28,8 @@
 // leaf ids (same sums, same scan, same order); the others are never read.
 //
 // Launches: k_setup, k_setup_finish, k_hist_root, k_scan<true> (root, plans
-// round 1), then per round k_part, k_gather, k_scan<false>, and k_leaf_ids.
+// round 1), then per round k_part, k_gather, k_scan<false>, and at the end
+// k_leaf_plan, k_leaf_ids (per-row leaf ids).
 // The controller writes the round count and the done flag to mapped host
 // memory; the host keeps at most LOOKAHEAD rounds in flight and stops when
 // the tree is done.
