@@ -158,10 +158,46 @@ __device__ __forceinline__ void hist_root_body(HistLds& L, const uint8_t* __rest
 
 constexpr int HENT = NB * HFL / HBLOCK;       // entries per thread in an unpack
 
+// Packed-word LDS of the gather (see hist_gather_packed); its callers keep it
+// in a union with HistLds, which the final flush reuses.
 struct HistLdsP {
     unsigned long long g[NB * HFL];           // sum q(g) (with the h channel)
     unsigned long long p[NB * HFL];           // packed (q << cb) + 1
 };
+
+// Final flush of the packed kernels: thread t holds cells i = t + k HBLOCK
+// (bin i / HFL, feature f0 + i % HFL) with sums g, h and counts c.  They go
+// through the block's LDS (a HistLds, 80 KB, which the kernels' LDS unions
+// hold) transposed to [feature][bin], so that a wave's global atomics cover
+// 64 consecutive bins of one feature: four 128-byte lines per instruction
+// instead of sixteen.  The caller has finished with its own LDS layout (a
+// barrier before the call); cells without rows and features >= F are
+// skipped.
+template <bool HCH>
+__device__ __forceinline__ void flush_cells(HistLds& T, const uint64_t (&g)[HENT], const int64_t (&h)[HENT],
+                                            const uint32_t (&c)[HENT], int64_t* out, int F, int f0) {
+#pragma unroll
+    for (int k = 0; k < HENT; ++k) {
+        const int i = threadIdx.x + k * HBLOCK;
+        const int j = (i % HFL) * NB + i / HFL;
+        T.g[j] = g[k];
+        if (HCH) T.h[j] = (unsigned long long)h[k];
+        T.c[j] = c[k];
+    }
+    __syncthreads();
+    const size_t plane = (size_t)F * NB;
+#pragma unroll
+    for (int k = 0; k < HENT; ++k) {
+        const int j = threadIdx.x + k * HBLOCK;
+        const int fi = f0 + j / NB;
+        const uint32_t cj = T.c[j];
+        if (fi >= F || cj == 0) continue;
+        const size_t at = (size_t)fi * NB + (size_t)(j % NB);
+        atomicAdd((unsigned long long*)(out + at), T.g[j]);
+        if (HCH) atomicAdd((unsigned long long*)(out + plane + at), T.h[j]);
+        atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)cj);
+    }
+}
 
 // log2 of the packing window for n rows, or -1 when a window would be
 // shorter than one block step (then the three-word layout is used).
@@ -327,18 +363,14 @@ __device__ __forceinline__ void hist_root_packed(HistLdsR& L, const uint8_t* __r
             atomicAdd((unsigned long long*)&q_tot->tot_h, (unsigned long long)sum_h);
         }
     }
-    const size_t plane = (size_t)F * NB;
+    uint64_t gv[HENT];
 #pragma unroll
     for (int k = 0; k < HENT; ++k) {
         const int i = threadIdx.x + k * HBLOCK;
-        const int fi = f0 + (i % HFL);
-        if (fi >= F || ca[k] == 0) continue;
-        const size_t at = (size_t)fi * NB + (size_t)(i / HFL);
-        atomicAdd((unsigned long long*)(out + at),
-                  HCH ? L.w[(i / HFL) * (2 * HFL) + (i % HFL)] : (unsigned long long)qa[k]);
-        if (HCH) atomicAdd((unsigned long long*)(out + plane + at), (unsigned long long)qa[k]);
-        atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)ca[k]);
+        gv[k] = HCH ? L.w[(i / HFL) * (2 * HFL) + (i % HFL)] : (uint64_t)qa[k];
     }
+    __syncthreads();   // every g cell read before the LDS is rewritten
+    flush_cells<HCH>(*reinterpret_cast<HistLds*>(&L), gv, qa, ca, out, F, f0);
 }
 
 // count_mode 0: all three channels; 1: no h channel when q->const_h.
@@ -623,17 +655,11 @@ __device__ __forceinline__ void hist_gather_packed(HistLdsP& L, const uint8_t* _
         for (int J = 0; J < HFL; ++J) bj[J] = bn[J];
     }
 #undef YABT_GATHER_BINS
-    const size_t plane = (size_t)F * NB;
+    uint64_t gv[HENT];
 #pragma unroll
-    for (int k = 0; k < HENT; ++k) {
-        const int i = threadIdx.x + k * HBLOCK;
-        const int fi = f0 + (i % HFL);
-        if (fi >= F || ca[k] == 0) continue;
-        const size_t at = (size_t)fi * NB + (size_t)(i / HFL);
-        atomicAdd((unsigned long long*)(out + at), HCH ? L.g[i] : (unsigned long long)qa[k]);
-        if (HCH) atomicAdd((unsigned long long*)(out + plane + at), (unsigned long long)qa[k]);
-        atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)ca[k]);
-    }
+    for (int k = 0; k < HENT; ++k) gv[k] = HCH ? L.g[threadIdx.x + k * HBLOCK] : (uint64_t)qa[k];
+    __syncthreads();   // every g cell read before the LDS is rewritten
+    flush_cells<HCH>(*reinterpret_cast<HistLds*>(&L), gv, qa, ca, out, F, f0);
 }
 
 // job->active == 0 or *done != 0 (done may be NULL): nothing to do.  wlog:
