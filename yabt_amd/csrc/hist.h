@@ -170,16 +170,20 @@ struct HistLdsP {
 // through the block's LDS (a HistLds, 80 KB, which the kernels' LDS unions
 // hold) transposed to [feature][bin], so that a wave's global atomics cover
 // 64 consecutive bins of one feature: four 128-byte lines per instruction
-// instead of sixteen.  The caller has finished with its own LDS layout (a
-// barrier before the call); cells without rows and features >= F are
-// skipped.
+// instead of sixteen.  Feature fl's bin b sits at fl NB + (b ^ 2 fl): the
+// swizzle spreads the 16 features a half-wave writes for two bins over 32
+// distinct bank pairs (unswizzled they share one), and stays inside each
+// aligned group of 64 bins, so a wave's reads still cover 64 consecutive
+// bins.  The caller has finished with its own LDS layout (a barrier before
+// the call); cells without rows and features >= F are skipped.
 template <bool HCH>
 __device__ __forceinline__ void flush_cells(HistLds& T, const uint64_t (&g)[HENT], const int64_t (&h)[HENT],
                                             const uint32_t (&c)[HENT], int64_t* out, int F, int f0) {
 #pragma unroll
     for (int k = 0; k < HENT; ++k) {
         const int i = threadIdx.x + k * HBLOCK;
-        const int j = (i % HFL) * NB + i / HFL;
+        const int fl = i % HFL;
+        const int j = fl * NB + ((i / HFL) ^ (2 * fl));
         T.g[j] = g[k];
         if (HCH) T.h[j] = (unsigned long long)h[k];
         T.c[j] = c[k];
@@ -189,10 +193,11 @@ __device__ __forceinline__ void flush_cells(HistLds& T, const uint64_t (&g)[HENT
 #pragma unroll
     for (int k = 0; k < HENT; ++k) {
         const int j = threadIdx.x + k * HBLOCK;
-        const int fi = f0 + j / NB;
+        const int fl = j / NB;
+        const int fi = f0 + fl;
         const uint32_t cj = T.c[j];
         if (fi >= F || cj == 0) continue;
-        const size_t at = (size_t)fi * NB + (size_t)(j % NB);
+        const size_t at = (size_t)fi * NB + (size_t)((j % NB) ^ (2 * fl));
         atomicAdd((unsigned long long*)(out + at), T.g[j]);
         if (HCH) atomicAdd((unsigned long long*)(out + plane + at), T.h[j]);
         atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)cj);
