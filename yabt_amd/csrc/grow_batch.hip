@@ -80,7 +80,8 @@ struct Pend {
     int64_t s, e, mid;
     int64_t tot[3], left[3];
     int64_t* new_hist;                   // the built child's slot
-    unsigned long long cursor[2];        // next write position, left / right
+    unsigned long long placed;           // rows placed: left count in the low 32 bits, right in the high 32
+    unsigned long long pad1;
     ScanRec child[2];                    // the children's best records (b = -1: none)
 };
 
@@ -212,8 +213,10 @@ __global__ void k_setup_finish(Args A) {
 // ---------------------------------------------------------------------------
 
 // Rows of [s, e) with bin <= b go to [s, mid), the others to [mid, e) of the
-// children's row list, through two atomic cursors per split (the order inside
-// a child depends on the schedule, which no exact sum does).  The blocks also
+// children's row list.  A tile reserves its places in both children with one
+// 64-bit atomic on the split's packed (left, right) count: a child holds at
+// most n < 2^32 rows, so the left half never carries into the right.  (The
+// order inside a child depends on the schedule, which no exact sum does.)  The blocks also
 // clear the round's new histogram slots, which the gather adds into.
 __global__ void __launch_bounds__(SB) k_part(const uint8_t* __restrict__ bins_fm, int64_t ld, int64_t n, State* st,
                                              Pend* pend, int64_t slot_n) {
@@ -268,8 +271,10 @@ __global__ void __launch_bounds__(SB) k_part(const uint8_t* __restrict__ bins_fm
                 tl += s_cnt[i][0];
                 tr += s_cnt[i][1];
             }
-            unsigned long long bl = atomicAdd(&P.cursor[0], (unsigned long long)tl);
-            unsigned long long br = atomicAdd(&P.cursor[1], (unsigned long long)tr);
+            const unsigned long long old =
+                atomicAdd(&P.placed, (unsigned long long)tl | ((unsigned long long)tr << 32));
+            unsigned long long bl = (unsigned long long)P.s + (old & 0xFFFFFFFFull);
+            unsigned long long br = (unsigned long long)P.mid + (old >> 32);
             for (int i = 0; i < SB / WAVE; ++i) {
                 s_base[i][0] = bl;
                 s_base[i][1] = br;
@@ -608,8 +613,8 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
             P.left[i] = Lv.left[i];
         }
         P.new_hist = A.hist + (size_t)(p + 1) * slot_elems(A.F);
-        P.cursor[0] = (unsigned long long)P.s;
-        P.cursor[1] = (unsigned long long)P.mid;
+        P.placed = 0;
+        P.pad1 = 0;
         P.child[0].b = P.child[1].b = -1;
         A.pend[p] = P;
         PendSum S;
