@@ -24,7 +24,7 @@
 //   max_leaves - 1 times (each kernel returns at once once the tree is done):
 //     k_split_partition      clear the built child's slot; one pass: the
 //                            children's rows to the other row list, written
-//                            through two atomic cursors (left, right)
+//                            through one atomic packed (left, right) count
 //     k_hist_gather          histogram of the smaller child
 //     k_scan<SPLIT>          fill, sibling = parent - child, scan both
 //                            children (one wave each), the last block picks
@@ -82,7 +82,8 @@ struct SplitJob {
     int64_t tot[3];            // parent totals
     int64_t left[3];           // left-child totals
     int64_t* new_hist;         // the built child's slot, cleared by the partition launch
-    unsigned long long cursor[2];   // next write position, left / right
+    unsigned long long placed;      // rows placed: left count in the low 32 bits, right in the high 32
+    unsigned long long pad1;
 };
 
 struct GrowState {
@@ -183,7 +184,7 @@ __global__ void k_setup_finish(GrowArgs A) {
 }
 
 // ---------------------------------------------------------------------------
-// partition: one pass, two atomic write cursors
+// partition: one pass, one packed atomic count per tile
 // ---------------------------------------------------------------------------
 
 // Rows of [s, e) with bin <= b go to [s, mid), the others to [mid, e) of the
@@ -248,8 +249,12 @@ __global__ void __launch_bounds__(SB) k_split_partition(const uint8_t* __restric
                 tl += s_cnt[i][0];
                 tr += s_cnt[i][1];
             }
-            unsigned long long bl = atomicAdd(&J.cursor[0], (unsigned long long)tl);
-            unsigned long long br = atomicAdd(&J.cursor[1], (unsigned long long)tr);
+            // one atomic reserves both children's places (a child holds at
+            // most n < 2^32 rows: the left half never carries)
+            const unsigned long long old =
+                atomicAdd(&J.placed, (unsigned long long)tl | ((unsigned long long)tr << 32));
+            unsigned long long bl = (unsigned long long)J.s + (old & 0xFFFFFFFFull);
+            unsigned long long br = (unsigned long long)J.mid + (old >> 32);
             for (int i = 0; i < SB / WAVE; ++i) {
                 s_base[i][0] = bl;
                 s_base[i][1] = br;
@@ -409,8 +414,8 @@ __device__ void select_next(const GrowArgs& A, const float* gpre, int n_pre, int
         J.left[i] = L.left[i];
     }
     J.new_hist = A.hist + (size_t)new_slot * slot_elems(A.F);
-    J.cursor[0] = (unsigned long long)s;
-    J.cursor[1] = (unsigned long long)(s + cl);
+    J.placed = 0;
+    J.pad1 = 0;
     HistJob& H = st->hist;
     H.rows = J.dst;
     H.lo = bl ? s : s + cl;
