@@ -268,15 +268,50 @@ __device__ void quant_reduce(const float* grad, const float* hess, int64_t n, Qu
     float mg = 0.0f, mh = 0.0f;
     uint32_t kmin = 0xffffffffu, kmax = 0u;
     int nf = 0;
-    for (int64_t i = (int64_t)blockIdx.x * NT + threadIdx.x; i < n; i += (int64_t)gridDim.x * NT) {
-        const float a = grad[i], c = hess[i];
+    auto take = [&](float a, float c) {
         if (!isfinite(a) || !isfinite(c)) nf = 1;
         mg = fmaxf(mg, fabsf(a));
         mh = fmaxf(mh, fabsf(c));
         const uint32_t kc = float_key(c);
         kmin = min(kmin, kc);
         kmax = max(kmax, kc);
+    };
+    const int64_t tid = (int64_t)blockIdx.x * NT + threadIdx.x, nth = (int64_t)gridDim.x * NT;
+    int64_t head = 0;   // rows [0, head) taken by the vector loop
+    if (((reinterpret_cast<uintptr_t>(grad) | reinterpret_cast<uintptr_t>(hess)) & 15) == 0) {
+        // 16-byte loads, four of g and four of h in flight per thread (the
+        // scalar loop kept one of each: ~1 TB/s); max, min and the finite
+        // test do not depend on the order
+        constexpr int U = 4;
+        const int64_t n4 = n / 4;
+        const float4* g4 = reinterpret_cast<const float4*>(grad);
+        const float4* h4 = reinterpret_cast<const float4*>(hess);
+        int64_t i = tid;
+        for (; i + (U - 1) * nth < n4; i += U * nth) {
+            float4 a[U], c[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                a[u] = g4[i + u * nth];
+                c[u] = h4[i + u * nth];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                take(a[u].x, c[u].x);
+                take(a[u].y, c[u].y);
+                take(a[u].z, c[u].z);
+                take(a[u].w, c[u].w);
+            }
+        }
+        for (; i < n4; i += nth) {
+            const float4 a = g4[i], c = h4[i];
+            take(a.x, c.x);
+            take(a.y, c.y);
+            take(a.z, c.z);
+            take(a.w, c.w);
+        }
+        head = n4 * 4;
     }
+    for (int64_t i = head + tid; i < n; i += nth) take(grad[i], hess[i]);
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
 #pragma unroll
     for (int d = WAVE / 2; d > 0; d >>= 1) {
@@ -300,10 +335,14 @@ __device__ void quant_reduce(const float* grad, const float* hess, int64_t n, Qu
             kmin = min(kmin, s_k[0][i]);
             kmax = max(kmax, s_k[1][i]);
         }
-        atomicMax(&q->maxg_bits, __float_as_uint(mg));
-        atomicMax(&q->maxh_bits, __float_as_uint(mh));
-        atomicMin(&q->hmin_key, kmin);
-        atomicMax(&q->hmax_key, kmax);
+        // The words only move one way, so a block whose value does not beat
+        // what a word already holds skips its atomic: most blocks do, and
+        // the atomics of a thousand blocks on four words serialise.
+        auto seen = [](uint32_t* w) { return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+        if (__float_as_uint(mg) > seen(&q->maxg_bits)) atomicMax(&q->maxg_bits, __float_as_uint(mg));
+        if (__float_as_uint(mh) > seen(&q->maxh_bits)) atomicMax(&q->maxh_bits, __float_as_uint(mh));
+        if (kmin < seen(&q->hmin_key)) atomicMin(&q->hmin_key, kmin);
+        if (kmax > seen(&q->hmax_key)) atomicMax(&q->hmax_key, kmax);
         if (s_nf) atomicOr(&q->nonfinite, 1);
     }
 }
