@@ -19,7 +19,8 @@ no eval set, no refinement; yabt/boosting.py:271-515): ``Binner``,
 
 It stores the per-tree node arrays, leaf models and predictions as .npz
 files; it runs only where the reference sources are mounted, and the
-fixtures are what tests/test_gpu_golden_booster.py reads.
+fixtures are what tests/test_gpu_grow_ref.py and tests/test_boost_oracle.py
+read.
 
     python tests/golden/make_booster_golden.py
 """

@@ -250,9 +250,21 @@ class Booster:
         full = torch.stack([torch.bincount(fm[f], minlength=256) for f in range(F)])
         return full.argmax(dim=1).to(torch.int32).contiguous()
 
+    def prepare(self, X: np.ndarray) -> tuple:
+        """Binning on the device: fit, then both bin layouts and the imputed
+        matrix from one pass over the raw X (binning.py:29-118).  The result
+        depends only on X and ``max_bins``, so boosters fitted on the same X
+        (one-vs-rest classes) can share it through ``fit(..., prepared=)``."""
+        dev = self._device()
+        Xd = torch.from_numpy(np.ascontiguousarray(np.asarray(X, dtype=np.float32))).to(dev)
+        binner = Binner(max_bins=self.p.max_bins).fit(Xd)
+        lay, Xraw = binner.layouts(Xd)
+        return binner, lay, Xraw
+
     def fit(self, X: np.ndarray, y: np.ndarray,
-            eval_set: tuple[np.ndarray, np.ndarray] | None = None) -> "Booster":
-        """The reference's training loop (boosting.py:271-534) on the device."""
+            eval_set: tuple[np.ndarray, np.ndarray] | None = None, prepared: tuple | None = None) -> "Booster":
+        """The reference's training loop (boosting.py:271-534) on the device.
+        ``prepared``: the result of ``prepare(X)`` for this X, if already made."""
         p = self.p
         check_supported(p)
         dev = self._device()
@@ -262,12 +274,7 @@ class Booster:
         self.best_iter = None
         self._forest = None
 
-        # binning on the device: fit, then both bin layouts and the imputed
-        # matrix from one pass over the raw X
-        Xd = torch.from_numpy(np.ascontiguousarray(np.asarray(X, dtype=np.float32))).to(dev)
-        self.binner = Binner(max_bins=p.max_bins).fit(Xd)
-        lay, Xraw = self.binner.layouts(Xd)
-        del Xd
+        self.binner, lay, Xraw = prepared if prepared is not None else self.prepare(X)
         n, F = Xraw.shape
         binned = lay.rm[:n, :F]          # (n, F) view, used for row subsamples
         yt = torch.as_tensor(np.asarray(y, dtype=np.float32), device=dev)
@@ -396,12 +403,15 @@ class MulticlassBooster:
             eval_set: tuple[np.ndarray, np.ndarray] | None = None) -> "MulticlassBooster":
         self.classes_ = np.unique(y)
         self.boosters_ = []
+        # every class's booster bins the same X the same way (multiclass.py:25-33):
+        # bin once and share the binner, the bin layouts and the imputed X
+        prepared = Booster(self.params, LogLoss()).prepare(X) if len(self.classes_) else None
         for label in self.classes_:
             yb = (y == label).astype(np.float32)
             evb = None
             if eval_set is not None:
                 evb = (eval_set[0], (eval_set[1] == label).astype(np.float32))
-            self.boosters_.append(Booster(self.params, LogLoss()).fit(X, yb, eval_set=evb))
+            self.boosters_.append(Booster(self.params, LogLoss()).fit(X, yb, eval_set=evb, prepared=prepared))
         return self
 
     def predict_margin(self, X: np.ndarray) -> np.ndarray:

@@ -613,16 +613,20 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : 2 * SCAN_FEATS * WA
 }
 
 // out[row] = leaf node id, from each leaf's segment of the final row lists.
-// Grid (chunks, nodes).
+// Grid (chunks, nodes).  Segments are clamped to [0, n) and row ids >= n are
+// dropped, so a workspace that no longer holds this tree's rows (grown over
+// since, with another n) cannot write outside `out`.
 __global__ void __launch_bounds__(SB) k_leaf_ids(const int64_t* feature, const int64_t* depth, const int64_t* seg_lo,
                                                  const int64_t* seg_hi, const uint32_t* rows0, const uint32_t* rows1,
-                                                 const int32_t* out_status, int64_t* out) {
+                                                 const int32_t* out_status, int64_t n, int64_t* out) {
     const int nid = blockIdx.y;
     if (nid >= out_status[0] || feature[nid] != LEAF) return;
-    const int64_t lo = seg_lo[nid], hi = seg_hi[nid], d = depth[nid];
+    const int64_t lo = max((int64_t)0, seg_lo[nid]), hi = min(n, seg_hi[nid]), d = depth[nid];
     const uint32_t* rows = (d == 0) ? nullptr : ((d & 1) ? rows1 : rows0);
-    for (int64_t i = lo + (int64_t)blockIdx.x * SB + threadIdx.x; i < hi; i += (int64_t)gridDim.x * SB)
-        out[rows ? (int64_t)rows[i] : i] = nid;
+    for (int64_t i = lo + (int64_t)blockIdx.x * SB + threadIdx.x; i < hi; i += (int64_t)gridDim.x * SB) {
+        const int64_t r = rows ? (int64_t)rows[i] : i;
+        if (r < n) out[r] = nid;
+    }
 }
 
 size_t carve_grow(char* base, int64_t n, int F, int max_leaves, GrowArgs* A) {
@@ -734,7 +738,7 @@ int yabt_grow_leaf_ids(void* workspace, int64_t n, int F, int max_leaves, const 
     memset(&A, 0, sizeof A);
     carve_grow((char*)workspace, n, F, max_leaves, &A);
     dim3 grid(launch_grid(n, SB * 8, 256), 2 * max_leaves + 1);
-    k_leaf_ids<<<grid, SB, 0, stream>>>(feature, depth, A.seg_lo, A.seg_hi, A.rows0, A.rows1, status, out);
+    k_leaf_ids<<<grid, SB, 0, stream>>>(feature, depth, A.seg_lo, A.seg_hi, A.rows0, A.rows1, status, n, out);
     return launch_status("yabt_grow_leaf_ids launch");
 }
 

@@ -1053,24 +1053,24 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
     A.depth = out_depth;
     A.out_status = out_status;
 
-    Flags* h_flags = nullptr;
-    hipError_t he = hipHostMalloc((void**)&h_flags, sizeof(Flags), hipHostMallocMapped | hipHostMallocCoherent);
-    if (he != hipSuccess) return hip_fail(he, "yabt_grow_batched: mapped flags");
-    // every return waits for the stream first: enqueued controllers write
+    // the mapped flags come from the library's pinned pool; every return waits
+    // for the stream before the buffer goes back: enqueued controllers write
     // the flags until the last of them has run
-    struct Free {
-        Flags* p;
+    struct Held {
+        PinnedHold hold;
         hipStream_t s;
-        ~Free() {
-            (void)hipStreamSynchronize(s);
-            (void)hipHostFree(p);
+        ~Held() {
+            if (hold.p) (void)hipStreamSynchronize(s);
         }
-    } free_flags{h_flags, stream};
+    } held;
+    held.s = stream;
+    if (int prc = held.hold.take(sizeof(Flags), hipHostMallocMapped | hipHostMallocCoherent)) return prc;
+    Flags* h_flags = static_cast<Flags*>(held.hold.p);
     h_flags->round = -1;
     h_flags->done = 0;
     h_flags->n_nodes = 0;
     h_flags->status = 0;
-    he = hipHostGetDevicePointer((void**)&A.flags, h_flags, 0);
+    const hipError_t he = hipHostGetDevicePointer((void**)&A.flags, h_flags, 0);
     if (he != hipSuccess) return hip_fail(he, "yabt_grow_batched: mapped flags");
 
     const int tiles = (F + HFL - 1) / HFL;

@@ -497,21 +497,24 @@ int yabt_grow_levelwise(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bi
     const int sblk = (F + LSCAN - 1) / LSCAN;
     const int tiles = (F + HFL - 1) / HFL;
 
-    // pinned staging for the per-depth records and tables
-    struct Pinned {
-        void* p = nullptr;
-        ~Pinned() {
-            if (p) (void)hipHostFree(p);
+    // pinned staging for the per-depth records and tables, from the library's
+    // pinned pool; every return waits for the stream before it goes back
+    struct Held {
+        PinnedHold hold;
+        hipStream_t s;
+        ~Held() {
+            if (hold.p) (void)hipStreamSynchronize(s);
         }
     } pin;
+    pin.s = stream;
     const size_t rec_bytes = (size_t)NP * sizeof(LNode), tab_bytes = (size_t)NP * sizeof(Route);
     const size_t list_bytes = (size_t)4 * P * sizeof(int32_t) + (size_t)P * sizeof(int32_t);
-    hipError_t he = hipHostMalloc(&pin.p, rec_bytes + tab_bytes + list_bytes + (size_t)NP * sizeof(int32_t),
-                                  hipHostMallocDefault);
-    if (he != hipSuccess) return hip_fail(he, "yabt_grow_levelwise: pinned staging");
-    LNode* h_nodes = (LNode*)pin.p;
-    Route* h_route = (Route*)((char*)pin.p + rec_bytes);
-    int32_t* h_lists = (int32_t*)((char*)pin.p + rec_bytes + tab_bytes);    // scan_list (2P), pairs (2P), built_slot (P)
+    if (int prc = pin.hold.take(rec_bytes + tab_bytes + list_bytes + (size_t)NP * sizeof(int32_t),
+                                hipHostMallocDefault))
+        return prc;
+    LNode* h_nodes = (LNode*)pin.hold.p;
+    Route* h_route = (Route*)((char*)pin.hold.p + rec_bytes);
+    int32_t* h_lists = (int32_t*)((char*)pin.hold.p + rec_bytes + tab_bytes);    // scan_list (2P), pairs (2P), built_slot (P)
     int32_t* h_remap = h_lists + 5 * P;
     int32_t* h_scan = h_lists;
     int32_t* h_pairs = h_lists + 2 * P;

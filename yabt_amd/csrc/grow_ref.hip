@@ -1156,28 +1156,23 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
     const int N = 2 * max_leaves + 1;
     const int L = max_leaves;
 
-    // host staging of a round, and the round's records in mapped host memory
-    Round* h_round = nullptr;
-    Res* h_res = nullptr;
-    hipError_t he = hipHostMalloc((void**)&h_round, sizeof(Round), hipHostMallocDefault);
-    if (he != hipSuccess) return hip_fail(he, "yabt_grow_ref: pinned round buffer");
-    he = hipHostMalloc((void**)&h_res, KR * sizeof(Res), hipHostMallocMapped | hipHostMallocCoherent);
-    if (he != hipSuccess) {
-        (void)hipHostFree(h_round);
-        return hip_fail(he, "yabt_grow_ref: pinned result buffer");
-    }
-    // every return waits for the stream first: enqueued picks write h_res and
-    // enqueued copies read h_round until they have run
-    struct Free {
-        Round* r;
-        Res* p;
+    // host staging of a round, and the round's records in mapped host memory,
+    // both from the library's pinned pool; every return waits for the stream
+    // before they go back: enqueued picks write h_res and enqueued copies read
+    // h_round until they have run
+    struct Held {
+        PinnedHold round, res;
         hipStream_t s;
-        ~Free() {
-            (void)hipStreamSynchronize(s);
-            (void)hipHostFree(r);
-            (void)hipHostFree(p);
+        ~Held() {
+            if (round.p || res.p) (void)hipStreamSynchronize(s);
         }
-    } free_bufs{h_round, h_res, stream};
+    } held;
+    held.s = stream;
+    if (int prc = held.round.take(sizeof(Round), hipHostMallocDefault)) return prc;
+    if (int prc = held.res.take(KR * sizeof(Res), hipHostMallocMapped | hipHostMallocCoherent)) return prc;
+    Round* h_round = static_cast<Round*>(held.round.p);
+    Res* h_res = static_cast<Res*>(held.res.p);
+    hipError_t he = hipSuccess;
     Res* d_res = nullptr;   // the device's address of h_res
     he = hipHostGetDevicePointer((void**)&d_res, h_res, 0);
     if (he != hipSuccess) return hip_fail(he, "yabt_grow_ref: mapped result buffer");

@@ -37,6 +37,36 @@ inline int launch_grid(int64_t work, int per_block, int cap) {
     return (int)g;
 }
 
+// Pinned host buffers reused across calls.  hipHostMalloc / hipHostFree
+// cost tens of microseconds and synchronise the device, which a tree of a
+// millisecond cannot afford; a buffer is held by one call at a time, so
+// concurrent calls (from several host threads) each get their own.  Buffers
+// are kept per (device, flags) and never freed before the process ends.
+int pinned_take(size_t bytes, unsigned flags, void** out, int* device);
+void pinned_give(void* p, size_t bytes, unsigned flags, int device);
+
+// Scoped hold of a pooled buffer; the holder's destructor returns it.
+struct PinnedHold {
+    void* p = nullptr;
+    size_t bytes = 0;
+    unsigned flags = 0;
+    int device = 0;
+    int take(size_t b, unsigned f) {
+        bytes = b;
+        flags = f;
+        return pinned_take(b, f, &p, &device);
+    }
+    ~PinnedHold() {
+        if (p) pinned_give(p, bytes, flags, device);
+    }
+};
+
+// yabt_hist's work on a caller's workspace of yabt_hist_workspace_bytes()
+// bytes (ops.hip); `who` names the entry point in error messages.
+int hist_enqueue(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm, const float* grad,
+                 const float* hess, int64_t n, int F, const uint32_t* rows, int64_t m, void* workspace, int64_t* out,
+                 int32_t* out_shifts, hipStream_t stream, const char* who);
+
 // Sequential carve of one workspace; with base == nullptr only sizes are summed.
 struct Carve {
     char* base;

@@ -11,11 +11,58 @@
 
 #include <string.h>
 
+#include <mutex>
+#include <vector>
+
 namespace yabt {
 
 char* error_buffer() {
     static thread_local char buf[ERROR_LEN] = "";
     return buf;
+}
+
+namespace {
+struct PinnedEntry {
+    void* p;
+    size_t bytes;
+    unsigned flags;
+    int device;
+};
+std::mutex g_pinned_mu;
+std::vector<PinnedEntry>& pinned_free() {
+    static std::vector<PinnedEntry>* v = new std::vector<PinnedEntry>();   // never destroyed: kept to exit
+    return *v;
+}
+}  // namespace
+
+int pinned_take(size_t bytes, unsigned flags, void** out, int* device) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return hip_fail(e, "pinned host buffer");
+    *device = dev;
+    {
+        std::lock_guard<std::mutex> lk(g_pinned_mu);
+        auto& v = pinned_free();
+        for (size_t i = 0; i < v.size(); ++i) {
+            if (v[i].bytes == bytes && v[i].flags == flags && v[i].device == dev) {
+                *out = v[i].p;
+                v[i] = v.back();
+                v.pop_back();
+                return 0;
+            }
+        }
+    }
+    e = hipHostMalloc(out, bytes, flags);
+    if (e != hipSuccess) {
+        *out = nullptr;
+        return hip_fail(e, "pinned host buffer");
+    }
+    return 0;
+}
+
+void pinned_give(void* p, size_t bytes, unsigned flags, int device) {
+    std::lock_guard<std::mutex> lk(g_pinned_mu);
+    pinned_free().push_back(PinnedEntry{p, bytes, flags, device});
 }
 
 constexpr int OB = 256;
@@ -194,6 +241,62 @@ __global__ void __launch_bounds__(OB) k_transpose(const uint8_t* __restrict__ sr
     }
 }
 
+static int check_hist_layout(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm,
+                             const float* grad, const float* hess, int64_t n, int F, const uint32_t* rows, int64_t m,
+                             const char* who) {
+    static thread_local char msg[160];
+    if (F < 1 || n < 0 || n > 0xFFFFFFFFll || !grad || !hess) {
+        snprintf(msg, sizeof msg, "%s: bad arguments", who);
+        return fail(-2, msg);
+    }
+    if (rows ? (!bins_rm || ld_rm < F || ld_rm % 16 || !aligned16(bins_rm) || m < 0)
+             : (!bins_fm || ld_fm < n || ld_fm % 16 || !aligned16(bins_fm))) {
+        snprintf(msg, sizeof msg, "%s: bins layout (pointer, alignment or leading dimension) invalid", who);
+        return fail(-2, msg);
+    }
+    if (!aligned16(grad) || !aligned16(hess)) {
+        snprintf(msg, sizeof msg, "%s: grad and hess must be 16-byte aligned", who);
+        return fail(-2, msg);
+    }
+    return 0;
+}
+
+// yabt_hist's work on a workspace of yabt_hist_workspace_bytes() (the
+// quantisation record, then the gather job).
+int hist_enqueue(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm, const float* grad,
+                 const float* hess, int64_t n, int F, const uint32_t* rows, int64_t m, void* workspace, int64_t* out,
+                 int32_t* out_shifts, hipStream_t stream, const char* who) {
+    static thread_local char msg[160];
+    if (!out || !workspace || !out_shifts) {
+        snprintf(msg, sizeof msg, "%s: bad arguments", who);
+        return fail(-2, msg);
+    }
+    const int rc0 = check_hist_layout(bins_fm, ld_fm, bins_rm, ld_rm, grad, hess, n, F, rows, m, who);
+    if (rc0) return rc0;
+    Carve c{(char*)workspace, 0};
+    Quant* q = c.take<Quant>(1);
+    HistJob* job = c.take<HistJob>(1);
+    k_quant_clear<<<1, 1, 0, stream>>>(q);
+    k_quant<<<launch_grid(n, OB * 16, 1024), OB, 0, stream>>>(grad, hess, n, q);
+    const int64_t ne = 3 * (int64_t)F * NB;
+    k_fill_i64<<<launch_grid(ne, OB, 1024), OB, 0, stream>>>(out, 0, ne);
+    const int tiles = (F + HFL - 1) / HFL;
+    if (!rows) {
+        if (n > 0) {
+            const int rc = root_chunks(n, tiles);
+            launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, q, 0.0, 0.0, nullptr, nullptr, out,
+                             0, nullptr);
+        }
+    } else if (m > 0) {
+        k_set_hist_job<<<1, 1, 0, stream>>>(job, rows, 0, m, out);
+        k_hist_gather<<<tiles * GATHER_MAX_CHUNKS, HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, q, 0.0, 0.0,
+                                                                        nullptr, job, 0, nullptr, pack_window_log2(n));
+    }
+    k_copy_shifts<<<1, 1, 0, stream>>>(q, out_shifts);
+    snprintf(msg, sizeof msg, "%s launch", who);
+    return launch_status(msg);
+}
+
 }  // namespace yabt
 
 using namespace yabt;
@@ -224,53 +327,12 @@ int yabt_apply(const float* X, int64_t ldx, int64_t n, int F, const int64_t* fea
 
 size_t yabt_hist_workspace_bytes(void) { return align_up(sizeof(Quant), 256) + align_up(sizeof(HistJob), 256); }
 
-static int check_hist_layout(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm,
-                             const float* grad, const float* hess, int64_t n, int F, const uint32_t* rows, int64_t m,
-                             const char* who) {
-    static thread_local char msg[160];
-    if (F < 1 || n < 0 || n > 0xFFFFFFFFll || !grad || !hess) {
-        snprintf(msg, sizeof msg, "%s: bad arguments", who);
-        return fail(-2, msg);
-    }
-    if (rows ? (!bins_rm || ld_rm < F || ld_rm % 16 || !aligned16(bins_rm) || m < 0)
-             : (!bins_fm || ld_fm < n || ld_fm % 16 || !aligned16(bins_fm))) {
-        snprintf(msg, sizeof msg, "%s: bins layout (pointer, alignment or leading dimension) invalid", who);
-        return fail(-2, msg);
-    }
-    if (!aligned16(grad) || !aligned16(hess)) {
-        snprintf(msg, sizeof msg, "%s: grad and hess must be 16-byte aligned", who);
-        return fail(-2, msg);
-    }
-    return 0;
-}
-
 int yabt_hist(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm, const float* grad,
               const float* hess, int64_t n, int F, const uint32_t* rows, int64_t m, void* workspace, int64_t* out,
               int32_t* out_shifts, hipStream_t stream) {
-    if (!out || !workspace || !out_shifts) return fail(-2, "yabt_hist: bad arguments");
-    const int rc0 = check_hist_layout(bins_fm, ld_fm, bins_rm, ld_rm, grad, hess, n, F, rows, m, "yabt_hist");
-    if (rc0) return rc0;
-    Carve c{(char*)workspace, 0};
-    Quant* q = c.take<Quant>(1);
-    HistJob* job = c.take<HistJob>(1);
-    k_quant_clear<<<1, 1, 0, stream>>>(q);
-    k_quant<<<launch_grid(n, OB * 16, 1024), OB, 0, stream>>>(grad, hess, n, q);
-    const int64_t ne = 3 * (int64_t)F * NB;
-    k_fill_i64<<<launch_grid(ne, OB, 1024), OB, 0, stream>>>(out, 0, ne);
-    const int tiles = (F + HFL - 1) / HFL;
-    if (!rows) {
-        if (n > 0) {
-            const int rc = root_chunks(n, tiles);
-            launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, q, 0.0, 0.0, nullptr, nullptr, out,
-                             0, nullptr);
-        }
-    } else if (m > 0) {
-        k_set_hist_job<<<1, 1, 0, stream>>>(job, rows, 0, m, out);
-        k_hist_gather<<<tiles * GATHER_MAX_CHUNKS, HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, q, 0.0, 0.0,
-                                                                        nullptr, job, 0, nullptr, pack_window_log2(n));
-    }
-    k_copy_shifts<<<1, 1, 0, stream>>>(q, out_shifts);
-    return launch_status("yabt_hist launch");
+    if (!workspace) return fail(-2, "yabt_hist: bad arguments");
+    return hist_enqueue(bins_fm, ld_fm, bins_rm, ld_rm, grad, hess, n, F, rows, m, workspace, out, out_shifts, stream,
+                        "yabt_hist");
 }
 
 int yabt_hist_accumulate(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm,

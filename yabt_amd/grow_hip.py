@@ -39,7 +39,6 @@ _CACHE_LOCK = threading.Lock()
 # id(binned) -> (state, layouts); an entry is dropped when its tensor dies (a
 # WeakKeyDictionary would compare tensor keys with ==, which is elementwise)
 _LAYOUTS: dict[int, tuple] = {}
-_WORKSPACES: dict = {}
 
 
 def _round16(x: int) -> int:
@@ -142,12 +141,11 @@ def layouts_for(binned: torch.Tensor, dev: torch.device,
 
 
 def _workspace(dev: torch.device, nbytes: int) -> torch.Tensor:
-    key = (dev, "grow")
-    ws = _WORKSPACES.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        _WORKSPACES[key] = ws
-    return ws
+    """Device workspace of one grow call, from torch's caching allocator on
+    the current stream (reused across calls without new allocations; each
+    call, and each host thread on its own stream, gets its own, as cgrow
+    takes its scratch per call, grow.c:271-287)."""
+    return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=dev)
 
 
 def nbins_of(binner, F: int) -> np.ndarray:
@@ -270,9 +268,14 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
         _ptr(out_i[0]), _ptr(out_i[1]), _ptr(out_i[2]), _ptr(out_i[3]), _ptr(value),
         _ptr(out_i[4]), _ptr(status), _stream(dev))
     _lib.check(rc, "yabt_grow")
-    # keep the argument tensors alive until the stream has consumed them
-    res = GrowResult(out_i[0], out_i[1], out_i[2], out_i[3], value, out_i[4], None, ws, status)
-    res._keep = (g, h, fm, im, nb, db)
+    # per-row leaf ids now, while the workspace still holds this tree's rows
+    leaf = torch.empty(max(n, 1), dtype=torch.int64, device=dev)
+    if n > 0:
+        _lib.check(lib.yabt_grow_leaf_ids(_ptr(ws), n, F, L, _ptr(out_i[0]), _ptr(out_i[4]), _ptr(status),
+                                          _ptr(leaf), _stream(dev)), "yabt_grow_leaf_ids")
+    res = GrowResult(out_i[0], out_i[1], out_i[2], out_i[3], value, out_i[4], None, None, status)
+    res.leaf_of_row = leaf[:n]
+    res._keep = (g, h, fm, im, nb, db, ws)   # alive until sync=False callers are done with the stream
     if sync:
         nn = int(status.item())
         if nn < 0:
@@ -342,11 +345,7 @@ def _grow_device_level(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, l
     nbytes = int(lib.yabt_grow_levelwise_workspace_bytes(n, F, L, int(max_depth)))
     if nbytes == 0:
         raise ValueError("yabt_grow_levelwise: invalid sizes")
-    key = (dev, "grow_level")
-    ws = _WORKSPACES.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        _WORKSPACES[key] = ws
+    ws = _workspace(dev, nbytes)
     out_i = torch.empty((5, N), dtype=torch.int64, device=dev)
     value = torch.empty(N, dtype=torch.float32, device=dev)
     leaf = torch.empty(max(n, 1), dtype=torch.int64, device=dev)
@@ -402,11 +401,7 @@ def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam
         raise ValueError("yabt_grow_ref: invalid sizes")
     if workspace_bytes is not None:
         nbytes = int(workspace_bytes)
-    key = (dev, "grow_ref")
-    ws = _WORKSPACES.get(key)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        _WORKSPACES[key] = ws
+    ws = _workspace(dev, nbytes)
     out_i = torch.empty((5, N), dtype=torch.int64, device=dev)
     value = torch.empty(N, dtype=torch.float32, device=dev)
     leaf = torch.empty(max(n, 1), dtype=torch.int64, device=dev)
@@ -428,15 +423,12 @@ def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam
 
 
 def leaf_ids(res: GrowResult, n: int, F: int, max_leaves: int) -> torch.Tensor:
-    """Per-row leaf node ids of a grown tree, from its final partition."""
-    if getattr(res, "leaf_of_row", None) is not None:
-        return res.leaf_of_row
-    lib = _lib.load()
-    dev = res.value.device
-    out = torch.empty(n, dtype=torch.int64, device=dev)
-    _lib.check(lib.yabt_grow_leaf_ids(_ptr(res._ws), n, F, int(max_leaves), _ptr(res.feature),
-                                      _ptr(res.depth), _ptr(res._status), _ptr(out), _stream(dev)),
-               "yabt_grow_leaf_ids")
+    """Per-row leaf node ids of a grown tree, from its final partition (every
+    grower fills them when it returns, so a later grow cannot change them)."""
+    del F, max_leaves
+    out = res.leaf_of_row
+    if out.shape[0] != n:
+        raise ValueError(f"leaf_ids: the tree was grown on {out.shape[0]} rows, not {n}")
     return out
 
 

@@ -14,8 +14,6 @@ import torch
 
 from . import _lib
 
-_WS: dict = {}
-
 
 def is_available() -> bool:
     """True if the HIP library loads and a device is present (cuda_hist.py:71-77)."""
@@ -40,10 +38,9 @@ def build_hist(binned: torch.Tensor, slot: torch.Tensor, g: torch.Tensor, h: tor
     nbytes = int(lib.yabt_hist_slots_workspace_bytes(n, F, K))
     if nbytes == 0:
         raise ValueError("build_hist: invalid sizes")
-    ws = _WS.get(dev)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        _WS[dev] = ws
+    # per call, from torch's caching allocator on the current stream: calls
+    # from several host threads on their own streams never share it
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     out = torch.empty((3, K, F, B), dtype=torch.float32, device=dev)
     status = torch.empty(4, dtype=torch.int32, device=dev)
     _lib.check(lib.yabt_hist_slots(b.data_ptr(), b.stride(0), s.data_ptr(), gg.data_ptr(), hh.data_ptr(),

@@ -22,8 +22,6 @@ import torch
 from . import _lib, boost_ops
 from .tree import LEAF, Tree
 
-_WS: dict = {}
-
 
 def _stream(dev: torch.device):
     return torch.cuda.current_stream(dev).cuda_stream
@@ -88,10 +86,9 @@ def leaf_fit(X: torch.Tensor, x_kind: int, feats: torch.Tensor, mu: torch.Tensor
     nbytes = int(lib.yabt_leaf_fit_workspace_bytes(n, N, K))
     if nbytes == 0:
         raise ValueError("yabt_leaf_fit: invalid sizes (1 <= K <= 8 inputs)")
-    ws = _WS.get(dev)
-    if ws is None or ws.numel() < nbytes:
-        ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-        _WS[dev] = ws
+    # per call, from torch's caching allocator on the current stream: calls
+    # from several host threads on their own streams never share it
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=dev)
     W = torch.empty((N, K), dtype=torch.float32, device=dev)
     b = torch.empty(N, dtype=torch.float32, device=dev)
     lo = torch.empty((N, K), dtype=torch.float32, device=dev)
@@ -193,5 +190,9 @@ def fit_leaf_networks_binned(tree: Tree, bins_fm: torch.Tensor, grad: torch.Tens
     W, db, lo, hi, cnt = leaf_fit(bins_fm, 1, feats, mu, sd, grad, hess, leaf_idx, feature,
                                   getattr(params, "leaf_net_min_samples", 50),
                                   getattr(params, "leaf_net_l2", 1.0))
+    # no eligible leaf: the tree is returned unchanged (neural_leaves.py:156-158)
+    eligible = (feature == LEAF) & (cnt >= getattr(params, "leaf_net_min_samples", 50))
+    if not bool(eligible.any()):
+        return tree
     tree_d = replace(tree, feature=feature, value=tree.value.to(dev))
     return fold(tree_d, W, db, mu, sd, params.learning_rate, feats, lo, hi)
