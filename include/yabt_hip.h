@@ -106,6 +106,23 @@ int yabt_hist_accumulate(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *b
                          const uint32_t *rows, int64_t m, int sg, int sh, void *workspace,
                          int64_t *out, yabt_stream_t stream);
 
+/* yabt_hist without a workspace argument, for callers that cannot allocate
+ * device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  No counterpart in the reference (whose
+ * grower mallocs its scratch per call, grow.c:271-287).  Same arguments,
+ * outputs and errors as yabt_hist minus `workspace`; the call allocates
+ * nothing (no hipMalloc, hipFree or allocating library routine).  Its
+ * scratch (the quantisation record and the gather job) is a static device
+ * array of 512 bytes per device, whatever n and F, held until the process
+ * ends; the device is the current one, and `stream` must belong to it.
+ * Every call on a device shares that device's array, and each call clears
+ * what must start at zero with kernels (no memset nodes under capture), so
+ * calls that overlap on one device -- on two streams or from two host
+ * threads -- race and must be serialised by the caller. */
+int yabt_hist_noalloc(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
+                      const float *grad, const float *hess, int64_t n, int F, const uint32_t *rows,
+                      int64_t m, int64_t *out, int32_t *out_shifts, yabt_stream_t stream);
+
 /* Workspace bytes of yabt_best_split for F features. */
 size_t yabt_best_split_workspace_bytes(int F);
 

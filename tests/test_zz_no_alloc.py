@@ -1,0 +1,53 @@
+"""yabt_hist_noalloc (no device allocation, scratch in a static device array)
+against yabt_hist through the C ABI: identical histograms and shifts on two
+calls in a row, the second on a smaller input, for the streaming root and for
+a gathered row list."""
+
+import numpy as np
+import pytest
+import torch
+
+from yabt_amd import _lib
+from yabt_amd import grow_hip as G
+
+pytestmark = pytest.mark.gpu
+
+DEV = torch.device("cuda", 0) if torch.cuda.is_available() else None
+
+
+def _noalloc():
+    return _lib.load().yabt_hist_noalloc
+
+
+def _case(n, F, seed, m):
+    rng = np.random.default_rng(seed)
+    bins = rng.integers(0, 256, size=(n, F)).astype(np.uint8)
+    g = rng.normal(size=n).astype(np.float32)
+    h = rng.uniform(0.1, 1.0, size=n).astype(np.float32)
+    lay = G.make_layouts(torch.from_numpy(bins), DEV)
+    rows = torch.from_numpy(np.sort(rng.choice(n, size=m, replace=False)).astype(np.int32)).to(DEV)
+    return lay, torch.from_numpy(g).to(DEV), torch.from_numpy(h).to(DEV), rows
+
+
+def _run_noalloc(fn, lay, g, h, rows):
+    out = torch.full((3, lay.F, 256), -7, dtype=torch.int64, device=DEV)
+    shifts = torch.full((2,), -99, dtype=torch.int32, device=DEV)
+    m = 0 if rows is None else rows.shape[0]
+    rc = fn(G._ptr(lay.fm), lay.ld_fm, G._ptr(lay.rm), lay.ld_rm, G._ptr(g), G._ptr(h), lay.n, lay.F,
+            G._ptr(rows), m, G._ptr(out), G._ptr(shifts), G._stream(DEV))
+    assert rc == 0, _lib.last_error()
+    torch.cuda.synchronize()
+    return out.cpu().numpy(), shifts.cpu().tolist()
+
+
+def test_noalloc_matches_yabt_hist_twice():
+    fn = _noalloc()
+    for n, F, seed, m in [(300_001, 37, 1, 120_000), (40_000, 20, 2, 9_000)]:
+        print(f"yabt_hist_noalloc n={n} F={F} rows={m}", flush=True)
+        lay, g, h, rows = _case(n, F, seed, m)
+        for r in (None, rows):
+            got, got_s = _run_noalloc(fn, lay, g, h, r)
+            want, want_s = G.hist(lay, g, h, r)
+            assert got_s == list(want_s)
+            assert np.array_equal(got, want.cpu().numpy())
+            assert int(got[2].sum()) == (n if r is None else m) * F

@@ -17,7 +17,7 @@ OUT_DIR = os.path.join(HERE, "_lib")
 OBJ_DIR = os.path.join(OUT_DIR, "obj")
 LIB = os.path.join(OUT_DIR, "libyabt_hip.so")
 SOURCES = ["grow.hip", "grow_batch.hip", "grow_level.hip", "grow_ref.hip", "ops.hip", "leaf.hip", "slots.hip",
-           "boost.hip", "binner.hip"]
+           "boost.hip", "binner.hip", "noalloc.hip"]
 ARCH = "gfx950"
 
 # -ffp-contract=off: no fused multiply-add may change a rounding that the

@@ -262,7 +262,7 @@ static int check_hist_layout(const uint8_t* bins_fm, int64_t ld_fm, const uint8_
 }
 
 // yabt_hist's work on a workspace of yabt_hist_workspace_bytes() (the
-// quantisation record, then the gather job).
+// quantisation record, then the gather job); shared with yabt_hist_noalloc.
 int hist_enqueue(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm, const float* grad,
                  const float* hess, int64_t n, int F, const uint32_t* rows, int64_t m, void* workspace, int64_t* out,
                  int32_t* out_shifts, hipStream_t stream, const char* who) {
