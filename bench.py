@@ -118,24 +118,26 @@ def gpu_inputs(torch, n, F, seed=0):
     return G.BinLayouts(fm, rm, n, F), g, h
 
 
-def time_root_hist(torch, lay, g, h, reps=20):
+def time_root_hist(torch, lay, g, h, reps=50, warm=50):
     """Average duration of the streaming root-histogram kernel (one launch per
-    call of yabt_hist_accumulate), HIP events on the launch stream."""
+    call of yabt_hist_root, the per-fit bin counts given), HIP events on the
+    launch stream, after ``warm`` untimed launches (the first few dozen run
+    slower while the device clocks up)."""
     from yabt_amd import grow_hip as G
     from yabt_amd import _lib
     dev = lay.fm.device
     lib = _lib.load()
     out = torch.zeros((3, lay.F, 256), dtype=torch.int64, device=dev)
     _, (sg, sh) = G.hist(lay, g, h)
+    counts = lay.counts()
     stream = torch.cuda.current_stream(dev)
 
     def launch():
-        _lib.check(lib.yabt_hist_accumulate(G._ptr(lay.fm), lay.ld_fm, G._ptr(lay.rm), lay.ld_rm,
-                                            G._ptr(g), G._ptr(h), lay.n, lay.F, None, 0, sg, sh,
-                                            None, G._ptr(out), G._stream(dev)),
-                   "yabt_hist_accumulate")
+        _lib.check(lib.yabt_hist_root(G._ptr(lay.fm), lay.ld_fm, G._ptr(g), G._ptr(h), lay.n, lay.F,
+                                      G._ptr(counts), sg, sh, G._ptr(out), G._stream(dev)),
+                   "yabt_hist_root")
 
-    for _ in range(3):
+    for _ in range(warm):
         launch()
     torch.cuda.synchronize()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(reps)]
@@ -147,6 +149,27 @@ def time_root_hist(torch, lay, g, h, reps=20):
     torch.cuda.synchronize()
     ms = [s.elapsed_time(e) for s, e in zip(starts, ends)]
     return float(np.mean(ms)), float(np.median(ms))
+
+
+def time_bin_counts(torch, lay, reps=5):
+    """Per-fit setup of the root histogram: yabt_bin_counts over the bins
+    (mean of ``reps`` calls, HIP events)."""
+    from yabt_amd import grow_hip as G
+    from yabt_amd import _lib
+    dev = lay.fm.device
+    lib = _lib.load()
+    c = torch.empty((lay.F, 256), dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    _lib.check(lib.yabt_bin_counts(G._ptr(lay.fm), lay.ld_fm, lay.n, lay.F, G._ptr(c), G._stream(dev)),
+               "yabt_bin_counts")
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(reps):
+        lib.yabt_bin_counts(G._ptr(lay.fm), lay.ld_fm, lay.n, lay.F, G._ptr(c), G._stream(dev))
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "k_hist_root_10Mx100_traffic.md")
@@ -169,11 +192,11 @@ def counter_launches(torch, lay, g, h) -> None:
     lib = _lib.load()
     out = torch.zeros((3, lay.F, 256), dtype=torch.int64, device=dev)
     _, (sg, sh) = G.hist(lay, g, h)
+    counts = lay.counts()
     for _ in range(3):
-        _lib.check(lib.yabt_hist_accumulate(G._ptr(lay.fm), lay.ld_fm, G._ptr(lay.rm), lay.ld_rm,
-                                            G._ptr(g), G._ptr(h), lay.n, lay.F, None, 0, sg, sh,
-                                            None, G._ptr(out), G._stream(dev)),
-                   "yabt_hist_accumulate")
+        _lib.check(lib.yabt_hist_root(G._ptr(lay.fm), lay.ld_fm, G._ptr(g), G._ptr(h), lay.n, lay.F,
+                                      G._ptr(counts), sg, sh, G._ptr(out), G._stream(dev)),
+                   "yabt_hist_root")
     torch.cuda.synchronize()
 
 
@@ -423,6 +446,7 @@ def main() -> None:
         return
 
     log("[bench] root histogram kernel")
+    ms_counts = time_bin_counts(torch, lay)
     root_mean_ms, root_med_ms = time_root_hist(torch, lay, g, h)
 
     from yabt_amd.neural_leaves import fit_leaf_networks_binned
@@ -493,6 +517,8 @@ def main() -> None:
                       "updates_per_s": round(n * F / (root_mean_ms * 1e-3) / 1e9, 3),
                       "unit": "G updates/s", "GBps": round(achieved, 1),
                       "frac_hbm": round(achieved / HBM_PEAK_GBS, 4)},
+        "fit_setup": {"bin_counts_ms": round(ms_counts, 4),
+                      "note": "per-fit count plane of the root histogram (yabt_bin_counts), outside the step"},
         "roofline": {"kernel": "k_hist_root<false> (streaming root histogram)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic()},

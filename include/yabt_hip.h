@@ -13,8 +13,15 @@
  *     message is available from yabt_last_error() (per calling thread);
  *   - histograms are exact int64 fixed point: the caller's grad/hess are
  *     quantised as q = rint(x * 2^s) with one shift per call,
- *     s = 61 - ceil(log2(n)) - e where max|x| < 2^e (s = 0 if max|x| = 0), so
- *     every sum over <= n rows is exact and below 2^62 in magnitude;
+ *     s = 30 - min(ceil(log2(n)), 11) - e where max|x| < 2^e (s = 0 if
+ *     max|x| = 0): q keeps 19 bits of the largest |x| (more for n <= 2048),
+ *     every sum over <= n rows is exact, and any 2048 of them sum below
+ *     2^31 in magnitude (the streaming root histogram packs q(g) and q(h)
+ *     into one 64-bit word per update);
+ *   - bin counts: the count plane of a root histogram depends only on the
+ *     bins, so callers that keep them for a whole fit (yabt_bin_counts) pass
+ *     them as `bin_counts` (F, 256) uint32; NULL makes the call count them
+ *     itself (one more pass over the feature-major bins);
  *   - bins: feature-major (F, ld_fm) uint8 with ld_fm >= n, ld_fm % 16 == 0,
  *     and a row-major copy (n, ld_rm) uint8 with ld_rm >= F, ld_rm % 16 == 0
  *     (yabt_transpose_bins builds it); bins, grad, hess 16-byte aligned.
@@ -50,14 +57,16 @@ size_t yabt_grow_workspace_bytes(int64_t n, int F, int max_leaves);
  *     builder's default-bin fill, grow.c:68-107, made exact).  Any bin is a
  *     correct choice; the most frequent one saves the most work;
  *   - B (always 256) and n_threads are dropped;
+ *   - `bin_counts` (may be NULL): the per-fit counts of the bins (above);
  *   - `workspace` (>= yabt_grow_workspace_bytes) replaces cgrow's mallocs;
  *   - the node count is written to out_status[0] on the device (cgrow's return
  *     value); out_status[0] = -1 if grad or hess holds a non-finite value.
  * Requires 0 <= n < 2^32, F >= 1, 1 <= max_leaves <= 32767. */
 int yabt_grow(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
               const float *grad, const float *hess, const uint8_t *fmask, const float *imat,
-              float ib, int use_imat, const int32_t *nbins, const int32_t *default_bin, int64_t n,
-              int F, float lam, float gamma, float mcw, int msl, float lr, int max_leaves,
+              float ib, int use_imat, const int32_t *nbins, const int32_t *default_bin,
+              const uint32_t *bin_counts, int64_t n, int F, float lam, float gamma, float mcw, int msl,
+              float lr, int max_leaves,
               int max_depth, void *workspace, size_t workspace_bytes, int64_t *out_feature,
               int64_t *out_thr_bin, int64_t *out_left, int64_t *out_right, float *out_value,
               int64_t *out_depth, int32_t *out_status, yabt_stream_t stream);
@@ -96,15 +105,32 @@ int yabt_hist(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int
               yabt_stream_t stream);
 
 /* yabt_hist with caller-given shifts (sg, sh), adding into `out` without
- * clearing it; with rows == NULL it is exactly one kernel launch (the
- * streaming root histogram), which is what a timing harness brackets.
- * workspace: >= yabt_hist_workspace_bytes() when rows != NULL, else unused.
+ * clearing it (rows == NULL: two launches, the bin counts and the streaming
+ * root histogram).  workspace: >= yabt_hist_workspace_bytes() when
+ * rows != NULL, else unused.
  * Replaces `build_hist` (yabt/_cgrow/grow.c:37-62) for callers that manage
  * the quantisation themselves. */
 int yabt_hist_accumulate(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm,
                          int64_t ld_rm, const float *grad, const float *hess, int64_t n, int F,
                          const uint32_t *rows, int64_t m, int sg, int sh, void *workspace,
                          int64_t *out, yabt_stream_t stream);
+
+/* Per-fit bin counts: out_counts[f * 256 + b] (uint32, F * 256) = number of
+ * rows r < n with bins_fm[f * ld_fm + r] == b.  The count plane of every root
+ * histogram over these bins; yabt_grow* take it as `bin_counts`.  Replaces
+ * nothing in the reference (cgrow counts every node's rows itself,
+ * grow.c:55-60); it is the setup of the packed root histogram. */
+int yabt_bin_counts(const uint8_t *bins_fm, int64_t ld_fm, int64_t n, int F, uint32_t *out_counts,
+                    yabt_stream_t stream);
+
+/* The streaming root histogram alone: adds sum q(g) and sum q(h) over all n
+ * rows (shifts sg, sh given) into planes 0 and 1 of out (3, F, 256) int64,
+ * and bin_counts (may be NULL: plane 2 untouched) into plane 2 -- exactly
+ * one kernel launch, which is what a timing harness brackets.  Replaces the
+ * root call of `build_hist` (yabt/_cgrow/grow.c:37-62, grow.c:296-300). */
+int yabt_hist_root(const uint8_t *bins_fm, int64_t ld_fm, const float *grad, const float *hess,
+                   int64_t n, int F, const uint32_t *bin_counts, int sg, int sh, int64_t *out,
+                   yabt_stream_t stream);
 
 /* yabt_hist without a workspace argument, for callers that cannot allocate
  * device memory: code under HIP graph capture, tight serving loops,
@@ -219,7 +245,8 @@ size_t yabt_grow_batched_workspace_bytes(int64_t n, int F, int max_leaves);
 int yabt_grow_batched(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
                       const float *grad, const float *hess, const uint8_t *fmask, const float *imat,
                       float ib, int use_imat, const int32_t *nbins, const int32_t *default_bin,
-                      int64_t n, int F, float lam, float gamma, float mcw, int msl, float lr,
+                      const uint32_t *bin_counts, int64_t n, int F, float lam, float gamma, float mcw,
+                      int msl, float lr,
                       int max_leaves, int max_depth, void *workspace, size_t workspace_bytes,
                       int64_t *out_feature, int64_t *out_thr_bin, int64_t *out_left,
                       int64_t *out_right, float *out_value, int64_t *out_depth,
@@ -240,8 +267,9 @@ size_t yabt_grow_levelwise_workspace_bytes(int64_t n, int F, int max_leaves, int
  * the call synchronises `stream`. */
 int yabt_grow_levelwise(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
                         const float *grad, const float *hess, const uint8_t *fmask, const float *imat,
-                        float ib, int use_imat, const int32_t *nbins, int64_t n, int F, float lam,
-                        float gamma, float mcw, int msl, float lr, int max_leaves, int max_depth,
+                        float ib, int use_imat, const int32_t *nbins, const uint32_t *bin_counts,
+                        int64_t n, int F, float lam, float gamma, float mcw, int msl, float lr,
+                        int max_leaves, int max_depth,
                         void *workspace, size_t workspace_bytes, int64_t *out_feature,
                         int64_t *out_thr_bin, int64_t *out_left, int64_t *out_right, float *out_value,
                         int64_t *out_depth, int64_t *out_leaf_of_row, int32_t *out_status,

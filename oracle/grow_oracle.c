@@ -18,7 +18,7 @@
  *
  *   OR_MODE_FIXED  the arithmetic contract of the HIP path: gradients and
  *                  hessians are quantised to int64 fixed point with one
- *                  power-of-two scale per call (or_quant_shift), histograms are
+ *                  power-of-two scale per call (or_hist_shift), histograms are
  *                  exact integer sums (order-free, so sibling subtraction and
  *                  the default-bin fill are exact), the partition is stable, and
  *                  the split scan evaluates the reference's double-precision
@@ -58,6 +58,21 @@ int or_quant_shift(float maxabs, int64_t n)
     return 61 - k - e;
 }
 
+/* The node histograms' shift (the contract of the exact grower): with
+ * max|x| < 2^e and n <= 2^k, s = 30 - min(k, 11) - e, so |q| <= 2^19 for
+ * n > 2048 (2^(30-k) below) and any 2^min(k,11) of them sum below 2^31 in
+ * magnitude -- the most the device's packed root histogram adds into one
+ * 32-bit half between two unpacks.  Zero input gets shift 0. */
+int or_hist_shift(float maxabs, int64_t n)
+{
+    if (!(maxabs > 0.0f)) return 0;
+    int e = 0;
+    (void)frexpf(maxabs, &e);
+    int k = 0;
+    while (k < 11 && ((int64_t)1 << k) < n) ++k;
+    return 30 - k - e;
+}
+
 static inline int64_t quantise(float x, double scale)
 {
     return (int64_t)rint((double)x * scale);
@@ -80,8 +95,8 @@ int or_quant_shifts(const float *grad, const float *hess, int64_t n, int *sg, in
 {
     float mg = 0.0f, mh = 0.0f;
     if (max_abs(grad, n, &mg) || max_abs(hess, n, &mh)) return -1;
-    *sg = or_quant_shift(mg, n);
-    *sh = or_quant_shift(mh, n);
+    *sg = or_hist_shift(mg, n);
+    *sh = or_hist_shift(mh, n);
     return 0;
 }
 

@@ -55,6 +55,8 @@ def lib():
         L = ctypes.CDLL(ORACLE_SO)
         L.or_quant_shift.restype = _int
         L.or_quant_shift.argtypes = [_flt, _i64]
+        L.or_hist_shift.restype = _int
+        L.or_hist_shift.argtypes = [_flt, _i64]
         L.or_quant_shifts.restype = _int
         L.or_quant_shifts.argtypes = [_vp, _vp, _i64, _vp, _vp]
         L.or_hist_f32.restype = None
@@ -187,6 +189,11 @@ def leaf_of_rows(res: dict, n: int) -> np.ndarray:
 
 def quant_shift(maxabs: float, n: int) -> int:
     return int(lib().or_quant_shift(_flt(float(maxabs)), _i64(int(n))))
+
+
+def hist_shift(maxabs: float, n: int) -> int:
+    """The node histograms' shift (30 - min(k, 11) - e), or_hist_shift."""
+    return int(lib().or_hist_shift(_flt(float(maxabs)), _i64(int(n))))
 
 
 def quant_shifts(grad, hess) -> tuple[int, int]:

@@ -77,7 +77,7 @@ def test_reference_grower_workspace_sizes():
 
 def test_argument_errors_are_reported_without_a_device():
     lib = _lib.load()
-    rc = lib.yabt_grow(None, 0, None, 0, None, None, None, None, ctypes.c_float(0.5), 0, None, None, 10, 0,
+    rc = lib.yabt_grow(None, 0, None, 0, None, None, None, None, ctypes.c_float(0.5), 0, None, None, None, 10, 0,
                        ctypes.c_float(1), ctypes.c_float(0), ctypes.c_float(1e-3), 20,
                        ctypes.c_float(0.1), 31, 64, None, 0, None, None, None, None, None, None,
                        None, None)

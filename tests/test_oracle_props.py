@@ -79,6 +79,37 @@ def test_quant_shift_closed_form():
         O.quant_shifts(np.array([1.0, np.inf], np.float32), np.ones(2, np.float32))
 
 
+@pytest.mark.parametrize("maxabs,n", [(1.0, 1), (0.75, 1000), (1.9999999, 2048), (1.9999999, 2049),
+                                      (5.5, 10_000_000), (1e-30, 3), (3e38, 2), (0.0, 10), (0.25, 4_000_000)])
+def test_hist_shift_bounds(maxabs, n):
+    """The node histograms' shift: any min(n, 2048) quantised values sum
+    below 2^31 in magnitude (one 32-bit half of the packed root word between
+    two unpacks), all n below 2^62, and the scale is the largest power of two
+    that does so (one more bit would break the 2048-row bound)."""
+    s = O.hist_shift(maxabs, n)
+    if maxabs == 0.0:
+        assert s == 0
+        return
+    w = min(int(np.ceil(np.log2(n))) if n > 1 else 0, 11)
+    q = np.rint(np.float64(np.float32(maxabs)) * 2.0 ** s)
+    assert q <= 2.0 ** (30 - w)
+    assert min(n, 2048) * q < 2.0 ** 31
+    assert n * q < 2.0 ** 62
+    # maximal: with s + 1, values just below 2^e (e: maxabs = m 2^e, m in [0.5, 1))
+    # would round to 2^(31 - w), and 2^w of them would reach 2^31
+    e = int(np.frexp(np.float32(maxabs))[1])
+    assert 2.0 ** (s + 1 + e) * 2 ** w >= 2.0 ** 31
+
+
+def test_hist_shift_closed_form():
+    assert O.hist_shift(1.0, 1) == 29          # 1.0 = 0.5 * 2^1, n <= 2^0: 30 - 0 - 1
+    assert O.hist_shift(1.0, 2048) == 18       # 30 - 11 - 1
+    assert O.hist_shift(1.0, 10_000_000) == 18  # the window caps k at 11
+    assert O.hist_shift(0.5, 1024) == 20       # 0.5 = 0.5 * 2^0: 30 - 10 - 0
+    # n = 2 (k = 1): max|g| = 1.5 = 0.75 * 2^1, max|h| = 0.5 = 0.5 * 2^0
+    assert O.quant_shifts(np.array([1.0, -1.5], np.float32), np.array([0.25, 0.5], np.float32)) == (28, 29)
+
+
 def _brute_split(bins_nf, g, h, lam, gamma, mcw, msl, nbins, fmask, boost):
     """Enumerate every (f, b), summing the rows on each side directly."""
     n, F = bins_nf.shape
@@ -123,7 +154,14 @@ def test_best_split_against_brute_force(seed):
     gfx, ffx, bfx = O.best_split_fixed(O.hist_fixed(bins.T, g, h, sg, sh), sg, sh, nbins, lam,
                                        gamma, mcw, msl, fmask, boost)
     assert (f32, b32) == (ref[2], ref[3]) == (ffx, bfx)
-    assert g32 == pytest.approx(ref[1], rel=1e-6) and gfx == pytest.approx(ref[1], rel=1e-9)
+    # q keeps 20 bits of max|g| here (n = 600): node sums carry ~1e-6 relative error
+    assert g32 == pytest.approx(ref[1], rel=1e-6) and gfx == pytest.approx(ref[1], rel=1e-5)
+    # on the quantised values themselves (q 2^-s, exact in fp64) the fixed-point
+    # scan is the brute force up to the fp64 rounding of the gain expression
+    gq = np.rint(g.astype(np.float64) * 2.0 ** sg) * 2.0 ** -sg
+    hq = np.rint(h.astype(np.float64) * 2.0 ** sh) * 2.0 ** -sh
+    refq = _brute_split(bins, gq, hq, lam, gamma, mcw, msl, nbins, fmask, boost)
+    assert (refq[2], refq[3]) == (ffx, bfx) and gfx == pytest.approx(refq[1], rel=1e-12)
 
 
 def test_best_split_tie_breaks():

@@ -40,7 +40,7 @@ _sz = ctypes.c_size_t
 SIGNATURES = {
     "yabt_last_error": (ctypes.c_char_p, []),
     "yabt_grow_workspace_bytes": (_sz, [_i64, _int, _int]),
-    "yabt_grow": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _vp, _i64, _int,
+    "yabt_grow": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _vp, _vp, _i64, _int,
                          _flt, _flt, _flt, _int, _flt, _int, _int, _vp, _sz,
                          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "yabt_grow_leaf_ids": (_int, [_vp, _i64, _int, _int, _vp, _vp, _vp, _vp, _vp]),
@@ -50,6 +50,8 @@ SIGNATURES = {
     "yabt_hist": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _int, _vp, _i64, _vp, _vp, _vp, _vp]),
     "yabt_hist_accumulate": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _int, _vp, _i64, _int, _int,
                                     _vp, _vp, _vp]),
+    "yabt_bin_counts": (_int, [_vp, _i64, _i64, _int, _vp, _vp]),
+    "yabt_hist_root": (_int, [_vp, _i64, _vp, _vp, _i64, _int, _vp, _int, _int, _vp, _vp]),
     "yabt_hist_noalloc": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _int, _vp, _i64, _vp, _vp, _vp]),
     "yabt_best_split_workspace_bytes": (_sz, [_int]),
     "yabt_best_split": (_int, [_vp, _int, _vp, _vp, _vp, _int, _int, _dbl, _dbl, _dbl, _int, _vp,
@@ -64,11 +66,12 @@ SIGNATURES = {
     "yabt_leaf_fit": (_int, [_int, _vp, _i64, _i64, _vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _int, _int,
                              _dbl, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "yabt_grow_batched_workspace_bytes": (_sz, [_i64, _int, _int]),
-    "yabt_grow_batched": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _vp, _i64, _int,
+    "yabt_grow_batched": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _vp, _vp, _i64,
+                                 _int,
                                  _flt, _flt, _flt, _int, _flt, _int, _int, _vp, _sz,
                                  _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "yabt_grow_levelwise_workspace_bytes": (_sz, [_i64, _int, _int, _int]),
-    "yabt_grow_levelwise": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _i64, _int,
+    "yabt_grow_levelwise": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _vp, _i64, _int,
                                    _flt, _flt, _flt, _int, _flt, _int, _int, _vp, _sz,
                                    _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "yabt_grow_ref_workspace_bytes": (_sz, [_i64, _int, _int, _int]),

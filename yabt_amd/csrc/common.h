@@ -15,7 +15,8 @@ constexpr int LEAF = -1;  // grow.c:28
 // ---------------------------------------------------------------------------
 // fixed-point quantisation, shared with oracle/grow_oracle.c (or_quant_shift):
 // q = rint(x * 2^s), s = 61 - k - e with max|x| < 2^e and n <= 2^k, so every
-// partial sum of <= n quantised values stays below 2^62 in magnitude.
+// partial sum of <= n quantised values stays below 2^62 in magnitude (the
+// K-slot histogram and the leaf-model sums).
 // ---------------------------------------------------------------------------
 
 __host__ __device__ inline int quant_shift(float maxabs, int64_t n) {
@@ -27,8 +28,34 @@ __host__ __device__ inline int quant_shift(float maxabs, int64_t n) {
     return 61 - k - e;
 }
 
+// Node histograms use a narrower shift: the streaming root kernel adds the
+// word (q(g) << 32) + q(h) into one 64-bit LDS cell per update and unpacks
+// the two 32-bit halves after every block step of 1024 rows.  With
+// s = 30 - min(k, 11) - e, |q| <= 2^(30 - min(k, 11)), so any min(n, 2048)
+// values -- two steps' worth -- sum within 2^30 < 2^31 in each half; q keeps
+// 19 bits of the largest |x| for n > 2048 (more below), and every partial sum
+// of <= n values stays below 2^51.  Shared with oracle/grow_oracle.c
+// (or_hist_shift).
+__host__ __device__ inline int hist_shift(float maxabs, int64_t n) {
+    if (!(maxabs > 0.0f)) return 0;
+    int e = 0;
+    (void)frexpf(maxabs, &e);
+    int k = 0;
+    while (k < 11 && ((int64_t)1 << k) < n) ++k;
+    return 30 - k - e;
+}
+
 __device__ __forceinline__ int64_t quantise(float x, double scale) {
     return (int64_t)rint((double)x * scale);
+}
+
+// quantise for the node histograms, whose shift keeps |x * 2^s| <= 2^30
+// (hist_shift): evaluated in fp32 -- the scaling by a power of two is exact
+// while the result is a normal float, anything smaller rounds to 0 either
+// way, and rounding to an integer is exact -- so it equals quantise, in
+// three VALU operations instead of eight.  `scale` is 2^s.
+__device__ __forceinline__ int64_t quantise_node(float x, double scale) {
+    return (int64_t)(int32_t)rintf(ldexpf(x, ilogb(scale)));
 }
 
 // Per-call quantisation record, filled on the device.
@@ -349,8 +376,8 @@ __device__ void quant_reduce(const float* grad, const float* hess, int64_t n, Qu
 
 __device__ inline void quant_finish(Quant* q, int64_t n) {
     const float mg = __uint_as_float(q->maxg_bits), mh = __uint_as_float(q->maxh_bits);
-    q->sg = quant_shift(mg, n);
-    q->sh = quant_shift(mh, n);
+    q->sg = hist_shift(mg, n);
+    q->sh = hist_shift(mh, n);
     q->scg = ldexp(1.0, q->sg);
     q->sch = ldexp(1.0, q->sh);
     q->ig = ldexp(1.0, -q->sg);
@@ -360,7 +387,7 @@ __device__ inline void quant_finish(Quant* q, int64_t n) {
     if (n > 0 && q->hmin_key == q->hmax_key) {
         const uint32_t k = q->hmin_key;
         const float h = __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-        const int64_t hq = quantise(h, q->sch);
+        const int64_t hq = quantise_node(h, q->sch);
         if (hq != 0) {
             q->const_h = 1;
             q->hq_const = hq;

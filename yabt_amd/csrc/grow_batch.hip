@@ -133,6 +133,7 @@ struct Args {
     int use_imat;
     const int32_t* nbins;
     const int32_t* dflt;
+    const uint32_t* counts;              // per-fit bin counts (F, 256), or NULL
     int64_t n;
     int F;
     float lam, gamma, mcw, lr;
@@ -1005,8 +1006,9 @@ size_t yabt_grow_batched_workspace_bytes(int64_t n, int F, int max_leaves) {
 
 int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm,
                       const float* grad, const float* hess, const uint8_t* fmask, const float* imat, float ib,
-                      int use_imat, const int32_t* nbins, const int32_t* default_bin, int64_t n, int F, float lam,
-                      float gamma, float mcw, int msl, float lr, int max_leaves, int max_depth, void* workspace,
+                      int use_imat, const int32_t* nbins, const int32_t* default_bin, const uint32_t* bin_counts,
+                      int64_t n, int F, float lam, float gamma, float mcw, int msl, float lr, int max_leaves,
+                      int max_depth, void* workspace,
                       size_t workspace_bytes, int64_t* out_feature, int64_t* out_thr_bin, int64_t* out_left,
                       int64_t* out_right, float* out_value, int64_t* out_depth, int64_t* out_leaf_of_row,
                       int32_t* out_status, hipStream_t stream) {
@@ -1036,6 +1038,7 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
     A.use_imat = use_imat ? 1 : 0;
     A.nbins = nbins;
     A.dflt = default_bin;
+    A.counts = bin_counts;
     A.n = n;
     A.F = F;
     A.lam = lam;
@@ -1078,7 +1081,8 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
     k_setup<<<launch_grid(n, SB * 16, 1024), SB, 0, stream>>>(A);
     k_setup_finish<<<1, 1, 0, stream>>>(A);
     const int rc = root_chunks(n, tiles);
-    launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, A.dflt, A.q, A.hist, 1,
+    launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, A.dflt, A.counts, A.q,
+                     A.hist, 1,
                      &A.st->done);
     const int scan_grid = (F + SCAN_FEATS - 1) / SCAN_FEATS;
     k_scan<true><<<scan_grid, SCAN_FEATS * WAVE, 0, stream>>>(A);

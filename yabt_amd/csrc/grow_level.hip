@@ -317,8 +317,8 @@ __global__ void __launch_bounds__(HBLOCK) k_hist(const uint8_t* __restrict__ bin
             uint64_t qg = 0, qh = 0;
             if (i0 + lane < b) {
                 r = sorted[i0 + lane];
-                qg = (uint64_t)quantise(grad[r], scg);
-                if (HCH) qh = (uint64_t)quantise(hess[r], sch);
+                qg = (uint64_t)quantise_node(grad[r], scg);
+                if (HCH) qh = (uint64_t)quantise_node(hess[r], sch);
             }
             const int nv = (int)min((int64_t)HFL, max((int64_t)0, b - (i0 + HFL * rg)));
             uint32_t bj[HFL];
@@ -473,7 +473,8 @@ size_t yabt_grow_levelwise_workspace_bytes(int64_t n, int F, int max_leaves, int
 
 int yabt_grow_levelwise(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm,
                         const float* grad, const float* hess, const uint8_t* fmask, const float* imat, float ib,
-                        int use_imat, const int32_t* nbins, int64_t n, int F, float lam, float gamma, float mcw,
+                        int use_imat, const int32_t* nbins, const uint32_t* bin_counts, int64_t n, int F,
+                        float lam, float gamma, float mcw,
                         int msl, float lr, int max_leaves, int max_depth, void* workspace, size_t workspace_bytes,
                         int64_t* out_feature, int64_t* out_thr_bin, int64_t* out_left, int64_t* out_right,
                         float* out_value, int64_t* out_depth, int64_t* out_leaf_of_row, int32_t* out_status,
@@ -548,8 +549,8 @@ int yabt_grow_levelwise(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bi
     k_setup_finish<<<1, 1, 0, stream>>>(w.q, n, w.nodes, w.scan_list, out_status);
     if (n > 0) {
         const int rc = root_chunks(n, tiles);
-        launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, w.q, 0.0, 0.0, nullptr, w.q, w.hist, 1,
-                         nullptr);
+        launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, w.q, 0.0, 0.0, nullptr, bin_counts, w.q,
+                         w.hist, 1, nullptr);
     }
     k_root_tot<<<1, 1, 0, stream>>>(w.q, n, w.nodes);
     if (max_depth > 0) {

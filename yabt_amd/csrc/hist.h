@@ -81,70 +81,6 @@ inline int root_chunks(int64_t n, int tiles) {
     return want < 8 ? 8 : want;
 }
 
-// Streaming histogram of rows [0, n) from the feature-major bins.
-// Grid: tiles * chunks blocks, block -> (tile = bid / chunks, chunk = bid % chunks).
-// q_tot (may be NULL): the tile-0 blocks add sum q(g), sum q(h) of all rows
-// (sum q(h) only with the h channel; without it the caller uses n * q(h)).
-template <bool HCH>
-__device__ __forceinline__ void hist_root_body(HistLds& L, const uint8_t* __restrict__ bins_fm, int64_t ld,
-                                               const float* __restrict__ grad, const float* __restrict__ hess,
-                                               int64_t n, int F, double scg, double sch,
-                                               const int32_t* __restrict__ dflt, Quant* q_tot, int64_t* out,
-                                               int chunks) {
-    const int tile = blockIdx.x / chunks, chunk = blockIdx.x % chunks;
-    const int f0 = tile * HFL;
-    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
-    const int fl = lane & (HFL - 1), rg = lane / HFL;
-    const int f = f0 + fl;
-    const bool fok = f < F;
-    const int64_t per = ((n + chunks - 1) / chunks + HSTEP - 1) / HSTEP * HSTEP;
-    const int64_t lo = (int64_t)chunk * per, hi = min(n, lo + per);
-    if (f0 >= F || lo >= hi) return;
-    const int d = (fok && dflt) ? dflt[f] : -1;
-    const bool totals = q_tot != nullptr && tile == 0;
-    hist_clear<HCH>(L);
-    __syncthreads();
-    const uint8_t* col = bins_fm + (size_t)(fok ? f : f0) * ld;
-    int64_t sum_g = 0, sum_h = 0;
-    for (int64_t r0 = lo + (int64_t)wave * WAVE; r0 < hi; r0 += HSTEP) {
-        const int64_t rl = r0 + lane;
-        uint64_t gq = 0, hq = 0;
-        if (rl < hi) {
-            gq = (uint64_t)quantise(grad[rl], scg);
-            if (HCH) hq = (uint64_t)quantise(hess[rl], sch);
-        }
-        sum_g += (int64_t)gq;
-        sum_h += (int64_t)hq;
-        // lane's 16 rows of its feature: r0 % 64 == 0, so base % 16 == 0; with
-        // base < hi <= n <= ld and ld % 16 == 0 the 16-byte load stays in the row
-        const int64_t base = r0 + HFL * rg;
-        const uint4 bv = base < hi ? *reinterpret_cast<const uint4*>(col + base) : make_uint4(0, 0, 0, 0);
-        const uint32_t w[4] = {bv.x, bv.y, bv.z, bv.w};
-        const int nv = (int)min((int64_t)HFL, max((int64_t)0, hi - base));
-#define YABT_ROOT_STEP(J)                                                        \
-        {                                                                        \
-            const uint64_t gj = row_bcast64<J>(gq), hj = HCH ? row_bcast64<J>(hq) : 0; \
-            const int b = (int)((w[(J) >> 2] >> (8 * ((J) & 3))) & 0xffu);       \
-            if (fok && (J) < nv && b != d) hist_add<HCH>(L, b, fl, gj, hj);       \
-        }
-        YABT_ROOT_STEP(0) YABT_ROOT_STEP(1) YABT_ROOT_STEP(2) YABT_ROOT_STEP(3)
-        YABT_ROOT_STEP(4) YABT_ROOT_STEP(5) YABT_ROOT_STEP(6) YABT_ROOT_STEP(7)
-        YABT_ROOT_STEP(8) YABT_ROOT_STEP(9) YABT_ROOT_STEP(10) YABT_ROOT_STEP(11)
-        YABT_ROOT_STEP(12) YABT_ROOT_STEP(13) YABT_ROOT_STEP(14) YABT_ROOT_STEP(15)
-#undef YABT_ROOT_STEP
-    }
-    if (totals) {
-        sum_g = wave_sum<int64_t>(sum_g);
-        sum_h = wave_sum<int64_t>(sum_h);
-        if (lane == 0) {
-            atomicAdd((unsigned long long*)&q_tot->tot_g, (unsigned long long)sum_g);
-            atomicAdd((unsigned long long*)&q_tot->tot_h, (unsigned long long)sum_h);
-        }
-    }
-    __syncthreads();
-    hist_flush<HCH>(L, out, F, f0);
-}
-
 // ---------------------------------------------------------------------------
 // Packed count channel.  The count rides in the low bits of one 64-bit LDS
 // word next to q (q(h), or q(g) without the h channel): every row adds
@@ -213,18 +149,16 @@ __host__ __device__ inline int pack_window_log2(int64_t n) {
     return w >= 10 ? (w > 16 ? 16 : w) : -1;   // 2^10 rows = one block step
 }
 
-// LDS of the streaming root histogram: 256 bins x 32 words of 8 bytes.  Word
-// fl of a bin is sum q(g) of feature f0 + fl (with the h channel), word
-// 16 + fl the packed (q << cb) + 1 of feature f0 + fl.  A bin's words span
-// 256 bytes, so the byte address of an entry is (bin << 8) | (fl << 3)
-// (+ 128 for the packed word): one byte permute of the loaded bin word
-// builds it.  Within the 16 lanes of a row group the 16 features hit 16
-// distinct bank pairs whatever the bins are.
+// LDS of the streaming root histogram: 256 bins x 32 words of 8 bytes, of
+// which words 0..15 of a bin are the cells of features f0 .. f0 + 15 in one
+// buffer and words 16..31 in the other.  The byte address of a cell is then
+// (bin << 8) | (buffer << 7) | (fl << 3): one byte permute of the loaded bin
+// word builds it.
+// Within the 16 lanes of a row group the 16 features hit 16 distinct bank
+// pairs whatever the bins are.
 struct HistLdsR {
     unsigned long long w[NB * 2 * HFL];
 };
-
-constexpr int ROOT_PW = HFL;                  // word offset of the packed words in a bin row
 
 // Byte J of `word` placed in bits 8..15 over `lo` (bits 0..7).
 template <int J>
@@ -232,133 +166,237 @@ __device__ __forceinline__ uint32_t bin_addr(uint32_t word, uint32_t lo) {
     return __builtin_amdgcn_perm(word, lo, 0x0c0c0000u | ((4u + J) << 8));
 }
 
-// SKIP: dflt is given (rows in a feature's default bin are not added).
-// Lanes of features >= F read feature f0's column and add into their own LDS
-// columns, which the flush ignores, so the adds need no feature test.  Each
-// wave loads the next step's g, h and bins before adding the current step.
+// bin_addr with J a compile-time constant of an unrolled loop.
+__device__ __forceinline__ uint32_t bin_addr_rt(uint32_t word, uint32_t lo, int j) {
+    return __builtin_amdgcn_perm(word, lo, 0x0c0c0000u | ((4u + (uint32_t)j) << 8));
+}
+
+// ---------------------------------------------------------------------------
+// Streaming root histogram: one LDS atomic per (row, feature).
+//
+// The count plane never needs the stream: it depends only on the bins, which
+// stay the same over a whole fit, so it comes from the per-fit counts
+// (F, 256) (k_bin_count, yabt_bin_counts), which each tile's chunk-0 block
+// adds at its flush.  The stream carries g and h only:
+//   HCH (h varies): each update adds the word (q(g) << 32) + q(h) (mod 2^64)
+//     into the cell [bin][feature]; each thread then reads its 4 cells and
+//     unpacks them -- lo, the
+//     sign-extended low 32 bits, is the h sum; (cell - lo) >> 32 the g sum.
+//     The cells come in two buffers that alternate every epoch of
+//     ROOT_UNPACK = 2 steps: after the barrier that ends an epoch, each thread
+//     reads and clears its cells of that epoch's buffer while the waves add
+//     the next epoch into the other one.  A cell so takes the rows of one
+//     epoch (2048, or n when smaller) between two reads, and no atomic
+//     targets it while it is read; with hist_shift's |q| <= 2^(30 -
+//     min(k, 11)) each half's sum stays within 2^30, so both are exact.
+//   !HCH (every h equal): the word is q(g) itself; no unpacking, and the h
+//     plane is left to the caller (count * q(h)).
+// Invalid rows of a step add zero words (their q is 0), so the loop needs no
+// per-row tail test; only the loads are bounded.  Each wave keeps the loads
+// of the next ROOT_DEPTH steps in flight (the adds of one step take far less
+// than a load's latency).
+//
+// SKIP: dflt is given (rows in a feature's default bin are not added, and
+// the chunk-0 block leaves that bin's count out too: the caller restores the
+// whole bin as node total minus the other bins).  Lanes of features >= F
+// read feature f0's column and add into their own LDS columns, which the
+// flush ignores.
+// ---------------------------------------------------------------------------
+
+// The streaming root kernel's blocks: 1024 threads (16 waves, 1024 rows per
+// step) and 64 KB of LDS.
+constexpr int RBLOCK = 1024;
+constexpr int RSTEP = RBLOCK;                  // rows per block step (64 per wave)
+constexpr int RENT = NB * HFL / RBLOCK;        // cells per thread in an unpack and the flush
+
+// LDS of the root kernel's flush: the block's cells transposed to
+// [feature][bin] (see flush_cells); shares the space of HistLdsR.
+struct RootFlushLds {
+    unsigned long long g[NB * HFL];
+    unsigned long long h[NB * HFL];
+};
+
+// Final flush of the streaming root kernel: as flush_cells, with the counts
+// read from the per-fit table (chunk-0 blocks only, `counts` may be NULL;
+// a feature's default bin, dflt[f] when dflt is given, is left out) and
+// cells whose g and h sums are zero skipped (adding zero changes nothing).
+template <bool HCH>
+__device__ __forceinline__ void flush_cells_gh(RootFlushLds& T, const int64_t (&g)[RENT], const int64_t (&h)[RENT],
+                                               const uint32_t* __restrict__ counts,
+                                               const int32_t* __restrict__ dflt, int64_t* out, int F, int f0) {
+#pragma unroll
+    for (int k = 0; k < RENT; ++k) {
+        const int i = threadIdx.x + k * RBLOCK;
+        const int fl = i % HFL;
+        const int j = fl * NB + ((i / HFL) ^ (2 * fl));
+        T.g[j] = (unsigned long long)g[k];
+        if (HCH) T.h[j] = (unsigned long long)h[k];
+    }
+    __syncthreads();
+    const size_t plane = (size_t)F * NB;
+#pragma unroll
+    for (int k = 0; k < RENT; ++k) {
+        const int j = threadIdx.x + k * RBLOCK;
+        const int fl = j / NB;
+        const int fi = f0 + fl;
+        if (fi >= F) continue;
+        const int b = (j % NB) ^ (2 * fl);
+        const size_t at = (size_t)fi * NB + (size_t)b;
+        const unsigned long long gj = T.g[j];
+        if (gj) atomicAdd((unsigned long long*)(out + at), gj);
+        if (HCH) {
+            const unsigned long long hj = T.h[j];
+            if (hj) atomicAdd((unsigned long long*)(out + plane + at), hj);
+        }
+        if (counts) {
+            const uint32_t cj = counts[at];
+            const int d = dflt ? dflt[fi] : -1;   // the default bin's count is left to the caller's fill
+            if (cj && b != d) atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)cj);
+        }
+    }
+}
+
+constexpr int ROOT_DEPTH = 4;    // steps of inputs loaded ahead of the adds
+constexpr int ROOT_UNPACK = 2;   // steps per epoch: 2 x 1024 = 2048 rows, hist_shift's bound
+constexpr bool ROOT_DBUF = true;   // two cell buffers (one barrier per epoch) or one (two barriers)
+static_assert(ROOT_DEPTH % (2 * ROOT_UNPACK) == 0, "a ring round is whole pairs of epochs");
+static_assert(ROOT_UNPACK * RSTEP <= 2048, "hist_shift bounds 2048 rows of a cell between two unpacks");
+
 template <bool HCH, bool SKIP>
-__device__ __forceinline__ void hist_root_packed(HistLdsR& L, const uint8_t* __restrict__ bins_fm, int64_t ld,
-                                                 const float* __restrict__ grad, const float* __restrict__ hess,
-                                                 int64_t n, int F, double scg, double sch,
-                                                 const int32_t* __restrict__ dflt, Quant* q_tot, int64_t* out,
-                                                 int chunks, int wlog) {
+__device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restrict__ bins_fm, int64_t ld,
+                                             const float* __restrict__ grad, const float* __restrict__ hess,
+                                             int64_t n, int F, double scg, double sch,
+                                             const int32_t* __restrict__ dflt, const uint32_t* __restrict__ counts,
+                                             Quant* q_tot, int64_t* out, int chunks) {
     const int tile = blockIdx.x / chunks, chunk = blockIdx.x % chunks;
     const int f0 = tile * HFL;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const int fl = lane & (HFL - 1), rg = lane / HFL;
     const int f = f0 + fl;
     const bool fok = f < F;
-    const int64_t per = ((n + chunks - 1) / chunks + HSTEP - 1) / HSTEP * HSTEP;
+    const int64_t per = ((n + chunks - 1) / chunks + RSTEP - 1) / RSTEP * RSTEP;
     const int64_t lo = (int64_t)chunk * per, hi = min(n, lo + per);
     if (f0 >= F || lo >= hi) return;
     const int d = (SKIP && fok) ? dflt[f] : -1;
     const bool totals = q_tot != nullptr && tile == 0;
-    const int cb = wlog + 1;
-    const uint64_t cmask = ((uint64_t)1 << cb) - 1;
-    const int64_t win_steps = (int64_t)1 << (wlog - 10);
-    for (int i = threadIdx.x; i < NB * 2 * HFL; i += HBLOCK) L.w[i] = 0;
+    for (int i = threadIdx.x; i < NB * 2 * HFL; i += RBLOCK) L.w[i] = 0;
     const uint32_t lbase = (uint32_t)fl << 3;
     char* const lds = reinterpret_cast<char*>(L.w);
-    int64_t qa[HENT];
-    uint32_t ca[HENT];
+    int64_t ag[RENT], ah[RENT];   // unpacked sums of this thread's cells
+    uint64_t prev[RENT];          // single buffer: each cell at its previous read
 #pragma unroll
-    for (int k = 0; k < HENT; ++k) {
-        qa[k] = 0;
-        ca[k] = 0;
+    for (int k = 0; k < RENT; ++k) {
+        ag[k] = 0;
+        ah[k] = 0;
+        prev[k] = 0;
     }
-    const uint8_t* col = bins_fm + (size_t)(fok ? f : f0) * ld;
-    // r0 % 64 == 0, so base % 16 == 0; base < hi <= n <= ld, ld % 16 == 0:
-    // the 16-byte load stays inside the row
-    float gx = 0.0f, hx = 0.0f;
-    uint4 bv = make_uint4(0, 0, 0, 0);
-    {
-        const int64_t r0 = lo + (int64_t)wave * WAVE;
-        if (r0 + lane < hi) {
-            gx = grad[r0 + lane];
-            if (HCH) hx = hess[r0 + lane];
+    // the cell a thread unpacks: cell i = t + k RBLOCK is bin i / HFL, feature i % HFL
+    auto cell = [](int k) { const int i = threadIdx.x + k * RBLOCK; return (i / HFL) * (2 * HFL) + (i % HFL); };
+    // add buffer p's cells to the sums and clear them (no atomic targets p
+    // meanwhile: the other buffer takes the current epoch)
+    auto unpack = [&](int p) {
+#pragma unroll
+        for (int k = 0; k < RENT; ++k) {
+            const int c = cell(k) + p * HFL;
+            const uint64_t v = L.w[c];
+            uint64_t dv = v;
+            if (ROOT_DBUF) {
+                L.w[c] = 0;
+            } else {
+                dv = v - prev[k];
+                prev[k] = v;
+            }
+            const int64_t hs = (int64_t)(int32_t)(uint32_t)dv;
+            ah[k] += hs;
+            ag[k] += (int64_t)(dv - (uint64_t)hs) >> 32;
         }
-        if (r0 + HFL * rg < hi) bv = *reinterpret_cast<const uint4*>(col + r0 + HFL * rg);
+    };
+    const uint8_t* col = bins_fm + (size_t)(fok ? f : f0) * ld;
+    // Inputs of step s: this lane's row's g and h, and 16 rows of its
+    // feature's bins.  The loads are unconditional, so the loop is straight
+    // code and each stage's registers are waited for on their own: a row past
+    // hi reads row hi - 1 (its word is zero below), and a row group past hi
+    // reads the chunk's first 16 rows (its rows' words are zero).  r0 % 64 ==
+    // 0 and lo % 16 == 0, so the bins base is a multiple of 16 below hi <= n
+    // <= ld (ld % 16 == 0): the 16-byte load stays inside the row.
+    auto load = [&](int64_t s, float& gv, float& hv, uint4& bw) {
+        const int64_t r0 = lo + s * RSTEP + (int64_t)wave * WAVE;
+        const int64_t r = min(r0 + lane, hi - 1);
+        gv = grad[r];
+        if (HCH) hv = hess[r];
+        const int64_t base = r0 + HFL * rg;
+        bw = *reinterpret_cast<const uint4*>(col + (base < hi ? base : lo));
+    };
+    const int64_t steps = (hi - lo + RSTEP - 1) / RSTEP;   // the same in every wave: barriers below
+    // Ring of ROOT_DEPTH stages: stage j holds step s0 + j and is then refilled
+    // with step s0 + j + ROOT_DEPTH (the ring is unrolled: no register moves).
+    // It starts one round early, at steps -ROOT_DEPTH .. -1, whose rows are
+    // all invalid (zero words at cell 0): that round only issues the first
+    // loads, in the same order as every later round.
+    float gs[ROOT_DEPTH], hs[ROOT_DEPTH];
+    uint4 bs[ROOT_DEPTH];
+#pragma unroll
+    for (int j = 0; j < ROOT_DEPTH; ++j) {
+        gs[j] = 0.0f;
+        hs[j] = 0.0f;
+        bs[j] = make_uint4(0, 0, 0, 0);
     }
     __syncthreads();
     int64_t sum_g = 0, sum_h = 0;
-    const int64_t steps = (hi - lo + HSTEP - 1) / HSTEP;   // the same in every wave: barriers below
-    for (int64_t s = 0; s < steps; ++s) {
-        const int64_t r0 = lo + s * HSTEP + (int64_t)wave * WAVE;
-        // next step's inputs
-        float gn = 0.0f, hn = 0.0f;
-        uint4 bn = make_uint4(0, 0, 0, 0);
-        {
-            const int64_t r1 = r0 + HSTEP;
-            if (r1 + lane < hi) {
-                gn = grad[r1 + lane];
-                if (HCH) hn = hess[r1 + lane];
-            }
-            if (r1 + HFL * rg < hi) bn = *reinterpret_cast<const uint4*>(col + r1 + HFL * rg);
-        }
-        const bool rok = r0 + lane < hi;
-        const int64_t gq = rok ? quantise(gx, scg) : 0;
-        const int64_t hq = (HCH && rok) ? quantise(hx, sch) : 0;
-        sum_g += gq;
-        sum_h += hq;
-        const uint64_t gw = HCH ? (uint64_t)gq : ((uint64_t)gq << cb) + 1;
-        const uint64_t pw = HCH ? ((uint64_t)hq << cb) + 1 : 0;
-        const uint32_t wv[4] = {bv.x, bv.y, bv.z, bv.w};
-#define YABT_PACK_ADD(J)                                                         \
-        {                                                                        \
-            char* const at = lds + bin_addr<(J) & 3>(wv[(J) >> 2], lbase);       \
-            unsigned long long* const pw_at = reinterpret_cast<unsigned long long*>(at + 8 * ROOT_PW); \
-            if (HCH) {                                                           \
-                atomicAdd(reinterpret_cast<unsigned long long*>(at), (unsigned long long)gj); \
-                atomicAdd(pw_at, (unsigned long long)pj);                        \
-            } else {                                                             \
-                atomicAdd(pw_at, (unsigned long long)gj);                        \
-            }                                                                    \
-        }
-#define YABT_PACK_STEP(J, TAIL)                                                  \
-        {                                                                        \
-            const uint64_t gj = row_bcast64<J>(gw);                              \
-            const uint64_t pj = HCH ? row_bcast64<J>(pw) : 0;                     \
-            if (!(TAIL) || (J) < nv) {                                           \
-                if (SKIP) {                                                      \
-                    const int b = (int)((wv[(J) >> 2] >> (8 * ((J) & 3))) & 0xffu); \
-                    if (b != d) YABT_PACK_ADD(J)                                 \
-                } else {                                                         \
-                    YABT_PACK_ADD(J)                                             \
-                }                                                                \
-            }                                                                    \
-        }
-        if (r0 + WAVE <= hi) {   // wave-uniform: all 64 rows valid
-            constexpr int nv = HFL;
-            YABT_PACK_STEP(0, 0) YABT_PACK_STEP(1, 0) YABT_PACK_STEP(2, 0) YABT_PACK_STEP(3, 0)
-            YABT_PACK_STEP(4, 0) YABT_PACK_STEP(5, 0) YABT_PACK_STEP(6, 0) YABT_PACK_STEP(7, 0)
-            YABT_PACK_STEP(8, 0) YABT_PACK_STEP(9, 0) YABT_PACK_STEP(10, 0) YABT_PACK_STEP(11, 0)
-            YABT_PACK_STEP(12, 0) YABT_PACK_STEP(13, 0) YABT_PACK_STEP(14, 0) YABT_PACK_STEP(15, 0)
-        } else if (r0 < hi) {
-            const int nv = (int)min((int64_t)HFL, max((int64_t)0, hi - (r0 + HFL * rg)));
-            YABT_PACK_STEP(0, 1) YABT_PACK_STEP(1, 1) YABT_PACK_STEP(2, 1) YABT_PACK_STEP(3, 1)
-            YABT_PACK_STEP(4, 1) YABT_PACK_STEP(5, 1) YABT_PACK_STEP(6, 1) YABT_PACK_STEP(7, 1)
-            YABT_PACK_STEP(8, 1) YABT_PACK_STEP(9, 1) YABT_PACK_STEP(10, 1) YABT_PACK_STEP(11, 1)
-            YABT_PACK_STEP(12, 1) YABT_PACK_STEP(13, 1) YABT_PACK_STEP(14, 1) YABT_PACK_STEP(15, 1)
-        }
-#undef YABT_PACK_STEP
-#undef YABT_PACK_ADD
-        if ((s + 1) % win_steps == 0 || s + 1 == steps) {
-            __syncthreads();
+    for (int64_t s0 = -ROOT_DEPTH; s0 < steps; s0 += ROOT_DEPTH) {
 #pragma unroll
-            for (int k = 0; k < HENT; ++k) {
-                const int i = threadIdx.x + k * HBLOCK;
-                const int pi = (i / HFL) * (2 * HFL) + ROOT_PW + (i % HFL);
-                const uint64_t v = L.w[pi];
-                L.w[pi] = 0;
-                const uint64_t c = v & cmask;
-                qa[k] += (int64_t)(v - c) >> cb;
-                ca[k] += (uint32_t)c;
+        for (int j = 0; j < ROOT_DEPTH; ++j) {
+            const int64_t s = s0 + j;
+            // keep the scheduler from hoisting a later stage's use of its
+            // loads above this stage's work (that would wait for them early);
+            // every stage runs, a step past the last being all invalid rows
+            __builtin_amdgcn_sched_barrier(0);
+            const int64_t r0 = lo + s * RSTEP + (int64_t)wave * WAVE;
+            const bool rok = s >= 0 && r0 + lane < hi;
+            const int64_t gq = rok ? quantise_node(gs[j], scg) : 0;
+            const int64_t hq = (HCH && rok) ? quantise_node(hs[j], sch) : 0;
+            // the 16 cell addresses (and, with SKIP, which rows are not added)
+            // come out of this stage's bins before its registers are refilled,
+            // so the old and new values are never live at once (else the refill
+            // lands in other registers and a copy at the loop's end waits for it)
+            const uint32_t lb = (ROOT_DBUF && HCH && (j / ROOT_UNPACK) % 2) ? lbase | 128u : lbase;   // the epoch's buffer
+            const uint32_t wv[4] = {bs[j].x, bs[j].y, bs[j].z, bs[j].w};
+            uint32_t at[HFL];
+            uint32_t keep = 0xffffu;
+#pragma unroll
+            for (int J = 0; J < HFL; ++J) {
+                at[J] = bin_addr_rt(wv[J >> 2], lb, J & 3);
+                if (SKIP && (int)((wv[J >> 2] >> (8 * (J & 3))) & 0xffu) == d) keep &= ~(1u << J);
             }
-            __syncthreads();
+            load(s + ROOT_DEPTH, gs[j], hs[j], bs[j]);
+            sum_g += gq;
+            sum_h += hq;
+            const uint64_t word = HCH ? ((uint64_t)gq << 32) + (uint64_t)hq : (uint64_t)gq;
+#define YABT_GH_ADD(J)                                                           \
+            {                                                                    \
+                const uint64_t wj = row_bcast64<J>(word);                        \
+                unsigned long long* const cp = reinterpret_cast<unsigned long long*>(lds + at[J]); \
+                if (!SKIP || ((keep >> (J)) & 1u)) atomicAdd(cp, (unsigned long long)wj); \
+            }
+            YABT_GH_ADD(0) YABT_GH_ADD(1) YABT_GH_ADD(2) YABT_GH_ADD(3)
+            YABT_GH_ADD(4) YABT_GH_ADD(5) YABT_GH_ADD(6) YABT_GH_ADD(7)
+            YABT_GH_ADD(8) YABT_GH_ADD(9) YABT_GH_ADD(10) YABT_GH_ADD(11)
+            YABT_GH_ADD(12) YABT_GH_ADD(13) YABT_GH_ADD(14) YABT_GH_ADD(15)
+#undef YABT_GH_ADD
+            if (HCH && (j + 1) % ROOT_UNPACK == 0) {
+                // end of an epoch: once every wave's adds into its buffer are
+                // done, read it while the next epoch adds into the other one
+                __syncthreads();
+                unpack(ROOT_DBUF ? (j / ROOT_UNPACK) % 2 : 0);
+                if (!ROOT_DBUF) __syncthreads();
+            }
         }
-        gx = gn;
-        hx = hn;
-        bv = bn;
+    }
+    __syncthreads();
+    if (HCH && !ROOT_DBUF) unpack(0);
+    if (!HCH) {   // one buffer, never unpacked: the cells are the g sums
+#pragma unroll
+        for (int k = 0; k < RENT; ++k) ag[k] = (int64_t)L.w[cell(k)];
     }
     if (totals) {
         sum_g = wave_sum<int64_t>(sum_g);
@@ -368,63 +406,104 @@ __device__ __forceinline__ void hist_root_packed(HistLdsR& L, const uint8_t* __r
             atomicAdd((unsigned long long*)&q_tot->tot_h, (unsigned long long)sum_h);
         }
     }
-    uint64_t gv[HENT];
-#pragma unroll
-    for (int k = 0; k < HENT; ++k) {
-        const int i = threadIdx.x + k * HBLOCK;
-        gv[k] = HCH ? L.w[(i / HFL) * (2 * HFL) + (i % HFL)] : (uint64_t)qa[k];
-    }
-    __syncthreads();   // every g cell read before the LDS is rewritten
-    flush_cells<HCH>(*reinterpret_cast<HistLds*>(&L), gv, qa, ca, out, F, f0);
+    __syncthreads();   // every cell read before the LDS is rewritten
+    flush_cells_gh<HCH>(*reinterpret_cast<RootFlushLds*>(&L), ag, ah, chunk == 0 ? counts : nullptr,
+                        SKIP ? dflt : nullptr, out, F, f0);
 }
 
-// count_mode 0: all three channels; 1: no h channel when q->const_h.
+// Bin counts of all n rows of the feature-major bins, per (feature, bin):
+// OUT64 false: added into a uint32 (F, 256) table (the per-fit counts);
+// OUT64 true: added into an int64 (F, 256) count plane.  dflt (may be NULL):
+// bin dflt[f] is not counted.  Same grid and row chunks as k_hist_root; one
+// 32-bit LDS atomic per (row, feature).
+template <bool OUT64>
+static __global__ __attribute__((unused)) void __launch_bounds__(HBLOCK)
+k_bin_count(const uint8_t* __restrict__ bins_fm, int64_t ld, int64_t n, int F, const int32_t* __restrict__ dflt,
+            void* out, int chunks) {
+    __shared__ uint32_t c[NB * HFL];   // [bin][feature]
+    const int tile = blockIdx.x / chunks, chunk = blockIdx.x % chunks;
+    const int f0 = tile * HFL;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int fl = lane & (HFL - 1), rg = lane / HFL;
+    const int f = f0 + fl;
+    const bool fok = f < F;
+    const int64_t per = ((n + chunks - 1) / chunks + HSTEP - 1) / HSTEP * HSTEP;
+    const int64_t lo = (int64_t)chunk * per, hi = min(n, lo + per);
+    if (f0 >= F || lo >= hi) return;
+    const int d = (fok && dflt) ? dflt[f] : -1;
+    for (int i = threadIdx.x; i < NB * HFL; i += HBLOCK) c[i] = 0;
+    __syncthreads();
+    const uint8_t* col = bins_fm + (size_t)(fok ? f : f0) * ld;
+    for (int64_t r0 = lo + (int64_t)wave * WAVE; r0 < hi; r0 += HSTEP) {
+        // base % 16 == 0 and base < hi <= n <= ld (ld % 16 == 0): in the row
+        const int64_t base = r0 + HFL * rg;
+        if (!fok || base >= hi) continue;
+        const uint4 bv = *reinterpret_cast<const uint4*>(col + base);
+        const uint32_t w[4] = {bv.x, bv.y, bv.z, bv.w};
+        const int nv = (int)min((int64_t)HFL, hi - base);
+#pragma unroll
+        for (int J = 0; J < HFL; ++J) {
+            const int b = (int)((w[J >> 2] >> (8 * (J & 3))) & 0xffu);
+            if (J < nv && b != d) atomicAdd(&c[b * HFL + fl], 1u);
+        }
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < NB * HFL; i += HBLOCK) {
+        const int fi = f0 + (i % HFL);
+        const uint32_t v = c[i];
+        if (fi >= F || v == 0) continue;
+        const size_t at = (size_t)fi * NB + (size_t)(i / HFL);
+        if (OUT64)
+            atomicAdd(reinterpret_cast<unsigned long long*>(out) + at, (unsigned long long)v);
+        else
+            atomicAdd(reinterpret_cast<uint32_t*>(out) + at, v);
+    }
+}
+
+// The streaming root histogram.  count_mode 0: g and h planes; 1: no h plane
+// when q->const_h.  counts: the per-fit bin counts, added into the count
+// plane by the chunk-0 blocks (NULL: the count plane is not touched).
 // SKIP: dflt is given (a separate kernel, so that the loops without the
 // default-bin test are compiled on their own).
 template <bool SKIP>
-static __global__ __attribute__((unused)) void __launch_bounds__(HBLOCK) k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld,
-                                                      const float* __restrict__ grad,
-                                                      const float* __restrict__ hess, int64_t n, int F,
-                                                      const Quant* q, double scg_v, double sch_v,
-                                                      const int32_t* __restrict__ dflt, Quant* q_tot,
-                                                      int64_t* out, int chunks, int count_mode,
-                                                      const int32_t* done) {
+static __global__ __attribute__((unused)) void __launch_bounds__(RBLOCK)
+k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld, const float* __restrict__ grad,
+            const float* __restrict__ hess, int64_t n, int F, const Quant* q, double scg_v, double sch_v,
+            const int32_t* __restrict__ dflt, const uint32_t* __restrict__ counts, Quant* q_tot, int64_t* out,
+            int chunks, int count_mode, const int32_t* done) {
     const int32_t dn = done ? *done : 0;
     const double scg = q ? q->scg : scg_v, sch = q ? q->sch : sch_v;
     const bool no_h = count_mode && q && q->const_h;
     if (dn) return;
-    __shared__ union {
-        HistLds u;
-        HistLdsR p;
-    } L;
-    const int wlog = pack_window_log2(n);
-    if (wlog >= 0) {
-        if (no_h)
-            hist_root_packed<false, SKIP>(L.p, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks,
-                                          wlog);
-        else
-            hist_root_packed<true, SKIP>(L.p, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks,
-                                         wlog);
-    } else if (no_h) {
-        hist_root_body<false>(L.u, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks);
-    } else {
-        hist_root_body<true>(L.u, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, q_tot, out, chunks);
-    }
+    __shared__ HistLdsR L;   // 64 KB, also the flush's RootFlushLds
+    static_assert(sizeof(RootFlushLds) <= sizeof(HistLdsR), "the flush reuses the cells' LDS");
+    if (no_h)
+        hist_root_gh<false, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks);
+    else
+        hist_root_gh<true, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks);
 }
 
-// Launch k_hist_root over `tiles * chunks` blocks (the instantiation with
-// the default-bin test only when dflt is given).
+// Launch the root histogram over `tiles * chunks` blocks into the (3, F, 256)
+// histogram `out` (cleared beforehand).  With counts == NULL the count plane
+// is counted from the bins first (k_bin_count, one more pass over them);
+// callers that keep the per-fit counts pass them instead.  The instantiation
+// with the default-bin test runs only when dflt is given.
 static __attribute__((unused)) void launch_hist_root(int tiles, int chunks, hipStream_t stream,
                                                      const uint8_t* bins_fm, int64_t ld, const float* grad,
                                                      const float* hess, int64_t n, int F, const Quant* q,
-                                                     double scg, double sch, const int32_t* dflt, Quant* q_tot,
-                                                     int64_t* out, int count_mode, const int32_t* done) {
+                                                     double scg, double sch, const int32_t* dflt,
+                                                     const uint32_t* counts, Quant* q_tot, int64_t* out,
+                                                     int count_mode, const int32_t* done) {
+    if (!counts)
+        k_bin_count<true><<<tiles * chunks, HBLOCK, 0, stream>>>(bins_fm, ld, n, F, dflt, out + (size_t)2 * F * NB,
+                                                                 chunks);
     if (dflt)
-        k_hist_root<true><<<tiles * chunks, HBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, dflt,
-                                                                 q_tot, out, chunks, count_mode, done);
+        k_hist_root<true><<<tiles * chunks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, dflt,
+                                                                 counts, q_tot, out, chunks, count_mode, done);
     else
-        k_hist_root<false><<<tiles * chunks, HBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch,
-                                                                  nullptr, q_tot, out, chunks, count_mode, done);
+        k_hist_root<false><<<tiles * chunks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch,
+                                                                  nullptr, counts, q_tot, out, chunks, count_mode,
+                                                                  done);
 }
 
 // Rows of one node for a gather launch.
@@ -479,7 +558,7 @@ __device__ __forceinline__ void hist_gather_body(HistLds& L, const uint8_t* __re
     __syncthreads();
     const uint8_t* fbase = bins_rm + f0 + (fok ? fl : 0);
     for (; i0 < hi; i0 += HSTEP) {
-        const uint64_t gq = (uint64_t)quantise(gx, scg), hq = HCH ? (uint64_t)quantise(hx, sch) : 0;
+        const uint64_t gq = (uint64_t)quantise_node(gx, scg), hq = HCH ? (uint64_t)quantise_node(hx, sch) : 0;
         const int nv = (int)min((int64_t)HFL, max((int64_t)0, hi - (i0 + HFL * rg)));
         int bj[HFL];
 #define YABT_GATHER_LOAD(J)                                                       \
@@ -607,8 +686,8 @@ __device__ __forceinline__ void hist_gather_packed(HistLdsP& L, const uint8_t* _
 #undef YABT_GATHER_NEXT
         // step s
         const bool rok = i0 + lane < hi;
-        const int64_t gq = rok ? quantise(gx, scg) : 0;
-        const int64_t hq = (HCH && rok) ? quantise(hx, sch) : 0;
+        const int64_t gq = rok ? quantise_node(gx, scg) : 0;
+        const int64_t hq = (HCH && rok) ? quantise_node(hx, sch) : 0;
         const uint64_t gw = HCH ? (uint64_t)gq : ((uint64_t)gq << cb) + 1;
         const uint64_t pw = HCH ? ((uint64_t)hq << cb) + 1 : 0;
 #define YABT_GATHER_STEP(J, TAIL)                                                \

@@ -79,6 +79,10 @@ __global__ void k_fill_i64(int64_t* p, int64_t v, int64_t count) {
     for (int64_t i = (int64_t)blockIdx.x * OB + threadIdx.x; i < count; i += (int64_t)gridDim.x * OB) p[i] = v;
 }
 
+__global__ void k_fill_u32(uint32_t* p, uint32_t v, int64_t count) {
+    for (int64_t i = (int64_t)blockIdx.x * OB + threadIdx.x; i < count; i += (int64_t)gridDim.x * OB) p[i] = v;
+}
+
 __global__ void k_set_hist_job(HistJob* j, const uint32_t* rows, int64_t lo, int64_t hi, int64_t* out) {
     j->active = 1;
     j->pad = 0;
@@ -284,8 +288,8 @@ int hist_enqueue(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, 
     if (!rows) {
         if (n > 0) {
             const int rc = root_chunks(n, tiles);
-            launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, q, 0.0, 0.0, nullptr, nullptr, out,
-                             0, nullptr);
+            launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, q, 0.0, 0.0, nullptr, nullptr,
+                             nullptr, out, 0, nullptr);
         }
     } else if (m > 0) {
         k_set_hist_job<<<1, 1, 0, stream>>>(job, rows, 0, m, out);
@@ -348,7 +352,7 @@ int yabt_hist_accumulate(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* b
         if (n > 0) {
             const int rc = root_chunks(n, tiles);
             launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, nullptr, scg, sch, nullptr, nullptr,
-                             out, 0, nullptr);
+                             nullptr, out, 0, nullptr);
         }
     } else if (m > 0) {
         Carve c{(char*)workspace, 0};
@@ -359,6 +363,36 @@ int yabt_hist_accumulate(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* b
                                                                         sch, nullptr, job, 0, nullptr, pack_window_log2(n));
     }
     return launch_status("yabt_hist_accumulate launch");
+}
+
+int yabt_bin_counts(const uint8_t* bins_fm, int64_t ld_fm, int64_t n, int F, uint32_t* out_counts,
+                    hipStream_t stream) {
+    if (!bins_fm || !out_counts || F < 1 || n < 0 || n > 0xFFFFFFFFll || ld_fm < n || ld_fm % 16 ||
+        !aligned16(bins_fm))
+        return fail(-2, "yabt_bin_counts: bad arguments");
+    const int64_t ne = (int64_t)F * NB;
+    k_fill_u32<<<launch_grid(ne, OB, 1024), OB, 0, stream>>>(out_counts, 0, ne);
+    if (n > 0) {
+        const int tiles = (F + HFL - 1) / HFL;
+        const int rc = root_chunks(n, tiles);
+        k_bin_count<false><<<tiles * rc, HBLOCK, 0, stream>>>(bins_fm, ld_fm, n, F, nullptr, out_counts, rc);
+    }
+    return launch_status("yabt_bin_counts launch");
+}
+
+int yabt_hist_root(const uint8_t* bins_fm, int64_t ld_fm, const float* grad, const float* hess, int64_t n, int F,
+                   const uint32_t* bin_counts, int sg, int sh, int64_t* out, hipStream_t stream) {
+    if (!out) return fail(-2, "yabt_hist_root: bad arguments");
+    const int rc0 = check_hist_layout(bins_fm, ld_fm, nullptr, 0, grad, hess, n, F, nullptr, 0, "yabt_hist_root");
+    if (rc0) return rc0;
+    if (n > 0) {
+        const int tiles = (F + HFL - 1) / HFL;
+        const int rc = root_chunks(n, tiles);
+        k_hist_root<false><<<tiles * rc, RBLOCK, 0, stream>>>(bins_fm, ld_fm, grad, hess, n, F, nullptr,
+                                                              ldexp(1.0, sg), ldexp(1.0, sh), nullptr, bin_counts,
+                                                              nullptr, out, rc, 0, nullptr);
+    }
+    return launch_status("yabt_hist_root launch");
 }
 
 size_t yabt_best_split_workspace_bytes(int F) {

@@ -75,6 +75,21 @@ class BinLayouts:
         self.ld_fm = fm.shape[1]
         self.ld_rm = rm.shape[1]
         self._default = None
+        self._counts = None
+
+    def counts(self) -> torch.Tensor:
+        """Per-(feature, bin) row counts (F, 256) uint32 of the bins, counted
+        once per layout (yabt_bin_counts): the count plane of every root
+        histogram over these bins, which the growers take instead of
+        recounting the rows each tree."""
+        if self._counts is None:
+            lib = _lib.load()
+            dev = self.fm.device
+            c = torch.empty((self.F, MAX_BINS), dtype=torch.int32, device=dev)
+            _lib.check(lib.yabt_bin_counts(_ptr(self.fm), self.ld_fm, self.n, self.F, _ptr(c), _stream(dev)),
+                       "yabt_bin_counts")
+            self._counts = c
+        return self._counts
 
     # a default bin is skipped only where it holds at least this share of the
     # sampled rows; below it the per-update test costs more than it saves
@@ -262,7 +277,7 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
     status = torch.zeros(1, dtype=torch.int32, device=dev)
     rc = lib.yabt_grow(
         _ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h), _ptr(fm), _ptr(im),
-        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), _ptr(db), n, F,
+        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), _ptr(db), _ptr(lay.counts()), n, F,
         ctypes.c_float(float(lam)), ctypes.c_float(float(gamma)), ctypes.c_float(float(mcw)),
         int(msl), ctypes.c_float(float(lr)), L, int(max_depth), _ptr(ws), ws.numel(),
         _ptr(out_i[0]), _ptr(out_i[1]), _ptr(out_i[2]), _ptr(out_i[3]), _ptr(value),
@@ -304,7 +319,7 @@ def _grow_device_rounds(lib, lay: BinLayouts, g, h, fm, im, use_imat, nb, db, *,
     status = torch.zeros(3, dtype=torch.int32, device=dev)
     rc = lib.yabt_grow_batched(
         _ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h), _ptr(fm), _ptr(im),
-        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), _ptr(db), n, F,
+        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), _ptr(db), _ptr(lay.counts()), n, F,
         ctypes.c_float(float(lam)), ctypes.c_float(float(gamma)), ctypes.c_float(float(mcw)),
         int(msl), ctypes.c_float(float(lr)), L, int(max_depth), _ptr(ws), ws.numel(),
         _ptr(out_i[0]), _ptr(out_i[1]), _ptr(out_i[2]), _ptr(out_i[3]), _ptr(value), _ptr(out_i[4]),
@@ -352,7 +367,7 @@ def _grow_device_level(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, l
     status = torch.zeros(1, dtype=torch.int32, device=dev)
     rc = lib.yabt_grow_levelwise(
         _ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h), _ptr(fm), _ptr(im),
-        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), n, F,
+        ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), _ptr(lay.counts()), n, F,
         ctypes.c_float(float(lam)), ctypes.c_float(float(gamma)), ctypes.c_float(float(mcw)),
         int(msl), ctypes.c_float(float(lr)), L, int(max_depth), _ptr(ws), ws.numel(),
         _ptr(out_i[0]), _ptr(out_i[1]), _ptr(out_i[2]), _ptr(out_i[3]), _ptr(value), _ptr(out_i[4]),
