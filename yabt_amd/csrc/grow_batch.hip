@@ -88,7 +88,9 @@ struct Pend {
 // What the controller needs of a computed split, packed.
 struct PendSum {
     float gain[2];                       // the children's table gains (depth cap applied)
-    int32_t child_pend[2];
+    int16_t child_pend[2];               // the children's computed splits, -1: none
+    int16_t origin;                      // the split leaf's origin (2 q + c, -1: the root)
+    int16_t committed;                   // 1 once the split is committed
 };
 
 struct State {
@@ -98,6 +100,8 @@ struct State {
     int32_t round;                       // controllers run
     uint32_t scan_ticket;
     int32_t pad;
+    int32_t root_pend;                   // the root's computed split, -1: none
+    float root_gain;                     // the root's table gain
     int32_t round_pend[KMAX];            // this round's Pend entries
     int64_t tile_off[KMAX + 1];          // partition tiles of this round's splits, prefix sums
     int32_t chunk_off[KMAX + 1];         // gather chunks of this round's built children, prefix sums
@@ -146,10 +150,8 @@ struct Args {
     int64_t rows_ld;
     int64_t* hist;
     uint8_t* pend_path;                  // (pend_cap, F) features on the path to each split's children
-    float* gains;                        // the leaf table: fp32 gain, computed split, origin, node id
-    int32_t* leaf_pend;
-    int32_t* leaf_src;
-    int32_t* leaf_node;
+    int32_t* leaf_src;                   // cgrow's leaf table after the commits: each leaf's origin
+    int32_t* leaf_node;                  // and node id (gains and computed splits follow from the origin)
     Pend* pend;
     PendSum* psum;
     ScanRec* rec;                        // (KMAX, 2, scan blocks)
@@ -197,6 +199,8 @@ __global__ void k_setup_finish(Args A) {
     st->n_pend = 0;
     st->round = 0;
     st->scan_ticket = 0;
+    st->root_pend = -1;
+    st->root_gain = -INFINITY;
     st->n_nodes = 1;
     st->n_leaves = 1;
     if (A.q->nonfinite) {
@@ -453,19 +457,114 @@ __device__ __forceinline__ LeafV leaf_view(const Args& A, int src, const ScanRec
 }
 
 // The controller's LDS: cgrow's leaf table (entry a: leaf a), the computed
-// splits' children, and the lists this controller fills.
+// splits' children, and the lists this controller fills.  The arrays live in
+// the scan launch's dynamic LDS, sized by the leaf budget and the Pend
+// capacity (table_bytes); the struct holds their addresses.
+// LDS pointers (address space 3): accesses through them compile to ds_*
+// instructions, where generic pointers would take the slower flat path.
+#define YABT_LDS __attribute__((address_space(3)))
+
 struct Table {
-    float gain[MAX_LEAVES];
-    int16_t pend[MAX_LEAVES];            // computed split, -1: none
-    int16_t src[MAX_LEAVES];             // origin
-    int16_t node[MAX_LEAVES];            // node id; while planning: the entry's split after the round
-    uint8_t moved[MAX_LEAVES];           // while planning: the entry no longer holds the committed leaf
-    float cgain[MAX_PEND][2];            // PendSum, per computed split
-    int16_t cpend[MAX_PEND][2];
-    int16_t commit_p[MAX_LEAVES];        // this controller's commits: split, parent node
-    int16_t commit_nid[MAX_LEAVES];
-    int16_t plan_src[KMAX];              // this round's splits: origin
+    YABT_LDS float* gain;                // [L]
+    YABT_LDS int16_t* pend;              // [L] computed split, -1: none
+    YABT_LDS int16_t* src;               // [L] origin
+    YABT_LDS int16_t* node;              // [L] node id (the committed table)
+    YABT_LDS float (*cgain)[2];          // [pend_cap] PendSum, per computed split
+    YABT_LDS int16_t (*cpend)[2];        // [pend_cap]
+    YABT_LDS int16_t* corigin;           // [pend_cap]
+    YABT_LDS uint8_t* ccommit;           // [pend_cap]
+    YABT_LDS float* ckey;                // [pend_cap] while planning: key of the split's node (+inf: not known)
+    YABT_LDS float* cbud;                // [pend_cap] while planning: that key where the split counts for the budget
+    YABT_LDS float* ckand;               // [L + 2 pend_cap] while planning: the candidates' keys
+    YABT_LDS int16_t* commit_p;          // [L] this controller's commits: split, parent node
+    YABT_LDS int16_t* commit_nid;        // [L]
+    YABT_LDS int16_t* plan_src;          // [KMAX] this round's splits: origin
+    YABT_LDS float* root_gain;           // the root's table gain and computed split
+    YABT_LDS int32_t* root_pend;
 };
+
+// Carve of the controller's LDS at `base` (null: size only).
+__host__ __device__ inline size_t table_carve(char* base, int L, int pend_cap, Table* T) {
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        off = (off + 15) / 16 * 16;
+        char* p = base ? base + off : nullptr;
+        off += bytes;
+        return p;
+    };
+    char* gain = take(sizeof(float) * L);
+    char* cgain = take(sizeof(float) * 2 * pend_cap);
+    char* ckey = take(sizeof(float) * pend_cap);
+    char* cbud = take(sizeof(float) * pend_cap);
+    char* ckand = take(sizeof(float) * (L + 2 * (size_t)pend_cap));
+    char* root_gain = take(sizeof(float));
+    char* root_pend = take(sizeof(int32_t));
+    char* pend = take(sizeof(int16_t) * L);
+    char* src = take(sizeof(int16_t) * L);
+    char* node = take(sizeof(int16_t) * L);
+    char* cpend = take(sizeof(int16_t) * 2 * pend_cap);
+    char* corigin = take(sizeof(int16_t) * pend_cap);
+    char* commit_p = take(sizeof(int16_t) * L);
+    char* commit_nid = take(sizeof(int16_t) * L);
+    char* plan_src = take(sizeof(int16_t) * KMAX);
+    char* ccommit = take(pend_cap);
+#if defined(__HIP_DEVICE_COMPILE__)
+    if (T) {
+        T->gain = (YABT_LDS float*)gain;
+        T->cgain = (YABT_LDS float(*)[2])cgain;
+        T->ckey = (YABT_LDS float*)ckey;
+        T->cbud = (YABT_LDS float*)cbud;
+        T->ckand = (YABT_LDS float*)ckand;
+        T->root_gain = (YABT_LDS float*)root_gain;
+        T->root_pend = (YABT_LDS int32_t*)root_pend;
+        T->pend = (YABT_LDS int16_t*)pend;
+        T->src = (YABT_LDS int16_t*)src;
+        T->node = (YABT_LDS int16_t*)node;
+        T->cpend = (YABT_LDS int16_t(*)[2])cpend;
+        T->corigin = (YABT_LDS int16_t*)corigin;
+        T->commit_p = (YABT_LDS int16_t*)commit_p;
+        T->commit_nid = (YABT_LDS int16_t*)commit_nid;
+        T->plan_src = (YABT_LDS int16_t*)plan_src;
+        T->ccommit = (YABT_LDS uint8_t*)ccommit;
+    }
+#else
+    (void)T;
+#endif
+    return (off + 15) / 16 * 16;
+}
+
+// wave_table_argmax over an LDS array.
+__device__ __forceinline__ int wave_table_argmax(const YABT_LDS float* s_gain, int na, int lane) {
+    float key = 0.0f;
+    int idx = INT_MAX;
+    constexpr int U = 4;
+    for (int a0 = lane; a0 < na; a0 += U * WAVE) {
+        float g[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int a = a0 + u * WAVE;
+            g[u] = a < na ? s_gain[a] : -INFINITY;
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            if (g[u] > key) {
+                key = g[u];
+                idx = a0 + u * WAVE;
+            }
+        }
+    }
+    const float m = wave_max_f32(key);
+    if (!(m > 0.0f)) return -1;
+    return wave_min_i32(key == m ? idx : INT_MAX);
+}
+
+// Table gain and computed split of the leaf with origin src.
+__device__ __forceinline__ float gain_of(const Table& T, int src) {
+    return src < 0 ? *T.root_gain : T.cgain[src >> 1][src & 1];
+}
+__device__ __forceinline__ int pend_of(const Table& T, int src) {
+    return src < 0 ? *T.root_pend : (int)T.cpend[src >> 1][src & 1];
+}
 
 // Node arrays of commit i (split p of node nid, children nl, nl + 1); the
 // parent's value is cleared afterwards (it may be a child of this batch).
@@ -487,13 +586,30 @@ __device__ __forceinline__ void write_commit(const Args& A, int p, int nid, int 
     A.value[nr] = node_value(tr, A.q, A.lr, A.lam);
     P.child_node[0] = nl;
     P.child_node[1] = nr;
+    A.psum[p].committed = 1;
 }
 
-// The controller, one wave: T holds the table (nn nodes, na leaves) and the
-// np computed splits' children.  Replay cgrow's leaf table over the computed
-// splits, store it, plan the next round (or finish the tree), publish.
+// The controller, one wave: T holds cgrow's leaf table as the previous
+// round's commits left it (nn nodes, na leaves, gains and computed splits
+// filled in from the origins) and the np computed splits' children.  Replay
+// cgrow's leaf table over the computed splits, store it, plan the next round
+// (or finish the tree), publish.
 // root: the root's record while the root is an uncomputed leaf (the first
 // controller), else null.
+//
+// Planning chooses the leaves whose splits the next round computes.  cgrow's
+// coming pops, run ahead of the commits with every computed split expanded,
+// come in the order of a key: the minimum of the gains on a leaf's path from
+// the committed leaf it hangs from (a child enters the table only when its
+// parent is popped, and the table always pops its maximum).  So the round
+// takes `best` -- the leaf the commits stopped at, cgrow's next split -- and
+// then the uncomputed leaves of largest key (committed leaves without a
+// computed split, uncomputed children of uncommitted computed splits) while
+// the leaves the run-ahead would hold at that pop (the committed ones, one
+// more per computed split of larger key, one per leaf taken) fit the budget.
+// Ties in key may be ordered otherwise than cgrow's table: the plan decides
+// only which splits are computed when, never the tree (the commits replay
+// cgrow's table exactly), and the split the commits wait for is always taken.
 __device__ void control(const Args& A, Table& T, int nn, int na, int np, const ScanRec* root, int lane) {
     State* st = A.st;
     const int L = A.max_leaves;
@@ -505,6 +621,7 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
         if (best < 0 || T.pend[best] < 0) break;
         const int p = T.pend[best];
         if (lane == 0) {
+            T.ccommit[p] = 1;
             T.commit_p[ncm] = (int16_t)p;
             T.commit_nid[ncm] = T.node[best];
             // left child replaces the split leaf, right child is appended
@@ -528,56 +645,88 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
     for (int i = lane; i < ncm; i += WAVE) write_commit(A, T.commit_p[i], T.commit_nid[i], nn0 + 2 * i);
     __threadfence();
     for (int i = lane; i < ncm; i += WAVE) A.value[T.commit_nid[i]] = 0.0f;
-    // store the table; T.node then holds each entry's split after planning
+    // store the committed table
     for (int a = lane; a < na; a += WAVE) {
-        A.gains[a] = T.gain[a];
         A.leaf_src[a] = T.src[a];
         A.leaf_node[a] = T.node[a];
-        T.node[a] = T.pend[a];
-        T.moved[a] = 0;
     }
-    wave_sync();
     int status = 0, j = 0;
     const int np0 = np;
     if (best >= 0) {
-        // plan: the table run ahead; entry `best` comes first
-        int nas = na, nls = na;
-        while (nls + j < L && j < KMAX) {
-            const int a = wave_table_argmax(T.gain, nas, lane);
-            if (a < 0) break;
+        // keys of the uncommitted computed splits' nodes: a committed leaf's
+        // split takes the leaf's gain, then (index order: a split's parent
+        // split has a lower index) a split below an uncommitted split q takes
+        // min(key of q, the child's gain)
+        for (int p = lane; p < np0; p += WAVE) T.ckey[p] = INFINITY;
+        wave_sync();
+        for (int a = lane; a < na; a += WAVE) {
             const int p = T.pend[a];
-            if (p >= 0) {
-                // a computed split: its children take its place
-                if (lane == 0) {
-                    T.gain[a] = T.cgain[p][0];
-                    T.pend[a] = T.cpend[p][0];
-                    T.src[a] = (int16_t)(2 * p);
-                    T.moved[a] = 1;
-                    T.gain[nas] = T.cgain[p][1];
-                    T.pend[nas] = T.cpend[p][1];
-                    T.src[nas] = (int16_t)(2 * p + 1);
-                    T.moved[nas] = 1;
+            if (p >= 0) T.ckey[p] = T.gain[a];
+        }
+        wave_sync();
+        for (int c0 = 0; c0 < np0; c0 += WAVE) {
+            const int p = c0 + lane;
+            for (;;) {
+                bool moved = false;
+                if (p < np0 && !T.ccommit[p] && T.ckey[p] == INFINITY) {
+                    const int o = T.corigin[p];
+                    const float kq = o >= 0 ? T.ckey[o >> 1] : INFINITY;
+                    if (o >= 0 && !T.ccommit[o >> 1] && kq != INFINITY) {
+                        T.ckey[p] = fminf(kq, T.cgain[o >> 1][o & 1]);
+                        moved = true;
+                    }
                 }
-                ++nas;
-                ++nls;
-            } else {
-                // Pend capacity: every controller may need one for the leaf
-                // it is blocked on, at most L - na more; extras keep
-                // np + L - na <= pend_cap - 1 (so the first, j == 0, fits)
-                if (np >= A.pend_cap) {
-                    status = -5;
-                    break;
-                }
-                if (j > 0 && np + L - na > A.pend_cap - 1) break;
-                if (lane == 0) {
-                    T.plan_src[j] = T.src[a];
-                    if (!T.moved[a]) T.node[a] = (int16_t)np;
-                    T.gain[a] = -INFINITY;
-                }
-                ++np;
-                ++j;
+                wave_sync();
+                if (__ballot(moved) == 0) break;
             }
+        }
+        // the candidates' keys (-inf: not a candidate): leaf a at a, child c
+        // of split p at na + 2 p + c; and each uncommitted computed split's
+        // key, where it adds a leaf to the run-ahead (the budget)
+        const int ncand = na + 2 * np0;
+        for (int a = lane; a < na; a += WAVE) T.ckand[a] = (T.pend[a] < 0 && a != best) ? T.gain[a] : -INFINITY;
+        for (int p = lane; p < np0; p += WAVE) {
+            const float kp = T.ckey[p];
+            const bool live = !T.ccommit[p] && kp != INFINITY;
+            T.cbud[p] = live ? kp : -INFINITY;
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+                T.ckand[na + 2 * p + c] = (live && T.cpend[p][c] == -1) ? fminf(kp, T.cgain[p][c]) : -INFINITY;
+        }
+        wave_sync();
+        // take best, then the largest keys (the lowest candidate on ties)
+        int cand = best;
+        for (;;) {
+            // Pend capacity: every controller may need one for the leaf it is
+            // blocked on, at most L - na more; extras keep np + L - na <=
+            // pend_cap - 1 (so the first, j == 0, fits)
+            if (np >= A.pend_cap) {
+                status = -5;
+                break;
+            }
+            if (j > 0 && np + L - na > A.pend_cap - 1) break;
+            if (lane == 0) {
+                T.plan_src[j] = cand < na ? T.src[cand] : (int16_t)(cand - na);
+                T.ckand[cand] = -INFINITY;
+            }
+            ++np;
+            ++j;
             wave_sync();
+            if (j >= KMAX) break;
+            cand = wave_table_argmax(T.ckand, ncand, lane);
+            if (cand < 0) break;
+            const float key = T.ckand[cand];
+            // the budget: leaves of the run-ahead when it pops this one
+            int e = 0;
+            for (int p0 = lane; p0 < np0; p0 += 4 * WAVE) {
+                float k[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) k[u] = p0 + u * WAVE < np0 ? T.cbud[p0 + u * WAVE] : -INFINITY;
+#pragma unroll
+                for (int u = 0; u < 4; ++u) e += k[u] >= key ? 1 : 0;
+            }
+            e = wave_sum<int>(e);
+            if (na + e + j >= L) break;
         }
     }
     // this round's splits, one per lane
@@ -621,13 +770,16 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
         PendSum S;
         S.gain[0] = S.gain[1] = -INFINITY;
         S.child_pend[0] = S.child_pend[1] = -1;
+        S.origin = (int16_t)src;
+        S.committed = 0;
         A.psum[p] = S;
         st->round_pend[lane] = p;
-        // the split's parent split names it (a committed leaf's entry too,
-        // through the leaf table, below)
+        // the split's parent split names it (the root's: st->root_pend)
         if (src >= 0) {
             A.pend[src >> 1].child_pend[src & 1] = p;
-            A.psum[src >> 1].child_pend[src & 1] = p;
+            A.psum[src >> 1].child_pend[src & 1] = (int16_t)p;
+        } else {
+            st->root_pend = p;
         }
     }
     tiles = wave_incl_scan<int64_t>(tiles, lane);
@@ -645,7 +797,6 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
             for (int c = lane; c < A.F; c += WAVE) out[c] = (c == fi) ? (uint8_t)1 : (pp ? pp[c] : (uint8_t)0);
         }
     }
-    for (int a = lane; a < na; a += WAVE) A.leaf_pend[a] = T.node[a];
     const int done = (status < 0 || j == 0) ? 1 : 0;
     if (lane == 0) {
         st->n_nodes = nn;
@@ -778,7 +929,9 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
     if (threadIdx.x == 0) st->scan_ticket = 0;
 
     // ---- controller ----
-    __shared__ Table T;
+    extern __shared__ __align__(16) char s_table[];
+    Table T;
+    table_carve(s_table, A.max_leaves, A.pend_cap, &T);
     if (ROOT) {
         __shared__ ScanRec s_root;
         if (w != 0) return;
@@ -791,6 +944,9 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
             T.pend[0] = -1;
             T.src[0] = -1;
             T.node[0] = 0;
+            *T.root_gain = T.gain[0];
+            *T.root_pend = -1;
+            st->root_gain = T.gain[0];
         }
         wave_sync();
         control(A, T, 1, 1, 0, &s_root, lane);
@@ -808,8 +964,6 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
         const int nn = st->n_nodes, na = st->n_leaves, np = st->n_pend;
         const int p0 = np - nr;                   // this round's splits: p0 .. np - 1
         for (int a = threadIdx.x; a < na; a += NT) {
-            T.gain[a] = A.gains[a];
-            T.pend[a] = (int16_t)A.leaf_pend[a];
             T.src[a] = (int16_t)A.leaf_src[a];
             T.node[a] = (int16_t)A.leaf_node[a];
         }
@@ -819,8 +973,20 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
                 T.cgain[p][0] = S.gain[0];
                 T.cgain[p][1] = S.gain[1];
             }
-            T.cpend[p][0] = (int16_t)S.child_pend[0];
-            T.cpend[p][1] = (int16_t)S.child_pend[1];
+            T.cpend[p][0] = S.child_pend[0];
+            T.cpend[p][1] = S.child_pend[1];
+            T.corigin[p] = S.origin;
+            T.ccommit[p] = (uint8_t)S.committed;
+        }
+        if (threadIdx.x == 0) {
+            *T.root_gain = st->root_gain;
+            *T.root_pend = st->root_pend;
+        }
+        __syncthreads();
+        // the committed leaves' gains and computed splits, from their origins
+        for (int a = threadIdx.x; a < na; a += NT) {
+            T.gain[a] = gain_of(T, T.src[a]);
+            T.pend[a] = (int16_t)pend_of(T, T.src[a]);
         }
         __syncthreads();
         // this round's children's gains, kept for later controllers
@@ -977,8 +1143,6 @@ size_t carve(char* base, int64_t n, int F, int max_leaves, Args* A) {
     a.rows = c.take<uint32_t>((size_t)2 * (size_t)a.rows_ld);
     a.hist = c.take<int64_t>((size_t)(pend_cap + 1) * 3 * (size_t)F * NB);
     a.pend_path = c.take<uint8_t>((size_t)pend_cap * (size_t)F);
-    a.gains = c.take<float>(N);
-    a.leaf_pend = c.take<int32_t>(N);
     a.leaf_src = c.take<int32_t>(N);
     a.leaf_node = c.take<int32_t>(N);
     a.pend = c.take<Pend>((size_t)pend_cap);
@@ -1085,7 +1249,8 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
                      A.hist, 1,
                      &A.st->done);
     const int scan_grid = (F + SCAN_FEATS - 1) / SCAN_FEATS;
-    k_scan<true><<<scan_grid, SCAN_FEATS * WAVE, 0, stream>>>(A);
+    const size_t table_lds = table_carve(nullptr, max_leaves, A.pend_cap, nullptr);
+    k_scan<true><<<scan_grid, SCAN_FEATS * WAVE, table_lds, stream>>>(A);
     int lrc = launch_status("yabt_grow_batched launch");
     if (lrc) return lrc;
     const int64_t slot_n = (int64_t)3 * F * NB;
@@ -1111,7 +1276,7 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
         k_part<<<PART_BLOCKS, SB, 0, stream>>>(bins_fm, ld_fm, n, A.st, A.pend, slot_n);
         k_gather<<<tiles * GCHUNKS, HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, A.q, A.dflt, A.st, A.pend,
                                                         wlog);
-        k_scan<false><<<dim3(scan_grid, KMAX), CT, 0, stream>>>(A);
+        k_scan<false><<<dim3(scan_grid, KMAX), CT, table_lds, stream>>>(A);
         if ((lrc = launch_status("yabt_grow_batched launch"))) return lrc;
     }
     if (out_leaf_of_row && n > 0) {
