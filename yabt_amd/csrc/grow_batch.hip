@@ -63,7 +63,6 @@ constexpr int CT = 2 * SCAN_FEATS * WAVE;        // threads of a split-scan bloc
 constexpr int LOOKAHEAD = 3;                     // rounds the host keeps in flight
 constexpr int MAX_LEAVES = 1024;                 // leaf table held in the controller's LDS
 constexpr int PEND_PER_LEAF = 3;                 // computed splits per leaf of the budget, at most
-constexpr int MAX_PEND = PEND_PER_LEAF * MAX_LEAVES + KMAX;
 constexpr int LEAF_CHUNK = 8192;                 // rows per leaf-id block
 constexpr int LEAF_PLAN = 1024;                  // threads of the leaf-id planning block
 
@@ -331,26 +330,20 @@ __global__ void __launch_bounds__(HBLOCK) k_gather(const uint8_t* __restrict__ b
         const int64_t lo = P.build_left ? P.s : P.mid, hi = P.build_left ? P.mid : P.e;
         const uint32_t* rows = P.dst;
         int64_t* out = P.new_hist;
-        if (wlog >= 0) {
-            if (no_h) {
-                if (dflt)
-                    hist_gather_packed<false, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi,
-                                                    out, wlog, tile, chunk);
-                else
-                    hist_gather_packed<false, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi,
-                                                     out, wlog, tile, chunk);
-            } else {
-                if (dflt)
-                    hist_gather_packed<true, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi,
-                                                   out, wlog, tile, chunk);
-                else
-                    hist_gather_packed<true, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi,
-                                                    out, wlog, tile, chunk);
-            }
-        } else if (no_h) {
-            hist_gather_body<false>(L.u, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out, tile, chunk);
+        if (no_h) {
+            if (dflt)
+                hist_gather_packed<false, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out,
+                                                wlog, tile, chunk);
+            else
+                hist_gather_packed<false, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out,
+                                                 wlog, tile, chunk);
         } else {
-            hist_gather_body<true>(L.u, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out, tile, chunk);
+            if (dflt)
+                hist_gather_packed<true, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out,
+                                               wlog, tile, chunk);
+            else
+                hist_gather_packed<true, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out,
+                                                wlog, tile, chunk);
         }
         __syncthreads();   // the next unit clears the LDS histogram
     }
@@ -529,6 +522,9 @@ __host__ __device__ inline size_t table_carve(char* base, int L, int pend_cap, T
     }
 #else
     (void)T;
+    for (char* p : {gain, cgain, ckey, cbud, ckand, root_gain, root_pend, pend, src, node, cpend, corigin, commit_p,
+                    commit_nid, plan_src, ccommit})
+        (void)p;
 #endif
     return (off + 15) / 16 * 16;
 }

@@ -1,16 +1,19 @@
 // Node-histogram kernels (exact int64 fixed point), shared by the grower and
 // the stand-alone entry points.
 //
-// Layout: a block owns a tile of HFL = 16 features and a chunk of rows.  In a
-// wave, lane = 16 * q + fl handles feature f0 + fl for row group q (4 row
-// groups x 16 rows = 64 rows per wave step), so the 64 lanes of every LDS
-// atomic touch 16 different features x 4 rows.  The LDS histogram is laid out
-// [bin][feature] (entry bin * 16 + fl), which keeps each atomic instruction
-// free of bank conflicts whatever the bin values are; a row-per-lane layout
-// sends all 64 lanes of an instruction to random bins of one feature.
-//
-// Each row's g and h are loaded and quantised once (one row per lane) and
-// handed to the 16 lanes of its row group with DPP row_newbcast.
+// A block owns a tile of HFL = 16 features and a chunk of rows; its LDS
+// histogram is laid out [bin][feature] (cell bin * 16 + fl).  An LDS atomic
+// instruction of a wave is processed a quarter wave at a time, and every
+// layout below sends the 16 lanes of a quarter wave to 16 different features
+// (16 different bank pairs) whatever the bins are; a row-per-lane layout
+// without that would send 64 lanes to random bins of one feature.
+//   * streaming root (feature-major bins): lane 16 q + fl handles feature
+//     f0 + fl for row group q, loads 16 consecutive bins of its feature with
+//     one 16-byte load, and gets each row's words from the lane that loaded
+//     them with DPP row_newbcast;
+//   * gathered children (row-major bins): each lane takes one row, loads its
+//     16 bins of the tile with one 16-byte load, and rotates them by lane % 16
+//     so that its J-th add goes to feature (J + lane) % 16.
 //
 // Optional skips, both exact because the sums are integers:
 //   * dflt[f] (may be NULL): rows whose bin equals dflt[f] are not added; the
@@ -36,39 +39,6 @@ struct HistLds {
     unsigned long long h[NB * HFL];
     uint32_t c[NB * HFL];
 };
-
-template <bool HCH>
-__device__ __forceinline__ void hist_clear(HistLds& L) {
-    for (int i = threadIdx.x; i < NB * HFL; i += HBLOCK) {
-        L.g[i] = 0;
-        if (HCH) L.h[i] = 0;
-        L.c[i] = 0;
-    }
-}
-
-// Add the block's histogram into out[3][F][256] (entries that received no row
-// are skipped).
-template <bool HCH>
-__device__ __forceinline__ void hist_flush(HistLds& L, int64_t* out, int F, int f0) {
-    const size_t plane = (size_t)F * NB;
-    for (int i = threadIdx.x; i < NB * HFL; i += HBLOCK) {
-        const int f = f0 + (i % HFL);
-        const uint32_t c = L.c[i];
-        if (f >= F || c == 0) continue;
-        const size_t at = (size_t)f * NB + (size_t)(i / HFL);
-        atomicAdd((unsigned long long*)(out + at), L.g[i]);
-        if (HCH) atomicAdd((unsigned long long*)(out + plane + at), L.h[i]);
-        atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)c);
-    }
-}
-
-template <bool HCH>
-__device__ __forceinline__ void hist_add(HistLds& L, int b, int fl, uint64_t g, uint64_t h) {
-    const int at = b * HFL + fl;
-    atomicAdd(&L.g[at], (unsigned long long)g);
-    if (HCH) atomicAdd(&L.h[at], (unsigned long long)h);
-    atomicAdd(&L.c[at], 1u);
-}
 
 // Rows per block chunk for the streaming kernel: about two resident blocks
 // per CU on 256 CUs, chunks a multiple of 8 so that all tiles of a row chunk
@@ -140,13 +110,13 @@ __device__ __forceinline__ void flush_cells(HistLds& T, const uint64_t (&g)[HENT
     }
 }
 
-// log2 of the packing window for n rows, or -1 when a window would be
-// shorter than one block step (then the three-word layout is used).
+// log2 of the packing window of the gathered histograms: windows of 2^16
+// rows.  With hist_shift's |q| <= 2^19 a window's sum of q stays below 2^35
+// and its count below 2^17 = 2^cb, cb = 17, so (sum q) << cb + count is exact
+// in 64 bits whatever n is.
 __host__ __device__ inline int pack_window_log2(int64_t n) {
-    int k = 0;
-    while (k < 62 && ((int64_t)1 << k) < n) ++k;
-    const int w = (k + 1) / 2;
-    return w >= 10 ? (w > 16 ? 16 : w) : -1;   // 2^10 rows = one block step
+    (void)n;
+    return 16;
 }
 
 // LDS of the streaming root histogram: 256 bins x 32 words of 8 bytes, of
@@ -521,87 +491,36 @@ __host__ __device__ inline int gather_chunks(int64_t m) {
     return (int)(c < GATHER_MAX_CHUNKS ? c : GATHER_MAX_CHUNKS);
 }
 
-// Histogram of the rows listed at rows[lo:hi], bins gathered from the
-// row-major copy: chunk `chunk` of the node's rows for features
-// [16 tile, 16 tile + 16).  A node uses gather_chunks(m) chunks; other chunk
-// numbers return at once.
-// Each wave loads the row ids, g and h of its next 64 rows one step ahead, so
-// the dependent row-id -> g/h loads overlap the LDS clear and the adds.
-template <bool HCH>
-__device__ __forceinline__ void hist_gather_body(HistLds& L, const uint8_t* __restrict__ bins_rm, int64_t ld,
-                                                 const float* __restrict__ grad, const float* __restrict__ hess,
-                                                 int F, double scg, double sch, const int32_t* __restrict__ dflt,
-                                                 const uint32_t* __restrict__ rows, int64_t jlo, int64_t jhi,
-                                                 int64_t* out, int tile, int chunk) {
-    const int f0 = tile * HFL;
-    const int64_t m = jhi - jlo;
-    if (f0 >= F || m <= 0) return;
-    const int nch = gather_chunks(m);
-    if (chunk >= nch) return;
-    const int64_t per = ((m + nch - 1) / nch + WAVE - 1) / WAVE * WAVE;
-    const int64_t lo = jlo + (int64_t)chunk * per, hi = min(jhi, lo + per);
-    if (lo >= hi) return;
-    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
-    const int fl = lane & (HFL - 1), rg = lane / HFL;
-    const int f = f0 + fl;
-    const bool fok = f < F;
-    const int d = (fok && dflt) ? dflt[f] : -1;
-    int64_t i0 = lo + (int64_t)wave * WAVE;
-    uint32_t r = 0;
-    float gx = 0.0f, hx = 0.0f;
-    if (i0 + lane < hi) {
-        r = rows[i0 + lane];
-        gx = grad[r];
-        if (HCH) hx = hess[r];
-    }
-    hist_clear<HCH>(L);
-    __syncthreads();
-    const uint8_t* fbase = bins_rm + f0 + (fok ? fl : 0);
-    for (; i0 < hi; i0 += HSTEP) {
-        const uint64_t gq = (uint64_t)quantise_node(gx, scg), hq = HCH ? (uint64_t)quantise_node(hx, sch) : 0;
-        const int nv = (int)min((int64_t)HFL, max((int64_t)0, hi - (i0 + HFL * rg)));
-        int bj[HFL];
-#define YABT_GATHER_LOAD(J)                                                       \
-        {                                                                         \
-            const uint32_t rj = row_bcast32<J>(r);                                \
-            bj[J] = (fok && (J) < nv) ? (int)fbase[(size_t)rj * ld] : -1;         \
-        }
-        YABT_GATHER_LOAD(0) YABT_GATHER_LOAD(1) YABT_GATHER_LOAD(2) YABT_GATHER_LOAD(3)
-        YABT_GATHER_LOAD(4) YABT_GATHER_LOAD(5) YABT_GATHER_LOAD(6) YABT_GATHER_LOAD(7)
-        YABT_GATHER_LOAD(8) YABT_GATHER_LOAD(9) YABT_GATHER_LOAD(10) YABT_GATHER_LOAD(11)
-        YABT_GATHER_LOAD(12) YABT_GATHER_LOAD(13) YABT_GATHER_LOAD(14) YABT_GATHER_LOAD(15)
-#undef YABT_GATHER_LOAD
-        // next step's rows
-        const int64_t in = i0 + HSTEP + lane;
-        uint32_t rn = 0;
-        float gn = 0.0f, hn = 0.0f;
-        if (in < hi) {
-            rn = rows[in];
-            gn = grad[rn];
-            if (HCH) hn = hess[rn];
-        }
-#define YABT_GATHER_ADD(J)                                                        \
-        {                                                                         \
-            const uint64_t gj = row_bcast64<J>(gq), hj = HCH ? row_bcast64<J>(hq) : 0; \
-            if (bj[J] >= 0 && bj[J] != d) hist_add<HCH>(L, bj[J], fl, gj, hj);    \
-        }
-        YABT_GATHER_ADD(0) YABT_GATHER_ADD(1) YABT_GATHER_ADD(2) YABT_GATHER_ADD(3)
-        YABT_GATHER_ADD(4) YABT_GATHER_ADD(5) YABT_GATHER_ADD(6) YABT_GATHER_ADD(7)
-        YABT_GATHER_ADD(8) YABT_GATHER_ADD(9) YABT_GATHER_ADD(10) YABT_GATHER_ADD(11)
-        YABT_GATHER_ADD(12) YABT_GATHER_ADD(13) YABT_GATHER_ADD(14) YABT_GATHER_ADD(15)
-#undef YABT_GATHER_ADD
-        r = rn;
-        gx = gn;
-        hx = hn;
-    }
-    __syncthreads();
-    hist_flush<HCH>(L, out, F, f0);
+// The 16 bytes of v rotated by k (0..15): byte j of the result is byte
+// (j + k) & 15 of v.
+__device__ __forceinline__ uint4 rotate_bytes16(uint4 v, int k) {
+    const bool d1 = (k >> 2) & 1, d2 = (k >> 3) & 1;
+    const uint32_t b0 = d1 ? v.y : v.x, b1 = d1 ? v.z : v.y, b2 = d1 ? v.w : v.z, b3 = d1 ? v.x : v.w;
+    const uint32_t c0 = d2 ? b2 : b0, c1 = d2 ? b3 : b1, c2 = d2 ? b0 : b2, c3 = d2 ? b1 : b3;
+    const uint32_t r = (uint32_t)(k & 3);
+    return make_uint4(__builtin_amdgcn_alignbyte(c1, c0, r), __builtin_amdgcn_alignbyte(c2, c1, r),
+                      __builtin_amdgcn_alignbyte(c3, c2, r), __builtin_amdgcn_alignbyte(c0, c3, r));
 }
 
-// Packed-word form of hist_gather_body (see hist_root_packed), with a
-// three-stage software pipeline per wave: at step s the wave adds step s,
-// loads g, h and the bins of step s + 1 (its row ids are already in
-// registers) and the row ids of step s + 2.
+// Histogram of the rows listed at rows[jlo:jhi] over features [16 tile,
+// 16 tile + 16), bins gathered from the row-major copy: chunk `chunk` of the
+// node's rows (a node uses gather_chunks(m) chunks; other chunk numbers
+// return at once), with the packed count of hist_root's kind: the count rides
+// in the low cb = wlog + 1 bits of one 64-bit LDS word, (q << cb) + 1 per row
+// (q = q(h), or q(g) when every h is equal), and each window of 2^wlog rows
+// is unpacked into registers; with the h channel q(g) has a word of its own.
+// Two 64-bit LDS atomics per update (one without the h channel).
+//
+// Each lane takes one row per step: its row id, its g and h, and the 16
+// bytes of its row's bins for the tile with one 16-byte load, so each lane
+// adds its own row's words (no broadcast).  The bytes are rotated by
+// k = lane % 16, and the lane's J-th add goes to feature (J + k) % 16: the 16
+// lanes of a quarter wave then hit 16 different features (bank pairs) at
+// every add, whatever the bins are.  Features >= F are the row-major copy's
+// zero padding, added into LDS columns the flush ignores; rows past the chunk
+// read row hi - 1 and add zero words.  A three-stage pipeline per wave: at
+// step s the wave adds step s, loads g, h and the bins of step s + 1 (its row
+// ids are in registers) and the row ids of step s + 2.
 template <bool HCH, bool SKIP>
 __device__ __forceinline__ void hist_gather_packed(HistLdsP& L, const uint8_t* __restrict__ bins_rm, int64_t ld,
                                                    const float* __restrict__ grad, const float* __restrict__ hess,
@@ -617,21 +536,36 @@ __device__ __forceinline__ void hist_gather_packed(HistLdsP& L, const uint8_t* _
     const int64_t lo = jlo + (int64_t)chunk * per, hi = min(jhi, lo + per);
     if (lo >= hi) return;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
-    const int fl = lane & (HFL - 1), rg = lane / HFL;
-    const int f = f0 + fl;
-    const bool fok = f < F;
-    const int d = (SKIP && fok) ? dflt[f] : -1;
+    int k = lane & (HFL - 1);
+    // k is opaque from here: values derived from it are computed per call, not
+    // hoisted out of a caller's loop over units and kept live across it
+    asm volatile("" : "+v"(k));
+    // with SKIP: byte j of dv is the default bin of feature f0 + (j + k) % 16,
+    // bit j of dmask says that feature has one
+    uint4 dv = make_uint4(0, 0, 0, 0);
+    uint32_t dmask = 0;
+    if (SKIP) {
+        uint32_t w[4] = {0, 0, 0, 0};
+#pragma unroll
+        for (int j = 0; j < HFL; ++j) {
+            const int fj = f0 + ((j + k) & (HFL - 1));
+            const int d = fj < F ? dflt[fj] : -1;
+            if (d >= 0) {
+                w[j >> 2] |= (uint32_t)d << (8 * (j & 3));
+                dmask |= 1u << j;
+            }
+        }
+        dv = make_uint4(w[0], w[1], w[2], w[3]);
+    }
     const int cb = wlog + 1;
     const uint64_t cmask = ((uint64_t)1 << cb) - 1;
     const int64_t win_steps = (int64_t)1 << (wlog - 10);
-    // lanes of features >= F gather feature f0's byte and add into their own
-    // LDS columns, which the flush ignores
-    const uint8_t* fbase = bins_rm + f0 + (fok ? fl : 0);
+    const uint8_t* tb = bins_rm + f0;                // a row's 16 bytes of the tile: tb + r * ld (ld % 16 == 0)
     const int64_t w0 = lo + (int64_t)wave * WAVE;   // this wave's rows at step s: w0 + s * HSTEP + [0, 64)
+    auto row_at = [&](int64_t i) { return rows[min(i, hi - 1)]; };
     // stage inputs: row ids of steps 0 and 1, g/h/bins of step 0
-    uint32_t r0 = 0, r1 = 0;
-    if (w0 + lane < hi) r0 = rows[w0 + lane];
-    if (w0 + HSTEP + lane < hi) r1 = rows[w0 + HSTEP + lane];
+    const uint32_t r0 = row_at(w0 + lane);
+    uint32_t r1 = row_at(w0 + HSTEP + lane);
     for (int i = threadIdx.x; i < NB * HFL; i += HBLOCK) {
         if (HCH) L.g[i] = 0;
         L.p[i] = 0;
@@ -639,109 +573,64 @@ __device__ __forceinline__ void hist_gather_packed(HistLdsP& L, const uint8_t* _
     int64_t qa[HENT];
     uint32_t ca[HENT];
 #pragma unroll
-    for (int k = 0; k < HENT; ++k) {
-        qa[k] = 0;
-        ca[k] = 0;
+    for (int e = 0; e < HENT; ++e) {
+        qa[e] = 0;
+        ca[e] = 0;
     }
-    float gx = 0.0f, hx = 0.0f;
-    uint32_t bj[HFL];
-#define YABT_GATHER_BINS(J, R, BASE)                                             \
-    {                                                                            \
-        const uint32_t rj = row_bcast32<J>(R);                                   \
-        bj[J] = ((BASE) + HFL * rg + (J) < hi) ? (uint32_t)fbase[(size_t)rj * ld] : 0u; \
-    }
-    if (w0 + lane < hi) {
-        gx = grad[r0];
-        if (HCH) hx = hess[r0];
-    }
-    YABT_GATHER_BINS(0, r0, w0) YABT_GATHER_BINS(1, r0, w0) YABT_GATHER_BINS(2, r0, w0)
-    YABT_GATHER_BINS(3, r0, w0) YABT_GATHER_BINS(4, r0, w0) YABT_GATHER_BINS(5, r0, w0)
-    YABT_GATHER_BINS(6, r0, w0) YABT_GATHER_BINS(7, r0, w0) YABT_GATHER_BINS(8, r0, w0)
-    YABT_GATHER_BINS(9, r0, w0) YABT_GATHER_BINS(10, r0, w0) YABT_GATHER_BINS(11, r0, w0)
-    YABT_GATHER_BINS(12, r0, w0) YABT_GATHER_BINS(13, r0, w0) YABT_GATHER_BINS(14, r0, w0)
-    YABT_GATHER_BINS(15, r0, w0)
+    float gx = grad[r0], hx = HCH ? hess[r0] : 0.0f;
+    uint4 bv = *reinterpret_cast<const uint4*>(tb + (size_t)r0 * ld);
     __syncthreads();
     const int64_t steps = (hi - lo + HSTEP - 1) / HSTEP;   // the same in every wave: barriers below
     for (int64_t s = 0; s < steps; ++s) {
         const int64_t i0 = w0 + s * HSTEP, i1 = i0 + HSTEP, i2 = i1 + HSTEP;
-        // stage: row ids of step s + 2
-        uint32_t r2 = 0;
-        if (i2 + lane < hi) r2 = rows[i2 + lane];
-        // stage: g, h and bins of step s + 1
-        float gn = 0.0f, hn = 0.0f;
-        if (i1 + lane < hi) {
-            gn = grad[r1];
-            if (HCH) hn = hess[r1];
-        }
-        uint32_t bn[HFL];
-#define YABT_GATHER_NEXT(J)                                                      \
-        {                                                                        \
-            const uint32_t rj = row_bcast32<J>(r1);                              \
-            bn[J] = (i1 + HFL * rg + (J) < hi) ? (uint32_t)fbase[(size_t)rj * ld] : 0u; \
-        }
-        YABT_GATHER_NEXT(0) YABT_GATHER_NEXT(1) YABT_GATHER_NEXT(2) YABT_GATHER_NEXT(3)
-        YABT_GATHER_NEXT(4) YABT_GATHER_NEXT(5) YABT_GATHER_NEXT(6) YABT_GATHER_NEXT(7)
-        YABT_GATHER_NEXT(8) YABT_GATHER_NEXT(9) YABT_GATHER_NEXT(10) YABT_GATHER_NEXT(11)
-        YABT_GATHER_NEXT(12) YABT_GATHER_NEXT(13) YABT_GATHER_NEXT(14) YABT_GATHER_NEXT(15)
-#undef YABT_GATHER_NEXT
+        // stage: row ids of step s + 2; g, h and bins of step s + 1
+        const uint32_t r2 = row_at(i2 + lane);
+        const float gn = grad[r1], hn = HCH ? hess[r1] : 0.0f;
+        const uint4 bn = *reinterpret_cast<const uint4*>(tb + (size_t)r1 * ld);
         // step s
         const bool rok = i0 + lane < hi;
         const int64_t gq = rok ? quantise_node(gx, scg) : 0;
         const int64_t hq = (HCH && rok) ? quantise_node(hx, sch) : 0;
-        const uint64_t gw = HCH ? (uint64_t)gq : ((uint64_t)gq << cb) + 1;
-        const uint64_t pw = HCH ? ((uint64_t)hq << cb) + 1 : 0;
-#define YABT_GATHER_STEP(J, TAIL)                                                \
-        {                                                                        \
-            const uint64_t gj = row_bcast64<J>(gw);                              \
-            const uint64_t pj = HCH ? row_bcast64<J>(pw) : 0;                     \
-            const int b = (int)bj[J];                                            \
-            if ((!(TAIL) || (J) < nv) && (!SKIP || b != d)) {                    \
-                const int at = b * HFL + fl;                                     \
-                if (HCH) {                                                       \
-                    atomicAdd(&L.g[at], (unsigned long long)gj);                 \
-                    atomicAdd(&L.p[at], (unsigned long long)pj);                 \
-                } else {                                                         \
-                    atomicAdd(&L.p[at], (unsigned long long)gj);                 \
-                }                                                                \
-            }                                                                    \
+        const uint64_t one = rok ? 1 : 0;
+        const uint64_t gw = HCH ? (uint64_t)gq : ((uint64_t)gq << cb) + one;
+        const uint64_t pw = HCH ? ((uint64_t)hq << cb) + one : 0;
+        const uint4 rb = rotate_bytes16(bv, k);
+        const uint32_t wv[4] = {rb.x, rb.y, rb.z, rb.w};
+        const uint32_t dw[4] = {dv.x, dv.y, dv.z, dv.w};
+#pragma unroll
+        for (int J = 0; J < HFL; ++J) {
+            const uint32_t b = (wv[J >> 2] >> (8 * (J & 3))) & 0xffu;
+            const int at = (int)(b * HFL) + ((J + k) & (HFL - 1));
+            if (!SKIP || !((dmask >> J) & 1u) || b != ((dw[J >> 2] >> (8 * (J & 3))) & 0xffu)) {
+                if (HCH) {
+                    atomicAdd(&L.g[at], (unsigned long long)gw);
+                    atomicAdd(&L.p[at], (unsigned long long)pw);
+                } else {
+                    atomicAdd(&L.p[at], (unsigned long long)gw);
+                }
+            }
         }
-        if (i0 + WAVE <= hi) {   // wave-uniform: all 64 rows valid
-            constexpr int nv = HFL;
-            YABT_GATHER_STEP(0, 0) YABT_GATHER_STEP(1, 0) YABT_GATHER_STEP(2, 0) YABT_GATHER_STEP(3, 0)
-            YABT_GATHER_STEP(4, 0) YABT_GATHER_STEP(5, 0) YABT_GATHER_STEP(6, 0) YABT_GATHER_STEP(7, 0)
-            YABT_GATHER_STEP(8, 0) YABT_GATHER_STEP(9, 0) YABT_GATHER_STEP(10, 0) YABT_GATHER_STEP(11, 0)
-            YABT_GATHER_STEP(12, 0) YABT_GATHER_STEP(13, 0) YABT_GATHER_STEP(14, 0) YABT_GATHER_STEP(15, 0)
-        } else if (i0 < hi) {
-            const int nv = (int)min((int64_t)HFL, max((int64_t)0, hi - (i0 + HFL * rg)));
-            YABT_GATHER_STEP(0, 1) YABT_GATHER_STEP(1, 1) YABT_GATHER_STEP(2, 1) YABT_GATHER_STEP(3, 1)
-            YABT_GATHER_STEP(4, 1) YABT_GATHER_STEP(5, 1) YABT_GATHER_STEP(6, 1) YABT_GATHER_STEP(7, 1)
-            YABT_GATHER_STEP(8, 1) YABT_GATHER_STEP(9, 1) YABT_GATHER_STEP(10, 1) YABT_GATHER_STEP(11, 1)
-            YABT_GATHER_STEP(12, 1) YABT_GATHER_STEP(13, 1) YABT_GATHER_STEP(14, 1) YABT_GATHER_STEP(15, 1)
-        }
-#undef YABT_GATHER_STEP
         if ((s + 1) % win_steps == 0 || s + 1 == steps) {
             __syncthreads();
 #pragma unroll
-            for (int k = 0; k < HENT; ++k) {
-                const int i = threadIdx.x + k * HBLOCK;
+            for (int e = 0; e < HENT; ++e) {
+                const int i = threadIdx.x + e * HBLOCK;
                 const uint64_t v = L.p[i];
                 L.p[i] = 0;
                 const uint64_t c = v & cmask;
-                qa[k] += (int64_t)(v - c) >> cb;
-                ca[k] += (uint32_t)c;
+                qa[e] += (int64_t)(v - c) >> cb;
+                ca[e] += (uint32_t)c;
             }
             __syncthreads();
         }
         r1 = r2;
         gx = gn;
         hx = hn;
-#pragma unroll
-        for (int J = 0; J < HFL; ++J) bj[J] = bn[J];
+        bv = bn;
     }
-#undef YABT_GATHER_BINS
     uint64_t gv[HENT];
 #pragma unroll
-    for (int k = 0; k < HENT; ++k) gv[k] = HCH ? L.g[threadIdx.x + k * HBLOCK] : (uint64_t)qa[k];
+    for (int e = 0; e < HENT; ++e) gv[e] = HCH ? L.g[threadIdx.x + e * HBLOCK] : (uint64_t)qa[e];
     __syncthreads();   // every g cell read before the LDS is rewritten
     flush_cells<HCH>(*reinterpret_cast<HistLds*>(&L), gv, qa, ca, out, F, f0);
 }
@@ -765,26 +654,20 @@ static __global__ __attribute__((unused)) void __launch_bounds__(HBLOCK) k_hist_
         HistLds u;
         HistLdsP p;
     } L;
-    if (wlog >= 0) {
-        if (no_h) {
-            if (dflt)
-                hist_gather_packed<false, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo,
-                                                jb.hi, jb.out, wlog, tile, chunk);
-            else
-                hist_gather_packed<false, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo,
-                                                 jb.hi, jb.out, wlog, tile, chunk);
-        } else {
-            if (dflt)
-                hist_gather_packed<true, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo,
-                                               jb.hi, jb.out, wlog, tile, chunk);
-            else
-                hist_gather_packed<true, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo,
-                                                jb.hi, jb.out, wlog, tile, chunk);
-        }
-    } else if (no_h) {
-        hist_gather_body<false>(L.u, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi, jb.out, tile, chunk);
+    if (no_h) {
+        if (dflt)
+            hist_gather_packed<false, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi,
+                                            jb.out, wlog, tile, chunk);
+        else
+            hist_gather_packed<false, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi,
+                                             jb.out, wlog, tile, chunk);
     } else {
-        hist_gather_body<true>(L.u, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi, jb.out, tile, chunk);
+        if (dflt)
+            hist_gather_packed<true, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi,
+                                           jb.out, wlog, tile, chunk);
+        else
+            hist_gather_packed<true, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi,
+                                            jb.out, wlog, tile, chunk);
     }
 }
 
