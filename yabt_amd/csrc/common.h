@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include <climits>
+#include <type_traits>
 
 namespace yabt {
 
@@ -157,6 +158,28 @@ __device__ __forceinline__ int64_t wave_sum_i64(int64_t v) {
            readlane64((int64_t)u, 48);
 }
 
+__device__ __forceinline__ int32_t wave_sum_i32(int32_t v) {
+    v += (int32_t)dpp32<DPP_ROW_ROR + 8>((uint32_t)v);
+    v += (int32_t)dpp32<DPP_ROW_ROR + 4>((uint32_t)v);
+    v += (int32_t)dpp32<DPP_ROW_ROR + 2>((uint32_t)v);
+    v += (int32_t)dpp32<DPP_ROW_ROR + 1>((uint32_t)v);
+    return __builtin_amdgcn_readlane(v, 0) + __builtin_amdgcn_readlane(v, 16) + __builtin_amdgcn_readlane(v, 32) +
+           __builtin_amdgcn_readlane(v, 48);
+}
+
+// Inclusive prefix sum over the 64 lanes of a 32-bit integer (as the 64-bit
+// one above).
+__device__ __forceinline__ int32_t wave_incl_scan_i32(int32_t v, int lane) {
+    uint32_t u = (uint32_t)v;
+    u += dpp32<DPP_ROW_SHR + 1>(u);
+    u += dpp32<DPP_ROW_SHR + 2>(u);
+    u += dpp32<DPP_ROW_SHR + 4>(u);
+    u += dpp32<DPP_ROW_SHR + 8>(u);
+    const int32_t t0 = __builtin_amdgcn_readlane((int)u, 15), t1 = __builtin_amdgcn_readlane((int)u, 31),
+                  t2 = __builtin_amdgcn_readlane((int)u, 47);
+    return (int32_t)u + (lane >= 16 ? t0 : 0) + (lane >= 32 ? t1 : 0) + (lane >= 48 ? t2 : 0);
+}
+
 // Maximum / minimum over the 64 lanes, returned in every lane (row rotations
 // leave each row's result in all of its lanes, then the four rows combine).
 __device__ __forceinline__ float wave_max_f32(float v) {
@@ -190,11 +213,19 @@ __device__ __forceinline__ T wave_excl_scan(T v, int lane) {
     return incl - v;
 }
 
+// Sum over the wave: DPP for integers (exact in any order), a butterfly of
+// shuffles for floating point (its fixed order).
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
+    if constexpr (std::is_integral<T>::value && sizeof(T) == 4) {
+        return (T)wave_sum_i32((int32_t)v);
+    } else if constexpr (std::is_integral<T>::value && sizeof(T) == 8) {
+        return (T)wave_sum_i64((int64_t)v);
+    } else {
 #pragma unroll
-    for (int d = WAVE / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, WAVE);
-    return v;
+        for (int d = WAVE / 2; d > 0; d >>= 1) v += __shfl_xor(v, d, WAVE);
+        return v;
+    }
 }
 
 // Block-wide exclusive scan of one value per thread (NT threads).

@@ -58,7 +58,8 @@ constexpr int PART_TILE = SB * PART_IPT;
 constexpr int PART_BLOCKS = 1024;
 constexpr int SCAN_FEATS = 4;                    // features per scan block
 constexpr int KMAX = 16;                         // splits computed per round, at most
-constexpr int GCHUNKS = 64;                      // gather blocks per 16-feature tile
+constexpr int GBLOCKS = 256;                     // gather blocks of a launch, about (multiple of XCDS)
+constexpr int XCDS = 8;                          // dies of the device; blocks go to them in turn
 constexpr int CT = 2 * SCAN_FEATS * WAVE;        // threads of a split-scan block (the controller)
 constexpr int LOOKAHEAD = 3;                     // rounds the host keeps in flight
 constexpr int MAX_LEAVES = 1024;                 // leaf table held in the controller's LDS
@@ -78,7 +79,7 @@ struct Pend {
     uint32_t* dst;                       // the children's rows
     int64_t s, e, mid;
     int64_t tot[3], left[3];
-    int64_t* new_hist;                   // the built child's slot
+    int64_t pad2;
     unsigned long long placed;           // rows placed: left count in the low 32 bits, right in the high 32
     unsigned long long pad1;
     ScanRec child[2];                    // the children's best records (b = -1: none)
@@ -103,7 +104,9 @@ struct State {
     float root_gain;                     // the root's table gain
     int32_t round_pend[KMAX];            // this round's Pend entries
     int64_t tile_off[KMAX + 1];          // partition tiles of this round's splits, prefix sums
-    int32_t chunk_off[KMAX + 1];         // gather chunks of this round's built children, prefix sums
+    int32_t unit_off[KMAX + 1];          // gather units of this round's built children, prefix sums
+    int32_t pad3;
+    int64_t unit_rows;                   // rows per gather unit (a child's last unit: the rest)
 };
 
 // A run of final-leaf rows for the leaf-id pass: positions [lo, hi) of a row
@@ -148,6 +151,7 @@ struct Args {
     uint32_t* rows;                      // two lists of rows_ld row ids
     int64_t rows_ld;
     int64_t* hist;
+    int64_t* pieces;                     // gather_units(tiles) slots: one per gather unit
     uint8_t* pend_path;                  // (pend_cap, F) features on the path to each split's children
     int32_t* leaf_src;                   // cgrow's leaf table after the commits: each leaf's origin
     int32_t* leaf_node;                  // and node id (gains and computed splits follow from the origin)
@@ -220,17 +224,11 @@ __global__ void k_setup_finish(Args A) {
 // children's row list.  A tile reserves its places in both children with one
 // 64-bit atomic on the split's packed (left, right) count: a child holds at
 // most n < 2^32 rows, so the left half never carries into the right.  (The
-// order inside a child depends on the schedule, which no exact sum does.)  The blocks also
-// clear the round's new histogram slots, which the gather adds into.
+// order inside a child depends on the schedule, which no exact sum does.)
 __global__ void __launch_bounds__(SB) k_part(const uint8_t* __restrict__ bins_fm, int64_t ld, int64_t n, State* st,
-                                             Pend* pend, int64_t slot_n) {
+                                             Pend* pend) {
     const int32_t done = st->done, nr = st->n_round;
     if (done || nr == 0) return;
-    for (int64_t i = (int64_t)blockIdx.x * SB + threadIdx.x; i < (int64_t)nr * slot_n;
-         i += (int64_t)gridDim.x * SB) {
-        const int j = (int)(i / slot_n);
-        pend[st->round_pend[j]].new_hist[i - (int64_t)j * slot_n] = 0;
-    }
     const int64_t T = st->tile_off[nr];
     const int w = threadIdx.x / WAVE;
     __shared__ uint32_t s_cnt[SB / WAVE][2];
@@ -305,47 +303,67 @@ __global__ void __launch_bounds__(SB) k_part(const uint8_t* __restrict__ bins_fm
 // gather: the built child of every split of the round, (split, chunk) units
 // ---------------------------------------------------------------------------
 
-// Block (tile, u0) takes units u0, u0 + GCHUNKS, ... of the round's flattened
-// chunk list; each unit is one chunk of one built child (hist.h's gather
-// bodies), added into that split's new slot.
+// Gather units of a round, about: a multiple of XCDS near GBLOCKS / tiles,
+// so that one unit per tile fills the device once.
+__host__ __device__ inline int gather_target(int tiles) {
+    const int g = GBLOCKS / XCDS / tiles;
+    return XCDS * (g > 1 ? g : 1);
+}
+// Units a round may use, at most (blocks per tile of the gather launch).
+__host__ __device__ inline int gather_units(int tiles) { return gather_target(tiles) + KMAX; }
+
+// Rows per gather unit of a round of nr splits gathering R rows in all: whole
+// waves, and large enough that the splits' units (ceil(rows / unit_rows)
+// each, at most R / unit_rows + nr in all) stay within gather_target when it
+// exceeds nr, and within gather_units always.
+__host__ __device__ inline int64_t gather_unit_rows(int64_t R, int nr, int tiles) {
+    const int t = gather_target(tiles);
+    const int64_t d = t > nr ? t - nr : 1;
+    const int64_t per = ((R + d - 1) / d + WAVE - 1) / WAVE * WAVE;
+    return per > 0 ? per : WAVE;
+}
+
+// Each built child is cut into units of unit_rows rows (split j owns units
+// unit_off[j] .. unit_off[j + 1]); block (tile, u) stores the histogram of
+// unit u's rows in slot u of `pieces` -- no atomics, no clearing -- and the
+// scan adds up a child's units.  Block ids go to the XCDS dies in turn and
+// the blocks of one unit (every tile of the same rows) are numbered to land
+// on one die, sharing its L2 for the rows' bins, ids and g, h.
 __global__ void __launch_bounds__(HBLOCK) k_gather(const uint8_t* __restrict__ bins_rm, int64_t ld,
                                                    const float* __restrict__ grad, const float* __restrict__ hess,
                                                    int F, const Quant* q, const int32_t* __restrict__ dflt,
-                                                   const State* st, const Pend* pend, int wlog) {
+                                                   const State* st, const Pend* pend, int64_t* pieces, int wlog) {
     const int32_t done = st->done, nr = st->n_round;
     const double scg = q->scg, sch = q->sch;
     const bool no_h = q->const_h != 0;
     if (done || nr == 0) return;
-    __shared__ union {
-        HistLds u;
-        HistLdsP p;
-    } L;
-    const int tile = blockIdx.x / GCHUNKS;
-    const int C = st->chunk_off[nr];
-    for (int u = blockIdx.x % GCHUNKS; u < C; u += GCHUNKS) {
-        int j = 0;
-        while (j + 1 < nr && st->chunk_off[j + 1] <= u) ++j;
-        const Pend& P = pend[st->round_pend[j]];
-        const int chunk = u - st->chunk_off[j];
-        const int64_t lo = P.build_left ? P.s : P.mid, hi = P.build_left ? P.mid : P.e;
-        const uint32_t* rows = P.dst;
-        int64_t* out = P.new_hist;
-        if (no_h) {
-            if (dflt)
-                hist_gather_packed<false, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out,
-                                                wlog, tile, chunk);
-            else
-                hist_gather_packed<false, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out,
-                                                 wlog, tile, chunk);
-        } else {
-            if (dflt)
-                hist_gather_packed<true, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out,
-                                               wlog, tile, chunk);
-            else
-                hist_gather_packed<true, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out,
-                                                wlog, tile, chunk);
-        }
-        __syncthreads();   // the next unit clears the LDS histogram
+    // block id -> (unit, tile): die x = id % XCDS holds units x, x + XCDS, ...
+    const int tiles = (F + HFL - 1) / HFL;
+    const int x = blockIdx.x % XCDS, k = blockIdx.x / XCDS;
+    const int tile = k % tiles, unit = (k / tiles) * XCDS + x;
+    if (unit >= st->unit_off[nr]) return;
+    int j = 0;
+    while (j + 1 < nr && st->unit_off[j + 1] <= unit) ++j;
+    const Pend& P = pend[st->round_pend[j]];
+    const int64_t per = st->unit_rows;
+    const int64_t c_lo = P.build_left ? P.s : P.mid, c_hi = P.build_left ? P.mid : P.e;
+    const int64_t lo = c_lo + (int64_t)(unit - st->unit_off[j]) * per, hi = min(c_hi, lo + per);
+    int64_t* out = pieces + (size_t)unit * slot_elems(F);
+    __shared__ GatherLds L;
+    if (no_h) {
+        if (dflt)
+            hist_gather_rows<false, true, true>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, P.dst, lo, hi, out,
+                                                wlog, tile);
+        else
+            hist_gather_rows<false, false, true>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, P.dst, lo, hi, out,
+                                                 wlog, tile);
+    } else {
+        if (dflt)
+            hist_gather_rows<true, true, true>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, P.dst, lo, hi, out,
+                                               wlog, tile);
+        else
+            hist_gather_rows<true, false, true>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, P.dst, lo, hi, out,
+                                                wlog, tile);
     }
 }
 
@@ -402,15 +420,12 @@ __device__ __forceinline__ int wave_table_argmax(const float* s_gain, int na, in
     return wave_min_i32(key == m ? idx : INT_MAX);
 }
 
-// Inclusive prefix sum over the wave.
+// Inclusive prefix sum over the wave (32- or 64-bit integers).
 template <typename T>
 __device__ __forceinline__ T wave_incl_scan(T v, int lane) {
-#pragma unroll
-    for (int d = 1; d < WAVE; d <<= 1) {
-        const T o = __shfl_up(v, d, WAVE);
-        if (lane >= d) v += o;
-    }
-    return v;
+    static_assert(std::is_integral<T>::value && (sizeof(T) == 4 || sizeof(T) == 8), "integer scan");
+    if constexpr (sizeof(T) == 4) return (T)wave_incl_scan_i32((int32_t)v, lane);
+    else return (T)wave_incl_scan_i64((int64_t)v, lane);
 }
 
 // A leaf as a split candidate, from its origin (2 p + c, or -1: the root
@@ -726,8 +741,8 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
         }
     }
     // this round's splits, one per lane
-    int64_t tiles = 0;
-    int chunks = 0, f = -1, src = -1;
+    int64_t tiles = 0, gathered = 0;
+    int f = -1, src = -1;
     if (lane < j) {
         src = T.plan_src[lane];
         const int p = np0 + lane;
@@ -736,7 +751,7 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
         const bool build_left = cl <= c - cl;        // the smaller child, ties left (grow.c:355)
         const int64_t built = build_left ? cl : c - cl;
         tiles = (m + PART_TILE - 1) / PART_TILE;
-        chunks = built > 0 ? gather_chunks(built) : 0;
+        gathered = built;
         f = Lv.f;
         Pend P;
         P.f = Lv.f;
@@ -758,7 +773,7 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
             P.tot[i] = Lv.tot[i];
             P.left[i] = Lv.left[i];
         }
-        P.new_hist = A.hist + (size_t)(p + 1) * slot_elems(A.F);
+        P.pad2 = 0;
         P.placed = 0;
         P.pad1 = 0;
         P.child[0].b = P.child[1].b = -1;
@@ -779,10 +794,13 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
         }
     }
     tiles = wave_incl_scan<int64_t>(tiles, lane);
-    chunks = wave_incl_scan<int>(chunks, lane);
+    // gather units: the round's rows over about gather_target units per tile
+    const int64_t R = wave_sum<int64_t>(gathered);
+    const int64_t per = gather_unit_rows(R, j, (A.F + HFL - 1) / HFL);
+    const int units = (int)wave_incl_scan<int64_t>((gathered + per - 1) / per, lane);
     if (lane < j) {
         st->tile_off[lane + 1] = tiles;
-        st->chunk_off[lane + 1] = chunks;
+        st->unit_off[lane + 1] = units;
     }
     if (A.use_imat) {
         // the children's path: the leaf's path plus its split feature
@@ -799,7 +817,8 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
         st->n_leaves = na;
         st->n_pend = np;
         st->tile_off[0] = 0;
-        st->chunk_off[0] = 0;
+        st->unit_off[0] = 0;
+        st->unit_rows = per;
         if (status < 0) {
             A.out_status[0] = status;
         } else if (done) {
@@ -822,6 +841,39 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
         fl->round = r;
     }
 }
+
+// Adds the bins of feature f (4 per lane) of slots r_begin, r_begin + step,
+// ... <= r_end of `base` into g4, h4, c4, two slots' loads in flight.
+__device__ __forceinline__ void add_slots(const int64_t* base, int F, int f, int lane, int r_begin, int r_end, int step,
+                                          int64_t g4[4], int64_t h4[4], int64_t c4[4], bool has_h) {
+    const size_t se = slot_elems(F);
+    int r = r_begin;
+    for (; r + step <= r_end; r += 2 * step) {
+        int64_t ag[4], ah[4], ac[4], bg[4], bh[4], bc[4];
+        load_bins(base + (size_t)r * se, F, f, lane, ag, ah, ac, has_h);
+        load_bins(base + (size_t)(r + step) * se, F, f, lane, bg, bh, bc, has_h);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            g4[i] += ag[i] + bg[i];
+            h4[i] += ah[i] + bh[i];
+            c4[i] += ac[i] + bc[i];
+        }
+    }
+    if (r <= r_end) {
+        int64_t ag[4], ah[4], ac[4];
+        load_bins(base + (size_t)r * se, F, f, lane, ag, ah, ac, has_h);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            g4[i] += ag[i];
+            h4[i] += ah[i];
+            c4[i] += ac[i];
+        }
+    }
+}
+
+// LDS of a split round's scan block: the exchange of the built child's
+// piece sums, 12 words per lane per wave (the controller's table reuses it).
+constexpr size_t SCAN_XCHG_BYTES = (size_t)(CT / WAVE) * 12 * WAVE * sizeof(int64_t);
 
 // Scan launch: SCAN_FEATS features per block and, for a split round, block y
 // scans both children of the round's split y (wave w: feature w % SCAN_FEATS,
@@ -859,7 +911,32 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
     int64_t* hn = A.hist + (size_t)(ROOT ? 0 : P->new_slot) * slot_elems(A.F);
     __shared__ ScanRec s_rec[NT / WAVE];
     __shared__ int s_last;
+    extern __shared__ __align__(16) char s_table[];
     int64_t g4[4], h4[4], c4[4];
+    if (ROOT) {
+        if (fok) load_bins(hn, A.F, f, lane, g4, h4, c4, has_h);
+    } else {
+        // the built child: the sum of its gather pieces, the two waves of a
+        // feature adding alternate pieces and exchanging their sums in LDS
+#pragma unroll
+        for (int i = 0; i < 4; ++i) g4[i] = h4[i] = c4[i] = 0;
+        if (fok) add_slots(A.pieces, A.F, f, lane, st->unit_off[y] + c, st->unit_off[y + 1] - 1, 2, g4, h4, c4, has_h);
+        YABT_LDS int64_t* xs = (YABT_LDS int64_t*)s_table;   // [wave][12][lane]
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            xs[(w * 12 + i) * WAVE + lane] = g4[i];
+            xs[(w * 12 + 4 + i) * WAVE + lane] = h4[i];
+            xs[(w * 12 + 8 + i) * WAVE + lane] = c4[i];
+        }
+        __syncthreads();
+        const int wp = (w + SCAN_FEATS) % (2 * SCAN_FEATS);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            g4[i] += xs[(wp * 12 + i) * WAVE + lane];
+            h4[i] += xs[(wp * 12 + 4 + i) * WAVE + lane];
+            c4[i] += xs[(wp * 12 + 8 + i) * WAVE + lane];
+        }
+    }
     if (fok) {
         int64_t tot[3];
         if (ROOT) {
@@ -869,7 +946,6 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
         } else {
             for (int i = 0; i < 3; ++i) tot[i] = bl ? P->left[i] : P->tot[i] - P->left[i];
         }
-        load_bins(hn, A.F, f, lane, g4, h4, c4, has_h);
         fill_default(g4, h4, c4, d, tot, has_h, lane);
         if (!built) {
             int64_t pg[4], ph[4], pc[4];
@@ -915,8 +991,10 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
     if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     // every wave of the block has loaded its bins (barriers above): store
     if (fok) {
-        if (built) {
+        if (ROOT) {
             if (d >= 0 && (d >> 2) == lane) store_bins(hn, A.F, f, lane, g4, h4, c4, has_h);
+        } else if (built) {
+            store_bins(hn, A.F, f, lane, g4, h4, c4, has_h);
         } else {
             store_bins(hp, A.F, f, lane, g4, h4, c4, has_h);
         }
@@ -925,7 +1003,6 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
     if (threadIdx.x == 0) st->scan_ticket = 0;
 
     // ---- controller ----
-    extern __shared__ __align__(16) char s_table[];
     Table T;
     table_carve(s_table, A.max_leaves, A.pend_cap, &T);
     if (ROOT) {
@@ -1138,6 +1215,7 @@ size_t carve(char* base, int64_t n, int F, int max_leaves, Args* A) {
     a.q = c.take<Quant>(1);
     a.rows = c.take<uint32_t>((size_t)2 * (size_t)a.rows_ld);
     a.hist = c.take<int64_t>((size_t)(pend_cap + 1) * 3 * (size_t)F * NB);
+    a.pieces = c.take<int64_t>((size_t)gather_units((F + HFL - 1) / HFL) * 3 * (size_t)F * NB);
     a.pend_path = c.take<uint8_t>((size_t)pend_cap * (size_t)F);
     a.leaf_src = c.take<int32_t>(N);
     a.leaf_node = c.take<int32_t>(N);
@@ -1247,9 +1325,9 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
     const int scan_grid = (F + SCAN_FEATS - 1) / SCAN_FEATS;
     const size_t table_lds = table_carve(nullptr, max_leaves, A.pend_cap, nullptr);
     k_scan<true><<<scan_grid, SCAN_FEATS * WAVE, table_lds, stream>>>(A);
+    const size_t scan_lds = table_lds > SCAN_XCHG_BYTES ? table_lds : SCAN_XCHG_BYTES;
     int lrc = launch_status("yabt_grow_batched launch");
     if (lrc) return lrc;
-    const int64_t slot_n = (int64_t)3 * F * NB;
     const int wlog = pack_window_log2(n);
     // rounds: at most max_leaves - 1 (one split each); the controller of round
     // r stamps r + 1 into h_flags->round, so round r may be enqueued once
@@ -1269,10 +1347,10 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
             }
         }
         if (fl->done) break;
-        k_part<<<PART_BLOCKS, SB, 0, stream>>>(bins_fm, ld_fm, n, A.st, A.pend, slot_n);
-        k_gather<<<tiles * GCHUNKS, HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, A.q, A.dflt, A.st, A.pend,
-                                                        wlog);
-        k_scan<false><<<dim3(scan_grid, KMAX), CT, table_lds, stream>>>(A);
+        k_part<<<PART_BLOCKS, SB, 0, stream>>>(bins_fm, ld_fm, n, A.st, A.pend);
+        k_gather<<<tiles * gather_units(tiles), HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, A.q, A.dflt,
+                                                                         A.st, A.pend, A.pieces, wlog);
+        k_scan<false><<<dim3(scan_grid, KMAX), CT, scan_lds, stream>>>(A);
         if ((lrc = launch_status("yabt_grow_batched launch"))) return lrc;
     }
     if (out_leaf_of_row && n > 0) {

@@ -70,6 +70,11 @@ struct HistLdsP {
     unsigned long long g[NB * HFL];           // sum q(g) (with the h channel)
     unsigned long long p[NB * HFL];           // packed (q << cb) + 1
 };
+// The gather's LDS: the packed words, then the final flush's HistLds.
+union GatherLds {
+    HistLds u;
+    HistLdsP p;
+};
 
 // Final flush of the packed kernels: thread t holds cells i = t + k HBLOCK
 // (bin i / HFL, feature f0 + i % HFL) with sums g, h and counts c.  They go
@@ -81,8 +86,10 @@ struct HistLdsP {
 // distinct bank pairs (unswizzled they share one), and stays inside each
 // aligned group of 64 bins, so a wave's reads still cover 64 consecutive
 // bins.  The caller has finished with its own LDS layout (a barrier before
-// the call); cells without rows and features >= F are skipped.
-template <bool HCH>
+// the call).  Features >= F are skipped; cells without rows are skipped when
+// adding (STORE false: global atomics into out's sums so far) and written as
+// zeros when storing (STORE true: out is this block's own piece).
+template <bool HCH, bool STORE = false>
 __device__ __forceinline__ void flush_cells(HistLds& T, const uint64_t (&g)[HENT], const int64_t (&h)[HENT],
                                             const uint32_t (&c)[HENT], int64_t* out, int F, int f0) {
 #pragma unroll
@@ -102,11 +109,17 @@ __device__ __forceinline__ void flush_cells(HistLds& T, const uint64_t (&g)[HENT
         const int fl = j / NB;
         const int fi = f0 + fl;
         const uint32_t cj = T.c[j];
-        if (fi >= F || cj == 0) continue;
+        if (fi >= F || (!STORE && cj == 0)) continue;
         const size_t at = (size_t)fi * NB + (size_t)((j % NB) ^ (2 * fl));
-        atomicAdd((unsigned long long*)(out + at), T.g[j]);
-        if (HCH) atomicAdd((unsigned long long*)(out + plane + at), T.h[j]);
-        atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)cj);
+        if (STORE) {
+            out[at] = (int64_t)T.g[j];
+            if (HCH) out[plane + at] = (int64_t)T.h[j];
+            out[2 * plane + at] = (int64_t)cj;
+        } else {
+            atomicAdd((unsigned long long*)(out + at), T.g[j]);
+            if (HCH) atomicAdd((unsigned long long*)(out + plane + at), T.h[j]);
+            atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)cj);
+        }
     }
 }
 
@@ -502,14 +515,15 @@ __device__ __forceinline__ uint4 rotate_bytes16(uint4 v, int k) {
                       __builtin_amdgcn_alignbyte(c3, c2, r), __builtin_amdgcn_alignbyte(c0, c3, r));
 }
 
-// Histogram of the rows listed at rows[jlo:jhi] over features [16 tile,
-// 16 tile + 16), bins gathered from the row-major copy: chunk `chunk` of the
-// node's rows (a node uses gather_chunks(m) chunks; other chunk numbers
-// return at once), with the packed count of hist_root's kind: the count rides
-// in the low cb = wlog + 1 bits of one 64-bit LDS word, (q << cb) + 1 per row
-// (q = q(h), or q(g) when every h is equal), and each window of 2^wlog rows
-// is unpacked into registers; with the h channel q(g) has a word of its own.
-// Two 64-bit LDS atomics per update (one without the h channel).
+// Histogram of the rows listed at rows[lo:hi] over features [16 tile,
+// 16 tile + 16), bins gathered from the row-major copy, into out (3, F, 256):
+// added with global atomics (STORE false: out holds the sums so far) or
+// stored (STORE true: out is this block's own piece), with the packed count
+// of hist_root's kind: the count rides in the low cb = wlog + 1 bits of one
+// 64-bit LDS word, (q << cb) + 1 per row (q = q(h), or q(g) when every h is
+// equal), and each window of 2^wlog rows is unpacked into registers; with the
+// h channel q(g) has a word of its own.  Two 64-bit LDS atomics per update
+// (one without the h channel).  The whole block calls it (barriers inside).
 //
 // Each lane takes one row per step: its row id, its g and h, and the 16
 // bytes of its row's bins for the tile with one 16-byte load, so each lane
@@ -517,24 +531,19 @@ __device__ __forceinline__ uint4 rotate_bytes16(uint4 v, int k) {
 // k = lane % 16, and the lane's J-th add goes to feature (J + k) % 16: the 16
 // lanes of a quarter wave then hit 16 different features (bank pairs) at
 // every add, whatever the bins are.  Features >= F are the row-major copy's
-// zero padding, added into LDS columns the flush ignores; rows past the chunk
-// read row hi - 1 and add zero words.  A three-stage pipeline per wave: at
-// step s the wave adds step s, loads g, h and the bins of step s + 1 (its row
-// ids are in registers) and the row ids of step s + 2.
-template <bool HCH, bool SKIP>
-__device__ __forceinline__ void hist_gather_packed(HistLdsP& L, const uint8_t* __restrict__ bins_rm, int64_t ld,
-                                                   const float* __restrict__ grad, const float* __restrict__ hess,
-                                                   int F, double scg, double sch, const int32_t* __restrict__ dflt,
-                                                   const uint32_t* __restrict__ rows, int64_t jlo, int64_t jhi,
-                                                   int64_t* out, int wlog, int tile, int chunk) {
+// zero padding, added into LDS columns the flush ignores; rows past hi read
+// row hi - 1 and add zero words.  A three-stage pipeline per wave: at step s
+// the wave adds step s, loads g, h and the bins of step s + 1 (its row ids
+// are in registers) and the row ids of step s + 2.
+template <bool HCH, bool SKIP, bool STORE = false>
+__device__ __forceinline__ void hist_gather_rows(GatherLds& LU, const uint8_t* __restrict__ bins_rm, int64_t ld,
+                                                 const float* __restrict__ grad, const float* __restrict__ hess,
+                                                 int F, double scg, double sch, const int32_t* __restrict__ dflt,
+                                                 const uint32_t* __restrict__ rows, int64_t lo, int64_t hi,
+                                                 int64_t* out, int wlog, int tile) {
     const int f0 = tile * HFL;
-    const int64_t m = jhi - jlo;
-    if (f0 >= F || m <= 0) return;
-    const int nch = gather_chunks(m);
-    if (chunk >= nch) return;
-    const int64_t per = ((m + nch - 1) / nch + WAVE - 1) / WAVE * WAVE;
-    const int64_t lo = jlo + (int64_t)chunk * per, hi = min(jhi, lo + per);
-    if (lo >= hi) return;
+    if (f0 >= F || lo >= hi) return;
+    HistLdsP& L = LU.p;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     int k = lane & (HFL - 1);
     // k is opaque from here: values derived from it are computed per call, not
@@ -632,7 +641,24 @@ __device__ __forceinline__ void hist_gather_packed(HistLdsP& L, const uint8_t* _
 #pragma unroll
     for (int e = 0; e < HENT; ++e) gv[e] = HCH ? L.g[threadIdx.x + e * HBLOCK] : (uint64_t)qa[e];
     __syncthreads();   // every g cell read before the LDS is rewritten
-    flush_cells<HCH>(*reinterpret_cast<HistLds*>(&L), gv, qa, ca, out, F, f0);
+    flush_cells<HCH, STORE>(LU.u, gv, qa, ca, out, F, f0);
+}
+
+// Chunk `chunk` of the rows listed at rows[jlo:jhi]: a node of m rows uses
+// gather_chunks(m) chunks of whole waves (other chunk numbers return at once).
+template <bool HCH, bool SKIP>
+__device__ __forceinline__ void hist_gather_packed(GatherLds& L, const uint8_t* __restrict__ bins_rm, int64_t ld,
+                                                   const float* __restrict__ grad, const float* __restrict__ hess,
+                                                   int F, double scg, double sch, const int32_t* __restrict__ dflt,
+                                                   const uint32_t* __restrict__ rows, int64_t jlo, int64_t jhi,
+                                                   int64_t* out, int wlog, int tile, int chunk) {
+    const int64_t m = jhi - jlo;
+    if (tile * HFL >= F || m <= 0) return;
+    const int nch = gather_chunks(m);
+    if (chunk >= nch) return;
+    const int64_t per = ((m + nch - 1) / nch + WAVE - 1) / WAVE * WAVE;
+    const int64_t lo = jlo + (int64_t)chunk * per, hi = min(jhi, lo + per);
+    hist_gather_rows<HCH, SKIP>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out, wlog, tile);
 }
 
 // job->active == 0 or *done != 0 (done may be NULL): nothing to do.  wlog:
@@ -650,23 +676,20 @@ static __global__ __attribute__((unused)) void __launch_bounds__(HBLOCK) k_hist_
     const bool no_h = count_mode && q && q->const_h;
     if (dn || !jb.active) return;
     const int tile = blockIdx.x / GATHER_MAX_CHUNKS, chunk = blockIdx.x % GATHER_MAX_CHUNKS;
-    __shared__ union {
-        HistLds u;
-        HistLdsP p;
-    } L;
+    __shared__ GatherLds L;
     if (no_h) {
         if (dflt)
-            hist_gather_packed<false, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi,
+            hist_gather_packed<false, true>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi,
                                             jb.out, wlog, tile, chunk);
         else
-            hist_gather_packed<false, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi,
+            hist_gather_packed<false, false>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi,
                                              jb.out, wlog, tile, chunk);
     } else {
         if (dflt)
-            hist_gather_packed<true, true>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi,
+            hist_gather_packed<true, true>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi,
                                            jb.out, wlog, tile, chunk);
         else
-            hist_gather_packed<true, false>(L.p, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi,
+            hist_gather_packed<true, false>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, jb.rows, jb.lo, jb.hi,
                                             jb.out, wlog, tile, chunk);
     }
 }
