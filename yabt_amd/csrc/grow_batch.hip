@@ -913,11 +913,14 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
     __shared__ int s_last;
     extern __shared__ __align__(16) char s_table[];
     int64_t g4[4], h4[4], c4[4];
+    int64_t pg[4], ph[4], pc[4];   // the sibling's wave: the parent's bins
     if (ROOT) {
         if (fok) load_bins(hn, A.F, f, lane, g4, h4, c4, has_h);
     } else {
         // the built child: the sum of its gather pieces, the two waves of a
-        // feature adding alternate pieces and exchanging their sums in LDS
+        // feature adding alternate pieces and exchanging their sums in LDS;
+        // the sibling's wave loads the parent's bins meanwhile
+        if (fok && !built) load_bins(hp, A.F, f, lane, pg, ph, pc, has_h);
 #pragma unroll
         for (int i = 0; i < 4; ++i) g4[i] = h4[i] = c4[i] = 0;
         if (fok) add_slots(A.pieces, A.F, f, lane, st->unit_off[y] + c, st->unit_off[y + 1] - 1, 2, g4, h4, c4, has_h);
@@ -948,8 +951,6 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
         }
         fill_default(g4, h4, c4, d, tot, has_h, lane);
         if (!built) {
-            int64_t pg[4], ph[4], pc[4];
-            load_bins(hp, A.F, f, lane, pg, ph, pc, has_h);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 g4[i] = pg[i] - g4[i];
@@ -1024,14 +1025,30 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
         wave_sync();
         control(A, T, 1, 1, 0, &s_root, lane);
     } else {
-        // the round's children: best record over the scan blocks, per child
-        for (int i = w; i < 2 * nr; i += NT / WAVE) {
-            const ScanRec r = wave_best_record(A.rec + (size_t)i * gridDim.x, gridDim.x, lane);
-            if (lane == 0) {
+        // the round's children: best record over the scan blocks, per child;
+        // wave w takes children w, w + 8, ..., their records' loads first
+        constexpr int CPW = 2 * KMAX / (NT / WAVE);   // children per wave, at most
+        static_assert(CPW * (NT / WAVE) == 2 * KMAX, "children per wave");
+        ScanRec rr[CPW];
+        if (gridDim.x <= WAVE) {
+            wave_best_records<CPW>(A.rec, gridDim.x, w, NT / WAVE, 2 * nr, lane, rr);
+        } else {
+#pragma unroll
+            for (int k = 0; k < CPW; ++k) {
+                const int i = w + k * (NT / WAVE);
+                if (i < 2 * nr) rr[k] = wave_best_record(A.rec + (size_t)i * gridDim.x, gridDim.x, lane);
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < CPW; ++k) {
+            const int i = w + k * (NT / WAVE);
+            if (i < 2 * nr && lane == 0) {
                 const int p = st->round_pend[i / 2];
                 Pend& Pp = A.pend[p];
-                Pp.child[i % 2] = r;
-                T.cgain[p][i % 2] = rec_gain(r, Pp.depth >= A.max_depth);
+                Pp.child[i % 2] = rr[k];
+                const float g = rec_gain(rr[k], Pp.depth >= A.max_depth);
+                T.cgain[p][i % 2] = g;
+                A.psum[p].gain[i % 2] = g;   // kept for later controllers
             }
         }
         const int nn = st->n_nodes, na = st->n_leaves, np = st->n_pend;
@@ -1062,11 +1079,6 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
             T.pend[a] = (int16_t)pend_of(T, T.src[a]);
         }
         __syncthreads();
-        // this round's children's gains, kept for later controllers
-        if (threadIdx.x < 2 * nr) {
-            const int p = p0 + threadIdx.x / 2;
-            A.psum[p].gain[threadIdx.x % 2] = T.cgain[p][threadIdx.x % 2];
-        }
         if (w != 0) return;
         control(A, T, nn, na, np, nullptr, lane);
     }

@@ -227,34 +227,41 @@ __device__ __forceinline__ bool rec_beats(double sa, int fa, int ba, double sb, 
     return ba >= 0 && (bb < 0 || sa > sb || (sa == sb && fa < fb));
 }
 
-// One wave: the best of rec[0, n) in every lane (b = -1: none valid).
-__device__ inline ScanRec wave_best_record(const ScanRec* rec, int n, int lane) {
-    ScanRec mine;
-    mine.sel = -INFINITY;
-    mine.gain = -INFINITY;
-    mine.b = -1;
-    mine.f = INT_MAX;
-    mine.left[0] = mine.left[1] = mine.left[2] = 0;
-    int my_idx = -1;
-    for (int i = lane; i < n; i += WAVE) {
-        const ScanRec r = rec[i];
-        if (rec_beats(r.sel, r.f, r.b, mine.sel, mine.f, mine.b)) {
-            mine = r;
-            my_idx = i;
-        }
-    }
+// One wave (all 64 lanes active): the best of the lanes' records `mine` (the
+// lane's index my_idx, -1: none) in every lane (b = -1: none valid).
+__device__ inline ScanRec wave_reduce_record(const ScanRec& mine, int my_idx) {
+    // rotations inside each 16-lane row leave the row's best in all of its
+    // lanes (valid records have distinct features: the order is total), then
+    // the four rows' bests meet
     double s = mine.sel;
     int f = mine.f, b = mine.b, idx = my_idx;
-#pragma unroll
-    for (int m = WAVE / 2; m > 0; m >>= 1) {
-        const double os = __shfl_xor(s, m, WAVE);
-        const int of = __shfl_xor(f, m, WAVE), ob = __shfl_xor(b, m, WAVE), oi = __shfl_xor(idx, m, WAVE);
+    auto take = [&](double os, int of, int ob, int oi) {
         if (rec_beats(os, of, ob, s, f, b)) {
             s = os;
             f = of;
             b = ob;
             idx = oi;
         }
+    };
+    take(dpp_f64<DPP_ROW_ROR + 8>(s), (int)dpp32<DPP_ROW_ROR + 8>((uint32_t)f), (int)dpp32<DPP_ROW_ROR + 8>((uint32_t)b),
+         (int)dpp32<DPP_ROW_ROR + 8>((uint32_t)idx));
+    take(dpp_f64<DPP_ROW_ROR + 4>(s), (int)dpp32<DPP_ROW_ROR + 4>((uint32_t)f), (int)dpp32<DPP_ROW_ROR + 4>((uint32_t)b),
+         (int)dpp32<DPP_ROW_ROR + 4>((uint32_t)idx));
+    take(dpp_f64<DPP_ROW_ROR + 2>(s), (int)dpp32<DPP_ROW_ROR + 2>((uint32_t)f), (int)dpp32<DPP_ROW_ROR + 2>((uint32_t)b),
+         (int)dpp32<DPP_ROW_ROR + 2>((uint32_t)idx));
+    take(dpp_f64<DPP_ROW_ROR + 1>(s), (int)dpp32<DPP_ROW_ROR + 1>((uint32_t)f), (int)dpp32<DPP_ROW_ROR + 1>((uint32_t)b),
+         (int)dpp32<DPP_ROW_ROR + 1>((uint32_t)idx));
+    {
+        const double s0 = s;
+        const int f0 = f, b0 = b, i0 = idx;
+        s = readlane_f64(s0, 0);
+        f = __builtin_amdgcn_readlane(f0, 0);
+        b = __builtin_amdgcn_readlane(b0, 0);
+        idx = __builtin_amdgcn_readlane(i0, 0);
+#pragma unroll
+        for (int row = 1; row < 4; ++row)
+            take(readlane_f64(s0, 16 * row), __builtin_amdgcn_readlane(f0, 16 * row),
+                 __builtin_amdgcn_readlane(b0, 16 * row), __builtin_amdgcn_readlane(i0, 16 * row));
     }
     ScanRec r;
     const uint64_t owner = __ballot(idx >= 0 && my_idx == idx);
@@ -273,6 +280,51 @@ __device__ inline ScanRec wave_best_record(const ScanRec* rec, int n, int lane) 
     r.left[1] = readlane64(mine.left[1], src);
     r.left[2] = readlane64(mine.left[2], src);
     return r;
+}
+
+__device__ __forceinline__ ScanRec empty_record() {
+    ScanRec e;
+    e.sel = -INFINITY;
+    e.gain = -INFINITY;
+    e.b = -1;
+    e.f = INT_MAX;
+    e.left[0] = e.left[1] = e.left[2] = 0;
+    return e;
+}
+
+// One wave (all 64 lanes active): the best of rec[0, n) in every lane (b = -1:
+// none valid).
+__device__ inline ScanRec wave_best_record(const ScanRec* rec, int n, int lane) {
+    ScanRec mine = empty_record();
+    int my_idx = -1;
+    for (int i = lane; i < n; i += WAVE) {
+        const ScanRec r = rec[i];
+        if (rec_beats(r.sel, r.f, r.b, mine.sel, mine.f, mine.b)) {
+            mine = r;
+            my_idx = i;
+        }
+    }
+    return wave_reduce_record(mine, my_idx);
+}
+
+// Several waves' worth of wave_best_record at once: out[k] = the best of
+// rec[i n, i n + n) for i = w0 + k stride < nchild (n <= 64: one record per
+// lane), all loads issued before any reduction.
+template <int K>
+__device__ inline void wave_best_records(const ScanRec* rec, int n, int w0, int stride, int nchild, int lane,
+                                         ScanRec (&out)[K]) {
+    ScanRec mine[K];
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int i = w0 + k * stride;
+        mine[k] = (i < nchild && lane < n) ? rec[(size_t)i * n + lane] : empty_record();
+    }
+#pragma unroll
+    for (int k = 0; k < K; ++k) {
+        const int i = w0 + k * stride;
+        if (i >= nchild) break;
+        out[k] = wave_reduce_record(mine[k], mine[k].b >= 0 ? lane : -1);
+    }
 }
 
 // Feature-major reduction of one node's records (grow.c:181-192), NT threads;
