@@ -53,8 +53,9 @@ namespace yabt {
 namespace rnd {
 
 constexpr int SB = 256;                          // threads of the partition / setup blocks
-constexpr int PART_IPT = 16;                     // rows per thread per partition tile
-constexpr int PART_TILE = SB * PART_IPT;
+constexpr int PART_IPT_WIDE = 16;                // rows per thread per partition tile: rounds
+constexpr int PART_IPT_NARROW = 8;               //   of more / fewer than PART_WIDE_ROWS rows
+constexpr int64_t PART_WIDE_ROWS = 1 << 20;
 constexpr int PART_BLOCKS = 1024;
 constexpr int SCAN_FEATS = 4;                    // features per scan block
 constexpr int KMAX = 16;                         // splits computed per round, at most
@@ -104,6 +105,8 @@ struct State {
     float root_gain;                     // the root's table gain
     int32_t round_pend[KMAX];            // this round's Pend entries
     int64_t tile_off[KMAX + 1];          // partition tiles of this round's splits, prefix sums
+    int32_t part_ipt;                    // rows per thread of this round's partition tiles
+    int32_t pad4;
     int32_t unit_off[KMAX + 1];          // gather units of this round's built children, prefix sums
     int32_t pad3;
     int64_t unit_rows;                   // rows per gather unit (a child's last unit: the rest)
@@ -225,36 +228,42 @@ __global__ void k_setup_finish(Args A) {
 // 64-bit atomic on the split's packed (left, right) count: a child holds at
 // most n < 2^32 rows, so the left half never carries into the right.  (The
 // order inside a child depends on the schedule, which no exact sum does.)
-__global__ void __launch_bounds__(SB) k_part(const uint8_t* __restrict__ bins_fm, int64_t ld, int64_t n, State* st,
-                                             Pend* pend) {
-    const int32_t done = st->done, nr = st->n_round;
-    if (done || nr == 0) return;
-    const int64_t T = st->tile_off[nr];
+template <int IPT>
+__device__ __forceinline__ void part_tiles(const uint8_t* __restrict__ bins_fm, int64_t ld, int64_t n, State* st,
+                                           Pend* pend, int nr) {
+    constexpr int TILE = SB * IPT;
     const int w = threadIdx.x / WAVE;
     __shared__ uint32_t s_cnt[SB / WAVE][2];
     __shared__ unsigned long long s_base[SB / WAVE][2];
+    __shared__ int64_t s_toff[KMAX + 1];
+    __shared__ int32_t s_rp[KMAX];
+    // the round's tile offsets and Pend entries, loaded together
+    if (threadIdx.x <= nr) s_toff[threadIdx.x] = st->tile_off[threadIdx.x];
+    if (threadIdx.x < nr) s_rp[threadIdx.x] = st->round_pend[threadIdx.x];
+    __syncthreads();
+    const int64_t T = s_toff[nr];
+    int j = 0;   // tiles t grow, so their splits j do
     for (int64_t t = blockIdx.x; t < T; t += gridDim.x) {
-        int j = 0;
-        while (j + 1 < nr && st->tile_off[j + 1] <= t) ++j;
-        Pend& P = pend[st->round_pend[j]];
-        const int64_t t0 = P.s + (t - st->tile_off[j]) * PART_TILE;
-        const int64_t hi = min(P.e, t0 + PART_TILE);
+        while (j + 1 < nr && s_toff[j + 1] <= t) ++j;
+        Pend& P = pend[s_rp[j]];
+        const int64_t t0 = P.s + (t - s_toff[j]) * TILE;
+        const int64_t hi = min(P.e, t0 + TILE);
         const uint8_t* col = bins_fm + (size_t)P.f * ld;
         const int b = P.b;
         const uint32_t* src = P.src;
         uint32_t* dst = P.dst;
-        uint32_t rid[PART_IPT];
+        uint32_t rid[IPT];
 #pragma unroll
-        for (int k = 0; k < PART_IPT; ++k) {
+        for (int k = 0; k < IPT; ++k) {
             const int64_t i = min(t0 + (int64_t)k * SB + threadIdx.x, hi - 1);
             rid[k] = src ? min(src[i], (uint32_t)(n - 1)) : (uint32_t)i;   // a row id stays a row id
         }
-        uint32_t bv[PART_IPT];
+        uint32_t bv[IPT];
 #pragma unroll
-        for (int k = 0; k < PART_IPT; ++k) bv[k] = col[rid[k]];
+        for (int k = 0; k < IPT; ++k) bv[k] = col[rid[k]];
         uint32_t left = 0, valid = 0, nl = 0, nv = 0;
 #pragma unroll
-        for (int k = 0; k < PART_IPT; ++k) {
+        for (int k = 0; k < IPT; ++k) {
             const bool v = t0 + (int64_t)k * SB + threadIdx.x < hi;
             const bool l = v && (int)bv[k] <= b;
             valid |= (v ? 1u : 0u) << k;
@@ -287,7 +296,7 @@ __global__ void __launch_bounds__(SB) k_part(const uint8_t* __restrict__ bins_fm
         __syncthreads();
         uint64_t pl = s_base[w][0], pr = s_base[w][1];
 #pragma unroll
-        for (int k = 0; k < PART_IPT; ++k) {
+        for (int k = 0; k < IPT; ++k) {
             const bool v = (valid >> k) & 1u, l = (left >> k) & 1u;
             const uint64_t ml = __ballot(l), mr = __ballot(v && !l);
             if (l) dst[pl + lane_prefix(ml)] = rid[k];
@@ -297,6 +306,16 @@ __global__ void __launch_bounds__(SB) k_part(const uint8_t* __restrict__ bins_fm
         }
         __syncthreads();
     }
+}
+
+__global__ void __launch_bounds__(SB) k_part(const uint8_t* __restrict__ bins_fm, int64_t ld, int64_t n, State* st,
+                                             Pend* pend) {
+    const int32_t done = st->done, nr = st->n_round;
+    if (done || nr == 0) return;
+    if (st->part_ipt == PART_IPT_WIDE)
+        part_tiles<PART_IPT_WIDE>(bins_fm, ld, n, st, pend, nr);
+    else
+        part_tiles<PART_IPT_NARROW>(bins_fm, ld, n, st, pend, nr);
 }
 
 // ---------------------------------------------------------------------------
@@ -750,7 +769,7 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
         const int64_t cl = Lv.left[2], c = Lv.tot[2], m = Lv.e - Lv.s;
         const bool build_left = cl <= c - cl;        // the smaller child, ties left (grow.c:355)
         const int64_t built = build_left ? cl : c - cl;
-        tiles = (m + PART_TILE - 1) / PART_TILE;
+        tiles = m;   // rows for now: tiles once the round's width is known
         gathered = built;
         f = Lv.f;
         Pend P;
@@ -793,6 +812,9 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
             st->root_pend = p;
         }
     }
+    // partition tiles: wide when the round moves many rows
+    const int ipt = wave_sum<int64_t>(tiles) > PART_WIDE_ROWS ? PART_IPT_WIDE : PART_IPT_NARROW;
+    tiles = (tiles + (int64_t)SB * ipt - 1) / ((int64_t)SB * ipt);
     tiles = wave_incl_scan<int64_t>(tiles, lane);
     // gather units: the round's rows over about gather_target units per tile
     const int64_t R = wave_sum<int64_t>(gathered);
@@ -819,6 +841,7 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
         st->tile_off[0] = 0;
         st->unit_off[0] = 0;
         st->unit_rows = per;
+        st->part_ipt = ipt;
         if (status < 0) {
             A.out_status[0] = status;
         } else if (done) {
