@@ -31,9 +31,12 @@ rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) over ``bench.py --counters``,
 which launches a plain copy kernel of known size (for the counter scale) and
 the root-histogram kernel, three times each.
 
-Also reported, outside the timed region: ``ms_grow_reference`` (one tree of
-the same workload grown with the reference's own fp32 arithmetic,
-yabt_grow_ref) and ``boosting`` (whole estimator fits, see boosting_fits).
+Also reported, outside the timed region: ``reference_arithmetic`` (the same
+tree grown with the reference's own fp32 arithmetic, yabt_grow_ref, whose
+trees equal grow.c's: ms per tree with and without the leaf models, its root
+histogram's time and share of HBM peak, and its split differences from the
+exact tree, see reference_arithmetic) and ``boosting`` (whole estimator fits,
+see boosting_fits).
 
 Usage: python bench.py [--gpus 1] [--steps 5] [--warmup 1] [--no-cpu]
                        [--ref-steps 1] [--no-boosting]
@@ -253,6 +256,78 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
     out["all_cores"] = {"threads": all_threads, "ms_per_tree": round(sec_all * 1e3, 1),
                         "value": round(upd / sec_all / 1e9, 4)}
     out["other_workloads"] = cpu_other_workloads(O, reference, threads)
+    return out
+
+
+def reference_arithmetic(torch, lay, g, h, nbins, steps: int, exact_res, neural: bool) -> dict:
+    """The same tree grown with the reference's own fp32 arithmetic
+    (yabt_grow_ref, whose trees equal grow.c's node for node): ms per tree for
+    the grower alone and with the leaf models, its root histogram (cgrow's
+    row-order fp32 chains from the per-fit rank table) with its share of HBM
+    peak, the per-fit rank table's cost, and the internal nodes whose
+    (feature, bin) differ from the exact tree's."""
+    from yabt_amd import grow_hip as G
+    from yabt_amd.neural_leaves import fit_leaf_networks_binned
+    from yabt_amd.tree import Tree
+    n, F = lay.n, lay.F
+    log(f"[bench] reference-arithmetic trees: {steps}")
+    t0 = time.perf_counter()
+    lay.ref_root_order()
+    torch.cuda.synchronize()
+    order_ms = (time.perf_counter() - t0) * 1e3
+
+    def grow():
+        return G.grow_device(lay, g, h, nbins, arithmetic="reference", **PARAMS)
+
+    def with_leaves():
+        res = grow()
+        leaf = G.leaf_ids(res, n, F, MAX_LEAVES)
+        tree = Tree(res.feature, res.thr_bin.float(), res.left, res.right, res.value, 0)
+        return res, fit_leaf_networks_binned(tree, lay.fm, g + h * res.value[leaf], h, leaf, LeafNetParams, n=n)
+
+    res = grow()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        res = grow()
+    torch.cuda.synchronize()
+    ms_grow = (time.perf_counter() - t0) * 1e3 / steps
+    out = {"ms_grow": round(ms_grow, 2)}
+    if neural:
+        with_leaves()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            with_leaves()
+        torch.cuda.synchronize()
+        out["ms_per_tree"] = round((time.perf_counter() - t0) * 1e3 / steps, 2)
+    # the root histogram alone, HIP events on the launch stream
+    for _ in range(5):
+        G.ref_root_hist(lay, g, h)
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 10
+    e0.record(stream)
+    for _ in range(reps):
+        G.ref_root_hist(lay, g, h)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    root_ms = e0.elapsed_time(e1) / reps
+    root_bytes = n * F + 8 * n
+    out["root_hist"] = {"ms": round(root_ms, 3), "GBps": round(root_bytes / (root_ms * 1e-3) / 1e9, 1),
+                        "frac_hbm": round(root_bytes / (root_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                        "kernel": "k_rank_chain (row-order fp32 chains, one block per feature)"}
+    out["fit_setup"] = {"root_order_ms": round(order_ms, 2),
+                        "note": "per-fit root rank table (yabt_ref_root_order), outside the step"}
+    # split sequence against the exact tree's
+    a = {k: getattr(exact_res, k)[:exact_res.n_nodes].cpu().numpy() for k in ("feature", "thr_bin", "left")}
+    b = {k: getattr(res, k)[:res.n_nodes].cpu().numpy() for k in ("feature", "thr_bin", "left")}
+    same_shape = a["feature"].shape == b["feature"].shape and np.array_equal(a["left"], b["left"])
+    m = min(a["feature"].size, b["feature"].size)
+    internal = (a["feature"][:m] >= 0) | (b["feature"][:m] >= 0)
+    differ = internal & ((a["feature"][:m] != b["feature"][:m]) | (a["thr_bin"][:m] != b["thr_bin"][:m]))
+    out["vs_exact"] = {"internal_nodes": int(internal.sum()), "split_differences": int(differ.sum()),
+                       "same_node_layout": bool(same_shape)}
     return out
 
 
@@ -524,14 +599,7 @@ def main() -> None:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic()},
     }
     if args.ref_steps > 0:
-        log(f"[bench] reference-arithmetic trees: {args.ref_steps}")
-        G.grow_device(lay, g, h, nbins, arithmetic="reference", **PARAMS)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.ref_steps):
-            G.grow_device(lay, g, h, nbins, arithmetic="reference", **PARAMS)
-        torch.cuda.synchronize()
-        line["ms_grow_reference"] = round((time.perf_counter() - t0) * 1e3 / args.ref_steps, 1)
+        line["reference_arithmetic"] = reference_arithmetic(torch, lay, g, h, nbins, args.ref_steps, res, neural)
     if not args.no_boosting:
         del lay, g, h
         torch.cuda.empty_cache()

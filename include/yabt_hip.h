@@ -307,17 +307,43 @@ size_t yabt_grow_ref_workspace_min_bytes(int64_t n, int F, int max_leaves, int s
  * int64) cgrow's final rows[] array.  cgrow's leaf table runs on the host,
  * which computes up to 16 splits per round (planned by running the table
  * ahead through the splits already computed) and commits them in cgrow's
- * order: one device round trip per round.  The call returns after the
- * stream has finished (it synchronises `stream`).  Requires n < 2^32, F >= 1,
- * 1 <= max_leaves <= 32767. */
+ * order: one device round trip per round.  root_order (NULL: the root is
+ * bucketed in the call): the rank table yabt_ref_root_order made for these
+ * bins_fm, n and F, which the dense builder's root then reads instead of
+ * bucketing its rows again (the sparse builder ignores it).  The call returns
+ * after the stream has finished (it synchronises `stream`).  Requires
+ * n < 2^32, F >= 1, 1 <= max_leaves <= 32767. */
 int yabt_grow_ref(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
                   const float *grad, const float *hess, const uint8_t *fmask, const float *imat,
                   float ib, int use_imat, const int32_t *nbins, const int32_t *default_bin,
                   int64_t n, int F, float lam, float gamma, float mcw, int msl, float lr,
                   int max_leaves, int max_depth, void *workspace, size_t workspace_bytes,
-                  int64_t *out_feature, int64_t *out_thr_bin, int64_t *out_left, int64_t *out_right,
+                  const void *root_order, int64_t *out_feature, int64_t *out_thr_bin, int64_t *out_left, int64_t *out_right,
                   float *out_value, int64_t *out_depth, int64_t *out_leaf_of_row, int64_t *out_rows,
                   int32_t *out_n_nodes, yabt_stream_t stream);
+
+/* Bytes of the root rank table of yabt_ref_root_order for n rows, F features
+ * (0: bad sizes). */
+size_t yabt_ref_root_order_bytes(int64_t n, int F);
+
+/* The root rank table of yabt_grow_ref's dense builder, once per fit: for
+ * every feature and every 4096-row tile of rows 0 .. n - 1, each row's rank
+ * among the tile's rows in its bin (row order) and the tile's bin starts --
+ * the bucketing of cgrow's row-order histogram chains (yabt/_cgrow/grow.c:
+ * 37-62) of the root, which is the same for every tree grown on these bins.
+ * out: device memory of at least yabt_ref_root_order_bytes(n, F) bytes.
+ * Replaces nothing in the reference (cgrow sums the root's rows directly);
+ * it is set-up that the device's root histogram reuses across trees. */
+int yabt_ref_root_order(const uint8_t *bins_fm, int64_t ld_fm, int64_t n, int F, void *out, size_t out_bytes,
+                        yabt_stream_t stream);
+
+/* The reference-arithmetic root histogram alone: out (3, F, 256) float32 =
+ * cgrow's dense build_hist over rows 0 .. n - 1 (yabt/_cgrow/grow.c:37-62):
+ * per (feature, bin) the fp32 sums of g, of h and of 1.0f in row order, from
+ * the rank table yabt_ref_root_order made for these bins (root_order_bytes:
+ * its size).  Replaces build_hist for the root node. */
+int yabt_ref_root_hist(const uint8_t *bins_fm, int64_t ld_fm, const float *grad, const float *hess, int64_t n,
+                       int F, const void *root_order, size_t root_order_bytes, float *out, yabt_stream_t stream);
 
 /* Bytes of device workspace yabt_bin_fit needs for an m-row sample of F features. */
 size_t yabt_bin_fit_workspace_bytes(int64_t m, int F);

@@ -75,6 +75,23 @@ def test_reference_grower_workspace_sizes():
     assert lib.yabt_grow_ref_workspace_min_bytes(100, 4, 0, 0) == 0
 
 
+def test_reference_root_order_sizes():
+    """The per-fit root rank table: a uint16 rank per (feature, row) padded to
+    whole 4096-row tiles, then 257 uint16 run starts and the uint16 longest
+    run per (feature, tile)."""
+    lib = _lib.load()
+    def rounded(b):
+        return (b + 255) // 256 * 256
+    for n, F in [(10_000_000, 100), (4097, 3), (1, 1)]:
+        tiles = -(-n // 4096)
+        want = rounded(2 * F * tiles * 4096) + rounded(2 * F * tiles * 257) + rounded(2 * F * tiles)
+        assert lib.yabt_ref_root_order_bytes(n, F) == want
+    assert lib.yabt_ref_root_order_bytes(100, 0) == 0
+    assert lib.yabt_ref_root_order_bytes(-1, 4) == 0
+    rc = lib.yabt_ref_root_order(None, 0, 100, 4, None, 0, None)
+    assert rc < 0 and "bad pointer" in _lib.last_error()
+
+
 def test_argument_errors_are_reported_without_a_device():
     lib = _lib.load()
     rc = lib.yabt_grow(None, 0, None, 0, None, None, None, None, ctypes.c_float(0.5), 0, None, None, None, 10, 0,

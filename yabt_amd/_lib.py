@@ -77,8 +77,11 @@ SIGNATURES = {
     "yabt_grow_ref_workspace_bytes": (_sz, [_i64, _int, _int, _int]),
     "yabt_grow_ref_workspace_min_bytes": (_sz, [_i64, _int, _int, _int]),
     "yabt_grow_ref": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _vp, _i64, _int,
-                             _flt, _flt, _flt, _int, _flt, _int, _int, _vp, _sz,
+                             _flt, _flt, _flt, _int, _flt, _int, _int, _vp, _sz, _vp,
                              _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "yabt_ref_root_order_bytes": (_sz, [_i64, _int]),
+    "yabt_ref_root_order": (_int, [_vp, _i64, _i64, _int, _vp, _sz, _vp]),
+    "yabt_ref_root_hist": (_int, [_vp, _i64, _vp, _vp, _i64, _int, _vp, _sz, _vp, _vp]),
     "yabt_bin_fit_workspace_bytes": (_sz, [_i64, _int]),
     "yabt_bin_fit": (_int, [_vp, _i64, _i64, _int, _vp, _i64, _int, _vp, _sz, _vp, _i64, _vp, _vp, _vp, _vp]),
     "yabt_bin_transform": (_int, [_vp, _i64, _i64, _int, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _i64, _vp, _i64,

@@ -676,6 +676,328 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb,
     }
 }
 
+// ---------------------------------------------------------------------------
+// the root's histogram from a per-fit rank table
+// ---------------------------------------------------------------------------
+//
+// The root's rows are 0 .. n - 1 in order (grow.c:289) and a fit's bins do
+// not change between its trees, so the bucketing of every (feature, WT-row
+// tile) of the root is the same for each tree of a fit.  k_root_rank computes
+// it once: for each position its rank inside its bin's run in its tile (runs
+// in row order, as k_walk_sort's), and each tile's run starts.  Each tree's
+// root then runs only the chains, k_rank_chain: one block per feature, thread
+// b = bin b, the tiles in order; a tile's g, h go into an LDS table T[rank][bin]
+// (a window of RW ranks at a time), so that step r of every thread reads its
+// run's r-th entry from one row of T -- 64 consecutive cells per wave, no bank
+// conflicts -- and adds it in fp32 as cgrow does (grow.c:55-59).
+
+constexpr int RW = 32;             // ranks per window of k_rank_chain's LDS table
+
+// The rank table of yabt_ref_root_order: ranks (uint16, F x ld_rank, position
+// t * WT + x of feature f at f * ld_rank + t * WT + x), the run starts
+// (uint16, F x tiles x ST, as k_walk_sort's), and each (feature, tile)'s
+// longest run (uint16, F x tiles).
+struct RootOrder {
+    uint16_t* rank;
+    uint16_t* starts;
+    uint16_t* maxrun;
+    int64_t ld_rank;
+    int64_t tiles;
+};
+
+__host__ __device__ inline size_t root_order_carve(char* base, int64_t n, int F, RootOrder* o) {
+    const int64_t tiles = (n + WT - 1) / WT > 0 ? (n + WT - 1) / WT : 1;
+    const int64_t ld = tiles * WT;
+    const size_t rank_bytes = ((size_t)F * (size_t)ld * sizeof(uint16_t) + 255) / 256 * 256;
+    const size_t st_bytes = ((size_t)F * (size_t)tiles * ST * sizeof(uint16_t) + 255) / 256 * 256;
+    const size_t mx_bytes = ((size_t)F * (size_t)tiles * sizeof(uint16_t) + 255) / 256 * 256;
+    if (o) {
+        o->rank = (uint16_t*)base;
+        o->starts = (uint16_t*)(base + rank_bytes);
+        o->maxrun = (uint16_t*)(base + rank_bytes + st_bytes);
+        o->ld_rank = ld;
+        o->tiles = tiles;
+    }
+    return rank_bytes + st_bytes + mx_bytes;
+}
+
+// Block (f, t): the ranks and run starts of feature f's tile t (tiles grid-
+// strided over y), bucketed as in k_walk_sort.
+__global__ void __launch_bounds__(RB) k_root_rank(const uint8_t* __restrict__ bins_fm, int64_t ld_fm, int64_t n,
+                                                  RootOrder o) {
+    __shared__ uint8_t s_bin[WT];
+    __shared__ uint64_t s_peer[SW][NB];
+    __shared__ uint32_t s_cnt[SW][NB];
+    __shared__ uint32_t s_scan[SW];
+    __shared__ uint32_t s_max;
+    const int f = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
+    for (int64_t t = blockIdx.y; t < o.tiles; t += gridDim.y) {
+        const int64_t t0 = t * WT;
+        const int tn = (int)max((int64_t)0, min((int64_t)WT, n - t0));
+        for (int i = tid; i < SW * NB; i += RB) {
+            (&s_cnt[0][0])[i] = 0;
+            (&s_peer[0][0])[i] = 0;
+        }
+        if (tid == 0) s_max = 0;
+#pragma unroll
+        for (int j = 0; j < TPT; ++j) {
+            const int x = j * RB + tid;
+            if (x < tn) s_bin[x] = bins_fm[(size_t)f * (size_t)ld_fm + (size_t)(t0 + x)];
+        }
+        __syncthreads();
+        uint32_t rk[SGR];
+        uint8_t qb[SGR];
+#pragma unroll
+        for (int q = 0; q < SGR; ++q) {
+            const int x = w * SSUB + q * WAVE + lane;
+            const bool v = x < tn;
+            const uint32_t bin = v ? (uint32_t)s_bin[x] : 0u;
+            qb[q] = (uint8_t)bin;
+            if (v) atomicOr(&s_peer[w][bin], 1ull << lane);
+            __builtin_amdgcn_wave_barrier();
+            const uint64_t peers = v ? s_peer[w][bin] : 0ull;
+            const uint32_t base = v ? s_cnt[w][bin] : 0u;
+            __builtin_amdgcn_wave_barrier();
+            const uint32_t r = lane_prefix(peers);
+            if (v) s_peer[w][bin] = 0ull;
+            if (v && r == 0) s_cnt[w][bin] = base + (uint32_t)__popcll(peers);
+            __builtin_amdgcn_wave_barrier();
+            rk[q] = base + r;
+        }
+        __syncthreads();
+        {
+            const int b = tid;
+            uint32_t c[SW];
+            uint32_t tb = 0;
+#pragma unroll
+            for (int u = 0; u < SW; ++u) {
+                c[u] = s_cnt[u][b];
+                tb += c[u];
+            }
+            uint32_t total;
+            atomicMax(&s_max, tb);
+            const uint32_t st = block_excl_scan<RB, uint32_t>(tb, s_scan, &total);
+            if (tid == 0) o.maxrun[(size_t)f * (size_t)o.tiles + (size_t)t] = (uint16_t)s_max;
+            uint16_t* st_out = o.starts + ((size_t)f * (size_t)o.tiles + (size_t)t) * ST;
+            st_out[b] = (uint16_t)st;
+            if (b == NB - 1) st_out[NB] = (uint16_t)(st + tb);
+            // wave u's share of bin b starts c[0] + .. + c[u - 1] into the run
+            uint32_t run = 0;
+#pragma unroll
+            for (int u = 0; u < SW; ++u) {
+                s_cnt[u][b] = run;
+                run += c[u];
+            }
+        }
+        __syncthreads();
+        uint16_t* ro = o.rank + (size_t)f * (size_t)o.ld_rank + (size_t)t0;
+#pragma unroll
+        for (int q = 0; q < SGR; ++q) {
+            const int x = w * SSUB + q * WAVE + lane;
+            if (x < tn) ro[x] = (uint16_t)(s_cnt[w][qb[q]] + rk[q]);
+        }
+        __syncthreads();
+    }
+}
+
+// One tile's positions for a producer thread of k_rank_chain, TPT in four
+// groups of four: entry j = 4 q + k is position t WT + q 4 RB + 4 slot + k,
+// so a wave's 16-byte loads of g (and of h) cover 1 KB in one piece and its
+// loads of ranks and bins 512 and 256 bytes.  The tile keeps the loaded words
+// as they are: unpacking them at load time would wait for the loads there,
+// and the loads are meant to run under earlier tiles' work.
+struct RankTile {
+    float4 g[4], h[4];
+    uint2 r[4];                    // ranks, 16 bits each; 0xffff: past the rows
+    uint32_t bw[4];                // bins, 8 bits each
+};
+
+__device__ __forceinline__ float rt_g(const RankTile& c, int j) {
+    const float4 v = c.g[j >> 2];
+    return (j & 3) == 0 ? v.x : (j & 3) == 1 ? v.y : (j & 3) == 2 ? v.z : v.w;
+}
+__device__ __forceinline__ float rt_h(const RankTile& c, int j) {
+    const float4 v = c.h[j >> 2];
+    return (j & 3) == 0 ? v.x : (j & 3) == 1 ? v.y : (j & 3) == 2 ? v.z : v.w;
+}
+__device__ __forceinline__ uint32_t rt_rank(const RankTile& c, int j) {
+    const uint32_t w = (j & 2) ? c.r[j >> 2].y : c.r[j >> 2].x;
+    return (j & 1) ? (w >> 16) : (w & 0xffffu);
+}
+__device__ __forceinline__ uint32_t rt_bin(const RankTile& c, int j) { return (c.bw[j >> 2] >> (8 * (j & 3))) & 0xffu; }
+
+// A whole tile ((t + 1) WT <= n) with 16-byte aligned g, h and bins: loads
+// only, no branch (a branch joining a second way of filling the tile would
+// make the compiler wait for these loads right here).
+__device__ __forceinline__ void rank_tile_load_vec(RankTile& c, const float* __restrict__ g,
+                                                   const float* __restrict__ h, const uint8_t* __restrict__ bn,
+                                                   const uint16_t* __restrict__ rk, int64_t t, int slot) {
+    static_assert(TPT == 16, "four groups of four positions per thread");
+    const int64_t x0 = t * WT + 4 * (int64_t)slot;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c.g[q] = *reinterpret_cast<const float4*>(g + x0 + q * 4 * RB);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c.h[q] = *reinterpret_cast<const float4*>(h + x0 + q * 4 * RB);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c.r[q] = *reinterpret_cast<const uint2*>(rk + x0 + q * 4 * RB);
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c.bw[q] = *reinterpret_cast<const uint32_t*>(bn + x0 + q * 4 * RB);
+}
+
+// Any tile, one position at a time (the last, partial tile, or unaligned data).
+__device__ __forceinline__ void rank_tile_load_any(RankTile& c, const float* __restrict__ g,
+                                                   const float* __restrict__ h, const uint8_t* __restrict__ bn,
+                                                   const uint16_t* __restrict__ rk, int64_t t, int64_t n, int slot) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int64_t x = t * WT + (int64_t)q * 4 * RB + 4 * (int64_t)slot;
+        float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, hv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+        uint32_t rv[4] = {0xffffu, 0xffffu, 0xffffu, 0xffffu}, bv = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            if (x + k < n) {
+                gv[k] = g[x + k];
+                hv[k] = h[x + k];
+                rv[k] = rk[x + k];
+                bv |= (uint32_t)bn[x + k] << (8 * k);
+            }
+        }
+        c.g[q] = make_float4(gv[0], gv[1], gv[2], gv[3]);
+        c.h[q] = make_float4(hv[0], hv[1], hv[2], hv[3]);
+        c.r[q] = make_uint2(rv[0] | (rv[1] << 16), rv[2] | (rv[3] << 16));
+        c.bw[q] = bv;
+    }
+}
+
+// A producer's window [w0, w0 + RW) of its tile's entries into T[rank - w0][bin].
+__device__ __forceinline__ void rank_stage(const RankTile& c, float2 (*T)[NB], uint32_t w0) {
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) {
+        // a rank below w0 wraps above RW; past the rows the rank is 0xffff
+        const uint32_t rank = rt_rank(c, j), r = rank - w0;
+        if (rank != 0xffffu && r < (uint32_t)RW) T[r][rt_bin(c, j)] = make_float2(rt_g(c, j), rt_h(c, j));
+    }
+}
+
+// Block f: the root's fp32 cells of feature f, cgrow's row-order chains
+// (grow.c:37-62); the count cell is cgrow's chain of 1.0f adds,
+// min(count, 2^24).  Threads 0 .. RB - 1 are the consumers, thread b adding
+// bin b's run of each tile in rank order from an LDS table T[rank][bin];
+// threads RB .. 2 RB - 1 are the producers, filling the other of two tables
+// with the next tile meanwhile (window 0 of every tile; a tile whose longest
+// run passes RW has its further windows staged and added in turn, its
+// positions reloaded).  The producers' next tiles load two tiles ahead.  VEC:
+// g, h and the bins are 16-byte aligned (every feature's column:
+// ld_fm % 16 == 0).
+template <bool VEC>
+__global__ void __launch_bounds__(2 * RB) k_rank_chain(const float* __restrict__ g, const float* __restrict__ h,
+                                                       const uint8_t* __restrict__ bins_fm, int64_t ld_fm, int64_t n,
+                                                       RootOrder o, float* __restrict__ hist, int F) {
+    __shared__ float2 T[2][RW][NB];
+    const int f = blockIdx.x;
+    const bool prod = threadIdx.x >= RB;
+    const int lt = threadIdx.x & (RB - 1);   // consumers: the bin; producers: the position slot
+    const uint8_t* bn = bins_fm + (size_t)f * (size_t)ld_fm;
+    const uint16_t* rk = o.rank + (size_t)f * (size_t)o.ld_rank;
+    const uint16_t* sf = o.starts + (size_t)f * (size_t)o.tiles * ST;
+    const uint16_t* mx = o.maxrun + (size_t)f * (size_t)o.tiles;
+    const int64_t tiles = (n + WT - 1) / WT;
+    const int64_t full = VEC ? n / WT : 0;      // tiles the producers load with 16-byte loads
+    float ag = 0.0f, ah = 0.0f;
+    int64_t cnt = 0;
+    // consumer: window [w0, w0 + RW) of tile t's run of bin lt from table Tb;
+    // steps to the tile's longest run in the window (uniform), eight reads in
+    // flight; past this thread's run a step adds +0.0f, which leaves the sums'
+    // bits unchanged (a sum that starts at +0.0f is never -0.0f)
+    auto run = [&](float2 (*Tb)[NB], uint32_t len, uint32_t mr, uint32_t w0) {
+        const uint32_t kend = min(len > w0 ? len - w0 : 0u, (uint32_t)RW);
+        const uint32_t kmax = min(mr - w0, (uint32_t)RW);
+        for (uint32_t r = 0; r < kmax; r += 8) {
+            float2 v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = Tb[r + u][lt];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const bool in = r + u < kend;
+                ag += in ? v[u].x : 0.0f;
+                ah += in ? v[u].y : 0.0f;
+            }
+        }
+    };
+    auto load = [&](RankTile& c, int64_t t) {
+        if (t < full)
+            rank_tile_load_vec(c, g, h, bn, rk, t, lt);
+        else
+            rank_tile_load_any(c, g, h, bn, rk, t, n, lt);
+    };
+    // producers: tile 0's window 0, and the ring (tiles 1 and 2)
+    RankTile A, B;
+    if (prod && tiles > 0) {
+        RankTile c;
+        load(c, 0);
+        rank_stage(c, T[0], 0);
+    }
+    if (prod && full > 0) {
+        rank_tile_load_vec(A, g, h, bn, rk, min((int64_t)1, full - 1), lt);
+        rank_tile_load_vec(B, g, h, bn, rk, min((int64_t)2, full - 1), lt);
+    }
+    __syncthreads();
+    // step t: the consumers add tile t's window 0 from T[t & 1] while the
+    // producers stage tile t + 1's from ring slot R (then reload R with tile
+    // t + 3); then tile t's further windows, if any
+    auto step = [&](int64_t t, RankTile& R) {
+        if (t >= tiles) return;
+        const uint32_t mr = (uint32_t)__builtin_amdgcn_readfirstlane((int)mx[t]);
+        uint32_t len = 0;
+        if (!prod) {
+            const uint16_t* st = sf + (size_t)t * ST;
+            len = (uint32_t)st[lt + 1] - (uint32_t)st[lt];
+            run(T[t & 1], len, mr, 0);
+            cnt += len;
+        } else if (t + 1 < tiles) {
+            if (t + 1 < full) {
+                rank_stage(R, T[(t + 1) & 1], 0);
+            } else {
+                RankTile c;
+                rank_tile_load_any(c, g, h, bn, rk, t + 1, n, lt);
+                rank_stage(c, T[(t + 1) & 1], 0);
+            }
+        }
+        if (prod && full > 0) rank_tile_load_vec(R, g, h, bn, rk, min(t + 3, full - 1), lt);
+        __syncthreads();
+        for (uint32_t w0 = RW; w0 < mr; w0 += RW) {
+            if (prod) {
+                RankTile c;
+                load(c, t);
+                rank_stage(c, T[t & 1], w0);
+            }
+            __syncthreads();
+            if (!prod) run(T[t & 1], len, mr, w0);
+            __syncthreads();
+        }
+    };
+    for (int64_t t = 0; t < tiles; t += 2) {
+        step(t, A);
+        step(t + 1, B);
+    }
+    if (!prod) {
+        hist[(size_t)f * NB + lt] = ag;
+        hist[(size_t)F * NB + (size_t)f * NB + lt] = ah;
+        hist[(size_t)2 * F * NB + (size_t)f * NB + lt] = (float)min(cnt, (int64_t)1 << 24);
+    }
+}
+
+inline void launch_rank_chain(const float* g, const float* h, const uint8_t* bins_fm, int64_t ld_fm, int64_t n,
+                              const RootOrder& o, float* hist, int F, hipStream_t stream) {
+    const bool vec = ((uintptr_t)g % 16 == 0) && ((uintptr_t)h % 16 == 0) && ((uintptr_t)bins_fm % 16 == 0) &&
+                     (ld_fm % 16 == 0);
+    if (vec)
+        k_rank_chain<true><<<F, 2 * RB, 0, stream>>>(g, h, bins_fm, ld_fm, n, o, hist, F);
+    else
+        k_rank_chain<false><<<F, 2 * RB, 0, stream>>>(g, h, bins_fm, ld_fm, n, o, hist, F);
+}
+
 // Sparse builder's default-bin cells (grow.c:101-106): 0 + (float)(node sum -
 // explicit sum) for g and h, 0 + (float)(rows in the default bin) for the count.
 // Block (., k): job k's built child.
@@ -1103,6 +1425,38 @@ using namespace yabt::ref;
 
 extern "C" {
 
+size_t yabt_ref_root_order_bytes(int64_t n, int F) {
+    if (n < 0 || n > 0xFFFFFFFFll || F < 1) return 0;
+    return root_order_carve(nullptr, n, F, nullptr);
+}
+
+int yabt_ref_root_order(const uint8_t* bins_fm, int64_t ld_fm, int64_t n, int F, void* out, size_t out_bytes,
+                        hipStream_t stream) {
+    if (n < 0 || n > 0xFFFFFFFFll || F < 1) return fail(-2, "yabt_ref_root_order: bad sizes");
+    if (!out || (n > 0 && (!bins_fm || ld_fm < n))) return fail(-2, "yabt_ref_root_order: bad pointer or layout");
+    if (out_bytes < root_order_carve(nullptr, n, F, nullptr))
+        return fail(-2, "yabt_ref_root_order: output buffer too small");
+    if (n == 0) return 0;
+    RootOrder o;
+    root_order_carve((char*)out, n, F, &o);
+    const unsigned ty = (unsigned)min((int64_t)65535, o.tiles);
+    k_root_rank<<<dim3((unsigned)F, ty), RB, 0, stream>>>(bins_fm, ld_fm, n, o);
+    return launch_status("yabt_ref_root_order launch");
+}
+
+int yabt_ref_root_hist(const uint8_t* bins_fm, int64_t ld_fm, const float* grad, const float* hess, int64_t n, int F,
+                       const void* root_order, size_t root_order_bytes, float* out, hipStream_t stream) {
+    if (n < 0 || n > 0xFFFFFFFFll || F < 1) return fail(-2, "yabt_ref_root_hist: bad sizes");
+    if (!out || !root_order || (n > 0 && (!bins_fm || !grad || !hess || ld_fm < n)))
+        return fail(-2, "yabt_ref_root_hist: bad pointer or layout");
+    if (root_order_bytes < root_order_carve(nullptr, n, F, nullptr))
+        return fail(-2, "yabt_ref_root_hist: root_order smaller than yabt_ref_root_order_bytes(n, F)");
+    RootOrder o;
+    root_order_carve((char*)const_cast<void*>(root_order), n, F, &o);
+    launch_rank_chain(grad, hess, bins_fm, ld_fm, n, o, out, F, stream);
+    return launch_status("yabt_ref_root_hist launch");
+}
+
 size_t yabt_grow_ref_workspace_bytes(int64_t n, int F, int max_leaves, int sparse) {
     if (n < 0 || n > 0xFFFFFFFFll || F < 1 || max_leaves < 1 || max_leaves > 32767) return 0;
     return carve(nullptr, n, F, max_leaves, sparse != 0, recommended_group(n, F, max_leaves, sparse != 0)).bytes;
@@ -1117,7 +1471,7 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
                   const float* hess, const uint8_t* fmask, const float* imat, float ib, int use_imat,
                   const int32_t* nbins, const int32_t* default_bin, int64_t n, int F, float lam, float gamma,
                   float mcw, int msl, float lr, int max_leaves, int max_depth, void* workspace,
-                  size_t workspace_bytes, int64_t* out_feature,
+                  size_t workspace_bytes, const void* root_order, int64_t* out_feature,
                   int64_t* out_thr_bin, int64_t* out_left, int64_t* out_right, float* out_value, int64_t* out_depth,
                   int64_t* out_leaf_of_row, int64_t* out_rows, int32_t* out_n_nodes, hipStream_t stream) {
     if (n < 0 || n > 0xFFFFFFFFll || F < 1 || max_leaves < 1 || max_leaves > 32767)
@@ -1244,7 +1598,13 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
         J.cs = 0;
         J.ce = n;
         if ((rc = launch_round())) return rc;
-        g.hist(true, 1, R.toff[1], grad, hess);
+        if (root_order && !sparse && n > 0) {
+            RootOrder o;
+            root_order_carve((char*)const_cast<void*>(root_order), n, F, &o);
+            launch_rank_chain(grad, hess, bins_fm, ld_fm, n, o, w.hist, F, stream);
+        } else {
+            g.hist(true, 1, R.toff[1], grad, hess);
+        }
         k_scan_feature<<<dim3(F, 1), WAVE, 0, stream>>>(w.hist, g.hsz, w.round, 1, w.path, P, w.fsel, w.fgain, w.fb);
         k_scan_pick<<<1, WAVE, 0, stream>>>(w.hist, g.hsz, w.round, 1, F, w.fsel, w.fgain, w.fb, lr, (double)lam,
                                              d_res);

@@ -76,6 +76,7 @@ class BinLayouts:
         self.ld_rm = rm.shape[1]
         self._default = None
         self._counts = None
+        self._root_order = None
 
     def counts(self) -> torch.Tensor:
         """Per-(feature, bin) row counts (F, 256) uint32 of the bins, counted
@@ -90,6 +91,23 @@ class BinLayouts:
                        "yabt_bin_counts")
             self._counts = c
         return self._counts
+
+    def ref_root_order(self) -> torch.Tensor:
+        """The root rank table of the reference-arithmetic grower's dense
+        builder (yabt_ref_root_order), built once per layout: each row's rank
+        in its bin inside its 4096-row tile, per feature, which every tree's
+        root histogram on these bins reuses."""
+        if self._root_order is None:
+            lib = _lib.load()
+            dev = self.fm.device
+            nbytes = int(lib.yabt_ref_root_order_bytes(self.n, self.F))
+            if nbytes == 0:
+                raise ValueError("yabt_ref_root_order: invalid sizes")
+            buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+            _lib.check(lib.yabt_ref_root_order(_ptr(self.fm), self.ld_fm, self.n, self.F, _ptr(buf), nbytes,
+                                               _stream(dev)), "yabt_ref_root_order")
+            self._root_order = buf
+        return self._root_order
 
     # a default bin is skipped only where it holds at least this share of the
     # sampled rows; below it the per-update test costs more than it saves
@@ -383,12 +401,14 @@ def _grow_device_level(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, l
 
 
 def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam, gamma, mcw, msl, lr,
-                     max_leaves, max_depth, default_bin=None, workspace_bytes=None) -> GrowResult:
+                     max_leaves, max_depth, default_bin=None, workspace_bytes=None,
+                     root_order: bool = True) -> GrowResult:
     """yabt_grow_ref: cgrow's arithmetic on the device (synchronous);
     default_bin selects cgrow's sparse builder.  workspace_bytes (None: the
     library's recommended size) may be anything from
     yabt_grow_ref_workspace_min_bytes up: features are bucketed in groups
-    that fit."""
+    that fit.  root_order: the dense builder's root reads the layout's cached
+    rank table (BinLayouts.ref_root_order) instead of bucketing every tree."""
     lib = _lib.load()
     dev = lay.fm.device
     n, F = lay.n, lay.F
@@ -417,6 +437,7 @@ def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam
     if workspace_bytes is not None:
         nbytes = int(workspace_bytes)
     ws = _workspace(dev, nbytes)
+    ro = lay.ref_root_order() if (root_order and db is None and n > 0) else None
     out_i = torch.empty((5, N), dtype=torch.int64, device=dev)
     value = torch.empty(N, dtype=torch.float32, device=dev)
     leaf = torch.empty(max(n, 1), dtype=torch.int64, device=dev)
@@ -426,7 +447,7 @@ def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam
         _ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h), _ptr(fm), _ptr(im),
         ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), _ptr(db), n, F,
         ctypes.c_float(float(lam)), ctypes.c_float(float(gamma)), ctypes.c_float(float(mcw)),
-        int(msl), ctypes.c_float(float(lr)), L, int(max_depth), _ptr(ws), nbytes,
+        int(msl), ctypes.c_float(float(lr)), L, int(max_depth), _ptr(ws), nbytes, _ptr(ro),
         _ptr(out_i[0]), _ptr(out_i[1]), _ptr(out_i[2]), _ptr(out_i[3]), _ptr(value), _ptr(out_i[4]),
         _ptr(leaf), _ptr(rows), _ptr(nn), _stream(dev))
     _lib.check(rc, "yabt_grow_ref")
@@ -565,6 +586,21 @@ def hist(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor,
                              _stream(dev)), "yabt_hist")
     s = shifts.cpu().tolist()
     return out, (int(s[0]), int(s[1]))
+
+
+def ref_root_hist(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor) -> torch.Tensor:
+    """The root's (3, F, 256) float32 histogram in the reference arithmetic
+    (cgrow's row-order fp32 sums, grow.c:37-62), from the layout's cached
+    root rank table."""
+    lib = _lib.load()
+    dev = lay.fm.device
+    g = _dev_f32(grad, dev)
+    h = _dev_f32(hess, dev)
+    ro = lay.ref_root_order()
+    out = torch.empty((3, lay.F, MAX_BINS), dtype=torch.float32, device=dev)
+    _lib.check(lib.yabt_ref_root_hist(_ptr(lay.fm), lay.ld_fm, _ptr(g), _ptr(h), lay.n, lay.F, _ptr(ro),
+                                      ro.numel(), _ptr(out), _stream(dev)), "yabt_ref_root_hist")
+    return out
 
 
 def best_split(qhist: torch.Tensor, sg: int, sh: int, nbins=None, lam=1.0, gamma=0.0, mcw=1e-3,
