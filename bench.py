@@ -22,8 +22,9 @@ Also reported:
     algorithmic bytes per launch = n*F (bins) + 8n (fp32 g, h) = 1.08 GB;
   * cpu_baseline: the reference grow.c (compiled from the reference sources
     into oracle/_ref/, kind "reference") or, if that library is absent, the
-    oracle's restatement of it (kind "port"), on a bounded row sample of the
-    same workload, timed on this host's cores.
+    oracle's restatement of it (kind "port"), on one tree of the full
+    10M x 100 workload (host RNG inputs of the same distribution), timed on
+    this host's cores with the host's CPU model and core count.
 
 ``roofline.traffic`` (HBM bytes per root-histogram launch) is read from the
 committed counter summary profiles/k_hist_root_10Mx100_traffic.md, made by two
@@ -214,13 +215,56 @@ def committed_traffic():
         return None
 
 
+def host_cpu() -> dict:
+    """The host's CPU model, physical cores and the logical CPUs this process
+    may use (from /proc/cpuinfo and the affinity mask)."""
+    model, cores = None, set()
+    phys = core = None
+    try:
+        with open("/proc/cpuinfo") as fh:
+            for line in fh:
+                k, _, v = line.partition(":")
+                k, v = k.strip(), v.strip()
+                if k == "model name" and model is None:
+                    model = v
+                elif k == "physical id":
+                    phys = v
+                elif k == "core id":
+                    core = v
+                elif not k and phys is not None and core is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+        if phys is not None and core is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    logical = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return {"model": model, "physical_cores": len(cores) or None, "logical_cpus": logical}
+
+
+def tree_updates_cpu(O, reference, bins_fm, res, threads, chunk=1_000_000) -> int:
+    """Histogram work of a CPU-grown tree (as tree_updates), its per-row leaf
+    ids routed in row chunks (fp32 copies of the bins, one chunk at a time)."""
+    F, n = bins_fm.shape
+    thr = np.where(res["feature"] >= 0, res["thr_bin"], 0).astype(np.float32)
+    leaf = np.empty(n, np.int64)
+    for r0 in range(0, n, chunk):
+        X = np.ascontiguousarray(bins_fm[:, r0:r0 + chunk].T, dtype=np.float32)
+        leaf[r0:r0 + chunk] = O.apply(X, res["feature"], thr, res["left"], res["right"], n_threads=threads,
+                                      reference=reference)
+    sizes = node_sizes(res["feature"], res["left"], res["right"], leaf)
+    return tree_updates(res["feature"], res["left"], res["right"], sizes, F)
+
+
 def cpu_baseline(budget_s: float = 20.0) -> dict:
-    """Reference grow.c (or its restatement) on a row sample of the workload."""
+    """Reference grow.c (or its restatement) on the full workload: one
+    255-leaf tree over the same 10M x 100 shape, host RNG inputs of the same
+    distribution."""
     from oracle import oracle as O
     reference = O.ref_available()
-    threads = min(os.cpu_count() or 1, 8)   # the reference default (grow_c.py:283-302)
-    F = N_FEAT
-    n = 1_000_000
+    cpu = host_cpu()
+    threads = min(cpu["logical_cpus"], 8)   # the reference default (grow_c.py:283-302)
+    F, n = N_FEAT, N_ROWS
     rng = np.random.default_rng(0)
     bins_fm = rng.integers(0, 256, size=(F, n), dtype=np.uint8)
     g = rng.normal(size=n).astype(np.float32)
@@ -237,24 +281,21 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
             break
     timed = times[1:] if len(times) > 1 else times
     sec = float(np.median(timed))
-    leaf = O.apply(bins_fm.T.astype(np.float32), res["feature"],
-                   np.where(res["feature"] >= 0, res["thr_bin"], 0).astype(np.float32),
-                   res["left"], res["right"], n_threads=threads)
-    sizes = node_sizes(res["feature"], res["left"], res["right"], leaf)
-    upd = tree_updates(res["feature"], res["left"], res["right"], sizes, F)
+    upd = tree_updates_cpu(O, reference, bins_fm, res, threads)
     out = {"value": round(upd / sec / 1e9, 4), "unit": "G row·feature updates/s",
            "cores": threads, "kind": "reference" if reference else "port",
            "ms_per_tree": round(sec * 1e3, 1),
-           "sample": f"one 255-leaf tree on 1,000,000 x 100 uniform u8 bins (1/10 of the rows), "
-                     f"{len(timed)} timed run(s) after 1 warm-up, median; {threads} OpenMP threads; "
-                     f"host has {os.cpu_count()} logical CPUs"}
-    # the same tree on every logical CPU of the host (one run after the warm-ups above)
-    all_threads = os.cpu_count() or 1
+           "sample": f"one 255-leaf tree on 10,000,000 x 100 uniform u8 bins (the full workload), "
+                     f"{len(timed)} timed run(s) after 1 warm-up, median; {threads} OpenMP threads",
+           "host_cpu": cpu}
+    # the same tree on every logical CPU the process may use
+    all_threads = cpu["logical_cpus"]
     t0 = time.perf_counter()
     O.grow(bins_fm, g, h, reference=reference, **dict(kw, n_threads=all_threads))
     sec_all = time.perf_counter() - t0
     out["all_cores"] = {"threads": all_threads, "ms_per_tree": round(sec_all * 1e3, 1),
                         "value": round(upd / sec_all / 1e9, 4)}
+    del bins_fm, g, h
     out["other_workloads"] = cpu_other_workloads(O, reference, threads)
     return out
 

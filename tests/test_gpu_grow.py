@@ -44,6 +44,8 @@ CASES = [
     # n > 2^18: packed root histogram, three channels and constant hessian
     dict(n=400_000, F=9, nb=256, kind="normal", max_leaves=63, msl=20),
     dict(n=400_000, F=9, nb=64, kind="laplace", max_leaves=63, msl=20),
+    # a 4-feature tail tile of the root (F % 16 = 4), odd n, constant hessian
+    dict(n=300_001, F=20, nb=256, kind="laplace", max_leaves=31, msl=20, skew=True),
 ]
 
 

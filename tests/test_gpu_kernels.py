@@ -39,6 +39,8 @@ def _hist_f64(bins, g, h):
     (65_536, 100, "logistic", False),
     # more rows per block than the 2048 a packed (q(g) << 32) + q(h) cell may take between unpacks
     (300_001, 20, "normal", False), (600_000, 7, "laplace", True), (1_048_577, 3, "logistic", False),
+    # tail tiles (F % 16 in 1..4: the last tile's features replicated over its columns), odd and even n
+    (2, 1, "normal", False), (3, 2, "normal", False), (2_500_001, 36, "normal", True), (777_777, 50, "laplace", False),
 ])
 def test_root_hist_exact(n, F, kind, skew):
     rng = np.random.default_rng(n + F)

@@ -1353,9 +1353,7 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
     k_quant_clear<<<1, 1, 0, stream>>>(A.q);
     k_setup<<<launch_grid(n, SB * 16, 1024), SB, 0, stream>>>(A);
     k_setup_finish<<<1, 1, 0, stream>>>(A);
-    const int rc = root_chunks(n, tiles);
-    launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, A.dflt, A.counts, A.q,
-                     A.hist, 1,
+    launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, A.dflt, A.counts, A.q, A.hist, 1,
                      &A.st->done);
     const int scan_grid = (F + SCAN_FEATS - 1) / SCAN_FEATS;
     const size_t table_lds = table_carve(nullptr, max_leaves, A.pend_cap, nullptr);

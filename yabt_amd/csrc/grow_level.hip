@@ -548,9 +548,8 @@ int yabt_grow_levelwise(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bi
         grad, hess, n, w.q, w.row_node, w.route, NP, w.path, (int64_t)NP * F, w.hist, (int64_t)slot_n);
     k_setup_finish<<<1, 1, 0, stream>>>(w.q, n, w.nodes, w.scan_list, out_status);
     if (n > 0) {
-        const int rc = root_chunks(n, tiles);
-        launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, w.q, 0.0, 0.0, nullptr, bin_counts, w.q,
-                         w.hist, 1, nullptr);
+        launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, w.q, 0.0, 0.0, nullptr, bin_counts, w.q, w.hist,
+                         1, nullptr);
     }
     k_root_tot<<<1, 1, 0, stream>>>(w.q, n, w.nodes);
     if (max_depth > 0) {

@@ -239,6 +239,58 @@ __device__ __forceinline__ void flush_cells_gh(RootFlushLds& T, const int64_t (&
     }
 }
 
+// Rows per chunk of the streaming root kernel's full tiles (whole block steps).
+__host__ __device__ inline int64_t root_chunk_rows(int64_t n, int chunks) {
+    return ((n + chunks - 1) / chunks + RSTEP - 1) / RSTEP * RSTEP;
+}
+
+constexpr int TAILF = 4;                 // features of a tail tile, at most
+constexpr int TSTEP = 2 * RBLOCK;        // rows per tail block step (128 per wave)
+
+// Grid of the streaming root kernel: `tail` blocks for the tail tile (block
+// ids 0 .. tail - 1, tail_rows rows each), then `tiles` full 16-feature tiles
+// of `chunks` row chunks each.  The last tile is a tail tile when it holds
+// 1..TAILF features and g and h can be read in aligned pairs (8-byte aligned,
+// n >= 2).  One 1024-thread block runs per CU, so the grid aims at two waves
+// of 256 blocks of equal length: a tail block's row costs about 3/8 of a full
+// block's (a quarter of the LDS atomics, with more VALU work per atomic), so
+// the tail counts as 3/8 of a tile when the chunks are sized, and its blocks
+// fill the rest of the 512 (at least 3/8 of a tile's worth).  chunks is a
+// multiple of 8, so every full tile of a row chunk runs on one XCD (block id
+// % 8) and shares its L2 for the chunk's g and h; the tail blocks read theirs
+// on their own.
+struct RootGrid {
+    int tiles, chunks, tail, blocks;
+    int64_t tail_rows;
+};
+
+inline RootGrid root_grid(int64_t n, int F, const void* grad, const void* hess) {
+    constexpr int SLOTS = 512;
+    const int rem = F % HFL;
+    const bool tail = rem >= 1 && rem <= TAILF && n >= 2 && (uintptr_t)grad % 8 == 0 && (uintptr_t)hess % 8 == 0;
+    RootGrid g;
+    g.tiles = tail ? F / HFL : (F + HFL - 1) / HFL;
+    g.chunks = 8;
+    if (g.tiles > 0) {
+        int want = tail ? 8 * SLOTS / (8 * g.tiles + 3) : SLOTS / g.tiles;
+        const int64_t useful = (n + RSTEP - 1) / RSTEP;
+        if (want > useful) want = (int)useful;
+        want = want / 8 * 8;
+        g.chunks = want < 8 ? 8 : want;
+    }
+    g.tail = 0;
+    g.tail_rows = 0;
+    if (tail) {
+        const int fill = SLOTS - g.tiles * g.chunks;
+        int64_t t = max(fill, (3 * g.chunks + 7) / 8);
+        t = min(t, (n + TSTEP - 1) / TSTEP);   // no empty tail block
+        g.tail_rows = ((n + t - 1) / t + TSTEP - 1) / TSTEP * TSTEP;
+        g.tail = (int)((n + g.tail_rows - 1) / g.tail_rows);
+    }
+    g.blocks = g.tail + g.tiles * g.chunks;
+    return g;
+}
+
 constexpr int ROOT_DEPTH = 4;    // steps of inputs loaded ahead of the adds
 constexpr int ROOT_UNPACK = 2;   // steps per epoch: 2 x 1024 = 2048 rows, hist_shift's bound
 constexpr bool ROOT_DBUF = true;   // two cell buffers (one barrier per epoch) or one (two barriers)
@@ -250,14 +302,14 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
                                              const float* __restrict__ grad, const float* __restrict__ hess,
                                              int64_t n, int F, double scg, double sch,
                                              const int32_t* __restrict__ dflt, const uint32_t* __restrict__ counts,
-                                             Quant* q_tot, int64_t* out, int chunks) {
-    const int tile = blockIdx.x / chunks, chunk = blockIdx.x % chunks;
+                                             Quant* q_tot, int64_t* out, int chunks, int bid) {
+    const int tile = bid / chunks, chunk = bid % chunks;
     const int f0 = tile * HFL;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const int fl = lane & (HFL - 1), rg = lane / HFL;
     const int f = f0 + fl;
     const bool fok = f < F;
-    const int64_t per = ((n + chunks - 1) / chunks + RSTEP - 1) / RSTEP * RSTEP;
+    const int64_t per = root_chunk_rows(n, chunks);
     const int64_t lo = (int64_t)chunk * per, hi = min(n, lo + per);
     if (f0 >= F || lo >= hi) return;
     const int d = (SKIP && fok) ? dflt[f] : -1;
@@ -394,6 +446,214 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
                         SKIP ? dflt : nullptr, out, F, f0);
 }
 
+// ---------------------------------------------------------------------------
+// Streaming root histogram of a tail tile: the last tile when it holds at
+// most TAILF = 4 features (F % 16 in 1..4), where the full kernel's lanes of
+// 12 or more of the 16 columns would add into cells the flush ignores.  Here
+// the 16 columns hold the tail's 4 features 4 times over (column 4 a + c:
+// feature f0 + c, replica a), lane 16 qw + 4 a + c adds feature c for
+// replica a, and the replicas take different rows, so every lane adds a live
+// feature and the 16 lanes of a quarter wave still hit 16 distinct columns
+// (bank pairs).  A wave step covers 128 rows: replica a of quarter qw takes
+// rows rA = r0 + 32 qw + 8 a .. rA + 7 (one 8-byte load of the lane's
+// feature's bins); lane (a, c) loads g and h of rows rA + 2 c and rA + 2 c + 1
+// (8-byte loads), and the J-th add of a replica's lanes takes row rA + J's
+// word from lane (a, J / 2) of the quad with a DPP quad_perm.  A block step
+// is 2048 rows, 512 per column, so an epoch (2048 rows of a cell between two
+// unpacks) is 4 steps: one round of the ring, whose cell buffer alternates by
+// round.  The flush sums a feature's 4 replicas before its global atomics.
+// Block tb takes rows [tb span, (tb + 1) span), span a multiple of 2048.  The
+// loop adds rows below n rounded down to even (the pairs); an odd n's last
+// row is added after it.
+// ---------------------------------------------------------------------------
+
+// This lane's copy of the 64-bit word of lane S of its quad (DPP quad_perm).
+template <int S>
+__device__ __forceinline__ uint64_t quad_bcast64(uint64_t v) {
+    constexpr int CTRL = S * 0x55;   // quad_perm [S, S, S, S]
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)v, CTRL, 0xf, 0xf, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_mov_dpp((int)(uint32_t)(v >> 32), CTRL, 0xf, 0xf, false);
+    return ((uint64_t)hi << 32) | lo;
+}
+
+// Final flush of a tail block: as flush_cells_gh, with each feature's 4
+// replica columns summed first (thread j: feature f0 + j / 256, bin j % 256).
+template <bool HCH>
+__device__ __forceinline__ void flush_tail_gh(RootFlushLds& T, const int64_t (&g)[RENT], const int64_t (&h)[RENT],
+                                              const uint32_t* __restrict__ counts,
+                                              const int32_t* __restrict__ dflt, int64_t* out, int F, int f0) {
+    static_assert(TAILF * NB == RBLOCK, "one thread per (tail feature, bin)");
+#pragma unroll
+    for (int k = 0; k < RENT; ++k) {
+        const int i = threadIdx.x + k * RBLOCK;
+        const int fl = i % HFL;
+        const int j = fl * NB + ((i / HFL) ^ (2 * fl));
+        T.g[j] = (unsigned long long)g[k];
+        if (HCH) T.h[j] = (unsigned long long)h[k];
+    }
+    __syncthreads();
+    const int c = threadIdx.x / NB, b = threadIdx.x % NB;
+    const int fi = f0 + c;
+    if (fi >= F) return;
+    unsigned long long sg = 0, sh = 0;
+#pragma unroll
+    for (int a = 0; a < HFL / TAILF; ++a) {
+        const int fl = c + TAILF * a;
+        const int j = fl * NB + (b ^ (2 * fl));
+        sg += T.g[j];
+        if (HCH) sh += T.h[j];
+    }
+    const size_t plane = (size_t)F * NB;
+    const size_t at = (size_t)fi * NB + (size_t)b;
+    if (sg) atomicAdd((unsigned long long*)(out + at), sg);
+    if (HCH && sh) atomicAdd((unsigned long long*)(out + plane + at), sh);
+    if (counts) {
+        const uint32_t cj = counts[at];
+        const int d = dflt ? dflt[fi] : -1;   // the default bin's count is left to the caller's fill
+        if (cj && b != d) atomicAdd((unsigned long long*)(out + 2 * plane + at), (unsigned long long)cj);
+    }
+}
+
+template <bool HCH, bool SKIP>
+__device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __restrict__ bins_fm, int64_t ld,
+                                               const float* __restrict__ grad, const float* __restrict__ hess,
+                                               int64_t n, int F, double scg, double sch,
+                                               const int32_t* __restrict__ dflt,
+                                               const uint32_t* __restrict__ counts, Quant* q_tot, int64_t* out,
+                                               int64_t span, int tb) {
+    const int f0 = F / HFL * HFL;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int col = lane & (HFL - 1), c = lane & (TAILF - 1), a = col / TAILF, qw = lane / HFL;
+    const int f = f0 + c;
+    const bool fok = f < F;
+    const int64_t lo = (int64_t)tb * span, hi = min(n, lo + span);
+    if (lo >= hi) return;
+    const int64_t n2 = n & ~(int64_t)1;   // the loop adds rows [lo, hi2): whole pairs
+    const int64_t hi2 = min(hi, n2);
+    const int d = (SKIP && fok) ? dflt[f] : -1;
+    const bool totals = q_tot != nullptr && f0 == 0;
+    for (int i = threadIdx.x; i < NB * 2 * HFL; i += RBLOCK) L.w[i] = 0;
+    const uint32_t lbase = (uint32_t)col << 3;
+    char* const lds = reinterpret_cast<char*>(L.w);
+    int64_t ag[RENT], ah[RENT];
+#pragma unroll
+    for (int k = 0; k < RENT; ++k) ag[k] = ah[k] = 0;
+    auto cell = [](int k) { const int i = threadIdx.x + k * RBLOCK; return (i / HFL) * (2 * HFL) + (i % HFL); };
+    auto unpack = [&](int p) {
+#pragma unroll
+        for (int k = 0; k < RENT; ++k) {
+            const int cc = cell(k) + p * HFL;
+            const uint64_t v = L.w[cc];
+            L.w[cc] = 0;
+            const int64_t hs = (int64_t)(int32_t)(uint32_t)v;
+            ah[k] += hs;
+            ag[k] += (int64_t)(v - (uint64_t)hs) >> 32;
+        }
+    };
+    const uint8_t* colp = bins_fm + (size_t)(fok ? f : f0) * ld;
+    // Inputs of step s (unconditional loads, as in hist_root_gh): g and h of
+    // this lane's row pair, clamped to the last whole pair (n2 >= 2, so the
+    // 8-byte loads stay inside the arrays), and 8 rows of its feature's bins:
+    // rA % 8 == 0 and rA < hi <= n <= ld (ld % 16 == 0), or lo when past hi.
+    auto load = [&](int64_t s, float2& gv, float2& hv, uint2& bw) {
+        const int64_t rA = lo + s * TSTEP + (int64_t)wave * (2 * WAVE) + 32 * qw + 8 * a;
+        const int64_t p = min(rA + 2 * c, n2 - 2);
+        gv = *reinterpret_cast<const float2*>(grad + p);
+        if (HCH) hv = *reinterpret_cast<const float2*>(hess + p);
+        bw = *reinterpret_cast<const uint2*>(colp + (rA < hi ? rA : lo));
+    };
+    const int64_t steps = (hi - lo + TSTEP - 1) / TSTEP;
+    float2 gs[ROOT_DEPTH], hs[ROOT_DEPTH];
+    uint2 bs[ROOT_DEPTH];
+#pragma unroll
+    for (int j = 0; j < ROOT_DEPTH; ++j) {
+        gs[j] = make_float2(0.0f, 0.0f);
+        hs[j] = make_float2(0.0f, 0.0f);
+        bs[j] = make_uint2(0, 0);
+    }
+    __syncthreads();
+    int64_t sum_g = 0, sum_h = 0;
+    uint32_t buf = 0;   // the cell buffer of this ring round's epoch
+    for (int64_t s0 = -ROOT_DEPTH; s0 < steps; s0 += ROOT_DEPTH) {
+        const uint32_t lb = HCH ? (lbase | (buf << 7)) : lbase;
+#pragma unroll
+        for (int j = 0; j < ROOT_DEPTH; ++j) {
+            const int64_t s = s0 + j;
+            __builtin_amdgcn_sched_barrier(0);
+            const int64_t p = lo + s * TSTEP + (int64_t)wave * (2 * WAVE) + 32 * qw + 8 * a + 2 * c;
+            const bool ok0 = s >= 0 && p < hi2, ok1 = s >= 0 && p + 1 < hi2;
+            const int64_t g0 = ok0 ? quantise_node(gs[j].x, scg) : 0;
+            const int64_t g1 = ok1 ? quantise_node(gs[j].y, scg) : 0;
+            const int64_t h0 = (HCH && ok0) ? quantise_node(hs[j].x, sch) : 0;
+            const int64_t h1 = (HCH && ok1) ? quantise_node(hs[j].y, sch) : 0;
+            const uint32_t wv[2] = {bs[j].x, bs[j].y};
+            uint32_t at[8];
+            uint32_t keep = 0xffu;
+#pragma unroll
+            for (int J = 0; J < 8; ++J) {
+                at[J] = bin_addr_rt(wv[J >> 2], lb, J & 3);
+                if (SKIP && (int)((wv[J >> 2] >> (8 * (J & 3))) & 0xffu) == d) keep &= ~(1u << J);
+            }
+            load(s + ROOT_DEPTH, gs[j], hs[j], bs[j]);
+            sum_g += g0 + g1;
+            sum_h += h0 + h1;
+            const uint64_t w0 = HCH ? ((uint64_t)g0 << 32) + (uint64_t)h0 : (uint64_t)g0;
+            const uint64_t w1 = HCH ? ((uint64_t)g1 << 32) + (uint64_t)h1 : (uint64_t)g1;
+#define YABT_TAIL_ADD(J)                                                         \
+            {                                                                    \
+                const uint64_t wj = quad_bcast64<(J) / 2>(((J) & 1) ? w1 : w0);  \
+                unsigned long long* const cp = reinterpret_cast<unsigned long long*>(lds + at[J]); \
+                if (!SKIP || ((keep >> (J)) & 1u)) atomicAdd(cp, (unsigned long long)wj); \
+            }
+            YABT_TAIL_ADD(0) YABT_TAIL_ADD(1) YABT_TAIL_ADD(2) YABT_TAIL_ADD(3)
+            YABT_TAIL_ADD(4) YABT_TAIL_ADD(5) YABT_TAIL_ADD(6) YABT_TAIL_ADD(7)
+#undef YABT_TAIL_ADD
+        }
+        if (HCH) {
+            // end of the epoch: read this round's buffer while the next round
+            // adds into the other one
+            __syncthreads();
+            unpack((int)buf);
+            buf ^= 1u;
+        }
+    }
+    // an odd n's last row, in the block that holds it (a block-uniform test)
+    if (n2 < n && hi == n) {
+        if (wave == 0 && qw == 0 && a == 0) {   // lanes c = 0 .. 3: one per feature
+            const int64_t r = n - 1;
+            const int64_t gq = quantise_node(grad[r], scg);
+            const int64_t hq = HCH ? quantise_node(hess[r], sch) : 0;
+            if (c == 0) {
+                sum_g += gq;
+                sum_h += hq;
+            }
+            const uint32_t b = colp[r];
+            const uint64_t word = HCH ? ((uint64_t)gq << 32) + (uint64_t)hq : (uint64_t)gq;
+            const uint32_t lb = HCH ? (lbase | (buf << 7)) : lbase;
+            if (!SKIP || (int)b != d)
+                atomicAdd(reinterpret_cast<unsigned long long*>(lds + ((b << 8) | lb)), (unsigned long long)word);
+        }
+        __syncthreads();
+        if (HCH) unpack((int)buf);
+    }
+    __syncthreads();
+    if (!HCH) {   // one buffer, never unpacked: the cells are the g sums
+#pragma unroll
+        for (int k = 0; k < RENT; ++k) ag[k] = (int64_t)L.w[cell(k)];
+    }
+    if (totals) {
+        sum_g = wave_sum<int64_t>(sum_g);
+        sum_h = wave_sum<int64_t>(sum_h);
+        if (lane == 0) {
+            atomicAdd((unsigned long long*)&q_tot->tot_g, (unsigned long long)sum_g);
+            atomicAdd((unsigned long long*)&q_tot->tot_h, (unsigned long long)sum_h);
+        }
+    }
+    __syncthreads();   // every cell read before the LDS is rewritten
+    flush_tail_gh<HCH>(*reinterpret_cast<RootFlushLds*>(&L), ag, ah, tb == 0 ? counts : nullptr,
+                       SKIP ? dflt : nullptr, out, F, f0);
+}
+
 // Bin counts of all n rows of the feature-major bins, per (feature, bin):
 // OUT64 false: added into a uint32 (F, 256) table (the per-fit counts);
 // OUT64 true: added into an int64 (F, 256) count plane.  dflt (may be NULL):
@@ -453,40 +713,55 @@ static __global__ __attribute__((unused)) void __launch_bounds__(RBLOCK)
 k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld, const float* __restrict__ grad,
             const float* __restrict__ hess, int64_t n, int F, const Quant* q, double scg_v, double sch_v,
             const int32_t* __restrict__ dflt, const uint32_t* __restrict__ counts, Quant* q_tot, int64_t* out,
-            int chunks, int count_mode, const int32_t* done) {
+            int chunks, int tail, int64_t tail_rows, int count_mode, const int32_t* done) {
     const int32_t dn = done ? *done : 0;
     const double scg = q ? q->scg : scg_v, sch = q ? q->sch : sch_v;
     const bool no_h = count_mode && q && q->const_h;
     if (dn) return;
     __shared__ HistLdsR L;   // 64 KB, also the flush's RootFlushLds
     static_assert(sizeof(RootFlushLds) <= sizeof(HistLdsR), "the flush reuses the cells' LDS");
+    const int bid = (int)blockIdx.x;
+    if (bid < tail) {
+        if (no_h)
+            hist_root_tail<false, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
+                                        tail_rows, bid);
+        else
+            hist_root_tail<true, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
+                                       tail_rows, bid);
+        return;
+    }
     if (no_h)
-        hist_root_gh<false, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks);
+        hist_root_gh<false, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks,
+                                  bid - tail);
     else
-        hist_root_gh<true, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks);
+        hist_root_gh<true, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks,
+                                 bid - tail);
 }
 
-// Launch the root histogram over `tiles * chunks` blocks into the (3, F, 256)
+// Launch the root histogram (grid from root_grid) into the (3, F, 256)
 // histogram `out` (cleared beforehand).  With counts == NULL the count plane
 // is counted from the bins first (k_bin_count, one more pass over them);
 // callers that keep the per-fit counts pass them instead.  The instantiation
 // with the default-bin test runs only when dflt is given.
-static __attribute__((unused)) void launch_hist_root(int tiles, int chunks, hipStream_t stream,
-                                                     const uint8_t* bins_fm, int64_t ld, const float* grad,
-                                                     const float* hess, int64_t n, int F, const Quant* q,
-                                                     double scg, double sch, const int32_t* dflt,
+static __attribute__((unused)) void launch_hist_root(hipStream_t stream, const uint8_t* bins_fm, int64_t ld,
+                                                     const float* grad, const float* hess, int64_t n, int F,
+                                                     const Quant* q, double scg, double sch, const int32_t* dflt,
                                                      const uint32_t* counts, Quant* q_tot, int64_t* out,
                                                      int count_mode, const int32_t* done) {
-    if (!counts)
-        k_bin_count<true><<<tiles * chunks, HBLOCK, 0, stream>>>(bins_fm, ld, n, F, dflt, out + (size_t)2 * F * NB,
-                                                                 chunks);
+    if (!counts) {
+        const int tiles = (F + HFL - 1) / HFL;
+        const int rc = root_chunks(n, tiles);
+        k_bin_count<true><<<tiles * rc, HBLOCK, 0, stream>>>(bins_fm, ld, n, F, dflt, out + (size_t)2 * F * NB, rc);
+    }
+    const RootGrid g = root_grid(n, F, grad, hess);
     if (dflt)
-        k_hist_root<true><<<tiles * chunks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, dflt,
-                                                                 counts, q_tot, out, chunks, count_mode, done);
+        k_hist_root<true><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, dflt, counts,
+                                                           q_tot, out, g.chunks, g.tail, g.tail_rows, count_mode,
+                                                           done);
     else
-        k_hist_root<false><<<tiles * chunks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch,
-                                                                  nullptr, counts, q_tot, out, chunks, count_mode,
-                                                                  done);
+        k_hist_root<false><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, nullptr,
+                                                            counts, q_tot, out, g.chunks, g.tail, g.tail_rows,
+                                                            count_mode, done);
 }
 
 // Rows of one node for a gather launch.

@@ -287,9 +287,8 @@ int hist_enqueue(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, 
     const int tiles = (F + HFL - 1) / HFL;
     if (!rows) {
         if (n > 0) {
-            const int rc = root_chunks(n, tiles);
-            launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, q, 0.0, 0.0, nullptr, nullptr,
-                             nullptr, out, 0, nullptr);
+            launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, q, 0.0, 0.0, nullptr, nullptr, nullptr, out, 0,
+                             nullptr);
         }
     } else if (m > 0) {
         k_set_hist_job<<<1, 1, 0, stream>>>(job, rows, 0, m, out);
@@ -350,9 +349,8 @@ int yabt_hist_accumulate(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* b
     const int tiles = (F + HFL - 1) / HFL;
     if (!rows) {
         if (n > 0) {
-            const int rc = root_chunks(n, tiles);
-            launch_hist_root(tiles, rc, stream, bins_fm, ld_fm, grad, hess, n, F, nullptr, scg, sch, nullptr, nullptr,
-                             nullptr, out, 0, nullptr);
+            launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, nullptr, scg, sch, nullptr, nullptr, nullptr,
+                             out, 0, nullptr);
         }
     } else if (m > 0) {
         Carve c{(char*)workspace, 0};
@@ -386,11 +384,10 @@ int yabt_hist_root(const uint8_t* bins_fm, int64_t ld_fm, const float* grad, con
     const int rc0 = check_hist_layout(bins_fm, ld_fm, nullptr, 0, grad, hess, n, F, nullptr, 0, "yabt_hist_root");
     if (rc0) return rc0;
     if (n > 0) {
-        const int tiles = (F + HFL - 1) / HFL;
-        const int rc = root_chunks(n, tiles);
-        k_hist_root<false><<<tiles * rc, RBLOCK, 0, stream>>>(bins_fm, ld_fm, grad, hess, n, F, nullptr,
-                                                              ldexp(1.0, sg), ldexp(1.0, sh), nullptr, bin_counts,
-                                                              nullptr, out, rc, 0, nullptr);
+        const RootGrid g = root_grid(n, F, grad, hess);
+        k_hist_root<false><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld_fm, grad, hess, n, F, nullptr, ldexp(1.0, sg),
+                                                            ldexp(1.0, sh), nullptr, bin_counts, nullptr, out,
+                                                            g.chunks, g.tail, g.tail_rows, 0, nullptr);
     }
     return launch_status("yabt_hist_root launch");
 }
