@@ -95,12 +95,12 @@ def test_hist_large_count_exact():
     assert got[1, 0, 0] * 2.0 ** -sh == 0.5 * n
 
 
-@pytest.mark.parametrize("n", [2048, (1 << 19) + 3, 1 << 22])
+@pytest.mark.parametrize("n", [2048, 3072, 3073, (1 << 19) + 3, 1 << 22])
 def test_hist_packed_window_extreme(n):
     """Every row in one bin with the largest |g| and h the shift allows (they
     round to |q| = 2^19, or 2^(30 - 11) at n = 2048): each half of the packed
-    root cell takes 2048 such rows, 2^30, between two unpacks, and the sums
-    must stay exact."""
+    root cell takes an epoch of 3072 such rows, 1.5 * 2^30, between two
+    unpacks, and the sums must stay exact."""
     bins = np.zeros((n, 1), np.uint8)
     g = np.full(n, -1.9999999, np.float32)
     h = np.full(n, 1.9999999, np.float32)

@@ -121,12 +121,12 @@ struct LeafRun {
     int64_t label;
 };
 
-// The host's view, in mapped host memory.
+// The host's view, in mapped host memory: one word, ((round + 1) << 1) |
+// done, written with a single 32-bit store so that no fence has to order
+// separate fields (0: no controller has run).
 struct Flags {
-    int32_t round;
-    int32_t done;
-    int32_t n_nodes;
-    int32_t status;
+    int32_t word;
+    int32_t pad[3];
 };
 
 struct Args {
@@ -214,8 +214,7 @@ __global__ void k_setup_finish(Args A) {
         A.out_status[0] = -1;
         A.out_status[1] = 0;
         A.out_status[2] = 0;
-        A.flags->status = -1;
-        A.flags->done = 1;
+        A.flags->word = 1;   // done before any round
     }
 }
 
@@ -408,37 +407,6 @@ __device__ __forceinline__ void wave_sync() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-// First maximum of s_gain[0..na) above 0 (cgrow's strict > from 0.0f, the
-// lowest index on ties), over one wave; -1: none.
-// Each lane keeps the first maximum above 0 of its entries (lane, lane + 64,
-// ...); the table's is the lowest index among the lanes holding the wave's
-// maximum.
-__device__ __forceinline__ int wave_table_argmax(const float* s_gain, int na, int lane) {
-    float key = 0.0f;
-    int idx = INT_MAX;
-    // four loads in flight before the compares (one LDS round trip per 256
-    // entries, not one per 64)
-    constexpr int U = 4;
-    for (int a0 = lane; a0 < na; a0 += U * WAVE) {
-        float g[U];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int a = a0 + u * WAVE;
-            g[u] = a < na ? s_gain[a] : -INFINITY;
-        }
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            if (g[u] > key) {
-                key = g[u];
-                idx = a0 + u * WAVE;
-            }
-        }
-    }
-    const float m = wave_max_f32(key);
-    if (!(m > 0.0f)) return -1;
-    return wave_min_i32(key == m ? idx : INT_MAX);
-}
-
 // Inclusive prefix sum over the wave (32- or 64-bit integers).
 template <typename T>
 __device__ __forceinline__ T wave_incl_scan(T v, int lane) {
@@ -502,7 +470,8 @@ struct Table {
     YABT_LDS uint8_t* ccommit;           // [pend_cap]
     YABT_LDS float* ckey;                // [pend_cap] while planning: key of the split's node (+inf: not known)
     YABT_LDS float* cbud;                // [pend_cap] while planning: that key where the split counts for the budget
-    YABT_LDS float* ckand;               // [L + 2 pend_cap] while planning: the candidates' keys
+    YABT_LDS float* ckand;               // [L + 2 pend_cap] while planning: the listed candidates' keys
+    YABT_LDS int16_t* cidx;              // [L + 2 pend_cap] and their indices
     YABT_LDS int16_t* commit_p;          // [L] this controller's commits: split, parent node
     YABT_LDS int16_t* commit_nid;        // [L]
     YABT_LDS int16_t* plan_src;          // [KMAX] this round's splits: origin
@@ -534,6 +503,7 @@ __host__ __device__ inline size_t table_carve(char* base, int L, int pend_cap, T
     char* commit_p = take(sizeof(int16_t) * L);
     char* commit_nid = take(sizeof(int16_t) * L);
     char* plan_src = take(sizeof(int16_t) * KMAX);
+    char* cidx = take(sizeof(int16_t) * (L + 2 * (size_t)pend_cap));
     char* ccommit = take(pend_cap);
 #if defined(__HIP_DEVICE_COMPILE__)
     if (T) {
@@ -552,18 +522,23 @@ __host__ __device__ inline size_t table_carve(char* base, int L, int pend_cap, T
         T->commit_p = (YABT_LDS int16_t*)commit_p;
         T->commit_nid = (YABT_LDS int16_t*)commit_nid;
         T->plan_src = (YABT_LDS int16_t*)plan_src;
+        T->cidx = (YABT_LDS int16_t*)cidx;
         T->ccommit = (YABT_LDS uint8_t*)ccommit;
     }
 #else
     (void)T;
     for (char* p : {gain, cgain, ckey, cbud, ckand, root_gain, root_pend, pend, src, node, cpend, corigin, commit_p,
-                    commit_nid, plan_src, ccommit})
+                    commit_nid, plan_src, cidx, ccommit})
         (void)p;
 #endif
     return (off + 15) / 16 * 16;
 }
 
-// wave_table_argmax over an LDS array.
+// First maximum of s_gain[0..na) above 0 (cgrow's strict > from 0.0f, the
+// lowest index on ties), over one wave; -1: none.  Each lane keeps the first
+// maximum above 0 of its entries (lane, lane + 64, ...), four LDS loads in
+// flight; the table's is the lowest index among the lanes holding the wave's
+// maximum.
 __device__ __forceinline__ int wave_table_argmax(const YABT_LDS float* s_gain, int na, int lane) {
     float key = 0.0f;
     int idx = INT_MAX;
@@ -586,6 +561,27 @@ __device__ __forceinline__ int wave_table_argmax(const YABT_LDS float* s_gain, i
     const float m = wave_max_f32(key);
     if (!(m > 0.0f)) return -1;
     return wave_min_i32(key == m ? idx : INT_MAX);
+}
+
+// Position of the best entry of a compacted candidate list (largest key
+// above 0, the lowest index on ties), over one wave; -1: none.
+__device__ __forceinline__ int wave_list_argmax(const YABT_LDS float* keys, const YABT_LDS int16_t* ids, int m,
+                                                int lane) {
+    float key = 0.0f;
+    int idx = INT_MAX, pos = INT_MAX;
+    for (int i = lane; i < m; i += WAVE) {
+        const float k = keys[i];
+        const int x = ids[i];
+        if (k > key || (k == key && k > 0.0f && x < idx)) {
+            key = k;
+            idx = x;
+            pos = i;
+        }
+    }
+    const float mx = wave_max_f32(key);
+    if (!(mx > 0.0f)) return -1;
+    const int wi = wave_min_i32(key == mx ? idx : INT_MAX);
+    return wave_min_i32((key == mx && idx == wi) ? pos : INT_MAX);
 }
 
 // Table gain and computed split of the leaf with origin src.
@@ -710,22 +706,72 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
                 if (__ballot(moved) == 0) break;
             }
         }
-        // the candidates' keys (-inf: not a candidate): leaf a at a, child c
-        // of split p at na + 2 p + c; and each uncommitted computed split's
-        // key, where it adds a leaf to the run-ahead (the budget)
-        const int ncand = na + 2 * np0;
-        for (int a = lane; a < na; a += WAVE) T.ckand[a] = (T.pend[a] < 0 && a != best) ? T.gain[a] : -INFINITY;
-        for (int p = lane; p < np0; p += WAVE) {
-            const float kp = T.ckey[p];
-            const bool live = !T.ccommit[p] && kp != INFINITY;
-            T.cbud[p] = live ? kp : -INFINITY;
+        // the candidates, compacted into (key, index) lists: leaf a is
+        // candidate a, child c of split p candidate na + 2 p + c, and only
+        // positive keys are listed (a pick needs a positive gain); and the
+        // budget's entries: each uncommitted computed split's key, where it
+        // adds a leaf to the run-ahead (only positive ones can count)
+        int m = 0, mb = 0;
+        auto append = [&](bool live, float key, int idx, YABT_LDS float* keys, YABT_LDS int16_t* ids, int& cnt) {
+            const uint64_t bal = __ballot(live);
+            const int pos = cnt + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                 __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+            if (live) {
+                keys[pos] = key;
+                if (ids) ids[pos] = (int16_t)idx;
+            }
+            cnt += __popcll(bal);
+        };
+        for (int a0 = 0; a0 < na; a0 += WAVE) {
+            const int a = a0 + lane;
+            const float g = (a < na && a != best && T.pend[a] < 0) ? T.gain[a] : -INFINITY;
+            append(g > 0.0f, g, a, T.ckand, T.cidx, m);
+        }
+        for (int p0 = 0; p0 < np0; p0 += WAVE) {
+            const int p = p0 + lane;
+            const bool in = p < np0;
+            const float kp = in ? T.ckey[p] : -INFINITY;
+            const bool live = in && !T.ccommit[p] && kp != INFINITY;
+            append(live && kp > 0.0f, kp, p, T.cbud, nullptr, mb);
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
-                T.ckand[na + 2 * p + c] = (live && T.cpend[p][c] == -1) ? fminf(kp, T.cgain[p][c]) : -INFINITY;
+            for (int c = 0; c < 2; ++c) {
+                const float kc = (live && T.cpend[p][c] == -1) ? fminf(kp, T.cgain[p][c]) : -INFINITY;
+                append(kc > 0.0f, kc, na + 2 * p + c, T.ckand, T.cidx, m);
+            }
         }
         wave_sync();
-        // take best, then the largest keys (the lowest candidate on ties)
-        int cand = best;
+        // take best, then the largest keys (the lowest candidate on ties).
+        // Short lists sit in registers, R entries per lane: each lane keeps
+        // its best candidate, a pick is two wave reductions, and the budget
+        // count a ballot per register.
+        constexpr int R = 4;
+        const bool in_regs = m <= R * WAVE && mb <= R * WAVE;
+        float ck[R], bk[R];
+        int ci[R];
+        float lbk = 0.0f;   // this lane's best candidate: key and index
+        int lbi = INT_MAX;
+        auto lane_best = [&]() {
+            lbk = 0.0f;
+            lbi = INT_MAX;
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                if (ck[r] > lbk || (ck[r] == lbk && ck[r] > 0.0f && ci[r] < lbi)) {
+                    lbk = ck[r];
+                    lbi = ci[r];
+                }
+            }
+        };
+        if (in_regs) {
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+                const int i = lane + r * WAVE;
+                ck[r] = i < m ? T.ckand[i] : -INFINITY;
+                ci[r] = i < m ? (int)T.cidx[i] : INT_MAX;
+                bk[r] = i < mb ? T.cbud[i] : -INFINITY;
+            }
+            lane_best();
+        }
+        int cand = best, cpos = -1;
         for (;;) {
             // Pend capacity: every controller may need one for the leaf it is
             // blocked on, at most L - na more; extras keep np + L - na <=
@@ -737,25 +783,35 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
             if (j > 0 && np + L - na > A.pend_cap - 1) break;
             if (lane == 0) {
                 T.plan_src[j] = cand < na ? T.src[cand] : (int16_t)(cand - na);
-                T.ckand[cand] = -INFINITY;
+                if (cpos >= 0) T.ckand[cpos] = -INFINITY;   // the list in LDS: taken
             }
             ++np;
             ++j;
             wave_sync();
             if (j >= KMAX) break;
-            cand = wave_table_argmax(T.ckand, ncand, lane);
-            if (cand < 0) break;
-            const float key = T.ckand[cand];
-            // the budget: leaves of the run-ahead when it pops this one
+            float key;
             int e = 0;
-            for (int p0 = lane; p0 < np0; p0 += 4 * WAVE) {
-                float k[4];
+            if (in_regs) {
+                key = wave_max_f32(lbk);
+                if (!(key > 0.0f)) break;
+                cand = wave_min_i32(lbk == key ? lbi : INT_MAX);
+                if (lbi == cand) {   // its lane drops it and looks again
 #pragma unroll
-                for (int u = 0; u < 4; ++u) k[u] = p0 + u * WAVE < np0 ? T.cbud[p0 + u * WAVE] : -INFINITY;
+                    for (int r = 0; r < R; ++r)
+                        if (ci[r] == cand) ck[r] = -INFINITY;
+                    lane_best();
+                }
 #pragma unroll
-                for (int u = 0; u < 4; ++u) e += k[u] >= key ? 1 : 0;
+                for (int r = 0; r < R; ++r) e += __popcll(__ballot(bk[r] >= key));
+            } else {
+                cpos = wave_list_argmax(T.ckand, T.cidx, m, lane);
+                if (cpos < 0) break;
+                cand = T.cidx[cpos];
+                key = T.ckand[cpos];
+                for (int i = lane; i < mb; i += WAVE) e += T.cbud[i] >= key ? 1 : 0;
+                e = wave_sum<int>(e);
             }
-            e = wave_sum<int>(e);
+            // the budget: leaves of the run-ahead when it pops this one
             if (na + e + j >= L) break;
         }
     }
@@ -855,13 +911,9 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
         st->n_round = done ? 0 : j;
         const int r = st->round + 1;
         st->round = r;
-        // the host's view: fields, then the round number, each after a
-        // system-scope fence
+        // the host's view: round and done in one store
         volatile Flags* fl = A.flags;
-        fl->n_nodes = nn;
-        fl->done = done;
-        __threadfence_system();
-        fl->round = r;
+        fl->word = ((r + 1) << 1) | done;
     }
 }
 
@@ -911,6 +963,17 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
     const int32_t done = st->done, nr = ROOT ? 1 : st->n_round;
     const int y = ROOT ? 0 : blockIdx.y;
     if (done || y >= nr) return;
+    // the start of the controller's table, loaded by every block together
+    // with its bins (whichever block finishes last is the controller and
+    // holds it in registers by then): leaf t and computed split t (a
+    // controller loads the entries past the block size itself)
+    uint32_t pf_leaf = 0;   // origin (low 16 bits) and node id of leaf t
+    PendSum pf_ps = {};
+    if (!ROOT) {
+        const int t = threadIdx.x;
+        if (t < st->n_leaves) pf_leaf = (uint32_t)(uint16_t)A.leaf_src[t] | ((uint32_t)A.leaf_node[t] << 16);
+        if (t < st->n_pend) pf_ps = A.psum[t];
+    }
     const bool derive = q->const_h != 0;
     const int64_t hqc = q->hq_const;
     const int pidx = ROOT ? 0 : st->round_pend[y];
@@ -1076,12 +1139,7 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
         }
         const int nn = st->n_nodes, na = st->n_leaves, np = st->n_pend;
         const int p0 = np - nr;                   // this round's splits: p0 .. np - 1
-        for (int a = threadIdx.x; a < na; a += NT) {
-            T.src[a] = (int16_t)A.leaf_src[a];
-            T.node[a] = (int16_t)A.leaf_node[a];
-        }
-        for (int p = threadIdx.x; p < np; p += NT) {
-            const PendSum S = A.psum[p];
+        auto put = [&](int p, const PendSum& S) {
             if (p < p0) {
                 T.cgain[p][0] = S.gain[0];
                 T.cgain[p][1] = S.gain[1];
@@ -1090,7 +1148,17 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
             T.cpend[p][1] = S.child_pend[1];
             T.corigin[p] = S.origin;
             T.ccommit[p] = (uint8_t)S.committed;
+        };
+        if (threadIdx.x < na) {
+            T.src[threadIdx.x] = (int16_t)(pf_leaf & 0xffffu);
+            T.node[threadIdx.x] = (int16_t)(pf_leaf >> 16);
         }
+        if (threadIdx.x < np) put(threadIdx.x, pf_ps);
+        for (int a = threadIdx.x + NT; a < na; a += NT) {
+            T.src[a] = (int16_t)A.leaf_src[a];
+            T.node[a] = (int16_t)A.leaf_node[a];
+        }
+        for (int p = threadIdx.x + NT; p < np; p += NT) put(p, A.psum[p]);
         if (threadIdx.x == 0) {
             *T.root_gain = st->root_gain;
             *T.root_pend = st->root_pend;
@@ -1342,10 +1410,7 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
     held.s = stream;
     if (int prc = held.hold.take(sizeof(Flags), hipHostMallocMapped | hipHostMallocCoherent)) return prc;
     Flags* h_flags = static_cast<Flags*>(held.hold.p);
-    h_flags->round = -1;
-    h_flags->done = 0;
-    h_flags->n_nodes = 0;
-    h_flags->status = 0;
+    h_flags->word = 0;
     const hipError_t he = hipHostGetDevicePointer((void**)&A.flags, h_flags, 0);
     if (he != hipSuccess) return hip_fail(he, "yabt_grow_batched: mapped flags");
 
@@ -1363,23 +1428,26 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
     if (lrc) return lrc;
     const int wlog = pack_window_log2(n);
     // rounds: at most max_leaves - 1 (one split each); the controller of round
-    // r stamps r + 1 into h_flags->round, so round r may be enqueued once
+    // r stamps r + 1 into the flags word, so round r may be enqueued once
     // round r - LOOKAHEAD has finished
     volatile Flags* fl = h_flags;
+    auto ready = [&](int r) {   // done, or round r - LOOKAHEAD finished
+        const int32_t w = fl->word;
+        return (w & 1) || (w >> 1) - 1 >= r - LOOKAHEAD;
+    };
     for (int r = 1; r < max_leaves; ++r) {
         for (uint64_t spin = 0;; ++spin) {
-            if (fl->done) break;
-            if (fl->round >= r - LOOKAHEAD) break;
+            if (ready(r)) break;
             if ((spin & 1023) == 1023) {
                 const hipError_t e = hipStreamQuery(stream);
                 if (e == hipSuccess) {
-                    if (fl->done || fl->round >= r - LOOKAHEAD) break;
+                    if (ready(r)) break;
                     return fail(-4, "yabt_grow_batched: stream finished without the round's result");
                 }
                 if (e != hipErrorNotReady) return hip_fail(e, "yabt_grow_batched: round");
             }
         }
-        if (fl->done) break;
+        if (fl->word & 1) break;
         k_part<<<PART_BLOCKS, SB, 0, stream>>>(bins_fm, ld_fm, n, A.st, A.pend);
         k_gather<<<tiles * gather_units(tiles), HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, A.q, A.dflt,
                                                                          A.st, A.pend, A.pieces, wlog);
@@ -1396,7 +1464,7 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
     if (e != hipSuccess) return hip_fail(e, "yabt_grow_batched: synchronisation");
     // every round commits at least one split, so max_leaves - 1 rounds finish
     // any tree
-    if (!fl->done) return fail(-4, "yabt_grow_batched: tree not finished after max_leaves - 1 rounds");
+    if (!(fl->word & 1)) return fail(-4, "yabt_grow_batched: tree not finished after max_leaves - 1 rounds");
     return 0;
 }
 

@@ -166,12 +166,13 @@ __device__ __forceinline__ uint32_t bin_addr_rt(uint32_t word, uint32_t lo, int 
 //     unpacks them -- lo, the
 //     sign-extended low 32 bits, is the h sum; (cell - lo) >> 32 the g sum.
 //     The cells come in two buffers that alternate every epoch of
-//     ROOT_UNPACK = 2 steps: after the barrier that ends an epoch, each thread
+//     ROOT_DEPTH = 3 steps: after the barrier that ends an epoch, each thread
 //     reads and clears its cells of that epoch's buffer while the waves add
 //     the next epoch into the other one.  A cell so takes the rows of one
-//     epoch (2048, or n when smaller) between two reads, and no atomic
+//     epoch (3072, or n when smaller) between two reads, and no atomic
 //     targets it while it is read; with hist_shift's |q| <= 2^(30 -
-//     min(k, 11)) each half's sum stays within 2^30, so both are exact.
+//     min(k, 11)) each half's sum stays within 3 * 2^29 < 2^31 (2^30 for
+//     n <= 2048), so both are exact.
 //   !HCH (every h equal): the word is q(g) itself; no unpacking, and the h
 //     plane is left to the caller (count * q(h)).
 // Invalid rows of a step add zero words (their q is 0), so the loop needs no
@@ -291,11 +292,13 @@ inline RootGrid root_grid(int64_t n, int F, const void* grad, const void* hess) 
     return g;
 }
 
-constexpr int ROOT_DEPTH = 4;    // steps of inputs loaded ahead of the adds
-constexpr int ROOT_UNPACK = 2;   // steps per epoch: 2 x 1024 = 2048 rows, hist_shift's bound
-constexpr bool ROOT_DBUF = true;   // two cell buffers (one barrier per epoch) or one (two barriers)
-static_assert(ROOT_DEPTH % (2 * ROOT_UNPACK) == 0, "a ring round is whole pairs of epochs");
-static_assert(ROOT_UNPACK * RSTEP <= 2048, "hist_shift bounds 2048 rows of a cell between two unpacks");
+constexpr int ROOT_DEPTH = 3;    // steps of inputs loaded ahead of the adds: one epoch
+constexpr int TAIL_DEPTH = 4;    // the same in a tail block (4 steps of 512 rows per column)
+// A cell takes the rows of one epoch between two unpacks: ROOT_DEPTH block
+// steps of RSTEP rows (3072), and with hist_shift's |q| <= 2^19 each half of
+// the packed cell then stays within 3072 * 2^19 < 2^31.
+static_assert((int64_t)ROOT_DEPTH * RSTEP * (1 << 19) < (1ll << 31), "an epoch's sums fit 32-bit halves");
+static_assert((int64_t)TAIL_DEPTH * TSTEP / 4 * (1 << 19) < (1ll << 31), "a tail epoch's sums fit 32-bit halves");
 
 template <bool HCH, bool SKIP>
 __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restrict__ bins_fm, int64_t ld,
@@ -318,12 +321,10 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
     const uint32_t lbase = (uint32_t)fl << 3;
     char* const lds = reinterpret_cast<char*>(L.w);
     int64_t ag[RENT], ah[RENT];   // unpacked sums of this thread's cells
-    uint64_t prev[RENT];          // single buffer: each cell at its previous read
 #pragma unroll
     for (int k = 0; k < RENT; ++k) {
         ag[k] = 0;
         ah[k] = 0;
-        prev[k] = 0;
     }
     // the cell a thread unpacks: cell i = t + k RBLOCK is bin i / HFL, feature i % HFL
     auto cell = [](int k) { const int i = threadIdx.x + k * RBLOCK; return (i / HFL) * (2 * HFL) + (i % HFL); };
@@ -334,16 +335,10 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
         for (int k = 0; k < RENT; ++k) {
             const int c = cell(k) + p * HFL;
             const uint64_t v = L.w[c];
-            uint64_t dv = v;
-            if (ROOT_DBUF) {
-                L.w[c] = 0;
-            } else {
-                dv = v - prev[k];
-                prev[k] = v;
-            }
-            const int64_t hs = (int64_t)(int32_t)(uint32_t)dv;
+            L.w[c] = 0;
+            const int64_t hs = (int64_t)(int32_t)(uint32_t)v;
             ah[k] += hs;
-            ag[k] += (int64_t)(dv - (uint64_t)hs) >> 32;
+            ag[k] += (int64_t)(v - (uint64_t)hs) >> 32;
         }
     };
     const uint8_t* col = bins_fm + (size_t)(fok ? f : f0) * ld;
@@ -365,9 +360,11 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
     const int64_t steps = (hi - lo + RSTEP - 1) / RSTEP;   // the same in every wave: barriers below
     // Ring of ROOT_DEPTH stages: stage j holds step s0 + j and is then refilled
     // with step s0 + j + ROOT_DEPTH (the ring is unrolled: no register moves).
-    // It starts one round early, at steps -ROOT_DEPTH .. -1, whose rows are
-    // all invalid (zero words at cell 0): that round only issues the first
-    // loads, in the same order as every later round.
+    // A round of the ring is one epoch; its cells are one of two buffers,
+    // which alternate by round.  The ring starts one round early, at steps
+    // -ROOT_DEPTH .. -1, whose rows are all invalid (zero words at cell 0):
+    // that round only issues the first loads, in the same order as every
+    // later round.
     float gs[ROOT_DEPTH], hs[ROOT_DEPTH];
     uint4 bs[ROOT_DEPTH];
 #pragma unroll
@@ -378,7 +375,9 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
     }
     __syncthreads();
     int64_t sum_g = 0, sum_h = 0;
+    uint32_t buf = 0;   // the cell buffer of this round's epoch
     for (int64_t s0 = -ROOT_DEPTH; s0 < steps; s0 += ROOT_DEPTH) {
+        const uint32_t lb = HCH ? (lbase | (buf << 7)) : lbase;
 #pragma unroll
         for (int j = 0; j < ROOT_DEPTH; ++j) {
             const int64_t s = s0 + j;
@@ -394,7 +393,6 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
             // come out of this stage's bins before its registers are refilled,
             // so the old and new values are never live at once (else the refill
             // lands in other registers and a copy at the loop's end waits for it)
-            const uint32_t lb = (ROOT_DBUF && HCH && (j / ROOT_UNPACK) % 2) ? lbase | 128u : lbase;   // the epoch's buffer
             const uint32_t wv[4] = {bs[j].x, bs[j].y, bs[j].z, bs[j].w};
             uint32_t at[HFL];
             uint32_t keep = 0xffffu;
@@ -418,17 +416,16 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
             YABT_GH_ADD(8) YABT_GH_ADD(9) YABT_GH_ADD(10) YABT_GH_ADD(11)
             YABT_GH_ADD(12) YABT_GH_ADD(13) YABT_GH_ADD(14) YABT_GH_ADD(15)
 #undef YABT_GH_ADD
-            if (HCH && (j + 1) % ROOT_UNPACK == 0) {
-                // end of an epoch: once every wave's adds into its buffer are
-                // done, read it while the next epoch adds into the other one
-                __syncthreads();
-                unpack(ROOT_DBUF ? (j / ROOT_UNPACK) % 2 : 0);
-                if (!ROOT_DBUF) __syncthreads();
-            }
+        }
+        if (HCH) {
+            // end of the epoch: once every wave's adds into its buffer are
+            // done, read it while the next epoch adds into the other one
+            __syncthreads();
+            unpack((int)buf);
+            buf ^= 1u;
         }
     }
     __syncthreads();
-    if (HCH && !ROOT_DBUF) unpack(0);
     if (!HCH) {   // one buffer, never unpacked: the cells are the g sums
 #pragma unroll
         for (int k = 0; k < RENT; ++k) ag[k] = (int64_t)L.w[cell(k)];
@@ -563,10 +560,10 @@ __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __res
         bw = *reinterpret_cast<const uint2*>(colp + (rA < hi ? rA : lo));
     };
     const int64_t steps = (hi - lo + TSTEP - 1) / TSTEP;
-    float2 gs[ROOT_DEPTH], hs[ROOT_DEPTH];
-    uint2 bs[ROOT_DEPTH];
+    float2 gs[TAIL_DEPTH], hs[TAIL_DEPTH];
+    uint2 bs[TAIL_DEPTH];
 #pragma unroll
-    for (int j = 0; j < ROOT_DEPTH; ++j) {
+    for (int j = 0; j < TAIL_DEPTH; ++j) {
         gs[j] = make_float2(0.0f, 0.0f);
         hs[j] = make_float2(0.0f, 0.0f);
         bs[j] = make_uint2(0, 0);
@@ -574,10 +571,10 @@ __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __res
     __syncthreads();
     int64_t sum_g = 0, sum_h = 0;
     uint32_t buf = 0;   // the cell buffer of this ring round's epoch
-    for (int64_t s0 = -ROOT_DEPTH; s0 < steps; s0 += ROOT_DEPTH) {
+    for (int64_t s0 = -TAIL_DEPTH; s0 < steps; s0 += TAIL_DEPTH) {
         const uint32_t lb = HCH ? (lbase | (buf << 7)) : lbase;
 #pragma unroll
-        for (int j = 0; j < ROOT_DEPTH; ++j) {
+        for (int j = 0; j < TAIL_DEPTH; ++j) {
             const int64_t s = s0 + j;
             __builtin_amdgcn_sched_barrier(0);
             const int64_t p = lo + s * TSTEP + (int64_t)wave * (2 * WAVE) + 32 * qw + 8 * a + 2 * c;
@@ -594,7 +591,7 @@ __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __res
                 at[J] = bin_addr_rt(wv[J >> 2], lb, J & 3);
                 if (SKIP && (int)((wv[J >> 2] >> (8 * (J & 3))) & 0xffu) == d) keep &= ~(1u << J);
             }
-            load(s + ROOT_DEPTH, gs[j], hs[j], bs[j]);
+            load(s + TAIL_DEPTH, gs[j], hs[j], bs[j]);
             sum_g += g0 + g1;
             sum_h += h0 + h1;
             const uint64_t w0 = HCH ? ((uint64_t)g0 << 32) + (uint64_t)h0 : (uint64_t)g0;
