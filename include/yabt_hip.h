@@ -178,7 +178,9 @@ size_t yabt_leaf_fit_workspace_bytes(int64_t n, int n_nodes, int K);
 /* Linear leaf models of one tree: for every leaf (feature[node] == -1) with at
  * least min_samples rows, theta = solve(M + diag(lam,..,lam,1e-8), b) with
  * x1 = [(x - mu) / sd (fp32), 1], M = sum h x1 x1^T, b = -sum g x1 over the
- * leaf's rows (fp64 products, summed exactly in int64 fixed point).
+ * leaf's rows.  gram_mode 0: the reference's fp64 products, each rounded once
+ * to int64 fixed point and summed exactly (order-free); 1: the same sums in
+ * fp64 on the matrix cores (v_mfma_f64_16x16x4_f64, a fixed order).
  * Replaces `_fit_linear` (yabt/neural_leaves.py:42-90) and the counts and
  * envelopes of `fit_leaf_networks` (yabt/neural_leaves.py:157-176).
  *   x_kind 0: X is fp32 row-major (n, ldx), input j of row i = X[i*ldx + feats[j]];
@@ -188,13 +190,24 @@ size_t yabt_leaf_fit_workspace_bytes(int64_t n, int n_nodes, int K);
  * inputs (zero where not fitted); out_lo/out_hi (n_nodes, K) per-node min/max of
  * the raw inputs (+inf/-inf for empty nodes); out_count (n_nodes) rows per node;
  * out_status[0] = 0, -1 (a leaf id out of range or a non-finite input) or -2
- * (a singular system, where the reference's torch.linalg.solve raises). */
+ * (a singular system, where the reference's torch.linalg.solve raises);
+ * out_status[1] = the number of leaves fitted. */
 int yabt_leaf_fit(int x_kind, const void *X, int64_t ldx, int64_t n, const int32_t *feats, int K,
                   const float *mu, const float *sd, const float *grad, const float *hess,
                   const int64_t *leaf_of_row, const int64_t *feature, int n_nodes, int min_samples,
-                  double lam, void *workspace, size_t workspace_bytes, float *out_W, float *out_b,
-                  float *out_lo, float *out_hi, int64_t *out_count, int32_t *out_status,
-                  yabt_stream_t stream);
+                  double lam, int gram_mode, void *workspace, size_t workspace_bytes, float *out_W,
+                  float *out_b, float *out_lo, float *out_hi, int64_t *out_count,
+                  int32_t *out_status, yabt_stream_t stream);
+
+/* The fold of the leaf models into raw space, in the fp32 order of the
+ * reference's torch expressions: per node, acc = sum_j W[j] * (mu[j] / sd[j])
+ * left to right, out_value = value_in + lr * (b - acc), out_linear[j] =
+ * (lr * W[j]) / sd[j].  W (n_nodes, K) and b (n_nodes) as yabt_leaf_fit
+ * writes them.  Replaces the fold of `fit_leaf_networks`
+ * (yabt/neural_leaves.py:178-184). */
+int yabt_leaf_fold(int n_nodes, int K, const float *W, const float *b, const float *mu,
+                   const float *sd, float lr, const float *value_in, float *out_value,
+                   float *out_linear, yabt_stream_t stream);
 
 /* Workspace bytes of yabt_leaf_moments for n rows. */
 size_t yabt_leaf_moments_workspace_bytes(int64_t n);

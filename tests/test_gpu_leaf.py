@@ -18,7 +18,8 @@ from tests.helpers import grad_hess, uniform_bins
 from yabt_amd import IdentityBinner, TreeParams, grow_tree_hip
 from yabt_amd import grow_hip as G
 from yabt_amd.losses import MSELoss
-from yabt_amd.neural_leaves import fit_leaf_networks, leaf_fit, leaf_moments
+from yabt_amd.neural_leaves import fit_leaf_networks, fold, leaf_fit, leaf_moments
+from yabt_amd.tree import Tree
 
 pytestmark = pytest.mark.gpu
 
@@ -56,20 +57,23 @@ def _oracle(Xf, feats, g, h, feature, leaf, mu, sd, min_samples, lam):
     return W, db, lo, hi, cnt
 
 
-def _gpu(X, x_kind, feats, g, h, feature, leaf, mu, sd, min_samples, lam):
+def _gpu(X, x_kind, feats, g, h, feature, leaf, mu, sd, min_samples, lam, gram="exact"):
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
     Xd = t(X) if x_kind == 0 else t(np.ascontiguousarray(X.T))
-    out = leaf_fit(Xd, x_kind, t(feats), t(mu), t(sd), t(g), t(h), t(leaf), t(feature), min_samples, lam)
+    out = leaf_fit(Xd, x_kind, t(feats), t(mu), t(sd), t(g), t(h), t(leaf), t(feature), min_samples, lam,
+                   gram=gram)
     return [o.cpu().numpy() for o in out]
 
 
+@pytest.mark.parametrize("gram", ["exact", "mfma"])
 @pytest.mark.parametrize("n,K,n_nodes,x_kind,lam", [
     (5000, 8, 61, 0, 1.0), (20_000, 5, 31, 1, 1e-3), (777, 1, 7, 0, 1.0), (300_000, 8, 511, 1, 1.0),
     (40_000, 3, 1501, 0, 0.5),   # more nodes than the LDS tables hold
+    (2_000_000, 8, 63, 1, 1e-3),   # leaves of ~60 000 rows: many Gram chunks per leaf
 ])
-def test_leaf_fit_matches_oracle(n, K, n_nodes, x_kind, lam):
+def test_leaf_fit_matches_oracle(n, K, n_nodes, x_kind, lam, gram):
     X, Xf, feats, g, h, feature, leaf, mu, sd = _problem(n + K, n, K, n_nodes, bins=x_kind == 1)
-    W, b, lo, hi, cnt = _gpu(X, x_kind, feats, g, h, feature, leaf, mu, sd, 50, lam)
+    W, b, lo, hi, cnt = _gpu(X, x_kind, feats, g, h, feature, leaf, mu, sd, 50, lam, gram)
     rW, rb, rlo, rhi, rcnt = _oracle(Xf, feats, g, h, feature, leaf, mu, sd, 50, lam)
     assert np.array_equal(cnt, rcnt)
     assert np.array_equal(lo, rlo) and np.array_equal(hi, rhi)
@@ -91,14 +95,42 @@ def test_leaf_moments(n, K, x_kind):
     assert np.array_equal(a[0], m) and np.array_equal(a[1], s)
 
 
-def test_leaf_fit_deterministic_and_u8_equals_f32():
+@pytest.mark.parametrize("gram", ["exact", "mfma"])
+def test_leaf_fit_deterministic_and_u8_equals_f32(gram):
     X, Xf, feats, g, h, feature, leaf, mu, sd = _problem(9, 50_000, 6, 63, bins=True)
-    a = _gpu(X, 1, feats, g, h, feature, leaf, mu, sd, 50, 1.0)
-    b = _gpu(X, 1, feats, g, h, feature, leaf, mu, sd, 50, 1.0)
-    c = _gpu(Xf, 0, feats, g, h, feature, leaf, mu, sd, 50, 1.0)
+    a = _gpu(X, 1, feats, g, h, feature, leaf, mu, sd, 50, 1.0, gram)
+    b = _gpu(X, 1, feats, g, h, feature, leaf, mu, sd, 50, 1.0, gram)
+    c = _gpu(Xf, 0, feats, g, h, feature, leaf, mu, sd, 50, 1.0, gram)
     for u, v, w in zip(a, b, c):
         assert np.array_equal(u, v)
         assert np.array_equal(u, w)
+
+
+@pytest.mark.parametrize("K", [1, 5, 8])
+def test_leaf_fold_equals_torch_expressions(K):
+    """yabt_leaf_fold bit for bit against the reference's own torch fold
+    (neural_leaves.py:178-184) evaluated on the device."""
+    rng = np.random.default_rng(K)
+    N = 301
+    W = torch.from_numpy(rng.normal(size=(N, K)).astype(np.float32)).to(DEV)
+    db = torch.from_numpy(rng.normal(size=N).astype(np.float32)).to(DEV)
+    mu = torch.from_numpy((rng.normal(size=K) * 3).astype(np.float32)).to(DEV)
+    sd = torch.from_numpy(rng.uniform(0.1, 5.0, size=K).astype(np.float32)).to(DEV)
+    value = torch.from_numpy(rng.normal(size=N).astype(np.float32)).to(DEV)
+    W[::7] = 0.0
+    db[::7] = 0.0
+    lr = 0.1
+    tree = Tree(torch.full((N,), -1, dtype=torch.int64), torch.zeros(N), torch.zeros(N, dtype=torch.int64),
+                torch.zeros(N, dtype=torch.int64), value, 0)
+    out = fold(tree, W, db, mu, sd, lr, torch.arange(K), None, None)
+    prod = W * (mu / sd)
+    acc = prod[:, 0].clone()
+    for j in range(1, K):
+        acc = acc + prod[:, j]
+    ref_value = value + lr * (db - acc)
+    ref_linear = lr * W / sd
+    assert torch.equal(out.value, ref_value)
+    assert torch.equal(out.leaf_net_linear, ref_linear)
 
 
 def test_leaf_fit_rejects_bad_leaf_ids():

@@ -49,7 +49,7 @@ struct LeafStats {
     uint32_t max_g_bits, max_h_bits;
     int32_t sM, sb;            // fixed-point shifts of M and b
     int32_t status;            // 0 ok; -1 a leaf id outside [0, n_nodes) or a non-finite input; -2 singular system
-    int32_t pad;
+    int32_t n_fit;             // leaves fitted
 };
 
 struct LeafArgs {
@@ -67,6 +67,7 @@ struct LeafArgs {
     int n_nodes;
     int min_samples;
     double lam;
+    int gram_f64;              // 1: M and b summed in fp64 by MFMA (parts and sums hold double bits)
     int64_t rows_per_block;    // stats/scatter rows per block
     // workspace
     LeafStats* st;
@@ -116,6 +117,7 @@ __global__ void __launch_bounds__(LB) k_leaf_init(LeafArgs A, int K) {
         A.st->max_g_bits = 0;
         A.st->max_h_bits = 0;
         A.st->status = 0;
+        A.st->n_fit = 0;
     }
 }
 
@@ -318,129 +320,270 @@ __device__ __forceinline__ bool leaf_eligible(const LeafArgs& A, int node) {
     return A.feature[node] == LEAF && (int64_t)A.count[node] >= (int64_t)A.min_samples;
 }
 
-// Sorted positions [blockIdx.x * LCHUNK, +LCHUNK): for each node run inside
-// the chunk, every thread sums the fixed-point products of its rows in
-// registers; waves reduce with DPP and add into the node's sums.
-// FAST (n > 1024, so every scaled product is below 2^51 in magnitude): the
-// product is rounded to an integer by adding 1.5 * 2^52 (round to nearest
-// even, like rint) and its bits are summed as they are; the constant's bits
-// are taken off once per row at the end.  Otherwise rint and a conversion.
-template <int K, bool FAST>
-__global__ void __launch_bounds__(LB) k_leaf_gram(LeafArgs A) {
-    constexpr int NE = gram_entries(K);
-    __shared__ int32_t s_fs[LKMAX];
-    __shared__ float s_mu[LKMAX], s_sd[LKMAX];
-    __shared__ int64_t s_part[LB / WAVE][NE];
-    if (threadIdx.x < K) {
-        s_fs[threadIdx.x] = A.feats[threadIdx.x];
-        s_mu[threadIdx.x] = A.mu[threadIdx.x];
-        s_sd[threadIdx.x] = A.sd[threadIdx.x];
+// Standardised uint8 inputs take 256 values per input: s_x1[j * 256 + b] =
+// (double)((float(b) - mu[j]) / sd[j]), x1 formed in fp32 as the reference
+// forms it (neural_leaves.py:152-155), one table per block in LDS.
+template <int K, int NT>
+__device__ __forceinline__ void x1_table(double* s_x1, const float* mu, const float* sd) {
+    for (int i = threadIdx.x; i < K * 256; i += NT) {
+        const int j = i / 256, b = i % 256;
+        s_x1[i] = (double)(((float)b - mu[j]) / sd[j]);
     }
-    __syncthreads();
-    const int64_t total = A.off[A.n_nodes];
-    const int64_t c0 = (int64_t)blockIdx.x * LCHUNK, c1 = min(total, c0 + LCHUNK);
-    if (c0 >= c1) return;
-    const double scM = ldexp(1.0, A.st->sM), scb = ldexp(1.0, A.st->sb);
-    // the node holding position c0: last l with off[l] <= c0
+}
+
+// The node holding sorted position c0: the last l with off[l] <= c0.
+__device__ __forceinline__ int node_at(const LeafArgs& A, int64_t c0) {
     int lo = 0, hi = A.n_nodes - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) / 2;
         if (A.off[mid] <= c0) lo = mid;
         else hi = mid - 1;
     }
+    return lo;
+}
+
+// The fixed-point products of half P of a row's gram_entries (P = 0: entries
+// [0, NE/2), 1: [NE/2, NE)), added into acc[t - the half's first entry].
+// FAST: rounded to integers through the bits of v + 1.5 * 2^52 (round to
+// nearest even, as rint; the constant's bits come off once per row later).
+template <int K, bool FAST, int P>
+__device__ __forceinline__ void gram_half(const double (&x1)[K + 1], const double (&xhs)[K + 1], double gs,
+                                          uint64_t (&acc)[(gram_entries(K) + 1) / 2]) {
+    constexpr int NE = gram_entries(K);
+    constexpr int T0 = P == 0 ? 0 : (NE + 1) / 2, T1 = P == 0 ? (NE + 1) / 2 : NE;
+    constexpr double MAGIC = 6755399441055744.0;   // 1.5 * 2^52
+    int t = 0;
+#pragma unroll
+    for (int a = 0; a <= K; ++a) {
+#pragma unroll
+        for (int b = a; b <= K; ++b, ++t) {
+            if (t < T0 || t >= T1) continue;
+            const double v = x1[a] * xhs[b];      // the reference's product, times 2^sM exactly
+            if (FAST) acc[t - T0] += (uint64_t)__double_as_longlong(v + MAGIC);
+            else acc[t - T0] += (uint64_t)(int64_t)rint(v);
+        }
+    }
+#pragma unroll
+    for (int a = 0; a <= K; ++a, ++t) {            // rhs = -(X1 * g)
+        if (t < T0 || t >= T1) continue;
+        const double v = -(x1[a] * gs);
+        if (FAST) acc[t - T0] += (uint64_t)__double_as_longlong(v + MAGIC);
+        else acc[t - T0] += (uint64_t)(int64_t)rint(v);
+    }
+}
+
+// One half-block's rows p = p0, p0 + LB / 2, ... < e of a segment: x1 and
+// x1 h from the row, then half P of its products into acc.
+template <int K, bool FAST, int P>
+__device__ __forceinline__ void gram_rows(const LeafArgs& A, const double* s_x1, const float* s_mu,
+                                          const float* s_sd, double scM, double scb, int64_t p0, int64_t e,
+                                          uint64_t (&acc)[(gram_entries(K) + 1) / 2]) {
+    constexpr double MAGIC = 6755399441055744.0;   // 1.5 * 2^52
+    uint64_t nrow = 0;
+    for (int64_t p = p0; p < e; p += LB / 2) {
+        const float2 gh = A.sorted_gh[p];
+        double x1[K + 1];
+        if (A.x_kind == 1) {
+            const uint2 v = reinterpret_cast<const uint2*>(A.sorted_x)[p];
+#pragma unroll
+            for (int j = 0; j < K; ++j) x1[j] = s_x1[j * 256 + (((j < 4 ? v.x : v.y) >> (8 * (j & 3))) & 0xffu)];
+        } else {
+            const float* src = reinterpret_cast<const float*>(A.sorted_x) + (size_t)p * K;
+#pragma unroll
+            for (int j = 0; j < K; ++j) x1[j] = (double)((src[j] - s_mu[j]) / s_sd[j]);
+        }
+        x1[K] = 1.0;
+        const double h = (double)gh.y;
+        const double gs = (double)gh.x * scb;           // exact power-of-two scaling
+        double xhs[K + 1];
+#pragma unroll
+        for (int b = 0; b <= K; ++b) xhs[b] = (x1[b] * h) * scM;   // Xh = X1 * h (neural_leaves.py:72), scaled
+        ++nrow;
+        gram_half<K, FAST, P>(x1, xhs, gs, acc);
+    }
+    if (FAST) {
+        const uint64_t off = nrow * (uint64_t)__double_as_longlong(MAGIC);
+#pragma unroll
+        for (int t = 0; t < (gram_entries(K) + 1) / 2; ++t) acc[t] -= off;
+    }
+}
+
+// Sorted positions [blockIdx.x * LCHUNK, +LCHUNK): for each node run inside
+// the chunk, the block's two halves (waves 0-1 and 2-3) each sum half of the
+// gram_entries over every row of the run, a thread's rows in registers
+// (half the accumulators per thread: twice the resident waves); waves reduce
+// with DPP and the block's sums go to the segment's own partial slot.
+// FAST (n > 1024, so every scaled product is below 2^51 in magnitude): the
+// products are rounded by the 1.5 * 2^52 trick; otherwise rint.
+template <int K, bool FAST>
+__global__ void __launch_bounds__(LB) k_leaf_gram(LeafArgs A) {
+    constexpr int NE = gram_entries(K);
+    constexpr int NH = (NE + 1) / 2;              // entries of the first half (the second has NE - NH)
+    constexpr int HT = LB / 2;                    // threads per half
+    __shared__ float s_mu[LKMAX], s_sd[LKMAX];
+    __shared__ int64_t s_part[LB / WAVE][NH];
+    __shared__ double s_x1[K * 256];
+    if (threadIdx.x < K) {
+        s_mu[threadIdx.x] = A.mu[threadIdx.x];
+        s_sd[threadIdx.x] = A.sd[threadIdx.x];
+    }
+    if (A.x_kind == 1) x1_table<K, LB>(s_x1, A.mu, A.sd);
+    __syncthreads();
+    const int64_t total = A.off[A.n_nodes];
+    const int64_t c0 = (int64_t)blockIdx.x * LCHUNK, c1 = min(total, c0 + LCHUNK);
+    if (c0 >= c1) return;
+    const double scM = ldexp(1.0, A.st->sM), scb = ldexp(1.0, A.st->sb);
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
-    for (int node = lo; node < A.n_nodes && A.off[node] < c1; ++node) {
+    const int half = threadIdx.x / HT, th = threadIdx.x % HT;   // wave-uniform half
+    for (int node = node_at(A, c0); node < A.n_nodes && A.off[node] < c1; ++node) {
         const int64_t s = max(c0, A.off[node]), e = min(c1, A.off[node + 1]);
         if (s >= e || !leaf_eligible(A, node)) continue;   // uniform across the block
-        constexpr double MAGIC = 6755399441055744.0;   // 1.5 * 2^52
-        uint64_t acc[NE];
+        uint64_t acc[NH];
 #pragma unroll
-        for (int t = 0; t < NE; ++t) acc[t] = 0;
-        uint64_t nrow = 0;
-        for (int64_t p = s + threadIdx.x; p < e; p += LB) {
-            const float2 gh = A.sorted_gh[p];
-            float x[K];
-            if (A.x_kind == 1) {
-                const uint2 v = reinterpret_cast<const uint2*>(A.sorted_x)[p];
-#pragma unroll
-                for (int j = 0; j < K; ++j) x[j] = (float)(((j < 4 ? v.x : v.y) >> (8 * (j & 3))) & 0xffu);
-            } else {
-                const float* src = reinterpret_cast<const float*>(A.sorted_x) + (size_t)p * K;
-#pragma unroll
-                for (int j = 0; j < K; ++j) x[j] = src[j];
-            }
-            const double h = (double)gh.y;
-            const double gs = (double)gh.x * scb;           // exact power-of-two scaling
-            double x1[K + 1], xhs[K + 1];
-#pragma unroll
-            for (int j = 0; j < K; ++j) x1[j] = (double)((x[j] - s_mu[j]) / s_sd[j]);
-            x1[K] = 1.0;
-#pragma unroll
-            for (int b = 0; b <= K; ++b) xhs[b] = (x1[b] * h) * scM;   // Xh = X1 * h (neural_leaves.py:72), scaled
-            ++nrow;
-            int t = 0;
-#pragma unroll
-            for (int a = 0; a <= K; ++a) {
-#pragma unroll
-                for (int b = a; b <= K; ++b) {
-                    const double v = x1[a] * xhs[b];      // the reference's product, times 2^sM exactly
-                    if (FAST) acc[t++] += (uint64_t)__double_as_longlong(v + MAGIC);
-                    else acc[t++] += (uint64_t)(int64_t)rint(v);
-                }
-            }
-#pragma unroll
-            for (int a = 0; a <= K; ++a) {                // rhs = -(X1 * g)
-                const double v = -(x1[a] * gs);
-                if (FAST) acc[t++] += (uint64_t)__double_as_longlong(v + MAGIC);
-                else acc[t++] += (uint64_t)(int64_t)rint(v);
-            }
-        }
-        if (FAST) {
-            const uint64_t off = nrow * (uint64_t)__double_as_longlong(MAGIC);
-#pragma unroll
-            for (int t = 0; t < NE; ++t) acc[t] -= off;
-        }
+        for (int t = 0; t < NH; ++t) acc[t] = 0;
+        if (half == 0) gram_rows<K, FAST, 0>(A, s_x1, s_mu, s_sd, scM, scb, s + th, e, acc);
+        else gram_rows<K, FAST, 1>(A, s_x1, s_mu, s_sd, scM, scb, s + th, e, acc);
         // block sum of this (chunk, node) segment into its own partial slot,
         // chunk + node: distinct for every segment (nodes and chunks both
         // advance along the sorted rows), so no atomics and no contention
+        const int nh = half == 0 ? NH : NE - NH;
 #pragma unroll
-        for (int t = 0; t < NE; ++t) {
+        for (int t = 0; t < NH; ++t) {
             const int64_t v = wave_sum_i64((int64_t)acc[t]);
-            if (lane == 0) s_part[w][t] = v;
+            if (lane == 0 && t < nh) s_part[w][t] = v;
         }
         __syncthreads();
         int64_t* out = A.parts + ((size_t)blockIdx.x + (size_t)node) * gram_entries(LKMAX);
+        constexpr int HW = HT / WAVE;                 // waves per half
         for (int t = threadIdx.x; t < NE; t += LB) {
+            const int hh = t < NH ? 0 : 1, tt = t < NH ? t : t - NH;
             int64_t v = 0;
 #pragma unroll
-            for (int i = 0; i < LB / WAVE; ++i) v += s_part[i][t];
+            for (int i = 0; i < HW; ++i) v += s_part[hh * HW + i][tt];
             out[t] = v;
         }
         __syncthreads();
     }
 }
 
-// One wave per eligible node: the sum of its segments' partials (chunks
-// first_chunk .. last_chunk of the sorted rows), in a fixed order.
+// The Gram on the matrix cores, in fp64: per (chunk, node) segment each wave
+// accumulates D = sum over groups of 4 rows of A B with
+// v_mfma_f64_16x16x4_f64, A[a][k] = x1_a of row k (a <= K, else 0) and
+// B[k][c] = x1_c h of row k (c <= K), -g of row k (c = K + 1), else 0, so
+// that D[a][c] = M[a][c] and D[a][K + 1] = b[a].  Lane l supplies A[l % 16]
+// [l / 16] and B[l / 16][l % 16] and holds D[4 r + l / 16][l % 16] in its
+// accumulator r.  The sums are fp64 (each product and addition rounded as the
+// matrix core rounds it, in a fixed order), written as double bits to the
+// segment's partial slot in gram_entries order; no fixed-point scaling.
 template <int K>
-__global__ void __launch_bounds__(WAVE) k_leaf_reduce(LeafArgs A) {
+__global__ void __launch_bounds__(LB) k_leaf_gram_mfma(LeafArgs A) {
+    typedef double d4 __attribute__((ext_vector_type(4)));
     constexpr int NE = gram_entries(K);
-    const int node = blockIdx.x, lane = threadIdx.x;
-    if (!leaf_eligible(A, node)) return;
-    const int64_t c0 = A.off[node] / LCHUNK, c1 = (A.off[node + 1] - 1) / LCHUNK;
-    int64_t acc[NE];
-#pragma unroll
-    for (int t = 0; t < NE; ++t) acc[t] = 0;
-    for (int64_t c = c0 + lane; c <= c1; c += WAVE) {
-        const int64_t* q = A.parts + ((size_t)c + (size_t)node) * gram_entries(LKMAX);
-#pragma unroll
-        for (int t = 0; t < NE; ++t) acc[t] += q[t];
+    static_assert(K + 2 <= 16, "the Gram and the rhs fit one 16 x 16 block");
+    __shared__ float s_mu[LKMAX], s_sd[LKMAX];
+    __shared__ double s_d[LB / WAVE][16 * 16];
+    __shared__ double s_x1[K * 256];
+    if (threadIdx.x < K) {
+        s_mu[threadIdx.x] = A.mu[threadIdx.x];
+        s_sd[threadIdx.x] = A.sd[threadIdx.x];
     }
-    int64_t* out = A.sums + (size_t)node * gram_entries(LKMAX);
+    if (A.x_kind == 1) x1_table<K, LB>(s_x1, A.mu, A.sd);
+    __syncthreads();
+    const int64_t total = A.off[A.n_nodes];
+    const int64_t c0 = (int64_t)blockIdx.x * LCHUNK, c1 = min(total, c0 + LCHUNK);
+    if (c0 >= c1) return;
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+    const int kr = lane >> 4, col = lane & 15;   // the lane's row of a 4-row group, its matrix index
+    for (int node = node_at(A, c0); node < A.n_nodes && A.off[node] < c1; ++node) {
+        const int64_t s = max(c0, A.off[node]), e = min(c1, A.off[node + 1]);
+        if (s >= e || !leaf_eligible(A, node)) continue;   // uniform across the block
+        d4 acc = {0.0, 0.0, 0.0, 0.0};
+        for (int64_t base = s + 4 * w; base < e; base += 4 * (LB / WAVE)) {
+            const int64_t p = base + kr;
+            double av = 0.0, bv = 0.0;
+            if (p < e) {
+                const float2 gh = A.sorted_gh[p];
+                double x1 = 0.0;
+                if (col < K) {
+                    if (A.x_kind == 1) {
+                        const uint2 v = reinterpret_cast<const uint2*>(A.sorted_x)[p];
+                        const uint32_t word = col < 4 ? v.x : v.y;
+                        x1 = s_x1[col * 256 + ((word >> (8 * (col & 3))) & 0xffu)];
+                    } else {
+                        const float xv = reinterpret_cast<const float*>(A.sorted_x)[(size_t)p * K + col];
+                        x1 = (double)((xv - s_mu[col]) / s_sd[col]);
+                    }
+                } else if (col == K) {
+                    x1 = 1.0;
+                }
+                av = x1;
+                bv = col <= K ? x1 * (double)gh.y : (col == K + 1 ? -(double)gh.x : 0.0);
+            }
+            acc = __builtin_amdgcn_mfma_f64_16x16x4f64(av, bv, acc, 0, 0, 0);
+        }
 #pragma unroll
-    for (int t = 0; t < NE; ++t) {
-        const int64_t v = wave_sum_i64(acc[t]);
-        if (lane == 0) out[t] = v;
+        for (int r = 0; r < 4; ++r) s_d[w][(4 * r + kr) * 16 + col] = acc[r];
+        __syncthreads();
+        // the segment: the waves' sums in order, entries in gram_entries order
+        int64_t* out = A.parts + ((size_t)blockIdx.x + (size_t)node) * gram_entries(LKMAX);
+        for (int t = threadIdx.x; t < NE; t += LB) {
+            int i;
+            if (t < (K + 1) * (K + 2) / 2) {   // M[a][b], a <= b, row by row
+                int a = 0, r = t;
+                while (r >= K + 1 - a) {
+                    r -= K + 1 - a;
+                    ++a;
+                }
+                i = a * 16 + a + r;
+            } else {                           // b[a] = D[a][K + 1]
+                i = (t - (K + 1) * (K + 2) / 2) * 16 + K + 1;
+            }
+            double v = s_d[0][i];
+#pragma unroll
+            for (int q = 1; q < LB / WAVE; ++q) v += s_d[q][i];
+            out[t] = __double_as_longlong(v);
+        }
+        __syncthreads();
+    }
+}
+
+// One block per eligible node: the sum of its segments' partials (chunks
+// first_chunk .. last_chunk of the sorted rows) in a fixed order -- wave w
+// takes segments w, w + RW, ... (lane t: entry t), then the waves' sums in
+// order.  F64: the partials are fp64 bits (k_leaf_gram_mfma).
+constexpr int RB = 1024;
+template <int K, bool F64>
+__global__ void __launch_bounds__(RB) k_leaf_reduce(LeafArgs A) {
+    constexpr int NE = gram_entries(K);
+    constexpr int RW = RB / WAVE;
+    static_assert(NE <= WAVE, "one lane per entry");
+    __shared__ int64_t s_w[RW][NE];
+    const int node = blockIdx.x;
+    if (!leaf_eligible(A, node)) return;
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+    const int64_t c0 = A.off[node] / LCHUNK, c1 = (A.off[node + 1] - 1) / LCHUNK;
+    if (lane < NE) {
+        int64_t ai = 0;
+        double ad = 0.0;
+        for (int64_t c = c0 + w; c <= c1; c += RW) {
+            const int64_t v = A.parts[((size_t)c + (size_t)node) * gram_entries(LKMAX) + lane];
+            if (F64) ad += __longlong_as_double(v);
+            else ai += v;
+        }
+        s_w[w][lane] = F64 ? __double_as_longlong(ad) : ai;
+    }
+    __syncthreads();
+    if (threadIdx.x < NE) {
+        int64_t* out = A.sums + (size_t)node * gram_entries(LKMAX);
+        if (F64) {
+            double v = __longlong_as_double(s_w[0][threadIdx.x]);
+            for (int q = 1; q < RW; ++q) v += __longlong_as_double(s_w[q][threadIdx.x]);
+            out[threadIdx.x] = __double_as_longlong(v);
+        } else {
+            int64_t v = 0;
+            for (int q = 0; q < RW; ++q) v += s_w[q][threadIdx.x];
+            out[threadIdx.x] = v;
+        }
     }
 }
 
@@ -463,6 +606,7 @@ __global__ void __launch_bounds__(LB) k_leaf_solve(LeafArgs A, float* out_W, flo
     out_b[node] = 0.0f;
     if (!leaf_eligible(A, node) || A.st->status != 0) return;
     const int64_t* q = A.sums + (size_t)node * gram_entries(LKMAX);
+    const bool f64 = A.gram_f64 != 0;   // fp64 sums (MFMA) or fixed point
     const double iM = ldexp(1.0, -A.st->sM), ib = ldexp(1.0, -A.st->sb);
     double M[N][N], r[N];
     int t = 0;
@@ -470,11 +614,15 @@ __global__ void __launch_bounds__(LB) k_leaf_solve(LeafArgs A, float* out_W, flo
     for (int a = 0; a < N; ++a)
 #pragma unroll
         for (int b = a; b < N; ++b) {
-            M[a][b] = (double)q[t++] * iM;
+            M[a][b] = f64 ? __longlong_as_double(q[t]) : (double)q[t] * iM;
+            ++t;
             M[b][a] = M[a][b];
         }
 #pragma unroll
-    for (int a = 0; a < N; ++a) r[a] = (double)q[t++] * ib;
+    for (int a = 0; a < N; ++a) {
+        r[a] = f64 ? __longlong_as_double(q[t]) : (double)q[t] * ib;
+        ++t;
+    }
 #pragma unroll
     for (int a = 0; a < K; ++a) M[a][a] += A.lam;    // reg = lam * I ...
     M[K][K] += 1e-8;                                  // ... but the bias (neural_leaves.py:85-86)
@@ -528,9 +676,32 @@ __global__ void __launch_bounds__(LB) k_leaf_solve(LeafArgs A, float* out_W, flo
 #pragma unroll
     for (int j = 0; j < K; ++j) out_W[node * K + j] = (float)th[j];
     out_b[node] = (float)th[K];
+    atomicAdd(&A.st->n_fit, 1);
 }
 
-__global__ void k_leaf_status(const LeafStats* st, int32_t* out) { out[0] = st->status; }
+__global__ void k_leaf_status(const LeafStats* st, int32_t* out) {
+    out[0] = st->status;
+    out[1] = st->n_fit;
+}
+
+// The fold of the linear models into raw space (neural_leaves.py:178-184) in
+// the order and fp32 roundings of the reference's torch expressions: per node,
+// prod_j = W[j] * (mu[j] / sd[j]), acc = prod_0 + prod_1 + ... left to right,
+// value = value_in + lr * (b - acc), linear[j] = (lr * W[j]) / sd[j].
+__global__ void __launch_bounds__(LB) k_leaf_fold(int n_nodes, int K, const float* W, const float* b,
+                                                  const float* mu, const float* sd, float lr,
+                                                  const float* value_in, float* out_value, float* out_linear) {
+    const int node = blockIdx.x * LB + threadIdx.x;
+    if (node >= n_nodes) return;
+    float acc = 0.0f;
+    for (int j = 0; j < K; ++j) {
+        const float wj = W[(size_t)node * K + j];
+        const float prod = wj * (mu[j] / sd[j]);
+        acc = j == 0 ? prod : acc + prod;
+        out_linear[(size_t)node * K + j] = (lr * wj) / sd[j];
+    }
+    out_value[node] = value_in[node] + lr * (b[node] - acc);
+}
 
 
 
@@ -715,9 +886,15 @@ void launch_leaf_fit(LeafArgs& A, float* out_W, float* out_b, float* out_lo, flo
     if (row_blocks > 0) {
         if (lds) k_leaf_scatter<K, true><<<row_blocks, LSB, 0, stream>>>(A);
         else k_leaf_scatter<K, false><<<row_blocks, LSB, 0, stream>>>(A);
-        if (A.n > 1024) k_leaf_gram<K, true><<<(int)((A.n + LCHUNK - 1) / LCHUNK), LB, 0, stream>>>(A);
-        else k_leaf_gram<K, false><<<(int)((A.n + LCHUNK - 1) / LCHUNK), LB, 0, stream>>>(A);
-        k_leaf_reduce<K><<<A.n_nodes, WAVE, 0, stream>>>(A);
+        const int chunks = (int)((A.n + LCHUNK - 1) / LCHUNK);
+        if (A.gram_f64) {
+            k_leaf_gram_mfma<K><<<chunks, LB, 0, stream>>>(A);
+            k_leaf_reduce<K, true><<<A.n_nodes, RB, 0, stream>>>(A);
+        } else {
+            if (A.n > 1024) k_leaf_gram<K, true><<<chunks, LB, 0, stream>>>(A);
+            else k_leaf_gram<K, false><<<chunks, LB, 0, stream>>>(A);
+            k_leaf_reduce<K, false><<<A.n_nodes, RB, 0, stream>>>(A);
+        }
     }
     k_leaf_solve<K><<<(A.n_nodes + LB - 1) / LB, LB, 0, stream>>>(A, out_W, out_b, out_lo, out_hi, out_count);
 }
@@ -735,11 +912,12 @@ size_t yabt_leaf_fit_workspace_bytes(int64_t n, int n_nodes, int K) {
 
 int yabt_leaf_fit(int x_kind, const void* X, int64_t ldx, int64_t n, const int32_t* feats, int K, const float* mu,
                   const float* sd, const float* grad, const float* hess, const int64_t* leaf_of_row,
-                  const int64_t* feature, int n_nodes, int min_samples, double lam, void* workspace,
-                  size_t workspace_bytes, float* out_W, float* out_b, float* out_lo, float* out_hi,
-                  int64_t* out_count, int32_t* out_status, hipStream_t stream) {
+                  const int64_t* feature, int n_nodes, int min_samples, double lam, int gram_mode,
+                  void* workspace, size_t workspace_bytes, float* out_W, float* out_b, float* out_lo,
+                  float* out_hi, int64_t* out_count, int32_t* out_status, hipStream_t stream) {
     if (n < 0 || n > 0xFFFFFFFFll || n_nodes < 1 || K < 1 || K > LKMAX || (x_kind != 0 && x_kind != 1))
         return fail(-2, "yabt_leaf_fit: bad sizes (need 0 <= n < 2^32, n_nodes >= 1, 1 <= K <= 8, x_kind 0 or 1)");
+    if (gram_mode != 0 && gram_mode != 1) return fail(-2, "yabt_leaf_fit: gram_mode must be 0 or 1");
     if (!X || !feats || !mu || !sd || !grad || !hess || !leaf_of_row || !feature || !workspace || !out_W || !out_b ||
         !out_lo || !out_hi || !out_count || !out_status)
         return fail(-2, "yabt_leaf_fit: null pointer argument");
@@ -762,6 +940,7 @@ int yabt_leaf_fit(int x_kind, const void* X, int64_t ldx, int64_t n, const int32
     A.n_nodes = n_nodes;
     A.min_samples = min_samples;
     A.lam = lam;
+    A.gram_f64 = gram_mode;
     switch (K) {
         case 1: launch_leaf_fit<1>(A, out_W, out_b, out_lo, out_hi, out_count, stream); break;
         case 2: launch_leaf_fit<2>(A, out_W, out_b, out_lo, out_hi, out_count, stream); break;
@@ -774,6 +953,16 @@ int yabt_leaf_fit(int x_kind, const void* X, int64_t ldx, int64_t n, const int32
     }
     k_leaf_status<<<1, 1, 0, stream>>>(A.st, out_status);
     return launch_status("yabt_leaf_fit launch");
+}
+
+int yabt_leaf_fold(int n_nodes, int K, const float* W, const float* b, const float* mu, const float* sd, float lr,
+                   const float* value_in, float* out_value, float* out_linear, hipStream_t stream) {
+    if (n_nodes < 1 || K < 1 || K > LKMAX) return fail(-2, "yabt_leaf_fold: bad sizes (n_nodes >= 1, 1 <= K <= 8)");
+    if (!W || !b || !mu || !sd || !value_in || !out_value || !out_linear)
+        return fail(-2, "yabt_leaf_fold: null pointer argument");
+    k_leaf_fold<<<(n_nodes + LB - 1) / LB, LB, 0, stream>>>(n_nodes, K, W, b, mu, sd, lr, value_in, out_value,
+                                                           out_linear);
+    return launch_status("yabt_leaf_fold launch");
 }
 
 size_t yabt_leaf_moments_workspace_bytes(int64_t n) {

@@ -20,7 +20,7 @@ from dataclasses import replace
 import torch
 
 from . import _lib, boost_ops
-from .tree import LEAF, Tree
+from .tree import Tree
 
 
 def _stream(dev: torch.device):
@@ -54,17 +54,23 @@ def _select_features(tree: Tree, Xraw: torch.Tensor, grad: torch.Tensor, k: int)
     return torch.cat([used, extra])
 
 
-def leaf_fit(X: torch.Tensor, x_kind: int, feats: torch.Tensor, mu: torch.Tensor, sd: torch.Tensor,
-             grad: torch.Tensor, hess: torch.Tensor, leaf_idx: torch.Tensor, feature: torch.Tensor,
-             min_samples: int, lam: float):
-    """One ``yabt_leaf_fit`` call.  X: fp32 (n, F) row-major (x_kind 0) or
-    uint8 feature-major (F, ld >= n) (x_kind 1).  Returns (W (N, K), b (N),
-    lo (N, K), hi (N, K), count (N)) on X's device; W, b act on the
-    standardised inputs."""
+# Gram sums of yabt_leaf_fit: "exact" (the fp64 products rounded to int64
+# fixed point and summed exactly) or "mfma" (fp64 sums on the matrix cores).
+GRAM_MODES = {"exact": 0, "mfma": 1}
+GRAM = "exact"
+
+
+def _leaf_fit(X: torch.Tensor, x_kind: int, feats: torch.Tensor, mu: torch.Tensor, sd: torch.Tensor,
+              grad: torch.Tensor, hess: torch.Tensor, leaf_idx: torch.Tensor, feature: torch.Tensor,
+              min_samples: int, lam: float, gram: str | None = None):
+    """Enqueue one ``yabt_leaf_fit`` call; returns (W, b, lo, hi, count,
+    status) on X's device without waiting: status = [0 / -1 / -2, leaves
+    fitted] (see _check_status)."""
     lib = _lib.load()
     dev = X.device
     if dev.type != "cuda":
         raise RuntimeError("yabt_leaf_fit needs device tensors")
+    mode = GRAM_MODES[GRAM if gram is None else gram]
     n = int(grad.shape[0])
     K = int(feats.numel())
     N = int(feature.shape[0])
@@ -94,17 +100,32 @@ def leaf_fit(X: torch.Tensor, x_kind: int, feats: torch.Tensor, mu: torch.Tensor
     lo = torch.empty((N, K), dtype=torch.float32, device=dev)
     hi = torch.empty((N, K), dtype=torch.float32, device=dev)
     cnt = torch.empty(N, dtype=torch.int64, device=dev)
-    status = torch.empty(1, dtype=torch.int32, device=dev)
+    status = torch.empty(2, dtype=torch.int32, device=dev)
     _lib.check(lib.yabt_leaf_fit(x_kind, X.data_ptr(), ldx, n, fi.data_ptr(), K, m.data_ptr(), s.data_ptr(),
                                  g.data_ptr(), h.data_ptr(), li.data_ptr(), ft.data_ptr(), N, int(min_samples),
-                                 float(lam), ws.data_ptr(), nbytes, W.data_ptr(), b.data_ptr(), lo.data_ptr(),
+                                 float(lam), mode, ws.data_ptr(), nbytes, W.data_ptr(), b.data_ptr(), lo.data_ptr(),
                                  hi.data_ptr(), cnt.data_ptr(), status.data_ptr(), _stream(dev)),
                "yabt_leaf_fit")
-    st = int(status.item())
+    return W, b, lo, hi, cnt, status
+
+
+def _check_status(st: int) -> None:
     if st == -1:
         raise ValueError("yabt_leaf_fit: a leaf id is out of range or an input is not finite")
     if st == -2:
         raise RuntimeError("yabt_leaf_fit: singular leaf system (torch.linalg.solve would raise)")
+
+
+def leaf_fit(X: torch.Tensor, x_kind: int, feats: torch.Tensor, mu: torch.Tensor, sd: torch.Tensor,
+             grad: torch.Tensor, hess: torch.Tensor, leaf_idx: torch.Tensor, feature: torch.Tensor,
+             min_samples: int, lam: float, gram: str | None = None):
+    """One ``yabt_leaf_fit`` call.  X: fp32 (n, F) row-major (x_kind 0) or
+    uint8 feature-major (F, ld >= n) (x_kind 1).  Returns (W (N, K), b (N),
+    lo (N, K), hi (N, K), count (N)) on X's device; W, b act on the
+    standardised inputs.  gram: "exact" or "mfma" (default GRAM)."""
+    W, b, lo, hi, cnt, status = _leaf_fit(X, x_kind, feats, mu, sd, grad, hess, leaf_idx, feature, min_samples,
+                                          lam, gram)
+    _check_status(int(status[0].item()))
     return W, b, lo, hi, cnt
 
 
@@ -130,16 +151,23 @@ def leaf_moments(X: torch.Tensor, x_kind: int, feats: torch.Tensor, n: int):
 
 
 def fold(tree: Tree, W, db, mu, sd, lr, feats, lo, hi) -> Tree:
-    """Normalisation and shrinkage folded into raw space (neural_leaves.py:178-184).
-    The K products are added left to right, the order torch's CPU reduction
-    takes for the reference's K = 8 inputs."""
-    prod = W * (mu / sd)
-    acc = prod[:, 0].clone()
-    for j in range(1, prod.shape[1]):
-        acc = acc + prod[:, j]
-    value = tree.value.to(W.device) + lr * (db - acc)
-    return replace(tree, value=value, leaf_net_feats=feats, leaf_net_linear=lr * W / sd,
-                   leaf_net_lo=lo, leaf_net_hi=hi)
+    """Normalisation and shrinkage folded into raw space (neural_leaves.py:178-184)
+    by ``yabt_leaf_fold``: the reference's torch expressions in their fp32
+    order, the K products added left to right as torch's CPU reduction adds
+    the reference's K = 8 inputs."""
+    lib = _lib.load()
+    dev = W.device
+    N, K = int(W.shape[0]), int(W.shape[1])
+    value_in = tree.value.to(dev, torch.float32).contiguous()
+    value = torch.empty_like(value_in)
+    linear = torch.empty((N, K), dtype=torch.float32, device=dev)
+    Wc, bc = W.contiguous(), db.contiguous()
+    m, s = mu.to(dev, torch.float32).contiguous(), sd.to(dev, torch.float32).contiguous()
+    _lib.check(lib.yabt_leaf_fold(N, K, Wc.data_ptr(), bc.data_ptr(), m.data_ptr(), s.data_ptr(), float(lr),
+                                  value_in.data_ptr(), value.data_ptr(), linear.data_ptr(), _stream(dev)),
+               "yabt_leaf_fold")
+    return replace(tree, value=value, leaf_net_feats=feats, leaf_net_linear=linear, leaf_net_lo=lo,
+                   leaf_net_hi=hi)
 
 
 def fit_leaf_networks(tree: Tree, Xraw: torch.Tensor, y: torch.Tensor, margin: torch.Tensor, loss_fn,
@@ -159,13 +187,14 @@ def fit_leaf_networks(tree: Tree, Xraw: torch.Tensor, y: torch.Tensor, margin: t
         return tree
     X = Xraw if Xraw.dtype == torch.float32 and Xraw.stride(1) == 1 else Xraw.float().contiguous()
     mu, sd = leaf_moments(X, 0, feats, X.shape[0])
-    W, db, lo, hi, cnt = leaf_fit(X, 0, feats, mu, sd, grad, hess, leaf_idx, tree_d.feature,
-                                  getattr(params, "leaf_net_min_samples", 50),
-                                  getattr(params, "leaf_net_l2", 1.0))
-    eligible = (tree_d.feature == LEAF) & (cnt >= getattr(params, "leaf_net_min_samples", 50))
-    if not bool(eligible.any()):
-        return tree
-    return fold(tree_d, W, db, mu, sd, params.learning_rate, feats, lo, hi)
+    W, db, lo, hi, cnt, status = _leaf_fit(X, 0, feats, mu, sd, grad, hess, leaf_idx, tree_d.feature,
+                                           getattr(params, "leaf_net_min_samples", 50),
+                                           getattr(params, "leaf_net_l2", 1.0))
+    folded = fold(tree_d, W, db, mu, sd, params.learning_rate, feats, lo, hi)
+    st, n_fit = status.tolist()   # the one wait for the device
+    _check_status(st)
+    # no eligible leaf: the tree is returned unchanged (neural_leaves.py:156-158)
+    return folded if n_fit > 0 else tree
 
 
 def fit_leaf_networks_binned(tree: Tree, bins_fm: torch.Tensor, grad: torch.Tensor, hess: torch.Tensor,
@@ -187,12 +216,12 @@ def fit_leaf_networks_binned(tree: Tree, bins_fm: torch.Tensor, grad: torch.Tens
         Xraw = bins_fm[:, :n].t().float()
         feats = _select_features(replace(tree, feature=feature), Xraw, grad, k)
     mu, sd = leaf_moments(bins_fm, 1, feats, n)
-    W, db, lo, hi, cnt = leaf_fit(bins_fm, 1, feats, mu, sd, grad, hess, leaf_idx, feature,
-                                  getattr(params, "leaf_net_min_samples", 50),
-                                  getattr(params, "leaf_net_l2", 1.0))
-    # no eligible leaf: the tree is returned unchanged (neural_leaves.py:156-158)
-    eligible = (feature == LEAF) & (cnt >= getattr(params, "leaf_net_min_samples", 50))
-    if not bool(eligible.any()):
-        return tree
+    W, db, lo, hi, cnt, status = _leaf_fit(bins_fm, 1, feats, mu, sd, grad, hess, leaf_idx, feature,
+                                           getattr(params, "leaf_net_min_samples", 50),
+                                           getattr(params, "leaf_net_l2", 1.0))
     tree_d = replace(tree, feature=feature, value=tree.value.to(dev))
-    return fold(tree_d, W, db, mu, sd, params.learning_rate, feats, lo, hi)
+    folded = fold(tree_d, W, db, mu, sd, params.learning_rate, feats, lo, hi)
+    st, n_fit = status.tolist()   # the one wait for the device
+    _check_status(st)
+    # no eligible leaf: the tree is returned unchanged (neural_leaves.py:156-158)
+    return folded if n_fit > 0 else tree
