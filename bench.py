@@ -36,12 +36,15 @@ Also reported, outside the timed region: ``reference_arithmetic`` (the same
 tree grown with the reference's own fp32 arithmetic, yabt_grow_ref, whose
 trees equal grow.c's: ms per tree with and without the leaf models, its root
 histogram's time and share of HBM peak, and its split differences from the
-exact tree, see reference_arithmetic) and ``boosting`` (whole estimator fits,
-see boosting_fits).
+exact tree, see reference_arithmetic), ``leaf_gram`` (the linear-leaf step
+with the Gram sums on the VALU in exact fixed point and in fp64 on the matrix
+cores, see leaf_gram_compare) and ``boosting`` (whole estimator fits, see
+boosting_fits).
 
 Usage: python bench.py [--gpus 1] [--steps 5] [--warmup 1] [--no-cpu]
                        [--ref-steps 1] [--no-boosting]
        python bench.py --counters
+       python bench.py --leaf-compare
        python bench.py --boosting-only
 """
 
@@ -372,6 +375,40 @@ def reference_arithmetic(torch, lay, g, h, nbins, steps: int, exact_res, neural:
     return out
 
 
+def leaf_gram_compare(torch, lay, g, h, nbins, reps: int = 10) -> dict:
+    """The linear-leaf step of one 255-leaf tree (moments, fit, fold; g, h at
+    margin + value[leaf] of a quadratic objective) with the Gram sums on the
+    VALU in exact int64 fixed point ("exact", the default) and in fp64 on the
+    matrix cores ("mfma": v_mfma_f64_16x16x4_f64): ms per step, mean of
+    ``reps`` after two warm-ups each, wall clock around device syncs."""
+    from yabt_amd import grow_hip as G
+    from yabt_amd import neural_leaves as NL
+    from yabt_amd.neural_leaves import fit_leaf_networks_binned
+    from yabt_amd.tree import Tree
+    n = lay.n
+    res = G.grow_device(lay, g, h, nbins, **PARAMS)
+    leaf = G.leaf_ids(res, n, lay.F, MAX_LEAVES)
+    tree = Tree(res.feature, res.thr_bin.float(), res.left, res.right, res.value, 0)
+    g2 = g + h * res.value[leaf]
+    out = {}
+    keep = NL.GRAM
+    try:
+        for mode in ("exact", "mfma"):
+            NL.GRAM = mode
+            for _ in range(2):
+                fit_leaf_networks_binned(tree, lay.fm, g2, h, leaf, LeafNetParams, n=n)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fit_leaf_networks_binned(tree, lay.fm, g2, h, leaf, LeafNetParams, n=n)
+            torch.cuda.synchronize()
+            out[f"ms_leaf_step_{mode}"] = round((time.perf_counter() - t0) * 1e3 / reps, 3)
+    finally:
+        NL.GRAM = keep
+    out["default"] = keep
+    return out
+
+
 def cpu_other_workloads(O, reference: bool, threads: int) -> dict:
     """The same C grower, one tree each, on the other tree workloads (context
     for the estimator timings): the binary 1M x 28 workload (28 bins, depth 8,
@@ -538,6 +575,8 @@ def main() -> None:
                     help="only the estimator fits and depth-6 trees (one JSON line of their timings)")
     ap.add_argument("--counters", action="store_true",
                     help="only launch the copy and root-histogram kernels for rocprofv3 --pmc")
+    ap.add_argument("--leaf-compare", action="store_true",
+                    help="only the linear-leaf step in both Gram modes (one JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (got --gpus {args.gpus}); the tree-growing path "
@@ -559,6 +598,10 @@ def main() -> None:
         log("[bench] copy and root-histogram kernels for counter passes")
         counter_launches(torch, lay, g, h)
         log("[bench] done")
+        return
+    if args.leaf_compare:
+        log("[bench] linear-leaf step, exact and fp64 MFMA Gram sums")
+        print(json.dumps({"leaf_gram": leaf_gram_compare(torch, lay, g, h, nbins)}), flush=True)
         return
 
     log("[bench] root histogram kernel")
@@ -641,6 +684,9 @@ def main() -> None:
     }
     if args.ref_steps > 0:
         line["reference_arithmetic"] = reference_arithmetic(torch, lay, g, h, nbins, args.ref_steps, res, neural)
+    if neural:
+        log("[bench] linear-leaf step, exact and fp64 MFMA Gram sums")
+        line["leaf_gram"] = leaf_gram_compare(torch, lay, g, h, nbins)
     if not args.no_boosting:
         del lay, g, h
         torch.cuda.empty_cache()
