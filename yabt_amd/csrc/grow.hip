@@ -520,9 +520,9 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : 2 * SCAN_FEATS * WA
                 const ScanRec& o = s_rec[cc * SCAN_FEATS + i];
                 if (rec_beats(o.sel, o.f, o.b, s_rec[bi].sel, s_rec[bi].f, s_rec[bi].b)) bi = cc * SCAN_FEATS + i;
             }
-            A.rec[(size_t)cc * gridDim.x + blockIdx.x] = s_rec[bi];
+            publish_record(&A.rec[(size_t)cc * gridDim.x + blockIdx.x], s_rec[bi]);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        record_published();
         const uint32_t t = atomicAdd(&st->scan_ticket, 1u);
         s_last = (t == gridDim.x - 1);
     }

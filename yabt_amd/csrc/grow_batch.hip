@@ -99,7 +99,7 @@ struct State {
     int32_t n_round;                     // splits computed this round
     int32_t n_pend;                      // Pend entries used
     int32_t round;                       // controllers run
-    uint32_t scan_ticket;
+    uint32_t scan_ticket;                // splits whose scan blocks have all finished
     int32_t pad;
     int32_t root_pend;                   // the root's computed split, -1: none
     float root_gain;                     // the root's table gain
@@ -110,6 +110,7 @@ struct State {
     int32_t unit_off[KMAX + 1];          // gather units of this round's built children, prefix sums
     int32_t pad3;
     int64_t unit_rows;                   // rows per gather unit (a child's last unit: the rest)
+    uint32_t split_ticket[KMAX];         // scan blocks of each split finished
 };
 
 // A run of final-leaf rows for the leaf-id pass: positions [lo, hi) of a row
@@ -205,6 +206,7 @@ __global__ void k_setup_finish(Args A) {
     st->n_pend = 0;
     st->round = 0;
     st->scan_ticket = 0;
+    for (int i = 0; i < KMAX; ++i) st->split_ticket[i] = 0;
     st->root_pend = -1;
     st->root_gain = -INFINITY;
     st->n_nodes = 1;
@@ -479,7 +481,7 @@ struct Table {
     YABT_LDS int32_t* root_pend;
 };
 
-// Carve of the controller's LDS at `base` (null: size only).
+// Carve of the controller's LDS at `base` into *T (base null: size only).
 __host__ __device__ inline size_t table_carve(char* base, int L, int pend_cap, Table* T) {
     size_t off = 0;
     auto take = [&](size_t bytes) {
@@ -506,7 +508,9 @@ __host__ __device__ inline size_t table_carve(char* base, int L, int pend_cap, T
     char* cidx = take(sizeof(int16_t) * (L + 2 * (size_t)pend_cap));
     char* ccommit = take(pend_cap);
 #if defined(__HIP_DEVICE_COMPILE__)
-    if (T) {
+    // tested on base, not on T: a null test of the table's own address keeps
+    // the table in private (scratch) memory
+    if (base) {
         T->gain = (YABT_LDS float*)gain;
         T->cgain = (YABT_LDS float(*)[2])cgain;
         T->ckey = (YABT_LDS float*)ckey;
@@ -636,7 +640,7 @@ __device__ __forceinline__ void write_commit(const Args& A, int p, int nid, int 
 // Ties in key may be ordered otherwise than cgrow's table: the plan decides
 // only which splits are computed when, never the tree (the commits replay
 // cgrow's table exactly), and the split the commits wait for is always taken.
-__device__ void control(const Args& A, Table& T, int nn, int na, int np, const ScanRec* root, int lane) {
+__device__ __forceinline__ void control(const Args& A, Table& T, int nn, int na, int np, const ScanRec* root, int lane) {
     State* st = A.st;
     const int L = A.max_leaves;
     const int nn0 = nn;
@@ -669,7 +673,9 @@ __device__ void control(const Args& A, Table& T, int nn, int na, int np, const S
     }
     // the commits' node arrays, then the cleared parent values
     for (int i = lane; i < ncm; i += WAVE) write_commit(A, T.commit_p[i], T.commit_nid[i], nn0 + 2 * i);
-    __threadfence();
+    // the wave's stores so far have completed (at this XCD's L2, where the
+    // clears below go too)
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     for (int i = lane; i < ncm; i += WAVE) A.value[T.commit_nid[i]] = 0.0f;
     // store the committed table
     for (int a = lane; a < na; a += WAVE) {
@@ -1067,11 +1073,17 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
                 const ScanRec& o = s_rec[cc * SCAN_FEATS + i];
                 if (rec_beats(o.sel, o.f, o.b, s_rec[bi].sel, s_rec[bi].f, s_rec[bi].b)) bi = cc * SCAN_FEATS + i;
             }
-            A.rec[((size_t)y * 2 + cc) * gridDim.x + blockIdx.x] = s_rec[bi];
+            publish_record(&A.rec[((size_t)y * 2 + cc) * gridDim.x + blockIdx.x], s_rec[bi]);
         }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-        const uint32_t t = atomicAdd(&st->scan_ticket, 1u);
-        s_last = (t == gridDim.x * (uint32_t)nr - 1);
+        record_published();
+        // two levels of tickets, so no one address takes every block's
+        // atomic: the last block of split y takes the launch's ticket
+        bool lst = false;
+        if (atomicAdd(&st->split_ticket[y], 1u) == gridDim.x - 1) {
+            st->split_ticket[y] = 0;
+            lst = atomicAdd(&st->scan_ticket, 1u) == (uint32_t)nr - 1;
+        }
+        s_last = lst;
     }
     __syncthreads();
     const bool last = s_last != 0;

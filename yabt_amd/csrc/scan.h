@@ -292,6 +292,29 @@ __device__ __forceinline__ ScanRec empty_record() {
     return e;
 }
 
+// A block's scan record for the block that takes the last ticket of the
+// launch (which may run on another XCD, behind another L2).  The record is
+// written with agent-scope atomic stores, which write through to the
+// device's point of coherence, and record_published() waits for them; the
+// ticket that follows can then be a relaxed atomic.  An agent-scope release
+// fence here would write back the whole L2's dirty lines instead, and with
+// tens of blocks per XCD those writebacks queue behind one another.  The
+// reader takes the last ticket, then an agent-scope acquire fence (which
+// invalidates its L2) before it loads the records.
+static_assert(sizeof(ScanRec) % 8 == 0, "a record is whole 64-bit words");
+__device__ __forceinline__ void publish_record(ScanRec* dst, const ScanRec& r) {
+    uint64_t w[sizeof(ScanRec) / 8];
+    __builtin_memcpy(w, &r, sizeof(ScanRec));
+    uint64_t* d = reinterpret_cast<uint64_t*>(dst);
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(ScanRec) / 8); ++i)
+        __hip_atomic_store(d + i, w[i], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The calling wave's stores so far have completed (publish_record's are at
+// the device's point of coherence).
+__device__ __forceinline__ void record_published() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // One wave (all 64 lanes active): the best of rec[0, n) in every lane (b = -1:
 // none valid).
 __device__ inline ScanRec wave_best_record(const ScanRec* rec, int n, int lane) {
