@@ -192,6 +192,22 @@ __device__ __forceinline__ float wave_max_f32(float v) {
                  fmaxf(__int_as_float(__builtin_amdgcn_readlane(b, 32)), __int_as_float(__builtin_amdgcn_readlane(b, 48))));
 }
 
+// Maximum of an unsigned 64-bit value over the 64 lanes, in every lane.
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
+    uint64_t o = dpp64<DPP_ROW_ROR + 8>(v);
+    v = o > v ? o : v;
+    o = dpp64<DPP_ROW_ROR + 4>(v);
+    v = o > v ? o : v;
+    o = dpp64<DPP_ROW_ROR + 2>(v);
+    v = o > v ? o : v;
+    o = dpp64<DPP_ROW_ROR + 1>(v);
+    v = o > v ? o : v;
+    const uint64_t a = (uint64_t)readlane64((int64_t)v, 0), b = (uint64_t)readlane64((int64_t)v, 16);
+    const uint64_t c = (uint64_t)readlane64((int64_t)v, 32), d = (uint64_t)readlane64((int64_t)v, 48);
+    const uint64_t ab = a > b ? a : b, cd = c > d ? c : d;
+    return ab > cd ? ab : cd;
+}
+
 __device__ __forceinline__ int wave_min_i32(int v) {
     v = min(v, (int)dpp32<DPP_ROW_ROR + 8>((uint32_t)v));
     v = min(v, (int)dpp32<DPP_ROW_ROR + 4>((uint32_t)v));

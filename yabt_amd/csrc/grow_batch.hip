@@ -683,6 +683,7 @@ __device__ __forceinline__ void control(const Args& A, Table& T, int nn, int na,
         A.leaf_node[a] = T.node[a];
     }
     int status = 0, j = 0;
+    int my_pick = -1;   // lane t: the candidate taken as the round's split t
     const int np0 = np;
     if (best >= 0) {
         // keys of the uncommitted computed splits' nodes: a committed leaf's
@@ -747,32 +748,27 @@ __device__ __forceinline__ void control(const Args& A, Table& T, int nn, int na,
         }
         wave_sync();
         // take best, then the largest keys (the lowest candidate on ties).
-        // Short lists sit in registers, R entries per lane: each lane keeps
-        // its best candidate, a pick is two wave reductions, and the budget
-        // count a ballot per register.
+        // Short lists sit in registers, R entries per lane, each candidate
+        // packed as its key's bits (positive floats order as unsigned
+        // integers) over its inverted index, so that a pick is one 64-bit
+        // wave maximum; each lane keeps its best, and the budget count is a
+        // ballot per register.  Lane t keeps the round's split t.
         constexpr int R = 4;
         const bool in_regs = m <= R * WAVE && mb <= R * WAVE;
-        float ck[R], bk[R];
-        int ci[R];
-        float lbk = 0.0f;   // this lane's best candidate: key and index
-        int lbi = INT_MAX;
+        float bk[R];
+        uint64_t pc[R];
+        uint64_t lb = 0;   // this lane's best packed candidate (0: none)
         auto lane_best = [&]() {
-            lbk = 0.0f;
-            lbi = INT_MAX;
+            lb = 0;
 #pragma unroll
-            for (int r = 0; r < R; ++r) {
-                if (ck[r] > lbk || (ck[r] == lbk && ck[r] > 0.0f && ci[r] < lbi)) {
-                    lbk = ck[r];
-                    lbi = ci[r];
-                }
-            }
+            for (int r = 0; r < R; ++r) lb = pc[r] > lb ? pc[r] : lb;
         };
         if (in_regs) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int i = lane + r * WAVE;
-                ck[r] = i < m ? T.ckand[i] : -INFINITY;
-                ci[r] = i < m ? (int)T.cidx[i] : INT_MAX;
+                const float k = i < m ? T.ckand[i] : 0.0f;   // listed keys are > 0
+                pc[r] = i < m ? ((uint64_t)__float_as_uint(k) << 32) | (uint32_t)(INT_MAX - (int)T.cidx[i]) : 0;
                 bk[r] = i < mb ? T.cbud[i] : -INFINITY;
             }
             lane_best();
@@ -787,24 +783,25 @@ __device__ __forceinline__ void control(const Args& A, Table& T, int nn, int na,
                 break;
             }
             if (j > 0 && np + L - na > A.pend_cap - 1) break;
-            if (lane == 0) {
-                T.plan_src[j] = cand < na ? T.src[cand] : (int16_t)(cand - na);
-                if (cpos >= 0) T.ckand[cpos] = -INFINITY;   // the list in LDS: taken
+            if (lane == j) my_pick = cand;
+            if (cpos >= 0) {   // the list in LDS: taken
+                if (lane == 0) T.ckand[cpos] = -INFINITY;
+                wave_sync();
             }
             ++np;
             ++j;
-            wave_sync();
             if (j >= KMAX) break;
             float key;
             int e = 0;
             if (in_regs) {
-                key = wave_max_f32(lbk);
-                if (!(key > 0.0f)) break;
-                cand = wave_min_i32(lbk == key ? lbi : INT_MAX);
-                if (lbi == cand) {   // its lane drops it and looks again
+                const uint64_t top = wave_max_u64(lb);
+                if (top == 0) break;
+                key = __uint_as_float((uint32_t)(top >> 32));
+                cand = INT_MAX - (int)(uint32_t)top;
+                if (lb == top) {   // its lane drops it and looks again
 #pragma unroll
                     for (int r = 0; r < R; ++r)
-                        if (ci[r] == cand) ck[r] = -INFINITY;
+                        if (pc[r] == top) pc[r] = 0;
                     lane_best();
                 }
 #pragma unroll
@@ -825,7 +822,7 @@ __device__ __forceinline__ void control(const Args& A, Table& T, int nn, int na,
     int64_t tiles = 0, gathered = 0;
     int f = -1, src = -1;
     if (lane < j) {
-        src = T.plan_src[lane];
+        src = my_pick < na ? T.src[my_pick] : my_pick - na;
         const int p = np0 + lane;
         const LeafV Lv = leaf_view(A, src, root);
         const int64_t cl = Lv.left[2], c = Lv.tot[2], m = Lv.e - Lv.s;
@@ -975,10 +972,11 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
     // controller loads the entries past the block size itself)
     uint32_t pf_leaf = 0;   // origin (low 16 bits) and node id of leaf t
     PendSum pf_ps = {};
+    const int np_now = ROOT ? 0 : st->n_pend;
     if (!ROOT) {
         const int t = threadIdx.x;
         if (t < st->n_leaves) pf_leaf = (uint32_t)(uint16_t)A.leaf_src[t] | ((uint32_t)A.leaf_node[t] << 16);
-        if (t < st->n_pend) pf_ps = A.psum[t];
+        if (t < np_now) pf_ps = A.psum[t];
     }
     const bool derive = q->const_h != 0;
     const int64_t hqc = q->hq_const;
@@ -1141,7 +1139,7 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
         for (int k = 0; k < CPW; ++k) {
             const int i = w + k * (NT / WAVE);
             if (i < 2 * nr && lane == 0) {
-                const int p = st->round_pend[i / 2];
+                const int p = np_now - nr + i / 2;   // the round's splits: the last nr Pend entries
                 Pend& Pp = A.pend[p];
                 Pp.child[i % 2] = rr[k];
                 const float g = rec_gain(rr[k], Pp.depth >= A.max_depth);
