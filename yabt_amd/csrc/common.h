@@ -208,6 +208,28 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
     return ab > cd ? ab : cd;
 }
 
+// wave_max_u64 without scalar registers: row rotations give each 16-lane
+// row its maximum, then gfx950's row and half swaps (v_permlane16_swap,
+// v_permlane32_swap) put each lane's partner row, then partner half, beside
+// it; whichever way a swap moves the data, a lane's two results are its own
+// value and its partner's.
+__device__ __forceinline__ uint64_t max_u64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+__device__ __forceinline__ uint64_t wave_max_u64_v(uint64_t v) {
+    v = max_u64(v, dpp64<DPP_ROW_ROR + 8>(v));
+    v = max_u64(v, dpp64<DPP_ROW_ROR + 4>(v));
+    v = max_u64(v, dpp64<DPP_ROW_ROR + 2>(v));
+    v = max_u64(v, dpp64<DPP_ROW_ROR + 1>(v));
+    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    const auto l16 = __builtin_amdgcn_permlane16_swap(lo, lo, false, false);
+    const auto h16 = __builtin_amdgcn_permlane16_swap(hi, hi, false, false);
+    v = max_u64(((uint64_t)h16[0] << 32) | l16[0], ((uint64_t)h16[1] << 32) | l16[1]);
+    lo = (uint32_t)v;
+    hi = (uint32_t)(v >> 32);
+    const auto l32 = __builtin_amdgcn_permlane32_swap(lo, lo, false, false);
+    const auto h32 = __builtin_amdgcn_permlane32_swap(hi, hi, false, false);
+    return max_u64(((uint64_t)h32[0] << 32) | l32[0], ((uint64_t)h32[1] << 32) | l32[1]);
+}
+
 __device__ __forceinline__ int wave_min_i32(int v) {
     v = min(v, (int)dpp32<DPP_ROW_ROR + 8>((uint32_t)v));
     v = min(v, (int)dpp32<DPP_ROW_ROR + 4>((uint32_t)v));

@@ -773,49 +773,73 @@ __device__ __forceinline__ void control(const Args& A, Table& T, int nn, int na,
             }
             lane_best();
         }
-        int cand = best, cpos = -1;
-        for (;;) {
-            // Pend capacity: every controller may need one for the leaf it is
-            // blocked on, at most L - na more; extras keep np + L - na <=
-            // pend_cap - 1 (so the first, j == 0, fits)
-            if (np >= A.pend_cap) {
-                status = -5;
-                break;
-            }
-            if (j > 0 && np + L - na > A.pend_cap - 1) break;
-            if (lane == j) my_pick = cand;
-            if (cpos >= 0) {   // the list in LDS: taken
-                if (lane == 0) T.ckand[cpos] = -INFINITY;
-                wave_sync();
-            }
-            ++np;
-            ++j;
-            if (j >= KMAX) break;
-            float key;
-            int e = 0;
-            if (in_regs) {
-                const uint64_t top = wave_max_u64(lb);
-                if (top == 0) break;
-                key = __uint_as_float((uint32_t)(top >> 32));
-                cand = INT_MAX - (int)(uint32_t)top;
-                if (lb == top) {   // its lane drops it and looks again
+        if (in_regs) {
+            // every pick at once: extraction t (the t-th largest candidate
+            // after best) and the budget count at its key go to lane t, with
+            // no scalar work between extractions; then the stopping rules
+            // below, as the one-at-a-time loop applies them
+            uint64_t pk = 0;   // lane t: extraction t
+            int pe = 0;        // lane t: budget entries >= its key
+            // a pick past the candidates or at na + t >= L stops the round
+            // whatever its budget count, so those are not extracted
+            const int t_end = min(KMAX, min(m, L - na - 1) + 1);
+#pragma unroll 1
+            for (int t = 1; t < t_end; ++t) {
+                const uint64_t top = wave_max_u64_v(lb);
+                const float key = __uint_as_float((uint32_t)(top >> 32));
+                int e = 0;
+#pragma unroll
+                for (int r = 0; r < R; ++r) e += __popcll(__ballot(bk[r] >= key));
+                if (lane == t) {
+                    pk = top;
+                    pe = e;
+                }
+                if (top != 0 && lb == top) {   // its lane drops it and looks again
 #pragma unroll
                     for (int r = 0; r < R; ++r)
                         if (pc[r] == top) pc[r] = 0;
                     lane_best();
                 }
-#pragma unroll
-                for (int r = 0; r < R; ++r) e += __popcll(__ballot(bk[r] >= key));
-            } else {
+            }
+            for (;;) {
+                if (np >= A.pend_cap) {
+                    status = -5;
+                    break;
+                }
+                if (j > 0 && np + L - na > A.pend_cap - 1) break;
+                ++np;
+                ++j;
+                if (j >= KMAX) break;
+                if (readlane64((int64_t)pk, j) == 0) break;
+                // the budget: leaves of the run-ahead when it pops this one
+                if (na + __builtin_amdgcn_readlane(pe, j) + j >= L) break;
+            }
+            my_pick = lane == 0 ? best : INT_MAX - (int)(uint32_t)pk;
+        } else {
+            int cand = best, cpos = -1;
+            for (;;) {
+                if (np >= A.pend_cap) {
+                    status = -5;
+                    break;
+                }
+                if (j > 0 && np + L - na > A.pend_cap - 1) break;
+                if (lane == j) my_pick = cand;
+                if (cpos >= 0) {   // the list in LDS: taken
+                    if (lane == 0) T.ckand[cpos] = -INFINITY;
+                    wave_sync();
+                }
+                ++np;
+                ++j;
+                if (j >= KMAX) break;
                 cpos = wave_list_argmax(T.ckand, T.cidx, m, lane);
                 if (cpos < 0) break;
                 cand = T.cidx[cpos];
-                key = T.ckand[cpos];
+                const float key = T.ckand[cpos];
+                int e = 0;
                 for (int i = lane; i < mb; i += WAVE) e += T.cbud[i] >= key ? 1 : 0;
                 e = wave_sum<int>(e);
+                if (na + e + j >= L) break;
             }
-            // the budget: leaves of the run-ahead when it pops this one
-            if (na + e + j >= L) break;
         }
     }
     // this round's splits, one per lane
@@ -1126,6 +1150,13 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
         constexpr int CPW = 2 * KMAX / (NT / WAVE);   // children per wave, at most
         static_assert(CPW * (NT / WAVE) == 2 * KMAX, "children per wave");
         ScanRec rr[CPW];
+        // the splits' depths (for the depth cap), loaded beside the records
+        int dep[CPW];
+#pragma unroll
+        for (int k = 0; k < CPW; ++k) {
+            const int i = w + k * (NT / WAVE);
+            dep[k] = (i < 2 * nr) ? A.pend[np_now - nr + i / 2].depth : 0;
+        }
         if (gridDim.x <= WAVE) {
             wave_best_records<CPW>(A.rec, gridDim.x, w, NT / WAVE, 2 * nr, lane, rr);
         } else {
@@ -1142,7 +1173,7 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
                 const int p = np_now - nr + i / 2;   // the round's splits: the last nr Pend entries
                 Pend& Pp = A.pend[p];
                 Pp.child[i % 2] = rr[k];
-                const float g = rec_gain(rr[k], Pp.depth >= A.max_depth);
+                const float g = rec_gain(rr[k], dep[k] >= A.max_depth);
                 T.cgain[p][i % 2] = g;
                 A.psum[p].gain[i % 2] = g;   // kept for later controllers
             }
