@@ -57,9 +57,19 @@ def _oracle(Xf, feats, g, h, feature, leaf, mu, sd, min_samples, lam):
     return W, db, lo, hi, cnt
 
 
-def _gpu(X, x_kind, feats, g, h, feature, leaf, mu, sd, min_samples, lam, gram="exact"):
+def _gpu(X, x_kind, feats, g, h, feature, leaf, mu, sd, min_samples, lam, gram="exact", pad=False):
+    """pad: uint8 inputs as (F, ld) with ld a multiple of 16 above n (the
+    grower's feature-major layout), so the 4-row vector loads apply."""
     t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
-    Xd = t(X) if x_kind == 0 else t(np.ascontiguousarray(X.T))
+    if x_kind == 0:
+        Xd = t(X)
+    elif pad:
+        n = X.shape[0]
+        Xp = np.zeros((X.shape[1], (n + 15) // 16 * 16 + 16), np.uint8)
+        Xp[:, :n] = X.T
+        Xd = t(Xp)
+    else:
+        Xd = t(np.ascontiguousarray(X.T))
     out = leaf_fit(Xd, x_kind, t(feats), t(mu), t(sd), t(g), t(h), t(leaf), t(feature), min_samples, lam,
                    gram=gram)
     return [o.cpu().numpy() for o in out]
@@ -79,6 +89,23 @@ def test_leaf_fit_matches_oracle(n, K, n_nodes, x_kind, lam, gram):
     assert np.array_equal(lo, rlo) and np.array_equal(hi, rhi)
     np.testing.assert_allclose(W, rW, rtol=1e-5, atol=1e-6)
     np.testing.assert_allclose(b, rb, rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("n,K,n_nodes", [(20_003, 5, 31), (4_097, 8, 15), (1_000_001, 7, 255)])
+def test_leaf_fit_vector_rows_match_oracle(n, K, n_nodes):
+    """uint8 inputs in the padded feature-major layout: four rows per thread
+    in the stats and scatter passes, the last n % 4 rows one by one."""
+    X, Xf, feats, g, h, feature, leaf, mu, sd = _problem(n + 7, n, K, n_nodes, bins=True)
+    W, b, lo, hi, cnt = _gpu(X, 1, feats, g, h, feature, leaf, mu, sd, 50, 1e-3, pad=True)
+    rW, rb, rlo, rhi, rcnt = _oracle(Xf, feats, g, h, feature, leaf, mu, sd, 50, 1e-3)
+    assert np.array_equal(cnt, rcnt)
+    assert np.array_equal(lo, rlo) and np.array_equal(hi, rhi)
+    np.testing.assert_allclose(W, rW, rtol=1e-5, atol=1e-6)
+    np.testing.assert_allclose(b, rb, rtol=1e-5, atol=1e-6)
+    # the same bits as the unpadded (one row at a time) layout
+    u = _gpu(X, 1, feats, g, h, feature, leaf, mu, sd, 50, 1e-3)
+    for x, y in zip((W, b, lo, hi, cnt), u):
+        assert np.array_equal(x, y)
 
 
 @pytest.mark.parametrize("n,K,x_kind", [(1, 1, 0), (1000, 3, 0), (100_003, 8, 1), (2_000_000, 5, 1)])
@@ -145,6 +172,13 @@ def test_leaf_fit_rejects_bad_leaf_ids():
     leaf[17] = 9
     with pytest.raises(ValueError):
         _gpu(X, 0, feats, g, h, feature, leaf, mu, sd, 50, 1.0)
+
+
+def test_leaf_fit_rejects_bad_leaf_ids_vector_rows():
+    X, Xf, feats, g, h, feature, leaf, mu, sd = _problem(5, 10_001, 4, 9, bins=True)
+    leaf[4_001] = -3
+    with pytest.raises(ValueError):
+        _gpu(X, 1, feats, g, h, feature, leaf, mu, sd, 50, 1.0, pad=True)
 
 
 def test_leaf_fit_rejects_nonfinite_inputs():

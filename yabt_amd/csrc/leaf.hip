@@ -68,7 +68,8 @@ struct LeafArgs {
     int min_samples;
     double lam;
     int gram_f64;              // 1: M and b summed in fp64 by MFMA (parts and sums hold double bits)
-    int64_t rows_per_block;    // stats/scatter rows per block
+    int64_t rows_per_block;    // stats/scatter rows per block (a multiple of 4)
+    int vec4;                  // 1: uint8 inputs, leaf ids, g and h aligned for 4-row vector loads
     // workspace
     LeafStats* st;
     uint32_t* count;           // (n_nodes)
@@ -121,6 +122,38 @@ __global__ void __launch_bounds__(LB) k_leaf_init(LeafArgs A, int K) {
     }
 }
 
+// Four consecutive rows i .. i + 3 (i % 4 == 0, A.vec4): their leaf ids, g
+// and h, and per input j one word holding the four rows' uint8 inputs (row
+// i + r in byte r) -- two 16-byte, two float4 and K 4-byte loads.
+template <int K>
+struct Rows4 {
+    int64_t node[4];
+    float g[4], h[4];
+    uint32_t xw[K];
+};
+template <int K>
+__device__ __forceinline__ void load_rows4(const LeafArgs& A, const int32_t* fs, int64_t i, Rows4<K>& R) {
+    const longlong2 la = *reinterpret_cast<const longlong2*>(A.leaf + i);
+    const longlong2 lb = *reinterpret_cast<const longlong2*>(A.leaf + i + 2);
+    const float4 g4 = *reinterpret_cast<const float4*>(A.grad + i);
+    const float4 h4 = *reinterpret_cast<const float4*>(A.hess + i);
+    const uint8_t* B = reinterpret_cast<const uint8_t*>(A.X);
+#pragma unroll
+    for (int j = 0; j < K; ++j) R.xw[j] = *reinterpret_cast<const uint32_t*>(B + (size_t)fs[j] * (size_t)A.ldx + (size_t)i);
+    R.node[0] = la.x;
+    R.node[1] = la.y;
+    R.node[2] = lb.x;
+    R.node[3] = lb.y;
+    R.g[0] = g4.x;
+    R.g[1] = g4.y;
+    R.g[2] = g4.z;
+    R.g[3] = g4.w;
+    R.h[0] = h4.x;
+    R.h[1] = h4.y;
+    R.h[2] = h4.z;
+    R.h[3] = h4.w;
+}
+
 // Rows [blockIdx.x * rows_per_block, +rows_per_block): counts, envelopes and
 // magnitudes.
 template <int K, bool LDS>
@@ -143,15 +176,11 @@ __global__ void __launch_bounds__(LSB) k_leaf_stats(LeafArgs A) {
     const int64_t lo = (int64_t)blockIdx.x * A.rows_per_block, hi = min(A.n, lo + A.rows_per_block);
     float mg = 0.0f, mh = 0.0f;
     int bad = 0;
-    for (int64_t i = lo + threadIdx.x; i < hi; i += LSB) {
-        const int64_t node = A.leaf[i];
+    auto add_row = [&](int64_t node, const float (&x)[K], float gi, float hi_) {
         if (node < 0 || node >= A.n_nodes) {
             bad = 1;
-            continue;
+            return;
         }
-        float x[K];
-        load_x<K>(A, i, s_fs, x);
-        const float gi = A.grad[i], hi_ = A.hess[i];
         if (!isfinite(gi) || !isfinite(hi_)) bad = 1;
         mg = fmaxf(mg, fabsf(gi));
         mh = fmaxf(mh, fabsf(hi_));
@@ -168,6 +197,33 @@ __global__ void __launch_bounds__(LSB) k_leaf_stats(LeafArgs A) {
         }
         if (LDS) atomicAdd(&s_cnt[node], 1u);
         else atomicAdd(&A.count[node], 1u);
+    };
+    int64_t first = lo;   // rows from here on take the one-row loop
+    if (A.vec4) {
+        // four consecutive rows per thread and step, every load a vector
+        const int64_t ng = (hi - lo) / 4;
+        for (int64_t q = threadIdx.x; q < ng; q += LSB) {
+            Rows4<K> R;
+            load_rows4<K>(A, s_fs, lo + 4 * q, R);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float x[K];
+#pragma unroll
+                for (int j = 0; j < K; ++j) x[j] = (float)((R.xw[j] >> (8 * r)) & 0xffu);
+                add_row(R.node[r], x, R.g[r], R.h[r]);
+            }
+        }
+        first = lo + 4 * ng;
+    }
+    for (int64_t i = first + threadIdx.x; i < hi; i += LSB) {
+        const int64_t node = A.leaf[i];
+        if (node < 0 || node >= A.n_nodes) {
+            bad = 1;
+            continue;
+        }
+        float x[K];
+        load_x<K>(A, i, s_fs, x);
+        add_row(node, x, A.grad[i], A.hess[i]);
     }
     if (bad) s_bad = 1;
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
@@ -291,7 +347,17 @@ __global__ void __launch_bounds__(LSB) k_leaf_scatter(LeafArgs A) {
     __syncthreads();
     const int64_t lo = (int64_t)blockIdx.x * A.rows_per_block, hi = min(A.n, lo + A.rows_per_block);
     if (LDS) {
-        for (int64_t i = lo + threadIdx.x; i < hi; i += LSB) {
+        // vec4: rows [lo, first) in groups of four per thread, the rest one by one
+        const int64_t ng = A.vec4 ? (hi - lo) / 4 : 0, first = lo + 4 * ng;
+        for (int64_t q = threadIdx.x; q < ng; q += LSB) {
+            const longlong2 la = *reinterpret_cast<const longlong2*>(A.leaf + lo + 4 * q);
+            const longlong2 lb = *reinterpret_cast<const longlong2*>(A.leaf + lo + 4 * q + 2);
+            const int64_t nd[4] = {la.x, la.y, lb.x, lb.y};
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                if (nd[r] >= 0 && nd[r] < A.n_nodes) atomicAdd(&s_cnt[nd[r]], 1u);
+        }
+        for (int64_t i = first + threadIdx.x; i < hi; i += LSB) {
             const int64_t node = A.leaf[i];
             if (node >= 0 && node < A.n_nodes) atomicAdd(&s_cnt[node], 1u);
         }
@@ -301,7 +367,26 @@ __global__ void __launch_bounds__(LSB) k_leaf_scatter(LeafArgs A) {
             s_cnt[i] = 0;
         }
         __syncthreads();
-        for (int64_t i = lo + threadIdx.x; i < hi; i += LSB) {
+        for (int64_t q = threadIdx.x; q < ng; q += LSB) {
+            Rows4<K> R;
+            load_rows4<K>(A, s_fs, lo + 4 * q, R);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t node = R.node[r];
+                if (node < 0 || node >= A.n_nodes) continue;
+                const uint64_t pos = s_base[node] + atomicAdd(&s_cnt[node], 1u);
+                A.sorted_gh[pos] = make_float2(R.g[r], R.h[r]);
+                uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+                for (int j = 0; j < K; ++j) {
+                    const uint32_t b = (R.xw[j] >> (8 * r)) & 0xffu;
+                    if (j < 4) w0 |= b << (8 * j);
+                    else w1 |= b << (8 * (j - 4));
+                }
+                reinterpret_cast<uint2*>(A.sorted_x)[pos] = make_uint2(w0, w1);
+            }
+        }
+        for (int64_t i = first + threadIdx.x; i < hi; i += LSB) {
             const int64_t node = A.leaf[i];
             if (node < 0 || node >= A.n_nodes) continue;
             const uint32_t r = atomicAdd(&s_cnt[node], 1u);
@@ -876,6 +961,11 @@ void launch_leaf_fit(LeafArgs& A, float* out_W, float* out_b, float* out_lo, flo
     int64_t per = (A.n + LROW_BLOCKS - 1) / LROW_BLOCKS;
     per = per < LROWS ? LROWS : (per + LSB - 1) / LSB * LSB;
     A.rows_per_block = per;
+    const auto al = [](const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; };
+    A.vec4 = (lds && A.x_kind == 1 && al(A.leaf, 16) && al(A.grad, 16) && al(A.hess, 16) && al(A.X, 4) &&
+              A.ldx % 4 == 0 && per % 4 == 0)
+                 ? 1
+                 : 0;
     const int row_blocks = (int)((A.n + per - 1) / per);
     k_leaf_init<<<launch_grid((int64_t)A.n_nodes * gram_entries(LKMAX), LB, 1024), LB, 0, stream>>>(A, K);
     if (row_blocks > 0) {
