@@ -16,13 +16,17 @@
 // sum below 2^62.  Rows are first counting-sorted by leaf (the order inside a
 // leaf is free), so each block accumulates one leaf at a time in registers.
 //
-// Launch sequence (caller's stream):
-//   k_leaf_init        clear counters, sums, envelopes
-//   k_leaf_stats<K>    rows per node, envelopes min/max of raw x, max |x1|, |g|, |h|
-//   k_leaf_offsets     node offsets of the sorted rows, fixed-point shifts
-//   k_leaf_scatter     rows -> sorted by node
-//   k_leaf_gram<K>     fixed-point sums of M and b per (chunk, leaf) segment
-//   k_leaf_reduce<K>   per-leaf sums of the segments
+// Launch sequence (caller's stream), node tables in LDS (n_nodes <= LDS_NODES):
+//   k_leaf_init          clear counters, sums, envelopes
+//   k_leaf_count         rows per node, per row block and in all (leaf ids only)
+//   k_leaf_offsets       node offsets of the sorted rows
+//   k_leaf_scatter_stats rows -> sorted by node; envelopes min/max of raw x, max |g|, |h|
+//   k_leaf_shifts        max |x1|, fixed-point shifts
+// more nodes: k_leaf_stats<K> (counts, envelopes, magnitudes), k_leaf_offsets,
+// k_leaf_shifts, k_leaf_scatter (rows -> sorted by node); then
+//   k_leaf_gram<K>     fixed-point sums of M and b per (chunk, leaf) segment, added
+//                      into the leaf's sums (k_leaf_gram_mfma and k_leaf_reduce<K>
+//                      for the fp64 MFMA sums: per-segment partials, then per leaf)
 //   k_leaf_solve<K>    fp64 LU with partial pivoting per eligible leaf
 
 #include "common.h"
@@ -73,6 +77,7 @@ struct LeafArgs {
     // workspace
     LeafStats* st;
     uint32_t* count;           // (n_nodes)
+    uint32_t* bcnt;            // (row blocks, n_nodes) rows per row block and node (node tables in LDS)
     int64_t* off;              // (n_nodes + 1)
     unsigned long long* cursor;   // (n_nodes)
     uint8_t* sorted_x;         // rows' inputs in sorted order: 8 bytes (uint8) or K floats per row
@@ -155,67 +160,19 @@ __device__ __forceinline__ void load_rows4(const LeafArgs& A, const int32_t* fs,
 }
 
 // Rows [blockIdx.x * rows_per_block, +rows_per_block): counts, envelopes and
-// magnitudes.
-template <int K, bool LDS>
+// magnitudes, into the global node tables (more nodes than LDS holds).
+template <int K>
 __global__ void __launch_bounds__(LSB) k_leaf_stats(LeafArgs A) {
-    __shared__ uint32_t s_cnt[LDS ? LDS_NODES : 1];
-    __shared__ uint32_t s_lo[LDS ? LDS_NODES * K : 1], s_hi[LDS ? LDS_NODES * K : 1];
     __shared__ float s_red[3][LSB / WAVE];
     __shared__ int s_bad;
     __shared__ int32_t s_fs[LKMAX];
     if (threadIdx.x < K) s_fs[threadIdx.x] = A.feats[threadIdx.x];
     if (threadIdx.x == 0) s_bad = 0;
-    if (LDS) {
-        for (int i = threadIdx.x; i < A.n_nodes; i += LSB) s_cnt[i] = 0;
-        for (int i = threadIdx.x; i < A.n_nodes * K; i += LSB) {
-            s_lo[i] = float_key(INFINITY);
-            s_hi[i] = float_key(-INFINITY);
-        }
-    }
     __syncthreads();
     const int64_t lo = (int64_t)blockIdx.x * A.rows_per_block, hi = min(A.n, lo + A.rows_per_block);
     float mg = 0.0f, mh = 0.0f;
     int bad = 0;
-    auto add_row = [&](int64_t node, const float (&x)[K], float gi, float hi_) {
-        if (node < 0 || node >= A.n_nodes) {
-            bad = 1;
-            return;
-        }
-        if (!isfinite(gi) || !isfinite(hi_)) bad = 1;
-        mg = fmaxf(mg, fabsf(gi));
-        mh = fmaxf(mh, fabsf(hi_));
-        // per-node envelopes; their extremes also bound |x1| (k_leaf_offsets) and
-        // expose non-finite inputs (keys beyond those of -inf / +inf)
-#pragma unroll
-        for (int j = 0; j < K; ++j) {
-            // the extremes settle quickly: read first, update only when improving
-            const uint32_t kx = float_key(x[j]);
-            uint32_t* plo = LDS ? &s_lo[node * K + j] : &A.lo_key[node * K + j];
-            uint32_t* phi = LDS ? &s_hi[node * K + j] : &A.hi_key[node * K + j];
-            if (kx < *(volatile uint32_t*)plo) atomicMin(plo, kx);
-            if (kx > *(volatile uint32_t*)phi) atomicMax(phi, kx);
-        }
-        if (LDS) atomicAdd(&s_cnt[node], 1u);
-        else atomicAdd(&A.count[node], 1u);
-    };
-    int64_t first = lo;   // rows from here on take the one-row loop
-    if (A.vec4) {
-        // four consecutive rows per thread and step, every load a vector
-        const int64_t ng = (hi - lo) / 4;
-        for (int64_t q = threadIdx.x; q < ng; q += LSB) {
-            Rows4<K> R;
-            load_rows4<K>(A, s_fs, lo + 4 * q, R);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float x[K];
-#pragma unroll
-                for (int j = 0; j < K; ++j) x[j] = (float)((R.xw[j] >> (8 * r)) & 0xffu);
-                add_row(R.node[r], x, R.g[r], R.h[r]);
-            }
-        }
-        first = lo + 4 * ng;
-    }
-    for (int64_t i = first + threadIdx.x; i < hi; i += LSB) {
+    for (int64_t i = lo + threadIdx.x; i < hi; i += LSB) {
         const int64_t node = A.leaf[i];
         if (node < 0 || node >= A.n_nodes) {
             bad = 1;
@@ -223,7 +180,22 @@ __global__ void __launch_bounds__(LSB) k_leaf_stats(LeafArgs A) {
         }
         float x[K];
         load_x<K>(A, i, s_fs, x);
-        add_row(node, x, A.grad[i], A.hess[i]);
+        const float gi = A.grad[i], hi_ = A.hess[i];
+        if (!isfinite(gi) || !isfinite(hi_)) bad = 1;
+        mg = fmaxf(mg, fabsf(gi));
+        mh = fmaxf(mh, fabsf(hi_));
+        // per-node envelopes; their extremes also bound |x1| (k_leaf_shifts) and
+        // expose non-finite inputs (keys beyond those of -inf / +inf)
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            // the extremes settle quickly: read first, update only when improving
+            const uint32_t kx = float_key(x[j]);
+            uint32_t* plo = &A.lo_key[node * K + j];
+            uint32_t* phi = &A.hi_key[node * K + j];
+            if (kx < *(volatile uint32_t*)plo) atomicMin(plo, kx);
+            if (kx > *(volatile uint32_t*)phi) atomicMax(phi, kx);
+        }
+        atomicAdd(&A.count[node], 1u);
     }
     if (bad) s_bad = 1;
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
@@ -247,31 +219,12 @@ __global__ void __launch_bounds__(LSB) k_leaf_stats(LeafArgs A) {
         atomicMax(&A.st->max_h_bits, __float_as_uint(mh));
         if (s_bad) atomicMin(&A.st->status, -1);
     }
-    if (LDS) {
-        for (int i = threadIdx.x; i < A.n_nodes; i += LSB)
-            if (s_cnt[i]) atomicAdd(&A.count[i], s_cnt[i]);
-        for (int i = threadIdx.x; i < A.n_nodes * K; i += LSB) {
-            if (s_lo[i] != float_key(INFINITY)) atomicMin(&A.lo_key[i], s_lo[i]);
-            if (s_hi[i] != float_key(-INFINITY)) atomicMax(&A.hi_key[i], s_hi[i]);
-        }
-    }
 }
 
-// One block: node offsets of the sorted rows (exclusive scan of the counts),
-// write cursors, and the fixed-point shifts.
-__global__ void __launch_bounds__(1024) k_leaf_offsets(LeafArgs A, int K) {
+// One block: node offsets of the sorted rows (exclusive scan of the counts)
+// and write cursors.
+__global__ void __launch_bounds__(1024) k_leaf_offsets(LeafArgs A) {
     __shared__ int64_t s_wave[1024 / WAVE];
-    __shared__ uint32_t s_xlo[LKMAX], s_xhi[LKMAX];
-    if (threadIdx.x < K) {
-        s_xlo[threadIdx.x] = float_key(INFINITY);
-        s_xhi[threadIdx.x] = float_key(-INFINITY);
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < A.n_nodes * K; i += 1024) {
-        atomicMin(&s_xlo[i % K], A.lo_key[i]);
-        atomicMax(&s_xhi[i % K], A.hi_key[i]);
-    }
-    __syncthreads();
     int64_t carry = 0;
     for (int base = 0; base < A.n_nodes; base += 1024) {
         const int i = base + threadIdx.x;
@@ -284,8 +237,31 @@ __global__ void __launch_bounds__(1024) k_leaf_offsets(LeafArgs A, int K) {
         }
         carry += tot;
     }
+    if (threadIdx.x == 0) A.off[A.n_nodes] = carry;
+}
+
+// One block: max |x1| from the envelopes, and the fixed-point shifts.
+__global__ void __launch_bounds__(1024) k_leaf_shifts(LeafArgs A, int K) {
+    __shared__ uint32_t s_xlo[LKMAX], s_xhi[LKMAX];
+    if (threadIdx.x < K) {
+        s_xlo[threadIdx.x] = float_key(INFINITY);
+        s_xhi[threadIdx.x] = float_key(-INFINITY);
+    }
+    __syncthreads();
+    // thread t takes input t % K of nodes t / K, t / K + 1024 / K, ... in
+    // registers, then one LDS atomic each
+    if (threadIdx.x < (1024 / K) * K) {
+        const int j = threadIdx.x % K, step = 1024 / K;
+        uint32_t lo = float_key(INFINITY), hi = float_key(-INFINITY);
+        for (int nd = threadIdx.x / K; nd < A.n_nodes; nd += step) {
+            lo = min(lo, A.lo_key[nd * K + j]);
+            hi = max(hi, A.hi_key[nd * K + j]);
+        }
+        atomicMin(&s_xlo[j], lo);
+        atomicMax(&s_xhi[j], hi);
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        A.off[A.n_nodes] = carry;
         // max |x1| <= max(1, max_j max(|xmax_j - mu_j|, |xmin_j - mu_j|) / sd_j),
         // taken 2^-20 above for the fp32 rounding of (x - mu) / sd
         double mx = 1.0;
@@ -312,8 +288,156 @@ __global__ void __launch_bounds__(1024) k_leaf_offsets(LeafArgs A, int K) {
     }
 }
 
+// Rows [blockIdx.x * rows_per_block, +rows_per_block): rows per node, into
+// the block's row of bcnt and the totals (node tables in LDS).  Reads only
+// the leaf ids.
+__global__ void __launch_bounds__(LSB) k_leaf_count(LeafArgs A) {
+    __shared__ uint32_t s_cnt[LDS_NODES];
+    __shared__ int s_bad;
+    if (threadIdx.x == 0) s_bad = 0;
+    for (int i = threadIdx.x; i < A.n_nodes; i += LSB) s_cnt[i] = 0;
+    __syncthreads();
+    const int64_t lo = (int64_t)blockIdx.x * A.rows_per_block, hi = min(A.n, lo + A.rows_per_block);
+    int bad = 0;
+    auto count = [&](int64_t node) {
+        if (node < 0 || node >= A.n_nodes) bad = 1;
+        else atomicAdd(&s_cnt[node], 1u);
+    };
+    const int64_t ng = A.vec4 ? (hi - lo) / 4 : 0, first = lo + 4 * ng;
+    for (int64_t q = threadIdx.x; q < ng; q += LSB) {
+        const longlong2 la = *reinterpret_cast<const longlong2*>(A.leaf + lo + 4 * q);
+        const longlong2 lb = *reinterpret_cast<const longlong2*>(A.leaf + lo + 4 * q + 2);
+        count(la.x);
+        count(la.y);
+        count(lb.x);
+        count(lb.y);
+    }
+    for (int64_t i = first + threadIdx.x; i < hi; i += LSB) count(A.leaf[i]);
+    if (bad) s_bad = 1;
+    __syncthreads();
+    for (int i = threadIdx.x; i < A.n_nodes; i += LSB) {
+        const uint32_t c = s_cnt[i];
+        A.bcnt[(size_t)blockIdx.x * (size_t)A.n_nodes + i] = c;
+        if (c) atomicAdd(&A.count[i], c);
+    }
+    if (threadIdx.x == 0 && s_bad) atomicMin(&A.st->status, -1);
+}
+
 // Rows [blockIdx.x * rows_per_block, +rows_per_block) to their node's range
-// of `sorted`; the block reserves one range per node with one atomic add.
+// of the sorted arrays (one range per node and block, reserved with one
+// atomic add from the block's counts), with the per-node envelopes and the
+// magnitudes of g and h taken on the way (node tables in LDS).
+template <int K>
+__global__ void __launch_bounds__(LSB) k_leaf_scatter_stats(LeafArgs A) {
+    __shared__ int32_t s_fs[LKMAX];
+    __shared__ uint32_t s_cnt[LDS_NODES];
+    __shared__ unsigned long long s_base[LDS_NODES];
+    __shared__ uint32_t s_lo[LDS_NODES * K], s_hi[LDS_NODES * K];
+    __shared__ float s_red[2][LSB / WAVE];
+    __shared__ int s_bad;
+    if (threadIdx.x < K) s_fs[threadIdx.x] = A.feats[threadIdx.x];
+    if (threadIdx.x == 0) s_bad = 0;
+    for (int i = threadIdx.x; i < A.n_nodes; i += LSB) {
+        const uint32_t c = A.bcnt[(size_t)blockIdx.x * (size_t)A.n_nodes + i];
+        s_base[i] = c ? atomicAdd(&A.cursor[i], (unsigned long long)c) : 0ull;
+        s_cnt[i] = 0;
+    }
+    for (int i = threadIdx.x; i < A.n_nodes * K; i += LSB) {
+        s_lo[i] = float_key(INFINITY);
+        s_hi[i] = float_key(-INFINITY);
+    }
+    __syncthreads();
+    const int64_t lo = (int64_t)blockIdx.x * A.rows_per_block, hi = min(A.n, lo + A.rows_per_block);
+    float mg = 0.0f, mh = 0.0f;
+    int bad = 0;
+    // a row of a valid node: its envelope and magnitude updates and its
+    // place; xw packs its uint8 inputs (K <= 8 bytes), or xf holds fp32 ones
+    auto put = [&](int64_t node, const float (&x)[K], float gi, float hi_, uint2 xw) {
+        if (!isfinite(gi) || !isfinite(hi_)) bad = 1;
+        mg = fmaxf(mg, fabsf(gi));
+        mh = fmaxf(mh, fabsf(hi_));
+#pragma unroll
+        for (int j = 0; j < K; ++j) {
+            const uint32_t kx = float_key(x[j]);
+            uint32_t* plo = &s_lo[node * K + j];
+            uint32_t* phi = &s_hi[node * K + j];
+            if (kx < *(volatile uint32_t*)plo) atomicMin(plo, kx);
+            if (kx > *(volatile uint32_t*)phi) atomicMax(phi, kx);
+        }
+        const uint64_t pos = s_base[node] + atomicAdd(&s_cnt[node], 1u);
+        A.sorted_gh[pos] = make_float2(gi, hi_);
+        if (A.x_kind == 1) {
+            reinterpret_cast<uint2*>(A.sorted_x)[pos] = xw;
+        } else {
+            float* dst = reinterpret_cast<float*>(A.sorted_x) + pos * K;
+#pragma unroll
+            for (int j = 0; j < K; ++j) dst[j] = x[j];
+        }
+    };
+    const int64_t ng = A.vec4 ? (hi - lo) / 4 : 0, first = lo + 4 * ng;
+    for (int64_t q = threadIdx.x; q < ng; q += LSB) {
+        Rows4<K> R;
+        load_rows4<K>(A, s_fs, lo + 4 * q, R);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int64_t node = R.node[r];
+            if (node < 0 || node >= A.n_nodes) continue;
+            float x[K];
+            uint32_t w0 = 0, w1 = 0;
+#pragma unroll
+            for (int j = 0; j < K; ++j) {
+                const uint32_t b = (R.xw[j] >> (8 * r)) & 0xffu;
+                x[j] = (float)b;
+                if (j < 4) w0 |= b << (8 * j);
+                else w1 |= b << (8 * (j - 4));
+            }
+            put(node, x, R.g[r], R.h[r], make_uint2(w0, w1));
+        }
+    }
+    for (int64_t i = first + threadIdx.x; i < hi; i += LSB) {
+        const int64_t node = A.leaf[i];
+        if (node < 0 || node >= A.n_nodes) continue;
+        float x[K];
+        load_x<K>(A, i, s_fs, x);
+        uint32_t w0 = 0, w1 = 0;
+        if (A.x_kind == 1) {
+#pragma unroll
+            for (int j = 0; j < K; ++j) {
+                const uint32_t b = (uint32_t)x[j];
+                if (j < 4) w0 |= b << (8 * j);
+                else w1 |= b << (8 * (j - 4));
+            }
+        }
+        put(node, x, A.grad[i], A.hess[i], make_uint2(w0, w1));
+    }
+    if (bad) s_bad = 1;
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+#pragma unroll
+    for (int d = WAVE / 2; d > 0; d >>= 1) {
+        mg = fmaxf(mg, __shfl_xor(mg, d, WAVE));
+        mh = fmaxf(mh, __shfl_xor(mh, d, WAVE));
+    }
+    if (lane == 0) {
+        s_red[0][w] = mg;
+        s_red[1][w] = mh;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int i = 1; i < LSB / WAVE; ++i) {
+            mg = fmaxf(mg, s_red[0][i]);
+            mh = fmaxf(mh, s_red[1][i]);
+        }
+        // |x| <= inf as float bits: non-negative floats order like their bits
+        atomicMax(&A.st->max_g_bits, __float_as_uint(mg));
+        atomicMax(&A.st->max_h_bits, __float_as_uint(mh));
+        if (s_bad) atomicMin(&A.st->status, -1);
+    }
+    for (int i = threadIdx.x; i < A.n_nodes * K; i += LSB) {
+        if (s_lo[i] != float_key(INFINITY)) atomicMin(&A.lo_key[i], s_lo[i]);
+        if (s_hi[i] != float_key(-INFINITY)) atomicMax(&A.hi_key[i], s_hi[i]);
+    }
+}
+
 // The inputs, g and h of row i go to position pos of the sorted arrays.
 template <int K>
 __device__ __forceinline__ void put_sorted(const LeafArgs& A, const int32_t* fs, int64_t i, uint64_t pos) {
@@ -336,68 +460,18 @@ __device__ __forceinline__ void put_sorted(const LeafArgs& A, const int32_t* fs,
     }
 }
 
-template <int K, bool LDS>
+// Rows [blockIdx.x * rows_per_block, +rows_per_block) to their node's range
+// of the sorted arrays, one cursor atomic per row (more nodes than LDS holds).
+template <int K>
 __global__ void __launch_bounds__(LSB) k_leaf_scatter(LeafArgs A) {
     __shared__ int32_t s_fs[LKMAX];
     if (threadIdx.x < K) s_fs[threadIdx.x] = A.feats[threadIdx.x];
-    __shared__ uint32_t s_cnt[LDS ? LDS_NODES : 1];
-    __shared__ unsigned long long s_base[LDS ? LDS_NODES : 1];
-    if (LDS)
-        for (int i = threadIdx.x; i < A.n_nodes; i += LSB) s_cnt[i] = 0;
     __syncthreads();
     const int64_t lo = (int64_t)blockIdx.x * A.rows_per_block, hi = min(A.n, lo + A.rows_per_block);
-    if (LDS) {
-        // vec4: rows [lo, first) in groups of four per thread, the rest one by one
-        const int64_t ng = A.vec4 ? (hi - lo) / 4 : 0, first = lo + 4 * ng;
-        for (int64_t q = threadIdx.x; q < ng; q += LSB) {
-            const longlong2 la = *reinterpret_cast<const longlong2*>(A.leaf + lo + 4 * q);
-            const longlong2 lb = *reinterpret_cast<const longlong2*>(A.leaf + lo + 4 * q + 2);
-            const int64_t nd[4] = {la.x, la.y, lb.x, lb.y};
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                if (nd[r] >= 0 && nd[r] < A.n_nodes) atomicAdd(&s_cnt[nd[r]], 1u);
-        }
-        for (int64_t i = first + threadIdx.x; i < hi; i += LSB) {
-            const int64_t node = A.leaf[i];
-            if (node >= 0 && node < A.n_nodes) atomicAdd(&s_cnt[node], 1u);
-        }
-        __syncthreads();
-        for (int i = threadIdx.x; i < A.n_nodes; i += LSB) {
-            s_base[i] = s_cnt[i] ? atomicAdd(&A.cursor[i], (unsigned long long)s_cnt[i]) : 0ull;
-            s_cnt[i] = 0;
-        }
-        __syncthreads();
-        for (int64_t q = threadIdx.x; q < ng; q += LSB) {
-            Rows4<K> R;
-            load_rows4<K>(A, s_fs, lo + 4 * q, R);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int64_t node = R.node[r];
-                if (node < 0 || node >= A.n_nodes) continue;
-                const uint64_t pos = s_base[node] + atomicAdd(&s_cnt[node], 1u);
-                A.sorted_gh[pos] = make_float2(R.g[r], R.h[r]);
-                uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-                for (int j = 0; j < K; ++j) {
-                    const uint32_t b = (R.xw[j] >> (8 * r)) & 0xffu;
-                    if (j < 4) w0 |= b << (8 * j);
-                    else w1 |= b << (8 * (j - 4));
-                }
-                reinterpret_cast<uint2*>(A.sorted_x)[pos] = make_uint2(w0, w1);
-            }
-        }
-        for (int64_t i = first + threadIdx.x; i < hi; i += LSB) {
-            const int64_t node = A.leaf[i];
-            if (node < 0 || node >= A.n_nodes) continue;
-            const uint32_t r = atomicAdd(&s_cnt[node], 1u);
-            put_sorted<K>(A, s_fs, i, s_base[node] + r);
-        }
-    } else {
-        for (int64_t i = lo + threadIdx.x; i < hi; i += LSB) {
-            const int64_t node = A.leaf[i];
-            if (node < 0 || node >= A.n_nodes) continue;
-            put_sorted<K>(A, s_fs, i, atomicAdd(&A.cursor[node], 1ull));
-        }
+    for (int64_t i = lo + threadIdx.x; i < hi; i += LSB) {
+        const int64_t node = A.leaf[i];
+        if (node < 0 || node >= A.n_nodes) continue;
+        put_sorted<K>(A, s_fs, i, atomicAdd(&A.cursor[node], 1ull));
     }
 }
 
@@ -478,11 +552,14 @@ __device__ __forceinline__ void gram_rows(const LeafArgs& A, const double* s_x1,
             for (int j = 0; j < K; ++j) x1[j] = (double)((src[j] - s_mu[j]) / s_sd[j]);
         }
         x1[K] = 1.0;
-        const double h = (double)gh.y;
-        const double gs = (double)gh.x * scb;           // exact power-of-two scaling
+        // Xh = X1 * h (neural_leaves.py:72), scaled by 2^sM: a power-of-two
+        // scale commutes with the fp64 rounding (no overflow or underflow at
+        // these magnitudes), so x1 * (h 2^sM) is (x1 * h) 2^sM exactly
+        const double hs = (double)gh.y * scM;
+        const double gs = (double)gh.x * scb;
         double xhs[K + 1];
 #pragma unroll
-        for (int b = 0; b <= K; ++b) xhs[b] = (x1[b] * h) * scM;   // Xh = X1 * h (neural_leaves.py:72), scaled
+        for (int b = 0; b <= K; ++b) xhs[b] = x1[b] * hs;
         ++nrow;
         gram_half<K, FAST, P>(x1, xhs, gs, acc);
     }
@@ -528,9 +605,10 @@ __global__ void __launch_bounds__(LB) k_leaf_gram(LeafArgs A) {
         for (int t = 0; t < NH; ++t) acc[t] = 0;
         if (half == 0) gram_rows<K, FAST, 0>(A, s_x1, s_mu, s_sd, scM, scb, s + th, e, acc);
         else gram_rows<K, FAST, 1>(A, s_x1, s_mu, s_sd, scM, scb, s + th, e, acc);
-        // block sum of this (chunk, node) segment into its own partial slot,
-        // chunk + node: distinct for every segment (nodes and chunks both
-        // advance along the sorted rows), so no atomics and no contention
+        // block sum of this (chunk, node) segment, added into the node's sums
+        // with 64-bit integer atomics (exact, so the order of the segments
+        // does not matter); a node's segments are its chunks, so an address
+        // takes at most rows / LCHUNK + 1 adds
         const int nh = half == 0 ? NH : NE - NH;
 #pragma unroll
         for (int t = 0; t < NH; ++t) {
@@ -538,14 +616,14 @@ __global__ void __launch_bounds__(LB) k_leaf_gram(LeafArgs A) {
             if (lane == 0 && t < nh) s_part[w][t] = v;
         }
         __syncthreads();
-        int64_t* out = A.parts + ((size_t)blockIdx.x + (size_t)node) * gram_entries(LKMAX);
+        unsigned long long* out = reinterpret_cast<unsigned long long*>(A.sums + (size_t)node * gram_entries(LKMAX));
         constexpr int HW = HT / WAVE;                 // waves per half
         for (int t = threadIdx.x; t < NE; t += LB) {
             const int hh = t < NH ? 0 : 1, tt = t < NH ? t : t - NH;
             int64_t v = 0;
 #pragma unroll
             for (int i = 0; i < HW; ++i) v += s_part[hh * HW + i][tt];
-            out[t] = v;
+            if (v) atomicAdd(&out[t], (unsigned long long)v);
         }
         __syncthreads();
     }
@@ -632,136 +710,145 @@ __global__ void __launch_bounds__(LB) k_leaf_gram_mfma(LeafArgs A) {
     }
 }
 
-// One block per eligible node: the sum of its segments' partials (chunks
-// first_chunk .. last_chunk of the sorted rows) in a fixed order -- wave w
-// takes segments w, w + RW, ... (lane t: entry t), then the waves' sums in
-// order.  F64: the partials are fp64 bits (k_leaf_gram_mfma).
+// Per-leaf fp64 sums of the MFMA Gram's segment partials (exact fixed-point
+// sums go straight to the node's sums with integer atomics instead).  One
+// block per eligible node, in a fixed order: wave w takes segments w,
+// w + RW, ... of chunks first_chunk .. last_chunk (lane t: entry t), then the
+// waves' sums in order.
 constexpr int RB = 1024;
-template <int K, bool F64>
+template <int K>
 __global__ void __launch_bounds__(RB) k_leaf_reduce(LeafArgs A) {
     constexpr int NE = gram_entries(K);
     constexpr int RW = RB / WAVE;
     static_assert(NE <= WAVE, "one lane per entry");
-    __shared__ int64_t s_w[RW][NE];
+    __shared__ double s_w[RW][NE];
     const int node = blockIdx.x;
     if (!leaf_eligible(A, node)) return;
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
     const int64_t c0 = A.off[node] / LCHUNK, c1 = (A.off[node + 1] - 1) / LCHUNK;
     if (lane < NE) {
-        int64_t ai = 0;
         double ad = 0.0;
-        for (int64_t c = c0 + w; c <= c1; c += RW) {
-            const int64_t v = A.parts[((size_t)c + (size_t)node) * gram_entries(LKMAX) + lane];
-            if (F64) ad += __longlong_as_double(v);
-            else ai += v;
-        }
-        s_w[w][lane] = F64 ? __double_as_longlong(ad) : ai;
+        for (int64_t c = c0 + w; c <= c1; c += RW)
+            ad += __longlong_as_double(A.parts[((size_t)c + (size_t)node) * gram_entries(LKMAX) + lane]);
+        s_w[w][lane] = ad;
     }
     __syncthreads();
     if (threadIdx.x < NE) {
-        int64_t* out = A.sums + (size_t)node * gram_entries(LKMAX);
-        if (F64) {
-            double v = __longlong_as_double(s_w[0][threadIdx.x]);
-            for (int q = 1; q < RW; ++q) v += __longlong_as_double(s_w[q][threadIdx.x]);
-            out[threadIdx.x] = __double_as_longlong(v);
-        } else {
-            int64_t v = 0;
-            for (int q = 0; q < RW; ++q) v += s_w[q][threadIdx.x];
-            out[threadIdx.x] = v;
-        }
+        double v = s_w[0][threadIdx.x];
+        for (int q = 1; q < RW; ++q) v += s_w[q][threadIdx.x];
+        A.sums[(size_t)node * gram_entries(LKMAX) + threadIdx.x] = __double_as_longlong(v);
     }
 }
 
-// One thread per node: assemble, regularise and solve the (K+1) system of an
-// eligible leaf with fp64 LU and partial pivoting (row swaps by selects, so
-// the matrix stays in registers); zeros elsewhere.
+// 16 lanes per node (lane i: row i of the system): assemble, regularise and
+// solve the (K+1) system of an eligible leaf with fp64 LU and partial
+// pivoting; zeros elsewhere.  The operations, their order and their
+// roundings are those of the one-thread elimination: pivot row p = the first
+// row from c on with the largest |M[i][c]| (a NaN diagonal keeps row c; NaN
+// elsewhere never wins), rows c and p swapped, then each row i > c updated
+// from row c (f = M[i][c] / M[c][c], M[i][j] -= f M[c][j] for j >= c), and
+// back substitution from the last row, subtracting the terms left to right.
+constexpr int SOLVE_LANES = 16;
 template <int K>
 __global__ void __launch_bounds__(LB) k_leaf_solve(LeafArgs A, float* out_W, float* out_b, float* out_lo,
                                                   float* out_hi, int64_t* out_count) {
     constexpr int N = K + 1;
-    const int node = blockIdx.x * LB + threadIdx.x;
-    if (node >= A.n_nodes) return;
-    out_count[node] = A.count[node];
-#pragma unroll
-    for (int j = 0; j < K; ++j) {
-        out_lo[node * K + j] = key_float(A.lo_key[node * K + j]);
-        out_hi[node * K + j] = key_float(A.hi_key[node * K + j]);
-        out_W[node * K + j] = 0.0f;
+    static_assert(N <= SOLVE_LANES, "a row per lane");
+    const int li = threadIdx.x % SOLVE_LANES;
+    const int gbase = (threadIdx.x & (WAVE - 1)) - li;   // the group's first lane in the wave
+    const int node = blockIdx.x * (LB / SOLVE_LANES) + threadIdx.x / SOLVE_LANES;
+    const bool live = node < A.n_nodes;   // uniform over the group (groups never straddle a node)
+    auto bcast = [&](double v, int src) { return __shfl(v, gbase + src, WAVE); };
+    if (live) {
+        if (li == 0) {
+            out_count[node] = A.count[node];
+            out_b[node] = 0.0f;
+        }
+        if (li < K) {
+            out_lo[node * K + li] = key_float(A.lo_key[node * K + li]);
+            out_hi[node * K + li] = key_float(A.hi_key[node * K + li]);
+            out_W[node * K + li] = 0.0f;
+        }
     }
-    out_b[node] = 0.0f;
-    if (!leaf_eligible(A, node) || A.st->status != 0) return;
-    const int64_t* q = A.sums + (size_t)node * gram_entries(LKMAX);
+    const bool go = live && leaf_eligible(A, node) && A.st->status == 0;
+    // the shuffles below take every lane of the wave: groups without a system
+    // run them on zeros and store nothing
+    const int64_t* q = A.sums + (size_t)(go ? node : 0) * gram_entries(LKMAX);
     const bool f64 = A.gram_f64 != 0;   // fp64 sums (MFMA) or fixed point
     const double iM = ldexp(1.0, -A.st->sM), ib = ldexp(1.0, -A.st->sb);
-    double M[N][N], r[N];
-    int t = 0;
+    auto entry = [&](int t, double sc) { return f64 ? __longlong_as_double(q[t]) : (double)q[t] * sc; };
+    // row li: M[li][b] from the upper triangle (entry t of (a, b), a <= b)
+    double row[N], r = 0.0;
 #pragma unroll
-    for (int a = 0; a < N; ++a)
+    for (int b = 0; b < N; ++b) row[b] = 0.0;
+    if (go && li < N) {
+        // entry of (a, b), a <= b: the rows before a, then b - a
+        auto tri = [](int a, int b) { return a * N - a * (a - 1) / 2 + (b - a); };
 #pragma unroll
-        for (int b = a; b < N; ++b) {
-            M[a][b] = f64 ? __longlong_as_double(q[t]) : (double)q[t] * iM;
-            ++t;
-            M[b][a] = M[a][b];
-        }
-#pragma unroll
-    for (int a = 0; a < N; ++a) {
-        r[a] = f64 ? __longlong_as_double(q[t]) : (double)q[t] * ib;
-        ++t;
+        for (int b = 0; b < N; ++b) row[b] = entry(b >= li ? tri(li, b) : tri(b, li), iM);
+        r = entry(N * (N + 1) / 2 + li, ib);
+        if (li < K) row[li] += A.lam;                // reg = lam * I ...
+        else row[K] += 1e-8;                          // ... but the bias (neural_leaves.py:85-86)
     }
-#pragma unroll
-    for (int a = 0; a < K; ++a) M[a][a] += A.lam;    // reg = lam * I ...
-    M[K][K] += 1e-8;                                  // ... but the bias (neural_leaves.py:85-86)
     bool singular = false;
 #pragma unroll
     for (int c = 0; c < N; ++c) {
-        int p = c;
-        double best = fabs(M[c][c]);
+        // pivot: key |M[i][c]| for i > c (NaN: never), |M[c][c]| for i = c (NaN: always)
+        const double mc = row[c];
+        double key = -1.0;
+        if (li == c) key = isnan(mc) ? INFINITY : fabs(mc);
+        else if (li > c && li < N) key = isnan(mc) ? -1.0 : fabs(mc);
+        double mk = key;
+        int pk = li;
 #pragma unroll
-        for (int i = c + 1; i < N; ++i)
-            if (fabs(M[i][c]) > best) {
-                best = fabs(M[i][c]);
-                p = i;
+        for (int d = SOLVE_LANES / 2; d > 0; d >>= 1) {
+            const double ok = __shfl_xor(mk, d, WAVE);
+            const int op = __shfl_xor(pk, d, WAVE);
+            if (ok > mk || (ok == mk && op < pk)) {
+                mk = ok;
+                pk = op;
             }
+        }
+        const int p = pk;
+        const double diag = bcast(row[c], c);
+        const double best = isnan(diag) ? diag : mk;
         if (best == 0.0) singular = true;
+        // swap rows c and p
+        const int src = li == c ? p : (li == p ? c : li);
 #pragma unroll
-        for (int i = c + 1; i < N; ++i)
-            if (i == p) {
-#pragma unroll
-                for (int j = 0; j < N; ++j) {
-                    const double tmp = M[c][j];
-                    M[c][j] = M[i][j];
-                    M[i][j] = tmp;
-                }
-                const double tr = r[c];
-                r[c] = r[i];
-                r[i] = tr;
-            }
+        for (int b = 0; b < N; ++b) row[b] = bcast(row[b], src);
+        r = bcast(r, src);
         if (best != 0.0) {
+            double pc[N];
 #pragma unroll
-            for (int i = c + 1; i < N; ++i) {
-                const double f = M[i][c] / M[c][c];
+            for (int b = 0; b < N; ++b) pc[b] = bcast(row[b], c);
+            const double rc = bcast(r, c);
+            if (li > c && li < N) {
+                const double f = row[c] / pc[c];
 #pragma unroll
-                for (int j = c; j < N; ++j) M[i][j] -= f * M[c][j];
-                r[i] -= f * r[c];
+                for (int b = c; b < N; ++b) row[b] -= f * pc[b];
+                r -= f * rc;
             }
         }
     }
+    if (!go) return;
     if (singular) {
-        atomicMin(&A.st->status, -2);
+        if (li == 0) atomicMin(&A.st->status, -2);
         return;
     }
-    double th[N];
+    double th[N], mine = 0.0;
 #pragma unroll
     for (int i = N - 1; i >= 0; --i) {
-        double v = r[i];
+        double v = r;
 #pragma unroll
-        for (int j = i + 1; j < N; ++j) v -= M[i][j] * th[j];
-        th[i] = v / M[i][i];
+        for (int j = i + 1; j < N; ++j) v -= row[j] * th[j];
+        const double ti = v / row[i];
+        if (li == i) mine = ti;
+        th[i] = bcast(ti, i);
     }
-#pragma unroll
-    for (int j = 0; j < K; ++j) out_W[node * K + j] = (float)th[j];
-    out_b[node] = (float)th[K];
-    atomicAdd(&A.st->n_fit, 1);
+    if (li < K) out_W[node * K + li] = (float)mine;
+    if (li == K) out_b[node] = (float)mine;
+    if (li == 0) atomicAdd(&A.st->n_fit, 1);
 }
 
 __global__ void k_leaf_status(const LeafStats* st, int32_t* out) {
@@ -943,6 +1030,7 @@ size_t carve_leaf(char* base, int64_t n, int n_nodes, int K, LeafArgs* A) {
     LeafArgs& a = A ? *A : tmp;
     a.st = c.take<LeafStats>(1);
     a.count = c.take<uint32_t>((size_t)n_nodes);
+    a.bcnt = c.take<uint32_t>(n_nodes <= LDS_NODES ? (size_t)LROW_BLOCKS * (size_t)n_nodes : 1);
     a.off = c.take<int64_t>((size_t)n_nodes + 1);
     a.cursor = c.take<unsigned long long>((size_t)n_nodes);
     a.sorted_x = c.take<uint8_t>((size_t)(n > 0 ? n : 1) * 4 * LKMAX);
@@ -968,25 +1056,30 @@ void launch_leaf_fit(LeafArgs& A, float* out_W, float* out_b, float* out_lo, flo
                  : 0;
     const int row_blocks = (int)((A.n + per - 1) / per);
     k_leaf_init<<<launch_grid((int64_t)A.n_nodes * gram_entries(LKMAX), LB, 1024), LB, 0, stream>>>(A, K);
-    if (row_blocks > 0) {
-        if (lds) k_leaf_stats<K, true><<<row_blocks, LSB, 0, stream>>>(A);
-        else k_leaf_stats<K, false><<<row_blocks, LSB, 0, stream>>>(A);
+    if (lds) {
+        if (row_blocks > 0) k_leaf_count<<<row_blocks, LSB, 0, stream>>>(A);
+        k_leaf_offsets<<<1, 1024, 0, stream>>>(A);
+        if (row_blocks > 0) k_leaf_scatter_stats<K><<<row_blocks, LSB, 0, stream>>>(A);
+        k_leaf_shifts<<<1, 1024, 0, stream>>>(A, K);
+    } else {
+        if (row_blocks > 0) k_leaf_stats<K><<<row_blocks, LSB, 0, stream>>>(A);
+        k_leaf_offsets<<<1, 1024, 0, stream>>>(A);
+        k_leaf_shifts<<<1, 1024, 0, stream>>>(A, K);
+        if (row_blocks > 0) k_leaf_scatter<K><<<row_blocks, LSB, 0, stream>>>(A);
     }
-    k_leaf_offsets<<<1, 1024, 0, stream>>>(A, K);
     if (row_blocks > 0) {
-        if (lds) k_leaf_scatter<K, true><<<row_blocks, LSB, 0, stream>>>(A);
-        else k_leaf_scatter<K, false><<<row_blocks, LSB, 0, stream>>>(A);
         const int chunks = (int)((A.n + LCHUNK - 1) / LCHUNK);
         if (A.gram_f64) {
             k_leaf_gram_mfma<K><<<chunks, LB, 0, stream>>>(A);
-            k_leaf_reduce<K, true><<<A.n_nodes, RB, 0, stream>>>(A);
+            k_leaf_reduce<K><<<A.n_nodes, RB, 0, stream>>>(A);
         } else {
             if (A.n > 1024) k_leaf_gram<K, true><<<chunks, LB, 0, stream>>>(A);
             else k_leaf_gram<K, false><<<chunks, LB, 0, stream>>>(A);
-            k_leaf_reduce<K, false><<<A.n_nodes, RB, 0, stream>>>(A);
         }
     }
-    k_leaf_solve<K><<<(A.n_nodes + LB - 1) / LB, LB, 0, stream>>>(A, out_W, out_b, out_lo, out_hi, out_count);
+    constexpr int per_block = LB / SOLVE_LANES;   // nodes per solve block
+    k_leaf_solve<K><<<(A.n_nodes + per_block - 1) / per_block, LB, 0, stream>>>(A, out_W, out_b, out_lo, out_hi,
+                                                                               out_count);
 }
 
 }  // namespace yabt

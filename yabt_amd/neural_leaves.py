@@ -170,6 +170,70 @@ def fold(tree: Tree, W, db, mu, sd, lr, feats, lo, hi) -> Tree:
                    leaf_net_hi=hi)
 
 
+def _leaf_step(tree: Tree, X: torch.Tensor, x_kind: int, n: int, feats: torch.Tensor, grad: torch.Tensor,
+               hess: torch.Tensor, leaf_idx: torch.Tensor, params) -> Tree:
+    """Moments, fit and fold of one tree's leaf models: every tensor and
+    workspace is prepared first, then the three launches go out back to back
+    (the device runs them without waiting on the host), then the one wait for
+    the status.  tree's node arrays are on X's device."""
+    lib = _lib.load()
+    dev = X.device
+    K, N = int(feats.numel()), int(tree.feature.shape[0])
+    mode = GRAM_MODES[GRAM]
+    if x_kind == 0 and (X.dtype != torch.float32 or X.dim() != 2 or X.shape[0] != n or X.stride(1) != 1):
+        raise ValueError("X must be fp32 (n, F) with unit column stride")
+    if x_kind == 1 and (X.dtype != torch.uint8 or X.dim() != 2 or X.shape[1] < n or X.stride(1) != 1):
+        raise ValueError("X must be uint8 (F, ld >= n)")
+    fi = feats.to(dev, torch.int32).contiguous()
+    g = grad.to(dev, torch.float32).contiguous()
+    h = hess.to(dev, torch.float32).contiguous()
+    li = leaf_idx.to(dev, torch.int64).contiguous()
+    ft = tree.feature.to(dev, torch.int64).contiguous()
+    value_in = tree.value.to(dev, torch.float32).contiguous()
+    mbytes = int(lib.yabt_leaf_moments_workspace_bytes(n))
+    fbytes = int(lib.yabt_leaf_fit_workspace_bytes(n, N, K))
+    if fbytes == 0:
+        raise ValueError("yabt_leaf_fit: invalid sizes (1 <= K <= 8 inputs)")
+    # two allocations per call from torch's caching allocator on the current
+    # stream, cut into 256-byte aligned pieces: the workspaces and the
+    # outputs used only here, and the outputs the tree keeps (a view keeps
+    # its whole allocation alive)
+    def carve(sizes):
+        up = [(v + 255) // 256 * 256 for v in sizes]
+        base = torch.empty(sum(up), dtype=torch.uint8, device=dev)
+        out, o = [], 0
+        for v, u in zip(sizes, up):
+            out.append(base[o:o + v])
+            o += u
+        return out
+    mws, fws, p_mu, p_sd, p_W, p_b, p_cnt, p_st = carve([max(mbytes, 1), fbytes, 4 * K, 4 * K, 4 * N * K, 4 * N,
+                                                          8 * N, 8])
+    p_lo, p_hi, p_value, p_linear = carve([4 * N * K, 4 * N * K, 4 * N, 4 * N * K])
+    mu, sd, b, value = (p.view(torch.float32) for p in (p_mu, p_sd, p_b, p_value))
+    W, lo, hi, linear = (p.view(torch.float32).view(N, K) for p in (p_W, p_lo, p_hi, p_linear))
+    cnt = p_cnt.view(torch.int64)
+    status = p_st.view(torch.int32)
+    ldx, st = X.stride(0), _stream(dev)
+    _lib.check(lib.yabt_leaf_moments(x_kind, X.data_ptr(), ldx, n, fi.data_ptr(), K, mws.data_ptr(), mbytes,
+                                     mu.data_ptr(), sd.data_ptr(), st), "yabt_leaf_moments")
+    _lib.check(lib.yabt_leaf_fit(x_kind, X.data_ptr(), ldx, n, fi.data_ptr(), K, mu.data_ptr(), sd.data_ptr(),
+                                 g.data_ptr(), h.data_ptr(), li.data_ptr(), ft.data_ptr(), N,
+                                 int(getattr(params, "leaf_net_min_samples", 50)),
+                                 float(getattr(params, "leaf_net_l2", 1.0)), mode, fws.data_ptr(), fbytes,
+                                 W.data_ptr(), b.data_ptr(), lo.data_ptr(), hi.data_ptr(), cnt.data_ptr(),
+                                 status.data_ptr(), st), "yabt_leaf_fit")
+    _lib.check(lib.yabt_leaf_fold(N, K, W.data_ptr(), b.data_ptr(), mu.data_ptr(), sd.data_ptr(),
+                                  float(params.learning_rate), value_in.data_ptr(), value.data_ptr(),
+                                  linear.data_ptr(), st), "yabt_leaf_fold")
+    st_, n_fit = status.tolist()   # the one wait for the device
+    _check_status(st_)
+    # no eligible leaf: the tree is returned unchanged (neural_leaves.py:156-158)
+    if n_fit == 0:
+        return tree
+    return replace(tree, value=value, leaf_net_feats=feats, leaf_net_linear=linear, leaf_net_lo=lo,
+                   leaf_net_hi=hi)
+
+
 def fit_leaf_networks(tree: Tree, Xraw: torch.Tensor, y: torch.Tensor, margin: torch.Tensor, loss_fn,
                       params, gen: torch.Generator | None = None, leaf_idx: torch.Tensor | None = None) -> Tree:
     """Drop-in for yabt.neural_leaves.fit_leaf_networks (neural_leaves.py:131-184),
@@ -186,15 +250,8 @@ def fit_leaf_networks(tree: Tree, Xraw: torch.Tensor, y: torch.Tensor, margin: t
     if feats.numel() == 0:
         return tree
     X = Xraw if Xraw.dtype == torch.float32 and Xraw.stride(1) == 1 else Xraw.float().contiguous()
-    mu, sd = leaf_moments(X, 0, feats, X.shape[0])
-    W, db, lo, hi, cnt, status = _leaf_fit(X, 0, feats, mu, sd, grad, hess, leaf_idx, tree_d.feature,
-                                           getattr(params, "leaf_net_min_samples", 50),
-                                           getattr(params, "leaf_net_l2", 1.0))
-    folded = fold(tree_d, W, db, mu, sd, params.learning_rate, feats, lo, hi)
-    st, n_fit = status.tolist()   # the one wait for the device
-    _check_status(st)
-    # no eligible leaf: the tree is returned unchanged (neural_leaves.py:156-158)
-    return folded if n_fit > 0 else tree
+    out = _leaf_step(tree_d, X, 0, X.shape[0], feats, grad, hess, leaf_idx, params)
+    return tree if out is tree_d else out
 
 
 def fit_leaf_networks_binned(tree: Tree, bins_fm: torch.Tensor, grad: torch.Tensor, hess: torch.Tensor,
@@ -215,13 +272,6 @@ def fit_leaf_networks_binned(tree: Tree, bins_fm: torch.Tensor, grad: torch.Tens
         # padding by gradient correlation needs the raw columns: take them as floats
         Xraw = bins_fm[:, :n].t().float()
         feats = _select_features(replace(tree, feature=feature), Xraw, grad, k)
-    mu, sd = leaf_moments(bins_fm, 1, feats, n)
-    W, db, lo, hi, cnt, status = _leaf_fit(bins_fm, 1, feats, mu, sd, grad, hess, leaf_idx, feature,
-                                           getattr(params, "leaf_net_min_samples", 50),
-                                           getattr(params, "leaf_net_l2", 1.0))
     tree_d = replace(tree, feature=feature, value=tree.value.to(dev))
-    folded = fold(tree_d, W, db, mu, sd, params.learning_rate, feats, lo, hi)
-    st, n_fit = status.tolist()   # the one wait for the device
-    _check_status(st)
-    # no eligible leaf: the tree is returned unchanged (neural_leaves.py:156-158)
-    return folded if n_fit > 0 else tree
+    out = _leaf_step(tree_d, bins_fm, 1, n, feats, grad, hess, leaf_idx, params)
+    return tree if out is tree_d else out
