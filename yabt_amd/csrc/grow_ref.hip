@@ -801,16 +801,25 @@ __global__ void __launch_bounds__(RB) k_root_rank(const uint8_t* __restrict__ bi
     }
 }
 
-// One tile's positions for a producer thread of k_rank_chain, TPT in four
-// groups of four: entry j = 4 q + k is position t WT + q 4 RB + 4 slot + k,
-// so a wave's 16-byte loads of g (and of h) cover 1 KB in one piece and its
-// loads of ranks and bins 512 and 256 bytes.  The tile keeps the loaded words
-// as they are: unpacking them at load time would wait for the loads there,
-// and the loads are meant to run under earlier tiles' work.
+// k_rank_chain's producers: RPROD threads, each loading RQ groups of four
+// positions of a tile.  Many producers with few positions each keep several
+// tiles in flight within the registers (RING tiles ahead).
+constexpr int RPROD = 2 * RB;
+constexpr int RQ = WT / (4 * RPROD);
+constexpr int RPT = 4 * RQ;                  // positions per producer and tile
+constexpr int RING = 3;
+static_assert(RQ * 4 * RPROD == WT, "a tile in whole groups of four per producer");
+
+// One tile's positions for a producer thread of k_rank_chain, RQ groups of
+// four: entry j = 4 q + k is position t WT + q 4 RPROD + 4 slot + k, so a
+// wave's 16-byte loads of g (and of h) cover 1 KB in one piece and its loads
+// of ranks and bins 512 and 256 bytes.  The tile keeps the loaded words as
+// they are: unpacking them at load time would wait for the loads there, and
+// the loads are meant to run under earlier tiles' work.
 struct RankTile {
-    float4 g[4], h[4];
-    uint2 r[4];                    // ranks, 16 bits each; 0xffff: past the rows
-    uint32_t bw[4];                // bins, 8 bits each
+    float4 g[RQ], h[RQ];
+    uint2 r[RQ];                   // ranks, 16 bits each; 0xffff: past the rows
+    uint32_t bw[RQ];               // bins, 8 bits each
 };
 
 __device__ __forceinline__ float rt_g(const RankTile& c, int j) {
@@ -833,16 +842,15 @@ __device__ __forceinline__ uint32_t rt_bin(const RankTile& c, int j) { return (c
 __device__ __forceinline__ void rank_tile_load_vec(RankTile& c, const float* __restrict__ g,
                                                    const float* __restrict__ h, const uint8_t* __restrict__ bn,
                                                    const uint16_t* __restrict__ rk, int64_t t, int slot) {
-    static_assert(TPT == 16, "four groups of four positions per thread");
     const int64_t x0 = t * WT + 4 * (int64_t)slot;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) c.g[q] = *reinterpret_cast<const float4*>(g + x0 + q * 4 * RB);
+    for (int q = 0; q < RQ; ++q) c.g[q] = *reinterpret_cast<const float4*>(g + x0 + q * 4 * RPROD);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) c.h[q] = *reinterpret_cast<const float4*>(h + x0 + q * 4 * RB);
+    for (int q = 0; q < RQ; ++q) c.h[q] = *reinterpret_cast<const float4*>(h + x0 + q * 4 * RPROD);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) c.r[q] = *reinterpret_cast<const uint2*>(rk + x0 + q * 4 * RB);
+    for (int q = 0; q < RQ; ++q) c.r[q] = *reinterpret_cast<const uint2*>(rk + x0 + q * 4 * RPROD);
 #pragma unroll
-    for (int q = 0; q < 4; ++q) c.bw[q] = *reinterpret_cast<const uint32_t*>(bn + x0 + q * 4 * RB);
+    for (int q = 0; q < RQ; ++q) c.bw[q] = *reinterpret_cast<const uint32_t*>(bn + x0 + q * 4 * RPROD);
 }
 
 // Any tile, one position at a time (the last, partial tile, or unaligned data).
@@ -850,8 +858,8 @@ __device__ __forceinline__ void rank_tile_load_any(RankTile& c, const float* __r
                                                    const float* __restrict__ h, const uint8_t* __restrict__ bn,
                                                    const uint16_t* __restrict__ rk, int64_t t, int64_t n, int slot) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        const int64_t x = t * WT + (int64_t)q * 4 * RB + 4 * (int64_t)slot;
+    for (int q = 0; q < RQ; ++q) {
+        const int64_t x = t * WT + (int64_t)q * 4 * RPROD + 4 * (int64_t)slot;
         float gv[4] = {0.0f, 0.0f, 0.0f, 0.0f}, hv[4] = {0.0f, 0.0f, 0.0f, 0.0f};
         uint32_t rv[4] = {0xffffu, 0xffffu, 0xffffu, 0xffffu}, bv = 0;
 #pragma unroll
@@ -873,7 +881,7 @@ __device__ __forceinline__ void rank_tile_load_any(RankTile& c, const float* __r
 // A producer's window [w0, w0 + RW) of its tile's entries into T[rank - w0][bin].
 __device__ __forceinline__ void rank_stage(const RankTile& c, float2 (*T)[NB], uint32_t w0) {
 #pragma unroll
-    for (int j = 0; j < TPT; ++j) {
+    for (int j = 0; j < RPT; ++j) {
         // a rank below w0 wraps above RW; past the rows the rank is 0xffff
         const uint32_t rank = rt_rank(c, j), r = rank - w0;
         if (rank != 0xffffu && r < (uint32_t)RW) T[r][rt_bin(c, j)] = make_float2(rt_g(c, j), rt_h(c, j));
@@ -884,20 +892,21 @@ __device__ __forceinline__ void rank_stage(const RankTile& c, float2 (*T)[NB], u
 // (grow.c:37-62); the count cell is cgrow's chain of 1.0f adds,
 // min(count, 2^24).  Threads 0 .. RB - 1 are the consumers, thread b adding
 // bin b's run of each tile in rank order from an LDS table T[rank][bin];
-// threads RB .. 2 RB - 1 are the producers, filling the other of two tables
-// with the next tile meanwhile (window 0 of every tile; a tile whose longest
-// run passes RW has its further windows staged and added in turn, its
-// positions reloaded).  The producers' next tiles load two tiles ahead.  VEC:
+// threads RB .. RB + RPROD - 1 are the producers, filling the other of two
+// tables with the next tile meanwhile (window 0 of every tile; a tile whose
+// longest run passes RW has its further windows staged and added in turn,
+// its positions reloaded).  The producers' next tiles load RING tiles ahead:
+// a step is shorter than a load's latency under load.  VEC:
 // g, h and the bins are 16-byte aligned (every feature's column:
 // ld_fm % 16 == 0).
 template <bool VEC>
-__global__ void __launch_bounds__(2 * RB) k_rank_chain(const float* __restrict__ g, const float* __restrict__ h,
+__global__ void __launch_bounds__(RB + RPROD) k_rank_chain(const float* __restrict__ g, const float* __restrict__ h,
                                                        const uint8_t* __restrict__ bins_fm, int64_t ld_fm, int64_t n,
                                                        RootOrder o, float* __restrict__ hist, int F) {
     __shared__ float2 T[2][RW][NB];
     const int f = blockIdx.x;
     const bool prod = threadIdx.x >= RB;
-    const int lt = threadIdx.x & (RB - 1);   // consumers: the bin; producers: the position slot
+    const int lt = prod ? (int)threadIdx.x - RB : (int)threadIdx.x;   // consumers: the bin; producers: the slot
     const uint8_t* bn = bins_fm + (size_t)f * (size_t)ld_fm;
     const uint16_t* rk = o.rank + (size_t)f * (size_t)o.ld_rank;
     const uint16_t* sf = o.starts + (size_t)f * (size_t)o.tiles * ST;
@@ -931,28 +940,42 @@ __global__ void __launch_bounds__(2 * RB) k_rank_chain(const float* __restrict__
         else
             rank_tile_load_any(c, g, h, bn, rk, t, n, lt);
     };
-    // producers: tile 0's window 0, and the ring (tiles 1 and 2)
-    RankTile A, B;
+    // every thread: tile t's longest run, RING tiles ahead in mrs[t % RING];
+    // consumers: their bin's run start and end in the tile, in se[t % RING]
+    // (a load used in the step it is issued would put a memory latency on
+    // every tile's path)
+    uint32_t mrs[RING], se[RING];
+    const uint16_t* sfl = sf + lt;   // consumers' start entries: tile t at sfl[t ST], its end at sfl[t ST + 1]
+    auto meta = [&](int k, int64_t t) {
+        if (t < tiles) {
+            mrs[k] = mx[t];
+            if (!prod) se[k] = (uint32_t)sfl[(size_t)t * ST] | ((uint32_t)sfl[(size_t)t * ST + 1] << 16);
+        }
+    };
+#pragma unroll
+    for (int k = 0; k < RING; ++k) meta(k, k);
+    // producers: tile 0's window 0, and the ring (tiles 1 .. RING)
+    RankTile ring[RING];
     if (prod && tiles > 0) {
         RankTile c;
         load(c, 0);
         rank_stage(c, T[0], 0);
     }
     if (prod && full > 0) {
-        rank_tile_load_vec(A, g, h, bn, rk, min((int64_t)1, full - 1), lt);
-        rank_tile_load_vec(B, g, h, bn, rk, min((int64_t)2, full - 1), lt);
+#pragma unroll
+        for (int k = 0; k < RING; ++k) rank_tile_load_vec(ring[k], g, h, bn, rk, min((int64_t)(1 + k), full - 1), lt);
     }
     __syncthreads();
     // step t: the consumers add tile t's window 0 from T[t & 1] while the
     // producers stage tile t + 1's from ring slot R (then reload R with tile
-    // t + 3); then tile t's further windows, if any
-    auto step = [&](int64_t t, RankTile& R) {
+    // t + 1 + RING); then tile t's further windows, if any
+    auto step = [&](int64_t t, RankTile& R, int k) {
         if (t >= tiles) return;
-        const uint32_t mr = (uint32_t)__builtin_amdgcn_readfirstlane((int)mx[t]);
+        const uint32_t mr = (uint32_t)__builtin_amdgcn_readfirstlane((int)mrs[k]);
         uint32_t len = 0;
+        if (!prod) len = (se[k] >> 16) - (se[k] & 0xffffu);
+        meta(k, t + RING);
         if (!prod) {
-            const uint16_t* st = sf + (size_t)t * ST;
-            len = (uint32_t)st[lt + 1] - (uint32_t)st[lt];
             run(T[t & 1], len, mr, 0);
             cnt += len;
         } else if (t + 1 < tiles) {
@@ -964,7 +987,7 @@ __global__ void __launch_bounds__(2 * RB) k_rank_chain(const float* __restrict__
                 rank_stage(c, T[(t + 1) & 1], 0);
             }
         }
-        if (prod && full > 0) rank_tile_load_vec(R, g, h, bn, rk, min(t + 3, full - 1), lt);
+        if (prod && full > 0) rank_tile_load_vec(R, g, h, bn, rk, min(t + 1 + RING, full - 1), lt);
         __syncthreads();
         for (uint32_t w0 = RW; w0 < mr; w0 += RW) {
             if (prod) {
@@ -977,9 +1000,9 @@ __global__ void __launch_bounds__(2 * RB) k_rank_chain(const float* __restrict__
             __syncthreads();
         }
     };
-    for (int64_t t = 0; t < tiles; t += 2) {
-        step(t, A);
-        step(t + 1, B);
+    for (int64_t t = 0; t < tiles; t += RING) {
+#pragma unroll
+        for (int k = 0; k < RING; ++k) step(t + k, ring[k], k);
     }
     if (!prod) {
         hist[(size_t)f * NB + lt] = ag;
@@ -993,9 +1016,9 @@ inline void launch_rank_chain(const float* g, const float* h, const uint8_t* bin
     const bool vec = ((uintptr_t)g % 16 == 0) && ((uintptr_t)h % 16 == 0) && ((uintptr_t)bins_fm % 16 == 0) &&
                      (ld_fm % 16 == 0);
     if (vec)
-        k_rank_chain<true><<<F, 2 * RB, 0, stream>>>(g, h, bins_fm, ld_fm, n, o, hist, F);
+        k_rank_chain<true><<<F, RB + RPROD, 0, stream>>>(g, h, bins_fm, ld_fm, n, o, hist, F);
     else
-        k_rank_chain<false><<<F, 2 * RB, 0, stream>>>(g, h, bins_fm, ld_fm, n, o, hist, F);
+        k_rank_chain<false><<<F, RB + RPROD, 0, stream>>>(g, h, bins_fm, ld_fm, n, o, hist, F);
 }
 
 // Sparse builder's default-bin cells (grow.c:101-106): 0 + (float)(node sum -
