@@ -1100,14 +1100,34 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
         record_published();
         // two levels of tickets, so no one address takes every block's
         // atomic: the last block of split y takes the launch's ticket
-        bool lst = false;
-        if (atomicAdd(&st->split_ticket[y], 1u) == gridDim.x - 1) {
-            st->split_ticket[y] = 0;
-            lst = atomicAdd(&st->scan_ticket, 1u) == (uint32_t)nr - 1;
-        }
-        s_last = lst;
+        const bool sl = atomicAdd(&st->split_ticket[y], 1u) == gridDim.x - 1;
+        if (sl) st->split_ticket[y] = 0;
+        s_last = sl;   // for now: the last of split y
     }
     __syncthreads();
+    if (!ROOT) {
+        // the last block of split y reduces the split's records: wave c the
+        // best over the launch's blocks for child c, into the Pend entry and
+        // its table gain (depth cap applied), published for the controller
+        // before this block takes the launch's ticket
+        const bool sl = s_last != 0;
+        if (sl && w < 2) {
+            const ScanRec r = wave_best_record_agent(A.rec + ((size_t)y * 2 + w) * gridDim.x, gridDim.x, lane);
+            if (lane == 0) {
+                Pend* Pw = A.pend + pidx;
+                publish_record(&Pw->child[w], r);
+                __hip_atomic_store(&A.psum[pidx].gain[w], rec_gain(r, P->depth >= A.max_depth), __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+                record_published();
+            }
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) s_last = sl && atomicAdd(&st->scan_ticket, 1u) == (uint32_t)nr - 1;
+        __syncthreads();
+    } else if (threadIdx.x == 0) {
+        s_last = s_last && atomicAdd(&st->scan_ticket, 1u) == 0u;
+    }
+    if (ROOT) __syncthreads();
     const bool last = s_last != 0;
     if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
     // every wave of the block has loaded its bins (barriers above): store
@@ -1145,41 +1165,14 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
         wave_sync();
         control(A, T, 1, 1, 0, &s_root, lane);
     } else {
-        // the round's children: best record over the scan blocks, per child;
-        // wave w takes children w, w + 8, ..., their records' loads first
-        constexpr int CPW = 2 * KMAX / (NT / WAVE);   // children per wave, at most
-        static_assert(CPW * (NT / WAVE) == 2 * KMAX, "children per wave");
-        ScanRec rr[CPW];
-        // the splits' depths (for the depth cap), loaded beside the records
-        int dep[CPW];
-#pragma unroll
-        for (int k = 0; k < CPW; ++k) {
-            const int i = w + k * (NT / WAVE);
-            dep[k] = (i < 2 * nr) ? A.pend[np_now - nr + i / 2].depth : 0;
-        }
-        if (gridDim.x <= WAVE) {
-            wave_best_records<CPW>(A.rec, gridDim.x, w, NT / WAVE, 2 * nr, lane, rr);
-        } else {
-#pragma unroll
-            for (int k = 0; k < CPW; ++k) {
-                const int i = w + k * (NT / WAVE);
-                if (i < 2 * nr) rr[k] = wave_best_record(A.rec + (size_t)i * gridDim.x, gridDim.x, lane);
-            }
-        }
-#pragma unroll
-        for (int k = 0; k < CPW; ++k) {
-            const int i = w + k * (NT / WAVE);
-            if (i < 2 * nr && lane == 0) {
-                const int p = np_now - nr + i / 2;   // the round's splits: the last nr Pend entries
-                Pend& Pp = A.pend[p];
-                Pp.child[i % 2] = rr[k];
-                const float g = rec_gain(rr[k], dep[k] >= A.max_depth);
-                T.cgain[p][i % 2] = g;
-                A.psum[p].gain[i % 2] = g;   // kept for later controllers
-            }
-        }
+        // the round's children: their records and table gains, reduced and
+        // published by each split's last scan block
         const int nn = st->n_nodes, na = st->n_leaves, np = st->n_pend;
         const int p0 = np - nr;                   // this round's splits: p0 .. np - 1
+        if (threadIdx.x < 2 * nr) {
+            const int p = p0 + threadIdx.x / 2, c = threadIdx.x & 1;
+            T.cgain[p][c] = __hip_atomic_load(&A.psum[p].gain[c], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         auto put = [&](int p, const PendSum& S) {
             if (p < p0) {
                 T.cgain[p][0] = S.gain[0];

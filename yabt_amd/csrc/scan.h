@@ -330,6 +330,28 @@ __device__ inline ScanRec wave_best_record(const ScanRec* rec, int n, int lane) 
     return wave_reduce_record(mine, my_idx);
 }
 
+// wave_best_record over records other blocks of the launch published with
+// publish_record: read with agent-scope atomic loads, which no stale line of
+// this XCD's L2 can serve.
+__device__ inline ScanRec wave_best_record_agent(const ScanRec* rec, int n, int lane) {
+    ScanRec mine = empty_record();
+    int my_idx = -1;
+    for (int i = lane; i < n; i += WAVE) {
+        uint64_t w[sizeof(ScanRec) / 8];
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(rec + i);
+#pragma unroll
+        for (int k = 0; k < (int)(sizeof(ScanRec) / 8); ++k)
+            w[k] = __hip_atomic_load(src + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        ScanRec r;
+        __builtin_memcpy(&r, w, sizeof(ScanRec));
+        if (rec_beats(r.sel, r.f, r.b, mine.sel, mine.f, mine.b)) {
+            mine = r;
+            my_idx = i;
+        }
+    }
+    return wave_reduce_record(mine, my_idx);
+}
+
 // Several waves' worth of wave_best_record at once: out[k] = the best of
 // rec[i n, i n + n) for i = w0 + k stride < nchild (n <= 64: one record per
 // lane), all loads issued before any reduction.
