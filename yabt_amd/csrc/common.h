@@ -230,6 +230,18 @@ __device__ __forceinline__ uint64_t wave_max_u64_v(uint64_t v) {
     return max_u64(((uint64_t)h32[0] << 32) | l32[0], ((uint64_t)h32[1] << 32) | l32[1]);
 }
 
+// The same for an unsigned 32-bit value (each step one DPP-fused max).
+__device__ __forceinline__ uint32_t wave_max_u32_v(uint32_t v) {
+    v = max(v, dpp32<DPP_ROW_ROR + 8>(v));
+    v = max(v, dpp32<DPP_ROW_ROR + 4>(v));
+    v = max(v, dpp32<DPP_ROW_ROR + 2>(v));
+    v = max(v, dpp32<DPP_ROW_ROR + 1>(v));
+    const auto s16 = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+    v = max((uint32_t)s16[0], (uint32_t)s16[1]);
+    const auto s32 = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+    return max((uint32_t)s32[0], (uint32_t)s32[1]);
+}
+
 __device__ __forceinline__ int wave_min_i32(int v) {
     v = min(v, (int)dpp32<DPP_ROW_ROR + 8>((uint32_t)v));
     v = min(v, (int)dpp32<DPP_ROW_ROR + 4>((uint32_t)v));

@@ -67,6 +67,10 @@ constexpr int MAX_LEAVES = 1024;                 // leaf table held in the contr
 constexpr int PEND_PER_LEAF = 3;                 // computed splits per leaf of the budget, at most
 constexpr int LEAF_CHUNK = 8192;                 // rows per leaf-id block
 constexpr int LEAF_PLAN = 1024;                  // threads of the leaf-id planning block
+// index bits of a packed planning candidate: candidates are the leaves and
+// both children of every computed split, below 2^PICK_IDX_BITS
+constexpr int PICK_IDX_BITS = 13;
+static_assert(MAX_LEAVES + 2 * (PEND_PER_LEAF * MAX_LEAVES + KMAX) <= (1 << PICK_IDX_BITS), "candidate indices");
 
 // A computed split.  Leaves of the table name their origin as 2 p + c (child
 // c of split p) or -1 (the root).
@@ -749,27 +753,31 @@ __device__ __forceinline__ void control(const Args& A, Table& T, int nn, int na,
         wave_sync();
         // take best, then the largest keys (the lowest candidate on ties).
         // Short lists sit in registers, R entries per lane, each candidate
-        // packed as its key's bits (positive floats order as unsigned
-        // integers) over its inverted index, so that a pick is one 64-bit
-        // wave maximum; each lane keeps its best, and the budget count is a
-        // ballot per register.  Lane t keeps the round's split t.
+        // packed into 32 bits as its key's top bits (positive floats order as
+        // unsigned integers) over its inverted index, so that a pick is one
+        // 32-bit wave maximum.  Keys that agree in those bits are picked by
+        // index and counted for the budget as equal: that changes which
+        // splits a round computes, never the tree (the commits replay the
+        // table).  Each lane keeps its best, the budget count is a ballot per
+        // register, and lane t keeps the round's split t.
         constexpr int R = 4;
+        constexpr uint32_t IDX = (1u << PICK_IDX_BITS) - 1;
         const bool in_regs = m <= R * WAVE && mb <= R * WAVE;
-        float bk[R];
-        uint64_t pc[R];
-        uint64_t lb = 0;   // this lane's best packed candidate (0: none)
+        uint32_t bk[R];   // budget keys, bucketed as the candidates' (0: none)
+        uint32_t pc[R];
+        uint32_t lb = 0;   // this lane's best packed candidate (0: none)
         auto lane_best = [&]() {
             lb = 0;
 #pragma unroll
-            for (int r = 0; r < R; ++r) lb = pc[r] > lb ? pc[r] : lb;
+            for (int r = 0; r < R; ++r) lb = max(lb, pc[r]);
         };
         if (in_regs) {
 #pragma unroll
             for (int r = 0; r < R; ++r) {
                 const int i = lane + r * WAVE;
-                const float k = i < m ? T.ckand[i] : 0.0f;   // listed keys are > 0
-                pc[r] = i < m ? ((uint64_t)__float_as_uint(k) << 32) | (uint32_t)(INT_MAX - (int)T.cidx[i]) : 0;
-                bk[r] = i < mb ? T.cbud[i] : -INFINITY;
+                // listed keys and budget entries are > 0
+                pc[r] = i < m ? (__float_as_uint(T.ckand[i]) & ~IDX) | (IDX - (uint32_t)T.cidx[i]) : 0u;
+                bk[r] = i < mb ? __float_as_uint(T.cbud[i]) & ~IDX : 0u;
             }
             lane_best();
         }
@@ -778,26 +786,26 @@ __device__ __forceinline__ void control(const Args& A, Table& T, int nn, int na,
             // after best) and the budget count at its key go to lane t, with
             // no scalar work between extractions; then the stopping rules
             // below, as the one-at-a-time loop applies them
-            uint64_t pk = 0;   // lane t: extraction t
+            uint32_t pk = 0;   // lane t: extraction t
             int pe = 0;        // lane t: budget entries >= its key
             // a pick past the candidates or at na + t >= L stops the round
             // whatever its budget count, so those are not extracted
             const int t_end = min(KMAX, min(m, L - na - 1) + 1);
 #pragma unroll 1
             for (int t = 1; t < t_end; ++t) {
-                const uint64_t top = wave_max_u64_v(lb);
-                const float key = __uint_as_float((uint32_t)(top >> 32));
+                const uint32_t top = wave_max_u32_v(lb);
+                const uint32_t key = top & ~IDX;
                 int e = 0;
 #pragma unroll
-                for (int r = 0; r < R; ++r) e += __popcll(__ballot(bk[r] >= key));
+                for (int r = 0; r < R; ++r) e += __popcll(__ballot(bk[r] != 0u && bk[r] >= key));
                 if (lane == t) {
                     pk = top;
                     pe = e;
                 }
-                if (top != 0 && lb == top) {   // its lane drops it and looks again
+                if (top != 0u && lb == top) {   // its lane drops it and looks again
 #pragma unroll
                     for (int r = 0; r < R; ++r)
-                        if (pc[r] == top) pc[r] = 0;
+                        if (pc[r] == top) pc[r] = 0u;
                     lane_best();
                 }
             }
@@ -810,11 +818,11 @@ __device__ __forceinline__ void control(const Args& A, Table& T, int nn, int na,
                 ++np;
                 ++j;
                 if (j >= KMAX) break;
-                if (readlane64((int64_t)pk, j) == 0) break;
+                if (__builtin_amdgcn_readlane((int)pk, j) == 0) break;
                 // the budget: leaves of the run-ahead when it pops this one
                 if (na + __builtin_amdgcn_readlane(pe, j) + j >= L) break;
             }
-            my_pick = lane == 0 ? best : INT_MAX - (int)(uint32_t)pk;
+            my_pick = lane == 0 ? best : (int)(IDX - (pk & IDX));
         } else {
             int cand = best, cpos = -1;
             for (;;) {
