@@ -365,9 +365,10 @@ __device__ inline bool last_block(uint32_t* ticket) {
 // quantisation passes
 // ---------------------------------------------------------------------------
 
-// Grid-stride max|g|, max|h|, min/max h and finiteness into q (NT threads).
+// Grid-stride max|g|, max|h|, min/max h and finiteness into q (NT threads);
+// with gh, also the interleaved copy gh[i] = (grad[i], hess[i]).
 template <int NT>
-__device__ void quant_reduce(const float* grad, const float* hess, int64_t n, Quant* q) {
+__device__ void quant_reduce(const float* grad, const float* hess, int64_t n, Quant* q, float2* gh = nullptr) {
     __shared__ float s_m[2][NT / WAVE];
     __shared__ uint32_t s_k[2][NT / WAVE];
     __shared__ int s_nf;
@@ -408,6 +409,11 @@ __device__ void quant_reduce(const float* grad, const float* hess, int64_t n, Qu
                 take(a[u].y, c[u].y);
                 take(a[u].z, c[u].z);
                 take(a[u].w, c[u].w);
+                if (gh) {
+                    float4* o = reinterpret_cast<float4*>(gh + 4 * (i + u * nth));
+                    o[0] = make_float4(a[u].x, c[u].x, a[u].y, c[u].y);
+                    o[1] = make_float4(a[u].z, c[u].z, a[u].w, c[u].w);
+                }
             }
         }
         for (; i < n4; i += nth) {
@@ -416,10 +422,18 @@ __device__ void quant_reduce(const float* grad, const float* hess, int64_t n, Qu
             take(a.y, c.y);
             take(a.z, c.z);
             take(a.w, c.w);
+            if (gh) {
+                float4* o = reinterpret_cast<float4*>(gh + 4 * i);
+                o[0] = make_float4(a.x, c.x, a.y, c.y);
+                o[1] = make_float4(a.z, c.z, a.w, c.w);
+            }
         }
         head = n4 * 4;
     }
-    for (int64_t i = head + tid; i < n; i += nth) take(grad[i], hess[i]);
+    for (int64_t i = head + tid; i < n; i += nth) {
+        take(grad[i], hess[i]);
+        if (gh) gh[i] = make_float2(grad[i], hess[i]);
+    }
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
 #pragma unroll
     for (int d = WAVE / 2; d > 0; d >>= 1) {

@@ -141,6 +141,7 @@ struct Args {
     int64_t ld_rm;
     const float* grad;
     const float* hess;
+    float2* gh;                          // (n) (g, h) interleaved, written by k_setup: one load per gathered row
     const uint8_t* fmask;
     const float* imat;
     float ib;
@@ -186,7 +187,7 @@ __device__ __forceinline__ size_t slot_elems(int F) { return (size_t)3 * (size_t
 // ---------------------------------------------------------------------------
 
 __global__ void __launch_bounds__(SB) k_setup(Args A) {
-    quant_reduce<SB>(A.grad, A.hess, A.n, A.q);
+    quant_reduce<SB>(A.grad, A.hess, A.n, A.q, A.gh);
     const int N = 2 * A.max_leaves + 1;
     const int64_t tid = (int64_t)blockIdx.x * SB + threadIdx.x;
     const int64_t stride = (int64_t)gridDim.x * SB;
@@ -355,6 +356,7 @@ __host__ __device__ inline int64_t gather_unit_rows(int64_t R, int nr, int tiles
 // on one die, sharing its L2 for the rows' bins, ids and g, h.
 __global__ void __launch_bounds__(HBLOCK) k_gather(const uint8_t* __restrict__ bins_rm, int64_t ld,
                                                    const float* __restrict__ grad, const float* __restrict__ hess,
+                                                   const float2* __restrict__ gh,
                                                    int F, const Quant* q, const int32_t* __restrict__ dflt,
                                                    const State* st, const Pend* pend, int64_t* pieces, int wlog) {
     const int32_t done = st->done, nr = st->n_round;
@@ -377,17 +379,17 @@ __global__ void __launch_bounds__(HBLOCK) k_gather(const uint8_t* __restrict__ b
     if (no_h) {
         if (dflt)
             hist_gather_rows<false, true, true>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, P.dst, lo, hi, out,
-                                                wlog, tile);
+                                                wlog, tile, gh);
         else
             hist_gather_rows<false, false, true>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, P.dst, lo, hi, out,
-                                                 wlog, tile);
+                                                 wlog, tile, gh);
     } else {
         if (dflt)
             hist_gather_rows<true, true, true>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, P.dst, lo, hi, out,
-                                               wlog, tile);
+                                               wlog, tile, gh);
         else
             hist_gather_rows<true, false, true>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, P.dst, lo, hi, out,
-                                                wlog, tile);
+                                                wlog, tile, gh);
     }
 }
 
@@ -1359,6 +1361,7 @@ size_t carve(char* base, int64_t n, int F, int max_leaves, Args* A) {
     a.st = c.take<State>(1);
     a.q = c.take<Quant>(1);
     a.rows = c.take<uint32_t>((size_t)2 * (size_t)a.rows_ld);
+    a.gh = c.take<float2>((size_t)(n > 0 ? n : 1));
     a.hist = c.take<int64_t>((size_t)(pend_cap + 1) * 3 * (size_t)F * NB);
     a.pieces = c.take<int64_t>((size_t)gather_units((F + HFL - 1) / HFL) * 3 * (size_t)F * NB);
     a.pend_path = c.take<uint8_t>((size_t)pend_cap * (size_t)F);
@@ -1491,7 +1494,7 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
         }
         if (fl->word & 1) break;
         k_part<<<PART_BLOCKS, SB, 0, stream>>>(bins_fm, ld_fm, n, A.st, A.pend);
-        k_gather<<<tiles * gather_units(tiles), HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, A.q, A.dflt,
+        k_gather<<<tiles * gather_units(tiles), HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, A.gh, F, A.q, A.dflt,
                                                                          A.st, A.pend, A.pieces, wlog);
         k_scan<false><<<dim3(scan_grid, KMAX), CT, scan_lds, stream>>>(A);
         if ((lrc = launch_status("yabt_grow_batched launch"))) return lrc;

@@ -812,7 +812,8 @@ __device__ __forceinline__ void hist_gather_rows(GatherLds& LU, const uint8_t* _
                                                  const float* __restrict__ grad, const float* __restrict__ hess,
                                                  int F, double scg, double sch, const int32_t* __restrict__ dflt,
                                                  const uint32_t* __restrict__ rows, int64_t lo, int64_t hi,
-                                                 int64_t* out, int wlog, int tile) {
+                                                 int64_t* out, int wlog, int tile,
+                                                 const float2* __restrict__ gh = nullptr) {
     const int f0 = tile * HFL;
     if (f0 >= F || lo >= hi) return;
     HistLdsP& L = LU.p;
@@ -858,7 +859,20 @@ __device__ __forceinline__ void hist_gather_rows(GatherLds& LU, const uint8_t* _
         qa[e] = 0;
         ca[e] = 0;
     }
-    float gx = grad[r0], hx = HCH ? hess[r0] : 0.0f;
+    // a row's g and h: one 8-byte load from the interleaved copy when given
+    // (one sector for both), else two
+    auto load_gh = [&](uint32_t r, float& g, float& h) {
+        if (gh) {
+            const float2 v = gh[r];
+            g = v.x;
+            h = HCH ? v.y : 0.0f;
+        } else {
+            g = grad[r];
+            h = HCH ? hess[r] : 0.0f;
+        }
+    };
+    float gx, hx;
+    load_gh(r0, gx, hx);
     uint4 bv = *reinterpret_cast<const uint4*>(tb + (size_t)r0 * ld);
     __syncthreads();
     const int64_t steps = (hi - lo + HSTEP - 1) / HSTEP;   // the same in every wave: barriers below
@@ -866,7 +880,8 @@ __device__ __forceinline__ void hist_gather_rows(GatherLds& LU, const uint8_t* _
         const int64_t i0 = w0 + s * HSTEP, i1 = i0 + HSTEP, i2 = i1 + HSTEP;
         // stage: row ids of step s + 2; g, h and bins of step s + 1
         const uint32_t r2 = row_at(i2 + lane);
-        const float gn = grad[r1], hn = HCH ? hess[r1] : 0.0f;
+        float gn, hn;
+        load_gh(r1, gn, hn);
         const uint4 bn = *reinterpret_cast<const uint4*>(tb + (size_t)r1 * ld);
         // step s
         const bool rok = i0 + lane < hi;
