@@ -64,6 +64,7 @@ constexpr int XCDS = 8;                          // dies of the device; blocks g
 constexpr int CT = 2 * SCAN_FEATS * WAVE;        // threads of a split-scan block (the controller)
 constexpr int LOOKAHEAD = 3;                     // rounds the host keeps in flight
 constexpr int MAX_LEAVES = 1024;                 // leaf table held in the controller's LDS
+constexpr int TABLE_REGS = 4;                    // leaf-table entries per lane when the replay holds it in registers
 constexpr int PEND_PER_LEAF = 3;                 // computed splits per leaf of the budget, at most
 constexpr int LEAF_CHUNK = 8192;                 // rows per leaf-id block
 constexpr int LEAF_PLAN = 1024;                  // threads of the leaf-id planning block
@@ -652,7 +653,88 @@ __device__ __forceinline__ void control(const Args& A, Table& T, int nn, int na,
     const int nn0 = nn;
     // replay (grow.c:321-330): commit the best leaf while its split is computed
     int best = -1, ncm = 0;
-    while (na < L) {
+    if (L <= TABLE_REGS * WAVE) {
+        // the table in registers, entry u * 64 + lane in slot u of the lane.
+        // A positive fp32 gain orders as its bits, so the best is a 32-bit
+        // wave maximum of the lanes' best bits (non-positive and NaN gains
+        // count as 0), and the lowest entry holding it is the lowest lane of
+        // the first slot whose ballot is not empty: cgrow's first maximum
+        // above 0.
+        float tg[TABLE_REGS];
+        int tp[TABLE_REGS], ts[TABLE_REGS], tn[TABLE_REGS];
+#pragma unroll
+        for (int u = 0; u < TABLE_REGS; ++u) {
+            const int a = u * WAVE + lane;
+            const bool in = a < na;
+            tg[u] = in ? T.gain[a] : -INFINITY;
+            tp[u] = in ? (int)T.pend[a] : -1;
+            ts[u] = in ? (int)T.src[a] : 0;
+            tn[u] = in ? (int)T.node[a] : 0;
+        }
+        auto bits = [](float g) { return g > 0.0f ? __float_as_uint(g) : 0u; };
+        while (na < L) {
+            uint32_t lb = 0;
+#pragma unroll
+            for (int u = 0; u < TABLE_REGS; ++u) lb = max(lb, bits(tg[u]));
+            const uint32_t m = (uint32_t)__builtin_amdgcn_readfirstlane((int)wave_max_u32_v(lb));
+            if (m == 0u) break;
+            int ub = 0;
+            uint64_t bal = 0;
+#pragma unroll
+            for (int u = TABLE_REGS - 1; u >= 0; --u) {
+                const uint64_t b = __ballot(bits(tg[u]) == m);
+                if (b != 0) {
+                    ub = u;
+                    bal = b;
+                }
+            }
+            const int bl = __builtin_ctzll(bal);
+            best = ub * WAVE + bl;
+            int pv = tp[0], nv = tn[0];
+#pragma unroll
+            for (int u = 1; u < TABLE_REGS; ++u) {
+                pv = ub == u ? tp[u] : pv;
+                nv = ub == u ? tn[u] : nv;
+            }
+            const int p = __builtin_amdgcn_readlane(pv, bl);
+            if (p < 0) break;
+            const int nid = __builtin_amdgcn_readlane(nv, bl);
+            const float g0 = T.cgain[p][0], g1 = T.cgain[p][1];
+            const int c0 = T.cpend[p][0], c1 = T.cpend[p][1];
+            // left child replaces the split leaf, right child is appended
+            // (grow.c:393-407)
+            const int un = na / WAVE, ln = na % WAVE;
+#pragma unroll
+            for (int u = 0; u < TABLE_REGS; ++u) {
+                const bool atb = u == ub && lane == bl, atn = u == un && lane == ln;
+                tg[u] = atb ? g0 : (atn ? g1 : tg[u]);
+                tp[u] = atb ? c0 : (atn ? c1 : tp[u]);
+                ts[u] = atb ? 2 * p : (atn ? 2 * p + 1 : ts[u]);
+                tn[u] = atb ? nn : (atn ? nn + 1 : tn[u]);
+            }
+            if (lane == 0) {
+                T.ccommit[p] = 1;
+                T.commit_p[ncm] = (int16_t)p;
+                T.commit_nid[ncm] = (int16_t)nid;
+            }
+            nn += 2;
+            ++na;
+            ++ncm;
+            best = -1;
+        }
+#pragma unroll
+        for (int u = 0; u < TABLE_REGS; ++u) {
+            const int a = u * WAVE + lane;
+            if (a < na) {
+                T.gain[a] = tg[u];
+                T.pend[a] = (int16_t)tp[u];
+                T.src[a] = (int16_t)ts[u];
+                T.node[a] = (int16_t)tn[u];
+            }
+        }
+        wave_sync();
+    }
+    while (L > TABLE_REGS * WAVE && na < L) {
         best = wave_table_argmax(T.gain, na, lane);
         if (best < 0 || T.pend[best] < 0) break;
         const int p = T.pend[best];
