@@ -209,6 +209,19 @@ int yabt_leaf_fold(int n_nodes, int K, const float *W, const float *b, const flo
                    const float *sd, float lr, const float *value_in, float *out_value,
                    float *out_linear, yabt_stream_t stream);
 
+/* The leaf models' inputs: the internal nodes' features (feature[i] >= 0 of
+ * n_nodes entries, 1 <= F <= 4096), most used first, equal counts in the
+ * order torch's CPU argsort gives them (libstdc++'s introsort over the
+ * ascending unique features), the first k (1..8) written to out_feats
+ * (int64) and out_feats32; positions past the used features get 0.
+ * *out_m (device) = the number of used features, -1 if a node names a
+ * feature >= F.  One block on `stream`, nothing read back: a caller may
+ * launch yabt_leaf_moments / yabt_leaf_fit on out_feats32 before reading
+ * *out_m, and falls back when *out_m < k.  Replaces the ranking of
+ * `_used_features` (yabt/neural_leaves.py:27-31). */
+int yabt_leaf_rank_features(const int64_t *feature, int n_nodes, int F, int k, int64_t *out_feats,
+                            int32_t *out_feats32, int32_t *out_m, yabt_stream_t stream);
+
 /* Workspace bytes of yabt_leaf_moments for n rows. */
 size_t yabt_leaf_moments_workspace_bytes(int64_t n);
 

@@ -237,3 +237,100 @@ def test_fit_leaf_networks_end_to_end():
     pred0 = value[leaf]
     pred1 = out.predict(Xd).cpu().numpy()
     assert ((pred1 - (y - margin)) ** 2).mean() < ((pred0 - (y - margin)) ** 2).mean()
+
+
+def _rank_device(feature, F, k):
+    """yabt_leaf_rank_features through the C ABI: (feats[:k] int64, n used)."""
+    from yabt_amd import _lib
+    lib = _lib.load()
+    ft = torch.as_tensor(feature, dtype=torch.int64, device=DEV)
+    out = torch.full((k,), -7, dtype=torch.int64, device=DEV)
+    out32 = torch.full((k,), -7, dtype=torch.int32, device=DEV)
+    m = torch.full((1,), -7, dtype=torch.int32, device=DEV)
+    st = torch.cuda.current_stream(DEV).cuda_stream
+    _lib.check(lib.yabt_leaf_rank_features(ft.data_ptr(), int(ft.numel()), F, k, out.data_ptr(), out32.data_ptr(),
+                                           m.data_ptr(), st), "yabt_leaf_rank_features")
+    torch.cuda.synchronize()
+    assert torch.equal(out.to(torch.int32), out32)
+    return out.cpu(), int(m.item())
+
+
+def _rank_cases():
+    rng = np.random.default_rng(11)
+    cases = []
+    for trial in range(160):
+        F = int(rng.choice([1, 3, 8, 28, 100, 500, 4096]))
+        N = int(rng.choice([1, 3, 31, 255, 511, 2047, 2049]))
+        spread = int(rng.integers(1, F + 1))
+        feature = rng.integers(0, spread, N)
+        if trial % 4 == 1:
+            feature = np.sort(feature)                     # ties met in sorted runs
+        if trial % 4 == 2:
+            feature[:N // 2] = rng.integers(0, max(1, spread // 8), N // 2)   # a few dominant features
+        feature[rng.random(N) < 0.5] = -1                  # leaves
+        cases.append((feature, F, int(rng.integers(1, 9))))
+    cases.append((np.full(7, -1, np.int64), 10, 8))        # no internal node
+    cases.append((np.arange(40, dtype=np.int64) % 20, 20, 8))   # 20 features, all counts equal
+    return cases
+
+
+def test_leaf_rank_features_equals_torch_cpu_argsort():
+    """The device ranking gives torch's unique + CPU argsort order (the
+    reference's _used_features), ties included, for trees using more or fewer
+    features than k."""
+    from yabt_amd.neural_leaves import _used_features
+    for feature, F, k in _rank_cases():
+        got, m = _rank_device(feature, F, k)
+        want = _used_features(torch.as_tensor(feature), k)
+        f = feature[feature >= 0]
+        assert m == len(np.unique(f))
+        assert got[:want.numel()].tolist() == want.tolist(), (F, k, m)
+        assert (got[want.numel():] == 0).all()
+
+
+def test_leaf_rank_features_flags_feature_out_of_range():
+    got, m = _rank_device(np.array([0, 5, -1, 2], np.int64), 5, 3)
+    assert m == -1
+
+
+def test_fit_binned_device_ranking_equals_host_ranking():
+    """fit_leaf_networks_binned with the device ranking (the default) gives
+    the same tree, bit for bit, as the host ranking path."""
+    from yabt_amd import neural_leaves as NL
+    rng = np.random.default_rng(5)
+    n, F = 50_000, 30
+    X = uniform_bins(rng, n, F)
+    fm = torch.as_tensor(np.ascontiguousarray(X.T), device=DEV)
+    g, h = grad_hess(rng, n)
+    gd, hd = torch.as_tensor(g, device=DEV), torch.as_tensor(h, device=DEV)
+    # a tree with many tied feature counts: random internal nodes over F features
+    N = 2 * 63 + 1
+    feature = np.full(N, -1, np.int64)
+    left = np.full(N, -1, np.int64)
+    right = np.full(N, -1, np.int64)
+    for i in range(62):
+        feature[i] = rng.integers(0, F)
+        left[i], right[i] = 2 * i + 1, 2 * i + 2
+    thr = torch.as_tensor(rng.integers(0, 255, N).astype(np.float32), device=DEV)
+    tr = Tree(torch.as_tensor(feature, device=DEV), thr, torch.as_tensor(left, device=DEV),
+            torch.as_tensor(right, device=DEV), torch.as_tensor(rng.normal(size=N).astype(np.float32), device=DEV), 0)
+    leaf = torch.as_tensor(rng.integers(62, 125, n), device=DEV)
+
+    @dataclass
+    class P:
+        learning_rate: float = 0.1
+        leaf_net_features: int = 8
+        leaf_net_min_samples: int = 50
+        leaf_net_l2: float = 1.0
+        leaf_net_hidden: int = 0
+    dev_out = NL.fit_leaf_networks_binned(tr, fm, gd, hd, leaf, P(), n=n)
+    keep = NL.RANK_MAX_FEATURES
+    try:
+        NL.RANK_MAX_FEATURES = 0                            # host ranking
+        host_out = NL.fit_leaf_networks_binned(tr, fm, gd, hd, leaf, P(), n=n)
+    finally:
+        NL.RANK_MAX_FEATURES = keep
+    assert dev_out.leaf_net_feats is not None
+    assert torch.equal(dev_out.leaf_net_feats.cpu(), host_out.leaf_net_feats.cpu())
+    for a in ("value", "leaf_net_linear", "leaf_net_lo", "leaf_net_hi"):
+        assert torch.equal(getattr(dev_out, a), getattr(host_out, a)), a

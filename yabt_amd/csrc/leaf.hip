@@ -1082,6 +1082,218 @@ void launch_leaf_fit(LeafArgs& A, float* out_W, float* out_b, float* out_lo, flo
                                                                                out_count);
 }
 
+// ---------------------------------------------------------------------------
+// the leaf models' inputs: the tree's split features, most used first
+// (neural_leaves.py:27-31), ranked on the device
+// ---------------------------------------------------------------------------
+//
+// The reference takes torch.unique of the internal nodes' features (ascending
+// features, their counts), then argsort of the counts, descending, on the
+// CPU.  That argsort is libstdc++'s std::sort over (count, position) pairs
+// compared by count alone, so its order of equal counts is the introsort's:
+// median-of-three partitions (pivot moved to the front, unguarded Hoare
+// scans) until 16 elements or 2 floor(log2 m) levels, a heap sort of a range
+// past that depth, then one insertion sort of the whole list (the first 16
+// guarded, the rest unguarded).  The ranking below runs those steps in one
+// lane over an LDS list; a range's steps depend only on the range, so a stack
+// of ranges replaces the recursion without changing the order.
+
+constexpr int RANK_T = 256;
+constexpr int RANK_MAX_F = 4096;               // features the device ranking takes, at most
+
+struct RankEl {
+    int32_t c, f;                              // count, feature
+};
+
+namespace rank {
+
+__device__ __forceinline__ bool gt(const RankEl& a, const RankEl& b) { return a.c > b.c; }
+__device__ __forceinline__ void swap_at(RankEl* v, int a, int b) {
+    const RankEl t = v[a];
+    v[a] = v[b];
+    v[b] = t;
+}
+
+// Sift a hole at `hole` down to a leaf of the heap v[0, len), then `value`
+// up from there (the heap's parent is never smaller under gt).
+__device__ __forceinline__ void adjust_heap(RankEl* v, int hole, int len, RankEl value) {
+    const int top = hole;
+    int child = hole;
+    while (child < (len - 1) / 2) {
+        child = 2 * (child + 1);
+        if (gt(v[child], v[child - 1])) --child;
+        v[hole] = v[child];
+        hole = child;
+    }
+    if ((len & 1) == 0 && child == (len - 2) / 2) {
+        child = 2 * (child + 1);
+        v[hole] = v[child - 1];
+        hole = child - 1;
+    }
+    int parent = (hole - 1) / 2;
+    while (hole > top && gt(v[parent], value)) {
+        v[hole] = v[parent];
+        hole = parent;
+        parent = (hole - 1) / 2;
+    }
+    v[hole] = value;
+}
+
+// Heap sort of v[0, len): build the heap, then pop its top to the back.
+__device__ __forceinline__ void heap_sort(RankEl* v, int len) {
+    if (len < 2) return;
+    for (int parent = (len - 2) / 2;; --parent) {
+        adjust_heap(v, parent, len, v[parent]);
+        if (parent == 0) break;
+    }
+    for (int last = len - 1; last > 0; --last) {
+        const RankEl value = v[last];
+        v[last] = v[0];
+        adjust_heap(v, 0, last, value);
+    }
+}
+
+// The median of v[a], v[b], v[c] swapped into v[r].
+__device__ __forceinline__ void median_to(RankEl* v, int r, int a, int b, int c) {
+    if (gt(v[a], v[b])) {
+        if (gt(v[b], v[c])) swap_at(v, r, b);
+        else if (gt(v[a], v[c])) swap_at(v, r, c);
+        else swap_at(v, r, a);
+    } else if (gt(v[a], v[c])) {
+        swap_at(v, r, a);
+    } else if (gt(v[b], v[c])) {
+        swap_at(v, r, c);
+    } else {
+        swap_at(v, r, b);
+    }
+}
+
+// Hoare partition of v[lo, hi) around v[p] (p < lo), without bounds tests.
+__device__ __forceinline__ int partition(RankEl* v, int lo, int hi, int p) {
+    for (;;) {
+        while (gt(v[lo], v[p])) ++lo;
+        --hi;
+        while (gt(v[p], v[hi])) --hi;
+        if (!(lo < hi)) return lo;
+        swap_at(v, lo, hi);
+        ++lo;
+    }
+}
+
+// Insert v[i] into the sorted run before it, without a bounds test.
+__device__ __forceinline__ void linear_insert(RankEl* v, int i) {
+    const RankEl val = v[i];
+    int j = i - 1;
+    while (gt(val, v[j])) {
+        v[i] = v[j];
+        i = j;
+        --j;
+    }
+    v[i] = val;
+}
+
+// The first k positions of std::sort over v[0, m).  Every element of a
+// partitioned range is >= every element of the ranges after it (the pivot
+// stays at the front of the left range), and the final insertion sort never
+// moves an element past one that is not smaller, so a range that starts at k
+// or later never reaches the first k: it is left unsorted, and the insertion
+// sort stops at the end E of the ranges holding positions below k.
+__device__ __forceinline__ void sort(RankEl* v, int m, int k, int* stk) {
+    if (m < 2) return;
+    int top = 0, E = 0;
+    int first = 0, last = m, depth = 2 * (31 - __clz(m));
+    for (;;) {
+        while (last - first > 16) {
+            if (depth == 0) {
+                heap_sort(v + first, last - first);
+                break;
+            }
+            --depth;
+            const int mid = first + (last - first) / 2;
+            median_to(v, first, first + 1, mid, last - 1);
+            const int cut = partition(v, first + 1, last, first);
+            if (cut < k) {   // [cut, last) at this depth, later
+                stk[3 * top] = cut;
+                stk[3 * top + 1] = last;
+                stk[3 * top + 2] = depth;
+                ++top;
+            }
+            last = cut;
+        }
+        E = last > E ? last : E;   // [first, last), first < k, is final
+        if (top == 0) break;
+        --top;
+        first = stk[3 * top];
+        last = stk[3 * top + 1];
+        depth = stk[3 * top + 2];
+    }
+    // the final insertion sort, over [0, E)
+    const int g = E > 16 ? 16 : E;
+    for (int i = 1; i < g; ++i) {
+        if (gt(v[i], v[0])) {
+            const RankEl val = v[i];
+            for (int j = i; j > 0; --j) v[j] = v[j - 1];
+            v[0] = val;
+        } else {
+            linear_insert(v, i);
+        }
+    }
+    for (int i = g; i < E; ++i) linear_insert(v, i);
+}
+
+}  // namespace rank
+
+// One block: counts per feature in LDS, the used features listed in
+// ascending order by wave 0, the list sorted by lane 0, the first k written
+// (positions past the list get feature 0, so that launches made before the
+// host reads *out_m stay in bounds).  *out_m: the number of used features,
+// -1 if a node names a feature outside [0, F).
+__global__ void __launch_bounds__(RANK_T) k_rank_features(const int64_t* __restrict__ feature, int n_nodes, int F,
+                                                          int k, int64_t* __restrict__ out64,
+                                                          int32_t* __restrict__ out32, int32_t* __restrict__ out_m) {
+    __shared__ uint32_t s_cnt[RANK_MAX_F];
+    __shared__ RankEl s_el[RANK_MAX_F];
+    __shared__ int s_stk[3 * 64];
+    __shared__ int s_m, s_bad;
+    for (int f = threadIdx.x; f < F; f += RANK_T) s_cnt[f] = 0u;
+    if (threadIdx.x == 0) s_bad = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < n_nodes; i += RANK_T) {
+        const int64_t f = feature[i];
+        if (f >= F) s_bad = 1;
+        else if (f >= 0) atomicAdd(&s_cnt[f], 1u);
+    }
+    __syncthreads();
+    if (threadIdx.x < WAVE) {
+        const int lane = threadIdx.x;
+        int m = 0;
+        for (int f0 = 0; f0 < F; f0 += WAVE) {
+            const int f = f0 + lane;
+            const uint32_t c = f < F ? s_cnt[f] : 0u;
+            const uint64_t bal = __ballot(c > 0u);
+            if (c > 0u) {
+                const int pos = m + (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                                   __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+                s_el[pos].c = (int32_t)c;
+                s_el[pos].f = f;
+            }
+            m += __popcll(bal);
+        }
+        if (lane == 0) {
+            s_m = m;
+            rank::sort(s_el, m, k, s_stk);
+        }
+    }
+    __syncthreads();
+    const int m = s_m;
+    if ((int)threadIdx.x < k) {
+        const int f = (int)threadIdx.x < m ? s_el[threadIdx.x].f : 0;
+        out64[threadIdx.x] = f;
+        out32[threadIdx.x] = f;
+    }
+    if (threadIdx.x == 0) out_m[0] = s_bad ? -1 : m;
+}
+
 }  // namespace yabt
 
 using namespace yabt;
@@ -1146,6 +1358,16 @@ int yabt_leaf_fold(int n_nodes, int K, const float* W, const float* b, const flo
     k_leaf_fold<<<(n_nodes + LB - 1) / LB, LB, 0, stream>>>(n_nodes, K, W, b, mu, sd, lr, value_in, out_value,
                                                            out_linear);
     return launch_status("yabt_leaf_fold launch");
+}
+
+int yabt_leaf_rank_features(const int64_t* feature, int n_nodes, int F, int k, int64_t* out_feats,
+                            int32_t* out_feats32, int32_t* out_m, hipStream_t stream) {
+    if (n_nodes < 1 || F < 1 || F > RANK_MAX_F || k < 1 || k > LKMAX)
+        return fail(-2, "yabt_leaf_rank_features: bad sizes (n_nodes >= 1, 1 <= F <= 4096, 1 <= k <= 8)");
+    if (!feature || !out_feats || !out_feats32 || !out_m)
+        return fail(-2, "yabt_leaf_rank_features: null pointer argument");
+    k_rank_features<<<1, RANK_T, 0, stream>>>(feature, n_nodes, F, k, out_feats, out_feats32, out_m);
+    return launch_status("yabt_leaf_rank_features launch");
 }
 
 size_t yabt_leaf_moments_workspace_bytes(int64_t n) {

@@ -6,10 +6,11 @@ model over up to ``leaf_net_features`` inputs, fitted to the Newton objective
 at ``margin + value[leaf]``, folded into raw space and shrunk by the learning
 rate, with per-leaf input envelopes.  The per-leaf Gram matrices, envelopes,
 counts, solves and the input moments run in the HIP kernels of
-``csrc/leaf.hip`` (``yabt_leaf_moments``, ``yabt_leaf_fit``), the targets g, h
-at margin + value[leaf] in ``yabt_grad_hess`` (``csrc/boost.hip``); feature
-selection and the fold are the reference's own torch expressions on the
-device.  Only the linear form
+``csrc/leaf.hip`` (``yabt_leaf_moments``, ``yabt_leaf_fit``, ``yabt_leaf_fold``,
+and for binned inputs the split-feature ranking, ``yabt_leaf_rank_features``),
+the targets g, h at margin + value[leaf] in ``yabt_grad_hess``
+(``csrc/boost.hip``); the padding of the features by correlation is the
+reference's own torch expressions.  Only the linear form
 (``leaf_net_hidden == 0``) is provided.
 """
 
@@ -57,6 +58,8 @@ def _select_features(tree: Tree, Xraw: torch.Tensor, grad: torch.Tensor, k: int)
 # Gram sums of yabt_leaf_fit: "exact" (the fp64 products rounded to int64
 # fixed point and summed exactly) or "mfma" (fp64 sums on the matrix cores).
 GRAM_MODES = {"exact": 0, "mfma": 1}
+# features up to which yabt_leaf_rank_features ranks the split features on the device
+RANK_MAX_FEATURES = 4096
 GRAM = "exact"
 
 
@@ -170,21 +173,24 @@ def fold(tree: Tree, W, db, mu, sd, lr, feats, lo, hi) -> Tree:
                    leaf_net_hi=hi)
 
 
-def _leaf_step(tree: Tree, X: torch.Tensor, x_kind: int, n: int, feats: torch.Tensor, grad: torch.Tensor,
-               hess: torch.Tensor, leaf_idx: torch.Tensor, params) -> Tree:
+def _leaf_step(tree: Tree, X: torch.Tensor, x_kind: int, n: int, feats: torch.Tensor | None, grad: torch.Tensor,
+               hess: torch.Tensor, leaf_idx: torch.Tensor, params, rank_k: int = 0) -> Tree | None:
     """Moments, fit and fold of one tree's leaf models: every tensor and
-    workspace is prepared first, then the three launches go out back to back
-    (the device runs them without waiting on the host), then the one wait for
-    the status.  tree's node arrays are on X's device."""
+    workspace is prepared first, then the launches go out back to back (the
+    device runs them without waiting on the host), then the one wait for the
+    status.  tree's node arrays are on X's device.  With rank_k > 0 (feats
+    None) the split features are ranked on the device first and the fit
+    takes the first rank_k; None if the tree uses fewer than rank_k features
+    (the caller then pads them on the host)."""
     lib = _lib.load()
     dev = X.device
-    K, N = int(feats.numel()), int(tree.feature.shape[0])
+    K, N = (rank_k if rank_k else int(feats.numel())), int(tree.feature.shape[0])
     mode = GRAM_MODES[GRAM]
     if x_kind == 0 and (X.dtype != torch.float32 or X.dim() != 2 or X.shape[0] != n or X.stride(1) != 1):
         raise ValueError("X must be fp32 (n, F) with unit column stride")
     if x_kind == 1 and (X.dtype != torch.uint8 or X.dim() != 2 or X.shape[1] < n or X.stride(1) != 1):
         raise ValueError("X must be uint8 (F, ld >= n)")
-    fi = feats.to(dev, torch.int32).contiguous()
+    fi = None if rank_k else feats.to(dev, torch.int32).contiguous()
     g = grad.to(dev, torch.float32).contiguous()
     h = hess.to(dev, torch.float32).contiguous()
     li = leaf_idx.to(dev, torch.int64).contiguous()
@@ -206,14 +212,18 @@ def _leaf_step(tree: Tree, X: torch.Tensor, x_kind: int, n: int, feats: torch.Te
             out.append(base[o:o + v])
             o += u
         return out
-    mws, fws, p_mu, p_sd, p_W, p_b, p_cnt, p_st = carve([max(mbytes, 1), fbytes, 4 * K, 4 * K, 4 * N * K, 4 * N,
-                                                          8 * N, 8])
-    p_lo, p_hi, p_value, p_linear = carve([4 * N * K, 4 * N * K, 4 * N, 4 * N * K])
+    mws, fws, p_mu, p_sd, p_W, p_b, p_cnt, p_st, p_fi = carve([max(mbytes, 1), fbytes, 4 * K, 4 * K, 4 * N * K,
+                                                                4 * N, 8 * N, 12, 4 * K])
+    p_lo, p_hi, p_value, p_linear, p_feats = carve([4 * N * K, 4 * N * K, 4 * N, 4 * N * K, 8 * K])
     mu, sd, b, value = (p.view(torch.float32) for p in (p_mu, p_sd, p_b, p_value))
     W, lo, hi, linear = (p.view(torch.float32).view(N, K) for p in (p_W, p_lo, p_hi, p_linear))
     cnt = p_cnt.view(torch.int64)
     status = p_st.view(torch.int32)
     ldx, st = X.stride(0), _stream(dev)
+    if rank_k:
+        feats, fi = p_feats.view(torch.int64), p_fi.view(torch.int32)
+        _lib.check(lib.yabt_leaf_rank_features(ft.data_ptr(), N, int(X.shape[0]), K, feats.data_ptr(),
+                                               fi.data_ptr(), status[2:].data_ptr(), st), "yabt_leaf_rank_features")
     _lib.check(lib.yabt_leaf_moments(x_kind, X.data_ptr(), ldx, n, fi.data_ptr(), K, mws.data_ptr(), mbytes,
                                      mu.data_ptr(), sd.data_ptr(), st), "yabt_leaf_moments")
     _lib.check(lib.yabt_leaf_fit(x_kind, X.data_ptr(), ldx, n, fi.data_ptr(), K, mu.data_ptr(), sd.data_ptr(),
@@ -225,7 +235,9 @@ def _leaf_step(tree: Tree, X: torch.Tensor, x_kind: int, n: int, feats: torch.Te
     _lib.check(lib.yabt_leaf_fold(N, K, W.data_ptr(), b.data_ptr(), mu.data_ptr(), sd.data_ptr(),
                                   float(params.learning_rate), value_in.data_ptr(), value.data_ptr(),
                                   linear.data_ptr(), st), "yabt_leaf_fold")
-    st_, n_fit = status.tolist()   # the one wait for the device
+    st_, n_fit, n_used = status.tolist()   # the one wait for the device
+    if rank_k and n_used < K:
+        return None
     _check_status(st_)
     # no eligible leaf: the tree is returned unchanged (neural_leaves.py:156-158)
     if n_fit == 0:
@@ -265,6 +277,11 @@ def fit_leaf_networks_binned(tree: Tree, bins_fm: torch.Tensor, grad: torch.Tens
     n = int(grad.shape[0]) if n is None else n
     feature = tree.feature.to(dev)
     k = min(getattr(params, "leaf_net_features", 8), bins_fm.shape[0])
+    if 1 <= k <= 8 and bins_fm.shape[0] <= RANK_MAX_FEATURES:
+        tree_d = replace(tree, feature=feature, value=tree.value.to(dev))
+        out = _fit_binned_ranked(tree_d, bins_fm, grad, hess, leaf_idx, params, n, k)
+        if out is not None:
+            return tree if out is tree_d else out
     feats = _used_features(feature, k).to(dev)
     if feats.numel() == 0:
         return tree
@@ -275,3 +292,11 @@ def fit_leaf_networks_binned(tree: Tree, bins_fm: torch.Tensor, grad: torch.Tens
     tree_d = replace(tree, feature=feature, value=tree.value.to(dev))
     out = _leaf_step(tree_d, bins_fm, 1, n, feats, grad, hess, leaf_idx, params)
     return tree if out is tree_d else out
+
+
+def _fit_binned_ranked(tree_d: Tree, bins_fm: torch.Tensor, grad: torch.Tensor, hess: torch.Tensor,
+                       leaf_idx: torch.Tensor, params, n: int, k: int) -> Tree | None:
+    """The binned fit with the split features ranked on the device: the
+    host never waits for the tree before the launches.  None when the tree
+    uses fewer than k features (or names one outside the bins)."""
+    return _leaf_step(tree_d, bins_fm, 1, n, None, grad, hess, leaf_idx, params, rank_k=k)
