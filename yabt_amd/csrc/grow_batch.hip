@@ -56,13 +56,13 @@ constexpr int SB = 256;                          // threads of the partition / s
 constexpr int PART_IPT_WIDE = 16;                // rows per thread per partition tile: rounds
 constexpr int PART_IPT_NARROW = 8;               //   of more / fewer than PART_WIDE_ROWS rows
 constexpr int64_t PART_WIDE_ROWS = 1 << 20;
-constexpr int PART_BLOCKS = 1024;
+constexpr int PART_BLOCKS = 2048;
 constexpr int SCAN_FEATS = 4;                    // features per scan block
 constexpr int KMAX = 16;                         // splits computed per round, at most
 constexpr int GBLOCKS = 256;                     // gather blocks of a launch, about (multiple of XCDS)
 constexpr int XCDS = 8;                          // dies of the device; blocks go to them in turn
 constexpr int CT = 2 * SCAN_FEATS * WAVE;        // threads of a split-scan block (the controller)
-constexpr int LOOKAHEAD = 3;                     // rounds the host keeps in flight
+constexpr int LOOKAHEAD = 2;                     // rounds the host keeps in flight
 constexpr int MAX_LEAVES = 1024;                 // leaf table held in the controller's LDS
 constexpr int TABLE_REGS = 4;                    // leaf-table entries per lane when the replay holds it in registers
 constexpr int PEND_PER_LEAF = 3;                 // computed splits per leaf of the budget, at most
