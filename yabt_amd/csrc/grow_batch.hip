@@ -1079,24 +1079,33 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
     constexpr int NC = ROOT ? 1 : 2;
     State* st = A.st;
     const Quant* q = A.q;
-    const int32_t done = st->done, nr = ROOT ? 1 : st->n_round;
     const int y = ROOT ? 0 : blockIdx.y;
-    if (done || y >= nr) return;
+    // the words of State this block needs, loaded before the exit test (y <
+    // KMAX indexes them all): the split's Pend index and its gather pieces'
+    // range do not wait for the test
+    const int32_t done = st->done, nr = ROOT ? 1 : st->n_round;
+    const int pidx = ROOT ? 0 : st->round_pend[y];
+    const int u0 = ROOT ? 0 : st->unit_off[y], u1 = ROOT ? 0 : st->unit_off[y + 1];
+    // one test over all of them (none is negative in a live round), so that
+    // they are loaded together rather than after the branch
+    if ((done != 0) | (y >= nr) | ((pidx | u0 | u1) < 0)) return;
     // the start of the controller's table, loaded by every block together
     // with its bins (whichever block finishes last is the controller and
     // holds it in registers by then): leaf t and computed split t (a
     // controller loads the entries past the block size itself)
-    uint32_t pf_leaf = 0;   // origin (low 16 bits) and node id of leaf t
+    // Unconditional loads at clamped indices: a load inside a branch is
+    // waited for inside it, these stay in flight through the scan.
+    int32_t pf_src = 0, pf_node = 0;   // origin and node id of leaf t
     PendSum pf_ps = {};
-    const int np_now = ROOT ? 0 : st->n_pend;
     if (!ROOT) {
-        const int t = threadIdx.x;
-        if (t < st->n_leaves) pf_leaf = (uint32_t)(uint16_t)A.leaf_src[t] | ((uint32_t)A.leaf_node[t] << 16);
-        if (t < np_now) pf_ps = A.psum[t];
+        const int nl_now = st->n_leaves, np_now = st->n_pend;
+        const int tl = min((int)threadIdx.x, max(nl_now - 1, 0)), tp = min((int)threadIdx.x, max(np_now - 1, 0));
+        pf_src = A.leaf_src[tl];
+        pf_node = A.leaf_node[tl];
+        pf_ps = A.psum[tp];
     }
     const bool derive = q->const_h != 0;
     const int64_t hqc = q->hq_const;
-    const int pidx = ROOT ? 0 : st->round_pend[y];
     const Pend* P = ROOT ? nullptr : A.pend + pidx;
     const int bl = ROOT ? 1 : P->build_left;
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
@@ -1125,11 +1134,23 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
     } else {
         // the built child: the sum of its gather pieces, the two waves of a
         // feature adding alternate pieces and exchanging their sums in LDS;
-        // the sibling's wave loads the parent's bins meanwhile
+        // the sibling's wave loads the parent's bins meanwhile.  A wave's
+        // first two pieces go out before the Pend entry is read (their range
+        // needs only State), the parent's bins once it is.
+        const size_t se = slot_elems(A.F);
+        const int r0 = u0 + c;
+        const bool la = fok && r0 < u1, lb = fok && r0 + 2 < u1;
+        int64_t ag[4], ah[4], ac[4], bg[4], bh[4], bc[4];
+        if (la) load_bins(A.pieces + (size_t)r0 * se, A.F, f, lane, ag, ah, ac, has_h);
+        if (lb) load_bins(A.pieces + (size_t)(r0 + 2) * se, A.F, f, lane, bg, bh, bc, has_h);
         if (fok && !built) load_bins(hp, A.F, f, lane, pg, ph, pc, has_h);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) g4[i] = h4[i] = c4[i] = 0;
-        if (fok) add_slots(A.pieces, A.F, f, lane, st->unit_off[y] + c, st->unit_off[y + 1] - 1, 2, g4, h4, c4, has_h);
+        for (int i = 0; i < 4; ++i) {
+            g4[i] = (la ? ag[i] : 0) + (lb ? bg[i] : 0);
+            h4[i] = (la ? ah[i] : 0) + (lb ? bh[i] : 0);
+            c4[i] = (la ? ac[i] : 0) + (lb ? bc[i] : 0);
+        }
+        if (fok) add_slots(A.pieces, A.F, f, lane, r0 + 4, u1 - 1, 2, g4, h4, c4, has_h);
         YABT_LDS int64_t* xs = (YABT_LDS int64_t*)s_table;   // [wave][12][lane]
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -1276,8 +1297,8 @@ __global__ void __launch_bounds__(ROOT ? SCAN_FEATS * WAVE : CT) k_scan(Args A) 
             T.ccommit[p] = (uint8_t)S.committed;
         };
         if (threadIdx.x < na) {
-            T.src[threadIdx.x] = (int16_t)(pf_leaf & 0xffffu);
-            T.node[threadIdx.x] = (int16_t)(pf_leaf >> 16);
+            T.src[threadIdx.x] = (int16_t)pf_src;
+            T.node[threadIdx.x] = (int16_t)pf_node;
         }
         if (threadIdx.x < np) put(threadIdx.x, pf_ps);
         for (int a = threadIdx.x + NT; a < na; a += NT) {
