@@ -53,6 +53,24 @@ def _stream(dev: torch.device):
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 
+# Read-only device tensors every call would otherwise rebuild (the all-ones
+# feature mask, the unused interaction matrix, a layout's bin counts): made
+# once per device and value, complete before first use, never written (the
+# C ABI takes them as const).
+_DEV_CONST: dict = {}
+
+
+def _dev_const(key, make) -> torch.Tensor:
+    t = _DEV_CONST.get(key)
+    if t is None:
+        if len(_DEV_CONST) >= 256:
+            _DEV_CONST.clear()
+        t = make()
+        torch.cuda.current_stream(t.device).synchronize()
+        _DEV_CONST[key] = t
+    return t
+
+
 def _dev_f32(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
     """Contiguous float32 copy on ``dev`` whose data is 16-byte aligned (the
     kernels use 16-byte vector loads)."""
@@ -267,14 +285,15 @@ def grow_device(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor, nbins: 
     h = _dev_f32(hess, dev)
     if g.shape[0] != n or h.shape[0] != n:
         raise ValueError("grad/hess length must equal the number of rows")
-    fm = (torch.ones(F, dtype=torch.uint8, device=dev) if fmask is None
+    fm = (_dev_const((dev, "ones_u8", F), lambda: torch.ones(F, dtype=torch.uint8, device=dev)) if fmask is None
           else torch.as_tensor(fmask).to(dev).bool().to(torch.uint8).contiguous())
     use_imat = imat is not None
     im = (torch.as_tensor(imat).to(dev, torch.float32).contiguous() if use_imat
-          else torch.zeros(1, dtype=torch.float32, device=dev))
+          else _dev_const((dev, "zero_f32"), lambda: torch.zeros(1, dtype=torch.float32, device=dev)))
     if use_imat and tuple(im.shape) != (F, F):
         raise ValueError("interaction_matrix must be (F, F)")
-    nb = torch.from_numpy(np.ascontiguousarray(nbins, dtype=np.int32)).to(dev)
+    nbc = np.ascontiguousarray(nbins, dtype=np.int32)
+    nb = _dev_const((dev, "nbins", nbc.tobytes()), lambda: torch.from_numpy(nbc.copy()).to(dev))
     if isinstance(default_bin, str):
         db = lay.default_bin()
     elif default_bin is None:
@@ -365,14 +384,15 @@ def _grow_device_level(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, l
     h = _dev_f32(hess, dev)
     if g.shape[0] != n or h.shape[0] != n:
         raise ValueError("grad/hess length must equal the number of rows")
-    fm = (torch.ones(F, dtype=torch.uint8, device=dev) if fmask is None
+    fm = (_dev_const((dev, "ones_u8", F), lambda: torch.ones(F, dtype=torch.uint8, device=dev)) if fmask is None
           else torch.as_tensor(fmask).to(dev).bool().to(torch.uint8).contiguous())
     use_imat = imat is not None
     im = (torch.as_tensor(imat).to(dev, torch.float32).contiguous() if use_imat
-          else torch.zeros(1, dtype=torch.float32, device=dev))
+          else _dev_const((dev, "zero_f32"), lambda: torch.zeros(1, dtype=torch.float32, device=dev)))
     if use_imat and tuple(im.shape) != (F, F):
         raise ValueError("interaction_matrix must be (F, F)")
-    nb = torch.from_numpy(np.ascontiguousarray(nbins, dtype=np.int32)).to(dev)
+    nbc = np.ascontiguousarray(nbins, dtype=np.int32)
+    nb = _dev_const((dev, "nbins", nbc.tobytes()), lambda: torch.from_numpy(nbc.copy()).to(dev))
     L = int(max_leaves)
     N = 2 * L + 1
     nbytes = int(lib.yabt_grow_levelwise_workspace_bytes(n, F, L, int(max_depth)))
@@ -416,14 +436,15 @@ def _grow_device_ref(lay: BinLayouts, grad, hess, nbins, *, fmask, imat, ib, lam
     h = _dev_f32(hess, dev)
     if g.shape[0] != n or h.shape[0] != n:
         raise ValueError("grad/hess length must equal the number of rows")
-    fm = (torch.ones(F, dtype=torch.uint8, device=dev) if fmask is None
+    fm = (_dev_const((dev, "ones_u8", F), lambda: torch.ones(F, dtype=torch.uint8, device=dev)) if fmask is None
           else torch.as_tensor(fmask).to(dev).bool().to(torch.uint8).contiguous())
     use_imat = imat is not None
     im = (torch.as_tensor(imat).to(dev, torch.float32).contiguous() if use_imat
-          else torch.zeros(1, dtype=torch.float32, device=dev))
+          else _dev_const((dev, "zero_f32"), lambda: torch.zeros(1, dtype=torch.float32, device=dev)))
     if use_imat and tuple(im.shape) != (F, F):
         raise ValueError("interaction_matrix must be (F, F)")
-    nb = torch.from_numpy(np.ascontiguousarray(nbins, dtype=np.int32)).to(dev)
+    nbc = np.ascontiguousarray(nbins, dtype=np.int32)
+    nb = _dev_const((dev, "nbins", nbc.tobytes()), lambda: torch.from_numpy(nbc.copy()).to(dev))
     db = None
     if default_bin is not None:
         db = torch.as_tensor(default_bin).to(dev, torch.int32).contiguous()
