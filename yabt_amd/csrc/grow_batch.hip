@@ -217,6 +217,10 @@ __global__ void k_setup_finish(Args A) {
     st->root_gain = -INFINITY;
     st->n_nodes = 1;
     st->n_leaves = 1;
+    // every word of the status is written here, so the caller need not clear it
+    A.out_status[0] = 0;
+    A.out_status[1] = 0;
+    A.out_status[2] = 0;
     if (A.q->nonfinite) {
         st->done = 1;
         A.out_status[0] = -1;

@@ -353,7 +353,7 @@ def _grow_device_rounds(lib, lay: BinLayouts, g, h, fm, im, use_imat, nb, db, *,
     out_i = torch.empty((5, N), dtype=torch.int64, device=dev)
     value = torch.empty(N, dtype=torch.float32, device=dev)
     leaf = torch.empty(max(n, 1), dtype=torch.int64, device=dev)
-    status = torch.zeros(3, dtype=torch.int32, device=dev)
+    status = torch.empty(3, dtype=torch.int32, device=dev)   # cleared by the grower's set-up launch
     rc = lib.yabt_grow_batched(
         _ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h), _ptr(fm), _ptr(im),
         ctypes.c_float(float(ib)), int(use_imat), _ptr(nb), _ptr(db), _ptr(lay.counts()), n, F,
