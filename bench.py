@@ -563,8 +563,8 @@ def boosting_fits(torch) -> dict:
 def main() -> None:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=5)
-    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--rows", type=int, default=N_ROWS)
     ap.add_argument("--no-neural", action="store_true", help="time the grower only")
@@ -618,7 +618,7 @@ def main() -> None:
         # node arrays are full length (2L + 1); unused slots are empty leaves
         leaf = G.leaf_ids(res, n, F, MAX_LEAVES)
         tree = Tree(res.feature, res.thr_bin.float(), res.left, res.right, res.value, 0)
-        g2 = g + h * res.value[leaf]
+        g2 = torch.addcmul(g, h, res.value[leaf])   # g + h * value[leaf], one pass
         return res, fit_leaf_networks_binned(tree, lay.fm, g2, h, leaf, LeafNetParams, n=n)
 
     def timed(neural: bool, steps: int) -> float:
