@@ -207,34 +207,38 @@ def _leaf_step(tree: Tree, X: torch.Tensor, x_kind: int, n: int, feats: torch.Te
     def carve(sizes):
         up = [(v + 255) // 256 * 256 for v in sizes]
         base = torch.empty(sum(up), dtype=torch.uint8, device=dev)
-        out, o = [], 0
-        for v, u in zip(sizes, up):
-            out.append(base[o:o + v])
+        offs, o = [], 0
+        for u in up:
+            offs.append(o)
             o += u
-        return out
-    mws, fws, p_mu, p_sd, p_W, p_b, p_cnt, p_st, p_fi = carve([max(mbytes, 1), fbytes, 4 * K, 4 * K, 4 * N * K,
-                                                                4 * N, 8 * N, 12, 4 * K])
-    p_lo, p_hi, p_value, p_linear, p_feats = carve([4 * N * K, 4 * N * K, 4 * N, 4 * N * K, 8 * K])
-    mu, sd, b, value = (p.view(torch.float32) for p in (p_mu, p_sd, p_b, p_value))
-    W, lo, hi, linear = (p.view(torch.float32).view(N, K) for p in (p_W, p_lo, p_hi, p_linear))
-    cnt = p_cnt.view(torch.int64)
-    status = p_st.view(torch.int32)
+        return base, offs
+    # the transient pieces go to the C ABI as addresses (no tensor views:
+    # each view costs host time while the device waits); the status and the
+    # outputs the tree keeps are views
+    tb, to = carve([max(mbytes, 1), fbytes, 4 * K, 4 * K, 4 * N * K, 4 * N, 8 * N, 12, 4 * K])
+    a0 = tb.data_ptr()
+    a_mws, a_fws, a_mu, a_sd, a_W, a_b, a_cnt, _, a_fi = (a0 + o for o in to)
+    status = tb[to[7]:to[7] + 12].view(torch.int32)
+    kb, ko = carve([4 * N * K, 4 * N * K, 4 * N, 4 * N * K, 8 * K])
+    lo, hi, linear = (kb[o:o + 4 * N * K].view(torch.float32).view(N, K) for o in (ko[0], ko[1], ko[3]))
+    value = kb[ko[2]:ko[2] + 4 * N].view(torch.float32)
     ldx, st = X.stride(0), _stream(dev)
     if rank_k:
-        feats, fi = p_feats.view(torch.int64), p_fi.view(torch.int32)
-        _lib.check(lib.yabt_leaf_rank_features(ft.data_ptr(), N, int(X.shape[0]), K, feats.data_ptr(),
-                                               fi.data_ptr(), status[2:].data_ptr(), st), "yabt_leaf_rank_features")
-    _lib.check(lib.yabt_leaf_moments(x_kind, X.data_ptr(), ldx, n, fi.data_ptr(), K, mws.data_ptr(), mbytes,
-                                     mu.data_ptr(), sd.data_ptr(), st), "yabt_leaf_moments")
-    _lib.check(lib.yabt_leaf_fit(x_kind, X.data_ptr(), ldx, n, fi.data_ptr(), K, mu.data_ptr(), sd.data_ptr(),
+        feats = kb[ko[4]:ko[4] + 8 * K].view(torch.int64)
+        _lib.check(lib.yabt_leaf_rank_features(ft.data_ptr(), N, int(X.shape[0]), K, feats.data_ptr(), a_fi,
+                                               status.data_ptr() + 8, st), "yabt_leaf_rank_features")
+    else:
+        a_fi = fi.data_ptr()
+    _lib.check(lib.yabt_leaf_moments(x_kind, X.data_ptr(), ldx, n, a_fi, K, a_mws, mbytes, a_mu, a_sd, st),
+               "yabt_leaf_moments")
+    _lib.check(lib.yabt_leaf_fit(x_kind, X.data_ptr(), ldx, n, a_fi, K, a_mu, a_sd,
                                  g.data_ptr(), h.data_ptr(), li.data_ptr(), ft.data_ptr(), N,
                                  int(getattr(params, "leaf_net_min_samples", 50)),
-                                 float(getattr(params, "leaf_net_l2", 1.0)), mode, fws.data_ptr(), fbytes,
-                                 W.data_ptr(), b.data_ptr(), lo.data_ptr(), hi.data_ptr(), cnt.data_ptr(),
-                                 status.data_ptr(), st), "yabt_leaf_fit")
-    _lib.check(lib.yabt_leaf_fold(N, K, W.data_ptr(), b.data_ptr(), mu.data_ptr(), sd.data_ptr(),
-                                  float(params.learning_rate), value_in.data_ptr(), value.data_ptr(),
-                                  linear.data_ptr(), st), "yabt_leaf_fold")
+                                 float(getattr(params, "leaf_net_l2", 1.0)), mode, a_fws, fbytes,
+                                 a_W, a_b, lo.data_ptr(), hi.data_ptr(), a_cnt, status.data_ptr(), st),
+               "yabt_leaf_fit")
+    _lib.check(lib.yabt_leaf_fold(N, K, a_W, a_b, a_mu, a_sd, float(params.learning_rate), value_in.data_ptr(),
+                                  value.data_ptr(), linear.data_ptr(), st), "yabt_leaf_fold")
     st_, n_fit, n_used = status.tolist()   # the one wait for the device
     if rank_k and n_used < K:
         return None
