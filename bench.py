@@ -135,13 +135,13 @@ def time_root_hist(torch, lay, g, h, reps=50, warm=50):
     dev = lay.fm.device
     lib = _lib.load()
     out = torch.zeros((3, lay.F, 256), dtype=torch.int64, device=dev)
-    _, (sg, sh) = G.hist(lay, g, h)
+    _, (sg, sh, wide) = G.hist(lay, g, h)
     counts = lay.counts()
     stream = torch.cuda.current_stream(dev)
 
     def launch():
         _lib.check(lib.yabt_hist_root(G._ptr(lay.fm), lay.ld_fm, G._ptr(g), G._ptr(h), lay.n, lay.F,
-                                      G._ptr(counts), sg, sh, G._ptr(out), G._stream(dev)),
+                                      G._ptr(counts), sg, sh, wide, G._ptr(out), G._stream(dev)),
                    "yabt_hist_root")
 
     for _ in range(warm):
@@ -198,11 +198,11 @@ def counter_launches(torch, lay, g, h) -> None:
     del x, y
     lib = _lib.load()
     out = torch.zeros((3, lay.F, 256), dtype=torch.int64, device=dev)
-    _, (sg, sh) = G.hist(lay, g, h)
+    _, (sg, sh, wide) = G.hist(lay, g, h)
     counts = lay.counts()
     for _ in range(3):
         _lib.check(lib.yabt_hist_root(G._ptr(lay.fm), lay.ld_fm, G._ptr(g), G._ptr(h), lay.n, lay.F,
-                                      G._ptr(counts), sg, sh, G._ptr(out), G._stream(dev)),
+                                      G._ptr(counts), sg, sh, wide, G._ptr(out), G._stream(dev)),
                    "yabt_hist_root")
     torch.cuda.synchronize()
 

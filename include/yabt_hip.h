@@ -12,12 +12,19 @@
  *   - return 0 on success, < 0 on a rejected argument or launch failure; the
  *     message is available from yabt_last_error() (per calling thread);
  *   - histograms are exact int64 fixed point: the caller's grad/hess are
- *     quantised as q = rint(x * 2^s) with one shift per call,
- *     s = 30 - min(ceil(log2(n)), 11) - e where max|x| < 2^e (s = 0 if
- *     max|x| = 0): q keeps 19 bits of the largest |x| (more for n <= 2048),
- *     every sum over <= n rows is exact, and any 2048 of them sum below
- *     2^31 in magnitude (the streaming root histogram packs q(g) and q(h)
- *     into one 64-bit word per update);
+ *     quantised as q = rint(x * 2^s) with one shift per channel and call,
+ *     under one of two contracts (k = ceil(log2(n)), max|x| < 2^e, s = 0 if
+ *     max|x| = 0):
+ *       narrow: s = 30 - min(k, 11) - e; q keeps 19 bits of the largest |x|
+ *         (more for n <= 2048) and any 2048 values sum below 2^31 in
+ *         magnitude (the streaming root histogram packs q(g) and q(h) into
+ *         one 64-bit word per update);
+ *       wide: s = 61 - max(k, 21) - e; q keeps 37 bits of the largest |x| at
+ *         10M rows (40 at <= 2M rows), g and h a 64-bit word each;
+ *     calls that choose the shifts themselves take narrow only when its
+ *     quantisation residual sum |x - q 2^-s| is at most 2^-17 of sum |x|
+ *     for both g and h (exact integer sums, so the choice is deterministic),
+ *     else wide; every sum over <= n rows is exact either way;
  *   - bin counts: the count plane of a root histogram depends only on the
  *     bins, so callers that keep them for a whole fit (yabt_bin_counts) pass
  *     them as `bin_counts` (F, 256) uint32; NULL makes the call count them
@@ -96,7 +103,8 @@ size_t yabt_hist_workspace_bytes(void);
 
 /* Exact node histogram out[3][F][256] int64 = (sum q(g), sum q(h), count) over
  * the rows rows[0:m] (row-major gather; every id < n), or over all n rows when
- * rows == NULL (feature-major stream).  out_shifts[0..1] (device int32) receive the shifts.
+ * rows == NULL (feature-major stream).  out_shifts[0..2] (device int32) receive
+ * the shifts (sg, sh) and the contract (0 narrow, 1 wide) chosen from grad/hess.
  * Replaces `build_hist` (yabt/_cgrow/grow.c:37-62) and the CUDA `hist_build`
  * K==1 path (yabt/_cuda/hist.cu:101-125, yabt/cuda_hist.py:79-89). */
 int yabt_hist(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int64_t ld_rm,
@@ -104,15 +112,16 @@ int yabt_hist(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm, int
               int64_t m, void *workspace, int64_t *out, int32_t *out_shifts,
               yabt_stream_t stream);
 
-/* yabt_hist with caller-given shifts (sg, sh), adding into `out` without
- * clearing it (rows == NULL: two launches, the bin counts and the streaming
- * root histogram).  workspace: >= yabt_hist_workspace_bytes() when
- * rows != NULL, else unused.
+/* yabt_hist with caller-given shifts (sg, sh) and contract (wide 0: narrow,
+ * the shifts keep |x * 2^s| within the narrow bound; 1: wide, within the wide
+ * bound), adding into `out` without clearing it (rows == NULL: two launches,
+ * the bin counts and the streaming root histogram).  workspace: >=
+ * yabt_hist_workspace_bytes() when rows != NULL, else unused.
  * Replaces `build_hist` (yabt/_cgrow/grow.c:37-62) for callers that manage
  * the quantisation themselves. */
 int yabt_hist_accumulate(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *bins_rm,
                          int64_t ld_rm, const float *grad, const float *hess, int64_t n, int F,
-                         const uint32_t *rows, int64_t m, int sg, int sh, void *workspace,
+                         const uint32_t *rows, int64_t m, int sg, int sh, int wide, void *workspace,
                          int64_t *out, yabt_stream_t stream);
 
 /* Per-fit bin counts: out_counts[f * 256 + b] (uint32, F * 256) = number of
@@ -124,13 +133,14 @@ int yabt_bin_counts(const uint8_t *bins_fm, int64_t ld_fm, int64_t n, int F, uin
                     yabt_stream_t stream);
 
 /* The streaming root histogram alone: adds sum q(g) and sum q(h) over all n
- * rows (shifts sg, sh given) into planes 0 and 1 of out (3, F, 256) int64,
+ * rows (shifts sg, sh and contract `wide` given, as in yabt_hist_accumulate)
+ * into planes 0 and 1 of out (3, F, 256) int64,
  * and bin_counts (may be NULL: plane 2 untouched) into plane 2 -- exactly
  * one kernel launch, which is what a timing harness brackets.  Replaces the
  * root call of `build_hist` (yabt/_cgrow/grow.c:37-62, grow.c:296-300). */
 int yabt_hist_root(const uint8_t *bins_fm, int64_t ld_fm, const float *grad, const float *hess,
-                   int64_t n, int F, const uint32_t *bin_counts, int sg, int sh, int64_t *out,
-                   yabt_stream_t stream);
+                   int64_t n, int F, const uint32_t *bin_counts, int sg, int sh, int wide,
+                   int64_t *out, yabt_stream_t stream);
 
 /* yabt_hist without a workspace argument, for callers that cannot allocate
  * device memory: code under HIP graph capture, tight serving loops,

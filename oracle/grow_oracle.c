@@ -18,7 +18,9 @@
  *
  *   OR_MODE_FIXED  the arithmetic contract of the HIP path: gradients and
  *                  hessians are quantised to int64 fixed point with one
- *                  power-of-two scale per call (or_hist_shift), histograms are
+ *                  power-of-two scale per channel and call (or_hist_contract:
+ *                  the narrow or_hist_shift when its residual is small, else
+ *                  the wide or_wide_shift), histograms are
  *                  exact integer sums (order-free, so sibling subtraction and
  *                  the default-bin fill are exact), the partition is stable, and
  *                  the split scan evaluates the reference's double-precision
@@ -73,9 +75,40 @@ int or_hist_shift(float maxabs, int64_t n)
     return 30 - k - e;
 }
 
+/* The wide contract's shift: s = 61 - max(k, 21) - e, so every partial sum
+ * of n quantised values stays below 2^61 (+ rounding). */
+int or_wide_shift(float maxabs, int64_t n)
+{
+    if (!(maxabs > 0.0f)) return 0;
+    int e = 0;
+    (void)frexpf(maxabs, &e);
+    int k = 0;
+    while (k < 62 && ((int64_t)1 << k) < n) ++k;
+    if (k < 21) k = 21;
+    return 61 - k - e;
+}
+
 static inline int64_t quantise(float x, double scale)
 {
     return (int64_t)rint((double)x * scale);
+}
+
+/* Residual and mass of one channel at the narrow shift s (the contract of
+ * the exact grower, yabt_amd/csrc/common.h hist_shift / quant_resid):
+ * R = sum rint(|y - rint(y)| * 2^21) and M = sum rint(|x| * 2^(s+10)) with
+ * y = x * 2^s, every step exact in fp32 (power-of-two scalings and the
+ * distance of y to its nearest integer), so R and M are exact integers. */
+static void resid_mass(const float *x, int64_t n, int s, uint64_t *r, uint64_t *m)
+{
+    uint64_t rr = 0, mm = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        const float y = ldexpf(x[i], s);
+        const float d = y - rintf(y);
+        rr += (uint64_t)rintf(ldexpf(fabsf(d), 21));
+        mm += (uint64_t)rintf(ldexpf(fabsf(x[i]), s + 10));
+    }
+    *r = rr;
+    *m = mm;
 }
 
 /* max |x| over n values; returns -1 if any value is not finite. */
@@ -91,12 +124,37 @@ static int max_abs(const float *x, int64_t n, float *out)
     return 0;
 }
 
-int or_quant_shifts(const float *grad, const float *hess, int64_t n, int *sg, int *sh)
+/* The per-call contract: the narrow shifts (or_hist_shift) when their
+ * quantisation residual is at most 2^-17 of the mass for both channels
+ * (64 R <= M), else the wide shifts (or_wide_shift).  out: sg, sh, wide;
+ * sums (may be NULL): R_g, R_h, M_g, M_h.  Returns -1 on a non-finite value. */
+int or_hist_contract(const float *grad, const float *hess, int64_t n, int *out, uint64_t *sums)
 {
     float mg = 0.0f, mh = 0.0f;
     if (max_abs(grad, n, &mg) || max_abs(hess, n, &mh)) return -1;
-    *sg = or_hist_shift(mg, n);
-    *sh = or_hist_shift(mh, n);
+    const int sgn = or_hist_shift(mg, n), shn = or_hist_shift(mh, n);
+    uint64_t rg, rh, mmg, mmh;
+    resid_mass(grad, n, sgn, &rg, &mmg);
+    resid_mass(hess, n, shn, &rh, &mmh);
+    const int narrow = 64 * rg <= mmg && 64 * rh <= mmh;
+    out[0] = narrow ? sgn : or_wide_shift(mg, n);
+    out[1] = narrow ? shn : or_wide_shift(mh, n);
+    out[2] = !narrow;
+    if (sums) {
+        sums[0] = rg;
+        sums[1] = rh;
+        sums[2] = mmg;
+        sums[3] = mmh;
+    }
+    return 0;
+}
+
+int or_quant_shifts(const float *grad, const float *hess, int64_t n, int *sg, int *sh)
+{
+    int c[3];
+    if (or_hist_contract(grad, hess, n, c, NULL)) return -1;
+    *sg = c[0];
+    *sh = c[1];
     return 0;
 }
 

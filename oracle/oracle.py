@@ -59,6 +59,10 @@ def lib():
         L.or_hist_shift.argtypes = [_flt, _i64]
         L.or_quant_shifts.restype = _int
         L.or_quant_shifts.argtypes = [_vp, _vp, _i64, _vp, _vp]
+        L.or_wide_shift.restype = _int
+        L.or_wide_shift.argtypes = [_flt, _i64]
+        L.or_hist_contract.restype = _int
+        L.or_hist_contract.argtypes = [_vp, _vp, _i64, _vp, _vp]
         L.or_hist_f32.restype = None
         L.or_hist_f32.argtypes = [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _vp]
         L.or_hist_sparse_f32.restype = None
@@ -194,6 +198,24 @@ def quant_shift(maxabs: float, n: int) -> int:
 def hist_shift(maxabs: float, n: int) -> int:
     """The node histograms' shift (30 - min(k, 11) - e), or_hist_shift."""
     return int(lib().or_hist_shift(_flt(float(maxabs)), _i64(int(n))))
+
+
+def wide_shift(maxabs: float, n: int) -> int:
+    """The wide contract's shift (61 - max(k, 21) - e), or_wide_shift."""
+    return int(lib().or_wide_shift(_flt(float(maxabs)), _i64(int(n))))
+
+
+def hist_contract(grad, hess) -> tuple[int, int, int, tuple[int, int, int, int]]:
+    """(sg, sh, wide, (R_g, R_h, M_g, M_h)) of or_hist_contract: the shifts the
+    exact grower uses for this g/h, whether they are the wide contract's, and
+    the narrow shifts' quantisation residuals and masses that decided it."""
+    g = np.ascontiguousarray(grad, np.float32)
+    h = np.ascontiguousarray(hess, np.float32)
+    out = np.zeros(3, np.int32)
+    sums = np.zeros(4, np.uint64)
+    if lib().or_hist_contract(_ptr(g), _ptr(h), _i64(g.shape[0]), _ptr(out), _ptr(sums)):
+        raise ValueError("non-finite gradient or hessian")
+    return int(out[0]), int(out[1]), int(out[2]), tuple(int(v) for v in sums)
 
 
 def quant_shifts(grad, hess) -> tuple[int, int]:

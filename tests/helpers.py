@@ -28,9 +28,34 @@ def grad_hess(rng, n, kind="normal"):
         p = np.full(n, 0.5, np.float32)
         g = (p - y).astype(np.float32)
         h = np.maximum(p * (1 - p), 1e-6).astype(np.float32)
+    elif kind.startswith("outlier"):
+        # N(0,1) gradients with one large value: "outlier" 50, "outlier1e3", "outlier1e5"
+        g = rng.normal(size=n).astype(np.float32)
+        g[n // 3] = float(kind[len("outlier"):] or 50)
+        h = rng.uniform(0.1, 1.0, size=n).astype(np.float32)
+    elif kind.split("_")[0] in ("lognormal2", "lognormal3", "studentt", "cauchy"):
+        # squared-loss gradients g = m - y at the mean (the base score) of a
+        # heavy-tailed target (boosting.py:49-54), h = 1, or U(0.1, 1) with "_h"
+        base = kind.split("_")[0]
+        if base.startswith("lognormal"):
+            y = rng.lognormal(0.0, float(base[-1]), size=n)
+        elif base == "studentt":
+            y = rng.standard_t(1.5, size=n)
+        else:
+            y = rng.standard_cauchy(size=n)
+        y = y.astype(np.float32)
+        g = (np.float32(y.astype(np.float64).mean()) - y).astype(np.float32)
+        h = (rng.uniform(0.1, 1.0, size=n).astype(np.float32) if kind.endswith("_h")
+             else np.ones(n, np.float32))
     else:
         raise ValueError(kind)
     return g, h
+
+
+# Input kinds whose quantisation residual at the narrow shift selects the
+# wide contract (tests check that the oracle agrees).
+WIDE_KINDS = ("outlier", "outlier1e3", "outlier1e5", "lognormal2", "lognormal3", "studentt", "cauchy",
+              "lognormal3_h", "studentt_h", "cauchy_h")
 
 
 def normwise_rel(a, b):

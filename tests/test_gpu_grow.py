@@ -5,7 +5,12 @@
 * against the reference arithmetic (oracle fp32 mode, itself pinned to the
   compiled reference grow.c by tests/golden): identical feature sequence and
   leaf membership; thr_bin equal or differing only across bins that are empty
-  in that node; leaf values within 1e-5.
+  in that node; leaf values within 1e-5;
+* with outliers and heavy-tailed squared-loss gradients, which select the wide
+  contract: the same against the reference, its leaf values within
+  1e-5 max(1, |ref|) of the reference's beyond the reference's own distance
+  from the values of the exact (fp64) sums, and within 1e-6 max(1, |v|) of
+  those.
 """
 
 import numpy as np
@@ -13,7 +18,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import empty_between, grad_hess, skewed_bins, tree_arrays_equal, uniform_bins
+from tests.helpers import WIDE_KINDS, empty_between, grad_hess, skewed_bins, tree_arrays_equal, uniform_bins
 from yabt_amd import IdentityBinner, TreeParams, grow_tree_hip
 from yabt_amd import grow_hip as G
 
@@ -120,3 +125,57 @@ def test_grow_rejects_nonfinite(growth):
     g[7] = np.nan
     with pytest.raises(ValueError):
         _grow_gpu(bins, g, h, np.full(F, 256, np.int32), max_leaves=4, growth=growth)
+
+
+WIDE_TREES = [dict(n=200_000, F=10, kind=k, max_leaves=31) for k in
+              ("outlier1e3", "outlier1e5", "lognormal2", "lognormal3", "studentt", "cauchy", "studentt_h",
+               "cauchy_h")]
+WIDE_TREES += [dict(n=50_000, F=24, kind="lognormal3_h", max_leaves=255),
+               dict(n=600_000, F=20, kind="cauchy", max_leaves=64, max_depth=6)]
+
+
+@pytest.mark.parametrize("growth", ["sequential", "rounds"])
+@pytest.mark.parametrize("case", WIDE_TREES, ids=lambda c: f"{c['kind']}-n{c['n']}L{c['max_leaves']}")
+def test_grow_wide_contract_vs_reference(case, growth):
+    """Outliers and heavy-tailed squared-loss targets (boosting.py:52-54: g is
+    unbounded) would make the narrow 19-bit quantum coarse against most rows;
+    the per-call residual test selects the wide contract, and the tree is
+    the fixed-point oracle's bit for bit and the reference's: same features,
+    same leaf membership, thresholds equal or across empty bins, and leaf
+    values that the reference's own fp32 rounding alone separates."""
+    print(f"wide case {case} growth {growth}", flush=True)
+    c = dict(case)
+    n, F, kind = c.pop("n"), c.pop("F"), c.pop("kind")
+    rng = np.random.default_rng(n + F + len(kind))
+    bins = uniform_bins(rng, n, F)
+    g, h = grad_hess(rng, n, kind)
+    assert O.hist_contract(g, h)[2] == 1 and kind in WIDE_KINDS
+    kw = dict(max_leaves=c.pop("max_leaves"), max_depth=c.pop("max_depth", 64), msl=20, lam=1.0, gamma=0.0,
+              mcw=1e-3, lr=0.1)
+    assert not c
+    nbins = np.full(F, 256, np.int32)
+    got, leaf = _grow_gpu(bins, g, h, nbins, default_bin="auto", growth=growth, **kw)
+    ref = O.grow(bins.T, g, h, mode=O.MODE_FIXED, nbins=nbins, **kw)
+    bad = tree_arrays_equal(got, ref)
+    assert bad is None, f"{bad} differs from the fixed-point oracle"
+    assert np.array_equal(leaf, O.leaf_of_rows(ref, n))
+
+    r32 = O.grow(bins.T, g, h, mode=O.MODE_FP32, nbins=nbins, **kw)
+    assert np.array_equal(got["feature"], r32["feature"])
+    assert np.array_equal(leaf, O.leaf_of_rows(r32, n))
+    for nid in np.nonzero(got["feature"] >= 0)[0]:
+        if got["thr_bin"][nid] != r32["thr_bin"][nid]:
+            rows = ref["rows"][ref["seg_lo"][nid]:ref["seg_hi"][nid]]
+            counts = np.bincount(bins[rows, got["feature"][nid]], minlength=256)
+            assert empty_between(counts, got["thr_bin"][nid], r32["thr_bin"][nid])
+    # leaf values: the exact values of each leaf's rows (fp64 sums), the
+    # reference's distance from them, and ours
+    leaves = np.nonzero(got["feature"] == -1)[0]
+    G64 = np.bincount(leaf, weights=g.astype(np.float64), minlength=len(got["feature"]))
+    H64 = np.bincount(leaf, weights=h.astype(np.float64), minlength=len(got["feature"]))
+    truth = (-np.float64(np.float32(0.1)) * G64 / (H64 + 1.0))[leaves]
+    ours = got["value"][leaves].astype(np.float64)
+    theirs = r32["value"][leaves].astype(np.float64)
+    scale_t = np.maximum(1.0, np.abs(truth))
+    assert (np.abs(ours - truth) <= 1e-6 * scale_t).all()
+    assert (np.abs(ours - theirs) <= 1e-5 * np.maximum(1.0, np.abs(theirs)) + np.abs(theirs - truth)).all()

@@ -1,8 +1,9 @@
 """Per-stage parity of the HIP kernels against the CPU oracle, through the C ABI.
 
-Histograms: bit-exact against the oracle's fixed-point histogram (same shifts),
-counts bit-exact against the reference-order fp32 histogram, g/h sums within
-1e-5 normwise of it.  Split scan: identical (gain bits, feature, bin) to the
+Histograms: bit-exact against the oracle's fixed-point histogram (same shifts
+and contract), counts bit-exact against the reference-order fp32 histogram,
+g/h sums within 1e-5 normwise of it, and within 1e-9 normwise of fp64 sums
+under the wide contract.  Split scan: identical (gain bits, feature, bin) to the
 oracle's fixed-point scan.  Partition: identical row order to the oracle's
 stable partition and the same membership as the reference two-pointer one.
 """
@@ -12,7 +13,7 @@ import pytest
 import torch
 
 from oracle import oracle as O
-from tests.helpers import grad_hess, normwise_rel, skewed_bins, uniform_bins
+from tests.helpers import WIDE_KINDS, grad_hess, normwise_rel, skewed_bins, uniform_bins
 from yabt_amd import grow_hip as G
 
 pytestmark = pytest.mark.gpu
@@ -41,15 +42,23 @@ def _hist_f64(bins, g, h):
     (300_001, 20, "normal", False), (600_000, 7, "laplace", True), (1_048_577, 3, "logistic", False),
     # tail tiles (F % 16 in 1..4: the last tile's features replicated over its columns), odd and even n
     (2, 1, "normal", False), (3, 2, "normal", False), (2_500_001, 36, "normal", True), (777_777, 50, "laplace", False),
+    # the wide contract: two 64-bit cells per update (h varies) or one (h = 1),
+    # full and tail tiles, skewed bins
+    (3, 2, "cauchy_h", False), (65_536, 100, "outlier1e5", False), (300_001, 20, "cauchy_h", False),
+    (777_777, 50, "studentt_h", False), (1_048_577, 3, "outlier1e3", False), (2_500_001, 36, "lognormal3", True),
+    (400_000, 17, "cauchy", False),
 ])
 def test_root_hist_exact(n, F, kind, skew):
+    print(f"root n={n} F={F} kind={kind} skew={skew}", flush=True)
     rng = np.random.default_rng(n + F)
     bins = skewed_bins(rng, n, F) if skew else uniform_bins(rng, n, F)
     g, h = grad_hess(rng, n, kind)
     lay = _layouts(bins)
-    got, (sg, sh) = G.hist(lay, torch.from_numpy(g), torch.from_numpy(h))
+    got, (sg, sh, wide) = G.hist(lay, torch.from_numpy(g), torch.from_numpy(h))
     got = got.cpu().numpy()
-    assert (sg, sh) == O.quant_shifts(g, h)
+    assert (sg, sh, wide) == O.hist_contract(g, h)[:3]
+    if kind in WIDE_KINDS and n > 3 or kind in ("normal", "logistic"):   # laplace sits near the threshold
+        assert wide == int(kind in WIDE_KINDS and n > 3)
     ref = O.hist_fixed(bins.T, g, h, sg, sh)
     assert np.array_equal(got, ref)
     f32 = O.hist_f32(bins.T, g, h)
@@ -61,23 +70,33 @@ def test_root_hist_exact(n, F, kind, skew):
     for c, s in ((0, sg), (1, sh)):
         slack = got[2] * 2.0 ** (-s - 1) + 1e-12 * np.abs(f64[c]).max()
         assert (np.abs(got[c] * 2.0 ** -s - f64[c]) <= slack).all()
-    if n <= 100_000:  # beyond that the reference's row-order fp32 sums drift past 1e-5 themselves
+        if wide:  # 37-40 bits of the largest |x|: the fp64 sums, normwise
+            assert normwise_rel(got[c] * 2.0 ** -s, f64[c]) < 1e-9
+    if n <= 100_000 and not wide:  # the reference's fp32 sums drift past 1e-5 on their own beyond that,
+        # and with an outlier or heavy tails (fp32 adds at the outlier's ulp)
         assert normwise_rel(got[0] * 2.0 ** -sg, f32[0]) < 1e-5
         assert normwise_rel(got[1] * 2.0 ** -sh, f32[1]) < 1e-5
 
 
-@pytest.mark.parametrize("n,F,m", [(5000, 16, 1), (5000, 16, 777), (40_000, 21, 19_999),
-                                   (40_000, 100, 40_000), (10, 3, 0),
-                                   # n > 2^18: packed words, pipelined gather
-                                   (300_000, 20, 5), (300_000, 17, 150_001), (600_000, 9, 600_000)])
-def test_gather_hist_exact(n, F, m):
+@pytest.mark.parametrize("n,F,m,kind", [(5000, 16, 1, "normal"), (5000, 16, 777, "normal"), (40_000, 21, 19_999, "normal"),
+                                        (40_000, 100, 40_000, "normal"), (10, 3, 0, "normal"),
+                                        # n > 2^18: packed words, pipelined gather
+                                        (300_000, 20, 5, "normal"), (300_000, 17, 150_001, "normal"),
+                                        (600_000, 9, 600_000, "normal"),
+                                        # the wide contract: windows of 2^10 .. 2^11 rows
+                                        (5000, 16, 777, "lognormal3"), (300_000, 17, 150_001, "cauchy_h"),
+                                        (600_000, 9, 600_000, "outlier1e5"), (3_000_000, 5, 2_500_000, "studentt_h")])
+def test_gather_hist_exact(n, F, m, kind):
+    print(f"gather n={n} F={F} m={m} kind={kind}", flush=True)
     rng = np.random.default_rng(m + 7)
     bins = uniform_bins(rng, n, F)
-    g, h = grad_hess(rng, n)
+    g, h = grad_hess(rng, n, kind)
     rows = np.sort(rng.choice(n, size=m, replace=False)).astype(np.int64)
     lay = _layouts(bins)
-    got, (sg, sh) = G.hist(lay, torch.from_numpy(g), torch.from_numpy(h),
-                           torch.from_numpy(rows.astype(np.int32)))
+    got, (sg, sh, wide) = G.hist(lay, torch.from_numpy(g), torch.from_numpy(h),
+                                 torch.from_numpy(rows.astype(np.int32)))
+    assert (sg, sh, wide) == O.hist_contract(g, h)[:3]
+    assert wide == int(kind in WIDE_KINDS)
     ref = O.hist_fixed(bins.T, g, h, sg, sh, rows=rows)
     assert np.array_equal(got.cpu().numpy(), ref)
 
@@ -88,7 +107,7 @@ def test_hist_large_count_exact():
     bins = np.zeros((n, 2), np.uint8)
     g = np.ones(n, np.float32)
     h = np.full(n, 0.5, np.float32)
-    got, (sg, sh) = G.hist(_layouts(bins), torch.from_numpy(g), torch.from_numpy(h))
+    got, (sg, sh, _) = G.hist(_layouts(bins), torch.from_numpy(g), torch.from_numpy(h))
     got = got.cpu().numpy()
     assert got[2, 0, 0] == n
     assert got[0, 0, 0] * 2.0 ** -sg == n
@@ -104,7 +123,7 @@ def test_hist_packed_window_extreme(n):
     bins = np.zeros((n, 1), np.uint8)
     g = np.full(n, -1.9999999, np.float32)
     h = np.full(n, 1.9999999, np.float32)
-    got, (sg, sh) = G.hist(_layouts(bins), torch.from_numpy(g), torch.from_numpy(h))
+    got, (sg, sh, _) = G.hist(_layouts(bins), torch.from_numpy(g), torch.from_numpy(h))
     got = got.cpu().numpy()
     qg = int(np.rint(np.float64(g[0]) * 2.0 ** sg))
     qh = int(np.rint(np.float64(h[0]) * 2.0 ** sh))
@@ -113,6 +132,32 @@ def test_hist_packed_window_extreme(n):
     assert int(got[0, 0, 0]) == n * qg
     assert int(got[1, 0, 0]) == n * qh
     assert (got[:, 0, 1:] == 0).all()
+
+
+@pytest.mark.parametrize("n", [(1 << 21) + 5, (1 << 22) + 3])
+def test_hist_wide_window_extreme(n):
+    """The wide contract's packed gather word at its bound: every h equal to
+    the largest value below 2^e (|q(h)| within 2^-23 of 2^(61 - K)), all rows in
+    one bin, so each window of 2^(K // 2) rows adds 2^(61 - K + K // 2) << cb
+    into one cell; g (N(0,1) with one 1e5 outlier) selects the wide contract."""
+    rng = np.random.default_rng(n)
+    bins = np.zeros((n, 2), np.uint8)
+    bins[:, 1] = rng.integers(0, 256, n)
+    g = rng.normal(size=n).astype(np.float32)
+    g[7] = 1e5
+    h = np.full(n, 1.9999999, np.float32)
+    rows = np.arange(n, dtype=np.int32)
+    got, (sg, sh, wide) = G.hist(_layouts(bins), torch.from_numpy(g), torch.from_numpy(h), torch.from_numpy(rows))
+    got = got.cpu().numpy()
+    assert wide == 1 and (sg, sh, wide) == O.hist_contract(g, h)[:3]
+    K = max(int(np.ceil(np.log2(n))), 21)
+    qh = int(np.rint(np.float64(h[0]) * 2.0 ** sh))
+    # 1.9999999 = 2 - 2^-23 is exactly (2^24 - 1) 2^-23: q(h) = 2^(61-K) - 2^(61-K-24+1), a hair below the bound
+    assert 2 ** (61 - K) - 2 ** (61 - K - 23) <= qh <= 2 ** (61 - K)
+    assert got[2, 0, 0] == n and int(got[1, 0, 0]) == n * qh
+    qg = np.rint(g.astype(np.float64) * 2.0 ** sg).astype(np.int64)
+    assert int(got[0, 0, 0]) == int(qg.sum())
+    assert np.array_equal(got, O.hist_fixed(bins.T, g, h, sg, sh, rows=rows.astype(np.int64)))
 
 
 def _random_qhist(rng, F, n=3000, nb=256):

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as O
-from tests.helpers import grad_hess, uniform_bins
+from tests.helpers import WIDE_KINDS, grad_hess, uniform_bins
 
 
 def _brute_hist(bins_nf, g, h, rows):
@@ -110,6 +110,91 @@ def test_hist_shift_closed_form():
     assert O.quant_shifts(np.array([1.0, -1.5], np.float32), np.array([0.25, 0.5], np.float32)) == (28, 29)
 
 
+@pytest.mark.parametrize("maxabs,n", [(1.0, 1), (0.75, 1000), (1.9999999, 1 << 21), (1.9999999, (1 << 21) + 1),
+                                      (5.5, 10_000_000), (1e-30, 3), (3e38, 2), (0.0, 10)])
+def test_wide_shift_bounds(maxabs, n):
+    """The wide contract's shift: every |q| <= 2^(61 - K) with K = max(k, 21),
+    so all n sum below 2^62 and a packing window of 2^(K // 2) rows, shifted
+    by its count bits K // 2 + 1, stays below 2^63; maximal (one more bit
+    would break the 2^(61 - K) bound)."""
+    s = O.wide_shift(maxabs, n)
+    if maxabs == 0.0:
+        assert s == 0
+        return
+    k = int(np.ceil(np.log2(n))) if n > 1 else 0
+    K = max(k, 21)
+    q = np.rint(np.float64(np.float32(maxabs)) * 2.0 ** s)
+    assert q <= 2.0 ** (61 - K)
+    assert n * q < 2.0 ** 62
+    w = K // 2
+    assert 2 ** w * q * 2.0 ** (w + 1) < 2.0 ** 63
+    e = int(np.frexp(np.float32(maxabs))[1])
+    assert 2.0 ** (s + 1 + e) > 2.0 ** (61 - K)
+
+
+def test_wide_shift_closed_form():
+    assert O.wide_shift(1.0, 1) == 39            # 61 - 21 - 1: small n count as 2^21 rows
+    assert O.wide_shift(1.0, 1 << 21) == 39
+    assert O.wide_shift(1.0, (1 << 21) + 1) == 38
+    assert O.wide_shift(5.5, 10_000_000) == 34   # 5.5 = 0.6875 * 2^3, k = 24
+
+
+def _resid_mass_np(x, s):
+    """The contract's residual and mass of one channel, restated in float64
+    (every step below is exact in float64 for float32 inputs)."""
+    y = x.astype(np.float64) * 2.0 ** s
+    r = np.rint(np.abs(y - np.rint(y)) * 2.0 ** 21)
+    m = np.rint(np.abs(x.astype(np.float64)) * 2.0 ** (s + 10))
+    return int(r.sum()), int(m.sum())
+
+
+@pytest.mark.parametrize("kind,n", [("normal", 1000), ("normal", 300_000), ("laplace", 50_000), ("logistic", 4096),
+                                    *[(k, 20_000) for k in WIDE_KINDS]])
+def test_hist_contract_against_numpy(kind, n):
+    """or_hist_contract's residuals and masses equal an independent float64
+    restatement, its decision is 64 R <= M on both channels, and its shifts
+    are the narrow or the wide ones accordingly; the outlier and heavy-tailed
+    kinds select wide, the well-scaled ones narrow."""
+    rng = np.random.default_rng(n)
+    g, h = grad_hess(rng, n, kind)
+    sg, sh, wide, sums = O.hist_contract(g, h)
+    sgn = O.hist_shift(float(np.abs(g).max()), n)
+    shn = O.hist_shift(float(np.abs(h).max()), n)
+    rg, mg = _resid_mass_np(g, sgn)
+    rh, mh = _resid_mass_np(h, shn)
+    assert sums == (rg, rh, mg, mh)
+    assert wide == int(not (64 * rg <= mg and 64 * rh <= mh))
+    assert wide == int(kind in WIDE_KINDS)
+    if wide:
+        assert (sg, sh) == (O.wide_shift(float(np.abs(g).max()), n), O.wide_shift(float(np.abs(h).max()), n))
+    else:
+        assert (sg, sh) == (sgn, shn)
+    assert O.quant_shifts(g, h) == (sg, sh)
+
+
+def test_hist_contract_closed_form():
+    """Values on the narrow grid have no residual (narrow); a value of half a
+    narrow quantum rounds to 0 (ties to even) with residual 2^20 and mass 2^9
+    in the contract's units, so enough of them select wide; all zeros keep
+    shift 0 and narrow."""
+    n = 4096
+    grid = np.array([1.0, -0.5, 0.25, 1.5], np.float32)   # max 1.5: e = 1, s = 30 - 11 - 1 = 18
+    g = np.tile(grid, n // 4)
+    h = np.ones(n, np.float32)
+    sg, sh, wide, sums = O.hist_contract(g, h)
+    assert (sg, sh, wide) == (18, 18, 0) and sums[0] == sums[1] == 0
+    m_grid = int((np.abs(grid.astype(np.float64)) * 2.0 ** 28).sum()) * (n // 4)
+    assert sums[2] == m_grid and sums[3] == n * 2 ** 28
+    for k, want_wide in ((200, 0), (3500, 1)):
+        g2 = g.copy()
+        g2[:k] = np.float32(2.0 ** -19)
+        _, _, wide2, (rg, _, mg, _) = O.hist_contract(g2, h)
+        assert rg == k * 2 ** 20
+        assert mg == m_grid - int((np.abs(g[:k].astype(np.float64)) * 2.0 ** 28).sum()) + k * 2 ** 9
+        assert wide2 == want_wide == int(64 * rg > mg)
+    assert O.hist_contract(np.zeros(8, np.float32), np.zeros(8, np.float32))[:3] == (0, 0, 0)
+
+
 def _brute_split(bins_nf, g, h, lam, gamma, mcw, msl, nbins, fmask, boost):
     """Enumerate every (f, b), summing the rows on each side directly."""
     n, F = bins_nf.shape
@@ -136,13 +221,14 @@ def _brute_split(bins_nf, g, h, lam, gamma, mcw, msl, nbins, fmask, boost):
     return best
 
 
+@pytest.mark.parametrize("kind", ["normal", "outlier"])
 @pytest.mark.parametrize("seed", range(4))
-def test_best_split_against_brute_force(seed):
+def test_best_split_against_brute_force(seed, kind):
     rng = np.random.default_rng(seed)
     n, F = 600, 5
     nb = 20
     bins = uniform_bins(rng, n, F, nb)
-    g, h = grad_hess(rng, n)
+    g, h = grad_hess(rng, n, kind)
     lam, gamma, mcw, msl = 1.0, 0.0, 1e-3, [1, 10, 30, 50][seed]
     nbins = np.full(F, nb, np.int32)
     fmask = np.array([1, 1, seed % 2, 1, 1], np.uint8)
@@ -154,8 +240,12 @@ def test_best_split_against_brute_force(seed):
     gfx, ffx, bfx = O.best_split_fixed(O.hist_fixed(bins.T, g, h, sg, sh), sg, sh, nbins, lam,
                                        gamma, mcw, msl, fmask, boost)
     assert (f32, b32) == (ref[2], ref[3]) == (ffx, bfx)
-    # q keeps 20 bits of max|g| here (n = 600): node sums carry ~1e-6 relative error
-    assert g32 == pytest.approx(ref[1], rel=1e-6) and gfx == pytest.approx(ref[1], rel=1e-5)
+    wide = O.hist_contract(g, h)[2]
+    assert wide == int(kind == "outlier")
+    # narrow: q keeps 20 bits of max|g| here (n = 600), node sums carry ~1e-6
+    # relative error; wide: 40 bits of max|g| = 50, the gain is the fp64 one
+    assert g32 == pytest.approx(ref[1], rel=1e-6)
+    assert gfx == pytest.approx(ref[1], rel=1e-9 if wide else 1e-5)
     # on the quantised values themselves (q 2^-s, exact in fp64) the fixed-point
     # scan is the brute force up to the fp64 rounding of the gain expression
     gq = np.rint(g.astype(np.float64) * 2.0 ** sg) * 2.0 ** -sg

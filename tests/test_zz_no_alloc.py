@@ -19,10 +19,12 @@ def _noalloc():
     return _lib.load().yabt_hist_noalloc
 
 
-def _case(n, F, seed, m):
+def _case(n, F, seed, m, outlier=None):
     rng = np.random.default_rng(seed)
     bins = rng.integers(0, 256, size=(n, F)).astype(np.uint8)
     g = rng.normal(size=n).astype(np.float32)
+    if outlier is not None:   # selects the wide contract
+        g[n // 2] = outlier
     h = rng.uniform(0.1, 1.0, size=n).astype(np.float32)
     lay = G.make_layouts(torch.from_numpy(bins), DEV)
     rows = torch.from_numpy(np.sort(rng.choice(n, size=m, replace=False)).astype(np.int32)).to(DEV)
@@ -31,7 +33,7 @@ def _case(n, F, seed, m):
 
 def _run_noalloc(fn, lay, g, h, rows):
     out = torch.full((3, lay.F, 256), -7, dtype=torch.int64, device=DEV)
-    shifts = torch.full((2,), -99, dtype=torch.int32, device=DEV)
+    shifts = torch.full((3,), -99, dtype=torch.int32, device=DEV)
     m = 0 if rows is None else rows.shape[0]
     rc = fn(G._ptr(lay.fm), lay.ld_fm, G._ptr(lay.rm), lay.ld_rm, G._ptr(g), G._ptr(h), lay.n, lay.F,
             G._ptr(rows), m, G._ptr(out), G._ptr(shifts), G._stream(DEV))
@@ -42,9 +44,10 @@ def _run_noalloc(fn, lay, g, h, rows):
 
 def test_noalloc_matches_yabt_hist_twice():
     fn = _noalloc()
-    for n, F, seed, m in [(300_001, 37, 1, 120_000), (40_000, 20, 2, 9_000)]:
-        print(f"yabt_hist_noalloc n={n} F={F} rows={m}", flush=True)
-        lay, g, h, rows = _case(n, F, seed, m)
+    for n, F, seed, m, outlier in [(300_001, 37, 1, 120_000, None), (40_000, 20, 2, 9_000, None),
+                                   (50_000, 18, 3, 20_000, 1e5)]:
+        print(f"yabt_hist_noalloc n={n} F={F} rows={m} outlier={outlier}", flush=True)
+        lay, g, h, rows = _case(n, F, seed, m, outlier)
         for r in (None, rows):
             got, got_s = _run_noalloc(fn, lay, g, h, r)
             want, want_s = G.hist(lay, g, h, r)

@@ -49,9 +49,9 @@ SIGNATURES = {
     "yabt_hist_workspace_bytes": (_sz, []),
     "yabt_hist": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _int, _vp, _i64, _vp, _vp, _vp, _vp]),
     "yabt_hist_accumulate": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _int, _vp, _i64, _int, _int,
-                                    _vp, _vp, _vp]),
+                                    _int, _vp, _vp, _vp]),
     "yabt_bin_counts": (_int, [_vp, _i64, _i64, _int, _vp, _vp]),
-    "yabt_hist_root": (_int, [_vp, _i64, _vp, _vp, _i64, _int, _vp, _int, _int, _vp, _vp]),
+    "yabt_hist_root": (_int, [_vp, _i64, _vp, _vp, _i64, _int, _vp, _int, _int, _int, _vp, _vp]),
     "yabt_hist_noalloc": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _int, _vp, _i64, _vp, _vp, _vp]),
     "yabt_best_split_workspace_bytes": (_sz, [_int]),
     "yabt_best_split": (_int, [_vp, _int, _vp, _vp, _vp, _int, _int, _dbl, _dbl, _dbl, _int, _vp,

@@ -29,21 +29,63 @@ __host__ __device__ inline int quant_shift(float maxabs, int64_t n) {
     return 61 - k - e;
 }
 
-// Node histograms use a narrower shift: the streaming root kernel adds the
-// word (q(g) << 32) + q(h) into one 64-bit LDS cell per update and unpacks
-// the two 32-bit halves after every block step of 1024 rows.  With
-// s = 30 - min(k, 11) - e, |q| <= 2^(30 - min(k, 11)), so any min(n, 2048)
-// values -- two steps' worth -- sum within 2^30 < 2^31 in each half; q keeps
-// 19 bits of the largest |x| for n > 2048 (more below), and every partial sum
-// of <= n values stays below 2^51.  Shared with oracle/grow_oracle.c
-// (or_hist_shift).
+// Node histograms use one of two contracts, chosen per call from the data
+// (quant_resid, quant_finish):
+//   narrow: s = 30 - min(k, 11) - e, so |q| <= 2^(30 - min(k, 11)) and any
+//     min(n, 2048) values sum within 2^30 < 2^31: the streaming root kernel
+//     adds the word (q(g) << 32) + q(h) into one 64-bit LDS cell per update
+//     and unpacks the two 32-bit halves after every epoch.  q keeps 19 bits
+//     of the largest |x| for n > 2048 (more below), and every partial sum of
+//     <= n values stays below 2^51;
+//   wide: s = 61 - max(k, 21) - e, so |q| <= 2^(61 - max(k, 21)) (37 bits of
+//     the largest |x| at 10M rows, 40 at <= 2M) and every partial sum of
+//     <= n values stays below 2^61; g and h take a 64-bit LDS cell each.
+// The narrow contract is used only when its quantisation residual is small
+// against the data: per channel, R = sum rint(|x 2^s - rint(x 2^s)| 2^21)
+// and M = sum rint(|x| 2^(s + 10)) at the narrow shift s (exact integers,
+// so the decision does not depend on any order), narrow iff 64 R <= M for
+// both g and h, i.e. sum |x - q 2^-s| <= 2^-17 sum |x| up to the rounding of
+// the two integer sums.  One large value among small ones (an outlier,
+// heavy-tailed targets) makes q coarse against most rows and selects wide.
+// Shared with oracle/grow_oracle.c (or_hist_shift, or_wide_shift,
+// or_hist_contract).
+__host__ __device__ inline int ceil_log2_rows(int64_t n, int cap) {
+    int k = 0;
+    while (k < cap && ((int64_t)1 << k) < n) ++k;
+    return k;
+}
+
 __host__ __device__ inline int hist_shift(float maxabs, int64_t n) {
     if (!(maxabs > 0.0f)) return 0;
     int e = 0;
     (void)frexpf(maxabs, &e);
-    int k = 0;
-    while (k < 11 && ((int64_t)1 << k) < n) ++k;
-    return 30 - k - e;
+    return 30 - ceil_log2_rows(n, 11) - e;
+}
+
+constexpr int WIDE_MIN_K = 21;   // the wide shift counts n as at least 2^21 rows
+
+__host__ __device__ inline int wide_shift(float maxabs, int64_t n) {
+    if (!(maxabs > 0.0f)) return 0;
+    int e = 0;
+    (void)frexpf(maxabs, &e);
+    const int k = ceil_log2_rows(n, 62);
+    return 61 - (k > WIDE_MIN_K ? k : WIDE_MIN_K) - e;
+}
+
+// log2 of the packing window of the gathered histograms (see
+// hist_gather_rows: the count rides in the low cb = w + 1 bits of a 64-bit
+// word, (q << cb) + 1 per row, unpacked every 2^w rows).  Narrow: |q| <= 2^19
+// (2^30 for tiny n, whose windows never fill), w = 16: a window's sum stays
+// below 2^35 << cb < 2^63.  Wide: |q| <= 2^(61 - K), K = max(k, 21),
+// w = K / 2: a window's sum times 2^cb is at most 2^(62 - K + 2w) <= 2^62.
+// Both are at least 10 (one block step of 1024 rows).
+constexpr int NARROW_WINDOW_LOG2 = 16;
+__host__ __device__ inline int wide_window_log2(int64_t n) {
+    const int k = ceil_log2_rows(n, 62);
+    return (k > WIDE_MIN_K ? k : WIDE_MIN_K) / 2;
+}
+__host__ __device__ inline int window_log2(int64_t n, bool wide) {
+    return wide ? wide_window_log2(n) : NARROW_WINDOW_LOG2;
 }
 
 __device__ __forceinline__ int64_t quantise(float x, double scale) {
@@ -57,6 +99,13 @@ __device__ __forceinline__ int64_t quantise(float x, double scale) {
 // three VALU operations instead of eight.  `scale` is 2^s.
 __device__ __forceinline__ int64_t quantise_node(float x, double scale) {
     return (int64_t)(int32_t)rintf(ldexpf(x, ilogb(scale)));
+}
+
+// quantise for either contract: the same fp32 steps, converted to 64 bits
+// (the wide shift's |x * 2^s| reaches 2^40); equal to quantise_node wherever
+// that one applies.
+__device__ __forceinline__ int64_t quantise_wide(float x, double scale) {
+    return (int64_t)rintf(ldexpf(x, ilogb(scale)));
 }
 
 // Per-call quantisation record, filled on the device.
@@ -73,7 +122,11 @@ struct Quant {
     int64_t hq_const;
     int64_t tot_g, tot_h;      // sum of q(g), q(h) over all rows (root totals)
     uint32_t ticket;
-    uint32_t pad;
+    int32_t wide;              // 1: the wide contract (hist_shift's notes)
+    int32_t wlog;              // the gathers' packing window, window_log2(n, wide)
+    int32_t pad2;
+    uint64_t res_g, res_h;     // quantisation residuals at the narrow shift (quant_resid)
+    uint64_t mass_g, mass_h;   // and the masses they are measured against
 };
 
 __device__ __forceinline__ uint32_t float_key(float x) {
@@ -469,10 +522,104 @@ __device__ void quant_reduce(const float* grad, const float* hess, int64_t n, Qu
     }
 }
 
+// Residual and mass of one value at the narrow shift s (hist_shift's notes):
+// x 2^s and its distance to the nearest integer are exact in fp32, and so are
+// the power-of-two scalings; rint(|d| 2^21) <= 2^20, rint(|x| 2^(s + 10)) <=
+// 2^40.  Non-finite values add nothing (the call reports them and stops).
+__device__ __forceinline__ void resid_take(float x, int s, uint64_t& r, uint64_t& m) {
+    if (!isfinite(x)) return;
+    const float y = ldexpf(x, s);
+    const float d = y - rintf(y);
+    r += (uint64_t)rintf(ldexpf(fabsf(d), 21));
+    m += (uint64_t)rintf(ldexpf(fabsf(x), s + 10));
+}
+
+// Grid-stride residuals and masses of g and h at the narrow shifts, after
+// quant_reduce has completed (a later launch): added into q->res_*, q->mass_*
+// (exact integer sums, so the result does not depend on the grid).
+template <int NT>
+__device__ void quant_resid(const float* grad, const float* hess, int64_t n, Quant* q) {
+    __shared__ uint64_t s_r[4][NT / WAVE];
+    const int sg = hist_shift(__uint_as_float(q->maxg_bits), n), sh = hist_shift(__uint_as_float(q->maxh_bits), n);
+    uint64_t rg = 0, rh = 0, mg = 0, mh = 0;
+    const int64_t tid = (int64_t)blockIdx.x * NT + threadIdx.x, nth = (int64_t)gridDim.x * NT;
+    int64_t head = 0;
+    if (((reinterpret_cast<uintptr_t>(grad) | reinterpret_cast<uintptr_t>(hess)) & 15) == 0) {
+        constexpr int U = 4;
+        const int64_t n4 = n / 4;
+        const float4* g4 = reinterpret_cast<const float4*>(grad);
+        const float4* h4 = reinterpret_cast<const float4*>(hess);
+        int64_t i = tid;
+        for (; i + (U - 1) * nth < n4; i += U * nth) {
+            float4 a[U], c[U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                a[u] = g4[i + u * nth];
+                c[u] = h4[i + u * nth];
+            }
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
+                resid_take(a[u].x, sg, rg, mg);
+                resid_take(a[u].y, sg, rg, mg);
+                resid_take(a[u].z, sg, rg, mg);
+                resid_take(a[u].w, sg, rg, mg);
+                resid_take(c[u].x, sh, rh, mh);
+                resid_take(c[u].y, sh, rh, mh);
+                resid_take(c[u].z, sh, rh, mh);
+                resid_take(c[u].w, sh, rh, mh);
+            }
+        }
+        for (; i < n4; i += nth) {
+            const float4 a = g4[i], c = h4[i];
+            resid_take(a.x, sg, rg, mg);
+            resid_take(a.y, sg, rg, mg);
+            resid_take(a.z, sg, rg, mg);
+            resid_take(a.w, sg, rg, mg);
+            resid_take(c.x, sh, rh, mh);
+            resid_take(c.y, sh, rh, mh);
+            resid_take(c.z, sh, rh, mh);
+            resid_take(c.w, sh, rh, mh);
+        }
+        head = n4 * 4;
+    }
+    for (int64_t i = head + tid; i < n; i += nth) {
+        resid_take(grad[i], sg, rg, mg);
+        resid_take(hess[i], sh, rh, mh);
+    }
+    const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
+    rg = (uint64_t)wave_sum_i64((int64_t)rg);
+    rh = (uint64_t)wave_sum_i64((int64_t)rh);
+    mg = (uint64_t)wave_sum_i64((int64_t)mg);
+    mh = (uint64_t)wave_sum_i64((int64_t)mh);
+    if (lane == 0) {
+        s_r[0][w] = rg;
+        s_r[1][w] = rh;
+        s_r[2][w] = mg;
+        s_r[3][w] = mh;
+    }
+    __syncthreads();
+    if (threadIdx.x < 4) {
+        uint64_t t = 0;
+        for (int i = 0; i < NT / WAVE; ++i) t += s_r[threadIdx.x][i];
+        uint64_t* dst = threadIdx.x == 0 ? &q->res_g : threadIdx.x == 1 ? &q->res_h
+                      : threadIdx.x == 2 ? &q->mass_g : &q->mass_h;
+        if (t) atomicAdd((unsigned long long*)dst, (unsigned long long)t);
+    }
+}
+
+// The contract of hist_shift's notes from the residuals: narrow iff
+// 64 R <= M for both channels (R <= n 2^20 < 2^52, so 64 R cannot wrap).
+__host__ __device__ inline bool narrow_contract(uint64_t rg, uint64_t mg, uint64_t rh, uint64_t mh) {
+    return 64 * rg <= mg && 64 * rh <= mh;
+}
+
 __device__ inline void quant_finish(Quant* q, int64_t n) {
     const float mg = __uint_as_float(q->maxg_bits), mh = __uint_as_float(q->maxh_bits);
-    q->sg = hist_shift(mg, n);
-    q->sh = hist_shift(mh, n);
+    const bool wide = !narrow_contract(q->res_g, q->mass_g, q->res_h, q->mass_h);
+    q->wide = wide ? 1 : 0;
+    q->wlog = window_log2(n, wide);
+    q->sg = wide ? wide_shift(mg, n) : hist_shift(mg, n);
+    q->sh = wide ? wide_shift(mh, n) : hist_shift(mh, n);
     q->scg = ldexp(1.0, q->sg);
     q->sch = ldexp(1.0, q->sh);
     q->ig = ldexp(1.0, -q->sg);
@@ -482,7 +629,7 @@ __device__ inline void quant_finish(Quant* q, int64_t n) {
     if (n > 0 && q->hmin_key == q->hmax_key) {
         const uint32_t k = q->hmin_key;
         const float h = __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
-        const int64_t hq = quantise_node(h, q->sch);
+        const int64_t hq = quantise_wide(h, q->sch);
         if (hq != 0) {
             q->const_h = 1;
             q->hq_const = hq;
@@ -501,6 +648,19 @@ static __global__ __attribute__((unused)) void k_quant_clear(Quant* q) {
     q->tot_g = 0;
     q->tot_h = 0;
     q->ticket = 0;
+    q->wide = 0;
+    q->wlog = NARROW_WINDOW_LOG2;
+    q->res_g = q->res_h = 0;
+    q->mass_g = q->mass_h = 0;
+}
+
+// Second pass of the per-call quantisation: residuals for the contract
+// (quant_resid), then, in the grid's last block, quant_finish.
+template <int NT>
+static __global__ __attribute__((unused)) void __launch_bounds__(NT)
+k_quant_resid(const float* grad, const float* hess, int64_t n, Quant* q) {
+    quant_resid<NT>(grad, hess, n, q);
+    if (last_block(&q->ticket) && threadIdx.x == 0) quant_finish(q, n);
 }
 
 }  // namespace yabt

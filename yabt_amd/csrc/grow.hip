@@ -6,7 +6,8 @@
 // written by the previous launch, so no split needs a host round trip.
 //
 // Arithmetic (bit-identical to oracle/grow_oracle.c OR_MODE_FIXED):
-//   * g and h are quantised once per call to int64 fixed point (quant_shift);
+//   * g and h are quantised once per call to int64 fixed point with the
+//     contract of common.h (hist_shift or wide_shift, chosen per call);
 //     node histograms are exact integer sums, so the accumulation order, the
 //     row order inside a node and sibling subtraction (grow.c:355-369) are
 //     exact and the result is deterministic;
@@ -17,8 +18,10 @@
 //     equal feature 0's 256 bins (grow.c:302-308, 371-379).
 //
 // Launch sequence of one tree (caller's stream):
-//   k_quant_clear, k_setup   max|g|,|h| -> shifts; table init; clear slot 0
-//   k_setup_finish           shifts, constant-hessian detection, tree state
+//   k_quant_clear, k_setup   max|g|,|h|; table init; clear slot 0
+//   k_quant_resid            quantisation residuals -> contract, shifts,
+//                            constant-hessian detection (common.h)
+//   k_setup_finish           tree state
 //   k_hist_root              streaming histogram of all rows (+ root totals)
 //   k_scan<ROOT>             default-bin fill, scan, controller: first split
 //   max_leaves - 1 times (each kernel returns at once once the tree is done):
@@ -166,7 +169,6 @@ __global__ void __launch_bounds__(SB) k_setup(GrowArgs A) {
 // One thread, after k_setup: shifts and tree state.
 __global__ void k_setup_finish(GrowArgs A) {
     GrowState* st = A.st;
-    quant_finish(A.q, A.n);
     st->status = 0;
     st->done = 0;
     st->active = 0;
@@ -713,8 +715,9 @@ int yabt_grow(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int
     const int tiles = (F + HFL - 1) / HFL;
     k_quant_clear<<<1, 1, 0, stream>>>(A.q);
     k_setup<<<launch_grid(n, SB * 16, 1024), SB, 0, stream>>>(A);
+    k_quant_resid<SB><<<launch_grid(n, SB * 16, 1024), SB, 0, stream>>>(grad, hess, n, A.q);
     k_setup_finish<<<1, 1, 0, stream>>>(A);
-    launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, A.dflt, A.counts, A.q, A.hist, 1,
+    launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, 0, A.dflt, A.counts, A.q, A.hist, 1,
                      &A.st->done);
     const int scan_grid = (F + SCAN_FEATS - 1) / SCAN_FEATS;
     k_scan<true><<<scan_grid, SCAN_FEATS * WAVE, 0, stream>>>(A);
@@ -724,7 +727,7 @@ int yabt_grow(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int
         k_split_partition<<<pgrid, SB, 0, stream>>>(bins_fm, ld_fm, A.st, slot_n);
         k_hist_gather<<<tiles * GATHER_MAX_CHUNKS, HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, A.q, 0.0,
                                                                         0.0, A.dflt, &A.st->hist, 1, &A.st->done,
-                                                                        pack_window_log2(n));
+                                                                        0);
         k_scan<false><<<scan_grid, 2 * SCAN_FEATS * WAVE, 0, stream>>>(A);
     }
     return launch_status("yabt_grow launch");

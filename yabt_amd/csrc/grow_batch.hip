@@ -27,7 +27,8 @@
 // Committed splits get exactly yabt_grow's node arrays, values and per-row
 // leaf ids (same sums, same scan, same order); the others are never read.
 //
-// Launches: k_setup, k_setup_finish, k_hist_root, k_scan<true> (root, plans
+// Launches: k_setup, k_quant_resid (the contract, common.h), k_setup_finish,
+// k_hist_root, k_scan<true> (root, plans
 // round 1), then per round k_part, k_gather, k_scan<false>, and at the end
 // k_leaf_plan, k_leaf_ids (per-row leaf ids).
 // The controller writes the round count and the done flag to mapped host
@@ -206,7 +207,6 @@ __global__ void __launch_bounds__(SB) k_setup(Args A) {
 
 __global__ void k_setup_finish(Args A) {
     State* st = A.st;
-    quant_finish(A.q, A.n);
     st->done = 0;
     st->n_round = 0;
     st->n_pend = 0;
@@ -363,9 +363,10 @@ __global__ void __launch_bounds__(HBLOCK) k_gather(const uint8_t* __restrict__ b
                                                    const float* __restrict__ grad, const float* __restrict__ hess,
                                                    const float2* __restrict__ gh,
                                                    int F, const Quant* q, const int32_t* __restrict__ dflt,
-                                                   const State* st, const Pend* pend, int64_t* pieces, int wlog) {
+                                                   const State* st, const Pend* pend, int64_t* pieces) {
     const int32_t done = st->done, nr = st->n_round;
     const double scg = q->scg, sch = q->sch;
+    const int wlog = q->wlog;
     const bool no_h = q->const_h != 0;
     if (done || nr == 0) return;
     // block id -> (unit, tile): die x = id % XCDS holds units x, x + XCDS, ...
@@ -1569,8 +1570,9 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
     const int tiles = (F + HFL - 1) / HFL;
     k_quant_clear<<<1, 1, 0, stream>>>(A.q);
     k_setup<<<launch_grid(n, SB * 16, 1024), SB, 0, stream>>>(A);
+    k_quant_resid<SB><<<launch_grid(n, SB * 16, 1024), SB, 0, stream>>>(grad, hess, n, A.q);
     k_setup_finish<<<1, 1, 0, stream>>>(A);
-    launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, A.dflt, A.counts, A.q, A.hist, 1,
+    launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, 0, A.dflt, A.counts, A.q, A.hist, 1,
                      &A.st->done);
     const int scan_grid = (F + SCAN_FEATS - 1) / SCAN_FEATS;
     const size_t table_lds = table_carve(nullptr, max_leaves, A.pend_cap, nullptr);
@@ -1578,7 +1580,6 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
     const size_t scan_lds = table_lds > SCAN_XCHG_BYTES ? table_lds : SCAN_XCHG_BYTES;
     int lrc = launch_status("yabt_grow_batched launch");
     if (lrc) return lrc;
-    const int wlog = pack_window_log2(n);
     // rounds: at most max_leaves - 1 (one split each); the controller of round
     // r stamps r + 1 into the flags word, so round r may be enqueued once
     // round r - LOOKAHEAD has finished
@@ -1602,7 +1603,7 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
         if (fl->word & 1) break;
         k_part<<<PART_BLOCKS, SB, 0, stream>>>(bins_fm, ld_fm, n, A.st, A.pend);
         k_gather<<<tiles * gather_units(tiles), HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, A.gh, F, A.q, A.dflt,
-                                                                         A.st, A.pend, A.pieces, wlog);
+                                                                         A.st, A.pend, A.pieces);
         k_scan<false><<<dim3(scan_grid, KMAX), CT, scan_lds, stream>>>(A);
         if ((lrc = launch_status("yabt_grow_batched launch"))) return lrc;
     }

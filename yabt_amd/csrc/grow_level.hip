@@ -122,7 +122,6 @@ __global__ void __launch_bounds__(LB) k_setup(const float* grad, const float* he
 }
 
 __global__ void k_setup_finish(Quant* q, int64_t n, LNode* nodes, int32_t* scan_list, int32_t* status) {
-    quant_finish(q, n);
     LNode& r = nodes[0];
     r.tot[0] = q->tot_g;
     r.tot[1] = 0;
@@ -317,8 +316,8 @@ __global__ void __launch_bounds__(HBLOCK) k_hist(const uint8_t* __restrict__ bin
             uint64_t qg = 0, qh = 0;
             if (i0 + lane < b) {
                 r = sorted[i0 + lane];
-                qg = (uint64_t)quantise_node(grad[r], scg);
-                if (HCH) qh = (uint64_t)quantise_node(hess[r], sch);
+                qg = (uint64_t)quantise_wide(grad[r], scg);
+                if (HCH) qh = (uint64_t)quantise_wide(hess[r], sch);
             }
             const int nv = (int)min((int64_t)HFL, max((int64_t)0, b - (i0 + HFL * rg)));
             uint32_t bj[HFL];
@@ -546,9 +545,10 @@ int yabt_grow_levelwise(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bi
     k_quant_clear<<<1, 1, 0, stream>>>(w.q);
     k_setup<<<launch_grid(max(n, (int64_t)slot_n), LB * 16, 1024), LB, 0, stream>>>(
         grad, hess, n, w.q, w.row_node, w.route, NP, w.path, (int64_t)NP * F, w.hist, (int64_t)slot_n);
+    k_quant_resid<LB><<<launch_grid(n, LB * 16, 1024), LB, 0, stream>>>(grad, hess, n, w.q);
     k_setup_finish<<<1, 1, 0, stream>>>(w.q, n, w.nodes, w.scan_list, out_status);
     if (n > 0) {
-        launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, w.q, 0.0, 0.0, nullptr, bin_counts, w.q, w.hist,
+        launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, w.q, 0.0, 0.0, 0, nullptr, bin_counts, w.q, w.hist,
                          1, nullptr);
     }
     k_root_tot<<<1, 1, 0, stream>>>(w.q, n, w.nodes);

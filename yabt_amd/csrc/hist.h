@@ -123,15 +123,6 @@ __device__ __forceinline__ void flush_cells(HistLds& T, const uint64_t (&g)[HENT
     }
 }
 
-// log2 of the packing window of the gathered histograms: windows of 2^16
-// rows.  With hist_shift's |q| <= 2^19 a window's sum of q stays below 2^35
-// and its count below 2^17 = 2^cb, cb = 17, so (sum q) << cb + count is exact
-// in 64 bits whatever n is.
-__host__ __device__ inline int pack_window_log2(int64_t n) {
-    (void)n;
-    return 16;
-}
-
 // LDS of the streaming root histogram: 256 bins x 32 words of 8 bytes, of
 // which words 0..15 of a bin are the cells of features f0 .. f0 + 15 in one
 // buffer and words 16..31 in the other.  The byte address of a cell is then
@@ -161,7 +152,8 @@ __device__ __forceinline__ uint32_t bin_addr_rt(uint32_t word, uint32_t lo, int 
 // stay the same over a whole fit, so it comes from the per-fit counts
 // (F, 256) (k_bin_count, yabt_bin_counts), which each tile's chunk-0 block
 // adds at its flush.  The stream carries g and h only:
-//   HCH (h varies): each update adds the word (q(g) << 32) + q(h) (mod 2^64)
+//   ROOT_PACKED (h varies, narrow contract): each update adds the word
+//     (q(g) << 32) + q(h) (mod 2^64)
 //     into the cell [bin][feature]; each thread then reads its 4 cells and
 //     unpacks them -- lo, the
 //     sign-extended low 32 bits, is the h sum; (cell - lo) >> 32 the g sum.
@@ -173,7 +165,9 @@ __device__ __forceinline__ uint32_t bin_addr_rt(uint32_t word, uint32_t lo, int 
 //     targets it while it is read; with hist_shift's |q| <= 2^(30 -
 //     min(k, 11)) each half's sum stays within 3 * 2^29 < 2^31 (2^30 for
 //     n <= 2048), so both are exact.
-//   !HCH (every h equal): the word is q(g) itself; no unpacking, and the h
+//   ROOT_WIDE (h varies, wide contract): q(g) and q(h) go to a 64-bit cell
+//     each (the two buffers), two atomics per update, no unpacking.
+//   ROOT_G (every h equal): the word is q(g) itself; no unpacking, and the h
 //     plane is left to the caller (count * q(h)).
 // Invalid rows of a step add zero words (their q is 0), so the loop needs no
 // per-row tail test; only the loads are bounded.  Each wave keeps the loads
@@ -292,6 +286,7 @@ inline RootGrid root_grid(int64_t n, int F, const void* grad, const void* hess) 
     return g;
 }
 
+constexpr int ROOT_G = 0, ROOT_PACKED = 1, ROOT_WIDE = 2;   // modes of the streaming root kernels
 constexpr int ROOT_DEPTH = 3;    // steps of inputs loaded ahead of the adds: one epoch
 constexpr int TAIL_DEPTH = 4;    // the same in a tail block (4 steps of 512 rows per column)
 // A cell takes the rows of one epoch between two unpacks: ROOT_DEPTH block
@@ -300,13 +295,18 @@ constexpr int TAIL_DEPTH = 4;    // the same in a tail block (4 steps of 512 row
 static_assert((int64_t)ROOT_DEPTH * RSTEP * (1 << 19) < (1ll << 31), "an epoch's sums fit 32-bit halves");
 static_assert((int64_t)TAIL_DEPTH * TSTEP / 4 * (1 << 19) < (1ll << 31), "a tail epoch's sums fit 32-bit halves");
 
-template <bool HCH, bool SKIP>
+// MODE: ROOT_G (every h equal: the word is q(g), never unpacked), ROOT_PACKED
+// (narrow contract: (q(g) << 32) + q(h) in one cell, epochs), ROOT_WIDE (wide
+// contract: q(g) and q(h) in a cell each -- the two buffers of the layout --
+// with one atomic per channel; 64-bit cells never need an unpack).
+template <int MODE, bool SKIP>
 __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restrict__ bins_fm, int64_t ld,
                                              const float* __restrict__ grad, const float* __restrict__ hess,
                                              int64_t n, int F, double scg, double sch,
                                              const int32_t* __restrict__ dflt, const uint32_t* __restrict__ counts,
                                              Quant* q_tot, int64_t* out, int chunks, int bid) {
     const int tile = bid / chunks, chunk = bid % chunks;
+    constexpr bool HCH = MODE != ROOT_G, PACK = MODE == ROOT_PACKED;
     const int f0 = tile * HFL;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const int fl = lane & (HFL - 1), rg = lane / HFL;
@@ -377,7 +377,7 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
     int64_t sum_g = 0, sum_h = 0;
     uint32_t buf = 0;   // the cell buffer of this round's epoch
     for (int64_t s0 = -ROOT_DEPTH; s0 < steps; s0 += ROOT_DEPTH) {
-        const uint32_t lb = HCH ? (lbase | (buf << 7)) : lbase;
+        const uint32_t lb = PACK ? (lbase | (buf << 7)) : lbase;
 #pragma unroll
         for (int j = 0; j < ROOT_DEPTH; ++j) {
             const int64_t s = s0 + j;
@@ -387,8 +387,8 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
             __builtin_amdgcn_sched_barrier(0);
             const int64_t r0 = lo + s * RSTEP + (int64_t)wave * WAVE;
             const bool rok = s >= 0 && r0 + lane < hi;
-            const int64_t gq = rok ? quantise_node(gs[j], scg) : 0;
-            const int64_t hq = (HCH && rok) ? quantise_node(hs[j], sch) : 0;
+            const int64_t gq = rok ? (PACK ? quantise_node(gs[j], scg) : quantise_wide(gs[j], scg)) : 0;
+            const int64_t hq = (HCH && rok) ? (PACK ? quantise_node(hs[j], sch) : quantise_wide(hs[j], sch)) : 0;
             // the 16 cell addresses (and, with SKIP, which rows are not added)
             // come out of this stage's bins before its registers are refilled,
             // so the old and new values are never live at once (else the refill
@@ -404,12 +404,18 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
             load(s + ROOT_DEPTH, gs[j], hs[j], bs[j]);
             sum_g += gq;
             sum_h += hq;
-            const uint64_t word = HCH ? ((uint64_t)gq << 32) + (uint64_t)hq : (uint64_t)gq;
+            const uint64_t word = PACK ? ((uint64_t)gq << 32) + (uint64_t)hq : (uint64_t)gq;
+            // ROOT_WIDE: the h cell is the g cell's twin in the other buffer
+            // (16 words, 128 bytes, further)
 #define YABT_GH_ADD(J)                                                           \
             {                                                                    \
                 const uint64_t wj = row_bcast64<J>(word);                        \
                 unsigned long long* const cp = reinterpret_cast<unsigned long long*>(lds + at[J]); \
-                if (!SKIP || ((keep >> (J)) & 1u)) atomicAdd(cp, (unsigned long long)wj); \
+                if (!SKIP || ((keep >> (J)) & 1u)) {                             \
+                    atomicAdd(cp, (unsigned long long)wj);                       \
+                    if (MODE == ROOT_WIDE)                                       \
+                        atomicAdd(cp + HFL, (unsigned long long)row_bcast64<J>((uint64_t)hq)); \
+                }                                                                \
             }
             YABT_GH_ADD(0) YABT_GH_ADD(1) YABT_GH_ADD(2) YABT_GH_ADD(3)
             YABT_GH_ADD(4) YABT_GH_ADD(5) YABT_GH_ADD(6) YABT_GH_ADD(7)
@@ -417,7 +423,7 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
             YABT_GH_ADD(12) YABT_GH_ADD(13) YABT_GH_ADD(14) YABT_GH_ADD(15)
 #undef YABT_GH_ADD
         }
-        if (HCH) {
+        if (PACK) {
             // end of the epoch: once every wave's adds into its buffer are
             // done, read it while the next epoch adds into the other one
             __syncthreads();
@@ -426,9 +432,12 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
         }
     }
     __syncthreads();
-    if (!HCH) {   // one buffer, never unpacked: the cells are the g sums
+    if (!PACK) {   // never unpacked: the cells are the g sums (and the h sums)
 #pragma unroll
-        for (int k = 0; k < RENT; ++k) ag[k] = (int64_t)L.w[cell(k)];
+        for (int k = 0; k < RENT; ++k) {
+            ag[k] = (int64_t)L.w[cell(k)];
+            if (HCH) ah[k] = (int64_t)L.w[cell(k) + HFL];
+        }
     }
     if (totals) {
         sum_g = wave_sum<int64_t>(sum_g);
@@ -511,13 +520,15 @@ __device__ __forceinline__ void flush_tail_gh(RootFlushLds& T, const int64_t (&g
     }
 }
 
-template <bool HCH, bool SKIP>
+// MODE as in hist_root_gh.
+template <int MODE, bool SKIP>
 __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __restrict__ bins_fm, int64_t ld,
                                                const float* __restrict__ grad, const float* __restrict__ hess,
                                                int64_t n, int F, double scg, double sch,
                                                const int32_t* __restrict__ dflt,
                                                const uint32_t* __restrict__ counts, Quant* q_tot, int64_t* out,
                                                int64_t span, int tb) {
+    constexpr bool HCH = MODE != ROOT_G, PACK = MODE == ROOT_PACKED;
     const int f0 = F / HFL * HFL;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
     const int col = lane & (HFL - 1), c = lane & (TAILF - 1), a = col / TAILF, qw = lane / HFL;
@@ -572,17 +583,17 @@ __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __res
     int64_t sum_g = 0, sum_h = 0;
     uint32_t buf = 0;   // the cell buffer of this ring round's epoch
     for (int64_t s0 = -TAIL_DEPTH; s0 < steps; s0 += TAIL_DEPTH) {
-        const uint32_t lb = HCH ? (lbase | (buf << 7)) : lbase;
+        const uint32_t lb = PACK ? (lbase | (buf << 7)) : lbase;
 #pragma unroll
         for (int j = 0; j < TAIL_DEPTH; ++j) {
             const int64_t s = s0 + j;
             __builtin_amdgcn_sched_barrier(0);
             const int64_t p = lo + s * TSTEP + (int64_t)wave * (2 * WAVE) + 32 * qw + 8 * a + 2 * c;
             const bool ok0 = s >= 0 && p < hi2, ok1 = s >= 0 && p + 1 < hi2;
-            const int64_t g0 = ok0 ? quantise_node(gs[j].x, scg) : 0;
-            const int64_t g1 = ok1 ? quantise_node(gs[j].y, scg) : 0;
-            const int64_t h0 = (HCH && ok0) ? quantise_node(hs[j].x, sch) : 0;
-            const int64_t h1 = (HCH && ok1) ? quantise_node(hs[j].y, sch) : 0;
+            const int64_t g0 = ok0 ? (PACK ? quantise_node(gs[j].x, scg) : quantise_wide(gs[j].x, scg)) : 0;
+            const int64_t g1 = ok1 ? (PACK ? quantise_node(gs[j].y, scg) : quantise_wide(gs[j].y, scg)) : 0;
+            const int64_t h0 = (HCH && ok0) ? (PACK ? quantise_node(hs[j].x, sch) : quantise_wide(hs[j].x, sch)) : 0;
+            const int64_t h1 = (HCH && ok1) ? (PACK ? quantise_node(hs[j].y, sch) : quantise_wide(hs[j].y, sch)) : 0;
             const uint32_t wv[2] = {bs[j].x, bs[j].y};
             uint32_t at[8];
             uint32_t keep = 0xffu;
@@ -594,19 +605,25 @@ __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __res
             load(s + TAIL_DEPTH, gs[j], hs[j], bs[j]);
             sum_g += g0 + g1;
             sum_h += h0 + h1;
-            const uint64_t w0 = HCH ? ((uint64_t)g0 << 32) + (uint64_t)h0 : (uint64_t)g0;
-            const uint64_t w1 = HCH ? ((uint64_t)g1 << 32) + (uint64_t)h1 : (uint64_t)g1;
+            const uint64_t w0 = PACK ? ((uint64_t)g0 << 32) + (uint64_t)h0 : (uint64_t)g0;
+            const uint64_t w1 = PACK ? ((uint64_t)g1 << 32) + (uint64_t)h1 : (uint64_t)g1;
+            // ROOT_WIDE: the h cell is the g cell's twin in the other buffer
 #define YABT_TAIL_ADD(J)                                                         \
             {                                                                    \
                 const uint64_t wj = quad_bcast64<(J) / 2>(((J) & 1) ? w1 : w0);  \
                 unsigned long long* const cp = reinterpret_cast<unsigned long long*>(lds + at[J]); \
-                if (!SKIP || ((keep >> (J)) & 1u)) atomicAdd(cp, (unsigned long long)wj); \
+                if (!SKIP || ((keep >> (J)) & 1u)) {                             \
+                    atomicAdd(cp, (unsigned long long)wj);                       \
+                    if (MODE == ROOT_WIDE)                                       \
+                        atomicAdd(cp + HFL, (unsigned long long)quad_bcast64<(J) / 2>(  \
+                                                ((J) & 1) ? (uint64_t)h1 : (uint64_t)h0)); \
+                }                                                                \
             }
             YABT_TAIL_ADD(0) YABT_TAIL_ADD(1) YABT_TAIL_ADD(2) YABT_TAIL_ADD(3)
             YABT_TAIL_ADD(4) YABT_TAIL_ADD(5) YABT_TAIL_ADD(6) YABT_TAIL_ADD(7)
 #undef YABT_TAIL_ADD
         }
-        if (HCH) {
+        if (PACK) {
             // end of the epoch: read this round's buffer while the next round
             // adds into the other one
             __syncthreads();
@@ -618,25 +635,31 @@ __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __res
     if (n2 < n && hi == n) {
         if (wave == 0 && qw == 0 && a == 0) {   // lanes c = 0 .. 3: one per feature
             const int64_t r = n - 1;
-            const int64_t gq = quantise_node(grad[r], scg);
-            const int64_t hq = HCH ? quantise_node(hess[r], sch) : 0;
+            const int64_t gq = PACK ? quantise_node(grad[r], scg) : quantise_wide(grad[r], scg);
+            const int64_t hq = HCH ? (PACK ? quantise_node(hess[r], sch) : quantise_wide(hess[r], sch)) : 0;
             if (c == 0) {
                 sum_g += gq;
                 sum_h += hq;
             }
             const uint32_t b = colp[r];
-            const uint64_t word = HCH ? ((uint64_t)gq << 32) + (uint64_t)hq : (uint64_t)gq;
-            const uint32_t lb = HCH ? (lbase | (buf << 7)) : lbase;
-            if (!SKIP || (int)b != d)
-                atomicAdd(reinterpret_cast<unsigned long long*>(lds + ((b << 8) | lb)), (unsigned long long)word);
+            const uint64_t word = PACK ? ((uint64_t)gq << 32) + (uint64_t)hq : (uint64_t)gq;
+            const uint32_t lb = PACK ? (lbase | (buf << 7)) : lbase;
+            if (!SKIP || (int)b != d) {
+                unsigned long long* const cp = reinterpret_cast<unsigned long long*>(lds + ((b << 8) | lb));
+                atomicAdd(cp, (unsigned long long)word);
+                if (MODE == ROOT_WIDE) atomicAdd(cp + HFL, (unsigned long long)hq);
+            }
         }
         __syncthreads();
-        if (HCH) unpack((int)buf);
+        if (PACK) unpack((int)buf);
     }
     __syncthreads();
-    if (!HCH) {   // one buffer, never unpacked: the cells are the g sums
+    if (!PACK) {   // never unpacked: the cells are the g sums (and the h sums)
 #pragma unroll
-        for (int k = 0; k < RENT; ++k) ag[k] = (int64_t)L.w[cell(k)];
+        for (int k = 0; k < RENT; ++k) {
+            ag[k] = (int64_t)L.w[cell(k)];
+            if (HCH) ah[k] = (int64_t)L.w[cell(k) + HFL];
+        }
     }
     if (totals) {
         sum_g = wave_sum<int64_t>(sum_g);
@@ -709,30 +732,37 @@ template <bool SKIP>
 static __global__ __attribute__((unused)) void __launch_bounds__(RBLOCK)
 k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld, const float* __restrict__ grad,
             const float* __restrict__ hess, int64_t n, int F, const Quant* q, double scg_v, double sch_v,
-            const int32_t* __restrict__ dflt, const uint32_t* __restrict__ counts, Quant* q_tot, int64_t* out,
-            int chunks, int tail, int64_t tail_rows, int count_mode, const int32_t* done) {
+            int wide_v, const int32_t* __restrict__ dflt, const uint32_t* __restrict__ counts, Quant* q_tot,
+            int64_t* out, int chunks, int tail, int64_t tail_rows, int count_mode, const int32_t* done) {
     const int32_t dn = done ? *done : 0;
     const double scg = q ? q->scg : scg_v, sch = q ? q->sch : sch_v;
     const bool no_h = count_mode && q && q->const_h;
+    const bool wide = q ? q->wide != 0 : wide_v != 0;
     if (dn) return;
     __shared__ HistLdsR L;   // 64 KB, also the flush's RootFlushLds
     static_assert(sizeof(RootFlushLds) <= sizeof(HistLdsR), "the flush reuses the cells' LDS");
     const int bid = (int)blockIdx.x;
     if (bid < tail) {
         if (no_h)
-            hist_root_tail<false, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
-                                        tail_rows, bid);
+            hist_root_tail<ROOT_G, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
+                                         tail_rows, bid);
+        else if (wide)
+            hist_root_tail<ROOT_WIDE, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
+                                            tail_rows, bid);
         else
-            hist_root_tail<true, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
-                                       tail_rows, bid);
+            hist_root_tail<ROOT_PACKED, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
+                                              tail_rows, bid);
         return;
     }
     if (no_h)
-        hist_root_gh<false, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks,
-                                  bid - tail);
+        hist_root_gh<ROOT_G, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks,
+                                   bid - tail);
+    else if (wide)
+        hist_root_gh<ROOT_WIDE, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks,
+                                      bid - tail);
     else
-        hist_root_gh<true, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks,
-                                 bid - tail);
+        hist_root_gh<ROOT_PACKED, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
+                                        chunks, bid - tail);
 }
 
 // Launch the root histogram (grid from root_grid) into the (3, F, 256)
@@ -742,9 +772,9 @@ k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld, const float* __rest
 // with the default-bin test runs only when dflt is given.
 static __attribute__((unused)) void launch_hist_root(hipStream_t stream, const uint8_t* bins_fm, int64_t ld,
                                                      const float* grad, const float* hess, int64_t n, int F,
-                                                     const Quant* q, double scg, double sch, const int32_t* dflt,
-                                                     const uint32_t* counts, Quant* q_tot, int64_t* out,
-                                                     int count_mode, const int32_t* done) {
+                                                     const Quant* q, double scg, double sch, int wide,
+                                                     const int32_t* dflt, const uint32_t* counts, Quant* q_tot,
+                                                     int64_t* out, int count_mode, const int32_t* done) {
     if (!counts) {
         const int tiles = (F + HFL - 1) / HFL;
         const int rc = root_chunks(n, tiles);
@@ -752,13 +782,13 @@ static __attribute__((unused)) void launch_hist_root(hipStream_t stream, const u
     }
     const RootGrid g = root_grid(n, F, grad, hess);
     if (dflt)
-        k_hist_root<true><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, dflt, counts,
-                                                           q_tot, out, g.chunks, g.tail, g.tail_rows, count_mode,
-                                                           done);
+        k_hist_root<true><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, wide, dflt,
+                                                           counts, q_tot, out, g.chunks, g.tail, g.tail_rows,
+                                                           count_mode, done);
     else
-        k_hist_root<false><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, nullptr,
-                                                            counts, q_tot, out, g.chunks, g.tail, g.tail_rows,
-                                                            count_mode, done);
+        k_hist_root<false><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, wide,
+                                                            nullptr, counts, q_tot, out, g.chunks, g.tail,
+                                                            g.tail_rows, count_mode, done);
 }
 
 // Rows of one node for a gather launch.
@@ -885,8 +915,8 @@ __device__ __forceinline__ void hist_gather_rows(GatherLds& LU, const uint8_t* _
         const uint4 bn = *reinterpret_cast<const uint4*>(tb + (size_t)r1 * ld);
         // step s
         const bool rok = i0 + lane < hi;
-        const int64_t gq = rok ? quantise_node(gx, scg) : 0;
-        const int64_t hq = (HCH && rok) ? quantise_node(hx, sch) : 0;
+        const int64_t gq = rok ? quantise_wide(gx, scg) : 0;
+        const int64_t hq = (HCH && rok) ? quantise_wide(hx, sch) : 0;
         const uint64_t one = rok ? 1 : 0;
         const uint64_t gw = HCH ? (uint64_t)gq : ((uint64_t)gq << cb) + one;
         const uint64_t pw = HCH ? ((uint64_t)hq << cb) + one : 0;
@@ -948,18 +978,20 @@ __device__ __forceinline__ void hist_gather_packed(GatherLds& L, const uint8_t* 
     hist_gather_rows<HCH, SKIP>(L, bins_rm, ld, grad, hess, F, scg, sch, dflt, rows, lo, hi, out, wlog, tile);
 }
 
-// job->active == 0 or *done != 0 (done may be NULL): nothing to do.  wlog:
-// pack_window_log2(n) for the n rows the shifts were chosen for.
+// job->active == 0 or *done != 0 (done may be NULL): nothing to do.  The
+// packing window is q->wlog, or wlog_v when q is NULL (window_log2(n, wide)
+// for the n rows and the contract the caller's shifts were chosen for).
 static __global__ __attribute__((unused)) void __launch_bounds__(HBLOCK) k_hist_gather(const uint8_t* __restrict__ bins_rm, int64_t ld,
                                                         const float* __restrict__ grad,
                                                         const float* __restrict__ hess, int F, const Quant* q,
                                                         double scg_v, double sch_v,
                                                         const int32_t* __restrict__ dflt, const HistJob* job,
-                                                        int count_mode, const int32_t* done, int wlog) {
+                                                        int count_mode, const int32_t* done, int wlog_v) {
     // independent loads first: the job record, the done flag, the shifts
     const HistJob jb = *job;
     const int32_t dn = done ? *done : 0;
     const double scg = q ? q->scg : scg_v, sch = q ? q->sch : sch_v;
+    const int wlog = q ? q->wlog : wlog_v;
     const bool no_h = count_mode && q && q->const_h;
     if (dn || !jb.active) return;
     const int tile = blockIdx.x / GATHER_MAX_CHUNKS, chunk = blockIdx.x % GATHER_MAX_CHUNKS;

@@ -72,7 +72,6 @@ constexpr int SPART_MAX_BLOCKS = 1024;
 
 __global__ void __launch_bounds__(OB) k_quant(const float* grad, const float* hess, int64_t n, Quant* q) {
     quant_reduce<OB>(grad, hess, n, q);
-    if (last_block(&q->ticket) && threadIdx.x == 0) quant_finish(q, n);
 }
 
 __global__ void k_fill_i64(int64_t* p, int64_t v, int64_t count) {
@@ -95,6 +94,7 @@ __global__ void k_set_hist_job(HistJob* j, const uint32_t* rows, int64_t lo, int
 __global__ void k_copy_shifts(const Quant* q, int32_t* out) {
     out[0] = q->sg;
     out[1] = q->sh;
+    out[2] = q->wide;
 }
 
 // ---- stable two-pass partition (input order kept on each side) ----
@@ -282,18 +282,19 @@ int hist_enqueue(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, 
     HistJob* job = c.take<HistJob>(1);
     k_quant_clear<<<1, 1, 0, stream>>>(q);
     k_quant<<<launch_grid(n, OB * 16, 1024), OB, 0, stream>>>(grad, hess, n, q);
+    k_quant_resid<OB><<<launch_grid(n, OB * 16, 1024), OB, 0, stream>>>(grad, hess, n, q);
     const int64_t ne = 3 * (int64_t)F * NB;
     k_fill_i64<<<launch_grid(ne, OB, 1024), OB, 0, stream>>>(out, 0, ne);
     const int tiles = (F + HFL - 1) / HFL;
     if (!rows) {
         if (n > 0) {
-            launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, q, 0.0, 0.0, nullptr, nullptr, nullptr, out, 0,
+            launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, q, 0.0, 0.0, 0, nullptr, nullptr, nullptr, out, 0,
                              nullptr);
         }
     } else if (m > 0) {
         k_set_hist_job<<<1, 1, 0, stream>>>(job, rows, 0, m, out);
         k_hist_gather<<<tiles * GATHER_MAX_CHUNKS, HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, q, 0.0, 0.0,
-                                                                        nullptr, job, 0, nullptr, pack_window_log2(n));
+                                                                        nullptr, job, 0, nullptr, 0);
     }
     k_copy_shifts<<<1, 1, 0, stream>>>(q, out_shifts);
     snprintf(msg, sizeof msg, "%s launch", who);
@@ -340,7 +341,7 @@ int yabt_hist(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int
 
 int yabt_hist_accumulate(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, int64_t ld_rm,
                          const float* grad, const float* hess, int64_t n, int F, const uint32_t* rows, int64_t m,
-                         int sg, int sh, void* workspace, int64_t* out, hipStream_t stream) {
+                         int sg, int sh, int wide, void* workspace, int64_t* out, hipStream_t stream) {
     if (!out || (rows && !workspace)) return fail(-2, "yabt_hist_accumulate: bad arguments");
     const int rc0 =
         check_hist_layout(bins_fm, ld_fm, bins_rm, ld_rm, grad, hess, n, F, rows, m, "yabt_hist_accumulate");
@@ -349,8 +350,8 @@ int yabt_hist_accumulate(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* b
     const int tiles = (F + HFL - 1) / HFL;
     if (!rows) {
         if (n > 0) {
-            launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, nullptr, scg, sch, nullptr, nullptr, nullptr,
-                             out, 0, nullptr);
+            launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, nullptr, scg, sch, wide, nullptr, nullptr,
+                             nullptr, out, 0, nullptr);
         }
     } else if (m > 0) {
         Carve c{(char*)workspace, 0};
@@ -358,7 +359,8 @@ int yabt_hist_accumulate(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* b
         HistJob* job = c.take<HistJob>(1);
         k_set_hist_job<<<1, 1, 0, stream>>>(job, rows, 0, m, out);
         k_hist_gather<<<tiles * GATHER_MAX_CHUNKS, HBLOCK, 0, stream>>>(bins_rm, ld_rm, grad, hess, F, nullptr, scg,
-                                                                        sch, nullptr, job, 0, nullptr, pack_window_log2(n));
+                                                                        sch, nullptr, job, 0, nullptr,
+                                                                        window_log2(n, wide != 0));
     }
     return launch_status("yabt_hist_accumulate launch");
 }
@@ -379,14 +381,14 @@ int yabt_bin_counts(const uint8_t* bins_fm, int64_t ld_fm, int64_t n, int F, uin
 }
 
 int yabt_hist_root(const uint8_t* bins_fm, int64_t ld_fm, const float* grad, const float* hess, int64_t n, int F,
-                   const uint32_t* bin_counts, int sg, int sh, int64_t* out, hipStream_t stream) {
+                   const uint32_t* bin_counts, int sg, int sh, int wide, int64_t* out, hipStream_t stream) {
     if (!out) return fail(-2, "yabt_hist_root: bad arguments");
     const int rc0 = check_hist_layout(bins_fm, ld_fm, nullptr, 0, grad, hess, n, F, nullptr, 0, "yabt_hist_root");
     if (rc0) return rc0;
     if (n > 0) {
         const RootGrid g = root_grid(n, F, grad, hess);
         k_hist_root<false><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld_fm, grad, hess, n, F, nullptr, ldexp(1.0, sg),
-                                                            ldexp(1.0, sh), nullptr, bin_counts, nullptr, out,
+                                                            ldexp(1.0, sh), wide, nullptr, bin_counts, nullptr, out,
                                                             g.chunks, g.tail, g.tail_rows, 0, nullptr);
     }
     return launch_status("yabt_hist_root launch");

@@ -589,8 +589,9 @@ def is_available() -> bool:
 # ---------------------------------------------------------------------------
 
 def hist(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor,
-         rows: torch.Tensor | None = None) -> tuple[torch.Tensor, tuple[int, int]]:
-    """Exact (3, F, 256) int64 histogram over ``rows`` (uint32/int) or all rows."""
+         rows: torch.Tensor | None = None) -> tuple[torch.Tensor, tuple[int, int, int]]:
+    """Exact (3, F, 256) int64 histogram over ``rows`` (uint32/int) or all rows,
+    with the shifts and the contract (sg, sh, wide) chosen from grad/hess."""
     lib = _lib.load()
     dev = lay.fm.device
     g = _dev_f32(grad, dev)
@@ -600,13 +601,13 @@ def hist(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor,
     if r is not None and m == 0:
         r = torch.zeros(1, dtype=torch.int32, device=dev)  # non-NULL: "no rows", not "all rows"
     out = torch.empty((3, lay.F, MAX_BINS), dtype=torch.int64, device=dev)
-    shifts = torch.zeros(2, dtype=torch.int32, device=dev)
+    shifts = torch.zeros(3, dtype=torch.int32, device=dev)
     ws = torch.empty(int(lib.yabt_hist_workspace_bytes()), dtype=torch.uint8, device=dev)
     _lib.check(lib.yabt_hist(_ptr(lay.fm), lay.ld_fm, _ptr(lay.rm), lay.ld_rm, _ptr(g), _ptr(h),
                              lay.n, lay.F, _ptr(r), m, _ptr(ws), _ptr(out), _ptr(shifts),
                              _stream(dev)), "yabt_hist")
     s = shifts.cpu().tolist()
-    return out, (int(s[0]), int(s[1]))
+    return out, (int(s[0]), int(s[1]), int(s[2]))
 
 
 def ref_root_hist(lay: BinLayouts, grad: torch.Tensor, hess: torch.Tensor) -> torch.Tensor:
