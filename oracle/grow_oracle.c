@@ -95,7 +95,7 @@ static inline int64_t quantise(float x, double scale)
 
 /* Residual and mass of one channel at the narrow shift s (the contract of
  * the exact grower, yabt_amd/csrc/common.h hist_shift / quant_resid):
- * R = sum rint(|y - rint(y)| * 2^21) and M = sum rint(|x| * 2^(s+10)) with
+ * R = sum rint(|y - rint(y)| * 2^21) and M = sum rint(|x| * 2^(s+1)) with
  * y = x * 2^s, every step exact in fp32 (power-of-two scalings and the
  * distance of y to its nearest integer), so R and M are exact integers. */
 static void resid_mass(const float *x, int64_t n, int s, uint64_t *r, uint64_t *m)
@@ -105,7 +105,7 @@ static void resid_mass(const float *x, int64_t n, int s, uint64_t *r, uint64_t *
         const float y = ldexpf(x[i], s);
         const float d = y - rintf(y);
         rr += (uint64_t)rintf(ldexpf(fabsf(d), 21));
-        mm += (uint64_t)rintf(ldexpf(fabsf(x[i]), s + 10));
+        mm += (uint64_t)rintf(ldexpf(fabsf(x[i]), s + 1));
     }
     *r = rr;
     *m = mm;
@@ -126,7 +126,8 @@ static int max_abs(const float *x, int64_t n, float *out)
 
 /* The per-call contract: the narrow shifts (or_hist_shift) when their
  * quantisation residual is at most 2^-17 of the mass for both channels
- * (64 R <= M), else the wide shifts (or_wide_shift).  out: sg, sh, wide;
+ * (R <= 8 M: R counts 2^-21 and M 2^-1 of a quantum), else the wide shifts
+ * (or_wide_shift).  out: sg, sh, wide;
  * sums (may be NULL): R_g, R_h, M_g, M_h.  Returns -1 on a non-finite value. */
 int or_hist_contract(const float *grad, const float *hess, int64_t n, int *out, uint64_t *sums)
 {
@@ -136,7 +137,7 @@ int or_hist_contract(const float *grad, const float *hess, int64_t n, int *out, 
     uint64_t rg, rh, mmg, mmh;
     resid_mass(grad, n, sgn, &rg, &mmg);
     resid_mass(hess, n, shn, &rh, &mmh);
-    const int narrow = 64 * rg <= mmg && 64 * rh <= mmh;
+    const int narrow = rg <= 8 * mmg && rh <= 8 * mmh;
     out[0] = narrow ? sgn : or_wide_shift(mg, n);
     out[1] = narrow ? shn : or_wide_shift(mh, n);
     out[2] = !narrow;

@@ -144,7 +144,7 @@ def _resid_mass_np(x, s):
     (every step below is exact in float64 for float32 inputs)."""
     y = x.astype(np.float64) * 2.0 ** s
     r = np.rint(np.abs(y - np.rint(y)) * 2.0 ** 21)
-    m = np.rint(np.abs(x.astype(np.float64)) * 2.0 ** (s + 10))
+    m = np.rint(np.abs(x.astype(np.float64)) * 2.0 ** (s + 1))
     return int(r.sum()), int(m.sum())
 
 
@@ -152,7 +152,7 @@ def _resid_mass_np(x, s):
                                     *[(k, 20_000) for k in WIDE_KINDS]])
 def test_hist_contract_against_numpy(kind, n):
     """or_hist_contract's residuals and masses equal an independent float64
-    restatement, its decision is 64 R <= M on both channels, and its shifts
+    restatement, its decision is R <= 8 M on both channels, and its shifts
     are the narrow or the wide ones accordingly; the outlier and heavy-tailed
     kinds select wide, the well-scaled ones narrow."""
     rng = np.random.default_rng(n)
@@ -163,7 +163,7 @@ def test_hist_contract_against_numpy(kind, n):
     rg, mg = _resid_mass_np(g, sgn)
     rh, mh = _resid_mass_np(h, shn)
     assert sums == (rg, rh, mg, mh)
-    assert wide == int(not (64 * rg <= mg and 64 * rh <= mh))
+    assert wide == int(not (rg <= 8 * mg and rh <= 8 * mh))
     assert wide == int(kind in WIDE_KINDS)
     if wide:
         assert (sg, sh) == (O.wide_shift(float(np.abs(g).max()), n), O.wide_shift(float(np.abs(h).max()), n))
@@ -174,7 +174,7 @@ def test_hist_contract_against_numpy(kind, n):
 
 def test_hist_contract_closed_form():
     """Values on the narrow grid have no residual (narrow); a value of half a
-    narrow quantum rounds to 0 (ties to even) with residual 2^20 and mass 2^9
+    narrow quantum rounds to 0 (ties to even) with residual 2^20 and mass 1
     in the contract's units, so enough of them select wide; all zeros keep
     shift 0 and narrow."""
     n = 4096
@@ -183,15 +183,15 @@ def test_hist_contract_closed_form():
     h = np.ones(n, np.float32)
     sg, sh, wide, sums = O.hist_contract(g, h)
     assert (sg, sh, wide) == (18, 18, 0) and sums[0] == sums[1] == 0
-    m_grid = int((np.abs(grid.astype(np.float64)) * 2.0 ** 28).sum()) * (n // 4)
-    assert sums[2] == m_grid and sums[3] == n * 2 ** 28
+    m_grid = int((np.abs(grid.astype(np.float64)) * 2.0 ** 19).sum()) * (n // 4)
+    assert sums[2] == m_grid and sums[3] == n * 2 ** 19
     for k, want_wide in ((200, 0), (3500, 1)):
         g2 = g.copy()
         g2[:k] = np.float32(2.0 ** -19)
         _, _, wide2, (rg, _, mg, _) = O.hist_contract(g2, h)
         assert rg == k * 2 ** 20
-        assert mg == m_grid - int((np.abs(g[:k].astype(np.float64)) * 2.0 ** 28).sum()) + k * 2 ** 9
-        assert wide2 == want_wide == int(64 * rg > mg)
+        assert mg == m_grid - int((np.abs(g[:k].astype(np.float64)) * 2.0 ** 19).sum()) + k
+        assert wide2 == want_wide == int(rg > 8 * mg)
     assert O.hist_contract(np.zeros(8, np.float32), np.zeros(8, np.float32))[:3] == (0, 0, 0)
 
 

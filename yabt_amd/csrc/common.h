@@ -42,10 +42,10 @@ __host__ __device__ inline int quant_shift(float maxabs, int64_t n) {
 //     <= n values stays below 2^61; g and h take a 64-bit LDS cell each.
 // The narrow contract is used only when its quantisation residual is small
 // against the data: per channel, R = sum rint(|x 2^s - rint(x 2^s)| 2^21)
-// and M = sum rint(|x| 2^(s + 10)) at the narrow shift s (exact integers,
-// so the decision does not depend on any order), narrow iff 64 R <= M for
+// and M = sum rint(|x| 2^(s + 1)) at the narrow shift s (exact integers,
+// so the decision does not depend on any order), narrow iff R <= 8 M for
 // both g and h, i.e. sum |x - q 2^-s| <= 2^-17 sum |x| up to the rounding of
-// the two integer sums.  One large value among small ones (an outlier,
+// the two integer sums (M counts half quanta, so it errs towards wide).  One large value among small ones (an outlier,
 // heavy-tailed targets) makes q coarse against most rows and selects wide.
 // Shared with oracle/grow_oracle.c (or_hist_shift, or_wide_shift,
 // or_hist_contract).
@@ -414,6 +414,28 @@ __device__ inline bool last_block(uint32_t* ticket) {
     return s_last != 0;
 }
 
+// last_block for grids in which only wave 0 of each block has written global
+// memory before the call: that wave alone releases its writes (an agent-scope
+// fence costs ~14 ns per fencing wave and the fences of a grid serialise, so
+// fencing every wave of 256 1024-thread blocks costs ~60 us); the last block
+// then acquires with every wave.
+__device__ inline bool last_block_w0(uint32_t* ticket) {
+    __shared__ int s_last;
+    if (threadIdx.x < WAVE) {
+        __threadfence();
+        if (threadIdx.x == 0) {
+            const uint32_t t = atomicAdd(ticket, 1u);
+            s_last = (t == gridDim.x * gridDim.y - 1);
+        }
+    }
+    __syncthreads();
+    if (s_last) {
+        __threadfence();
+        if (threadIdx.x == 0) *ticket = 0;
+    }
+    return s_last != 0;
+}
+
 // ---------------------------------------------------------------------------
 // quantisation passes
 // ---------------------------------------------------------------------------
@@ -524,14 +546,16 @@ __device__ void quant_reduce(const float* grad, const float* hess, int64_t n, Qu
 
 // Residual and mass of one value at the narrow shift s (hist_shift's notes):
 // x 2^s and its distance to the nearest integer are exact in fp32, and so are
-// the power-of-two scalings; rint(|d| 2^21) <= 2^20, rint(|x| 2^(s + 10)) <=
-// 2^40.  Non-finite values add nothing (the call reports them and stops).
+// the power-of-two scalings; rint(|d| 2^21) <= 2^20 and rint(|x| 2^(s + 1))
+// <= 2^31 (|x 2^s| <= 2^30), so both convert to 32 bits exactly.  Non-finite
+// values add nothing (the call reports them and stops); no branch.
 __device__ __forceinline__ void resid_take(float x, int s, uint64_t& r, uint64_t& m) {
-    if (!isfinite(x)) return;
+    const bool ok = isfinite(x);
     const float y = ldexpf(x, s);
-    const float d = y - rintf(y);
-    r += (uint64_t)rintf(ldexpf(fabsf(d), 21));
-    m += (uint64_t)rintf(ldexpf(fabsf(x), s + 10));
+    const float d = ok ? fabsf(y - rintf(y)) : 0.0f;
+    const float a = ok ? fabsf(x) : 0.0f;
+    r += (uint32_t)rintf(ldexpf(d, 21));
+    m += (uint32_t)rintf(ldexpf(a, s + 1));
 }
 
 // Grid-stride residuals and masses of g and h at the narrow shifts, after
@@ -608,9 +632,10 @@ __device__ void quant_resid(const float* grad, const float* hess, int64_t n, Qua
 }
 
 // The contract of hist_shift's notes from the residuals: narrow iff
-// 64 R <= M for both channels (R <= n 2^20 < 2^52, so 64 R cannot wrap).
+// R <= 8 M for both channels (M <= n 2^31 < 2^63 / 8 for n < 2^32 rows,
+// so 8 M cannot wrap).
 __host__ __device__ inline bool narrow_contract(uint64_t rg, uint64_t mg, uint64_t rh, uint64_t mh) {
-    return 64 * rg <= mg && 64 * rh <= mh;
+    return rg <= 8 * mg && rh <= 8 * mh;
 }
 
 __device__ inline void quant_finish(Quant* q, int64_t n) {
@@ -655,12 +680,23 @@ static __global__ __attribute__((unused)) void k_quant_clear(Quant* q) {
 }
 
 // Second pass of the per-call quantisation: residuals for the contract
-// (quant_resid), then, in the grid's last block, quant_finish.
-template <int NT>
-static __global__ __attribute__((unused)) void __launch_bounds__(NT)
+// (quant_resid), then, in the grid's last block, quant_finish.  Blocks of
+// 1024 threads, at most 256 of them: every block adds its four sums into
+// four words of one cache line, and those atomics serialise.
+constexpr int QRB = 1024;
+static __global__ __attribute__((unused)) void __launch_bounds__(QRB)
 k_quant_resid(const float* grad, const float* hess, int64_t n, Quant* q) {
-    quant_resid<NT>(grad, hess, n, q);
-    if (last_block(&q->ticket) && threadIdx.x == 0) quant_finish(q, n);
+    quant_resid<QRB>(grad, hess, n, q);   // global writes: wave 0's four atomics
+    if (last_block_w0(&q->ticket) && threadIdx.x == 0) quant_finish(q, n);
+}
+
+// Enqueue k_quant_resid after the pass that filled q's maxima.
+static __attribute__((unused)) void launch_quant_resid(hipStream_t stream, const float* grad, const float* hess,
+                                                       int64_t n, Quant* q) {
+    const int64_t per = (int64_t)QRB * 16;   // rows per block, at least
+    int64_t blocks = (n + per - 1) / per;
+    blocks = blocks < 1 ? 1 : (blocks > 256 ? 256 : blocks);
+    k_quant_resid<<<(unsigned)blocks, QRB, 0, stream>>>(grad, hess, n, q);
 }
 
 }  // namespace yabt

@@ -1570,7 +1570,7 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
     const int tiles = (F + HFL - 1) / HFL;
     k_quant_clear<<<1, 1, 0, stream>>>(A.q);
     k_setup<<<launch_grid(n, SB * 16, 1024), SB, 0, stream>>>(A);
-    k_quant_resid<SB><<<launch_grid(n, SB * 16, 1024), SB, 0, stream>>>(grad, hess, n, A.q);
+    launch_quant_resid(stream, grad, hess, n, A.q);
     k_setup_finish<<<1, 1, 0, stream>>>(A);
     launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, A.q, 0.0, 0.0, 0, A.dflt, A.counts, A.q, A.hist, 1,
                      &A.st->done);

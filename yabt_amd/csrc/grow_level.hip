@@ -545,7 +545,7 @@ int yabt_grow_levelwise(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bi
     k_quant_clear<<<1, 1, 0, stream>>>(w.q);
     k_setup<<<launch_grid(max(n, (int64_t)slot_n), LB * 16, 1024), LB, 0, stream>>>(
         grad, hess, n, w.q, w.row_node, w.route, NP, w.path, (int64_t)NP * F, w.hist, (int64_t)slot_n);
-    k_quant_resid<LB><<<launch_grid(n, LB * 16, 1024), LB, 0, stream>>>(grad, hess, n, w.q);
+    launch_quant_resid(stream, grad, hess, n, w.q);
     k_setup_finish<<<1, 1, 0, stream>>>(w.q, n, w.nodes, w.scan_list, out_status);
     if (n > 0) {
         launch_hist_root(stream, bins_fm, ld_fm, grad, hess, n, F, w.q, 0.0, 0.0, 0, nullptr, bin_counts, w.q, w.hist,

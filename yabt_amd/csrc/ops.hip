@@ -282,7 +282,7 @@ int hist_enqueue(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm, 
     HistJob* job = c.take<HistJob>(1);
     k_quant_clear<<<1, 1, 0, stream>>>(q);
     k_quant<<<launch_grid(n, OB * 16, 1024), OB, 0, stream>>>(grad, hess, n, q);
-    k_quant_resid<OB><<<launch_grid(n, OB * 16, 1024), OB, 0, stream>>>(grad, hess, n, q);
+    launch_quant_resid(stream, grad, hess, n, q);
     const int64_t ne = 3 * (int64_t)F * NB;
     k_fill_i64<<<launch_grid(ne, OB, 1024), OB, 0, stream>>>(out, 0, ne);
     const int tiles = (F + HFL - 1) / HFL;
