@@ -70,32 +70,30 @@ def sparse_regression(n, F, seed):
 
 
 # The reference's sparse-layout helpers live in yabt/grow_numba.py, whose
-# import needs numba (absent here); these two follow them step for step.
+# import needs numba (absent here); these two compute the same layout and
+# density from the binned matrix.
 def build_sparse_layout(binned):
-    """yabt/grow_numba.py:341-367: per-feature most common bin (np.argmax of
-    the counts: lowest on ties) and the row-major CSR of the other cells."""
-    bn = np.ascontiguousarray(binned.detach().cpu().numpy())
-    n, F = bn.shape
-    counts = np.zeros((F, 256), dtype=np.int64)
-    np.add.at(counts, (np.arange(F)[None, :].repeat(n, 0).ravel(), bn.ravel()), 1)
-    default_bin = counts.argmax(axis=1).astype(np.int64)
-    nondef = bn != default_bin[None, :].astype(bn.dtype)
-    indptr = np.zeros(n + 1, dtype=np.int64)
-    np.cumsum(nondef.sum(axis=1), out=indptr[1:])
-    rows_idx, cols_idx = np.nonzero(nondef)
-    return indptr, cols_idx.astype(np.int64), bn[rows_idx, cols_idx].astype(np.int64), default_bin
+    """The CSR layout of yabt/grow_numba.py:341-367: default_bin[f] is column
+    f's most frequent bin (the lowest of equally frequent ones), and row r's
+    explicit cells are its columns whose bin differs, in column order, as
+    (indptr, indices, data, default_bin), all int64."""
+    b = np.ascontiguousarray(binned.detach().cpu().numpy())
+    n, F = b.shape
+    default_bin = np.array([np.bincount(b[:, f], minlength=256).argmax() for f in range(F)], dtype=np.int64)
+    r, c = np.nonzero(b != default_bin.astype(b.dtype))     # row-major: grouped by row, columns ascending
+    indptr = np.searchsorted(r, np.arange(n + 1)).astype(np.int64)
+    return indptr, c.astype(np.int64), b[r, c].astype(np.int64), default_bin
 
 
 def estimate_density(binned, sample_rows=4096):
-    """yabt/grow_numba.py:375-395: non-modal share over linspace-sampled rows."""
-    bn = binned.detach().cpu().numpy()
-    n, F = bn.shape
-    if n > sample_rows:
-        bn = bn[np.linspace(0, n - 1, sample_rows).astype(np.int64)]
-    m = bn.shape[0]
-    counts = np.zeros((F, 256), dtype=np.int64)
-    np.add.at(counts, (np.arange(F)[None, :].repeat(m, 0).ravel(), bn.ravel()), 1)
-    return float(1.0 - counts.max(axis=1).sum() / max(1, m * F))
+    """yabt/grow_numba.py:375-395's estimate: the share of cells outside their
+    column's most frequent bin, over an evenly spaced sample of at most
+    sample_rows rows (np.linspace indices, truncated)."""
+    b = binned.detach().cpu().numpy()
+    if b.shape[0] > sample_rows:
+        b = b[np.linspace(0, b.shape[0] - 1, sample_rows).astype(np.int64)]
+    modal = sum(int(np.bincount(col, minlength=256).max()) for col in b.T)
+    return float(1.0 - modal / max(1, b.size))
 
 
 def digest(*arrays) -> str:

@@ -80,3 +80,48 @@ def test_two_threads_grow_their_own_trees():
         t.join(timeout=100)
     assert not any(t.is_alive() for t in threads), "a grower thread did not finish"
     assert not errors, errors
+
+
+def test_first_use_of_a_fresh_layout_on_two_streams():
+    """Two threads, each on its own stream, make a fresh layout's lazily built
+    tables (bin counts, default bins, the reference root rank table) at the
+    same time; every tree equals the one grown alone on another layout of
+    the same bins."""
+    n, F, nb = 120_000, 36, 256
+    rng = np.random.default_rng(11)
+    bins_np = rng.integers(0, nb, size=(n, F)).astype(np.uint8)
+    bins_np[rng.random((n, F)) < 0.6] = 0      # a modal bin worth skipping
+    bins = torch.from_numpy(bins_np)
+    g = torch.from_numpy(rng.normal(size=n).astype(np.float32)).to(DEV)
+    h = torch.from_numpy(rng.uniform(0.1, 1.0, size=n).astype(np.float32)).to(DEV)
+    nbins = np.full(F, nb, np.int32)
+    kws = [dict(max_leaves=63), dict(max_leaves=31, arithmetic="reference")]
+    lone = G.make_layouts(bins, DEV)
+    torch.cuda.synchronize()
+    alone = [_grow((n, F, nb, 0, kw), (lone, g, h, nbins)) for kw in kws]
+    for rep in range(3):
+        fresh = G.make_layouts(bins, DEV)
+        torch.cuda.synchronize()
+        barrier = threading.Barrier(2)
+        errors = []
+
+        def worker(tid):
+            try:
+                stream = torch.cuda.Stream(device=DEV)   # default priority
+                with torch.cuda.stream(stream):
+                    barrier.wait(timeout=60)
+                    for k in (tid, 1 - tid):
+                        got = _grow((n, F, nb, 0, kws[k]), (fresh, g, h, nbins))
+                        if not _same(got, alone[k]):
+                            errors.append(f"rep {rep} thread {tid}: grower {k} differs from its lone run")
+            except Exception as e:  # noqa: BLE001 - reported by the main thread
+                errors.append(f"rep {rep} thread {tid}: {e!r}")
+
+        print(f"fresh layout, two streams, rep {rep}", flush=True)
+        threads = [threading.Thread(target=worker, args=(t,)) for t in range(2)]
+        for t in threads:
+            t.start()
+        for t in threads:
+            t.join(timeout=100)
+        assert not any(t.is_alive() for t in threads), "a grower thread did not finish"
+        assert not errors, errors

@@ -23,6 +23,7 @@ missing, ``grow_tree_hip`` raises.
 
 from __future__ import annotations
 
+import collections
 import ctypes
 import threading
 import weakref
@@ -54,21 +55,31 @@ def _stream(dev: torch.device):
 
 
 # Read-only device tensors every call would otherwise rebuild (the all-ones
-# feature mask, the unused interaction matrix, a layout's bin counts): made
-# once per device and value, complete before first use, never written (the
-# C ABI takes them as const).
-_DEV_CONST: dict = {}
+# feature mask, the unused interaction matrix, an nbins table): made once per
+# device and value, complete before first use (the making stream is waited
+# for), never written (the C ABI takes them as const).  Shared by every host
+# thread under a lock; at most _DEV_CONST_MAX entries, least recently used
+# first out.  Each use records the caller's stream on the tensor, so when an
+# evicted entry's memory returns to torch's caching allocator it is not
+# reused before the kernels already enqueued on those streams have run.
+_DEV_CONST: collections.OrderedDict = collections.OrderedDict()
+_DEV_CONST_LOCK = threading.Lock()
+_DEV_CONST_MAX = 256
 
 
 def _dev_const(key, make) -> torch.Tensor:
-    t = _DEV_CONST.get(key)
-    if t is None:
-        if len(_DEV_CONST) >= 256:
-            _DEV_CONST.clear()
-        t = make()
-        torch.cuda.current_stream(t.device).synchronize()
-        _DEV_CONST[key] = t
-    return t
+    with _DEV_CONST_LOCK:
+        t = _DEV_CONST.get(key)
+        if t is None:
+            t = make()
+            torch.cuda.current_stream(t.device).synchronize()
+            _DEV_CONST[key] = t
+            if len(_DEV_CONST) > _DEV_CONST_MAX:
+                _DEV_CONST.popitem(last=False)
+        else:
+            _DEV_CONST.move_to_end(key)
+        t.record_stream(torch.cuda.current_stream(t.device))
+        return t
 
 
 def _dev_f32(t: torch.Tensor, dev: torch.device) -> torch.Tensor:
@@ -95,6 +106,15 @@ class BinLayouts:
         self._default = None
         self._counts = None
         self._root_order = None
+        # The lazily made tables below are shared by every host thread that
+        # grows on this layout, each on its own stream: one thread makes a
+        # table under the lock, waits for its stream, and only then publishes
+        # it, so a kernel on another stream never reads it half written.
+        self._lock = threading.Lock()
+
+    def _publish(self, t: torch.Tensor) -> torch.Tensor:
+        torch.cuda.current_stream(self.fm.device).synchronize()
+        return t
 
     def counts(self) -> torch.Tensor:
         """Per-(feature, bin) row counts (F, 256) uint32 of the bins, counted
@@ -102,30 +122,48 @@ class BinLayouts:
         histogram over these bins, which the growers take instead of
         recounting the rows each tree."""
         if self._counts is None:
-            lib = _lib.load()
-            dev = self.fm.device
-            c = torch.empty((self.F, MAX_BINS), dtype=torch.int32, device=dev)
-            _lib.check(lib.yabt_bin_counts(_ptr(self.fm), self.ld_fm, self.n, self.F, _ptr(c), _stream(dev)),
-                       "yabt_bin_counts")
-            self._counts = c
+            with self._lock:
+                if self._counts is None:
+                    lib = _lib.load()
+                    dev = self.fm.device
+                    c = torch.empty((self.F, MAX_BINS), dtype=torch.int32, device=dev)
+                    _lib.check(lib.yabt_bin_counts(_ptr(self.fm), self.ld_fm, self.n, self.F, _ptr(c),
+                                                   _stream(dev)), "yabt_bin_counts")
+                    self._counts = self._publish(c)
         return self._counts
 
     def ref_root_order(self) -> torch.Tensor:
         """The root rank table of the reference-arithmetic grower's dense
         builder (yabt_ref_root_order), built once per layout: each row's rank
         in its bin inside its 4096-row tile, per feature, which every tree's
-        root histogram on these bins reuses."""
+        root histogram on these bins reuses.  F * ceil(n / 4096) * 4096
+        uint16 ranks plus the tiles' bin starts (yabt_ref_root_order_bytes):
+        2.0 GB at 10M rows x 100 features, kept until the layout dies or
+        release_ref_root_order() drops it."""
         if self._root_order is None:
-            lib = _lib.load()
-            dev = self.fm.device
-            nbytes = int(lib.yabt_ref_root_order_bytes(self.n, self.F))
-            if nbytes == 0:
-                raise ValueError("yabt_ref_root_order: invalid sizes")
-            buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
-            _lib.check(lib.yabt_ref_root_order(_ptr(self.fm), self.ld_fm, self.n, self.F, _ptr(buf), nbytes,
-                                               _stream(dev)), "yabt_ref_root_order")
-            self._root_order = buf
+            with self._lock:
+                if self._root_order is None:
+                    lib = _lib.load()
+                    dev = self.fm.device
+                    nbytes = int(lib.yabt_ref_root_order_bytes(self.n, self.F))
+                    if nbytes == 0:
+                        raise ValueError("yabt_ref_root_order: invalid sizes")
+                    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+                    _lib.check(lib.yabt_ref_root_order(_ptr(self.fm), self.ld_fm, self.n, self.F, _ptr(buf),
+                                                       nbytes, _stream(dev)), "yabt_ref_root_order")
+                    self._root_order = self._publish(buf)
         return self._root_order
+
+    def release_ref_root_order(self) -> None:
+        """Drop the reference-arithmetic root rank table (the largest per-fit
+        table, see ref_root_order); the next reference-arithmetic tree on this
+        layout rebuilds it.  Call it when no grower on this layout is running:
+        the memory goes back to torch's caching allocator (the device is
+        waited for first, so no enqueued kernel can still read it)."""
+        with self._lock:
+            if self._root_order is not None:
+                torch.cuda.synchronize(self.fm.device)
+                self._root_order = None
 
     # a default bin is skipped only where it holds at least this share of the
     # sampled rows; below it the per-update test costs more than it saves
@@ -138,21 +176,24 @@ class BinLayouts:
         None when no feature qualifies.  Any choice gives identical
         histograms; this one skips the most rows where skipping pays."""
         if self._default is None:
-            F, n = self.F, self.n
-            if n == 0:
-                self._default = False
-            else:
-                idx = torch.linspace(0, n - 1, min(n, sample), device=self.fm.device).long()
-                cols = self.fm[:, idx].long()                       # (F, s)
-                counts = torch.zeros((F, MAX_BINS), dtype=torch.int64, device=self.fm.device)
-                counts.scatter_add_(1, cols, torch.ones_like(cols))
-                top, arg = counts.max(dim=1)
-                frequent = top.double() >= self.SKIP_MIN_SHARE * idx.numel()
-                if bool(frequent.any()):
-                    self._default = torch.where(frequent, arg, torch.full_like(arg, -1)).to(torch.int32).contiguous()
-                else:
-                    self._default = False
+            with self._lock:
+                if self._default is None:
+                    self._default = self._make_default_bin(sample)
         return self._default if self._default is not False else None
+
+    def _make_default_bin(self, sample: int):
+        F, n = self.F, self.n
+        if n == 0:
+            return False
+        idx = torch.linspace(0, n - 1, min(n, sample), device=self.fm.device).long()
+        cols = self.fm[:, idx].long()                       # (F, s)
+        counts = torch.zeros((F, MAX_BINS), dtype=torch.int64, device=self.fm.device)
+        counts.scatter_add_(1, cols, torch.ones_like(cols))
+        top, arg = counts.max(dim=1)
+        frequent = top.double() >= self.SKIP_MIN_SHARE * idx.numel()
+        if not bool(frequent.any()):   # waits for the stream
+            return False
+        return self._publish(torch.where(frequent, arg, torch.full_like(arg, -1)).to(torch.int32).contiguous())
 
 
 def make_layouts(binned: torch.Tensor, dev: torch.device,
@@ -183,6 +224,9 @@ def layouts_for(binned: torch.Tensor, dev: torch.device,
         if hit is not None and hit[0] == key_state:
             return hit[1]
     lay = make_layouts(binned, dev, binned_fmajor)
+    # the copies and the transpose ran on this thread's stream; the cached
+    # layout may be used from other streams next
+    torch.cuda.current_stream(dev).synchronize()
     with _CACHE_LOCK:
         if key not in _LAYOUTS:
             # runs when binned dies, before its id can be reused
