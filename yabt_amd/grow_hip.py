@@ -210,6 +210,9 @@ def make_layouts(binned: torch.Tensor, dev: torch.device,
     lib = _lib.load()
     _lib.check(lib.yabt_transpose_bins(_ptr(fm), ld_fm, n, F, _ptr(rm), ld_rm, _stream(dev)),
                "yabt_transpose_bins")
+    # the copies and the transpose ran on this thread's stream; the layouts
+    # may be used from other streams next (layouts_for shares them)
+    torch.cuda.current_stream(dev).synchronize()
     return BinLayouts(fm, rm, n, F)
 
 
@@ -224,9 +227,6 @@ def layouts_for(binned: torch.Tensor, dev: torch.device,
         if hit is not None and hit[0] == key_state:
             return hit[1]
     lay = make_layouts(binned, dev, binned_fmajor)
-    # the copies and the transpose ran on this thread's stream; the cached
-    # layout may be used from other streams next
-    torch.cuda.current_stream(dev).synchronize()
     with _CACHE_LOCK:
         if key not in _LAYOUTS:
             # runs when binned dies, before its id can be reused
