@@ -73,12 +73,19 @@ class Binner:
         X = np.asarray(X, dtype=np.float32)
         return np.where(np.isnan(X), self.medians_, X).astype(np.float32)
 
-    def transform(self, X: np.ndarray) -> np.ndarray:
-        """(n, F) uint8, bin = #{edges < x} (searchsorted, left)."""
-        Xi = self.impute(X)
+    def transform(self, X: np.ndarray, imputed: bool = False) -> np.ndarray:
+        """(n, F) uint8, bin = #{edges < x} (searchsorted, left); features in
+        a thread pool (searchsorted releases the GIL).  ``imputed``: X is
+        already impute(X)."""
+        from concurrent.futures import ThreadPoolExecutor
+        Xi = np.asarray(X, np.float32) if imputed else self.impute(X)
         out = np.empty(Xi.shape, np.uint8)
-        for f, e in enumerate(self.edges_):
-            out[:, f] = np.searchsorted(e, Xi[:, f], side="left").astype(np.uint8)
+
+        def one(f):
+            out[:, f] = np.searchsorted(self.edges_[f], Xi[:, f], side="left").astype(np.uint8)
+
+        with ThreadPoolExecutor(max_workers=8) as ex:
+            list(ex.map(one, range(len(self.edges_))))
         return out
 
     def nbins(self) -> np.ndarray:
@@ -275,24 +282,37 @@ def tree_output(tree: dict, X: np.ndarray, node: np.ndarray) -> np.ndarray:
 # the loop
 # --------------------------------------------------------------------------
 
+def prepare(X: np.ndarray, max_bins: int = 256) -> tuple:
+    """(binner, bins (n, F) uint8, imputed X) of Booster.fit's set-up
+    (boosting.py:305-307): what depends only on X and max_bins."""
+    binner = Binner(max_bins).fit(X)
+    Xr = binner.impute(X)
+    return binner, binner.transform(Xr, imputed=True), Xr
+
+
 def fit(X: np.ndarray, y: np.ndarray, *, loss: str = "mse", n_estimators: int = 10, learning_rate: float = 0.1,
         max_leaves: int = 31, max_depth: int = 64, reg_lambda: float = 1.0, gamma: float = 0.0,
         min_child_weight: float = 1e-3, min_samples_leaf: int = 20, max_bins: int = 256,
         subsample: float = 1.0, colsample: float = 1.0, seed: int = 0,
         interaction_aware: bool = True, interaction_boost: float = 0.5, neural_leaves: bool = True,
         leaf_net_features: int = 8, leaf_net_l2: float = 1.0, leaf_net_min_samples: int = 50,
-        sparse_hist="auto", sparse_hist_max_density: float = 0.5, mode: int = O.MODE_FIXED) -> dict:
+        sparse_hist="auto", sparse_hist_max_density: float = 0.5, mode: int = O.MODE_FIXED,
+        prepared: tuple | None = None, on_tree=None) -> dict:
     """Booster.fit (boosting.py:271-534).  Row and column samples are drawn
     from a CPU torch generator seeded with ``seed``, rows first, by the same
     calls as the reference (boosting.py:369-383).  Trees grown on all rows
     use the sparse histogram builder when ``sparse_hist`` is True, or "auto"
     and the estimated density is at most ``sparse_hist_max_density``
-    (boosting.py:240-258, 438-439); it changes only the fp32 mode's sums."""
+    (boosting.py:240-258, 438-439); it changes only the fp32 mode's sums.
+    ``prepared``: prepare(X, max_bins) for this X, shared by one-vs-rest
+    classes (multiclass.py:25-33 fits every class's binner on the same X).
+    ``on_tree``: called after each tree as on_tree(t, inputs, grown) with the
+    tree's grower inputs (dict: g, h, imat, fmask, rows, margin before the
+    tree) and the grower's trace (O.grow's dict) -- for tests that grow the
+    same tree another way."""
     import torch
     gen = torch.Generator(device="cpu").manual_seed(seed)
-    binner = Binner(max_bins).fit(X)
-    bins = binner.transform(X)
-    Xr = binner.impute(X)
+    binner, bins, Xr = prepared if prepared is not None else prepare(X, max_bins)
     yt = np.asarray(y, np.float32)
     n, F = Xr.shape
     bins_fm = np.ascontiguousarray(bins.T)
@@ -321,6 +341,8 @@ def fit(X: np.ndarray, y: np.ndarray, *, loss: str = "mse", n_estimators: int = 
                    sparse=sl if rows is None else None,
                    lam=reg_lambda, gamma=gamma, mcw=min_child_weight, msl=min_samples_leaf,
                    lr=learning_rate, max_leaves=max_leaves, max_depth=max_depth)
+        if on_tree is not None:
+            on_tree(len(trees), dict(g=g, h=h, imat=imat, fmask=fmask, rows=rows, margin=margin.copy()), t)
         tree = {k: t[k] for k in ("feature", "thr_bin", "left", "right", "value")}
         tree["threshold"] = thresholds(binner, tree["feature"], tree["thr_bin"])
         if rows is None:

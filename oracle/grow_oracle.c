@@ -591,7 +591,7 @@ int or_grow(int mode, const uint8_t *bins_fm, const float *grad, const float *he
             int64_t *o_feature, int64_t *o_thr, int64_t *o_left, int64_t *o_right,
             float *o_value, int64_t *o_depth,
             int64_t *rows_out, int64_t *seg_lo, int64_t *seg_hi, double *split_gain,
-            int *quant)
+            int *quant, void *hist_out)
 {
 #ifdef _OPENMP
     if (n_threads > 0) omp_set_num_threads(n_threads);
@@ -762,6 +762,11 @@ int or_grow(int mode, const uint8_t *bins_fm, const float *grad, const float *he
         for (int i = 0; i < n_nodes; ++i) seg_lo[i] = lo[i];
     if (seg_hi)
         for (int i = 0; i < n_nodes; ++i) seg_hi[i] = hi[i];
+    /* every node's histogram as the grower held it when it scanned the node
+     * (fp32 or fixed point by mode; a split node's slot is not reused) */
+    if (hist_out)
+        memcpy(hist_out, mode == OR_MODE_FP32 ? (void *)G.hf : (void *)G.hq,
+               (size_t)n_nodes * G.slot * (mode == OR_MODE_FP32 ? sizeof(float) : sizeof(int64_t)));
 
 done:
     free(lo);

@@ -22,12 +22,19 @@ def counts(leaf: np.ndarray, n_nodes: int) -> np.ndarray:
 
 def envelopes(Xs: np.ndarray, leaf: np.ndarray, n_nodes: int):
     """Per-node min / max of the raw inputs, +inf / -inf for empty nodes
-    (scatter_reduce amin / amax with include_self, neural_leaves.py:170-176)."""
+    (scatter_reduce amin / amax with include_self, neural_leaves.py:170-176).
+    Rows grouped by node (a stable sort), then one min and one max per run."""
     K = Xs.shape[1]
     lo = np.full((n_nodes, K), np.inf, np.float32)
     hi = np.full((n_nodes, K), -np.inf, np.float32)
-    np.minimum.at(lo, leaf, Xs.astype(np.float32))
-    np.maximum.at(hi, leaf, Xs.astype(np.float32))
+    if leaf.size == 0:
+        return lo, hi
+    order = np.argsort(leaf, kind="stable")
+    sl = leaf[order]
+    starts = np.concatenate([[0], np.nonzero(np.diff(sl))[0] + 1])
+    Xo = Xs.astype(np.float32)[order]
+    lo[sl[starts]] = np.minimum.reduceat(Xo, starts, axis=0)
+    hi[sl[starts]] = np.maximum.reduceat(Xo, starts, axis=0)
     return lo, hi
 
 
@@ -54,8 +61,14 @@ def gram(Xn: np.ndarray, g: np.ndarray, h: np.ndarray, leaf: np.ndarray, n_nodes
     rhs = -(X1 * g.astype(np.float64)[:, None])
     M = np.zeros((n_nodes, K + 1, K + 1))
     b = np.zeros((n_nodes, K + 1))
-    np.add.at(M, leaf, X1[:, :, None] * Xh[:, None, :])
-    np.add.at(b, leaf, rhs)
+    # every entry is a float64 sum over the node's rows in row order
+    # (bincount adds its weights in input order)
+    for i in range(K + 1):
+        for j in range(i, K + 1):
+            M[:, i, j] = np.bincount(leaf, weights=X1[:, i] * Xh[:, j], minlength=n_nodes)
+            M[:, j, i] = M[:, i, j] if i == j else np.bincount(leaf, weights=X1[:, j] * Xh[:, i],
+                                                                 minlength=n_nodes)
+        b[:, i] = np.bincount(leaf, weights=rhs[:, i], minlength=n_nodes)
     return M, b
 
 

@@ -84,7 +84,7 @@ def lib():
         L.or_grow.restype = _int
         L.or_grow.argtypes = ([_int, _vp, _vp, _vp, _vp, _vp, _flt, _int, _vp, _vp, _vp, _vp,
                                _int, _vp, _i64, _int, _flt, _flt, _flt, _int, _flt, _int, _int,
-                               _int] + [_vp] * 6 + [_vp] * 5)
+                               _int] + [_vp] * 6 + [_vp] * 6)
         L.or_apply.restype = None
         L.or_apply.argtypes = [_vp, _vp, _vp, _vp, _vp, _i64, _int, _int, _vp]
         _LIB = L
@@ -141,10 +141,12 @@ def _common_inputs(bins_fm, grad, hess, fmask, imat, sparse, nbins):
 
 def grow(bins_fm, grad, hess, *, mode=MODE_FP32, fmask=None, imat=None, ib=0.5, sparse=None,
          nbins=None, lam=1.0, gamma=0.0, mcw=1e-3, msl=20, lr=0.1, max_leaves=31,
-         max_depth=64, n_threads=0, reference=False) -> dict:
+         max_depth=64, n_threads=0, reference=False, keep_hist=False) -> dict:
     """Grow one tree.  ``reference=True`` runs the compiled reference cgrow
     (fp32 arithmetic only, no traces).  Returns the node arrays trimmed to
-    n_nodes, plus rows/seg_lo/seg_hi/split_gain/quant traces for the oracle."""
+    n_nodes, plus rows/seg_lo/seg_hi/split_gain/quant traces for the oracle;
+    ``keep_hist``: also "hist", every node's (3, F, 256) histogram as the
+    grower scanned it (float32 in MODE_FP32, int64 fixed point in MODE_FIXED)."""
     bins_fm, F, n, grad, hess, fm, use_imat, im, sp, use_sparse, nb = _common_inputs(
         bins_fm, grad, hess, fmask, imat, sparse, nbins)
     nodes = 2 * int(max_leaves) + 1
@@ -166,15 +168,20 @@ def grow(bins_fm, grad, hess, *, mode=MODE_FP32, fmask=None, imat=None, ib=0.5, 
     seg_hi = np.empty(nodes, np.int64)
     split_gain = np.empty(nodes, np.float64)
     quant = np.zeros(2, np.int32)
+    hist = (np.empty((nodes, 3, F, B), np.float32 if mode == MODE_FP32 else np.int64) if keep_hist
+            else None)
     nn = lib().or_grow(_int(mode), _ptr(bins_fm), _ptr(grad), _ptr(hess), _ptr(fm), _ptr(im),
                        _flt(float(ib)), _int(int(use_imat)), *[_ptr(a) for a in sp],
                        _int(use_sparse), _ptr(nb), _i64(n), _int(F), *scalars, *outs,
-                       _ptr(rows), _ptr(seg_lo), _ptr(seg_hi), _ptr(split_gain), _ptr(quant))
+                       _ptr(rows), _ptr(seg_lo), _ptr(seg_hi), _ptr(split_gain), _ptr(quant),
+                       _vp(0) if hist is None else _ptr(hist))
     if nn < 0:
         raise ValueError(f"oracle grow failed with status {nn}")
     res = {k: v[:nn] for k, v in out.items()}
     res.update(n_nodes=nn, rows=rows[:n], seg_lo=seg_lo[:nn], seg_hi=seg_hi[:nn],
                split_gain=split_gain[:nn], quant=(int(quant[0]), int(quant[1])))
+    if hist is not None:
+        res["hist"] = hist[:nn]
     return res
 
 

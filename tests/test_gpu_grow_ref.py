@@ -172,6 +172,23 @@ def test_classifier_matches_reference_golden():
     assert np.abs(clf.predict_proba(Xt)[:, 1] - d["proba"]).max() <= 1e-6
 
 
+def test_classifier_golden_exact_departures_are_explained():
+    """The logistic golden fit's trajectory (the oracle's fp32 fit equals the
+    golden trees): each tree grown in the exact arithmetic from that tree's
+    own inputs either has the reference's split set (compared by path) or
+    departs at a node whose two candidate splits have float64 gains closer
+    than the arithmetic's error bounds (yabt_amd.divergence)."""
+    from tests.test_gpu_full_fits import _check_shadow, shadow_fit
+    d = _golden("booster_logistic_50kx28.npz")
+    X, y = _logistic(50_000, 28, 1)
+    model, out = shadow_fit(X, y, 10, 28, loss="log", max_leaves=256, max_depth=8, neural_leaves=False)
+    off = d["node_off"]
+    for t, tree in enumerate(model["trees"]):
+        assert np.array_equal(tree["feature"], d["feature"][off[t]:off[t + 1]]), f"oracle tree {t} is not the golden's"
+    differing = _check_shadow(out, 10)
+    print(f"exact arithmetic on the golden trajectory: {len(differing)} of 10 trees differ as split sets", flush=True)
+
+
 def _modal_bins(rng, n, F, share=0.7):
     """Each column: a random bin with probability ``share``, else uniform."""
     b = rng.integers(0, 256, size=(n, F))

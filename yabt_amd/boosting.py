@@ -262,9 +262,15 @@ class Booster:
         return binner, lay, Xraw
 
     def fit(self, X: np.ndarray, y: np.ndarray,
-            eval_set: tuple[np.ndarray, np.ndarray] | None = None, prepared: tuple | None = None) -> "Booster":
+            eval_set: tuple[np.ndarray, np.ndarray] | None = None, prepared: tuple | None = None,
+            on_tree=None) -> "Booster":
         """The reference's training loop (boosting.py:271-534) on the device.
-        ``prepared``: the result of ``prepare(X)`` for this X, if already made."""
+        ``prepared``: the result of ``prepare(X)`` for this X, if already made.
+        ``on_tree``: called after each tree grown on all rows as
+        on_tree(t, inputs, result) with the grower's inputs (dict: layouts,
+        grad, hess, nbins, imat, fmask, and the grower keywords) and its
+        GrowResult -- e.g. to grow the same tree in the other arithmetic
+        (yabt_amd.divergence)."""
         p = self.p
         check_supported(p)
         dev = self._device()
@@ -323,12 +329,14 @@ class Booster:
                 imat = self.interaction_detector.normalized_matrix()
 
             if rows is None:
-                res = grow_device(lay, grad, hess, nbins, fmask=fmask, imat=imat, ib=p.interaction_boost,
-                                  lam=tp_t.reg_lambda, gamma=tp_t.gamma, mcw=tp_t.min_child_weight,
-                                  msl=tp_t.min_samples_leaf, lr=tp_t.learning_rate,
-                                  max_leaves=tp_t.max_leaves, max_depth=tp_t.max_depth,
+                gkw = dict(fmask=fmask, imat=imat, ib=p.interaction_boost, lam=tp_t.reg_lambda, gamma=tp_t.gamma,
+                           mcw=tp_t.min_child_weight, msl=tp_t.min_samples_leaf, lr=tp_t.learning_rate,
+                           max_leaves=tp_t.max_leaves, max_depth=tp_t.max_depth)
+                res = grow_device(lay, grad, hess, nbins, **gkw,
                                   default_bin=sparse_db if sparse_db is not None else "auto",
                                   arithmetic=p.grower_arithmetic)
+                if on_tree is not None:
+                    on_tree(t, dict(layouts=lay, grad=grad, hess=hess, nbins=nbins, **gkw), res)
                 tree = tree_from_result(res, self.binner, F, dev)
                 leaf_idx = leaf_ids(res, n, F, tp_t.max_leaves)
             else:
