@@ -517,6 +517,54 @@ def multiclass_fit(torch) -> dict:
             "multiclass_2Mx50_ms_per_tree": round(sec * 1e3 / (20 * C), 2)}
 
 
+def exact_departures(torch, X, y, n_trees=100) -> dict:
+    """Untimed: the binary fit in the reference arithmetic (cgrow's trees),
+    and at each of its trees the same grower inputs (g, h, interaction
+    matrix, parameters) grown again in the exact arithmetic.  The two trees
+    are compared as split sets, node by node along paths from the root
+    (yabt_amd.divergence: with 256 leaves at depth 8 the order of splits
+    cannot change the set); for each tree that differs, the first differing
+    node's rows give the float64 gains of the two arithmetics' choices and
+    the bound on how far either arithmetic's gains can be from them."""
+    from yabt_amd import Booster, LogLoss, YABTClassifier
+    from yabt_amd import divergence as D
+    from yabt_amd import grow_hip as G
+    keys = ("feature", "thr_bin", "left", "right", "value")
+    diffs = []
+
+    def on_tree(t, inp, res):
+        lay, g, h, nb = inp["layouts"], inp["grad"], inp["hess"], inp["nbins"]
+        kw = {k: inp[k] for k in ("fmask", "imat", "ib", "lam", "gamma", "mcw", "msl", "lr", "max_leaves",
+                                  "max_depth")}
+        ex = G.grow_device(lay, g, h, nb, arithmetic="exact", **kw)
+        a = {k: getattr(ex, k).cpu().numpy() for k in keys}
+        b = {k: getattr(res, k).cpu().numpy() for k in keys}
+        cd = D.canonical_first_difference(a, b)
+        if cd is None:
+            return
+        rec = {"tree": t, "exact_split": cd["a"], "reference_split": cd["b"]}
+        if cd["a"] is not None and cd["b"] is not None:
+            _, (sg, sh, _) = G.hist(lay, g, h)
+            imat = None if inp["imat"] is None else inp["imat"].cpu().numpy()
+            node = cd["node_b"]
+            gap = D.decision_gap(b, {"a": (node,) + cd["a"], "b": (node,) + cd["b"]}, lay.fm[:, :lay.n], g, h,
+                                 nb, (sg, sh), lam=float(inp["lam"]), gamma=float(inp["gamma"]),
+                                 boost_of=None if imat is None else
+                                 (lambda k: D.path_boost(b, k, imat, float(inp["ib"]))))
+            rec.update(rows=gap["rows"], gain_exact=round(gap["exact"]["gain"], 6),
+                       gain_reference=round(gap["reference"]["gain"], 6),
+                       gap_rel=float(f"{gap['gap'] / max(abs(gap['exact']['gain']), 1e-300):.3g}"),
+                       bound_rel=float(f"{gap['bound'] / max(abs(gap['exact']['gain']), 1e-300):.3g}"),
+                       explained=bool(gap["explained"]))
+        diffs.append(rec)
+
+    est = YABTClassifier(n_estimators=n_trees, max_leaves=256, max_depth=8, max_bins=28, neural_leaves=False,
+                         grower_arithmetic="reference")
+    Booster(est._boost_params(), LogLoss()).fit(X, y, on_tree=on_tree)
+    return {"trees": n_trees, "differing_split_sets": len(diffs),
+            "all_explained": all(d.get("explained", False) for d in diffs), "differences": diffs}
+
+
 def boosting_fits(torch) -> dict:
     """Wall time of whole estimator fits (binning included, after one warm-up
     fit) in both grower arithmetics:
@@ -557,6 +605,8 @@ def boosting_fits(torch) -> dict:
         mk().fit(X, y)
         torch.cuda.synchronize()
         out[f"binary_1Mx28_100trees_s_{arith}"] = round(time.perf_counter() - t0, 2)
+    log("[bench] exact vs reference arithmetic along the binary fit's trajectory (untimed)")
+    out["binary_1Mx28_exact_vs_reference"] = exact_departures(torch, X, y)
     return out
 
 
