@@ -165,7 +165,7 @@ def time_bin_counts(torch, lay, reps=5):
     from yabt_amd import _lib
     dev = lay.fm.device
     lib = _lib.load()
-    c = torch.empty((lay.F, 256), dtype=torch.int32, device=dev)
+    c = torch.empty(int(lib.yabt_bin_counts_words(lay.n, lay.F)), dtype=torch.int32, device=dev)
     stream = torch.cuda.current_stream(dev)
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     _lib.check(lib.yabt_bin_counts(G._ptr(lay.fm), lay.ld_fm, lay.n, lay.F, G._ptr(c), G._stream(dev)),
@@ -728,7 +728,7 @@ def main() -> None:
                       "frac_hbm": round(achieved / HBM_PEAK_GBS, 4)},
         "fit_setup": {"bin_counts_ms": round(ms_counts, 4),
                       "note": "per-fit count plane of the root histogram (yabt_bin_counts), outside the step"},
-        "roofline": {"kernel": "k_hist_root<false> (streaming root histogram)", "bound": "hbm",
+        "roofline": {"kernel": "k_hist_root<false, true> (streaming root histogram)", "bound": "hbm",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic()},
     }

@@ -26,9 +26,12 @@
  *     for both g and h (exact integer sums, so the choice is deterministic),
  *     else wide; every sum over <= n rows is exact either way;
  *   - bin counts: the count plane of a root histogram depends only on the
- *     bins, so callers that keep them for a whole fit (yabt_bin_counts) pass
- *     them as `bin_counts` (F, 256) uint32; NULL makes the call count them
- *     itself (one more pass over the feature-major bins);
+ *     bins, so callers that keep them for a whole fit pass the table
+ *     yabt_bin_counts made for these bins and this n as `bin_counts`
+ *     (yabt_bin_counts_words(n, F) uint32: the (F, 256) counts, then the
+ *     per-segment maxima that let the root skip its packed cells' epochs);
+ *     NULL makes the call count them itself (one more pass over the
+ *     feature-major bins);
  *   - bins: feature-major (F, ld_fm) uint8 with ld_fm >= n, ld_fm % 16 == 0,
  *     and a row-major copy (n, ld_rm) uint8 with ld_rm >= F, ld_rm % 16 == 0
  *     (yabt_transpose_bins builds it); bins, grad, hess 16-byte aligned.
@@ -124,11 +127,16 @@ int yabt_hist_accumulate(const uint8_t *bins_fm, int64_t ld_fm, const uint8_t *b
                          const uint32_t *rows, int64_t m, int sg, int sh, int wide, void *workspace,
                          int64_t *out, yabt_stream_t stream);
 
-/* Per-fit bin counts: out_counts[f * 256 + b] (uint32, F * 256) = number of
- * rows r < n with bins_fm[f * ld_fm + r] == b.  The count plane of every root
- * histogram over these bins; yabt_grow* take it as `bin_counts`.  Replaces
- * nothing in the reference (cgrow counts every node's rows itself,
+/* Per-fit count table of the bins (uint32, yabt_bin_counts_words(n, F)
+ * words): out_counts[f * 256 + b] = number of rows r < n with
+ * bins_fm[f * ld_fm + r] == b, the count plane of every root histogram over
+ * these bins; then out_counts[F * 256 + f * S + s], S = ceil(n / 65536) =
+ * the largest count of any bin of feature f among rows
+ * [65536 s, 65536 (s + 1)), which bounds the rows any cell of a root chunk
+ * takes.  yabt_grow* and yabt_hist_root take the table as `bin_counts`.
+ * Replaces nothing in the reference (cgrow counts every node's rows itself,
  * grow.c:55-60); it is the setup of the packed root histogram. */
+size_t yabt_bin_counts_words(int64_t n, int F);
 int yabt_bin_counts(const uint8_t *bins_fm, int64_t ld_fm, int64_t n, int F, uint32_t *out_counts,
                     yabt_stream_t stream);
 

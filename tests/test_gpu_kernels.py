@@ -78,6 +78,55 @@ def test_root_hist_exact(n, F, kind, skew):
         assert normwise_rel(got[1] * 2.0 ** -sh, f32[1]) < 1e-5
 
 
+def _count_table(bins, seg=65536):
+    """The per-fit count table on the CPU: (F, 256) counts, then per feature
+    and 65536-row segment the largest count of any bin."""
+    n, F = bins.shape
+    nseg = (n + seg - 1) // seg
+    counts = np.zeros((F, 256), np.int64)
+    segmax = np.zeros((F, nseg), np.int64)
+    for f in range(F):
+        counts[f] = np.bincount(bins[:, f], minlength=256)
+        for s in range(nseg):
+            segmax[f, s] = np.bincount(bins[s * seg:(s + 1) * seg, f], minlength=256).max()
+    return counts, segmax
+
+
+@pytest.mark.parametrize("n,F,kind,hot", [
+    (300_001, 20, "normal", None), (1_000_003, 17, "normal", None), (4_000_000, 36, "normal", None),
+    (2_500_001, 36, "normal", "skew"), (600_000, 7, "laplace", "skew"), (65_536, 100, "logistic", None),
+    # one feature holds 70 000 rows of one bin in one place: the chunks that
+    # contain them need the packed cells' epochs, the others do not
+    (1_200_000, 100, "normal", "hot"), (1_200_000, 100, "cauchy_h", "hot"), (1_200_000, 100, "laplace", "hot"),
+])
+def test_root_hist_count_table(n, F, kind, hot):
+    """yabt_bin_counts' table (counts and per-segment maxima) against numpy,
+    and the root histogram that reads it (packed cells without epochs where
+    the table allows) against the oracle's exact sums."""
+    print(f"root table n={n} F={F} kind={kind} hot={hot}", flush=True)
+    rng = np.random.default_rng(n + 3 * F)
+    bins = skewed_bins(rng, n, F) if hot == "skew" else uniform_bins(rng, n, F)
+    if hot == "hot":
+        bins[400_000:470_000, 5] = 77
+    g, h = grad_hess(rng, n, kind)
+    lay = _layouts(bins)
+    lib = G._lib.load()
+    table = lay.counts()
+    assert table.numel() == int(lib.yabt_bin_counts_words(n, F))
+    counts, segmax = _count_table(bins)
+    tab = table.cpu().numpy().view(np.uint32).astype(np.int64)
+    assert np.array_equal(tab[:F * 256].reshape(F, 256), counts)
+    assert np.array_equal(tab[F * 256:].reshape(F, -1), segmax)
+    sg, sh, wide = O.hist_contract(g, h)[:3]
+    gd, hd = G._dev_f32(torch.from_numpy(g), DEV), G._dev_f32(torch.from_numpy(h), DEV)
+    out = torch.zeros((3, F, 256), dtype=torch.int64, device=DEV)
+    G._lib.check(lib.yabt_hist_root(G._ptr(lay.fm), lay.ld_fm, G._ptr(gd), G._ptr(hd), n, F, G._ptr(table),
+                                    sg, sh, wide, G._ptr(out), G._stream(DEV)), "yabt_hist_root")
+    got = out.cpu().numpy()
+    ref = O.hist_fixed(bins.T, g, h, sg, sh)
+    assert np.array_equal(got, ref)
+
+
 @pytest.mark.parametrize("n,F,m,kind", [(5000, 16, 1, "normal"), (5000, 16, 777, "normal"), (40_000, 21, 19_999, "normal"),
                                         (40_000, 100, 40_000, "normal"), (10, 3, 0, "normal"),
                                         # n > 2^18: packed words, pipelined gather

@@ -50,6 +50,7 @@ SIGNATURES = {
     "yabt_hist": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _int, _vp, _i64, _vp, _vp, _vp, _vp]),
     "yabt_hist_accumulate": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _int, _vp, _i64, _int, _int,
                                     _int, _vp, _vp, _vp]),
+    "yabt_bin_counts_words": (_sz, [_i64, _int]),
     "yabt_bin_counts": (_int, [_vp, _i64, _i64, _int, _vp, _vp]),
     "yabt_hist_root": (_int, [_vp, _i64, _vp, _vp, _i64, _int, _vp, _int, _int, _int, _vp, _vp]),
     "yabt_hist_noalloc": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _int, _vp, _i64, _vp, _vp, _vp]),

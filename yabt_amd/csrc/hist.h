@@ -246,21 +246,22 @@ constexpr int TSTEP = 2 * RBLOCK;        // rows per tail block step (128 per wa
 // ids 0 .. tail - 1, tail_rows rows each), then `tiles` full 16-feature tiles
 // of `chunks` row chunks each.  The last tile is a tail tile when it holds
 // 1..TAILF features and g and h can be read in aligned pairs (8-byte aligned,
-// n >= 2).  One 1024-thread block runs per CU, so the grid aims at two waves
-// of 256 blocks of equal length: a tail block's row costs about 3/8 of a full
-// block's (a quarter of the LDS atomics, with more VALU work per atomic), so
-// the tail counts as 3/8 of a tile when the chunks are sized, and its blocks
-// fill the rest of the 512 (at least 3/8 of a tile's worth).  chunks is a
-// multiple of 8, so every full tile of a row chunk runs on one XCD (block id
-// % 8) and shares its L2 for the chunk's g and h; the tail blocks read theirs
-// on their own.
+// n >= 2).  One 1024-thread block runs per CU, so the grid aims at one wave
+// of 256 blocks of equal length (two waves of 256 took 1-2% longer: the
+// second wave starts behind the first one's slowest blocks): a tail block's
+// row costs about 3/8 of a full block's (a quarter of the LDS atomics, with
+// more VALU work per atomic), so the tail counts as 3/8 of a tile when the
+// chunks are sized, and its blocks fill the rest of the 256 (at least 3/8 of
+// a tile's worth).  chunks is a multiple of 8, so every full tile of a row
+// chunk runs on one XCD (block id % 8) and shares its L2 for the chunk's g
+// and h; the tail blocks read theirs on their own.
 struct RootGrid {
     int tiles, chunks, tail, blocks;
     int64_t tail_rows;
 };
 
 inline RootGrid root_grid(int64_t n, int F, const void* grad, const void* hess) {
-    constexpr int SLOTS = 512;
+    constexpr int SLOTS = 256;
     const int rem = F % HFL;
     const bool tail = rem >= 1 && rem <= TAILF && n >= 2 && (uintptr_t)grad % 8 == 0 && (uintptr_t)hess % 8 == 0;
     RootGrid g;
@@ -288,18 +289,51 @@ inline RootGrid root_grid(int64_t n, int F, const void* grad, const void* hess) 
 
 constexpr int ROOT_G = 0, ROOT_PACKED = 1, ROOT_WIDE = 2;   // modes of the streaming root kernels
 constexpr int ROOT_DEPTH = 3;    // steps of inputs loaded ahead of the adds: one epoch
+// A packed cell stays exact while it takes fewer than PACKED_CELL_ROWS rows:
+// with hist_shift's |q| <= 2^19 (n > 2048; below, |q| <= 2^30 / n) each half
+// then stays below 2^31.
+constexpr int64_t PACKED_CELL_ROWS = 4096;
+// Rows of a count segment: the per-fit count table also holds, per feature
+// and segment, the largest count of any bin in the segment (yabt_bin_counts),
+// which bounds the rows any cell of a root chunk can take.
+constexpr int64_t SEG_ROWS = 65536;
+__host__ __device__ inline int64_t count_segments(int64_t n) { return (n + SEG_ROWS - 1) / SEG_ROWS; }
 constexpr int TAIL_DEPTH = 4;    // the same in a tail block (4 steps of 512 rows per column)
 // A cell takes the rows of one epoch between two unpacks: ROOT_DEPTH block
 // steps of RSTEP rows (3072), and with hist_shift's |q| <= 2^19 each half of
 // the packed cell then stays within 3072 * 2^19 < 2^31.
 static_assert((int64_t)ROOT_DEPTH * RSTEP * (1 << 19) < (1ll << 31), "an epoch's sums fit 32-bit halves");
+static_assert(PACKED_CELL_ROWS * (1 << 19) <= (1ll << 31) && ROOT_DEPTH * RSTEP <= PACKED_CELL_ROWS,
+              "a cell below PACKED_CELL_ROWS rows is exact");
 static_assert((int64_t)TAIL_DEPTH * TSTEP / 4 * (1 << 19) < (1ll << 31), "a tail epoch's sums fit 32-bit halves");
+
+// Buffer resource over `bytes` bytes at p (raw, untyped): a load at an offset
+// past the end returns zeros instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
+// Whether a root chunk of `per` rows over bins of leading dimension ld can be
+// read through buffer resources: every 32-bit offset of a tile's loads (a
+// lane's column, fl ld, plus the row of a step, the ring's steps past the
+// chunk included) and of the chunk's g and h (4 bytes a row) fits 32 bits.
+__host__ __device__ inline bool root_buffers(int64_t ld, int64_t per) {
+    const int64_t rows = per + 8 * RSTEP;
+    return (int64_t)HFL * ld + rows < (1ll << 32) && 4 * rows < (1ll << 32);
+}
 
 // MODE: ROOT_G (every h equal: the word is q(g), never unpacked), ROOT_PACKED
 // (narrow contract: (q(g) << 32) + q(h) in one cell, epochs), ROOT_WIDE (wide
 // contract: q(g) and q(h) in a cell each -- the two buffers of the layout --
 // with one atomic per channel; 64-bit cells never need an unpack).
-template <int MODE, bool SKIP>
+// BUF (root_buffers holds): the loads go through buffer resources bounded at
+// the chunk's end -- g and h past it read as 0, so their words are 0 and no
+// row needs a test, and the steps' offsets are scalar -- else through global
+// pointers with each row clamped into the chunk and its word masked.
+// The root totals (q_tot, tile 0) are the sums of feature 0's cells (every
+// row has one bin of feature 0), or with SKIP (default bins left out) the
+// per-row sums.
+template <int MODE, bool SKIP, bool BUF>
 __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restrict__ bins_fm, int64_t ld,
                                              const float* __restrict__ grad, const float* __restrict__ hess,
                                              int64_t n, int F, double scg, double sch,
@@ -341,42 +375,82 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
             ag[k] += (int64_t)(v - (uint64_t)hs) >> 32;
         }
     };
-    const uint8_t* col = bins_fm + (size_t)(fok ? f : f0) * ld;
     // Inputs of step s: this lane's row's g and h, and 16 rows of its
-    // feature's bins.  The loads are unconditional, so the loop is straight
-    // code and each stage's registers are waited for on their own: a row past
-    // hi reads row hi - 1 (its word is zero below), and a row group past hi
-    // reads the chunk's first 16 rows (its rows' words are zero).  r0 % 64 ==
-    // 0 and lo % 16 == 0, so the bins base is a multiple of 16 below hi <= n
-    // <= ld (ld % 16 == 0): the 16-byte load stays inside the row.
+    // feature's bins.
+    //   BUF: offsets from the chunk's first row; the bins' resource starts at
+    //   row lo of feature f0 and ends with the tile's last feature below F, so
+    //   lanes of features >= F read zeros (their columns are never flushed).
+    //   Otherwise the loads are unconditional: a row past hi reads row hi - 1
+    //   (its word is masked to zero below), and a row group past hi reads the
+    //   chunk's first 16 rows (their rows' words are zero); r0 % 64 == 0 and
+    //   lo % 16 == 0, so the bins base is a multiple of 16 below hi <= n <= ld
+    //   (ld % 16 == 0): the 16-byte load stays inside the row.
+    const int nf = min(HFL, F - f0);
+    const __amdgpu_buffer_rsrc_t rsg = raw_rsrc(grad + lo, BUF ? (uint32_t)((hi - lo) * 4) : 0u);
+    const __amdgpu_buffer_rsrc_t rsh = raw_rsrc(hess + lo, (BUF && HCH) ? (uint32_t)((hi - lo) * 4) : 0u);
+    const __amdgpu_buffer_rsrc_t rsb =
+        raw_rsrc(bins_fm + (size_t)f0 * ld + lo, BUF ? (uint32_t)((int64_t)nf * ld - lo) : 0u);
+    const uint32_t vg = (uint32_t)(wave * WAVE + lane) * 4u;
+    const uint32_t vb = (uint32_t)((int64_t)fl * ld) + (uint32_t)(wave * WAVE + HFL * rg);
+    const uint8_t* col = bins_fm + (size_t)(fok ? f : f0) * ld;
     auto load = [&](int64_t s, float& gv, float& hv, uint4& bw) {
-        const int64_t r0 = lo + s * RSTEP + (int64_t)wave * WAVE;
-        const int64_t r = min(r0 + lane, hi - 1);
-        gv = grad[r];
-        if (HCH) hv = hess[r];
-        const int64_t base = r0 + HFL * rg;
-        bw = *reinterpret_cast<const uint4*>(col + (base < hi ? base : lo));
+        if (BUF) {
+            typedef int v4i __attribute__((ext_vector_type(4)));
+            const int so = (int)(s * RSTEP);
+            // issued in this order wherever load runs (see the ring below)
+            gv = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsg, (int)vg, so * 4, 0));
+            __builtin_amdgcn_sched_barrier(0);
+            if (HCH) hv = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(rsh, (int)vg, so * 4, 0));
+            __builtin_amdgcn_sched_barrier(0);
+            const v4i b = __builtin_amdgcn_raw_buffer_load_b128(rsb, (int)vb, so, 0);
+            __builtin_amdgcn_sched_barrier(0);
+            bw = make_uint4((uint32_t)b.x, (uint32_t)b.y, (uint32_t)b.z, (uint32_t)b.w);
+        } else {
+            const int64_t r0 = lo + s * RSTEP + (int64_t)wave * WAVE;
+            const int64_t r = min(r0 + lane, hi - 1);
+            gv = grad[r];
+            if (HCH) hv = hess[r];
+            const int64_t base = r0 + HFL * rg;
+            bw = *reinterpret_cast<const uint4*>(col + (base < hi ? base : lo));
+        }
     };
     const int64_t steps = (hi - lo + RSTEP - 1) / RSTEP;   // the same in every wave: barriers below
+    // Packed cells need epochs only when one of them could take
+    // PACKED_CELL_ROWS rows of the chunk: the per-fit table bounds a cell's
+    // rows by the sum, over the count segments the chunk touches, of its
+    // feature's largest bin count in each (uniform over the block; no table:
+    // epochs).  Without epochs every row goes to buffer 0, unpacked once at
+    // the end.
+    bool epochs = PACK;
+    if (PACK && counts) {
+        const uint32_t* segmax = counts + (size_t)F * NB;
+        const int64_t nseg = count_segments(n);
+        uint32_t bound = 0;
+        if (fok)
+            for (int64_t sg = lo / SEG_ROWS; sg <= (hi - 1) / SEG_ROWS; ++sg) bound += segmax[(size_t)f * nseg + sg];
+        bound = (uint32_t)__builtin_amdgcn_readfirstlane((int)wave_max_u32_v(bound));
+        epochs = (int64_t)bound >= PACKED_CELL_ROWS;
+    }
     // Ring of ROOT_DEPTH stages: stage j holds step s0 + j and is then refilled
     // with step s0 + j + ROOT_DEPTH (the ring is unrolled: no register moves).
     // A round of the ring is one epoch; its cells are one of two buffers,
-    // which alternate by round.  The ring starts one round early, at steps
-    // -ROOT_DEPTH .. -1, whose rows are all invalid (zero words at cell 0):
-    // that round only issues the first loads, in the same order as every
-    // later round.
+    // which alternate by round.  The first round's loads are issued before
+    // the loop, in the loop's own order (scheduling barriers between them),
+    // so that the compiler's waits at the loop's head, which must hold for
+    // the entry as well as the back edge, wait only for the stage's own
+    // loads.
     float gs[ROOT_DEPTH], hs[ROOT_DEPTH];
     uint4 bs[ROOT_DEPTH];
 #pragma unroll
     for (int j = 0; j < ROOT_DEPTH; ++j) {
-        gs[j] = 0.0f;
         hs[j] = 0.0f;
-        bs[j] = make_uint4(0, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load(j, gs[j], hs[j], bs[j]);
     }
     __syncthreads();
     int64_t sum_g = 0, sum_h = 0;
     uint32_t buf = 0;   // the cell buffer of this round's epoch
-    for (int64_t s0 = -ROOT_DEPTH; s0 < steps; s0 += ROOT_DEPTH) {
+    for (int64_t s0 = 0; s0 < steps; s0 += ROOT_DEPTH) {
         const uint32_t lb = PACK ? (lbase | (buf << 7)) : lbase;
 #pragma unroll
         for (int j = 0; j < ROOT_DEPTH; ++j) {
@@ -385,10 +459,22 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
             // loads above this stage's work (that would wait for them early);
             // every stage runs, a step past the last being all invalid rows
             __builtin_amdgcn_sched_barrier(0);
-            const int64_t r0 = lo + s * RSTEP + (int64_t)wave * WAVE;
-            const bool rok = s >= 0 && r0 + lane < hi;
-            const int64_t gq = rok ? (PACK ? quantise_node(gs[j], scg) : quantise_wide(gs[j], scg)) : 0;
-            const int64_t hq = (HCH && rok) ? (PACK ? quantise_node(hs[j], sch) : quantise_wide(hs[j], sch)) : 0;
+            const bool rok = BUF || lo + s * RSTEP + (int64_t)wave * WAVE + lane < hi;
+            int64_t gq, hq;
+            uint64_t word;
+            if (PACK) {
+                // |q| <= 2^30 (hist_shift): 32-bit halves, the word's high half
+                // borrowing one from it when q(h) is negative
+                const int32_t g32 = rok ? (int32_t)quantise_node(gs[j], scg) : 0;
+                const int32_t h32 = rok ? (int32_t)quantise_node(hs[j], sch) : 0;
+                gq = g32;
+                hq = h32;
+                word = ((uint64_t)((uint32_t)g32 + (uint32_t)(h32 >> 31)) << 32) | (uint32_t)h32;
+            } else {
+                gq = rok ? quantise_wide(gs[j], scg) : 0;
+                hq = (HCH && rok) ? quantise_wide(hs[j], sch) : 0;
+                word = (uint64_t)gq;
+            }
             // the 16 cell addresses (and, with SKIP, which rows are not added)
             // come out of this stage's bins before its registers are refilled,
             // so the old and new values are never live at once (else the refill
@@ -402,9 +488,10 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
                 if (SKIP && (int)((wv[J >> 2] >> (8 * (J & 3))) & 0xffu) == d) keep &= ~(1u << J);
             }
             load(s + ROOT_DEPTH, gs[j], hs[j], bs[j]);
-            sum_g += gq;
-            sum_h += hq;
-            const uint64_t word = PACK ? ((uint64_t)gq << 32) + (uint64_t)hq : (uint64_t)gq;
+            if (SKIP) {
+                sum_g += gq;
+                sum_h += hq;
+            }
             // ROOT_WIDE: the h cell is the g cell's twin in the other buffer
             // (16 words, 128 bytes, further)
 #define YABT_GH_ADD(J)                                                           \
@@ -423,7 +510,7 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
             YABT_GH_ADD(12) YABT_GH_ADD(13) YABT_GH_ADD(14) YABT_GH_ADD(15)
 #undef YABT_GH_ADD
         }
-        if (PACK) {
+        if (epochs) {
             // end of the epoch: once every wave's adds into its buffer are
             // done, read it while the next epoch adds into the other one
             __syncthreads();
@@ -432,6 +519,7 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
         }
     }
     __syncthreads();
+    if (PACK && !epochs) unpack(0);
     if (!PACK) {   // never unpacked: the cells are the g sums (and the h sums)
 #pragma unroll
         for (int k = 0; k < RENT; ++k) {
@@ -440,6 +528,17 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
         }
     }
     if (totals) {
+        if (!SKIP) {   // thread t's cells are of feature t % HFL
+            sum_g = 0;
+            sum_h = 0;
+            if (threadIdx.x % HFL == 0) {
+#pragma unroll
+                for (int k = 0; k < RENT; ++k) {
+                    sum_g += ag[k];
+                    sum_h += ah[k];
+                }
+            }
+        }
         sum_g = wave_sum<int64_t>(sum_g);
         sum_h = wave_sum<int64_t>(sum_h);
         if (lane == 0) {
@@ -674,6 +773,59 @@ __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __res
                        SKIP ? dflt : nullptr, out, F, f0);
 }
 
+// Per-fit count table of the feature-major bins (yabt_bin_counts): counts
+// (F, 256) -- rows r < n with bin b in feature f, added into (cleared
+// beforehand) -- then segmax (F, count_segments(n)): the largest count of any
+// bin of feature f among rows [s SEG_ROWS, (s + 1) SEG_ROWS), written.  Block
+// (tile, s) counts segment s of its 16 features in LDS (one 32-bit LDS
+// atomic per row and feature).
+static __global__ __attribute__((unused)) void __launch_bounds__(HBLOCK)
+k_bin_count_seg(const uint8_t* __restrict__ bins_fm, int64_t ld, int64_t n, int F, uint32_t* __restrict__ table) {
+    __shared__ uint32_t c[NB * HFL];   // [bin][feature]
+    __shared__ uint32_t mx[HFL];
+    const int64_t nseg = count_segments(n);
+    const int tile = (int)(blockIdx.x / nseg);
+    const int64_t sg = blockIdx.x % nseg;
+    const int f0 = tile * HFL;
+    const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
+    const int fl = lane & (HFL - 1), rg = lane / HFL;
+    const int f = f0 + fl;
+    const bool fok = f < F;
+    const int64_t lo = sg * SEG_ROWS, hi = min(n, lo + SEG_ROWS);
+    for (int i = threadIdx.x; i < NB * HFL; i += HBLOCK) c[i] = 0;
+    if (threadIdx.x < HFL) mx[threadIdx.x] = 0;
+    __syncthreads();
+    const uint8_t* col = bins_fm + (size_t)(fok ? f : f0) * ld;
+    for (int64_t r0 = lo + (int64_t)wave * WAVE; r0 < hi; r0 += HSTEP) {
+        // base % 16 == 0 and base < hi <= n <= ld (ld % 16 == 0): in the row
+        const int64_t base = r0 + HFL * rg;
+        if (!fok || base >= hi) continue;
+        const uint4 bv = *reinterpret_cast<const uint4*>(col + base);
+        const uint32_t w[4] = {bv.x, bv.y, bv.z, bv.w};
+        const int nv = (int)min((int64_t)HFL, hi - base);
+#pragma unroll
+        for (int J = 0; J < HFL; ++J) {
+            const int b = (int)((w[J >> 2] >> (8 * (J & 3))) & 0xffu);
+            if (J < nv) atomicAdd(&c[b * HFL + fl], 1u);
+        }
+    }
+    __syncthreads();
+    // thread t's cells t + k HBLOCK all hold feature t % HFL
+    uint32_t m = 0;
+    for (int i = threadIdx.x; i < NB * HFL; i += HBLOCK) {
+        const int fi = f0 + (i % HFL);
+        const uint32_t v = c[i];
+        m = max(m, v);
+        if (fi < F && v) atomicAdd(table + (size_t)fi * NB + (size_t)(i / HFL), v);
+    }
+    m = max(m, (uint32_t)__shfl_xor((int)m, HFL, WAVE));
+    m = max(m, (uint32_t)__shfl_xor((int)m, 2 * HFL, WAVE));
+    if (lane < HFL) atomicMax(&mx[lane], m);
+    __syncthreads();
+    if (threadIdx.x < HFL && f0 + (int)threadIdx.x < F)
+        table[(size_t)F * NB + (size_t)(f0 + threadIdx.x) * nseg + sg] = mx[threadIdx.x];
+}
+
 // Bin counts of all n rows of the feature-major bins, per (feature, bin):
 // OUT64 false: added into a uint32 (F, 256) table (the per-fit counts);
 // OUT64 true: added into an int64 (F, 256) count plane.  dflt (may be NULL):
@@ -727,8 +879,9 @@ k_bin_count(const uint8_t* __restrict__ bins_fm, int64_t ld, int64_t n, int F, c
 // when q->const_h.  counts: the per-fit bin counts, added into the count
 // plane by the chunk-0 blocks (NULL: the count plane is not touched).
 // SKIP: dflt is given (a separate kernel, so that the loops without the
-// default-bin test are compiled on their own).
-template <bool SKIP>
+// default-bin test are compiled on their own).  BUF: root_buffers holds for
+// the full tiles' chunks (hist_root_gh).
+template <bool SKIP, bool BUF>
 static __global__ __attribute__((unused)) void __launch_bounds__(RBLOCK)
 k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld, const float* __restrict__ grad,
             const float* __restrict__ hess, int64_t n, int F, const Quant* q, double scg_v, double sch_v,
@@ -755,14 +908,37 @@ k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld, const float* __rest
         return;
     }
     if (no_h)
-        hist_root_gh<ROOT_G, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks,
+        hist_root_gh<ROOT_G, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks,
                                    bid - tail);
     else if (wide)
-        hist_root_gh<ROOT_WIDE, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks,
+        hist_root_gh<ROOT_WIDE, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks,
                                       bid - tail);
     else
-        hist_root_gh<ROOT_PACKED, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
+        hist_root_gh<ROOT_PACKED, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
                                         chunks, bid - tail);
+}
+
+// One launch of k_hist_root over grid g: the instantiation with the
+// default-bin test when dflt is given, with buffer loads when the chunks
+// allow them.
+static __attribute__((unused)) void launch_root_kernel(hipStream_t stream, const RootGrid& g, const uint8_t* bins_fm,
+                                                       int64_t ld, const float* grad, const float* hess, int64_t n,
+                                                       int F, const Quant* q, double scg, double sch, int wide,
+                                                       const int32_t* dflt, const uint32_t* counts, Quant* q_tot,
+                                                       int64_t* out, int count_mode, const int32_t* done) {
+    const bool buf = root_buffers(ld, root_chunk_rows(n, g.chunks));
+#define YABT_ROOT_LAUNCH(S, B)                                                                                     \
+    k_hist_root<S, B><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, wide, dflt,   \
+                                                       counts, q_tot, out, g.chunks, g.tail, g.tail_rows,          \
+                                                       count_mode, done)
+    if (dflt) {
+        if (buf) YABT_ROOT_LAUNCH(true, true);
+        else YABT_ROOT_LAUNCH(true, false);
+    } else {
+        if (buf) YABT_ROOT_LAUNCH(false, true);
+        else YABT_ROOT_LAUNCH(false, false);
+    }
+#undef YABT_ROOT_LAUNCH
 }
 
 // Launch the root histogram (grid from root_grid) into the (3, F, 256)
@@ -780,15 +956,8 @@ static __attribute__((unused)) void launch_hist_root(hipStream_t stream, const u
         const int rc = root_chunks(n, tiles);
         k_bin_count<true><<<tiles * rc, HBLOCK, 0, stream>>>(bins_fm, ld, n, F, dflt, out + (size_t)2 * F * NB, rc);
     }
-    const RootGrid g = root_grid(n, F, grad, hess);
-    if (dflt)
-        k_hist_root<true><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, wide, dflt,
-                                                           counts, q_tot, out, g.chunks, g.tail, g.tail_rows,
-                                                           count_mode, done);
-    else
-        k_hist_root<false><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, wide,
-                                                            nullptr, counts, q_tot, out, g.chunks, g.tail,
-                                                            g.tail_rows, count_mode, done);
+    launch_root_kernel(stream, root_grid(n, F, grad, hess), bins_fm, ld, grad, hess, n, F, q, scg, sch, wide, dflt,
+                       counts, q_tot, out, count_mode, done);
 }
 
 // Rows of one node for a gather launch.

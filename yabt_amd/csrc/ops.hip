@@ -365,6 +365,11 @@ int yabt_hist_accumulate(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* b
     return launch_status("yabt_hist_accumulate launch");
 }
 
+size_t yabt_bin_counts_words(int64_t n, int F) {
+    if (F < 1 || n < 0 || n > 0xFFFFFFFFll) return 0;
+    return (size_t)F * NB + (size_t)F * (size_t)count_segments(n);
+}
+
 int yabt_bin_counts(const uint8_t* bins_fm, int64_t ld_fm, int64_t n, int F, uint32_t* out_counts,
                     hipStream_t stream) {
     if (!bins_fm || !out_counts || F < 1 || n < 0 || n > 0xFFFFFFFFll || ld_fm < n || ld_fm % 16 ||
@@ -373,9 +378,8 @@ int yabt_bin_counts(const uint8_t* bins_fm, int64_t ld_fm, int64_t n, int F, uin
     const int64_t ne = (int64_t)F * NB;
     k_fill_u32<<<launch_grid(ne, OB, 1024), OB, 0, stream>>>(out_counts, 0, ne);
     if (n > 0) {
-        const int tiles = (F + HFL - 1) / HFL;
-        const int rc = root_chunks(n, tiles);
-        k_bin_count<false><<<tiles * rc, HBLOCK, 0, stream>>>(bins_fm, ld_fm, n, F, nullptr, out_counts, rc);
+        const int64_t blocks = (int64_t)((F + HFL - 1) / HFL) * count_segments(n);
+        k_bin_count_seg<<<(unsigned)blocks, HBLOCK, 0, stream>>>(bins_fm, ld_fm, n, F, out_counts);
     }
     return launch_status("yabt_bin_counts launch");
 }
@@ -386,10 +390,8 @@ int yabt_hist_root(const uint8_t* bins_fm, int64_t ld_fm, const float* grad, con
     const int rc0 = check_hist_layout(bins_fm, ld_fm, nullptr, 0, grad, hess, n, F, nullptr, 0, "yabt_hist_root");
     if (rc0) return rc0;
     if (n > 0) {
-        const RootGrid g = root_grid(n, F, grad, hess);
-        k_hist_root<false><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld_fm, grad, hess, n, F, nullptr, ldexp(1.0, sg),
-                                                            ldexp(1.0, sh), wide, nullptr, bin_counts, nullptr, out,
-                                                            g.chunks, g.tail, g.tail_rows, 0, nullptr);
+        launch_root_kernel(stream, root_grid(n, F, grad, hess), bins_fm, ld_fm, grad, hess, n, F, nullptr,
+                           ldexp(1.0, sg), ldexp(1.0, sh), wide, nullptr, bin_counts, nullptr, out, 0, nullptr);
     }
     return launch_status("yabt_hist_root launch");
 }

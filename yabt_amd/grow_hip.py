@@ -117,16 +117,19 @@ class BinLayouts:
         return t
 
     def counts(self) -> torch.Tensor:
-        """Per-(feature, bin) row counts (F, 256) uint32 of the bins, counted
-        once per layout (yabt_bin_counts): the count plane of every root
-        histogram over these bins, which the growers take instead of
-        recounting the rows each tree."""
+        """The per-fit count table of the bins (yabt_bin_counts), made once
+        per layout: the per-(feature, bin) row counts (F, 256) uint32, the
+        count plane of every root histogram over these bins, which the
+        growers take instead of recounting the rows each tree, then each
+        feature's largest bin count per 65536-row segment, which tells the
+        root which row chunks need no epochs."""
         if self._counts is None:
             with self._lock:
                 if self._counts is None:
                     lib = _lib.load()
                     dev = self.fm.device
-                    c = torch.empty((self.F, MAX_BINS), dtype=torch.int32, device=dev)
+                    words = int(lib.yabt_bin_counts_words(self.n, self.F))
+                    c = torch.empty(words, dtype=torch.int32, device=dev)
                     _lib.check(lib.yabt_bin_counts(_ptr(self.fm), self.ld_fm, self.n, self.F, _ptr(c),
                                                    _stream(dev)), "yabt_bin_counts")
                     self._counts = self._publish(c)
