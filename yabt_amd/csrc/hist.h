@@ -313,10 +313,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* p, uint32
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
 }
 
-// Whether a root chunk of `per` rows over bins of leading dimension ld can be
-// read through buffer resources: every 32-bit offset of a tile's loads (a
-// lane's column, fl ld, plus the row of a step, the ring's steps past the
-// chunk included) and of the chunk's g and h (4 bytes a row) fits 32 bits.
+// Whether root chunks (or tail spans) of up to `per` rows over bins of
+// leading dimension ld can be read through buffer resources: every 32-bit
+// offset of a tile's loads (a lane's column, fl ld, plus the row of a step,
+// the ring's steps past the chunk included) and of the chunk's g and h (4
+// bytes a row) fits 32 bits.
 __host__ __device__ inline bool root_buffers(int64_t ld, int64_t per) {
     const int64_t rows = per + 8 * RSTEP;
     return (int64_t)HFL * ld + rows < (1ll << 32) && 4 * rows < (1ll << 32);
@@ -619,8 +620,9 @@ __device__ __forceinline__ void flush_tail_gh(RootFlushLds& T, const int64_t (&g
     }
 }
 
-// MODE as in hist_root_gh.
-template <int MODE, bool SKIP>
+// MODE as in hist_root_gh; BUF: root_buffers holds for the tail's spans
+// (loads through buffer resources bounded at the span's last whole pair).
+template <int MODE, bool SKIP, bool BUF>
 __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __restrict__ bins_fm, int64_t ld,
                                                const float* __restrict__ grad, const float* __restrict__ hess,
                                                int64_t n, int F, double scg, double sch,
@@ -658,37 +660,82 @@ __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __res
         }
     };
     const uint8_t* colp = bins_fm + (size_t)(fok ? f : f0) * ld;
-    // Inputs of step s (unconditional loads, as in hist_root_gh): g and h of
-    // this lane's row pair, clamped to the last whole pair (n2 >= 2, so the
-    // 8-byte loads stay inside the arrays), and 8 rows of its feature's bins:
-    // rA % 8 == 0 and rA < hi <= n <= ld (ld % 16 == 0), or lo when past hi.
+    // Inputs of step s: g and h of this lane's row pair, and 8 rows of its
+    // feature's bins.
+    //   BUF: offsets from the span's first row (even, like the pairs, so no
+    //   8-byte load straddles the end hi2 of the resources: pairs past it
+    //   read zeros); the bins' resource ends with the last feature below F.
+    //   Otherwise unconditional loads: the pair clamped to the last whole
+    //   pair (n2 >= 2, so the 8-byte loads stay inside the arrays; its words
+    //   are masked below), and the bins at rA % 8 == 0 with rA < hi <= n <=
+    //   ld (ld % 16 == 0), or at lo when past hi.
+    const int nf = F - f0;
+    const uint32_t rpos = (uint32_t)(wave * (2 * WAVE) + 32 * qw + 8 * a);
+    const __amdgpu_buffer_rsrc_t rsg = raw_rsrc(grad + lo, BUF ? (uint32_t)((hi2 - lo) * 4) : 0u);
+    const __amdgpu_buffer_rsrc_t rsh = raw_rsrc(hess + lo, (BUF && HCH) ? (uint32_t)((hi2 - lo) * 4) : 0u);
+    const __amdgpu_buffer_rsrc_t rsb =
+        raw_rsrc(bins_fm + (size_t)f0 * ld + lo, BUF ? (uint32_t)((int64_t)nf * ld - lo) : 0u);
+    const uint32_t vg = (rpos + 2u * (uint32_t)c) * 4u;
+    const uint32_t vb = (uint32_t)((int64_t)c * ld) + rpos;
     auto load = [&](int64_t s, float2& gv, float2& hv, uint2& bw) {
-        const int64_t rA = lo + s * TSTEP + (int64_t)wave * (2 * WAVE) + 32 * qw + 8 * a;
-        const int64_t p = min(rA + 2 * c, n2 - 2);
-        gv = *reinterpret_cast<const float2*>(grad + p);
-        if (HCH) hv = *reinterpret_cast<const float2*>(hess + p);
-        bw = *reinterpret_cast<const uint2*>(colp + (rA < hi ? rA : lo));
+        if (BUF) {
+            typedef int v2i __attribute__((ext_vector_type(2)));
+            const int so = (int)(s * TSTEP);
+            // issued in this order wherever load runs (see the ring below)
+            const v2i gw = __builtin_amdgcn_raw_buffer_load_b64(rsg, (int)vg, so * 4, 0);
+            gv = make_float2(__int_as_float(gw.x), __int_as_float(gw.y));
+            __builtin_amdgcn_sched_barrier(0);
+            if (HCH) {
+                const v2i hw = __builtin_amdgcn_raw_buffer_load_b64(rsh, (int)vg, so * 4, 0);
+                hv = make_float2(__int_as_float(hw.x), __int_as_float(hw.y));
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            const v2i b = __builtin_amdgcn_raw_buffer_load_b64(rsb, (int)vb, so, 0);
+            bw = make_uint2((uint32_t)b.x, (uint32_t)b.y);
+            __builtin_amdgcn_sched_barrier(0);
+        } else {
+            const int64_t rA = lo + s * TSTEP + rpos;
+            const int64_t p = min(rA + 2 * c, n2 - 2);
+            gv = *reinterpret_cast<const float2*>(grad + p);
+            if (HCH) hv = *reinterpret_cast<const float2*>(hess + p);
+            bw = *reinterpret_cast<const uint2*>(colp + (rA < hi ? rA : lo));
+        }
     };
     const int64_t steps = (hi - lo + TSTEP - 1) / TSTEP;
+    // Packed cells need epochs only where the per-fit table's bound over the
+    // span (each column takes a quarter of its rows, at most) reaches
+    // PACKED_CELL_ROWS, as in hist_root_gh.
+    bool epochs = PACK;
+    if (PACK && counts) {
+        const uint32_t* segmax = counts + (size_t)F * NB;
+        const int64_t nseg = count_segments(n);
+        uint32_t bound = 0;
+        if (fok)
+            for (int64_t sg = lo / SEG_ROWS; sg <= (hi - 1) / SEG_ROWS; ++sg) bound += segmax[(size_t)f * nseg + sg];
+        bound = (uint32_t)__builtin_amdgcn_readfirstlane((int)wave_max_u32_v(bound));
+        epochs = (int64_t)bound >= PACKED_CELL_ROWS;
+    }
+    // The ring as in hist_root_gh: TAIL_DEPTH stages, the first round's loads
+    // issued before the loop in the loop's order.
     float2 gs[TAIL_DEPTH], hs[TAIL_DEPTH];
     uint2 bs[TAIL_DEPTH];
 #pragma unroll
     for (int j = 0; j < TAIL_DEPTH; ++j) {
-        gs[j] = make_float2(0.0f, 0.0f);
         hs[j] = make_float2(0.0f, 0.0f);
-        bs[j] = make_uint2(0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        load(j, gs[j], hs[j], bs[j]);
     }
     __syncthreads();
     int64_t sum_g = 0, sum_h = 0;
     uint32_t buf = 0;   // the cell buffer of this ring round's epoch
-    for (int64_t s0 = -TAIL_DEPTH; s0 < steps; s0 += TAIL_DEPTH) {
+    for (int64_t s0 = 0; s0 < steps; s0 += TAIL_DEPTH) {
         const uint32_t lb = PACK ? (lbase | (buf << 7)) : lbase;
 #pragma unroll
         for (int j = 0; j < TAIL_DEPTH; ++j) {
             const int64_t s = s0 + j;
             __builtin_amdgcn_sched_barrier(0);
-            const int64_t p = lo + s * TSTEP + (int64_t)wave * (2 * WAVE) + 32 * qw + 8 * a + 2 * c;
-            const bool ok0 = s >= 0 && p < hi2, ok1 = s >= 0 && p + 1 < hi2;
+            const int64_t p = lo + s * TSTEP + rpos + 2 * c;
+            const bool ok0 = BUF || p < hi2, ok1 = BUF || p + 1 < hi2;
             const int64_t g0 = ok0 ? (PACK ? quantise_node(gs[j].x, scg) : quantise_wide(gs[j].x, scg)) : 0;
             const int64_t g1 = ok1 ? (PACK ? quantise_node(gs[j].y, scg) : quantise_wide(gs[j].y, scg)) : 0;
             const int64_t h0 = (HCH && ok0) ? (PACK ? quantise_node(hs[j].x, sch) : quantise_wide(hs[j].x, sch)) : 0;
@@ -702,8 +749,10 @@ __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __res
                 if (SKIP && (int)((wv[J >> 2] >> (8 * (J & 3))) & 0xffu) == d) keep &= ~(1u << J);
             }
             load(s + TAIL_DEPTH, gs[j], hs[j], bs[j]);
-            sum_g += g0 + g1;
-            sum_h += h0 + h1;
+            if (SKIP) {
+                sum_g += g0 + g1;
+                sum_h += h0 + h1;
+            }
             const uint64_t w0 = PACK ? ((uint64_t)g0 << 32) + (uint64_t)h0 : (uint64_t)g0;
             const uint64_t w1 = PACK ? ((uint64_t)g1 << 32) + (uint64_t)h1 : (uint64_t)g1;
             // ROOT_WIDE: the h cell is the g cell's twin in the other buffer
@@ -722,7 +771,7 @@ __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __res
             YABT_TAIL_ADD(4) YABT_TAIL_ADD(5) YABT_TAIL_ADD(6) YABT_TAIL_ADD(7)
 #undef YABT_TAIL_ADD
         }
-        if (PACK) {
+        if (epochs) {
             // end of the epoch: read this round's buffer while the next round
             // adds into the other one
             __syncthreads();
@@ -736,7 +785,7 @@ __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __res
             const int64_t r = n - 1;
             const int64_t gq = PACK ? quantise_node(grad[r], scg) : quantise_wide(grad[r], scg);
             const int64_t hq = HCH ? (PACK ? quantise_node(hess[r], sch) : quantise_wide(hess[r], sch)) : 0;
-            if (c == 0) {
+            if (SKIP && c == 0) {
                 sum_g += gq;
                 sum_h += hq;
             }
@@ -750,9 +799,10 @@ __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __res
             }
         }
         __syncthreads();
-        if (PACK) unpack((int)buf);
+        if (epochs) unpack((int)buf);
     }
     __syncthreads();
+    if (PACK && !epochs) unpack(0);
     if (!PACK) {   // never unpacked: the cells are the g sums (and the h sums)
 #pragma unroll
         for (int k = 0; k < RENT; ++k) {
@@ -761,6 +811,17 @@ __device__ __forceinline__ void hist_root_tail(HistLdsR& L, const uint8_t* __res
         }
     }
     if (totals) {
+        if (!SKIP) {   // thread t's cells are of column t % HFL, feature t % TAILF
+            sum_g = 0;
+            sum_h = 0;
+            if (threadIdx.x % TAILF == 0) {
+#pragma unroll
+                for (int k = 0; k < RENT; ++k) {
+                    sum_g += ag[k];
+                    sum_h += ah[k];
+                }
+            }
+        }
         sum_g = wave_sum<int64_t>(sum_g);
         sum_h = wave_sum<int64_t>(sum_h);
         if (lane == 0) {
@@ -897,13 +958,13 @@ k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld, const float* __rest
     const int bid = (int)blockIdx.x;
     if (bid < tail) {
         if (no_h)
-            hist_root_tail<ROOT_G, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
+            hist_root_tail<ROOT_G, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
                                          tail_rows, bid);
         else if (wide)
-            hist_root_tail<ROOT_WIDE, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
+            hist_root_tail<ROOT_WIDE, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
                                             tail_rows, bid);
         else
-            hist_root_tail<ROOT_PACKED, SKIP>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
+            hist_root_tail<ROOT_PACKED, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
                                               tail_rows, bid);
         return;
     }
@@ -926,7 +987,7 @@ static __attribute__((unused)) void launch_root_kernel(hipStream_t stream, const
                                                        int F, const Quant* q, double scg, double sch, int wide,
                                                        const int32_t* dflt, const uint32_t* counts, Quant* q_tot,
                                                        int64_t* out, int count_mode, const int32_t* done) {
-    const bool buf = root_buffers(ld, root_chunk_rows(n, g.chunks));
+    const bool buf = root_buffers(ld, max(root_chunk_rows(n, g.chunks), g.tail_rows));
 #define YABT_ROOT_LAUNCH(S, B)                                                                                     \
     k_hist_root<S, B><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, wide, dflt,   \
                                                        counts, q_tot, out, g.chunks, g.tail, g.tail_rows,          \
