@@ -203,6 +203,10 @@ size_t yabt_leaf_fit_workspace_bytes(int64_t n, int n_nodes, int K);
  * envelopes of `fit_leaf_networks` (yabt/neural_leaves.py:157-176).
  *   x_kind 0: X is fp32 row-major (n, ldx), input j of row i = X[i*ldx + feats[j]];
  *   x_kind 1: X is uint8 feature-major (F, ldx >= n), input = (float)X[feats[j]*ldx + i];
+ *   x_kind 2: X is fp32 feature-major (F, ldx >= n), input = X[feats[j]*ldx + i]
+ *     (the same results as x_kind 0 on the transposed matrix; the row passes
+ *     read four rows of a column with one 16-byte load when X is 16-byte
+ *     aligned and ldx % 4 == 0);
  *   leaf_of_row (n) node ids in [0, n_nodes); mu, sd (K) fp32; 1 <= K <= 8.
  * Outputs (device): out_W (n_nodes, K) and out_b (n_nodes) in the standardised
  * inputs (zero where not fitted); out_lo/out_hi (n_nodes, K) per-node min/max of
@@ -436,7 +440,8 @@ int yabt_grad_hess(int loss, const float *margin, const int64_t *leaf_of_row, co
  *   l = leaf_of_row[i] in [0, n_nodes) (rows with other ids are left unchanged);
  *   K = 0 adds value[l] only (no leaf models);
  * inputs x_ij as in yabt_leaf_fit (x_kind 0: fp32 row-major X[i*ldx + feats[j]];
- * x_kind 1: uint8 feature-major X[feats[j]*ldx + i]); 0 <= K <= 8.
+ * x_kind 1: uint8 feature-major X[feats[j]*ldx + i]; x_kind 2: fp32
+ * feature-major X[feats[j]*ldx + i]); 0 <= K <= 8.
  * Replaces `contrib = tree.value[leaf_idx] + tree.net_contribution(Xraw,
  * leaf_idx); margin = margin + contrib` (yabt/boosting.py:508-511,
  * yabt/tree.py:118-128). */

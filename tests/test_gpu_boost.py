@@ -128,6 +128,12 @@ def test_margin_update_bit_exact(K):
     boost_ops.margin_update(out, _t(leaf), _tree_of(d), _t(Xpad)[:, :F], x_kind=0)
     want = (margin + BO.tree_output(d, X, leaf)).astype(np.float32)
     assert np.array_equal(out.cpu().numpy(), want)
+    # the same inputs fp32 feature-major (the estimators' per-fit copy)
+    Xfm = np.zeros((F, n + 3), np.float32)
+    Xfm[:, :n] = X.T
+    out = _t(margin)
+    boost_ops.margin_update(out, _t(leaf), _tree_of(d), _t(Xfm), x_kind=2)
+    assert np.array_equal(out.cpu().numpy(), want)
     # uint8 feature-major inputs, x = float(bin)
     bins = rng.integers(0, 256, size=(F, n + 13), dtype=np.uint8)
     if K:

@@ -140,6 +140,29 @@ def test_leaf_fit_deterministic_and_u8_equals_f32(gram):
             np.testing.assert_allclose(u, w, rtol=1e-6, atol=1e-9)
 
 
+@pytest.mark.parametrize("n,K,n_nodes,ld_pad", [(50_000, 6, 63, 0), (20_003, 8, 31, 1), (777, 1, 7, 3),
+                                                 (1_000_001, 7, 255, 0), (40_000, 3, 1501, 1)])
+def test_leaf_fit_f32_feature_major_equals_row_major(n, K, n_nodes, ld_pad):
+    """fp32 inputs feature-major (x_kind 2, the estimators' per-fit copy):
+    the same bits as row-major (x_kind 0), fit and moments, with the 4-row
+    vector loads (ld a multiple of 4, ld_pad 0) and without them (odd ld)."""
+    X, Xf, feats, g, h, feature, leaf, mu, sd = _problem(n + 11, n, K, n_nodes)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+    ld = (n + 3) // 4 * 4 + ld_pad
+    Xp = np.zeros((Xf.shape[1], ld), np.float32)
+    Xp[:, :n] = Xf.T
+    row = leaf_fit(t(Xf), 0, t(feats), t(mu), t(sd), t(g), t(h), t(leaf), t(feature), 50, 1e-3)
+    col = leaf_fit(t(Xp), 2, t(feats), t(mu), t(sd), t(g), t(h), t(leaf), t(feature), 50, 1e-3)
+    for u, v in zip(row, col):
+        assert np.array_equal(u.cpu().numpy(), v.cpu().numpy())
+    m0 = [v.cpu().numpy() for v in leaf_moments(t(Xf), 0, t(feats), n)]
+    m2 = [v.cpu().numpy() for v in leaf_moments(t(Xp), 2, t(feats), n)]
+    assert np.array_equal(m0[0], m2[0]) and np.array_equal(m0[1], m2[1])
+    rW, rb, rlo, rhi, rcnt = _oracle(Xf, feats, g, h, feature, leaf, mu, sd, 50, 1e-3)
+    np.testing.assert_allclose(col[0].cpu().numpy(), rW, rtol=1e-5, atol=1e-6)
+    assert np.array_equal(col[4].cpu().numpy(), rcnt)
+
+
 @pytest.mark.parametrize("K", [1, 5, 8])
 def test_leaf_fold_equals_torch_expressions(K):
     """yabt_leaf_fold bit for bit against the reference's own torch fold

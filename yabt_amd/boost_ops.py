@@ -69,8 +69,8 @@ def grad_hess(loss, margin: torch.Tensor, y: torch.Tensor, leaf: torch.Tensor | 
 def margin_update(margin: torch.Tensor, leaf: torch.Tensor, tree: Tree, X: torch.Tensor,
                   x_kind: int = 0) -> torch.Tensor:
     """In place: margin += tree.value[leaf] (+ tree.net_contribution(X, leaf)).
-    X is fp32 (n, F) row-major (x_kind 0) or uint8 feature-major (F, ld >= n)
-    (x_kind 1, inputs float(bin))."""
+    X is fp32 (n, F) row-major (x_kind 0), uint8 feature-major (F, ld >= n)
+    (x_kind 1, inputs float(bin)) or fp32 feature-major (F, ld >= n) (x_kind 2)."""
     dev = _need_device(margin, leaf)
     if margin.dtype != torch.float32 or not margin.is_contiguous():
         raise ValueError("margin must be a contiguous float32 tensor (updated in place)")
@@ -97,8 +97,9 @@ def margin_update(margin: torch.Tensor, leaf: torch.Tensor, tree: Tree, X: torch
             if int(feats.max()) >= X.shape[1] or int(feats.min()) < 0:
                 raise ValueError("leaf-model inputs out of range of X")
         else:
-            if X.dtype != torch.uint8 or X.dim() != 2 or X.shape[1] < n or X.stride(1) != 1:
-                raise ValueError("X must be uint8 (F, ld >= n)")
+            dt = torch.uint8 if x_kind == 1 else torch.float32
+            if X.dtype != dt or X.dim() != 2 or X.shape[1] < n or X.stride(1) != 1:
+                raise ValueError(f"X must be {'uint8' if x_kind == 1 else 'fp32'} (F, ld >= n)")
             if int(feats.max()) >= X.shape[0] or int(feats.min()) < 0:
                 raise ValueError("leaf-model inputs out of range of X")
         Xp, ldx = X, X.stride(0)

@@ -43,7 +43,7 @@ from . import boost_ops
 from .binning import Binner
 from .grow_hip import grow_device, grow_tree_hip, leaf_ids, nbins_of, tree_from_result
 from .losses import LogLoss, MSELoss
-from .neural_leaves import fit_leaf_networks
+from .neural_leaves import feature_major, fit_leaf_networks
 from .tree import Tree, TreeParams
 
 # interaction steering is switched off below this row count (boosting.py:21-24)
@@ -306,6 +306,7 @@ class Booster:
         # arithmetic depends on it (exact sums are the same either way)
         sparse_db = (self._sparse_default_bins(lay, n, F) if p.grower_arithmetic == "reference" else None)
 
+        X_fm = None   # feature-major copy of Xraw for the leaf models, made at the first tree
         for t in range(p.n_estimators):
             grad, hess = boost_ops.grad_hess(self.loss, margin, yt)
 
@@ -346,12 +347,18 @@ class Booster:
                 leaf_idx = tree.apply(Xraw)
 
             if p.neural_leaves:
-                tree = fit_leaf_networks(tree, Xraw, yt, margin, self.loss, p, gen, leaf_idx=leaf_idx)
+                if X_fm is None:
+                    X_fm = feature_major(Xraw)
+                tree = fit_leaf_networks(tree, Xraw, yt, margin, self.loss, p, gen, leaf_idx=leaf_idx,
+                                         X_fmajor=X_fm)
 
             if self.interaction_detector is not None:
                 self.interaction_detector.update_from_path_pairs(tree.path_feature_pairs())
 
-            boost_ops.margin_update(margin, leaf_idx, tree, Xraw)
+            if X_fm is not None:
+                boost_ops.margin_update(margin, leaf_idx, tree, X_fm, x_kind=2)
+            else:
+                boost_ops.margin_update(margin, leaf_idx, tree, Xraw)
             self.trees.append(tree)
 
             if eval_set is not None:

@@ -62,8 +62,9 @@ __global__ void __launch_bounds__(BB) k_margin_update(float* __restrict__ margin
             float net = 0.0f;
 #pragma unroll
             for (int j = 0; j < K; ++j) {
-                float x = x_kind == 0 ? reinterpret_cast<const float*>(X)[(size_t)i * (size_t)ldx + s_fs[j]]
-                                      : (float)reinterpret_cast<const uint8_t*>(X)[(size_t)s_fs[j] * (size_t)ldx + i];
+                float x = x_kind == 0   ? reinterpret_cast<const float*>(X)[(size_t)i * (size_t)ldx + s_fs[j]]
+                          : x_kind == 2 ? reinterpret_cast<const float*>(X)[(size_t)s_fs[j] * (size_t)ldx + i]
+                                        : (float)reinterpret_cast<const uint8_t*>(X)[(size_t)s_fs[j] * (size_t)ldx + i];
                 x = fminf(fmaxf(x, lo[node * K + j]), hi[node * K + j]);
                 net += lin[node * K + j] * x;
             }
@@ -152,8 +153,8 @@ int yabt_grad_hess(int loss, const float* margin, const int64_t* leaf_of_row, co
 int yabt_margin_update(float* margin, int64_t n, const int64_t* leaf_of_row, const float* value, int64_t n_nodes,
                        int K, const int32_t* feats, const float* linear, const float* lo, const float* hi, int x_kind,
                        const void* X, int64_t ldx, hipStream_t stream) {
-    if (n < 0 || n_nodes < 1 || K < 0 || K > 8 || (K > 0 && x_kind != 0 && x_kind != 1))
-        return fail(-2, "yabt_margin_update: bad sizes (n_nodes >= 1, 0 <= K <= 8, x_kind 0 or 1)");
+    if (n < 0 || n_nodes < 1 || K < 0 || K > 8 || (K > 0 && (x_kind < 0 || x_kind > 2)))
+        return fail(-2, "yabt_margin_update: bad sizes (n_nodes >= 1, 0 <= K <= 8, x_kind 0, 1 or 2)");
     if (n == 0) return 0;
     if (!margin || !leaf_of_row || !value || (K > 0 && (!feats || !linear || !lo || !hi || !X)))
         return fail(-2, "yabt_margin_update: null pointer argument");

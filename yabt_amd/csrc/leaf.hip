@@ -57,7 +57,8 @@ struct LeafStats {
 };
 
 struct LeafArgs {
-    int x_kind;                // 0: fp32 row-major (n, ldx); 1: uint8 feature-major (F, ldx)
+    int x_kind;                // 0: fp32 row-major (n, ldx); 1: uint8 feature-major (F, ldx);
+                               // 2: fp32 feature-major (F, ldx)
     const void* X;
     int64_t ldx;
     int64_t n;
@@ -73,7 +74,8 @@ struct LeafArgs {
     double lam;
     int gram_f64;              // 1: M and b summed in fp64 by MFMA (parts and sums hold double bits)
     int64_t rows_per_block;    // stats/scatter rows per block (a multiple of 4)
-    int vec4;                  // 1: uint8 inputs, leaf ids, g and h aligned for 4-row vector loads
+    int vec4;                  // leaf ids, g, h and feature-major inputs aligned for 4-row vector
+                               // loads: 1 uint8 inputs, 2 fp32 inputs; 0 none
     // workspace
     LeafStats* st;
     uint32_t* count;           // (n_nodes)
@@ -99,6 +101,10 @@ __device__ __forceinline__ void load_x(const LeafArgs& A, int64_t i, const int32
         const float* row = reinterpret_cast<const float*>(A.X) + (size_t)i * (size_t)A.ldx;
 #pragma unroll
         for (int j = 0; j < K; ++j) x[j] = row[fs[j]];
+    } else if (A.x_kind == 2) {
+        const float* Xf = reinterpret_cast<const float*>(A.X);
+#pragma unroll
+        for (int j = 0; j < K; ++j) x[j] = Xf[(size_t)fs[j] * (size_t)A.ldx + (size_t)i];
     } else {
         const uint8_t* B = reinterpret_cast<const uint8_t*>(A.X);
 #pragma unroll
@@ -145,6 +151,37 @@ __device__ __forceinline__ void load_rows4(const LeafArgs& A, const int32_t* fs,
     const uint8_t* B = reinterpret_cast<const uint8_t*>(A.X);
 #pragma unroll
     for (int j = 0; j < K; ++j) R.xw[j] = *reinterpret_cast<const uint32_t*>(B + (size_t)fs[j] * (size_t)A.ldx + (size_t)i);
+    R.node[0] = la.x;
+    R.node[1] = la.y;
+    R.node[2] = lb.x;
+    R.node[3] = lb.y;
+    R.g[0] = g4.x;
+    R.g[1] = g4.y;
+    R.g[2] = g4.z;
+    R.g[3] = g4.w;
+    R.h[0] = h4.x;
+    R.h[1] = h4.y;
+    R.h[2] = h4.z;
+    R.h[3] = h4.w;
+}
+
+// The same four rows with fp32 feature-major inputs (A.vec4 == 2): one float4
+// per input column.
+template <int K>
+struct Rows4F {
+    int64_t node[4];
+    float g[4], h[4];
+    float4 x[K];
+};
+template <int K>
+__device__ __forceinline__ void load_rows4f(const LeafArgs& A, const int32_t* fs, int64_t i, Rows4F<K>& R) {
+    const longlong2 la = *reinterpret_cast<const longlong2*>(A.leaf + i);
+    const longlong2 lb = *reinterpret_cast<const longlong2*>(A.leaf + i + 2);
+    const float4 g4 = *reinterpret_cast<const float4*>(A.grad + i);
+    const float4 h4 = *reinterpret_cast<const float4*>(A.hess + i);
+    const float* Xf = reinterpret_cast<const float*>(A.X);
+#pragma unroll
+    for (int j = 0; j < K; ++j) R.x[j] = *reinterpret_cast<const float4*>(Xf + (size_t)fs[j] * (size_t)A.ldx + (size_t)i);
     R.node[0] = la.x;
     R.node[1] = la.y;
     R.node[2] = lb.x;
@@ -375,7 +412,22 @@ __global__ void __launch_bounds__(LSB) k_leaf_scatter_stats(LeafArgs A) {
         }
     };
     const int64_t ng = A.vec4 ? (hi - lo) / 4 : 0, first = lo + 4 * ng;
-    for (int64_t q = threadIdx.x; q < ng; q += LSB) {
+    if (A.vec4 == 2) {
+        for (int64_t q = threadIdx.x; q < ng; q += LSB) {
+            Rows4F<K> R;
+            load_rows4f<K>(A, s_fs, lo + 4 * q, R);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int64_t node = R.node[r];
+                if (node < 0 || node >= A.n_nodes) continue;
+                float x[K];
+#pragma unroll
+                for (int j = 0; j < K; ++j) x[j] = r == 0 ? R.x[j].x : r == 1 ? R.x[j].y : r == 2 ? R.x[j].z : R.x[j].w;
+                put(node, x, R.g[r], R.h[r], make_uint2(0, 0));
+            }
+        }
+    }
+    for (int64_t q = threadIdx.x; A.vec4 == 1 && q < ng; q += LSB) {
         Rows4<K> R;
         load_rows4<K>(A, s_fs, lo + 4 * q, R);
 #pragma unroll
@@ -453,10 +505,11 @@ __device__ __forceinline__ void put_sorted(const LeafArgs& A, const int32_t* fs,
         }
         reinterpret_cast<uint2*>(A.sorted_x)[pos] = make_uint2(w0, w1);
     } else {
-        const float* row = reinterpret_cast<const float*>(A.X) + (size_t)i * (size_t)A.ldx;
+        float x[K];
+        load_x<K>(A, i, fs, x);
         float* dst = reinterpret_cast<float*>(A.sorted_x) + pos * K;
 #pragma unroll
-        for (int j = 0; j < K; ++j) dst[j] = row[fs[j]];
+        for (int j = 0; j < K; ++j) dst[j] = x[j];
     }
 }
 
@@ -1050,10 +1103,8 @@ void launch_leaf_fit(LeafArgs& A, float* out_W, float* out_b, float* out_lo, flo
     per = per < LROWS ? LROWS : (per + LSB - 1) / LSB * LSB;
     A.rows_per_block = per;
     const auto al = [](const void* p, uintptr_t a) { return ((uintptr_t)p % a) == 0; };
-    A.vec4 = (lds && A.x_kind == 1 && al(A.leaf, 16) && al(A.grad, 16) && al(A.hess, 16) && al(A.X, 4) &&
-              A.ldx % 4 == 0 && per % 4 == 0)
-                 ? 1
-                 : 0;
+    const bool rows_al = lds && al(A.leaf, 16) && al(A.grad, 16) && al(A.hess, 16) && A.ldx % 4 == 0 && per % 4 == 0;
+    A.vec4 = (rows_al && A.x_kind == 1 && al(A.X, 4)) ? 1 : (rows_al && A.x_kind == 2 && al(A.X, 16)) ? 2 : 0;
     const int row_blocks = (int)((A.n + per - 1) / per);
     k_leaf_init<<<launch_grid((int64_t)A.n_nodes * gram_entries(LKMAX), LB, 1024), LB, 0, stream>>>(A, K);
     if (lds) {
@@ -1310,13 +1361,13 @@ int yabt_leaf_fit(int x_kind, const void* X, int64_t ldx, int64_t n, const int32
                   const int64_t* feature, int n_nodes, int min_samples, double lam, int gram_mode,
                   void* workspace, size_t workspace_bytes, float* out_W, float* out_b, float* out_lo,
                   float* out_hi, int64_t* out_count, int32_t* out_status, hipStream_t stream) {
-    if (n < 0 || n > 0xFFFFFFFFll || n_nodes < 1 || K < 1 || K > LKMAX || (x_kind != 0 && x_kind != 1))
-        return fail(-2, "yabt_leaf_fit: bad sizes (need 0 <= n < 2^32, n_nodes >= 1, 1 <= K <= 8, x_kind 0 or 1)");
+    if (n < 0 || n > 0xFFFFFFFFll || n_nodes < 1 || K < 1 || K > LKMAX || x_kind < 0 || x_kind > 2)
+        return fail(-2, "yabt_leaf_fit: bad sizes (need 0 <= n < 2^32, n_nodes >= 1, 1 <= K <= 8, x_kind 0, 1 or 2)");
     if (gram_mode != 0 && gram_mode != 1) return fail(-2, "yabt_leaf_fit: gram_mode must be 0 or 1");
     if (!X || !feats || !mu || !sd || !grad || !hess || !leaf_of_row || !feature || !workspace || !out_W || !out_b ||
         !out_lo || !out_hi || !out_count || !out_status)
         return fail(-2, "yabt_leaf_fit: null pointer argument");
-    if (x_kind == 1 ? ldx < n : ldx < 1) return fail(-2, "yabt_leaf_fit: leading dimension too small");
+    if (x_kind != 0 ? ldx < n : ldx < 1) return fail(-2, "yabt_leaf_fit: leading dimension too small");
     LeafArgs A;
     memset(&A, 0, sizeof A);
     const size_t need = carve_leaf((char*)workspace, n, n_nodes, K, &A);
@@ -1379,10 +1430,10 @@ size_t yabt_leaf_moments_workspace_bytes(int64_t n) {
 
 int yabt_leaf_moments(int x_kind, const void* X, int64_t ldx, int64_t n, const int32_t* feats, int K,
                       void* workspace, size_t workspace_bytes, float* out_mu, float* out_sd, hipStream_t stream) {
-    if (n < 1 || K < 1 || K > LKMAX || (x_kind != 0 && x_kind != 1))
-        return fail(-2, "yabt_leaf_moments: bad sizes (need n >= 1, 1 <= K <= 8, x_kind 0 or 1)");
+    if (n < 1 || K < 1 || K > LKMAX || x_kind < 0 || x_kind > 2)
+        return fail(-2, "yabt_leaf_moments: bad sizes (need n >= 1, 1 <= K <= 8, x_kind 0, 1 or 2)");
     if (!X || !feats || !workspace || !out_mu || !out_sd) return fail(-2, "yabt_leaf_moments: null pointer argument");
-    if (x_kind == 1 ? ldx < n : ldx < 1) return fail(-2, "yabt_leaf_moments: leading dimension too small");
+    if (x_kind != 0 ? ldx < n : ldx < 1) return fail(-2, "yabt_leaf_moments: leading dimension too small");
     if (workspace_bytes < yabt_leaf_moments_workspace_bytes(n)) return fail(-2, "yabt_leaf_moments: workspace too small");
     const int nb = (int)((n + MROWS - 1) / MROWS);
     double* part = (double*)workspace;

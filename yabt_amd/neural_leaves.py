@@ -82,8 +82,9 @@ def _leaf_fit(X: torch.Tensor, x_kind: int, feats: torch.Tensor, mu: torch.Tenso
             raise ValueError("X must be fp32 (n, F) with unit column stride")
         ldx = X.stride(0)
     else:
-        if X.dtype != torch.uint8 or X.dim() != 2 or X.shape[1] < n or X.stride(1) != 1:
-            raise ValueError("X must be uint8 (F, ld >= n)")
+        dt = torch.uint8 if x_kind == 1 else torch.float32
+        if X.dtype != dt or X.dim() != 2 or X.shape[1] < n or X.stride(1) != 1:
+            raise ValueError(f"X must be {'uint8' if x_kind == 1 else 'fp32'} (F, ld >= n)")
         ldx = X.stride(0)
     fi = feats.to(dev, torch.int32).contiguous()
     m = mu.to(dev, torch.float32).contiguous()
@@ -122,8 +123,9 @@ def _check_status(st: int) -> None:
 def leaf_fit(X: torch.Tensor, x_kind: int, feats: torch.Tensor, mu: torch.Tensor, sd: torch.Tensor,
              grad: torch.Tensor, hess: torch.Tensor, leaf_idx: torch.Tensor, feature: torch.Tensor,
              min_samples: int, lam: float, gram: str | None = None):
-    """One ``yabt_leaf_fit`` call.  X: fp32 (n, F) row-major (x_kind 0) or
-    uint8 feature-major (F, ld >= n) (x_kind 1).  Returns (W (N, K), b (N),
+    """One ``yabt_leaf_fit`` call.  X: fp32 (n, F) row-major (x_kind 0),
+    uint8 feature-major (F, ld >= n) (x_kind 1) or fp32 feature-major (F, ld
+    >= n) (x_kind 2).  Returns (W (N, K), b (N),
     lo (N, K), hi (N, K), count (N)) on X's device; W, b act on the
     standardised inputs.  gram: "exact" or "mfma" (default GRAM)."""
     W, b, lo, hi, cnt, status = _leaf_fit(X, x_kind, feats, mu, sd, grad, hess, leaf_idx, feature, min_samples,
@@ -142,6 +144,8 @@ def leaf_moments(X: torch.Tensor, x_kind: int, feats: torch.Tensor, n: int):
         raise ValueError("X must be fp32 (n, F) with unit column stride")
     if x_kind == 1 and (X.dtype != torch.uint8 or X.shape[1] < n or X.stride(1) != 1):
         raise ValueError("X must be uint8 (F, ld >= n)")
+    if x_kind == 2 and (X.dtype != torch.float32 or X.shape[1] < n or X.stride(1) != 1):
+        raise ValueError("X must be fp32 (F, ld >= n)")
     fi = feats.to(dev, torch.int32).contiguous()
     nbytes = int(lib.yabt_leaf_moments_workspace_bytes(n))
     ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
@@ -190,6 +194,8 @@ def _leaf_step(tree: Tree, X: torch.Tensor, x_kind: int, n: int, feats: torch.Te
         raise ValueError("X must be fp32 (n, F) with unit column stride")
     if x_kind == 1 and (X.dtype != torch.uint8 or X.dim() != 2 or X.shape[1] < n or X.stride(1) != 1):
         raise ValueError("X must be uint8 (F, ld >= n)")
+    if x_kind == 2 and (X.dtype != torch.float32 or X.dim() != 2 or X.shape[1] < n or X.stride(1) != 1):
+        raise ValueError("X must be fp32 (F, ld >= n)")
     fi = None if rank_k else feats.to(dev, torch.int32).contiguous()
     g = grad.to(dev, torch.float32).contiguous()
     h = hess.to(dev, torch.float32).contiguous()
@@ -250,10 +256,26 @@ def _leaf_step(tree: Tree, X: torch.Tensor, x_kind: int, n: int, feats: torch.Te
                    leaf_net_hi=hi)
 
 
+def feature_major(Xraw: torch.Tensor) -> torch.Tensor:
+    """A feature-major fp32 copy (F, ld) of the raw inputs (n, F), ld the
+    row count rounded up to a multiple of 4, so that every column starts
+    16-byte aligned: the leaf models' row passes then read four rows of an
+    input with one vector load (yabt_leaf_fit's x_kind 2).  Made once per fit
+    (n F 4 bytes: 400 MB at 2M x 50)."""
+    n, F = Xraw.shape
+    ld = (n + 3) // 4 * 4
+    out = torch.zeros((F, ld), dtype=torch.float32, device=Xraw.device)
+    out[:, :n] = Xraw.t()
+    return out
+
+
 def fit_leaf_networks(tree: Tree, Xraw: torch.Tensor, y: torch.Tensor, margin: torch.Tensor, loss_fn,
-                      params, gen: torch.Generator | None = None, leaf_idx: torch.Tensor | None = None) -> Tree:
+                      params, gen: torch.Generator | None = None, leaf_idx: torch.Tensor | None = None,
+                      X_fmajor: torch.Tensor | None = None) -> Tree:
     """Drop-in for yabt.neural_leaves.fit_leaf_networks (neural_leaves.py:131-184),
-    linear leaves; Xraw (n, F) fp32 on a HIP device."""
+    linear leaves; Xraw (n, F) fp32 on a HIP device.  ``X_fmajor``: the same
+    inputs feature-major (``feature_major(Xraw)``), kept by a caller that
+    fits many trees on them; the models are the same either way."""
     if getattr(params, "leaf_net_hidden", 0) != 0:
         raise NotImplementedError("MLP leaves (leaf_net_hidden > 0) are not provided by this backend")
     dev = Xraw.device
@@ -262,9 +284,21 @@ def fit_leaf_networks(tree: Tree, Xraw: torch.Tensor, y: torch.Tensor, margin: t
     if leaf_idx is None:
         leaf_idx = tree_d.apply(Xraw)
     grad, hess = boost_ops.grad_hess(loss_fn, margin, y, leaf_idx, tree_d.value)
+    n, F = Xraw.shape
+    k = min(getattr(params, "leaf_net_features", 8), F)
+    if X_fmajor is not None and 1 <= k <= 8 and F <= RANK_MAX_FEATURES:
+        # the split features ranked on the device (the reference's order,
+        # neural_leaves.py:27-31); None when the tree uses fewer than k, which
+        # the host then pads by gradient correlation
+        out = _leaf_step(tree_d, X_fmajor, 2, n, None, grad, hess, leaf_idx, params, rank_k=k)
+        if out is not None:
+            return tree if out is tree_d else out
     feats = _select_features(tree_d, Xraw, grad, getattr(params, "leaf_net_features", 8))
     if feats.numel() == 0:
         return tree
+    if X_fmajor is not None:
+        out = _leaf_step(tree_d, X_fmajor, 2, Xraw.shape[0], feats, grad, hess, leaf_idx, params)
+        return tree if out is tree_d else out
     X = Xraw if Xraw.dtype == torch.float32 and Xraw.stride(1) == 1 else Xraw.float().contiguous()
     out = _leaf_step(tree_d, X, 0, X.shape[0], feats, grad, hess, leaf_idx, params)
     return tree if out is tree_d else out
