@@ -86,3 +86,28 @@ def test_ten_class_linear_leaves(max_leaves, n_trees, K_padded):
     assert np.abs(P - Po).max() <= 1e-5
     assert np.allclose(P.sum(axis=1), 1.0)
     assert (est.predict(Xt) == np.argmax(Po, axis=1)).mean() > 0.999
+
+
+def test_concurrent_class_fits_equal_sequential():
+    """The class boosters fitted on concurrent streams (4 threads) are the
+    sequential fit's, bit for bit: node arrays, values, leaf models and the
+    training margins."""
+    from yabt_amd.boosting import BoostParams, MulticlassBooster
+    print("10-class one-vs-rest, concurrent vs sequential class fits, 60000 x 30", flush=True)
+    X, y = _softmax_classes(60_000, 30, 10, seed=23)
+    p = BoostParams(n_estimators=4, max_leaves=31, learning_rate=0.1, max_bins=256, neural_leaves=True,
+                    leaf_net_features=8, leaf_net_l2=1e-3)
+    seq = MulticlassBooster(p, concurrency=1).fit(X, y)
+    con = MulticlassBooster(p, concurrency=4).fit(X, y)
+    assert len(seq.boosters_) == len(con.boosters_) == 10
+    for a, b in zip(seq.boosters_, con.boosters_):
+        assert np.array_equal(a.margin_.cpu().numpy().view(np.uint32), b.margin_.cpu().numpy().view(np.uint32))
+        for ta, tb in zip(a.trees, b.trees):
+            for k in ("feature", "threshold", "left", "right", "value", "leaf_net_feats", "leaf_net_linear",
+                      "leaf_net_lo", "leaf_net_hi"):
+                u, v = getattr(ta, k), getattr(tb, k)
+                assert (u is None) == (v is None)
+                if u is not None:
+                    assert np.array_equal(u.cpu().numpy(), v.cpu().numpy()), k
+    Xt, _ = _softmax_classes(2000, 30, 10, seed=24)
+    assert np.array_equal(seq.predict_proba(Xt), con.predict_proba(Xt))

@@ -34,6 +34,8 @@ There is no CPU execution: ``device="cpu"`` is rejected.
 
 from __future__ import annotations
 
+import threading
+from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass, fields, replace
 
 import numpy as np
@@ -265,7 +267,9 @@ class Booster:
             eval_set: tuple[np.ndarray, np.ndarray] | None = None, prepared: tuple | None = None,
             on_tree=None) -> "Booster":
         """The reference's training loop (boosting.py:271-534) on the device.
-        ``prepared``: the result of ``prepare(X)`` for this X, if already made.
+        ``prepared``: the result of ``prepare(X)`` for this X, if already made
+        (optionally followed by ``feature_major`` of its imputed X, for the
+        leaf models).
         ``on_tree``: called after each tree grown on all rows as
         on_tree(t, inputs, result) with the grower's inputs (dict: layouts,
         grad, hess, nbins, imat, fmask, and the grower keywords) and its
@@ -280,7 +284,7 @@ class Booster:
         self.best_iter = None
         self._forest = None
 
-        self.binner, lay, Xraw = prepared if prepared is not None else self.prepare(X)
+        self.binner, lay, Xraw = (prepared if prepared is not None else self.prepare(X))[:3]
         n, F = Xraw.shape
         binned = lay.rm[:n, :F]          # (n, F) view, used for row subsamples
         yt = torch.as_tensor(np.asarray(y, dtype=np.float32), device=dev)
@@ -306,7 +310,8 @@ class Booster:
         # arithmetic depends on it (exact sums are the same either way)
         sparse_db = (self._sparse_default_bins(lay, n, F) if p.grower_arithmetic == "reference" else None)
 
-        X_fm = None   # feature-major copy of Xraw for the leaf models, made at the first tree
+        # feature-major copy of Xraw for the leaf models, made at the first tree
+        X_fm = prepared[3] if prepared is not None and len(prepared) > 3 else None
         for t in range(p.n_estimators):
             grad, hess = boost_ops.grad_hess(self.loss, margin, yt)
 
@@ -407,10 +412,20 @@ class Booster:
 
 class MulticlassBooster:
     """One-vs-rest: one LogLoss booster per class, softmax over the per-class
-    margins (multiclass.py:9-48)."""
+    margins (multiclass.py:9-48).
 
-    def __init__(self, params: BoostParams):
+    The class boosters do not depend on each other, so they are fitted
+    concurrently: ``concurrency`` host threads (default 4, the device's
+    hardware queues per process), each fitting one class at a time on a
+    default-priority stream of its own.  A single tree's growth leaves most
+    of the device idle (its rounds are latency-bound), so the classes' trees
+    overlap.  Each class's booster is the one a sequential fit would make:
+    its inputs are its own, its sums exact and its random generator seeded
+    per booster."""
+
+    def __init__(self, params: BoostParams, concurrency: int = 4):
         self.params = params
+        self.concurrency = concurrency
         self.boosters_: list[Booster] = []
         self.classes_: np.ndarray | None = None
 
@@ -421,12 +436,42 @@ class MulticlassBooster:
         # every class's booster bins the same X the same way (multiclass.py:25-33):
         # bin once and share the binner, the bin layouts and the imputed X
         prepared = Booster(self.params, LogLoss()).prepare(X) if len(self.classes_) else None
-        for label in self.classes_:
+        if prepared is not None and self.params.neural_leaves:
+            prepared = prepared + (feature_major(prepared[2]),)
+        if prepared is not None:
+            # the shared inputs are complete before any other stream reads them
+            torch.cuda.current_stream(prepared[2].device).synchronize()
+
+        def one(label):
             yb = (y == label).astype(np.float32)
             evb = None
             if eval_set is not None:
                 evb = (eval_set[0], (eval_set[1] == label).astype(np.float32))
-            self.boosters_.append(Booster(self.params, LogLoss()).fit(X, yb, eval_set=evb, prepared=prepared))
+            return Booster(self.params, LogLoss()).fit(X, yb, eval_set=evb, prepared=prepared)
+
+        workers = max(1, min(int(self.concurrency), len(self.classes_)))
+        if workers == 1:
+            self.boosters_ = [one(label) for label in self.classes_]
+            return self
+        dev = prepared[2].device
+        streams = [torch.cuda.Stream(dev) for _ in range(workers)]
+        free = list(streams)
+        lock = threading.Lock()
+
+        def on_stream(label):
+            with lock:
+                s = free.pop()
+            try:
+                with torch.cuda.stream(s):
+                    b = one(label)
+                    s.synchronize()
+                return b
+            finally:
+                with lock:
+                    free.append(s)
+
+        with ThreadPoolExecutor(max_workers=workers) as ex:
+            self.boosters_ = list(ex.map(on_stream, list(self.classes_)))
         return self
 
     def predict_margin(self, X: np.ndarray) -> np.ndarray:
