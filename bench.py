@@ -259,19 +259,27 @@ def tree_updates_cpu(O, reference, bins_fm, res, threads, chunk=1_000_000) -> in
     return tree_updates(res["feature"], res["left"], res["right"], sizes, F)
 
 
-def cpu_baseline(budget_s: float = 20.0) -> dict:
+def cpu_baseline(inputs=None, gpu_ref_tree=None, budget_s: float = 20.0) -> dict:
     """Reference grow.c (or its restatement) on the full workload: one
-    255-leaf tree over the same 10M x 100 shape, host RNG inputs of the same
-    distribution."""
+    255-leaf tree over the same 10M x 100 inputs the GPU lines used (copied
+    to the host: feature-major bins, g, h), or host RNG inputs of the same
+    distribution when none are given.  With the GPU's reference-arithmetic
+    tree of the same inputs (node arrays), whether the two trees are equal
+    node for node (features, thresholds, children, value bits)."""
     from oracle import oracle as O
     reference = O.ref_available()
     cpu = host_cpu()
     threads = min(cpu["logical_cpus"], 8)   # the reference default (grow_c.py:283-302)
     F, n = N_FEAT, N_ROWS
-    rng = np.random.default_rng(0)
-    bins_fm = rng.integers(0, 256, size=(F, n), dtype=np.uint8)
-    g = rng.normal(size=n).astype(np.float32)
-    h = rng.uniform(0.1, 1.0, size=n).astype(np.float32)
+    if inputs is not None:
+        bins_fm, g, h = inputs
+        source = "the GPU lines' own inputs (device RNG, seed 0), copied to the host"
+    else:
+        rng = np.random.default_rng(0)
+        bins_fm = rng.integers(0, 256, size=(F, n), dtype=np.uint8)
+        g = rng.normal(size=n).astype(np.float32)
+        h = rng.uniform(0.1, 1.0, size=n).astype(np.float32)
+        source = "host RNG inputs of the same distribution"
     kw = dict(PARAMS, nbins=np.full(F, 256, np.int32), n_threads=threads)
     times = []
     res = None
@@ -289,8 +297,13 @@ def cpu_baseline(budget_s: float = 20.0) -> dict:
            "cores": threads, "kind": "reference" if reference else "port",
            "ms_per_tree": round(sec * 1e3, 1),
            "sample": f"one 255-leaf tree on 10,000,000 x 100 uniform u8 bins (the full workload), "
-                     f"{len(timed)} timed run(s) after 1 warm-up, median; {threads} OpenMP threads",
+                     f"{source}, {len(timed)} timed run(s) after 1 warm-up, median; {threads} OpenMP threads",
            "host_cpu": cpu}
+    if gpu_ref_tree is not None and reference:
+        same = all(np.array_equal(np.asarray(res[k]), gpu_ref_tree[k]) for k in ("feature", "thr_bin", "left", "right"))
+        same = same and np.array_equal(np.asarray(res["value"], np.float32).view(np.uint32),
+                                       gpu_ref_tree["value"].view(np.uint32))
+        out["same_tree_as_gpu_reference_arithmetic"] = bool(same)
     # the same tree on every logical CPU the process may use
     all_threads = cpu["logical_cpus"]
     t0 = time.perf_counter()
@@ -372,7 +385,9 @@ def reference_arithmetic(torch, lay, g, h, nbins, steps: int, exact_res, neural:
     differ = internal & ((a["feature"][:m] != b["feature"][:m]) | (a["thr_bin"][:m] != b["thr_bin"][:m]))
     out["vs_exact"] = {"internal_nodes": int(internal.sum()), "split_differences": int(differ.sum()),
                        "same_node_layout": bool(same_shape)}
-    return out
+    tree = {k: getattr(res, k)[:res.n_nodes].cpu().numpy() for k in ("feature", "thr_bin", "left", "right",
+                                                                      "value")}
+    return out, tree
 
 
 def leaf_gram_compare(torch, lay, g, h, nbins, reps: int = 10) -> dict:
@@ -732,8 +747,14 @@ def main() -> None:
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": committed_traffic()},
     }
+    ref_tree = None
     if args.ref_steps > 0:
-        line["reference_arithmetic"] = reference_arithmetic(torch, lay, g, h, nbins, args.ref_steps, res, neural)
+        line["reference_arithmetic"], ref_tree = reference_arithmetic(torch, lay, g, h, nbins, args.ref_steps, res,
+                                                                      neural)
+    # the CPU baseline grows its tree on these same inputs
+    host_inputs = None
+    if not args.no_cpu:
+        host_inputs = (np.ascontiguousarray(lay.fm[:, :n].cpu().numpy()), g.cpu().numpy(), h.cpu().numpy())
     if neural:
         log("[bench] linear-leaf step, exact and fp64 MFMA Gram sums")
         line["leaf_gram"] = leaf_gram_compare(torch, lay, g, h, nbins)
@@ -743,7 +764,7 @@ def main() -> None:
         line["boosting"] = boosting_fits(torch)
     if not args.no_cpu:
         log("[bench] CPU baseline")
-        line["cpu_baseline"] = cpu_baseline()
+        line["cpu_baseline"] = cpu_baseline(host_inputs, ref_tree)
     print(json.dumps(line), flush=True)
 
 
