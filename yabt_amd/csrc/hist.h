@@ -242,49 +242,118 @@ __host__ __device__ inline int64_t root_chunk_rows(int64_t n, int chunks) {
 constexpr int TAILF = 4;                 // features of a tail tile, at most
 constexpr int TSTEP = 2 * RBLOCK;        // rows per tail block step (128 per wave)
 
-// Grid of the streaming root kernel: `tail` blocks for the tail tile (block
-// ids 0 .. tail - 1, tail_rows rows each), then `tiles` full 16-feature tiles
-// of `chunks` row chunks each.  The last tile is a tail tile when it holds
-// 1..TAILF features and g and h can be read in aligned pairs (8-byte aligned,
-// n >= 2).  One 1024-thread block runs per CU, so the grid aims at one wave
-// of 256 blocks of equal length (two waves of 256 took 1-2% longer: the
-// second wave starts behind the first one's slowest blocks): a tail block's
-// row costs about 3/8 of a full block's (a quarter of the LDS atomics, with
-// more VALU work per atomic), so the tail counts as 3/8 of a tile when the
-// chunks are sized, and its blocks fill the rest of the 256 (at least 3/8 of
-// a tile's worth).  chunks is a multiple of 8, so every full tile of a row
-// chunk runs on one XCD (block id % 8) and shares its L2 for the chunk's g
-// and h; the tail blocks read theirs on their own.
+// Grid of the streaming root kernel: `tiles` full 16-feature tiles of
+// `chunks` row chunks each, and `tail` blocks of tail_rows rows for the tail
+// tile.  The last tile is a tail tile when it holds 1..TAILF features and g
+// and h can be read in aligned pairs (8-byte aligned, n >= 2).  One
+// 1024-thread block runs per CU, so the grid is one wave: RXCD dies of RSLOTS
+// CUs, block id b on die b % RXCD (the dispatcher's round robin).  Die x
+// runs the full tiles of chunks x, x + RXCD, ... -- every tile of a chunk on
+// one die, sharing its L2 for the chunk's g and h -- and tail blocks in its
+// remaining slots (root_block); chunks is chosen so that the slowest block is
+// as short as it can be: a full block costs 16 per row and a tail block
+// TAIL_COST (its quarter of the LDS atomics comes with more VALU work and
+// loads of g and h of its own: 7 per row, measured against the full
+// blocks' 16).  At 10M x 100: 39 chunks (234 full blocks of 257 024 rows)
+// and 22 tail blocks (454 656 rows); with chunks a multiple of 8 it was 40
+// and 16 (626 688 rows), and the tail blocks ended 15-20 µs after the full
+// ones.  With more than RSLOTS tiles a chunk cannot fit one die and the
+// tiles go in order (tile-major, chunks a multiple of 8, tail blocks first).
+constexpr int RXCD = 8, RSLOTS = 32;   // dies, one-block-per-CU slots per die
+constexpr int TAIL_COST = 7;           // a tail block's cost per row, a full block's being 16
+
 struct RootGrid {
     int tiles, chunks, tail, blocks;
+    int xcd;                           // 1: die-aware layout (root_block); 0: tail blocks, then tile-major
     int64_t tail_rows;
 };
 
+// Chunks whose full tiles die x runs in the die-aware layout.
+__host__ __device__ inline int xcd_chunks(int chunks, int x) { return chunks > x ? (chunks - x + RXCD - 1) / RXCD : 0; }
+
 inline RootGrid root_grid(int64_t n, int F, const void* grad, const void* hess) {
-    constexpr int SLOTS = 256;
+    constexpr int SLOTS = RXCD * RSLOTS;
     const int rem = F % HFL;
     const bool tail = rem >= 1 && rem <= TAILF && n >= 2 && (uintptr_t)grad % 8 == 0 && (uintptr_t)hess % 8 == 0;
     RootGrid g;
     g.tiles = tail ? F / HFL : (F + HFL - 1) / HFL;
-    g.chunks = 8;
-    if (g.tiles > 0) {
+    g.xcd = g.tiles <= RSLOTS ? 1 : 0;
+    const int64_t useful = max((int64_t)1, (n + RSTEP - 1) / RSTEP);   // chunks with rows
+    const int64_t tail_useful = (n + TSTEP - 1) / TSTEP;               // tail blocks with rows
+    g.chunks = 0;
+    int T = 0;
+    if (g.xcd) {
+        if (g.tiles > 0) {
+            const int cmax = (int)min((int64_t)(RSLOTS / g.tiles * RXCD), useful);
+            g.chunks = cmax;
+            if (tail) {
+                // the chunk count whose slowest block is shortest: full blocks
+                // cost 16 / c of the rows each, tail blocks TAIL_COST / T
+                int64_t best_num = -1, best_den = 1;
+                for (int c = 1; c <= cmax; ++c) {
+                    const int t = (int)min((int64_t)(SLOTS - g.tiles * c), tail_useful);
+                    if (t < 1) break;
+                    // max(16 / c, TAIL_COST / t) as a fraction num / den
+                    const int64_t a_num = 16 * (int64_t)t, b_num = (int64_t)TAIL_COST * c, den = (int64_t)c * t;
+                    const int64_t num = a_num > b_num ? a_num : b_num;
+                    if (best_num < 0 || num * best_den < best_num * den) {
+                        best_num = num;
+                        best_den = den;
+                        g.chunks = c;
+                    }
+                }
+                T = (int)min((int64_t)(SLOTS - g.tiles * g.chunks), tail_useful);
+            }
+        } else {
+            T = (int)min((int64_t)SLOTS, tail_useful);
+        }
+    } else {
         int want = tail ? 8 * SLOTS / (8 * g.tiles + 3) : SLOTS / g.tiles;
-        const int64_t useful = (n + RSTEP - 1) / RSTEP;
         if (want > useful) want = (int)useful;
         want = want / 8 * 8;
         g.chunks = want < 8 ? 8 : want;
+        if (tail) T = (int)min((int64_t)max(SLOTS - g.tiles * g.chunks, (3 * g.chunks + 7) / 8), tail_useful);
     }
     g.tail = 0;
     g.tail_rows = 0;
-    if (tail) {
-        const int fill = SLOTS - g.tiles * g.chunks;
-        int64_t t = max(fill, (3 * g.chunks + 7) / 8);
-        t = min(t, (n + TSTEP - 1) / TSTEP);   // no empty tail block
-        g.tail_rows = ((n + t - 1) / t + TSTEP - 1) / TSTEP * TSTEP;
-        g.tail = (int)((n + g.tail_rows - 1) / g.tail_rows);
+    if (tail && T > 0) {
+        g.tail_rows = ((n + T - 1) / T + TSTEP - 1) / TSTEP * TSTEP;
+        g.tail = (int)((n + g.tail_rows - 1) / g.tail_rows);   // no empty tail block
     }
-    g.blocks = g.tail + g.tiles * g.chunks;
+    g.blocks = g.xcd ? (g.tiles > 0 ? SLOTS : g.tail) : g.tail + g.tiles * g.chunks;
     return g;
+}
+
+// Block bid of a root grid: a full block (tile, chunk) with tb = -1, or tail
+// block tb; false for an idle slot.
+__host__ __device__ __forceinline__ bool root_block(int bid, int tiles, int chunks, int tail, int xcd, int& tile,
+                                                    int& chunk, int& tb) {
+    tile = chunk = 0;
+    tb = -1;
+    if (!xcd) {
+        if (bid < tail) {
+            tb = bid;
+            return true;
+        }
+        tile = (bid - tail) / chunks;
+        chunk = (bid - tail) % chunks;
+        return true;
+    }
+    if (tiles == 0) {
+        tb = bid;
+        return bid < tail;
+    }
+    const int x = bid % RXCD, k = bid / RXCD;
+    const int nx = xcd_chunks(chunks, x) * tiles;
+    if (k < nx) {
+        tile = k % tiles;
+        chunk = (k / tiles) * RXCD + x;
+        return true;
+    }
+    int pre = 0;   // tail slots of the dies before x
+    for (int y = 0; y < x; ++y) pre += RSLOTS - xcd_chunks(chunks, y) * tiles;
+    tb = pre + (k - nx);
+    return tb < tail;
 }
 
 constexpr int ROOT_G = 0, ROOT_PACKED = 1, ROOT_WIDE = 2;   // modes of the streaming root kernels
@@ -339,8 +408,7 @@ __device__ __forceinline__ void hist_root_gh(HistLdsR& L, const uint8_t* __restr
                                              const float* __restrict__ grad, const float* __restrict__ hess,
                                              int64_t n, int F, double scg, double sch,
                                              const int32_t* __restrict__ dflt, const uint32_t* __restrict__ counts,
-                                             Quant* q_tot, int64_t* out, int chunks, int bid) {
-    const int tile = bid / chunks, chunk = bid % chunks;
+                                             Quant* q_tot, int64_t* out, int chunks, int tile, int chunk) {
     constexpr bool HCH = MODE != ROOT_G, PACK = MODE == ROOT_PACKED;
     const int f0 = tile * HFL;
     const int lane = threadIdx.x & (WAVE - 1), wave = threadIdx.x / WAVE;
@@ -947,7 +1015,8 @@ static __global__ __attribute__((unused)) void __launch_bounds__(RBLOCK)
 k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld, const float* __restrict__ grad,
             const float* __restrict__ hess, int64_t n, int F, const Quant* q, double scg_v, double sch_v,
             int wide_v, const int32_t* __restrict__ dflt, const uint32_t* __restrict__ counts, Quant* q_tot,
-            int64_t* out, int chunks, int tail, int64_t tail_rows, int count_mode, const int32_t* done) {
+            int64_t* out, int tiles, int chunks, int tail, int64_t tail_rows, int xcd, int count_mode,
+            const int32_t* done) {
     const int32_t dn = done ? *done : 0;
     const double scg = q ? q->scg : scg_v, sch = q ? q->sch : sch_v;
     const bool no_h = count_mode && q && q->const_h;
@@ -955,28 +1024,29 @@ k_hist_root(const uint8_t* __restrict__ bins_fm, int64_t ld, const float* __rest
     if (dn) return;
     __shared__ HistLdsR L;   // 64 KB, also the flush's RootFlushLds
     static_assert(sizeof(RootFlushLds) <= sizeof(HistLdsR), "the flush reuses the cells' LDS");
-    const int bid = (int)blockIdx.x;
-    if (bid < tail) {
+    int tile, chunk, tb;
+    if (!root_block((int)blockIdx.x, tiles, chunks, tail, xcd, tile, chunk, tb)) return;
+    if (tb >= 0) {
         if (no_h)
             hist_root_tail<ROOT_G, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
-                                         tail_rows, bid);
+                                              tail_rows, tb);
         else if (wide)
-            hist_root_tail<ROOT_WIDE, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
-                                            tail_rows, bid);
+            hist_root_tail<ROOT_WIDE, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot,
+                                                 out, tail_rows, tb);
         else
-            hist_root_tail<ROOT_PACKED, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
-                                              tail_rows, bid);
+            hist_root_tail<ROOT_PACKED, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot,
+                                                   out, tail_rows, tb);
         return;
     }
     if (no_h)
         hist_root_gh<ROOT_G, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks,
-                                   bid - tail);
+                                        tile, chunk);
     else if (wide)
-        hist_root_gh<ROOT_WIDE, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out, chunks,
-                                      bid - tail);
+        hist_root_gh<ROOT_WIDE, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
+                                           chunks, tile, chunk);
     else
         hist_root_gh<ROOT_PACKED, SKIP, BUF>(L, bins_fm, ld, grad, hess, n, F, scg, sch, dflt, counts, q_tot, out,
-                                        chunks, bid - tail);
+                                             chunks, tile, chunk);
 }
 
 // One launch of k_hist_root over grid g: the instantiation with the
@@ -987,11 +1057,11 @@ static __attribute__((unused)) void launch_root_kernel(hipStream_t stream, const
                                                        int F, const Quant* q, double scg, double sch, int wide,
                                                        const int32_t* dflt, const uint32_t* counts, Quant* q_tot,
                                                        int64_t* out, int count_mode, const int32_t* done) {
-    const bool buf = root_buffers(ld, max(root_chunk_rows(n, g.chunks), g.tail_rows));
+    const bool buf = root_buffers(ld, max(g.chunks > 0 ? root_chunk_rows(n, g.chunks) : 0, g.tail_rows));
 #define YABT_ROOT_LAUNCH(S, B)                                                                                     \
     k_hist_root<S, B><<<g.blocks, RBLOCK, 0, stream>>>(bins_fm, ld, grad, hess, n, F, q, scg, sch, wide, dflt,   \
-                                                       counts, q_tot, out, g.chunks, g.tail, g.tail_rows,          \
-                                                       count_mode, done)
+                                                       counts, q_tot, out, g.tiles, g.chunks, g.tail, g.tail_rows, \
+                                                       g.xcd, count_mode, done)
     if (dflt) {
         if (buf) YABT_ROOT_LAUNCH(true, true);
         else YABT_ROOT_LAUNCH(true, false);
