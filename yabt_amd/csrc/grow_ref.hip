@@ -878,13 +878,26 @@ __device__ __forceinline__ void rank_tile_load_any(RankTile& c, const float* __r
     }
 }
 
+// One window of a tile's entries, g and h in separate tables: a producer
+// writes each value as it was loaded (pairing g with h for one 8-byte store
+// would have the compiler permute the loaded registers right after the
+// loads, which waits for them).
+struct RankTable {
+    float g[RW][NB];
+    float h[RW][NB];
+};
+
 // A producer's window [w0, w0 + RW) of its tile's entries into T[rank - w0][bin].
-__device__ __forceinline__ void rank_stage(const RankTile& c, float2 (*T)[NB], uint32_t w0) {
+__device__ __forceinline__ void rank_stage(const RankTile& c, RankTable& T, uint32_t w0) {
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
         // a rank below w0 wraps above RW; past the rows the rank is 0xffff
         const uint32_t rank = rt_rank(c, j), r = rank - w0;
-        if (rank != 0xffffu && r < (uint32_t)RW) T[r][rt_bin(c, j)] = make_float2(rt_g(c, j), rt_h(c, j));
+        if (rank != 0xffffu && r < (uint32_t)RW) {
+            const uint32_t b = rt_bin(c, j);
+            T.g[r][b] = rt_g(c, j);
+            T.h[r][b] = rt_h(c, j);
+        }
     }
 }
 
@@ -903,7 +916,7 @@ template <bool VEC>
 __global__ void __launch_bounds__(RB + RPROD) k_rank_chain(const float* __restrict__ g, const float* __restrict__ h,
                                                        const uint8_t* __restrict__ bins_fm, int64_t ld_fm, int64_t n,
                                                        RootOrder o, float* __restrict__ hist, int F) {
-    __shared__ float2 T[2][RW][NB];
+    __shared__ RankTable T[2];
     const int f = blockIdx.x;
     const bool prod = threadIdx.x >= RB;
     const int lt = prod ? (int)threadIdx.x - RB : (int)threadIdx.x;   // consumers: the bin; producers: the slot
@@ -919,18 +932,21 @@ __global__ void __launch_bounds__(RB + RPROD) k_rank_chain(const float* __restri
     // steps to the tile's longest run in the window (uniform), eight reads in
     // flight; past this thread's run a step adds +0.0f, which leaves the sums'
     // bits unchanged (a sum that starts at +0.0f is never -0.0f)
-    auto run = [&](float2 (*Tb)[NB], uint32_t len, uint32_t mr, uint32_t w0) {
+    auto run = [&](const RankTable& Tb, uint32_t len, uint32_t mr, uint32_t w0) {
         const uint32_t kend = min(len > w0 ? len - w0 : 0u, (uint32_t)RW);
         const uint32_t kmax = min(mr - w0, (uint32_t)RW);
         for (uint32_t r = 0; r < kmax; r += 8) {
-            float2 v[8];
+            float vg[8], vh[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) v[u] = Tb[r + u][lt];
+            for (int u = 0; u < 8; ++u) {
+                vg[u] = Tb.g[r + u][lt];
+                vh[u] = Tb.h[r + u][lt];
+            }
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 const bool in = r + u < kend;
-                ag += in ? v[u].x : 0.0f;
-                ah += in ? v[u].y : 0.0f;
+                ag += in ? vg[u] : 0.0f;
+                ah += in ? vh[u] : 0.0f;
             }
         }
     };
