@@ -388,7 +388,7 @@ __device__ __forceinline__ uint32_t node_bin(const uint8_t* __restrict__ bins_fm
 // count s_cnt[w][bin].  Sparse builder (dbin): the default bin gets no run,
 // and xperm lists the tile's other positions in row order.
 template <bool ROOT, bool SPARSE>
-__global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bins_fm, int64_t ld_fm,
+__global__ void __launch_bounds__(RB, 8) k_walk_sort(const uint8_t* __restrict__ bins_fm, int64_t ld_fm,
                                                   const uint8_t* __restrict__ bins_rm, int64_t ld_rm,
                                                   const uint32_t* __restrict__ rows, int64_t rows_ld,
                                                   const Round* __restrict__ R, int fg0,
@@ -396,10 +396,11 @@ __global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bi
                                                   uint16_t* __restrict__ xperm, int64_t ld_perm,
                                                   uint16_t* __restrict__ starts, int64_t n_tiles) {
     __shared__ uint8_t s_bin[WT];
-    __shared__ uint64_t s_peer[SW][NB];
+    __shared__ uint64_t s_peer[SW][NB];            // once the tile is ranked: its bucketed positions
     __shared__ uint32_t s_cnt[SW][NB];
-    __shared__ uint16_t s_perm[WT];
     __shared__ uint16_t s_xperm[SPARSE ? WT : 1];
+    static_assert(sizeof(s_peer) == WT * sizeof(uint16_t), "the bucketed positions fill the peer masks' space");
+    uint16_t* s_perm = reinterpret_cast<uint16_t*>(&s_peer[0][0]);
     __shared__ uint32_t s_scan[SW];
     __shared__ uint32_t s_xoff[SW + 1];
     const int fl = blockIdx.x, f = fg0 + fl;       // buffers by group position, bins by feature
@@ -418,21 +419,21 @@ __global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bi
         (&s_cnt[0][0])[i] = 0;
         (&s_peer[0][0])[i] = 0;
     }
-#pragma unroll
+#pragma unroll 2
     for (int j = 0; j < TPT; ++j) {
         const int x = j * RB + tid;
         if (x < tn) s_bin[x] = (uint8_t)node_bin<ROOT>(bins_fm, ld_fm, bins_rm, ld_rm, crow, cs, f, t0 + x);
     }
     __syncthreads();
-    uint32_t rk[SGR], xr[SGR];
-    uint8_t qb[SGR];
+    // per group: the rank (bits 0-9), the sparse rank outside the default bin
+    // (bits 10-19) and the bin (bits 24-31) in one register
+    uint32_t pk[SGR];
     uint32_t xrun = 0;
 #pragma unroll
     for (int q = 0; q < SGR; ++q) {
         const int x = w * SSUB + q * WAVE + lane;
         const bool v = x < tn;
         const uint32_t bin = v ? (uint32_t)s_bin[x] : 0u;
-        qb[q] = (uint8_t)bin;
         if (v) atomicOr(&s_peer[w][bin], 1ull << lane);
         __builtin_amdgcn_wave_barrier();
         const uint64_t peers = v ? s_peer[w][bin] : 0ull;
@@ -442,12 +443,15 @@ __global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bi
         if (v) s_peer[w][bin] = 0ull;
         if (v && r == 0) s_cnt[w][bin] = base + (uint32_t)__popcll(peers);
         __builtin_amdgcn_wave_barrier();
-        rk[q] = base + r;
+        pk[q] = (base + r) | (bin << 24);
         if (SPARSE) {
             const uint64_t xb = __ballot(v && (int)bin != df);
-            xr[q] = xrun + lane_prefix(xb);
+            pk[q] |= (xrun + lane_prefix(xb)) << 10;
             xrun += (uint32_t)__popcll(xb);
         }
+        // packed here, not where it is used: otherwise its three parts stay
+        // live in registers of their own through the remaining groups
+        asm volatile("" : "+v"(pk[q]));
     }
     if (SPARSE && lane == 0) s_xoff[w] = xrun;
     __syncthreads();
@@ -488,9 +492,10 @@ __global__ void __launch_bounds__(RB) k_walk_sort(const uint8_t* __restrict__ bi
 #pragma unroll
     for (int q = 0; q < SGR; ++q) {
         const int x = w * SSUB + q * WAVE + lane;
-        if (x < tn && (!SPARSE || (int)qb[q] != df)) {
-            s_perm[s_cnt[w][qb[q]] + rk[q]] = (uint16_t)x;
-            if (SPARSE) s_xperm[s_xoff[w] + xr[q]] = (uint16_t)x;
+        const uint32_t bin = pk[q] >> 24;
+        if (x < tn && (!SPARSE || (int)bin != df)) {
+            s_perm[s_cnt[w][bin] + (pk[q] & 1023u)] = (uint16_t)x;
+            if (SPARSE) s_xperm[s_xoff[w] + ((pk[q] >> 10) & 1023u)] = (uint16_t)x;
         }
     }
     __syncthreads();
@@ -723,7 +728,7 @@ __host__ __device__ inline size_t root_order_carve(char* base, int64_t n, int F,
 
 // Block (f, t): the ranks and run starts of feature f's tile t (tiles grid-
 // strided over y), bucketed as in k_walk_sort.
-__global__ void __launch_bounds__(RB) k_root_rank(const uint8_t* __restrict__ bins_fm, int64_t ld_fm, int64_t n,
+__global__ void __launch_bounds__(RB, 8) k_root_rank(const uint8_t* __restrict__ bins_fm, int64_t ld_fm, int64_t n,
                                                   RootOrder o) {
     __shared__ uint8_t s_bin[WT];
     __shared__ uint64_t s_peer[SW][NB];
@@ -746,14 +751,12 @@ __global__ void __launch_bounds__(RB) k_root_rank(const uint8_t* __restrict__ bi
             if (x < tn) s_bin[x] = bins_fm[(size_t)f * (size_t)ld_fm + (size_t)(t0 + x)];
         }
         __syncthreads();
-        uint32_t rk[SGR];
-        uint8_t qb[SGR];
+        uint32_t pk[SGR];   // per group: the rank (bits 0-9) and the bin (bits 24-31)
 #pragma unroll
         for (int q = 0; q < SGR; ++q) {
             const int x = w * SSUB + q * WAVE + lane;
             const bool v = x < tn;
             const uint32_t bin = v ? (uint32_t)s_bin[x] : 0u;
-            qb[q] = (uint8_t)bin;
             if (v) atomicOr(&s_peer[w][bin], 1ull << lane);
             __builtin_amdgcn_wave_barrier();
             const uint64_t peers = v ? s_peer[w][bin] : 0ull;
@@ -763,7 +766,8 @@ __global__ void __launch_bounds__(RB) k_root_rank(const uint8_t* __restrict__ bi
             if (v) s_peer[w][bin] = 0ull;
             if (v && r == 0) s_cnt[w][bin] = base + (uint32_t)__popcll(peers);
             __builtin_amdgcn_wave_barrier();
-            rk[q] = base + r;
+            pk[q] = (base + r) | (bin << 24);
+            asm volatile("" : "+v"(pk[q]));   // packed here, not at its use
         }
         __syncthreads();
         {
@@ -795,7 +799,7 @@ __global__ void __launch_bounds__(RB) k_root_rank(const uint8_t* __restrict__ bi
 #pragma unroll
         for (int q = 0; q < SGR; ++q) {
             const int x = w * SSUB + q * WAVE + lane;
-            if (x < tn) ro[x] = (uint16_t)(s_cnt[w][qb[q]] + rk[q]);
+            if (x < tn) ro[x] = (uint16_t)(s_cnt[w][pk[q] >> 24] + (pk[q] & 1023u));
         }
         __syncthreads();
     }
