@@ -168,6 +168,12 @@ __device__ __forceinline__ double dpp_f64(double v) {
     return __longlong_as_double((long long)dpp64<CTRL>((uint64_t)__double_as_longlong(v)));
 }
 
+// Buffer resource over `bytes` bytes at p (raw, untyped): a load at an offset
+// past the end returns zeros instead of faulting.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+
 // Number of set bits of mask in the lanes below this one.
 __device__ __forceinline__ uint32_t lane_prefix(uint64_t mask) {
     return __builtin_amdgcn_mbcnt_hi((uint32_t)(mask >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)mask, 0u));

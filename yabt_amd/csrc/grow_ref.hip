@@ -217,12 +217,21 @@ __global__ void __launch_bounds__(RB) k_init(uint32_t* rows, int64_t n, uint8_t*
 // leaves of a round have disjoint segments), p and q hold positions relative
 // to the leaf's start.
 
-// Flags (row goes left) and the left count of each PT-row block.
-__global__ void __launch_bounds__(RB) k_part_flags(const uint8_t* __restrict__ bins_fm, int64_t ld,
-                                                   const Round* __restrict__ R, const uint32_t* __restrict__ rows,
+// Flags (row goes left) and the left count of each PT-row block.  The
+// round's job table comes as the kernel argument Rv (no copy of its own
+// ahead of the round); block 0 stores it at Rd for the round's other kernels.
+__global__ void __launch_bounds__(RB) k_part_flags(const uint8_t* __restrict__ bins_fm, int64_t ld, const Round Rv,
+                                                   Round* __restrict__ Rd, const uint32_t* __restrict__ rows,
                                                    int64_t rows_ld, uint8_t* __restrict__ flag,
                                                    uint32_t* __restrict__ blk) {
     __shared__ uint32_t s_red[RB / WAVE];
+    if (blockIdx.x == 0) {
+        static_assert(sizeof(Round) % 4 == 0, "the job table in words");
+        const uint32_t* src = reinterpret_cast<const uint32_t*>(&Rv);
+        uint32_t* dst = reinterpret_cast<uint32_t*>(Rd);
+        for (int i = threadIdx.x; i < (int)(sizeof(Round) / 4); i += RB) dst[i] = src[i];
+    }
+    const Round* R = &Rv;
     const int k = job_of(R->boff, R->K, blockIdx.x);
     const Job& J = R->job[k];
     const int64_t s = J.s, m = J.e - J.s;
@@ -388,7 +397,7 @@ __device__ __forceinline__ uint32_t node_bin(const uint8_t* __restrict__ bins_fm
 // count s_cnt[w][bin].  Sparse builder (dbin): the default bin gets no run,
 // and xperm lists the tile's other positions in row order.
 template <bool ROOT, bool SPARSE>
-__global__ void __launch_bounds__(RB, 8) k_walk_sort(const uint8_t* __restrict__ bins_fm, int64_t ld_fm,
+__global__ void __launch_bounds__(RB, SPARSE ? 5 : 8) k_walk_sort(const uint8_t* __restrict__ bins_fm, int64_t ld_fm,
                                                   const uint8_t* __restrict__ bins_rm, int64_t ld_rm,
                                                   const uint32_t* __restrict__ rows, int64_t rows_ld,
                                                   const Round* __restrict__ R, int fg0,
@@ -1825,10 +1834,10 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
         }
         if (j == 0) break;
         R.K = j;
-        // partition, histograms of the built children, both children's scans
-        if ((rc = launch_round())) return rc;
+        // partition (the job table goes in with its first kernel),
+        // histograms of the built children, both children's scans
         const int nblk = R.boff[j];
-        k_part_flags<<<nblk, RB, 0, stream>>>(bins_fm, ld_fm, w.round, w.rows, w.rows_ld, w.flag, w.blk);
+        k_part_flags<<<nblk, RB, 0, stream>>>(bins_fm, ld_fm, R, w.round, w.rows, w.rows_ld, w.flag, w.blk);
         k_part_offsets<<<j, RB, 0, stream>>>(w.blk, w.round);
         k_part_rank<<<nblk, RB, 0, stream>>>(w.flag, w.blk, w.round, w.rank, w.p, w.q);
         k_part_permute<<<nblk, RB, 0, stream>>>(w.flag, w.rank, w.p, w.q, w.round, w.rows, w.rows_ld, grad, hess,

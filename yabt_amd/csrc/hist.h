@@ -376,12 +376,6 @@ static_assert(PACKED_CELL_ROWS * (1 << 19) <= (1ll << 31) && ROOT_DEPTH * RSTEP 
               "a cell below PACKED_CELL_ROWS rows is exact");
 static_assert((int64_t)TAIL_DEPTH * TSTEP / 4 * (1 << 19) < (1ll << 31), "a tail epoch's sums fit 32-bit halves");
 
-// Buffer resource over `bytes` bytes at p (raw, untyped): a load at an offset
-// past the end returns zeros instead of faulting.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t raw_rsrc(const void* p, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
-}
-
 // Whether root chunks (or tail spans) of up to `per` rows over bins of
 // leading dimension ld can be read through buffer resources: every 32-bit
 // offset of a tile's loads (a lane's column, fl ld, plus the row of a step,
