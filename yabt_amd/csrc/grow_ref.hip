@@ -543,6 +543,55 @@ __device__ __forceinline__ void run_f32(const float2* s_gh, const uint16_t* idx,
     }
 }
 
+// Sequential fp32 sums of the pairs s[k], k in [lo, hi) (hi <= WT): blocks of
+// 16 read 8 ahead of the adds, so that a long run (a bin that holds most of a
+// tile, as the features on a node's path do) waits about one LDS latency per
+// 16 pairs rather than two per 8.  The block's last prefetch reads inside the
+// array whether or not it is used.
+__device__ __forceinline__ void run_f32_sorted(const float2* s, uint32_t lo, uint32_t hi, float& ag, float& ah) {
+    uint32_t k = lo;
+    const uint32_t nb = (hi - lo) / 16;
+    if (nb > 0) {
+        float2 a[8], b[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a[u] = s[k + u];
+        for (uint32_t blk = 0; blk < nb; ++blk) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) b[u] = s[k + 8 + u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                ag += a[u].x;
+                ah += a[u].y;
+            }
+            const uint32_t kn = min(k + 16, (uint32_t)(WT - 8));
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a[u] = s[kn + u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                ag += b[u].x;
+                ah += b[u].y;
+            }
+            k += 16;
+        }
+    }
+    if (k + 8 <= hi) {
+        float2 p[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) p[u] = s[k + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            ag += p[u].x;
+            ah += p[u].y;
+        }
+        k += 8;
+    }
+    for (; k < hi; ++k) {
+        const float2 p = s[k];
+        ag += p.x;
+        ah += p.y;
+    }
+}
+
 // Sequential double sums of the fp32 pairs s_gh[idx[k]] (idx null: s_gh[k]),
 // k in [0, hi).
 __device__ __forceinline__ void run_f64(const float2* s_gh, const uint16_t* idx, uint32_t hi, double& ag,
@@ -614,7 +663,10 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb,
                                                    float* __restrict__ hist_base, size_t hsz,
                                                    double* __restrict__ eout_b, double* __restrict__ tot_b) {
     __shared__ float2 s_gh[WT];
-    __shared__ uint16_t s_idx[WT];
+    // dense: the tile's pairs in bucket order (each bin's run contiguous);
+    // sparse: the bucket lists' positions
+    __shared__ float2 s_sorted[SPARSE ? 1 : WT];
+    __shared__ uint16_t s_idx[SPARSE ? WT : 1];
     __shared__ uint16_t s_xidx[SPARSE ? WT : 1];
     __shared__ uint16_t s_st[ST];
     const int kj = blockIdx.y;
@@ -645,9 +697,9 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb,
             const int x = j * RB + tid;
             if (x < tn) {
                 s_gh[x] = make_float2(nxt.g[j], nxt.h[j]);
-                if (!totals) {
+                if (SPARSE && !totals) {
                     s_idx[x] = (uint16_t)nxt.idx[j];
-                    if (SPARSE) s_xidx[x] = (uint16_t)nxt.xidx[j];
+                    s_xidx[x] = (uint16_t)nxt.xidx[j];
                 }
             }
         }
@@ -656,6 +708,19 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb,
             if (tid == 0) s_st[NB] = (uint16_t)nxt.st_end;
         }
         __syncthreads();
+        if (!SPARSE) {
+            // the pairs in bucket order: entry k of the lists is position idx
+            // (every read issued before the first write)
+            float2 v[TPT];
+#pragma unroll
+            for (int j = 0; j < TPT; ++j) v[j] = s_gh[j * RB + tid < tn ? nxt.idx[j] : 0u];
+#pragma unroll
+            for (int j = 0; j < TPT; ++j) {
+                const int k = j * RB + tid;
+                if (k < tn) s_sorted[k] = v[j];
+            }
+            __syncthreads();
+        }
         if (t0 + WT < m) chain_load<SPARSE>(nxt, G, H, pf, xf, sf, totals, t + 1, m);
         if (totals) {
             if (tid == 0) run_f64(s_gh, nullptr, (uint32_t)tn, eg, eh);
@@ -665,7 +730,8 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb,
             cnt += (int64_t)tn - nx;
         } else {
             const uint32_t lo = s_st[tid], hi = s_st[tid + 1];
-            run_f32(s_gh, s_idx, lo, hi, ag, ah);
+            if (SPARSE) run_f32(s_gh, s_idx, lo, hi, ag, ah);
+            else run_f32_sorted(s_sorted, lo, hi, ag, ah);
             cnt += hi - lo;
         }
         __syncthreads();
