@@ -361,14 +361,16 @@ __global__ void __launch_bounds__(RB) k_part_permute(const uint8_t* __restrict__
 // cgrow adds each row into its (feature, bin) cell in fp32, in rows[] order
 // (grow.c:37-62).  The node's rows are cut into tiles of WT rows in that
 // order.  k_walk_sort buckets every (feature, tile) by bin, stably, in
-// parallel over the whole device; k_walk_chain then runs one block per
-// feature over the tiles in order, thread b adding bin b's run of each tile
+// parallel over the whole device; a chain kernel then runs one block per
+// (feature, split) over the tiles in order, adding bin b's run of each tile
 // to its fp32 accumulators, so every cell is cgrow's sequential sum.
+// Dense (k_walk_chain_dense): the tile's g and h permuted into bucket order
+// in LDS, one thread per (bin, channel).
 //
-// Sparse builder (grow.c:68-107, default bins dbin): the default bin gets no
-// run; its thread instead adds, in double and in row order, the tile's rows
-// outside the default bin; block F adds the node's g and h in double in row
-// order; k_hist_default combines them.
+// Sparse builder (grow.c:68-107, default bins dbin; k_walk_chain<true>): the
+// default bin gets no run; its thread instead adds, in double and in row
+// order, the tile's rows outside the default bin; block F adds the node's g
+// and h in double in row order; k_hist_default combines them.
 
 constexpr int SW = RB / WAVE;             // waves per sort / chain block
 constexpr int SSUB = WT / SW;             // rows per wave per tile (sort)
@@ -543,55 +545,6 @@ __device__ __forceinline__ void run_f32(const float2* s_gh, const uint16_t* idx,
     }
 }
 
-// Sequential fp32 sums of the pairs s[k], k in [lo, hi) (hi <= WT): blocks of
-// 16 read 8 ahead of the adds, so that a long run (a bin that holds most of a
-// tile, as the features on a node's path do) waits about one LDS latency per
-// 16 pairs rather than two per 8.  The block's last prefetch reads inside the
-// array whether or not it is used.
-__device__ __forceinline__ void run_f32_sorted(const float2* s, uint32_t lo, uint32_t hi, float& ag, float& ah) {
-    uint32_t k = lo;
-    const uint32_t nb = (hi - lo) / 16;
-    if (nb > 0) {
-        float2 a[8], b[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) a[u] = s[k + u];
-        for (uint32_t blk = 0; blk < nb; ++blk) {
-#pragma unroll
-            for (int u = 0; u < 8; ++u) b[u] = s[k + 8 + u];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                ag += a[u].x;
-                ah += a[u].y;
-            }
-            const uint32_t kn = min(k + 16, (uint32_t)(WT - 8));
-#pragma unroll
-            for (int u = 0; u < 8; ++u) a[u] = s[kn + u];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                ag += b[u].x;
-                ah += b[u].y;
-            }
-            k += 16;
-        }
-    }
-    if (k + 8 <= hi) {
-        float2 p[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) p[u] = s[k + u];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            ag += p[u].x;
-            ah += p[u].y;
-        }
-        k += 8;
-    }
-    for (; k < hi; ++k) {
-        const float2 p = s[k];
-        ag += p.x;
-        ah += p.y;
-    }
-}
-
 // Sequential double sums of the fp32 pairs s_gh[idx[k]] (idx null: s_gh[k]),
 // k in [0, hi).
 __device__ __forceinline__ void run_f64(const float2* s_gh, const uint16_t* idx, uint32_t hi, double& ag,
@@ -644,13 +597,14 @@ __device__ __forceinline__ void chain_load(ChainTile& c, const float* __restrict
     }
 }
 
-// The chains (block f, thread b = bin): the node's tiles in order, each
-// tile's g, h and bucketed positions staged in LDS, bin b's run added in fp32
-// in row order (grow.c:55-59); the count cell is cgrow's chain of 1.0f adds,
-// which is min(count, 2^24) exactly.  Sparse builder: the default bin's
-// thread adds the tile's other rows in double in row order (xperm), and
-// block F adds the node's g and h in double in row order (grow.c:85-97);
-// k_hist_default combines them.  G, H hold the node's g, h by position.
+// The chains with default bins (block f, thread b = bin; SPARSE; dense
+// chains run in k_walk_chain_dense): the node's tiles in order, each tile's
+// g, h and bucketed positions staged in LDS, bin b's run added in fp32 in row
+// order (grow.c:55-59); the count cell is cgrow's chain of 1.0f adds, which
+// is min(count, 2^24) exactly.  The default bin's thread adds the tile's
+// other rows in double in row order (xperm), and block F adds the node's g
+// and h in double in row order (grow.c:85-97); k_hist_default combines them.
+// G, H hold the node's g, h by position.
 // Block (f, k): job k's built child (its tiles R->toff[k] ..); G, H hold the
 // g, h of the child's rows at their positions.
 template <bool SPARSE>
@@ -663,10 +617,7 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb,
                                                    float* __restrict__ hist_base, size_t hsz,
                                                    double* __restrict__ eout_b, double* __restrict__ tot_b) {
     __shared__ float2 s_gh[WT];
-    // dense: the tile's pairs in bucket order (each bin's run contiguous);
-    // sparse: the bucket lists' positions
-    __shared__ float2 s_sorted[SPARSE ? 1 : WT];
-    __shared__ uint16_t s_idx[SPARSE ? WT : 1];
+    __shared__ uint16_t s_idx[WT];
     __shared__ uint16_t s_xidx[SPARSE ? WT : 1];
     __shared__ uint16_t s_st[ST];
     const int kj = blockIdx.y;
@@ -697,9 +648,9 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb,
             const int x = j * RB + tid;
             if (x < tn) {
                 s_gh[x] = make_float2(nxt.g[j], nxt.h[j]);
-                if (SPARSE && !totals) {
+                if (!totals) {
                     s_idx[x] = (uint16_t)nxt.idx[j];
-                    s_xidx[x] = (uint16_t)nxt.xidx[j];
+                    if (SPARSE) s_xidx[x] = (uint16_t)nxt.xidx[j];
                 }
             }
         }
@@ -708,19 +659,6 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb,
             if (tid == 0) s_st[NB] = (uint16_t)nxt.st_end;
         }
         __syncthreads();
-        if (!SPARSE) {
-            // the pairs in bucket order: entry k of the lists is position idx
-            // (every read issued before the first write)
-            float2 v[TPT];
-#pragma unroll
-            for (int j = 0; j < TPT; ++j) v[j] = s_gh[j * RB + tid < tn ? nxt.idx[j] : 0u];
-#pragma unroll
-            for (int j = 0; j < TPT; ++j) {
-                const int k = j * RB + tid;
-                if (k < tn) s_sorted[k] = v[j];
-            }
-            __syncthreads();
-        }
         if (t0 + WT < m) chain_load<SPARSE>(nxt, G, H, pf, xf, sf, totals, t + 1, m);
         if (totals) {
             if (tid == 0) run_f64(s_gh, nullptr, (uint32_t)tn, eg, eh);
@@ -730,8 +668,7 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb,
             cnt += (int64_t)tn - nx;
         } else {
             const uint32_t lo = s_st[tid], hi = s_st[tid + 1];
-            if (SPARSE) run_f32(s_gh, s_idx, lo, hi, ag, ah);
-            else run_f32_sorted(s_sorted, lo, hi, ag, ah);
+            run_f32(s_gh, s_idx, lo, hi, ag, ah);
             cnt += hi - lo;
         }
         __syncthreads();
@@ -754,6 +691,131 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb,
         hist[(size_t)1 * F * NB + (size_t)f * NB + tid] = ah;
         hist[(size_t)2 * F * NB + (size_t)f * NB + tid] = (float)min(cnt, (int64_t)1 << 24);
     }
+}
+
+// Sequential fp32 sum of s[k], k in [lo, hi) (hi <= WT): blocks of 16 read 8
+// ahead of the adds, so that a long run (a bin that holds most of a tile, as
+// the features on a node's path do) waits about one LDS latency per 16
+// values rather than per 8; the block's last prefetch reads inside the
+// array whether or not it is used.
+__device__ __forceinline__ void run_f32_one(const float* s, uint32_t lo, uint32_t hi, float& acc) {
+    uint32_t k = lo;
+    const uint32_t nb = (hi - lo) / 16;
+    if (nb > 0) {
+        float a[8], b[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a[u] = s[k + u];
+        for (uint32_t blk = 0; blk < nb; ++blk) {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) b[u] = s[k + 8 + u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += a[u];
+            const uint32_t kn = min(k + 16, (uint32_t)(WT - 8));
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a[u] = s[kn + u];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) acc += b[u];
+            k += 16;
+        }
+    }
+    if (k + 8 <= hi) {
+        float p[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) p[u] = s[k + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) acc += p[u];
+        k += 8;
+    }
+    for (; k < hi; ++k) acc += s[k];
+}
+
+constexpr int CB = 2 * RB;           // threads of a dense chain block: bin b's g chain, then its h chain
+constexpr int CPT = WT / CB;         // positions per thread per tile
+
+// One tile of a dense chain block, CPT positions per thread, loaded a tile ahead.
+struct DenseTile {
+    float g[CPT], h[CPT];
+    uint32_t idx[CPT];
+    uint32_t st;                     // threads 0 .. NB: bucket start (NB: the run total)
+};
+
+__device__ __forceinline__ void dense_load(DenseTile& c, const float* __restrict__ G, const float* __restrict__ H,
+                                           const uint16_t* __restrict__ pf, const uint16_t* __restrict__ sf,
+                                           int64_t t, int64_t m) {
+    const int64_t t0 = t * WT;
+#pragma unroll
+    for (int j = 0; j < CPT; ++j) {
+        const int64_t x = t0 + j * CB + threadIdx.x;
+        if (x < m) {
+            c.g[j] = G[x];
+            c.h[j] = H[x];
+            c.idx[j] = pf[x];
+        }
+    }
+    if (threadIdx.x <= NB) c.st = sf[(size_t)t * ST + threadIdx.x];
+}
+
+// Dense chains (no default bins): block (f, k), thread b (< NB) adds bin b's
+// g and thread NB + b its h, each in fp32 in row order (grow.c:55-59), from
+// the tile's pairs permuted into bucket order in LDS (channel by channel,
+// so a bin's run is contiguous); the count cell is cgrow's chain of 1.0f
+// adds, min(count, 2^24).  A bin's two channels run in different waves:
+// one dependent add per row and thread.
+__global__ void __launch_bounds__(CB) k_walk_chain_dense(const float* __restrict__ Gb, const float* __restrict__ Hb,
+                                                         const Round* __restrict__ R, int F, int fg0,
+                                                         const uint16_t* __restrict__ perm, int64_t ld_perm,
+                                                         const uint16_t* __restrict__ starts, int64_t n_tiles,
+                                                         float* __restrict__ hist_base, size_t hsz) {
+    __shared__ float2 s_gh[WT];
+    __shared__ float s_ch[2][WT];    // g, h in bucket order
+    __shared__ uint16_t s_st[ST];
+    const int kj = blockIdx.y;
+    const Job& J = R->job[kj];
+    const int64_t m = J.ce - J.cs;
+    const int64_t tile0 = R->toff[kj];
+    const float* G = Gb + J.cs;
+    const float* H = Hb + J.cs;
+    const int tid = threadIdx.x, ch = tid / NB, b = tid % NB;
+    const int fl = blockIdx.x, f = fg0 + fl;       // buffers by group position, cells by feature
+    const uint16_t* pf = perm + (size_t)fl * (size_t)ld_perm + (size_t)tile0 * WT;
+    const uint16_t* sf = starts + ((size_t)fl * (size_t)n_tiles + (size_t)tile0) * ST;
+    float acc = 0.0f;
+    int64_t cnt = 0;
+    DenseTile nxt;
+    if (m > 0) dense_load(nxt, G, H, pf, sf, 0, m);
+    for (int64_t t = 0, t0 = 0; t0 < m; ++t, t0 += WT) {
+        const int tn = (int)min((int64_t)WT, m - t0);
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int x = j * CB + tid;
+            if (x < tn) s_gh[x] = make_float2(nxt.g[j], nxt.h[j]);
+        }
+        if (tid <= NB) s_st[tid] = (uint16_t)nxt.st;
+        __syncthreads();
+        // bucket order: entry k of the lists is position idx (every read
+        // issued before the first write)
+        float2 v[CPT];
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) v[j] = s_gh[j * CB + tid < tn ? nxt.idx[j] : 0u];
+#pragma unroll
+        for (int j = 0; j < CPT; ++j) {
+            const int k = j * CB + tid;
+            if (k < tn) {
+                s_ch[0][k] = v[j].x;
+                s_ch[1][k] = v[j].y;
+            }
+        }
+        __syncthreads();
+        if (t0 + WT < m) dense_load(nxt, G, H, pf, sf, t + 1, m);
+        const uint32_t lo = s_st[b], hi = s_st[b + 1];
+        run_f32_one(s_ch[ch], lo, hi, acc);
+        cnt += hi - lo;
+        __syncthreads();
+    }
+    const int slot = J.build_left ? J.slot_l : J.slot_r;
+    float* hist = hist_base + (size_t)slot * hsz;
+    hist[(size_t)ch * F * NB + (size_t)f * NB + b] = acc;
+    if (ch == 0) hist[(size_t)2 * F * NB + (size_t)f * NB + b] = (float)min(cnt, (int64_t)1 << 24);
 }
 
 // ---------------------------------------------------------------------------
@@ -1506,8 +1568,8 @@ struct Grower {
                 k_walk_chain<true><<<cgrid, RB, 0, st>>>(G, H, w.round, F, fg0, nf, dbin, w.perm, w.xperm, w.ld_perm,
                                                          w.starts, w.n_tiles, w.hist, hsz, w.expl, w.tot);
             else
-                k_walk_chain<false><<<cgrid, RB, 0, st>>>(G, H, w.round, F, fg0, nf, dbin, w.perm, w.xperm,
-                                                          w.ld_perm, w.starts, w.n_tiles, w.hist, hsz, w.expl, w.tot);
+                k_walk_chain_dense<<<cgrid, CB, 0, st>>>(G, H, w.round, F, fg0, w.perm, w.ld_perm, w.starts,
+                                                         w.n_tiles, w.hist, hsz);
         }
         if (dbin)
             k_hist_default<<<dim3((F + RB - 1) / RB, (unsigned)K), RB, 0, st>>>(dbin, w.expl, w.tot, F, w.hist, hsz,
