@@ -61,7 +61,7 @@ constexpr int PT = 2048;           // partition rows per block
 constexpr int WT = 4096;           // histogram rows per tile
 constexpr int ST = NB + 1;         // bucket starts per (feature, tile)
 constexpr int KR = 16;             // splits computed per round, at most
-constexpr int RA = 6;              // row arrays: a node at depth d uses array d % RA
+constexpr int RA = 16;             // row arrays: a node at depth d uses array d % RA
 constexpr int PEND_PER_LEAF = 3;   // computed splits per leaf of the budget, at most
 
 // One split of a round (the root's histogram: a pseudo-job with the whole
