@@ -196,8 +196,8 @@ size_t yabt_leaf_fit_workspace_bytes(int64_t n, int n_nodes, int K);
 /* Linear leaf models of one tree: for every leaf (feature[node] == -1) with at
  * least min_samples rows, theta = solve(M + diag(lam,..,lam,1e-8), b) with
  * x1 = [(x - mu) / sd (fp32), 1], M = sum h x1 x1^T, b = -sum g x1 over the
- * leaf's rows.  gram_mode 0: the reference's fp64 products, each rounded once
- * to int64 fixed point and summed exactly (order-free); 1: the same sums in
+ * leaf's rows.  gram_mode 0: each product of the reference's fp64 factors
+ * rounded once to int64 fixed point and summed exactly (order-free); 1: the same sums in
  * fp64 on the matrix cores (v_mfma_f64_16x16x4_f64, a fixed order).
  * Replaces `_fit_linear` (yabt/neural_leaves.py:42-90) and the counts and
  * envelopes of `fit_leaf_networks` (yabt/neural_leaves.py:157-176).

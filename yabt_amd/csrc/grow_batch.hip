@@ -1589,9 +1589,9 @@ int yabt_grow_batched(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins
         return (w & 1) || (w >> 1) - 1 >= r - LOOKAHEAD;
     };
     for (int r = 1; r < max_leaves; ++r) {
-        for (uint64_t spin = 0;; ++spin) {
+        for (SpinWait sw;;) {
             if (ready(r)) break;
-            if ((spin & 1023) == 1023) {
+            if (sw.stream_check()) {
                 const hipError_t e = hipStreamQuery(stream);
                 if (e == hipSuccess) {
                     if (ready(r)) break;

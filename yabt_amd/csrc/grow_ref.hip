@@ -1738,12 +1738,12 @@ int yabt_grow_ref(const uint8_t* bins_fm, int64_t ld_fm, const uint8_t* bins_rm,
                     if (R[k].c[c].seq != seq) return false;
             return true;
         };
-        for (uint64_t spin = 0;; ++spin) {
+        for (SpinWait sw;;) {
             if (all()) {
                 std::atomic_thread_fence(std::memory_order_acquire);
                 return 0;
             }
-            if ((spin & 1023) == 1023) {
+            if (sw.stream_check()) {
                 const hipError_t e = hipStreamQuery(stream);
                 if (e == hipSuccess) {
                     if (all()) return 0;

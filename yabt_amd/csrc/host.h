@@ -5,6 +5,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <chrono>
+
 namespace yabt {
 
 // Per-thread message of the last rejected call (yabt_last_error).
@@ -25,6 +27,23 @@ inline int launch_status(const char* what) {
     const hipError_t e = hipGetLastError();
     return e == hipSuccess ? 0 : hip_fail(e, what);
 }
+
+// A host spin on flags in mapped memory, which a kernel of the stream
+// writes: stream_check() says when to ask the stream whether it failed or
+// ended without writing them.  hipStreamQuery on a stream whose last kernel
+// has no completion signal enqueues a marker behind it, and each marker held
+// the next kernel ~5.7 us on the device; so the stream is asked only once the
+// wait has lasted SPIN_CHECK_MS, which no healthy round takes.
+constexpr int SPIN_CHECK_MS = 50;
+struct SpinWait {
+    std::chrono::steady_clock::time_point t0 = std::chrono::steady_clock::now();
+    uint64_t spin = 0;
+    bool stream_check() {
+        if ((++spin & 1023) != 0) return false;
+        const auto dt = std::chrono::steady_clock::now() - t0;
+        return dt >= std::chrono::milliseconds(SPIN_CHECK_MS);
+    }
+};
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 

@@ -535,11 +535,11 @@ __device__ __forceinline__ bool leaf_eligible(const LeafArgs& A, int node) {
 // Standardised uint8 inputs take 256 values per input: s_x1[j * 256 + b] =
 // (double)((float(b) - mu[j]) / sd[j]), x1 formed in fp32 as the reference
 // forms it (neural_leaves.py:152-155), one table per block in LDS.
-template <int K, int NT>
-__device__ __forceinline__ void x1_table(double* s_x1, const float* mu, const float* sd) {
+template <int K, int NT, typename T>
+__device__ __forceinline__ void x1_table(T* s_x1, const float* mu, const float* sd) {
     for (int i = threadIdx.x; i < K * 256; i += NT) {
         const int j = i / 256, b = i % 256;
-        s_x1[i] = (double)(((float)b - mu[j]) / sd[j]);
+        s_x1[i] = (T)(((float)b - mu[j]) / sd[j]);
     }
 }
 
@@ -554,90 +554,228 @@ __device__ __forceinline__ int node_at(const LeafArgs& A, int64_t c0) {
     return lo;
 }
 
+// How each fixed-point product is rounded and summed (every form is exact
+// and independent of the order of the rows):
+//   GRAM_RINT  n <= 1024: rint of the fp64 product, summed as int64;
+//   GRAM_MAGIC n <= 2^15: the same rounding through the bits of
+//              v + 1.5 * 2^52 (round to nearest even; the constant's bits
+//              come off once per row later);
+//   GRAM_ACC   n > 2^15: one fma per product into a double accumulator that
+//              stays in [2^52, 2^53), where the ulp is 1, so that
+//              fma(x1, y, acc) = acc + (x1 y rounded to an integer) exactly.
+// GRAM_ACC's second factor y has its lowest mantissa bit set (a change of at
+// most 2^-52 of it), so that no product is ever exactly halfway between two
+// integers: with y = m 2^(e - 52), m odd and >= 2^52, and x1's lowest set
+// bit 2^f, the product's lowest set bit is 2^(f + e - 52), which is 2^-1
+// only if |x1 y| >= 2^(f + e) = 2^51, above every scaled product (|p| <
+// 2^(61 - k) <= 2^45 for n > 2^15, k = ceil(log2 n)).  Without a tie the
+// rounding does not depend on the accumulator's parity, so the sums do not
+// depend on the order of the rows.  A thread adds at most LCHUNK / (LB / 2)
+// = 32 products per entry and segment, |sum| <= 32 * 2^45 = 2^50, so the
+// accumulator never leaves the binade.
+enum GramMode { GRAM_RINT = 0, GRAM_MAGIC = 1, GRAM_ACC = 2 };
+constexpr double GRAM_MAGIC_C = 6755399441055744.0;   // 1.5 * 2^52
+static_assert(LCHUNK / (LB / 2) <= 32, "GRAM_ACC: at most 32 products per entry and thread in a segment");
+
+__host__ __device__ constexpr int gram_half_entries(int K) { return (gram_entries(K) + 1) / 2; }
+
+__device__ __forceinline__ double sticky_f64(double v) {
+    return __longlong_as_double(__double_as_longlong(v) | 1ll);
+}
+
 // The fixed-point products of half P of a row's gram_entries (P = 0: entries
-// [0, NE/2), 1: [NE/2, NE)), added into acc[t - the half's first entry].
-// FAST: rounded to integers through the bits of v + 1.5 * 2^52 (round to
-// nearest even, as rint; the constant's bits come off once per row later).
-template <int K, bool FAST, int P>
+// [0, NE/2), 1: [NE/2, NE)), added into acc[t - the half's first entry]
+// (integer sums for GRAM_RINT and GRAM_MAGIC, the binade accumulators for
+// GRAM_ACC, as double bits).
+template <int K, int MODE, int P>
 __device__ __forceinline__ void gram_half(const double (&x1)[K + 1], const double (&xhs)[K + 1], double gs,
-                                          uint64_t (&acc)[(gram_entries(K) + 1) / 2]) {
+                                          uint64_t (&acc)[gram_half_entries(K)]) {
     constexpr int NE = gram_entries(K);
     constexpr int T0 = P == 0 ? 0 : (NE + 1) / 2, T1 = P == 0 ? (NE + 1) / 2 : NE;
-    constexpr double MAGIC = 6755399441055744.0;   // 1.5 * 2^52
+    auto add = [&](uint64_t& a, double x, double y) {   // a += round(x y)
+        if constexpr (MODE == GRAM_ACC) {
+            a = (uint64_t)__double_as_longlong(fma(x, y, __longlong_as_double((long long)a)));
+        } else {
+            const double v = x * y;
+            if constexpr (MODE == GRAM_MAGIC) a += (uint64_t)__double_as_longlong(v + GRAM_MAGIC_C);
+            else a += (uint64_t)(int64_t)rint(v);
+        }
+    };
     int t = 0;
 #pragma unroll
     for (int a = 0; a <= K; ++a) {
 #pragma unroll
         for (int b = a; b <= K; ++b, ++t) {
             if (t < T0 || t >= T1) continue;
-            const double v = x1[a] * xhs[b];      // the reference's product, times 2^sM exactly
-            if (FAST) acc[t - T0] += (uint64_t)__double_as_longlong(v + MAGIC);
-            else acc[t - T0] += (uint64_t)(int64_t)rint(v);
+            add(acc[t - T0], x1[a], xhs[b]);          // the reference's x1 (x1 h), times 2^sM
         }
     }
 #pragma unroll
     for (int a = 0; a <= K; ++a, ++t) {            // rhs = -(X1 * g)
         if (t < T0 || t >= T1) continue;
-        const double v = -(x1[a] * gs);
-        if (FAST) acc[t - T0] += (uint64_t)__double_as_longlong(v + MAGIC);
-        else acc[t - T0] += (uint64_t)(int64_t)rint(v);
+        add(acc[t - T0], -x1[a], gs);
     }
 }
 
 // One half-block's rows p = p0, p0 + LB / 2, ... < e of a segment: x1 and
-// x1 h from the row, then half P of its products into acc.
-template <int K, bool FAST, int P>
-__device__ __forceinline__ void gram_rows(const LeafArgs& A, const double* s_x1, const float* s_mu,
+// x1 h from the row, then half P of its products into acc (integer sums on
+// return, whatever the mode).
+template <int K, int MODE, int P>
+__device__ __forceinline__ void gram_rows(const LeafArgs& A, const float* s_x1, const float* s_mu,
                                           const float* s_sd, double scM, double scb, int64_t p0, int64_t e,
-                                          uint64_t (&acc)[(gram_entries(K) + 1) / 2]) {
-    constexpr double MAGIC = 6755399441055744.0;   // 1.5 * 2^52
+                                          uint64_t (&acc)[gram_half_entries(K)]) {
+    constexpr int NH = gram_half_entries(K);
+    const uint64_t magic_bits = (uint64_t)__double_as_longlong(GRAM_MAGIC_C);
+    if constexpr (MODE == GRAM_ACC) {
+#pragma unroll
+        for (int t = 0; t < NH; ++t) acc[t] = magic_bits;
+    }
     uint64_t nrow = 0;
-    for (int64_t p = p0; p < e; p += LB / 2) {
-        const float2 gh = A.sorted_gh[p];
-        double x1[K + 1];
-        if (A.x_kind == 1) {
-            const uint2 v = reinterpret_cast<const uint2*>(A.sorted_x)[p];
-#pragma unroll
-            for (int j = 0; j < K; ++j) x1[j] = s_x1[j * 256 + (((j < 4 ? v.x : v.y) >> (8 * (j & 3))) & 0xffu)];
-        } else {
-            const float* src = reinterpret_cast<const float*>(A.sorted_x) + (size_t)p * K;
-#pragma unroll
-            for (int j = 0; j < K; ++j) x1[j] = (double)((src[j] - s_mu[j]) / s_sd[j]);
-        }
-        x1[K] = 1.0;
+    // one row: x1 from its inputs, x1 h, then the products
+    auto row = [&](const double (&x1)[K + 1], float2 gh) {
         // Xh = X1 * h (neural_leaves.py:72), scaled by 2^sM: a power-of-two
         // scale commutes with the fp64 rounding (no overflow or underflow at
         // these magnitudes), so x1 * (h 2^sM) is (x1 * h) 2^sM exactly
         const double hs = (double)gh.y * scM;
-        const double gs = (double)gh.x * scb;
+        double gs = (double)gh.x * scb;
         double xhs[K + 1];
 #pragma unroll
         for (int b = 0; b <= K; ++b) xhs[b] = x1[b] * hs;
-        ++nrow;
-        gram_half<K, FAST, P>(x1, xhs, gs, acc);
-    }
-    if (FAST) {
-        const uint64_t off = nrow * (uint64_t)__double_as_longlong(MAGIC);
+        if constexpr (MODE == GRAM_ACC) {
 #pragma unroll
-        for (int t = 0; t < (gram_entries(K) + 1) / 2; ++t) acc[t] -= off;
+            for (int b = 0; b <= K; ++b) xhs[b] = sticky_f64(xhs[b]);
+            gs = sticky_f64(gs);
+        }
+        ++nrow;
+        gram_half<K, MODE, P>(x1, xhs, gs, acc);
+    };
+    if (A.x_kind == 1) {
+        // uint8 inputs: the next row's inputs and g, h are loaded while this
+        // row is summed (two named buffers, loads at clamped positions, so
+        // that each wait covers only the row about to be used)
+        constexpr int64_t ST = LB / 2;
+        const uint2* xs = reinterpret_cast<const uint2*>(A.sorted_x);
+        auto table = [&](uint2 v, double (&x1)[K + 1]) {
+#pragma unroll
+            for (int j = 0; j < K; ++j)
+                x1[j] = (double)s_x1[j * 256 + (((j < 4 ? v.x : v.y) >> (8 * (j & 3))) & 0xffu)];
+            x1[K] = 1.0;
+        };
+        if (p0 < e) {
+            uint2 va = xs[p0], vb;
+            float2 ga = A.sorted_gh[p0], gb;
+            for (int64_t p = p0;; p += 2 * ST) {
+                const int64_t pb = min(p + ST, e - 1);
+                vb = xs[pb];
+                gb = A.sorted_gh[pb];
+                asm volatile("" ::: "memory");        // keeps the loads here (not sunk to their use)
+                {
+                    double x1[K + 1];
+                    table(va, x1);
+                    row(x1, ga);
+                }
+                if (p + ST >= e) break;
+                const int64_t pa = min(p + 2 * ST, e - 1);
+                va = xs[pa];
+                ga = A.sorted_gh[pa];
+                asm volatile("" ::: "memory");
+                {
+                    double x1[K + 1];
+                    table(vb, x1);
+                    row(x1, gb);
+                }
+                if (p + 2 * ST >= e) break;
+            }
+        }
+    } else {
+        for (int64_t p = p0; p < e; p += LB / 2) {
+            const float2 gh = A.sorted_gh[p];
+            double x1[K + 1];
+            const float* src = reinterpret_cast<const float*>(A.sorted_x) + (size_t)p * K;
+#pragma unroll
+            for (int j = 0; j < K; ++j) x1[j] = (double)((src[j] - s_mu[j]) / s_sd[j]);
+            x1[K] = 1.0;
+            row(x1, gh);
+        }
+    }
+    if constexpr (MODE != GRAM_RINT) {
+        // GRAM_ACC: bits(acc) - bits(1.5 * 2^52) is the integer sum (one
+        // binade, ulp 1); GRAM_MAGIC: the constant's bits once per row
+        const uint64_t off = MODE == GRAM_ACC ? magic_bits : nrow * magic_bits;
+#pragma unroll
+        for (int t = 0; t < NH; ++t) acc[t] -= off;
     }
 }
+
+// Block sums of a half's NH integer accumulators: a reduce-scatter over the
+// wave -- v_permlane32_swap pairs entry i with entry i + S/2 (one lane half
+// keeps the sum of one, the other half of the other), v_permlane16_swap does
+// the same between rows, and DPP row rotations add up each row -- so that
+// lane 16 r of value i holds the wave's total of entry id[i] in row r.  The
+// entry a lane holds is found by passing the entry numbers through the same
+// swaps (make_ids), which also makes the layout independent of the direction
+// in which each swap moves data: after a swap a lane's two operands hold the
+// same entry, its own and its partner's partial sums.
+template <int NH>
+struct GramScatter {
+    static constexpr int S = (NH + 3) / 4 * 4;       // entries padded to a multiple of 4
+    static constexpr int V = S / 4;                  // values per lane after the swaps
+    int id[V];
+
+    __device__ __forceinline__ void make_ids() {
+        uint32_t a[S / 2];
+#pragma unroll
+        for (int i = 0; i < S / 2; ++i) {
+            const auto sw = __builtin_amdgcn_permlane32_swap((uint32_t)i, (uint32_t)(i + S / 2), false, false);
+            a[i] = sw[0];
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const auto sw = __builtin_amdgcn_permlane16_swap(a[i], a[i + V], false, false);
+            id[i] = (int)sw[0];
+        }
+    }
+
+    // acc (NH values, every lane of the wave active) -> out[i]: the wave's
+    // total of entry id[i] in every lane of row (lane / 16)
+    __device__ __forceinline__ void reduce(const uint64_t (&acc)[NH], uint64_t (&out)[V]) const {
+        uint64_t a[S / 2];
+#pragma unroll
+        for (int i = 0; i < S / 2; ++i) {
+            const uint64_t x = acc[i], y = i + S / 2 < NH ? acc[i + S / 2] : 0;
+            const auto lo = __builtin_amdgcn_permlane32_swap((uint32_t)x, (uint32_t)y, false, false);
+            const auto hi = __builtin_amdgcn_permlane32_swap((uint32_t)(x >> 32), (uint32_t)(y >> 32), false, false);
+            a[i] = ((((uint64_t)hi[0]) << 32) | lo[0]) + ((((uint64_t)hi[1]) << 32) | lo[1]);
+        }
+#pragma unroll
+        for (int i = 0; i < V; ++i) {
+            const uint64_t x = a[i], y = a[i + V];
+            const auto lo = __builtin_amdgcn_permlane16_swap((uint32_t)x, (uint32_t)y, false, false);
+            const auto hi = __builtin_amdgcn_permlane16_swap((uint32_t)(x >> 32), (uint32_t)(y >> 32), false, false);
+            uint64_t u = ((((uint64_t)hi[0]) << 32) | lo[0]) + ((((uint64_t)hi[1]) << 32) | lo[1]);
+            u += dpp64<DPP_ROW_ROR + 8>(u);
+            u += dpp64<DPP_ROW_ROR + 4>(u);
+            u += dpp64<DPP_ROW_ROR + 2>(u);
+            u += dpp64<DPP_ROW_ROR + 1>(u);
+            out[i] = u;
+        }
+    }
+};
 
 // Sorted positions [blockIdx.x * LCHUNK, +LCHUNK): for each node run inside
 // the chunk, the block's two halves (waves 0-1 and 2-3) each sum half of the
 // gram_entries over every row of the run, a thread's rows in registers
 // (half the accumulators per thread: twice the resident waves); waves reduce
-// with DPP and the block's sums go to the segment's own partial slot.
-// FAST (n > 1024, so every scaled product is below 2^51 in magnitude): the
-// products are rounded by the 1.5 * 2^52 trick; otherwise rint.
-template <int K, bool FAST>
+// by the reduce-scatter above and the block's sums are added into the node's
+// sums.  MODE: GramMode, by the row count.
+template <int K, int MODE>
 __global__ void __launch_bounds__(LB) k_leaf_gram(LeafArgs A) {
     constexpr int NE = gram_entries(K);
-    constexpr int NH = (NE + 1) / 2;              // entries of the first half (the second has NE - NH)
+    constexpr int NH = gram_half_entries(K);      // entries of the first half (the second has NE - NH)
     constexpr int HT = LB / 2;                    // threads per half
     __shared__ float s_mu[LKMAX], s_sd[LKMAX];
     __shared__ int64_t s_part[LB / WAVE][NH];
-    __shared__ double s_x1[K * 256];
+    __shared__ float s_x1[K * 256];           // x1 is an fp32 value: half the LDS bytes of doubles
     if (threadIdx.x < K) {
         s_mu[threadIdx.x] = A.mu[threadIdx.x];
         s_sd[threadIdx.x] = A.sd[threadIdx.x];
@@ -650,23 +788,27 @@ __global__ void __launch_bounds__(LB) k_leaf_gram(LeafArgs A) {
     const double scM = ldexp(1.0, A.st->sM), scb = ldexp(1.0, A.st->sb);
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
     const int half = threadIdx.x / HT, th = threadIdx.x % HT;   // wave-uniform half
+    GramScatter<NH> R;
     for (int node = node_at(A, c0); node < A.n_nodes && A.off[node] < c1; ++node) {
         const int64_t s = max(c0, A.off[node]), e = min(c1, A.off[node + 1]);
         if (s >= e || !leaf_eligible(A, node)) continue;   // uniform across the block
         uint64_t acc[NH];
 #pragma unroll
         for (int t = 0; t < NH; ++t) acc[t] = 0;
-        if (half == 0) gram_rows<K, FAST, 0>(A, s_x1, s_mu, s_sd, scM, scb, s + th, e, acc);
-        else gram_rows<K, FAST, 1>(A, s_x1, s_mu, s_sd, scM, scb, s + th, e, acc);
+        if (half == 0) gram_rows<K, MODE, 0>(A, s_x1, s_mu, s_sd, scM, scb, s + th, e, acc);
+        else gram_rows<K, MODE, 1>(A, s_x1, s_mu, s_sd, scM, scb, s + th, e, acc);
         // block sum of this (chunk, node) segment, added into the node's sums
         // with 64-bit integer atomics (exact, so the order of the segments
         // does not matter); a node's segments are its chunks, so an address
         // takes at most rows / LCHUNK + 1 adds
         const int nh = half == 0 ? NH : NE - NH;
+        uint64_t tot[GramScatter<NH>::V];
+        R.reduce(acc, tot);
+        R.make_ids();                                 // here, not held across the rows (registers)
+        if ((lane & 15) == 0) {
 #pragma unroll
-        for (int t = 0; t < NH; ++t) {
-            const int64_t v = wave_sum_i64((int64_t)acc[t]);
-            if (lane == 0 && t < nh) s_part[w][t] = v;
+            for (int i = 0; i < GramScatter<NH>::V; ++i)
+                if (R.id[i] < nh) s_part[w][R.id[i]] = (int64_t)tot[i];
         }
         __syncthreads();
         unsigned long long* out = reinterpret_cast<unsigned long long*>(A.sums + (size_t)node * gram_entries(LKMAX));
@@ -1124,8 +1266,9 @@ void launch_leaf_fit(LeafArgs& A, float* out_W, float* out_b, float* out_lo, flo
             k_leaf_gram_mfma<K><<<chunks, LB, 0, stream>>>(A);
             k_leaf_reduce<K><<<A.n_nodes, RB, 0, stream>>>(A);
         } else {
-            if (A.n > 1024) k_leaf_gram<K, true><<<chunks, LB, 0, stream>>>(A);
-            else k_leaf_gram<K, false><<<chunks, LB, 0, stream>>>(A);
+            if (A.n > 32768) k_leaf_gram<K, GRAM_ACC><<<chunks, LB, 0, stream>>>(A);
+            else if (A.n > 1024) k_leaf_gram<K, GRAM_MAGIC><<<chunks, LB, 0, stream>>>(A);
+            else k_leaf_gram<K, GRAM_RINT><<<chunks, LB, 0, stream>>>(A);
         }
     }
     constexpr int per_block = LB / SOLVE_LANES;   // nodes per solve block
