@@ -35,6 +35,11 @@
 
 #include <string.h>
 
+#include <algorithm>
+#include <map>
+#include <mutex>
+#include <tuple>
+
 namespace yabt {
 
 constexpr int LKMAX = 8;                       // model inputs per leaf, at most
@@ -74,6 +79,7 @@ struct LeafArgs {
     double lam;
     int gram_f64;              // 1: M and b summed in fp64 by MFMA (parts and sums hold double bits)
     int64_t rows_per_block;    // stats/scatter rows per block (a multiple of 4)
+    int64_t gram_chunk;        // sorted positions per exact-Gram block (a multiple of LB / 2)
     int vec4;                  // leaf ids, g, h and feature-major inputs aligned for 4-row vector
                                // loads: 1 uint8 inputs, 2 fp32 inputs; 0 none
     // workspace
@@ -570,12 +576,12 @@ __device__ __forceinline__ int node_at(const LeafArgs& A, int64_t c0) {
 // only if |x1 y| >= 2^(f + e) = 2^51, above every scaled product (|p| <
 // 2^(61 - k) <= 2^45 for n > 2^15, k = ceil(log2 n)).  Without a tie the
 // rounding does not depend on the accumulator's parity, so the sums do not
-// depend on the order of the rows.  A thread adds at most LCHUNK / (LB / 2)
-// = 32 products per entry and segment, |sum| <= 32 * 2^45 = 2^50, so the
-// accumulator never leaves the binade.
+// depend on the order of the rows.  A thread adds at most gram_chunk / (LB
+// / 2) products per entry and segment, which the host keeps at most
+// 2^(k - 11), so |sum| <= 2^(k - 11) 2^(61 - k) = 2^50 and the accumulator
+// never leaves the binade.
 enum GramMode { GRAM_RINT = 0, GRAM_MAGIC = 1, GRAM_ACC = 2 };
 constexpr double GRAM_MAGIC_C = 6755399441055744.0;   // 1.5 * 2^52
-static_assert(LCHUNK / (LB / 2) <= 32, "GRAM_ACC: at most 32 products per entry and thread in a segment");
 
 __host__ __device__ constexpr int gram_half_entries(int K) { return (gram_entries(K) + 1) / 2; }
 
@@ -762,36 +768,59 @@ struct GramScatter {
     }
 };
 
-// Sorted positions [blockIdx.x * LCHUNK, +LCHUNK): for each node run inside
-// the chunk, the block's two halves (waves 0-1 and 2-3) each sum half of the
-// gram_entries over every row of the run, a thread's rows in registers
-// (half the accumulators per thread: twice the resident waves); waves reduce
-// by the reduce-scatter above and the block's sums are added into the node's
-// sums.  MODE: GramMode, by the row count.
+// Sorted positions [blockIdx.x * gram_chunk, +gram_chunk): the block lists
+// the chunk's segments (the eligible nodes whose rows meet it); for each, the
+// block's two halves (waves 0-1 and 2-3) each sum half of the gram_entries
+// over the segment's rows, a thread's rows in registers (half the
+// accumulators per thread: twice the resident waves); waves reduce by the
+// reduce-scatter above and the block's sums are added into the node's sums.
+// MODE: GramMode, by the row count.
 template <int K, int MODE>
 __global__ void __launch_bounds__(LB) k_leaf_gram(LeafArgs A) {
     constexpr int NE = gram_entries(K);
     constexpr int NH = gram_half_entries(K);      // entries of the first half (the second has NE - NH)
     constexpr int HT = LB / 2;                    // threads per half
     __shared__ float s_mu[LKMAX], s_sd[LKMAX];
-    __shared__ int64_t s_part[LB / WAVE][NH];
+    __shared__ int64_t s_part[2][LB / WAVE][NH];  // two, alternating by segment: one barrier each
     __shared__ float s_x1[K * 256];           // x1 is an fp32 value: half the LDS bytes of doubles
+    __shared__ int s_nseg;
+    extern __shared__ int s_seg[];                // min(n_nodes, gram_chunk) entries (launch's dynamic LDS)
+    // the loads the prologue waits for, issued together
+    const int64_t total = A.off[A.n_nodes];
+    const int32_t sM = A.st->sM, sb = A.st->sb;
     if (threadIdx.x < K) {
         s_mu[threadIdx.x] = A.mu[threadIdx.x];
         s_sd[threadIdx.x] = A.sd[threadIdx.x];
     }
+    if (threadIdx.x == 0) s_nseg = 0;
     if (A.x_kind == 1) x1_table<K, LB>(s_x1, A.mu, A.sd);
+    const int64_t c0 = (int64_t)blockIdx.x * A.gram_chunk, c1 = min(total, c0 + A.gram_chunk);
     __syncthreads();
-    const int64_t total = A.off[A.n_nodes];
-    const int64_t c0 = (int64_t)blockIdx.x * LCHUNK, c1 = min(total, c0 + LCHUNK);
+    // the chunk's segments, every thread testing its share of the nodes at
+    // once: the eligible nodes whose rows meet [c0, c1), listed in LDS in no
+    // particular order (the sums are exact).  The node ranges are disjoint,
+    // so at most min(n_nodes, c1 - c0) are listed.  A node-by-node walk with
+    // its dependent loads had cost ~3 us a segment, and a chunk of many small
+    // leaves twice a chunk's time.
+    if (c0 < c1) {
+        for (int t = threadIdx.x; t < A.n_nodes; t += LB) {
+            const int64_t lo = A.off[t], hi = A.off[t + 1];
+            if (lo < c1 && hi > c0 && leaf_eligible(A, t)) s_seg[atomicAdd(&s_nseg, 1)] = t;
+        }
+    }
+    __syncthreads();
     if (c0 >= c1) return;
-    const double scM = ldexp(1.0, A.st->sM), scb = ldexp(1.0, A.st->sb);
+    const double scM = ldexp(1.0, sM), scb = ldexp(1.0, sb);
     const int lane = threadIdx.x & (WAVE - 1), w = threadIdx.x / WAVE;
     const int half = threadIdx.x / HT, th = threadIdx.x % HT;   // wave-uniform half
     GramScatter<NH> R;
-    for (int node = node_at(A, c0); node < A.n_nodes && A.off[node] < c1; ++node) {
+    int buf = 0;
+    // the node and count read from LDS are the same in every lane:
+    // readfirstlane keeps them (and what is derived from them) scalar
+    const int nseg = __builtin_amdgcn_readfirstlane(s_nseg);
+    for (int k = 0; k < nseg; ++k) {
+        const int node = __builtin_amdgcn_readfirstlane(s_seg[k]);
         const int64_t s = max(c0, A.off[node]), e = min(c1, A.off[node + 1]);
-        if (s >= e || !leaf_eligible(A, node)) continue;   // uniform across the block
         uint64_t acc[NH];
 #pragma unroll
         for (int t = 0; t < NH; ++t) acc[t] = 0;
@@ -800,7 +829,8 @@ __global__ void __launch_bounds__(LB) k_leaf_gram(LeafArgs A) {
         // block sum of this (chunk, node) segment, added into the node's sums
         // with 64-bit integer atomics (exact, so the order of the segments
         // does not matter); a node's segments are its chunks, so an address
-        // takes at most rows / LCHUNK + 1 adds
+        // takes at most rows / gram_chunk + 1 adds.  The next segment writes
+        // the other s_part, so one barrier separates the writes from the reads.
         const int nh = half == 0 ? NH : NE - NH;
         uint64_t tot[GramScatter<NH>::V];
         R.reduce(acc, tot);
@@ -808,7 +838,7 @@ __global__ void __launch_bounds__(LB) k_leaf_gram(LeafArgs A) {
         if ((lane & 15) == 0) {
 #pragma unroll
             for (int i = 0; i < GramScatter<NH>::V; ++i)
-                if (R.id[i] < nh) s_part[w][R.id[i]] = (int64_t)tot[i];
+                if (R.id[i] < nh) s_part[buf][w][R.id[i]] = (int64_t)tot[i];
         }
         __syncthreads();
         unsigned long long* out = reinterpret_cast<unsigned long long*>(A.sums + (size_t)node * gram_entries(LKMAX));
@@ -817,10 +847,10 @@ __global__ void __launch_bounds__(LB) k_leaf_gram(LeafArgs A) {
             const int hh = t < NH ? 0 : 1, tt = t < NH ? t : t - NH;
             int64_t v = 0;
 #pragma unroll
-            for (int i = 0; i < HW; ++i) v += s_part[hh * HW + i][tt];
+            for (int i = 0; i < HW; ++i) v += s_part[buf][hh * HW + i][tt];
             if (v) atomicAdd(&out[t], (unsigned long long)v);
         }
-        __syncthreads();
+        buf ^= 1;
     }
 }
 
@@ -1237,6 +1267,49 @@ size_t carve_leaf(char* base, int64_t n, int n_nodes, int K, LeafArgs* A) {
     return align_up(c.off, 256);
 }
 
+// Blocks of a Gram kernel resident on the current device at once (its
+// occupancy with `lds` bytes of dynamic LDS, times the CU count), per device
+// and LDS size, made on first use.
+template <typename Kern>
+int64_t gram_slots(Kern kern, size_t lds) {
+    static std::mutex mu;
+    static std::map<std::tuple<int, const void*, size_t>, int64_t> cache;
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 1024;
+    const auto key = std::make_tuple(dev, reinterpret_cast<const void*>(kern), lds);
+    std::lock_guard<std::mutex> g(mu);
+    const auto it = cache.find(key);
+    if (it != cache.end()) return it->second;
+    int per_cu = 0, cus = 0;
+    int64_t slots = 1024;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, LB, lds) == hipSuccess &&
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && per_cu > 0 &&
+        cus > 0)
+        slots = (int64_t)per_cu * cus;
+    cache[key] = slots;
+    return slots;
+}
+
+// GRAM_ACC's chunk: LCHUNK positions, or, when that makes more than one full
+// wave of resident blocks, the size that makes the chunk count a whole
+// multiple of them (a last, partial wave of blocks had left most of the
+// device idle for a block's lifetime: 2442 chunks of 4096 at 10M rows on
+// 1024 slots), rounded up to whole rows per thread and kept at most
+// (LB / 2) 2^(k - 11) so that a thread adds at most 2^(k - 11) products per
+// entry and segment (k = ceil(log2 n) >= 16 here).
+inline int64_t gram_chunk(int64_t n, int64_t slots) {
+    int64_t chunk = LCHUNK;
+    const int64_t waves = n / (slots * LCHUNK);
+    if (waves >= 1) {
+        chunk = (n + slots * waves - 1) / (slots * waves);
+        chunk = (chunk + LB / 2 - 1) / (LB / 2) * (LB / 2);
+    }
+    int k = 0;
+    while (k < 62 && ((int64_t)1 << k) < n) ++k;
+    const int64_t cap = (int64_t)(LB / 2) << (k > 11 ? k - 11 : 0);
+    return chunk < cap ? chunk : cap;
+}
+
 template <int K>
 void launch_leaf_fit(LeafArgs& A, float* out_W, float* out_b, float* out_lo, float* out_hi, int64_t* out_count,
                      hipStream_t stream) {
@@ -1266,9 +1339,14 @@ void launch_leaf_fit(LeafArgs& A, float* out_W, float* out_b, float* out_lo, flo
             k_leaf_gram_mfma<K><<<chunks, LB, 0, stream>>>(A);
             k_leaf_reduce<K><<<A.n_nodes, RB, 0, stream>>>(A);
         } else {
-            if (A.n > 32768) k_leaf_gram<K, GRAM_ACC><<<chunks, LB, 0, stream>>>(A);
-            else if (A.n > 1024) k_leaf_gram<K, GRAM_MAGIC><<<chunks, LB, 0, stream>>>(A);
-            else k_leaf_gram<K, GRAM_RINT><<<chunks, LB, 0, stream>>>(A);
+            // dynamic LDS: the chunk's segment list
+            A.gram_chunk = LCHUNK;
+            if (A.n > 32768) A.gram_chunk = gram_chunk(A.n, gram_slots(k_leaf_gram<K, GRAM_ACC>, 0));
+            const size_t seg_lds = sizeof(int) * (size_t)std::min<int64_t>(A.n_nodes, A.gram_chunk);
+            const int gc = (int)((A.n + A.gram_chunk - 1) / A.gram_chunk);
+            if (A.n > 32768) k_leaf_gram<K, GRAM_ACC><<<gc, LB, seg_lds, stream>>>(A);
+            else if (A.n > 1024) k_leaf_gram<K, GRAM_MAGIC><<<gc, LB, seg_lds, stream>>>(A);
+            else k_leaf_gram<K, GRAM_RINT><<<gc, LB, seg_lds, stream>>>(A);
         }
     }
     constexpr int per_block = LB / SOLVE_LANES;   // nodes per solve block
