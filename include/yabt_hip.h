@@ -244,6 +244,27 @@ int yabt_leaf_fold(int n_nodes, int K, const float *W, const float *b, const flo
 int yabt_leaf_rank_features(const int64_t *feature, int n_nodes, int F, int k, int64_t *out_feats,
                             int32_t *out_feats32, int32_t *out_m, yabt_stream_t stream);
 
+/* One tree's leaf models in one call: yabt_leaf_rank_features (the first K
+ * of the tree's split features, F = the features of X), yabt_leaf_moments on
+ * them, yabt_leaf_fit and yabt_leaf_fold, launched back to back on `stream`
+ * with nothing read back, so that the device runs the step without waiting
+ * for the host between the calls (the same kernels and results as the four
+ * calls).  ws_moments and ws_fit: the workspaces of yabt_leaf_moments and
+ * yabt_leaf_fit; out_feats, out_feats32 as yabt_leaf_rank_features; out_mu,
+ * out_sd as yabt_leaf_moments; out_W .. out_count as yabt_leaf_fit;
+ * out_value, out_linear as yabt_leaf_fold; out_status (3): [0] and [1] as
+ * yabt_leaf_fit, [2] the number of used features (yabt_leaf_rank_features'
+ * out_m: the results hold only when it is >= K).  Replaces the sequence of
+ * `fit_leaf_networks` (yabt/neural_leaves.py:131-184) for one tree. */
+int yabt_leaf_step(int x_kind, const void *X, int64_t ldx, int64_t n, int F, int K, const float *grad,
+                   const float *hess, const int64_t *leaf_of_row, const int64_t *feature,
+                   const float *value_in, int n_nodes, int min_samples, double lam, float lr,
+                   int gram_mode, void *ws_moments, size_t ws_moments_bytes, void *ws_fit,
+                   size_t ws_fit_bytes, int64_t *out_feats, int32_t *out_feats32, float *out_mu,
+                   float *out_sd, float *out_W, float *out_b, float *out_lo, float *out_hi,
+                   int64_t *out_count, float *out_value, float *out_linear, int32_t *out_status,
+                   yabt_stream_t stream);
+
 /* Workspace bytes of yabt_leaf_moments for n rows. */
 size_t yabt_leaf_moments_workspace_bytes(int64_t n);
 

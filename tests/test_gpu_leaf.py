@@ -317,8 +317,10 @@ def test_leaf_rank_features_flags_feature_out_of_range():
 
 
 def test_fit_binned_device_ranking_equals_host_ranking():
-    """fit_leaf_networks_binned with the device ranking (the default) gives
-    the same tree, bit for bit, as the host ranking path."""
+    """fit_leaf_networks_binned with the device ranking (the default: one
+    yabt_leaf_step call) gives the same tree, bit for bit, as the host
+    ranking path (separate yabt_leaf_moments, yabt_leaf_fit and
+    yabt_leaf_fold calls)."""
     from yabt_amd import neural_leaves as NL
     rng = np.random.default_rng(5)
     n, F = 50_000, 30

@@ -68,6 +68,9 @@ SIGNATURES = {
                              _dbl, _int, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "yabt_leaf_fold": (_int, [_int, _int, _vp, _vp, _vp, _vp, _flt, _vp, _vp, _vp, _vp]),
     "yabt_leaf_rank_features": (_int, [_vp, _int, _int, _int, _vp, _vp, _vp, _vp]),
+    "yabt_leaf_step": (_int, [_int, _vp, _i64, _i64, _int, _int, _vp, _vp, _vp, _vp, _vp, _int, _int, _dbl,
+                              _flt, _int, _vp, _sz, _vp, _sz, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                              _vp, _vp, _vp, _vp]),
     "yabt_grow_batched_workspace_bytes": (_sz, [_i64, _int, _int]),
     "yabt_grow_batched": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _vp, _vp, _flt, _int, _vp, _vp, _vp, _i64,
                                  _int,

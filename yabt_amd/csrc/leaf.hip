@@ -1622,6 +1622,25 @@ int yabt_leaf_fit(int x_kind, const void* X, int64_t ldx, int64_t n, const int32
     return launch_status("yabt_leaf_fit launch");
 }
 
+int yabt_leaf_step(int x_kind, const void* X, int64_t ldx, int64_t n, int F, int K, const float* grad,
+                   const float* hess, const int64_t* leaf_of_row, const int64_t* feature, const float* value_in,
+                   int n_nodes, int min_samples, double lam, float lr, int gram_mode, void* ws_moments,
+                   size_t ws_moments_bytes, void* ws_fit, size_t ws_fit_bytes, int64_t* out_feats,
+                   int32_t* out_feats32, float* out_mu, float* out_sd, float* out_W, float* out_b, float* out_lo,
+                   float* out_hi, int64_t* out_count, float* out_value, float* out_linear, int32_t* out_status,
+                   hipStream_t stream) {
+    if (!out_status) return fail(-2, "yabt_leaf_step: null pointer argument");
+    int rc = yabt_leaf_rank_features(feature, n_nodes, F, K, out_feats, out_feats32, out_status + 2, stream);
+    if (rc) return rc;
+    rc = yabt_leaf_moments(x_kind, X, ldx, n, out_feats32, K, ws_moments, ws_moments_bytes, out_mu, out_sd, stream);
+    if (rc) return rc;
+    rc = yabt_leaf_fit(x_kind, X, ldx, n, out_feats32, K, out_mu, out_sd, grad, hess, leaf_of_row, feature, n_nodes,
+                       min_samples, lam, gram_mode, ws_fit, ws_fit_bytes, out_W, out_b, out_lo, out_hi, out_count,
+                       out_status, stream);
+    if (rc) return rc;
+    return yabt_leaf_fold(n_nodes, K, out_W, out_b, out_mu, out_sd, lr, value_in, out_value, out_linear, stream);
+}
+
 int yabt_leaf_fold(int n_nodes, int K, const float* W, const float* b, const float* mu, const float* sd, float lr,
                    const float* value_in, float* out_value, float* out_linear, hipStream_t stream) {
     if (n_nodes < 1 || K < 1 || K > LKMAX) return fail(-2, "yabt_leaf_fold: bad sizes (n_nodes >= 1, 1 <= K <= 8)");

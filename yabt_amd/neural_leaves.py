@@ -229,22 +229,29 @@ def _leaf_step(tree: Tree, X: torch.Tensor, x_kind: int, n: int, feats: torch.Te
     lo, hi, linear = (kb[o:o + 4 * N * K].view(torch.float32).view(N, K) for o in (ko[0], ko[1], ko[3]))
     value = kb[ko[2]:ko[2] + 4 * N].view(torch.float32)
     ldx, st = X.stride(0), _stream(dev)
+    min_samples = int(getattr(params, "leaf_net_min_samples", 50))
+    lam = float(getattr(params, "leaf_net_l2", 1.0))
+    lr = float(params.learning_rate)
     if rank_k:
+        # ranking, moments, fit and fold in one call: the launches go out
+        # without a return to Python between them
         feats = kb[ko[4]:ko[4] + 8 * K].view(torch.int64)
-        _lib.check(lib.yabt_leaf_rank_features(ft.data_ptr(), N, int(X.shape[0]), K, feats.data_ptr(), a_fi,
-                                               status.data_ptr() + 8, st), "yabt_leaf_rank_features")
+        _lib.check(lib.yabt_leaf_step(x_kind, X.data_ptr(), ldx, n, int(X.shape[0]), K, g.data_ptr(),
+                                      h.data_ptr(), li.data_ptr(), ft.data_ptr(), value_in.data_ptr(), N,
+                                      min_samples, lam, lr, mode, a_mws, mbytes, a_fws, fbytes, feats.data_ptr(),
+                                      a_fi, a_mu, a_sd, a_W, a_b, lo.data_ptr(), hi.data_ptr(), a_cnt,
+                                      value.data_ptr(), linear.data_ptr(), status.data_ptr(), st),
+                   "yabt_leaf_step")
     else:
         a_fi = fi.data_ptr()
-    _lib.check(lib.yabt_leaf_moments(x_kind, X.data_ptr(), ldx, n, a_fi, K, a_mws, mbytes, a_mu, a_sd, st),
-               "yabt_leaf_moments")
-    _lib.check(lib.yabt_leaf_fit(x_kind, X.data_ptr(), ldx, n, a_fi, K, a_mu, a_sd,
-                                 g.data_ptr(), h.data_ptr(), li.data_ptr(), ft.data_ptr(), N,
-                                 int(getattr(params, "leaf_net_min_samples", 50)),
-                                 float(getattr(params, "leaf_net_l2", 1.0)), mode, a_fws, fbytes,
-                                 a_W, a_b, lo.data_ptr(), hi.data_ptr(), a_cnt, status.data_ptr(), st),
-               "yabt_leaf_fit")
-    _lib.check(lib.yabt_leaf_fold(N, K, a_W, a_b, a_mu, a_sd, float(params.learning_rate), value_in.data_ptr(),
-                                  value.data_ptr(), linear.data_ptr(), st), "yabt_leaf_fold")
+        _lib.check(lib.yabt_leaf_moments(x_kind, X.data_ptr(), ldx, n, a_fi, K, a_mws, mbytes, a_mu, a_sd, st),
+                   "yabt_leaf_moments")
+        _lib.check(lib.yabt_leaf_fit(x_kind, X.data_ptr(), ldx, n, a_fi, K, a_mu, a_sd,
+                                     g.data_ptr(), h.data_ptr(), li.data_ptr(), ft.data_ptr(), N, min_samples,
+                                     lam, mode, a_fws, fbytes, a_W, a_b, lo.data_ptr(), hi.data_ptr(), a_cnt,
+                                     status.data_ptr(), st), "yabt_leaf_fit")
+        _lib.check(lib.yabt_leaf_fold(N, K, a_W, a_b, a_mu, a_sd, lr, value_in.data_ptr(), value.data_ptr(),
+                                      linear.data_ptr(), st), "yabt_leaf_fold")
     st_, n_fit, n_used = status.tolist()   # the one wait for the device
     if rank_k and n_used < K:
         return None
