@@ -1084,11 +1084,18 @@ __global__ void k_leaf_status(const LeafStats* st, int32_t* out) {
 // The fold of the linear models into raw space (neural_leaves.py:178-184) in
 // the order and fp32 roundings of the reference's torch expressions: per node,
 // prod_j = W[j] * (mu[j] / sd[j]), acc = prod_0 + prod_1 + ... left to right,
-// value = value_in + lr * (b - acc), linear[j] = (lr * W[j]) / sd[j].
+// value = value_in + lr * (b - acc), linear[j] = (lr * W[j]) / sd[j].  With
+// st, the fit's status words go to out_status too (the fit's k_leaf_status,
+// folded into this launch when the two run back to back).
 __global__ void __launch_bounds__(LB) k_leaf_fold(int n_nodes, int K, const float* W, const float* b,
                                                   const float* mu, const float* sd, float lr,
-                                                  const float* value_in, float* out_value, float* out_linear) {
+                                                  const float* value_in, float* out_value, float* out_linear,
+                                                  const LeafStats* st, int32_t* out_status) {
     const int node = blockIdx.x * LB + threadIdx.x;
+    if (st && node == 0) {
+        out_status[0] = st->status;
+        out_status[1] = st->n_fit;
+    }
     if (node >= n_nodes) return;
     float acc = 0.0f;
     for (int j = 0; j < K; ++j) {
@@ -1577,11 +1584,16 @@ size_t yabt_leaf_fit_workspace_bytes(int64_t n, int n_nodes, int K) {
     return carve_leaf(nullptr, n, n_nodes, K, nullptr);
 }
 
-int yabt_leaf_fit(int x_kind, const void* X, int64_t ldx, int64_t n, const int32_t* feats, int K, const float* mu,
-                  const float* sd, const float* grad, const float* hess, const int64_t* leaf_of_row,
-                  const int64_t* feature, int n_nodes, int min_samples, double lam, int gram_mode,
-                  void* workspace, size_t workspace_bytes, float* out_W, float* out_b, float* out_lo,
-                  float* out_hi, int64_t* out_count, int32_t* out_status, hipStream_t stream) {
+}  // extern "C"
+
+// yabt_leaf_fit's launches; the status words by k_leaf_status unless the
+// caller takes the fit's LeafStats (*st_out) to copy them itself.
+static int leaf_fit_launch(int x_kind, const void* X, int64_t ldx, int64_t n, const int32_t* feats, int K,
+                           const float* mu, const float* sd, const float* grad, const float* hess,
+                           const int64_t* leaf_of_row, const int64_t* feature, int n_nodes, int min_samples,
+                           double lam, int gram_mode, void* workspace, size_t workspace_bytes, float* out_W,
+                           float* out_b, float* out_lo, float* out_hi, int64_t* out_count, int32_t* out_status,
+                           hipStream_t stream, const LeafStats** st_out) {
     if (n < 0 || n > 0xFFFFFFFFll || n_nodes < 1 || K < 1 || K > LKMAX || x_kind < 0 || x_kind > 2)
         return fail(-2, "yabt_leaf_fit: bad sizes (need 0 <= n < 2^32, n_nodes >= 1, 1 <= K <= 8, x_kind 0, 1 or 2)");
     if (gram_mode != 0 && gram_mode != 1) return fail(-2, "yabt_leaf_fit: gram_mode must be 0 or 1");
@@ -1618,8 +1630,21 @@ int yabt_leaf_fit(int x_kind, const void* X, int64_t ldx, int64_t n, const int32
         case 7: launch_leaf_fit<7>(A, out_W, out_b, out_lo, out_hi, out_count, stream); break;
         default: launch_leaf_fit<8>(A, out_W, out_b, out_lo, out_hi, out_count, stream); break;
     }
-    k_leaf_status<<<1, 1, 0, stream>>>(A.st, out_status);
+    if (st_out) *st_out = A.st;
+    else k_leaf_status<<<1, 1, 0, stream>>>(A.st, out_status);
     return launch_status("yabt_leaf_fit launch");
+}
+
+extern "C" {
+
+int yabt_leaf_fit(int x_kind, const void* X, int64_t ldx, int64_t n, const int32_t* feats, int K, const float* mu,
+                  const float* sd, const float* grad, const float* hess, const int64_t* leaf_of_row,
+                  const int64_t* feature, int n_nodes, int min_samples, double lam, int gram_mode,
+                  void* workspace, size_t workspace_bytes, float* out_W, float* out_b, float* out_lo,
+                  float* out_hi, int64_t* out_count, int32_t* out_status, hipStream_t stream) {
+    return leaf_fit_launch(x_kind, X, ldx, n, feats, K, mu, sd, grad, hess, leaf_of_row, feature, n_nodes,
+                           min_samples, lam, gram_mode, workspace, workspace_bytes, out_W, out_b, out_lo, out_hi,
+                           out_count, out_status, stream, nullptr);
 }
 
 int yabt_leaf_step(int x_kind, const void* X, int64_t ldx, int64_t n, int F, int K, const float* grad,
@@ -1634,11 +1659,15 @@ int yabt_leaf_step(int x_kind, const void* X, int64_t ldx, int64_t n, int F, int
     if (rc) return rc;
     rc = yabt_leaf_moments(x_kind, X, ldx, n, out_feats32, K, ws_moments, ws_moments_bytes, out_mu, out_sd, stream);
     if (rc) return rc;
-    rc = yabt_leaf_fit(x_kind, X, ldx, n, out_feats32, K, out_mu, out_sd, grad, hess, leaf_of_row, feature, n_nodes,
-                       min_samples, lam, gram_mode, ws_fit, ws_fit_bytes, out_W, out_b, out_lo, out_hi, out_count,
-                       out_status, stream);
+    const LeafStats* st = nullptr;
+    rc = leaf_fit_launch(x_kind, X, ldx, n, out_feats32, K, out_mu, out_sd, grad, hess, leaf_of_row, feature,
+                         n_nodes, min_samples, lam, gram_mode, ws_fit, ws_fit_bytes, out_W, out_b, out_lo, out_hi,
+                         out_count, out_status, stream, &st);
     if (rc) return rc;
-    return yabt_leaf_fold(n_nodes, K, out_W, out_b, out_mu, out_sd, lr, value_in, out_value, out_linear, stream);
+    if (!out_value || !out_linear || !value_in) return fail(-2, "yabt_leaf_step: null pointer argument");
+    k_leaf_fold<<<(n_nodes + LB - 1) / LB, LB, 0, stream>>>(n_nodes, K, out_W, out_b, out_mu, out_sd, lr, value_in,
+                                                           out_value, out_linear, st, out_status);
+    return launch_status("yabt_leaf_step launch");
 }
 
 int yabt_leaf_fold(int n_nodes, int K, const float* W, const float* b, const float* mu, const float* sd, float lr,
@@ -1647,7 +1676,7 @@ int yabt_leaf_fold(int n_nodes, int K, const float* W, const float* b, const flo
     if (!W || !b || !mu || !sd || !value_in || !out_value || !out_linear)
         return fail(-2, "yabt_leaf_fold: null pointer argument");
     k_leaf_fold<<<(n_nodes + LB - 1) / LB, LB, 0, stream>>>(n_nodes, K, W, b, mu, sd, lr, value_in, out_value,
-                                                           out_linear);
+                                                           out_linear, nullptr, nullptr);
     return launch_status("yabt_leaf_fold launch");
 }
 
