@@ -545,25 +545,299 @@ __device__ __forceinline__ void run_f32(const float2* s_gh, const uint16_t* idx,
     }
 }
 
-// Sequential double sums of the fp32 pairs s_gh[idx[k]] (idx null: s_gh[k]),
-// k in [0, hi).
+// Sequential double sums of the fp32 pairs s_gh[idx[k]] (IDX false: s_gh[k]),
+// k in [0, hi) (hi <= WT), in k order (grow.c:85-97).  The pairs go in blocks
+// of 8, the next block's (and its indices the block after) loaded while a
+// block is added, so that the dependent adds -- the node totals' chain over
+// all its rows is the longest of a sparse round -- do not wait on the LDS
+// for each block: ~22 -> ~10 cycles a row.  Prefetches past hi read
+// positions clamped inside the arrays and indices clamped below WT; their
+// values are never added.
+template <bool IDX>
 __device__ __forceinline__ void run_f64(const float2* s_gh, const uint16_t* idx, uint32_t hi, double& ag,
                                         double& ah) {
-    uint32_t k = 0;
-    for (; k + 8 <= hi; k += 8) {
-        float2 p[8];
+    const uint32_t nb = hi / 8;
+    auto pos = [](uint32_t blk) { return min(blk * 8u, (uint32_t)(WT - 8)); };
+    auto ids = [&](uint32_t blk, uint32_t (&i)[8]) {   // loads only: clamped at their use
+        const uint32_t p0 = pos(blk);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) p[j] = s_gh[idx ? (uint32_t)idx[k + j] : k + j];
+        for (int j = 0; j < 8; ++j) i[j] = IDX ? (uint32_t)idx[p0 + j] : p0 + j;
+    };
+    auto pairs = [&](const uint32_t (&i)[8], float2 (&p)[8]) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) p[j] = s_gh[min(i[j], (uint32_t)(WT - 1))];
+    };
+    auto add = [&](const float2 (&p)[8]) {
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             ag += (double)p[j].x;
             ah += (double)p[j].y;
         }
+    };
+    if (nb > 0) {
+        uint32_t ia[8], ib[8];
+        float2 a[8], b[8];
+        ids(0, ia);
+        pairs(ia, a);
+        ids(1, ib);
+        // (the compiler barriers keep each block's loads where they are issued,
+        // rather than sunk to their use)
+        for (uint32_t blk = 0;; blk += 2) {
+            pairs(ib, b);          // block blk + 1
+            ids(blk + 2, ia);
+            asm volatile("" ::: "memory");
+            add(a);                // block blk
+            if (blk + 1 >= nb) break;
+            pairs(ia, a);          // block blk + 2
+            ids(blk + 3, ib);
+            asm volatile("" ::: "memory");
+            add(b);                // block blk + 1
+            if (blk + 2 >= nb) break;
+        }
     }
-    for (; k < hi; ++k) {
-        const float2 p = s_gh[idx ? (uint32_t)idx[k] : k];
+    for (uint32_t k = nb * 8; k < hi; ++k) {
+        const float2 p = s_gh[IDX ? (uint32_t)idx[k] : k];
         ag += (double)p.x;
         ah += (double)p.y;
+    }
+}
+
+// Sequential double sum of channel C (0: g, 1: h) of the fp32 pairs s_gh[k],
+// k in [0, hi) (hi <= WT), in k order: the node totals (grow.c:85-97), one
+// channel per thread so that each wave's chain is one convert and one
+// dependent add per row (a wave issues each of them for all 64 lanes, so two
+// channels on one thread had cost twice the issue time of a row); the pairs
+// go in blocks of 16, the next block loaded while one is added (prefetches
+// past hi read positions clamped inside the array and are never added).
+template <int C>
+__device__ __forceinline__ void run_f64_chan(const float2* s_gh, uint32_t hi, double& acc) {
+    const uint32_t nb = hi / 16;
+    const float4* s4 = reinterpret_cast<const float4*>(s_gh);   // two pairs per float4
+    auto load = [&](uint32_t blk, float4 (&q)[8]) {
+        const uint32_t p0 = min(blk * 8u, (uint32_t)(WT / 2 - 8));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) q[j] = s4[p0 + j];
+    };
+    auto add = [&](const float4 (&q)[8]) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            acc += (double)(C == 0 ? q[j].x : q[j].y);
+            acc += (double)(C == 0 ? q[j].z : q[j].w);
+        }
+    };
+    if (nb > 0) {
+        float4 a[8], b[8];
+        load(0, a);
+        for (uint32_t blk = 0;; blk += 2) {
+            load(blk + 1, b);
+            asm volatile("" ::: "memory");   // the loads stay here, not sunk to their use
+            add(a);
+            if (blk + 1 >= nb) break;
+            load(blk + 2, a);
+            asm volatile("" ::: "memory");
+            add(b);
+            if (blk + 2 >= nb) break;
+        }
+    }
+    for (uint32_t k = nb * 16; k < hi; ++k) acc += (double)(C == 0 ? s_gh[k].x : s_gh[k].y);
+}
+
+// The sequential double sum S <- RN(S + (double)x_k), k = 0 .. tn - 1 in
+// order, of each channel of the fp32 pairs s_gh[k] (cgrow's node totals,
+// grow.c:85-97), computed by the whole block with the same result.  A step
+// rounds only when the exact partial sum does not fit a double's 53 bits,
+// and with fp32 addends that is rare (an addend far below |S|, or |S|
+// growing past a binade with its lowest bit set); the steps before the first
+// rounding give the exact sum, which any order computes.  So, in fixed point
+// with unit u = 2^(Emax - 61), where 2^Emax bounds |S| + sum |x_k| (every
+// exact partial sum below 2^62 u): each thread takes its share of the
+// elements as integers x_k / u, a block scan gives every exact prefix, and
+// the first element that is not a multiple of u or whose exact prefix does
+// not fit a double is added on its own as cgrow adds it; the tile then
+// starts again from the new S.  S is kept as S_int u + S_lo, |S_lo| < u: a
+// prefix T u + S_lo has S_lo's lowest bit, so it fits if |T| < 2^(l + 53 -
+// log2 u), l the exponent of that bit; with S_lo = 0 it fits if T's odd
+// part is below 2^53.  After TSE_TRIES restarts in one tile the remaining
+// elements are added one by one by one thread.  Every thread holds the same S.
+constexpr int TSE_TRIES = 8;
+__device__ __forceinline__ float tse_x(const float2* s_gh, int ch, int k) { return ch ? s_gh[k].y : s_gh[k].x; }
+
+// The exponent of x's lowest set bit (x finite, nonzero).
+__device__ __forceinline__ int tse_lsb_exp(double x) {
+    const uint64_t b = (uint64_t)__double_as_longlong(x) & 0x7fffffffffffffffull;
+    const int e = (int)(b >> 52);
+    uint64_t m = b & 0x000fffffffffffffull;
+    if (e == 0) return -1074 + __builtin_ctzll(m);
+    m |= 0x0010000000000000ull;
+    return e - 1075 + __builtin_ctzll(m);
+}
+
+// Both channels at once (g: c = 0, h: c = 1), so that they share the
+// block's passes and barriers; each channel restarts on its own.  s_wave:
+// 2 x RB / WAVE words, s_k, s_s, s_m: two each.
+__device__ void tile_sum_exact(const float2* s_gh, int tn, double (&S)[2], int64_t* s_wave, int* s_k,
+                               double* s_s, double* s_m) {
+    const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
+    constexpr int NW = RB / WAVE;
+    int k0[2] = {0, 0}, tries[2] = {0, 0};
+    for (;;) {
+        bool act[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) act[c] = k0[c] < tn;
+        if (!act[0] && !act[1]) return;
+        // a channel with many restarts: its rest one by one (threads 0 and 1)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+            if (act[c] && tries[c] >= TSE_TRIES) {
+                if (tid == c) {
+                    double a = S[c];
+                    for (int k = k0[c]; k < tn; ++k) a += (double)tse_x(s_gh, c, k);
+                    s_s[c] = a;
+                }
+            }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+            if (act[c] && tries[c] >= TSE_TRIES) {
+                S[c] = s_s[c];
+                k0[c] = tn;
+                act[c] = false;
+            }
+        __syncthreads();
+        if (!act[0] && !act[1]) return;
+        int kb[2], ke[2];
+        double am[2] = {0.0, 0.0};
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int cnt = tn - k0[c], per = (cnt + RB - 1) / RB;
+            kb[c] = k0[c] + tid * per;
+            ke[c] = min(tn, kb[c] + per);
+            if (act[c])
+                for (int k = kb[c]; k < ke[c]; ++k) am[c] += fabs((double)tse_x(s_gh, c, k));
+#pragma unroll
+            for (int d = WAVE / 2; d > 0; d >>= 1) am[c] += __shfl_xor(am[c], d, WAVE);
+        }
+        if (tid < 2) s_m[tid] = 0.0;
+        __syncthreads();
+        if (lane == 0) {
+            atomicAdd(&s_m[0], am[0]);
+            atomicAdd(&s_m[1], am[1]);
+        }
+        __syncthreads();
+        double M[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) M[c] = (fabs(S[c]) + s_m[c]) * (1.0 + 0x1p-30);
+        int ue[2];
+        double sc[2], Slo[2];
+        int64_t Sint[2], TL[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            if (act[c] && M[c] == 0.0) {      // S and the rest are zeros
+                k0[c] = tn;
+                act[c] = false;
+            }
+            if (act[c] && !(M[c] <= 0x1p1000)) {   // inf, NaN or near them: the rest one by one
+                tries[c] = TSE_TRIES;
+                act[c] = false;               // (this round does nothing for c)
+            }
+            int Emax = 0;
+            if (act[c]) (void)frexp(M[c], &Emax);   // 2^(Emax - 1) <= M < 2^Emax
+            ue[c] = Emax - 61;                // u = 2^ue: |partial sums| < 2^Emax = 2^61 u
+            sc[c] = ldexp(1.0, -ue[c]);
+            Sint[c] = act[c] ? (int64_t)(S[c] * sc[c]) : 0;   // exact scale, truncated
+            Slo[c] = act[c] ? S[c] - ldexp((double)Sint[c], ue[c]) : 0.0;
+            TL[c] = 0;
+            if (Slo[c] != 0.0) {
+                const int sh = tse_lsb_exp(Slo[c]) + 53 - ue[c];
+                TL[c] = sh > 0 ? ((int64_t)1 << sh) - 1 : 0;
+            }
+        }
+        auto fits = [&](int c, int64_t T) -> bool {
+            if (Slo[c] != 0.0) return (T < 0 ? -T : T) <= TL[c];
+            if (T == 0) return true;
+            uint64_t t = (uint64_t)(T < 0 ? -T : T);
+            t >>= __builtin_ctzll(t);
+            return t < ((uint64_t)1 << 53);
+        };
+        auto unit = [&](int c, int k, int64_t& r) -> bool {   // x_k / u, if an integer
+            const double v = (double)tse_x(s_gh, c, k) * sc[c];
+            if (v != rint(v) || fabs(v) >= 0x1p62) return false;
+            r = (int64_t)v;
+            return true;
+        };
+        int64_t loc[2] = {0, 0};
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+            if (act[c])
+                for (int k = kb[c]; k < ke[c]; ++k) {
+                    int64_t r = 0;
+                    if (unit(c, k, r)) loc[c] += r;
+                }
+        // exclusive scans of both channels' sums over the block
+        int64_t ex[2], total[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int64_t e = wave_incl_scan_i64(loc[c], lane) - loc[c];
+            if (lane == WAVE - 1) s_wave[c * NW + w] = e + loc[c];
+            ex[c] = e;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            int64_t off = 0, tot = 0;
+#pragma unroll
+            for (int i = 0; i < NW; ++i) {
+                const int64_t v = s_wave[c * NW + i];
+                if (i < w) off += v;
+                tot += v;
+            }
+            ex[c] += off;
+            total[c] = tot;
+        }
+        int bad[2] = {INT_MAX, INT_MAX};
+        int64_t Tbad[2] = {0, 0};
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+            if (act[c]) {
+                int64_t T = Sint[c] + ex[c];
+                for (int k = kb[c]; k < ke[c]; ++k) {
+                    int64_t r = 0;
+                    if (!unit(c, k, r) || !fits(c, T + r)) {
+                        bad[c] = k;
+                        Tbad[c] = T;          // the exact prefix before element k
+                        break;
+                    }
+                    T += r;
+                }
+            }
+        // first failures of both channels over the block
+        const int m0 = wave_min_i32(bad[0]), m1 = wave_min_i32(bad[1]);
+        if (tid < 2) s_k[tid] = INT_MAX;
+        __syncthreads();                      // (also: every wave has read s_wave)
+        if (lane == 0) {
+            atomicMin(&s_k[0], m0);
+            atomicMin(&s_k[1], m1);
+        }
+        __syncthreads();
+        const int kf[2] = {s_k[0], s_k[1]};
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+            if (act[c] && kf[c] != INT_MAX && kb[c] <= kf[c] && kf[c] < ke[c])   // cgrow's add of element kf
+                s_s[c] = (ldexp((double)Tbad[c], ue[c]) + Slo[c]) + (double)tse_x(s_gh, c, kf[c]);
+        __syncthreads();
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            if (!act[c]) continue;
+            if (kf[c] == INT_MAX) {           // no rounding in the rest: the exact sum
+                S[c] = ldexp((double)(Sint[c] + total[c]), ue[c]) + Slo[c];
+                k0[c] = tn;
+            } else {
+                S[c] = s_s[c];
+                k0[c] = kf[c] + 1;
+                ++tries[c];
+            }
+        }
+        __syncthreads();                      // s_s, s_k and s_m are rewritten next round
     }
 }
 
@@ -616,10 +890,13 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb,
                                                    const uint16_t* __restrict__ starts, int64_t n_tiles,
                                                    float* __restrict__ hist_base, size_t hsz,
                                                    double* __restrict__ eout_b, double* __restrict__ tot_b) {
-    __shared__ float2 s_gh[WT];
+    __shared__ __align__(16) float2 s_gh[WT];
     __shared__ uint16_t s_idx[WT];
     __shared__ uint16_t s_xidx[SPARSE ? WT : 1];
     __shared__ uint16_t s_st[ST];
+    __shared__ int64_t s_tw[2 * (RB / WAVE)];         // the totals block's scans
+    __shared__ int s_tk[2];
+    __shared__ double s_ts[2], s_tm[2];
     const int kj = blockIdx.y;
     const Job& J = R->job[kj];
     const int64_t m = J.ce - J.cs;
@@ -661,10 +938,14 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb,
         __syncthreads();
         if (t0 + WT < m) chain_load<SPARSE>(nxt, G, H, pf, xf, sf, totals, t + 1, m);
         if (totals) {
-            if (tid == 0) run_f64(s_gh, nullptr, (uint32_t)tn, eg, eh);
+            // the node's g and h in double in row order, by the whole block
+            double S2[2] = {eg, eh};
+            tile_sum_exact(s_gh, tn, S2, s_tw, s_tk, s_ts, s_tm);
+            eg = S2[0];
+            eh = S2[1];
         } else if (SPARSE && tid == df) {
             const uint32_t nx = s_st[NB];      // the tile's rows outside the default bin
-            run_f64(s_gh, s_xidx, nx, eg, eh);
+            run_f64<true>(s_gh, s_xidx, nx, eg, eh);
             cnt += (int64_t)tn - nx;
         } else {
             const uint32_t lo = s_st[tid], hi = s_st[tid + 1];
@@ -766,7 +1047,7 @@ __global__ void __launch_bounds__(CB) k_walk_chain_dense(const float* __restrict
                                                          const uint16_t* __restrict__ perm, int64_t ld_perm,
                                                          const uint16_t* __restrict__ starts, int64_t n_tiles,
                                                          float* __restrict__ hist_base, size_t hsz) {
-    __shared__ float2 s_gh[WT];
+    __shared__ __align__(16) float2 s_gh[WT];
     __shared__ float s_ch[2][WT];    // g, h in bucket order
     __shared__ uint16_t s_st[ST];
     const int kj = blockIdx.y;
