@@ -215,6 +215,12 @@ SPARSE_CASES = [
     dict(n=300_000, F=5, bins="skew", kind="laplace", max_leaves=63),
     dict(n=200_000, F=33, bins="skew", kind="laplace", max_leaves=40, max_depth=6),
     dict(n=10_000, F=9, bins="uniform", kind="normal", max_leaves=31, arbitrary=True),
+    # the node totals' double sums (computed in parallel up to each step that
+    # rounds): addends over ~76 binary orders, exact halves and zeros (ties
+    # and exact steps), one huge addend that later ones cannot move
+    dict(n=300_000, F=12, bins="skew", kind="laplace", max_leaves=63, gvals="wide"),
+    dict(n=200_000, F=10, bins="skew", kind="normal", max_leaves=31, gvals="halves"),
+    dict(n=150_000, F=8, bins="skew", kind="normal", max_leaves=31, gvals="outlier"),
 ]
 
 
@@ -228,6 +234,15 @@ def test_sparse_builder_matches_fp32_oracle(case):
     bins = {"skew": lambda: skewed_bins(rng, n, F), "modal": lambda: _modal_bins(rng, n, F),
             "uniform": lambda: uniform_bins(rng, n, F)}[kind]()
     g, h = grad_hess(rng, n, c.pop("kind"))
+    gvals = c.pop("gvals", None)
+    if gvals == "wide":
+        g, h = wide_gradients(rng, bins, g, h)
+    elif gvals == "halves":
+        g = (np.rint(g * 4.0) / 2.0).astype(np.float32)             # multiples of 1/2, many zeros
+        h = (np.rint(h * 8.0) / 8.0 + 0.125).astype(np.float32)
+    elif gvals == "outlier":
+        g = g.copy()
+        g[n // 3] = np.float32(3e12)
     kw = dict(max_leaves=c.pop("max_leaves"), max_depth=c.pop("max_depth", 64), msl=c.pop("msl", 20))
     if c.pop("imat", False):
         im = rng.random((F, F)).astype(np.float32)

@@ -602,46 +602,6 @@ __device__ __forceinline__ void run_f64(const float2* s_gh, const uint16_t* idx,
     }
 }
 
-// Sequential double sum of channel C (0: g, 1: h) of the fp32 pairs s_gh[k],
-// k in [0, hi) (hi <= WT), in k order: the node totals (grow.c:85-97), one
-// channel per thread so that each wave's chain is one convert and one
-// dependent add per row (a wave issues each of them for all 64 lanes, so two
-// channels on one thread had cost twice the issue time of a row); the pairs
-// go in blocks of 16, the next block loaded while one is added (prefetches
-// past hi read positions clamped inside the array and are never added).
-template <int C>
-__device__ __forceinline__ void run_f64_chan(const float2* s_gh, uint32_t hi, double& acc) {
-    const uint32_t nb = hi / 16;
-    const float4* s4 = reinterpret_cast<const float4*>(s_gh);   // two pairs per float4
-    auto load = [&](uint32_t blk, float4 (&q)[8]) {
-        const uint32_t p0 = min(blk * 8u, (uint32_t)(WT / 2 - 8));
-#pragma unroll
-        for (int j = 0; j < 8; ++j) q[j] = s4[p0 + j];
-    };
-    auto add = [&](const float4 (&q)[8]) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            acc += (double)(C == 0 ? q[j].x : q[j].y);
-            acc += (double)(C == 0 ? q[j].z : q[j].w);
-        }
-    };
-    if (nb > 0) {
-        float4 a[8], b[8];
-        load(0, a);
-        for (uint32_t blk = 0;; blk += 2) {
-            load(blk + 1, b);
-            asm volatile("" ::: "memory");   // the loads stay here, not sunk to their use
-            add(a);
-            if (blk + 1 >= nb) break;
-            load(blk + 2, a);
-            asm volatile("" ::: "memory");
-            add(b);
-            if (blk + 2 >= nb) break;
-        }
-    }
-    for (uint32_t k = nb * 16; k < hi; ++k) acc += (double)(C == 0 ? s_gh[k].x : s_gh[k].y);
-}
-
 // The sequential double sum S <- RN(S + (double)x_k), k = 0 .. tn - 1 in
 // order, of each channel of the fp32 pairs s_gh[k] (cgrow's node totals,
 // grow.c:85-97), computed by the whole block with the same result.  A step
