@@ -545,63 +545,6 @@ __device__ __forceinline__ void run_f32(const float2* s_gh, const uint16_t* idx,
     }
 }
 
-// Sequential double sums of the fp32 pairs s_gh[idx[k]] (IDX false: s_gh[k]),
-// k in [0, hi) (hi <= WT), in k order (grow.c:85-97).  The pairs go in blocks
-// of 8, the next block's (and its indices the block after) loaded while a
-// block is added, so that the dependent adds -- the node totals' chain over
-// all its rows is the longest of a sparse round -- do not wait on the LDS
-// for each block: ~22 -> ~10 cycles a row.  Prefetches past hi read
-// positions clamped inside the arrays and indices clamped below WT; their
-// values are never added.
-template <bool IDX>
-__device__ __forceinline__ void run_f64(const float2* s_gh, const uint16_t* idx, uint32_t hi, double& ag,
-                                        double& ah) {
-    const uint32_t nb = hi / 8;
-    auto pos = [](uint32_t blk) { return min(blk * 8u, (uint32_t)(WT - 8)); };
-    auto ids = [&](uint32_t blk, uint32_t (&i)[8]) {   // loads only: clamped at their use
-        const uint32_t p0 = pos(blk);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) i[j] = IDX ? (uint32_t)idx[p0 + j] : p0 + j;
-    };
-    auto pairs = [&](const uint32_t (&i)[8], float2 (&p)[8]) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) p[j] = s_gh[min(i[j], (uint32_t)(WT - 1))];
-    };
-    auto add = [&](const float2 (&p)[8]) {
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            ag += (double)p[j].x;
-            ah += (double)p[j].y;
-        }
-    };
-    if (nb > 0) {
-        uint32_t ia[8], ib[8];
-        float2 a[8], b[8];
-        ids(0, ia);
-        pairs(ia, a);
-        ids(1, ib);
-        // (the compiler barriers keep each block's loads where they are issued,
-        // rather than sunk to their use)
-        for (uint32_t blk = 0;; blk += 2) {
-            pairs(ib, b);          // block blk + 1
-            ids(blk + 2, ia);
-            asm volatile("" ::: "memory");
-            add(a);                // block blk
-            if (blk + 1 >= nb) break;
-            pairs(ia, a);          // block blk + 2
-            ids(blk + 3, ib);
-            asm volatile("" ::: "memory");
-            add(b);                // block blk + 1
-            if (blk + 2 >= nb) break;
-        }
-    }
-    for (uint32_t k = nb * 8; k < hi; ++k) {
-        const float2 p = s_gh[IDX ? (uint32_t)idx[k] : k];
-        ag += (double)p.x;
-        ah += (double)p.y;
-    }
-}
-
 // The sequential double sum S <- RN(S + (double)x_k), k = 0 .. tn - 1 in
 // order, of each channel of the fp32 pairs s_gh[k] (cgrow's node totals,
 // grow.c:85-97), computed by the whole block with the same result.  A step
@@ -620,7 +563,12 @@ __device__ __forceinline__ void run_f64(const float2* s_gh, const uint16_t* idx,
 // part is below 2^53.  After TSE_TRIES restarts in one tile the remaining
 // elements are added one by one by one thread.  Every thread holds the same S.
 constexpr int TSE_TRIES = 8;
-__device__ __forceinline__ float tse_x(const float2* s_gh, int ch, int k) { return ch ? s_gh[k].y : s_gh[k].x; }
+// Element k of the sum: channel ch of s_gh[k], or of s_gh[idx[k]] with IDX.
+template <bool IDX>
+__device__ __forceinline__ float tse_x(const float2* s_gh, const uint16_t* idx, int ch, int k) {
+    const float2 p = s_gh[IDX ? (int)idx[k] : k];
+    return ch ? p.y : p.x;
+}
 
 // The exponent of x's lowest set bit (x finite, nonzero).
 __device__ __forceinline__ int tse_lsb_exp(double x) {
@@ -635,8 +583,9 @@ __device__ __forceinline__ int tse_lsb_exp(double x) {
 // Both channels at once (g: c = 0, h: c = 1), so that they share the
 // block's passes and barriers; each channel restarts on its own.  s_wave:
 // 2 x RB / WAVE words, s_k, s_s, s_m: two each.
-__device__ void tile_sum_exact(const float2* s_gh, int tn, double (&S)[2], int64_t* s_wave, int* s_k,
-                               double* s_s, double* s_m) {
+template <bool IDX>
+__device__ void tile_sum_exact(const float2* s_gh, const uint16_t* idx, int tn, double (&S)[2], int64_t* s_wave,
+                               int* s_k, double* s_s, double* s_m) {
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
     constexpr int NW = RB / WAVE;
     int k0[2] = {0, 0}, tries[2] = {0, 0};
@@ -651,7 +600,7 @@ __device__ void tile_sum_exact(const float2* s_gh, int tn, double (&S)[2], int64
             if (act[c] && tries[c] >= TSE_TRIES) {
                 if (tid == c) {
                     double a = S[c];
-                    for (int k = k0[c]; k < tn; ++k) a += (double)tse_x(s_gh, c, k);
+                    for (int k = k0[c]; k < tn; ++k) a += (double)tse_x<IDX>(s_gh, idx, c, k);
                     s_s[c] = a;
                 }
             }
@@ -673,7 +622,7 @@ __device__ void tile_sum_exact(const float2* s_gh, int tn, double (&S)[2], int64
             kb[c] = k0[c] + tid * per;
             ke[c] = min(tn, kb[c] + per);
             if (act[c])
-                for (int k = kb[c]; k < ke[c]; ++k) am[c] += fabs((double)tse_x(s_gh, c, k));
+                for (int k = kb[c]; k < ke[c]; ++k) am[c] += fabs((double)tse_x<IDX>(s_gh, idx, c, k));
 #pragma unroll
             for (int d = WAVE / 2; d > 0; d >>= 1) am[c] += __shfl_xor(am[c], d, WAVE);
         }
@@ -720,7 +669,7 @@ __device__ void tile_sum_exact(const float2* s_gh, int tn, double (&S)[2], int64
             return t < ((uint64_t)1 << 53);
         };
         auto unit = [&](int c, int k, int64_t& r) -> bool {   // x_k / u, if an integer
-            const double v = (double)tse_x(s_gh, c, k) * sc[c];
+            const double v = (double)tse_x<IDX>(s_gh, idx, c, k) * sc[c];
             if (v != rint(v) || fabs(v) >= 0x1p62) return false;
             r = (int64_t)v;
             return true;
@@ -783,7 +732,7 @@ __device__ void tile_sum_exact(const float2* s_gh, int tn, double (&S)[2], int64
 #pragma unroll
         for (int c = 0; c < 2; ++c)
             if (act[c] && kf[c] != INT_MAX && kb[c] <= kf[c] && kf[c] < ke[c])   // cgrow's add of element kf
-                s_s[c] = (ldexp((double)Tbad[c], ue[c]) + Slo[c]) + (double)tse_x(s_gh, c, kf[c]);
+                s_s[c] = (ldexp((double)Tbad[c], ue[c]) + Slo[c]) + (double)tse_x<IDX>(s_gh, idx, c, kf[c]);
         __syncthreads();
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
@@ -900,17 +849,25 @@ __global__ void __launch_bounds__(RB) k_walk_chain(const float* __restrict__ Gb,
         if (totals) {
             // the node's g and h in double in row order, by the whole block
             double S2[2] = {eg, eh};
-            tile_sum_exact(s_gh, tn, S2, s_tw, s_tk, s_ts, s_tm);
+            tile_sum_exact<false>(s_gh, nullptr, tn, S2, s_tw, s_tk, s_ts, s_tm);
             eg = S2[0];
             eh = S2[1];
-        } else if (SPARSE && tid == df) {
-            const uint32_t nx = s_st[NB];      // the tile's rows outside the default bin
-            run_f64<true>(s_gh, s_xidx, nx, eg, eh);
-            cnt += (int64_t)tn - nx;
         } else {
-            const uint32_t lo = s_st[tid], hi = s_st[tid + 1];
-            run_f32(s_gh, s_idx, lo, hi, ag, ah);
-            cnt += hi - lo;
+            if (SPARSE && tid == df) {
+                cnt += (int64_t)tn - s_st[NB];
+            } else {
+                const uint32_t lo = s_st[tid], hi = s_st[tid + 1];
+                run_f32(s_gh, s_idx, lo, hi, ag, ah);
+                cnt += hi - lo;
+            }
+            if (SPARSE) {
+                // the tile's rows outside the default bin (xidx, in row
+                // order), their g and h in double, by the whole block
+                double S2[2] = {eg, eh};
+                tile_sum_exact<true>(s_gh, s_xidx, (int)s_st[NB], S2, s_tw, s_tk, s_ts, s_tm);
+                eg = S2[0];
+                eh = S2[1];
+            }
         }
         __syncthreads();
     }
