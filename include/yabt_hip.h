@@ -397,7 +397,8 @@ size_t yabt_ref_root_order_bytes(int64_t n, int F);
 
 /* The root rank table of yabt_grow_ref's dense builder, once per fit: for
  * every feature and every 4096-row tile of rows 0 .. n - 1, each row's rank
- * among the tile's rows in its bin (row order) and the tile's bin starts --
+ * among the tile's rows in its bin (row order), the tile's bin starts, its
+ * longest run and its largest bin --
  * the bucketing of cgrow's row-order histogram chains (yabt/_cgrow/grow.c:
  * 37-62) of the root, which is the same for every tree grown on these bins.
  * out: device memory of at least yabt_ref_root_order_bytes(n, F) bytes.

@@ -77,14 +77,15 @@ def test_reference_grower_workspace_sizes():
 
 def test_reference_root_order_sizes():
     """The per-fit root rank table: a uint16 rank per (feature, row) padded to
-    whole 4096-row tiles, then 257 uint16 run starts and the uint16 longest
-    run per (feature, tile)."""
+    whole 4096-row tiles, then 257 uint16 run starts, the uint16 longest run
+    and the uint8 largest bin per (feature, tile)."""
     lib = _lib.load()
     def rounded(b):
         return (b + 255) // 256 * 256
     for n, F in [(10_000_000, 100), (4097, 3), (1, 1)]:
         tiles = -(-n // 4096)
-        want = rounded(2 * F * tiles * 4096) + rounded(2 * F * tiles * 257) + rounded(2 * F * tiles)
+        want = (rounded(2 * F * tiles * 4096) + rounded(2 * F * tiles * 257) + rounded(2 * F * tiles)
+                + rounded(F * tiles))
         assert lib.yabt_ref_root_order_bytes(n, F) == want
     assert lib.yabt_ref_root_order_bytes(100, 0) == 0
     assert lib.yabt_ref_root_order_bytes(-1, 4) == 0

@@ -1027,20 +1027,22 @@ __global__ void __launch_bounds__(CB) k_walk_chain_dense(const float* __restrict
 // in row order, as k_walk_sort's), and each tile's run starts.  Each tree's
 // root then runs only the chains, k_rank_chain: one block per feature, thread
 // b = bin b, the tiles in order; a tile's g, h go into an LDS table T[rank][bin]
-// (a window of RW ranks at a time), so that step r of every thread reads its
-// run's r-th entry from one row of T -- 64 consecutive cells per wave, no bank
-// conflicts -- and adds it in fp32 as cgrow does (grow.c:55-59).
+// (a window of ranks at a time: RW of 256 bins, more of fewer), so that step r
+// of every thread reads its run's r-th entry from one row of T -- consecutive
+// cells across a wave, no bank conflicts -- and adds it in fp32 as cgrow does
+// (grow.c:55-59).
 
-constexpr int RW = 32;             // ranks per window of k_rank_chain's LDS table
+constexpr int RW = 32;             // ranks per window of k_rank_chain's LDS table at 256 bins
 
 // The rank table of yabt_ref_root_order: ranks (uint16, F x ld_rank, position
 // t * WT + x of feature f at f * ld_rank + t * WT + x), the run starts
-// (uint16, F x tiles x ST, as k_walk_sort's), and each (feature, tile)'s
-// longest run (uint16, F x tiles).
+// (uint16, F x tiles x ST, as k_walk_sort's), each (feature, tile)'s longest
+// run (uint16, F x tiles) and its largest bin present (uint8, F x tiles).
 struct RootOrder {
     uint16_t* rank;
     uint16_t* starts;
     uint16_t* maxrun;
+    uint8_t* maxbin;
     int64_t ld_rank;
     int64_t tiles;
 };
@@ -1051,14 +1053,16 @@ __host__ __device__ inline size_t root_order_carve(char* base, int64_t n, int F,
     const size_t rank_bytes = ((size_t)F * (size_t)ld * sizeof(uint16_t) + 255) / 256 * 256;
     const size_t st_bytes = ((size_t)F * (size_t)tiles * ST * sizeof(uint16_t) + 255) / 256 * 256;
     const size_t mx_bytes = ((size_t)F * (size_t)tiles * sizeof(uint16_t) + 255) / 256 * 256;
+    const size_t mb_bytes = ((size_t)F * (size_t)tiles + 255) / 256 * 256;
     if (o) {
         o->rank = (uint16_t*)base;
         o->starts = (uint16_t*)(base + rank_bytes);
         o->maxrun = (uint16_t*)(base + rank_bytes + st_bytes);
+        o->maxbin = (uint8_t*)(base + rank_bytes + st_bytes + mx_bytes);
         o->ld_rank = ld;
         o->tiles = tiles;
     }
-    return rank_bytes + st_bytes + mx_bytes;
+    return rank_bytes + st_bytes + mx_bytes + mb_bytes;
 }
 
 // Block (f, t): the ranks and run starts of feature f's tile t (tiles grid-
@@ -1069,7 +1073,7 @@ __global__ void __launch_bounds__(RB, 8) k_root_rank(const uint8_t* __restrict__
     __shared__ uint64_t s_peer[SW][NB];
     __shared__ uint32_t s_cnt[SW][NB];
     __shared__ uint32_t s_scan[SW];
-    __shared__ uint32_t s_max;
+    __shared__ uint32_t s_max, s_mb;
     const int f = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & (WAVE - 1), w = tid / WAVE;
     for (int64_t t = blockIdx.y; t < o.tiles; t += gridDim.y) {
@@ -1079,7 +1083,10 @@ __global__ void __launch_bounds__(RB, 8) k_root_rank(const uint8_t* __restrict__
             (&s_cnt[0][0])[i] = 0;
             (&s_peer[0][0])[i] = 0;
         }
-        if (tid == 0) s_max = 0;
+        if (tid == 0) {
+            s_max = 0;
+            s_mb = 0;
+        }
 #pragma unroll
         for (int j = 0; j < TPT; ++j) {
             const int x = j * RB + tid;
@@ -1116,8 +1123,12 @@ __global__ void __launch_bounds__(RB, 8) k_root_rank(const uint8_t* __restrict__
             }
             uint32_t total;
             atomicMax(&s_max, tb);
+            if (tb) atomicMax(&s_mb, (uint32_t)b);
             const uint32_t st = block_excl_scan<RB, uint32_t>(tb, s_scan, &total);
-            if (tid == 0) o.maxrun[(size_t)f * (size_t)o.tiles + (size_t)t] = (uint16_t)s_max;
+            if (tid == 0) {
+                o.maxrun[(size_t)f * (size_t)o.tiles + (size_t)t] = (uint16_t)s_max;
+                o.maxbin[(size_t)f * (size_t)o.tiles + (size_t)t] = (uint8_t)s_mb;
+            }
             uint16_t* st_out = o.starts + ((size_t)f * (size_t)o.tiles + (size_t)t) * ST;
             st_out[b] = (uint16_t)st;
             if (b == NB - 1) st_out[NB] = (uint16_t)(st + tb);
@@ -1220,22 +1231,26 @@ __device__ __forceinline__ void rank_tile_load_any(RankTile& c, const float* __r
 // One window of a tile's entries, g and h in separate tables: a producer
 // writes each value as it was loaded (pairing g with h for one 8-byte store
 // would have the compiler permute the loaded registers right after the
-// loads, which waits for them).
+// loads, which waits for them).  Cell (r, b) is at (r << lg) + b, where
+// 2^lg >= 1 + the feature's largest bin: a window holds RW NB >> lg ranks, so
+// a feature of few bins (long runs per tile) takes a tile in one window.
 struct RankTable {
-    float g[RW][NB];
-    float h[RW][NB];
+    float g[RW * NB];
+    float h[RW * NB];
 };
 
-// A producer's window [w0, w0 + RW) of its tile's entries into T[rank - w0][bin].
-__device__ __forceinline__ void rank_stage(const RankTile& c, RankTable& T, uint32_t w0) {
+// A producer's window [w0, w0 + rw) of its tile's entries into T[rank - w0][bin]
+// (rw = RW NB >> lg; a bin past 2^lg, which the rank table rules out, is
+// dropped rather than written into another rank's cells).
+__device__ __forceinline__ void rank_stage(const RankTile& c, RankTable& T, uint32_t w0, uint32_t rw, int lg) {
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
-        // a rank below w0 wraps above RW; past the rows the rank is 0xffff
+        // a rank below w0 wraps above rw; past the rows the rank is 0xffff
         const uint32_t rank = rt_rank(c, j), r = rank - w0;
-        if (rank != 0xffffu && r < (uint32_t)RW) {
-            const uint32_t b = rt_bin(c, j);
-            T.g[r][b] = rt_g(c, j);
-            T.h[r][b] = rt_h(c, j);
+        const uint32_t b = rt_bin(c, j);
+        if (rank != 0xffffu && r < rw && (b >> lg) == 0) {
+            T.g[(r << lg) + b] = rt_g(c, j);
+            T.h[(r << lg) + b] = rt_h(c, j);
         }
     }
 }
@@ -1243,10 +1258,11 @@ __device__ __forceinline__ void rank_stage(const RankTile& c, RankTable& T, uint
 // Block f: the root's fp32 cells of feature f, cgrow's row-order chains
 // (grow.c:37-62); the count cell is cgrow's chain of 1.0f adds,
 // min(count, 2^24).  Threads 0 .. RB - 1 are the consumers, thread b adding
-// bin b's run of each tile in rank order from an LDS table T[rank][bin];
+// bin b's run of each tile in rank order from an LDS table T[rank][bin]
+// (2^lg bins a rank, lg from the largest bin of the feature's tiles);
 // threads RB .. RB + RPROD - 1 are the producers, filling the other of two
 // tables with the next tile meanwhile (window 0 of every tile; a tile whose
-// longest run passes RW has its further windows staged and added in turn,
+// longest run passes the window has its further windows staged and added in turn,
 // its positions reloaded).  The producers' next tiles load RING tiles ahead:
 // a step is shorter than a load's latency under load.  VEC:
 // g, h and the bins are 16-byte aligned (every feature's column:
@@ -1256,6 +1272,7 @@ __global__ void __launch_bounds__(RB + RPROD) k_rank_chain(const float* __restri
                                                        const uint8_t* __restrict__ bins_fm, int64_t ld_fm, int64_t n,
                                                        RootOrder o, float* __restrict__ hist, int F) {
     __shared__ RankTable T[2];
+    __shared__ uint32_t s_mb;
     const int f = blockIdx.x;
     const bool prod = threadIdx.x >= RB;
     const int lt = prod ? (int)threadIdx.x - RB : (int)threadIdx.x;   // consumers: the bin; producers: the slot
@@ -1265,21 +1282,40 @@ __global__ void __launch_bounds__(RB + RPROD) k_rank_chain(const float* __restri
     const uint16_t* mx = o.maxrun + (size_t)f * (size_t)o.tiles;
     const int64_t tiles = (n + WT - 1) / WT;
     const int64_t full = VEC ? n / WT : 0;      // tiles the producers load with 16-byte loads
-    float ag = 0.0f, ah = 0.0f;
+    {
+        if (threadIdx.x == 0) s_mb = 0;
+        __syncthreads();
+        uint32_t m = 0;
+        const uint8_t* mb = o.maxbin + (size_t)f * (size_t)o.tiles;
+        for (int64_t t = threadIdx.x; t < tiles; t += blockDim.x) m = max(m, (uint32_t)mb[t]);
+        atomicMax(&s_mb, m);
+        __syncthreads();
+    }
+    const int lg = 32 - __builtin_clz(__builtin_amdgcn_readfirstlane((int)s_mb) | 1);   // 2^lg > the largest bin
+    const uint32_t rw = (uint32_t)(RW * NB) >> lg;                                     // ranks per window
+    // consumers: at 256 bins (both) thread lt runs both chains of bin lt;
+    // below, thread lt runs the one chain of channel cch = lt >> lg (0: g,
+    // 1: h) of bin cb = lt mod 2^lg, and threads from 2^(lg + 1) on idle
+    const bool both = lg == 8;
+    const int cb = both ? lt : (lt & ((1 << lg) - 1));
+    const int cch = both ? 0 : (lt >> lg);
+    const bool live = prod || cch < 2;
+    float ag = 0.0f, ah = 0.0f;   // both: g and h; else: channel cch in ag
     int64_t cnt = 0;
-    // consumer: window [w0, w0 + RW) of tile t's run of bin lt from table Tb;
-    // steps to the tile's longest run in the window (uniform), eight reads in
-    // flight; past this thread's run a step adds +0.0f, which leaves the sums'
-    // bits unchanged (a sum that starts at +0.0f is never -0.0f)
-    auto run = [&](const RankTable& Tb, uint32_t len, uint32_t mr, uint32_t w0) {
-        const uint32_t kend = min(len > w0 ? len - w0 : 0u, (uint32_t)RW);
-        const uint32_t kmax = min(mr - w0, (uint32_t)RW);
+    // consumer: window [w0, w0 + rw) of tile t's run of its bin from table Tb;
+    // steps to the tile's longest run in the window (uniform); past this
+    // thread's run a step adds +0.0f, which leaves the sums' bits unchanged (a
+    // sum that starts at +0.0f is never -0.0f).  Both chains: eight ranks'
+    // reads in flight, then their adds.
+    auto run2 = [&](const RankTable& Tb, uint32_t len, uint32_t mr, uint32_t w0) {
+        const uint32_t kend = min(len > w0 ? len - w0 : 0u, rw);
+        const uint32_t kmax = min(mr - w0, rw);
         for (uint32_t r = 0; r < kmax; r += 8) {
             float vg[8], vh[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
-                vg[u] = Tb.g[r + u][lt];
-                vh[u] = Tb.h[r + u][lt];
+                vg[u] = Tb.g[((r + u) << 8) + lt];
+                vh[u] = Tb.h[((r + u) << 8) + lt];
             }
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
@@ -1288,6 +1324,38 @@ __global__ void __launch_bounds__(RB + RPROD) k_rank_chain(const float* __restri
                 ah += in ? vh[u] : 0.0f;
             }
         }
+    };
+    // One chain (tb: the channel's table at the bin's column), sixteen ranks a
+    // turn in two register sets: each set's next reads are issued before the
+    // other set's adds (the accumulator passes through the asm after the
+    // reads, so the adds cannot move above them); groups past the window
+    // read a clamped group in it, unused.
+    auto run1 = [&](const float* tb, uint32_t len, uint32_t mr, uint32_t w0) {
+        const uint32_t kend = min(len > w0 ? len - w0 : 0u, rw);
+        const uint32_t kmax = min(mr - w0, rw);
+        if (kmax == 0) return;
+        float a[8], b[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) a[u] = tb[u << lg];
+        for (uint32_t r = 0; r < kmax; r += 16) {
+            const uint32_t rb = min(r + 8, rw - 8), ra = min(r + 16, rw - 8);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) b[u] = tb[(rb + u) << lg];
+            asm volatile("" : "+v"(ag) : : "memory");
+#pragma unroll
+            for (int u = 0; u < 8; ++u) ag += r + u < kend ? a[u] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 8; ++u) a[u] = tb[(ra + u) << lg];
+            asm volatile("" : "+v"(ag) : : "memory");
+#pragma unroll
+            for (int u = 0; u < 8; ++u) ag += r + 8 + u < kend ? b[u] : 0.0f;
+        }
+    };
+    auto run = [&](const RankTable& Tb, uint32_t len, uint32_t mr, uint32_t w0) {
+        if (both)
+            run2(Tb, len, mr, w0);
+        else
+            run1((cch ? Tb.h : Tb.g) + cb, len, mr, w0);
     };
     auto load = [&](RankTile& c, int64_t t) {
         if (t < full)
@@ -1300,7 +1368,7 @@ __global__ void __launch_bounds__(RB + RPROD) k_rank_chain(const float* __restri
     // (a load used in the step it is issued would put a memory latency on
     // every tile's path)
     uint32_t mrs[RING], se[RING];
-    const uint16_t* sfl = sf + lt;   // consumers' start entries: tile t at sfl[t ST], its end at sfl[t ST + 1]
+    const uint16_t* sfl = sf + (prod ? 0 : cb);   // consumers' start entries: tile t at sfl[t ST], its end at sfl[t ST + 1]
     auto meta = [&](int k, int64_t t) {
         if (t < tiles) {
             mrs[k] = mx[t];
@@ -1314,7 +1382,7 @@ __global__ void __launch_bounds__(RB + RPROD) k_rank_chain(const float* __restri
     if (prod && tiles > 0) {
         RankTile c;
         load(c, 0);
-        rank_stage(c, T[0], 0);
+        rank_stage(c, T[0], 0, rw, lg);
     }
     if (prod && full > 0) {
 #pragma unroll
@@ -1331,27 +1399,27 @@ __global__ void __launch_bounds__(RB + RPROD) k_rank_chain(const float* __restri
         if (!prod) len = (se[k] >> 16) - (se[k] & 0xffffu);
         meta(k, t + RING);
         if (!prod) {
-            run(T[t & 1], len, mr, 0);
+            if (live) run(T[t & 1], len, mr, 0);
             cnt += len;
         } else if (t + 1 < tiles) {
             if (t + 1 < full) {
-                rank_stage(R, T[(t + 1) & 1], 0);
+                rank_stage(R, T[(t + 1) & 1], 0, rw, lg);
             } else {
                 RankTile c;
                 rank_tile_load_any(c, g, h, bn, rk, t + 1, n, lt);
-                rank_stage(c, T[(t + 1) & 1], 0);
+                rank_stage(c, T[(t + 1) & 1], 0, rw, lg);
             }
         }
         if (prod && full > 0) rank_tile_load_vec(R, g, h, bn, rk, min(t + 1 + RING, full - 1), lt);
         __syncthreads();
-        for (uint32_t w0 = RW; w0 < mr; w0 += RW) {
+        for (uint32_t w0 = rw; w0 < mr; w0 += rw) {
             if (prod) {
                 RankTile c;
                 load(c, t);
-                rank_stage(c, T[t & 1], w0);
+                rank_stage(c, T[t & 1], w0, rw, lg);
             }
             __syncthreads();
-            if (!prod) run(T[t & 1], len, mr, w0);
+            if (!prod && live) run(T[t & 1], len, mr, w0);
             __syncthreads();
         }
     };
@@ -1359,10 +1427,25 @@ __global__ void __launch_bounds__(RB + RPROD) k_rank_chain(const float* __restri
 #pragma unroll
         for (int k = 0; k < RING; ++k) step(t + k, ring[k], k);
     }
+    // below 256 bins the chains' sums meet in LDS (T[0], free after the last
+    // step's barrier): s_o[ch NB + bin], the counts at T[0].h; bins from 2^lg
+    // on are empty
+    float* s_o = T[0].g;
+    __syncthreads();
+    if (!both && !prod && cch < 2) s_o[cch * NB + cb] = ag;
+    if (!both && !prod && cch == 0) T[0].h[cb] = (float)min(cnt, (int64_t)1 << 24);
+    __syncthreads();
     if (!prod) {
-        hist[(size_t)f * NB + lt] = ag;
-        hist[(size_t)F * NB + (size_t)f * NB + lt] = ah;
-        hist[(size_t)2 * F * NB + (size_t)f * NB + lt] = (float)min(cnt, (int64_t)1 << 24);
+        float vg = ag, vh = ah, vc = (float)min(cnt, (int64_t)1 << 24);
+        if (!both) {
+            const bool in = (lt >> lg) == 0;
+            vg = in ? s_o[lt] : 0.0f;
+            vh = in ? s_o[NB + lt] : 0.0f;
+            vc = in ? T[0].h[lt] : 0.0f;
+        }
+        hist[(size_t)f * NB + lt] = vg;
+        hist[(size_t)F * NB + (size_t)f * NB + lt] = vh;
+        hist[(size_t)2 * F * NB + (size_t)f * NB + lt] = vc;
     }
 }
 
