@@ -347,22 +347,7 @@ __global__ void __launch_bounds__(LSB) k_leaf_count(LeafArgs A) {
         else atomicAdd(&s_cnt[node], 1u);
     };
     const int64_t ng = A.vec4 ? (hi - lo) / 4 : 0, first = lo + 4 * ng;
-    int64_t q = threadIdx.x;
-    // four groups' loads in flight before their counts
-    for (; q + 3 * LSB < ng; q += 4 * LSB) {
-        longlong2 v[8];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            v[2 * u] = *reinterpret_cast<const longlong2*>(A.leaf + lo + 4 * (q + u * LSB));
-            v[2 * u + 1] = *reinterpret_cast<const longlong2*>(A.leaf + lo + 4 * (q + u * LSB) + 2);
-        }
-#pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            count(v[u].x);
-            count(v[u].y);
-        }
-    }
-    for (; q < ng; q += LSB) {
+    for (int64_t q = threadIdx.x; q < ng; q += LSB) {
         const longlong2 la = *reinterpret_cast<const longlong2*>(A.leaf + lo + 4 * q);
         const longlong2 lb = *reinterpret_cast<const longlong2*>(A.leaf + lo + 4 * q + 2);
         count(la.x);
@@ -414,20 +399,13 @@ __global__ void __launch_bounds__(LSB) k_leaf_scatter_stats(LeafArgs A) {
         if (!isfinite(gi) || !isfinite(hi_)) bad = 1;
         mg = fmaxf(mg, fabsf(gi));
         mh = fmaxf(mh, fabsf(hi_));
-        // the extremes settle quickly: the node's 2K cells are read together
-        // (one wait), and only an improving input is sent as an atomic; a
-        // stale read can only add an atomic that changes nothing
-        uint32_t clo[K], chi[K];
-#pragma unroll
-        for (int j = 0; j < K; ++j) {
-            clo[j] = s_lo[node * K + j];
-            chi[j] = s_hi[node * K + j];
-        }
 #pragma unroll
         for (int j = 0; j < K; ++j) {
             const uint32_t kx = float_key(x[j]);
-            if (kx < clo[j]) atomicMin(&s_lo[node * K + j], kx);
-            if (kx > chi[j]) atomicMax(&s_hi[node * K + j], kx);
+            uint32_t* plo = &s_lo[node * K + j];
+            uint32_t* phi = &s_hi[node * K + j];
+            if (kx < *(volatile uint32_t*)plo) atomicMin(plo, kx);
+            if (kx > *(volatile uint32_t*)phi) atomicMax(phi, kx);
         }
         const uint64_t pos = s_base[node] + atomicAdd(&s_cnt[node], 1u);
         A.sorted_gh[pos] = make_float2(gi, hi_);
@@ -455,14 +433,9 @@ __global__ void __launch_bounds__(LSB) k_leaf_scatter_stats(LeafArgs A) {
             }
         }
     }
-    // uint8 inputs: the next group's loads are issued before this group's
-    // updates (clamped to the last group: a repeated load, unused)
-    Rows4<K> R;
-    if (A.vec4 == 1 && threadIdx.x < ng) load_rows4<K>(A, s_fs, lo + 4 * (int64_t)threadIdx.x, R);
     for (int64_t q = threadIdx.x; A.vec4 == 1 && q < ng; q += LSB) {
-        Rows4<K> Rn;
-        load_rows4<K>(A, s_fs, lo + 4 * min(q + LSB, ng - 1), Rn);
-        asm volatile("" ::: "memory");
+        Rows4<K> R;
+        load_rows4<K>(A, s_fs, lo + 4 * q, R);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int64_t node = R.node[r];
@@ -478,7 +451,6 @@ __global__ void __launch_bounds__(LSB) k_leaf_scatter_stats(LeafArgs A) {
             }
             put(node, x, R.g[r], R.h[r], make_uint2(w0, w1));
         }
-        R = Rn;
     }
     for (int64_t i = first + threadIdx.x; i < hi; i += LSB) {
         const int64_t node = A.leaf[i];
